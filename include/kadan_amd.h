@@ -1,0 +1,157 @@
+/*
+ * kadan_amd: MI355X (gfx950) quantized-weight matmul path -- the C ABI.
+ *
+ * This is the drop-in boundary below the reference worker's C++ projection
+ * interface kadan::DenseCompute (IW/include/kadan/dense_compute.hpp:60-342,
+ * IW = services/hikari/inference_worker).  Every entry point takes plain device
+ * pointers, sizes and a hipStream_t passed as void*; no C++ or torch type crosses
+ * it.  All pointers are device pointers unless stated otherwise.  Calls enqueue on
+ * `stream` and return without synchronizing; a status code other than KDQ_OK means
+ * nothing was enqueued (argument errors are detected before any launch).
+ *
+ * Encodings are named by their GGML type id, as IW/include/kadan/gguf_quantization.hpp:30-55
+ * maps them (Q4_0 = 2 is added here; the reference has no kadan encoding for it).
+ */
+#ifndef KADAN_AMD_H
+#define KADAN_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes.  The reference reports these conditions as exception strings
+ * (IW/src/cuda/h3_compute.cu:34-37,1767-1830,2178,4047); the host C++ layer
+ * (kadan_amd/csrc/hip_dense_compute.cpp) maps each code back to such a string. */
+enum kdq_status {
+    KDQ_OK = 0,
+    KDQ_ERR_ARGUMENT = 1,     /* null pointer, zero or overflowing size */
+    KDQ_ERR_SHAPE = 2,        /* "h3_cuda_projection_shape" */
+    KDQ_ERR_UNSUPPORTED = 3,  /* encoding/shape outside this implementation */
+    KDQ_ERR_ALIAS = 4,        /* "h3_cuda_alias": output overlaps an input */
+    KDQ_ERR_HIP = 5,          /* a HIP runtime call failed */
+    KDQ_ERR_SCRATCH = 6,      /* "h3_cuda_projection_scratch": workspace allocation */
+    KDQ_ERR_ALIGNMENT = 7     /* device pointer alignment the kernels need */
+};
+
+/* ---- encodings (GGML type ids) */
+enum kdq_encoding { KDQ_Q4_0 = 2, KDQ_Q8_0 = 8, KDQ_Q4_K = 12 };
+
+/* Human-readable name of a status code (static storage). */
+const char* kdq_status_string(int status);
+
+/* Last HIP error text recorded on this thread by a KDQ_ERR_HIP return. */
+const char* kdq_last_hip_error(void);
+
+/* Values and bytes per packed block: IW/include/kadan/gguf_quantization.hpp:65-95
+ * (gguf::block_values / block_bytes); 0 for an unknown encoding. */
+size_t kdq_block_values(int encoding);
+size_t kdq_block_bytes(int encoding);
+
+/* Bytes of one packed row of `in` values: IW/include/kadan/device_placement.hpp:115-124
+ * (gguf_projection_row_bytes).  0 when `in` is not a whole number of blocks. */
+size_t kdq_row_bytes(int encoding, size_t in);
+
+/* ---- prefill decode (replaces gguf_decode_kernel, IW/src/cuda/h3_compute.cu:76-95)
+ * Decodes `rows` packed rows of `in` values to fp32 [rows x in], bit-exact to
+ * kadan::gguf::decode (IW/include/kadan/gguf_quantization.hpp:631-762) and, for Q4_0,
+ * to ggml dequantize_row_q4_0.  When `status` is non-null, *status |= 1 if any decoded
+ * value is not finite (the caller zeroes it). */
+int kdq_dequantize(int encoding, const void* packed, size_t row_bytes, size_t rows, size_t in,
+                   float* out, unsigned* status, void* stream);
+
+/* ---- decode-time product (replaces gguf_matvec_kernel / launch_matvec(const MatvecJob&),
+ * IW/src/cuda/h3_compute.cu:165-240,294-306)
+ * y[r*stride + c] = sum_k decode(W[c, k]) * x[r*in + k] for r < rows, c < out.
+ * W: `out` packed rows of `row_bytes` each.  x: fp32 [rows x in], y: fp32.
+ * rows: 1..4096 (more than one pass when needed; gguf_batch_max_rows,
+ * IW/include/kadan/dense_compute.hpp:201).  fp32 accumulation; the activation
+ * operand is carried as 16-bit block fixed point per 32 values (relative error
+ * below 2^-15 of the block maximum), products exact in int32.
+ * `status`: as kdq_dequantize, set when a block scale is not finite. */
+int kdq_gemv(int encoding, const void* weights, size_t row_bytes, const float* x, size_t rows,
+             size_t in, size_t out, float* y, size_t stride, unsigned* status, void* stream);
+
+/* The exact-decode reference kernel: every weight decoded as kdq_dequantize does and
+ * multiplied into an fp32 fused multiply-add chain, one wavefront per output.  Any
+ * in % 32 == 0.  Slower; kept as the cross-check and for shapes kdq_gemv rejects. */
+int kdq_gemv_exact(int encoding, const void* weights, size_t row_bytes, const float* x,
+                   size_t rows, size_t in, size_t out, float* y, size_t stride,
+                   unsigned* status, void* stream);
+
+/* One job of a decode submission: the fields of MatvecJob (IW/src/cuda/h3_compute.cu:110-121)
+ * that a caller sets.  All pointers are device pointers. */
+typedef struct kdq_matvec_job {
+    const void* weights;  /* `columns` packed rows */
+    const float* input;   /* rows x in */
+    float* output;        /* output[r*stride + c] */
+    unsigned* status;     /* optional nonfinite flag */
+    size_t row_bytes, stride;
+    uint32_t in, columns, rows;
+    int32_t encoding;
+} kdq_matvec_job;
+
+/* Every job in one submission (replaces launch_matvec(vector<MatvecJob>&, table),
+ * IW/src/cuda/h3_compute.cu:367-382, as used by dense_gguf_batch :3963-4375).
+ * `jobs` is a HOST array; jobs that share an input pointer stage it once per pass. */
+int kdq_gemv_batch(const kdq_matvec_job* jobs, size_t count, void* stream);
+
+/* ---- prefill Q4_0 GEMM (no reference device counterpart; the reference decodes to
+ * F32 and calls cublasSgemm, IW/src/cuda/h3_compute.cu:2451, and its CPU path runs
+ * ggml vec_dot_q4_0_q8_0, G/src/ggml-cpu/quants.c:225-260).
+ * Activations: fp16 [m x k] quantized per 32 to int8 with an fp32 scale
+ * (amax/127, codes round-half-even(x*127/amax), G/src/ggml-cpu/arch/x86/quants.c:302-398).
+ * y[m x n] fp16 = sum_b float(sumi_b) * d_w * d_x, fp32 accumulation.
+ * k % 256 == 0; any m, n >= 1. */
+int kdq_gemm_q4_0(const void* weights, size_t n, size_t k, const uint16_t* x_f16, size_t m,
+                  uint16_t* y_f16, void* stream);
+
+/* The activation quantizer of kdq_gemm_q4_0 on its own (for bit-exact checks):
+ * q int8 [m x k], d fp32 [m x k/32]. */
+int kdq_quantize_q8(const uint16_t* x_f16, size_t m, size_t k, int8_t* q, float* d,
+                    void* stream);
+
+/* ---- MXFP4 mixture-of-experts layer (the reference has no device MoE; this composes
+ * MoeLayer::forward, IW/src/models/text/qwen_layers.cpp:378-492, with the MXFP4
+ * product semantics of IW/src/weights/quantization.cpp:79-99,207-247).
+ * Weights in the GPT-OSS layout (IW/include/kadan/checkpoint.hpp:151-163):
+ *   gate/up blocks u8 [experts, inter, hidden/2], scales u8 [experts, inter, hidden/32]
+ *   down    blocks u8 [experts, hidden, inter/2], scales u8 [experts, hidden, inter/32]
+ * element 2i = low nibble of byte i; w = e2m1(code) * 2^(scale-127). */
+
+/* Router + top-k + permutation, IW/src/models/text/qwen_layers.cpp:403-451.
+ * logits fp32 [tokens x experts]; top_k <= 8; experts <= 256.
+ * idx int32 [tokens x top_k] (selection order: probability descending, equal values
+ * keep the lower expert), w fp32 [tokens x top_k] renormalised weights,
+ * offsets int32 [experts + 1], perm int32 [tokens*top_k] = slots (token*top_k + i)
+ * grouped by expert ascending, slot ascending within an expert. */
+int kdq_moe_route(const float* logits, size_t tokens, size_t experts, size_t top_k,
+                  int32_t* idx, float* w, int32_t* offsets, int32_t* perm, void* stream);
+
+/* Decodes MXFP4 rows to fp32 exactly (IW/src/weights/quantization.cpp:193-205):
+ * blocks [rows x cols/2], scales [rows x cols/32] -> out [rows x cols].
+ * *status |= 1 for a scale byte of 255, |= 2 for a value that overflows fp32. */
+int kdq_mxfp4_dequantize(const uint8_t* blocks, const uint8_t* scales, size_t rows,
+                         size_t cols, float* out, unsigned* status, void* stream);
+
+/* The whole layer: y fp32 [tokens x hidden] from x bf16 [tokens x hidden] and logits.
+ * Also returns the routing (idx, w, offsets, perm as kdq_moe_route) when those
+ * pointers are non-null.  hidden % 64 == 0, inter % 64 == 0. */
+int kdq_moe_mxfp4(const uint16_t* x_bf16, const float* logits, size_t tokens, size_t hidden,
+                  size_t inter, size_t experts, size_t top_k,
+                  const uint8_t* gate_blocks, const uint8_t* gate_scales,
+                  const uint8_t* up_blocks, const uint8_t* up_scales,
+                  const uint8_t* down_blocks, const uint8_t* down_scales,
+                  float* y, int32_t* idx, float* w, int32_t* offsets, int32_t* perm,
+                  void* stream);
+
+/* Frees this thread's current device's cached workspace (synchronizes the device).
+ * IW/include/kadan/dense_compute.hpp:66-68 release_scratch counterpart. */
+int kdq_release_scratch(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,112 @@
+"""kadan_amd: MI355X (gfx950) quantized-weight matmul path.
+
+Python access to the C ABI of include/kadan_amd.h (libkadan_amd.so, built in-tree by
+``kadan_amd.build``).  torch provides device memory and streams only; every
+computation runs in the HIP kernels of kadan_amd/csrc.  There is no CPU fallback:
+if the library is missing, ``lib()`` raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+PACKAGE = os.path.dirname(os.path.abspath(__file__))
+LIBRARY = os.path.join(PACKAGE, "libkadan_amd.so")
+HOST_LIBRARY = os.path.join(PACKAGE, "libkadan_amd_host.so")
+
+Q4_0, Q8_0, Q4_K = 2, 8, 12
+BLOCK_VALUES = {Q4_0: 32, Q8_0: 32, Q4_K: 256}
+BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144}
+
+STATUS = {0: "ok", 1: "kdq_argument", 2: "kdq_projection_shape", 3: "kdq_unsupported",
+          4: "kdq_alias", 5: "kdq_hip", 6: "kdq_projection_scratch", 7: "kdq_alignment"}
+
+
+class KdqError(RuntimeError):
+    def __init__(self, function: str, status: int, hip: str = ""):
+        self.status = status
+        text = STATUS.get(status, f"status {status}")
+        super().__init__(f"{function}: {text}" + (f" ({hip})" if hip else ""))
+
+
+class KdqUnsupported(KdqError):
+    pass
+
+
+# (name, argtypes); every entry point returns int
+_SZ, _VP, _I = C.c_size_t, C.c_void_p, C.c_int
+_SIGNATURES = {
+    "kdq_dequantize": [_I, _VP, _SZ, _SZ, _SZ, _VP, _VP, _VP],
+    "kdq_gemv": [_I, _VP, _SZ, _VP, _SZ, _SZ, _SZ, _VP, _SZ, _VP, _VP],
+    "kdq_gemv_exact": [_I, _VP, _SZ, _VP, _SZ, _SZ, _SZ, _VP, _SZ, _VP, _VP],
+    "kdq_gemv_batch": [_VP, _SZ, _VP],
+    "kdq_gemm_q4_0": [_VP, _SZ, _SZ, _VP, _SZ, _VP, _VP],
+    "kdq_quantize_q8": [_VP, _SZ, _SZ, _VP, _VP, _VP],
+    "kdq_moe_route": [_VP, _SZ, _SZ, _SZ, _VP, _VP, _VP, _VP, _VP],
+    "kdq_mxfp4_dequantize": [_VP, _VP, _SZ, _SZ, _VP, _VP, _VP],
+    "kdq_moe_mxfp4": [_VP, _VP, _SZ, _SZ, _SZ, _SZ, _SZ, _VP, _VP, _VP, _VP, _VP, _VP,
+                      _VP, _VP, _VP, _VP, _VP, _VP],
+    "kdq_release_scratch": [],
+}
+_OTHER = {
+    "kdq_status_string": (C.c_char_p, [_I]),
+    "kdq_last_hip_error": (C.c_char_p, []),
+    "kdq_block_values": (_SZ, [_I]),
+    "kdq_block_bytes": (_SZ, [_I]),
+    "kdq_row_bytes": (_SZ, [_I, _SZ]),
+}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """The loaded product library.  Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIBRARY):
+            raise RuntimeError(
+                f"{LIBRARY} is missing: build it with `python -m kadan_amd.build` "
+                "(there is no CPU fallback)")
+        handle = C.CDLL(LIBRARY)
+        for name, args in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = C.c_int
+            fn.argtypes = args
+        for name, (res, args) in _OTHER.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def exported_symbols() -> list[str]:
+    return list(_SIGNATURES) + list(_OTHER)
+
+
+class MatvecJob(C.Structure):
+    """kdq_matvec_job of include/kadan_amd.h."""
+    _fields_ = [("weights", C.c_void_p), ("input", C.c_void_p), ("output", C.c_void_p),
+                ("status", C.c_void_p), ("row_bytes", C.c_size_t), ("stride", C.c_size_t),
+                ("in_", C.c_uint32), ("columns", C.c_uint32), ("rows", C.c_uint32),
+                ("encoding", C.c_int32)]
+
+
+def check(function: str, status: int) -> None:
+    if status == 0:
+        return
+    hip = lib().kdq_last_hip_error().decode() if status == 5 else ""
+    if status == 3:
+        raise KdqUnsupported(function, status, hip)
+    raise KdqError(function, status, hip)
+
+
+def call(function: str, *args) -> None:
+    check(function, getattr(lib(), function)(*args))
+
+
+def row_bytes(encoding: int, n_in: int) -> int:
+    return int(lib().kdq_row_bytes(encoding, n_in))
+
+
+from . import ops  # noqa: E402,F401  (torch-facing wrappers)

@@ -1,0 +1,700 @@
+// GGUF block-quantized decode and decode-time products (Q8_0, Q4_0, Q4_K) for
+// gfx950.  Replaces the reference's gguf_decode_kernel and gguf_matvec_kernel
+// (IW/src/cuda/h3_compute.cu:76-95,165-240; IW = services/hikari/inference_worker)
+// behind the C ABI of include/kadan_amd.h.
+//
+// Kernels:
+//   decode_kernel   exact decode of packed rows to fp32 (one thread per run of 8)
+//   exact_gemv      exactly decoded weights x fp32 inputs, fp32 FMA chain, one
+//                   wavefront per output (the reference semantics, wave64)
+//   fast_gemv       HBM-streaming product: 1024-thread workgroups stage the
+//                   activation rows in LDS as 16-bit block fixed point (two int8
+//                   planes per 32 values), every lane owns 64 consecutive weights of
+//                   a row (one Q4_K sub-block pair, or two Q8_0/Q4_0 blocks), loads
+//                   them with 16-byte loads, multiplies with v_dot4_i32_i8 and
+//                   applies the per-32 weight and activation scales in fp32.
+#include "kdq_common.hpp"
+
+#include <algorithm>
+#include <cmath>
+
+namespace kdq {
+namespace {
+
+// ------------------------------------------------------------------ decode
+
+template <int ENC> struct Format;
+template <> struct Format<KDQ_Q8_0> {
+    static constexpr int values = 32, bytes = 34;
+};
+template <> struct Format<KDQ_Q4_0> {
+    static constexpr int values = 32, bytes = 18;
+};
+template <> struct Format<KDQ_Q4_K> {
+    static constexpr int values = 256, bytes = 144;
+};
+
+__device__ __forceinline__ unsigned half_bits_at(const uint8_t* p) {
+    return unsigned(p[0]) | (unsigned(p[1]) << 8);
+}
+
+// Q4_K sub-block g: 6-bit scale and min from the 12 packed bytes at `s`.
+__device__ __forceinline__ void q4k_scale_min(const uint8_t* s, unsigned g, unsigned& sc,
+                                              unsigned& m) {
+    if (g < 4) {
+        sc = s[g] & 63u;
+        m = s[g + 4] & 63u;
+    } else {
+        sc = (s[g + 4] & 15u) | ((unsigned(s[g - 4]) >> 6) << 4);
+        m = (unsigned(s[g + 4]) >> 4) | ((unsigned(s[g]) >> 6) << 4);
+    }
+}
+
+// Eight values from element `within` (a multiple of 8) of one block, each equal to
+// the reference's single-value decode.
+template <int ENC>
+__device__ __forceinline__ void decode_run(const uint8_t* block, unsigned within, float* v) {
+    const float d = half_exact(half_bits_at(block));
+    if constexpr (ENC == KDQ_Q8_0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            v[i] = mul_rn(d, float(int8_t(block[2 + within + i])));
+    } else if constexpr (ENC == KDQ_Q4_0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const unsigned e = within + i;
+            const unsigned byte = block[2 + (e & 15u)];
+            const int code = int(e < 16 ? (byte & 15u) : (byte >> 4)) - 8;
+            v[i] = mul_rn(float(code), d);
+        }
+    } else {
+        const float dmin = half_exact(half_bits_at(block + 2));
+        const unsigned g = within / 32;
+        unsigned sc, m;
+        q4k_scale_min(block + 4, g, sc, m);
+        const float scaled = mul_rn(d, float(sc));
+        const float offset = mul_rn(dmin, float(m));
+        const uint8_t* codes = block + 16 + (within / 64) * 32 + (within % 32);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const unsigned code = (g & 1u) ? (codes[i] >> 4) : (codes[i] & 15u);
+            v[i] = sub_rn(mul_rn(scaled, float(code)), offset);
+        }
+    }
+}
+
+template <int ENC>
+__global__ __launch_bounds__(256) void decode_kernel(const uint8_t* packed, size_t row_bytes,
+                                                     size_t rows, size_t in, float* out,
+                                                     unsigned* status) {
+    using F = Format<ENC>;
+    const size_t runs = in / 8;
+    const size_t t = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    bool bad = false;
+    if (t < rows * runs) {
+        const size_t row = t / runs, e0 = (t % runs) * 8;
+        float v[8];
+        decode_run<ENC>(packed + row * row_bytes + (e0 / F::values) * F::bytes,
+                        unsigned(e0 % F::values), v);
+        float4* o = reinterpret_cast<float4*>(out + row * in + e0);
+        o[0] = make_float4(v[0], v[1], v[2], v[3]);
+        o[1] = make_float4(v[4], v[5], v[6], v[7]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            bad |= !isfinite(v[i]);
+    }
+    if (status && __any(bad) && (threadIdx.x % 64) == 0)
+        atomicOr(status, 1u);
+}
+
+// ------------------------------------------------------------- exact GEMV
+
+template <int ENC, int ROWS>
+__global__ __launch_bounds__(256) void exact_gemv(const uint8_t* weights, size_t row_bytes,
+                                                  const float* x, unsigned rows, unsigned in,
+                                                  unsigned out, float* y, size_t stride,
+                                                  unsigned* status) {
+    using F = Format<ENC>;
+    const unsigned column = blockIdx.x * 4 + threadIdx.x / 64;
+    const unsigned lane = threadIdx.x % 64;
+    if (column >= out)
+        return;
+    const uint8_t* row = weights + size_t(column) * row_bytes;
+    float sums[ROWS] = {};
+    bool finite = true;
+    for (unsigned i = lane * 8; i < in; i += 64 * 8) {
+        float w[8];
+        decode_run<ENC>(row + size_t(i / F::values) * F::bytes, i % F::values, w);
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            finite = finite && isfinite(w[k]);
+#pragma unroll
+        for (unsigned r = 0; r < ROWS; ++r)
+            if (ROWS == 1 || r < rows) {
+                const float* xr = x + size_t(r) * in + i;
+                float s = sums[r];
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    s = fmaf(w[k], xr[k], s);
+                sums[r] = s;
+            }
+    }
+    if (status && __any(!finite) && lane == 0)
+        atomicOr(status, 1u);
+#pragma unroll
+    for (unsigned r = 0; r < ROWS; ++r) {
+        if (ROWS > 1 && r >= rows)
+            break;
+        const float s = wave_sum(sums[r]);
+        if (lane == 0)
+            y[size_t(r) * stride + column] = s;
+    }
+}
+
+// -------------------------------------------------------------- fast GEMV
+
+constexpr int kThreads = 1024, kWaves = 16;
+constexpr int kSlot = 64;         // weights per lane per row step
+constexpr int kWindow = 64 * kSlot;  // weights per wavefront per row step
+
+// LDS byte offset, inside one 128-byte slot, of the (hi, lo) dword pair holding the
+// four activation values that start at position p (p % 4 == 0) of the slot.  The
+// pairing follows how each format's packed dwords expand: pair m holds values A
+// (read against the low nibbles / first dword) and B (high nibbles / second dword).
+template <int ENC> __device__ __forceinline__ unsigned pair_offset(unsigned p) {
+    unsigned m, which;
+    if constexpr (ENC == KDQ_Q4_K) {  // sub-block pair: A = first 32, B = second 32
+        which = p >= 32;
+        m = (p % 32) / 4;
+    } else if constexpr (ENC == KDQ_Q4_0) {  // per block: A = values 0..15, B = 16..31
+        const unsigned q = p % 32;
+        which = q >= 16;
+        m = (p / 32) * 4 + (q % 16) / 4;
+    } else {  // Q8_0: A, B = consecutive dwords of codes
+        m = p / 8;
+        which = (p / 4) % 2;
+    }
+    return m * 16 + which * 8;
+}
+
+// Quantizes R activation rows into LDS:
+//   xq[(r*slots + slot)*128 + ...]  hi/lo int8 planes in pair order
+//   xs[r*slots + slot] = (s0, sum0, s1, sum1) for the slot's two 32-value groups
+// x_q = round(x * 32639 / amax) split as x_q = 256*hi + lo, hi, lo in int8.
+template <int ENC, int R>
+__device__ void stage_activations(const float* __restrict__ x, unsigned in, uint8_t* xq,
+                                  float* xs) {
+    const unsigned slots = in / kSlot;
+    const unsigned units = R * in / 8;
+    for (unsigned u = threadIdx.x; u < units; u += kThreads) {
+        const unsigned r = u / (in / 8), e = (u % (in / 8)) * 8;
+        const float4* src = reinterpret_cast<const float4*>(x + size_t(r) * in + e);
+        const float4 a = src[0], b = src[1];
+        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        float amax = 0.f, sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            amax = fmaxf(amax, fabsf(v[i]));
+            sum += v[i];
+        }
+        bool finite = true;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            finite = finite && isfinite(v[i]);
+        // four consecutive threads hold one 32-value group
+        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        finite = __shfl_xor(int(finite), 1, 64) && finite;
+        finite = __shfl_xor(int(finite), 2, 64) && finite;
+        const float inv = amax > 0.f ? 32639.0f / amax : 0.f;
+        const float scale = finite ? amax / 32639.0f : __builtin_nanf("");
+        unsigned hi[2] = {0, 0}, lo[2] = {0, 0};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            int q = __float2int_rn(v[i] * inv);
+            q = min(32639, max(-32639, q));
+            const int h = (q + 128) >> 8;
+            const int l = q - h * 256;
+            hi[i / 4] |= (unsigned(h) & 255u) << (8 * (i % 4));
+            lo[i / 4] |= (unsigned(l) & 255u) << (8 * (i % 4));
+        }
+        const unsigned slot = e / kSlot, p = e % kSlot;
+        uint8_t* base = xq + (size_t(r) * slots + slot) * 128;
+        *reinterpret_cast<uint2*>(base + pair_offset<ENC>(p)) = make_uint2(hi[0], lo[0]);
+        *reinterpret_cast<uint2*>(base + pair_offset<ENC>(p + 4)) = make_uint2(hi[1], lo[1]);
+        if ((u & 3u) == 0)
+            *reinterpret_cast<float2*>(xs + (size_t(r) * slots + slot) * 4 + (p / 32) * 2) =
+                make_float2(scale, sum);
+    }
+}
+
+// Packed weights of one lane for one row step.
+struct Lane {
+    unsigned w[17];
+};
+
+template <int ENC>
+__device__ __forceinline__ void load_lane(const uint8_t* row, unsigned slot, Lane& L) {
+    if constexpr (ENC == KDQ_Q4_K) {
+        const uint8_t* block = row + size_t(slot / 4) * 144;
+        const unsigned pair = slot % 4;
+        const u32x4 h = load16(block);
+        const u32x4 q0 = load16(block + 16 + 32 * pair);
+        const u32x4 q1 = load16(block + 32 + 32 * pair);
+        L.w[0] = h.x, L.w[1] = h.y, L.w[2] = h.z, L.w[3] = h.w;
+        L.w[4] = q0.x, L.w[5] = q0.y, L.w[6] = q0.z, L.w[7] = q0.w;
+        L.w[8] = q1.x, L.w[9] = q1.y, L.w[10] = q1.z, L.w[11] = q1.w;
+    } else if constexpr (ENC == KDQ_Q4_0) {
+        const uint8_t* p = row + size_t(slot) * 36;
+        const u32x4 a = load16(p), b = load16(p + 16);
+        L.w[0] = a.x, L.w[1] = a.y, L.w[2] = a.z, L.w[3] = a.w;
+        L.w[4] = b.x, L.w[5] = b.y, L.w[6] = b.z, L.w[7] = b.w;
+        L.w[8] = load4(p + 32);
+    } else {
+        const uint8_t* p = row + size_t(slot) * 68;
+        const u32x4 a = load16(p), b = load16(p + 16), c = load16(p + 32), d = load16(p + 48);
+        L.w[0] = a.x, L.w[1] = a.y, L.w[2] = a.z, L.w[3] = a.w;
+        L.w[4] = b.x, L.w[5] = b.y, L.w[6] = b.z, L.w[7] = b.w;
+        L.w[8] = c.x, L.w[9] = c.y, L.w[10] = c.z, L.w[11] = c.w;
+        L.w[12] = d.x, L.w[13] = d.y, L.w[14] = d.z, L.w[15] = d.w;
+        L.w[16] = load4(p + 64);
+    }
+}
+
+struct XSlot {
+    u32x4 q[8];
+    float4 s;
+};
+
+__device__ __forceinline__ void load_x(const uint8_t* xq, const float* xs, size_t index,
+                                       XSlot& X) {
+    const u32x4* q = reinterpret_cast<const u32x4*>(xq + index * 128);
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+        X.q[m] = q[m];
+    X.s = reinterpret_cast<const float4*>(xs)[index];
+}
+
+// Contribution of one lane's 64 weights against one activation slot; sets `bad`
+// when a block scale is not finite (then some decoded weight is not finite).
+template <int ENC>
+__device__ __forceinline__ float lane_dot(const Lane& L, unsigned slot, const XSlot& X,
+                                          bool& bad) {
+    if constexpr (ENC == KDQ_Q4_K) {
+        const float d = half_hw(L.w[0] & 0xffffu), dmin = half_hw(L.w[0] >> 16);
+        bad |= !isfinite(d) || !isfinite(dmin);
+        // sub-blocks ga = 2*pair and gb = 2*pair + 1 of the block
+        const unsigned pair = slot % 4;
+        const unsigned shift = 8 * ((2 * pair) & 3);
+        const unsigned b1 = L.w[1] >> shift, b2 = L.w[2] >> shift, b3 = L.w[3] >> shift;
+        unsigned sca, ma, scb, mb;
+        if (pair < 2) {
+            sca = b1 & 63u, ma = b2 & 63u;
+            scb = (b1 >> 8) & 63u, mb = (b2 >> 8) & 63u;
+        } else {
+            sca = (b3 & 15u) | ((b1 >> 2) & 48u);
+            ma = ((b3 >> 4) & 15u) | ((b2 >> 2) & 48u);
+            scb = ((b3 >> 8) & 15u) | ((b1 >> 10) & 48u);
+            mb = ((b3 >> 12) & 15u) | ((b2 >> 10) & 48u);
+        }
+        int ah = 0, al = 0, bh = 0, bl = 0;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            const unsigned q = L.w[4 + m];
+            const unsigned lo4 = q & 0x0f0f0f0fu, hi4 = (q >> 4) & 0x0f0f0f0fu;
+            ah = sdot4(lo4, X.q[m].x, ah);
+            al = sdot4(lo4, X.q[m].y, al);
+            bh = sdot4(hi4, X.q[m].z, bh);
+            bl = sdot4(hi4, X.q[m].w, bl);
+        }
+        const float A = float(ah * 256 + al), B = float(bh * 256 + bl);
+        const float fa = d * float(sca), fb = d * float(scb);
+        const float oa = dmin * float(ma), ob = dmin * float(mb);
+        float acc = fa * (X.s.x * A);
+        acc = fmaf(fb, X.s.z * B, acc);
+        acc = fmaf(-oa, X.s.y, acc);
+        return fmaf(-ob, X.s.w, acc);
+    } else if constexpr (ENC == KDQ_Q4_0) {
+        const float d0 = half_hw(L.w[0] & 0xffffu), d1 = half_hw(L.w[4] >> 16);
+        bad |= !isfinite(d0) || !isfinite(d1);
+        int h0 = 0, l0 = 0, h1 = 0, l1 = 0;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {  // block 0 codes start 2 bytes into dword 0
+            const unsigned q = __builtin_amdgcn_alignbyte(L.w[m + 1], L.w[m], 2);
+            const unsigned lo4 = q & 0x0f0f0f0fu, hi4 = (q >> 4) & 0x0f0f0f0fu;
+            h0 = sdot4(lo4, X.q[m].x, h0);
+            l0 = sdot4(lo4, X.q[m].y, l0);
+            h0 = sdot4(hi4, X.q[m].z, h0);
+            l0 = sdot4(hi4, X.q[m].w, l0);
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {  // block 1 codes are dword aligned
+            const unsigned q = L.w[5 + m];
+            const unsigned lo4 = q & 0x0f0f0f0fu, hi4 = (q >> 4) & 0x0f0f0f0fu;
+            h1 = sdot4(lo4, X.q[4 + m].x, h1);
+            l1 = sdot4(lo4, X.q[4 + m].y, l1);
+            h1 = sdot4(hi4, X.q[4 + m].z, h1);
+            l1 = sdot4(hi4, X.q[4 + m].w, l1);
+        }
+        // sum (q - 8) x = s * sum q x_q - 8 * sum x
+        const float t0 = fmaf(X.s.x, float(h0 * 256 + l0), -8.f * X.s.y);
+        const float t1 = fmaf(X.s.z, float(h1 * 256 + l1), -8.f * X.s.w);
+        return fmaf(d1, t1, d0 * t0);
+    } else {
+        const float d0 = half_hw(L.w[0] & 0xffffu), d1 = half_hw(L.w[8] >> 16);
+        bad |= !isfinite(d0) || !isfinite(d1);
+        int h0 = 0, l0 = 0, h1 = 0, l1 = 0;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {  // block 0 codes start 2 bytes into dword 0
+            const unsigned a = __builtin_amdgcn_alignbyte(L.w[2 * m + 1], L.w[2 * m], 2);
+            const unsigned b = __builtin_amdgcn_alignbyte(L.w[2 * m + 2], L.w[2 * m + 1], 2);
+            h0 = sdot4(a, X.q[m].x, h0);
+            l0 = sdot4(a, X.q[m].y, l0);
+            h0 = sdot4(b, X.q[m].z, h0);
+            l0 = sdot4(b, X.q[m].w, l0);
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {  // block 1 codes are dwords 9..16
+            const unsigned a = L.w[9 + 2 * m], b = L.w[10 + 2 * m];
+            h1 = sdot4(a, X.q[4 + m].x, h1);
+            l1 = sdot4(a, X.q[4 + m].y, l1);
+            h1 = sdot4(b, X.q[4 + m].z, h1);
+            l1 = sdot4(b, X.q[4 + m].w, l1);
+        }
+        return fmaf(d1 * X.s.z, float(h1 * 256 + l1), d0 * X.s.x * float(h0 * 256 + l0));
+    }
+}
+
+// Rows whose packed weights are loaded before any of them is reduced.
+template <int R> constexpr int rows_in_flight = R == 1 ? 4 : 2;
+
+// Workgroup: 16 wavefronts.  The row is cut into `nw` windows of 4096 values (nw
+// divides 16); wavefront w takes window w % nw of the rows r0 + w/nw, r0 + w/nw +
+// 16/nw, ...  in [r0, r0 + rows_per_wg).  With nw > 1 the window partials meet in LDS
+// and are summed in window order.
+template <int ENC, int R>
+__global__ __launch_bounds__(kThreads) void fast_gemv(const uint8_t* __restrict__ weights,
+                                                      size_t row_bytes,
+                                                      const float* __restrict__ x, unsigned in,
+                                                      unsigned out, float* __restrict__ y,
+                                                      size_t stride, unsigned* status,
+                                                      unsigned rows_per_wg, unsigned nw) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const unsigned slots = in / kSlot;
+    uint8_t* xq = lds;
+    float* xs = reinterpret_cast<float*>(lds + size_t(R) * slots * 128);
+    float* partial = xs + size_t(R) * slots * 4;
+
+    stage_activations<ENC, R>(x, in, xq, xs);
+    __syncthreads();
+
+    const unsigned wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const unsigned window = wave % nw, groups = kWaves / nw, group = wave / nw;
+    const unsigned slot = window * 64 + lane;
+    const bool active = slot < slots;
+    const unsigned r0 = blockIdx.x * rows_per_wg;
+    const unsigned r1 = min(out, r0 + rows_per_wg);
+    bool bad = false;
+
+    XSlot X[1];  // single-row passes keep the activation slot in registers
+    if constexpr (R == 1) {
+        if (active)
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                load_x(xq, xs, size_t(r) * slots + slot, X[r]);
+    }
+
+    constexpr int kRowsInFlight = rows_in_flight<R>;
+    for (unsigned base = r0 + group; base < r1; base += kRowsInFlight * groups) {
+        Lane L[kRowsInFlight];
+#pragma unroll
+        for (int u = 0; u < kRowsInFlight; ++u) {
+            const unsigned n = base + u * groups;
+            if (active && n < r1)
+                load_lane<ENC>(weights + size_t(n) * row_bytes, slot, L[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < kRowsInFlight; ++u) {
+            const unsigned n = base + u * groups;
+            if (n >= r1)
+                break;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float v = 0.f;
+                if (active) {
+                    if constexpr (R == 1) {
+                        v = lane_dot<ENC>(L[u], slot, X[0], bad);
+                    } else {
+                        XSlot Xr;
+                        load_x(xq, xs, size_t(r) * slots + slot, Xr);
+                        v = lane_dot<ENC>(L[u], slot, Xr, bad);
+                    }
+                }
+                v = wave_sum(v);
+                if (lane == 0) {
+                    if (nw == 1)
+                        y[size_t(r) * stride + n] = v;
+                    else
+                        partial[(size_t(n - r0) * R + r) * nw + window] = v;
+                }
+            }
+        }
+    }
+    if (status && __any(bad) && lane == 0)
+        atomicOr(status, 1u);
+    if (nw > 1) {
+        __syncthreads();
+        const unsigned count = (r1 > r0 ? r1 - r0 : 0) * R;
+        for (unsigned t = threadIdx.x; t < count; t += kThreads) {
+            float s = 0.f;
+            for (unsigned w = 0; w < nw; ++w)
+                s += partial[size_t(t) * nw + w];
+            const unsigned n = r0 + t / R, r = t % R;
+            y[size_t(r) * stride + n] = s;
+        }
+    }
+}
+
+// ----------------------------------------------------------------- host side
+
+template <int ENC>
+int launch_decode(const void* packed, size_t row_bytes, size_t rows, size_t in, float* out,
+                  unsigned* status, hipStream_t stream) {
+    const size_t threads = rows * (in / 8);
+    const size_t grid = (threads + 255) / 256;
+    if (grid > 0x7fffffffu)
+        return KDQ_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL((decode_kernel<ENC>), dim3(unsigned(grid)), dim3(256), 0, stream,
+                       static_cast<const uint8_t*>(packed), row_bytes, rows, in, out, status);
+    KDQ_HIP(hipGetLastError());
+    return KDQ_OK;
+}
+
+template <int ENC>
+int launch_exact(const void* w, size_t row_bytes, const float* x, size_t rows, size_t in,
+                 size_t out, float* y, size_t stride, unsigned* status, hipStream_t stream) {
+    const unsigned grid = unsigned((out + 3) / 4);
+    for (size_t first = 0; first < rows; first += 8) {
+        const unsigned group = unsigned(std::min<size_t>(8, rows - first));
+        if (group == 1)
+            hipLaunchKernelGGL((exact_gemv<ENC, 1>), dim3(grid), dim3(256), 0, stream,
+                               static_cast<const uint8_t*>(w), row_bytes, x + first * in, 1u,
+                               unsigned(in), unsigned(out), y + first * stride, stride, status);
+        else
+            hipLaunchKernelGGL((exact_gemv<ENC, 8>), dim3(grid), dim3(256), 0, stream,
+                               static_cast<const uint8_t*>(w), row_bytes, x + first * in, group,
+                               unsigned(in), unsigned(out), y + first * stride, stride, status);
+        KDQ_HIP(hipGetLastError());
+    }
+    return KDQ_OK;
+}
+
+struct FastPlan {
+    unsigned nw, rows_per_wg, grid, batch;
+    size_t lds;
+};
+
+// Window count (power of two dividing 16), rows per workgroup, batch rows per pass.
+bool plan_fast(size_t rows, size_t in, size_t out, FastPlan& p) {
+    const size_t windows = (in + kWindow - 1) / kWindow;
+    unsigned nw = 1;
+    while (nw < windows)
+        nw *= 2;
+    if (nw > 16)
+        return false;
+    const unsigned groups = kWaves / nw;
+    // batch rows per pass: the staged activations (2.25 bytes per value) must fit
+    unsigned batch = 1;
+    while (batch < 8 && batch < rows && size_t(batch * 2) * in * 9 / 4 <= 96 * 1024)
+        batch *= 2;
+    // about two rows per wavefront group, and at most ~512 workgroups
+    size_t rows_per_wg = std::max<size_t>(size_t(groups) * 2, (out + 511) / 512);
+    rows_per_wg = (rows_per_wg + groups - 1) / groups * groups;
+    p.nw = nw;
+    p.batch = batch;
+    p.rows_per_wg = unsigned(rows_per_wg);
+    p.grid = unsigned((out + rows_per_wg - 1) / rows_per_wg);
+    p.lds = size_t(batch) * (in / kSlot) * 144 + (nw > 1 ? rows_per_wg * batch * nw * 4 : 0);
+    return p.lds <= 160 * 1024;
+}
+
+template <int ENC, int R>
+int launch_fast_pass(const FastPlan& p, const void* w, size_t row_bytes, const float* x,
+                     size_t in, size_t out, float* y, size_t stride, unsigned* status,
+                     hipStream_t stream) {
+    static bool configured = false;  // one attribute call per instantiation
+    if (!configured) {
+        KDQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&fast_gemv<ENC, R>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+        configured = true;
+    }
+    hipLaunchKernelGGL((fast_gemv<ENC, R>), dim3(p.grid), dim3(kThreads), p.lds, stream,
+                       static_cast<const uint8_t*>(w), row_bytes, x, unsigned(in),
+                       unsigned(out), y, stride, status, p.rows_per_wg, p.nw);
+    KDQ_HIP(hipGetLastError());
+    return KDQ_OK;
+}
+
+template <int ENC>
+int launch_fast(const void* w, size_t row_bytes, const float* x, size_t rows, size_t in,
+                size_t out, float* y, size_t stride, unsigned* status, hipStream_t stream) {
+    FastPlan p;
+    if (!plan_fast(rows, in, out, p))
+        return KDQ_ERR_UNSUPPORTED;
+    for (size_t first = 0; first < rows;) {
+        const size_t left = rows - first;
+        unsigned r = p.batch;
+        while (r > left)
+            r /= 2;
+        FastPlan q = p;
+        q.lds = size_t(r) * (in / kSlot) * 144 + (p.nw > 1 ? size_t(p.rows_per_wg) * r * p.nw * 4 : 0);
+        int rc;
+        const float* xs = x + first * in;
+        float* ys = y + first * stride;
+        switch (r) {
+        case 1:
+            rc = launch_fast_pass<ENC, 1>(q, w, row_bytes, xs, in, out, ys, stride, status, stream);
+            break;
+        case 2:
+            rc = launch_fast_pass<ENC, 2>(q, w, row_bytes, xs, in, out, ys, stride, status, stream);
+            break;
+        case 4:
+            rc = launch_fast_pass<ENC, 4>(q, w, row_bytes, xs, in, out, ys, stride, status, stream);
+            break;
+        default:
+            rc = launch_fast_pass<ENC, 8>(q, w, row_bytes, xs, in, out, ys, stride, status, stream);
+            break;
+        }
+        if (rc)
+            return rc;
+        first += r;
+    }
+    return KDQ_OK;
+}
+
+bool aligned(const void* p, size_t a) {
+    return (reinterpret_cast<uintptr_t>(p) % a) == 0;
+}
+
+// Shared argument checks of the product entry points.
+int check_product(int encoding, const void* weights, size_t row_bytes, const float* x,
+                  size_t rows, size_t in, size_t out, const float* y, size_t stride) {
+    const size_t values = block_values(encoding);
+    if (!values)
+        return KDQ_ERR_UNSUPPORTED;
+    if (!weights || !x || !y || !rows || !in || !out)
+        return KDQ_ERR_ARGUMENT;
+    if (in % values || in % 8 || row_bytes < in / values * block_bytes(encoding) ||
+        stride < out || rows > 4096 || in > 0xffffffffu || out > 0xffffffffu)
+        return KDQ_ERR_SHAPE;
+    if (mul_overflows(out, row_bytes) || mul_overflows(rows, in) || mul_overflows(rows, stride))
+        return KDQ_ERR_ARGUMENT;
+    const size_t ybytes = ((rows - 1) * stride + out) * sizeof(float);
+    if (overlaps(y, ybytes, weights, out * row_bytes) ||
+        overlaps(y, ybytes, x, rows * in * sizeof(float)))
+        return KDQ_ERR_ALIAS;
+    if (!aligned(x, 16))
+        return KDQ_ERR_ALIGNMENT;
+    return KDQ_OK;
+}
+
+}  // namespace
+}  // namespace kdq
+
+using namespace kdq;
+
+extern "C" int kdq_dequantize(int encoding, const void* packed, size_t row_bytes, size_t rows,
+                              size_t in, float* out, unsigned* status, void* stream) {
+    const size_t values = block_values(encoding);
+    if (!values)
+        return KDQ_ERR_UNSUPPORTED;
+    if (!packed || !out || !rows || !in)
+        return KDQ_ERR_ARGUMENT;
+    if (in % values || row_bytes < in / values * block_bytes(encoding))
+        return KDQ_ERR_SHAPE;
+    if (mul_overflows(rows, in) || mul_overflows(rows, row_bytes))
+        return KDQ_ERR_ARGUMENT;
+    if (!aligned(out, 16))
+        return KDQ_ERR_ALIGNMENT;
+    if (overlaps(out, rows * in * sizeof(float), packed, rows * row_bytes))
+        return KDQ_ERR_ALIAS;
+    auto s = static_cast<hipStream_t>(stream);
+    switch (encoding) {
+    case KDQ_Q8_0:
+        return launch_decode<KDQ_Q8_0>(packed, row_bytes, rows, in, out, status, s);
+    case KDQ_Q4_0:
+        return launch_decode<KDQ_Q4_0>(packed, row_bytes, rows, in, out, status, s);
+    default:
+        return launch_decode<KDQ_Q4_K>(packed, row_bytes, rows, in, out, status, s);
+    }
+}
+
+extern "C" int kdq_gemv_exact(int encoding, const void* weights, size_t row_bytes,
+                              const float* x, size_t rows, size_t in, size_t out, float* y,
+                              size_t stride, unsigned* status, void* stream) {
+    int rc = check_product(encoding, weights, row_bytes, x, rows, in, out, y, stride);
+    if (rc)
+        return rc;
+    auto s = static_cast<hipStream_t>(stream);
+    switch (encoding) {
+    case KDQ_Q8_0:
+        return launch_exact<KDQ_Q8_0>(weights, row_bytes, x, rows, in, out, y, stride, status, s);
+    case KDQ_Q4_0:
+        return launch_exact<KDQ_Q4_0>(weights, row_bytes, x, rows, in, out, y, stride, status, s);
+    default:
+        return launch_exact<KDQ_Q4_K>(weights, row_bytes, x, rows, in, out, y, stride, status, s);
+    }
+}
+
+extern "C" int kdq_gemv(int encoding, const void* weights, size_t row_bytes, const float* x,
+                        size_t rows, size_t in, size_t out, float* y, size_t stride,
+                        unsigned* status, void* stream) {
+    int rc = check_product(encoding, weights, row_bytes, x, rows, in, out, y, stride);
+    if (rc)
+        return rc;
+    auto s = static_cast<hipStream_t>(stream);
+    // The streaming kernel needs whole 64-value lane slots, 4-byte aligned rows and
+    // packed rows of exactly the format's size; anything else takes the exact kernel.
+    const bool fast = in % 256 == 0 && row_bytes % 4 == 0 && aligned(weights, 4) &&
+                      (encoding != KDQ_Q4_K || (row_bytes % 16 == 0 && aligned(weights, 16)));
+    if (fast) {
+        switch (encoding) {
+        case KDQ_Q8_0:
+            rc = launch_fast<KDQ_Q8_0>(weights, row_bytes, x, rows, in, out, y, stride, status, s);
+            break;
+        case KDQ_Q4_0:
+            rc = launch_fast<KDQ_Q4_0>(weights, row_bytes, x, rows, in, out, y, stride, status, s);
+            break;
+        default:
+            rc = launch_fast<KDQ_Q4_K>(weights, row_bytes, x, rows, in, out, y, stride, status, s);
+            break;
+        }
+        if (rc != KDQ_ERR_UNSUPPORTED)
+            return rc;
+    }
+    return kdq_gemv_exact(encoding, weights, row_bytes, x, rows, in, out, y, stride, status,
+                          stream);
+}
+
+extern "C" int kdq_gemv_batch(const kdq_matvec_job* jobs, size_t count, void* stream) {
+    if (count && !jobs)
+        return KDQ_ERR_ARGUMENT;
+    // Validate the whole submission before the first launch.
+    for (size_t i = 0; i < count; ++i) {
+        const auto& j = jobs[i];
+        const int rc = check_product(j.encoding, j.weights, j.row_bytes, j.input, j.rows, j.in,
+                                     j.columns, j.output, j.stride);
+        if (rc)
+            return rc;
+    }
+    for (size_t i = 0; i < count; ++i) {
+        const auto& j = jobs[i];
+        const int rc = kdq_gemv(j.encoding, j.weights, j.row_bytes, j.input, j.rows, j.in,
+                                j.columns, j.output, j.stride, j.status, stream);
+        if (rc)
+            return rc;
+    }
+    return KDQ_OK;
+}

@@ -1,0 +1,122 @@
+// Shared device/host helpers for the gfx950 kernels of the quantized matmul path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "kadan_amd.h"
+
+namespace kdq {
+
+// 16-byte load that only assumes 4-byte alignment (gfx950 global loads of four
+// dwords need dword alignment only; the compiler emits global_load_dwordx4).
+typedef unsigned u32x4 __attribute__((ext_vector_type(4), aligned(4)));
+
+__device__ __forceinline__ u32x4 load16(const uint8_t* p) {
+    return *reinterpret_cast<const u32x4*>(p);
+}
+
+__device__ __forceinline__ unsigned load4(const uint8_t* p) {
+    return *reinterpret_cast<const unsigned*>(p);
+}
+
+// Exact IEEE binary16 -> binary32 by integer construction (keeps NaN payloads),
+// IW/include/kadan/gguf_quantization.hpp:576-593 semantics.
+__device__ __forceinline__ float half_exact(unsigned h) {
+    const unsigned sign = (h & 0x8000u) << 16;
+    const unsigned e = (h >> 10) & 31u;
+    const unsigned m = h & 1023u;
+    if (e == 31u)
+        return __uint_as_float(sign | 0x7f800000u | (m << 13));
+    if (e == 0u)  // zero / subnormal: m * 2^-24 is exact
+        return __uint_as_float(sign | __float_as_uint(float(m) * 0x1p-24f));
+    return __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+// Hardware conversion (exact for every finite half; NaNs come out quiet).
+__device__ __forceinline__ float half_hw(unsigned h) {
+    return float(__builtin_bit_cast(_Float16, static_cast<unsigned short>(h)));
+}
+
+// Separately rounded fp32 operations (the decode must never be contracted into an
+// FMA: IW/include/kadan/gguf_quantization.hpp:595-621).
+__device__ __forceinline__ float mul_rn(float a, float b) {
+    return __fmul_rn(a, b);
+}
+__device__ __forceinline__ float sub_rn(float a, float b) {
+    return __fsub_rn(a, b);
+}
+
+__device__ __forceinline__ int sdot4(unsigned a, unsigned b, int c) {
+    return __builtin_amdgcn_sdot4(int(a), int(b), c, false);
+}
+
+// Sum across the 64 lanes of a wavefront (result valid in every lane).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1)
+        v += __shfl_xor(v, offset, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1)
+        v = fmaxf(v, __shfl_xor(v, offset, 64));
+    return v;
+}
+
+// Host helpers --------------------------------------------------------------
+
+inline size_t block_values(int encoding) {
+    switch (encoding) {
+    case KDQ_Q4_0:
+    case KDQ_Q8_0:
+        return 32;
+    case KDQ_Q4_K:
+        return 256;
+    default:
+        return 0;
+    }
+}
+
+inline size_t block_bytes(int encoding) {
+    switch (encoding) {
+    case KDQ_Q4_0:
+        return 18;
+    case KDQ_Q8_0:
+        return 34;
+    case KDQ_Q4_K:
+        return 144;
+    default:
+        return 0;
+    }
+}
+
+// Records a HIP failure for kdq_last_hip_error() and returns KDQ_ERR_HIP.
+int hip_failure(hipError_t error);
+
+// Per-device cached workspace (grown on demand, released by kdq_release_scratch).
+void* workspace(size_t bytes, int* status);
+
+inline bool overlaps(const void* a, size_t an, const void* b, size_t bn) {
+    if (!a || !b || !an || !bn)
+        return false;
+    const auto x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return x <= y ? y - x < an : x - y < bn;
+}
+
+inline bool mul_overflows(size_t a, size_t b) {
+    return b && a > SIZE_MAX / b;
+}
+
+}  // namespace kdq
+
+#define KDQ_HIP(call)                                   \
+    do {                                                \
+        const hipError_t kdq_error_ = (call);           \
+        if (kdq_error_ != hipSuccess)                   \
+            return ::kdq::hip_failure(kdq_error_);      \
+    } while (0)

@@ -1,0 +1,151 @@
+"""torch-facing wrappers over the C ABI (device tensors in, device tensors out).
+
+Each function validates shapes on the host, passes raw device pointers and the
+current HIP stream to the corresponding ``kdq_*`` entry point, and raises
+``KdqError`` on a non-zero status.  Nothing here computes on the CPU.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import BLOCK_BYTES, BLOCK_VALUES, MatvecJob, call, lib
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _need(t: torch.Tensor, dtype, name: str) -> None:
+    if not t.is_cuda or t.dtype != dtype or not t.is_contiguous():
+        raise ValueError(f"{name}: expected a contiguous {dtype} device tensor")
+
+
+def dequantize(encoding: int, packed: torch.Tensor, n_in: int,
+               status: torch.Tensor | None = None) -> torch.Tensor:
+    """packed: uint8 [rows, row_bytes] -> fp32 [rows, n_in] (kdq_dequantize)."""
+    _need(packed, torch.uint8, "packed")
+    rows = packed.shape[0]
+    out = torch.empty(rows, n_in, dtype=torch.float32, device=packed.device)
+    call("kdq_dequantize", encoding, packed.data_ptr(), packed.shape[1], rows, n_in,
+         out.data_ptr(), _ptr(status), _stream())
+    return out
+
+
+def gemv(encoding: int, weights: torch.Tensor, x: torch.Tensor, n_out: int,
+         out: torch.Tensor | None = None, status: torch.Tensor | None = None,
+         exact: bool = False) -> torch.Tensor:
+    """y[r, c] = sum_k decode(W[c, k]) x[r, k].  weights uint8 [n_out, row_bytes],
+    x fp32 [rows, n_in] -> y fp32 [rows, n_out] (kdq_gemv / kdq_gemv_exact)."""
+    _need(weights, torch.uint8, "weights")
+    _need(x, torch.float32, "x")
+    x2 = x.reshape(-1, x.shape[-1])
+    rows, n_in = x2.shape
+    if weights.shape[0] != n_out:
+        raise ValueError("weights rows != n_out")
+    if out is None:
+        out = torch.empty(rows, n_out, dtype=torch.float32, device=x.device)
+    fn = "kdq_gemv_exact" if exact else "kdq_gemv"
+    call(fn, encoding, weights.data_ptr(), weights.shape[1], x2.data_ptr(), rows, n_in, n_out,
+         out.data_ptr(), out.stride(0) if out.dim() == 2 else n_out, _ptr(status), _stream())
+    return out
+
+
+def gemv_batch(jobs: list[dict]) -> None:
+    """One submission of several products (kdq_gemv_batch).  Each job: dict with
+    encoding, weights (uint8 [columns, row_bytes]), input (fp32 [rows, in]),
+    output (fp32 [rows, stride]), optional status."""
+    import ctypes as C
+    table = (MatvecJob * len(jobs))()
+    for i, j in enumerate(jobs):
+        w, x, y = j["weights"], j["input"], j["output"]
+        x2 = x.reshape(-1, x.shape[-1])
+        table[i] = MatvecJob(w.data_ptr(), x2.data_ptr(), y.data_ptr(),
+                             _ptr(j.get("status")) or 0, w.shape[1],
+                             y.stride(0) if y.dim() == 2 else w.shape[0],
+                             x2.shape[1], w.shape[0], x2.shape[0], j["encoding"])
+    call("kdq_gemv_batch", C.addressof(table) if jobs else None, len(jobs), _stream())
+
+
+def quantize_q8(x_f16: torch.Tensor):
+    """fp16 [m, k] -> (int8 [m, k], fp32 [m, k/32]) (kdq_quantize_q8)."""
+    _need(x_f16, torch.float16, "x")
+    m, k = x_f16.shape
+    q = torch.empty(m, k, dtype=torch.int8, device=x_f16.device)
+    d = torch.empty(m, k // 32, dtype=torch.float32, device=x_f16.device)
+    call("kdq_quantize_q8", x_f16.data_ptr(), m, k, q.data_ptr(), d.data_ptr(), _stream())
+    return q, d
+
+
+def gemm_q4_0(weights: torch.Tensor, x_f16: torch.Tensor, n_out: int,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    """Q4_0 weights uint8 [n_out, k/32*18] x fp16 [m, k] -> fp16 [m, n_out] (kdq_gemm_q4_0)."""
+    _need(weights, torch.uint8, "weights")
+    _need(x_f16, torch.float16, "x")
+    m, k = x_f16.shape
+    if out is None:
+        out = torch.empty(m, n_out, dtype=torch.float16, device=x_f16.device)
+    call("kdq_gemm_q4_0", weights.data_ptr(), n_out, k, x_f16.data_ptr(), m, out.data_ptr(),
+         _stream())
+    return out
+
+
+def moe_route(logits: torch.Tensor, top_k: int):
+    """fp32 [tokens, experts] -> idx, w, offsets, perm (kdq_moe_route)."""
+    _need(logits, torch.float32, "logits")
+    t, e = logits.shape
+    dev = logits.device
+    idx = torch.empty(t, top_k, dtype=torch.int32, device=dev)
+    w = torch.empty(t, top_k, dtype=torch.float32, device=dev)
+    offsets = torch.empty(e + 1, dtype=torch.int32, device=dev)
+    perm = torch.empty(t * top_k, dtype=torch.int32, device=dev)
+    call("kdq_moe_route", logits.data_ptr(), t, e, top_k, idx.data_ptr(), w.data_ptr(),
+         offsets.data_ptr(), perm.data_ptr(), _stream())
+    return idx, w, offsets, perm
+
+
+def mxfp4_dequantize(blocks: torch.Tensor, scales: torch.Tensor, rows: int, cols: int,
+                     status: torch.Tensor | None = None) -> torch.Tensor:
+    _need(blocks, torch.uint8, "blocks")
+    _need(scales, torch.uint8, "scales")
+    out = torch.empty(rows, cols, dtype=torch.float32, device=blocks.device)
+    call("kdq_mxfp4_dequantize", blocks.data_ptr(), scales.data_ptr(), rows, cols,
+         out.data_ptr(), _ptr(status), _stream())
+    return out
+
+
+def moe_mxfp4(x_bf16: torch.Tensor, logits: torch.Tensor, top_k: int, gate_blocks, gate_scales,
+              up_blocks, up_scales, down_blocks, down_scales, routing: bool = False,
+              out: torch.Tensor | None = None):
+    """The MXFP4 MoE layer (kdq_moe_mxfp4).  Returns y fp32 [tokens, hidden], plus
+    (idx, w, offsets, perm) when ``routing``."""
+    _need(x_bf16, torch.bfloat16, "x")
+    _need(logits, torch.float32, "logits")
+    t, h = x_bf16.shape
+    e = logits.shape[1]
+    inter = gate_scales.shape[1]
+    dev = x_bf16.device
+    for name, a in (("gate_blocks", gate_blocks), ("gate_scales", gate_scales),
+                    ("up_blocks", up_blocks), ("up_scales", up_scales),
+                    ("down_blocks", down_blocks), ("down_scales", down_scales)):
+        _need(a, torch.uint8, name)
+    if out is None:
+        out = torch.empty(t, h, dtype=torch.float32, device=dev)
+    extra = [None] * 4
+    if routing:
+        extra = [torch.empty(t, top_k, dtype=torch.int32, device=dev),
+                 torch.empty(t, top_k, dtype=torch.float32, device=dev),
+                 torch.empty(e + 1, dtype=torch.int32, device=dev),
+                 torch.empty(t * top_k, dtype=torch.int32, device=dev)]
+    call("kdq_moe_mxfp4", x_bf16.data_ptr(), logits.data_ptr(), t, h, inter, e, top_k,
+         gate_blocks.data_ptr(), gate_scales.data_ptr(), up_blocks.data_ptr(),
+         up_scales.data_ptr(), down_blocks.data_ptr(), down_scales.data_ptr(), out.data_ptr(),
+         *[_ptr(a) for a in extra], _stream())
+    return (out, *extra) if routing else out
+
+
+__all__ = ["dequantize", "gemv", "gemv_batch", "quantize_q8", "gemm_q4_0", "moe_route",
+           "mxfp4_dequantize", "moe_mxfp4", "lib", "BLOCK_BYTES", "BLOCK_VALUES"]

@@ -1,0 +1,293 @@
+"""ctypes bindings for the CPU checkers.  TEST INFRASTRUCTURE ONLY.
+
+Only tests/, tests/golden/, ``__graft_entry__.smoke()`` and bench.py's
+cpu_baseline leg may import this package.  The product library
+(kadan_amd/libkadan_amd.so) never loads it.
+
+* ``Oracle``  -- liboracle.so, the plain-C restatement of the reference path
+  (oracle.c; every function cites the reference file:line it follows).
+* ``Reference`` -- _ref/libkadan_ref.so, the reference's own sources compiled
+  from /root/reference by oracle/Makefile (absent where the reference is absent).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libkadan_ref.so")
+REFERENCE_ROOT = "/root/reference/services/hikari/inference_worker"
+
+Q4_0, Q8_0, Q4_K = 2, 8, 12
+BLOCK_VALUES = {Q4_0: 32, Q8_0: 32, Q4_K: 256}
+BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144}
+
+
+def build(reference: bool | None = None) -> None:
+    """Compile liboracle.so, and _ref/ when the reference sources are present."""
+    subprocess.check_call(["make", "-s", "-C", HERE, "-B", "oracle"])
+    if reference is None:
+        reference = os.path.isdir(REFERENCE_ROOT)
+    if reference:
+        subprocess.check_call(["make", "-s", "-C", HERE, "-B", "ref"])
+
+
+def _p(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+class Oracle:
+    def __init__(self, path: str = ORACLE_SO):
+        if not os.path.exists(path):
+            build(reference=False)
+        lib = C.CDLL(path)
+        self.lib = lib
+        sz, vp, i = C.c_size_t, C.c_void_p, C.c_int
+        lib.kdo_half_to_float.restype = C.c_float
+        lib.kdo_half_to_float.argtypes = [C.c_uint16]
+        lib.kdo_float_to_half.restype = C.c_uint16
+        lib.kdo_float_to_half.argtypes = [C.c_float]
+        lib.kdo_dequantize_row.argtypes = [i, vp, sz, vp]
+        lib.kdo_gemv.argtypes = [i, vp, sz, vp, sz, sz, sz, vp, sz]
+        lib.kdo_quantize_row_q8_0.argtypes = [vp, sz, vp, vp]
+        lib.kdo_quantize_row_q8_K.argtypes = [vp, sz, vp, vp, vp]
+        lib.kdo_quantize_q8_f16.argtypes = [vp, sz, sz, vp, vp]
+        lib.kdo_cpu_matvec.argtypes = [i, vp, sz, vp, sz, sz, sz, vp, i]
+        lib.kdo_gemm_q4_0_q8.argtypes = [vp, sz, sz, vp, vp, sz, vp]
+        lib.kdo_e2m1.restype = C.c_float
+        lib.kdo_e2m1.argtypes = [C.c_uint8]
+        lib.kdo_mxfp4_decode_rows.argtypes = [vp, vp, sz, sz, vp]
+        lib.kdo_mxfp4_matvec.argtypes = [vp, vp, sz, sz, vp, vp]
+        lib.kdo_moe_route.argtypes = [vp, sz, sz, sz, vp, vp]
+        lib.kdo_moe_permute.argtypes = [vp, sz, sz, sz, vp, vp]
+        lib.kdo_moe_forward.argtypes = [vp, vp, sz, sz, sz, sz, sz, vp, vp, vp, vp, vp, vp,
+                                        vp, vp, vp, vp, vp, i]
+
+    # -- scalars
+    def half_to_float(self, bits: int) -> float:
+        return self.lib.kdo_half_to_float(bits)
+
+    def halves_to_float(self, bits: np.ndarray) -> np.ndarray:
+        """Vectorised through the Q8_0 decode of code 1 (d * 1 is exact)."""
+        bits = np.ascontiguousarray(bits, dtype=np.uint16).ravel()
+        blocks = np.zeros((bits.size, 34), np.uint8)
+        blocks[:, 0] = bits & 0xFF
+        blocks[:, 1] = bits >> 8
+        blocks[:, 2] = 1
+        out = self.dequantize(Q8_0, blocks.reshape(1, -1), bits.size * 32)
+        return out.reshape(bits.size, 32)[:, 0].copy()
+
+    def float_to_half(self, value: float) -> int:
+        return self.lib.kdo_float_to_half(value)
+
+    # -- GGUF blocks
+    def dequantize(self, encoding: int, rows: np.ndarray, n_in: int) -> np.ndarray:
+        rows = np.ascontiguousarray(rows, dtype=np.uint8)
+        rows2 = rows.reshape(-1, rows.shape[-1])
+        out = np.empty((rows2.shape[0], n_in), np.float32)
+        for r in range(rows2.shape[0]):
+            rc = self.lib.kdo_dequantize_row(encoding, _p(rows2[r]), n_in, _p(out[r]))
+            if rc:
+                raise ValueError(f"kdo_dequantize_row rc={rc}")
+        return out
+
+    def gemv(self, encoding, weights, x, n_in, n_out):
+        weights = np.ascontiguousarray(weights, dtype=np.uint8)
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, n_in)
+        y = np.empty((x.shape[0], n_out), np.float32)
+        row_bytes = weights.size // n_out
+        rc = self.lib.kdo_gemv(encoding, _p(weights), row_bytes, _p(x), x.shape[0], n_in, n_out,
+                               _p(y), n_out)
+        if rc:
+            raise ValueError(f"kdo_gemv rc={rc}")
+        return y
+
+    def cpu_matvec(self, encoding, weights, x, n_in, n_out, threads=1):
+        weights = np.ascontiguousarray(weights, dtype=np.uint8)
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, n_in)
+        y = np.empty((x.shape[0], n_out), np.float32)
+        rc = self.lib.kdo_cpu_matvec(encoding, _p(weights), weights.size // n_out, _p(x),
+                                     x.shape[0], n_in, n_out, _p(y), threads)
+        if rc:
+            raise ValueError(f"kdo_cpu_matvec rc={rc}")
+        return y
+
+    # -- activation quantizers
+    def quantize_row_q8_0(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+        qs = np.empty(x.size, np.int8)
+        d = np.empty(x.size // 32, np.uint16)
+        self.lib.kdo_quantize_row_q8_0(_p(x), x.size, _p(qs), _p(d))
+        return qs, d
+
+    def quantize_row_q8_K(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+        qs = np.empty(x.size, np.int8)
+        d = np.empty(x.size // 256, np.float32)
+        bsums = np.empty(x.size // 16, np.int16)
+        self.lib.kdo_quantize_row_q8_K(_p(x), x.size, _p(qs), _p(d), _p(bsums))
+        return qs, d, bsums
+
+    def quantize_q8_f16(self, x_half: np.ndarray):
+        x_half = np.ascontiguousarray(x_half, dtype=np.uint16)
+        m, k = x_half.shape
+        qs = np.empty((m, k), np.int8)
+        d = np.empty((m, k // 32), np.float32)
+        self.lib.kdo_quantize_q8_f16(_p(x_half), m, k, _p(qs), _p(d))
+        return qs, d
+
+    def gemm_q4_0_q8(self, weights, n_out, k, xq, xd):
+        weights = np.ascontiguousarray(weights, dtype=np.uint8)
+        xq = np.ascontiguousarray(xq, dtype=np.int8)
+        xd = np.ascontiguousarray(xd, dtype=np.float32)
+        m = xq.shape[0]
+        y = np.empty((m, n_out), np.float32)
+        rc = self.lib.kdo_gemm_q4_0_q8(_p(weights), n_out, k, _p(xq), _p(xd), m, _p(y))
+        if rc:
+            raise ValueError(f"kdo_gemm_q4_0_q8 rc={rc}")
+        return y
+
+    # -- MXFP4 / MoE
+    def e2m1(self, code: int) -> float:
+        return self.lib.kdo_e2m1(code)
+
+    def mxfp4_decode_rows(self, blocks, scales, rows, cols):
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+        scales = np.ascontiguousarray(scales, dtype=np.uint8)
+        out = np.empty((rows, cols), np.float32)
+        rc = self.lib.kdo_mxfp4_decode_rows(_p(blocks), _p(scales), rows, cols, _p(out))
+        return rc, out
+
+    def mxfp4_matvec(self, blocks, scales, rows, cols, x):
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+        scales = np.ascontiguousarray(scales, dtype=np.uint8)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty(rows, np.float32)
+        rc = self.lib.kdo_mxfp4_matvec(_p(blocks), _p(scales), rows, cols, _p(x), _p(y))
+        return rc, y
+
+    def moe_route(self, logits, top_k):
+        logits = np.ascontiguousarray(logits, dtype=np.float32)
+        t, e = logits.shape
+        idx = np.empty((t, top_k), np.int32)
+        w = np.empty((t, top_k), np.float32)
+        self.lib.kdo_moe_route(_p(logits), t, e, top_k, _p(idx), _p(w))
+        return idx, w
+
+    def moe_permute(self, idx, experts):
+        idx = np.ascontiguousarray(idx, dtype=np.int32)
+        t, k = idx.shape
+        offsets = np.empty(experts + 1, np.int32)
+        perm = np.empty(t * k, np.int32)
+        self.lib.kdo_moe_permute(_p(idx), t, k, experts, _p(offsets), _p(perm))
+        return offsets, perm
+
+    def moe_forward(self, x_bf16, logits, top_k, gate_b, gate_s, up_b, up_s, down_b, down_s,
+                    threads=1):
+        x_bf16 = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+        logits = np.ascontiguousarray(logits, dtype=np.float32)
+        t, h = x_bf16.shape
+        e = logits.shape[1]
+        inter = gate_s.shape[1]
+        arrays = [np.ascontiguousarray(a, dtype=np.uint8)
+                  for a in (gate_b, gate_s, up_b, up_s, down_b, down_s)]
+        y = np.empty((t, h), np.float32)
+        idx = np.empty((t, top_k), np.int32)
+        w = np.empty((t, top_k), np.float32)
+        offsets = np.empty(e + 1, np.int32)
+        perm = np.empty(t * top_k, np.int32)
+        rc = self.lib.kdo_moe_forward(_p(x_bf16), _p(logits), t, h, inter, e, top_k,
+                                      *[_p(a) for a in arrays], _p(y), _p(idx), _p(w),
+                                      _p(offsets), _p(perm), threads)
+        if rc:
+            raise ValueError(f"kdo_moe_forward rc={rc}")
+        return y, idx, w, offsets, perm
+
+
+class Reference:
+    """The reference's own compiled code (oracle/_ref).  ``available()`` first."""
+
+    @staticmethod
+    def available() -> bool:
+        return os.path.exists(REF_SO)
+
+    def __init__(self, path: str = REF_SO):
+        lib = C.CDLL(path)
+        self.lib = lib
+        sz, vp, i = C.c_size_t, C.c_void_p, C.c_int
+        lib.kdr_half_to_float.restype = C.c_float
+        lib.kdr_half_to_float.argtypes = [C.c_uint16]
+        lib.kdr_ggml_to_float.argtypes = [i, vp, C.c_int64, vp]
+        lib.kdr_kadan_decode_block.argtypes = [i, vp, vp]
+        lib.kdr_quantize_row.argtypes = [i, vp, vp, C.c_int64]
+        lib.kdr_vec_dot.argtypes = [i, i, vp, vp, vp]
+        lib.kdr_cpu_matvec.argtypes = [i, vp, sz, vp, sz, sz, sz, vp, i]
+        lib.kdr_e2m1.restype = C.c_float
+        lib.kdr_e2m1.argtypes = [C.c_uint8]
+        lib.kdr_mxfp4_decode_rows.argtypes = [vp, vp, sz, sz, vp]
+        lib.kdr_mxfp4_matvec.argtypes = [vp, vp, sz, sz, vp, vp]
+
+    def half_to_float(self, bits: int) -> float:
+        return self.lib.kdr_half_to_float(bits)
+
+    def to_float(self, ggml_type: int, rows: np.ndarray, n: int) -> np.ndarray:
+        rows = np.ascontiguousarray(rows, dtype=np.uint8)
+        rows2 = rows.reshape(-1, rows.shape[-1])
+        out = np.empty((rows2.shape[0], n), np.float32)
+        for r in range(rows2.shape[0]):
+            if self.lib.kdr_ggml_to_float(ggml_type, _p(rows2[r]), n, _p(out[r])):
+                raise ValueError("kdr_ggml_to_float")
+        return out
+
+    def kadan_decode_block(self, ggml_type: int, block: np.ndarray) -> np.ndarray | None:
+        block = np.ascontiguousarray(block, dtype=np.uint8)
+        out = np.empty(BLOCK_VALUES[ggml_type], np.float32)
+        if self.lib.kdr_kadan_decode_block(ggml_type, _p(block), _p(out)):
+            return None
+        return out
+
+    def quantize_row(self, dot_type: int, x: np.ndarray, nbytes: int) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+        y = np.zeros(nbytes, np.uint8)
+        if self.lib.kdr_quantize_row(dot_type, _p(x), _p(y), x.size):
+            raise ValueError("kdr_quantize_row")
+        return y
+
+    def vec_dot(self, ggml_type: int, n: int, w: np.ndarray, xq: np.ndarray) -> float:
+        out = np.zeros(1, np.float32)
+        if self.lib.kdr_vec_dot(ggml_type, n, _p(np.ascontiguousarray(w)),
+                                _p(np.ascontiguousarray(xq)), _p(out)):
+            raise ValueError("kdr_vec_dot")
+        return float(out[0])
+
+    def cpu_matvec(self, ggml_type, weights, x, n_in, n_out, threads=1):
+        weights = np.ascontiguousarray(weights, dtype=np.uint8)
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, n_in)
+        y = np.empty((x.shape[0], n_out), np.float32)
+        rc = self.lib.kdr_cpu_matvec(ggml_type, _p(weights), weights.size // n_out, _p(x),
+                                     x.shape[0], n_in, n_out, _p(y), threads)
+        if rc:
+            raise ValueError(f"kdr_cpu_matvec rc={rc}")
+        return y
+
+    def e2m1(self, code: int) -> float:
+        return self.lib.kdr_e2m1(code)
+
+    def mxfp4_decode_rows(self, blocks, scales, rows, cols):
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+        scales = np.ascontiguousarray(scales, dtype=np.uint8)
+        out = np.empty((rows, cols), np.float32)
+        rc = self.lib.kdr_mxfp4_decode_rows(_p(blocks), _p(scales), rows, cols, _p(out))
+        return rc, out
+
+    def mxfp4_matvec(self, blocks, scales, rows, cols, x):
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+        scales = np.ascontiguousarray(scales, dtype=np.uint8)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty(rows, np.float32)
+        rc = self.lib.kdr_mxfp4_matvec(_p(blocks), _p(scales), rows, cols, _p(x), _p(y))
+        return rc, y

@@ -1,0 +1,654 @@
+/*
+ * CPU oracle for the quantized-weight matmul path: TEST INFRASTRUCTURE ONLY.
+ * See oracle.h for the contract, the reference citations and the pinning of
+ * every function.  Compile with -ffp-contract=off (oracle/Makefile does).
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdatomic.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------ scalars */
+
+static float bits_to_float(uint32_t bits) {
+    float f;
+    memcpy(&f, &bits, sizeof f);
+    return f;
+}
+
+static uint32_t float_to_bits(float f) {
+    uint32_t bits;
+    memcpy(&bits, &f, sizeof bits);
+    return bits;
+}
+
+float kdo_half_to_float(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t exponent = (h >> 10) & 0x1fu;
+    const uint32_t mantissa = h & 0x3ffu;
+    if (exponent == 0x1fu) /* inf / NaN: payload kept in the top mantissa bits */
+        return bits_to_float(sign | 0x7f800000u | (mantissa << 13));
+    if (exponent == 0) {
+        /* zero or subnormal: mantissa * 2^-24 is exact in binary32 */
+        const float magnitude = (float)mantissa * 0x1p-24f;
+        return bits_to_float(sign | float_to_bits(magnitude));
+    }
+    return bits_to_float(sign | ((exponent + 112u) << 23) | (mantissa << 13));
+}
+
+uint16_t kdo_float_to_half(float value) {
+    const uint32_t bits = float_to_bits(value);
+    const uint16_t sign = (uint16_t)((bits >> 16) & 0x8000u);
+    const uint32_t magnitude = bits & 0x7fffffffu;
+    if (magnitude >= 0x7f800000u) { /* inf or NaN (quiet bit forced for NaN) */
+        if (magnitude == 0x7f800000u)
+            return sign | 0x7c00u;
+        return sign | 0x7e00u | (uint16_t)((magnitude >> 13) & 0x3ffu);
+    }
+    if (magnitude >= 0x477ff000u) /* rounds to >= 65520 -> inf */
+        return sign | 0x7c00u;
+    if (magnitude < 0x38800000u) {
+        /* result is a half subnormal (or zero): value / 2^-24 rounded to an integer */
+        const float scaled = bits_to_float(magnitude) * 0x1p24f; /* exact */
+        const float rounded = nearbyintf(scaled);               /* RNE */
+        return sign | (uint16_t)rounded;
+    }
+    /* normal: rebias, round the 13 dropped bits to nearest even */
+    uint32_t h = ((magnitude >> 13) - (112u << 10));
+    const uint32_t dropped = magnitude & 0x1fffu;
+    if (dropped > 0x1000u || (dropped == 0x1000u && (h & 1u)))
+        h += 1u;
+    return sign | (uint16_t)h;
+}
+
+float kdo_bf16_to_float(uint16_t bits) {
+    return bits_to_float((uint32_t)bits << 16);
+}
+
+uint16_t kdo_float_to_bf16(float value) {
+    uint32_t bits = float_to_bits(value);
+    if ((bits & 0x7fffffffu) > 0x7f800000u)
+        return (uint16_t)((bits >> 16) | 0x40u);
+    bits += 0x7fffu + ((bits >> 16) & 1u);
+    return (uint16_t)(bits >> 16);
+}
+
+static uint16_t load_u16(const uint8_t* p) {
+    return (uint16_t)(p[0] | (p[1] << 8));
+}
+
+/* ------------------------------------------------------------ block layouts */
+
+int kdo_block_values(int encoding) {
+    switch (encoding) {
+    case KDO_Q4_0:
+    case KDO_Q8_0:
+        return 32;
+    case KDO_Q4_K:
+        return 256;
+    default:
+        return 0;
+    }
+}
+
+int kdo_block_bytes(int encoding) {
+    switch (encoding) {
+    case KDO_Q4_0:
+        return 18; /* fp16 d + 16 bytes of nibbles */
+    case KDO_Q8_0:
+        return 34; /* fp16 d + 32 int8 */
+    case KDO_Q4_K:
+        return 144; /* fp16 d, fp16 dmin, 12 packed 6-bit scales, 128 bytes of nibbles */
+    default:
+        return 0;
+    }
+}
+
+/* Q4_K sub-block g (0..7): 6-bit scale and min packed into 12 bytes. */
+static void q4k_scale_min(const uint8_t* packed, unsigned g, unsigned* scale, unsigned* min) {
+    if (g < 4) {
+        *scale = packed[g] & 0x3fu;
+        *min = packed[g + 4] & 0x3fu;
+    } else {
+        *scale = (packed[g + 4] & 0x0fu) | ((unsigned)(packed[g - 4] >> 6) << 4);
+        *min = (unsigned)(packed[g + 4] >> 4) | ((unsigned)(packed[g] >> 6) << 4);
+    }
+}
+
+static void decode_block(int encoding, const uint8_t* block, float* out) {
+    const float d = kdo_half_to_float(load_u16(block));
+    if (encoding == KDO_Q8_0) {
+        for (int i = 0; i < 32; ++i)
+            out[i] = d * (float)(int8_t)block[2 + i];
+    } else if (encoding == KDO_Q4_0) {
+        for (int i = 0; i < 16; ++i) {
+            const uint8_t byte = block[2 + i];
+            out[i] = (float)((int)(byte & 0x0f) - 8) * d;
+            out[i + 16] = (float)((int)(byte >> 4) - 8) * d;
+        }
+    } else { /* Q4_K */
+        const float dmin = kdo_half_to_float(load_u16(block + 2));
+        const uint8_t* packed = block + 4;
+        const uint8_t* nibbles = block + 16;
+        for (unsigned g = 0; g < 8; ++g) {
+            unsigned sc, m;
+            q4k_scale_min(packed, g, &sc, &m);
+            const float step = d * (float)sc;     /* rounded */
+            const float offset = dmin * (float)m; /* rounded */
+            const uint8_t* bytes = nibbles + (g / 2) * 32;
+            for (unsigned i = 0; i < 32; ++i) {
+                const unsigned code = (g & 1u) ? (bytes[i] >> 4) : (bytes[i] & 0x0fu);
+                const float scaled = step * (float)code; /* rounded */
+                out[g * 32 + i] = scaled - offset;       /* rounded, never fused */
+            }
+        }
+    }
+}
+
+int kdo_dequantize_row(int encoding, const uint8_t* row, size_t in, float* out) {
+    const int values = kdo_block_values(encoding);
+    if (!values || in % (size_t)values)
+        return -1;
+    const int bytes = kdo_block_bytes(encoding);
+    for (size_t b = 0; b < in / (size_t)values; ++b)
+        decode_block(encoding, row + b * (size_t)bytes, out + b * (size_t)values);
+    return 0;
+}
+
+int kdo_gemv(int encoding, const uint8_t* weights, size_t row_bytes, const float* x,
+             size_t rows, size_t in, size_t out, float* y, size_t stride) {
+    float* decoded = (float*)malloc((in ? in : 1) * sizeof(float));
+    if (!decoded)
+        return -2;
+    for (size_t c = 0; c < out; ++c) {
+        if (kdo_dequantize_row(encoding, weights + c * row_bytes, in, decoded)) {
+            free(decoded);
+            return -1;
+        }
+        for (size_t r = 0; r < rows; ++r) {
+            double sum = 0.0;
+            const float* xr = x + r * in;
+            for (size_t k = 0; k < in; ++k)
+                sum += (double)decoded[k] * (double)xr[k];
+            y[r * stride + c] = (float)sum;
+        }
+    }
+    free(decoded);
+    return 0;
+}
+
+/* ------------------------------------------------------ activation quantizers */
+
+static float block_absmax(const float* x, size_t n) {
+    float amax = 0.0f;
+    for (size_t j = 0; j < n; ++j) {
+        const float a = fabsf(x[j]);
+        amax = a > amax ? a : amax;
+    }
+    return amax;
+}
+
+void kdo_quantize_row_q8_0(const float* x, size_t k, int8_t* qs, uint16_t* d_half) {
+    for (size_t b = 0; b < k / 32; ++b) {
+        const float* xb = x + b * 32;
+        const float amax = block_absmax(xb, 32);
+        d_half[b] = kdo_float_to_half(amax / 127.0f);
+        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        for (int j = 0; j < 32; ++j)
+            qs[b * 32 + j] = (int8_t)(int)nearbyintf(xb[j] * id); /* round half even */
+    }
+}
+
+void kdo_quantize_q8_f16(const uint16_t* x, size_t m, size_t k, int8_t* qs, float* d) {
+    float block[32];
+    for (size_t r = 0; r < m; ++r)
+        for (size_t b = 0; b < k / 32; ++b) {
+            for (int j = 0; j < 32; ++j)
+                block[j] = kdo_half_to_float(x[r * k + b * 32 + j]);
+            const float amax = block_absmax(block, 32);
+            d[r * (k / 32) + b] = amax / 127.0f;
+            const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+            for (int j = 0; j < 32; ++j)
+                qs[r * k + b * 32 + j] = (int8_t)(int)nearbyintf(block[j] * id);
+        }
+}
+
+/* G/src/ggml-quants.c:621-626 nearest_int: round half to even via the 1.5*2^23 trick. */
+static int nearest_even(float v) {
+    return (int)nearbyintf(v);
+}
+
+void kdo_quantize_row_q8_K(const float* x, size_t k, int8_t* qs, float* d, int16_t* bsums) {
+    for (size_t b = 0; b < k / 256; ++b) {
+        const float* xb = x + b * 256;
+        float amax = 0.0f, max = 0.0f;
+        for (int j = 0; j < 256; ++j) {
+            const float a = fabsf(xb[j]);
+            if (a > amax) {
+                amax = a;
+                max = xb[j];
+            }
+        }
+        int8_t* q = qs + b * 256;
+        if (amax == 0.0f) {
+            d[b] = 0.0f;
+            memset(q, 0, 256);
+            memset(bsums + b * 16, 0, 16 * sizeof(int16_t));
+            continue;
+        }
+        const float iscale = -127.0f / max;
+        for (int j = 0; j < 256; ++j) {
+            const int v = nearest_even(iscale * xb[j]);
+            q[j] = (int8_t)(v < 127 ? v : 127);
+        }
+        for (int g = 0; g < 16; ++g) {
+            int sum = 0;
+            for (int i = 0; i < 16; ++i)
+                sum += q[g * 16 + i];
+            bsums[b * 16 + g] = (int16_t)sum;
+        }
+        d[b] = 1.0f / iscale;
+    }
+}
+
+/* --------------------------------------------------------------- CPU dots */
+
+float kdo_vec_dot_q8_0_q8_0(size_t k, const uint8_t* w, const int8_t* xq, const uint16_t* xd) {
+    float total = 0.0f;
+    for (size_t b = 0; b < k / 32; ++b) {
+        const uint8_t* block = w + b * 34;
+        int dot = 0;
+        for (int j = 0; j < 32; ++j)
+            dot += (int)(int8_t)block[2 + j] * (int)xq[b * 32 + j];
+        total += (float)dot * (kdo_half_to_float(load_u16(block)) * kdo_half_to_float(xd[b]));
+    }
+    return total;
+}
+
+float kdo_vec_dot_q4_0_q8_0(size_t k, const uint8_t* w, const int8_t* xq, const uint16_t* xd) {
+    float total = 0.0f;
+    for (size_t b = 0; b < k / 32; ++b) {
+        const uint8_t* block = w + b * 18;
+        const int8_t* q = xq + b * 32;
+        int dot = 0;
+        for (int j = 0; j < 16; ++j) {
+            dot += ((int)(block[2 + j] & 0x0f) - 8) * (int)q[j];
+            dot += ((int)(block[2 + j] >> 4) - 8) * (int)q[j + 16];
+        }
+        total += (float)dot * kdo_half_to_float(load_u16(block)) * kdo_half_to_float(xd[b]);
+    }
+    return total;
+}
+
+float kdo_vec_dot_q4_K_q8_K(size_t k, const uint8_t* w, const int8_t* xq, const float* xd,
+                            const int16_t* bsums) {
+    float total = 0.0f;
+    for (size_t b = 0; b < k / 256; ++b) {
+        const uint8_t* block = w + b * 144;
+        const int8_t* q = xq + b * 256;
+        int scaled = 0, offset = 0;
+        for (unsigned g = 0; g < 8; ++g) {
+            unsigned sc, m;
+            q4k_scale_min(block + 4, g, &sc, &m);
+            const uint8_t* bytes = block + 16 + (g / 2) * 32;
+            int dot = 0;
+            for (unsigned i = 0; i < 32; ++i) {
+                const int code = (g & 1u) ? (bytes[i] >> 4) : (bytes[i] & 0x0f);
+                dot += code * (int)q[g * 32 + i];
+            }
+            scaled += (int)sc * dot;
+            offset += (int)m * ((int)bsums[b * 16 + 2 * g] + (int)bsums[b * 16 + 2 * g + 1]);
+        }
+        const float d = kdo_half_to_float(load_u16(block)) * xd[b];
+        const float dmin = kdo_half_to_float(load_u16(block + 2)) * xd[b];
+        total += d * (float)scaled - dmin * (float)offset;
+    }
+    return total;
+}
+
+/* ----------------------------------------------------- threaded CPU matvec */
+
+typedef struct {
+    int encoding;
+    const uint8_t* weights;
+    size_t row_bytes, rows, in, out;
+    const int8_t* xq;
+    const void* xd; /* uint16_t* (q8_0) or float* (q8_K) */
+    const int16_t* bsums;
+    float* y;
+    atomic_size_t next;
+} matvec_work;
+
+enum { UNIT_COLUMNS = 64 };
+
+static void* matvec_worker(void* arg) {
+    matvec_work* m = (matvec_work*)arg;
+    const size_t units = (m->out + UNIT_COLUMNS - 1) / UNIT_COLUMNS;
+    for (;;) {
+        const size_t u = atomic_fetch_add(&m->next, 1);
+        if (u >= units)
+            break;
+        const size_t end = (u + 1) * UNIT_COLUMNS < m->out ? (u + 1) * UNIT_COLUMNS : m->out;
+        for (size_t c = u * UNIT_COLUMNS; c < end; ++c)
+            for (size_t r = 0; r < m->rows; ++r) {
+                const uint8_t* row = m->weights + c * m->row_bytes;
+                const int8_t* q = m->xq + r * m->in;
+                float v;
+                if (m->encoding == KDO_Q4_K)
+                    v = kdo_vec_dot_q4_K_q8_K(m->in, row, q, (const float*)m->xd + r * (m->in / 256),
+                                              m->bsums + r * (m->in / 16));
+                else if (m->encoding == KDO_Q8_0)
+                    v = kdo_vec_dot_q8_0_q8_0(m->in, row, q, (const uint16_t*)m->xd + r * (m->in / 32));
+                else
+                    v = kdo_vec_dot_q4_0_q8_0(m->in, row, q, (const uint16_t*)m->xd + r * (m->in / 32));
+                m->y[r * m->out + c] = v;
+            }
+    }
+    return NULL;
+}
+
+int kdo_cpu_matvec(int encoding, const uint8_t* weights, size_t row_bytes, const float* x,
+                   size_t rows, size_t in, size_t out, float* y, int threads) {
+    if (!kdo_block_values(encoding) || in % (size_t)kdo_block_values(encoding) || threads < 1)
+        return -1;
+    int8_t* xq = (int8_t*)malloc(rows * in + 1);
+    void* xd = malloc(rows * (in / 16 + 1) * sizeof(float));
+    int16_t* bsums = (int16_t*)malloc(rows * (in / 16 + 1) * sizeof(int16_t));
+    if (!xq || !xd || !bsums) {
+        free(xq), free(xd), free(bsums);
+        return -2;
+    }
+    for (size_t r = 0; r < rows; ++r) {
+        if (encoding == KDO_Q4_K)
+            kdo_quantize_row_q8_K(x + r * in, in, xq + r * in, (float*)xd + r * (in / 256),
+                                  bsums + r * (in / 16));
+        else
+            kdo_quantize_row_q8_0(x + r * in, in, xq + r * in, (uint16_t*)xd + r * (in / 32));
+    }
+    matvec_work work = {encoding, weights, row_bytes, rows, in, out, xq, xd, bsums, y, 0};
+    pthread_t* pool = (pthread_t*)malloc(sizeof(pthread_t) * (size_t)threads);
+    int started = 0;
+    for (int t = 1; t < threads && pool; ++t)
+        if (pthread_create(&pool[started], NULL, matvec_worker, &work) == 0)
+            ++started;
+    matvec_worker(&work); /* the caller is the last worker */
+    for (int t = 0; t < started; ++t)
+        pthread_join(pool[t], NULL);
+    free(pool);
+    free(xq), free(xd), free(bsums);
+    return 0;
+}
+
+/* ------------------------------------------------------------ Q4_0 GEMM */
+
+int kdo_gemm_q4_0_q8(const uint8_t* weights, size_t n_out, size_t k, const int8_t* xq,
+                     const float* xd, size_t m, float* y) {
+    if (k % 32)
+        return -1;
+    const size_t blocks = k / 32;
+    for (size_t n = 0; n < n_out; ++n) {
+        const uint8_t* row = weights + n * blocks * 18;
+        for (size_t r = 0; r < m; ++r) {
+            double sum = 0.0;
+            for (size_t b = 0; b < blocks; ++b) {
+                const uint8_t* block = row + b * 18;
+                const int8_t* q = xq + r * k + b * 32;
+                int dot = 0;
+                for (int j = 0; j < 16; ++j) {
+                    dot += ((int)(block[2 + j] & 0x0f) - 8) * (int)q[j];
+                    dot += ((int)(block[2 + j] >> 4) - 8) * (int)q[j + 16];
+                }
+                sum += (double)dot * (double)kdo_half_to_float(load_u16(block)) *
+                       (double)xd[r * blocks + b];
+            }
+            y[r * n_out + n] = (float)sum;
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------ MXFP4 */
+
+float kdo_e2m1(uint8_t code) {
+    /* sign bit 3; exponent bits 2..1; mantissa bit 0; subnormal step 0.5 */
+    static const float magnitude[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+    const float v = magnitude[code & 7u];
+    return (code & 8u) ? -v : v;
+}
+
+/* One decoded row of MXFP4 weights; returns 0 or a negative error. */
+static int mxfp4_row(const uint8_t* blocks, const uint8_t* scales, size_t cols, float* out) {
+    for (size_t c = 0; c < cols; ++c) {
+        const uint8_t scale = scales[c / 32];
+        if (scale == 255)
+            return -2;
+        const uint8_t code = (uint8_t)((blocks[c / 2] >> (4 * (c % 2))) & 15u);
+        const double value = ldexp((double)kdo_e2m1(code), (int)scale - 127);
+        if (!isfinite(value) || fabs(value) > 3.4028234663852886e38)
+            return -3;
+        out[c] = (float)value;
+    }
+    return 0;
+}
+
+int kdo_mxfp4_decode_rows(const uint8_t* blocks, const uint8_t* scales, size_t rows,
+                          size_t cols, float* out) {
+    if (!cols || cols % 32)
+        return -1;
+    for (size_t r = 0; r < rows; ++r) {
+        const int rc = mxfp4_row(blocks + r * (cols / 2), scales + r * (cols / 32), cols,
+                                 out + r * cols);
+        if (rc)
+            return rc;
+    }
+    return 0;
+}
+
+static int finite_to_float(double v, float* out) {
+    if (!isfinite(v) || fabs(v) > 3.4028234663852886e38)
+        return -3;
+    *out = (float)v;
+    return 0;
+}
+
+int kdo_mxfp4_matvec(const uint8_t* blocks, const uint8_t* scales, size_t rows, size_t cols,
+                     const float* x, float* y) {
+    if (!cols || cols % 32)
+        return -1;
+    for (size_t c = 0; c < cols; ++c)
+        if (!isfinite(x[c]))
+            return -4;
+    float* row = (float*)malloc(cols * sizeof(float));
+    if (!row)
+        return -5;
+    for (size_t r = 0; r < rows; ++r) {
+        int rc = mxfp4_row(blocks + r * (cols / 2), scales + r * (cols / 32), cols, row);
+        double sum = 0.0;
+        for (size_t c = 0; !rc && c < cols; ++c)
+            sum += (double)row[c] * (double)x[c];
+        if (!rc)
+            rc = finite_to_float(sum, &y[r]);
+        if (rc) {
+            free(row);
+            return rc;
+        }
+    }
+    free(row);
+    return 0;
+}
+
+/* -------------------------------------------------------------------- MoE */
+
+void kdo_moe_route(const float* logits, size_t tokens, size_t experts, size_t top_k,
+                   int32_t* idx, float* w) {
+    float* p = (float*)malloc(experts * sizeof(float));
+    unsigned char* taken = (unsigned char*)malloc(experts);
+    for (size_t t = 0; t < tokens; ++t) {
+        const float* l = logits + t * experts;
+        float maximum = l[0];
+        for (size_t e = 1; e < experts; ++e)
+            maximum = l[e] > maximum ? l[e] : maximum;
+        double total = 0.0;
+        for (size_t e = 0; e < experts; ++e) {
+            p[e] = expf(l[e] - maximum);
+            total += (double)p[e];
+        }
+        for (size_t e = 0; e < experts; ++e)
+            p[e] = (float)((double)p[e] / total);
+        memset(taken, 0, experts);
+        float sum = 0.0f;
+        for (size_t i = 0; i < top_k; ++i) {
+            size_t best = experts;
+            for (size_t e = 0; e < experts; ++e)
+                if (!taken[e] && (best == experts || p[e] > p[best]))
+                    best = e; /* strict >: equal probabilities keep the lower expert */
+            taken[best] = 1;
+            idx[t * top_k + i] = (int32_t)best;
+            w[t * top_k + i] = p[best];
+            sum += p[best];
+        }
+        sum = sum > 6.103515625e-5f ? sum : 6.103515625e-5f;
+        for (size_t i = 0; i < top_k; ++i)
+            w[t * top_k + i] /= sum;
+    }
+    free(p);
+    free(taken);
+}
+
+void kdo_moe_permute(const int32_t* idx, size_t tokens, size_t top_k, size_t experts,
+                     int32_t* offsets, int32_t* perm) {
+    const size_t slots = tokens * top_k;
+    memset(offsets, 0, (experts + 1) * sizeof(int32_t));
+    for (size_t s = 0; s < slots; ++s)
+        offsets[idx[s] + 1] += 1;
+    for (size_t e = 0; e < experts; ++e)
+        offsets[e + 1] += offsets[e];
+    size_t position = 0;
+    for (size_t e = 0; e < experts; ++e)
+        for (size_t s = 0; s < slots; ++s)
+            if ((size_t)idx[s] == e)
+                perm[position++] = (int32_t)s;
+}
+
+static float silu(float v) {
+    return v / (1.0f + expf(-v));
+}
+
+typedef struct {
+    const uint16_t* x;
+    size_t tokens, hidden, inter, experts, top_k;
+    const uint8_t *gate_blocks, *gate_scales, *up_blocks, *up_scales, *down_blocks, *down_scales;
+    const int32_t *offsets, *perm;
+    const float* w;
+    float* contribution; /* [slots * hidden] */
+    atomic_size_t next;
+    atomic_int error;
+} moe_work;
+
+static void* moe_worker(void* arg) {
+    moe_work* m = (moe_work*)arg;
+    const size_t H = m->hidden, I = m->inter;
+    float* xrow = (float*)malloc(H * sizeof(float) * 1);
+    float* wrow = (float*)malloc((H > I ? H : I) * sizeof(float));
+    for (;;) {
+        const size_t e = atomic_fetch_add(&m->next, 1);
+        if (e >= m->experts || atomic_load(&m->error))
+            break;
+        const size_t first = (size_t)m->offsets[e], count = (size_t)m->offsets[e + 1] - first;
+        if (!count)
+            continue;
+        float* xs = (float*)malloc(count * H * sizeof(float));
+        float* g = (float*)malloc(count * I * sizeof(float));
+        float* u = (float*)malloc(count * I * sizeof(float));
+        for (size_t r = 0; r < count; ++r) {
+            const size_t token = (size_t)m->perm[first + r] / m->top_k;
+            for (size_t c = 0; c < H; ++c)
+                xs[r * H + c] = kdo_bf16_to_float(m->x[token * H + c]);
+        }
+        int rc = 0;
+        /* gate and up: [I rows x H cols] per expert */
+        for (int which = 0; which < 2 && !rc; ++which) {
+            const uint8_t* blocks = (which ? m->up_blocks : m->gate_blocks) + e * I * (H / 2);
+            const uint8_t* scales = (which ? m->up_scales : m->gate_scales) + e * I * (H / 32);
+            float* outp = which ? u : g;
+            for (size_t n = 0; n < I && !rc; ++n) {
+                rc = mxfp4_row(blocks + n * (H / 2), scales + n * (H / 32), H, wrow);
+                for (size_t r = 0; r < count && !rc; ++r) {
+                    double sum = 0.0;
+                    for (size_t c = 0; c < H; ++c)
+                        sum += (double)wrow[c] * (double)xs[r * H + c];
+                    rc = finite_to_float(sum, &outp[r * I + n]);
+                }
+            }
+        }
+        /* h = silu(g) * u, in float */
+        for (size_t i = 0; i < count * I && !rc; ++i)
+            g[i] = silu(g[i]) * u[i];
+        /* down: [H rows x I cols]; contribution = down * w[slot] */
+        const uint8_t* blocks = m->down_blocks + e * H * (I / 2);
+        const uint8_t* scales = m->down_scales + e * H * (I / 32);
+        for (size_t d = 0; d < H && !rc; ++d) {
+            rc = mxfp4_row(blocks + d * (I / 2), scales + d * (I / 32), I, wrow);
+            for (size_t r = 0; r < count && !rc; ++r) {
+                double sum = 0.0;
+                for (size_t c = 0; c < I; ++c)
+                    sum += (double)wrow[c] * (double)g[r * I + c];
+                float down = 0.0f;
+                rc = finite_to_float(sum, &down);
+                const size_t slot = (size_t)m->perm[first + r];
+                m->contribution[slot * H + d] = down * m->w[slot];
+            }
+        }
+        free(xs), free(g), free(u);
+        if (rc)
+            atomic_store(&m->error, rc);
+    }
+    free(xrow);
+    free(wrow);
+    return NULL;
+}
+
+int kdo_moe_forward(const uint16_t* x, const float* logits, size_t tokens, size_t hidden,
+                    size_t inter, size_t experts, size_t top_k,
+                    const uint8_t* gate_blocks, const uint8_t* gate_scales,
+                    const uint8_t* up_blocks, const uint8_t* up_scales,
+                    const uint8_t* down_blocks, const uint8_t* down_scales,
+                    float* y, int32_t* idx, float* w, int32_t* offsets, int32_t* perm,
+                    int threads) {
+    if (!hidden || !inter || hidden % 32 || inter % 32 || !top_k || top_k > experts || threads < 1)
+        return -1;
+    for (size_t i = 0; i < tokens * hidden; ++i)
+        if (!isfinite(kdo_bf16_to_float(x[i])))
+            return -4;
+    kdo_moe_route(logits, tokens, experts, top_k, idx, w);
+    kdo_moe_permute(idx, tokens, top_k, experts, offsets, perm);
+    float* contribution = (float*)calloc(tokens * top_k * hidden + 1, sizeof(float));
+    if (!contribution)
+        return -5;
+    moe_work work = {x, tokens, hidden, inter, experts, top_k, gate_blocks, gate_scales,
+                     up_blocks, up_scales, down_blocks, down_scales, offsets, perm, w,
+                     contribution, 0, 0};
+    pthread_t* pool = (pthread_t*)malloc(sizeof(pthread_t) * (size_t)threads);
+    int started = 0;
+    for (int t = 1; t < threads && pool; ++t)
+        if (pthread_create(&pool[started], NULL, moe_worker, &work) == 0)
+            ++started;
+    moe_worker(&work);
+    for (int t = 0; t < started; ++t)
+        pthread_join(pool[t], NULL);
+    free(pool);
+    const int rc = atomic_load(&work.error);
+    if (!rc)
+        for (size_t t = 0; t < tokens; ++t)
+            for (size_t d = 0; d < hidden; ++d) {
+                float sum = 0.0f;
+                for (size_t i = 0; i < top_k; ++i)
+                    sum += contribution[(t * top_k + i) * hidden + d];
+                y[t * hidden + d] = sum;
+            }
+    free(contribution);
+    return rc;
+}

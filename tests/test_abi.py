@@ -1,0 +1,106 @@
+"""CPU checks of the C ABI: the library loads, exports every entry point that
+include/kadan_amd.h declares, and rejects invalid arguments before any launch."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "kadan_amd.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kdq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    for expected in ["kdq_dequantize", "kdq_gemv", "kdq_gemv_batch", "kdq_gemm_q4_0",
+                     "kdq_moe_route", "kdq_moe_mxfp4", "kdq_mxfp4_dequantize"]:
+        assert expected in names
+
+
+def test_library_exports_every_declared_symbol():
+    import kadan_amd
+    lib = kadan_amd.lib()
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    # the Python wrapper binds exactly the declared set
+    assert sorted(kadan_amd.exported_symbols()) == declared_functions()
+
+
+def test_block_geometry():
+    import kadan_amd
+    lib = kadan_amd.lib()
+    assert (lib.kdq_block_values(2), lib.kdq_block_bytes(2)) == (32, 18)
+    assert (lib.kdq_block_values(8), lib.kdq_block_bytes(8)) == (32, 34)
+    assert (lib.kdq_block_values(12), lib.kdq_block_bytes(12)) == (256, 144)
+    assert lib.kdq_block_values(3) == 0
+    assert lib.kdq_row_bytes(12, 4096) == 2304
+    assert lib.kdq_row_bytes(8, 4096) == 4352
+    assert lib.kdq_row_bytes(2, 4096) == 2304
+    assert lib.kdq_row_bytes(12, 100) == 0
+
+
+def test_status_strings():
+    import kadan_amd
+    lib = kadan_amd.lib()
+    assert lib.kdq_status_string(0) == b"ok"
+    assert lib.kdq_status_string(2) == b"kdq_projection_shape"
+    assert lib.kdq_status_string(4) == b"kdq_alias"
+
+
+# Argument validation happens on the host before any HIP call, so these run without
+# a GPU: the pointers are never dereferenced.
+FAKE_W, FAKE_X, FAKE_Y = 0x10000000, 0x20000000, 0x30000000
+
+
+def test_gemv_argument_errors():
+    import kadan_amd
+    lib = kadan_amd.lib()
+    # unknown encoding
+    assert lib.kdq_gemv(3, FAKE_W, 144, FAKE_X, 1, 256, 4, FAKE_Y, 4, None, None) == 3
+    # null pointers / zero sizes
+    assert lib.kdq_gemv(12, None, 144, FAKE_X, 1, 256, 4, FAKE_Y, 4, None, None) == 1
+    assert lib.kdq_gemv(12, FAKE_W, 144, FAKE_X, 0, 256, 4, FAKE_Y, 4, None, None) == 1
+    # ragged row, short row bytes, stride < out, too many rows
+    assert lib.kdq_gemv(12, FAKE_W, 144, FAKE_X, 1, 200, 4, FAKE_Y, 4, None, None) == 2
+    assert lib.kdq_gemv(12, FAKE_W, 100, FAKE_X, 1, 256, 4, FAKE_Y, 4, None, None) == 2
+    assert lib.kdq_gemv(12, FAKE_W, 144, FAKE_X, 1, 256, 4, FAKE_Y, 3, None, None) == 2
+    assert lib.kdq_gemv(12, FAKE_W, 144, FAKE_X, 4097, 256, 4, FAKE_Y, 4, None, None) == 2
+    # output overlapping the weights or the input
+    assert lib.kdq_gemv(12, FAKE_W, 144, FAKE_X, 1, 256, 4, FAKE_W + 16, 4, None, None) == 4
+    assert lib.kdq_gemv(12, FAKE_W, 144, FAKE_X, 1, 256, 4, FAKE_X, 4, None, None) == 4
+    # misaligned activations
+    assert lib.kdq_gemv(12, FAKE_W, 144, FAKE_X + 4, 1, 256, 4, FAKE_Y, 4, None, None) == 7
+
+
+def test_batch_validates_every_job_first():
+    import kadan_amd
+    lib = kadan_amd.lib()
+    jobs = (kadan_amd.MatvecJob * 2)()
+    jobs[0] = kadan_amd.MatvecJob(FAKE_W, FAKE_X, FAKE_Y, 0, 144, 4, 256, 4, 1, 12)
+    jobs[1] = kadan_amd.MatvecJob(FAKE_W, FAKE_X, FAKE_Y + 4096, 0, 144, 4, 200, 4, 1, 12)
+    # the second job is ragged: nothing may be launched for the first one either
+    assert lib.kdq_gemv_batch(C.addressof(jobs), 2, None) == 2
+    assert lib.kdq_gemv_batch(None, 0, None) == 0
+
+
+def test_dequantize_argument_errors():
+    import kadan_amd
+    lib = kadan_amd.lib()
+    assert lib.kdq_dequantize(12, FAKE_W, 144, 1, 200, FAKE_Y, None, None) == 2
+    assert lib.kdq_dequantize(12, FAKE_W, 144, 1, 256, FAKE_Y + 4, None, None) == 7
+    assert lib.kdq_dequantize(12, FAKE_W, 144, 1, 256, FAKE_W, None, None) == 4
+
+
+def test_product_path_has_no_cpu_fallback(monkeypatch, tmp_path):
+    """Without the built library the package raises instead of computing on the CPU."""
+    import kadan_amd
+    monkeypatch.setattr(kadan_amd, "LIBRARY", str(tmp_path / "missing.so"))
+    monkeypatch.setattr(kadan_amd, "_lib", None)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        kadan_amd.lib()
