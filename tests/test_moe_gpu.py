@@ -1,0 +1,140 @@
+"""GPU parity of the MXFP4 MoE layer (kdq_moe_route, kdq_mxfp4_dequantize, kdq_moe_mxfp4).
+
+Top-k indices and the permutation must be bit-exact; routing weights and the layer
+output within rel-L2 <= 1e-3 and max-abs <= 2e-2 of the output RMS (the MoE outputs
+are far from unit scale at these distributions, so max-abs is normalised) against the
+oracle's composition of the reference pieces (double-accumulated MXFP4 products).
+"""
+import numpy as np
+import pytest
+
+from kadan_amd import synth
+from tests.util import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def no_boundary_ties(oracle, logits, top_k):
+    """True when no token has equal float probabilities across its top-k boundary (the
+    reference orders equal probabilities arbitrarily)."""
+    for row in logits:
+        m = row.max()
+        p = np.exp((row - m).astype(np.float32)).astype(np.float32)
+        p = (p.astype(np.float64) / p.astype(np.float64).sum()).astype(np.float32)
+        s = np.sort(p)[::-1]
+        if top_k < len(s) and s[top_k - 1] == s[top_k]:
+            return False
+    return True
+
+
+@pytest.mark.parametrize("tokens,experts,top_k", [(1, 32, 4), (7, 8, 2), (256, 32, 4),
+                                                  (2048, 128, 4), (300, 256, 8), (5, 4, 4)])
+def test_route_and_permutation_bit_exact(device, oracle, tokens, experts, top_k):
+    torch = _torch()
+    _, logits = synth.moe_inputs(0xC4 + tokens, tokens, 64, experts,
+                                 hot=8 if experts >= 128 else 0)
+    assert no_boundary_ties(oracle, logits, top_k)
+    idx, w = oracle.moe_route(logits, top_k)
+    offsets, perm = oracle.moe_permute(idx, experts)
+    from kadan_amd import ops
+    gi, gw, go, gp = ops.moe_route(torch.from_numpy(logits).to(device), top_k)
+    assert np.array_equal(gi.cpu().numpy(), idx)
+    assert np.array_equal(go.cpu().numpy(), offsets)
+    assert np.array_equal(gp.cpu().numpy(), perm)
+    assert_close(gw.cpu().numpy(), w, rel=1e-6, mabs=1e-5, what="routing weights")
+
+
+def test_route_equal_logits_keep_lower_expert(device):
+    torch = _torch()
+    logits = np.zeros((3, 16), np.float32)
+    logits[1, [3, 9, 12]] = 1.0
+    logits[2, :] = -np.inf
+    logits[2, 5] = 0.0
+    from kadan_amd import ops
+    gi, gw, _, _ = ops.moe_route(torch.from_numpy(logits).to(device), 4)
+    gi = gi.cpu().numpy()
+    assert list(gi[0]) == [0, 1, 2, 3]
+    assert list(gi[1]) == [3, 9, 12, 0]
+    assert list(gi[2]) == [5, 0, 1, 2]
+    np.testing.assert_allclose(gw.cpu().numpy()[0], 0.25, rtol=1e-6)
+
+
+def test_mxfp4_dequantize_bit_exact(device, oracle):
+    torch = _torch()
+    rows, cols = 64, 256
+    blocks = synth.random_bytes(5, 1, rows * cols // 2).reshape(rows, cols // 2)
+    scales = (synth.random_bytes(5, 2, rows * cols // 32) % 200 + 20).astype(np.uint8)
+    scales = scales.reshape(rows, cols // 32)
+    scales[0, 0], scales[1, 0], scales[2, 0] = 0, 254, 1  # extremes that stay finite
+    blocks[1, :16] = 0x11  # 0.5 * 2^127 values
+    rc, expected = oracle.mxfp4_decode_rows(blocks, scales, rows, cols)
+    assert rc == 0
+    from kadan_amd import ops
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    got = ops.mxfp4_dequantize(torch.from_numpy(blocks).to(device),
+                               torch.from_numpy(scales).to(device), rows, cols, status=status)
+    assert np.array_equal(got.cpu().numpy().view(np.uint32), expected.view(np.uint32))
+    assert int(status.item()) == 0
+    bad = scales.copy()
+    bad[3, 1] = 255
+    status.zero_()
+    ops.mxfp4_dequantize(torch.from_numpy(blocks).to(device), torch.from_numpy(bad).to(device),
+                         rows, cols, status=status)
+    assert int(status.item()) & 1
+
+
+def run_layer(device, oracle, tokens, hidden, inter, experts, top_k, seed, hot=0, threads=8):
+    torch = _torch()
+    x, logits = synth.moe_inputs(seed, tokens, hidden, experts, hot=hot)
+    (gb, gs), (ub, us), (db, ds) = synth.moe_weights(seed, experts, hidden, inter)
+    y, idx, w, offsets, perm = oracle.moe_forward(x, logits, top_k, gb, gs, ub, us, db, ds,
+                                                  threads=threads)
+    from kadan_amd import ops
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)
+    gy, gi, gw, go, gp = ops.moe_mxfp4(dev(x).view(torch.bfloat16), dev(logits), top_k,
+                                       dev(gb), dev(gs), dev(ub), dev(us), dev(db), dev(ds),
+                                       routing=True)
+    assert np.array_equal(gi.cpu().numpy(), idx)
+    assert np.array_equal(gp.cpu().numpy(), perm)
+    assert np.array_equal(go.cpu().numpy(), offsets)
+    assert_close(gy.cpu().numpy(), y, what=f"moe T={tokens} H={hidden} I={inter} E={experts}")
+
+
+@pytest.mark.parametrize("tokens,hidden,inter,experts,top_k", [
+    (1, 64, 64, 4, 2), (3, 128, 192, 8, 2), (37, 256, 128, 8, 4), (130, 128, 128, 4, 4),
+    (16, 2880, 2880, 32, 4),
+])
+def test_moe_layer_parity(device, oracle, tokens, hidden, inter, experts, top_k):
+    run_layer(device, oracle, tokens, hidden, inter, experts, top_k, seed=0xC4 + tokens)
+
+
+def test_moe_layer_decode_shape(device, oracle):
+    """C4 decode: gpt-oss-20b-like layer at 1 token."""
+    run_layer(device, oracle, 1, 2880, 2880, 32, 4, seed=0xC4)
+
+
+def test_moe_layer_skewed_routing(device, oracle):
+    """C5-like skew (25% of tokens favour 8 hot experts) at a size the oracle finishes."""
+    run_layer(device, oracle, 64, 256, 256, 128, 4, seed=0xC5, hot=8)
+
+
+def test_moe_prefill_256_properties(device):
+    """C4 prefill (256 tokens) at full size: determinism across calls, and permutation
+    invariance (reversing the token order reverses the output rows)."""
+    torch = _torch()
+    x, logits = synth.moe_inputs(0xC4, 256, 2880, 32)
+    (gb, gs), (ub, us), (db, ds) = synth.moe_weights(0xC4, 32, 2880, 2880)
+    from kadan_amd import ops
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)
+    wts = [dev(a) for a in (gb, gs, ub, us, db, ds)]
+    xb = dev(x).view(torch.bfloat16)
+    y1 = ops.moe_mxfp4(xb, dev(logits), 4, *wts).cpu().numpy()
+    y2 = ops.moe_mxfp4(xb, dev(logits), 4, *wts).cpu().numpy()
+    assert np.array_equal(y1, y2)
+    yr = ops.moe_mxfp4(dev(x[::-1]).view(torch.bfloat16), dev(logits[::-1]), 4, *wts)
+    assert_close(yr.cpu().numpy()[::-1], y1, rel=1e-6, mabs=1e-5, what="token order")
