@@ -1,0 +1,290 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X quantized-weight matmul path (one GPU).
+
+Headline (``value``): Q4_K GEMV weight throughput in GB/s at the Llama-3-8B FFN
+decode shape gate/up 4096 -> 14336, batch 1, with the inputs
+resident in HBM.  A "step" is one kdq_gemv launch over one weight copy; the timed
+steps rotate over 16 distinct weight copies (528 MB, twice the 256 MB Infinity Cache)
+so the cache cannot serve the weights.
+
+The same line carries
+  roofline      the GEMV kernel's algorithmic bytes / measured average launch time
+                against the 8 TB/s HBM3E peak (traffic from profiles/traffic.json,
+                the rocprofv3 FETCH_SIZE/WRITE_SIZE measurement, when present)
+  cpu_baseline  the reference CPU path on this host: kadan::text::CpuMatvec over ggml's
+                x86 quantize_row_q8_K + vec_dot_q4_K_q8_K (oracle/_ref, compiled from the
+                reference sources), on the reference worker split (64-column units,
+                clamp(cores/2, 1, 16) threads), on a bounded sample of the same workload
+  extra         the other BASELINE configurations (C1 Q8_0 GEMV, C2 down, C3 Q4_0 GEMM,
+                C4 MoE at 1 and 256 tokens, C5 MoE at 2048 skewed tokens), each timed
+                with events over back-to-back launches (median of repetitions)
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-extra] [--skip-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+FP16_PEAK_TFLOPS = 2500.0      # dense fp16/bf16 MFMA
+FP4_PEAK_TFLOPS = 10100.0      # dense MXFP4 MFMA
+Q4_K, Q8_0, Q4_0 = 12, 8, 2
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=2000)
+    p.add_argument("--warmup", type=int, default=50)
+    p.add_argument("--skip-extra", action="store_true")
+    p.add_argument("--skip-cpu", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    return p.parse_args()
+
+
+def rotated_copies(torch, base: np.ndarray, copies: int, keep: np.ndarray, seed: int):
+    """`copies` distinct device copies of packed weights: copy 0 is `base`, copy c XORs
+    every byte outside `keep` (the scale bytes) with a seeded byte stream, which keeps
+    codes uniform and leaves the scale distribution unchanged."""
+    dev = torch.device("cuda:0")
+    first = torch.from_numpy(np.ascontiguousarray(base)).to(dev)
+    out = [first]
+    mask = torch.from_numpy(np.ascontiguousarray(~keep)).to(dev)
+    g = torch.Generator(device=dev)
+    for c in range(1, copies):
+        g.manual_seed(seed * 1000 + c)
+        noise = torch.randint(0, 256, first.shape, dtype=torch.uint8, device=dev, generator=g)
+        out.append(torch.where(mask, first ^ noise, first))
+    return out
+
+
+def keep_mask(encoding: int, shape) -> np.ndarray:
+    """True for the scale bytes of each packed row (d, dmin) that must stay as generated."""
+    rows, row_bytes = shape
+    keep = np.zeros(row_bytes, bool)
+    block = {Q4_K: 144, Q8_0: 34, Q4_0: 18}[encoding]
+    head = 4 if encoding == Q4_K else 2
+    for b in range(0, row_bytes, block):
+        keep[b:b + head] = True
+    return np.broadcast_to(keep, shape).copy()
+
+
+def time_launches(torch, launch, count: int, reps: int = 1):
+    """Average ms per launch over `count` back-to-back launches, events on the launch
+    stream; median of `reps` repetitions."""
+    stream = torch.cuda.current_stream()
+    results = []
+    for _ in range(reps):
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(stream)
+        for i in range(count):
+            launch(i)
+        stop.record(stream)
+        stop.synchronize()
+        results.append(start.elapsed_time(stop) / count)
+    return statistics.median(results)
+
+
+def gemv_bytes(n_in: int, n_out: int, encoding: int) -> int:
+    from kadan_amd import row_bytes
+    return n_out * row_bytes(encoding, n_in) + 4 * n_in + 4 * n_out
+
+
+def traffic_for(workload: str):
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(workload)
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(seconds: float):
+    """Reference CPU path on a bounded sample of the C2 gate/up workload."""
+    from kadan_amd import synth
+    n_in, n_out = 4096, 14336
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count() or 1
+    threads = max(1, min(16, affinity // 2))  # IW/src/models/text/gguf_weights.cpp:615-618
+    w = synth.q4_k_weights(0xC2A, n_out, n_in)
+    x = synth.normal(0xC2A, 50, n_in).reshape(1, n_in)
+    import oracle
+    if oracle.Reference.available():
+        impl, kind = oracle.Reference(), "reference"
+    else:
+        impl, kind = oracle.Oracle(), "port"
+    impl.cpu_matvec(Q4_K, w, x, n_in, n_out, threads)  # warm-up
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        impl.cpu_matvec(Q4_K, w, x, n_in, n_out, threads)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {
+        "value": round(gemv_bytes(n_in, n_out, Q4_K) / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": kind,
+        "sample": (f"{len(times)} runs (median) of the C2 gate/up Q4_K matvec 4096->14336, "
+                   f"batch 1: quantize_row_q8_K + vec_dot_q4_K_q8_K via CpuMatvec, "
+                   f"64-column units on {threads} threads of {affinity} available"),
+    }
+
+
+def bench_gemv(torch, encoding, n_in, n_out, steps, warmup, seed, copies=16):
+    from kadan_amd import ops, synth
+    w = synth.gguf_weights(encoding, seed, n_out, n_in)
+    ws = rotated_copies(torch, w, copies, keep_mask(encoding, w.shape), seed)
+    x = torch.from_numpy(synth.normal(seed, 50, n_in).reshape(1, n_in)).cuda()
+    y = torch.empty(1, n_out, device="cuda")
+    launch = lambda i: ops.gemv(encoding, ws[i % copies], x, n_out, out=y)
+    for i in range(warmup):
+        launch(i)
+    return time_launches(torch, launch, steps)
+
+
+def bench_gemm(torch, reps=10, count=20):
+    from kadan_amd import ops, synth
+    m, k, n = 512, 4096, 14336
+    w = synth.q4_0_weights(0xC3, n, k)
+    ws = rotated_copies(torch, w, 16, keep_mask(Q4_0, w.shape), 0xC3)
+    x = torch.from_numpy(synth.normal(0xC3, 9, m * k).reshape(m, k).astype(np.float16)).cuda()
+    y = torch.empty(m, n, dtype=torch.float16, device="cuda")
+    launch = lambda i: ops.gemm_q4_0(ws[i % 16], x, n, out=y)
+    for i in range(5):
+        launch(i)
+    ms = time_launches(torch, launch, count, reps)
+    flops = 2.0 * m * k * n
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"workload": "C3 Q4_0 GEMM M512 K4096 N14336 (fp16 out)", "ms": round(ms, 4),
+            "tflops": round(tflops, 2), "mfma_peak_tflops": FP16_PEAK_TFLOPS,
+            "mfma_frac": round(tflops / FP16_PEAK_TFLOPS, 4),
+            "note": "per launch: activation quantize + fp16-MFMA GEMM"}
+
+
+def moe_bytes(tokens, hidden, inter, experts_touched):
+    per_expert = 3 * inter * hidden // 2 + 3 * inter * hidden // 32
+    return experts_touched * per_expert + tokens * hidden * 2 + tokens * hidden * 4
+
+
+def bench_moe(torch, tokens, experts, hot, seed, copies, reps=10, count=10):
+    from kadan_amd import ops, synth
+    hidden = inter = 2880
+    top_k = 4
+    x, logits = synth.moe_inputs(seed, tokens, hidden, experts, hot=hot)
+    (gb, gs), (ub, us), (db, ds) = synth.moe_weights(seed, experts, hidden, inter)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    sets = []
+    for c in range(copies):
+        arrays = [dev(a) for a in (gb, gs, ub, us, db, ds)]
+        if c:
+            g = torch.Generator(device="cuda")
+            g.manual_seed(seed + c)
+            for i in (0, 2, 4):  # code bytes only; scales unchanged
+                arrays[i] ^= torch.randint(0, 256, arrays[i].shape, dtype=torch.uint8,
+                                           device="cuda", generator=g)
+        sets.append(arrays)
+    del gb, gs, ub, us, db, ds
+    xb = dev(x).view(torch.bfloat16)
+    lg = dev(logits)
+    y = torch.empty(tokens, hidden, device="cuda")
+    launch = lambda i: ops.moe_mxfp4(xb, lg, top_k, *sets[i % copies], out=y)
+    for i in range(3):
+        launch(i)
+    ms = time_launches(torch, launch, count, reps)
+    touched = len(np.unique(_route_host(logits, top_k)))
+    nbytes = moe_bytes(tokens, hidden, inter, touched)
+    flops = 2.0 * tokens * top_k * 3 * hidden * inter
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    tflops = flops / (ms * 1e-3) / 1e12
+    del sets
+    torch.cuda.empty_cache()
+    return {"workload": f"MXFP4 MoE H=I=2880 E={experts} top-4 T={tokens}" + (" skewed" if hot else ""),
+            "ms": round(ms, 4), "tokens_per_s": round(tokens / (ms * 1e-3), 1),
+            "experts_touched": int(touched), "algorithmic_bytes": int(nbytes),
+            "gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "tflops": round(tflops, 2),
+            "fp4_mfma_frac": round(tflops / FP4_PEAK_TFLOPS, 5),
+            "bf16_mfma_frac": round(tflops / FP16_PEAK_TFLOPS, 4),
+            "note": "products on bf16 MFMA over exactly dequantised FP4 weights"}
+
+
+def _route_host(logits, top_k):
+    """Experts touched by a routing (argsort on logits; only counts distinct experts)."""
+    return np.argsort(-logits, axis=1, kind="stable")[:, :top_k]
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only (the path runs on one "
+                          "MI355X with no sharding); run with --gpus 1"}))
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(1)
+    import kadan_amd
+    kadan_amd.lib()
+
+    n_in, n_out = 4096, 14336
+    ms = bench_gemv(torch, Q4_K, n_in, n_out, args.steps, args.warmup, 0xC2A)
+    nbytes = gemv_bytes(n_in, n_out, Q4_K)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    workload = "C2 Q4_K GEMV 4096->14336 batch 1"
+    result = {
+        "metric": "Q4_K GEMV weight GB/s (% HBM peak); MXFP4 MoE layer tokens/s (% MFMA peak)",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k x f32 (int8 dot4, f32 accumulate)",
+        "data": "synthetic (seeded SplitMix64 GGUF blocks, 16 rotated weight copies)",
+        "config": {"workload": workload, "n_in": n_in, "n_out": n_out, "batch": 1,
+                   "weight_copies": 16},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_for(workload),
+                     "algorithmic_bytes": nbytes},
+    }
+    if not args.skip_extra:
+        extra = {}
+        for name, enc, a, b, seed in (("c1_q8_0_gemv_4096x4096", Q8_0, 4096, 4096, 0xC1),
+                                      ("c2_q4_k_gemv_14336_to_4096", Q4_K, 14336, 4096, 0xC2B)):
+            t = bench_gemv(torch, enc, a, b, 500, 20, seed)
+            nb = gemv_bytes(a, b, enc)
+            extra[name] = {"ms": round(t, 6), "gbs": round(nb / (t * 1e-3) / 1e9, 1),
+                           "hbm_frac": round(nb / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        extra["c3_q4_0_gemm"] = bench_gemm(torch)
+        extra["c4_moe_t1"] = bench_moe(torch, 1, 32, 0, 0xC4, copies=2, count=50)
+        extra["c4_moe_t256"] = bench_moe(torch, 256, 32, 0, 0xC4, copies=2)
+        extra["c5_moe_t2048_skewed"] = bench_moe(torch, 2048, 128, 8, 0xC5, copies=1, reps=5,
+                                                 count=5)
+        result["extra"] = extra
+    if not args.skip_cpu:
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()
