@@ -1,0 +1,155 @@
+// kadan_amd host C++ layer: the GGUF / MXFP4 part of the reference worker's projection
+// interface kadan::DenseCompute (IW/include/kadan/dense_compute.hpp:60-342, IW =
+// services/hikari/inference_worker), implemented over the C ABI of kadan_amd.h.
+//
+// The types below restate the reference's (same names, members and meaning) so the
+// model code that calls DenseCompute needs no change: a kadan::DenseCompute subclass
+// forwards its GGUF virtuals to HipDenseCompute (INTEGRATION.md shows the adapter).
+// Contract, as the reference states it (dense_compute.hpp:58-59,174-179,215-218):
+//   * host spans are borrowed: owned by the caller until return, never retained;
+//   * every call is synchronous: all device work and source callbacks finish first;
+//   * `unsupported` is returned before any source read or output write;
+//   * execution failures throw std::runtime_error and are never retried.
+#pragma once
+
+#include <atomic>
+#include <cstddef>
+#include <cstdint>
+#include <functional>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <optional>
+#include <span>
+#include <tuple>
+#include <vector>
+
+namespace kadan_amd {
+
+// IW/include/kadan/dense_compute.hpp:44-56
+enum class ProjectionResult { unsupported, unvalidated, finite };
+
+// IW/include/kadan/weight_identity.hpp:7-19
+struct WeightIdentity {
+    std::uint64_t device = 0;
+    std::uint64_t inode = 0;
+    std::uint64_t file_size = 0;
+    std::uint64_t modified_seconds = 0;
+    std::uint64_t modified_nanoseconds = 0;
+    std::uint64_t changed_seconds = 0;
+    std::uint64_t changed_nanoseconds = 0;
+    std::uint64_t payload_begin = 0;
+    std::uint64_t payload_end = 0;
+
+    auto operator<=>(const WeightIdentity&) const = default;
+};
+
+namespace gguf {
+// IW/include/kadan/gguf_quantization.hpp:16-27, plus q4_0 (GGML type 2), which the
+// reference has no encoding for.  Only q4_0, q8_0 and q4_k run on this implementation.
+enum class Encoding { q3_k, q4_k, q8_0, q6_k, iq3_xxs, iq4_nl, iq4_xs, iq2_s, iq3_s, bf16, q4_0 };
+
+// GGML type id -> encoding (IW/include/kadan/gguf_quantization.hpp:30-55, plus type 2).
+std::optional<Encoding> encoding(std::uint32_t ggml_type);
+bool supported(Encoding);                 // runs on this implementation
+std::size_t block_values(Encoding);      // gguf_quantization.hpp:65-69 (+ q4_0: 32)
+std::size_t block_bytes(Encoding);       // gguf_quantization.hpp:71-95 (+ q4_0: 18)
+}  // namespace gguf
+
+class HipDenseCompute {
+public:
+    // IW/include/kadan/dense_compute.hpp:170-172: whole packed rows; first is a row.
+    using GgufWeightSource = std::function<void(std::size_t, std::span<std::byte>)>;
+
+    // IW/include/kadan/dense_compute.hpp:197,201
+    static constexpr std::size_t gguf_batch_rows = 8;
+    static constexpr std::size_t gguf_batch_max_rows = 4096;
+
+    // IW/include/kadan/dense_compute.hpp:205-213
+    struct GgufBatchJob {
+        const WeightIdentity* identity;
+        std::optional<gguf::Encoding> encoding;
+        const GgufWeightSource* source;
+        std::span<const float> input;
+        std::size_t in, out;
+        std::span<float> output;
+        bool retain_misses;
+    };
+
+    // One MXFP4 expert tensor set in the GPT-OSS layout (IW/include/kadan/checkpoint.hpp:
+    // 151-163): gate/up [experts, inter, hidden/2] + scales [experts, inter, hidden/32],
+    // down [experts, hidden, inter/2] + scales [experts, hidden, inter/32].
+    struct Mxfp4Experts {
+        const WeightIdentity* identity;  // bank key of the whole set
+        std::size_t experts, hidden, inter;
+        std::span<const std::uint8_t> gate_blocks, gate_scales, up_blocks, up_scales,
+            down_blocks, down_scales;
+    };
+
+    explicit HipDenseCompute(int device = 0);
+    ~HipDenseCompute();
+    HipDenseCompute(const HipDenseCompute&) = delete;
+    HipDenseCompute& operator=(const HipDenseCompute&) = delete;
+
+    // IW/include/kadan/dense_compute.hpp:180-194.  Rows <= gguf_batch_rows run the
+    // decode-time product; more rows run it per group of gguf_batch_rows.  Bias is added
+    // to every output row.  `precise` is accepted for interface parity (fp32 products).
+    ProjectionResult dense_gguf_source(const WeightIdentity&, gguf::Encoding,
+                                       const GgufWeightSource&, std::span<const float> bias,
+                                       std::span<const float> input, std::size_t in,
+                                       std::size_t out, std::span<float> output,
+                                       const std::atomic_bool& cancel, bool precise = false,
+                                       bool retain_misses = true);
+
+    // IW/include/kadan/dense_compute.hpp:215-221: every job in one synchronous
+    // submission; jobs sharing an input span upload it once.  Returns unvalidated (the
+    // caller checks finiteness, IW/src/models/text/gguf_weights.cpp:478-484).
+    ProjectionResult dense_gguf_batch(std::span<const GgufBatchJob>, const std::atomic_bool&);
+
+    // Prefill with quantized activations (no reference device counterpart: the reference's
+    // CPU path, IW/src/models/text/cpu_matvec.cpp:28-66, quantizes activations the same
+    // way).  Q4_0 weights only; fp16 inputs [rows x in] -> fp16 outputs [rows x out].
+    ProjectionResult dense_gguf_q8_source(const WeightIdentity&, gguf::Encoding,
+                                          const GgufWeightSource&,
+                                          std::span<const std::uint16_t> input_f16,
+                                          std::size_t in, std::size_t out,
+                                          std::span<std::uint16_t> output_f16,
+                                          const std::atomic_bool& cancel);
+
+    // The MXFP4 MoE layer (MoeLayer::forward semantics, IW/src/models/text/qwen_layers.cpp:
+    // 378-492, no shared expert).  x: bf16 [tokens x hidden]; logits fp32 [tokens x experts];
+    // output fp32 [tokens x hidden]; selected/weights [tokens x top_k] are optional.
+    ProjectionResult moe_mxfp4(const Mxfp4Experts&, std::span<const std::uint16_t> x_bf16,
+                               std::span<const float> logits, std::size_t tokens,
+                               std::size_t top_k, std::span<float> output,
+                               std::span<std::int32_t> selected, std::span<float> weights,
+                               const std::atomic_bool& cancel);
+
+    // IW/include/kadan/dense_compute.hpp:72-80: retire these identities from the bank.
+    std::size_t release_weights(std::span<const WeightIdentity>);
+    // Device bytes held by the weight bank.
+    std::size_t retained_weight_bytes() const;
+    // IW/include/kadan/dense_compute.hpp:63-66: release scratch (workspace) memory.
+    void release_scratch();
+
+private:
+    struct Resident;
+    using BankKey = std::tuple<WeightIdentity, int, std::size_t, std::size_t>;
+
+    const Resident& weights_for(const WeightIdentity&, gguf::Encoding, std::size_t in,
+                                std::size_t out, const GgufWeightSource&, bool retain,
+                                const std::atomic_bool& cancel,
+                                std::unique_ptr<Resident>& transient);
+    void* device_buffer(std::size_t slot, std::size_t bytes);
+    void synchronize();
+
+    int device_;
+    void* stream_ = nullptr;
+    mutable std::mutex mutex_;
+    std::map<BankKey, std::unique_ptr<Resident>> bank_;
+    std::vector<std::pair<void*, std::size_t>> buffers_;  // reusable device scratch
+    void* pinned_ = nullptr;
+    std::size_t pinned_bytes_ = 0;
+};
+
+}  // namespace kadan_amd

@@ -21,6 +21,8 @@ DEVICE_SOURCES = ["capi.hip", "gguf_gemv.hip", "q4_0_gemm.hip", "moe_mxfp4.hip"]
 HOST_SOURCES = ["hip_dense_compute.cpp"]
 LIBRARY = os.path.join(PACKAGE, "libkadan_amd.so")
 HOST_LIBRARY = os.path.join(PACKAGE, "libkadan_amd_host.so")
+PROBE_SOURCE = os.path.join(ROOT, "tests", "cpp", "dense_compute_probe.cpp")
+PROBE_LIBRARY = os.path.join(ROOT, "tests", "cpp", "libdense_compute_probe.so")
 
 # gfx950 only.  Packed-fp32 instructions are disabled (the compiler would otherwise
 # form v_pk_*_f32 from scalar float code).  No FMA contraction: every fused
@@ -69,6 +71,13 @@ def build(verbose: bool = False) -> str:
     _run([HIPCC, "-shared", "-fPIC", "-o", tmp, *host_objects, "-L", PACKAGE,
           "-lkadan_amd", "-Wl,-rpath,$ORIGIN"])
     os.replace(tmp, HOST_LIBRARY)
+    # the tests' C shim over the host layer (tests/cpp), built here so no test compiles
+    if os.path.exists(PROBE_SOURCE):
+        tmp = PROBE_LIBRARY + ".tmp"
+        _run([HIPCC, "-O2", "-std=c++20", "-fPIC", "-Wall", "-shared", "-I", INCLUDE,
+              PROBE_SOURCE, "-o", tmp, "-L", PACKAGE, "-lkadan_amd_host", "-lkadan_amd",
+              "-Wl,-rpath,$ORIGIN/../../kadan_amd"])
+        os.replace(tmp, PROBE_LIBRARY)
     return LIBRARY
 
 

@@ -1,2 +1,516 @@
-// Host C++ layer (placeholder until the DenseCompute mirror lands).
+// kadan_amd::HipDenseCompute: the DenseCompute-compatible host layer over the C ABI.
+// Restates the reference's validation and result contract (IW/src/cuda/h3_compute.cu:
+// 1760-1830 validate/alias checks, :3503-3536 dense_gguf_source, :3963-4375
+// dense_gguf_batch; IW = services/hikari/inference_worker) on one HIP stream.
+#include "kadan_amd_dense_compute.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+#include <cmath>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+
 #include "kadan_amd.h"
+
+namespace kadan_amd {
+namespace {
+
+void require(bool ok, const char* what) {
+    if (!ok)
+        throw std::runtime_error(what);
+}
+
+void hip_check(hipError_t e) {
+    if (e != hipSuccess)
+        throw std::runtime_error(std::string("kdq_hip: ") + hipGetErrorString(e));
+}
+
+void kdq_check(int status) {
+    if (status == KDQ_OK)
+        return;
+    std::string what = kdq_status_string(status);
+    if (status == KDQ_ERR_HIP)
+        what += std::string(": ") + kdq_last_hip_error();
+    throw std::runtime_error(what);
+}
+
+int ggml_type(gguf::Encoding e) {
+    switch (e) {
+    case gguf::Encoding::q4_0:
+        return KDQ_Q4_0;
+    case gguf::Encoding::q8_0:
+        return KDQ_Q8_0;
+    case gguf::Encoding::q4_k:
+        return KDQ_Q4_K;
+    default:
+        return -1;
+    }
+}
+
+bool overlap(const void* a, std::size_t an, const void* b, std::size_t bn) {
+    if (!an || !bn)
+        return false;
+    const auto x = reinterpret_cast<std::uintptr_t>(a), y = reinterpret_cast<std::uintptr_t>(b);
+    return x <= y ? y - x < an : x - y < bn;
+}
+
+template <class T, class U> bool overlap(std::span<T> a, std::span<U> b) {
+    return overlap(a.data(), a.size_bytes(), b.data(), b.size_bytes());
+}
+
+// Whole packed rows cross the host boundary through at most this much pinned staging
+// (IW/include/kadan/device_placement.hpp:111).
+constexpr std::size_t kStagingBytes = std::size_t(16) << 20;
+
+std::size_t align16(std::size_t n) {
+    return (n + 15) & ~std::size_t(15);
+}
+
+}  // namespace
+
+namespace gguf {
+
+std::optional<Encoding> encoding(std::uint32_t ggml_type) {
+    switch (ggml_type) {
+    case 2:
+        return Encoding::q4_0;
+    case 8:
+        return Encoding::q8_0;
+    case 11:
+        return Encoding::q3_k;
+    case 12:
+        return Encoding::q4_k;
+    case 14:
+        return Encoding::q6_k;
+    case 18:
+        return Encoding::iq3_xxs;
+    case 20:
+        return Encoding::iq4_nl;
+    case 21:
+        return Encoding::iq3_s;
+    case 22:
+        return Encoding::iq2_s;
+    case 23:
+        return Encoding::iq4_xs;
+    case 30:
+        return Encoding::bf16;
+    default:
+        return std::nullopt;
+    }
+}
+
+bool supported(Encoding e) {
+    return e == Encoding::q4_0 || e == Encoding::q8_0 || e == Encoding::q4_k;
+}
+
+std::size_t block_values(Encoding e) {
+    switch (e) {
+    case Encoding::bf16:
+        return 1;
+    case Encoding::q8_0:
+    case Encoding::iq4_nl:
+    case Encoding::q4_0:
+        return 32;
+    default:
+        return 256;
+    }
+}
+
+std::size_t block_bytes(Encoding e) {
+    switch (e) {
+    case Encoding::q3_k:
+        return 110;
+    case Encoding::q4_k:
+        return 144;
+    case Encoding::q8_0:
+        return 34;
+    case Encoding::q6_k:
+        return 210;
+    case Encoding::iq3_xxs:
+        return 98;
+    case Encoding::iq4_nl:
+        return 18;
+    case Encoding::iq4_xs:
+        return 136;
+    case Encoding::iq2_s:
+        return 82;
+    case Encoding::iq3_s:
+        return 110;
+    case Encoding::bf16:
+        return 2;
+    case Encoding::q4_0:
+        return 18;
+    }
+    return 0;
+}
+
+}  // namespace gguf
+
+struct HipDenseCompute::Resident {
+    void* device = nullptr;
+    std::size_t bytes = 0, row_bytes = 0;
+    ~Resident() {
+        if (device)
+            (void)hipFree(device);
+    }
+};
+
+HipDenseCompute::HipDenseCompute(int device) : device_(device) {
+    hip_check(hipSetDevice(device));
+    hipStream_t s = nullptr;
+    hip_check(hipStreamCreate(&s));  // default priority
+    stream_ = s;
+}
+
+HipDenseCompute::~HipDenseCompute() {
+    (void)hipSetDevice(device_);
+    if (stream_)
+        (void)hipStreamSynchronize(static_cast<hipStream_t>(stream_));
+    bank_.clear();
+    for (auto& b : buffers_)
+        if (b.first)
+            (void)hipFree(b.first);
+    if (pinned_)
+        (void)hipHostFree(pinned_);
+    if (stream_)
+        (void)hipStreamDestroy(static_cast<hipStream_t>(stream_));
+}
+
+void HipDenseCompute::synchronize() {
+    hip_check(hipStreamSynchronize(static_cast<hipStream_t>(stream_)));
+}
+
+void* HipDenseCompute::device_buffer(std::size_t slot, std::size_t bytes) {
+    if (buffers_.size() <= slot)
+        buffers_.resize(slot + 1, {nullptr, 0});
+    auto& b = buffers_[slot];
+    if (b.second < bytes) {
+        synchronize();
+        if (b.first)
+            hip_check(hipFree(b.first));
+        b = {nullptr, 0};
+        const std::size_t grown = std::max<std::size_t>(bytes, 1 << 20);
+        hip_check(hipMalloc(&b.first, grown));
+        b.second = grown;
+    }
+    return b.first;
+}
+
+const HipDenseCompute::Resident& HipDenseCompute::weights_for(
+    const WeightIdentity& identity, gguf::Encoding enc, std::size_t in, std::size_t out,
+    const GgufWeightSource& source, bool retain, const std::atomic_bool& cancel,
+    std::unique_ptr<Resident>& transient) {
+    const BankKey key{identity, int(enc), in, out};
+    if (auto it = bank_.find(key); it != bank_.end())
+        return *it->second;
+    const std::size_t row_bytes = in / gguf::block_values(enc) * gguf::block_bytes(enc);
+    auto r = std::make_unique<Resident>();
+    r->row_bytes = row_bytes;
+    r->bytes = out * row_bytes;
+    hip_check(hipMalloc(&r->device, r->bytes));
+    const std::size_t rows_per_chunk = std::max<std::size_t>(1, kStagingBytes / row_bytes);
+    const std::size_t chunk_bytes = std::min(out, rows_per_chunk) * row_bytes;
+    if (pinned_bytes_ < chunk_bytes) {
+        if (pinned_)
+            hip_check(hipHostFree(pinned_));
+        pinned_ = nullptr;
+        pinned_bytes_ = 0;
+        hip_check(hipHostMalloc(&pinned_, chunk_bytes, hipHostMallocDefault));
+        pinned_bytes_ = chunk_bytes;
+    }
+    auto* bytes = static_cast<std::byte*>(pinned_);
+    for (std::size_t first = 0; first < out; first += rows_per_chunk) {
+        require(!cancel.load(), "kdq_cancelled");
+        const std::size_t n = std::min(rows_per_chunk, out - first);
+        source(first, std::span<std::byte>(bytes, n * row_bytes));
+        hip_check(hipMemcpyAsync(static_cast<std::uint8_t*>(r->device) + first * row_bytes,
+                                 pinned_, n * row_bytes, hipMemcpyHostToDevice,
+                                 static_cast<hipStream_t>(stream_)));
+        synchronize();  // the staging buffer is reused by the next chunk
+    }
+    if (!retain) {
+        transient = std::move(r);
+        return *transient;
+    }
+    auto& slot = bank_[key];
+    slot = std::move(r);
+    return *slot;
+}
+
+ProjectionResult HipDenseCompute::dense_gguf_source(
+    const WeightIdentity& identity, gguf::Encoding enc, const GgufWeightSource& source,
+    std::span<const float> bias, std::span<const float> input, std::size_t in, std::size_t out,
+    std::span<float> output, const std::atomic_bool& cancel, bool precise, bool retain_misses) {
+    (void)precise;  // products are fp32 either way
+    std::lock_guard<std::mutex> lock(mutex_);
+    if (!gguf::supported(enc) || !in || in % gguf::block_values(enc) || in % 8)
+        return ProjectionResult::unsupported;
+    require(!cancel.load(), "kdq_cancelled");
+    require(in && out && in <= std::size_t(INT_MAX) && out <= std::size_t(INT_MAX) &&
+                !input.empty() && input.size() % in == 0 &&
+                output.size() == input.size() / in * out && (bias.empty() || bias.size() == out),
+            "kdq_projection_shape");
+    for (float v : input)
+        require(std::isfinite(v), "kdq_nonfinite_input");
+    for (float v : bias)
+        require(std::isfinite(v), "kdq_nonfinite_bias");
+    require(!overlap(output, input) && !overlap(output, bias), "kdq_alias");
+    hip_check(hipSetDevice(device_));
+    const std::size_t rows = input.size() / in;
+    std::unique_ptr<Resident> transient;
+    const Resident& w = weights_for(identity, enc, in, out, source, retain_misses, cancel, transient);
+    auto st = static_cast<hipStream_t>(stream_);
+    auto* dx = static_cast<float*>(device_buffer(0, rows * in * sizeof(float)));
+    auto* dy = static_cast<float*>(device_buffer(1, rows * out * sizeof(float)));
+    auto* dstatus = static_cast<unsigned*>(device_buffer(2, 256));
+    hip_check(hipMemsetAsync(dstatus, 0, sizeof(unsigned), st));
+    hip_check(hipMemcpyAsync(dx, input.data(), input.size_bytes(), hipMemcpyHostToDevice, st));
+    for (std::size_t first = 0; first < rows; first += gguf_batch_max_rows) {
+        require(!cancel.load(), "kdq_cancelled");
+        const std::size_t n = std::min(gguf_batch_max_rows, rows - first);
+        kdq_check(kdq_gemv(ggml_type(enc), w.device, w.row_bytes, dx + first * in, n, in, out,
+                           dy + first * out, out, dstatus, st));
+    }
+    unsigned status = 0;
+    hip_check(hipMemcpyAsync(output.data(), dy, output.size_bytes(), hipMemcpyDeviceToHost, st));
+    hip_check(hipMemcpyAsync(&status, dstatus, sizeof status, hipMemcpyDeviceToHost, st));
+    synchronize();
+    require(status == 0, "kdq_nonfinite_weight");
+    bool finite = true;
+    for (std::size_t r = 0; r < rows; ++r)
+        for (std::size_t c = 0; c < out; ++c) {
+            float& v = output[r * out + c];
+            if (!bias.empty())
+                v += bias[c];
+            finite = finite && std::isfinite(v);
+        }
+    return finite ? ProjectionResult::finite : ProjectionResult::unvalidated;
+}
+
+ProjectionResult HipDenseCompute::dense_gguf_batch(std::span<const GgufBatchJob> jobs,
+                                                   const std::atomic_bool& cancel) {
+    std::lock_guard<std::mutex> lock(mutex_);
+    // Eligibility of IW/include/kadan/gguf_batch_partition.hpp:15-37, restricted to the
+    // encodings this implementation runs; decided before any source read.
+    if (jobs.empty())
+        return ProjectionResult::unsupported;
+    for (const auto& j : jobs) {
+        if (!j.identity || !j.source || !j.in || !j.out || j.in > std::size_t(INT_MAX) ||
+            j.out > std::size_t(INT_MAX) || j.input.empty() || j.input.size() % j.in ||
+            j.input.size() / j.in > gguf_batch_max_rows ||
+            j.output.size() != j.input.size() / j.in * j.out || !j.encoding ||
+            !gguf::supported(*j.encoding) || j.in % gguf::block_values(*j.encoding) ||
+            j.in / gguf::block_values(*j.encoding) > kStagingBytes / gguf::block_bytes(*j.encoding) ||
+            j.in % 8)
+            return ProjectionResult::unsupported;
+    }
+    require(!cancel.load(), "kdq_cancelled");
+    for (const auto& j : jobs) {
+        for (float v : j.input)
+            require(std::isfinite(v), "kdq_nonfinite_input");
+        for (const auto& k : jobs)
+            require(!overlap(j.output, k.input), "kdq_alias");
+    }
+    hip_check(hipSetDevice(device_));
+    auto st = static_cast<hipStream_t>(stream_);
+    std::vector<std::unique_ptr<Resident>> transients(jobs.size());
+    std::vector<const Resident*> weights(jobs.size());
+    for (std::size_t i = 0; i < jobs.size(); ++i)
+        weights[i] = &weights_for(*jobs[i].identity, *jobs[i].encoding, jobs[i].in, jobs[i].out,
+                                  *jobs[i].source, jobs[i].retain_misses, cancel, transients[i]);
+    // One upload of each distinct input span, one device output region per job.
+    std::vector<std::size_t> input_at(jobs.size()), output_at(jobs.size());
+    std::size_t in_bytes = 0, out_bytes = 0;
+    for (std::size_t i = 0; i < jobs.size(); ++i) {
+        std::size_t same = i;
+        for (std::size_t k = 0; k < i; ++k)
+            if (jobs[k].input.data() == jobs[i].input.data() &&
+                jobs[k].input.size() == jobs[i].input.size()) {
+                same = k;
+                break;
+            }
+        if (same != i) {
+            input_at[i] = input_at[same];
+        } else {
+            input_at[i] = in_bytes;
+            in_bytes += align16(jobs[i].input.size_bytes());
+        }
+        output_at[i] = out_bytes;
+        out_bytes += align16(jobs[i].output.size_bytes());
+    }
+    auto* dx = static_cast<std::uint8_t*>(device_buffer(0, in_bytes));
+    auto* dy = static_cast<std::uint8_t*>(device_buffer(1, out_bytes));
+    auto* dstatus = static_cast<unsigned*>(device_buffer(2, 256));
+    hip_check(hipMemsetAsync(dstatus, 0, sizeof(unsigned), st));
+    std::vector<kdq_matvec_job> table(jobs.size());
+    for (std::size_t i = 0; i < jobs.size(); ++i) {
+        const auto& j = jobs[i];
+        bool first_use = true;
+        for (std::size_t k = 0; k < i; ++k)
+            first_use = first_use && input_at[k] != input_at[i];
+        if (first_use)
+            hip_check(hipMemcpyAsync(dx + input_at[i], j.input.data(), j.input.size_bytes(),
+                                     hipMemcpyHostToDevice, st));
+        table[i] = kdq_matvec_job{weights[i]->device,
+                                  reinterpret_cast<const float*>(dx + input_at[i]),
+                                  reinterpret_cast<float*>(dy + output_at[i]),
+                                  dstatus,
+                                  weights[i]->row_bytes,
+                                  j.out,
+                                  std::uint32_t(j.in),
+                                  std::uint32_t(j.out),
+                                  std::uint32_t(j.input.size() / j.in),
+                                  ggml_type(*j.encoding)};
+    }
+    require(!cancel.load(), "kdq_cancelled");
+    kdq_check(kdq_gemv_batch(table.data(), table.size(), st));
+    for (std::size_t i = 0; i < jobs.size(); ++i)
+        hip_check(hipMemcpyAsync(jobs[i].output.data(), dy + output_at[i],
+                                 jobs[i].output.size_bytes(), hipMemcpyDeviceToHost, st));
+    unsigned status = 0;
+    hip_check(hipMemcpyAsync(&status, dstatus, sizeof status, hipMemcpyDeviceToHost, st));
+    synchronize();
+    require(status == 0, "kdq_nonfinite_weight");
+    return ProjectionResult::unvalidated;
+}
+
+ProjectionResult HipDenseCompute::dense_gguf_q8_source(
+    const WeightIdentity& identity, gguf::Encoding enc, const GgufWeightSource& source,
+    std::span<const std::uint16_t> input, std::size_t in, std::size_t out,
+    std::span<std::uint16_t> output, const std::atomic_bool& cancel) {
+    std::lock_guard<std::mutex> lock(mutex_);
+    if (enc != gguf::Encoding::q4_0 || !in || in % 256)
+        return ProjectionResult::unsupported;
+    require(!cancel.load(), "kdq_cancelled");
+    require(out && in <= std::size_t(INT_MAX) && out <= std::size_t(INT_MAX) && !input.empty() &&
+                input.size() % in == 0 && output.size() == input.size() / in * out,
+            "kdq_projection_shape");
+    require(!overlap(output, input), "kdq_alias");
+    hip_check(hipSetDevice(device_));
+    const std::size_t rows = input.size() / in;
+    std::unique_ptr<Resident> transient;
+    const Resident& w = weights_for(identity, enc, in, out, source, true, cancel, transient);
+    auto st = static_cast<hipStream_t>(stream_);
+    auto* dx = static_cast<std::uint16_t*>(device_buffer(0, input.size_bytes()));
+    auto* dy = static_cast<std::uint16_t*>(device_buffer(1, output.size_bytes()));
+    hip_check(hipMemcpyAsync(dx, input.data(), input.size_bytes(), hipMemcpyHostToDevice, st));
+    kdq_check(kdq_gemm_q4_0(w.device, out, in, dx, rows, dy, st));
+    hip_check(hipMemcpyAsync(output.data(), dy, output.size_bytes(), hipMemcpyDeviceToHost, st));
+    synchronize();
+    return ProjectionResult::unvalidated;
+}
+
+ProjectionResult HipDenseCompute::moe_mxfp4(const Mxfp4Experts& e,
+                                            std::span<const std::uint16_t> x,
+                                            std::span<const float> logits, std::size_t tokens,
+                                            std::size_t top_k, std::span<float> output,
+                                            std::span<std::int32_t> selected,
+                                            std::span<float> weights,
+                                            const std::atomic_bool& cancel) {
+    std::lock_guard<std::mutex> lock(mutex_);
+    if (!e.identity || !e.experts || e.experts > 256 || !e.hidden || !e.inter ||
+        e.hidden % 64 || e.inter % 64 || !top_k || top_k > 8 || top_k > e.experts || !tokens)
+        return ProjectionResult::unsupported;
+    require(!cancel.load(), "kdq_cancelled");
+    const std::size_t E = e.experts, H = e.hidden, I = e.inter;
+    require(e.gate_blocks.size() == E * I * H / 2 && e.up_blocks.size() == E * I * H / 2 &&
+                e.gate_scales.size() == E * I * H / 32 && e.up_scales.size() == E * I * H / 32 &&
+                e.down_blocks.size() == E * H * I / 2 && e.down_scales.size() == E * H * I / 32 &&
+                x.size() == tokens * H && logits.size() == tokens * E &&
+                output.size() == tokens * H &&
+                (selected.empty() || selected.size() == tokens * top_k) &&
+                (weights.empty() || weights.size() == tokens * top_k),
+            "kdq_projection_shape");
+    for (float v : logits)
+        require(std::isfinite(v), "kdq_nonfinite_input");
+    require(!overlap(output, x) && !overlap(output, logits), "kdq_alias");
+    hip_check(hipSetDevice(device_));
+    auto st = static_cast<hipStream_t>(stream_);
+    // The expert set lives in the bank as one allocation: six arrays, 256-byte aligned.
+    const std::span<const std::uint8_t> parts[6] = {e.gate_blocks, e.gate_scales, e.up_blocks,
+                                                    e.up_scales,   e.down_blocks, e.down_scales};
+    std::size_t at[6], total = 0;
+    for (int i = 0; i < 6; ++i) {
+        at[i] = total;
+        total += (parts[i].size() + 255) & ~std::size_t(255);
+    }
+    const BankKey key{*e.identity, -1, H, I * E};
+    auto it = bank_.find(key);
+    if (it == bank_.end()) {
+        for (int i : {1, 3, 5})  // IW/src/weights/quantization.cpp:51-53: 255 is not a scale
+            for (std::uint8_t s : parts[i])
+                require(s != 255, "kdq_invalid_block_scale");
+        auto r = std::make_unique<Resident>();
+        r->bytes = total;
+        hip_check(hipMalloc(&r->device, total));
+        for (int i = 0; i < 6; ++i)
+            hip_check(hipMemcpyAsync(static_cast<std::uint8_t*>(r->device) + at[i],
+                                     parts[i].data(), parts[i].size(), hipMemcpyHostToDevice, st));
+        synchronize();
+        it = bank_.emplace(key, std::move(r)).first;
+    }
+    auto* base = static_cast<const std::uint8_t*>(it->second->device);
+    auto* dx = static_cast<std::uint16_t*>(device_buffer(0, align16(x.size_bytes()) + logits.size_bytes()));
+    auto* dl = reinterpret_cast<float*>(reinterpret_cast<std::uint8_t*>(dx) + align16(x.size_bytes()));
+    auto* dy = static_cast<float*>(device_buffer(1, output.size_bytes()));
+    auto* route = static_cast<std::uint8_t*>(device_buffer(3, align16(tokens * top_k * 4) * 2));
+    auto* didx = reinterpret_cast<std::int32_t*>(route);
+    auto* dw = reinterpret_cast<float*>(route + align16(tokens * top_k * 4));
+    hip_check(hipMemcpyAsync(dx, x.data(), x.size_bytes(), hipMemcpyHostToDevice, st));
+    hip_check(hipMemcpyAsync(dl, logits.data(), logits.size_bytes(), hipMemcpyHostToDevice, st));
+    kdq_check(kdq_moe_mxfp4(dx, dl, tokens, H, I, E, top_k, base + at[0], base + at[1],
+                            base + at[2], base + at[3], base + at[4], base + at[5], dy, didx, dw,
+                            nullptr, nullptr, st));
+    hip_check(hipMemcpyAsync(output.data(), dy, output.size_bytes(), hipMemcpyDeviceToHost, st));
+    if (!selected.empty())
+        hip_check(hipMemcpyAsync(selected.data(), didx, selected.size_bytes(),
+                                 hipMemcpyDeviceToHost, st));
+    if (!weights.empty())
+        hip_check(hipMemcpyAsync(weights.data(), dw, weights.size_bytes(), hipMemcpyDeviceToHost, st));
+    synchronize();
+    for (float v : output)
+        if (!std::isfinite(v))
+            return ProjectionResult::unvalidated;
+    return ProjectionResult::finite;
+}
+
+std::size_t HipDenseCompute::release_weights(std::span<const WeightIdentity> identities) {
+    std::lock_guard<std::mutex> lock(mutex_);
+    synchronize();
+    std::size_t freed = 0;
+    for (auto it = bank_.begin(); it != bank_.end();) {
+        const bool retire = std::find(identities.begin(), identities.end(),
+                                      std::get<0>(it->first)) != identities.end();
+        if (retire) {
+            freed += it->second->bytes;
+            it = bank_.erase(it);
+        } else {
+            ++it;
+        }
+    }
+    return freed;
+}
+
+std::size_t HipDenseCompute::retained_weight_bytes() const {
+    std::lock_guard<std::mutex> lock(mutex_);
+    std::size_t total = 0;
+    for (const auto& [key, r] : bank_)
+        total += r->bytes;
+    return total;
+}
+
+void HipDenseCompute::release_scratch() {
+    std::lock_guard<std::mutex> lock(mutex_);
+    synchronize();
+    for (auto& b : buffers_) {
+        if (b.first)
+            hip_check(hipFree(b.first));
+        b = {nullptr, 0};
+    }
+    kdq_check(kdq_release_scratch());
+}
+
+}  // namespace kadan_amd

@@ -1,0 +1,255 @@
+"""GPU tests of the C++ host layer kadan_amd::HipDenseCompute (include/
+kadan_amd_dense_compute.hpp), driven through the C shim tests/cpp/dense_compute_probe.cpp.
+
+Follows the contract the reference's DenseCompute tests check (IW/tests/
+projection_validation.cpp, IW/tests/gguf_batch_partition.cpp:18-100, IW/tests/
+worker_compute.cpp:540-601; IW = services/hikari/inference_worker): `unsupported`
+before any source read or output write, bank hits read no rows,
+non-retained weights are not banked, rejected inputs throw, batch results are
+`unvalidated`.  Products must match the oracle within rel-L2 <= 1e-3 and max-abs <=
+2e-2 of the output RMS.
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+from kadan_amd import synth
+from tests.util import assert_close
+
+pytestmark = pytest.mark.gpu
+
+PROBE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "cpp",
+                     "libdense_compute_probe.so")
+Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
+UNSUPPORTED, UNVALIDATED, FINITE = 0, 1, 2
+
+c_p = ctypes.c_void_p
+c_sz = ctypes.c_size_t
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(c_p)
+
+
+class Probe:
+    def __init__(self):
+        if not os.path.exists(PROBE):
+            raise RuntimeError("tests/cpp/libdense_compute_probe.so is not built (run build())")
+        self.lib = ctypes.CDLL(PROBE)
+        L = self.lib
+        L.kdc_create.restype = c_p
+        L.kdc_create.argtypes = [ctypes.c_int, ctypes.c_char_p, c_sz]
+        L.kdc_destroy.argtypes = [c_p]
+        L.kdc_source_reads.restype = c_sz
+        L.kdc_source_reads.argtypes = [c_p]
+        L.kdc_retained.restype = c_sz
+        L.kdc_retained.argtypes = [c_p]
+        L.kdc_release.restype = c_sz
+        L.kdc_release.argtypes = [c_p, ctypes.c_ulonglong]
+        L.kdc_release_scratch.argtypes = [c_p, ctypes.c_char_p, c_sz]
+        L.kdc_dense_gguf.argtypes = [c_p, ctypes.c_ulonglong, ctypes.c_uint, c_p, c_sz, c_p, c_p,
+                                     c_sz, c_sz, c_sz, c_p, ctypes.c_int, ctypes.c_int, c_p,
+                                     ctypes.c_char_p, c_sz]
+        L.kdc_dense_gguf_batch.argtypes = [c_p, c_sz, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p,
+                                           c_p, ctypes.c_char_p, c_sz]
+        L.kdc_dense_gguf_q8.argtypes = [c_p, ctypes.c_ulonglong, c_p, c_sz, c_p, c_sz, c_sz, c_sz,
+                                        c_p, c_p, ctypes.c_char_p, c_sz]
+        L.kdc_moe_mxfp4.argtypes = [c_p, ctypes.c_ulonglong, c_sz, c_sz, c_sz] + [c_p] * 8 + [
+            c_sz, c_sz, c_p, c_p, c_p, c_p, ctypes.c_char_p, c_sz]
+        self.err = ctypes.create_string_buffer(512)
+        self.h = L.kdc_create(0, self.err, 512)
+        if not self.h:
+            raise RuntimeError(self.err.value.decode())
+
+    def close(self):
+        self.lib.kdc_destroy(self.h)
+
+    def _done(self, rc, result):
+        if rc:
+            raise RuntimeError(self.err.value.decode())
+        return int(result.value)
+
+    @property
+    def reads(self):
+        return self.lib.kdc_source_reads(self.h)
+
+    @property
+    def retained(self):
+        return self.lib.kdc_retained(self.h)
+
+    def release(self, ident):
+        return self.lib.kdc_release(self.h, ident)
+
+    def release_scratch(self):
+        if self.lib.kdc_release_scratch(self.h, self.err, 512):
+            raise RuntimeError(self.err.value.decode())
+
+    def gguf(self, ident, enc, w, x, n_out, bias=None, retain=True, cancel=False):
+        w = np.ascontiguousarray(w, np.uint8)
+        x = np.ascontiguousarray(x, np.float32)
+        rows, n_in = x.shape
+        y = np.full((rows, n_out), np.nan, np.float32)
+        res = ctypes.c_int(-1)
+        bias = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        rc = self.lib.kdc_dense_gguf(self.h, ident, enc, _p(w), w.size // n_out, _p(bias), _p(x),
+                                     rows, n_in, n_out, _p(y), int(retain), int(cancel),
+                                     ctypes.byref(res), self.err, 512)
+        return self._done(rc, res), y
+
+    def batch(self, jobs):
+        """jobs: (ident, enc, weights, x, n_out); x objects may repeat to share an input."""
+        n = len(jobs)
+        ws = [np.ascontiguousarray(j[2], np.uint8) for j in jobs]
+        xs = [j[3] for j in jobs]
+        ys = [np.full((x.shape[0], j[4]), np.nan, np.float32) for x, j in zip(xs, jobs)]
+        arr = lambda t, v: (t * n)(*v)
+        res = ctypes.c_int(-1)
+        rc = self.lib.kdc_dense_gguf_batch(
+            self.h, n, arr(ctypes.c_ulonglong, [j[0] for j in jobs]),
+            arr(ctypes.c_uint, [j[1] for j in jobs]), arr(c_p, [w.ctypes.data for w in ws]),
+            arr(c_sz, [w.size // j[4] for w, j in zip(ws, jobs)]),
+            arr(c_p, [x.ctypes.data for x in xs]), arr(c_sz, [x.shape[0] for x in xs]),
+            arr(c_sz, [x.shape[1] for x in xs]), arr(c_sz, [j[4] for j in jobs]),
+            arr(c_p, [y.ctypes.data for y in ys]), ctypes.byref(res), self.err, 512)
+        return self._done(rc, res), ys
+
+    def q8(self, ident, w, x_half, n_out):
+        w = np.ascontiguousarray(w, np.uint8)
+        x_half = np.ascontiguousarray(x_half, np.uint16)
+        rows, n_in = x_half.shape
+        y = np.zeros((rows, n_out), np.uint16)
+        res = ctypes.c_int(-1)
+        rc = self.lib.kdc_dense_gguf_q8(self.h, ident, _p(w), w.size // n_out, _p(x_half), rows,
+                                        n_in, n_out, _p(y), ctypes.byref(res), self.err, 512)
+        return self._done(rc, res), y
+
+    def moe(self, ident, experts, hidden, inter, weights, x_bf16, logits, top_k):
+        tokens = x_bf16.shape[0]
+        y = np.full((tokens, hidden), np.nan, np.float32)
+        sel = np.full((tokens, top_k), -1, np.int32)
+        rw = np.zeros((tokens, top_k), np.float32)
+        weights = [np.ascontiguousarray(a, np.uint8) for a in weights]
+        res = ctypes.c_int(-1)
+        rc = self.lib.kdc_moe_mxfp4(self.h, ident, experts, hidden, inter,
+                                    *[_p(a) for a in weights],
+                                    _p(np.ascontiguousarray(x_bf16, np.uint16)),
+                                    _p(np.ascontiguousarray(logits, np.float32)), tokens, top_k,
+                                    _p(y), _p(sel), _p(rw), ctypes.byref(res), self.err, 512)
+        return self._done(rc, res), y, sel, rw
+
+
+@pytest.fixture()
+def probe(device):
+    p = Probe()
+    yield p
+    p.close()
+
+
+@pytest.mark.parametrize("enc", [Q8_0, Q4_0, Q4_K])
+@pytest.mark.parametrize("rows", [1, 3, 8, 20])
+def test_dense_gguf_source_parity_and_bank(probe, oracle, enc, rows):
+    n_in, n_out = 1024, 96
+    w = synth.gguf_weights(enc, 0xD0 + enc, n_out, n_in)
+    x = synth.normal(0xD1, rows, rows * n_in).reshape(rows, n_in)
+    bias = synth.normal(0xD2, 1, n_out)
+    want = oracle.gemv(enc, w, x, n_in, n_out) + bias[None, :]
+    res, y = probe.gguf(7, enc, w, x, n_out, bias=bias)
+    assert res == FINITE
+    assert_close(y, want, what=f"dense_gguf_source enc={enc} rows={rows}")
+    assert probe.reads == n_out
+    assert probe.retained == w.size
+    res, y2 = probe.gguf(7, enc, w, x, n_out, bias=bias)  # bank hit: no source read
+    assert res == FINITE and probe.reads == n_out
+    assert np.array_equal(y, y2)
+    assert probe.release(7) == w.size and probe.retained == 0
+
+
+def test_dense_gguf_source_not_retained(probe, oracle):
+    w = synth.gguf_weights(Q4_K, 0xD3, 64, 512)
+    x = synth.normal(0xD4, 1, 512).reshape(1, 512)
+    for _ in range(2):
+        res, y = probe.gguf(9, Q4_K, w, x, 64, retain=False)
+        assert res == FINITE
+        assert_close(y, oracle.gemv(Q4_K, w, x, 512, 64), what="retain_misses=false")
+    assert probe.reads == 128 and probe.retained == 0
+
+
+def test_dense_gguf_source_unsupported_reads_nothing(probe):
+    x = np.ones((1, 512), np.float32)
+    w = np.zeros(64 * 512, np.uint8)
+    res, y = probe.gguf(1, Q6_K, w, x, 64)  # encoding not run here
+    assert res == UNSUPPORTED
+    res, _ = probe.gguf(1, Q4_0, w, np.ones((1, 48), np.float32), 64)  # 48 % 32 != 0
+    assert res == UNSUPPORTED
+    assert probe.reads == 0 and np.isnan(y).all()
+
+
+def test_dense_gguf_source_rejections(probe):
+    w = synth.gguf_weights(Q8_0, 0xD5, 32, 256)
+    x = synth.normal(0xD6, 1, 256).reshape(1, 256)
+    x[0, 3] = np.nan
+    with pytest.raises(RuntimeError, match="kdq_nonfinite_input"):
+        probe.gguf(2, Q8_0, w, x, 32)
+    with pytest.raises(RuntimeError, match="kdq_cancelled"):
+        probe.gguf(2, Q8_0, w, np.ones((1, 256), np.float32), 32, cancel=True)
+    bad = w.reshape(32, -1).copy()
+    bad[4, 0], bad[4, 1] = 0x00, 0x7C  # +inf block scale
+    with pytest.raises(RuntimeError, match="kdq_nonfinite_weight"):
+        probe.gguf(3, Q8_0, bad, np.ones((1, 256), np.float32), 32)
+    assert probe.reads == 32  # only the inf-scale weights were read
+
+
+def test_dense_gguf_batch_shared_input(probe, oracle):
+    """gate + up share one input span, down reads another (the reference's FFN batch)."""
+    h, f = 512, 1536
+    x = synth.normal(0xD7, 1, 2 * h).reshape(2, h)
+    xf = synth.normal(0xD8, 1, 2 * f).reshape(2, f)
+    wg = synth.gguf_weights(Q4_K, 0xD9, f, h)
+    wu = synth.gguf_weights(Q4_0, 0xDA, f, h)
+    wd = synth.gguf_weights(Q8_0, 0xDB, h, f)
+    res, ys = probe.batch([(11, Q4_K, wg, x, f), (12, Q4_0, wu, x, f), (13, Q8_0, wd, xf, h)])
+    assert res == UNVALIDATED
+    assert_close(ys[0], oracle.gemv(Q4_K, wg, x, h, f), what="batch gate")
+    assert_close(ys[1], oracle.gemv(Q4_0, wu, x, h, f), what="batch up")
+    assert_close(ys[2], oracle.gemv(Q8_0, wd, xf, f, h), what="batch down")
+    assert probe.reads == 2 * f + h
+
+
+def test_dense_gguf_batch_unsupported_job_reads_nothing(probe):
+    x = np.ones((1, 256), np.float32)
+    w = synth.gguf_weights(Q8_0, 0xDC, 32, 256)
+    res, ys = probe.batch([(1, Q8_0, w, x, 32), (2, Q6_K, np.zeros(32 * 210, np.uint8), x, 32)])
+    assert res == UNSUPPORTED and probe.reads == 0 and np.isnan(ys[0]).all()
+
+
+def test_dense_gguf_q8_source(probe, oracle):
+    rows, n_in, n_out = 40, 512, 192
+    w = synth.q4_0_weights(0xDD, n_out, n_in)
+    xh = synth.normal(0xDE, 1, rows * n_in).reshape(rows, n_in).astype(np.float16)
+    res, y = probe.q8(21, w, xh.view(np.uint16), n_out)
+    assert res == UNVALIDATED
+    xq, xd = oracle.quantize_q8_f16(xh.view(np.uint16))
+    want = oracle.gemm_q4_0_q8(w, n_out, n_in, xq, xd)
+    assert_close(y.view(np.float16).astype(np.float32), want, what="dense_gguf_q8_source")
+
+
+def test_moe_mxfp4_host_layer(probe, oracle):
+    tokens, hidden, inter, experts, top_k = 9, 128, 192, 8, 2
+    x, logits = synth.moe_inputs(0xDF, tokens, hidden, experts)
+    (gb, gs), (ub, us), (db, ds) = synth.moe_weights(0xDF, experts, hidden, inter)
+    want, idx, w, _, _ = oracle.moe_forward(x, logits, top_k, gb, gs, ub, us, db, ds)
+    res, y, sel, rw = probe.moe(31, experts, hidden, inter, (gb, gs, ub, us, db, ds), x, logits,
+                                top_k)
+    assert res == FINITE
+    assert np.array_equal(sel, idx)
+    assert_close(rw, w, rel=1e-6, mabs=1e-5, what="routing weights")
+    assert_close(y, want, what="moe host layer")
+    banked = probe.retained
+    assert banked >= gb.size + gs.size + ub.size + us.size + db.size + ds.size
+    res, y2, _, _ = probe.moe(31, experts, hidden, inter, (gb, gs, ub, us, db, ds), x, logits,
+                              top_k)
+    assert res == FINITE and np.array_equal(y, y2) and probe.retained == banked
+    assert probe.release(31) == banked
+    probe.release_scratch()
