@@ -3,9 +3,10 @@
 
 Headline (``value``): Q4_K GEMV weight throughput in GB/s at the Llama-3-8B FFN
 decode shape gate/up 4096 -> 14336, batch 1, with the inputs
-resident in HBM.  A "step" is one kdq_gemv launch over one weight copy; the timed
-steps rotate over 16 distinct weight copies (528 MB, twice the 256 MB Infinity Cache)
-so the cache cannot serve the weights.
+resident in HBM.  A "step" is one GEMV over one weight copy (one kernel launch,
+enqueued through kdq_gemv_batch 16 jobs at a time); the timed steps rotate over 16
+distinct weight copies (528 MB, twice the 256 MB Infinity Cache) so the cache cannot
+serve the weights.
 
 The same line carries
   roofline      the GEMV kernel's algorithmic bytes / measured average launch time
@@ -15,6 +16,7 @@ The same line carries
                 x86 quantize_row_q8_K + vec_dot_q4_K_q8_K (oracle/_ref, compiled from the
                 reference sources), on the reference worker split (64-column units,
                 clamp(cores/2, 1, 16) threads), on a bounded sample of the same workload
+                rotating over 4 weight copies
   extra         the other BASELINE configurations (C1 Q8_0 GEMV, C2 down, C3 Q4_0 GEMM,
                 C4 MoE at 1 and 256 tokens, C5 MoE at 2048 skewed tokens), each timed
                 with events over back-to-back launches (median of repetitions)
@@ -49,6 +51,8 @@ def parse():
     p.add_argument("--skip-extra", action="store_true")
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="also run a 256 MiB device copy (reference for counter scaling)")
     return p.parse_args()
 
 
@@ -97,22 +101,40 @@ def time_launches(torch, launch, count: int, reps: int = 1):
     return statistics.median(results)
 
 
+def time_steps(torch, submit, steps: int):
+    """ms per step over `steps` steps issued by `submit(n)` (which enqueues n steps),
+    events on the launch stream."""
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    submit(steps)
+    stop.record(stream)
+    stop.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
 def gemv_bytes(n_in: int, n_out: int, encoding: int) -> int:
     from kadan_amd import row_bytes
     return n_out * row_bytes(encoding, n_in) + 4 * n_in + 4 * n_out
 
 
 def traffic_for(workload: str):
+    """HBM bytes per launch of the workload's kernel from the committed rocprofv3
+    FETCH_SIZE/WRITE_SIZE measurement (profiles/traffic.json), or None."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
-            return json.load(f).get(workload)
+            entry = json.load(f).get(workload)
     except (OSError, ValueError):
         return None
+    return entry.get("bytes") if isinstance(entry, dict) else None
 
 
-def cpu_baseline(seconds: float):
-    """Reference CPU path on a bounded sample of the C2 gate/up workload."""
+def cpu_baseline(seconds: float, copies: int = 4):
+    """Reference CPU path on a bounded sample of the C2 gate/up workload, rotating over
+    `copies` distinct weight copies (235 MB) so the host caches cannot hold them."""
     from kadan_amd import synth
     n_in, n_out = 4096, 14336
     try:
@@ -120,19 +142,25 @@ def cpu_baseline(seconds: float):
     except AttributeError:
         affinity = os.cpu_count() or 1
     threads = max(1, min(16, affinity // 2))  # IW/src/models/text/gguf_weights.cpp:615-618
-    w = synth.q4_k_weights(0xC2A, n_out, n_in)
+    base = synth.q4_k_weights(0xC2A, n_out, n_in)
+    keep = keep_mask(Q4_K, base.shape)
+    ws = [base]
+    for c in range(1, copies):
+        noise = synth.random_bytes(0xC2A, 100 + c, base.size).reshape(base.shape)
+        ws.append(np.where(keep, base, base ^ noise))
     x = synth.normal(0xC2A, 50, n_in).reshape(1, n_in)
     import oracle
     if oracle.Reference.available():
         impl, kind = oracle.Reference(), "reference"
     else:
         impl, kind = oracle.Oracle(), "port"
-    impl.cpu_matvec(Q4_K, w, x, n_in, n_out, threads)  # warm-up
+    for w in ws:  # warm-up, one pass over every copy
+        impl.cpu_matvec(Q4_K, w, x, n_in, n_out, threads)
     times = []
     t_end = time.perf_counter() + seconds
     while time.perf_counter() < t_end or len(times) < 3:
         t0 = time.perf_counter()
-        impl.cpu_matvec(Q4_K, w, x, n_in, n_out, threads)
+        impl.cpu_matvec(Q4_K, ws[len(times) % copies], x, n_in, n_out, threads)
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
     return {
@@ -141,21 +169,50 @@ def cpu_baseline(seconds: float):
         "cores": threads,
         "kind": kind,
         "sample": (f"{len(times)} runs (median) of the C2 gate/up Q4_K matvec 4096->14336, "
-                   f"batch 1: quantize_row_q8_K + vec_dot_q4_K_q8_K via CpuMatvec, "
-                   f"64-column units on {threads} threads of {affinity} available"),
+                   f"batch 1, over {copies} rotated weight copies: quantize_row_q8_K + "
+                   f"vec_dot_q4_K_q8_K via CpuMatvec, 64-column units on {threads} threads "
+                   f"of {affinity} available"),
     }
 
 
 def bench_gemv(torch, encoding, n_in, n_out, steps, warmup, seed, copies=16):
-    from kadan_amd import ops, synth
+    """ms per GEMV step.  Steps go through kdq_gemv_batch, one job per weight copy and
+    up to `copies` jobs per submission, so the host enqueues launches faster than the
+    GPU retires them and the events time the kernels rather than Python."""
+    import kadan_amd
+    from kadan_amd import synth
     w = synth.gguf_weights(encoding, seed, n_out, n_in)
     ws = rotated_copies(torch, w, copies, keep_mask(encoding, w.shape), seed)
     x = torch.from_numpy(synth.normal(seed, 50, n_in).reshape(1, n_in)).cuda()
     y = torch.empty(1, n_out, device="cuda")
-    launch = lambda i: ops.gemv(encoding, ws[i % copies], x, n_out, out=y)
-    for i in range(warmup):
-        launch(i)
-    return time_launches(torch, launch, steps)
+    table = (kadan_amd.MatvecJob * copies)()
+    for c, wc in enumerate(ws):
+        table[c] = kadan_amd.MatvecJob(wc.data_ptr(), x.data_ptr(), y.data_ptr(), 0,
+                                       wc.shape[1], n_out, n_in, n_out, 1, encoding)
+    import ctypes
+    address = ctypes.addressof(table)
+    fn = kadan_amd.lib().kdq_gemv_batch
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def submit(n):
+        full, rest = divmod(n, copies)
+        for _ in range(full):
+            kadan_amd.check("kdq_gemv_batch", fn(address, copies, stream))
+        if rest:
+            kadan_amd.check("kdq_gemv_batch", fn(address, rest, stream))
+
+    submit(warmup)
+    return time_steps(torch, submit, steps)
+
+
+def calibrate_copy(torch, mib: int = 256, count: int = 5):
+    """A plain device copy of known size, for scaling the FETCH_SIZE/WRITE_SIZE counters
+    of a profiling run of this command (not part of the JSON line)."""
+    src = torch.ones(mib << 18, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(count):  # an elementwise kernel that reads and writes `mib` MiB
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
 
 
 def bench_gemm(torch, reps=10, count=20):
@@ -242,6 +299,8 @@ def main():
     import kadan_amd
     kadan_amd.lib()
 
+    if args.calibrate_copy:
+        calibrate_copy(torch)
     n_in, n_out = 4096, 14336
     ms = bench_gemv(torch, Q4_K, n_in, n_out, args.steps, args.warmup, 0xC2A)
     nbytes = gemv_bytes(n_in, n_out, Q4_K)
