@@ -58,6 +58,11 @@ class Oracle:
         lib.kdo_quantize_q8_f16.argtypes = [vp, sz, sz, vp, vp]
         lib.kdo_cpu_matvec.argtypes = [i, vp, sz, vp, sz, sz, sz, vp, i]
         lib.kdo_gemm_q4_0_q8.argtypes = [vp, sz, sz, vp, vp, sz, vp]
+        for name in ("kdo_vec_dot_q8_0_q8_0", "kdo_vec_dot_q4_0_q8_0"):
+            getattr(lib, name).restype = C.c_float
+            getattr(lib, name).argtypes = [sz, vp, vp, vp]
+        lib.kdo_vec_dot_q4_K_q8_K.restype = C.c_float
+        lib.kdo_vec_dot_q4_K_q8_K.argtypes = [sz, vp, vp, vp, vp]
         lib.kdo_e2m1.restype = C.c_float
         lib.kdo_e2m1.argtypes = [C.c_uint8]
         lib.kdo_mxfp4_decode_rows.argtypes = [vp, vp, sz, sz, vp]
@@ -115,6 +120,18 @@ class Oracle:
         if rc:
             raise ValueError(f"kdo_cpu_matvec rc={rc}")
         return y
+
+    def vec_dot(self, encoding, w, qs, d, bsums=None) -> float:
+        """One weight row against quantized activations (Q8_0 codes + fp16 scales for
+        Q8_0/Q4_0 weights; Q8_K codes + fp32 scales + bsums for Q4_K)."""
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        qs = np.ascontiguousarray(qs, dtype=np.int8)
+        if encoding == Q4_K:
+            return self.lib.kdo_vec_dot_q4_K_q8_K(qs.size, _p(w), _p(qs),
+                                                  _p(np.ascontiguousarray(d, np.float32)),
+                                                  _p(np.ascontiguousarray(bsums, np.int16)))
+        fn = self.lib.kdo_vec_dot_q8_0_q8_0 if encoding == Q8_0 else self.lib.kdo_vec_dot_q4_0_q8_0
+        return fn(qs.size, _p(w), _p(qs), _p(np.ascontiguousarray(d, np.uint16)))
 
     # -- activation quantizers
     def quantize_row_q8_0(self, x):

@@ -1,0 +1,141 @@
+"""Writes tests/golden/reference_vectors.npz: input/output vectors of the reference's own
+compiled code (oracle/_ref, built from /root/reference by oracle/Makefile), so that the
+oracle stays pinned where the reference is absent (the GPU box, later rounds).
+
+    python tests/golden/make_golden.py      # needs oracle/_ref/libkadan_ref.so
+
+Contents (all little-endian, plain arrays, no pickles):
+  decode_<fmt>_blocks / decode_<fmt>_values   ggml to_float of 64 blocks per format
+      (Q4_0, Q8_0, Q4_K), random bytes from xorshift32 seeded 0x31415926 as
+      IW/tests/gguf_quantization.cpp:93-147 seeds its own; the first 16 blocks carry
+      the special fp16 scales of that test (zeros, subnormals, max, inf, NaN).
+  q8_0_x / q8_0_bytes        ggml x86 quantize_row_q8_0 (G/src/ggml-cpu/arch/x86/quants.c:302-398)
+  q8_K_x / q8_K_bytes        ggml quantize_row_q8_K (G/src/ggml-quants.c:2769-2806)
+  dot_<fmt>_w / dot_<fmt>_x / dot_<fmt>_out   ggml AVX2 vec_dot against the dot type
+  matvec_<fmt>_w / _x / _y   kadan::text::CpuMatvec (IW/src/models/text/cpu_matvec.cpp:28-66)
+  mxfp4_blocks / mxfp4_scales / mxfp4_values / mxfp4_x / mxfp4_y
+                             kadan quantization::decode_rows / matvec
+                             (IW/src/weights/quantization.cpp:193-247)
+"""
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+
+from oracle import BLOCK_BYTES, BLOCK_VALUES, Q4_0, Q4_K, Q8_0, Reference  # noqa: E402
+
+OUT = os.path.join(HERE, "reference_vectors.npz")
+NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k"}
+SPECIAL_HALVES = [0x0000, 0x8000, 0x0001, 0x8001, 0x03FF, 0x83FF, 0x0400, 0x8400, 0x3C00,
+                  0xBC00, 0x7BFF, 0xFBFF, 0x7C00, 0xFC00, 0x7E01, 0x7C01]
+
+
+class XorShift32:
+    def __init__(self, state=0x31415926):
+        self.s = state
+
+    def __call__(self):
+        s = self.s
+        s ^= (s << 13) & 0xFFFFFFFF
+        s ^= s >> 17
+        s ^= (s << 5) & 0xFFFFFFFF
+        self.s = s
+        return s
+
+
+def random_blocks(encoding, count, rng):
+    size = BLOCK_BYTES[encoding]
+    blocks = np.zeros((count, size), np.uint8)
+    for t in range(count):
+        for i in range(size):
+            blocks[t, i] = rng() & 255
+        scale = (SPECIAL_HALVES[t] if t < 16
+                 else (rng() & 0x83FF) | ((rng() % 31) << 10))
+        blocks[t, 0], blocks[t, 1] = scale & 255, scale >> 8
+        if encoding == Q4_K:
+            minimum = (SPECIAL_HALVES[15 - t] if t < 16
+                       else (rng() & 0x83FF) | ((rng() % 31) << 10))
+            blocks[t, 2], blocks[t, 3] = minimum & 255, minimum >> 8
+    return blocks
+
+
+def finite_weights(encoding, n_out, n_in, rng):
+    """Packed rows with finite, modest scales (every code byte random)."""
+    blocks = random_blocks(encoding, n_out * n_in // BLOCK_VALUES[encoding], rng)
+    for b in blocks:
+        b[1] = 0x18 + (b[1] & 7)  # fp16 exponent 6..7: scales ~1e-3
+        if encoding == Q4_K:
+            b[3] = 0x14 + (b[3] & 7)
+    return blocks.reshape(n_out, -1)
+
+
+def main():
+    if not Reference.available():
+        raise SystemExit("oracle/_ref/libkadan_ref.so is not built (make -C oracle ref)")
+    ref = Reference()
+    rng = XorShift32()
+    data = {}
+    for enc in (Q4_0, Q8_0, Q4_K):
+        blocks = random_blocks(enc, 64, rng)
+        data[f"decode_{NAMES[enc]}_blocks"] = blocks
+        data[f"decode_{NAMES[enc]}_values"] = ref.to_float(enc, blocks.reshape(1, -1),
+                                                           64 * BLOCK_VALUES[enc]).reshape(64, -1)
+    # activation quantizers: N(0,1) values plus exact half-way cases after scaling
+    g = np.random.default_rng(0x5EED)
+    x = g.standard_normal(512).astype(np.float32)
+    x[:32] = np.arange(32, dtype=np.float32) - 15.5  # amax 15.5: id = 127/15.5
+    x[32:64] = 0.0
+    x[64] = 127.0
+    x[65:68] = [0.5, 1.5, -2.5]  # id = 1: ties to even
+    x[68:96] = 0.25
+    data["q8_0_x"] = x
+    data["q8_0_bytes"] = ref.quantize_row(Q8_0, x, 512 // 32 * 34)
+    xk = g.standard_normal(512).astype(np.float32) * 3
+    xk[256:512] = -np.abs(xk[256:512])  # negative signed max
+    data["q8_K_x"] = xk
+    data["q8_K_bytes"] = ref.quantize_row(15, xk, 2 * (4 + 256 + 32))
+    # AVX2 vec_dot against the quantized activations
+    for enc, dot_type, xbytes in ((Q8_0, Q8_0, 34), (Q4_0, Q8_0, 34), (Q4_K, 15, 292)):
+        n = 512
+        w = finite_weights(enc, 4, n, rng)
+        xv = g.standard_normal((4, n)).astype(np.float32)
+        per_block = 32 if dot_type == Q8_0 else 256
+        xq = np.stack([ref.quantize_row(dot_type, xv[r], n // per_block * xbytes)
+                       for r in range(4)])
+        out = np.array([ref.vec_dot(enc, n, w[r], xq[r]) for r in range(4)], np.float32)
+        data[f"dot_{NAMES[enc]}_w"] = w
+        data[f"dot_{NAMES[enc]}_x"] = xq
+        data[f"dot_{NAMES[enc]}_out"] = out
+    # CpuMatvec over 64-column units (the CPU baseline path)
+    for enc in (Q8_0, Q4_0, Q4_K):
+        n_in, n_out = 512, 96
+        w = finite_weights(enc, n_out, n_in, rng)
+        xv = g.standard_normal((2, n_in)).astype(np.float32)
+        data[f"matvec_{NAMES[enc]}_w"] = w
+        data[f"matvec_{NAMES[enc]}_x"] = xv
+        data[f"matvec_{NAMES[enc]}_y"] = ref.cpu_matvec(enc, w, xv, n_in, n_out, 2)
+    # MXFP4 decode and exact matvec
+    rows, cols = 8, 128
+    blocks = np.array([rng() & 255 for _ in range(rows * cols // 2)], np.uint8).reshape(rows, -1)
+    scales = np.array([110 + rng() % 30 for _ in range(rows * cols // 32)], np.uint8).reshape(rows, -1)
+    scales[0, 0], scales[1, 1] = 0, 254  # 2^-127 and 2^127 block scales
+    blocks[1, 16:32] = 0x9A  # codes -0.5 and -1.0 stay finite at 2^127
+    rc, values = ref.mxfp4_decode_rows(blocks, scales, rows, cols)
+    assert rc == 0, rc
+    xm = g.standard_normal(cols).astype(np.float32)
+    scales_mv = scales.copy()
+    scales_mv[1, 1] = 130  # the matvec needs finite products
+    rc, ym = ref.mxfp4_matvec(blocks, scales_mv, rows, cols, xm)
+    assert rc == 0, rc
+    data.update(mxfp4_blocks=blocks, mxfp4_scales=scales, mxfp4_values=values,
+                mxfp4_mv_scales=scales_mv, mxfp4_x=xm, mxfp4_y=ym)
+    np.savez_compressed(OUT, **data)
+    print(OUT, os.path.getsize(OUT), "bytes,", len(data), "arrays")
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,438 @@
+"""Pins the CPU oracle (oracle/) before anything is checked against it.
+
+Each oracle function is checked against something other than itself:
+  * the reference's own known answers, restated as data (IW/tests/gguf_quantization.cpp:
+    36-91, IW/tests/quantization.cpp:97-351; IW = services/hikari/inference_worker);
+  * vectors of the reference's compiled code (tests/golden/reference_vectors.npz, made by
+    tests/golden/make_golden.py from oracle/_ref), and oracle/_ref itself when built here;
+  * closed forms and independent formulations (numpy's IEEE conversions, vectorised
+    decodes, float64 brute-force products, stable argsort) chosen so that a dropped
+    term, a wrong sign or index, or a transposed operand fails.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from kadan_amd import synth
+
+Q4_0, Q8_0, Q4_K = 2, 8, 12
+BV = {Q4_0: 32, Q8_0: 32, Q4_K: 256}
+BB = {Q4_0: 18, Q8_0: 34, Q4_K: 144}
+NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k"}
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                      "reference_vectors.npz")
+
+
+@pytest.fixture(scope="module")
+def golden():
+    with np.load(GOLDEN, allow_pickle=False) as f:
+        return {k: f[k] for k in f.files}
+
+
+def same_bits(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return bool(np.all((a.view(np.uint32) == b.view(np.uint32)) | (np.isnan(a) & np.isnan(b))))
+
+
+# ---------------------------------------------------------------- fp16 / bf16
+
+def test_half_to_float_exhaustive_vs_ieee(oracle):
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = oracle.halves_to_float(bits)
+    want = bits.view(np.float16).astype(np.float32)  # IEEE binary16 -> binary32, exact
+    finite = ~np.isnan(want)
+    assert np.array_equal(got.view(np.uint32)[finite], want.view(np.uint32)[finite])
+    # NaN patterns decode to NaN of the same sign (the vectorised route multiplies by a
+    # code of 1, which quiets signalling NaNs, as the reference decode does)
+    assert np.isnan(got[~finite]).all()
+    assert np.array_equal(np.signbit(got[~finite]), (bits[~finite] & 0x8000) != 0)
+
+
+def test_half_to_float_vs_compiled_reference(oracle, reference):
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = oracle.halves_to_float(bits)
+    want = np.array([reference.half_to_float(int(b)) for b in bits], np.float32)
+    assert same_bits(got, want)
+
+
+def test_float_to_half_round_to_nearest_even(oracle):
+    g = np.random.default_rng(1)
+    x = np.concatenate([g.standard_normal(4000) * 10.0 ** g.integers(-8, 5, 4000),
+                        [65504.0, 65519.9, 65520.0, 6.0e-8, 2.98e-8, 1.0 + 2.0 ** -11,
+                         1.0 + 3 * 2.0 ** -11, -0.0]]).astype(np.float32)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)  # numpy: IEEE RNE
+    got = np.array([oracle.float_to_half(float(v)) for v in x], np.uint16)
+    assert np.array_equal(got, want)
+
+
+# ---------------------------------------------------------------- GGUF decode
+
+def half_bits(block, offset, bits):
+    block[offset] = bits & 0xFF
+    block[offset + 1] = bits >> 8
+
+
+def test_q8_0_literal_block(oracle):
+    """IW/tests/gguf_quantization.cpp:37-44: d = 0.5, codes 0..15 then -16..-31."""
+    block = np.zeros(34, np.uint8)
+    half_bits(block, 0, 0x3800)
+    for i in range(32):
+        block[2 + i] = i if i < 16 else 256 - i
+    want = np.array([0.5 * (i if i < 16 else -i) for i in range(32)], np.float32)
+    assert same_bits(oracle.dequantize(Q8_0, block[None], 32)[0], want)
+
+
+def test_q4_k_literal_block(oracle):
+    """IW/tests/gguf_quantization.cpp:61-78: d = 2, dmin = 0.5, packed scales 1..8 and
+    mins 8..1, every code byte 0xc3 (low nibble 3, high nibble 12)."""
+    block = np.zeros(144, np.uint8)
+    half_bits(block, 0, 0x4000)
+    half_bits(block, 2, 0x3800)
+    block[4:16] = [1, 2, 3, 4, 8, 7, 6, 5, 0x45, 0x36, 0x27, 0x18]
+    block[16:] = 0xC3
+    g = np.arange(256) // 32
+    want = (2.0 * (g + 1) * np.where(g % 2, 12.0, 3.0) - 0.5 * (8 - g)).astype(np.float32)
+    assert same_bits(oracle.dequantize(Q4_K, block[None], 256)[0], want)
+
+
+def test_q4_0_literal_block(oracle):
+    """G/src/ggml-quants.c:459-476: value j is the low nibble of byte j, value j+16 its
+    high nibble, w = (q - 8) * d."""
+    block = np.zeros(18, np.uint8)
+    half_bits(block, 0, 0xC000)  # d = -2
+    block[2:] = [(15 - j) << 4 | j for j in range(16)]
+    q = np.concatenate([np.arange(16), 15 - np.arange(16)])
+    assert same_bits(oracle.dequantize(Q4_0, block[None], 32)[0],
+                     ((q - 8) * -2.0).astype(np.float32))
+
+
+def numpy_decode(encoding, blocks):
+    """Independent vectorised decode (float32 numpy ops, each one rounded)."""
+    d = blocks[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    if encoding == Q8_0:
+        return blocks[:, 2:].view(np.int8).astype(np.float32) * d[:, None]
+    if encoding == Q4_0:
+        qs = blocks[:, 2:]
+        q = np.concatenate([qs & 15, qs >> 4], axis=1).astype(np.int32) - 8
+        return q.astype(np.float32) * d[:, None]
+    dmin = blocks[:, 2:4].copy().view(np.float16).astype(np.float32)[:, 0]
+    s = blocks[:, 4:16].astype(np.int32)
+    sc = np.empty((len(blocks), 8), np.int32)
+    mn = np.empty((len(blocks), 8), np.int32)
+    sc[:, :4], mn[:, :4] = s[:, 0:4] & 63, s[:, 4:8] & 63
+    sc[:, 4:] = (s[:, 8:12] & 15) | ((s[:, 0:4] >> 6) << 4)
+    mn[:, 4:] = (s[:, 8:12] >> 4) | ((s[:, 4:8] >> 6) << 4)
+    qs = blocks[:, 16:].reshape(-1, 4, 32).astype(np.int32)
+    codes = np.stack([qs & 15, qs >> 4], axis=2).reshape(-1, 8, 32)  # sub-block g
+    scaled = (d[:, None] * sc.astype(np.float32))[:, :, None]
+    offset = (dmin[:, None] * mn.astype(np.float32))[:, :, None]
+    return (scaled * codes.astype(np.float32) - offset).reshape(-1, 256)
+
+
+@pytest.mark.parametrize("encoding", [Q4_0, Q8_0, Q4_K])
+def test_decode_vs_independent_numpy(oracle, encoding):
+    raw = synth.random_bytes(7, encoding, 512 * BB[encoding]).reshape(512, BB[encoding])
+    raw[:, 1] = 0x10 + (raw[:, 1] & 0x1F)  # finite scales of many magnitudes
+    if encoding == Q4_K:
+        raw[:, 3] = 0x10 + (raw[:, 3] & 0x1F)
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = numpy_decode(encoding, raw)
+    got = oracle.dequantize(encoding, raw.reshape(64, -1), 8 * BV[encoding]).reshape(512, -1)
+    assert same_bits(got, want)
+
+
+@pytest.mark.parametrize("encoding", [Q4_0, Q8_0, Q4_K])
+def test_decode_vs_reference_vectors(oracle, golden, encoding):
+    blocks = golden[f"decode_{NAMES[encoding]}_blocks"]
+    want = golden[f"decode_{NAMES[encoding]}_values"]
+    got = oracle.dequantize(encoding, blocks, BV[encoding])
+    assert same_bits(got, want)
+
+
+@pytest.mark.parametrize("encoding", [Q4_0, Q8_0, Q4_K])
+def test_decode_vs_compiled_reference(oracle, reference, encoding):
+    raw = synth.random_bytes(11, encoding, 2048 * BB[encoding])
+    got = oracle.dequantize(encoding, raw[None], 2048 * BV[encoding])
+    want = reference.to_float(encoding, raw[None], 2048 * BV[encoding])
+    assert same_bits(got, want)
+    if encoding != Q4_0:  # kadan's own decode (no Q4_0 encoding in the reference)
+        for b in range(0, 64):
+            blk = raw[b * BB[encoding]:(b + 1) * BB[encoding]]
+            mine = oracle.dequantize(encoding, blk[None], BV[encoding])[0]
+            assert same_bits(mine, reference.kadan_decode_block(encoding, blk))
+
+
+# ---------------------------------------------------------------- quantizers
+
+def test_quantize_q8_0_vs_reference_vectors(oracle, golden):
+    x = golden["q8_0_x"]
+    ref = golden["q8_0_bytes"].reshape(-1, 34)
+    qs, d = oracle.quantize_row_q8_0(x)
+    assert np.array_equal(qs, ref[:, 2:].view(np.int8).ravel())
+    assert np.array_equal(d, ref[:, :2].copy().view(np.uint16).ravel())
+
+
+def test_quantize_q8_0_ties_round_to_even(oracle):
+    x = np.zeros(32, np.float32)
+    x[:5] = [127.0, 0.5, 1.5, -2.5, 3.5]  # amax 127: id = 1, codes = RNE(x)
+    qs, d = oracle.quantize_row_q8_0(x)
+    assert list(qs[:5]) == [127, 0, 2, -2, 4]
+    assert d[0] == np.float16(1.0).view(np.uint16)
+    qs, d = oracle.quantize_row_q8_0(np.zeros(32, np.float32))
+    assert not qs.any() and d[0] == 0
+
+
+def test_quantize_q8_K_vs_reference_vectors(oracle, golden):
+    x = golden["q8_K_x"]
+    ref = golden["q8_K_bytes"].reshape(2, -1)
+    qs, d, bsums = oracle.quantize_row_q8_K(x)
+    assert np.array_equal(d, ref[:, :4].copy().view(np.float32).ravel())
+    assert np.array_equal(qs, ref[:, 4:260].view(np.int8).ravel())
+    assert np.array_equal(bsums, ref[:, 260:].copy().view(np.int16).ravel())
+    # bsums are sums of 16 codes (a closed form the reference states)
+    assert np.array_equal(bsums, qs.reshape(-1, 16).astype(np.int32).sum(1))
+
+
+def test_quantize_q8_f16_is_x86_q8_0_with_fp32_scale(oracle):
+    """The prefill quantizer: x86 quantize_row_q8_0 codes on fp32(x_half), d = amax/127
+    kept in fp32 (not rounded to fp16)."""
+    xh = (synth.normal(3, 1, 4 * 256) * 3).astype(np.float16).reshape(4, 256)
+    xh[0, :32] = 0
+    qs, d = oracle.quantize_q8_f16(xh.view(np.uint16))
+    for r in range(4):
+        q_row, _ = oracle.quantize_row_q8_0(xh[r].astype(np.float32))
+        assert np.array_equal(qs[r], q_row)
+    amax = np.abs(xh.astype(np.float32)).reshape(4, -1, 32).max(2)
+    assert np.array_equal(d, (amax / np.float32(127)).astype(np.float32))
+
+
+# ---------------------------------------------------------------- dots and products
+
+@pytest.mark.parametrize("encoding", [Q8_0, Q4_0, Q4_K])
+def test_vec_dot_vs_reference_vectors_and_closed_form(oracle, golden, encoding):
+    w = golden[f"dot_{NAMES[encoding]}_w"]
+    xq = golden[f"dot_{NAMES[encoding]}_x"]
+    want = golden[f"dot_{NAMES[encoding]}_out"]
+    n = 512
+    for r in range(4):
+        if encoding == Q4_K:
+            blk = xq[r].reshape(2, 292)
+            d = blk[:, :4].copy().view(np.float32).ravel()
+            qs = blk[:, 4:260].view(np.int8).ravel()
+            bs = blk[:, 260:].copy().view(np.int16).ravel()
+            got = oracle.vec_dot(encoding, w[r], qs, d, bs)
+            xs = np.repeat(d.astype(np.float64), 256) * qs
+        else:
+            blk = xq[r].reshape(-1, 34)
+            d = blk[:, :2].copy().view(np.uint16).ravel()
+            qs = blk[:, 2:].view(np.int8).ravel()
+            got = oracle.vec_dot(encoding, w[r], qs, d)
+            xs = np.repeat(d.view(np.float16).astype(np.float64), 32) * qs
+        # AVX2 summation order differs from the scalar restatement: fp32 tolerance
+        assert abs(got - want[r]) <= 1e-5 * max(1.0, abs(want[r])), (r, got, want[r])
+        exact = float(oracle.dequantize(encoding, w[r][None], n)[0].astype(np.float64) @ xs)
+        assert abs(got - exact) <= 1e-4 * max(1.0, abs(exact))
+
+
+@pytest.mark.parametrize("encoding", [Q8_0, Q4_0, Q4_K])
+def test_cpu_matvec_port_vs_reference_vectors(oracle, golden, encoding):
+    w = golden[f"matvec_{NAMES[encoding]}_w"]
+    x = golden[f"matvec_{NAMES[encoding]}_x"]
+    want = golden[f"matvec_{NAMES[encoding]}_y"]
+    got = oracle.cpu_matvec(encoding, w, x, 512, 96, threads=2)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5 * np.abs(want).max())
+
+
+@pytest.mark.parametrize("encoding", [Q8_0, Q4_0, Q4_K])
+def test_gemv_is_float64_product_of_decoded_weights(oracle, encoding):
+    n_in, n_out = 512, 48
+    w = synth.gguf_weights(encoding, 5, n_out, n_in)
+    x = synth.normal(5, 9, 3 * n_in).reshape(3, n_in)
+    decoded = oracle.dequantize(encoding, w, n_in).astype(np.float64)
+    want = x.astype(np.float64) @ decoded.T
+    got = oracle.gemv(encoding, w, x, n_in, n_out)
+    np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-6 * np.abs(want).max())
+    # a transposed or shifted operand is far off
+    assert np.abs(got - x.astype(np.float64) @ np.roll(decoded, 1, axis=0).T).max() > 1e-3
+
+
+def test_gemm_q4_0_q8_is_float64_product(oracle):
+    m, k, n = 5, 256, 40
+    w = synth.q4_0_weights(6, n, k)
+    xh = synth.normal(6, 1, m * k).reshape(m, k).astype(np.float16)
+    qs, d = oracle.quantize_q8_f16(xh.view(np.uint16))
+    xdeq = qs.astype(np.float64) * np.repeat(d.astype(np.float64), 32, axis=1)
+    want = xdeq @ oracle.dequantize(Q4_0, w, k).astype(np.float64).T
+    got = oracle.gemm_q4_0_q8(w, n, k, qs, d)
+    np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-6 * np.abs(want).max())
+
+
+# ---------------------------------------------------------------- MXFP4
+
+def test_e2m1_golden_table(oracle):
+    """IW/tests/quantization.cpp:97-105."""
+    table = [0, .5, 1, 1.5, 2, 3, 4, 6, -0.0, -.5, -1, -1.5, -2, -3, -4, -6]
+    for code, v in enumerate(table):
+        got = oracle.e2m1(code)
+        assert got == v and np.signbit(got) == (code >= 8)
+
+
+def test_mxfp4_two_by_sixty_four_fixture(oracle):
+    """IW/tests/quantization.cpp:250-270: low nibble first, one exponent per 32."""
+    packed = np.full(64, 0xA2, np.uint8)
+    packed[0] = 0x71
+    scales = np.array([127, 128, 126, 129], np.uint8)
+    factor = np.repeat([1.0, 2.0, 0.5, 4.0], 32)
+    want = np.where(np.arange(128) % 2, -factor, factor).astype(np.float32)
+    want[0], want[1] = 0.5, 6.0
+    rc, got = oracle.mxfp4_decode_rows(packed.reshape(2, 32), scales.reshape(2, 2), 2, 64)
+    assert rc == 0 and np.array_equal(got.ravel(), want)
+    bad = scales.copy()
+    bad[3] = 255  # invalid E8M0
+    rc, _ = oracle.mxfp4_decode_rows(packed.reshape(2, 32), bad.reshape(2, 2), 2, 64)
+    assert rc != 0
+
+
+def test_mxfp4_extremes(oracle):
+    """IW/tests/quantization.cpp:293-317."""
+    packed = np.full(16, 0xA2, np.uint8)
+
+    def decode(p, s):
+        return oracle.mxfp4_decode_rows(p.reshape(1, 16), np.array([[s]], np.uint8), 1, 32)
+
+    rc, v = decode(packed, 0)
+    assert rc == 0 and v[0, 0] == 2.0 ** -127 and v[0, 1] == -(2.0 ** -127)
+    rc, v = decode(packed, 254)
+    assert rc == 0 and v[0, 0] == 2.0 ** 127 and v[0, 1] == -(2.0 ** 127)
+    p = packed.copy()
+    p[0] = 0x11
+    rc, v = decode(p, 0)
+    assert rc == 0 and v[0, 0] == 2.0 ** -128
+    zeros = np.full(16, 0x80, np.uint8)
+    for s in (0, 127, 254):
+        rc, v = decode(zeros, s)
+        assert rc == 0 and v[0, 0] == 0 and not np.signbit(v[0, 0]) and np.signbit(v[0, 1])
+    p = packed.copy()
+    p[0] = 0x77
+    rc, _ = decode(p, 253)  # 6 * 2^126 overflows: the reference refuses it
+    assert rc != 0
+
+
+def test_mxfp4_matvec_known_answer(oracle):
+    """IW/tests/quantization.cpp:319-330: 2x32, x = (3, 1, 0...), y = {2, 8}."""
+    packed = np.full(32, 0xA2, np.uint8).reshape(2, 16)
+    scales = np.array([[127], [129]], np.uint8)
+    x = np.zeros(32, np.float32)
+    x[0], x[1] = 3, 1
+    rc, y = oracle.mxfp4_matvec(packed, scales, 2, 32, x)
+    assert rc == 0 and list(y) == [2.0, 8.0]
+
+
+def test_mxfp4_vs_reference_vectors(oracle, golden):
+    rc, v = oracle.mxfp4_decode_rows(golden["mxfp4_blocks"], golden["mxfp4_scales"], 8, 128)
+    assert rc == 0 and np.array_equal(v.view(np.uint32), golden["mxfp4_values"].view(np.uint32))
+    rc, y = oracle.mxfp4_matvec(golden["mxfp4_blocks"], golden["mxfp4_mv_scales"], 8, 128,
+                                golden["mxfp4_x"])
+    assert rc == 0 and np.array_equal(y.view(np.uint32), golden["mxfp4_y"].view(np.uint32))
+
+
+def test_mxfp4_vs_compiled_reference(oracle, reference):
+    blocks = synth.random_bytes(8, 1, 16 * 128).reshape(16, 128)
+    scales = (synth.random_bytes(8, 2, 16 * 8) % 24 + 116).astype(np.uint8).reshape(16, 8)
+    x = synth.normal(8, 3, 256)
+    a, b = oracle.mxfp4_decode_rows(blocks, scales, 16, 256), reference.mxfp4_decode_rows(
+        blocks, scales, 16, 256)
+    assert a[0] == b[0] == 0 and np.array_equal(a[1], b[1])
+    a, b = oracle.mxfp4_matvec(blocks, scales, 16, 256, x), reference.mxfp4_matvec(
+        blocks, scales, 16, 256, x)
+    assert a[0] == b[0] == 0 and np.array_equal(a[1].view(np.uint32), b[1].view(np.uint32))
+
+
+# ---------------------------------------------------------------- MoE routing
+
+def brute_route(logits, top_k):
+    """Router of IW/src/models/text/qwen_layers.cpp:403-425 restated with numpy."""
+    idx = np.empty((len(logits), top_k), np.int32)
+    w = np.empty((len(logits), top_k), np.float32)
+    for t, row in enumerate(logits.astype(np.float32)):
+        e = np.exp(row - row.max()).astype(np.float32)
+        p = (e.astype(np.float64) / e.astype(np.float64).sum()).astype(np.float32)
+        order = np.argsort(-p, kind="stable")[:top_k]  # ties: lower expert first
+        idx[t] = order
+        s = np.float32(0)
+        for v in p[order]:
+            s = np.float32(s + v)
+        w[t] = p[order] / max(s, np.float32(6.103515625e-5))
+    return idx, w
+
+
+def test_route_hand_case(oracle):
+    # probabilities proportional to 1, 2, 3, 4: top-2 = experts 3, 2 with weights 4/7, 3/7
+    logits = np.log(np.array([[1, 2, 3, 4], [4, 3, 2, 1]], np.float64)).astype(np.float32)
+    idx, w = oracle.moe_route(logits, 2)
+    assert idx.tolist() == [[3, 2], [0, 1]]
+    np.testing.assert_allclose(w, [[4 / 7, 3 / 7], [4 / 7, 3 / 7]], rtol=1e-6)
+
+
+def test_route_ties_and_masked_experts(oracle):
+    logits = np.zeros((3, 6), np.float32)
+    logits[1, [4, 1]] = 2.0
+    logits[2, :] = -np.inf
+    logits[2, 3] = 0.0
+    idx, w = oracle.moe_route(logits, 3)
+    assert idx.tolist() == [[0, 1, 2], [1, 4, 0], [3, 0, 1]]
+    np.testing.assert_allclose(w[0], 1 / 3, rtol=1e-6)
+    assert w[2].tolist() == [1.0, 0.0, 0.0]
+
+
+@pytest.mark.parametrize("tokens,experts,top_k", [(64, 8, 2), (50, 32, 4), (20, 128, 8)])
+def test_route_vs_numpy(oracle, tokens, experts, top_k):
+    _, logits = synth.moe_inputs(9 + experts, tokens, 32, experts, hot=4 if experts > 8 else 0)
+    idx, w = oracle.moe_route(logits, top_k)
+    bi, bw = brute_route(logits, top_k)
+    assert np.array_equal(idx, bi)
+    # numpy's float32 exp may differ from the C library's expf by an ulp
+    np.testing.assert_allclose(w, bw, rtol=5e-7, atol=0)
+    np.testing.assert_allclose(w.sum(1), 1.0, rtol=1e-6)
+
+
+@pytest.mark.parametrize("tokens,experts,top_k", [(1, 4, 2), (37, 8, 4), (300, 64, 8)])
+def test_permute_is_stable_sort_by_expert(oracle, tokens, experts, top_k):
+    _, logits = synth.moe_inputs(10, tokens, 32, experts)
+    idx, _ = oracle.moe_route(logits, top_k)
+    offsets, perm = oracle.moe_permute(idx, experts)
+    assert np.array_equal(perm, np.argsort(idx.ravel(), kind="stable"))
+    assert np.array_equal(offsets, np.concatenate([[0], np.cumsum(np.bincount(idx.ravel(),
+                                                                              minlength=experts))]))
+
+
+def test_moe_forward_vs_numpy_composition(oracle):
+    """MoeLayer::forward (IW/src/models/text/qwen_layers.cpp:378-492) composed in float64
+    from pinned parts; the composition itself is unpinned against the reference, which
+    never runs MXFP4 weights through MoeLayer."""
+    tokens, hidden, inter, experts, top_k = 6, 64, 96, 4, 2
+    x, logits = synth.moe_inputs(12, tokens, hidden, experts)
+    (gb, gs), (ub, us), (db, ds) = synth.moe_weights(12, experts, hidden, inter)
+    y, idx, w, _, _ = oracle.moe_forward(x, logits, top_k, gb, gs, ub, us, db, ds)
+    xf = synth.bf16_bits_to_float(x).astype(np.float64)
+
+    def dec(b, s, rows, cols, e):
+        rc, v = oracle.mxfp4_decode_rows(b[e].reshape(rows, -1), s[e].reshape(rows, -1), rows,
+                                         cols)
+        assert rc == 0
+        return v.astype(np.float64)
+
+    want = np.zeros((tokens, hidden))
+    for t in range(tokens):
+        for i in range(top_k):
+            e = idx[t, i]
+            g = dec(gb, gs, inter, hidden, e) @ xf[t]
+            u = dec(ub, us, inter, hidden, e) @ xf[t]
+            h = g / (1 + np.exp(-g)) * u
+            want[t] += (dec(db, ds, hidden, inter, e) @ h) * w[t, i]
+    np.testing.assert_allclose(y, want, rtol=1e-5, atol=1e-5 * np.abs(want).max())
+    # dropping the routing weight, or the up projection, is far off
+    assert np.abs(y - want / np.maximum(w.max(), 1e-9)).max() > 1e-4 * np.abs(want).max()
