@@ -54,6 +54,26 @@ void* workspace(size_t bytes, int* status) {
     *status = KDQ_OK;
     return w.ptr;
 }
+
+unsigned compute_units() {
+    static std::mutex mutex;
+    static std::vector<unsigned> cached;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess)
+        return 256;
+    std::lock_guard<std::mutex> lock(mutex);
+    if (cached.size() <= size_t(device))
+        cached.resize(size_t(device) + 1, 0);
+    if (!cached[size_t(device)]) {
+        int count = 0;
+        cached[size_t(device)] =
+            hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device) ==
+                        hipSuccess && count > 0
+                ? unsigned(count)
+                : 256u;
+    }
+    return cached[size_t(device)];
+}
 }  // namespace kdq
 
 extern "C" const char* kdq_status_string(int status) {

@@ -156,6 +156,11 @@ __global__ __launch_bounds__(256) void exact_gemv(const uint8_t* weights, size_t
 constexpr int kThreads = 1024, kWaves = 16;
 constexpr int kSlot = 64;         // weights per lane per row step
 constexpr int kWindow = 64 * kSlot;  // weights per wavefront per row step
+// LDS bytes per staged slot: 128 bytes of hi/lo planes padded to 144, so that 16-byte
+// reads by consecutive lanes (stride 144 = 36 banks) touch every bank once per pass,
+// plus the slot's 16 bytes of scales and sums.
+constexpr int kXPitch = 144;
+constexpr int kSlotLds = kXPitch + 16;
 
 // LDS byte offset, inside one 128-byte slot, of the (hi, lo) dword pair holding the
 // four activation values that start at position p (p % 4 == 0) of the slot.  The
@@ -178,56 +183,66 @@ template <int ENC> __device__ __forceinline__ unsigned pair_offset(unsigned p) {
 }
 
 // Quantizes R activation rows into LDS:
-//   xq[(r*slots + slot)*128 + ...]  hi/lo int8 planes in pair order
+//   xq[(r*slots + slot)*kXPitch + ...]  hi/lo int8 planes in pair order
 //   xs[r*slots + slot] = (s0, sum0, s1, sum1) for the slot's two 32-value groups
 // x_q = round(x * 32639 / amax) split as x_q = 256*hi + lo, hi, lo in int8.
-template <int ENC, int R>
-__device__ void stage_activations(const float* __restrict__ x, unsigned in, uint8_t* xq,
-                                  float* xs) {
+// A unit is 8 consecutive values of one row; unit u is row u / (in/8).
+struct XUnit {
+    float4 a, b;
+};
+
+__device__ __forceinline__ void load_unit(const float* x, unsigned in, unsigned u, XUnit& v) {
+    const unsigned r = u / (in / 8), e = (u % (in / 8)) * 8;
+    const float4* src = reinterpret_cast<const float4*>(x + size_t(r) * in + e);
+    v.a = src[0];
+    v.b = src[1];
+}
+
+// Every thread of a group of four (one 32-value group) must call this together.
+template <int ENC>
+__device__ __forceinline__ void stage_unit(unsigned in, unsigned u, const XUnit& xu,
+                                           uint8_t* xq, float* xs) {
     const unsigned slots = in / kSlot;
-    const unsigned units = R * in / 8;
-    for (unsigned u = threadIdx.x; u < units; u += kThreads) {
-        const unsigned r = u / (in / 8), e = (u % (in / 8)) * 8;
-        const float4* src = reinterpret_cast<const float4*>(x + size_t(r) * in + e);
-        const float4 a = src[0], b = src[1];
-        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-        float amax = 0.f, sum = 0.f;
+    const unsigned r = u / (in / 8), e = (u % (in / 8)) * 8;
+    const float v[8] = {xu.a.x, xu.a.y, xu.a.z, xu.a.w, xu.b.x, xu.b.y, xu.b.z, xu.b.w};
+    float amax = 0.f, sum = 0.f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            amax = fmaxf(amax, fabsf(v[i]));
-            sum += v[i];
-        }
-        bool finite = true;
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            finite = finite && isfinite(v[i]);
-        // four consecutive threads hold one 32-value group
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);
-        finite = __shfl_xor(int(finite), 1, 64) && finite;
-        finite = __shfl_xor(int(finite), 2, 64) && finite;
-        const float inv = amax > 0.f ? 32639.0f / amax : 0.f;
-        const float scale = finite ? amax / 32639.0f : __builtin_nanf("");
-        unsigned hi[2] = {0, 0}, lo[2] = {0, 0};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            int q = __float2int_rn(v[i] * inv);
-            q = min(32639, max(-32639, q));
-            const int h = (q + 128) >> 8;
-            const int l = q - h * 256;
-            hi[i / 4] |= (unsigned(h) & 255u) << (8 * (i % 4));
-            lo[i / 4] |= (unsigned(l) & 255u) << (8 * (i % 4));
-        }
-        const unsigned slot = e / kSlot, p = e % kSlot;
-        uint8_t* base = xq + (size_t(r) * slots + slot) * 128;
-        *reinterpret_cast<uint2*>(base + pair_offset<ENC>(p)) = make_uint2(hi[0], lo[0]);
-        *reinterpret_cast<uint2*>(base + pair_offset<ENC>(p + 4)) = make_uint2(hi[1], lo[1]);
-        if ((u & 3u) == 0)
-            *reinterpret_cast<float2*>(xs + (size_t(r) * slots + slot) * 4 + (p / 32) * 2) =
-                make_float2(scale, sum);
+    for (int i = 0; i < 8; ++i) {
+        amax = fmaxf(amax, fabsf(v[i]));
+        sum += v[i];
     }
+    bool finite = true;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        finite = finite && isfinite(v[i]);
+    // four consecutive threads (one DPP quad) hold one 32-value group
+    amax = fmaxf(amax, quad_xor1(amax));
+    amax = fmaxf(amax, quad_xor2(amax));
+    sum += quad_xor1(sum);
+    sum += quad_xor2(sum);
+    int ok = finite;
+    ok &= quad_xor1(ok);
+    ok &= quad_xor2(ok);
+    finite = ok != 0;
+    const float inv = amax > 0.f ? 32639.0f / amax : 0.f;
+    const float scale = finite ? amax / 32639.0f : __builtin_nanf("");
+    unsigned hi[2] = {0, 0}, lo[2] = {0, 0};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        int q = __float2int_rn(v[i] * inv);
+        q = min(32639, max(-32639, q));
+        const int h = (q + 128) >> 8;
+        const int l = q - h * 256;
+        hi[i / 4] |= (unsigned(h) & 255u) << (8 * (i % 4));
+        lo[i / 4] |= (unsigned(l) & 255u) << (8 * (i % 4));
+    }
+    const unsigned slot = e / kSlot, p = e % kSlot;
+    uint8_t* base = xq + (size_t(r) * slots + slot) * kXPitch;
+    *reinterpret_cast<uint2*>(base + pair_offset<ENC>(p)) = make_uint2(hi[0], lo[0]);
+    *reinterpret_cast<uint2*>(base + pair_offset<ENC>(p + 4)) = make_uint2(hi[1], lo[1]);
+    if ((u & 3u) == 0)
+        *reinterpret_cast<float2*>(xs + (size_t(r) * slots + slot) * 4 + (p / 32) * 2) =
+            make_float2(scale, sum);
 }
 
 // Packed weights of one lane for one row step.
@@ -270,7 +285,7 @@ struct XSlot {
 
 __device__ __forceinline__ void load_x(const uint8_t* xq, const float* xs, size_t index,
                                        XSlot& X) {
-    const u32x4* q = reinterpret_cast<const u32x4*>(xq + index * 128);
+    const u32x4* q = reinterpret_cast<const u32x4*>(xq + index * kXPitch);
 #pragma unroll
     for (int m = 0; m < 8; ++m)
         X.q[m] = q[m];
@@ -370,25 +385,37 @@ __device__ __forceinline__ float lane_dot(const Lane& L, unsigned slot, const XS
 // Rows whose packed weights are loaded before any of them is reduced.
 template <int R> constexpr int rows_in_flight = R == 1 ? 4 : 2;
 
-// Workgroup: 16 wavefronts.  The row is cut into `nw` windows of 4096 values (nw
-// divides 16); wavefront w takes window w % nw of the rows r0 + w/nw, r0 + w/nw +
-// 16/nw, ...  in [r0, r0 + rows_per_wg).  With nw > 1 the window partials meet in LDS
-// and are summed in window order.
+// Packed weights of the rows base, base + stride, ... (kRows of them, those below r1).
+template <int ENC, int kRows>
+__device__ __forceinline__ void load_rows(const uint8_t* weights, size_t row_bytes,
+                                          unsigned base, unsigned stride, unsigned r1,
+                                          unsigned slot, bool active, Lane (&L)[kRows]) {
+#pragma unroll
+    for (int u = 0; u < kRows; ++u) {
+        const unsigned n = base + u * stride;
+        if (active && n < r1)
+            load_lane<ENC>(weights + size_t(n) * row_bytes, slot, L[u]);
+    }
+}
+
+// Workgroup: 16 wavefronts, one workgroup per compute unit.  The row is cut into `nw`
+// windows of 4096 values (nw divides 16); wavefront w takes window w % nw of the rows
+// r0 + w/nw, r0 + w/nw + 16/nw, ...  in [r0, r0 + rows_per_wg).  With nw > 1 the window
+// partials meet in LDS and are summed in window order.  The first rows' packed weights
+// are requested before the activations are staged, so their HBM latency overlaps the
+// staging instead of following it.
 template <int ENC, int R>
 __global__ __launch_bounds__(kThreads) void fast_gemv(const uint8_t* __restrict__ weights,
-                                                      size_t row_bytes,
-                                                      const float* __restrict__ x, unsigned in,
-                                                      unsigned out, float* __restrict__ y,
-                                                      size_t stride, unsigned* status,
-                                                      unsigned rows_per_wg, unsigned nw) {
+                                                      size_t row_bytes, const float* x,
+                                                      unsigned in, unsigned out,
+                                                      float* __restrict__ y, size_t stride,
+                                                      unsigned* status, unsigned rows_per_wg,
+                                                      unsigned nw) {
     extern __shared__ __align__(16) uint8_t lds[];
     const unsigned slots = in / kSlot;
     uint8_t* xq = lds;
-    float* xs = reinterpret_cast<float*>(lds + size_t(R) * slots * 128);
+    float* xs = reinterpret_cast<float*>(lds + size_t(R) * slots * kXPitch);
     float* partial = xs + size_t(R) * slots * 4;
-
-    stage_activations<ENC, R>(x, in, xq, xs);
-    __syncthreads();
 
     const unsigned wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const unsigned window = wave % nw, groups = kWaves / nw, group = wave / nw;
@@ -396,7 +423,35 @@ __global__ __launch_bounds__(kThreads) void fast_gemv(const uint8_t* __restrict_
     const bool active = slot < slots;
     const unsigned r0 = blockIdx.x * rows_per_wg;
     const unsigned r1 = min(out, r0 + rows_per_wg);
+    constexpr int kRowsInFlight = rows_in_flight<R>;
     bool bad = false;
+
+    // Load order: this thread's first activation unit, then the first rows' packed
+    // weights, then the staging that uses the activations.  Both load sets are issued
+    // by every lane unconditionally (indices past the end are clamped to valid data),
+    // so the wait before the staging counts exactly the weight loads and does not wait
+    // for them.
+    const unsigned units = R * in / 8;
+    XUnit first_unit;
+    load_unit(x, in, min(unsigned(threadIdx.x), units - 1), first_unit);
+    asm volatile("" ::: "memory");  // x is not restrict: its loads stay before this point
+    __builtin_amdgcn_sched_barrier(0);
+    Lane L[kRowsInFlight];
+    unsigned base = r0 + group;
+#pragma unroll
+    for (int u = 0; u < kRowsInFlight; ++u)
+        load_lane<ENC>(weights + size_t(min(base + u * groups, r1 - 1)) * row_bytes,
+                       min(slot, slots - 1), L[u]);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    if (threadIdx.x < units)
+        stage_unit<ENC>(in, threadIdx.x, first_unit, xq, xs);
+    for (unsigned u = threadIdx.x + kThreads; u < units; u += kThreads) {
+        XUnit more;
+        load_unit(x, in, u, more);
+        stage_unit<ENC>(in, u, more, xq, xs);
+    }
+    __syncthreads();
 
     XSlot X[1];  // single-row passes keep the activation slot in registers
     if constexpr (R == 1) {
@@ -406,15 +461,9 @@ __global__ __launch_bounds__(kThreads) void fast_gemv(const uint8_t* __restrict_
                 load_x(xq, xs, size_t(r) * slots + slot, X[r]);
     }
 
-    constexpr int kRowsInFlight = rows_in_flight<R>;
-    for (unsigned base = r0 + group; base < r1; base += kRowsInFlight * groups) {
-        Lane L[kRowsInFlight];
-#pragma unroll
-        for (int u = 0; u < kRowsInFlight; ++u) {
-            const unsigned n = base + u * groups;
-            if (active && n < r1)
-                load_lane<ENC>(weights + size_t(n) * row_bytes, slot, L[u]);
-        }
+    for (bool first = true; base < r1; base += kRowsInFlight * groups, first = false) {
+        if (!first)
+            load_rows<ENC, kRowsInFlight>(weights, row_bytes, base, groups, r1, slot, active, L);
 #pragma unroll
         for (int u = 0; u < kRowsInFlight; ++u) {
             const unsigned n = base + u * groups;
@@ -432,7 +481,7 @@ __global__ __launch_bounds__(kThreads) void fast_gemv(const uint8_t* __restrict_
                         v = lane_dot<ENC>(L[u], slot, Xr, bad);
                     }
                 }
-                v = wave_sum(v);
+                v = wave_total(v);
                 if (lane == 0) {
                     if (nw == 1)
                         y[size_t(r) * stride + n] = v;
@@ -504,19 +553,17 @@ bool plan_fast(size_t rows, size_t in, size_t out, FastPlan& p) {
         nw *= 2;
     if (nw > 16)
         return false;
-    const unsigned groups = kWaves / nw;
-    // batch rows per pass: the staged activations (2.25 bytes per value) must fit
+    // batch rows per pass: the staged activations (2.5 bytes per value) must fit
     unsigned batch = 1;
-    while (batch < 8 && batch < rows && size_t(batch * 2) * in * 9 / 4 <= 96 * 1024)
+    while (batch < 8 && batch < rows && size_t(batch * 2) * (in / kSlot) * kSlotLds <= 96 * 1024)
         batch *= 2;
-    // about two rows per wavefront group, and at most ~512 workgroups
-    size_t rows_per_wg = std::max<size_t>(size_t(groups) * 2, (out + 511) / 512);
-    rows_per_wg = (rows_per_wg + groups - 1) / groups * groups;
+    // one workgroup per compute unit: every wavefront's rows are requested up front
+    const size_t rows_per_wg = std::max<size_t>(1, (out + compute_units() - 1) / compute_units());
     p.nw = nw;
     p.batch = batch;
     p.rows_per_wg = unsigned(rows_per_wg);
     p.grid = unsigned((out + rows_per_wg - 1) / rows_per_wg);
-    p.lds = size_t(batch) * (in / kSlot) * 144 + (nw > 1 ? rows_per_wg * batch * nw * 4 : 0);
+    p.lds = size_t(batch) * (in / kSlot) * kSlotLds + (nw > 1 ? rows_per_wg * batch * nw * 4 : 0);
     return p.lds <= 160 * 1024;
 }
 
@@ -549,7 +596,8 @@ int launch_fast(const void* w, size_t row_bytes, const float* x, size_t rows, si
         while (r > left)
             r /= 2;
         FastPlan q = p;
-        q.lds = size_t(r) * (in / kSlot) * 144 + (p.nw > 1 ? size_t(p.rows_per_wg) * r * p.nw * 4 : 0);
+        q.lds = size_t(r) * (in / kSlot) * kSlotLds +
+                (p.nw > 1 ? size_t(p.rows_per_wg) * r * p.nw * 4 : 0);
         int rc;
         const float* xs = x + first * in;
         float* ys = y + first * stride;

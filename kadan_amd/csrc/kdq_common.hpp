@@ -61,6 +61,42 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Lanes of the rows in ROW_MASK read lane-permuted `v` (DPP control CTRL); the other
+// rows read 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_read(float v) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+// Sum over the 64 lanes with DPP row operations (no LDS traffic): pairs, quads, half
+// rows and rows of 16 by permutation, then the row totals are chained into lane 63,
+// whose value every lane returns.  Needs all 64 lanes active.
+__device__ __forceinline__ float wave_total(float v) {
+    v += dpp_read<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]
+    v += dpp_read<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]
+    v += dpp_read<0x141, 0xf>(v);  // row_half_mirror
+    v += dpp_read<0x140, 0xf>(v);  // row_mirror: every lane holds its row's sum
+    v += dpp_read<0x142, 0xa>(v);  // row_bcast:15 -> rows 1 and 3
+    v += dpp_read<0x143, 0xc>(v);  // row_bcast:31 -> rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Butterfly partner within each group of four lanes (xor 1 / xor 2) by DPP quad
+// permutation; all four lanes of a group must be active.
+__device__ __forceinline__ float quad_xor1(float v) {
+    return dpp_read<0xb1, 0xf>(v);
+}
+__device__ __forceinline__ float quad_xor2(float v) {
+    return dpp_read<0x4e, 0xf>(v);
+}
+__device__ __forceinline__ int quad_xor1(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, 0xb1, 0xf, 0xf, false);
+}
+__device__ __forceinline__ int quad_xor2(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, 0x4e, 0xf, 0xf, false);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int offset = 32; offset > 0; offset >>= 1)
@@ -100,6 +136,9 @@ int hip_failure(hipError_t error);
 
 // Per-device cached workspace (grown on demand, released by kdq_release_scratch).
 void* workspace(size_t bytes, int* status);
+
+// Compute units of the current device (cached per device; 256 if the query fails).
+unsigned compute_units();
 
 inline bool overlaps(const void* a, size_t an, const void* b, size_t bn) {
     if (!a || !b || !an || !bn)
