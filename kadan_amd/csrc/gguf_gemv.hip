@@ -506,6 +506,323 @@ __global__ __launch_bounds__(kThreads) void fast_gemv(const uint8_t* __restrict_
     }
 }
 
+// -------------------------------------------------------------- MFMA GEMV
+//
+// The product on v_mfma_i32_16x16x64_i8.  One MFMA multiplies a 16 x 64 activation
+// operand A by a 64 x 16 weight operand B: the 16 columns of B are 16 weight rows (a
+// tile), and its 64 k values are four lane groups G of 16, where group G carries the
+// 64-value chunk G of a 256-value group g of the row (Q4_K: the sub-block pair G of the
+// super-block; Q8_0 / Q4_0: the block pair 2G, 2G+1).  Within a chunk, block (or
+// sub-block) b = 0, 1 holds positions t = 0..31, and MFMA m (0..3) takes positions
+// 8m..8m+7 of both: B element e of group G is position 8m + e%8 of block e/8.
+// A is block-diagonal: row 4G + 2b + plane carries, in group G's k values of block b,
+// the activation codes of plane `plane` (0: high byte, 1: low byte of the 16-bit code);
+// so C row 4G + v (v = 2b + plane) of column j is the exact integer sum of block b of
+// chunk G of weight row j against one byte plane.  Every lane of C holds useful sums:
+// lane l = 16G + j has rows 4G..4G+3 of column j.  Weight scales are applied to those
+// integers in fp32, per lane, from the lane's own row header; the 64 per-(row, chunk)
+// partials meet in LDS at the end of a pass and are summed in a fixed order.
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMThreads = 1024;   // 16 wavefronts
+constexpr int kAGroup = 1024;     // LDS bytes of A operands per 256-value group
+constexpr int kPartialPitch = 17; // floats per lane in the pass partials (bank spread)
+
+// Tiles of 16 rows per pass, and units (tile, 256-value group) in flight per wavefront.
+template <int R> constexpr int mfma_tiles = R >= 4 ? 1 : 4 / R;
+template <int ENC, int R>
+constexpr int mfma_units = R == 1 ? (ENC == KDQ_Q8_0 ? 2 : 4) : (R == 2 ? 2 : 1);
+
+// LDS layout of mfma_gemv (bytes):
+//   [0, 1024)                                       zeros (A operand of non-carrier lanes)
+//   A table, per batch row r and group g:           kAGroup bytes, entry (m*16 + 4G + v)
+//       is the 16-byte A register of MFMA m for lane 16G + 4G + v (v = 2b + plane):
+//       bytes 8b..8b+7 hold plane `plane` of positions 8m..8m+7 of block b of chunk
+//       4g + G; the other 8 bytes are zero
+//   block table, per batch row r and 32-value block: float4 (s, sum x, sum of codes as
+//       int bits, 0)
+//   partials [R][tiles][64 lanes][kPartialPitch] floats
+struct MfmaLds {
+    size_t a, blocks, partial, total;
+};
+
+__host__ __device__ inline MfmaLds mfma_layout(unsigned batch, unsigned in) {
+    const size_t tiles = batch >= 4 ? 1 : 4 / batch;
+    MfmaLds l;
+    l.a = 1024;
+    l.blocks = l.a + size_t(batch) * (in / 256) * kAGroup;
+    l.partial = l.blocks + size_t(batch) * (in / 32) * 16;
+    l.total = l.partial + size_t(batch) * tiles * 64 * kPartialPitch * 4;
+    return l;
+}
+
+// Quantizes one unit of 8 activation values (the 16-bit block code of stage_unit) into
+// the A table and the block table.  The four threads of a DPP quad hold one block.
+__device__ __forceinline__ void mstage_unit(unsigned in, unsigned u, const XUnit& xu,
+                                            uint8_t* atab, float4* blocks) {
+    const unsigned r = u / (in / 8), e0 = (u % (in / 8)) * 8;
+    const unsigned g = e0 / 256, G = (e0 % 256) / 64, b = (e0 % 64) / 32, m = (e0 % 32) / 8;
+    const float v[8] = {xu.a.x, xu.a.y, xu.a.z, xu.a.w, xu.b.x, xu.b.y, xu.b.z, xu.b.w};
+    float amax = 0.f, sum = 0.f;
+    int ok = 1;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        amax = fmaxf(amax, fabsf(v[i]));
+        sum += v[i];
+        ok &= int(isfinite(v[i]));
+    }
+    amax = fmaxf(amax, quad_xor1(amax));
+    amax = fmaxf(amax, quad_xor2(amax));
+    sum += quad_xor1(sum);
+    sum += quad_xor2(sum);
+    ok &= quad_xor1(ok);
+    ok &= quad_xor2(ok);
+    const float inv = amax > 0.f ? 32639.0f / amax : 0.f;
+    const float scale = ok ? amax / 32639.0f : __builtin_nanf("");
+    unsigned hi[2] = {0, 0}, lo[2] = {0, 0};
+    int codes = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        int q = __float2int_rn(v[i] * inv);
+        q = min(32639, max(-32639, q));
+        codes += q;
+        const int h = (q + 128) >> 8;
+        const int l = q - h * 256;
+        hi[i / 4] |= (unsigned(h) & 255u) << (8 * (i % 4));
+        lo[i / 4] |= (unsigned(l) & 255u) << (8 * (i % 4));
+    }
+    codes += quad_xor1(codes);
+    codes += quad_xor2(codes);
+    uint8_t* entry = atab + (size_t(r) * (in / 256) + g) * kAGroup + (m * 16 + 4 * G + 2 * b) * 16;
+    *reinterpret_cast<uint4*>(entry) = b ? make_uint4(0, 0, hi[0], hi[1]) : make_uint4(hi[0], hi[1], 0, 0);
+    *reinterpret_cast<uint4*>(entry + 16) =
+        b ? make_uint4(0, 0, lo[0], lo[1]) : make_uint4(lo[0], lo[1], 0, 0);
+    if (m == 0)
+        blocks[size_t(r) * (in / 32) + e0 / 32] = make_float4(scale, sum, __int_as_float(codes), 0.f);
+}
+
+// B operand of MFMA m from one lane's packed chunk (load_lane layout).
+template <int ENC>
+__device__ __forceinline__ i32x4 b_operand(const Lane& L, int m) {
+    if constexpr (ENC == KDQ_Q4_K) {
+        // code bytes 8m..8m+7 of the pair: low nibbles are sub-block 2G (kept as 0..15),
+        // high nibbles sub-block 2G+1, kept in place as 16q - 128 (one bit operation)
+        const unsigned w0 = L.w[4 + 2 * m], w1 = L.w[5 + 2 * m];
+        return i32x4{int(w0 & 0x0f0f0f0fu), int(w1 & 0x0f0f0f0fu),
+                     int((w0 & 0xf0f0f0f0u) ^ 0x80808080u),
+                     int((w1 & 0xf0f0f0f0u) ^ 0x80808080u)};
+    } else if constexpr (ENC == KDQ_Q8_0) {
+        // block 0 codes start 2 bytes into dword 0, block 1 codes at dword 9
+        return i32x4{int(__builtin_amdgcn_alignbyte(L.w[2 * m + 1], L.w[2 * m], 2)),
+                     int(__builtin_amdgcn_alignbyte(L.w[2 * m + 2], L.w[2 * m + 1], 2)),
+                     int(L.w[9 + 2 * m]), int(L.w[10 + 2 * m])};
+    } else {
+        // positions 0..15 are low nibbles of code bytes 0..15, 16..31 high nibbles
+        const int k = 2 * (m % 2);
+        const unsigned a0 = __builtin_amdgcn_alignbyte(L.w[k + 1], L.w[k], 2);
+        const unsigned a1 = __builtin_amdgcn_alignbyte(L.w[k + 2], L.w[k + 1], 2);
+        const unsigned c0 = L.w[5 + k], c1 = L.w[6 + k];
+        const int shift = m >= 2 ? 4 : 0;
+        return i32x4{int((a0 >> shift) & 0x0f0f0f0fu), int((a1 >> shift) & 0x0f0f0f0fu),
+                     int((c0 >> shift) & 0x0f0f0f0fu), int((c1 >> shift) & 0x0f0f0f0fu)};
+    }
+}
+
+// Per-lane constants of the Q4_K scale decode for sub-blocks 2G, 2G+1.
+struct ScaleSel {
+    unsigned shift;
+    bool high;
+};
+
+// The chunk's contribution from the four integer sums of this lane (c.x, c.y: block 0
+// high and low planes; c.z, c.w: block 1) with the activation block entries x0, x1.
+template <int ENC>
+__device__ __forceinline__ float chunk_value(const Lane& L, ScaleSel sel, i32x4 c, float4 x0,
+                                             float4 x1, bool& bad) {
+    const float A0 = float(c.x * 256 + c.y);
+    if constexpr (ENC == KDQ_Q4_K) {
+        const float d = half_hw(L.w[0] & 0xffffu), dmin = half_hw(L.w[0] >> 16);
+        bad |= !isfinite(d) || !isfinite(dmin);
+        const unsigned b1 = L.w[1] >> sel.shift, b2 = L.w[2] >> sel.shift,
+                       b3 = L.w[3] >> sel.shift;
+        unsigned sca, ma, scb, mb;
+        if (!sel.high) {
+            sca = b1 & 63u, ma = b2 & 63u;
+            scb = (b1 >> 8) & 63u, mb = (b2 >> 8) & 63u;
+        } else {
+            sca = (b3 & 15u) | ((b1 >> 2) & 48u);
+            ma = ((b3 >> 4) & 15u) | ((b2 >> 2) & 48u);
+            scb = ((b3 >> 8) & 15u) | ((b1 >> 10) & 48u);
+            mb = ((b3 >> 12) & 15u) | ((b2 >> 10) & 48u);
+        }
+        // block 1 codes entered as 16q - 128: sum q x = (sum (16q - 128) x + 128 sum x) / 16
+        const float A1 = float((c.z * 256 + c.w + 128 * __float_as_int(x1.z)) >> 4);
+        const float fa = d * float(sca), fb = d * float(scb);
+        const float oa = dmin * float(ma), ob = dmin * float(mb);
+        float acc = fa * (x0.x * A0);
+        acc = fmaf(fb, x1.x * A1, acc);
+        acc = fmaf(-oa, x0.y, acc);
+        return fmaf(-ob, x1.y, acc);
+    } else if constexpr (ENC == KDQ_Q4_0) {
+        const float d0 = half_hw(L.w[0] & 0xffffu), d1 = half_hw(L.w[4] >> 16);
+        bad |= !isfinite(d0) || !isfinite(d1);
+        const float A1 = float(c.z * 256 + c.w);
+        // sum (q - 8) x = s * sum q x_q - 8 * sum x
+        const float t0 = fmaf(x0.x, A0, -8.f * x0.y);
+        const float t1 = fmaf(x1.x, A1, -8.f * x1.y);
+        return fmaf(d1, t1, d0 * t0);
+    } else {
+        const float d0 = half_hw(L.w[0] & 0xffffu), d1 = half_hw(L.w[8] >> 16);
+        bad |= !isfinite(d0) || !isfinite(d1);
+        const float A1 = float(c.z * 256 + c.w);
+        return fmaf(d1 * x1.x, A1, d0 * x0.x * A0);
+    }
+}
+
+// Sum over each aligned group of 16 lanes (DPP row), returned to every lane of it.
+__device__ __forceinline__ float row16_total(float v) {
+    v += dpp_read<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]
+    v += dpp_read<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]
+    v += dpp_read<0x141, 0xf>(v);  // row_half_mirror
+    v += dpp_read<0x140, 0xf>(v);  // row_mirror
+    return v;
+}
+
+// A wavefront's position in its unit sequence: group g = wave + 16q, tile t.
+struct UnitCursor {
+    unsigned g, t;
+    __device__ __forceinline__ void next(unsigned tiles) {
+        if (++t == tiles) {
+            t = 0;
+            g += 16;
+        }
+    }
+};
+
+// Workgroup: 16 wavefronts, one workgroup per compute unit, rows [r0, r1), processed in
+// passes of up to kTiles tiles.  In a pass, wavefront w takes the units (g, t) for
+// g = w, w + 16, ... and every tile t, kUnits at a time.  Loads are issued by every lane
+// unconditionally (rows past r1 and units past the wavefront's last are clamped to valid
+// data and their results discarded), so waits count exactly.  Order: this thread's first
+// activation unit, the first units' packed weights, then the staging.
+template <int ENC, int R>
+__global__ __launch_bounds__(kMThreads) void mfma_gemv(const uint8_t* __restrict__ weights,
+                                                       size_t row_bytes, const float* x,
+                                                       unsigned in, unsigned out,
+                                                       float* __restrict__ y, size_t stride,
+                                                       unsigned* status, unsigned rows_per_wg) {
+    constexpr int kTiles = mfma_tiles<R>;
+    constexpr int kUnits = mfma_units<ENC, R>;
+    constexpr int kRowUnroll = R <= 2 ? R : 1;  // larger batches: one row's operands at a time
+    extern __shared__ __align__(16) uint8_t lds[];
+    const MfmaLds layout = mfma_layout(R, in);
+    const unsigned groups = in / 256;
+    uint8_t* atab = lds + layout.a;
+    float4* blocks = reinterpret_cast<float4*>(lds + layout.blocks);
+    float* partial = reinterpret_cast<float*>(lds + layout.partial);
+
+    const unsigned wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const unsigned lane = threadIdx.x % 64;
+    const unsigned j = lane % 16, G = lane / 16;
+    // A operand base: carrier lanes (row j of A lies in their group) read their table
+    // entry, the others a zero region; MFMA m adds m * 256 bytes
+    const bool carrier = j / 4 == G;
+    const ScaleSel sel{8 * ((2 * G) & 3), G >= 2};
+    const unsigned r0 = blockIdx.x * rows_per_wg, r1 = min(out, r0 + rows_per_wg);
+    bool bad = false;
+
+    for (unsigned t = threadIdx.x; t < 256; t += kMThreads)
+        reinterpret_cast<uint32_t*>(lds)[t] = 0u;
+
+    auto pass_tiles = [&](unsigned p0) { return min(unsigned(kTiles), (r1 - p0 + 15) / 16); };
+    auto load_units = [&](unsigned p0, UnitCursor cur, Lane(&L)[kUnits]) {
+        const unsigned tiles = pass_tiles(p0);
+#pragma unroll
+        for (int k = 0; k < kUnits; ++k) {
+            const bool valid = cur.g < groups;
+            const unsigned g = valid ? cur.g : wave % groups, t = valid ? cur.t : 0;
+            const unsigned n = min(p0 + 16 * t + j, r1 - 1);
+            load_lane<ENC>(weights + size_t(n) * row_bytes, 4 * g + G, L[k]);
+            cur.next(tiles);
+        }
+    };
+
+    const unsigned units_x = R * in / 8;
+    XUnit first_unit;
+    load_unit(x, in, min(unsigned(threadIdx.x), units_x - 1), first_unit);
+    asm volatile("" ::: "memory");  // x is not restrict: its loads stay before this point
+    __builtin_amdgcn_sched_barrier(0);
+    Lane L[kUnits];
+    load_units(r0, UnitCursor{wave, 0}, L);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    if (threadIdx.x < units_x)
+        mstage_unit(in, threadIdx.x, first_unit, atab, blocks);
+    for (unsigned u = threadIdx.x + kMThreads; u < units_x; u += kMThreads) {
+        XUnit more;
+        load_unit(x, in, u, more);
+        mstage_unit(in, u, more, atab, blocks);
+    }
+    __syncthreads();
+
+    bool first = true;
+    for (unsigned p0 = r0; p0 < r1; p0 += 16 * kTiles) {
+        const unsigned tiles = pass_tiles(p0);
+        // partial[((r*kTiles + t)*64 + lane)*kPartialPitch + wave] belongs to this thread
+        float* mine = partial + size_t(lane) * kPartialPitch + wave;
+#pragma unroll
+        for (int i = 0; i < R * kTiles; ++i)
+            mine[size_t(i) * 64 * kPartialPitch] = 0.f;
+        for (UnitCursor cur{wave, 0}; cur.g < groups;) {
+            if (!first)
+                load_units(p0, cur, L);
+            first = false;
+#pragma unroll
+            for (int k = 0; k < kUnits; ++k) {
+                if (cur.g >= groups)
+                    break;
+                const unsigned chunk = 4 * cur.g + G;
+#pragma unroll kRowUnroll
+                for (int r = 0; r < R; ++r) {
+                    const uint8_t* a = carrier ? atab + (size_t(r) * groups + cur.g) * kAGroup +
+                                                     (4 * G + j % 4) * 16
+                                               : lds;
+                    i32x4 c = {0, 0, 0, 0};
+#pragma unroll
+                    for (int m = 0; m < 4; ++m)
+                        c = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                            *reinterpret_cast<const i32x4*>(a + m * 256),
+                            b_operand<ENC>(L[k], m), c, 0, 0, 0);
+                    const float4* xb = blocks + size_t(r) * (in / 32) + 2 * chunk;
+                    mine[size_t(r * kTiles + cur.t) * 64 * kPartialPitch] +=
+                        chunk_value<ENC>(L[k], sel, c, xb[0], xb[1], bad);
+                }
+                cur.next(tiles);
+            }
+        }
+        first = false;  // a wavefront without units in the first pass never used its loads
+        __syncthreads();
+        // output o = (r*tiles + t)*16 + jj: 16 threads (one DPP row), thread k sums
+        // wavefront k's four lane groups, then the row of 16 is summed
+        const unsigned outputs = R * tiles * 16;
+        for (unsigned o = threadIdx.x / 16; o < outputs; o += kMThreads / 16) {
+            const unsigned k = threadIdx.x % 16;
+            const unsigned jj = o % 16, t = (o / 16) % tiles, r = o / (16 * tiles);
+            const float* src = partial + (size_t(r * kTiles + t) * 64 + jj) * kPartialPitch + k;
+            float v = ((src[0] + src[16 * kPartialPitch]) + src[32 * kPartialPitch]) +
+                      src[48 * kPartialPitch];
+            v = row16_total(v);
+            const unsigned n = p0 + 16 * t + jj;
+            if (k == 0 && n < r1)
+                y[size_t(r) * stride + n] = v;
+        }
+        __syncthreads();
+    }
+    if (status && __any(bad) && lane == 0)
+        atomicOr(status, 1u);
+}
+
 // ----------------------------------------------------------------- host side
 
 template <int ENC>
@@ -622,6 +939,83 @@ int launch_fast(const void* w, size_t row_bytes, const float* x, size_t rows, si
     return KDQ_OK;
 }
 
+// LDS bytes of mfma_gemv for `batch` rows.
+size_t mfma_lds(size_t batch, size_t in) {
+    return mfma_layout(unsigned(batch), unsigned(in)).total;
+}
+
+struct MfmaPlan {
+    unsigned rows_per_wg, grid, batch;
+};
+
+// One workgroup per compute unit; batch rows per pass as the LDS allows (at most 8).
+bool plan_mfma(size_t rows, size_t in, size_t out, MfmaPlan& p) {
+    constexpr size_t limit = 160 * 1024;
+    if (in % 256 || mfma_lds(1, in) > limit)
+        return false;
+    unsigned batch = 1;
+    while (batch < 8 && batch < rows && mfma_lds(batch * 2, in) <= limit)
+        batch *= 2;
+    const size_t cus = compute_units();
+    const size_t rows_per_wg = std::max<size_t>(1, (out + cus - 1) / cus);
+    p.batch = batch;
+    p.rows_per_wg = unsigned(rows_per_wg);
+    p.grid = unsigned((out + rows_per_wg - 1) / rows_per_wg);
+    return true;
+}
+
+template <int ENC, int R>
+int launch_mfma_pass(const MfmaPlan& p, const void* w, size_t row_bytes, const float* x,
+                     size_t in, size_t out, float* y, size_t stride, unsigned* status,
+                     hipStream_t stream) {
+    static bool configured = false;  // one attribute call per instantiation
+    if (!configured) {
+        KDQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&mfma_gemv<ENC, R>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+        configured = true;
+    }
+    hipLaunchKernelGGL((mfma_gemv<ENC, R>), dim3(p.grid), dim3(kMThreads), mfma_lds(R, in),
+                       stream, static_cast<const uint8_t*>(w), row_bytes, x, unsigned(in),
+                       unsigned(out), y, stride, status, p.rows_per_wg);
+    KDQ_HIP(hipGetLastError());
+    return KDQ_OK;
+}
+
+template <int ENC>
+int launch_mfma(const void* w, size_t row_bytes, const float* x, size_t rows, size_t in,
+                size_t out, float* y, size_t stride, unsigned* status, hipStream_t stream) {
+    MfmaPlan p;
+    if (!plan_mfma(rows, in, out, p))
+        return KDQ_ERR_UNSUPPORTED;
+    for (size_t first = 0; first < rows;) {
+        const size_t left = rows - first;
+        unsigned r = p.batch;
+        while (r > left)
+            r /= 2;
+        const float* xs = x + first * in;
+        float* ys = y + first * stride;
+        int rc;
+        switch (r) {
+        case 1:
+            rc = launch_mfma_pass<ENC, 1>(p, w, row_bytes, xs, in, out, ys, stride, status, stream);
+            break;
+        case 2:
+            rc = launch_mfma_pass<ENC, 2>(p, w, row_bytes, xs, in, out, ys, stride, status, stream);
+            break;
+        case 4:
+            rc = launch_mfma_pass<ENC, 4>(p, w, row_bytes, xs, in, out, ys, stride, status, stream);
+            break;
+        default:
+            rc = launch_mfma_pass<ENC, 8>(p, w, row_bytes, xs, in, out, ys, stride, status, stream);
+            break;
+        }
+        if (rc)
+            return rc;
+        first += r;
+    }
+    return KDQ_OK;
+}
+
 bool aligned(const void* p, size_t a) {
     return (reinterpret_cast<uintptr_t>(p) % a) == 0;
 }
@@ -708,6 +1102,19 @@ extern "C" int kdq_gemv(int encoding, const void* weights, size_t row_bytes, con
     const bool fast = in % 256 == 0 && row_bytes % 4 == 0 && aligned(weights, 4) &&
                       (encoding != KDQ_Q4_K || (row_bytes % 16 == 0 && aligned(weights, 16)));
     if (fast) {
+        switch (encoding) {
+        case KDQ_Q8_0:
+            rc = launch_mfma<KDQ_Q8_0>(weights, row_bytes, x, rows, in, out, y, stride, status, s);
+            break;
+        case KDQ_Q4_0:
+            rc = launch_mfma<KDQ_Q4_0>(weights, row_bytes, x, rows, in, out, y, stride, status, s);
+            break;
+        default:
+            rc = launch_mfma<KDQ_Q4_K>(weights, row_bytes, x, rows, in, out, y, stride, status, s);
+            break;
+        }
+        if (rc != KDQ_ERR_UNSUPPORTED)
+            return rc;
         switch (encoding) {
         case KDQ_Q8_0:
             rc = launch_fast<KDQ_Q8_0>(weights, row_bytes, x, rows, in, out, y, stride, status, s);
