@@ -525,7 +525,6 @@ __global__ __launch_bounds__(kThreads) void fast_gemv(const uint8_t* __restrict_
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kMThreads = 1024;   // 16 wavefronts
 constexpr int kAGroup = 1024;     // LDS bytes of A operands per 256-value group
 constexpr int kPartialPitch = 17; // floats per lane in the pass partials (bank spread)
 
@@ -689,25 +688,25 @@ __device__ __forceinline__ float row16_total(float v) {
     return v;
 }
 
-// A wavefront's position in its unit sequence: group g = wave + 16q, tile t.
+// A wavefront's position in its unit sequence: group g = wave + W q, tile t.
 struct UnitCursor {
     unsigned g, t;
-    __device__ __forceinline__ void next(unsigned tiles) {
+    __device__ __forceinline__ void next(unsigned tiles, unsigned waves) {
         if (++t == tiles) {
             t = 0;
-            g += 16;
+            g += waves;
         }
     }
 };
 
-// Workgroup: 16 wavefronts, one workgroup per compute unit, rows [r0, r1), processed in
-// passes of up to kTiles tiles.  In a pass, wavefront w takes the units (g, t) for
-// g = w, w + 16, ... and every tile t, kUnits at a time.  Loads are issued by every lane
+// Workgroup: W wavefronts (W <= 16), rows [r0, r1), processed in passes of up to kTiles
+// tiles.  In a pass, wavefront w takes the units (g, t) for g = w, w + W, ... and every
+// tile t, kUnits at a time.  Loads are issued by every lane
 // unconditionally (rows past r1 and units past the wavefront's last are clamped to valid
 // data and their results discarded), so waits count exactly.  Order: this thread's first
 // activation unit, the first units' packed weights, then the staging.
-template <int ENC, int R>
-__global__ __launch_bounds__(kMThreads) void mfma_gemv(const uint8_t* __restrict__ weights,
+template <int ENC, int R, int W>
+__global__ __launch_bounds__(W * 64) void mfma_gemv(const uint8_t* __restrict__ weights,
                                                        size_t row_bytes, const float* x,
                                                        unsigned in, unsigned out,
                                                        float* __restrict__ y, size_t stride,
@@ -715,6 +714,7 @@ __global__ __launch_bounds__(kMThreads) void mfma_gemv(const uint8_t* __restrict
     constexpr int kTiles = mfma_tiles<R>;
     constexpr int kUnits = mfma_units<ENC, R>;
     constexpr int kRowUnroll = R <= 2 ? R : 1;  // larger batches: one row's operands at a time
+    constexpr unsigned kThreads = W * 64;
     extern __shared__ __align__(16) uint8_t lds[];
     const MfmaLds layout = mfma_layout(R, in);
     const unsigned groups = in / 256;
@@ -732,7 +732,7 @@ __global__ __launch_bounds__(kMThreads) void mfma_gemv(const uint8_t* __restrict
     const unsigned r0 = blockIdx.x * rows_per_wg, r1 = min(out, r0 + rows_per_wg);
     bool bad = false;
 
-    for (unsigned t = threadIdx.x; t < 256; t += kMThreads)
+    for (unsigned t = threadIdx.x; t < 256; t += kThreads)
         reinterpret_cast<uint32_t*>(lds)[t] = 0u;
 
     auto pass_tiles = [&](unsigned p0) { return min(unsigned(kTiles), (r1 - p0 + 15) / 16); };
@@ -744,7 +744,7 @@ __global__ __launch_bounds__(kMThreads) void mfma_gemv(const uint8_t* __restrict
             const unsigned g = valid ? cur.g : wave % groups, t = valid ? cur.t : 0;
             const unsigned n = min(p0 + 16 * t + j, r1 - 1);
             load_lane<ENC>(weights + size_t(n) * row_bytes, 4 * g + G, L[k]);
-            cur.next(tiles);
+            cur.next(tiles, W);
         }
     };
 
@@ -759,7 +759,7 @@ __global__ __launch_bounds__(kMThreads) void mfma_gemv(const uint8_t* __restrict
     __builtin_amdgcn_sched_barrier(0);
     if (threadIdx.x < units_x)
         mstage_unit(in, threadIdx.x, first_unit, atab, blocks);
-    for (unsigned u = threadIdx.x + kMThreads; u < units_x; u += kMThreads) {
+    for (unsigned u = threadIdx.x + kThreads; u < units_x; u += kThreads) {
         XUnit more;
         load_unit(x, in, u, more);
         mstage_unit(in, u, more, atab, blocks);
@@ -798,20 +798,21 @@ __global__ __launch_bounds__(kMThreads) void mfma_gemv(const uint8_t* __restrict
                     mine[size_t(r * kTiles + cur.t) * 64 * kPartialPitch] +=
                         chunk_value<ENC>(L[k], sel, c, xb[0], xb[1], bad);
                 }
-                cur.next(tiles);
+                cur.next(tiles, W);
             }
         }
         first = false;  // a wavefront without units in the first pass never used its loads
         __syncthreads();
-        // output o = (r*tiles + t)*16 + jj: 16 threads (one DPP row), thread k sums
+        // output o = (r*tiles + t)*16 + jj: 16 threads (one DPP row), thread k < W sums
         // wavefront k's four lane groups, then the row of 16 is summed
         const unsigned outputs = R * tiles * 16;
-        for (unsigned o = threadIdx.x / 16; o < outputs; o += kMThreads / 16) {
+        for (unsigned o = threadIdx.x / 16; o < outputs; o += kThreads / 16) {
             const unsigned k = threadIdx.x % 16;
             const unsigned jj = o % 16, t = (o / 16) % tiles, r = o / (16 * tiles);
             const float* src = partial + (size_t(r * kTiles + t) * 64 + jj) * kPartialPitch + k;
-            float v = ((src[0] + src[16 * kPartialPitch]) + src[32 * kPartialPitch]) +
-                      src[48 * kPartialPitch];
+            float v = k < W ? ((src[0] + src[16 * kPartialPitch]) + src[32 * kPartialPitch]) +
+                                  src[48 * kPartialPitch]
+                            : 0.f;
             v = row16_total(v);
             const unsigned n = p0 + 16 * t + jj;
             if (k == 0 && n < r1)
@@ -945,10 +946,11 @@ size_t mfma_lds(size_t batch, size_t in) {
 }
 
 struct MfmaPlan {
-    unsigned rows_per_wg, grid, batch;
+    unsigned rows_per_wg, grid, batch, waves;
 };
 
-// One workgroup per compute unit; batch rows per pass as the LDS allows (at most 8).
+// Batch rows per pass as the LDS allows (at most 8); `waves` wavefronts per workgroup and
+// ceil(out / (compute units * per_cu)) rows per workgroup.
 bool plan_mfma(size_t rows, size_t in, size_t out, MfmaPlan& p) {
     constexpr size_t limit = 160 * 1024;
     if (in % 256 || mfma_lds(1, in) > limit)
@@ -959,26 +961,42 @@ bool plan_mfma(size_t rows, size_t in, size_t out, MfmaPlan& p) {
     const size_t cus = compute_units();
     const size_t rows_per_wg = std::max<size_t>(1, (out + cus - 1) / cus);
     p.batch = batch;
+    p.waves = 16;
     p.rows_per_wg = unsigned(rows_per_wg);
     p.grid = unsigned((out + rows_per_wg - 1) / rows_per_wg);
     return true;
+}
+
+template <int ENC, int R, int W>
+int launch_mfma_shape(const MfmaPlan& p, const void* w, size_t row_bytes, const float* x,
+                      size_t in, size_t out, float* y, size_t stride, unsigned* status,
+                      hipStream_t stream) {
+    static bool configured = false;  // one attribute call per instantiation
+    if (!configured) {
+        KDQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&mfma_gemv<ENC, R, W>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+        configured = true;
+    }
+    hipLaunchKernelGGL((mfma_gemv<ENC, R, W>), dim3(p.grid), dim3(W * 64), mfma_lds(R, in),
+                       stream, static_cast<const uint8_t*>(w), row_bytes, x, unsigned(in),
+                       unsigned(out), y, stride, status, p.rows_per_wg);
+    KDQ_HIP(hipGetLastError());
+    return KDQ_OK;
 }
 
 template <int ENC, int R>
 int launch_mfma_pass(const MfmaPlan& p, const void* w, size_t row_bytes, const float* x,
                      size_t in, size_t out, float* y, size_t stride, unsigned* status,
                      hipStream_t stream) {
-    static bool configured = false;  // one attribute call per instantiation
-    if (!configured) {
-        KDQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&mfma_gemv<ENC, R>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-        configured = true;
+    switch (p.waves) {
+    case 4:
+        return launch_mfma_shape<ENC, R, 4>(p, w, row_bytes, x, in, out, y, stride, status, stream);
+    case 8:
+        return launch_mfma_shape<ENC, R, 8>(p, w, row_bytes, x, in, out, y, stride, status, stream);
+    default:
+        return launch_mfma_shape<ENC, R, 16>(p, w, row_bytes, x, in, out, y, stride, status,
+                                             stream);
     }
-    hipLaunchKernelGGL((mfma_gemv<ENC, R>), dim3(p.grid), dim3(kMThreads), mfma_lds(R, in),
-                       stream, static_cast<const uint8_t*>(w), row_bytes, x, unsigned(in),
-                       unsigned(out), y, stride, status, p.rows_per_wg);
-    KDQ_HIP(hipGetLastError());
-    return KDQ_OK;
 }
 
 template <int ENC>
