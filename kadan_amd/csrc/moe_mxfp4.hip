@@ -27,7 +27,9 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kMaxTopK = 8, kMaxExperts = 256;
-constexpr int kTileRows = 32, kTiles = 4, kItemRows = kTileRows * kTiles;
+constexpr int kTileRows = 32, kTiles = 2, kItemRows = kTileRows * kTiles;
+constexpr int kGemmWaves = 4;  // wavefronts per grouped-GEMM workgroup, 32 features each
+constexpr int kStepK = 64;     // K values per step: 16 FP4 bytes per lane
 
 // ------------------------------------------------------------------ routing
 
@@ -118,7 +120,8 @@ __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* __restrict
                                                        int32_t* __restrict__ offsets,
                                                        int32_t* __restrict__ perm,
                                                        int32_t* __restrict__ items,
-                                                       int32_t* __restrict__ item_count) {
+                                                       int32_t* __restrict__ item_count,
+                                                       int32_t* __restrict__ position) {
     __shared__ int counts[kMaxExperts], base[kMaxExperts];
     __shared__ int wave_counts[16][kMaxExperts];
     const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
@@ -168,6 +171,8 @@ __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* __restrict
             for (unsigned w = 0; w < wave; ++w)
                 r += wave_counts[w][e];
             perm[r] = int(s);
+            if (position)
+                position[s] = r;  // inverse permutation
         }
         __syncthreads();
         for (unsigned x = tid; x < experts; x += 1024) {
@@ -184,26 +189,6 @@ __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* __restrict
 
 __device__ __forceinline__ float e8m0(unsigned s) {
     return __uint_as_float(s << 23);  // exponent field only: the converter reads 2^(s-127)
-}
-
-// 32 FP4 values (16 bytes, low nibble first) times 2^(scale-127) -> 32 exact bf16,
-// as four 8-value MFMA operands.
-__device__ __forceinline__ void dequant32(const u32x4 codes, unsigned scale, bf16x8 out[4]) {
-    const float s = e8m0(scale);
-    const unsigned w[4] = {codes.x, codes.y, codes.z, codes.w};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[q], s, 0);
-        const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[q], s, 1);
-        const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[q], s, 2);
-        const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[q], s, 3);
-        out[q] = bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
-    }
-}
-
-__device__ __forceinline__ bf16x8 load_bf16x8(const uint16_t* p) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(p);
-    return __builtin_bit_cast(bf16x8, v);
 }
 
 __device__ __forceinline__ float silu(float x) {
@@ -232,132 +217,262 @@ __device__ __forceinline__ Item load_item(const int32_t* items, const int32_t* o
     return it;
 }
 
-// Workgroup: `waves` wavefronts, wavefront w owns output features
-// (blockIdx.x * waves + w) * 32 .. +31 of both gate and up; blockIdx.y is the item.
-// The k axis runs in chunks of 64: lane group g (lane / 32) holds the 32 values
-// 64c + 32g .. +31 of its row (one MXFP4 scale block), fed to four MFMAs of 16.
-__global__ __launch_bounds__(256) void gate_up_kernel(
-    const uint16_t* __restrict__ x, unsigned hidden, unsigned inter, unsigned top_k,
-    const uint8_t* __restrict__ gate_blocks, const uint8_t* __restrict__ gate_scales,
-    const uint8_t* __restrict__ up_blocks, const uint8_t* __restrict__ up_scales,
-    const int32_t* __restrict__ offsets, const int32_t* __restrict__ perm,
-    const int32_t* __restrict__ items, const int32_t* __restrict__ item_count,
-    uint16_t* __restrict__ h_hi, uint16_t* __restrict__ h_lo) {
-    if (int(blockIdx.y) >= *item_count)
-        return;
-    const Item it = load_item(items, offsets, blockIdx.y);
-    const unsigned waves = blockDim.x / 64, wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-    const unsigned i32 = lane % 32, g = lane / 32;
-    const unsigned f = (blockIdx.x * waves + wave) * 32 + i32;
-    const int tiles = (it.count + kTileRows - 1) / kTileRows;
+// Grouped GEMMs on v_mfma_f32_32x32x16_bf16.  A workgroup of kGemmWaves wavefronts works
+// on one work item (expert e, up to kItemRows consecutive rows of its segment) and one K
+// slice.  The weight operand B streams from HBM: lane (f = lane % 32, g = lane / 32) of a
+// wavefront owning 32 weight rows loads per 64-value step the 16 bytes (32 FP4 values)
+// k = 64q + 32g .. +31 of its row and their E8M0 scale, and MFMA t takes values
+// 32g + 8t .. +7 of them (the activation operand uses the same k order), dequantized
+// with v_cvt_scalef32_pk_bf16_fp4, which is exact.  The activation operand A (the item's
+// rows) is staged per chunk of steps into LDS by the whole workgroup, double-buffered.
+// Per chunk, every lane issues the next chunk's activation loads first and the next
+// chunk's weight loads second, all unconditionally (indices past the end are clamped to
+// valid data), so the wait before the activations are stored to LDS does not include
+// the weight loads, which stay in flight across the barrier.
 
-    const uint16_t* xrow[kTiles];
+// Staged rows: PLANES planes of CHUNK steps of 64 bf16 values per row, 16 bytes of pad.
+template <int CHUNK, int PLANES> struct Stage {
+    static constexpr int pitch = CHUNK * PLANES * kStepK * 2 + 16;
+    static constexpr int buffer = kItemRows * pitch;
+    static constexpr int pieces = CHUNK * PLANES * 8;  // 16-byte pieces per row
+    static constexpr int per_thread = kItemRows * pieces / (kGemmWaves * 64);
+};
+
+// This thread's pieces of the staged chunk: piece i is row (tid / pieces + i * rows_step)
+// at offset (tid % pieces) of the row; the same rows for every chunk.
+template <int CHUNK, int PLANES> struct StageThread {
+    using S = Stage<CHUNK, PLANES>;
+    static constexpr int rows_step = kGemmWaves * 64 / S::pieces;
+    const uint16_t* src[S::per_thread];  // row start in its plane (a valid row)
+    bool valid[S::per_thread];
+    unsigned step, plane, sub;
+};
+
+// `row_offset(p, r)` is the element offset of row r in plane p, or -1 past the item.
+template <int CHUNK, int PLANES, class RowOffset>
+__device__ __forceinline__ StageThread<CHUNK, PLANES> stage_thread(
+    const uint16_t* const (&planes)[PLANES], RowOffset row_offset) {
+    using T = StageThread<CHUNK, PLANES>;
+    using S = Stage<CHUNK, PLANES>;
+    T t;
+    const unsigned within = threadIdx.x % S::pieces;
+    t.step = within / (8 * PLANES);
+    t.plane = (within / 8) % PLANES;
+    t.sub = within % 8;
 #pragma unroll
-    for (int m = 0; m < kTiles; ++m) {
-        const int r = m * kTileRows + int(i32);
-        xrow[m] = r < it.count ? x + size_t(perm[it.segment + it.first + r] / int(top_k)) * hidden
-                               : nullptr;
+    for (int i = 0; i < S::per_thread; ++i) {
+        const unsigned row = threadIdx.x / S::pieces + i * T::rows_step;
+        const long long at = row_offset(t.plane, row);
+        t.valid[i] = at >= 0;
+        t.src[i] = planes[t.plane] + (at >= 0 ? at : row_offset(t.plane, 0));
     }
-    const size_t wrow = (size_t(it.expert) * inter + f);
-    const uint8_t* gb = gate_blocks + wrow * (hidden / 2);
-    const uint8_t* ub = up_blocks + wrow * (hidden / 2);
-    const uint8_t* gs = gate_scales + wrow * (hidden / 32);
-    const uint8_t* us = up_scales + wrow * (hidden / 32);
+    return t;
+}
 
-    f32x16 acc_g[kTiles], acc_u[kTiles];
+template <int CHUNK, int PLANES> struct StagePieces {
+    u32x4 v[Stage<CHUNK, PLANES>::per_thread];
+};
+
+// Loads the pieces of the chunk starting at step q (steps past `last` re-read `last`).
+template <int CHUNK, int PLANES>
+__device__ __forceinline__ void stage_load(const StageThread<CHUNK, PLANES>& t, unsigned q,
+                                           unsigned last, StagePieces<CHUNK, PLANES>& P) {
+    const unsigned step = min(q + t.step, last);
 #pragma unroll
-    for (int m = 0; m < kTiles; ++m)
-        acc_g[m] = acc_u[m] = f32x16{};
+    for (int i = 0; i < Stage<CHUNK, PLANES>::per_thread; ++i)
+        P.v[i] = *reinterpret_cast<const u32x4*>(t.src[i] + size_t(step) * kStepK + t.sub * 8);
+}
 
-    for (unsigned c = 0; c < hidden / 64; ++c) {
-        const unsigned kb = 64 * c + 32 * g;
-        bf16x8 bg[4], bu[4];
-        dequant32(load16(gb + kb / 2), gs[kb / 32], bg);
-        dequant32(load16(ub + kb / 2), us[kb / 32], bu);
+template <int CHUNK, int PLANES>
+__device__ __forceinline__ void stage_store(const StageThread<CHUNK, PLANES>& t,
+                                            const StagePieces<CHUNK, PLANES>& P, unsigned steps,
+                                            uint8_t* buf) {
+    using S = Stage<CHUNK, PLANES>;
+    if (t.step >= steps)
+        return;
+#pragma unroll
+    for (int i = 0; i < S::per_thread; ++i) {
+        const unsigned row = threadIdx.x / S::pieces + i * StageThread<CHUNK, PLANES>::rows_step;
+        *reinterpret_cast<u32x4*>(buf + row * S::pitch + (t.step * PLANES + t.plane) * 128 +
+                                  t.sub * 16) = t.valid[i] ? P.v[i] : u32x4{0, 0, 0, 0};
+    }
+}
+
+// 8 exact bf16 values from dword t of a lane's 16 FP4 bytes.
+__device__ __forceinline__ bf16x8 dequant8(unsigned word, float scale) {
+    const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 0);
+    const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 1);
+    const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 2);
+    const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 3);
+    return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+__device__ __forceinline__ bf16x8 lds_bf16x8(const uint8_t* p) {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(p));
+}
+
+// Packed weights of one lane for one step (16 FP4 bytes and their scale).
+struct WStep {
+    u32x4 codes;
+    unsigned scale;
+};
+
+__device__ __forceinline__ WStep load_wstep(const uint8_t* row, const uint8_t* srow, unsigned q,
+                                            unsigned g) {
+    WStep w;
+    w.codes = load16(row + size_t(q) * 32 + 16 * g);
+    w.scale = srow[size_t(q) * 2 + g];
+    return w;
+}
+
+// Steps of K slice `slice` of `steps` total: [begin, end).
+__device__ __forceinline__ void slice_steps(unsigned steps, unsigned slices, unsigned slice,
+                                            unsigned& begin, unsigned& end) {
+    const unsigned per = (steps + slices - 1) / slices;
+    begin = min(steps, slice * per);
+    end = min(steps, begin + per);
+}
+
+// One step of MFMAs for one weight matrix: acc[m] += A(tile m, step s) * B(step).
+template <int PLANES>
+__device__ __forceinline__ void step_mfma(const WStep& w, const uint8_t* buf, int pitch, int s,
+                                          int tiles, unsigned i32, unsigned g,
+                                          f32x16 (&acc)[kTiles]) {
+    const float scale = e8m0(w.scale);
+    const unsigned c[4] = {w.codes.x, w.codes.y, w.codes.z, w.codes.w};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const bf16x8 b = dequant8(c[t], scale);
 #pragma unroll
         for (int m = 0; m < kTiles; ++m) {
             if (m >= tiles)
                 break;
-            bf16x8 a[4];
+            const uint8_t* rowp = buf + (m * kTileRows + i32) * pitch + s * PLANES * 128 +
+                                  (32 * g + 8 * t) * 2;
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                a[j] = xrow[m] ? load_bf16x8(xrow[m] + kb + 8 * j) : bf16x8{};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc_g[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[j], bg[j], acc_g[m], 0, 0, 0);
-                acc_u[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[j], bu[j], acc_u[m], 0, 0, 0);
-            }
-        }
-    }
-#pragma unroll
-    for (int m = 0; m < kTiles; ++m) {
-        if (m >= tiles)
-            break;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int r = m * kTileRows + 8 * (v / 4) + 4 * int(g) + (v % 4);
-            if (r < it.count) {
-                const float h = silu(acc_g[m][v]) * acc_u[m][v];
-                const uint16_t hi = bf16_rne(h);
-                const uint16_t lo = bf16_rne(h - bf16_value(hi));
-                const size_t at = size_t(it.segment + it.first + r) * inter + f;
-                h_hi[at] = hi;
-                h_lo[at] = lo;
-            }
+            for (int p = 0; p < PLANES; ++p)
+                acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lds_bf16x8(rowp + p * 128), b,
+                                                                 acc[m], 0, 0, 0);
         }
     }
 }
 
-// contribution[slot, d] = w[slot] * sum_k (h_hi + h_lo)[p, k] * down[e, d, k]
-__global__ __launch_bounds__(256) void down_kernel(
-    const uint16_t* __restrict__ h_hi, const uint16_t* __restrict__ h_lo, unsigned hidden,
-    unsigned inter, const uint8_t* __restrict__ down_blocks,
-    const uint8_t* __restrict__ down_scales, const int32_t* __restrict__ offsets,
-    const int32_t* __restrict__ perm, const float* __restrict__ weight,
+// gate/up: grid (feature groups of 64, items, K slices).  Wavefront w multiplies the gate
+// (w even) or up (w odd) rows of features n0 + 32 (w / 2) .. +31.  One slice: h =
+// silu(g) * u as bf16 hi + lo (g passes through LDS); more: fp32 partials of g and u
+// (summed by finalize_kernel).
+__global__ __launch_bounds__(kGemmWaves * 64) void gate_up_kernel(
+    const uint16_t* x, unsigned hidden, unsigned inter, unsigned top_k,
+    const uint8_t* __restrict__ gate_blocks, const uint8_t* __restrict__ gate_scales,
+    const uint8_t* __restrict__ up_blocks, const uint8_t* __restrict__ up_scales,
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ perm,
     const int32_t* __restrict__ items, const int32_t* __restrict__ item_count,
-    float* __restrict__ contribution) {
+    uint16_t* __restrict__ h_hi, uint16_t* __restrict__ h_lo, float* __restrict__ part_g,
+    float* __restrict__ part_u, size_t part_stride) {
+    constexpr int CHUNK = 2;
+    using S = Stage<CHUNK, 1>;
+    __shared__ __align__(16) uint8_t stage[2][S::buffer];
+    __shared__ long long src[kItemRows];
     if (int(blockIdx.y) >= *item_count)
         return;
     const Item it = load_item(items, offsets, blockIdx.y);
-    const unsigned waves = blockDim.x / 64, wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const unsigned wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const unsigned i32 = lane % 32, g = lane / 32;
-    const unsigned d = (blockIdx.x * waves + wave) * 32 + i32;
+    const unsigned mat = wave % 2, tile = wave / 2;
+    const unsigned f0 = blockIdx.x * 64 + tile * 32;
+    const bool active = f0 < inter;  // uniform per wavefront
+    const unsigned f = active ? f0 + i32 : i32;
     const int tiles = (it.count + kTileRows - 1) / kTileRows;
+    unsigned q0, q1;
+    slice_steps(hidden / kStepK, gridDim.z, blockIdx.z, q0, q1);
+    if (q0 >= q1)
+        return;
 
-    const size_t wrow = size_t(it.expert) * hidden + d;
-    const uint8_t* db = down_blocks + wrow * (inter / 2);
-    const uint8_t* ds = down_scales + wrow * (inter / 32);
-
-    size_t hrow[kTiles];
-    bool valid[kTiles];
-#pragma unroll
-    for (int m = 0; m < kTiles; ++m) {
-        const int r = m * kTileRows + int(i32);
-        valid[m] = r < it.count;
-        hrow[m] = size_t(it.segment + it.first + (valid[m] ? r : 0)) * inter;
+    if (threadIdx.x < kItemRows) {
+        const int r = int(threadIdx.x);
+        src[r] = r < it.count ? (long long)(perm[it.segment + it.first + r] / int(top_k)) * hidden
+                              : -1;
     }
+    __syncthreads();
+    const uint16_t* planes[1] = {x};
+    const auto st = stage_thread<CHUNK, 1>(planes, [&](unsigned, unsigned r) { return src[r]; });
+    const size_t wrow = size_t(it.expert) * inter + f;
+    const uint8_t* wb = (mat ? up_blocks : gate_blocks) + wrow * (hidden / 2);
+    const uint8_t* ws = (mat ? up_scales : gate_scales) + wrow * (hidden / 32);
+
     f32x16 acc[kTiles];
 #pragma unroll
     for (int m = 0; m < kTiles; ++m)
         acc[m] = f32x16{};
 
-    for (unsigned c = 0; c < inter / 64; ++c) {
-        const unsigned kb = 64 * c + 32 * g;
-        bf16x8 b[4];
-        dequant32(load16(db + kb / 2), ds[kb / 32], b);
+    StagePieces<CHUNK, 1> P;
+    stage_load(st, q0, q1 - 1, P);
+    asm volatile("" ::: "memory");  // activations before weights (x is not restrict)
+    __builtin_amdgcn_sched_barrier(0);
+    WStep w[CHUNK];
+#pragma unroll
+    for (int s = 0; s < CHUNK; ++s)
+        w[s] = load_wstep(wb, ws, min(q0 + s, q1 - 1), g);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    stage_store(st, P, min(unsigned(CHUNK), q1 - q0), stage[0]);
+    __syncthreads();
+
+    unsigned buf = 0;
+    for (unsigned q = q0; q < q1; q += CHUNK, buf ^= 1) {
+        const unsigned steps = min(unsigned(CHUNK), q1 - q), qn = q + CHUNK;
+        stage_load(st, qn, q1 - 1, P);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        WStep wn[CHUNK];
+#pragma unroll
+        for (int s = 0; s < CHUNK; ++s)
+            wn[s] = load_wstep(wb, ws, min(qn + s, q1 - 1), g);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        if (active) {
+#pragma unroll
+            for (int s = 0; s < CHUNK; ++s)
+                if (unsigned(s) < steps)
+                    step_mfma<1>(w[s], stage[buf], S::pitch, s, tiles, i32, g, acc);
+        }
+        if (qn < q1)
+            stage_store(st, P, min(unsigned(CHUNK), q1 - qn), stage[buf ^ 1]);
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < CHUNK; ++s)
+            w[s] = wn[s];
+    }
+
+    if (gridDim.z > 1) {
+        if (!active)
+            return;
+        float* part = (mat ? part_u : part_g) + blockIdx.z * part_stride;
 #pragma unroll
         for (int m = 0; m < kTiles; ++m) {
             if (m >= tiles)
                 break;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const bf16x8 ah = valid[m] ? load_bf16x8(h_hi + hrow[m] + kb + 8 * j) : bf16x8{};
-                const bf16x8 al = valid[m] ? load_bf16x8(h_lo + hrow[m] + kb + 8 * j) : bf16x8{};
-                acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, b[j], acc[m], 0, 0, 0);
-                acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, b[j], acc[m], 0, 0, 0);
+            for (int v = 0; v < 16; ++v) {
+                const int r = m * kTileRows + 8 * (v / 4) + 4 * int(g) + (v % 4);
+                if (r < it.count)
+                    part[size_t(it.segment + it.first + r) * inter + f] = acc[m][v];
             }
         }
+        return;
     }
+    // gate values of feature tile `tile` pass to the up wavefront through LDS (the stage
+    // buffers are free after the last barrier): xg[tile][m][v][lane]
+    float* xg = reinterpret_cast<float*>(&stage[0][0]);
+    if (mat == 0 && active)
+#pragma unroll
+        for (int m = 0; m < kTiles; ++m)
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                xg[((tile * kTiles + m) * 16 + v) * 64 + lane] = acc[m][v];
+    __syncthreads();
+    if (mat == 0 || !active)
+        return;
 #pragma unroll
     for (int m = 0; m < kTiles; ++m) {
         if (m >= tiles)
@@ -366,14 +481,123 @@ __global__ __launch_bounds__(256) void down_kernel(
         for (int v = 0; v < 16; ++v) {
             const int r = m * kTileRows + 8 * (v / 4) + 4 * int(g) + (v % 4);
             if (r < it.count) {
-                const int slot = perm[it.segment + it.first + r];
-                contribution[size_t(slot) * hidden + d] = acc[m][v] * weight[slot];
+                const float gv = xg[((tile * kTiles + m) * 16 + v) * 64 + lane];
+                const float h = silu(gv) * acc[m][v];
+                const uint16_t hi = bf16_rne(h);
+                const size_t at = size_t(it.segment + it.first + r) * inter + f;
+                h_hi[at] = hi;
+                h_lo[at] = bf16_rne(h - bf16_value(hi));
             }
         }
     }
 }
 
-__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ contribution,
+// h = silu(sum_s g_s) * (sum_s u_s), slices summed in order, as bf16 hi + lo.
+__global__ __launch_bounds__(256) void finalize_kernel(const float* __restrict__ part_g,
+                                                       const float* __restrict__ part_u,
+                                                       size_t count, unsigned slices,
+                                                       uint16_t* __restrict__ h_hi,
+                                                       uint16_t* __restrict__ h_lo) {
+    const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= count)
+        return;
+    float gs = 0.f, us = 0.f;
+    for (unsigned s = 0; s < slices; ++s) {
+        gs += part_g[s * count + i];
+        us += part_u[s * count + i];
+    }
+    const float h = silu(gs) * us;
+    const uint16_t hi = bf16_rne(h);
+    h_hi[i] = hi;
+    h_lo[i] = bf16_rne(h - bf16_value(hi));
+}
+
+// down: grid (feature groups of 128, items, K slices); fp32 partial sums of h x down
+// (hi and lo planes) per slice, indexed by the slot's position in the permutation.
+__global__ __launch_bounds__(kGemmWaves * 64) void down_kernel(
+    const uint16_t* h_hi, const uint16_t* h_lo, unsigned hidden, unsigned inter,
+    const uint8_t* __restrict__ down_blocks, const uint8_t* __restrict__ down_scales,
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ items,
+    const int32_t* __restrict__ item_count, float* __restrict__ part_d, size_t part_stride) {
+    constexpr int CHUNK = 1;
+    using S = Stage<CHUNK, 2>;
+    __shared__ __align__(16) uint8_t stage[2][S::buffer];
+    if (int(blockIdx.y) >= *item_count)
+        return;
+    const Item it = load_item(items, offsets, blockIdx.y);
+    const unsigned wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const unsigned i32 = lane % 32, g = lane / 32;
+    const unsigned d0 = (blockIdx.x * kGemmWaves + wave) * 32;
+    const bool active = d0 < hidden;
+    const unsigned d = active ? d0 + i32 : i32;
+    const int tiles = (it.count + kTileRows - 1) / kTileRows;
+    unsigned q0, q1;
+    slice_steps(inter / kStepK, gridDim.z, blockIdx.z, q0, q1);
+    if (q0 >= q1)
+        return;
+
+    const uint16_t* planes[2] = {h_hi, h_lo};
+    const auto st = stage_thread<CHUNK, 2>(planes, [&](unsigned, unsigned r) {
+        return r < unsigned(it.count) ? (long long)(it.segment + it.first + r) * inter : -1ll;
+    });
+    const size_t wrow = size_t(it.expert) * hidden + d;
+    const uint8_t* db = down_blocks + wrow * (inter / 2);
+    const uint8_t* ds = down_scales + wrow * (inter / 32);
+
+    f32x16 acc[kTiles];
+#pragma unroll
+    for (int m = 0; m < kTiles; ++m)
+        acc[m] = f32x16{};
+
+    // weights: the step being multiplied and two ahead
+    StagePieces<CHUNK, 2> P;
+    stage_load(st, q0, q1 - 1, P);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    WStep w0 = load_wstep(db, ds, q0, g);
+    WStep w1 = load_wstep(db, ds, min(q0 + 1, q1 - 1), g);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    stage_store(st, P, 1, stage[0]);
+    __syncthreads();
+
+    unsigned buf = 0;
+    for (unsigned q = q0; q < q1; ++q, buf ^= 1) {
+        stage_load(st, q + 1, q1 - 1, P);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        const WStep w2 = load_wstep(db, ds, min(q + 2, q1 - 1), g);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        if (active)
+            step_mfma<2>(w0, stage[buf], S::pitch, 0, tiles, i32, g, acc);
+        if (q + 1 < q1)
+            stage_store(st, P, 1, stage[buf ^ 1]);
+        __syncthreads();
+        w0 = w1;
+        w1 = w2;
+    }
+    if (!active)
+        return;
+#pragma unroll
+    for (int m = 0; m < kTiles; ++m) {
+        if (m >= tiles)
+            break;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int r = m * kTileRows + 8 * (v / 4) + 4 * int(g) + (v % 4);
+            if (r < it.count)
+                part_d[blockIdx.z * part_stride + size_t(it.segment + it.first + r) * hidden + d] =
+                    acc[m][v];
+        }
+    }
+}
+
+// y[t, d] = sum_i w[t k + i] * (sum_s part_d[s, position(t k + i), d]), in selection order.
+__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ part_d,
+                                                      size_t part_stride, unsigned slices,
+                                                      const int32_t* __restrict__ position,
+                                                      const float* __restrict__ weight,
                                                       unsigned tokens, unsigned hidden,
                                                       unsigned top_k, float* __restrict__ y) {
     const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -381,8 +605,14 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
         return;
     const size_t t = i / hidden, d = i % hidden;
     float sum = 0.f;
-    for (unsigned k = 0; k < top_k; ++k)
-        sum += contribution[(t * top_k + k) * hidden + d];
+    for (unsigned k = 0; k < top_k; ++k) {
+        const size_t slot = t * top_k + k;
+        const size_t at = size_t(position[slot]) * hidden + d;
+        float down = 0.f;
+        for (unsigned s = 0; s < slices; ++s)
+            down += part_d[s * part_stride + at];
+        sum += down * weight[slot];
+    }
     y[i] = sum;
 }
 
@@ -419,25 +649,47 @@ __global__ __launch_bounds__(256) void mxfp4_dequant_kernel(const uint8_t* __res
 
 // Workspace carve-up (device bytes, 256-aligned pieces).
 struct MoeScratch {
-    int32_t *idx, *offsets, *perm, *items, *item_count;
+    int32_t *idx, *offsets, *perm, *position, *items, *item_count;
     float* weight;
     uint16_t *h_hi, *h_lo;
-    float* contribution;
+    float *part_g, *part_u, *part_d;
 };
+
+// K slices of the grouped GEMMs: enough workgroups for about two per compute unit when
+// the items are few (decode), one slice otherwise; no slice is empty.
+struct MoeSlices {
+    unsigned gate_up, down;
+};
+
+MoeSlices moe_slices(size_t tokens, size_t hidden, size_t inter, size_t experts,
+                     size_t top_k) {
+    const size_t items = std::min(tokens * top_k, experts);  // at least this many
+    const size_t target = 2 * size_t(compute_units());
+    auto slices = [&](size_t groups, size_t steps) {
+        size_t ks = std::max<size_t>(1, (target + groups * items - 1) / (groups * items));
+        ks = std::min(ks, steps);
+        const size_t per = (steps + ks - 1) / ks;
+        return unsigned((steps + per - 1) / per);
+    };
+    return MoeSlices{slices((inter + 63) / 64, hidden / kStepK),
+                     slices((hidden / 32 + kGemmWaves - 1) / kGemmWaves, inter / kStepK)};
+}
 
 size_t align256(size_t n) {
     return (n + 255) & ~size_t(255);
 }
 
 size_t moe_scratch_bytes(size_t tokens, size_t hidden, size_t inter, size_t experts,
-                         size_t top_k) {
+                         size_t top_k, MoeSlices ks) {
     const size_t slots = tokens * top_k, items = slots / kItemRows + experts + 1;
-    return align256(slots * 4) * 3 + align256((experts + 1) * 4) + align256(items * 8) +
-           align256(4) + 2 * align256(slots * inter * 2) + align256(slots * hidden * 4);
+    const size_t partial_gu = ks.gate_up > 1 ? 2 * align256(ks.gate_up * slots * inter * 4) : 0;
+    return align256(slots * 4) * 4 + align256((experts + 1) * 4) + align256(items * 8) +
+           align256(4) + 2 * align256(slots * inter * 2) + partial_gu +
+           align256(ks.down * slots * hidden * 4);
 }
 
 MoeScratch carve(uint8_t* p, size_t tokens, size_t hidden, size_t inter, size_t experts,
-                 size_t top_k) {
+                 size_t top_k, MoeSlices ks) {
     const size_t slots = tokens * top_k, items = slots / kItemRows + experts + 1;
     MoeScratch s;
     auto take = [&](size_t n) {
@@ -448,12 +700,18 @@ MoeScratch carve(uint8_t* p, size_t tokens, size_t hidden, size_t inter, size_t 
     s.idx = reinterpret_cast<int32_t*>(take(slots * 4));
     s.weight = reinterpret_cast<float*>(take(slots * 4));
     s.perm = reinterpret_cast<int32_t*>(take(slots * 4));
+    s.position = reinterpret_cast<int32_t*>(take(slots * 4));
     s.offsets = reinterpret_cast<int32_t*>(take((experts + 1) * 4));
     s.items = reinterpret_cast<int32_t*>(take(items * 8));
     s.item_count = reinterpret_cast<int32_t*>(take(4));
     s.h_hi = reinterpret_cast<uint16_t*>(take(slots * inter * 2));
     s.h_lo = reinterpret_cast<uint16_t*>(take(slots * inter * 2));
-    s.contribution = reinterpret_cast<float*>(take(slots * hidden * 4));
+    s.part_g = s.part_u = nullptr;
+    if (ks.gate_up > 1) {
+        s.part_g = reinterpret_cast<float*>(take(ks.gate_up * slots * inter * 4));
+        s.part_u = reinterpret_cast<float*>(take(ks.gate_up * slots * inter * 4));
+    }
+    s.part_d = reinterpret_cast<float*>(take(ks.down * slots * hidden * 4));
     return s;
 }
 
@@ -466,25 +724,15 @@ int check_route(const float* logits, size_t tokens, size_t experts, size_t top_k
     return KDQ_OK;
 }
 
-// Waves per workgroup for an N dimension of n features (32 per wave): the largest of
-// 4, 3, 2, 1 dividing n / 32.
-unsigned waves_for(size_t n) {
-    const size_t tiles = n / 32;
-    for (unsigned w : {4u, 3u, 2u})
-        if (tiles % w == 0)
-            return w;
-    return 1;
-}
-
 int launch_route(const float* logits, size_t tokens, size_t experts, size_t top_k,
                  int32_t* idx, float* w, int32_t* offsets, int32_t* perm, int32_t* items,
-                 int32_t* item_count, hipStream_t stream) {
+                 int32_t* item_count, int32_t* position, hipStream_t stream) {
     hipLaunchKernelGGL(route_kernel, dim3(unsigned((tokens + 3) / 4)), dim3(256), 0, stream,
                        logits, unsigned(tokens), unsigned(experts), unsigned(top_k), idx, w);
     KDQ_HIP(hipGetLastError());
     hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, stream, idx,
                        unsigned(tokens * top_k), unsigned(experts), offsets, perm, items,
-                       item_count);
+                       item_count, position);
     KDQ_HIP(hipGetLastError());
     return KDQ_OK;
 }
@@ -507,7 +755,7 @@ extern "C" int kdq_moe_route(const float* logits, size_t tokens, size_t experts,
     if (rc)
         return rc;
     return launch_route(logits, tokens, experts, top_k, idx, w, offsets, perm, scratch,
-                        scratch + items * 2, static_cast<hipStream_t>(stream));
+                        scratch + items * 2, nullptr, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int kdq_mxfp4_dequantize(const uint8_t* blocks, const uint8_t* scales, size_t rows,
@@ -542,11 +790,12 @@ extern "C" int kdq_moe_mxfp4(const uint16_t* x_bf16, const float* logits, size_t
     if (overlaps(y, tokens * hidden * 4, x_bf16, tokens * hidden * 2) ||
         overlaps(y, tokens * hidden * 4, logits, tokens * experts * 4))
         return KDQ_ERR_ALIAS;
-    const size_t bytes = moe_scratch_bytes(tokens, hidden, inter, experts, top_k);
+    const MoeSlices ks = moe_slices(tokens, hidden, inter, experts, top_k);
+    const size_t bytes = moe_scratch_bytes(tokens, hidden, inter, experts, top_k, ks);
     auto* base = static_cast<uint8_t*>(workspace(bytes, &rc));
     if (rc)
         return rc;
-    MoeScratch s = carve(base, tokens, hidden, inter, experts, top_k);
+    MoeScratch s = carve(base, tokens, hidden, inter, experts, top_k, ks);
     if (idx)
         s.idx = idx;
     if (w)
@@ -557,26 +806,34 @@ extern "C" int kdq_moe_mxfp4(const uint16_t* x_bf16, const float* logits, size_t
         s.perm = perm;
     auto st = static_cast<hipStream_t>(stream);
     rc = launch_route(logits, tokens, experts, top_k, s.idx, s.weight, s.offsets, s.perm,
-                      s.items, s.item_count, st);
+                      s.items, s.item_count, s.position, st);
     if (rc)
         return rc;
     const size_t slots = tokens * top_k;
-    const unsigned max_items = unsigned(slots / kItemRows + experts + 1);
-    const unsigned wg = waves_for(inter);
-    hipLaunchKernelGGL(gate_up_kernel, dim3(unsigned(inter / 32 / wg), max_items), dim3(64 * wg),
-                       0, st, x_bf16, unsigned(hidden), unsigned(inter), unsigned(top_k),
-                       gate_blocks, gate_scales, up_blocks, up_scales, s.offsets, s.perm,
-                       s.items, s.item_count, s.h_hi, s.h_lo);
+    const unsigned max_items = unsigned(std::min(slots, slots / kItemRows + experts + 1));
+    const unsigned groups_gu = unsigned((inter + 63) / 64);
+    const unsigned groups_d = unsigned((hidden / 32 + kGemmWaves - 1) / kGemmWaves);
+    hipLaunchKernelGGL(gate_up_kernel, dim3(groups_gu, max_items, ks.gate_up),
+                       dim3(kGemmWaves * 64), 0, st, x_bf16, unsigned(hidden), unsigned(inter),
+                       unsigned(top_k), gate_blocks, gate_scales, up_blocks, up_scales,
+                       s.offsets, s.perm, s.items, s.item_count, s.h_hi, s.h_lo, s.part_g,
+                       s.part_u, slots * inter);
     KDQ_HIP(hipGetLastError());
-    const unsigned wd = waves_for(hidden);
-    hipLaunchKernelGGL(down_kernel, dim3(unsigned(hidden / 32 / wd), max_items), dim3(64 * wd), 0,
-                       st, s.h_hi, s.h_lo, unsigned(hidden), unsigned(inter), down_blocks,
-                       down_scales, s.offsets, s.perm, s.weight, s.items, s.item_count,
-                       s.contribution);
+    if (ks.gate_up > 1) {
+        const size_t n = slots * inter;
+        hipLaunchKernelGGL(finalize_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st,
+                           s.part_g, s.part_u, n, ks.gate_up, s.h_hi, s.h_lo);
+        KDQ_HIP(hipGetLastError());
+    }
+    hipLaunchKernelGGL(down_kernel, dim3(groups_d, max_items, ks.down), dim3(kGemmWaves * 64),
+                       0, st, s.h_hi, s.h_lo, unsigned(hidden), unsigned(inter), down_blocks,
+                       down_scales, s.offsets, s.items, s.item_count, s.part_d,
+                       slots * hidden);
     KDQ_HIP(hipGetLastError());
     const size_t n = tokens * hidden;
     hipLaunchKernelGGL(combine_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st,
-                       s.contribution, unsigned(tokens), unsigned(hidden), unsigned(top_k), y);
+                       s.part_d, slots * hidden, ks.down, s.position, s.weight,
+                       unsigned(tokens), unsigned(hidden), unsigned(top_k), y);
     KDQ_HIP(hipGetLastError());
     return KDQ_OK;
 }
