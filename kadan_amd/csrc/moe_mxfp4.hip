@@ -28,7 +28,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kMaxTopK = 8, kMaxExperts = 256;
 constexpr int kTileRows = 32, kTiles = 2, kItemRows = kTileRows * kTiles;
-constexpr int kGemmWaves = 4;  // wavefronts per grouped-GEMM workgroup, 32 features each
+constexpr int kGemmWaves = 8;  // wavefronts per grouped-GEMM workgroup, 32 weight rows each
 constexpr int kStepK = 64;     // K values per step: 16 FP4 bytes per lane
 
 // ------------------------------------------------------------------ routing
@@ -218,41 +218,44 @@ __device__ __forceinline__ Item load_item(const int32_t* items, const int32_t* o
 }
 
 // Grouped GEMMs on v_mfma_f32_32x32x16_bf16.  A workgroup of kGemmWaves wavefronts works
-// on one work item (expert e, up to kItemRows consecutive rows of its segment) and one K
-// slice.  The weight operand B streams from HBM: lane (f = lane % 32, g = lane / 32) of a
-// wavefront owning 32 weight rows loads per 64-value step the 16 bytes (32 FP4 values)
-// k = 64q + 32g .. +31 of its row and their E8M0 scale, and MFMA t takes values
-// 32g + 8t .. +7 of them (the activation operand uses the same k order), dequantized
-// with v_cvt_scalef32_pk_bf16_fp4, which is exact.  The activation operand A (the item's
-// rows) is staged per chunk of steps into LDS by the whole workgroup, double-buffered.
-// Per chunk, every lane issues the next chunk's activation loads first and the next
-// chunk's weight loads second, all unconditionally (indices past the end are clamped to
-// valid data), so the wait before the activations are stored to LDS does not include
-// the weight loads, which stay in flight across the barrier.
+// on one work item (expert e, up to kItemRows consecutive rows of its segment: one or two
+// MFMA row tiles of 32) and one K slice; every wavefront owns 32 weight rows.  The weight
+// operand B streams from HBM: lane (f = lane % 32, g = lane / 32) loads per 64-value step
+// the 16 bytes (32 FP4 values) k = 64q + 32g .. +31 of its row and their E8M0 scale, and
+// MFMA t takes values 32g + 8t .. +7 of them (the activation operand uses the same k
+// order), dequantized with v_cvt_scalef32_pk_bf16_fp4, which is exact.  The activation
+// operand A (the item's occupied row tiles) is staged per chunk of steps into LDS by the
+// whole workgroup, double-buffered; one staged chunk serves all 8 wavefronts (256 weight
+// rows).  Every lane issues chunk c + 2's activation loads, then its weight loads, while
+// chunk c is multiplied and chunk c + 1 is stored to LDS; all loads are unconditional
+// (indices past the end are clamped to valid data), so each wait counts exactly the loads
+// the next step needs and the weight loads stay in flight across the chunk barrier.
 
 // Staged rows: PLANES planes of CHUNK steps of 64 bf16 values per row, 16 bytes of pad.
 template <int CHUNK, int PLANES> struct Stage {
     static constexpr int pitch = CHUNK * PLANES * kStepK * 2 + 16;
     static constexpr int buffer = kItemRows * pitch;
     static constexpr int pieces = CHUNK * PLANES * 8;  // 16-byte pieces per row
-    static constexpr int per_thread = kItemRows * pieces / (kGemmWaves * 64);
 };
 
-// This thread's pieces of the staged chunk: piece i is row (tid / pieces + i * rows_step)
-// at offset (tid % pieces) of the row; the same rows for every chunk.
-template <int CHUNK, int PLANES> struct StageThread {
+// This thread's share of a staged chunk of ROWS rows: pieces i = 0..per_thread-1 are row
+// (tid / pieces + i * rows_step) at the same offset (tid % pieces) for every chunk.
+template <int CHUNK, int PLANES, int ROWS> struct StageThread {
     using S = Stage<CHUNK, PLANES>;
-    static constexpr int rows_step = kGemmWaves * 64 / S::pieces;
-    const uint16_t* src[S::per_thread];  // row start in its plane (a valid row)
-    bool valid[S::per_thread];
+    static constexpr int threads = kGemmWaves * 64;
+    static constexpr int per_thread = (ROWS * S::pieces + threads - 1) / threads;
+    static constexpr int rows_step = threads / S::pieces;
+    const uint16_t* src[per_thread];  // row start in its plane (always a valid row)
+    bool valid[per_thread];           // the row exists (else it is stored as zeros)
+    bool stores[per_thread];          // the piece lies inside the ROWS staged rows
     unsigned step, plane, sub;
 };
 
 // `row_offset(p, r)` is the element offset of row r in plane p, or -1 past the item.
-template <int CHUNK, int PLANES, class RowOffset>
-__device__ __forceinline__ StageThread<CHUNK, PLANES> stage_thread(
+template <int CHUNK, int PLANES, int ROWS, class RowOffset>
+__device__ __forceinline__ StageThread<CHUNK, PLANES, ROWS> stage_thread(
     const uint16_t* const (&planes)[PLANES], RowOffset row_offset) {
-    using T = StageThread<CHUNK, PLANES>;
+    using T = StageThread<CHUNK, PLANES, ROWS>;
     using S = Stage<CHUNK, PLANES>;
     T t;
     const unsigned within = threadIdx.x % S::pieces;
@@ -260,45 +263,48 @@ __device__ __forceinline__ StageThread<CHUNK, PLANES> stage_thread(
     t.plane = (within / 8) % PLANES;
     t.sub = within % 8;
 #pragma unroll
-    for (int i = 0; i < S::per_thread; ++i) {
+    for (int i = 0; i < T::per_thread; ++i) {
         const unsigned row = threadIdx.x / S::pieces + i * T::rows_step;
-        const long long at = row_offset(t.plane, row);
+        const long long at = row < unsigned(ROWS) ? row_offset(t.plane, row) : -1;
+        t.stores[i] = row < unsigned(ROWS);
         t.valid[i] = at >= 0;
         t.src[i] = planes[t.plane] + (at >= 0 ? at : row_offset(t.plane, 0));
     }
     return t;
 }
 
-template <int CHUNK, int PLANES> struct StagePieces {
-    u32x4 v[Stage<CHUNK, PLANES>::per_thread];
+template <int CHUNK, int PLANES, int ROWS> struct StagePieces {
+    u32x4 v[StageThread<CHUNK, PLANES, ROWS>::per_thread];
 };
 
 // Loads the pieces of the chunk starting at step q (steps past `last` re-read `last`).
-template <int CHUNK, int PLANES>
-__device__ __forceinline__ void stage_load(const StageThread<CHUNK, PLANES>& t, unsigned q,
-                                           unsigned last, StagePieces<CHUNK, PLANES>& P) {
+template <int CHUNK, int PLANES, int ROWS>
+__device__ __forceinline__ void stage_load(const StageThread<CHUNK, PLANES, ROWS>& t, unsigned q,
+                                           unsigned last, StagePieces<CHUNK, PLANES, ROWS>& P) {
     const unsigned step = min(q + t.step, last);
 #pragma unroll
-    for (int i = 0; i < Stage<CHUNK, PLANES>::per_thread; ++i)
+    for (int i = 0; i < StageThread<CHUNK, PLANES, ROWS>::per_thread; ++i)
         P.v[i] = *reinterpret_cast<const u32x4*>(t.src[i] + size_t(step) * kStepK + t.sub * 8);
 }
 
-template <int CHUNK, int PLANES>
-__device__ __forceinline__ void stage_store(const StageThread<CHUNK, PLANES>& t,
-                                            const StagePieces<CHUNK, PLANES>& P, unsigned steps,
-                                            uint8_t* buf) {
+template <int CHUNK, int PLANES, int ROWS>
+__device__ __forceinline__ void stage_store(const StageThread<CHUNK, PLANES, ROWS>& t,
+                                            const StagePieces<CHUNK, PLANES, ROWS>& P,
+                                            unsigned steps, uint8_t* buf) {
+    using T = StageThread<CHUNK, PLANES, ROWS>;
     using S = Stage<CHUNK, PLANES>;
     if (t.step >= steps)
         return;
 #pragma unroll
-    for (int i = 0; i < S::per_thread; ++i) {
-        const unsigned row = threadIdx.x / S::pieces + i * StageThread<CHUNK, PLANES>::rows_step;
-        *reinterpret_cast<u32x4*>(buf + row * S::pitch + (t.step * PLANES + t.plane) * 128 +
-                                  t.sub * 16) = t.valid[i] ? P.v[i] : u32x4{0, 0, 0, 0};
+    for (int i = 0; i < T::per_thread; ++i) {
+        const unsigned row = threadIdx.x / S::pieces + i * T::rows_step;
+        if (t.stores[i])
+            *reinterpret_cast<u32x4*>(buf + row * S::pitch + (t.step * PLANES + t.plane) * 128 +
+                                      t.sub * 16) = t.valid[i] ? P.v[i] : u32x4{0, 0, 0, 0};
     }
 }
 
-// 8 exact bf16 values from dword t of a lane's 16 FP4 bytes.
+// 8 exact bf16 values from one dword of a lane's 16 FP4 bytes.
 __device__ __forceinline__ bf16x8 dequant8(unsigned word, float scale) {
     const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 0);
     const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 1);
@@ -334,19 +340,16 @@ __device__ __forceinline__ void slice_steps(unsigned steps, unsigned slices, uns
 }
 
 // One step of MFMAs for one weight matrix: acc[m] += A(tile m, step s) * B(step).
-template <int PLANES>
+template <int PLANES, int TILES>
 __device__ __forceinline__ void step_mfma(const WStep& w, const uint8_t* buf, int pitch, int s,
-                                          int tiles, unsigned i32, unsigned g,
-                                          f32x16 (&acc)[kTiles]) {
+                                          unsigned i32, unsigned g, f32x16 (&acc)[TILES]) {
     const float scale = e8m0(w.scale);
     const unsigned c[4] = {w.codes.x, w.codes.y, w.codes.z, w.codes.w};
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         const bf16x8 b = dequant8(c[t], scale);
 #pragma unroll
-        for (int m = 0; m < kTiles; ++m) {
-            if (m >= tiles)
-                break;
+        for (int m = 0; m < TILES; ++m) {
             const uint8_t* rowp = buf + (m * kTileRows + i32) * pitch + s * PLANES * 128 +
                                   (32 * g + 8 * t) * 2;
 #pragma unroll
@@ -354,10 +357,81 @@ __device__ __forceinline__ void step_mfma(const WStep& w, const uint8_t* buf, in
                 acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lds_bf16x8(rowp + p * 128), b,
                                                                  acc[m], 0, 0, 0);
         }
+        __builtin_amdgcn_sched_barrier(0);  // one MFMA group's operands live at a time
     }
 }
 
-// gate/up: grid (feature groups of 64, items, K slices).  Wavefront w multiplies the gate
+__device__ __forceinline__ void issue_fence() {
+    asm volatile("" ::: "memory");  // keeps the load issue order (activation pointers are
+    __builtin_amdgcn_sched_barrier(0);  // not restrict)
+}
+
+// The K loop shared by both GEMMs: acc += A(rows, [q0, q1)) * B(rows w of one matrix).
+// Activations run two chunks ahead of the MFMAs, weights WDEPTH - 1 chunks ahead; a
+// chunk's weight loads for one lane are consecutive 16-byte pieces of its row, issued
+// back to back so each 128-byte line is requested once.
+template <int CHUNK, int PLANES, int TILES, int WDEPTH>
+__device__ __forceinline__ void gemm_loop(const StageThread<CHUNK, PLANES, TILES * kTileRows>& st,
+                                          const uint8_t* wb, const uint8_t* ws, unsigned q0,
+                                          unsigned q1, bool active, unsigned i32, unsigned g,
+                                          uint8_t (&stage)[2][Stage<CHUNK, PLANES>::buffer],
+                                          f32x16 (&acc)[TILES]) {
+    static_assert(WDEPTH == 2 || WDEPTH == 3, "weight ring");
+    using S = Stage<CHUNK, PLANES>;
+    constexpr int ROWS = TILES * kTileRows;
+    auto load_w = [&](unsigned q, WStep(&w)[CHUNK]) {
+#pragma unroll
+        for (int s = 0; s < CHUNK; ++s)
+            w[s] = load_wstep(wb, ws, min(q + s, q1 - 1), g);
+    };
+#pragma unroll
+    for (int m = 0; m < TILES; ++m)
+        acc[m] = f32x16{};
+    StagePieces<CHUNK, PLANES, ROWS> pa, pb;
+    WStep wa[CHUNK], wm[CHUNK], wn[CHUNK];
+    stage_load(st, q0, q1 - 1, pa);
+    issue_fence();
+    load_w(q0, wa);
+    issue_fence();
+    stage_load(st, q0 + CHUNK, q1 - 1, pb);
+    issue_fence();
+    if constexpr (WDEPTH == 3) {
+        load_w(q0 + CHUNK, wm);
+        issue_fence();
+    }
+    stage_store(st, pa, min(unsigned(CHUNK), q1 - q0), stage[0]);
+    __syncthreads();
+    pa = pb;
+    unsigned buf = 0;
+    for (unsigned q = q0; q < q1; q += CHUNK, buf ^= 1) {
+        const unsigned steps = min(unsigned(CHUNK), q1 - q), qn = q + CHUNK;
+        stage_load(st, qn + CHUNK, q1 - 1, pb);
+        issue_fence();
+        if constexpr (WDEPTH == 3)
+            load_w(qn + CHUNK, wn);
+        else
+            load_w(qn, wm);
+        issue_fence();
+        if (active) {
+#pragma unroll
+            for (int s = 0; s < CHUNK; ++s)
+                if (unsigned(s) < steps)
+                    step_mfma<PLANES, TILES>(wa[s], stage[buf], S::pitch, s, i32, g, acc);
+        }
+        if (qn < q1)
+            stage_store(st, pa, min(unsigned(CHUNK), q1 - qn), stage[buf ^ 1]);
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < CHUNK; ++s) {
+            wa[s] = wm[s];
+            if constexpr (WDEPTH == 3)
+                wm[s] = wn[s];
+        }
+        pa = pb;
+    }
+}
+
+// gate/up: grid (feature groups of 128, items, K slices).  Wavefront w multiplies the gate
 // (w even) or up (w odd) rows of features n0 + 32 (w / 2) .. +31.  One slice: h =
 // silu(g) * u as bf16 hi + lo (g passes through LDS); more: fp32 partials of g and u
 // (summed by finalize_kernel).
@@ -371,6 +445,7 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gate_up_kernel(
     float* __restrict__ part_u, size_t part_stride) {
     constexpr int CHUNK = 2;
     using S = Stage<CHUNK, 1>;
+    static_assert(2 * S::buffer >= (kGemmWaves / 2) * kTiles * 16 * 64 * 4, "gate exchange");
     __shared__ __align__(16) uint8_t stage[2][S::buffer];
     __shared__ long long src[kItemRows];
     if (int(blockIdx.y) >= *item_count)
@@ -379,117 +454,75 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gate_up_kernel(
     const unsigned wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const unsigned i32 = lane % 32, g = lane / 32;
     const unsigned mat = wave % 2, tile = wave / 2;
-    const unsigned f0 = blockIdx.x * 64 + tile * 32;
+    const unsigned f0 = blockIdx.x * (kGemmWaves / 2) * 32 + tile * 32;
     const bool active = f0 < inter;  // uniform per wavefront
     const unsigned f = active ? f0 + i32 : i32;
-    const int tiles = (it.count + kTileRows - 1) / kTileRows;
     unsigned q0, q1;
     slice_steps(hidden / kStepK, gridDim.z, blockIdx.z, q0, q1);
     if (q0 >= q1)
         return;
-
     if (threadIdx.x < kItemRows) {
         const int r = int(threadIdx.x);
         src[r] = r < it.count ? (long long)(perm[it.segment + it.first + r] / int(top_k)) * hidden
                               : -1;
     }
     __syncthreads();
-    const uint16_t* planes[1] = {x};
-    const auto st = stage_thread<CHUNK, 1>(planes, [&](unsigned, unsigned r) { return src[r]; });
     const size_t wrow = size_t(it.expert) * inter + f;
     const uint8_t* wb = (mat ? up_blocks : gate_blocks) + wrow * (hidden / 2);
     const uint8_t* ws = (mat ? up_scales : gate_scales) + wrow * (hidden / 32);
+    const uint16_t* planes[1] = {x};
 
-    f32x16 acc[kTiles];
+    // straight-line code per tile count: no accumulator moves between control paths
+    auto run = [&]<int TILES>() {
+        const auto st = stage_thread<CHUNK, 1, TILES * kTileRows>(
+            planes, [&](unsigned, unsigned r) { return src[r]; });
+        f32x16 acc[TILES];
+        gemm_loop<CHUNK, 1, TILES, 3>(st, wb, ws, q0, q1, active, i32, g, stage, acc);
+        if (gridDim.z > 1) {
+            if (!active)
+                return;
+            float* part = (mat ? part_u : part_g) + blockIdx.z * part_stride;
 #pragma unroll
-    for (int m = 0; m < kTiles; ++m)
-        acc[m] = f32x16{};
-
-    StagePieces<CHUNK, 1> P;
-    stage_load(st, q0, q1 - 1, P);
-    asm volatile("" ::: "memory");  // activations before weights (x is not restrict)
-    __builtin_amdgcn_sched_barrier(0);
-    WStep w[CHUNK];
+            for (int m = 0; m < TILES; ++m)
 #pragma unroll
-    for (int s = 0; s < CHUNK; ++s)
-        w[s] = load_wstep(wb, ws, min(q0 + s, q1 - 1), g);
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    stage_store(st, P, min(unsigned(CHUNK), q1 - q0), stage[0]);
-    __syncthreads();
-
-    unsigned buf = 0;
-    for (unsigned q = q0; q < q1; q += CHUNK, buf ^= 1) {
-        const unsigned steps = min(unsigned(CHUNK), q1 - q), qn = q + CHUNK;
-        stage_load(st, qn, q1 - 1, P);
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
-        WStep wn[CHUNK];
-#pragma unroll
-        for (int s = 0; s < CHUNK; ++s)
-            wn[s] = load_wstep(wb, ws, min(qn + s, q1 - 1), g);
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
-        if (active) {
-#pragma unroll
-            for (int s = 0; s < CHUNK; ++s)
-                if (unsigned(s) < steps)
-                    step_mfma<1>(w[s], stage[buf], S::pitch, s, tiles, i32, g, acc);
-        }
-        if (qn < q1)
-            stage_store(st, P, min(unsigned(CHUNK), q1 - qn), stage[buf ^ 1]);
-        __syncthreads();
-#pragma unroll
-        for (int s = 0; s < CHUNK; ++s)
-            w[s] = wn[s];
-    }
-
-    if (gridDim.z > 1) {
-        if (!active)
+                for (int v = 0; v < 16; ++v) {
+                    const int r = m * kTileRows + 8 * (v / 4) + 4 * int(g) + (v % 4);
+                    if (r < it.count)
+                        part[size_t(it.segment + it.first + r) * inter + f] = acc[m][v];
+                }
             return;
-        float* part = (mat ? part_u : part_g) + blockIdx.z * part_stride;
+        }
+        // the gate values of feature tile `tile` pass to its up wavefront through LDS (the
+        // stage buffers are free after the last barrier): xg[tile][m][v][lane]
+        float* xg = reinterpret_cast<float*>(&stage[0][0]);
+        if (mat == 0 && active)
 #pragma unroll
-        for (int m = 0; m < kTiles; ++m) {
-            if (m >= tiles)
-                break;
+            for (int m = 0; m < TILES; ++m)
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+                    xg[((tile * kTiles + m) * 16 + v) * 64 + lane] = acc[m][v];
+        __syncthreads();
+        if (mat == 0 || !active)
+            return;
+#pragma unroll
+        for (int m = 0; m < TILES; ++m)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int r = m * kTileRows + 8 * (v / 4) + 4 * int(g) + (v % 4);
-                if (r < it.count)
-                    part[size_t(it.segment + it.first + r) * inter + f] = acc[m][v];
+                if (r < it.count) {
+                    const float gv = xg[((tile * kTiles + m) * 16 + v) * 64 + lane];
+                    const float h = silu(gv) * acc[m][v];
+                    const uint16_t hi = bf16_rne(h);
+                    const size_t at = size_t(it.segment + it.first + r) * inter + f;
+                    h_hi[at] = hi;
+                    h_lo[at] = bf16_rne(h - bf16_value(hi));
+                }
             }
-        }
-        return;
-    }
-    // gate values of feature tile `tile` pass to the up wavefront through LDS (the stage
-    // buffers are free after the last barrier): xg[tile][m][v][lane]
-    float* xg = reinterpret_cast<float*>(&stage[0][0]);
-    if (mat == 0 && active)
-#pragma unroll
-        for (int m = 0; m < kTiles; ++m)
-#pragma unroll
-            for (int v = 0; v < 16; ++v)
-                xg[((tile * kTiles + m) * 16 + v) * 64 + lane] = acc[m][v];
-    __syncthreads();
-    if (mat == 0 || !active)
-        return;
-#pragma unroll
-    for (int m = 0; m < kTiles; ++m) {
-        if (m >= tiles)
-            break;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int r = m * kTileRows + 8 * (v / 4) + 4 * int(g) + (v % 4);
-            if (r < it.count) {
-                const float gv = xg[((tile * kTiles + m) * 16 + v) * 64 + lane];
-                const float h = silu(gv) * acc[m][v];
-                const uint16_t hi = bf16_rne(h);
-                const size_t at = size_t(it.segment + it.first + r) * inter + f;
-                h_hi[at] = hi;
-                h_lo[at] = bf16_rne(h - bf16_value(hi));
-            }
-        }
-    }
+    };
+    if (it.count <= kTileRows)
+        run.template operator()<1>();
+    else
+        run.template operator()<2>();
 }
 
 // h = silu(sum_s g_s) * (sum_s u_s), slices summed in order, as bf16 hi + lo.
@@ -512,7 +545,7 @@ __global__ __launch_bounds__(256) void finalize_kernel(const float* __restrict__
     h_lo[i] = bf16_rne(h - bf16_value(hi));
 }
 
-// down: grid (feature groups of 128, items, K slices); fp32 partial sums of h x down
+// down: grid (feature groups of 256, items, K slices); fp32 partial sums of h x down
 // (hi and lo planes) per slice, indexed by the slot's position in the permutation.
 __global__ __launch_bounds__(kGemmWaves * 64) void down_kernel(
     const uint16_t* h_hi, const uint16_t* h_lo, unsigned hidden, unsigned inter,
@@ -520,8 +553,7 @@ __global__ __launch_bounds__(kGemmWaves * 64) void down_kernel(
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ items,
     const int32_t* __restrict__ item_count, float* __restrict__ part_d, size_t part_stride) {
     constexpr int CHUNK = 1;
-    using S = Stage<CHUNK, 2>;
-    __shared__ __align__(16) uint8_t stage[2][S::buffer];
+    __shared__ __align__(16) uint8_t stage[2][Stage<CHUNK, 2>::buffer];
     if (int(blockIdx.y) >= *item_count)
         return;
     const Item it = load_item(items, offsets, blockIdx.y);
@@ -530,67 +562,37 @@ __global__ __launch_bounds__(kGemmWaves * 64) void down_kernel(
     const unsigned d0 = (blockIdx.x * kGemmWaves + wave) * 32;
     const bool active = d0 < hidden;
     const unsigned d = active ? d0 + i32 : i32;
-    const int tiles = (it.count + kTileRows - 1) / kTileRows;
     unsigned q0, q1;
     slice_steps(inter / kStepK, gridDim.z, blockIdx.z, q0, q1);
     if (q0 >= q1)
         return;
-
-    const uint16_t* planes[2] = {h_hi, h_lo};
-    const auto st = stage_thread<CHUNK, 2>(planes, [&](unsigned, unsigned r) {
-        return r < unsigned(it.count) ? (long long)(it.segment + it.first + r) * inter : -1ll;
-    });
     const size_t wrow = size_t(it.expert) * hidden + d;
     const uint8_t* db = down_blocks + wrow * (inter / 2);
     const uint8_t* ds = down_scales + wrow * (inter / 32);
-
-    f32x16 acc[kTiles];
+    const uint16_t* planes[2] = {h_hi, h_lo};
+    auto row_offset = [&](unsigned, unsigned r) {
+        return r < unsigned(it.count) ? (long long)(it.segment + it.first + r) * inter : -1ll;
+    };
+    auto run = [&]<int TILES>() {
+        const auto st = stage_thread<CHUNK, 2, TILES * kTileRows>(planes, row_offset);
+        f32x16 acc[TILES];
+        gemm_loop<CHUNK, 2, TILES, 3>(st, db, ds, q0, q1, active, i32, g, stage, acc);
+        if (!active)
+            return;
 #pragma unroll
-    for (int m = 0; m < kTiles; ++m)
-        acc[m] = f32x16{};
-
-    // weights: the step being multiplied and two ahead
-    StagePieces<CHUNK, 2> P;
-    stage_load(st, q0, q1 - 1, P);
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    WStep w0 = load_wstep(db, ds, q0, g);
-    WStep w1 = load_wstep(db, ds, min(q0 + 1, q1 - 1), g);
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    stage_store(st, P, 1, stage[0]);
-    __syncthreads();
-
-    unsigned buf = 0;
-    for (unsigned q = q0; q < q1; ++q, buf ^= 1) {
-        stage_load(st, q + 1, q1 - 1, P);
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
-        const WStep w2 = load_wstep(db, ds, min(q + 2, q1 - 1), g);
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
-        if (active)
-            step_mfma<2>(w0, stage[buf], S::pitch, 0, tiles, i32, g, acc);
-        if (q + 1 < q1)
-            stage_store(st, P, 1, stage[buf ^ 1]);
-        __syncthreads();
-        w0 = w1;
-        w1 = w2;
-    }
-    if (!active)
-        return;
+        for (int m = 0; m < TILES; ++m)
 #pragma unroll
-    for (int m = 0; m < kTiles; ++m) {
-        if (m >= tiles)
-            break;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int r = m * kTileRows + 8 * (v / 4) + 4 * int(g) + (v % 4);
-            if (r < it.count)
-                part_d[blockIdx.z * part_stride + size_t(it.segment + it.first + r) * hidden + d] =
-                    acc[m][v];
-        }
-    }
+            for (int v = 0; v < 16; ++v) {
+                const int r = m * kTileRows + 8 * (v / 4) + 4 * int(g) + (v % 4);
+                if (r < it.count)
+                    part_d[blockIdx.z * part_stride +
+                           size_t(it.segment + it.first + r) * hidden + d] = acc[m][v];
+            }
+    };
+    if (it.count <= kTileRows)
+        run.template operator()<1>();
+    else
+        run.template operator()<2>();
 }
 
 // y[t, d] = sum_i w[t k + i] * (sum_s part_d[s, position(t k + i), d]), in selection order.
@@ -671,7 +673,7 @@ MoeSlices moe_slices(size_t tokens, size_t hidden, size_t inter, size_t experts,
         const size_t per = (steps + ks - 1) / ks;
         return unsigned((steps + per - 1) / per);
     };
-    return MoeSlices{slices((inter + 63) / 64, hidden / kStepK),
+    return MoeSlices{slices((inter / 32 + kGemmWaves / 2 - 1) / (kGemmWaves / 2), hidden / kStepK),
                      slices((hidden / 32 + kGemmWaves - 1) / kGemmWaves, inter / kStepK)};
 }
 
@@ -811,7 +813,7 @@ extern "C" int kdq_moe_mxfp4(const uint16_t* x_bf16, const float* logits, size_t
         return rc;
     const size_t slots = tokens * top_k;
     const unsigned max_items = unsigned(std::min(slots, slots / kItemRows + experts + 1));
-    const unsigned groups_gu = unsigned((inter + 63) / 64);
+    const unsigned groups_gu = unsigned((inter / 32 + kGemmWaves / 2 - 1) / (kGemmWaves / 2));
     const unsigned groups_d = unsigned((hidden / 32 + kGemmWaves - 1) / kGemmWaves);
     hipLaunchKernelGGL(gate_up_kernel, dim3(groups_gu, max_items, ks.gate_up),
                        dim3(kGemmWaves * 64), 0, st, x_bf16, unsigned(hidden), unsigned(inter),
