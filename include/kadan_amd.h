@@ -138,7 +138,10 @@ int kdq_mxfp4_dequantize(const uint8_t* blocks, const uint8_t* scales, size_t ro
 
 /* The whole layer: y fp32 [tokens x hidden] from x bf16 [tokens x hidden] and logits.
  * Also returns the routing (idx, w, offsets, perm as kdq_moe_route) when those
- * pointers are non-null.  hidden % 64 == 0, inter % 64 == 0. */
+ * pointers are non-null.  hidden % 64 == 0, inter % 64 == 0; x, y and the three block
+ * arrays 16-byte aligned.  The weights are repacked (kdq_moe_mxfp4_pack) into the
+ * workspace on every call: callers that keep weights resident pack once and call
+ * kdq_moe_mxfp4_packed.  Counterpart of MoeLayer::forward (qwen_layers.cpp:378-492). */
 int kdq_moe_mxfp4(const uint16_t* x_bf16, const float* logits, size_t tokens, size_t hidden,
                   size_t inter, size_t experts, size_t top_k,
                   const uint8_t* gate_blocks, const uint8_t* gate_scales,
@@ -146,6 +149,29 @@ int kdq_moe_mxfp4(const uint16_t* x_bf16, const float* logits, size_t tokens, si
                   const uint8_t* down_blocks, const uint8_t* down_scales,
                   float* y, int32_t* idx, float* w, int32_t* offsets, int32_t* perm,
                   void* stream);
+
+/* Device bytes of one packed projection tensor of `experts` x [rows x cols] MXFP4 values
+ * (0 unless rows % 32 == 0 and cols % 64 == 0).  No reference counterpart: the packed
+ * layout is this library's resident weight format (the reference keeps resident GGUF
+ * weights in its bank, IW/src/cuda/h3_compute.cu weight cache; MoE weights stay on the
+ * host, IW/src/models/text/qwen_layers.cpp:455-489). */
+size_t kdq_moe_mxfp4_packed_bytes(size_t experts, size_t rows, size_t cols);
+
+/* Repacks one projection tensor (gate, up: rows = inter, cols = hidden; down: rows =
+ * hidden, cols = inter) from the GPT-OSS layout into `packed` (kdq_moe_mxfp4_packed_bytes,
+ * 256-byte aligned; blocks 16-byte aligned).  Per expert, per group of 32 rows and step of
+ * 64 values, the codes form one 1 KB block (lane i + 32h: bytes 32q + 16h .. +15 of row
+ * 32g + i); per 4 steps the scales form one 256-byte block (lane dword byte j: scale of
+ * step 4p + j, half h).  Codes and scale bytes are copied unchanged. */
+int kdq_moe_mxfp4_pack(const uint8_t* blocks, const uint8_t* scales, size_t experts,
+                       size_t rows, size_t cols, uint8_t* packed, void* stream);
+
+/* kdq_moe_mxfp4 over packed weights (each 256-byte aligned). */
+int kdq_moe_mxfp4_packed(const uint16_t* x_bf16, const float* logits, size_t tokens,
+                         size_t hidden, size_t inter, size_t experts, size_t top_k,
+                         const uint8_t* gate_packed, const uint8_t* up_packed,
+                         const uint8_t* down_packed, float* y, int32_t* idx, float* w,
+                         int32_t* offsets, int32_t* perm, void* stream);
 
 /* Frees this thread's current device's cached workspace (synchronizes the device).
  * IW/include/kadan/dense_compute.hpp:66-68 release_scratch counterpart. */

@@ -46,6 +46,9 @@ _SIGNATURES = {
     "kdq_mxfp4_dequantize": [_VP, _VP, _SZ, _SZ, _VP, _VP, _VP],
     "kdq_moe_mxfp4": [_VP, _VP, _SZ, _SZ, _SZ, _SZ, _SZ, _VP, _VP, _VP, _VP, _VP, _VP,
                       _VP, _VP, _VP, _VP, _VP, _VP],
+    "kdq_moe_mxfp4_pack": [_VP, _VP, _SZ, _SZ, _SZ, _VP, _VP],
+    "kdq_moe_mxfp4_packed": [_VP, _VP, _SZ, _SZ, _SZ, _SZ, _SZ, _VP, _VP, _VP, _VP, _VP, _VP,
+                             _VP, _VP, _VP],
     "kdq_release_scratch": [],
 }
 _OTHER = {
@@ -54,6 +57,7 @@ _OTHER = {
     "kdq_block_values": (_SZ, [_I]),
     "kdq_block_bytes": (_SZ, [_I]),
     "kdq_row_bytes": (_SZ, [_I, _SZ]),
+    "kdq_moe_mxfp4_packed_bytes": (_SZ, [_SZ, _SZ, _SZ]),
 }
 
 _lib = None

@@ -429,14 +429,12 @@ ProjectionResult HipDenseCompute::moe_mxfp4(const Mxfp4Experts& e,
     require(!overlap(output, x) && !overlap(output, logits), "kdq_alias");
     hip_check(hipSetDevice(device_));
     auto st = static_cast<hipStream_t>(stream_);
-    // The expert set lives in the bank as one allocation: six arrays, 256-byte aligned.
+    // The expert set lives in the bank as one allocation in the packed layout of
+    // kdq_moe_mxfp4_pack: gate, up, down, each 256-byte aligned.
     const std::span<const std::uint8_t> parts[6] = {e.gate_blocks, e.gate_scales, e.up_blocks,
                                                     e.up_scales,   e.down_blocks, e.down_scales};
-    std::size_t at[6], total = 0;
-    for (int i = 0; i < 6; ++i) {
-        at[i] = total;
-        total += (parts[i].size() + 255) & ~std::size_t(255);
-    }
+    const std::size_t gu = (kdq_moe_mxfp4_packed_bytes(E, I, H) + 255) & ~std::size_t(255);
+    const std::size_t dn = (kdq_moe_mxfp4_packed_bytes(E, H, I) + 255) & ~std::size_t(255);
     const BankKey key{*e.identity, -1, H, I * E};
     auto it = bank_.find(key);
     if (it == bank_.end()) {
@@ -444,11 +442,25 @@ ProjectionResult HipDenseCompute::moe_mxfp4(const Mxfp4Experts& e,
             for (std::uint8_t s : parts[i])
                 require(s != 255, "kdq_invalid_block_scale");
         auto r = std::make_unique<Resident>();
-        r->bytes = total;
-        hip_check(hipMalloc(&r->device, total));
+        r->bytes = 2 * gu + dn;
+        hip_check(hipMalloc(&r->device, r->bytes));
+        // the six arrays pass through one temporary device copy in the GPT-OSS layout
+        std::size_t at[6], total = 0;
+        for (int i = 0; i < 6; ++i) {
+            at[i] = total;
+            total += (parts[i].size() + 255) & ~std::size_t(255);
+        }
+        Resident raw;
+        raw.bytes = total;
+        hip_check(hipMalloc(&raw.device, total));
+        auto* src = static_cast<std::uint8_t*>(raw.device);
+        auto* dst = static_cast<std::uint8_t*>(r->device);
         for (int i = 0; i < 6; ++i)
-            hip_check(hipMemcpyAsync(static_cast<std::uint8_t*>(r->device) + at[i],
-                                     parts[i].data(), parts[i].size(), hipMemcpyHostToDevice, st));
+            hip_check(hipMemcpyAsync(src + at[i], parts[i].data(), parts[i].size(),
+                                     hipMemcpyHostToDevice, st));
+        kdq_check(kdq_moe_mxfp4_pack(src + at[0], src + at[1], E, I, H, dst, st));
+        kdq_check(kdq_moe_mxfp4_pack(src + at[2], src + at[3], E, I, H, dst + gu, st));
+        kdq_check(kdq_moe_mxfp4_pack(src + at[4], src + at[5], E, H, I, dst + 2 * gu, st));
         synchronize();
         it = bank_.emplace(key, std::move(r)).first;
     }
@@ -461,9 +473,8 @@ ProjectionResult HipDenseCompute::moe_mxfp4(const Mxfp4Experts& e,
     auto* dw = reinterpret_cast<float*>(route + align16(tokens * top_k * 4));
     hip_check(hipMemcpyAsync(dx, x.data(), x.size_bytes(), hipMemcpyHostToDevice, st));
     hip_check(hipMemcpyAsync(dl, logits.data(), logits.size_bytes(), hipMemcpyHostToDevice, st));
-    kdq_check(kdq_moe_mxfp4(dx, dl, tokens, H, I, E, top_k, base + at[0], base + at[1],
-                            base + at[2], base + at[3], base + at[4], base + at[5], dy, didx, dw,
-                            nullptr, nullptr, st));
+    kdq_check(kdq_moe_mxfp4_packed(dx, dl, tokens, H, I, E, top_k, base, base + gu,
+                                   base + 2 * gu, dy, didx, dw, nullptr, nullptr, st));
     hip_check(hipMemcpyAsync(output.data(), dy, output.size_bytes(), hipMemcpyDeviceToHost, st));
     if (!selected.empty())
         hip_check(hipMemcpyAsync(selected.data(), didx, selected.size_bytes(),

@@ -147,6 +147,10 @@ inline bool overlaps(const void* a, size_t an, const void* b, size_t bn) {
     return x <= y ? y - x < an : x - y < bn;
 }
 
+inline bool misaligned(const void* p, size_t alignment) {
+    return reinterpret_cast<uintptr_t>(p) % alignment != 0;
+}
+
 inline bool mul_overflows(size_t a, size_t b) {
     return b && a > SIZE_MAX / b;
 }

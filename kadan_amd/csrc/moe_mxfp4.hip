@@ -28,7 +28,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kMaxTopK = 8, kMaxExperts = 256;
 constexpr int kTileRows = 32, kTiles = 2, kItemRows = kTileRows * kTiles;
-constexpr int kGemmWaves = 8;  // wavefronts per grouped-GEMM workgroup, 32 weight rows each
+constexpr int kGemmWaves = 4;  // wavefronts per grouped-GEMM workgroup, 64 weight rows each
 constexpr int kStepK = 64;     // K values per step: 16 FP4 bytes per lane
 
 // ------------------------------------------------------------------ routing
@@ -217,19 +217,79 @@ __device__ __forceinline__ Item load_item(const int32_t* items, const int32_t* o
     return it;
 }
 
+// ------------------------------------------------------------ packed weights
+//
+// The grouped GEMMs read expert weights in a packed layout, written once per weight set
+// by kdq_moe_mxfp4_pack from the reference layout (blocks [E][R][C/2], scales
+// [E][R][C/32]).  For each expert and each group of 32 rows (R % 32 == 0) and each step of
+// 64 values (C % 64 == 0):
+//   codes:  one 1 KB block, lane l = i + 32h holding bytes 32q + 16h .. +15 of row 32G + i
+//           (values 64q + 32h .. +31): a wavefront's load of a step is 8 whole lines;
+//   scales: per 4 steps one 256-byte block, byte j of lane l's dword = the E8M0 scale of
+//           values 64(4p + j) + 32h .. +31 of row 32G + i (zero past the last step).
+// Layout: codes [E][R/32][C/64][64][16 B], then scales [E][R/32][ceil(C/256)][64][4 B].
+
+struct Packed {
+    size_t groups, steps, scale_groups;  // per expert: row groups, steps, scale groups
+    size_t code_bytes, scale_bytes;      // whole tensor
+};
+
+__host__ __device__ inline Packed packed_shape(size_t experts, size_t rows, size_t cols) {
+    Packed p;
+    p.groups = rows / 32;
+    p.steps = cols / 64;
+    p.scale_groups = (p.steps + 3) / 4;
+    p.code_bytes = experts * rows * cols / 2;
+    p.scale_bytes = experts * p.groups * p.scale_groups * 256;
+    return p;
+}
+
+__global__ __launch_bounds__(256) void pack_codes_kernel(const uint8_t* __restrict__ blocks,
+                                                         size_t units, size_t steps, size_t cols,
+                                                         uint8_t* __restrict__ out) {
+    const size_t u = size_t(blockIdx.x) * blockDim.x + threadIdx.x;  // one 16-byte unit
+    if (u >= units)
+        return;
+    const unsigned l = unsigned(u % 64);
+    const size_t q = (u / 64) % steps, eg = u / (64 * steps);  // eg = expert * groups + group
+    const size_t row = eg * 32 + l % 32;
+    *reinterpret_cast<u32x4*>(out + u * 16) =
+        load16(blocks + row * (cols / 2) + q * 32 + 16 * (l / 32));
+}
+
+__global__ __launch_bounds__(256) void pack_scales_kernel(const uint8_t* __restrict__ scales,
+                                                          size_t words, size_t scale_groups,
+                                                          size_t steps, size_t cols,
+                                                          unsigned* __restrict__ out) {
+    const size_t u = size_t(blockIdx.x) * blockDim.x + threadIdx.x;  // one dword
+    if (u >= words)
+        return;
+    const unsigned l = unsigned(u % 64);
+    const size_t p = (u / 64) % scale_groups, eg = u / (64 * scale_groups);
+    const uint8_t* row = scales + (eg * 32 + l % 32) * (cols / 32);
+    unsigned word = 0;
+#pragma unroll
+    for (unsigned j = 0; j < 4; ++j) {
+        const size_t q = 4 * p + j;
+        if (q < steps)
+            word |= unsigned(row[2 * q + l / 32]) << (8 * j);
+    }
+    out[u] = word;
+}
+
 // Grouped GEMMs on v_mfma_f32_32x32x16_bf16.  A workgroup of kGemmWaves wavefronts works
 // on one work item (expert e, up to kItemRows consecutive rows of its segment: one or two
-// MFMA row tiles of 32) and one K slice; every wavefront owns 32 weight rows.  The weight
-// operand B streams from HBM: lane (f = lane % 32, g = lane / 32) loads per 64-value step
-// the 16 bytes (32 FP4 values) k = 64q + 32g .. +31 of its row and their E8M0 scale, and
-// MFMA t takes values 32g + 8t .. +7 of them (the activation operand uses the same k
-// order), dequantized with v_cvt_scalef32_pk_bf16_fp4, which is exact.  The activation
-// operand A (the item's occupied row tiles) is staged per chunk of steps into LDS by the
-// whole workgroup, double-buffered; one staged chunk serves all 8 wavefronts (256 weight
-// rows).  Every lane issues chunk c + 2's activation loads, then its weight loads, while
-// chunk c is multiplied and chunk c + 1 is stored to LDS; all loads are unconditional
-// (indices past the end are clamped to valid data), so each wait counts exactly the loads
-// the next step needs and the weight loads stay in flight across the chunk barrier.
+// MFMA row tiles of 32) and one K slice.  Every wavefront owns two 32-row weight groups
+// (gate and up of the same 32 features, or two groups of down rows) and multiplies each
+// staged activation fragment into both.  The weight operand B streams from the packed
+// layout: per 64-value step, lane (f = lane % 32, h = lane / 32) holds 32 FP4 values of its
+// row (16 bytes) and MFMA t takes values 32h + 8t .. +7 of them (the activation operand
+// uses the same k order), dequantized with v_cvt_scalef32_pk_bf16_fp4, which is exact.
+// The activation operand A (the item's occupied row tiles) is staged per chunk of steps
+// into LDS by the whole workgroup, double-buffered.  Each lane issues chunk c + 2's
+// activation loads, then chunk c + 1's weight loads, while chunk c is multiplied and chunk
+// c + 1 is stored to LDS; all loads are unconditional (indices past the end are clamped
+// to valid data), so each wait counts exactly the loads the next step needs.
 
 // Staged rows: PLANES planes of CHUNK steps of 64 bf16 values per row, 16 bytes of pad.
 template <int CHUNK, int PLANES> struct Stage {
@@ -243,18 +303,21 @@ template <int CHUNK, int PLANES> struct Stage {
 template <int CHUNK, int PLANES, int ROWS> struct StageThread {
     using S = Stage<CHUNK, PLANES>;
     static constexpr int threads = kGemmWaves * 64;
-    static constexpr int per_thread = (ROWS * S::pieces + threads - 1) / threads;
+    static_assert(ROWS * S::pieces % threads == 0, "pieces cover the threads exactly");
+    static constexpr int per_thread = ROWS * S::pieces / threads;
     static constexpr int rows_step = threads / S::pieces;
     const uint16_t* src[per_thread];  // row start in its plane (always a valid row)
     bool valid[per_thread];           // the row exists (else it is stored as zeros)
-    bool stores[per_thread];          // the piece lies inside the ROWS staged rows
     unsigned step, plane, sub;
 };
 
-// `row_offset(p, r)` is the element offset of row r in plane p, or -1 past the item.
+// Plane p of the staged operand starts at base + p * plane_stride (one base pointer keeps
+// the loads global: a per-thread choice between pointers would make them flat);
+// `row_offset(r)` is the element offset of row r within a plane, or -1 past the item.
 template <int CHUNK, int PLANES, int ROWS, class RowOffset>
-__device__ __forceinline__ StageThread<CHUNK, PLANES, ROWS> stage_thread(
-    const uint16_t* const (&planes)[PLANES], RowOffset row_offset) {
+__device__ __forceinline__ StageThread<CHUNK, PLANES, ROWS> stage_thread(const uint16_t* base,
+                                                                         size_t plane_stride,
+                                                                         RowOffset row_offset) {
     using T = StageThread<CHUNK, PLANES, ROWS>;
     using S = Stage<CHUNK, PLANES>;
     T t;
@@ -265,10 +328,9 @@ __device__ __forceinline__ StageThread<CHUNK, PLANES, ROWS> stage_thread(
 #pragma unroll
     for (int i = 0; i < T::per_thread; ++i) {
         const unsigned row = threadIdx.x / S::pieces + i * T::rows_step;
-        const long long at = row < unsigned(ROWS) ? row_offset(t.plane, row) : -1;
-        t.stores[i] = row < unsigned(ROWS);
+        const long long at = row_offset(row);
         t.valid[i] = at >= 0;
-        t.src[i] = planes[t.plane] + (at >= 0 ? at : row_offset(t.plane, 0));
+        t.src[i] = base + t.plane * plane_stride + (at >= 0 ? at : row_offset(0));
     }
     return t;
 }
@@ -287,20 +349,20 @@ __device__ __forceinline__ void stage_load(const StageThread<CHUNK, PLANES, ROWS
         P.v[i] = *reinterpret_cast<const u32x4*>(t.src[i] + size_t(step) * kStepK + t.sub * 8);
 }
 
+// Stores a loaded chunk to LDS: every piece, also those of steps past the end of the K
+// range (they land in buffer space no MFMA reads), without branches, so no path leaves
+// a load outstanding.
 template <int CHUNK, int PLANES, int ROWS>
 __device__ __forceinline__ void stage_store(const StageThread<CHUNK, PLANES, ROWS>& t,
                                             const StagePieces<CHUNK, PLANES, ROWS>& P,
-                                            unsigned steps, uint8_t* buf) {
+                                            uint8_t* buf) {
     using T = StageThread<CHUNK, PLANES, ROWS>;
     using S = Stage<CHUNK, PLANES>;
-    if (t.step >= steps)
-        return;
 #pragma unroll
     for (int i = 0; i < T::per_thread; ++i) {
         const unsigned row = threadIdx.x / S::pieces + i * T::rows_step;
-        if (t.stores[i])
-            *reinterpret_cast<u32x4*>(buf + row * S::pitch + (t.step * PLANES + t.plane) * 128 +
-                                      t.sub * 16) = t.valid[i] ? P.v[i] : u32x4{0, 0, 0, 0};
+        *reinterpret_cast<u32x4*>(buf + row * S::pitch + (t.step * PLANES + t.plane) * 128 +
+                                  t.sub * 16) = t.valid[i] ? P.v[i] : u32x4{0, 0, 0, 0};
     }
 }
 
@@ -317,48 +379,34 @@ __device__ __forceinline__ bf16x8 lds_bf16x8(const uint8_t* p) {
     return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(p));
 }
 
-// Packed weights of one lane for one step (16 FP4 bytes and their scale).
-struct WStep {
-    u32x4 codes;
-    unsigned scale;
+// One wavefront's two packed weight groups (codes at + step * 1 KB, scales at + group * 64
+// dwords, both already offset by the lane).
+struct WavePair {
+    const uint8_t* codes[2];
+    const unsigned* scales[2];
 };
 
-__device__ __forceinline__ WStep load_wstep(const uint8_t* row, const uint8_t* srow, unsigned q,
-                                            unsigned g) {
-    WStep w;
-    w.codes = load16(row + size_t(q) * 32 + 16 * g);
-    w.scale = srow[size_t(q) * 2 + g];
+__device__ __forceinline__ WavePair wave_pair(const uint8_t* packed, const Packed& shape,
+                                              size_t group0, size_t group1, unsigned lane) {
+    WavePair w;
+    const size_t g[2] = {group0, group1};
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+        w.codes[m] = packed + g[m] * shape.steps * 1024 + lane * 16;
+        w.scales[m] = reinterpret_cast<const unsigned*>(packed + shape.code_bytes +
+                                                        g[m] * shape.scale_groups * 256) +
+                      lane;
+    }
     return w;
 }
 
-// Steps of K slice `slice` of `steps` total: [begin, end).
+// K slice `slice` of `slices`: [begin, end) in steps, begin a multiple of 8 (two scale
+// groups).
 __device__ __forceinline__ void slice_steps(unsigned steps, unsigned slices, unsigned slice,
                                             unsigned& begin, unsigned& end) {
-    const unsigned per = (steps + slices - 1) / slices;
+    const unsigned per = ((steps + slices - 1) / slices + 7) / 8 * 8;
     begin = min(steps, slice * per);
     end = min(steps, begin + per);
-}
-
-// One step of MFMAs for one weight matrix: acc[m] += A(tile m, step s) * B(step).
-template <int PLANES, int TILES>
-__device__ __forceinline__ void step_mfma(const WStep& w, const uint8_t* buf, int pitch, int s,
-                                          unsigned i32, unsigned g, f32x16 (&acc)[TILES]) {
-    const float scale = e8m0(w.scale);
-    const unsigned c[4] = {w.codes.x, w.codes.y, w.codes.z, w.codes.w};
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const bf16x8 b = dequant8(c[t], scale);
-#pragma unroll
-        for (int m = 0; m < TILES; ++m) {
-            const uint8_t* rowp = buf + (m * kTileRows + i32) * pitch + s * PLANES * 128 +
-                                  (32 * g + 8 * t) * 2;
-#pragma unroll
-            for (int p = 0; p < PLANES; ++p)
-                acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lds_bf16x8(rowp + p * 128), b,
-                                                                 acc[m], 0, 0, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);  // one MFMA group's operands live at a time
-    }
 }
 
 __device__ __forceinline__ void issue_fence() {
@@ -366,99 +414,129 @@ __device__ __forceinline__ void issue_fence() {
     __builtin_amdgcn_sched_barrier(0);  // not restrict)
 }
 
-// The K loop shared by both GEMMs: acc += A(rows, [q0, q1)) * B(rows w of one matrix).
-// Activations run two chunks ahead of the MFMAs, weights WDEPTH - 1 chunks ahead; a
-// chunk's weight loads for one lane are consecutive 16-byte pieces of its row, issued
-// back to back so each 128-byte line is requested once.
-template <int CHUNK, int PLANES, int TILES, int WDEPTH>
-__device__ __forceinline__ void gemm_loop(const StageThread<CHUNK, PLANES, TILES * kTileRows>& st,
-                                          const uint8_t* wb, const uint8_t* ws, unsigned q0,
-                                          unsigned q1, bool active, unsigned i32, unsigned g,
+// acc[m][t] += A(rows of tile t, steps [q0, q1)) * B(group m of the pair), q0 % 8 == 0.
+// Activations are loaded two chunks ahead of their MFMAs (stored to LDS one chunk ahead),
+// weights one chunk ahead, scale dwords with the first chunk of their 4 steps.  The loop
+// runs whole periods of 8 steps (two scale groups) unrolled, so every ring slot stays in
+// fixed registers (a rotating copy would wait for the loads just issued) and no early exit
+// reaches the loop head with loads outstanding; chunks past the end multiply nothing.
+template <int CHUNK, int PLANES, int TILES>
+__device__ __forceinline__ void gemm_pair(const StageThread<CHUNK, PLANES, TILES * kTileRows>& st,
+                                          const WavePair& w, unsigned q0, unsigned q1,
+                                          bool active, unsigned i32, unsigned h,
                                           uint8_t (&stage)[2][Stage<CHUNK, PLANES>::buffer],
-                                          f32x16 (&acc)[TILES]) {
-    static_assert(WDEPTH == 2 || WDEPTH == 3, "weight ring");
+                                          f32x16 (&acc)[2][TILES]) {
+    static_assert(CHUNK == 1 || CHUNK == 2 || CHUNK == 4, "chunks tile the scale groups");
     using S = Stage<CHUNK, PLANES>;
-    constexpr int ROWS = TILES * kTileRows;
-    auto load_w = [&](unsigned q, WStep(&w)[CHUNK]) {
+    constexpr int ROWS = TILES * kTileRows, PERIOD = 8 / CHUNK;
+    auto load_codes = [&](unsigned q, u32x4(&c)[CHUNK][2]) {
 #pragma unroll
         for (int s = 0; s < CHUNK; ++s)
-            w[s] = load_wstep(wb, ws, min(q + s, q1 - 1), g);
+#pragma unroll
+            for (int m = 0; m < 2; ++m)
+                c[s][m] = load16(w.codes[m] + size_t(min(q + s, q1 - 1)) * 1024);
+    };
+    auto load_scales = [&](unsigned q, unsigned(&sc)[2]) {
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+            sc[m] = w.scales[m][size_t(min(q, q1 - 1) / 4) * 64];
     };
 #pragma unroll
-    for (int m = 0; m < TILES; ++m)
-        acc[m] = f32x16{};
-    StagePieces<CHUNK, PLANES, ROWS> pa, pb;
-    WStep wa[CHUNK], wm[CHUNK], wn[CHUNK];
-    stage_load(st, q0, q1 - 1, pa);
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int t = 0; t < TILES; ++t)
+            acc[m][t] = f32x16{};
+    StagePieces<CHUNK, PLANES, ROWS> xr[2];
+    u32x4 wc[2][CHUNK][2];
+    unsigned sc[2][2];
+    stage_load(st, q0, q1 - 1, xr[0]);
     issue_fence();
-    load_w(q0, wa);
+    load_codes(q0, wc[0]);
+    load_scales(q0, sc[0]);
     issue_fence();
-    stage_load(st, q0 + CHUNK, q1 - 1, pb);
+    stage_load(st, q0 + CHUNK, q1 - 1, xr[1]);
     issue_fence();
-    if constexpr (WDEPTH == 3) {
-        load_w(q0 + CHUNK, wm);
-        issue_fence();
-    }
-    stage_store(st, pa, min(unsigned(CHUNK), q1 - q0), stage[0]);
+    stage_store(st, xr[0], stage[0]);
     __syncthreads();
-    pa = pb;
-    unsigned buf = 0;
-    for (unsigned q = q0; q < q1; q += CHUNK, buf ^= 1) {
-        const unsigned steps = min(unsigned(CHUNK), q1 - q), qn = q + CHUNK;
-        stage_load(st, qn + CHUNK, q1 - 1, pb);
-        issue_fence();
-        if constexpr (WDEPTH == 3)
-            load_w(qn + CHUNK, wn);
-        else
-            load_w(qn, wm);
-        issue_fence();
-        if (active) {
+    const unsigned chunks = (q1 - q0 + CHUNK - 1) / CHUNK;
+    const unsigned periods = (chunks + PERIOD - 1) / PERIOD;
+    for (unsigned p = 0; p < periods; ++p) {
 #pragma unroll
-            for (int s = 0; s < CHUNK; ++s)
-                if (unsigned(s) < steps)
-                    step_mfma<PLANES, TILES>(wa[s], stage[buf], S::pitch, s, i32, g, acc);
-        }
-        if (qn < q1)
-            stage_store(st, pa, min(unsigned(CHUNK), q1 - qn), stage[buf ^ 1]);
-        __syncthreads();
+        for (int u = 0; u < PERIOD; ++u) {
+            const unsigned q = q0 + (p * PERIOD + u) * CHUNK;
+            stage_load(st, q + 2 * CHUNK, q1 - 1, xr[u % 2]);
+            issue_fence();
+            load_codes(q + CHUNK, wc[(u + 1) % 2]);
+            if ((u + 1) * CHUNK % 4 == 0)
+                load_scales(q + CHUNK, sc[((u + 1) * CHUNK / 4) % 2]);
+            issue_fence();
+            if (active) {
+                const unsigned steps = q < q1 ? min(unsigned(CHUNK), q1 - q) : 0u;
 #pragma unroll
-        for (int s = 0; s < CHUNK; ++s) {
-            wa[s] = wm[s];
-            if constexpr (WDEPTH == 3)
-                wm[s] = wn[s];
+                for (int s = 0; s < CHUNK; ++s) {
+                    if (unsigned(s) >= steps)
+                        continue;
+                    const int qs = u * CHUNK + s;  // step within the period
+                    float scale[2];
+#pragma unroll
+                    for (int m = 0; m < 2; ++m)
+                        scale[m] = e8m0((sc[(qs / 4) % 2][m] >> (8 * (qs % 4))) & 0xffu);
+                    const uint8_t* buf = stage[u % 2];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const bf16x8 b0 = dequant8(wc[u % 2][s][0][k], scale[0]);
+                        const bf16x8 b1 = dequant8(wc[u % 2][s][1][k], scale[1]);
+#pragma unroll
+                        for (int t = 0; t < TILES; ++t) {
+                            const uint8_t* rowp = buf + (t * kTileRows + i32) * S::pitch +
+                                                  s * PLANES * 128 + (32 * h + 8 * k) * 2;
+#pragma unroll
+                            for (int pl = 0; pl < PLANES; ++pl) {
+                                const bf16x8 a = lds_bf16x8(rowp + pl * 128);
+                                acc[0][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                                    a, b0, acc[0][t], 0, 0, 0);
+                                acc[1][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                                    a, b1, acc[1][t], 0, 0, 0);
+                            }
+                        }
+                    }
+                }
+            }
+            stage_store(st, xr[(u + 1) % 2], stage[(u + 1) % 2]);  // also past the end
+            __syncthreads();
         }
-        pa = pb;
     }
 }
 
-// gate/up: grid (feature groups of 128, items, K slices).  Wavefront w multiplies the gate
-// (w even) or up (w odd) rows of features n0 + 32 (w / 2) .. +31.  One slice: h =
-// silu(g) * u as bf16 hi + lo (g passes through LDS); more: fp32 partials of g and u
-// (summed by finalize_kernel).
+// Output row of accumulator element v in lane half h of tile t (32x32 MFMA layout).
+__device__ __forceinline__ int acc_row(int t, int v, unsigned h) {
+    return t * kTileRows + 8 * (v / 4) + 4 * int(h) + (v % 4);
+}
+
+// gate/up: grid (groups of 4 feature groups of 32, items, K slices).  Wavefront w
+// multiplies gate and up rows of features 32 (4 x + w) .. +31.  One slice: h = silu(g) * u
+// as bf16 hi + lo; more: fp32 partials of g and u (summed by finalize_kernel).
 __global__ __launch_bounds__(kGemmWaves * 64) void gate_up_kernel(
-    const uint16_t* x, unsigned hidden, unsigned inter, unsigned top_k,
-    const uint8_t* __restrict__ gate_blocks, const uint8_t* __restrict__ gate_scales,
-    const uint8_t* __restrict__ up_blocks, const uint8_t* __restrict__ up_scales,
+    const uint16_t* x, unsigned hidden, unsigned inter, unsigned experts, unsigned top_k,
+    const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up,
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ perm,
     const int32_t* __restrict__ items, const int32_t* __restrict__ item_count,
     uint16_t* __restrict__ h_hi, uint16_t* __restrict__ h_lo, float* __restrict__ part_g,
     float* __restrict__ part_u, size_t part_stride) {
     constexpr int CHUNK = 2;
-    using S = Stage<CHUNK, 1>;
-    static_assert(2 * S::buffer >= (kGemmWaves / 2) * kTiles * 16 * 64 * 4, "gate exchange");
-    __shared__ __align__(16) uint8_t stage[2][S::buffer];
+    __shared__ __align__(16) uint8_t stage[2][Stage<CHUNK, 1>::buffer];
     __shared__ long long src[kItemRows];
     if (int(blockIdx.y) >= *item_count)
         return;
     const Item it = load_item(items, offsets, blockIdx.y);
     const unsigned wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-    const unsigned i32 = lane % 32, g = lane / 32;
-    const unsigned mat = wave % 2, tile = wave / 2;
-    const unsigned f0 = blockIdx.x * (kGemmWaves / 2) * 32 + tile * 32;
-    const bool active = f0 < inter;  // uniform per wavefront
-    const unsigned f = active ? f0 + i32 : i32;
+    const unsigned i32 = lane % 32, h = lane / 32;
+    const Packed shape = packed_shape(1, inter, hidden);  // per expert
+    const unsigned fg = blockIdx.x * kGemmWaves + wave;   // feature group of 32
+    const bool active = fg < shape.groups;                // uniform per wavefront
+    const unsigned f = (active ? fg : 0) * 32 + i32;
     unsigned q0, q1;
-    slice_steps(hidden / kStepK, gridDim.z, blockIdx.z, q0, q1);
+    slice_steps(unsigned(shape.steps), gridDim.z, blockIdx.z, q0, q1);
     if (q0 >= q1)
         return;
     if (threadIdx.x < kItemRows) {
@@ -467,55 +545,47 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gate_up_kernel(
                               : -1;
     }
     __syncthreads();
-    const size_t wrow = size_t(it.expert) * inter + f;
-    const uint8_t* wb = (mat ? up_blocks : gate_blocks) + wrow * (hidden / 2);
-    const uint8_t* ws = (mat ? up_scales : gate_scales) + wrow * (hidden / 32);
-    const uint16_t* planes[1] = {x};
+    const Packed whole = packed_shape(experts, inter, hidden);
+    const size_t group = size_t(it.expert) * shape.groups + (active ? fg : 0);
+    WavePair wg = wave_pair(gate, whole, group, group, lane);
+    const WavePair wu = wave_pair(up, whole, group, group, lane);
+    wg.codes[1] = wu.codes[0];
+    wg.scales[1] = wu.scales[0];
 
     // straight-line code per tile count: no accumulator moves between control paths
     auto run = [&]<int TILES>() {
         const auto st = stage_thread<CHUNK, 1, TILES * kTileRows>(
-            planes, [&](unsigned, unsigned r) { return src[r]; });
-        f32x16 acc[TILES];
-        gemm_loop<CHUNK, 1, TILES, 3>(st, wb, ws, q0, q1, active, i32, g, stage, acc);
+            x, 0, [&](unsigned r) { return src[r]; });
+        f32x16 acc[2][TILES];
+        gemm_pair<CHUNK, 1, TILES>(st, wg, q0, q1, active, i32, h, stage, acc);
+        if (!active)
+            return;
         if (gridDim.z > 1) {
-            if (!active)
-                return;
-            float* part = (mat ? part_u : part_g) + blockIdx.z * part_stride;
 #pragma unroll
-            for (int m = 0; m < TILES; ++m)
+            for (int t = 0; t < TILES; ++t)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
-                    const int r = m * kTileRows + 8 * (v / 4) + 4 * int(g) + (v % 4);
-                    if (r < it.count)
-                        part[size_t(it.segment + it.first + r) * inter + f] = acc[m][v];
+                    const int r = acc_row(t, v, h);
+                    if (r < it.count) {
+                        const size_t at = blockIdx.z * part_stride +
+                                          size_t(it.segment + it.first + r) * inter + f;
+                        part_g[at] = acc[0][t][v];
+                        part_u[at] = acc[1][t][v];
+                    }
                 }
             return;
         }
-        // the gate values of feature tile `tile` pass to its up wavefront through LDS (the
-        // stage buffers are free after the last barrier): xg[tile][m][v][lane]
-        float* xg = reinterpret_cast<float*>(&stage[0][0]);
-        if (mat == 0 && active)
 #pragma unroll
-            for (int m = 0; m < TILES; ++m)
-#pragma unroll
-                for (int v = 0; v < 16; ++v)
-                    xg[((tile * kTiles + m) * 16 + v) * 64 + lane] = acc[m][v];
-        __syncthreads();
-        if (mat == 0 || !active)
-            return;
-#pragma unroll
-        for (int m = 0; m < TILES; ++m)
+        for (int t = 0; t < TILES; ++t)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const int r = m * kTileRows + 8 * (v / 4) + 4 * int(g) + (v % 4);
+                const int r = acc_row(t, v, h);
                 if (r < it.count) {
-                    const float gv = xg[((tile * kTiles + m) * 16 + v) * 64 + lane];
-                    const float h = silu(gv) * acc[m][v];
-                    const uint16_t hi = bf16_rne(h);
+                    const float hv = silu(acc[0][t][v]) * acc[1][t][v];
+                    const uint16_t hi = bf16_rne(hv);
                     const size_t at = size_t(it.segment + it.first + r) * inter + f;
                     h_hi[at] = hi;
-                    h_lo[at] = bf16_rne(h - bf16_value(hi));
+                    h_lo[at] = bf16_rne(hv - bf16_value(hi));
                 }
             }
     };
@@ -539,55 +609,60 @@ __global__ __launch_bounds__(256) void finalize_kernel(const float* __restrict__
         gs += part_g[s * count + i];
         us += part_u[s * count + i];
     }
-    const float h = silu(gs) * us;
-    const uint16_t hi = bf16_rne(h);
+    const float hv = silu(gs) * us;
+    const uint16_t hi = bf16_rne(hv);
     h_hi[i] = hi;
-    h_lo[i] = bf16_rne(h - bf16_value(hi));
+    h_lo[i] = bf16_rne(hv - bf16_value(hi));
 }
 
-// down: grid (feature groups of 256, items, K slices); fp32 partial sums of h x down
-// (hi and lo planes) per slice, indexed by the slot's position in the permutation.
+// down: grid (groups of 4 row pairs of 64, items, K slices); wavefront w multiplies the
+// down rows 64 (4 x + w) .. +63 (two groups of 32).  fp32 partial sums of h x down (hi
+// plane at h, lo plane at h + plane_stride) per slice, indexed by the slot's position in
+// the permutation.
 __global__ __launch_bounds__(kGemmWaves * 64) void down_kernel(
-    const uint16_t* h_hi, const uint16_t* h_lo, unsigned hidden, unsigned inter,
-    const uint8_t* __restrict__ down_blocks, const uint8_t* __restrict__ down_scales,
-    const int32_t* __restrict__ offsets, const int32_t* __restrict__ items,
-    const int32_t* __restrict__ item_count, float* __restrict__ part_d, size_t part_stride) {
+    const uint16_t* hp, size_t plane_stride, unsigned hidden, unsigned inter, unsigned experts,
+    const uint8_t* __restrict__ down, const int32_t* __restrict__ offsets,
+    const int32_t* __restrict__ items, const int32_t* __restrict__ item_count,
+    float* __restrict__ part_d, size_t part_stride) {
     constexpr int CHUNK = 1;
     __shared__ __align__(16) uint8_t stage[2][Stage<CHUNK, 2>::buffer];
     if (int(blockIdx.y) >= *item_count)
         return;
     const Item it = load_item(items, offsets, blockIdx.y);
     const unsigned wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-    const unsigned i32 = lane % 32, g = lane / 32;
-    const unsigned d0 = (blockIdx.x * kGemmWaves + wave) * 32;
-    const bool active = d0 < hidden;
-    const unsigned d = active ? d0 + i32 : i32;
+    const unsigned i32 = lane % 32, h = lane / 32;
+    const Packed shape = packed_shape(1, hidden, inter);  // per expert
+    const unsigned pair = blockIdx.x * kGemmWaves + wave;
+    const bool active = pair < shape.groups / 2;
+    const unsigned g0 = (active ? pair : 0) * 2;
     unsigned q0, q1;
-    slice_steps(inter / kStepK, gridDim.z, blockIdx.z, q0, q1);
+    slice_steps(unsigned(shape.steps), gridDim.z, blockIdx.z, q0, q1);
     if (q0 >= q1)
         return;
-    const size_t wrow = size_t(it.expert) * hidden + d;
-    const uint8_t* db = down_blocks + wrow * (inter / 2);
-    const uint8_t* ds = down_scales + wrow * (inter / 32);
-    const uint16_t* planes[2] = {h_hi, h_lo};
-    auto row_offset = [&](unsigned, unsigned r) {
+    const Packed whole = packed_shape(experts, hidden, inter);
+    const size_t base = size_t(it.expert) * shape.groups + g0;
+    const WavePair w = wave_pair(down, whole, base, base + 1, lane);
+    auto row_offset = [&](unsigned r) {
         return r < unsigned(it.count) ? (long long)(it.segment + it.first + r) * inter : -1ll;
     };
     auto run = [&]<int TILES>() {
-        const auto st = stage_thread<CHUNK, 2, TILES * kTileRows>(planes, row_offset);
-        f32x16 acc[TILES];
-        gemm_loop<CHUNK, 2, TILES, 3>(st, db, ds, q0, q1, active, i32, g, stage, acc);
+        const auto st = stage_thread<CHUNK, 2, TILES * kTileRows>(hp, plane_stride, row_offset);
+        f32x16 acc[2][TILES];
+        gemm_pair<CHUNK, 2, TILES>(st, w, q0, q1, active, i32, h, stage, acc);
         if (!active)
             return;
 #pragma unroll
-        for (int m = 0; m < TILES; ++m)
+        for (int m = 0; m < 2; ++m)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int r = m * kTileRows + 8 * (v / 4) + 4 * int(g) + (v % 4);
-                if (r < it.count)
-                    part_d[blockIdx.z * part_stride +
-                           size_t(it.segment + it.first + r) * hidden + d] = acc[m][v];
-            }
+            for (int t = 0; t < TILES; ++t)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int r = acc_row(t, v, h);
+                    if (r < it.count)
+                        part_d[blockIdx.z * part_stride +
+                               size_t(it.segment + it.first + r) * hidden + (g0 + m) * 32 + i32] =
+                            acc[m][t][v];
+                }
     };
     if (it.count <= kTileRows)
         run.template operator()<1>();
@@ -595,27 +670,46 @@ __global__ __launch_bounds__(kGemmWaves * 64) void down_kernel(
         run.template operator()<2>();
 }
 
-// y[t, d] = sum_i w[t k + i] * (sum_s part_d[s, position(t k + i), d]), in selection order.
+// y[t, d] = sum_i w[t k + i] * (sum_s part_d[s, position(t k + i), d]), in selection order;
+// one thread per 4 consecutive d.  Every load is issued before the sums (slot indices past
+// top_k are clamped and their terms dropped), so the partials arrive together.
+template <int SLICES>
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ part_d,
                                                       size_t part_stride, unsigned slices,
                                                       const int32_t* __restrict__ position,
                                                       const float* __restrict__ weight,
                                                       unsigned tokens, unsigned hidden,
                                                       unsigned top_k, float* __restrict__ y) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
     const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= size_t(tokens) * hidden)
+    const unsigned quads = hidden / 4;
+    if (i >= size_t(tokens) * quads)
         return;
-    const size_t t = i / hidden, d = i % hidden;
-    float sum = 0.f;
-    for (unsigned k = 0; k < top_k; ++k) {
-        const size_t slot = t * top_k + k;
-        const size_t at = size_t(position[slot]) * hidden + d;
-        float down = 0.f;
-        for (unsigned s = 0; s < slices; ++s)
-            down += part_d[s * part_stride + at];
-        sum += down * weight[slot];
+    const size_t t = i / quads, d = (i % quads) * 4;
+    int pos[kMaxTopK];
+    float wk[kMaxTopK];
+#pragma unroll
+    for (unsigned k = 0; k < kMaxTopK; ++k) {
+        const size_t slot = t * top_k + min(k, top_k - 1);
+        pos[k] = position[slot];
+        wk[k] = weight[slot];
     }
-    y[i] = sum;
+    const unsigned ns = SLICES ? unsigned(SLICES) : slices;
+    f32x4 down[kMaxTopK];
+#pragma unroll
+    for (unsigned k = 0; k < kMaxTopK; ++k)
+        down[k] = *reinterpret_cast<const f32x4*>(part_d + size_t(pos[k]) * hidden + d);
+    for (unsigned s = 1; s < ns; ++s)
+#pragma unroll
+        for (unsigned k = 0; k < kMaxTopK; ++k)
+            down[k] += *reinterpret_cast<const f32x4*>(part_d + s * part_stride +
+                                                       size_t(pos[k]) * hidden + d);
+    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (unsigned k = 0; k < kMaxTopK; ++k)
+        if (k < top_k)
+            sum += down[k] * wk[k];
+    *reinterpret_cast<f32x4*>(y + t * hidden + d) = sum;
 }
 
 __global__ __launch_bounds__(256) void mxfp4_dequant_kernel(const uint8_t* __restrict__ blocks,
@@ -657,8 +751,19 @@ struct MoeScratch {
     float *part_g, *part_u, *part_d;
 };
 
-// K slices of the grouped GEMMs: enough workgroups for about two per compute unit when
-// the items are few (decode), one slice otherwise; no slice is empty.
+// Grid columns of the grouped GEMMs: kGemmWaves feature groups of 32 (gate/up) or row
+// pairs of 64 (down) per workgroup.
+unsigned gate_up_columns(size_t inter) {
+    return unsigned((inter / 32 + kGemmWaves - 1) / kGemmWaves);
+}
+
+unsigned down_columns(size_t hidden) {
+    return unsigned((hidden / 64 + kGemmWaves - 1) / kGemmWaves);
+}
+
+// K slices of the grouped GEMMs: enough workgroups for about two per compute unit (two
+// fit at once) when the items are few (decode), one slice otherwise; slices are whole
+// multiples of 8 steps and none is empty.
 struct MoeSlices {
     unsigned gate_up, down;
 };
@@ -667,14 +772,14 @@ MoeSlices moe_slices(size_t tokens, size_t hidden, size_t inter, size_t experts,
                      size_t top_k) {
     const size_t items = std::min(tokens * top_k, experts);  // at least this many
     const size_t target = 2 * size_t(compute_units());
-    auto slices = [&](size_t groups, size_t steps) {
-        size_t ks = std::max<size_t>(1, (target + groups * items - 1) / (groups * items));
+    auto slices = [&](size_t columns, size_t steps) {
+        size_t ks = std::max<size_t>(1, (target + columns * items - 1) / (columns * items));
         ks = std::min(ks, steps);
-        const size_t per = (steps + ks - 1) / ks;
+        const size_t per = ((steps + ks - 1) / ks + 7) / 8 * 8;
         return unsigned((steps + per - 1) / per);
     };
-    return MoeSlices{slices((inter / 32 + kGemmWaves / 2 - 1) / (kGemmWaves / 2), hidden / kStepK),
-                     slices((hidden / 32 + kGemmWaves - 1) / kGemmWaves, inter / kStepK)};
+    return MoeSlices{slices(gate_up_columns(inter), hidden / kStepK),
+                     slices(down_columns(hidden), inter / kStepK)};
 }
 
 size_t align256(size_t n) {
@@ -715,6 +820,41 @@ MoeScratch carve(uint8_t* p, size_t tokens, size_t hidden, size_t inter, size_t 
     }
     s.part_d = reinterpret_cast<float*>(take(ks.down * slots * hidden * 4));
     return s;
+}
+
+size_t packed_bytes(size_t experts, size_t rows, size_t cols) {
+    const Packed p = packed_shape(experts, rows, cols);
+    return p.code_bytes + p.scale_bytes;
+}
+
+int launch_pack(const uint8_t* blocks, const uint8_t* scales, size_t experts, size_t rows,
+                size_t cols, uint8_t* packed, hipStream_t stream) {
+    const Packed p = packed_shape(experts, rows, cols);
+    const size_t units = p.code_bytes / 16, words = p.scale_bytes / 4;
+    hipLaunchKernelGGL(pack_codes_kernel, dim3(unsigned((units + 255) / 256)), dim3(256), 0,
+                       stream, blocks, units, p.steps, cols, packed);
+    KDQ_HIP(hipGetLastError());
+    hipLaunchKernelGGL(pack_scales_kernel, dim3(unsigned((words + 255) / 256)), dim3(256), 0,
+                       stream, scales, words, p.scale_groups, p.steps, cols,
+                       reinterpret_cast<unsigned*>(packed + p.code_bytes));
+    KDQ_HIP(hipGetLastError());
+    return KDQ_OK;
+}
+
+int check_pack(const uint8_t* blocks, const uint8_t* scales, size_t experts, size_t rows,
+               size_t cols, const uint8_t* packed) {
+    if (!blocks || !scales || !packed || !experts || !rows || !cols)
+        return KDQ_ERR_ARGUMENT;
+    if (rows % 32 || cols % 64 || experts > kMaxExperts || rows > (1u << 20) ||
+        cols > (1u << 20))
+        return KDQ_ERR_SHAPE;
+    if (misaligned(blocks, 16) || misaligned(packed, 256))
+        return KDQ_ERR_ALIGNMENT;
+    const size_t bytes = packed_bytes(experts, rows, cols);
+    if (overlaps(packed, bytes, blocks, experts * rows * cols / 2) ||
+        overlaps(packed, bytes, scales, experts * rows * cols / 32))
+        return KDQ_ERR_ALIAS;
+    return KDQ_OK;
 }
 
 int check_route(const float* logits, size_t tokens, size_t experts, size_t top_k) {
@@ -774,30 +914,33 @@ extern "C" int kdq_mxfp4_dequantize(const uint8_t* blocks, const uint8_t* scales
     return KDQ_OK;
 }
 
-extern "C" int kdq_moe_mxfp4(const uint16_t* x_bf16, const float* logits, size_t tokens,
-                             size_t hidden, size_t inter, size_t experts, size_t top_k,
-                             const uint8_t* gate_blocks, const uint8_t* gate_scales,
-                             const uint8_t* up_blocks, const uint8_t* up_scales,
-                             const uint8_t* down_blocks, const uint8_t* down_scales, float* y,
-                             int32_t* idx, float* w, int32_t* offsets, int32_t* perm,
-                             void* stream) {
+namespace kdq {
+namespace {
+
+int check_layer(const uint16_t* x_bf16, const float* logits, size_t tokens, size_t hidden,
+                size_t inter, size_t experts, size_t top_k, float* y) {
     int rc = check_route(logits, tokens, experts, top_k);
     if (rc)
         return rc;
-    if (!x_bf16 || !y || !gate_blocks || !gate_scales || !up_blocks || !up_scales ||
-        !down_blocks || !down_scales || !hidden || !inter)
+    if (!x_bf16 || !y || !hidden || !inter)
         return KDQ_ERR_ARGUMENT;
     if (hidden % 64 || inter % 64 || hidden > (1u << 20) || inter > (1u << 20))
         return KDQ_ERR_SHAPE;
+    if (misaligned(x_bf16, 16) || misaligned(y, 16))
+        return KDQ_ERR_ALIGNMENT;
     if (overlaps(y, tokens * hidden * 4, x_bf16, tokens * hidden * 2) ||
         overlaps(y, tokens * hidden * 4, logits, tokens * experts * 4))
         return KDQ_ERR_ALIAS;
-    const MoeSlices ks = moe_slices(tokens, hidden, inter, experts, top_k);
-    const size_t bytes = moe_scratch_bytes(tokens, hidden, inter, experts, top_k, ks);
-    auto* base = static_cast<uint8_t*>(workspace(bytes, &rc));
-    if (rc)
-        return rc;
-    MoeScratch s = carve(base, tokens, hidden, inter, experts, top_k, ks);
+    return KDQ_OK;
+}
+
+// The layer over packed weights; `scratch` holds moe_scratch_bytes(...).
+int launch_layer(const uint16_t* x_bf16, const float* logits, size_t tokens, size_t hidden,
+                 size_t inter, size_t experts, size_t top_k, const uint8_t* gate,
+                 const uint8_t* up, const uint8_t* down, float* y, int32_t* idx, float* w,
+                 int32_t* offsets, int32_t* perm, uint8_t* scratch, MoeSlices ks,
+                 hipStream_t st) {
+    MoeScratch s = carve(scratch, tokens, hidden, inter, experts, top_k, ks);
     if (idx)
         s.idx = idx;
     if (w)
@@ -806,20 +949,16 @@ extern "C" int kdq_moe_mxfp4(const uint16_t* x_bf16, const float* logits, size_t
         s.offsets = offsets;
     if (perm)
         s.perm = perm;
-    auto st = static_cast<hipStream_t>(stream);
-    rc = launch_route(logits, tokens, experts, top_k, s.idx, s.weight, s.offsets, s.perm,
-                      s.items, s.item_count, s.position, st);
+    int rc = launch_route(logits, tokens, experts, top_k, s.idx, s.weight, s.offsets, s.perm,
+                          s.items, s.item_count, s.position, st);
     if (rc)
         return rc;
     const size_t slots = tokens * top_k;
     const unsigned max_items = unsigned(std::min(slots, slots / kItemRows + experts + 1));
-    const unsigned groups_gu = unsigned((inter / 32 + kGemmWaves / 2 - 1) / (kGemmWaves / 2));
-    const unsigned groups_d = unsigned((hidden / 32 + kGemmWaves - 1) / kGemmWaves);
-    hipLaunchKernelGGL(gate_up_kernel, dim3(groups_gu, max_items, ks.gate_up),
+    hipLaunchKernelGGL(gate_up_kernel, dim3(gate_up_columns(inter), max_items, ks.gate_up),
                        dim3(kGemmWaves * 64), 0, st, x_bf16, unsigned(hidden), unsigned(inter),
-                       unsigned(top_k), gate_blocks, gate_scales, up_blocks, up_scales,
-                       s.offsets, s.perm, s.items, s.item_count, s.h_hi, s.h_lo, s.part_g,
-                       s.part_u, slots * inter);
+                       unsigned(experts), unsigned(top_k), gate, up, s.offsets, s.perm, s.items, s.item_count,
+                       s.h_hi, s.h_lo, s.part_g, s.part_u, slots * inter);
     KDQ_HIP(hipGetLastError());
     if (ks.gate_up > 1) {
         const size_t n = slots * inter;
@@ -827,15 +966,98 @@ extern "C" int kdq_moe_mxfp4(const uint16_t* x_bf16, const float* logits, size_t
                            s.part_g, s.part_u, n, ks.gate_up, s.h_hi, s.h_lo);
         KDQ_HIP(hipGetLastError());
     }
-    hipLaunchKernelGGL(down_kernel, dim3(groups_d, max_items, ks.down), dim3(kGemmWaves * 64),
-                       0, st, s.h_hi, s.h_lo, unsigned(hidden), unsigned(inter), down_blocks,
-                       down_scales, s.offsets, s.items, s.item_count, s.part_d,
-                       slots * hidden);
+    hipLaunchKernelGGL(down_kernel, dim3(down_columns(hidden), max_items, ks.down),
+                       dim3(kGemmWaves * 64), 0, st, s.h_hi, size_t(s.h_lo - s.h_hi),
+                       unsigned(hidden), unsigned(inter), unsigned(experts), down, s.offsets,
+                       s.items, s.item_count, s.part_d, slots * hidden);
     KDQ_HIP(hipGetLastError());
-    const size_t n = tokens * hidden;
-    hipLaunchKernelGGL(combine_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st,
-                       s.part_d, slots * hidden, ks.down, s.position, s.weight,
-                       unsigned(tokens), unsigned(hidden), unsigned(top_k), y);
+    const size_t n = tokens * hidden / 4;
+    const dim3 grid(unsigned((n + 255) / 256));
+    const size_t stride = slots * hidden;
+    if (ks.down == 1)
+        hipLaunchKernelGGL(combine_kernel<1>, grid, dim3(256), 0, st, s.part_d, stride, 1u,
+                           s.position, s.weight, unsigned(tokens), unsigned(hidden),
+                           unsigned(top_k), y);
+    else if (ks.down == 2)
+        hipLaunchKernelGGL(combine_kernel<2>, grid, dim3(256), 0, st, s.part_d, stride, 2u,
+                           s.position, s.weight, unsigned(tokens), unsigned(hidden),
+                           unsigned(top_k), y);
+    else
+        hipLaunchKernelGGL(combine_kernel<0>, grid, dim3(256), 0, st, s.part_d, stride, ks.down,
+                           s.position, s.weight, unsigned(tokens), unsigned(hidden),
+                           unsigned(top_k), y);
     KDQ_HIP(hipGetLastError());
     return KDQ_OK;
+}
+
+}  // namespace
+}  // namespace kdq
+
+extern "C" size_t kdq_moe_mxfp4_packed_bytes(size_t experts, size_t rows, size_t cols) {
+    if (!experts || !rows || !cols || rows % 32 || cols % 64)
+        return 0;
+    return packed_bytes(experts, rows, cols);
+}
+
+extern "C" int kdq_moe_mxfp4_pack(const uint8_t* blocks, const uint8_t* scales, size_t experts,
+                                  size_t rows, size_t cols, uint8_t* packed, void* stream) {
+    const int rc = check_pack(blocks, scales, experts, rows, cols, packed);
+    if (rc)
+        return rc;
+    return launch_pack(blocks, scales, experts, rows, cols, packed,
+                       static_cast<hipStream_t>(stream));
+}
+
+extern "C" int kdq_moe_mxfp4_packed(const uint16_t* x_bf16, const float* logits, size_t tokens,
+                                    size_t hidden, size_t inter, size_t experts, size_t top_k,
+                                    const uint8_t* gate, const uint8_t* up, const uint8_t* down,
+                                    float* y, int32_t* idx, float* w, int32_t* offsets,
+                                    int32_t* perm, void* stream) {
+    int rc = check_layer(x_bf16, logits, tokens, hidden, inter, experts, top_k, y);
+    if (rc)
+        return rc;
+    if (!gate || !up || !down)
+        return KDQ_ERR_ARGUMENT;
+    if (misaligned(gate, 256) || misaligned(up, 256) || misaligned(down, 256))
+        return KDQ_ERR_ALIGNMENT;
+    const MoeSlices ks = moe_slices(tokens, hidden, inter, experts, top_k);
+    auto* scratch = static_cast<uint8_t*>(
+        workspace(moe_scratch_bytes(tokens, hidden, inter, experts, top_k, ks), &rc));
+    if (rc)
+        return rc;
+    return launch_layer(x_bf16, logits, tokens, hidden, inter, experts, top_k, gate, up, down,
+                        y, idx, w, offsets, perm, scratch, ks, static_cast<hipStream_t>(stream));
+}
+
+// Reference-layout weights: packed into the workspace on every call, then the layer.
+extern "C" int kdq_moe_mxfp4(const uint16_t* x_bf16, const float* logits, size_t tokens,
+                             size_t hidden, size_t inter, size_t experts, size_t top_k,
+                             const uint8_t* gate_blocks, const uint8_t* gate_scales,
+                             const uint8_t* up_blocks, const uint8_t* up_scales,
+                             const uint8_t* down_blocks, const uint8_t* down_scales, float* y,
+                             int32_t* idx, float* w, int32_t* offsets, int32_t* perm,
+                             void* stream) {
+    int rc = check_layer(x_bf16, logits, tokens, hidden, inter, experts, top_k, y);
+    if (rc)
+        return rc;
+    if (!gate_blocks || !gate_scales || !up_blocks || !up_scales || !down_blocks ||
+        !down_scales)
+        return KDQ_ERR_ARGUMENT;
+    if (misaligned(gate_blocks, 16) || misaligned(up_blocks, 16) || misaligned(down_blocks, 16))
+        return KDQ_ERR_ALIGNMENT;
+    const size_t gu = align256(packed_bytes(experts, inter, hidden));
+    const size_t dn = align256(packed_bytes(experts, hidden, inter));
+    const MoeSlices ks = moe_slices(tokens, hidden, inter, experts, top_k);
+    auto* base = static_cast<uint8_t*>(
+        workspace(2 * gu + dn + moe_scratch_bytes(tokens, hidden, inter, experts, top_k, ks), &rc));
+    if (rc)
+        return rc;
+    auto st = static_cast<hipStream_t>(stream);
+    uint8_t *gate = base, *up = base + gu, *down = base + 2 * gu;
+    if ((rc = launch_pack(gate_blocks, gate_scales, experts, inter, hidden, gate, st)) ||
+        (rc = launch_pack(up_blocks, up_scales, experts, inter, hidden, up, st)) ||
+        (rc = launch_pack(down_blocks, down_scales, experts, hidden, inter, down, st)))
+        return rc;
+    return launch_layer(x_bf16, logits, tokens, hidden, inter, experts, top_k, gate, up, down,
+                        y, idx, w, offsets, perm, base + 2 * gu + dn, ks, st);
 }

@@ -147,5 +147,45 @@ def moe_mxfp4(x_bf16: torch.Tensor, logits: torch.Tensor, top_k: int, gate_block
     return (out, *extra) if routing else out
 
 
+def moe_mxfp4_pack(blocks: torch.Tensor, scales: torch.Tensor, experts: int, rows: int,
+                   cols: int) -> torch.Tensor:
+    """One projection tensor in the packed resident layout (kdq_moe_mxfp4_pack)."""
+    _need(blocks, torch.uint8, "blocks")
+    _need(scales, torch.uint8, "scales")
+    n = lib().kdq_moe_mxfp4_packed_bytes(experts, rows, cols)
+    if not n:
+        raise ValueError("rows % 32 and cols % 64 must be 0")
+    packed = torch.empty(n, dtype=torch.uint8, device=blocks.device)
+    call("kdq_moe_mxfp4_pack", blocks.data_ptr(), scales.data_ptr(), experts, rows, cols,
+         packed.data_ptr(), _stream())
+    return packed
+
+
+def moe_mxfp4_packed(x_bf16: torch.Tensor, logits: torch.Tensor, top_k: int, inter: int,
+                     gate: torch.Tensor, up: torch.Tensor, down: torch.Tensor,
+                     routing: bool = False, out: torch.Tensor | None = None):
+    """kdq_moe_mxfp4_packed: the layer over packed weights (moe_mxfp4_pack)."""
+    _need(x_bf16, torch.bfloat16, "x")
+    _need(logits, torch.float32, "logits")
+    t, h = x_bf16.shape
+    e = logits.shape[1]
+    dev = x_bf16.device
+    for name, a in (("gate", gate), ("up", up), ("down", down)):
+        _need(a, torch.uint8, name)
+    if out is None:
+        out = torch.empty(t, h, dtype=torch.float32, device=dev)
+    extra = [None] * 4
+    if routing:
+        extra = [torch.empty(t, top_k, dtype=torch.int32, device=dev),
+                 torch.empty(t, top_k, dtype=torch.float32, device=dev),
+                 torch.empty(e + 1, dtype=torch.int32, device=dev),
+                 torch.empty(t * top_k, dtype=torch.int32, device=dev)]
+    call("kdq_moe_mxfp4_packed", x_bf16.data_ptr(), logits.data_ptr(), t, h, inter, e, top_k,
+         gate.data_ptr(), up.data_ptr(), down.data_ptr(), out.data_ptr(),
+         *[_ptr(a) for a in extra], _stream())
+    return (out, *extra) if routing else out
+
+
 __all__ = ["dequantize", "gemv", "gemv_batch", "quantize_q8", "gemm_q4_0", "moe_route",
-           "mxfp4_dequantize", "moe_mxfp4", "lib", "BLOCK_BYTES", "BLOCK_VALUES"]
+           "mxfp4_dequantize", "moe_mxfp4", "moe_mxfp4_pack", "moe_mxfp4_packed", "lib",
+           "BLOCK_BYTES", "BLOCK_VALUES"]

@@ -19,7 +19,8 @@ def declared_functions():
 def test_header_declares_entry_points():
     names = declared_functions()
     for expected in ["kdq_dequantize", "kdq_gemv", "kdq_gemv_batch", "kdq_gemm_q4_0",
-                     "kdq_moe_route", "kdq_moe_mxfp4", "kdq_mxfp4_dequantize"]:
+                     "kdq_moe_route", "kdq_moe_mxfp4", "kdq_mxfp4_dequantize",
+                     "kdq_moe_mxfp4_pack", "kdq_moe_mxfp4_packed", "kdq_moe_mxfp4_packed_bytes"]:
         assert expected in names
 
 
@@ -95,6 +96,22 @@ def test_dequantize_argument_errors():
     assert lib.kdq_dequantize(12, FAKE_W, 144, 1, 200, FAKE_Y, None, None) == 2
     assert lib.kdq_dequantize(12, FAKE_W, 144, 1, 256, FAKE_Y + 4, None, None) == 7
     assert lib.kdq_dequantize(12, FAKE_W, 144, 1, 256, FAKE_W, None, None) == 4
+
+
+def test_moe_packed_geometry_and_argument_errors():
+    import kadan_amd
+    lib = kadan_amd.lib()
+    # 32 experts x 2880 x 2880: codes E*R*C/2, scales E * R/32 * ceil(45/4) * 256
+    assert lib.kdq_moe_mxfp4_packed_bytes(32, 2880, 2880) == 32 * 2880 * 1440 + 32 * 90 * 12 * 256
+    assert lib.kdq_moe_mxfp4_packed_bytes(1, 32, 64) == 1024 + 256
+    assert lib.kdq_moe_mxfp4_packed_bytes(1, 48, 64) == 0
+    assert lib.kdq_moe_mxfp4_packed_bytes(1, 32, 96) == 0
+    pack = lib.kdq_moe_mxfp4_pack
+    assert pack(FAKE_W, FAKE_W + 65536, 1, 48, 64, FAKE_Y, None) == 2
+    assert pack(FAKE_W, FAKE_W + 65536, 1, 32, 64, FAKE_Y + 16, None) == 7
+    assert pack(FAKE_W + 4, FAKE_W + 65536, 1, 32, 64, FAKE_Y, None) == 7
+    assert pack(FAKE_W, FAKE_W + 65536, 1, 32, 64, FAKE_W + 256, None) == 4
+    assert pack(None, FAKE_W, 1, 32, 64, FAKE_Y, None) == 1
 
 
 def test_product_path_has_no_cpu_fallback(monkeypatch, tmp_path):

@@ -138,3 +138,81 @@ def test_moe_prefill_256_properties(device):
     assert np.array_equal(y1, y2)
     yr = ops.moe_mxfp4(dev(x[::-1]).view(torch.bfloat16), dev(logits[::-1]), 4, *wts)
     assert_close(yr.cpu().numpy()[::-1], y1, rel=1e-6, mabs=1e-5, what="token order")
+
+
+def unpack_reference(packed, experts, rows, cols):
+    """The GPT-OSS layout back from the packed one (the layout as include/kadan_amd.h states
+    it): codes [E][R/32][C/64][lane i + 32h][16 B], scales [E][R/32][ceil(C/256)][lane][4 B]."""
+    groups, steps = rows // 32, cols // 64
+    sgroups = (steps + 3) // 4
+    code_bytes = experts * rows * cols // 2
+    codes = packed[:code_bytes].reshape(experts, groups, steps, 2, 32, 16)
+    blocks = codes.transpose(0, 1, 4, 2, 3, 5).reshape(experts, rows, cols // 2)
+    sc = packed[code_bytes:].reshape(experts, groups, sgroups, 2, 32, 4)
+    sc = sc.transpose(0, 1, 4, 2, 5, 3).reshape(experts, rows, sgroups * 4 * 2)
+    return blocks, sc[:, :, :cols // 32], sc[:, :, cols // 32:]
+
+
+@pytest.mark.parametrize("experts,rows,cols", [(3, 64, 2880), (2, 96, 192), (1, 32, 256)])
+def test_moe_pack_layout(device, experts, rows, cols):
+    """kdq_moe_mxfp4_pack moves every code and scale byte to its stated place and zero-fills
+    the scale slots past the last step."""
+    torch = _torch()
+    blocks = synth.random_bytes(7, 1, experts * rows * cols // 2).reshape(experts, rows, -1)
+    scales = synth.random_bytes(7, 2, experts * rows * cols // 32).reshape(experts, rows, -1)
+    from kadan_amd import ops
+    packed = ops.moe_mxfp4_pack(torch.from_numpy(blocks).to(device),
+                                torch.from_numpy(scales).to(device), experts, rows, cols)
+    packed = packed.cpu().numpy()
+    import kadan_amd
+    assert packed.size == kadan_amd.lib().kdq_moe_mxfp4_packed_bytes(experts, rows, cols)
+    b, s, pad = unpack_reference(packed, experts, rows, cols)
+    assert np.array_equal(b, blocks)
+    assert np.array_equal(s, scales)
+    assert not pad.any()
+
+
+@pytest.mark.parametrize("tokens,hidden,inter,experts,top_k", [
+    (1, 2880, 2880, 32, 4), (256, 2880, 2880, 32, 4), (37, 256, 192, 8, 4), (1, 64, 64, 4, 2),
+])
+def test_moe_packed_matches_reference_layout(device, tokens, hidden, inter, experts, top_k):
+    """The packed entry point over resident packed weights gives the reference-layout
+    entry point's output and routing bit for bit."""
+    torch = _torch()
+    x, logits = synth.moe_inputs(0xAB + tokens, tokens, hidden, experts)
+    (gb, gs), (ub, us), (db, ds) = synth.moe_weights(0xAB, experts, hidden, inter)
+    from kadan_amd import ops
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)
+    wts = [dev(a) for a in (gb, gs, ub, us, db, ds)]
+    xb, lg = dev(x).view(torch.bfloat16), dev(logits)
+    ref = ops.moe_mxfp4(xb, lg, top_k, *wts, routing=True)
+    packed = [ops.moe_mxfp4_pack(wts[0], wts[1], experts, inter, hidden),
+              ops.moe_mxfp4_pack(wts[2], wts[3], experts, inter, hidden),
+              ops.moe_mxfp4_pack(wts[4], wts[5], experts, hidden, inter)]
+    got = ops.moe_mxfp4_packed(xb, lg, top_k, inter, *packed, routing=True)
+    for a, b in zip(got, ref):
+        assert np.array_equal(a.cpu().numpy().view(np.uint8), b.cpu().numpy().view(np.uint8))
+
+
+def test_moe_alignment_rejected(device):
+    torch = _torch()
+    import kadan_amd
+    from kadan_amd import ops
+    tokens, hidden, inter, experts = 2, 64, 64, 4
+    x, logits = synth.moe_inputs(1, tokens, hidden, experts)
+    (gb, gs), (ub, us), (db, ds) = synth.moe_weights(1, experts, hidden, inter)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)
+    wts = [dev(a) for a in (gb, gs, ub, us, db, ds)]
+    xs = torch.zeros(tokens * hidden + 8, dtype=torch.bfloat16, device=device)
+    shifted = xs[1:1 + tokens * hidden].view(tokens, hidden)  # 2-byte offset
+    with pytest.raises(kadan_amd.KdqError, match="align"):
+        ops.moe_mxfp4(shifted, dev(logits), 2, *wts)
+    packed = [ops.moe_mxfp4_pack(wts[0], wts[1], experts, inter, hidden),
+              ops.moe_mxfp4_pack(wts[2], wts[3], experts, inter, hidden),
+              ops.moe_mxfp4_pack(wts[4], wts[5], experts, hidden, inter)]
+    with pytest.raises(kadan_amd.KdqError, match="align"):
+        ops.moe_mxfp4_packed(dev(x).view(torch.bfloat16), dev(logits), 2, inter,
+                             packed[0][16:], packed[1], packed[2])
+    with pytest.raises(kadan_amd.KdqError, match="shape"):
+        kadan_amd.call("kdq_moe_mxfp4_pack", wts[0].data_ptr(), wts[1].data_ptr(), experts,
+                       48, hidden, packed[0].data_ptr(), None)
