@@ -175,31 +175,36 @@ def cpu_baseline(seconds: float, copies: int = 4):
     }
 
 
-def bench_gemv(torch, encoding, n_in, n_out, steps, warmup, seed, copies=16):
-    """ms per GEMV step.  Steps go through kdq_gemv_batch, one job per weight copy and
-    up to `copies` jobs per submission, so the host enqueues launches faster than the
-    GPU retires them and the events time the kernels rather than Python."""
+def bench_gemv(torch, encoding, n_in, n_out, steps, warmup, seed, copies=16, per_step=1):
+    """ms per step.  A step is one kdq_gemv_batch submission of `per_step` jobs over
+    distinct weight copies (rotated through `copies`) that share one input and write
+    separate outputs; the library runs a submission of one shape as one launch.  The host
+    enqueues submissions faster than the GPU retires them (a ctypes call and a launch
+    take less than a kernel), so the events time the kernels rather than Python."""
+    import ctypes
     import kadan_amd
     from kadan_amd import synth
     w = synth.gguf_weights(encoding, seed, n_out, n_in)
     ws = rotated_copies(torch, w, copies, keep_mask(encoding, w.shape), seed)
     x = torch.from_numpy(synth.normal(seed, 50, n_in).reshape(1, n_in)).cuda()
-    y = torch.empty(1, n_out, device="cuda")
-    table = (kadan_amd.MatvecJob * copies)()
-    for c, wc in enumerate(ws):
-        table[c] = kadan_amd.MatvecJob(wc.data_ptr(), x.data_ptr(), y.data_ptr(), 0,
-                                       wc.shape[1], n_out, n_in, n_out, 1, encoding)
-    import ctypes
-    address = ctypes.addressof(table)
+    ys = [torch.empty(1, n_out, device="cuda") for _ in range(per_step)]
+    tables = []
+    for first in range(0, copies - per_step + 1, per_step):
+        table = (kadan_amd.MatvecJob * per_step)()
+        for k in range(per_step):
+            wc = ws[first + k]
+            table[k] = kadan_amd.MatvecJob(wc.data_ptr(), x.data_ptr(), ys[k].data_ptr(), 0,
+                                           wc.shape[1], n_out, n_in, n_out, 1, encoding)
+        tables.append(table)
+    addresses = [ctypes.addressof(t) for t in tables]
     fn = kadan_amd.lib().kdq_gemv_batch
     stream = torch.cuda.current_stream().cuda_stream
 
     def submit(n):
-        full, rest = divmod(n, copies)
-        for _ in range(full):
-            kadan_amd.check("kdq_gemv_batch", fn(address, copies, stream))
-        if rest:
-            kadan_amd.check("kdq_gemv_batch", fn(address, rest, stream))
+        for i in range(n):
+            status = fn(addresses[i % len(addresses)], per_step, stream)
+            if status:
+                kadan_amd.check("kdq_gemv_batch", status)
 
     submit(warmup)
     return time_steps(torch, submit, steps)
@@ -338,6 +343,13 @@ def main():
             nb = gemv_bytes(a, b, enc)
             extra[name] = {"ms": round(t, 6), "gbs": round(nb / (t * 1e-3) / 1e9, 1),
                            "hbm_frac": round(nb / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        t = bench_gemv(torch, Q4_K, n_in, n_out, 1000, 20, 0xC2C, per_step=2)
+        nb = 2 * gemv_bytes(n_in, n_out, Q4_K) - 4 * n_in  # one shared input
+        extra["c2_q4_k_gate_up_pair"] = {
+            "workload": "C2 Q4_K gate+up 2 x (4096->14336), batch 1, one kdq_gemv_batch "
+                        "submission (one fused launch)",
+            "ms": round(t, 6), "gbs": round(nb / (t * 1e-3) / 1e9, 1),
+            "hbm_frac": round(nb / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         extra["c3_q4_0_gemm"] = bench_gemm(torch)
         extra["c4_moe_t1"] = bench_moe(torch, 1, 32, 0, 0xC4, copies=2, count=50)
         extra["c4_moe_t256"] = bench_moe(torch, 256, 32, 0, 0xC4, copies=2)

@@ -95,7 +95,10 @@ typedef struct kdq_matvec_job {
 
 /* Every job in one submission (replaces launch_matvec(vector<MatvecJob>&, table),
  * IW/src/cuda/h3_compute.cu:367-382, as used by dense_gguf_batch :3963-4375).
- * `jobs` is a HOST array; jobs that share an input pointer stage it once per pass. */
+ * `jobs` is a HOST array.  Jobs of one shape (encoding, rows in {1, 2, 4, 8}, in) that
+ * the streaming kernel takes run together, up to 8 per launch, as the reference runs a
+ * submission in one launch per format (h3_compute.cu:336-382); results are bit-identical
+ * to one kdq_gemv per job. */
 int kdq_gemv_batch(const kdq_matvec_job* jobs, size_t count, void* stream);
 
 /* ---- prefill Q4_0 GEMM (no reference device counterpart; the reference decodes to

@@ -17,6 +17,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <vector>
 
 namespace kdq {
 namespace {
@@ -699,18 +700,41 @@ struct UnitCursor {
     }
 };
 
-// Workgroup: W wavefronts (W <= 16), rows [r0, r1), processed in passes of up to kTiles
-// tiles.  In a pass, wavefront w takes the units (g, t) for g = w, w + W, ... and every
+// Up to kMaxFused products of one shape (encoding, batch rows, in) in one launch: job
+// blockIdx.y, output rows blockIdx.x * rows_per_wg .. + rows_per_wg (workgroups past a
+// job's rows exit at once).  The table travels in the kernel arguments and is indexed by
+// blockIdx.y, so its fields load in the kernel's first round of argument loads (the
+// reference runs every job of a submission in one launch per format,
+// IW/src/cuda/h3_compute.cu:336-382).
+constexpr int kMaxFused = 8;
+struct MfmaJob {  // one job's fields together: one scalar load brings them
+    const uint8_t* weights;
+    const float* x;
+    float* y;
+    unsigned* status;
+    size_t row_bytes, stride;
+    unsigned out, pad;
+};
+struct MfmaJobs {
+    MfmaJob job[kMaxFused];
+    unsigned count, columns, in, rows_per_wg;
+};
+
+// Workgroup: W wavefronts (W <= 16), rows [r0, r1) of its job, processed in passes of up
+// to kTiles tiles.  In a pass, wavefront w takes the units (g, t) for g = w, w + W, ... and every
 // tile t, kUnits at a time.  Loads are issued by every lane
 // unconditionally (rows past r1 and units past the wavefront's last are clamped to valid
 // data and their results discarded), so waits count exactly.  Order: this thread's first
 // activation unit, the first units' packed weights, then the staging.
 template <int ENC, int R, int W>
-__global__ __launch_bounds__(W * 64) void mfma_gemv(const uint8_t* __restrict__ weights,
-                                                       size_t row_bytes, const float* x,
-                                                       unsigned in, unsigned out,
-                                                       float* __restrict__ y, size_t stride,
-                                                       unsigned* status, unsigned rows_per_wg) {
+__global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
+    const MfmaJob& jb = jobs.job[blockIdx.y];
+    const uint8_t* __restrict__ weights = jb.weights;
+    const size_t row_bytes = jb.row_bytes, stride = jb.stride;
+    const float* x = jb.x;
+    float* __restrict__ y = jb.y;
+    unsigned* status = jb.status;
+    const unsigned in = jobs.in, out = jb.out, rows_per_wg = jobs.rows_per_wg;
     constexpr int kTiles = mfma_tiles<R>;
     constexpr int kUnits = mfma_units<ENC, R>;
     constexpr int kRowUnroll = R <= 2 ? R : 1;  // larger batches: one row's operands at a time
@@ -729,7 +753,12 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const uint8_t* __restrict__ 
     // entry, the others a zero region; MFMA m adds m * 256 bytes
     const bool carrier = j / 4 == G;
     const ScaleSel sel{8 * ((2 * G) & 3), G >= 2};
+    // every argument in one round of scalar loads, then the exit test
+    asm volatile("" ::"s"(weights), "s"(x), "s"(y), "s"(status), "s"(row_bytes), "s"(stride),
+                 "s"(in), "s"(out), "s"(rows_per_wg));
     const unsigned r0 = blockIdx.x * rows_per_wg, r1 = min(out, r0 + rows_per_wg);
+    if (r0 >= out)
+        return;  // the whole workgroup, before any barrier
     bool bad = false;
 
     for (unsigned t = threadIdx.x; t < 256; t += kThreads)
@@ -950,8 +979,9 @@ struct MfmaPlan {
 };
 
 // Batch rows per pass as the LDS allows (at most 8); `waves` wavefronts per workgroup and
-// ceil(out / (compute units * per_cu)) rows per workgroup.
-bool plan_mfma(size_t rows, size_t in, size_t out, MfmaPlan& p) {
+// ceil(total_out / compute units) rows per workgroup, total_out summed over the jobs of
+// one launch.
+bool plan_mfma(size_t rows, size_t in, size_t total_out, MfmaPlan& p) {
     constexpr size_t limit = 160 * 1024;
     if (in % 256 || mfma_lds(1, in) > limit)
         return false;
@@ -959,43 +989,60 @@ bool plan_mfma(size_t rows, size_t in, size_t out, MfmaPlan& p) {
     while (batch < 8 && batch < rows && mfma_lds(batch * 2, in) <= limit)
         batch *= 2;
     const size_t cus = compute_units();
-    const size_t rows_per_wg = std::max<size_t>(1, (out + cus - 1) / cus);
+    const size_t rows_per_wg = std::max<size_t>(1, (total_out + cus - 1) / cus);
     p.batch = batch;
     p.waves = 16;
     p.rows_per_wg = unsigned(rows_per_wg);
-    p.grid = unsigned((out + rows_per_wg - 1) / rows_per_wg);
+    p.grid = unsigned((total_out + rows_per_wg - 1) / rows_per_wg);
     return true;
 }
 
+// Sets rows_per_wg and the grid columns (workgroups of the largest job) of `jobs`
+// (count, out[] set).
+void number_workgroups(MfmaJobs& jobs, unsigned rows_per_wg) {
+    jobs.rows_per_wg = rows_per_wg;
+    jobs.columns = 0;
+    for (unsigned k = 0; k < jobs.count; ++k)
+        jobs.columns = std::max(jobs.columns, (jobs.job[k].out + rows_per_wg - 1) / rows_per_wg);
+}
+
 template <int ENC, int R, int W>
-int launch_mfma_shape(const MfmaPlan& p, const void* w, size_t row_bytes, const float* x,
-                      size_t in, size_t out, float* y, size_t stride, unsigned* status,
-                      hipStream_t stream) {
+int launch_mfma_shape(const MfmaJobs& jobs, hipStream_t stream) {
     static bool configured = false;  // one attribute call per instantiation
     if (!configured) {
         KDQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&mfma_gemv<ENC, R, W>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
         configured = true;
     }
-    hipLaunchKernelGGL((mfma_gemv<ENC, R, W>), dim3(p.grid), dim3(W * 64), mfma_lds(R, in),
-                       stream, static_cast<const uint8_t*>(w), row_bytes, x, unsigned(in),
-                       unsigned(out), y, stride, status, p.rows_per_wg);
+    hipLaunchKernelGGL((mfma_gemv<ENC, R, W>), dim3(jobs.columns, jobs.count), dim3(W * 64),
+                       mfma_lds(R, jobs.in), stream, jobs);
     KDQ_HIP(hipGetLastError());
     return KDQ_OK;
 }
 
 template <int ENC, int R>
-int launch_mfma_pass(const MfmaPlan& p, const void* w, size_t row_bytes, const float* x,
-                     size_t in, size_t out, float* y, size_t stride, unsigned* status,
-                     hipStream_t stream) {
-    switch (p.waves) {
+int launch_mfma_pass(unsigned waves, const MfmaJobs& jobs, hipStream_t stream) {
+    switch (waves) {
     case 4:
-        return launch_mfma_shape<ENC, R, 4>(p, w, row_bytes, x, in, out, y, stride, status, stream);
+        return launch_mfma_shape<ENC, R, 4>(jobs, stream);
     case 8:
-        return launch_mfma_shape<ENC, R, 8>(p, w, row_bytes, x, in, out, y, stride, status, stream);
+        return launch_mfma_shape<ENC, R, 8>(jobs, stream);
     default:
-        return launch_mfma_shape<ENC, R, 16>(p, w, row_bytes, x, in, out, y, stride, status,
-                                             stream);
+        return launch_mfma_shape<ENC, R, 16>(jobs, stream);
+    }
+}
+
+template <int ENC>
+int launch_mfma_rows(unsigned r, unsigned waves, const MfmaJobs& jobs, hipStream_t stream) {
+    switch (r) {
+    case 1:
+        return launch_mfma_pass<ENC, 1>(waves, jobs, stream);
+    case 2:
+        return launch_mfma_pass<ENC, 2>(waves, jobs, stream);
+    case 4:
+        return launch_mfma_pass<ENC, 4>(waves, jobs, stream);
+    default:
+        return launch_mfma_pass<ENC, 8>(waves, jobs, stream);
     }
 }
 
@@ -1010,23 +1057,13 @@ int launch_mfma(const void* w, size_t row_bytes, const float* x, size_t rows, si
         unsigned r = p.batch;
         while (r > left)
             r /= 2;
-        const float* xs = x + first * in;
-        float* ys = y + first * stride;
-        int rc;
-        switch (r) {
-        case 1:
-            rc = launch_mfma_pass<ENC, 1>(p, w, row_bytes, xs, in, out, ys, stride, status, stream);
-            break;
-        case 2:
-            rc = launch_mfma_pass<ENC, 2>(p, w, row_bytes, xs, in, out, ys, stride, status, stream);
-            break;
-        case 4:
-            rc = launch_mfma_pass<ENC, 4>(p, w, row_bytes, xs, in, out, ys, stride, status, stream);
-            break;
-        default:
-            rc = launch_mfma_pass<ENC, 8>(p, w, row_bytes, xs, in, out, ys, stride, status, stream);
-            break;
-        }
+        MfmaJobs jobs{};
+        jobs.count = 1;
+        jobs.in = unsigned(in);
+        jobs.job[0] = MfmaJob{static_cast<const uint8_t*>(w), x + first * in, y + first * stride,
+                              status, row_bytes, stride, unsigned(out), 0};
+        number_workgroups(jobs, p.rows_per_wg);
+        const int rc = launch_mfma_rows<ENC>(r, p.waves, jobs, stream);
         if (rc)
             return rc;
         first += r;
@@ -1036,6 +1073,13 @@ int launch_mfma(const void* w, size_t row_bytes, const float* x, size_t rows, si
 
 bool aligned(const void* p, size_t a) {
     return (reinterpret_cast<uintptr_t>(p) % a) == 0;
+}
+
+// The streaming kernels need whole 64-value lane slots, 4-byte aligned rows and packed
+// rows of exactly the format's size (16-byte aligned for Q4_K).
+bool streams(int encoding, const void* weights, size_t row_bytes, size_t in) {
+    return in % 256 == 0 && row_bytes % 4 == 0 && aligned(weights, 4) &&
+           (encoding != KDQ_Q4_K || (row_bytes % 16 == 0 && aligned(weights, 16)));
 }
 
 // Shared argument checks of the product entry points.
@@ -1115,10 +1159,8 @@ extern "C" int kdq_gemv(int encoding, const void* weights, size_t row_bytes, con
     if (rc)
         return rc;
     auto s = static_cast<hipStream_t>(stream);
-    // The streaming kernel needs whole 64-value lane slots, 4-byte aligned rows and
-    // packed rows of exactly the format's size; anything else takes the exact kernel.
-    const bool fast = in % 256 == 0 && row_bytes % 4 == 0 && aligned(weights, 4) &&
-                      (encoding != KDQ_Q4_K || (row_bytes % 16 == 0 && aligned(weights, 16)));
+    // Shapes the streaming kernels do not take run on the exact kernel.
+    const bool fast = streams(encoding, weights, row_bytes, in);
     if (fast) {
         switch (encoding) {
         case KDQ_Q8_0:
@@ -1151,6 +1193,48 @@ extern "C" int kdq_gemv(int encoding, const void* weights, size_t row_bytes, con
                           stream);
 }
 
+namespace kdq {
+namespace {
+
+// One fused MFMA launch for jobs[idx[0..n)] (same encoding, rows, in; checked).
+int launch_fused(const kdq_matvec_job* jobs, const size_t* idx, size_t n, hipStream_t stream) {
+    const kdq_matvec_job& j0 = jobs[idx[0]];
+    size_t total = 0;
+    for (size_t k = 0; k < n; ++k)
+        total += jobs[idx[k]].columns;
+    MfmaPlan p;
+    if (!plan_mfma(j0.rows, j0.in, total, p))
+        return KDQ_ERR_UNSUPPORTED;
+    MfmaJobs mj{};
+    mj.count = unsigned(n);
+    mj.in = j0.in;
+    for (size_t k = 0; k < n; ++k) {
+        const kdq_matvec_job& j = jobs[idx[k]];
+        mj.job[k] = MfmaJob{static_cast<const uint8_t*>(j.weights), j.input, j.output,
+                            j.status, j.row_bytes, j.stride, j.columns, 0};
+    }
+    number_workgroups(mj, p.rows_per_wg);
+    switch (j0.encoding) {
+    case KDQ_Q8_0:
+        return launch_mfma_rows<KDQ_Q8_0>(j0.rows, p.waves, mj, stream);
+    case KDQ_Q4_0:
+        return launch_mfma_rows<KDQ_Q4_0>(j0.rows, p.waves, mj, stream);
+    default:
+        return launch_mfma_rows<KDQ_Q4_K>(j0.rows, p.waves, mj, stream);
+    }
+}
+
+// Jobs the fused launch takes: streaming shapes whose rows fit one pass of the MFMA
+// kernel (1, 2, 4 or 8 rows, within its LDS batch).
+bool fusable(const kdq_matvec_job& j) {
+    MfmaPlan p;
+    return streams(j.encoding, j.weights, j.row_bytes, j.in) && (j.rows & (j.rows - 1)) == 0 &&
+           plan_mfma(j.rows, j.in, j.columns, p) && p.batch >= j.rows;
+}
+
+}  // namespace
+}  // namespace kdq
+
 extern "C" int kdq_gemv_batch(const kdq_matvec_job* jobs, size_t count, void* stream) {
     if (count && !jobs)
         return KDQ_ERR_ARGUMENT;
@@ -1162,7 +1246,30 @@ extern "C" int kdq_gemv_batch(const kdq_matvec_job* jobs, size_t count, void* st
         if (rc)
             return rc;
     }
+    auto s = static_cast<hipStream_t>(stream);
+    // Jobs of one shape (encoding, rows, in) run together, up to kMaxFused per launch, in
+    // submission order; the rest one launch each.
+    std::vector<char> done(count, 0);
     for (size_t i = 0; i < count; ++i) {
+        if (done[i] || !fusable(jobs[i]))
+            continue;
+        size_t idx[kMaxFused], n = 0;
+        for (size_t k = i; k < count && n < size_t(kMaxFused); ++k) {
+            const auto& a = jobs[i];
+            const auto& b = jobs[k];
+            if (!done[k] && b.encoding == a.encoding && b.rows == a.rows && b.in == a.in &&
+                fusable(b))
+                idx[n++] = k;
+        }
+        const int rc = launch_fused(jobs, idx, n, s);
+        if (rc)
+            return rc;
+        for (size_t k = 0; k < n; ++k)
+            done[idx[k]] = 1;
+    }
+    for (size_t i = 0; i < count; ++i) {
+        if (done[i])
+            continue;
         const auto& j = jobs[i];
         const int rc = kdq_gemv(j.encoding, j.weights, j.row_bytes, j.input, j.rows, j.in,
                                 j.columns, j.output, j.stride, j.status, stream);

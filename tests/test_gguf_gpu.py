@@ -174,6 +174,38 @@ def test_gemv_batch_matches_single_calls(device, oracle):
         assert_close(j["output"].cpu().numpy(), e)
 
 
+@pytest.mark.parametrize("rows", [1, 2, 4])
+def test_gemv_batch_fused_bit_identical(device, oracle, rows):
+    """Jobs of one shape run as one fused launch (the reference runs a submission as one
+    launch per format); every output must equal its own single kdq_gemv bit for bit.
+    Mixed submission: 9 Q4_K gate/up-like jobs (over the 8-job launch limit) sharing one
+    input, two Q8_0 jobs, a Q4_K job with another input, and a Q4_K job with in=4352
+    (a different shape)."""
+    torch = _torch()
+    from kadan_amd import ops
+    x = synth.normal(31, 1, rows * 4096).reshape(rows, 4096)
+    x2 = synth.normal(32, 1, rows * 4096).reshape(rows, 4096)
+    x3 = synth.normal(33, 1, rows * 4352).reshape(rows, 4352)
+    xs, xs2, xs3 = (torch.from_numpy(a).to(device) for a in (x, x2, x3))
+    specs = [(Q4_K, 1000 + 37 * i, xs, 40 + i) for i in range(9)]
+    specs += [(Q8_0, 513, xs, 60), (Q8_0, 77, xs2, 61), (Q4_K, 300, xs2, 62),
+              (Q4_K, 129, xs3, 63)]
+    jobs, singles = [], []
+    for enc, n_out, inp, seed in specs:
+        n_in = inp.shape[1]
+        w = torch.from_numpy(synth.gguf_weights(enc, seed, n_out, n_in)).to(device)
+        jobs.append({"encoding": enc, "weights": w, "input": inp,
+                     "output": torch.full((rows, n_out), -3.0, device=device)})
+        singles.append(ops.gemv(enc, w, inp, n_out))
+    ops.gemv_batch(jobs)
+    for j, single in zip(jobs, singles):
+        assert np.array_equal(j["output"].cpu().numpy().view(np.uint32),
+                              single.cpu().numpy().view(np.uint32))
+    # and one of them against the oracle
+    w0 = synth.gguf_weights(Q4_K, 40, 1000, 4096)
+    assert_close(jobs[0]["output"].cpu().numpy(), oracle.gemv(Q4_K, w0, x, 4096, 1000))
+
+
 def test_gemv_rejects_alias_and_shape(device):
     torch = _torch()
     import kadan_amd
