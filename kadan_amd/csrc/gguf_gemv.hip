@@ -529,10 +529,13 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 constexpr int kAGroup = 1024;     // LDS bytes of A operands per 256-value group
 constexpr int kPartialPitch = 17; // floats per lane in the pass partials (bank spread)
 
-// Tiles of 16 rows per pass, and units (tile, 256-value group) in flight per wavefront.
+// Tiles of 16 rows per pass, and units (tile, 256-value group) in flight per wavefront:
+// two for one activation row (with all of a wavefront's units requested at once, the
+// memory system answers them in its own order and the in-order waits make the first
+// MFMA wait for most of them).
 template <int R> constexpr int mfma_tiles = R >= 4 ? 1 : 4 / R;
 template <int ENC, int R>
-constexpr int mfma_units = R == 1 ? (ENC == KDQ_Q8_0 ? 2 : 4) : (R == 2 ? 2 : 1);
+constexpr int mfma_units = R == 1 ? 2 : (R == 2 ? 2 : 1);
 
 // LDS layout of mfma_gemv (bytes):
 //   [0, 1024)                                       zeros (A operand of non-carrier lanes)
