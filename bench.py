@@ -175,6 +175,102 @@ def cpu_baseline(seconds: float, copies: int = 4):
     }
 
 
+def cpu_thread_counts():
+    """1 thread, the reference policy clamp(cores/2, 1, 16) (IW/src/models/text/
+    gguf_weights.cpp:615-618), and every core this process may use (at most 16, the
+    GPU box's share of one GPU)."""
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    return cores, sorted({1, max(1, min(16, cores // 2)), max(1, min(16, cores))})
+
+
+def timed_median(fn, seconds: float, least: int = 3):
+    t0 = time.perf_counter()
+    fn()  # warm-up; a run longer than the budget counts as the sample itself
+    first = time.perf_counter() - t0
+    if first > seconds:
+        return first, 1
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < least:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_baselines(seconds: float = 2.0):
+    """The reference CPU path (oracle/_ref where built, else the oracle restatement) for
+    C1, C2, C3 and C4 at each thread count of cpu_thread_counts(), bounded samples of
+    about `seconds` each; C3 and C4 T=256 time a stated subset of rows or tokens."""
+    from kadan_amd import synth
+    import oracle
+    cores, counts = cpu_thread_counts()
+    ref = oracle.Reference() if oracle.Reference.available() else None
+    impl = ref or oracle.Oracle()
+    kind = "reference" if ref else "port"
+    port = oracle.Oracle()
+    out = {"cores_available": cores, "threads": counts}
+
+    def gemv_leg(name, encoding, n_in, n_out, seed, copies=4):
+        base = synth.gguf_weights(encoding, seed, n_out, n_in)
+        keep = keep_mask(encoding, base.shape)
+        ws = [base] + [np.where(keep, base, base ^ synth.random_bytes(seed, 100 + c, base.size)
+                                .reshape(base.shape)) for c in range(1, copies)]
+        x = synth.normal(seed, 50, n_in).reshape(1, n_in)
+        nb = gemv_bytes(n_in, n_out, encoding)
+        legs = {}
+        for th in counts:
+            state = {"i": 0}
+
+            def run():
+                impl.cpu_matvec(encoding, ws[state["i"] % copies], x, n_in, n_out, th)
+                state["i"] += 1
+            med, n = timed_median(run, seconds)
+            legs[str(th)] = {"gbs": round(nb / med / 1e9, 3), "ms": round(med * 1e3, 3),
+                             "runs": n}
+        out[name] = {"kind": kind, "unit": "GB/s of algorithmic bytes", "by_threads": legs,
+                     "sample": f"whole {n_in}->{n_out} matvec, batch 1, {copies} rotated "
+                               "weight copies; median of the runs"}
+
+    gemv_leg("c1_q8_0_gemv_4096x4096", Q8_0, 4096, 4096, 0xC1)
+    gemv_leg("c2_q4_k_gemv_4096_to_14336", Q4_K, 4096, 14336, 0xC2A)
+
+    # C3: Q8_0-quantised activation rows x Q4_0 weights (CpuMatvec over the rows)
+    n_out, k, rows = 14336, 4096, 32
+    w = synth.gguf_weights(Q4_0, 0xC3, n_out, k)
+    x16 = synth.normal(0xC3, 60, rows * k).astype(np.float16).astype(np.float32)
+    x16 = x16.reshape(rows, k)
+    legs = {}
+    for th in counts:
+        med, n = timed_median(lambda: impl.cpu_matvec(Q4_0, w, x16, k, n_out, th), seconds)
+        legs[str(th)] = {"tflops": round(2.0 * rows * k * n_out / med / 1e12, 4),
+                         "ms": round(med * 1e3, 2), "runs": n}
+    out["c3_q4_0_gemm"] = {"kind": kind, "unit": "TFLOP/s", "by_threads": legs,
+                           "sample": f"{rows} of the 512 activation rows (fp16 values in "
+                                     "fp32), all 14336 outputs: quantize_row_q8_0 + "
+                                     "vec_dot_q4_0_q8_0 via CpuMatvec"}
+
+    # C4: the MoE layer flow with exact MXFP4 products (the oracle's composition: the
+    # reference has no compiled MXFP4 MoeLayer)
+    (gb, gs), (ub, us), (db, ds) = synth.moe_weights(0xC4, 32, 2880, 2880)
+    for name, tokens, sample in (("c4_moe_t1", 1, 1), ("c4_moe_t256", 256, 4)):
+        xa, la = synth.moe_inputs(0xC4, tokens, 2880, 32)
+        xa, la = xa[:sample], la[:sample]
+        legs = {}
+        for th in counts:
+            med, n = timed_median(lambda: port.moe_forward(xa, la, 4, gb, gs, ub, us, db, ds,
+                                                           threads=th), seconds, least=1)
+            legs[str(th)] = {"tokens_per_s": round(sample / med, 2), "ms": round(med * 1e3, 2),
+                             "runs": n}
+        out[name] = {"kind": "port", "unit": "tokens/s", "by_threads": legs,
+                     "sample": f"{sample} token(s) of the T={tokens} inputs, 32 experts, "
+                               "top-4, double-accumulated MXFP4 products"}
+    return out
+
+
 def bench_gemv(torch, encoding, n_in, n_out, steps, warmup, seed, copies=16, per_step=1):
     """ms per step.  A step is one kdq_gemv_batch submission of `per_step` jobs over
     distinct weight copies (rotated through `copies`) that share one input and write
@@ -358,6 +454,8 @@ def main():
         result["extra"] = extra
     if not args.skip_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        if not args.skip_extra:
+            result["cpu_baselines"] = cpu_baselines()
     print(json.dumps(result))
 
 
