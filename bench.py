@@ -3,10 +3,10 @@
 
 Headline (``value``): Q4_K GEMV weight throughput in GB/s at the Llama-3-8B FFN
 decode shape gate/up 4096 -> 14336, batch 1, with the inputs
-resident in HBM.  A "step" is one GEMV over one weight copy (one kernel launch,
-enqueued through kdq_gemv_batch 16 jobs at a time); the timed steps rotate over 16
-distinct weight copies (528 MB, twice the 256 MB Infinity Cache) so the cache cannot
-serve the weights.
+resident in HBM in the library's tile-packed layout (kdq_gguf_pack, the form its weight
+bank keeps).  A "step" is one GEMV over one weight copy (one kernel launch, one
+kdq_gemv_packed_batch submission); the timed steps rotate over 16 distinct weight
+copies (528 MB, twice the 256 MB Infinity Cache) so the cache cannot serve the weights.
 
 The same line carries
   roofline      the GEMV kernel's algorithmic bytes / measured average launch time
@@ -271,17 +271,23 @@ def cpu_baselines(seconds: float = 2.0):
     return out
 
 
-def bench_gemv(torch, encoding, n_in, n_out, steps, warmup, seed, copies=16, per_step=1):
-    """ms per step.  A step is one kdq_gemv_batch submission of `per_step` jobs over
-    distinct weight copies (rotated through `copies`) that share one input and write
-    separate outputs; the library runs a submission of one shape as one launch.  The host
+def bench_gemv(torch, encoding, n_in, n_out, steps, warmup, seed, copies=16, per_step=1,
+               packed=True):
+    """ms per step.  A step is one kdq_gemv_packed_batch submission (kdq_gemv_batch with
+    packed=False) of `per_step` jobs over distinct weight copies (rotated through `copies`)
+    that share one input and write separate outputs; the library runs a submission of one
+    shape as one launch.  Packed weights are the resident form the host layer's bank
+    keeps (kdq_gguf_pack, done once per copy outside the timed region).  The host
     enqueues submissions faster than the GPU retires them (a ctypes call and a launch
     take less than a kernel), so the events time the kernels rather than Python."""
     import ctypes
     import kadan_amd
-    from kadan_amd import synth
+    from kadan_amd import ops, synth
     w = synth.gguf_weights(encoding, seed, n_out, n_in)
     ws = rotated_copies(torch, w, copies, keep_mask(encoding, w.shape), seed)
+    if packed:
+        ws = [ops.gguf_pack(encoding, c, n_in) for c in ws]
+        torch.cuda.synchronize()
     x = torch.from_numpy(synth.normal(seed, 50, n_in).reshape(1, n_in)).cuda()
     ys = [torch.empty(1, n_out, device="cuda") for _ in range(per_step)]
     tables = []
@@ -290,17 +296,18 @@ def bench_gemv(torch, encoding, n_in, n_out, steps, warmup, seed, copies=16, per
         for k in range(per_step):
             wc = ws[first + k]
             table[k] = kadan_amd.MatvecJob(wc.data_ptr(), x.data_ptr(), ys[k].data_ptr(), 0,
-                                           wc.shape[1], n_out, n_in, n_out, 1, encoding)
+                                           0 if packed else wc.shape[1], n_out, n_in, n_out,
+                                           1, encoding)
         tables.append(table)
     addresses = [ctypes.addressof(t) for t in tables]
-    fn = kadan_amd.lib().kdq_gemv_batch
+    fn = kadan_amd.lib().kdq_gemv_packed_batch if packed else kadan_amd.lib().kdq_gemv_batch
     stream = torch.cuda.current_stream().cuda_stream
 
     def submit(n):
         for i in range(n):
             status = fn(addresses[i % len(addresses)], per_step, stream)
             if status:
-                kadan_amd.check("kdq_gemv_batch", status)
+                kadan_amd.check("kdq_gemv_packed_batch" if packed else "kdq_gemv_batch", status)
 
     submit(warmup)
     return time_steps(torch, submit, steps)
@@ -422,10 +429,11 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_k x f32 (int8 dot4, f32 accumulate)",
-        "data": "synthetic (seeded SplitMix64 GGUF blocks, 16 rotated weight copies)",
+        "dtype": "q4_k x f32 (int8 MFMA on 16-bit block fixed-point activations, f32 accumulate)",
+        "data": "synthetic (seeded SplitMix64 GGUF blocks, 16 rotated weight copies, "
+                "resident in the tile-packed layout)",
         "config": {"workload": workload, "n_in": n_in, "n_out": n_out, "batch": 1,
-                   "weight_copies": 16},
+                   "weight_copies": 16, "layout": "tile-packed (kdq_gguf_pack)"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic_for(workload),
@@ -439,6 +447,13 @@ def main():
             nb = gemv_bytes(a, b, enc)
             extra[name] = {"ms": round(t, 6), "gbs": round(nb / (t * 1e-3) / 1e9, 1),
                            "hbm_frac": round(nb / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        t = bench_gemv(torch, Q4_K, n_in, n_out, 1000, 20, 0xC2A, packed=False)
+        nb = gemv_bytes(n_in, n_out, Q4_K)
+        extra["c2_q4_k_gemv_row_major"] = {
+            "workload": "C2 Q4_K GEMV 4096->14336, batch 1, over the row-major GGUF bytes "
+                        "(kdq_gemv_batch; no resident repack)",
+            "ms": round(t, 6), "gbs": round(nb / (t * 1e-3) / 1e9, 1),
+            "hbm_frac": round(nb / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         t = bench_gemv(torch, Q4_K, n_in, n_out, 1000, 20, 0xC2C, per_step=2)
         nb = 2 * gemv_bytes(n_in, n_out, Q4_K) - 4 * n_in  # one shared input
         extra["c2_q4_k_gate_up_pair"] = {

@@ -101,6 +101,34 @@ typedef struct kdq_matvec_job {
  * to one kdq_gemv per job. */
 int kdq_gemv_batch(const kdq_matvec_job* jobs, size_t count, void* stream);
 
+/* ---- resident GGUF weights in the tile-packed layout.  No reference counterpart as a
+ * format: the reference's device weight bank keeps uploaded packed rows byte for byte
+ * (IW/src/cuda/h3_compute.cu:2065-2073,4090-4095); this library's bank (and any caller
+ * that keeps weights resident) reorders them once so every wavefront load of the
+ * product is whole 128-byte lines.  The bytes are the same bytes, reordered: tiles of
+ * 16 rows (zero rows after the last), per tile and 256-value group one unit of
+ * 16 x group bytes (Q4_K 2304, Q4_0 2304, Q8_0 4352) of 1 KB code pieces (lane
+ * l = 16*chunk + row%16 at 16*l) followed by the block headers / scales.
+ *
+ * Device bytes of the packed form of `out` rows of `in` values (0 unless in % 256 == 0). */
+size_t kdq_gguf_packed_bytes(int encoding, size_t in, size_t out);
+
+/* Packs `out` rows (`row_bytes` apart, any alignment) into `packed` (16-byte aligned,
+ * kdq_gguf_packed_bytes). */
+int kdq_gguf_pack(int encoding, const void* weights, size_t row_bytes, size_t in, size_t out,
+                  void* packed, void* stream);
+
+/* kdq_gemv over packed weights (replaces gguf_matvec_kernel over resident weights,
+ * IW/src/cuda/h3_compute.cu:165-240): same arguments without row_bytes, same results
+ * bit for bit as kdq_gemv on the row-major bytes when kdq_gemv runs its MFMA kernel
+ * (in % 256 == 0 and in up to ~32K values; larger `in` is KDQ_ERR_UNSUPPORTED here). */
+int kdq_gemv_packed(int encoding, const void* packed, const float* x, size_t rows, size_t in,
+                    size_t out, float* y, size_t stride, unsigned* status, void* stream);
+
+/* kdq_gemv_batch over packed weights (every job's `weights` packed; `row_bytes` is
+ * ignored).  Counterpart of launch_matvec over a submission, h3_compute.cu:367-382. */
+int kdq_gemv_packed_batch(const kdq_matvec_job* jobs, size_t count, void* stream);
+
 /* ---- prefill Q4_0 GEMM (no reference device counterpart; the reference decodes to
  * F32 and calls cublasSgemm, IW/src/cuda/h3_compute.cu:2451, and its CPU path runs
  * ggml vec_dot_q4_0_q8_0, G/src/ggml-cpu/quants.c:225-260).

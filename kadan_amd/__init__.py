@@ -40,6 +40,9 @@ _SIGNATURES = {
     "kdq_gemv": [_I, _VP, _SZ, _VP, _SZ, _SZ, _SZ, _VP, _SZ, _VP, _VP],
     "kdq_gemv_exact": [_I, _VP, _SZ, _VP, _SZ, _SZ, _SZ, _VP, _SZ, _VP, _VP],
     "kdq_gemv_batch": [_VP, _SZ, _VP],
+    "kdq_gguf_pack": [_I, _VP, _SZ, _SZ, _SZ, _VP, _VP],
+    "kdq_gemv_packed": [_I, _VP, _VP, _SZ, _SZ, _SZ, _VP, _SZ, _VP, _VP],
+    "kdq_gemv_packed_batch": [_VP, _SZ, _VP],
     "kdq_gemm_q4_0": [_VP, _SZ, _SZ, _VP, _SZ, _VP, _VP],
     "kdq_quantize_q8": [_VP, _SZ, _SZ, _VP, _VP, _VP],
     "kdq_moe_route": [_VP, _SZ, _SZ, _SZ, _VP, _VP, _VP, _VP, _VP],
@@ -57,6 +60,7 @@ _OTHER = {
     "kdq_block_values": (_SZ, [_I]),
     "kdq_block_bytes": (_SZ, [_I]),
     "kdq_row_bytes": (_SZ, [_I, _SZ]),
+    "kdq_gguf_packed_bytes": (_SZ, [_I, _SZ, _SZ]),
     "kdq_moe_mxfp4_packed_bytes": (_SZ, [_SZ, _SZ, _SZ]),
 }
 

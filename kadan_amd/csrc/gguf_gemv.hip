@@ -605,10 +605,69 @@ __device__ __forceinline__ void mstage_unit(unsigned in, unsigned u, const XUnit
         blocks[size_t(r) * (in / 32) + e0 / 32] = make_float4(scale, sum, __int_as_float(codes), 0.f);
 }
 
-// B operand of MFMA m from one lane's packed chunk (load_lane layout).
+// Tile-packed weights (kdq_gguf_pack), this library's resident GGUF layout.  Rows are
+// taken 16 at a time (tile T = rows 16T .. 16T+15, zero rows past the end); the unit of
+// tile T and 256-value group g sits at (T * groups + g) * unit bytes and holds, for lane
+// l = 16G + s (row slot s = row % 16, 64-value chunk G of the group):
+//   code piece p (p < pieces): the 16 bytes at p * 1024 + 16 l
+//     Q4_K  pieces 0, 1: code bytes 0..15, 16..31 of sub-block pair G
+//     Q4_0  piece c: the 16 code bytes of block 2G + c of the group
+//     Q8_0  piece 2c + h: code bytes 16h .. 16h+15 of block 2G + c
+//   side data at pieces * 1024:
+//     Q4_K  the 16-byte block header (d, dmin, scales) of row slot s at + 16 s
+//     Q4_0, Q8_0  one dword at + 4 l: d of block 2G | d of block 2G + 1 << 16
+// A wavefront's load of one piece is 1 KB contiguous; the bytes are the row bytes
+// reordered (unit = 16 rows x one group's bytes), nothing is added or converted.
+template <int ENC> struct PackedFormat;
+template <> struct PackedFormat<KDQ_Q4_K> {
+    static constexpr int pieces = 2, unit = 2304;
+};
+template <> struct PackedFormat<KDQ_Q4_0> {
+    static constexpr int pieces = 2, unit = 2304;
+};
+template <> struct PackedFormat<KDQ_Q8_0> {
+    static constexpr int pieces = 4, unit = 4352;
+};
+
+// One lane's chunk from a packed unit, in the register image the packed operand
+// functions read: Q4_K exactly as load_lane (w[0..3] header, w[4..11] codes); Q4_0 and
+// Q8_0 code pieces in w[0 .. 4*pieces) and the scale dword in w[4*pieces].  The code
+// pieces are requested first: the MFMAs need them before the scales.
 template <int ENC>
-__device__ __forceinline__ i32x4 b_operand(const Lane& L, int m) {
+__device__ __forceinline__ void load_packed(const uint8_t* unit, unsigned G, unsigned s, Lane& L) {
+    constexpr int P = PackedFormat<ENC>::pieces;
+    const unsigned l = 16 * G + s;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const u32x4 q = load16(unit + p * 1024 + 16 * l);
+        const int at = ENC == KDQ_Q4_K ? 4 + 4 * p : 4 * p;
+        L.w[at] = q.x, L.w[at + 1] = q.y, L.w[at + 2] = q.z, L.w[at + 3] = q.w;
+    }
     if constexpr (ENC == KDQ_Q4_K) {
+        const u32x4 h = load16(unit + P * 1024 + 16 * s);
+        L.w[0] = h.x, L.w[1] = h.y, L.w[2] = h.z, L.w[3] = h.w;
+    } else {
+        L.w[4 * P] = load4(unit + P * 1024 + 4 * l);
+    }
+}
+
+// B operand of MFMA m from one lane's packed chunk (load_lane layout, or load_packed's
+// when PACKED).
+template <int ENC, bool PACKED = false>
+__device__ __forceinline__ i32x4 b_operand(const Lane& L, int m) {
+    if constexpr (PACKED && ENC == KDQ_Q8_0) {
+        // block 0 codes in w[0..7], block 1 in w[8..15]
+        return i32x4{int(L.w[2 * m]), int(L.w[2 * m + 1]), int(L.w[8 + 2 * m]),
+                     int(L.w[9 + 2 * m])};
+    } else if constexpr (PACKED && ENC == KDQ_Q4_0) {
+        // block 0 code bytes in w[0..3], block 1 in w[4..7]; positions 0..15 are low
+        // nibbles, 16..31 high nibbles
+        const int k = 2 * (m % 2);
+        const int shift = m >= 2 ? 4 : 0;
+        return i32x4{int((L.w[k] >> shift) & 0x0f0f0f0fu), int((L.w[k + 1] >> shift) & 0x0f0f0f0fu),
+                     int((L.w[4 + k] >> shift) & 0x0f0f0f0fu),
+                     int((L.w[5 + k] >> shift) & 0x0f0f0f0fu)};
+    } else if constexpr (ENC == KDQ_Q4_K) {
         // code bytes 8m..8m+7 of the pair: low nibbles are sub-block 2G (kept as 0..15),
         // high nibbles sub-block 2G+1, kept in place as 16q - 128 (one bit operation)
         const unsigned w0 = L.w[4 + 2 * m], w1 = L.w[5 + 2 * m];
@@ -640,9 +699,23 @@ struct ScaleSel {
 
 // The chunk's contribution from the four integer sums of this lane (c.x, c.y: block 0
 // high and low planes; c.z, c.w: block 1) with the activation block entries x0, x1.
-template <int ENC>
+template <int ENC, bool PACKED = false>
 __device__ __forceinline__ float chunk_value(const Lane& L, ScaleSel sel, i32x4 c, float4 x0,
                                              float4 x1, bool& bad) {
+    if constexpr (PACKED && ENC != KDQ_Q4_K) {
+        // the two block scales share one dword after the code pieces
+        const unsigned sc = L.w[4 * PackedFormat<ENC>::pieces];
+        const float d0 = half_hw(sc & 0xffffu), d1 = half_hw(sc >> 16);
+        bad |= !isfinite(d0) || !isfinite(d1);
+        const float A0 = float(c.x * 256 + c.y), A1 = float(c.z * 256 + c.w);
+        if constexpr (ENC == KDQ_Q4_0) {
+            const float t0 = fmaf(x0.x, A0, -8.f * x0.y);
+            const float t1 = fmaf(x1.x, A1, -8.f * x1.y);
+            return fmaf(d1, t1, d0 * t0);
+        } else {
+            return fmaf(d1 * x1.x, A1, d0 * x0.x * A0);
+        }
+    }
     const float A0 = float(c.x * 256 + c.y);
     if constexpr (ENC == KDQ_Q4_K) {
         const float d = half_hw(L.w[0] & 0xffffu), dmin = half_hw(L.w[0] >> 16);
@@ -729,7 +802,7 @@ struct MfmaJobs {
 // unconditionally (rows past r1 and units past the wavefront's last are clamped to valid
 // data and their results discarded), so waits count exactly.  Order: this thread's first
 // activation unit, the first units' packed weights, then the staging.
-template <int ENC, int R, int W>
+template <int ENC, int R, int W, bool PACKED>
 __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
     const MfmaJob& jb = jobs.job[blockIdx.y];
     const uint8_t* __restrict__ weights = jb.weights;
@@ -775,7 +848,11 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
             const bool valid = cur.g < groups;
             const unsigned g = valid ? cur.g : wave % groups, t = valid ? cur.t : 0;
             const unsigned n = min(p0 + 16 * t + j, r1 - 1);
-            load_lane<ENC>(weights + size_t(n) * row_bytes, 4 * g + G, L[k]);
+            if constexpr (PACKED)
+                load_packed<ENC>(weights + (size_t(n / 16) * groups + g) * PackedFormat<ENC>::unit,
+                                 G, n % 16, L[k]);
+            else
+                load_lane<ENC>(weights + size_t(n) * row_bytes, 4 * g + G, L[k]);
             cur.next(tiles, W);
         }
     };
@@ -825,10 +902,10 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
                     for (int m = 0; m < 4; ++m)
                         c = __builtin_amdgcn_mfma_i32_16x16x64_i8(
                             *reinterpret_cast<const i32x4*>(a + m * 256),
-                            b_operand<ENC>(L[k], m), c, 0, 0, 0);
+                            b_operand<ENC, PACKED>(L[k], m), c, 0, 0, 0);
                     const float4* xb = blocks + size_t(r) * (in / 32) + 2 * chunk;
                     mine[size_t(r * kTiles + cur.t) * 64 * kPartialPitch] +=
-                        chunk_value<ENC>(L[k], sel, c, xb[0], xb[1], bad);
+                        chunk_value<ENC, PACKED>(L[k], sel, c, xb[0], xb[1], bad);
                 }
                 cur.next(tiles, W);
             }
@@ -983,8 +1060,9 @@ struct MfmaPlan {
 
 // Batch rows per pass as the LDS allows (at most 8); `waves` wavefronts per workgroup and
 // ceil(total_out / compute units) rows per workgroup, total_out summed over the jobs of
-// one launch.
-bool plan_mfma(size_t rows, size_t in, size_t total_out, MfmaPlan& p) {
+// one launch.  Over packed weights the rows per workgroup are a multiple of 8, so every
+// 128-byte line of a unit (8 row slots of one chunk) belongs to one workgroup.
+bool plan_mfma(size_t rows, size_t in, size_t total_out, MfmaPlan& p, bool packed = false) {
     constexpr size_t limit = 160 * 1024;
     if (in % 256 || mfma_lds(1, in) > limit)
         return false;
@@ -992,7 +1070,9 @@ bool plan_mfma(size_t rows, size_t in, size_t total_out, MfmaPlan& p) {
     while (batch < 8 && batch < rows && mfma_lds(batch * 2, in) <= limit)
         batch *= 2;
     const size_t cus = compute_units();
-    const size_t rows_per_wg = std::max<size_t>(1, (total_out + cus - 1) / cus);
+    size_t rows_per_wg = std::max<size_t>(1, (total_out + cus - 1) / cus);
+    if (packed)
+        rows_per_wg = (rows_per_wg + 7) & ~size_t(7);
     p.batch = batch;
     p.waves = 16;
     p.rows_per_wg = unsigned(rows_per_wg);
@@ -1009,51 +1089,53 @@ void number_workgroups(MfmaJobs& jobs, unsigned rows_per_wg) {
         jobs.columns = std::max(jobs.columns, (jobs.job[k].out + rows_per_wg - 1) / rows_per_wg);
 }
 
-template <int ENC, int R, int W>
+template <int ENC, int R, int W, bool PACKED>
 int launch_mfma_shape(const MfmaJobs& jobs, hipStream_t stream) {
     static bool configured = false;  // one attribute call per instantiation
     if (!configured) {
-        KDQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&mfma_gemv<ENC, R, W>),
+        KDQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&mfma_gemv<ENC, R, W, PACKED>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
         configured = true;
     }
-    hipLaunchKernelGGL((mfma_gemv<ENC, R, W>), dim3(jobs.columns, jobs.count), dim3(W * 64),
-                       mfma_lds(R, jobs.in), stream, jobs);
+    hipLaunchKernelGGL((mfma_gemv<ENC, R, W, PACKED>), dim3(jobs.columns, jobs.count),
+                       dim3(W * 64), mfma_lds(R, jobs.in), stream, jobs);
     KDQ_HIP(hipGetLastError());
     return KDQ_OK;
 }
 
-template <int ENC, int R>
+template <int ENC, int R, bool PACKED>
 int launch_mfma_pass(unsigned waves, const MfmaJobs& jobs, hipStream_t stream) {
     switch (waves) {
     case 4:
-        return launch_mfma_shape<ENC, R, 4>(jobs, stream);
+        return launch_mfma_shape<ENC, R, 4, PACKED>(jobs, stream);
     case 8:
-        return launch_mfma_shape<ENC, R, 8>(jobs, stream);
+        return launch_mfma_shape<ENC, R, 8, PACKED>(jobs, stream);
     default:
-        return launch_mfma_shape<ENC, R, 16>(jobs, stream);
+        return launch_mfma_shape<ENC, R, 16, PACKED>(jobs, stream);
     }
 }
 
-template <int ENC>
+template <int ENC, bool PACKED>
 int launch_mfma_rows(unsigned r, unsigned waves, const MfmaJobs& jobs, hipStream_t stream) {
     switch (r) {
     case 1:
-        return launch_mfma_pass<ENC, 1>(waves, jobs, stream);
+        return launch_mfma_pass<ENC, 1, PACKED>(waves, jobs, stream);
     case 2:
-        return launch_mfma_pass<ENC, 2>(waves, jobs, stream);
+        return launch_mfma_pass<ENC, 2, PACKED>(waves, jobs, stream);
     case 4:
-        return launch_mfma_pass<ENC, 4>(waves, jobs, stream);
+        return launch_mfma_pass<ENC, 4, PACKED>(waves, jobs, stream);
     default:
-        return launch_mfma_pass<ENC, 8>(waves, jobs, stream);
+        return launch_mfma_pass<ENC, 8, PACKED>(waves, jobs, stream);
     }
 }
 
-template <int ENC>
+// `rows` activation rows in passes of the plan's batch (the largest power of two that
+// fits what is left).  `row_bytes` is unused over packed weights.
+template <int ENC, bool PACKED>
 int launch_mfma(const void* w, size_t row_bytes, const float* x, size_t rows, size_t in,
                 size_t out, float* y, size_t stride, unsigned* status, hipStream_t stream) {
     MfmaPlan p;
-    if (!plan_mfma(rows, in, out, p))
+    if (!plan_mfma(rows, in, out, p, PACKED))
         return KDQ_ERR_UNSUPPORTED;
     for (size_t first = 0; first < rows;) {
         const size_t left = rows - first;
@@ -1066,11 +1148,105 @@ int launch_mfma(const void* w, size_t row_bytes, const float* x, size_t rows, si
         jobs.job[0] = MfmaJob{static_cast<const uint8_t*>(w), x + first * in, y + first * stride,
                               status, row_bytes, stride, unsigned(out), 0};
         number_workgroups(jobs, p.rows_per_wg);
-        const int rc = launch_mfma_rows<ENC>(r, p.waves, jobs, stream);
+        const int rc = launch_mfma_rows<ENC, PACKED>(r, p.waves, jobs, stream);
         if (rc)
             return rc;
         first += r;
     }
+    return KDQ_OK;
+}
+
+template <bool PACKED>
+int launch_mfma_any(int encoding, const void* w, size_t row_bytes, const float* x, size_t rows,
+                    size_t in, size_t out, float* y, size_t stride, unsigned* status,
+                    hipStream_t s) {
+    switch (encoding) {
+    case KDQ_Q8_0:
+        return launch_mfma<KDQ_Q8_0, PACKED>(w, row_bytes, x, rows, in, out, y, stride, status, s);
+    case KDQ_Q4_0:
+        return launch_mfma<KDQ_Q4_0, PACKED>(w, row_bytes, x, rows, in, out, y, stride, status, s);
+    default:
+        return launch_mfma<KDQ_Q4_K, PACKED>(w, row_bytes, x, rows, in, out, y, stride, status, s);
+    }
+}
+
+// ------------------------------------------------------------- packing
+
+size_t packed_unit(int encoding) {
+    switch (encoding) {
+    case KDQ_Q4_K:
+        return PackedFormat<KDQ_Q4_K>::unit;
+    case KDQ_Q4_0:
+        return PackedFormat<KDQ_Q4_0>::unit;
+    case KDQ_Q8_0:
+        return PackedFormat<KDQ_Q8_0>::unit;
+    default:
+        return 0;
+    }
+}
+
+// Four bytes from any alignment, little-endian.
+__device__ __forceinline__ unsigned bytes4(const uint8_t* p) {
+    return unsigned(p[0]) | unsigned(p[1]) << 8 | unsigned(p[2]) << 16 | unsigned(p[3]) << 24;
+}
+
+__device__ __forceinline__ uint4 bytes16(const uint8_t* p) {
+    return make_uint4(bytes4(p), bytes4(p + 4), bytes4(p + 8), bytes4(p + 12));
+}
+
+// One thread per (tile, group, lane): writes that lane's code pieces and side data of
+// the unit (PackedFormat layout); rows past `out` are written as zeros.
+template <int ENC>
+__global__ __launch_bounds__(256) void pack_kernel(const uint8_t* __restrict__ raw,
+                                                   size_t row_bytes, unsigned groups,
+                                                   unsigned out, size_t lanes,
+                                                   uint8_t* __restrict__ packed) {
+    const size_t id = size_t(blockIdx.x) * 256 + threadIdx.x;
+    if (id >= lanes)
+        return;
+    constexpr int P = PackedFormat<ENC>::pieces;
+    const unsigned l = unsigned(id % 64), G = l / 16, s = l % 16;
+    const size_t unit_index = id / 64;
+    const unsigned g = unsigned(unit_index % groups);
+    const size_t n = (unit_index / groups) * 16 + s;
+    uint8_t* unit = packed + unit_index * PackedFormat<ENC>::unit;
+    const bool live = n < out;
+    const uint8_t* row = raw + (live ? n : 0) * row_bytes;
+    const uint4 zero = make_uint4(0, 0, 0, 0);
+    if constexpr (ENC == KDQ_Q4_K) {
+        const uint8_t* block = row + size_t(g) * 144;
+#pragma unroll
+        for (int p = 0; p < P; ++p)
+            *reinterpret_cast<uint4*>(unit + p * 1024 + 16 * l) =
+                live ? bytes16(block + 16 + 32 * G + 16 * p) : zero;
+        if (G == 0)
+            *reinterpret_cast<uint4*>(unit + P * 1024 + 16 * s) = live ? bytes16(block) : zero;
+    } else {
+        constexpr int bytes = Format<ENC>::bytes;
+        const uint8_t* b0 = row + (size_t(g) * 8 + 2 * G) * bytes;
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const uint8_t* src = ENC == KDQ_Q4_0 ? b0 + p * bytes + 2
+                                                 : b0 + (p / 2) * bytes + 2 + 16 * (p % 2);
+            *reinterpret_cast<uint4*>(unit + p * 1024 + 16 * l) = live ? bytes16(src) : zero;
+        }
+        const unsigned side = live ? (half_bits_at(b0) | half_bits_at(b0 + bytes) << 16) : 0u;
+        *reinterpret_cast<unsigned*>(unit + P * 1024 + 4 * l) = side;
+    }
+}
+
+template <int ENC>
+int launch_pack(const void* raw, size_t row_bytes, size_t in, size_t out, void* packed,
+                hipStream_t stream) {
+    const size_t groups = in / 256, tiles = (out + 15) / 16;
+    const size_t lanes = tiles * groups * 64;
+    const size_t grid = (lanes + 255) / 256;
+    if (grid > 0x7fffffffu)
+        return KDQ_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL((pack_kernel<ENC>), dim3(unsigned(grid)), dim3(256), 0, stream,
+                       static_cast<const uint8_t*>(raw), row_bytes, unsigned(groups),
+                       unsigned(out), lanes, static_cast<uint8_t*>(packed));
+    KDQ_HIP(hipGetLastError());
     return KDQ_OK;
 }
 
@@ -1165,17 +1341,8 @@ extern "C" int kdq_gemv(int encoding, const void* weights, size_t row_bytes, con
     // Shapes the streaming kernels do not take run on the exact kernel.
     const bool fast = streams(encoding, weights, row_bytes, in);
     if (fast) {
-        switch (encoding) {
-        case KDQ_Q8_0:
-            rc = launch_mfma<KDQ_Q8_0>(weights, row_bytes, x, rows, in, out, y, stride, status, s);
-            break;
-        case KDQ_Q4_0:
-            rc = launch_mfma<KDQ_Q4_0>(weights, row_bytes, x, rows, in, out, y, stride, status, s);
-            break;
-        default:
-            rc = launch_mfma<KDQ_Q4_K>(weights, row_bytes, x, rows, in, out, y, stride, status, s);
-            break;
-        }
+        rc = launch_mfma_any<false>(encoding, weights, row_bytes, x, rows, in, out, y, stride,
+                                    status, s);
         if (rc != KDQ_ERR_UNSUPPORTED)
             return rc;
         switch (encoding) {
@@ -1196,17 +1363,91 @@ extern "C" int kdq_gemv(int encoding, const void* weights, size_t row_bytes, con
                           stream);
 }
 
+extern "C" size_t kdq_gguf_packed_bytes(int encoding, size_t in, size_t out) {
+    const size_t unit = packed_unit(encoding);
+    if (!unit || !in || !out || in % 256 || in > 0xffffffffu || out > 0xffffffffu)
+        return 0;
+    const size_t units = (out + 15) / 16 * (in / 256);
+    return mul_overflows(units, unit) ? 0 : units * unit;
+}
+
+extern "C" int kdq_gguf_pack(int encoding, const void* weights, size_t row_bytes, size_t in,
+                             size_t out, void* packed, void* stream) {
+    if (!block_values(encoding))
+        return KDQ_ERR_UNSUPPORTED;
+    if (!weights || !packed || !in || !out)
+        return KDQ_ERR_ARGUMENT;
+    const size_t bytes = kdq_gguf_packed_bytes(encoding, in, out);
+    if (!bytes || row_bytes < in / block_values(encoding) * block_bytes(encoding))
+        return KDQ_ERR_SHAPE;
+    if (mul_overflows(out, row_bytes))
+        return KDQ_ERR_ARGUMENT;
+    if (!aligned(packed, 16))
+        return KDQ_ERR_ALIGNMENT;
+    if (overlaps(packed, bytes, weights, out * row_bytes))
+        return KDQ_ERR_ALIAS;
+    auto s = static_cast<hipStream_t>(stream);
+    switch (encoding) {
+    case KDQ_Q8_0:
+        return launch_pack<KDQ_Q8_0>(weights, row_bytes, in, out, packed, s);
+    case KDQ_Q4_0:
+        return launch_pack<KDQ_Q4_0>(weights, row_bytes, in, out, packed, s);
+    default:
+        return launch_pack<KDQ_Q4_K>(weights, row_bytes, in, out, packed, s);
+    }
+}
+
+namespace kdq {
+namespace {
+
+// Argument checks of the packed product entry points (check_product with the packed
+// size in place of out * row_bytes, and 16-byte aligned packed weights).
+int check_packed(int encoding, const void* packed, const float* x, size_t rows, size_t in,
+                 size_t out, const float* y, size_t stride) {
+    if (!block_values(encoding))
+        return KDQ_ERR_UNSUPPORTED;
+    if (!packed || !x || !y || !rows || !in || !out)
+        return KDQ_ERR_ARGUMENT;
+    const size_t bytes = kdq_gguf_packed_bytes(encoding, in, out);
+    if (!bytes || stride < out || rows > 4096)
+        return KDQ_ERR_SHAPE;
+    if (mul_overflows(rows, in) || mul_overflows(rows, stride))
+        return KDQ_ERR_ARGUMENT;
+    const size_t ybytes = ((rows - 1) * stride + out) * sizeof(float);
+    if (overlaps(y, ybytes, packed, bytes) || overlaps(y, ybytes, x, rows * in * sizeof(float)))
+        return KDQ_ERR_ALIAS;
+    if (!aligned(x, 16) || !aligned(packed, 16))
+        return KDQ_ERR_ALIGNMENT;
+    return KDQ_OK;
+}
+
+}  // namespace
+}  // namespace kdq
+
+extern "C" int kdq_gemv_packed(int encoding, const void* packed, const float* x, size_t rows,
+                               size_t in, size_t out, float* y, size_t stride,
+                               unsigned* status, void* stream) {
+    const int rc = check_packed(encoding, packed, x, rows, in, out, y, stride);
+    if (rc)
+        return rc;
+    // no other kernel reads the packed layout: shapes beyond the MFMA kernel's LDS
+    // (in above ~32K values) are unsupported here
+    return launch_mfma_any<true>(encoding, packed, 0, x, rows, in, out, y, stride, status,
+                                 static_cast<hipStream_t>(stream));
+}
+
 namespace kdq {
 namespace {
 
 // One fused MFMA launch for jobs[idx[0..n)] (same encoding, rows, in; checked).
+template <bool PACKED>
 int launch_fused(const kdq_matvec_job* jobs, const size_t* idx, size_t n, hipStream_t stream) {
     const kdq_matvec_job& j0 = jobs[idx[0]];
     size_t total = 0;
     for (size_t k = 0; k < n; ++k)
         total += jobs[idx[k]].columns;
     MfmaPlan p;
-    if (!plan_mfma(j0.rows, j0.in, total, p))
+    if (!plan_mfma(j0.rows, j0.in, total, p, PACKED))
         return KDQ_ERR_UNSUPPORTED;
     MfmaJobs mj{};
     mj.count = unsigned(n);
@@ -1214,25 +1455,65 @@ int launch_fused(const kdq_matvec_job* jobs, const size_t* idx, size_t n, hipStr
     for (size_t k = 0; k < n; ++k) {
         const kdq_matvec_job& j = jobs[idx[k]];
         mj.job[k] = MfmaJob{static_cast<const uint8_t*>(j.weights), j.input, j.output,
-                            j.status, j.row_bytes, j.stride, j.columns, 0};
+                            j.status, PACKED ? 0 : j.row_bytes, j.stride, j.columns, 0};
     }
     number_workgroups(mj, p.rows_per_wg);
     switch (j0.encoding) {
     case KDQ_Q8_0:
-        return launch_mfma_rows<KDQ_Q8_0>(j0.rows, p.waves, mj, stream);
+        return launch_mfma_rows<KDQ_Q8_0, PACKED>(j0.rows, p.waves, mj, stream);
     case KDQ_Q4_0:
-        return launch_mfma_rows<KDQ_Q4_0>(j0.rows, p.waves, mj, stream);
+        return launch_mfma_rows<KDQ_Q4_0, PACKED>(j0.rows, p.waves, mj, stream);
     default:
-        return launch_mfma_rows<KDQ_Q4_K>(j0.rows, p.waves, mj, stream);
+        return launch_mfma_rows<KDQ_Q4_K, PACKED>(j0.rows, p.waves, mj, stream);
     }
 }
 
-// Jobs the fused launch takes: streaming shapes whose rows fit one pass of the MFMA
-// kernel (1, 2, 4 or 8 rows, within its LDS batch).
-bool fusable(const kdq_matvec_job& j) {
+// Jobs the fused launch takes: shapes whose rows fit one pass of the MFMA kernel (1, 2,
+// 4 or 8 rows, within its LDS batch), streaming ones when the weights are row-major.
+bool fusable(const kdq_matvec_job& j, bool packed) {
     MfmaPlan p;
-    return streams(j.encoding, j.weights, j.row_bytes, j.in) && (j.rows & (j.rows - 1)) == 0 &&
-           plan_mfma(j.rows, j.in, j.columns, p) && p.batch >= j.rows;
+    return (packed || streams(j.encoding, j.weights, j.row_bytes, j.in)) &&
+           (j.rows & (j.rows - 1)) == 0 && plan_mfma(j.rows, j.in, j.columns, p, packed) &&
+           p.batch >= j.rows;
+}
+
+// kdq_gemv_batch / kdq_gemv_packed_batch after validation: jobs of one shape (encoding,
+// rows, in) run together, up to kMaxFused per launch, in submission order; the rest one
+// launch each.
+template <bool PACKED>
+int run_batch(const kdq_matvec_job* jobs, size_t count, void* stream) {
+    auto s = static_cast<hipStream_t>(stream);
+    std::vector<char> done(count, 0);
+    for (size_t i = 0; i < count; ++i) {
+        if (done[i] || !fusable(jobs[i], PACKED))
+            continue;
+        size_t idx[kMaxFused], n = 0;
+        for (size_t k = i; k < count && n < size_t(kMaxFused); ++k) {
+            const auto& a = jobs[i];
+            const auto& b = jobs[k];
+            if (!done[k] && b.encoding == a.encoding && b.rows == a.rows && b.in == a.in &&
+                fusable(b, PACKED))
+                idx[n++] = k;
+        }
+        const int rc = launch_fused<PACKED>(jobs, idx, n, s);
+        if (rc)
+            return rc;
+        for (size_t k = 0; k < n; ++k)
+            done[idx[k]] = 1;
+    }
+    for (size_t i = 0; i < count; ++i) {
+        if (done[i])
+            continue;
+        const auto& j = jobs[i];
+        const int rc =
+            PACKED ? kdq_gemv_packed(j.encoding, j.weights, j.input, j.rows, j.in, j.columns,
+                                     j.output, j.stride, j.status, stream)
+                   : kdq_gemv(j.encoding, j.weights, j.row_bytes, j.input, j.rows, j.in,
+                              j.columns, j.output, j.stride, j.status, stream);
+        if (rc)
+            return rc;
+    }
+    return KDQ_OK;
 }
 
 }  // namespace
@@ -1249,35 +1530,18 @@ extern "C" int kdq_gemv_batch(const kdq_matvec_job* jobs, size_t count, void* st
         if (rc)
             return rc;
     }
-    auto s = static_cast<hipStream_t>(stream);
-    // Jobs of one shape (encoding, rows, in) run together, up to kMaxFused per launch, in
-    // submission order; the rest one launch each.
-    std::vector<char> done(count, 0);
+    return run_batch<false>(jobs, count, stream);
+}
+
+extern "C" int kdq_gemv_packed_batch(const kdq_matvec_job* jobs, size_t count, void* stream) {
+    if (count && !jobs)
+        return KDQ_ERR_ARGUMENT;
     for (size_t i = 0; i < count; ++i) {
-        if (done[i] || !fusable(jobs[i]))
-            continue;
-        size_t idx[kMaxFused], n = 0;
-        for (size_t k = i; k < count && n < size_t(kMaxFused); ++k) {
-            const auto& a = jobs[i];
-            const auto& b = jobs[k];
-            if (!done[k] && b.encoding == a.encoding && b.rows == a.rows && b.in == a.in &&
-                fusable(b))
-                idx[n++] = k;
-        }
-        const int rc = launch_fused(jobs, idx, n, s);
-        if (rc)
-            return rc;
-        for (size_t k = 0; k < n; ++k)
-            done[idx[k]] = 1;
-    }
-    for (size_t i = 0; i < count; ++i) {
-        if (done[i])
-            continue;
         const auto& j = jobs[i];
-        const int rc = kdq_gemv(j.encoding, j.weights, j.row_bytes, j.input, j.rows, j.in,
-                                j.columns, j.output, j.stride, j.status, stream);
+        const int rc = check_packed(j.encoding, j.weights, j.input, j.rows, j.in, j.columns,
+                                    j.output, j.stride);
         if (rc)
             return rc;
     }
-    return KDQ_OK;
+    return run_batch<true>(jobs, count, stream);
 }

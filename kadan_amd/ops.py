@@ -70,6 +70,57 @@ def gemv_batch(jobs: list[dict]) -> None:
     call("kdq_gemv_batch", C.addressof(table) if jobs else None, len(jobs), _stream())
 
 
+def gguf_packed_bytes(encoding: int, n_in: int, n_out: int) -> int:
+    return int(lib().kdq_gguf_packed_bytes(encoding, n_in, n_out))
+
+
+def gguf_pack(encoding: int, weights: torch.Tensor, n_in: int) -> torch.Tensor:
+    """Row-major packed rows uint8 [n_out, row_bytes] -> the tile-packed resident form,
+    uint8 [kdq_gguf_packed_bytes] (kdq_gguf_pack)."""
+    _need(weights, torch.uint8, "weights")
+    n_out = weights.shape[0]
+    nbytes = gguf_packed_bytes(encoding, n_in, n_out)
+    if not nbytes:
+        raise ValueError("shape has no packed form (in % 256 != 0)")
+    out = torch.empty(nbytes, dtype=torch.uint8, device=weights.device)
+    call("kdq_gguf_pack", encoding, weights.data_ptr(), weights.shape[1], n_in, n_out,
+         out.data_ptr(), _stream())
+    return out
+
+
+def gemv_packed(encoding: int, packed: torch.Tensor, x: torch.Tensor, n_out: int,
+                out: torch.Tensor | None = None,
+                status: torch.Tensor | None = None) -> torch.Tensor:
+    """gemv over tile-packed weights (kdq_gemv_packed)."""
+    _need(packed, torch.uint8, "packed")
+    _need(x, torch.float32, "x")
+    x2 = x.reshape(-1, x.shape[-1])
+    rows, n_in = x2.shape
+    if packed.numel() != gguf_packed_bytes(encoding, n_in, n_out):
+        raise ValueError("packed size does not match (encoding, n_in, n_out)")
+    if out is None:
+        out = torch.empty(rows, n_out, dtype=torch.float32, device=x.device)
+    call("kdq_gemv_packed", encoding, packed.data_ptr(), x2.data_ptr(), rows, n_in, n_out,
+         out.data_ptr(), out.stride(0) if out.dim() == 2 else n_out, _ptr(status), _stream())
+    return out
+
+
+def gemv_packed_batch(jobs: list[dict]) -> None:
+    """One submission over packed weights (kdq_gemv_packed_batch).  Each job: dict with
+    encoding, weights (packed uint8), columns, input (fp32 [rows, in]), output
+    (fp32 [rows, stride]), optional status."""
+    import ctypes as C
+    table = (MatvecJob * len(jobs))()
+    for i, j in enumerate(jobs):
+        w, x, y = j["weights"], j["input"], j["output"]
+        x2 = x.reshape(-1, x.shape[-1])
+        table[i] = MatvecJob(w.data_ptr(), x2.data_ptr(), y.data_ptr(),
+                             _ptr(j.get("status")) or 0, 0,
+                             y.stride(0) if y.dim() == 2 else j["columns"],
+                             x2.shape[1], j["columns"], x2.shape[0], j["encoding"])
+    call("kdq_gemv_packed_batch", C.addressof(table) if jobs else None, len(jobs), _stream())
+
+
 def quantize_q8(x_f16: torch.Tensor):
     """fp16 [m, k] -> (int8 [m, k], fp32 [m, k/32]) (kdq_quantize_q8)."""
     _need(x_f16, torch.float16, "x")

@@ -121,3 +121,34 @@ def test_product_path_has_no_cpu_fallback(monkeypatch, tmp_path):
     monkeypatch.setattr(kadan_amd, "_lib", None)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         kadan_amd.lib()
+
+
+def test_gguf_packed_geometry_and_argument_errors():
+    import kadan_amd
+    lib = kadan_amd.lib()
+    # tiles of 16 rows x groups of 256 values, one unit of 16 x group bytes each
+    assert lib.kdq_gguf_packed_bytes(12, 4096, 14336) == 14336 * 2304
+    assert lib.kdq_gguf_packed_bytes(12, 256, 17) == 2 * 2304
+    assert lib.kdq_gguf_packed_bytes(8, 512, 16) == 2 * 4352
+    assert lib.kdq_gguf_packed_bytes(2, 512, 1) == 2 * 2304
+    assert lib.kdq_gguf_packed_bytes(2, 96, 16) == 0
+    assert lib.kdq_gguf_packed_bytes(3, 256, 16) == 0
+    pack = lib.kdq_gguf_pack
+    assert pack(3, FAKE_W, 144, 256, 16, FAKE_Y, None) == 3
+    assert pack(12, None, 144, 256, 16, FAKE_Y, None) == 1
+    assert pack(12, FAKE_W, 100, 256, 16, FAKE_Y, None) == 2
+    assert pack(2, FAKE_W, 54, 96, 16, FAKE_Y, None) == 2
+    assert pack(12, FAKE_W, 144, 256, 16, FAKE_Y + 4, None) == 7
+    assert pack(12, FAKE_W, 144, 256, 16, FAKE_W + 256, None) == 4
+    gp = lib.kdq_gemv_packed
+    assert gp(12, FAKE_W, FAKE_X, 1, 200, 4, FAKE_Y, 4, None, None) == 2
+    assert gp(12, FAKE_W, FAKE_X, 1, 256, 4, FAKE_Y, 3, None, None) == 2
+    assert gp(12, FAKE_W, FAKE_X, 4097, 256, 4, FAKE_Y, 4, None, None) == 2
+    assert gp(12, FAKE_W, FAKE_X, 1, 256, 4, FAKE_W + 16, 4, None, None) == 4
+    assert gp(12, FAKE_W + 4, FAKE_X, 1, 256, 4, FAKE_Y, 4, None, None) == 7
+    assert gp(12, FAKE_W, FAKE_X + 4, 1, 256, 4, FAKE_Y, 4, None, None) == 7
+    jobs = (kadan_amd.MatvecJob * 2)()
+    jobs[0] = kadan_amd.MatvecJob(FAKE_W, FAKE_X, FAKE_Y, 0, 0, 4, 256, 4, 1, 12)
+    jobs[1] = kadan_amd.MatvecJob(FAKE_W, FAKE_X, FAKE_Y + 4096, 0, 0, 4, 200, 4, 1, 12)
+    assert lib.kdq_gemv_packed_batch(C.addressof(jobs), 2, None) == 2
+    assert lib.kdq_gemv_packed_batch(None, 0, None) == 0
