@@ -129,6 +129,12 @@ int kdq_gemv_packed(int encoding, const void* packed, const float* x, size_t row
  * ignored).  Counterpart of launch_matvec over a submission, h3_compute.cu:367-382. */
 int kdq_gemv_packed_batch(const kdq_matvec_job* jobs, size_t count, void* stream);
 
+/* 1 when kdq_gemv_packed takes rows of `in` values of this encoding (a packed form
+ * exists and the staged activations fit the kernel's LDS), else 0.  Lets a weight bank
+ * choose the resident layout before packing (the reference's gguf_batch_supported,
+ * IW/include/kadan/gguf_batch_partition.hpp:15-37, plays this role for its bank). */
+int kdq_gemv_packed_supported(int encoding, size_t in);
+
 /* ---- prefill Q4_0 GEMM (no reference device counterpart; the reference decodes to
  * F32 and calls cublasSgemm, IW/src/cuda/h3_compute.cu:2451, and its CPU path runs
  * ggml vec_dot_q4_0_q8_0, G/src/ggml-cpu/quants.c:225-260).

@@ -136,10 +136,13 @@ private:
     struct Resident;
     using BankKey = std::tuple<WeightIdentity, int, std::size_t, std::size_t>;
 
+    // The resident weights of one projection, uploaded through the pinned staging on a
+    // miss.  `product`: for the decode-time product (tile-packed where the packed kernel
+    // takes the shape), else row-major rows (the prefill GEMM).
     const Resident& weights_for(const WeightIdentity&, gguf::Encoding, std::size_t in,
                                 std::size_t out, const GgufWeightSource&, bool retain,
                                 const std::atomic_bool& cancel,
-                                std::unique_ptr<Resident>& transient);
+                                std::unique_ptr<Resident>& transient, bool product);
     void* device_buffer(std::size_t slot, std::size_t bytes);
     void synchronize();
 

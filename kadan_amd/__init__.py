@@ -61,6 +61,7 @@ _OTHER = {
     "kdq_block_bytes": (_SZ, [_I]),
     "kdq_row_bytes": (_SZ, [_I, _SZ]),
     "kdq_gguf_packed_bytes": (_SZ, [_I, _SZ, _SZ]),
+    "kdq_gemv_packed_supported": (_I, [_I, _SZ]),
     "kdq_moe_mxfp4_packed_bytes": (_SZ, [_SZ, _SZ, _SZ]),
 }
 

@@ -152,6 +152,7 @@ std::size_t block_bytes(Encoding e) {
 struct HipDenseCompute::Resident {
     void* device = nullptr;
     std::size_t bytes = 0, row_bytes = 0;
+    bool packed = false;  // the tile-packed layout of kdq_gguf_pack (else row-major rows)
     ~Resident() {
         if (device)
             (void)hipFree(device);
@@ -202,16 +203,23 @@ void* HipDenseCompute::device_buffer(std::size_t slot, std::size_t bytes) {
 const HipDenseCompute::Resident& HipDenseCompute::weights_for(
     const WeightIdentity& identity, gguf::Encoding enc, std::size_t in, std::size_t out,
     const GgufWeightSource& source, bool retain, const std::atomic_bool& cancel,
-    std::unique_ptr<Resident>& transient) {
-    const BankKey key{identity, int(enc), in, out};
+    std::unique_ptr<Resident>& transient, bool product) {
+    // Products keep the tile-packed layout when the packed kernel takes the shape; the
+    // prefill GEMM reads row-major rows.  The layout is part of the bank key.
+    const bool packed = product && kdq_gemv_packed_supported(ggml_type(enc), in);
+    const BankKey key{identity, 2 * int(enc) + (packed ? 1 : 0), in, out};
     if (auto it = bank_.find(key); it != bank_.end())
         return *it->second;
     const std::size_t row_bytes = in / gguf::block_values(enc) * gguf::block_bytes(enc);
     auto r = std::make_unique<Resident>();
     r->row_bytes = row_bytes;
-    r->bytes = out * row_bytes;
+    r->packed = packed;
+    r->bytes = packed ? kdq_gguf_packed_bytes(ggml_type(enc), in, out) : out * row_bytes;
     hip_check(hipMalloc(&r->device, r->bytes));
-    const std::size_t rows_per_chunk = std::max<std::size_t>(1, kStagingBytes / row_bytes);
+    // chunks of whole 16-row tiles when packing (each chunk packs into its own tiles)
+    std::size_t rows_per_chunk = std::max<std::size_t>(1, kStagingBytes / row_bytes);
+    if (packed)
+        rows_per_chunk = std::max<std::size_t>(16, rows_per_chunk / 16 * 16);
     const std::size_t chunk_bytes = std::min(out, rows_per_chunk) * row_bytes;
     if (pinned_bytes_ < chunk_bytes) {
         if (pinned_)
@@ -221,15 +229,24 @@ const HipDenseCompute::Resident& HipDenseCompute::weights_for(
         hip_check(hipHostMalloc(&pinned_, chunk_bytes, hipHostMallocDefault));
         pinned_bytes_ = chunk_bytes;
     }
+    const std::size_t tile_bytes = packed ? kdq_gguf_packed_bytes(ggml_type(enc), in, 16) : 0;
+    auto* raw = packed ? static_cast<std::uint8_t*>(device_buffer(4, chunk_bytes)) : nullptr;
     auto* bytes = static_cast<std::byte*>(pinned_);
+    auto st = static_cast<hipStream_t>(stream_);
     for (std::size_t first = 0; first < out; first += rows_per_chunk) {
         require(!cancel.load(), "kdq_cancelled");
         const std::size_t n = std::min(rows_per_chunk, out - first);
         source(first, std::span<std::byte>(bytes, n * row_bytes));
-        hip_check(hipMemcpyAsync(static_cast<std::uint8_t*>(r->device) + first * row_bytes,
-                                 pinned_, n * row_bytes, hipMemcpyHostToDevice,
-                                 static_cast<hipStream_t>(stream_)));
-        synchronize();  // the staging buffer is reused by the next chunk
+        if (packed) {
+            hip_check(hipMemcpyAsync(raw, pinned_, n * row_bytes, hipMemcpyHostToDevice, st));
+            kdq_check(kdq_gguf_pack(ggml_type(enc), raw, row_bytes, in, n,
+                                    static_cast<std::uint8_t*>(r->device) + first / 16 * tile_bytes,
+                                    st));
+        } else {
+            hip_check(hipMemcpyAsync(static_cast<std::uint8_t*>(r->device) + first * row_bytes,
+                                     pinned_, n * row_bytes, hipMemcpyHostToDevice, st));
+        }
+        synchronize();  // the staging buffers are reused by the next chunk
     }
     if (!retain) {
         transient = std::move(r);
@@ -261,7 +278,8 @@ ProjectionResult HipDenseCompute::dense_gguf_source(
     hip_check(hipSetDevice(device_));
     const std::size_t rows = input.size() / in;
     std::unique_ptr<Resident> transient;
-    const Resident& w = weights_for(identity, enc, in, out, source, retain_misses, cancel, transient);
+    const Resident& w = weights_for(identity, enc, in, out, source, retain_misses, cancel, transient,
+                                    true);
     auto st = static_cast<hipStream_t>(stream_);
     auto* dx = static_cast<float*>(device_buffer(0, rows * in * sizeof(float)));
     auto* dy = static_cast<float*>(device_buffer(1, rows * out * sizeof(float)));
@@ -271,8 +289,10 @@ ProjectionResult HipDenseCompute::dense_gguf_source(
     for (std::size_t first = 0; first < rows; first += gguf_batch_max_rows) {
         require(!cancel.load(), "kdq_cancelled");
         const std::size_t n = std::min(gguf_batch_max_rows, rows - first);
-        kdq_check(kdq_gemv(ggml_type(enc), w.device, w.row_bytes, dx + first * in, n, in, out,
-                           dy + first * out, out, dstatus, st));
+        kdq_check(w.packed ? kdq_gemv_packed(ggml_type(enc), w.device, dx + first * in, n, in,
+                                             out, dy + first * out, out, dstatus, st)
+                           : kdq_gemv(ggml_type(enc), w.device, w.row_bytes, dx + first * in, n,
+                                      in, out, dy + first * out, out, dstatus, st));
     }
     unsigned status = 0;
     hip_check(hipMemcpyAsync(output.data(), dy, output.size_bytes(), hipMemcpyDeviceToHost, st));
@@ -320,7 +340,8 @@ ProjectionResult HipDenseCompute::dense_gguf_batch(std::span<const GgufBatchJob>
     std::vector<const Resident*> weights(jobs.size());
     for (std::size_t i = 0; i < jobs.size(); ++i)
         weights[i] = &weights_for(*jobs[i].identity, *jobs[i].encoding, jobs[i].in, jobs[i].out,
-                                  *jobs[i].source, jobs[i].retain_misses, cancel, transients[i]);
+                                  *jobs[i].source, jobs[i].retain_misses, cancel, transients[i],
+                                  true);
     // One upload of each distinct input span, one device output region per job.
     std::vector<std::size_t> input_at(jobs.size()), output_at(jobs.size());
     std::size_t in_bytes = 0, out_bytes = 0;
@@ -366,7 +387,15 @@ ProjectionResult HipDenseCompute::dense_gguf_batch(std::span<const GgufBatchJob>
                                   ggml_type(*j.encoding)};
     }
     require(!cancel.load(), "kdq_cancelled");
-    kdq_check(kdq_gemv_batch(table.data(), table.size(), st));
+    // packed and row-major residents go in one submission each (jobs keep their order
+    // within each; every job writes its own output region)
+    std::vector<kdq_matvec_job> packed_jobs, row_jobs;
+    for (std::size_t i = 0; i < jobs.size(); ++i)
+        (weights[i]->packed ? packed_jobs : row_jobs).push_back(table[i]);
+    if (!packed_jobs.empty())
+        kdq_check(kdq_gemv_packed_batch(packed_jobs.data(), packed_jobs.size(), st));
+    if (!row_jobs.empty())
+        kdq_check(kdq_gemv_batch(row_jobs.data(), row_jobs.size(), st));
     for (std::size_t i = 0; i < jobs.size(); ++i)
         hip_check(hipMemcpyAsync(jobs[i].output.data(), dy + output_at[i],
                                  jobs[i].output.size_bytes(), hipMemcpyDeviceToHost, st));
@@ -392,7 +421,8 @@ ProjectionResult HipDenseCompute::dense_gguf_q8_source(
     hip_check(hipSetDevice(device_));
     const std::size_t rows = input.size() / in;
     std::unique_ptr<Resident> transient;
-    const Resident& w = weights_for(identity, enc, in, out, source, true, cancel, transient);
+    const Resident& w = weights_for(identity, enc, in, out, source, true, cancel, transient,
+                                    false);
     auto st = static_cast<hipStream_t>(stream_);
     auto* dx = static_cast<std::uint16_t*>(device_buffer(0, input.size_bytes()));
     auto* dy = static_cast<std::uint16_t*>(device_buffer(1, output.size_bytes()));

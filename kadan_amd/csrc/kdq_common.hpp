@@ -22,6 +22,17 @@ __device__ __forceinline__ unsigned load4(const uint8_t* p) {
     return *reinterpret_cast<const unsigned*>(p);
 }
 
+// Non-temporal (streaming) variants for weight bytes read once per launch: the loads
+// carry the nt cache policy so a weight stream larger than the caches does not evict
+// what is reused (activations, outputs).  Same alignment rules as load16 / load4.
+__device__ __forceinline__ u32x4 stream16(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+__device__ __forceinline__ unsigned stream4(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(p));
+}
+
 // Exact IEEE binary16 -> binary32 by integer construction (keeps NaN payloads),
 // IW/include/kadan/gguf_quantization.hpp:576-593 semantics.
 __device__ __forceinline__ float half_exact(unsigned h) {

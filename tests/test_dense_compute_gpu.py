@@ -253,3 +253,18 @@ def test_moe_mxfp4_host_layer(probe, oracle):
     assert res == FINITE and np.array_equal(y, y2) and probe.retained == banked
     assert probe.release(31) == banked
     probe.release_scratch()
+
+
+def test_bank_keeps_products_packed(probe, oracle):
+    """The bank keeps weights for the decode-time product in the tile-packed form (16-row
+    tiles: 40 rows occupy 48 rows' bytes) and returns the same results from it."""
+    import kadan_amd
+    n_in, n_out, rows = 512, 40, 3
+    w = synth.gguf_weights(Q4_K, 0xDA, n_out, n_in)
+    x = synth.normal(0xDB, rows, rows * n_in).reshape(rows, n_in)
+    res, y = probe.gguf(41, Q4_K, w, x, n_out)
+    assert res == FINITE
+    assert_close(y, oracle.gemv(Q4_K, w, x, n_in, n_out), what="packed bank")
+    packed = kadan_amd.lib().kdq_gguf_packed_bytes(Q4_K, n_in, n_out)
+    assert packed == 3 * 2 * 2304 and probe.retained == packed
+    assert probe.release(41) == packed and probe.retained == 0
