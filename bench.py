@@ -390,7 +390,9 @@ def bench_moe(torch, tokens, experts, hot, seed, copies, reps=10, count=10):
             "fp4_mfma_frac": round(tflops / FP4_PEAK_TFLOPS, 5),
             "bf16_mfma_frac": round(tflops / FP16_PEAK_TFLOPS, 4),
             "note": "resident weights in the packed layout (packed once, outside the timed "
-                    "region); products on bf16 MFMA over exactly dequantised FP4 weights"}
+                    "region); grouped GEMMs on the scaled MFMA v_mfma_scale_f32_32x32x64_f8f6f4 "
+                    "(FP4 E2M1 weights with their E8M0 scales as they lie, activations as FP8 "
+                    "E4M3 terms with E8M0 block scales: 2 terms for x, 3 for h)"}
 
 
 def _route_host(logits, top_k):

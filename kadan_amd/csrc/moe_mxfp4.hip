@@ -4,17 +4,18 @@
 // IW/src/weights/quantization.cpp:79-99,207-247, behind include/kadan_amd.h.
 //
 //   route_kernel      one wavefront per token: softmax (float exp, double total),
-//                     top-k by logit (equal logits keep the lower expert), renormalise
+//                     top-k by logit (equal logits keep the lower expert), renormalise;
+//                     the token's activations as FP8 terms with E8M0 block scales
 //   permute_kernel    one workgroup: stable counting sort of the slots by expert
 //                     (expert-major, slot ascending) plus the list of work items
 //                     (expert, first row) of at most kItemRows rows each
-//   gate_up_kernel    grouped GEMM over work items: gathered bf16 token rows x FP4
-//                     gate and up rows dequantized in registers to bf16
-//                     (v_cvt_scalef32_pk_bf16_fp4, exact), v_mfma_f32_32x32x16_bf16 with
-//                     fp32 accumulation, fused h = silu(g) * u stored as bf16 hi + lo
-//   down_kernel       grouped GEMM h x FP4 down rows (hi and lo terms), scaled by the
-//                     routing weight of the row's slot
-//   combine_kernel    y[t] = sum_i contribution[t*k + i] in selection order (float)
+//   gate_up_kernel    grouped GEMM over work items on the scaled MFMA
+//                     (v_mfma_scale_f32_32x32x64_f8f6f4): FP8 activation terms x the packed
+//                     FP4 gate and up rows with their E8M0 scales, fp32 accumulation, fused
+//                     h = silu(g) * u stored as FP8 terms for the down product
+//   finalize_kernel   (K-sliced decode only) slices summed in order, then h as above
+//   down_kernel       grouped GEMM h x FP4 down rows, fp32 partial rows per slot
+//   combine_kernel    y[t] = sum_i w[t*k + i] * down[t*k + i] in selection order (float)
 #include "kdq_common.hpp"
 
 #include <cmath>
@@ -277,106 +278,183 @@ __global__ __launch_bounds__(256) void pack_scales_kernel(const uint8_t* __restr
     out[u] = word;
 }
 
-// Grouped GEMMs on v_mfma_f32_32x32x16_bf16.  A workgroup of kGemmWaves wavefronts works
-// on one work item (expert e, up to kItemRows consecutive rows of its segment: one or two
-// MFMA row tiles of 32) and one K slice.  Every wavefront owns two 32-row weight groups
-// (gate and up of the same 32 features, or two groups of down rows) and multiplies each
-// staged activation fragment into both.  The weight operand B streams from the packed
-// layout: per 64-value step, lane (f = lane % 32, h = lane / 32) holds 32 FP4 values of its
-// row (16 bytes) and MFMA t takes values 32h + 8t .. +7 of them (the activation operand
-// uses the same k order), dequantized with v_cvt_scalef32_pk_bf16_fp4, which is exact.
-// The activation operand A (the item's occupied row tiles) is staged per chunk of steps
-// into LDS by the whole workgroup, double-buffered.  Each lane issues chunk c + 2's
-// activation loads, then chunk c + 1's weight loads, while chunk c is multiplied and chunk
-// c + 1 is stored to LDS; all loads are unconditional (indices past the end are clamped
-// to valid data), so each wait counts exactly the loads the next step needs.
+// ------------------------------------------------------------- FP8 activation tiles
+//
+// The grouped GEMMs run on v_mfma_scale_f32_32x32x64_f8f6f4: FP8 (E4M3) activations times
+// the FP4 (E2M1) weights, each operand with an E8M0 scale per 32 K values.  An activation
+// value is carried as a sum of FP8 terms sharing one block scale 2^e per 32 values (e such
+// that the block's largest magnitude lands in [128, 256)): term 1 is the value rounded to
+// E4M3 (round to nearest even), term 2 the remainder rounded, and so on.  Two terms hold
+// every bf16 value exactly (8 significant bits: 4 + 4; values under 2^-2 of the scale
+// keep an absolute error below 2^-10 of it); three terms carry h = silu(g) * u to about
+// 12 significant bits.  A block with a non-finite value gets the E8M0 NaN scale (255),
+// so every product that touches it is NaN, as in fp32.
+//
+// Activations reach the MFMAs as tiles: tile tau = 2 * item + t holds rows 32t .. 32t+31
+// of work item `item` (its slots in permutation order), gathered once so that every
+// wavefront load of an A operand is 1 KB contiguous, as the packed weights are.  For
+// step q (64 K values) of tile tau, with TERMS terms:
+//   codes  tile_codes(tau) + (q * TERMS + k) * 2048 + piece * 1024 + 16 * lane, 16 bytes:
+//          lane r + 32h holds row r's values 16h + i (piece 0) and 32 + 16h + i (piece 1)
+//          of the step, i = 0..15 (the lane's half of the MFMA A operand), term k
+//   scales tile_scales(tau) + (q / 4) * 256 + 4 * lane + q % 4: the E8M0 scale of row r's
+//          values 64q + 32h .. +31 (lane r + 32h supplies the scale of K block h)
+// codes of all tiles first (steps * TERMS * 2 KB each), then their scales
+// (ceil(steps / 4) * 256 bytes each).
 
-// Staged rows: PLANES planes of CHUNK steps of 64 bf16 values per row, 16 bytes of pad.
-template <int CHUNK, int PLANES> struct Stage {
-    static constexpr int pitch = CHUNK * PLANES * kStepK * 2 + 16;
-    static constexpr int buffer = kItemRows * pitch;
-    static constexpr int pieces = CHUNK * PLANES * 8;  // 16-byte pieces per row
+typedef int v8i32 __attribute__((ext_vector_type(8)));
+typedef int v4i32 __attribute__((ext_vector_type(4)));
+
+constexpr int kXTerms = 2, kHTerms = 3;
+
+struct Tiles {
+    uint8_t* codes;   // tile 0's codes
+    uint8_t* scales;  // tile 0's scales
+    size_t code_stride, scale_stride;  // bytes per tile
 };
 
-// This thread's share of a staged chunk of ROWS rows: pieces i = 0..per_thread-1 are row
-// (tid / pieces + i * rows_step) at the same offset (tid % pieces) for every chunk.
-template <int CHUNK, int PLANES, int ROWS> struct StageThread {
-    using S = Stage<CHUNK, PLANES>;
-    static constexpr int threads = kGemmWaves * 64;
-    static_assert(ROWS * S::pieces % threads == 0, "pieces cover the threads exactly");
-    static constexpr int per_thread = ROWS * S::pieces / threads;
-    static constexpr int rows_step = threads / S::pieces;
-    const uint16_t* src[per_thread];  // row start in its plane (always a valid row)
-    bool valid[per_thread];           // the row exists (else it is stored as zeros)
-    unsigned step, plane, sub;
-};
-
-// Plane p of the staged operand starts at base + p * plane_stride (one base pointer keeps
-// the loads global: a per-thread choice between pointers would make them flat);
-// `row_offset(r)` is the element offset of row r within a plane, or -1 past the item.
-template <int CHUNK, int PLANES, int ROWS, class RowOffset>
-__device__ __forceinline__ StageThread<CHUNK, PLANES, ROWS> stage_thread(const uint16_t* base,
-                                                                         size_t plane_stride,
-                                                                         RowOffset row_offset) {
-    using T = StageThread<CHUNK, PLANES, ROWS>;
-    using S = Stage<CHUNK, PLANES>;
-    T t;
-    const unsigned within = threadIdx.x % S::pieces;
-    t.step = within / (8 * PLANES);
-    t.plane = (within / 8) % PLANES;
-    t.sub = within % 8;
-#pragma unroll
-    for (int i = 0; i < T::per_thread; ++i) {
-        const unsigned row = threadIdx.x / S::pieces + i * T::rows_step;
-        const long long at = row_offset(row);
-        t.valid[i] = at >= 0;
-        t.src[i] = base + t.plane * plane_stride + (at >= 0 ? at : row_offset(0));
-    }
-    return t;
+__host__ __device__ inline Tiles tile_layout(uint8_t* base, size_t tiles, size_t steps, int terms) {
+    Tiles l;
+    l.code_stride = steps * size_t(terms) * 2048;
+    l.scale_stride = (steps + 3) / 4 * 256;
+    l.codes = base;
+    l.scales = base + tiles * l.code_stride;
+    return l;
 }
 
-template <int CHUNK, int PLANES, int ROWS> struct StagePieces {
-    u32x4 v[StageThread<CHUNK, PLANES, ROWS>::per_thread];
-};
-
-// Loads the pieces of the chunk starting at step q (steps past `last` re-read `last`).
-template <int CHUNK, int PLANES, int ROWS>
-__device__ __forceinline__ void stage_load(const StageThread<CHUNK, PLANES, ROWS>& t, unsigned q,
-                                           unsigned last, StagePieces<CHUNK, PLANES, ROWS>& P) {
-    const unsigned step = min(q + t.step, last);
-#pragma unroll
-    for (int i = 0; i < StageThread<CHUNK, PLANES, ROWS>::per_thread; ++i)
-        P.v[i] = *reinterpret_cast<const u32x4*>(t.src[i] + size_t(step) * kStepK + t.sub * 8);
+__host__ __device__ inline size_t tile_bytes(size_t tiles, size_t steps, int terms) {
+    return tiles * (steps * size_t(terms) * 2048 + (steps + 3) / 4 * 256);
 }
 
-// Stores a loaded chunk to LDS: every piece, also those of steps past the end of the K
-// range (they land in buffer space no MFMA reads), without branches, so no path leaves
-// a load outstanding.
-template <int CHUNK, int PLANES, int ROWS>
-__device__ __forceinline__ void stage_store(const StageThread<CHUNK, PLANES, ROWS>& t,
-                                            const StagePieces<CHUNK, PLANES, ROWS>& P,
-                                            uint8_t* buf) {
-    using T = StageThread<CHUNK, PLANES, ROWS>;
-    using S = Stage<CHUNK, PLANES>;
+// e with 2^-e * amax in [128, 256) for a finite amax > 0, within the E8M0 range.
+__device__ __forceinline__ int block_exponent(float amax) {
+    const int ex = int((__float_as_uint(amax) >> 23) & 255u) - 127;
+    return max(-127, min(127, ex - 7));
+}
+
+// TERMS FP8 terms of 16 values already multiplied by 2^-e, four bytes per dword in value
+// order; v is consumed.
+template <int TERMS>
+__device__ __forceinline__ void fp8_terms16(float (&v)[16], u32x4 (&out)[TERMS]) {
 #pragma unroll
-    for (int i = 0; i < T::per_thread; ++i) {
-        const unsigned row = threadIdx.x / S::pieces + i * T::rows_step;
-        *reinterpret_cast<u32x4*>(buf + row * S::pitch + (t.step * PLANES + t.plane) * 128 +
-                                  t.sub * 16) = t.valid[i] ? P.v[i] : u32x4{0, 0, 0, 0};
+    for (int t = 0; t < TERMS; ++t) {
+        unsigned w[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * d], v[4 * d + 1], 0, false);
+            const int both = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * d + 2], v[4 * d + 3], lo, true);
+            w[d] = unsigned(both);
+            if (t + 1 < TERMS) {  // the remainder is exact in fp32 (Sterbenz)
+                v[4 * d] -= __builtin_amdgcn_cvt_f32_fp8(both, 0);
+                v[4 * d + 1] -= __builtin_amdgcn_cvt_f32_fp8(both, 1);
+                v[4 * d + 2] -= __builtin_amdgcn_cvt_f32_fp8(both, 2);
+                v[4 * d + 3] -= __builtin_amdgcn_cvt_f32_fp8(both, 3);
+            }
+        }
+        out[t] = u32x4{w[0], w[1], w[2], w[3]};
     }
 }
 
-// 8 exact bf16 values from one dword of a lane's 16 FP4 bytes.
-__device__ __forceinline__ bf16x8 dequant8(unsigned word, float scale) {
-    const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 0);
-    const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 1);
-    const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 2);
-    const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 3);
-    return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+// Row r's 32-value block b of one tile (codes/scales of that tile): block b = 2q + hb of
+// step q; its values 0..15 belong to lane r (piece hb), 16..31 to lane r + 32 (piece hb).
+template <int TERMS>
+__device__ __forceinline__ void store_tile_block(float (&v)[32], bool finite, uint8_t* codes,
+                                                 uint8_t* scales, unsigned r, unsigned b) {
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+        amax = fmaxf(amax, fabsf(v[i]));
+    const int e = block_exponent(amax);
+    float lo[16], hi[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        lo[i] = finite ? __builtin_amdgcn_ldexpf(v[i], -e) : 0.f;
+        hi[i] = finite ? __builtin_amdgcn_ldexpf(v[16 + i], -e) : 0.f;
+    }
+    u32x4 tl[TERMS], th[TERMS];
+    fp8_terms16<TERMS>(lo, tl);
+    fp8_terms16<TERMS>(hi, th);
+    const unsigned q = b / 2, hb = b % 2;
+    uint8_t* at = codes + size_t(q) * TERMS * 2048 + hb * 1024;
+#pragma unroll
+    for (int k = 0; k < TERMS; ++k) {
+        *reinterpret_cast<u32x4*>(at + k * 2048 + 16 * r) = tl[k];
+        *reinterpret_cast<u32x4*>(at + k * 2048 + 16 * (r + 32)) = th[k];
+    }
+    scales[(q / 4) * 256 + 4 * (r + 32 * hb) + q % 4] = finite ? uint8_t(e + 127) : uint8_t(255);
 }
 
-__device__ __forceinline__ bf16x8 lds_bf16x8(const uint8_t* p) {
-    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(p));
+// x (bf16 [tokens][hidden]) gathered by the permutation into gate/up's activation tiles as
+// kXTerms FP8 terms: grid (row-blocks / 256, tiles); one thread per (tile row, 32-value
+// block).  Rows past an item's count are zeros; absent tiles are not written.
+__global__ __launch_bounds__(256) void gather_kernel(const uint16_t* __restrict__ x,
+                                                     unsigned hidden, unsigned top_k,
+                                                     const int32_t* __restrict__ offsets,
+                                                     const int32_t* __restrict__ perm,
+                                                     const int32_t* __restrict__ items,
+                                                     const int32_t* __restrict__ item_count,
+                                                     uint8_t* __restrict__ xa, size_t tiles) {
+    const unsigned blocks = hidden / 32;
+    const unsigned id = blockIdx.x * 256 + threadIdx.x;
+    const unsigned tau = blockIdx.y, item = tau / 2, t = tau % 2;
+    if (id >= 32 * blocks || int(item) >= *item_count)
+        return;
+    const Item it = load_item(items, offsets, item);
+    if (int(32 * t) >= it.count)
+        return;
+    const unsigned r = id / blocks, b = id % blocks;
+    const int row = int(32 * t + r);
+    float v[32];
+    bool finite = true;
+    if (row < it.count) {
+        const size_t token = size_t(perm[it.segment + it.first + row] / int(top_k));
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(x + token * hidden + 32 * b);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const u32x4 w = load16(src + 16 * c);
+            const unsigned ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {  // bf16 -> fp32 is exact
+                v[8 * c + 2 * i] = __uint_as_float(ws[i] << 16);
+                v[8 * c + 2 * i + 1] = __uint_as_float(ws[i] & 0xffff0000u);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 32; ++i)
+            finite = finite && isfinite(v[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i)
+            v[i] = 0.f;
+    }
+    const Tiles l = tile_layout(xa, tiles, hidden / 64, kXTerms);
+    store_tile_block<kXTerms>(v, finite, l.codes + tau * l.code_stride,
+                              l.scales + tau * l.scale_stride, r, b);
+}
+
+// ------------------------------------------------------------- grouped GEMMs
+//
+// A workgroup of kGemmWaves wavefronts takes one work item (expert e, up to kItemRows
+// consecutive rows of its segment: one or two activation tiles of 32 rows) and one K
+// slice; every wavefront owns two 32-row weight groups (gate and up of the same 32
+// features, or two groups of down rows) and multiplies the item's tiles into both.  Per
+// 64-value step a lane loads its 16 FP4 bytes of each group (the packed layout is the
+// MFMA's B operand as it lies; 1 KB contiguous per wavefront) and, per 4 steps, one scale
+// dword per group and per tile, whose byte the MFMA's op_sel picks.  The loop runs whole
+// periods of four steps unrolled, so every register slot stays fixed, every load is
+// unconditional (steps past the end re-read the last one) and each wait counts exactly
+// the loads the next step needs.
+
+// A operand from a lane's two 16-byte pieces; B operand from its 16 FP4 bytes (the MFMA
+// reads four registers of an FP4 operand; the other four are left undefined).
+__device__ __forceinline__ v8i32 a_operand(const u32x4& lo, const u32x4& hi) {
+    return v8i32{int(lo.x), int(lo.y), int(lo.z), int(lo.w),
+                 int(hi.x), int(hi.y), int(hi.z), int(hi.w)};
+}
+
+__device__ __forceinline__ v8i32 b_operand(const u32x4& c) {
+    const v4i32 v{int(c.x), int(c.y), int(c.z), int(c.w)};
+    return __builtin_shufflevector(v, v, 0, 1, 2, 3, -1, -1, -1, -1);
 }
 
 // One wavefront's two packed weight groups (codes at + step * 1 KB, scales at + group * 64
@@ -400,8 +478,7 @@ __device__ __forceinline__ WavePair wave_pair(const uint8_t* packed, const Packe
     return w;
 }
 
-// K slice `slice` of `slices`: [begin, end) in steps, begin a multiple of 8 (two scale
-// groups).
+// K slice `slice` of `slices`: [begin, end) in steps, begin a multiple of 8.
 __device__ __forceinline__ void slice_steps(unsigned steps, unsigned slices, unsigned slice,
                                             unsigned& begin, unsigned& end) {
     const unsigned per = ((steps + slices - 1) / slices + 7) / 8 * 8;
@@ -409,101 +486,146 @@ __device__ __forceinline__ void slice_steps(unsigned steps, unsigned slices, uns
     end = min(steps, begin + per);
 }
 
-__device__ __forceinline__ void issue_fence() {
+__device__ __forceinline__ void issue_order() {
     asm volatile("" ::: "memory");  // keeps the load issue order (activation pointers are
     __builtin_amdgcn_sched_barrier(0);  // not restrict)
 }
 
-// acc[m][t] += A(rows of tile t, steps [q0, q1)) * B(group m of the pair), q0 % 8 == 0.
-// Activations are loaded two chunks ahead of their MFMAs (stored to LDS one chunk ahead),
-// weights one chunk ahead, scale dwords with the first chunk of their 4 steps.  The loop
-// runs whole periods of 8 steps (two scale groups) unrolled, so every ring slot stays in
-// fixed registers (a rotating copy would wait for the loads just issued) and no early exit
-// reaches the loop head with loads outstanding; chunks past the end multiply nothing.
-template <int CHUNK, int PLANES, int TILES>
-__device__ __forceinline__ void gemm_pair(const StageThread<CHUNK, PLANES, TILES * kTileRows>& st,
-                                          const WavePair& w, unsigned q0, unsigned q1,
-                                          bool active, unsigned i32, unsigned h,
-                                          uint8_t (&stage)[2][Stage<CHUNK, PLANES>::buffer],
-                                          f32x16 (&acc)[2][TILES]) {
-    static_assert(CHUNK == 1 || CHUNK == 2 || CHUNK == 4, "chunks tile the scale groups");
-    using S = Stage<CHUNK, PLANES>;
-    constexpr int ROWS = TILES * kTileRows, PERIOD = 8 / CHUNK;
-    auto load_codes = [&](unsigned q, u32x4(&c)[CHUNK][2]) {
+// The item's activation tiles pass through LDS: per chunk of kChunk steps the workgroup
+// copies the chunk of every tile it multiplies (contiguous in the tile layout: kChunk *
+// TERMS * 2 KB per tile) into one of two LDS buffers, 16 bytes per thread per piece, and
+// every wavefront reads its MFMA A operands from there at lane * 16 (conflict free): one
+// activation load per thread and piece instead of one per wavefront.  A chunk is loaded
+// while the one before it is multiplied and stored behind it, with one workgroup barrier
+// per chunk; weights stream per wavefront BRING - 1 steps ahead.  (Measured at T = 256,
+// 32 experts: activations loaded by every wavefront from L2 kept the address unit 60 %
+// busy and the MFMAs 18 %; staging two chunks ahead or weights seven steps ahead were
+// slower; so was a register cap for three workgroups per compute unit, which spills.)
+constexpr int kChunk = 2;
+
+template <int TERMS, int TILES> struct StageCopy {
+    static constexpr int chunk_bytes = TILES * kChunk * TERMS * 2048;  // one LDS buffer
+    static constexpr int pieces = chunk_bytes / 16 / (kGemmWaves * 64);  // per thread
+    const uint8_t* src[pieces];  // piece j of this thread at step 0 (tile base + offset)
+    unsigned step[pieces];       // step of the piece within the chunk
+};
+
+template <int TERMS, int TILES>
+__device__ __forceinline__ StageCopy<TERMS, TILES> stage_copy(const Tiles& l, unsigned item) {
+    using C = StageCopy<TERMS, TILES>;
+    C c;
+    constexpr int per_tile = kChunk * TERMS * 2048;
 #pragma unroll
-        for (int s = 0; s < CHUNK; ++s)
+    for (int j = 0; j < C::pieces; ++j) {
+        const unsigned o = (threadIdx.x + j * kGemmWaves * 64) * 16;  // byte in the chunk
+        const unsigned t = o / per_tile, within = o % per_tile;
+        c.step[j] = within / (TERMS * 2048);
+        c.src[j] = l.codes + (2 * size_t(item) + t) * l.code_stride + within % (TERMS * 2048);
+    }
+    return c;
+}
+
+
+// acc[m][t] += A(tile t, steps [q0, q1)) * B(group m), q0 % 8 == 0; A through LDS, weights
+// BRING - 1 steps ahead (BRING = 4 or 8 steps: whole scale groups and LDS buffer pairs).
+template <int TERMS, int TILES, int BRING = 4>
+__device__ __forceinline__ void staged_pair(const Tiles& l, unsigned item, unsigned lane,
+                                            const WavePair& w, unsigned q0, unsigned q1,
+                                            bool active, uint8_t* stage,
+                                            f32x16 (&acc)[2][TILES]) {
+    using C = StageCopy<TERMS, TILES>;
+    const C cp = stage_copy<TERMS, TILES>(l, item);
+    const unsigned* ascale[TILES];
 #pragma unroll
-            for (int m = 0; m < 2; ++m)
-                c[s][m] = load16(w.codes[m] + size_t(min(q + s, q1 - 1)) * 1024);
+    for (int t = 0; t < TILES; ++t)
+        ascale[t] = reinterpret_cast<const unsigned*>(l.scales + (2 * size_t(item) + t) * l.scale_stride) +
+                    lane;
+    struct BSlot {
+        u32x4 c[2];
+        unsigned s[2];
+        unsigned as[TILES];
     };
-    auto load_scales = [&](unsigned q, unsigned(&sc)[2]) {
+    auto load_b = [&](unsigned q, BSlot& B) {
+        q = min(q, q1 - 1);
 #pragma unroll
         for (int m = 0; m < 2; ++m)
-            sc[m] = w.scales[m][size_t(min(q, q1 - 1) / 4) * 64];
+            B.c[m] = load16(w.codes[m] + size_t(q) * 1024);
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+            B.s[m] = w.scales[m][size_t(q / 4) * 64];
+#pragma unroll
+        for (int t = 0; t < TILES; ++t)
+            B.as[t] = ascale[t][size_t(q / 4) * 64];
+    };
+    struct Pieces {
+        u32x4 v[C::pieces];
+    };
+    auto stage_load = [&](unsigned qc, Pieces& P) {  // chunk starting at step qc
+#pragma unroll
+        for (int j = 0; j < C::pieces; ++j)
+            P.v[j] = load16(cp.src[j] + size_t(min(qc + cp.step[j], q1 - 1)) * TERMS * 2048);
+    };
+    auto stage_store = [&](const Pieces& P, int buffer) {
+#pragma unroll
+        for (int j = 0; j < C::pieces; ++j)
+            *reinterpret_cast<u32x4*>(stage + buffer * C::chunk_bytes +
+                                      (threadIdx.x + j * kGemmWaves * 64) * 16) = P.v[j];
     };
 #pragma unroll
     for (int m = 0; m < 2; ++m)
 #pragma unroll
         for (int t = 0; t < TILES; ++t)
             acc[m][t] = f32x16{};
-    StagePieces<CHUNK, PLANES, ROWS> xr[2];
-    u32x4 wc[2][CHUNK][2];
-    unsigned sc[2][2];
-    stage_load(st, q0, q1 - 1, xr[0]);
-    issue_fence();
-    load_codes(q0, wc[0]);
-    load_scales(q0, sc[0]);
-    issue_fence();
-    stage_load(st, q0 + CHUNK, q1 - 1, xr[1]);
-    issue_fence();
-    stage_store(st, xr[0], stage[0]);
+    BSlot bs[BRING];
+    Pieces xr;
+    stage_load(q0, xr);
+    issue_order();
+#pragma unroll
+    for (int d = 0; d + 1 < BRING; ++d)
+        load_b(q0 + d, bs[d]);
+    issue_order();
+    stage_store(xr, 0);
     __syncthreads();
-    const unsigned chunks = (q1 - q0 + CHUNK - 1) / CHUNK;
-    const unsigned periods = (chunks + PERIOD - 1) / PERIOD;
-    for (unsigned p = 0; p < periods; ++p) {
+    // one chunk (kChunk = 2 steps) per call; CI = chunk index within the BRING-step period
+    auto chunk = [&]<int CI>(unsigned qc) {
+        constexpr int C2 = CI % 2;  // LDS buffer
+        stage_load(qc + kChunk, xr);
+        issue_order();
+        auto step = [&]<int S>() {
+            constexpr int U = CI * kChunk + S;  // step within the period
+            const unsigned q = qc + S;
+            load_b(q + BRING - 1, bs[(U + BRING - 1) % BRING]);
+            if (active && q < q1) {
+                const BSlot& B = bs[U];
+                const uint8_t* buf = stage + C2 * C::chunk_bytes + 16 * lane;
 #pragma unroll
-        for (int u = 0; u < PERIOD; ++u) {
-            const unsigned q = q0 + (p * PERIOD + u) * CHUNK;
-            stage_load(st, q + 2 * CHUNK, q1 - 1, xr[u % 2]);
-            issue_fence();
-            load_codes(q + CHUNK, wc[(u + 1) % 2]);
-            if ((u + 1) * CHUNK % 4 == 0)
-                load_scales(q + CHUNK, sc[((u + 1) * CHUNK / 4) % 2]);
-            issue_fence();
-            if (active) {
-                const unsigned steps = q < q1 ? min(unsigned(CHUNK), q1 - q) : 0u;
+                for (int t = 0; t < TILES; ++t)
 #pragma unroll
-                for (int s = 0; s < CHUNK; ++s) {
-                    if (unsigned(s) >= steps)
-                        continue;
-                    const int qs = u * CHUNK + s;  // step within the period
-                    float scale[2];
+                    for (int k = 0; k < TERMS; ++k) {
+                        const uint8_t* p = buf + ((t * kChunk + S) * TERMS + k) * 2048;
+                        const v8i32 av = a_operand(*reinterpret_cast<const u32x4*>(p),
+                                                   *reinterpret_cast<const u32x4*>(p + 1024));
 #pragma unroll
-                    for (int m = 0; m < 2; ++m)
-                        scale[m] = e8m0((sc[(qs / 4) % 2][m] >> (8 * (qs % 4))) & 0xffu);
-                    const uint8_t* buf = stage[u % 2];
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        const bf16x8 b0 = dequant8(wc[u % 2][s][0][k], scale[0]);
-                        const bf16x8 b1 = dequant8(wc[u % 2][s][1][k], scale[1]);
-#pragma unroll
-                        for (int t = 0; t < TILES; ++t) {
-                            const uint8_t* rowp = buf + (t * kTileRows + i32) * S::pitch +
-                                                  s * PLANES * 128 + (32 * h + 8 * k) * 2;
-#pragma unroll
-                            for (int pl = 0; pl < PLANES; ++pl) {
-                                const bf16x8 a = lds_bf16x8(rowp + pl * 128);
-                                acc[0][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                                    a, b0, acc[0][t], 0, 0, 0);
-                                acc[1][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                                    a, b1, acc[1][t], 0, 0, 0);
-                            }
-                        }
+                        for (int m = 0; m < 2; ++m)
+                            acc[m][t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                                av, b_operand(B.c[m]), acc[m][t], 0 /* A: fp8 e4m3 */,
+                                4 /* B: fp4 e2m1 */, U % 4, int(B.as[t]), U % 4, int(B.s[m]));
                     }
-                }
             }
-            stage_store(st, xr[(u + 1) % 2], stage[(u + 1) % 2]);  // also past the end
-            __syncthreads();
+        };
+        step.template operator()<0>();
+        step.template operator()<1>();
+        stage_store(xr, (C2 + 1) % 2);  // also past the end (never read)
+        __syncthreads();
+    };
+    const unsigned periods = (q1 - q0 + BRING - 1) / BRING;
+    for (unsigned p = 0; p < periods; ++p) {
+        const unsigned qc = q0 + p * BRING;
+        chunk.template operator()<0>(qc);
+        chunk.template operator()<1>(qc + kChunk);
+        if constexpr (BRING == 8) {
+            chunk.template operator()<2>(qc + 2 * kChunk);
+            chunk.template operator()<3>(qc + 3 * kChunk);
         }
     }
 }
@@ -513,19 +635,52 @@ __device__ __forceinline__ int acc_row(int t, int v, unsigned h) {
     return t * kTileRows + 8 * (v / 4) + 4 * int(h) + (v % 4);
 }
 
-// gate/up: grid (groups of 4 feature groups of 32, items, K slices).  Wavefront w
-// multiplies gate and up rows of features 32 (4 x + w) .. +31.  One slice: h = silu(g) * u
-// as bf16 hi + lo; more: fp32 partials of g and u (summed by finalize_kernel).
+// Maximum over the 32 lanes of this lane's half of the wavefront.
+__device__ __forceinline__ float half_max(float v) {
+    v = fmaxf(v, dpp_read<0xb1, 0xf>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_read<0x4e, 0xf>(v));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_read<0x141, 0xf>(v));  // row_half_mirror
+    v = fmaxf(v, dpp_read<0x140, 0xf>(v));  // row_mirror: the row of 16's maximum
+    return fmaxf(v, __shfl_xor(v, 16, 64));
+}
+
+// h for row r (0..31) of an activation tile of the down product, feature f, held with the
+// other 31 features of its 32-value block by the 32 lanes of this half of the wavefront
+// (one row per register).  The block scale comes from the half; each lane writes its
+// value's terms as single bytes (codes/scales of that tile).
+__device__ __forceinline__ void store_h(float hv, unsigned r, unsigned f, uint8_t* codes,
+                                        uint8_t* scales, bool store) {
+    const bool finite = half_max(isfinite(hv) ? 0.f : 1.f) == 0.f;
+    const int e = block_exponent(half_max(fabsf(hv)));
+    float v = finite ? __builtin_amdgcn_ldexpf(hv, -e) : 0.f;
+    if (!store)
+        return;
+    const unsigned q = f / 64, k = f % 64;
+    // value k of step q: lane r + 32 ((k / 16) % 2), piece k / 32, byte k % 16
+    uint8_t* at = codes + size_t(q) * kHTerms * 2048 + (k / 32) * 1024 +
+                  16 * (r + 32 * ((k / 16) % 2)) + k % 16;
+#pragma unroll
+    for (int t = 0; t < kHTerms; ++t) {
+        const int c = __builtin_amdgcn_cvt_pk_fp8_f32(v, 0.f, 0, false);
+        at[t * 2048] = uint8_t(c & 0xff);
+        v -= __builtin_amdgcn_cvt_f32_fp8(c, 0);
+    }
+    if (f % 32 == 0)
+        scales[(q / 4) * 256 + 4 * (r + 32 * ((f / 32) % 2)) + q % 4] =
+            finite ? uint8_t(e + 127) : uint8_t(255);
+}
+
+// gate/up: grid (groups of kGemmWaves feature groups of 32, items, K slices).  Wavefront w
+// multiplies gate and up rows of features 32 (kGemmWaves x + w) .. +31.  One slice:
+// h = silu(g) * u into the down product's activation tiles; more: fp32 partials of g and u
+// per (tile row, feature) (finalize_kernel).
 __global__ __launch_bounds__(kGemmWaves * 64) void gate_up_kernel(
-    const uint16_t* x, unsigned hidden, unsigned inter, unsigned experts, unsigned top_k,
-    const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up,
-    const int32_t* __restrict__ offsets, const int32_t* __restrict__ perm,
-    const int32_t* __restrict__ items, const int32_t* __restrict__ item_count,
-    uint16_t* __restrict__ h_hi, uint16_t* __restrict__ h_lo, float* __restrict__ part_g,
-    float* __restrict__ part_u, size_t part_stride) {
-    constexpr int CHUNK = 2;
-    __shared__ __align__(16) uint8_t stage[2][Stage<CHUNK, 1>::buffer];
-    __shared__ long long src[kItemRows];
+    const uint8_t* __restrict__ xa, unsigned hidden, unsigned inter, unsigned experts,
+    size_t tiles, const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up,
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ items,
+    const int32_t* __restrict__ item_count, uint8_t* __restrict__ ha,
+    float* __restrict__ part_g, float* __restrict__ part_u, size_t part_stride) {
+    __shared__ __align__(16) uint8_t stage[2 * StageCopy<kXTerms, 2>::chunk_bytes];
     if (int(blockIdx.y) >= *item_count)
         return;
     const Item it = load_item(items, offsets, blockIdx.y);
@@ -539,25 +694,18 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gate_up_kernel(
     slice_steps(unsigned(shape.steps), gridDim.z, blockIdx.z, q0, q1);
     if (q0 >= q1)
         return;
-    if (threadIdx.x < kItemRows) {
-        const int r = int(threadIdx.x);
-        src[r] = r < it.count ? (long long)(perm[it.segment + it.first + r] / int(top_k)) * hidden
-                              : -1;
-    }
-    __syncthreads();
     const Packed whole = packed_shape(experts, inter, hidden);
     const size_t group = size_t(it.expert) * shape.groups + (active ? fg : 0);
-    WavePair wg = wave_pair(gate, whole, group, group, lane);
+    WavePair wp = wave_pair(gate, whole, group, group, lane);
     const WavePair wu = wave_pair(up, whole, group, group, lane);
-    wg.codes[1] = wu.codes[0];
-    wg.scales[1] = wu.scales[0];
+    wp.codes[1] = wu.codes[0];
+    wp.scales[1] = wu.scales[0];
+    const Tiles xl = tile_layout(const_cast<uint8_t*>(xa), tiles, hidden / 64, kXTerms);
+    const Tiles hl = tile_layout(ha, tiles, inter / 64, kHTerms);
 
-    // straight-line code per tile count: no accumulator moves between control paths
     auto run = [&]<int TILES>() {
-        const auto st = stage_thread<CHUNK, 1, TILES * kTileRows>(
-            x, 0, [&](unsigned r) { return src[r]; });
         f32x16 acc[2][TILES];
-        gemm_pair<CHUNK, 1, TILES>(st, wg, q0, q1, active, i32, h, stage, acc);
+        staged_pair<kXTerms, TILES>(xl, blockIdx.y, lane, wp, q0, q1, active, stage, acc);
         if (!active)
             return;
         if (gridDim.z > 1) {
@@ -568,7 +716,7 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gate_up_kernel(
                     const int r = acc_row(t, v, h);
                     if (r < it.count) {
                         const size_t at = blockIdx.z * part_stride +
-                                          size_t(it.segment + it.first + r) * inter + f;
+                                          (size_t(blockIdx.y) * kItemRows + r) * inter + f;
                         part_g[at] = acc[0][t][v];
                         part_u[at] = acc[1][t][v];
                     }
@@ -576,18 +724,16 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gate_up_kernel(
             return;
         }
 #pragma unroll
-        for (int t = 0; t < TILES; ++t)
+        for (int t = 0; t < TILES; ++t) {
+            const size_t tau = 2 * size_t(blockIdx.y) + t;
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int r = acc_row(t, v, h);
-                if (r < it.count) {
-                    const float hv = silu(acc[0][t][v]) * acc[1][t][v];
-                    const uint16_t hi = bf16_rne(hv);
-                    const size_t at = size_t(it.segment + it.first + r) * inter + f;
-                    h_hi[at] = hi;
-                    h_lo[at] = bf16_rne(hv - bf16_value(hi));
-                }
+                const float hv = silu(acc[0][t][v]) * acc[1][t][v];
+                store_h(hv, unsigned(r - t * kTileRows), f, hl.codes + tau * hl.code_stride,
+                        hl.scales + tau * hl.scale_stride, r < it.count);
             }
+        }
     };
     if (it.count <= kTileRows)
         run.template operator()<1>();
@@ -595,37 +741,46 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gate_up_kernel(
         run.template operator()<2>();
 }
 
-// h = silu(sum_s g_s) * (sum_s u_s), slices summed in order, as bf16 hi + lo.
+// h = silu(sum_s g_s) * (sum_s u_s), slices summed in order, into the down product's
+// activation tiles: grid (inter / 256, item rows); one thread per (item row, feature), each
+// half wavefront one 32-feature block (inter % 64 == 0).
 __global__ __launch_bounds__(256) void finalize_kernel(const float* __restrict__ part_g,
                                                        const float* __restrict__ part_u,
-                                                       size_t count, unsigned slices,
-                                                       uint16_t* __restrict__ h_hi,
-                                                       uint16_t* __restrict__ h_lo) {
-    const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= count)
+                                                       size_t part_stride, unsigned inter,
+                                                       unsigned slices,
+                                                       const int32_t* __restrict__ offsets,
+                                                       const int32_t* __restrict__ items,
+                                                       const int32_t* __restrict__ item_count,
+                                                       uint8_t* __restrict__ ha, size_t tiles) {
+    const unsigned item = blockIdx.y / kItemRows, row = blockIdx.y % kItemRows;
+    if (int(item) >= *item_count)
         return;
+    const Item it = load_item(items, offsets, item);
+    if (int(row) >= it.count)
+        return;  // the whole workgroup
+    const unsigned f = blockIdx.x * 256 + threadIdx.x;
+    const bool live = f < inter;
+    const size_t at = size_t(blockIdx.y) * inter + (live ? f : 0);
     float gs = 0.f, us = 0.f;
     for (unsigned s = 0; s < slices; ++s) {
-        gs += part_g[s * count + i];
-        us += part_u[s * count + i];
+        gs += part_g[s * part_stride + at];
+        us += part_u[s * part_stride + at];
     }
-    const float hv = silu(gs) * us;
-    const uint16_t hi = bf16_rne(hv);
-    h_hi[i] = hi;
-    h_lo[i] = bf16_rne(hv - bf16_value(hi));
+    const Tiles hl = tile_layout(ha, tiles, inter / 64, kHTerms);
+    const size_t tau = 2 * size_t(item) + row / kTileRows;
+    store_h(silu(gs) * us, row % kTileRows, live ? f : 0, hl.codes + tau * hl.code_stride,
+            hl.scales + tau * hl.scale_stride, live);
 }
 
-// down: grid (groups of 4 row pairs of 64, items, K slices); wavefront w multiplies the
-// down rows 64 (4 x + w) .. +63 (two groups of 32).  fp32 partial sums of h x down (hi
-// plane at h, lo plane at h + plane_stride) per slice, indexed by the slot's position in
-// the permutation.
+// down: grid (groups of kGemmWaves row pairs of 64, items, K slices); wavefront w
+// multiplies the down rows 64 (kGemmWaves x + w) .. +63 (two groups of 32).  fp32 partial
+// sums of h x down per slice, indexed by the slot's position in the permutation.
 __global__ __launch_bounds__(kGemmWaves * 64) void down_kernel(
-    const uint16_t* hp, size_t plane_stride, unsigned hidden, unsigned inter, unsigned experts,
-    const uint8_t* __restrict__ down, const int32_t* __restrict__ offsets,
+    const uint8_t* __restrict__ ha, size_t tiles, unsigned hidden, unsigned inter,
+    unsigned experts, const uint8_t* __restrict__ down, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ items, const int32_t* __restrict__ item_count,
     float* __restrict__ part_d, size_t part_stride) {
-    constexpr int CHUNK = 1;
-    __shared__ __align__(16) uint8_t stage[2][Stage<CHUNK, 2>::buffer];
+    __shared__ __align__(16) uint8_t stage[2 * StageCopy<kHTerms, 2>::chunk_bytes];
     if (int(blockIdx.y) >= *item_count)
         return;
     const Item it = load_item(items, offsets, blockIdx.y);
@@ -642,13 +797,10 @@ __global__ __launch_bounds__(kGemmWaves * 64) void down_kernel(
     const Packed whole = packed_shape(experts, hidden, inter);
     const size_t base = size_t(it.expert) * shape.groups + g0;
     const WavePair w = wave_pair(down, whole, base, base + 1, lane);
-    auto row_offset = [&](unsigned r) {
-        return r < unsigned(it.count) ? (long long)(it.segment + it.first + r) * inter : -1ll;
-    };
+    const Tiles hl = tile_layout(const_cast<uint8_t*>(ha), tiles, inter / 64, kHTerms);
     auto run = [&]<int TILES>() {
-        const auto st = stage_thread<CHUNK, 2, TILES * kTileRows>(hp, plane_stride, row_offset);
         f32x16 acc[2][TILES];
-        gemm_pair<CHUNK, 2, TILES>(st, w, q0, q1, active, i32, h, stage, acc);
+        staged_pair<kHTerms, TILES>(hl, blockIdx.y, lane, w, q0, q1, active, stage, acc);
         if (!active)
             return;
 #pragma unroll
@@ -747,7 +899,7 @@ __global__ __launch_bounds__(256) void mxfp4_dequant_kernel(const uint8_t* __res
 struct MoeScratch {
     int32_t *idx, *offsets, *perm, *position, *items, *item_count;
     float* weight;
-    uint16_t *h_hi, *h_lo;
+    uint8_t *xa, *ha;  // activation tiles of gate/up (x) and of down (h)
     float *part_g, *part_u, *part_d;
 };
 
@@ -786,18 +938,27 @@ size_t align256(size_t n) {
     return (n + 255) & ~size_t(255);
 }
 
+// Work items of a layer (upper bound) and activation tiles (two per item).
+size_t max_items(size_t slots, size_t experts) {
+    return std::min(slots, slots / kItemRows + experts + 1);
+}
+
 size_t moe_scratch_bytes(size_t tokens, size_t hidden, size_t inter, size_t experts,
                          size_t top_k, MoeSlices ks) {
     const size_t slots = tokens * top_k, items = slots / kItemRows + experts + 1;
-    const size_t partial_gu = ks.gate_up > 1 ? 2 * align256(ks.gate_up * slots * inter * 4) : 0;
+    const size_t tiles = 2 * max_items(slots, experts);
+    const size_t partial_gu =
+        ks.gate_up > 1 ? 2 * align256(ks.gate_up * tiles * kTileRows * inter * 4) : 0;
     return align256(slots * 4) * 4 + align256((experts + 1) * 4) + align256(items * 8) +
-           align256(4) + 2 * align256(slots * inter * 2) + partial_gu +
+           align256(4) + align256(tile_bytes(tiles, hidden / 64, kXTerms)) +
+           align256(tile_bytes(tiles, inter / 64, kHTerms)) + partial_gu +
            align256(ks.down * slots * hidden * 4);
 }
 
 MoeScratch carve(uint8_t* p, size_t tokens, size_t hidden, size_t inter, size_t experts,
                  size_t top_k, MoeSlices ks) {
     const size_t slots = tokens * top_k, items = slots / kItemRows + experts + 1;
+    const size_t tiles = 2 * max_items(slots, experts);
     MoeScratch s;
     auto take = [&](size_t n) {
         uint8_t* q = p;
@@ -811,12 +972,12 @@ MoeScratch carve(uint8_t* p, size_t tokens, size_t hidden, size_t inter, size_t 
     s.offsets = reinterpret_cast<int32_t*>(take((experts + 1) * 4));
     s.items = reinterpret_cast<int32_t*>(take(items * 8));
     s.item_count = reinterpret_cast<int32_t*>(take(4));
-    s.h_hi = reinterpret_cast<uint16_t*>(take(slots * inter * 2));
-    s.h_lo = reinterpret_cast<uint16_t*>(take(slots * inter * 2));
+    s.xa = take(tile_bytes(tiles, hidden / 64, kXTerms));
+    s.ha = take(tile_bytes(tiles, inter / 64, kHTerms));
     s.part_g = s.part_u = nullptr;
     if (ks.gate_up > 1) {
-        s.part_g = reinterpret_cast<float*>(take(ks.gate_up * slots * inter * 4));
-        s.part_u = reinterpret_cast<float*>(take(ks.gate_up * slots * inter * 4));
+        s.part_g = reinterpret_cast<float*>(take(ks.gate_up * tiles * kTileRows * inter * 4));
+        s.part_u = reinterpret_cast<float*>(take(ks.gate_up * tiles * kTileRows * inter * 4));
     }
     s.part_d = reinterpret_cast<float*>(take(ks.down * slots * hidden * 4));
     return s;
@@ -954,22 +1115,28 @@ int launch_layer(const uint16_t* x_bf16, const float* logits, size_t tokens, siz
     if (rc)
         return rc;
     const size_t slots = tokens * top_k;
-    const unsigned max_items = unsigned(std::min(slots, slots / kItemRows + experts + 1));
-    hipLaunchKernelGGL(gate_up_kernel, dim3(gate_up_columns(inter), max_items, ks.gate_up),
-                       dim3(kGemmWaves * 64), 0, st, x_bf16, unsigned(hidden), unsigned(inter),
-                       unsigned(experts), unsigned(top_k), gate, up, s.offsets, s.perm, s.items, s.item_count,
-                       s.h_hi, s.h_lo, s.part_g, s.part_u, slots * inter);
+    const unsigned items = unsigned(max_items(slots, experts));
+    const size_t tiles = 2 * size_t(items);
+    hipLaunchKernelGGL(gather_kernel, dim3(unsigned((32 * (hidden / 32) + 255) / 256), unsigned(tiles)),
+                       dim3(256), 0, st, x_bf16, unsigned(hidden), unsigned(top_k), s.offsets,
+                       s.perm, s.items, s.item_count, s.xa, tiles);
+    KDQ_HIP(hipGetLastError());
+    const size_t part_gu = tiles * kTileRows * inter;
+    hipLaunchKernelGGL(gate_up_kernel, dim3(gate_up_columns(inter), items, ks.gate_up),
+                       dim3(kGemmWaves * 64), 0, st, s.xa, unsigned(hidden), unsigned(inter),
+                       unsigned(experts), tiles, gate, up, s.offsets, s.items, s.item_count,
+                       s.ha, s.part_g, s.part_u, part_gu);
     KDQ_HIP(hipGetLastError());
     if (ks.gate_up > 1) {
-        const size_t n = slots * inter;
-        hipLaunchKernelGGL(finalize_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st,
-                           s.part_g, s.part_u, n, ks.gate_up, s.h_hi, s.h_lo);
+        hipLaunchKernelGGL(finalize_kernel, dim3(unsigned((inter + 255) / 256), items * kItemRows),
+                           dim3(256), 0, st, s.part_g, s.part_u, part_gu, unsigned(inter),
+                           ks.gate_up, s.offsets, s.items, s.item_count, s.ha, tiles);
         KDQ_HIP(hipGetLastError());
     }
-    hipLaunchKernelGGL(down_kernel, dim3(down_columns(hidden), max_items, ks.down),
-                       dim3(kGemmWaves * 64), 0, st, s.h_hi, size_t(s.h_lo - s.h_hi),
-                       unsigned(hidden), unsigned(inter), unsigned(experts), down, s.offsets,
-                       s.items, s.item_count, s.part_d, slots * hidden);
+    hipLaunchKernelGGL(down_kernel, dim3(down_columns(hidden), items, ks.down),
+                       dim3(kGemmWaves * 64), 0, st, s.ha, tiles, unsigned(hidden),
+                       unsigned(inter), unsigned(experts), down, s.offsets, s.items,
+                       s.item_count, s.part_d, slots * hidden);
     KDQ_HIP(hipGetLastError());
     const size_t n = tokens * hidden / 4;
     const dim3 grid(unsigned((n + 255) / 256));
