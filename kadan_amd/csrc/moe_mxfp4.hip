@@ -13,7 +13,10 @@
 //                     (v_mfma_scale_f32_32x32x64_f8f6f4): FP8 activation terms x the packed
 //                     FP4 gate and up rows with their E8M0 scales, fp32 accumulation, fused
 //                     h = silu(g) * u stored as FP8 terms for the down product
-//   finalize_kernel   (K-sliced decode only) slices summed in order, then h as above
+//   gather_kernel     x gathered by the permutation into per-item activation tiles as FP8
+//                     terms (the grouped GEMMs' A operand, 1 KB contiguous per load)
+//   prologue_kernel   small layers: route + permute + gather in one workgroup
+//   finalize_kernel   (K-sliced layers only) slices summed in order, then h as FP8 terms
 //   down_kernel       grouped GEMM h x FP4 down rows, fp32 partial rows per slot
 //   combine_kernel    y[t] = sum_i w[t*k + i] * down[t*k + i] in selection order (float)
 #include "kdq_common.hpp"
@@ -31,6 +34,7 @@ constexpr int kMaxTopK = 8, kMaxExperts = 256;
 constexpr int kTileRows = 32, kTiles = 2, kItemRows = kTileRows * kTiles;
 constexpr int kGemmWaves = 4;  // wavefronts per grouped-GEMM workgroup, 64 weight rows each
 constexpr int kStepK = 64;     // K values per step: 16 FP4 bytes per lane
+constexpr int kPrologueSlots = 64;  // layers of at most this many slots use prologue_kernel
 
 // ------------------------------------------------------------------ routing
 
@@ -41,14 +45,11 @@ __device__ __forceinline__ double wave_sum_double(double v) {
     return v;
 }
 
-__global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ logits,
-                                                    unsigned tokens, unsigned experts,
-                                                    unsigned top_k, int32_t* __restrict__ idx,
-                                                    float* __restrict__ weight) {
-    const unsigned lane = threadIdx.x % 64;
-    const unsigned t = blockIdx.x * 4 + threadIdx.x / 64;
-    if (t >= tokens)
-        return;
+// Token t by one whole wavefront (lane = its lane).
+__device__ __forceinline__ void route_token(const float* __restrict__ logits, unsigned t,
+                                            unsigned experts, unsigned top_k,
+                                            int32_t* __restrict__ idx, float* __restrict__ weight,
+                                            unsigned lane) {
     const float* l = logits + size_t(t) * experts;
     float v[4], p[4];
     float maximum = -INFINITY;
@@ -115,14 +116,23 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
     }
 }
 
-// Stable counting sort of slots by expert, in one workgroup; also the work items.
-__global__ __launch_bounds__(1024) void permute_kernel(const int32_t* __restrict__ idx,
-                                                       unsigned slots, unsigned experts,
-                                                       int32_t* __restrict__ offsets,
-                                                       int32_t* __restrict__ perm,
-                                                       int32_t* __restrict__ items,
-                                                       int32_t* __restrict__ item_count,
-                                                       int32_t* __restrict__ position) {
+__global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ logits,
+                                                    unsigned tokens, unsigned experts,
+                                                    unsigned top_k, int32_t* __restrict__ idx,
+                                                    float* __restrict__ weight) {
+    const unsigned t = blockIdx.x * 4 + threadIdx.x / 64;
+    if (t < tokens)
+        route_token(logits, t, experts, top_k, idx, weight, threadIdx.x % 64);
+}
+
+// Stable counting sort of slots by expert by one workgroup of 1024 threads (every thread
+// calls it); also the work items.
+__device__ __forceinline__ void permute_slots(const int32_t* __restrict__ idx, unsigned slots,
+                                              unsigned experts, int32_t* __restrict__ offsets,
+                                              int32_t* __restrict__ perm,
+                                              int32_t* __restrict__ items,
+                                              int32_t* __restrict__ item_count,
+                                              int32_t* __restrict__ position) {
     __shared__ int counts[kMaxExperts], base[kMaxExperts];
     __shared__ int wave_counts[16][kMaxExperts];
     const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
@@ -184,6 +194,16 @@ __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* __restrict
         }
         __syncthreads();
     }
+}
+
+__global__ __launch_bounds__(1024) void permute_kernel(const int32_t* __restrict__ idx,
+                                                       unsigned slots, unsigned experts,
+                                                       int32_t* __restrict__ offsets,
+                                                       int32_t* __restrict__ perm,
+                                                       int32_t* __restrict__ items,
+                                                       int32_t* __restrict__ item_count,
+                                                       int32_t* __restrict__ position) {
+    permute_slots(idx, slots, experts, offsets, perm, items, item_count, position);
 }
 
 // --------------------------------------------------------------- grouped GEMMs
@@ -384,9 +404,36 @@ __device__ __forceinline__ void store_tile_block(float (&v)[32], bool finite, ui
     scales[(q / 4) * 256 + 4 * (r + 32 * hb) + q % 4] = finite ? uint8_t(e + 127) : uint8_t(255);
 }
 
-// x (bf16 [tokens][hidden]) gathered by the permutation into gate/up's activation tiles as
-// kXTerms FP8 terms: grid (row-blocks / 256, tiles); one thread per (tile row, 32-value
-// block).  Rows past an item's count are zeros; absent tiles are not written.
+// Row r (of 32) of activation tile tau from token row `token` of x (bf16 [tokens][hidden]),
+// 32-value block b: its kXTerms FP8 terms and scale in the tile layout.
+__device__ __forceinline__ void gather_block(const uint16_t* __restrict__ x, unsigned hidden,
+                                             size_t token, uint8_t* __restrict__ xa,
+                                             size_t tiles, size_t tau, unsigned r, unsigned b) {
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(x + token * hidden + 32 * b);
+    float v[32];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const u32x4 w = load16(src + 16 * c);
+        const unsigned ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {  // bf16 -> fp32 is exact
+            v[8 * c + 2 * i] = __uint_as_float(ws[i] << 16);
+            v[8 * c + 2 * i + 1] = __uint_as_float(ws[i] & 0xffff0000u);
+        }
+    }
+    bool finite = true;
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+        finite = finite && isfinite(v[i]);
+    const Tiles l = tile_layout(xa, tiles, hidden / 64, kXTerms);
+    store_tile_block<kXTerms>(v, finite, l.codes + tau * l.code_stride,
+                              l.scales + tau * l.scale_stride, r, b);
+}
+
+// x gathered by the permutation into gate/up's activation tiles as kXTerms FP8 terms:
+// grid (row-blocks / 256, tiles); thread `id` of tile tau takes tile row id / blocks,
+// 32-value block id % blocks.  Rows past an item's count and absent tiles are not written:
+// a row of an MFMA's A operand only reaches the same row of its result, which is not stored.
 __global__ __launch_bounds__(256) void gather_kernel(const uint16_t* __restrict__ x,
                                                      unsigned hidden, unsigned top_k,
                                                      const int32_t* __restrict__ offsets,
@@ -394,42 +441,61 @@ __global__ __launch_bounds__(256) void gather_kernel(const uint16_t* __restrict_
                                                      const int32_t* __restrict__ items,
                                                      const int32_t* __restrict__ item_count,
                                                      uint8_t* __restrict__ xa, size_t tiles) {
-    const unsigned blocks = hidden / 32;
-    const unsigned id = blockIdx.x * 256 + threadIdx.x;
+    const unsigned blocks = hidden / 32, id = blockIdx.x * 256 + threadIdx.x;
     const unsigned tau = blockIdx.y, item = tau / 2, t = tau % 2;
     if (id >= 32 * blocks || int(item) >= *item_count)
         return;
     const Item it = load_item(items, offsets, item);
-    if (int(32 * t) >= it.count)
+    const int row = int(32 * t + id / blocks);
+    if (row >= it.count)
         return;
-    const unsigned r = id / blocks, b = id % blocks;
-    const int row = int(32 * t + r);
-    float v[32];
-    bool finite = true;
-    if (row < it.count) {
-        const size_t token = size_t(perm[it.segment + it.first + row] / int(top_k));
-        const uint8_t* src = reinterpret_cast<const uint8_t*>(x + token * hidden + 32 * b);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const u32x4 w = load16(src + 16 * c);
-            const unsigned ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {  // bf16 -> fp32 is exact
-                v[8 * c + 2 * i] = __uint_as_float(ws[i] << 16);
-                v[8 * c + 2 * i + 1] = __uint_as_float(ws[i] & 0xffff0000u);
-            }
+    const size_t token = size_t(perm[it.segment + it.first + row] / int(top_k));
+    gather_block(x, hidden, token, xa, tiles, tau, id / blocks % 32, id % blocks);
+}
+
+// Small layers (decode): routing, permutation and gather in one workgroup of 1024 threads,
+// one launch instead of three.  Phases are separated by workgroup barriers, which make
+// each phase's global writes visible to the next (all of them run on this compute unit).
+// The gather walks the items' occupied rows only, from a row prefix kept in LDS.
+__global__ __launch_bounds__(1024) void prologue_kernel(
+    const float* __restrict__ logits, unsigned tokens, unsigned experts, unsigned top_k,
+    int32_t* __restrict__ idx, float* __restrict__ weight, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ perm, int32_t* __restrict__ items, int32_t* __restrict__ item_count,
+    int32_t* __restrict__ position, const uint16_t* __restrict__ x, unsigned hidden,
+    uint8_t* __restrict__ xa, size_t tiles) {
+    __shared__ int row0[kPrologueSlots + 1], first_pos[kPrologueSlots];
+    __shared__ int n_items;
+    const unsigned wave = threadIdx.x / 64;
+    for (unsigned t = wave; t < tokens; t += 16)
+        route_token(logits, t, experts, top_k, idx, weight, threadIdx.x % 64);
+    __syncthreads();
+    permute_slots(idx, unsigned(tokens * top_k), experts, offsets, perm, items, item_count,
+                  position);
+    __syncthreads();
+    if (threadIdx.x == 0) {  // items hold at least one row each: at most one per slot
+        const int n = *item_count;
+        int acc = 0;
+        for (int i = 0; i < n; ++i) {
+            const Item it = load_item(items, offsets, unsigned(i));
+            row0[i] = acc;
+            first_pos[i] = it.segment + it.first;
+            acc += it.count;
         }
-#pragma unroll
-        for (int i = 0; i < 32; ++i)
-            finite = finite && isfinite(v[i]);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 32; ++i)
-            v[i] = 0.f;
+        row0[n] = acc;
+        n_items = n;
     }
-    const Tiles l = tile_layout(xa, tiles, hidden / 64, kXTerms);
-    store_tile_block<kXTerms>(v, finite, l.codes + tau * l.code_stride,
-                              l.scales + tau * l.scale_stride, r, b);
+    __syncthreads();
+    const unsigned blocks = hidden / 32;
+    const unsigned units = unsigned(row0[n_items]) * blocks;
+    for (unsigned u = threadIdx.x; u < units; u += 1024) {
+        const int g = int(u / blocks);  // occupied row, counted over the items
+        int i = 0;
+        while (row0[i + 1] <= g)
+            ++i;
+        const unsigned row = unsigned(g - row0[i]);
+        const size_t token = size_t(perm[first_pos[i] + int(row)] / int(top_k));
+        gather_block(x, hidden, token, xa, tiles, 2 * size_t(i) + row / 32, row % 32, u % blocks);
+    }
 }
 
 // ------------------------------------------------------------- grouped GEMMs
@@ -943,6 +1009,7 @@ size_t max_items(size_t slots, size_t experts) {
     return std::min(slots, slots / kItemRows + experts + 1);
 }
 
+
 size_t moe_scratch_bytes(size_t tokens, size_t hidden, size_t inter, size_t experts,
                          size_t top_k, MoeSlices ks) {
     const size_t slots = tokens * top_k, items = slots / kItemRows + experts + 1;
@@ -1110,17 +1177,27 @@ int launch_layer(const uint16_t* x_bf16, const float* logits, size_t tokens, siz
         s.offsets = offsets;
     if (perm)
         s.perm = perm;
-    int rc = launch_route(logits, tokens, experts, top_k, s.idx, s.weight, s.offsets, s.perm,
-                          s.items, s.item_count, s.position, st);
-    if (rc)
-        return rc;
     const size_t slots = tokens * top_k;
     const unsigned items = unsigned(max_items(slots, experts));
     const size_t tiles = 2 * size_t(items);
-    hipLaunchKernelGGL(gather_kernel, dim3(unsigned((32 * (hidden / 32) + 255) / 256), unsigned(tiles)),
-                       dim3(256), 0, st, x_bf16, unsigned(hidden), unsigned(top_k), s.offsets,
-                       s.perm, s.items, s.item_count, s.xa, tiles);
-    KDQ_HIP(hipGetLastError());
+    const bool small = slots <= size_t(kPrologueSlots);
+    if (small) {
+        hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(1024), 0, st, logits, unsigned(tokens),
+                           unsigned(experts), unsigned(top_k), s.idx, s.weight, s.offsets, s.perm,
+                           s.items, s.item_count, s.position, x_bf16, unsigned(hidden), s.xa,
+                           tiles);
+        KDQ_HIP(hipGetLastError());
+    } else {
+        int rc = launch_route(logits, tokens, experts, top_k, s.idx, s.weight, s.offsets, s.perm,
+                              s.items, s.item_count, s.position, st);
+        if (rc)
+            return rc;
+        hipLaunchKernelGGL(gather_kernel,
+                           dim3(unsigned((32 * (hidden / 32) + 255) / 256), unsigned(tiles)),
+                           dim3(256), 0, st, x_bf16, unsigned(hidden), unsigned(top_k),
+                           s.offsets, s.perm, s.items, s.item_count, s.xa, tiles);
+        KDQ_HIP(hipGetLastError());
+    }
     const size_t part_gu = tiles * kTileRows * inter;
     hipLaunchKernelGGL(gate_up_kernel, dim3(gate_up_columns(inter), items, ks.gate_up),
                        dim3(kGemmWaves * 64), 0, st, s.xa, unsigned(hidden), unsigned(inter),
@@ -1133,14 +1210,14 @@ int launch_layer(const uint16_t* x_bf16, const float* logits, size_t tokens, siz
                            ks.gate_up, s.offsets, s.items, s.item_count, s.ha, tiles);
         KDQ_HIP(hipGetLastError());
     }
+    const size_t stride = slots * hidden;
     hipLaunchKernelGGL(down_kernel, dim3(down_columns(hidden), items, ks.down),
                        dim3(kGemmWaves * 64), 0, st, s.ha, tiles, unsigned(hidden),
                        unsigned(inter), unsigned(experts), down, s.offsets, s.items,
-                       s.item_count, s.part_d, slots * hidden);
+                       s.item_count, s.part_d, stride);
     KDQ_HIP(hipGetLastError());
     const size_t n = tokens * hidden / 4;
     const dim3 grid(unsigned((n + 255) / 256));
-    const size_t stride = slots * hidden;
     if (ks.down == 1)
         hipLaunchKernelGGL(combine_kernel<1>, grid, dim3(256), 0, st, s.part_d, stride, 1u,
                            s.position, s.weight, unsigned(tokens), unsigned(hidden),
