@@ -593,8 +593,9 @@ __device__ __forceinline__ StageCopy<TERMS, TILES> stage_copy(const Tiles& l, un
 
 
 // acc[m][t] += A(tile t, steps [q0, q1)) * B(group m), q0 % 8 == 0; A through LDS, weights
-// BRING - 1 steps ahead (BRING = 4 or 8 steps: whole scale groups and LDS buffer pairs).
-template <int TERMS, int TILES, int BRING = 4>
+// BRING - 1 steps ahead (BRING = 4 or 8 steps: whole scale groups and LDS buffer pairs),
+// with the non-temporal policy when NT (weights read once per layer call).
+template <int TERMS, int TILES, bool NT, int BRING = 4>
 __device__ __forceinline__ void staged_pair(const Tiles& l, unsigned item, unsigned lane,
                                             const WavePair& w, unsigned q0, unsigned q1,
                                             bool active, uint8_t* stage,
@@ -615,7 +616,8 @@ __device__ __forceinline__ void staged_pair(const Tiles& l, unsigned item, unsig
         q = min(q, q1 - 1);
 #pragma unroll
         for (int m = 0; m < 2; ++m)
-            B.c[m] = load16(w.codes[m] + size_t(q) * 1024);
+            B.c[m] = NT ? stream16(w.codes[m] + size_t(q) * 1024)
+                        : load16(w.codes[m] + size_t(q) * 1024);
 #pragma unroll
         for (int m = 0; m < 2; ++m)
             B.s[m] = w.scales[m][size_t(q / 4) * 64];
@@ -740,7 +742,10 @@ __device__ __forceinline__ void store_h(float hv, unsigned r, unsigned f, uint8_
 // multiplies gate and up rows of features 32 (kGemmWaves x + w) .. +31.  One slice:
 // h = silu(g) * u into the down product's activation tiles; more: fp32 partials of g and u
 // per (tile row, feature) (finalize_kernel).
-__global__ __launch_bounds__(kGemmWaves * 64) void gate_up_kernel(
+// Three workgroups per compute unit (168 registers, no spill): measured 187 -> 174 us at
+// T = 256 and 0.79 -> 0.75 ms at C5.  (down_kernel would spill at that cap.)
+template <bool NT>
+__global__ __launch_bounds__(kGemmWaves * 64, 3) void gate_up_kernel(
     const uint8_t* __restrict__ xa, unsigned hidden, unsigned inter, unsigned experts,
     size_t tiles, const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up,
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ items,
@@ -771,7 +776,7 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gate_up_kernel(
 
     auto run = [&]<int TILES>() {
         f32x16 acc[2][TILES];
-        staged_pair<kXTerms, TILES>(xl, blockIdx.y, lane, wp, q0, q1, active, stage, acc);
+        staged_pair<kXTerms, TILES, NT>(xl, blockIdx.y, lane, wp, q0, q1, active, stage, acc);
         if (!active)
             return;
         if (gridDim.z > 1) {
@@ -841,6 +846,7 @@ __global__ __launch_bounds__(256) void finalize_kernel(const float* __restrict__
 // down: grid (groups of kGemmWaves row pairs of 64, items, K slices); wavefront w
 // multiplies the down rows 64 (kGemmWaves x + w) .. +63 (two groups of 32).  fp32 partial
 // sums of h x down per slice, indexed by the slot's position in the permutation.
+template <bool NT>
 __global__ __launch_bounds__(kGemmWaves * 64) void down_kernel(
     const uint8_t* __restrict__ ha, size_t tiles, unsigned hidden, unsigned inter,
     unsigned experts, const uint8_t* __restrict__ down, const int32_t* __restrict__ offsets,
@@ -866,7 +872,7 @@ __global__ __launch_bounds__(kGemmWaves * 64) void down_kernel(
     const Tiles hl = tile_layout(const_cast<uint8_t*>(ha), tiles, inter / 64, kHTerms);
     auto run = [&]<int TILES>() {
         f32x16 acc[2][TILES];
-        staged_pair<kHTerms, TILES>(hl, blockIdx.y, lane, w, q0, q1, active, stage, acc);
+        staged_pair<kHTerms, TILES, NT>(hl, blockIdx.y, lane, w, q0, q1, active, stage, acc);
         if (!active)
             return;
 #pragma unroll
@@ -1198,11 +1204,21 @@ int launch_layer(const uint16_t* x_bf16, const float* logits, size_t tokens, siz
                            s.offsets, s.perm, s.items, s.item_count, s.xa, tiles);
         KDQ_HIP(hipGetLastError());
     }
+    // Weights stream with the non-temporal policy when an average expert's rows fit one
+    // work item (each weight byte is then read once per call); with more rows, items of
+    // one expert re-read its weights and the caches help (C4 T=256: 174 -> 169 us with
+    // it; C5: 0.75 -> 0.77 ms).
+    const bool nt = slots <= experts * (kItemRows / 2);
     const size_t part_gu = tiles * kTileRows * inter;
-    hipLaunchKernelGGL(gate_up_kernel, dim3(gate_up_columns(inter), items, ks.gate_up),
-                       dim3(kGemmWaves * 64), 0, st, s.xa, unsigned(hidden), unsigned(inter),
-                       unsigned(experts), tiles, gate, up, s.offsets, s.items, s.item_count,
-                       s.ha, s.part_g, s.part_u, part_gu);
+    const dim3 gu_grid(gate_up_columns(inter), items, ks.gate_up);
+    if (nt)
+        hipLaunchKernelGGL(gate_up_kernel<true>, gu_grid, dim3(kGemmWaves * 64), 0, st, s.xa,
+                           unsigned(hidden), unsigned(inter), unsigned(experts), tiles, gate, up,
+                           s.offsets, s.items, s.item_count, s.ha, s.part_g, s.part_u, part_gu);
+    else
+        hipLaunchKernelGGL(gate_up_kernel<false>, gu_grid, dim3(kGemmWaves * 64), 0, st, s.xa,
+                           unsigned(hidden), unsigned(inter), unsigned(experts), tiles, gate, up,
+                           s.offsets, s.items, s.item_count, s.ha, s.part_g, s.part_u, part_gu);
     KDQ_HIP(hipGetLastError());
     if (ks.gate_up > 1) {
         hipLaunchKernelGGL(finalize_kernel, dim3(unsigned((inter + 255) / 256), items * kItemRows),
@@ -1211,10 +1227,15 @@ int launch_layer(const uint16_t* x_bf16, const float* logits, size_t tokens, siz
         KDQ_HIP(hipGetLastError());
     }
     const size_t stride = slots * hidden;
-    hipLaunchKernelGGL(down_kernel, dim3(down_columns(hidden), items, ks.down),
-                       dim3(kGemmWaves * 64), 0, st, s.ha, tiles, unsigned(hidden),
-                       unsigned(inter), unsigned(experts), down, s.offsets, s.items,
-                       s.item_count, s.part_d, stride);
+    const dim3 d_grid(down_columns(hidden), items, ks.down);
+    if (nt)
+        hipLaunchKernelGGL(down_kernel<true>, d_grid, dim3(kGemmWaves * 64), 0, st, s.ha, tiles,
+                           unsigned(hidden), unsigned(inter), unsigned(experts), down, s.offsets,
+                           s.items, s.item_count, s.part_d, stride);
+    else
+        hipLaunchKernelGGL(down_kernel<false>, d_grid, dim3(kGemmWaves * 64), 0, st, s.ha, tiles,
+                           unsigned(hidden), unsigned(inter), unsigned(experts), down, s.offsets,
+                           s.items, s.item_count, s.part_d, stride);
     KDQ_HIP(hipGetLastError());
     const size_t n = tokens * hidden / 4;
     const dim3 grid(unsigned((n + 255) / 256));
