@@ -307,8 +307,8 @@ __global__ __launch_bounds__(256) void pack_scales_kernel(const uint8_t* __restr
 // E4M3 (round to nearest even), term 2 the remainder rounded, and so on.  Two terms hold
 // every bf16 value exactly (8 significant bits: 4 + 4; values under 2^-2 of the scale
 // keep an absolute error below 2^-10 of it); three terms carry h = silu(g) * u to about
-// 12 significant bits.  A block with a non-finite value gets the E8M0 NaN scale (255),
-// so every product that touches it is NaN, as in fp32.
+// 12 significant bits.  A block with a non-finite value gets the E8M0 NaN scale (255) and
+// FP8 NaN codes, so every product that touches it is NaN, as in fp32.
 //
 // Activations reach the MFMAs as tiles: tile tau = 2 * item + t holds rows 32t .. 32t+31
 // of work item `item` (its slots in permutation order), gathered once so that every
@@ -394,6 +394,11 @@ __device__ __forceinline__ void store_tile_block(float (&v)[32], bool finite, ui
     u32x4 tl[TERMS], th[TERMS];
     fp8_terms16<TERMS>(lo, tl);
     fp8_terms16<TERMS>(hi, th);
+    if (!finite) {  // FP8 NaN codes as well as the NaN scale: NaN however it is read
+#pragma unroll
+        for (int k = 0; k < TERMS; ++k)
+            tl[k] = th[k] = u32x4{0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu};
+    }
     const unsigned q = b / 2, hb = b % 2;
     uint8_t* at = codes + size_t(q) * TERMS * 2048 + hb * 1024;
 #pragma unroll
@@ -730,7 +735,7 @@ __device__ __forceinline__ void store_h(float hv, unsigned r, unsigned f, uint8_
 #pragma unroll
     for (int t = 0; t < kHTerms; ++t) {
         const int c = __builtin_amdgcn_cvt_pk_fp8_f32(v, 0.f, 0, false);
-        at[t * 2048] = uint8_t(c & 0xff);
+        at[t * 2048] = finite ? uint8_t(c & 0xff) : uint8_t(0x7f);  // 0x7f: FP8 NaN
         v -= __builtin_amdgcn_cvt_f32_fp8(c, 0);
     }
     if (f % 32 == 0)

@@ -194,6 +194,32 @@ def test_moe_packed_matches_reference_layout(device, tokens, hidden, inter, expe
         assert np.array_equal(a.cpu().numpy().view(np.uint8), b.cpu().numpy().view(np.uint8))
 
 
+@pytest.mark.parametrize("tokens", [3, 40])  # the one-workgroup prologue and the large path
+@pytest.mark.parametrize("bad", [float("nan"), float("inf")])
+def test_moe_nonfinite_activation(device, tokens, bad):
+    """A non-finite activation poisons its own token's outputs and nothing else: the FP8
+    terms of its 32-value block carry NaN codes and the NaN block scale, so every product
+    that touches it is NaN (as an fp32 product would be); the other tokens' outputs are
+    bit-identical to a run without it."""
+    torch = _torch()
+    from kadan_amd import ops
+    hidden = inter = 256
+    experts, top_k = 8, 4
+    x, logits = synth.moe_inputs(0xBAD, tokens, hidden, experts)
+    (gb, gs), (ub, us), (db, ds) = synth.moe_weights(0xBAD, experts, hidden, inter)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)
+    wts = [dev(a) for a in (gb, gs, ub, us, db, ds)]
+    clean = ops.moe_mxfp4(dev(x).view(torch.bfloat16), dev(logits), top_k, *wts).cpu().numpy()
+    poisoned = x.copy()
+    bits = np.array([bad], np.float32).view(np.uint32)[0] >> 16
+    poisoned[1, 37] = np.uint16(bits)
+    got = ops.moe_mxfp4(dev(poisoned).view(torch.bfloat16), dev(logits), top_k,
+                        *wts).cpu().numpy()
+    assert not np.isfinite(got[1]).any()
+    others = [t for t in range(tokens) if t != 1]
+    assert np.array_equal(got[others], clean[others])
+
+
 def test_moe_alignment_rejected(device):
     torch = _torch()
     import kadan_amd
