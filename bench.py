@@ -323,21 +323,27 @@ def calibrate_copy(torch, mib: int = 256, count: int = 5):
     torch.cuda.synchronize()
 
 
-def bench_gemm(torch, reps=10, count=20):
+def bench_gemm(torch, reps=10, count=20, packed=True):
     from kadan_amd import ops, synth
     m, k, n = 512, 4096, 14336
     w = synth.q4_0_weights(0xC3, n, k)
     ws = rotated_copies(torch, w, 16, keep_mask(Q4_0, w.shape), 0xC3)
+    if packed:  # the resident form the weight bank keeps (shared with the decode GEMV)
+        ws = [ops.gguf_pack(Q4_0, wi, k) for wi in ws]
     x = torch.from_numpy(synth.normal(0xC3, 9, m * k).reshape(m, k).astype(np.float16)).cuda()
     y = torch.empty(m, n, dtype=torch.float16, device="cuda")
-    launch = lambda i: ops.gemm_q4_0(ws[i % 16], x, n, out=y)
+    if packed:
+        launch = lambda i: ops.gemm_q4_0_packed(ws[i % 16], x, n, out=y)
+    else:
+        launch = lambda i: ops.gemm_q4_0(ws[i % 16], x, n, out=y)
     for i in range(5):
         launch(i)
     ms = time_launches(torch, launch, count, reps)
     flops = 2.0 * m * k * n
     tflops = flops / (ms * 1e-3) / 1e12
-    return {"workload": "C3 Q4_0 GEMM M512 K4096 N14336 (fp16 out)", "ms": round(ms, 4),
-            "tflops": round(tflops, 2), "mfma_peak_tflops": FP16_PEAK_TFLOPS,
+    layout = "tile-packed weights" if packed else "row-major GGUF weights"
+    return {"workload": f"C3 Q4_0 GEMM M512 K4096 N14336 (fp16 out, {layout})",
+            "ms": round(ms, 4), "tflops": round(tflops, 2), "mfma_peak_tflops": FP16_PEAK_TFLOPS,
             "mfma_frac": round(tflops / FP16_PEAK_TFLOPS, 4),
             "note": "per launch: activation quantize + fp16-MFMA GEMM"}
 
@@ -464,6 +470,7 @@ def main():
             "ms": round(t, 6), "gbs": round(nb / (t * 1e-3) / 1e9, 1),
             "hbm_frac": round(nb / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         extra["c3_q4_0_gemm"] = bench_gemm(torch)
+        extra["c3_q4_0_gemm_row_major"] = bench_gemm(torch, packed=False)
         extra["c4_moe_t1"] = bench_moe(torch, 1, 32, 0, 0xC4, copies=2, count=50)
         extra["c4_moe_t256"] = bench_moe(torch, 256, 32, 0, 0xC4, copies=2)
         extra["c5_moe_t2048_skewed"] = bench_moe(torch, 2048, 128, 8, 0xC5, copies=1, reps=5,

@@ -145,6 +145,15 @@ int kdq_gemv_packed_supported(int encoding, size_t in);
 int kdq_gemm_q4_0(const void* weights, size_t n, size_t k, const uint16_t* x_f16, size_t m,
                   uint16_t* y_f16, void* stream);
 
+/* kdq_gemm_q4_0 over the tile-packed Q4_0 layout of kdq_gguf_pack (the resident form
+ * the decode product kdq_gemv_packed reads, so one resident copy serves decode and
+ * prefill): `packed` holds kdq_gguf_packed_bytes(KDQ_Q4_0, k, n) bytes, 16-byte
+ * aligned.  Same semantics as kdq_gemm_q4_0 (same activation quantisation, fp16
+ * products of fp16(code * d_x) and fp16((q - 8) * d_w), fp32 accumulation); results
+ * may differ from kdq_gemm_q4_0 in the last fp32 bits (summation order). */
+int kdq_gemm_q4_0_packed(const void* packed, size_t n, size_t k, const uint16_t* x_f16,
+                         size_t m, uint16_t* y_f16, void* stream);
+
 /* The activation quantizer of kdq_gemm_q4_0 on its own (for bit-exact checks):
  * q int8 [m x k], d fp32 [m x k/32]. */
 int kdq_quantize_q8(const uint16_t* x_f16, size_t m, size_t k, int8_t* q, float* d,

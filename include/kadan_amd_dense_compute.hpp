@@ -137,8 +137,8 @@ private:
     using BankKey = std::tuple<WeightIdentity, int, std::size_t, std::size_t>;
 
     // The resident weights of one projection, uploaded through the pinned staging on a
-    // miss.  `product`: for the decode-time product (tile-packed where the packed kernel
-    // takes the shape), else row-major rows (the prefill GEMM).
+    // miss.  `product`: for the decode GEMV or the prefill GEMM (tile-packed where the
+    // packed GEMV takes the shape, one copy for both), else row-major rows.
     const Resident& weights_for(const WeightIdentity&, gguf::Encoding, std::size_t in,
                                 std::size_t out, const GgufWeightSource&, bool retain,
                                 const std::atomic_bool& cancel,

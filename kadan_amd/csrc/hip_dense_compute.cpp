@@ -204,8 +204,9 @@ const HipDenseCompute::Resident& HipDenseCompute::weights_for(
     const WeightIdentity& identity, gguf::Encoding enc, std::size_t in, std::size_t out,
     const GgufWeightSource& source, bool retain, const std::atomic_bool& cancel,
     std::unique_ptr<Resident>& transient, bool product) {
-    // Products keep the tile-packed layout when the packed kernel takes the shape; the
-    // prefill GEMM reads row-major rows.  The layout is part of the bank key.
+    // Products (decode GEMV and prefill GEMM) keep the tile-packed layout when the packed
+    // GEMV takes the shape, so one resident copy serves both; the layout is part of the
+    // bank key.
     const bool packed = product && kdq_gemv_packed_supported(ggml_type(enc), in);
     const BankKey key{identity, 2 * int(enc) + (packed ? 1 : 0), in, out};
     if (auto it = bank_.find(key); it != bank_.end())
@@ -421,13 +422,17 @@ ProjectionResult HipDenseCompute::dense_gguf_q8_source(
     hip_check(hipSetDevice(device_));
     const std::size_t rows = input.size() / in;
     std::unique_ptr<Resident> transient;
+    // the same resident copy (tile-packed when the decode product takes it) serves both
     const Resident& w = weights_for(identity, enc, in, out, source, true, cancel, transient,
-                                    false);
+                                    true);
     auto st = static_cast<hipStream_t>(stream_);
     auto* dx = static_cast<std::uint16_t*>(device_buffer(0, input.size_bytes()));
     auto* dy = static_cast<std::uint16_t*>(device_buffer(1, output.size_bytes()));
     hip_check(hipMemcpyAsync(dx, input.data(), input.size_bytes(), hipMemcpyHostToDevice, st));
-    kdq_check(kdq_gemm_q4_0(w.device, out, in, dx, rows, dy, st));
+    if (w.packed)
+        kdq_check(kdq_gemm_q4_0_packed(w.device, out, in, dx, rows, dy, st));
+    else
+        kdq_check(kdq_gemm_q4_0(w.device, out, in, dx, rows, dy, st));
     hip_check(hipMemcpyAsync(output.data(), dy, output.size_bytes(), hipMemcpyDeviceToHost, st));
     synchronize();
     return ProjectionResult::unvalidated;

@@ -144,6 +144,22 @@ def gemm_q4_0(weights: torch.Tensor, x_f16: torch.Tensor, n_out: int,
     return out
 
 
+def gemm_q4_0_packed(packed: torch.Tensor, x_f16: torch.Tensor, n_out: int,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """Tile-packed Q4_0 weights (gguf_pack) x fp16 [m, k] -> fp16 [m, n_out]
+    (kdq_gemm_q4_0_packed)."""
+    _need(packed, torch.uint8, "packed")
+    _need(x_f16, torch.float16, "x")
+    m, k = x_f16.shape
+    if packed.numel() != gguf_packed_bytes(2, k, n_out):  # KDQ_Q4_0
+        raise ValueError("packed size does not match (k, n_out)")
+    if out is None:
+        out = torch.empty(m, n_out, dtype=torch.float16, device=x_f16.device)
+    call("kdq_gemm_q4_0_packed", packed.data_ptr(), n_out, k, x_f16.data_ptr(), m,
+         out.data_ptr(), _stream())
+    return out
+
+
 def moe_route(logits: torch.Tensor, top_k: int):
     """fp32 [tokens, experts] -> idx, w, offsets, perm (kdq_moe_route)."""
     _need(logits, torch.float32, "logits")
@@ -237,6 +253,7 @@ def moe_mxfp4_packed(x_bf16: torch.Tensor, logits: torch.Tensor, top_k: int, int
     return (out, *extra) if routing else out
 
 
-__all__ = ["dequantize", "gemv", "gemv_batch", "quantize_q8", "gemm_q4_0", "moe_route",
+__all__ = ["dequantize", "gemv", "gemv_batch", "quantize_q8", "gemm_q4_0", "gemm_q4_0_packed",
+           "moe_route",
            "mxfp4_dequantize", "moe_mxfp4", "moe_mxfp4_pack", "moe_mxfp4_packed", "lib",
            "BLOCK_BYTES", "BLOCK_VALUES"]

@@ -19,6 +19,7 @@ def declared_functions():
 def test_header_declares_entry_points():
     names = declared_functions()
     for expected in ["kdq_dequantize", "kdq_gemv", "kdq_gemv_batch", "kdq_gemm_q4_0",
+                     "kdq_gemm_q4_0_packed",
                      "kdq_moe_route", "kdq_moe_mxfp4", "kdq_mxfp4_dequantize",
                      "kdq_moe_mxfp4_pack", "kdq_moe_mxfp4_packed", "kdq_moe_mxfp4_packed_bytes"]:
         assert expected in names
@@ -152,3 +153,18 @@ def test_gguf_packed_geometry_and_argument_errors():
     jobs[1] = kadan_amd.MatvecJob(FAKE_W, FAKE_X, FAKE_Y + 4096, 0, 0, 4, 200, 4, 1, 12)
     assert lib.kdq_gemv_packed_batch(C.addressof(jobs), 2, None) == 2
     assert lib.kdq_gemv_packed_batch(None, 0, None) == 0
+
+
+def test_gemm_packed_argument_errors():
+    import kadan_amd
+    lib = kadan_amd.lib()
+    g = lib.kdq_gemm_q4_0_packed
+    assert g(None, 16, 256, FAKE_X, 1, FAKE_Y, None) == 1
+    assert g(FAKE_W, 16, 256, FAKE_X, 0, FAKE_Y, None) == 1
+    assert g(FAKE_W, 16, 200, FAKE_X, 1, FAKE_Y, None) == 2        # k % 256
+    assert g(FAKE_W, 1 << 24, 256, FAKE_X, 1, FAKE_Y, None) == 2   # n too large
+    assert g(FAKE_W + 4, 16, 256, FAKE_X, 1, FAKE_Y, None) == 7    # packed not 16-aligned
+    assert g(FAKE_W, 16, 256, FAKE_X + 8, 1, FAKE_Y, None) == 7    # activations not 16-aligned
+    assert g(FAKE_W, 16, 256, FAKE_X, 1, FAKE_Y + 1, None) == 7    # output not 2-aligned
+    assert g(FAKE_W, 16, 256, FAKE_X, 1, FAKE_W + 32, None) == 4   # output inside packed
+    assert g(FAKE_W, 16, 256, FAKE_X, 1, FAKE_X + 64, None) == 4   # output inside x

@@ -268,3 +268,24 @@ def test_bank_keeps_products_packed(probe, oracle):
     packed = kadan_amd.lib().kdq_gguf_packed_bytes(Q4_K, n_in, n_out)
     assert packed == 3 * 2 * 2304 and probe.retained == packed
     assert probe.release(41) == packed and probe.retained == 0
+
+
+def test_bank_shares_one_copy_between_decode_and_prefill(probe, oracle):
+    """Q4_0 weights banked by the decode product (tile-packed) serve the prefill GEMM of
+    the same identity without a second upload, and the GEMM reads the packed copy."""
+    import kadan_amd
+    n_in, n_out, rows = 768, 72, 2
+    w = synth.q4_0_weights(0xE1, n_out, n_in)
+    x = synth.normal(0xE2, rows, rows * n_in).reshape(rows, n_in)
+    res, y = probe.gguf(43, Q4_0, w, x, n_out)
+    assert res == FINITE
+    assert_close(y, oracle.gemv(Q4_0, w, x, n_in, n_out), what="decode from the bank")
+    packed = kadan_amd.lib().kdq_gguf_packed_bytes(Q4_0, n_in, n_out)
+    assert probe.retained == packed
+    xh = synth.normal(0xE3, 1, 130 * n_in).reshape(130, n_in).astype(np.float16)
+    res, yq = probe.q8(43, w, xh.view(np.uint16), n_out)
+    assert res == UNVALIDATED and probe.reads == n_out and probe.retained == packed
+    xq, xd = oracle.quantize_q8_f16(xh.view(np.uint16))
+    want = oracle.gemm_q4_0_q8(w, n_out, n_in, xq, xd)
+    assert_close(yq.view(np.float16).astype(np.float32), want, what="prefill from the bank")
+    assert probe.release(43) == packed and probe.retained == 0
