@@ -36,8 +36,21 @@ enum kdq_status {
     KDQ_ERR_ALIGNMENT = 7     /* device pointer alignment the kernels need */
 };
 
-/* ---- encodings (GGML type ids) */
-enum kdq_encoding { KDQ_Q4_0 = 2, KDQ_Q8_0 = 8, KDQ_Q4_K = 12 };
+/* ---- encodings (GGML type ids; IW/include/kadan/gguf_quantization.hpp:16-55).
+ * Every one decodes (kdq_dequantize) and multiplies (kdq_gemv, kdq_gemv_exact,
+ * kdq_gemv_batch); Q4_0, Q8_0 and Q4_K also run the streaming / MFMA products and
+ * have the tile-packed layout.  Q4_0 is not a kadan device encoding: it is ggml's
+ * block_q4_0, added for the prefill GEMM and the products. */
+enum kdq_encoding {
+    KDQ_Q4_0 = 2,
+    KDQ_Q8_0 = 8,
+    KDQ_Q3_K = 11,
+    KDQ_Q4_K = 12,
+    KDQ_Q6_K = 14,
+    KDQ_IQ4_NL = 20,
+    KDQ_IQ4_XS = 23,
+    KDQ_BF16 = 30
+};
 
 /* Human-readable name of a status code (static storage). */
 const char* kdq_status_string(int status);
@@ -67,16 +80,18 @@ int kdq_dequantize(int encoding, const void* packed, size_t row_bytes, size_t ro
  * y[r*stride + c] = sum_k decode(W[c, k]) * x[r*in + k] for r < rows, c < out.
  * W: `out` packed rows of `row_bytes` each.  x: fp32 [rows x in], y: fp32.
  * rows: 1..4096 (more than one pass when needed; gguf_batch_max_rows,
- * IW/include/kadan/dense_compute.hpp:201).  fp32 accumulation; the activation
- * operand is carried as 16-bit block fixed point per 32 values (relative error
- * below 2^-15 of the block maximum), products exact in int32.
+ * IW/include/kadan/dense_compute.hpp:201).  fp32 accumulation.  Q4_0 / Q8_0 / Q4_K
+ * (in % 256 == 0, 4-byte aligned rows): the activation operand is carried as 16-bit
+ * block fixed point per 32 values (relative error below 2^-15 of the block maximum),
+ * products exact in int32; every other shape and encoding runs kdq_gemv_exact.
  * `status`: as kdq_dequantize, set when a block scale is not finite. */
 int kdq_gemv(int encoding, const void* weights, size_t row_bytes, const float* x, size_t rows,
              size_t in, size_t out, float* y, size_t stride, unsigned* status, void* stream);
 
 /* The exact-decode reference kernel: every weight decoded as kdq_dequantize does and
  * multiplied into an fp32 fused multiply-add chain, one wavefront per output.  Any
- * in % 32 == 0.  Slower; kept as the cross-check and for shapes kdq_gemv rejects. */
+ * `in` that is a whole number of blocks and a multiple of 8.  The product of the
+ * encodings without a streaming kernel, and the cross-check of the others. */
 int kdq_gemv_exact(int encoding, const void* weights, size_t row_bytes, const float* x,
                    size_t rows, size_t in, size_t out, float* y, size_t stride,
                    unsigned* status, void* stream);

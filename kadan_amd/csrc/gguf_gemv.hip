@@ -1,5 +1,6 @@
-// GGUF block-quantized decode and decode-time products (Q8_0, Q4_0, Q4_K) for
-// gfx950.  Replaces the reference's gguf_decode_kernel and gguf_matvec_kernel
+// GGUF block-quantized decode and decode-time products for gfx950: Q8_0, Q4_0, Q4_K on
+// every kernel below, Q3_K, Q6_K, IQ4_NL, IQ4_XS and BF16 on decode_kernel and
+// exact_gemv.  Replaces the reference's gguf_decode_kernel and gguf_matvec_kernel
 // (IW/src/cuda/h3_compute.cu:76-95,165-240; IW = services/hikari/inference_worker)
 // behind the C ABI of include/kadan_amd.h.
 //
@@ -17,6 +18,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 #include <vector>
 
 namespace kdq {
@@ -34,6 +36,31 @@ template <> struct Format<KDQ_Q4_0> {
 template <> struct Format<KDQ_Q4_K> {
     static constexpr int values = 256, bytes = 144;
 };
+template <> struct Format<KDQ_Q3_K> {
+    static constexpr int values = 256, bytes = 110;
+};
+template <> struct Format<KDQ_Q6_K> {
+    static constexpr int values = 256, bytes = 210;
+};
+template <> struct Format<KDQ_IQ4_NL> {
+    static constexpr int values = 32, bytes = 18;
+};
+template <> struct Format<KDQ_IQ4_XS> {
+    static constexpr int values = 256, bytes = 136;
+};
+template <> struct Format<KDQ_BF16> {
+    static constexpr int values = 1, bytes = 2;
+};
+
+// The 16 IQ4 code points (IQ4_NL and IQ4_XS; the format's fixed non-linear grid,
+// G/src/ggml-common.h:1120-1122), looked up two per nibble pair with v_perm.
+__device__ __forceinline__ float iq4_value(unsigned index) {
+    // bytes of the signed grid, four per word
+    const unsigned words[4] = {0xbfad9881u, 0xf6eaddcfu, 0x26190d01u, 0x71594535u};
+    const unsigned w = index < 8 ? (index < 4 ? words[0] : words[1])
+                                 : (index < 12 ? words[2] : words[3]);
+    return float(int8_t(w >> (8 * (index % 4))));
+}
 
 __device__ __forceinline__ unsigned half_bits_at(const uint8_t* p) {
     return unsigned(p[0]) | (unsigned(p[1]) << 8);
@@ -52,9 +79,71 @@ __device__ __forceinline__ void q4k_scale_min(const uint8_t* s, unsigned g, unsi
 }
 
 // Eight values from element `within` (a multiple of 8) of one block, each equal to
-// the reference's single-value decode.
+// the reference's single-value decode (IW/include/kadan/gguf_quantization.hpp:631-762;
+// a run of eight never crosses a scale group).  BF16 runs read eight one-value blocks.
 template <int ENC>
 __device__ __forceinline__ void decode_run(const uint8_t* block, unsigned within, float* v) {
+    if constexpr (ENC == KDQ_BF16) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            v[i] = __uint_as_float(half_bits_at(block + 2 * i) << 16);
+        return;
+    } else if constexpr (ENC == KDQ_Q3_K) {
+        // 16 groups of 16 with 6-bit scales (low nibbles at 96.., high pairs at 104..),
+        // 2-bit code fields, minus 4 unless the value's high-mask bit is set
+        const float d = half_exact(half_bits_at(block + 108));
+        const unsigned g = within / 16;
+        const uint8_t* scales = block + 96;
+        const unsigned low = g < 8 ? scales[g] & 15u : unsigned(scales[g - 8]) >> 4;
+        const unsigned high = (unsigned(scales[8 + g % 4]) >> (2 * (g / 4))) & 3u;
+        const float step = mul_rn(d, float(int(low | (high << 4)) - 32));
+        const unsigned shift = 2 * ((within % 128) / 32), mask_bit = within / 32;
+        const uint8_t* codes = block + 32 + (within / 128) * 32;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const unsigned lane = (within + i) % 32;
+            const int code = int((unsigned(codes[lane]) >> shift) & 3u) -
+                             ((unsigned(block[lane]) >> mask_bit) & 1u ? 0 : 4);
+            v[i] = mul_rn(step, float(code));
+        }
+        return;
+    } else if constexpr (ENC == KDQ_Q6_K) {
+        // halves of 128: low nibble from ql, two high bits from qh, int8 scale per 16
+        const float d = half_exact(half_bits_at(block + 208));
+        const unsigned k = within / 128, off = within % 128, q = off / 32;
+        const float step = mul_rn(d, float(int8_t(block[192 + 8 * k + (off % 32) / 16 + 2 * q])));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const unsigned lane = (off + i) % 32;
+            const unsigned byte = block[64 * k + lane + 32 * (q & 1u)];
+            const unsigned low = q < 2 ? byte & 15u : byte >> 4;
+            const unsigned high = (unsigned(block[128 + 32 * k + lane]) >> (2 * q)) & 3u;
+            v[i] = mul_rn(step, float(int(low | (high << 4)) - 32));
+        }
+        return;
+    } else if constexpr (ENC == KDQ_IQ4_NL) {
+        const float d = half_exact(half_bits_at(block));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const unsigned e = within + i, byte = block[2 + e % 16];
+            v[i] = mul_rn(d, iq4_value(e < 16 ? byte & 15u : byte >> 4));
+        }
+        return;
+    } else if constexpr (ENC == KDQ_IQ4_XS) {
+        // 8 groups of 32 with 6-bit scales minus 32, indices laid out as IQ4_NL
+        const float d = half_exact(half_bits_at(block));
+        const unsigned g = within / 32, at = within % 32;
+        const unsigned high = half_bits_at(block + 2);
+        const int scale = int(((unsigned(block[4 + g / 2]) >> (4 * (g % 2))) & 15u) |
+                              (((high >> (2 * g)) & 3u) << 4)) - 32;
+        const float step = mul_rn(d, float(scale));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const unsigned e = at + i, byte = block[8 + 16 * g + e % 16];
+            v[i] = mul_rn(step, iq4_value(e < 16 ? byte & 15u : byte >> 4));
+        }
+        return;
+    }
     const float d = half_exact(half_bits_at(block));
     if constexpr (ENC == KDQ_Q8_0) {
 #pragma unroll
@@ -1168,8 +1257,10 @@ int launch_mfma_any(int encoding, const void* w, size_t row_bytes, const float* 
         return launch_mfma<KDQ_Q8_0, PACKED>(w, row_bytes, x, rows, in, out, y, stride, status, s);
     case KDQ_Q4_0:
         return launch_mfma<KDQ_Q4_0, PACKED>(w, row_bytes, x, rows, in, out, y, stride, status, s);
-    default:
+    case KDQ_Q4_K:
         return launch_mfma<KDQ_Q4_K, PACKED>(w, row_bytes, x, rows, in, out, y, stride, status, s);
+    default:
+        return KDQ_ERR_UNSUPPORTED;
     }
 }
 
@@ -1257,10 +1348,42 @@ bool aligned(const void* p, size_t a) {
     return (reinterpret_cast<uintptr_t>(p) % a) == 0;
 }
 
+// Calls f(std::integral_constant<int, ENC>) for every encoding the decode and the
+// exact product take; KDQ_ERR_UNSUPPORTED otherwise.
+template <typename F>
+int with_encoding(int encoding, F&& f) {
+    switch (encoding) {
+    case KDQ_Q8_0:
+        return f(std::integral_constant<int, KDQ_Q8_0>{});
+    case KDQ_Q4_0:
+        return f(std::integral_constant<int, KDQ_Q4_0>{});
+    case KDQ_Q4_K:
+        return f(std::integral_constant<int, KDQ_Q4_K>{});
+    case KDQ_Q3_K:
+        return f(std::integral_constant<int, KDQ_Q3_K>{});
+    case KDQ_Q6_K:
+        return f(std::integral_constant<int, KDQ_Q6_K>{});
+    case KDQ_IQ4_NL:
+        return f(std::integral_constant<int, KDQ_IQ4_NL>{});
+    case KDQ_IQ4_XS:
+        return f(std::integral_constant<int, KDQ_IQ4_XS>{});
+    case KDQ_BF16:
+        return f(std::integral_constant<int, KDQ_BF16>{});
+    default:
+        return KDQ_ERR_UNSUPPORTED;
+    }
+}
+
+// The encodings the streaming and MFMA products (and the packed layout) take.
+bool streamed_encoding(int encoding) {
+    return encoding == KDQ_Q8_0 || encoding == KDQ_Q4_0 || encoding == KDQ_Q4_K;
+}
+
 // The streaming kernels need whole 64-value lane slots, 4-byte aligned rows and packed
 // rows of exactly the format's size (16-byte aligned for Q4_K).
 bool streams(int encoding, const void* weights, size_t row_bytes, size_t in) {
-    return in % 256 == 0 && row_bytes % 4 == 0 && aligned(weights, 4) &&
+    return streamed_encoding(encoding) && in % 256 == 0 && row_bytes % 4 == 0 &&
+           aligned(weights, 4) &&
            (encoding != KDQ_Q4_K || (row_bytes % 16 == 0 && aligned(weights, 16)));
 }
 
@@ -1307,14 +1430,9 @@ extern "C" int kdq_dequantize(int encoding, const void* packed, size_t row_bytes
     if (overlaps(out, rows * in * sizeof(float), packed, rows * row_bytes))
         return KDQ_ERR_ALIAS;
     auto s = static_cast<hipStream_t>(stream);
-    switch (encoding) {
-    case KDQ_Q8_0:
-        return launch_decode<KDQ_Q8_0>(packed, row_bytes, rows, in, out, status, s);
-    case KDQ_Q4_0:
-        return launch_decode<KDQ_Q4_0>(packed, row_bytes, rows, in, out, status, s);
-    default:
-        return launch_decode<KDQ_Q4_K>(packed, row_bytes, rows, in, out, status, s);
-    }
+    return with_encoding(encoding, [&](auto enc) {
+        return launch_decode<decltype(enc)::value>(packed, row_bytes, rows, in, out, status, s);
+    });
 }
 
 extern "C" int kdq_gemv_exact(int encoding, const void* weights, size_t row_bytes,
@@ -1324,14 +1442,10 @@ extern "C" int kdq_gemv_exact(int encoding, const void* weights, size_t row_byte
     if (rc)
         return rc;
     auto s = static_cast<hipStream_t>(stream);
-    switch (encoding) {
-    case KDQ_Q8_0:
-        return launch_exact<KDQ_Q8_0>(weights, row_bytes, x, rows, in, out, y, stride, status, s);
-    case KDQ_Q4_0:
-        return launch_exact<KDQ_Q4_0>(weights, row_bytes, x, rows, in, out, y, stride, status, s);
-    default:
-        return launch_exact<KDQ_Q4_K>(weights, row_bytes, x, rows, in, out, y, stride, status, s);
-    }
+    return with_encoding(encoding, [&](auto enc) {
+        return launch_exact<decltype(enc)::value>(weights, row_bytes, x, rows, in, out, y,
+                                                  stride, status, s);
+    });
 }
 
 extern "C" int kdq_gemv(int encoding, const void* weights, size_t row_bytes, const float* x,
@@ -1355,8 +1469,11 @@ extern "C" int kdq_gemv(int encoding, const void* weights, size_t row_bytes, con
         case KDQ_Q4_0:
             rc = launch_fast<KDQ_Q4_0>(weights, row_bytes, x, rows, in, out, y, stride, status, s);
             break;
-        default:
+        case KDQ_Q4_K:
             rc = launch_fast<KDQ_Q4_K>(weights, row_bytes, x, rows, in, out, y, stride, status, s);
+            break;
+        default:
+            rc = KDQ_ERR_UNSUPPORTED;
             break;
         }
         if (rc != KDQ_ERR_UNSUPPORTED)
@@ -1395,8 +1512,10 @@ extern "C" int kdq_gguf_pack(int encoding, const void* weights, size_t row_bytes
         return launch_pack<KDQ_Q8_0>(weights, row_bytes, in, out, packed, s);
     case KDQ_Q4_0:
         return launch_pack<KDQ_Q4_0>(weights, row_bytes, in, out, packed, s);
-    default:
+    case KDQ_Q4_K:
         return launch_pack<KDQ_Q4_K>(weights, row_bytes, in, out, packed, s);
+    default:
+        return KDQ_ERR_UNSUPPORTED;
     }
 }
 
@@ -1471,8 +1590,10 @@ int launch_fused(const kdq_matvec_job* jobs, const size_t* idx, size_t n, hipStr
         return launch_mfma_rows<KDQ_Q8_0, PACKED>(j0.rows, p.waves, mj, stream);
     case KDQ_Q4_0:
         return launch_mfma_rows<KDQ_Q4_0, PACKED>(j0.rows, p.waves, mj, stream);
-    default:
+    case KDQ_Q4_K:
         return launch_mfma_rows<KDQ_Q4_K, PACKED>(j0.rows, p.waves, mj, stream);
+    default:
+        return KDQ_ERR_UNSUPPORTED;
     }
 }
 

@@ -45,6 +45,16 @@ int ggml_type(gguf::Encoding e) {
         return KDQ_Q8_0;
     case gguf::Encoding::q4_k:
         return KDQ_Q4_K;
+    case gguf::Encoding::q3_k:
+        return KDQ_Q3_K;
+    case gguf::Encoding::q6_k:
+        return KDQ_Q6_K;
+    case gguf::Encoding::iq4_nl:
+        return KDQ_IQ4_NL;
+    case gguf::Encoding::iq4_xs:
+        return KDQ_IQ4_XS;
+    case gguf::Encoding::bf16:
+        return KDQ_BF16;
     default:
         return -1;
     }
@@ -103,7 +113,7 @@ std::optional<Encoding> encoding(std::uint32_t ggml_type) {
 }
 
 bool supported(Encoding e) {
-    return e == Encoding::q4_0 || e == Encoding::q8_0 || e == Encoding::q4_k;
+    return ggml_type(e) >= 0;
 }
 
 std::size_t block_values(Encoding e) {

@@ -119,10 +119,16 @@ __device__ __forceinline__ float wave_max(float v) {
 
 inline size_t block_values(int encoding) {
     switch (encoding) {
+    case KDQ_BF16:
+        return 1;
     case KDQ_Q4_0:
     case KDQ_Q8_0:
+    case KDQ_IQ4_NL:
         return 32;
+    case KDQ_Q3_K:
     case KDQ_Q4_K:
+    case KDQ_Q6_K:
+    case KDQ_IQ4_XS:
         return 256;
     default:
         return 0;
@@ -132,11 +138,20 @@ inline size_t block_values(int encoding) {
 inline size_t block_bytes(int encoding) {
     switch (encoding) {
     case KDQ_Q4_0:
+    case KDQ_IQ4_NL:
         return 18;
     case KDQ_Q8_0:
         return 34;
     case KDQ_Q4_K:
         return 144;
+    case KDQ_Q3_K:
+        return 110;
+    case KDQ_Q6_K:
+        return 210;
+    case KDQ_IQ4_XS:
+        return 136;
+    case KDQ_BF16:
+        return 2;
     default:
         return 0;
     }

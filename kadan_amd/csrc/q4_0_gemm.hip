@@ -352,19 +352,23 @@ __global__ __launch_bounds__(256, 1) void packed_gemm_kernel(const uint16_t* __r
     for (int c = 0; c < NB; ++c)
         wrow[c] = w + size_t(min(tile0 + 2 * c + r / 16, wtiles - 1)) * groups * kUnitBytes +
                   16 * (16 * h + r % 16);
-    auto load_weights = [&](unsigned g, RowGroup* rg) {
+    // weight item i of a group (6 per operand: four code pieces, two scale dwords)
+    auto load_weight = [&](unsigned g, RowGroup* rg, int i) {
         const size_t off = size_t(g) * kUnitBytes;
-#pragma unroll
-        for (int c = 0; c < NB; ++c) {
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-#pragma unroll
-                for (int p = 0; p < 2; ++p)
-                    rg[c].code[j][p] = load16(wrow[c] + off + 1024 * p + 512 * j);
-                // scale dword of packed position 16(2j + h) + r % 16
-                rg[c].scale[j] = load4(wrow[c] + off + 2048 + 128 * j - 12 * (16 * h + r % 16));
-            }
+        const int c = i / 6, e = i % 6;
+        if (e < 4) {
+            const int j = e / 2, p = e % 2;
+            rg[c].code[j][p] = load16(wrow[c] + off + 1024 * p + 512 * j);
+        } else {
+            // scale dword of packed position 16(2j + h) + r % 16
+            const int j = e - 4;
+            rg[c].scale[j] = load4(wrow[c] + off + 2048 + 128 * j - 12 * (16 * h + r % 16));
         }
+    };
+    auto load_weights = [&](unsigned g, RowGroup* rg) {
+#pragma unroll
+        for (int i = 0; i < 6 * NB; ++i)
+            load_weight(g, rg, i);
     };
 
     // DMA: instruction J = wave * DMAS + j covers tokens 2J, 2J + 1 of the tile; lane L
@@ -377,15 +381,28 @@ __global__ __launch_bounds__(256, 1) void packed_gemm_kernel(const uint16_t* __r
         xlane[jm] = unsigned(tok * row_pitch) + 16 * ((lane % 32) ^ tok);
     }
     const uint8_t* xtile = reinterpret_cast<const uint8_t*>(xs) + size_t(m0) * row_pitch;
+    auto stage_one = [&](unsigned g, unsigned buf, int j) {
+        const unsigned J = wave * DMAS + j;
+        __builtin_amdgcn_global_load_lds(
+            (global_void*)(xtile + size_t(g) * 512 + (J / 8) * (16 * row_pitch) + xlane[J % 8]),
+            (lds_void*)(lds + buf * kStageBytes + J * 1024), 16, 0, 0);
+    };
     auto stage = [&](unsigned g, unsigned buf) {
-        const uint8_t* src = xtile + size_t(g) * 512;
-        uint8_t* dst = lds + buf * kStageBytes;
 #pragma unroll
-        for (int j = 0; j < DMAS; ++j) {
-            const unsigned J = wave * DMAS + j;
-            __builtin_amdgcn_global_load_lds(
-                (global_void*)(src + (J / 8) * (16 * row_pitch) + xlane[J % 8]),
-                (lds_void*)(dst + J * 1024), 16, 0, 0);
+        for (int j = 0; j < DMAS; ++j)
+            stage_one(g, buf, j);
+    };
+    // the next group's loads (DMAS activation DMAs, then 6 * NB weight loads), issued a
+    // few per sub-step so that a burst of loads never blocks the MFMA issue
+    constexpr int kLoads = DMAS + 6 * NB, kPerStep = 4;
+    static_assert(kLoads <= 16 * kPerStep, "the loads must fit the group's sub-steps");
+    auto issue = [&](int s, unsigned g, unsigned buf, RowGroup* rg) {
+#pragma unroll
+        for (int i = kPerStep * s; i < kPerStep * (s + 1) && i < kLoads; ++i) {
+            if (i < DMAS)
+                stage_one(g, buf, i);
+            else
+                load_weight(g, rg, i - DMAS);
         }
     };
 
@@ -403,7 +420,8 @@ __global__ __launch_bounds__(256, 1) void packed_gemm_kernel(const uint16_t* __r
     // LDS and its weight operands dequantised, and the instruction order interleaves
     // them (one MFMA, then up to four VALU ops / one LDS read): with one wavefront per
     // SIMD nothing else fills the issue slots behind a run of back-to-back MFMAs.
-    auto compute = [&](unsigned buf, const RowGroup* rg) {
+    auto compute = [&](unsigned buf, const RowGroup* rg, unsigned next_g, unsigned next_buf,
+                       RowGroup* next_rg) {
         const uint8_t* a = lds + buf * kStageBytes + r * kStageRow;
         auto read_x = [&](int s, f16x8* xf) {
             const unsigned q = 16 * (s / 8) + 8 * h + 4 * ((s / 4) % 2) + s % 4;
@@ -412,14 +430,21 @@ __global__ __launch_bounds__(256, 1) void packed_gemm_kernel(const uint16_t* __r
                 xf[b] = *reinterpret_cast<const f16x8*>(a + b * 32 * kStageRow +
                                                          16 * (q ^ (r % 16)));
         };
+        // fp16 scale pairs (d, d) of the four blocks each operand lane touches this group
+        f16x2 d[NB][2][2];
+#pragma unroll
+        for (int c = 0; c < NB; ++c)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const unsigned sc = rg[c].scale[j];
+                d[c][j][0] = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(sc, sc, 0x01000100u));
+                d[c][j][1] = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(sc, sc, 0x03020302u));
+            }
         auto weights = [&](int s, f16x8* wf) {
             const int j = s / 8, p = (s / 4) % 2, u = s % 4;
 #pragma unroll
-            for (int c = 0; c < NB; ++c) {
-                const unsigned bits = (rg[c].scale[j] >> (16 * p)) & 0xffffu;
-                const f16x2 d = __builtin_bit_cast(f16x2, bits | (bits << 16));
-                wf[c] = dequant_dword(rg[c].code[j][p][u], d, magic);
-            }
+            for (int c = 0; c < NB; ++c)
+                wf[c] = dequant_dword(rg[c].code[j][p][u], d[c][j][p], magic);
         };
         f16x8 xf[2][4], wf[2][NB];
         read_x(0, xf[0]);
@@ -427,6 +452,7 @@ __global__ __launch_bounds__(256, 1) void packed_gemm_kernel(const uint16_t* __r
 #pragma unroll
         for (int s = 0; s < 16; ++s) {
             __builtin_amdgcn_sched_barrier(0);
+            issue(s, next_g, next_buf, next_rg);
             if (s + 1 < 16) {
                 read_x(s + 1, xf[(s + 1) % 2]);
                 weights(s + 1, wf[(s + 1) % 2]);
@@ -443,13 +469,16 @@ __global__ __launch_bounds__(256, 1) void packed_gemm_kernel(const uint16_t* __r
                 __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // up to four VALU
                 if (q < 4)
                     __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+                if (q < kPerStep)
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
             }
         }
     };
 
     // Ping-pong over group pairs: group g in buffer 0 / registers ra, g + 1 in buffer 1 /
-    // rb.  After the last pair the prefetch reloads the last group (consumed only when
-    // the group count is odd); the accumulators never change registers between paths.
+    // rb; each compute issues the other buffer's loads.  After the last pair the prefetch
+    // reloads the last group (consumed only when the group count is odd); the
+    // accumulators never change registers between paths.
     RowGroup ra[NB], rb[NB];
     const unsigned last = groups - 1;
     stage(0, 0);
@@ -458,19 +487,16 @@ __global__ __launch_bounds__(256, 1) void packed_gemm_kernel(const uint16_t* __r
     for (; g + 1 < groups; g += 2) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        stage(g + 1, 1);
-        load_weights(g + 1, rb);
-        compute(0, ra);
+        compute(0, ra, g + 1, 1, rb);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        stage(min(g + 2, last), 0);
-        load_weights(min(g + 2, last), ra);
-        compute(1, rb);
+        compute(1, rb, min(g + 2, last), 0, ra);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA outlives the workgroup
     if (g < groups) {  // odd group count: the last group sits in buffer 0 / ra
         __syncthreads();
-        compute(0, ra);
+        compute(0, ra, last, 1, rb);  // its prefetch reloads the last group (never used)
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
 
     // Output tile through LDS (free after the K loop): D of operand c, token block b holds

@@ -101,6 +101,33 @@ def q4_k_weights(seed: int, n_out: int, n_in: int, scale: float = 0.005) -> np.n
     return blocks.reshape(n_out, nb * 144)
 
 
+# (block values, block bytes, byte offset of the fp16 block scale, scale magnitude) of
+# the formats whose code bytes may be uniform random: every code, sub-block scale and
+# high-bit byte is then a valid encoding
+_RANDOM_CODE_FORMATS = {11: (256, 110, 108, 0.005),   # Q3_K
+                        14: (256, 210, 208, 0.0005),  # Q6_K
+                        20: (32, 18, 0, 0.0005),      # IQ4_NL
+                        23: (256, 136, 0, 0.0002)}    # IQ4_XS
+
+
+def random_code_weights(encoding: int, seed: int, n_out: int, n_in: int) -> np.ndarray:
+    """[n_out, n_in/values*bytes]: uniform code and scale bytes, the fp16 block scale
+    d = fp16(|N|*scale) (Q3_K, Q6_K, IQ4_NL, IQ4_XS)."""
+    values, nbytes, at, scale = _RANDOM_CODE_FORMATS[encoding]
+    nb = n_in // values
+    blocks = random_bytes(seed, 1, n_out * nb * nbytes).reshape(n_out, nb, nbytes)
+    d = to_half_bits(np.abs(normal(seed, 2, n_out * nb)) * scale).reshape(n_out, nb)
+    blocks[:, :, at] = d & 0xFF
+    blocks[:, :, at + 1] = d >> 8
+    return blocks.reshape(n_out, nb * nbytes)
+
+
+def bf16_weights(seed: int, n_out: int, n_in: int, scale: float = 0.02) -> np.ndarray:
+    """[n_out, 2*n_in]: bf16 bits of N(0,1)*scale."""
+    b = to_bf16_bits(normal(seed, 1, n_out * n_in) * scale)
+    return b.view(np.uint8).reshape(n_out, 2 * n_in)
+
+
 def gguf_weights(encoding: int, seed: int, n_out: int, n_in: int) -> np.ndarray:
     if encoding == 8:
         return q8_0_weights(seed, n_out, n_in)
@@ -108,6 +135,10 @@ def gguf_weights(encoding: int, seed: int, n_out: int, n_in: int) -> np.ndarray:
         return q4_0_weights(seed, n_out, n_in)
     if encoding == 12:
         return q4_k_weights(seed, n_out, n_in)
+    if encoding == 30:
+        return bf16_weights(seed, n_out, n_in)
+    if encoding in _RANDOM_CODE_FORMATS:
+        return random_code_weights(encoding, seed, n_out, n_in)
     raise ValueError(encoding)
 
 

@@ -84,10 +84,16 @@ static uint16_t load_u16(const uint8_t* p) {
 
 int kdo_block_values(int encoding) {
     switch (encoding) {
+    case KDO_BF16:
+        return 1;
     case KDO_Q4_0:
     case KDO_Q8_0:
+    case KDO_IQ4_NL:
         return 32;
+    case KDO_Q3_K:
     case KDO_Q4_K:
+    case KDO_Q6_K:
+    case KDO_IQ4_XS:
         return 256;
     default:
         return 0;
@@ -102,8 +108,88 @@ int kdo_block_bytes(int encoding) {
         return 34; /* fp16 d + 32 int8 */
     case KDO_Q4_K:
         return 144; /* fp16 d, fp16 dmin, 12 packed 6-bit scales, 128 bytes of nibbles */
+    case KDO_Q3_K:
+        return 110; /* 32 high-bit bytes, 64 bytes of 2-bit codes, 12 scale bytes, fp16 d */
+    case KDO_Q6_K:
+        return 210; /* 128 low-nibble bytes, 64 high-pair bytes, 16 int8 scales, fp16 d */
+    case KDO_IQ4_NL:
+        return 18; /* fp16 d + 16 bytes of table indices */
+    case KDO_IQ4_XS:
+        return 136; /* fp16 d, 16-bit high scale bits, 4 low scale bytes, 128 index bytes */
+    case KDO_BF16:
+        return 2;
     default:
         return 0;
+    }
+}
+
+/* The 16 IQ4 code points (the non-linear 4-bit grid of IQ4_NL / IQ4_XS, fixed by the
+ * format: G/src/ggml-common.h kvalues_iq4nl). */
+static const int8_t iq4_grid[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                    1,    13,   25,  38,  53,  69,  89,  113};
+
+/* Q3_K: 16 sub-blocks of 16 values with 6-bit signed scales (low 4 bits in bytes
+ * 96..103 as nibbles, high 2 bits in bytes 104..107); value v of the block is the
+ * 2-bit field (v % 128) / 32 of code byte 32 + (v / 128) * 32 + v % 32, minus 4 unless
+ * bit v / 32 of high-bit byte v % 32 is set; w = (d * scale) * code. */
+static void decode_q3_k(const uint8_t* block, float* out) {
+    const float d = kdo_half_to_float(load_u16(block + 108));
+    const uint8_t* scales = block + 96;
+    for (unsigned s = 0; s < 16; ++s) {
+        const unsigned low = s < 8 ? scales[s] & 15u : (unsigned)scales[s - 8] >> 4;
+        const unsigned high = ((unsigned)scales[8 + s % 4] >> (2 * (s / 4))) & 3u;
+        const float step = d * (float)((int)(low | (high << 4)) - 32); /* rounded */
+        for (unsigned i = 0; i < 16; ++i) {
+            const unsigned v = 16 * s + i, lane = v % 32;
+            const unsigned bits = ((unsigned)block[32 + (v / 128) * 32 + lane] >> (2 * ((v % 128) / 32))) & 3u;
+            const int code = (int)bits - ((block[lane] >> (v / 32)) & 1u ? 0 : 4);
+            out[v] = step * (float)code; /* rounded */
+        }
+    }
+}
+
+/* Q6_K: two halves of 128; in half k, quarter q (32 values) of lane l takes the low
+ * (q < 2) or high nibble of ql[64k + 32(q & 1) + l] and bits 2q..2q+1 of
+ * qh[32k + l] as its top two bits; code - 32 scaled by int8 scale 8k + l/16 + 2q. */
+static void decode_q6_k(const uint8_t* block, float* out) {
+    const float d = kdo_half_to_float(load_u16(block + 208));
+    for (unsigned k = 0; k < 2; ++k)
+        for (unsigned q = 0; q < 4; ++q)
+            for (unsigned l = 0; l < 32; ++l) {
+                const unsigned byte = block[64 * k + 32 * (q & 1u) + l];
+                const unsigned low = q < 2 ? byte & 15u : byte >> 4;
+                const unsigned high = ((unsigned)block[128 + 32 * k + l] >> (2 * q)) & 3u;
+                const int scale = (int8_t)block[192 + 8 * k + l / 16 + 2 * q];
+                const float step = d * (float)scale; /* rounded */
+                out[128 * k + 32 * q + l] = step * (float)((int)(low | (high << 4)) - 32);
+            }
+}
+
+/* IQ4_NL: 32 values; value i < 16 is the low nibble of byte 2 + i, value i + 16 its
+ * high nibble, each an index into the IQ4 grid; w = d * grid. */
+static void decode_iq4_nl(const uint8_t* block, float* out) {
+    const float d = kdo_half_to_float(load_u16(block));
+    for (unsigned i = 0; i < 16; ++i) {
+        out[i] = d * (float)iq4_grid[block[2 + i] & 15u];
+        out[i + 16] = d * (float)iq4_grid[block[2 + i] >> 4];
+    }
+}
+
+/* IQ4_XS: 8 sub-blocks of 32 with 6-bit scales (low nibble from byte 4 + s/2, high two
+ * bits from the 16-bit word at byte 2), offset by 32; sub-block s holds 16 index bytes
+ * at 8 + 16s laid out as IQ4_NL; w = (d * scale) * grid. */
+static void decode_iq4_xs(const uint8_t* block, float* out) {
+    const float d = kdo_half_to_float(load_u16(block));
+    const unsigned high = load_u16(block + 2);
+    for (unsigned s = 0; s < 8; ++s) {
+        const unsigned low = ((unsigned)block[4 + s / 2] >> (4 * (s % 2))) & 15u;
+        const int scale = (int)(low | (((high >> (2 * s)) & 3u) << 4)) - 32;
+        const float step = d * (float)scale; /* rounded */
+        for (unsigned i = 0; i < 16; ++i) {
+            const unsigned byte = block[8 + 16 * s + i];
+            out[32 * s + i] = step * (float)iq4_grid[byte & 15u];
+            out[32 * s + 16 + i] = step * (float)iq4_grid[byte >> 4];
+        }
     }
 }
 
@@ -119,6 +205,21 @@ static void q4k_scale_min(const uint8_t* packed, unsigned g, unsigned* scale, un
 }
 
 static void decode_block(int encoding, const uint8_t* block, float* out) {
+    switch (encoding) {
+    case KDO_Q3_K:
+        return decode_q3_k(block, out);
+    case KDO_Q6_K:
+        return decode_q6_k(block, out);
+    case KDO_IQ4_NL:
+        return decode_iq4_nl(block, out);
+    case KDO_IQ4_XS:
+        return decode_iq4_xs(block, out);
+    case KDO_BF16:
+        out[0] = kdo_bf16_to_float(load_u16(block));
+        return;
+    default:
+        break;
+    }
     const float d = kdo_half_to_float(load_u16(block));
     if (encoding == KDO_Q8_0) {
         for (int i = 0; i < 32; ++i)
@@ -352,7 +453,8 @@ static void* matvec_worker(void* arg) {
 
 int kdo_cpu_matvec(int encoding, const uint8_t* weights, size_t row_bytes, const float* x,
                    size_t rows, size_t in, size_t out, float* y, int threads) {
-    if (!kdo_block_values(encoding) || in % (size_t)kdo_block_values(encoding) || threads < 1)
+    if ((encoding != KDO_Q4_0 && encoding != KDO_Q8_0 && encoding != KDO_Q4_K) ||
+        in % (size_t)kdo_block_values(encoding) || threads < 1)
         return -1;
     int8_t* xq = (int8_t*)malloc(rows * in + 1);
     void* xd = malloc(rows * (in / 16 + 1) * sizeof(float));

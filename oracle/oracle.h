@@ -40,7 +40,16 @@ extern "C" {
 #endif
 
 /* GGML type ids, as IW/include/kadan/gguf_quantization.hpp:30-55 maps them. */
-enum { KDO_Q4_0 = 2, KDO_Q8_0 = 8, KDO_Q4_K = 12 };
+enum {
+    KDO_Q4_0 = 2,
+    KDO_Q8_0 = 8,
+    KDO_Q3_K = 11,
+    KDO_Q4_K = 12,
+    KDO_Q6_K = 14,
+    KDO_IQ4_NL = 20,
+    KDO_IQ4_XS = 23,
+    KDO_BF16 = 30
+};
 
 /* IW/include/kadan/gguf_quantization.hpp:576-593: exact IEEE binary16 -> binary32. */
 float kdo_half_to_float(uint16_t bits);
@@ -56,9 +65,14 @@ int kdo_block_values(int encoding);
 int kdo_block_bytes(int encoding);
 
 /* One packed row of `in` values -> fp32, bit-exact to the reference decode:
- * Q8_0  IW/include/kadan/gguf_quantization.hpp:637-641
- * Q4_K  IW/include/kadan/gguf_quantization.hpp:749-761
- * Q4_0  G/src/ggml-quants.c:459-476 (dequantize_row_q4_0)
+ * Q8_0    IW/include/kadan/gguf_quantization.hpp:637-641
+ * Q4_K    IW/include/kadan/gguf_quantization.hpp:749-761
+ * Q3_K    IW/include/kadan/gguf_quantization.hpp:642-657 (G/src/ggml-quants.c:1306, dequantize_row_q3_K)
+ * Q6_K    IW/include/kadan/gguf_quantization.hpp:658-673 (G/src/ggml-quants.c:1940, dequantize_row_q6_K)
+ * IQ4_NL  IW/include/kadan/gguf_quantization.hpp:695-701 (G/src/ggml-quants.c:2726, dequantize_row_iq4_nl)
+ * IQ4_XS  IW/include/kadan/gguf_quantization.hpp:736-748 (G/src/ggml-quants.c:2744, dequantize_row_iq4_xs)
+ * BF16    IW/include/kadan/gguf_quantization.hpp:633-636 (one value per 2-byte block)
+ * Q4_0    G/src/ggml-quants.c:459-476 (dequantize_row_q4_0)
  * Returns 0, or -1 for an unknown encoding / ragged row. */
 int kdo_dequantize_row(int encoding, const uint8_t* row, size_t in, float* out);
 

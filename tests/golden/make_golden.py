@@ -9,6 +9,12 @@ Contents (all little-endian, plain arrays, no pickles):
       (Q4_0, Q8_0, Q4_K), random bytes from xorshift32 seeded 0x31415926 as
       IW/tests/gguf_quantization.cpp:93-147 seeds its own; the first 16 blocks carry
       the special fp16 scales of that test (zeros, subnormals, max, inf, NaN).
+      Q3_K, Q6_K, IQ4_NL, IQ4_XS the same way from a second generator (seed
+      0x27182818, so the arrays above keep their bytes), the scale at the format's
+      offset (108 for Q3_K, 208 for Q6_K) as that test places it; BF16 as 256 values
+      (512 random bytes, the first 16 values the special patterns).
+  kadan_<fmt>_values         kadan::gguf::decode of the same blocks (the reference's own
+                             device decode, IW/include/kadan/gguf_quantization.hpp:631-762)
   q8_0_x / q8_0_bytes        ggml x86 quantize_row_q8_0 (G/src/ggml-cpu/arch/x86/quants.c:302-398)
   q8_K_x / q8_K_bytes        ggml quantize_row_q8_K (G/src/ggml-quants.c:2769-2806)
   dot_<fmt>_w / dot_<fmt>_x / dot_<fmt>_out   ggml AVX2 vec_dot against the dot type
@@ -26,10 +32,13 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
 
-from oracle import BLOCK_BYTES, BLOCK_VALUES, Q4_0, Q4_K, Q8_0, Reference  # noqa: E402
+from oracle import (BF16, BLOCK_BYTES, BLOCK_VALUES, IQ4_NL, IQ4_XS, Q3_K, Q4_0, Q4_K,  # noqa: E402
+                    Q6_K, Q8_0, Reference)
 
 OUT = os.path.join(HERE, "reference_vectors.npz")
-NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k"}
+NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q3_K: "q3_k", Q6_K: "q6_k",
+         IQ4_NL: "iq4_nl", IQ4_XS: "iq4_xs", BF16: "bf16"}
+SCALE_OFFSET = {Q3_K: 108, Q6_K: 208}
 SPECIAL_HALVES = [0x0000, 0x8000, 0x0001, 0x8001, 0x03FF, 0x83FF, 0x0400, 0x8400, 0x3C00,
                   0xBC00, 0x7BFF, 0xFBFF, 0x7C00, 0xFC00, 0x7E01, 0x7C01]
 
@@ -55,7 +64,8 @@ def random_blocks(encoding, count, rng):
             blocks[t, i] = rng() & 255
         scale = (SPECIAL_HALVES[t] if t < 16
                  else (rng() & 0x83FF) | ((rng() % 31) << 10))
-        blocks[t, 0], blocks[t, 1] = scale & 255, scale >> 8
+        at = SCALE_OFFSET.get(encoding, 0)
+        blocks[t, at], blocks[t, at + 1] = scale & 255, scale >> 8
         if encoding == Q4_K:
             minimum = (SPECIAL_HALVES[15 - t] if t < 16
                        else (rng() & 0x83FF) | ((rng() % 31) << 10))
@@ -84,6 +94,19 @@ def main():
         data[f"decode_{NAMES[enc]}_blocks"] = blocks
         data[f"decode_{NAMES[enc]}_values"] = ref.to_float(enc, blocks.reshape(1, -1),
                                                            64 * BLOCK_VALUES[enc]).reshape(64, -1)
+    rng2 = XorShift32(0x27182818)
+    for enc in (Q3_K, Q6_K, IQ4_NL, IQ4_XS):
+        blocks = random_blocks(enc, 64, rng2)
+        data[f"decode_{NAMES[enc]}_blocks"] = blocks
+        data[f"decode_{NAMES[enc]}_values"] = ref.to_float(enc, blocks.reshape(1, -1),
+                                                           64 * BLOCK_VALUES[enc]).reshape(64, -1)
+        data[f"kadan_{NAMES[enc]}_values"] = np.stack(
+            [ref.kadan_decode_block(enc, b) for b in blocks])
+    bf = np.array([rng2() & 255 for _ in range(512)], np.uint8)
+    bf.view(np.uint16)[:16] = SPECIAL_HALVES  # 0, -0, subnormals, max, inf, NaNs as bf16 bits
+    data["decode_bf16_blocks"] = bf.reshape(256, 2)
+    data["decode_bf16_values"] = ref.to_float(BF16, bf.reshape(1, -1), 256).reshape(256, 1)
+    data["kadan_bf16_values"] = np.stack([ref.kadan_decode_block(BF16, b) for b in bf.reshape(256, 2)])
     # activation quantizers: N(0,1) values plus exact half-way cases after scaling
     g = np.random.default_rng(0x5EED)
     x = g.standard_normal(512).astype(np.float32)

@@ -17,9 +17,12 @@ import pytest
 from kadan_amd import synth
 
 Q4_0, Q8_0, Q4_K = 2, 8, 12
-BV = {Q4_0: 32, Q8_0: 32, Q4_K: 256}
-BB = {Q4_0: 18, Q8_0: 34, Q4_K: 144}
-NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k"}
+Q3_K, Q6_K, IQ4_NL, IQ4_XS, BF16 = 11, 14, 20, 23, 30
+NEW = [Q3_K, Q6_K, IQ4_NL, IQ4_XS, BF16]
+BV = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q3_K: 256, Q6_K: 256, IQ4_NL: 32, IQ4_XS: 256, BF16: 1}
+BB = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q3_K: 110, Q6_K: 210, IQ4_NL: 18, IQ4_XS: 136, BF16: 2}
+NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q3_K: "q3_k", Q6_K: "q6_k",
+         IQ4_NL: "iq4_nl", IQ4_XS: "iq4_xs", BF16: "bf16"}
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
                       "reference_vectors.npz")
 
@@ -107,6 +110,97 @@ def test_q4_0_literal_block(oracle):
     q = np.concatenate([np.arange(16), 15 - np.arange(16)])
     assert same_bits(oracle.dequantize(Q4_0, block[None], 32)[0],
                      ((q - 8) * -2.0).astype(np.float32))
+
+
+def test_q3_k_literal_block(oracle):
+    """IW/tests/gguf_quantization.cpp:46-59: high-bit bytes 0x55 (bit j set for even j),
+    code bytes 0xe4 (fields 0, 1, 2, 3 in consecutive 32-value groups), scale nibbles 1
+    and high scale bits 2 (every 6-bit scale 33 - 32 = +1), d = -2."""
+    block = np.zeros(110, np.uint8)
+    block[0:32] = 0x55
+    block[32:96] = 0xE4
+    block[96:104] = 0x11
+    block[104:108] = 0xAA
+    half_bits(block, 108, 0xC000)
+    g = np.arange(256) // 32
+    code = g % 4 - np.where(g % 2, 4, 0)
+    assert same_bits(oracle.dequantize(Q3_K, block[None], 256)[0],
+                     (-2.0 * code).astype(np.float32))
+
+
+def test_q6_k_literal_block(oracle):
+    """Closed form of the Q6_K layout: low nibbles 5 / high nibbles 9 (ql bytes 0x95),
+    high pairs 0b11100100 (fields 0, 1, 2, 3 for quarters 0..3), int8 scales s = 1..16
+    alternating in sign, d = 0.25: value v of half k, quarter q, lane l has code
+    (nibble | field << 4) - 32 and scale s[8k + l/16 + 2q]."""
+    block = np.zeros(210, np.uint8)
+    block[0:128] = 0x95
+    block[128:192] = 0xE4
+    scales = np.array([(i + 1) * (-1) ** i for i in range(16)], np.int8)
+    block[192:208] = scales.view(np.uint8)
+    half_bits(block, 208, 0x3400)
+    v = np.arange(256)
+    k, q, l = v // 128, (v % 128) // 32, v % 32
+    nibble = np.where(q < 2, 5, 9)
+    code = (nibble | (q << 4)) - 32
+    s = scales[8 * k + l // 16 + 2 * q].astype(np.float32)
+    assert same_bits(oracle.dequantize(Q6_K, block[None], 256)[0],
+                     ((0.25 * s) * code).astype(np.float32))
+
+
+def test_iq4_literal_blocks(oracle):
+    """IQ4_NL / IQ4_XS code points are ggml's kvalues_iq4nl (G/src/ggml-common.h:1120-1122):
+    index i in byte 2 + i (low nibble) and its high nibble decode to d * grid."""
+    grid = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89,
+                     113], np.float32)
+    block = np.zeros(18, np.uint8)
+    half_bits(block, 0, 0x3C00)  # d = 1
+    block[2:] = [(15 - j) << 4 | j for j in range(16)]
+    want = np.concatenate([grid, grid[::-1]])
+    assert same_bits(oracle.dequantize(IQ4_NL, block[None], 32)[0], want)
+    # IQ4_XS: sub-block s has scale (low nibble s % 16) | (high bits 2) << 4 minus 32 =
+    # s + 0; d = 0.5; every index byte 0x70 (low 0, high 7)
+    xs = np.zeros(136, np.uint8)
+    half_bits(xs, 0, 0x3800)
+    xs[2], xs[3] = 0xAA, 0xAA  # high bits 2 for every sub-block: +32
+    xs[4:8] = [0x10, 0x32, 0x54, 0x76]  # low nibbles 0..7
+    xs[8:] = 0x70
+    s = np.repeat(np.arange(8), 32).astype(np.float32)
+    idx = np.tile(np.concatenate([np.zeros(16, int), np.full(16, 7)]), 8)
+    assert same_bits(oracle.dequantize(IQ4_XS, xs[None], 256)[0],
+                     ((0.5 * s) * grid[idx]).astype(np.float32))
+
+
+def test_bf16_is_the_upper_half_of_binary32(oracle):
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = oracle.dequantize(BF16, bits.view(np.uint8)[None], 65536)[0]
+    want = (bits.astype(np.uint32) << 16).view(np.float32)
+    assert same_bits(got, want)
+
+
+@pytest.mark.parametrize("encoding", NEW)
+def test_new_formats_vs_reference_vectors(oracle, golden, encoding):
+    """ggml to_float and kadan::gguf::decode of the same blocks (specials included)."""
+    blocks = golden[f"decode_{NAMES[encoding]}_blocks"]
+    got = oracle.dequantize(encoding, blocks, BV[encoding])
+    assert same_bits(got, golden[f"decode_{NAMES[encoding]}_values"])
+    assert same_bits(got, golden[f"kadan_{NAMES[encoding]}_values"])
+
+
+@pytest.mark.parametrize("encoding", NEW)
+def test_new_formats_vs_compiled_reference(oracle, reference, encoding):
+    count = 2048 if encoding != BF16 else 65536
+    raw = synth.random_bytes(13, encoding, count * BB[encoding])
+    if encoding in (Q3_K, Q6_K):  # finite scales at the format's offset
+        at = 108 if encoding == Q3_K else 208
+        raw.reshape(count, -1)[:, at + 1] = 0x10 + (raw.reshape(count, -1)[:, at + 1] & 0x1F)
+    got = oracle.dequantize(encoding, raw[None], count * BV[encoding])
+    assert same_bits(got, reference.to_float(encoding, raw[None], count * BV[encoding]))
+    step = BB[encoding]
+    for b in range(0, 64):
+        blk = raw[b * step:(b + 1) * step]
+        mine = oracle.dequantize(encoding, blk[None], BV[encoding])[0]
+        assert same_bits(mine, reference.kadan_decode_block(encoding, blk))
 
 
 def numpy_decode(encoding, blocks):
