@@ -41,6 +41,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 FP16_PEAK_TFLOPS = 2500.0      # dense fp16/bf16 MFMA
 FP4_PEAK_TFLOPS = 10100.0      # dense MXFP4 MFMA
 Q4_K, Q8_0, Q4_0 = 12, 8, 2
+Q3_K, Q6_K, IQ4_NL, IQ4_XS, BF16 = 11, 14, 20, 23, 30
 
 
 def parse():
@@ -50,6 +51,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=50)
     p.add_argument("--skip-extra", action="store_true")
     p.add_argument("--skip-cpu", action="store_true")
+    p.add_argument("--only", action="append", default=None,
+                   help="run only these extra workloads (repeatable), e.g. c3_q4_0_gemm")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also run a 256 MiB device copy (reference for counter scaling)")
@@ -73,13 +76,16 @@ def rotated_copies(torch, base: np.ndarray, copies: int, keep: np.ndarray, seed:
 
 
 def keep_mask(encoding: int, shape) -> np.ndarray:
-    """True for the scale bytes of each packed row (d, dmin) that must stay as generated."""
+    """True for the scale bytes of each packed row (d, dmin) that must stay as generated
+    (BF16: every byte, so the copies stay the same finite values)."""
     rows, row_bytes = shape
+    if encoding == BF16:
+        return np.ones(shape, bool)
     keep = np.zeros(row_bytes, bool)
-    block = {Q4_K: 144, Q8_0: 34, Q4_0: 18}[encoding]
-    head = 4 if encoding == Q4_K else 2
+    block = {Q4_K: 144, Q8_0: 34, Q4_0: 18, Q3_K: 110, Q6_K: 210, IQ4_NL: 18, IQ4_XS: 136}[encoding]
+    at, head = {Q4_K: (0, 4), Q3_K: (108, 2), Q6_K: (208, 2)}.get(encoding, (0, 2))
     for b in range(0, row_bytes, block):
-        keep[b:b + head] = True
+        keep[b + at:b + at + head] = True
     return np.broadcast_to(keep, shape).copy()
 
 
@@ -449,32 +455,44 @@ def main():
     }
     if not args.skip_extra:
         extra = {}
-        for name, enc, a, b, seed in (("c1_q8_0_gemv_4096x4096", Q8_0, 4096, 4096, 0xC1),
-                                      ("c2_q4_k_gemv_14336_to_4096", Q4_K, 14336, 4096, 0xC2B)):
-            t = bench_gemv(torch, enc, a, b, 500, 20, seed)
-            nb = gemv_bytes(a, b, enc)
-            extra[name] = {"ms": round(t, 6), "gbs": round(nb / (t * 1e-3) / 1e9, 1),
-                           "hbm_frac": round(nb / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
-        t = bench_gemv(torch, Q4_K, n_in, n_out, 1000, 20, 0xC2A, packed=False)
-        nb = gemv_bytes(n_in, n_out, Q4_K)
-        extra["c2_q4_k_gemv_row_major"] = {
-            "workload": "C2 Q4_K GEMV 4096->14336, batch 1, over the row-major GGUF bytes "
-                        "(kdq_gemv_batch; no resident repack)",
-            "ms": round(t, 6), "gbs": round(nb / (t * 1e-3) / 1e9, 1),
-            "hbm_frac": round(nb / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
-        t = bench_gemv(torch, Q4_K, n_in, n_out, 1000, 20, 0xC2C, per_step=2)
-        nb = 2 * gemv_bytes(n_in, n_out, Q4_K) - 4 * n_in  # one shared input
-        extra["c2_q4_k_gate_up_pair"] = {
-            "workload": "C2 Q4_K gate+up 2 x (4096->14336), batch 1, one kdq_gemv_batch "
-                        "submission (one fused launch)",
-            "ms": round(t, 6), "gbs": round(nb / (t * 1e-3) / 1e9, 1),
-            "hbm_frac": round(nb / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
-        extra["c3_q4_0_gemm"] = bench_gemm(torch)
-        extra["c3_q4_0_gemm_row_major"] = bench_gemm(torch, packed=False)
-        extra["c4_moe_t1"] = bench_moe(torch, 1, 32, 0, 0xC4, copies=2, count=50)
-        extra["c4_moe_t256"] = bench_moe(torch, 256, 32, 0, 0xC4, copies=2)
-        extra["c5_moe_t2048_skewed"] = bench_moe(torch, 2048, 128, 8, 0xC5, copies=1, reps=5,
-                                                 count=5)
+        want = (lambda name: True) if not args.only else (lambda name: name in args.only)
+
+        def gemv_line(name, enc, a, b, seed, steps, workload=None, **kw):
+            if not want(name):
+                return
+            t = bench_gemv(torch, enc, a, b, steps, 20, seed, **kw)
+            per = kw.get("per_step", 1)
+            nb = per * gemv_bytes(a, b, enc) - (per - 1) * 4 * a  # one shared input
+            line = {"ms": round(t, 6), "gbs": round(nb / (t * 1e-3) / 1e9, 1),
+                    "hbm_frac": round(nb / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            if workload:
+                line = {"workload": workload, **line}
+            extra[name] = line
+
+        gemv_line("c1_q8_0_gemv_4096x4096", Q8_0, 4096, 4096, 0xC1, 500)
+        gemv_line("c2_q4_k_gemv_14336_to_4096", Q4_K, 14336, 4096, 0xC2B, 500)
+        gemv_line("c2_q4_k_gemv_row_major", Q4_K, n_in, n_out, 0xC2A, 1000,
+                  "C2 Q4_K GEMV 4096->14336, batch 1, over the row-major GGUF bytes "
+                  "(kdq_gemv_batch; no resident repack)", packed=False)
+        gemv_line("c2_q4_k_gate_up_pair", Q4_K, n_in, n_out, 0xC2C, 1000,
+                  "C2 Q4_K gate+up 2 x (4096->14336), batch 1, one kdq_gemv_batch "
+                  "submission (one fused launch)", per_step=2)
+        for enc, tag in ((Q6_K, "q6_k"), (Q3_K, "q3_k"), (IQ4_XS, "iq4_xs"), (BF16, "bf16")):
+            gemv_line(f"gemv_{tag}_4096x14336_exact", enc, n_in, n_out, 0xF0 + enc, 50,
+                      f"{tag.upper()} GEMV 4096->14336, batch 1, row-major bytes (exact-decode "
+                      "product: no streaming kernel for this encoding yet)", packed=False,
+                      copies=4)
+        if want("c3_q4_0_gemm"):
+            extra["c3_q4_0_gemm"] = bench_gemm(torch)
+        if want("c3_q4_0_gemm_row_major"):
+            extra["c3_q4_0_gemm_row_major"] = bench_gemm(torch, packed=False)
+        if want("c4_moe_t1"):
+            extra["c4_moe_t1"] = bench_moe(torch, 1, 32, 0, 0xC4, copies=2, count=50)
+        if want("c4_moe_t256"):
+            extra["c4_moe_t256"] = bench_moe(torch, 256, 32, 0, 0xC4, copies=2)
+        if want("c5_moe_t2048_skewed"):
+            extra["c5_moe_t2048_skewed"] = bench_moe(torch, 2048, 128, 8, 0xC5, copies=1,
+                                                     reps=5, count=5)
         result["extra"] = extra
     if not args.skip_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
