@@ -47,7 +47,10 @@ enum kdq_encoding {
     KDQ_Q3_K = 11,
     KDQ_Q4_K = 12,
     KDQ_Q6_K = 14,
+    KDQ_IQ3_XXS = 18,
     KDQ_IQ4_NL = 20,
+    KDQ_IQ3_S = 21,
+    KDQ_IQ2_S = 22,
     KDQ_IQ4_XS = 23,
     KDQ_BF16 = 30
 };

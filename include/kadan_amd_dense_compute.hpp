@@ -46,8 +46,7 @@ struct WeightIdentity {
 
 namespace gguf {
 // IW/include/kadan/gguf_quantization.hpp:16-27, plus q4_0 (GGML type 2), which the
-// reference has no encoding for.  iq3_xxs, iq2_s and iq3_s do not run on this
-// implementation yet (supported() is false: the calls return `unsupported`).
+// reference has no encoding for.  Every encoding runs on this implementation.
 enum class Encoding { q3_k, q4_k, q8_0, q6_k, iq3_xxs, iq4_nl, iq4_xs, iq2_s, iq3_s, bf16, q4_0 };
 
 // GGML type id -> encoding (IW/include/kadan/gguf_quantization.hpp:30-55, plus type 2).

@@ -1,6 +1,6 @@
 // GGUF block-quantized decode and decode-time products for gfx950: Q8_0, Q4_0, Q4_K on
-// every kernel below, Q3_K, Q6_K, IQ4_NL, IQ4_XS and BF16 on decode_kernel and
-// exact_gemv.  Replaces the reference's gguf_decode_kernel and gguf_matvec_kernel
+// every kernel below, Q3_K, Q6_K, IQ4_NL, IQ4_XS, IQ3_XXS, IQ2_S, IQ3_S and BF16 on
+// decode_kernel and exact_gemv.  Replaces the reference's gguf_decode_kernel and gguf_matvec_kernel
 // (IW/src/cuda/h3_compute.cu:76-95,165-240; IW = services/hikari/inference_worker)
 // behind the C ABI of include/kadan_amd.h.
 //
@@ -51,6 +51,32 @@ template <> struct Format<KDQ_IQ4_XS> {
 template <> struct Format<KDQ_BF16> {
     static constexpr int values = 1, bytes = 2;
 };
+template <> struct Format<KDQ_IQ3_XXS> {
+    static constexpr int values = 256, bytes = 98;
+};
+template <> struct Format<KDQ_IQ2_S> {
+    static constexpr int values = 256, bytes = 82;
+};
+template <> struct Format<KDQ_IQ3_S> {
+    static constexpr int values = 256, bytes = 110;
+};
+
+// IQ2_S / IQ3_XXS / IQ3_S lattice grids (the formats' tables, re-encoded as lane indices
+// into their magnitude levels by gen_iq_grids.py).
+#define IQ_GRID_TABLE static __device__ const
+#include "iq_grids.inc"
+#undef IQ_GRID_TABLE
+
+__device__ __forceinline__ unsigned word_at(const uint8_t* p) {
+    return unsigned(p[0]) | (unsigned(p[1]) << 8) | (unsigned(p[2]) << 16) |
+           (unsigned(p[3]) << 24);
+}
+
+// v[i] = +-(scale * level): the sign is a separate product by -1 or 1, as the reference
+// decode takes it.
+__device__ __forceinline__ float signed_level(float scale, unsigned level, unsigned negative) {
+    return mul_rn(mul_rn(scale, float(level)), negative ? -1.0f : 1.0f);
+}
 
 // The 16 IQ4 code points (IQ4_NL and IQ4_XS; the format's fixed non-linear grid,
 // G/src/ggml-common.h:1120-1122), looked up two per nibble pair with v_perm.
@@ -128,6 +154,50 @@ __device__ __forceinline__ void decode_run(const uint8_t* block, unsigned within
             const unsigned e = within + i, byte = block[2 + e % 16];
             v[i] = mul_rn(d, iq4_value(e < 16 ? byte & 15u : byte >> 4));
         }
+        return;
+    } else if constexpr (ENC == KDQ_IQ3_XXS) {
+        // group word: four 7-bit sign sets (eighth sign = their parity), 4-bit scale on top
+        const float d = half_exact(half_bits_at(block));
+        const unsigned g = within / 32, pair = (within % 32) / 8;
+        const unsigned aux = word_at(block + 66 + 4 * g);
+        const float scale = mul_rn(mul_rn(d, 0.5f + float(aux >> 28)), 0.5f);
+        unsigned signs = (aux >> (7 * pair)) & 127u;
+        signs |= (__builtin_popcount(signs) & 1u) << 7;
+        const unsigned e[2] = {kIq3xxsGrid[block[2 + 8 * g + 2 * pair]],
+                               kIq3xxsGrid[block[2 + 8 * g + 2 * pair + 1]]};
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            v[i] = signed_level(scale, kIq3xxsGridLevels[(e[i / 4] >> (3 * (i % 4))) & 7u],
+                                (signs >> i) & 1u);
+        return;
+    } else if constexpr (ENC == KDQ_IQ2_S) {
+        // quarter q of group g: grid index (10 bits), sign byte, 4-bit scale
+        const float d = half_exact(half_bits_at(block));
+        const unsigned g = within / 32, q = (within % 32) / 8;
+        const unsigned nibble = q < 2 ? block[74 + g] & 15u : unsigned(block[74 + g]) >> 4;
+        const float scale = mul_rn(mul_rn(d, 0.5f + float(nibble)), 0.25f);
+        const unsigned index = block[2 + 4 * g + q] |
+                               ((unsigned(block[66 + g]) << (8 - 2 * q)) & 0x300u);
+        const unsigned e = kIq2sGrid[index], signs = block[34 + 4 * g + q];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            v[i] = signed_level(scale, kIq2sGridLevels[(e >> (2 * i)) & 3u], (signs >> i) & 1u);
+        return;
+    } else if constexpr (ENC == KDQ_IQ3_S) {
+        // quarter q of group g: two grid entries (9-bit indices), sign byte, scale 1 + 2s
+        const float d = half_exact(half_bits_at(block));
+        const unsigned g = within / 32, q = (within % 32) / 8;
+        const unsigned nibble = g % 2 ? unsigned(block[106 + g / 2]) >> 4 : block[106 + g / 2] & 15u;
+        const float scale = mul_rn(d, float(int(1 + 2 * nibble)));
+        const unsigned high = block[66 + g], signs = block[74 + 4 * g + q];
+        unsigned e[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            e[h] = kIq3sGrid[block[2 + 8 * g + 2 * q + h] | ((high << (8 - 2 * q - h)) & 256u)];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            v[i] = signed_level(scale, kIq3sGridLevels[(e[i / 4] >> (3 * (i % 4))) & 7u],
+                                (signs >> i) & 1u);
         return;
     } else if constexpr (ENC == KDQ_IQ4_XS) {
         // 8 groups of 32 with 6-bit scales minus 32, indices laid out as IQ4_NL
@@ -1369,6 +1439,12 @@ int with_encoding(int encoding, F&& f) {
         return f(std::integral_constant<int, KDQ_IQ4_XS>{});
     case KDQ_BF16:
         return f(std::integral_constant<int, KDQ_BF16>{});
+    case KDQ_IQ3_XXS:
+        return f(std::integral_constant<int, KDQ_IQ3_XXS>{});
+    case KDQ_IQ2_S:
+        return f(std::integral_constant<int, KDQ_IQ2_S>{});
+    case KDQ_IQ3_S:
+        return f(std::integral_constant<int, KDQ_IQ3_S>{});
     default:
         return KDQ_ERR_UNSUPPORTED;
     }

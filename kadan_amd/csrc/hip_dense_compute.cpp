@@ -55,6 +55,12 @@ int ggml_type(gguf::Encoding e) {
         return KDQ_IQ4_XS;
     case gguf::Encoding::bf16:
         return KDQ_BF16;
+    case gguf::Encoding::iq3_xxs:
+        return KDQ_IQ3_XXS;
+    case gguf::Encoding::iq2_s:
+        return KDQ_IQ2_S;
+    case gguf::Encoding::iq3_s:
+        return KDQ_IQ3_S;
     default:
         return -1;
     }

@@ -129,6 +129,9 @@ inline size_t block_values(int encoding) {
     case KDQ_Q4_K:
     case KDQ_Q6_K:
     case KDQ_IQ4_XS:
+    case KDQ_IQ3_XXS:
+    case KDQ_IQ2_S:
+    case KDQ_IQ3_S:
         return 256;
     default:
         return 0;
@@ -145,7 +148,12 @@ inline size_t block_bytes(int encoding) {
     case KDQ_Q4_K:
         return 144;
     case KDQ_Q3_K:
+    case KDQ_IQ3_S:
         return 110;
+    case KDQ_IQ3_XXS:
+        return 98;
+    case KDQ_IQ2_S:
+        return 82;
     case KDQ_Q6_K:
         return 210;
     case KDQ_IQ4_XS:

@@ -107,12 +107,15 @@ def q4_k_weights(seed: int, n_out: int, n_in: int, scale: float = 0.005) -> np.n
 _RANDOM_CODE_FORMATS = {11: (256, 110, 108, 0.005),   # Q3_K
                         14: (256, 210, 208, 0.0005),  # Q6_K
                         20: (32, 18, 0, 0.0005),      # IQ4_NL
-                        23: (256, 136, 0, 0.0002)}    # IQ4_XS
+                        23: (256, 136, 0, 0.0002),    # IQ4_XS
+                        18: (256, 98, 0, 0.0001),     # IQ3_XXS
+                        22: (256, 82, 0, 0.0002),     # IQ2_S
+                        21: (256, 110, 0, 0.0001)}    # IQ3_S
 
 
 def random_code_weights(encoding: int, seed: int, n_out: int, n_in: int) -> np.ndarray:
     """[n_out, n_in/values*bytes]: uniform code and scale bytes, the fp16 block scale
-    d = fp16(|N|*scale) (Q3_K, Q6_K, IQ4_NL, IQ4_XS)."""
+    d = fp16(|N|*scale) (Q3_K, Q6_K, IQ4_NL, IQ4_XS, IQ3_XXS, IQ2_S, IQ3_S)."""
     values, nbytes, at, scale = _RANDOM_CODE_FORMATS[encoding]
     nb = n_in // values
     blocks = random_bytes(seed, 1, n_out * nb * nbytes).reshape(n_out, nb, nbytes)

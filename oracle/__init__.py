@@ -24,10 +24,11 @@ REFERENCE_ROOT = "/root/reference/services/hikari/inference_worker"
 
 Q4_0, Q8_0, Q4_K = 2, 8, 12
 Q3_K, Q6_K, IQ4_NL, IQ4_XS, BF16 = 11, 14, 20, 23, 30
+IQ3_XXS, IQ3_S, IQ2_S = 18, 21, 22
 BLOCK_VALUES = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q3_K: 256, Q6_K: 256, IQ4_NL: 32, IQ4_XS: 256,
-                BF16: 1}
+                BF16: 1, IQ3_XXS: 256, IQ3_S: 256, IQ2_S: 256}
 BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q3_K: 110, Q6_K: 210, IQ4_NL: 18, IQ4_XS: 136,
-               BF16: 2}
+               BF16: 2, IQ3_XXS: 98, IQ3_S: 110, IQ2_S: 82}
 
 
 def build(reference: bool | None = None) -> None:

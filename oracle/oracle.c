@@ -94,6 +94,9 @@ int kdo_block_values(int encoding) {
     case KDO_Q4_K:
     case KDO_Q6_K:
     case KDO_IQ4_XS:
+    case KDO_IQ3_XXS:
+    case KDO_IQ2_S:
+    case KDO_IQ3_S:
         return 256;
     default:
         return 0;
@@ -118,8 +121,96 @@ int kdo_block_bytes(int encoding) {
         return 136; /* fp16 d, 16-bit high scale bits, 4 low scale bytes, 128 index bytes */
     case KDO_BF16:
         return 2;
+    case KDO_IQ3_XXS:
+        return 98; /* fp16 d, 64 grid bytes, 8 sign/scale words */
+    case KDO_IQ2_S:
+        return 82; /* fp16 d, 32 grid bytes, 32 sign bytes, 8 high-bit bytes, 8 scale bytes */
+    case KDO_IQ3_S:
+        return 110; /* fp16 d, 64 grid bytes, 8 high-bit bytes, 32 sign bytes, 4 scale bytes */
     default:
         return 0;
+    }
+}
+
+/* IQ2_S / IQ3_XXS / IQ3_S lattice grids (format tables, re-encoded as lane indices into
+ * their magnitude levels by kadan_amd/csrc/gen_iq_grids.py). */
+#define IQ_GRID_TABLE static const
+#include "../kadan_amd/csrc/iq_grids.inc"
+
+static unsigned iq2s_level(unsigned index, unsigned lane) {
+    return kIq2sGridLevels[(kIq2sGrid[index] >> (2 * lane)) & 3u];
+}
+static unsigned iq3xxs_level(unsigned index, unsigned lane) {
+    return kIq3xxsGridLevels[(kIq3xxsGrid[index] >> (3 * lane)) & 7u];
+}
+static unsigned iq3s_level(unsigned index, unsigned lane) {
+    return kIq3sGridLevels[(kIq3sGrid[index] >> (3 * lane)) & 7u];
+}
+
+static uint32_t load_u32(const uint8_t* p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+/* IQ3_XXS: 8 groups of 32.  Group g's 32-bit word at 66 + 4g holds four 7-bit sign sets
+ * (the eighth sign is their parity) and a 4-bit scale s in its top bits; the group's 8
+ * grid bytes at 2 + 8g pick IQ3_XXS grid entries of 4 magnitudes each.
+ * w = +-((d * (0.5 + s)) * 0.5) * magnitude, every product rounded. */
+static void decode_iq3_xxs(const uint8_t* block, float* out) {
+    const float d = kdo_half_to_float(load_u16(block));
+    for (unsigned g = 0; g < 8; ++g) {
+        const uint32_t aux = load_u32(block + 66 + 4 * g);
+        const float scale = (d * (0.5f + (float)(aux >> 28))) * 0.5f;
+        for (unsigned pair = 0; pair < 4; ++pair) {
+            unsigned signs = (aux >> (7 * pair)) & 127u;
+            const unsigned parity = (unsigned)__builtin_popcount(signs) & 1u;
+            signs |= parity << 7;
+            for (unsigned lane = 0; lane < 8; ++lane) {
+                const unsigned index = block[2 + 8 * g + 2 * pair + lane / 4];
+                const float magnitude = scale * (float)iq3xxs_level(index, lane % 4);
+                out[32 * g + 8 * pair + lane] = magnitude * ((signs >> lane) & 1u ? -1.0f : 1.0f);
+            }
+        }
+    }
+}
+
+/* IQ2_S: 8 groups of 32, quarters of 8.  Quarter q of group g: grid index = byte
+ * 2 + 4g + q with bits 8..9 from byte 66 + g (bits 2q..2q+1), sign bits from byte
+ * 34 + 4g + q, 4-bit scale from byte 74 + g (low nibble for q < 2).
+ * w = +-((d * (0.5 + s)) * 0.25) * magnitude. */
+static void decode_iq2_s(const uint8_t* block, float* out) {
+    const float d = kdo_half_to_float(load_u16(block));
+    for (unsigned g = 0; g < 8; ++g)
+        for (unsigned q = 0; q < 4; ++q) {
+            const unsigned nibble = q < 2 ? block[74 + g] & 15u : (unsigned)block[74 + g] >> 4;
+            const float scale = (d * (0.5f + (float)nibble)) * 0.25f;
+            const unsigned index = block[2 + 4 * g + q] | (((unsigned)block[66 + g] << (8 - 2 * q)) & 0x300u);
+            const unsigned signs = block[34 + 4 * g + q];
+            for (unsigned lane = 0; lane < 8; ++lane) {
+                const float magnitude = scale * (float)iq2s_level(index, lane);
+                out[32 * g + 8 * q + lane] = magnitude * ((signs >> lane) & 1u ? -1.0f : 1.0f);
+            }
+        }
+}
+
+/* IQ3_S: 8 groups of 32, quarters of 8 (two grid entries of 4 each).  Entry h of quarter
+ * q of group g: index = byte 2 + 8g + 2q + h with bit 8 from byte 66 + g (bit 2q + h);
+ * sign bits from byte 74 + 4g + q; scale d * (1 + 2s) with the 4-bit s of byte 106 + g/2
+ * (low nibble for even g). */
+static void decode_iq3_s(const uint8_t* block, float* out) {
+    const float d = kdo_half_to_float(load_u16(block));
+    for (unsigned g = 0; g < 8; ++g) {
+        const unsigned nibble = g % 2 ? (unsigned)block[106 + g / 2] >> 4 : block[106 + g / 2] & 15u;
+        const float scale = d * (float)(int)(1 + 2 * nibble);
+        for (unsigned q = 0; q < 4; ++q) {
+            const unsigned signs = block[74 + 4 * g + q];
+            for (unsigned lane = 0; lane < 8; ++lane) {
+                const unsigned h = lane / 4;
+                const unsigned index = block[2 + 8 * g + 2 * q + h] |
+                                       (((unsigned)block[66 + g] << (8 - 2 * q - h)) & 256u);
+                const float magnitude = scale * (float)iq3s_level(index, lane % 4);
+                out[32 * g + 8 * q + lane] = magnitude * ((signs >> lane) & 1u ? -1.0f : 1.0f);
+            }
+        }
     }
 }
 
@@ -217,6 +308,12 @@ static void decode_block(int encoding, const uint8_t* block, float* out) {
     case KDO_BF16:
         out[0] = kdo_bf16_to_float(load_u16(block));
         return;
+    case KDO_IQ3_XXS:
+        return decode_iq3_xxs(block, out);
+    case KDO_IQ2_S:
+        return decode_iq2_s(block, out);
+    case KDO_IQ3_S:
+        return decode_iq3_s(block, out);
     default:
         break;
     }

@@ -46,7 +46,10 @@ enum {
     KDO_Q3_K = 11,
     KDO_Q4_K = 12,
     KDO_Q6_K = 14,
+    KDO_IQ3_XXS = 18,
     KDO_IQ4_NL = 20,
+    KDO_IQ3_S = 21,
+    KDO_IQ2_S = 22,
     KDO_IQ4_XS = 23,
     KDO_BF16 = 30
 };
@@ -72,6 +75,10 @@ int kdo_block_bytes(int encoding);
  * IQ4_NL  IW/include/kadan/gguf_quantization.hpp:695-701 (G/src/ggml-quants.c:2726, dequantize_row_iq4_nl)
  * IQ4_XS  IW/include/kadan/gguf_quantization.hpp:736-748 (G/src/ggml-quants.c:2744, dequantize_row_iq4_xs)
  * BF16    IW/include/kadan/gguf_quantization.hpp:633-636 (one value per 2-byte block)
+ * IQ3_XXS IW/include/kadan/gguf_quantization.hpp:674-694 (G/src/ggml-quants.c dequantize_row_iq3_xxs)
+ * IQ2_S   IW/include/kadan/gguf_quantization.hpp:702-718 (dequantize_row_iq2_s)
+ * IQ3_S   IW/include/kadan/gguf_quantization.hpp:719-735 (dequantize_row_iq3_s)
+ *         (the three lattice grids: kadan_amd/csrc/iq_grids.inc, ggml's tables re-encoded)
  * Q4_0    G/src/ggml-quants.c:459-476 (dequantize_row_q4_0)
  * Returns 0, or -1 for an unknown encoding / ragged row. */
 int kdo_dequantize_row(int encoding, const uint8_t* row, size_t in, float* out);

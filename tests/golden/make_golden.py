@@ -12,9 +12,12 @@ Contents (all little-endian, plain arrays, no pickles):
       Q3_K, Q6_K, IQ4_NL, IQ4_XS the same way from a second generator (seed
       0x27182818, so the arrays above keep their bytes), the scale at the format's
       offset (108 for Q3_K, 208 for Q6_K) as that test places it; BF16 as 256 values
-      (512 random bytes, the first 16 values the special patterns).
-  kadan_<fmt>_values         kadan::gguf::decode of the same blocks (the reference's own
-                             device decode, IW/include/kadan/gguf_quantization.hpp:631-762)
+      (512 random bytes, the first 16 values the special patterns); IQ3_XXS, IQ2_S,
+      IQ3_S as 256 random blocks each from a third generator (seed 0x14142135) plus
+      blocks whose grid indices enumerate the whole grid.
+  (for these formats the script also checks kadan::gguf::decode, the reference's own
+  device decode, IW/include/kadan/gguf_quantization.hpp:631-762, equal to ggml on every
+  block, and stores the values once)
   q8_0_x / q8_0_bytes        ggml x86 quantize_row_q8_0 (G/src/ggml-cpu/arch/x86/quants.c:302-398)
   q8_K_x / q8_K_bytes        ggml quantize_row_q8_K (G/src/ggml-quants.c:2769-2806)
   dot_<fmt>_w / dot_<fmt>_x / dot_<fmt>_out   ggml AVX2 vec_dot against the dot type
@@ -32,12 +35,13 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
 
-from oracle import (BF16, BLOCK_BYTES, BLOCK_VALUES, IQ4_NL, IQ4_XS, Q3_K, Q4_0, Q4_K,  # noqa: E402
-                    Q6_K, Q8_0, Reference)
+from oracle import (BF16, BLOCK_BYTES, BLOCK_VALUES, IQ2_S, IQ3_S, IQ3_XXS, IQ4_NL,  # noqa: E402
+                    IQ4_XS, Q3_K, Q4_0, Q4_K, Q6_K, Q8_0, Reference)
 
 OUT = os.path.join(HERE, "reference_vectors.npz")
 NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q3_K: "q3_k", Q6_K: "q6_k",
-         IQ4_NL: "iq4_nl", IQ4_XS: "iq4_xs", BF16: "bf16"}
+         IQ4_NL: "iq4_nl", IQ4_XS: "iq4_xs", BF16: "bf16", IQ3_XXS: "iq3_xxs",
+         IQ2_S: "iq2_s", IQ3_S: "iq3_s"}
 SCALE_OFFSET = {Q3_K: 108, Q6_K: 208}
 SPECIAL_HALVES = [0x0000, 0x8000, 0x0001, 0x8001, 0x03FF, 0x83FF, 0x0400, 0x8400, 0x3C00,
                   0xBC00, 0x7BFF, 0xFBFF, 0x7C00, 0xFC00, 0x7E01, 0x7C01]
@@ -83,6 +87,37 @@ def finite_weights(encoding, n_out, n_in, rng):
     return blocks.reshape(n_out, -1)
 
 
+def grid_blocks(enc, rng):
+    """Random blocks whose grid indices enumerate every entry of the format's grid (32
+    IQ2_S blocks, 4 IQ3_XXS, 8 IQ3_S), so the fixture pins each table entry."""
+    entries = {IQ2_S: 1024, IQ3_XXS: 256, IQ3_S: 512}[enc]
+    per_block = {IQ2_S: 32, IQ3_XXS: 64, IQ3_S: 64}[enc]
+    blocks = random_blocks(enc, entries // per_block, rng)
+    for t, block in enumerate(blocks):
+        index = np.arange(t * per_block, (t + 1) * per_block)
+        if enc == IQ3_XXS:
+            block[2:66] = index
+        elif enc == IQ2_S:  # slot 4g + q: low byte, bits 8..9 in byte 66 + g at 2q
+            block[2:34] = index & 255
+            high = (index >> 8).reshape(8, 4)
+            block[66:74] = (high << (2 * np.arange(4))).sum(axis=1)
+        else:  # IQ3_S slot 8g + 2q + h: low byte, bit 8 in byte 66 + g at 2q + h
+            block[2:66] = index & 255
+            high = (index >> 8).reshape(8, 8)
+            block[66:74] = (high << np.arange(8)).sum(axis=1)
+    return blocks
+
+
+def check_kadan_equals_ggml(ref, enc, blocks, ggml_values):
+    """kadan::gguf::decode (the reference's device decode) must equal ggml to_float on
+    every block, bit for bit (NaN matches NaN), as IW/tests/gguf_quantization.cpp:93-147
+    requires; the fixture then stores the ggml values once."""
+    for b, want in zip(blocks, ggml_values):
+        got = ref.kadan_decode_block(enc, b)
+        same = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+        assert same.all(), NAMES[enc]
+
+
 def main():
     if not Reference.available():
         raise SystemExit("oracle/_ref/libkadan_ref.so is not built (make -C oracle ref)")
@@ -100,13 +135,19 @@ def main():
         data[f"decode_{NAMES[enc]}_blocks"] = blocks
         data[f"decode_{NAMES[enc]}_values"] = ref.to_float(enc, blocks.reshape(1, -1),
                                                            64 * BLOCK_VALUES[enc]).reshape(64, -1)
-        data[f"kadan_{NAMES[enc]}_values"] = np.stack(
-            [ref.kadan_decode_block(enc, b) for b in blocks])
+        check_kadan_equals_ggml(ref, enc, blocks, data[f"decode_{NAMES[enc]}_values"])
     bf = np.array([rng2() & 255 for _ in range(512)], np.uint8)
     bf.view(np.uint16)[:16] = SPECIAL_HALVES  # 0, -0, subnormals, max, inf, NaNs as bf16 bits
     data["decode_bf16_blocks"] = bf.reshape(256, 2)
     data["decode_bf16_values"] = ref.to_float(BF16, bf.reshape(1, -1), 256).reshape(256, 1)
-    data["kadan_bf16_values"] = np.stack([ref.kadan_decode_block(BF16, b) for b in bf.reshape(256, 2)])
+    check_kadan_equals_ggml(ref, BF16, bf.reshape(256, 2), data["decode_bf16_values"])
+    rng3 = XorShift32(0x14142135)
+    for enc in (IQ3_XXS, IQ2_S, IQ3_S):
+        blocks = np.concatenate([random_blocks(enc, 256, rng3), grid_blocks(enc, rng3)])
+        data[f"decode_{NAMES[enc]}_blocks"] = blocks
+        data[f"decode_{NAMES[enc]}_values"] = ref.to_float(
+            enc, blocks.reshape(1, -1), len(blocks) * BLOCK_VALUES[enc]).reshape(len(blocks), -1)
+        check_kadan_equals_ggml(ref, enc, blocks, data[f"decode_{NAMES[enc]}_values"])
     # activation quantizers: N(0,1) values plus exact half-way cases after scaling
     g = np.random.default_rng(0x5EED)
     x = g.standard_normal(512).astype(np.float32)

@@ -148,7 +148,7 @@ def probe(device):
     p.close()
 
 
-@pytest.mark.parametrize("enc", [Q8_0, Q4_0, Q4_K, Q3_K, Q6_K, IQ4_NL, IQ4_XS, BF16])
+@pytest.mark.parametrize("enc", [Q8_0, Q4_0, Q4_K, Q3_K, Q6_K, IQ4_NL, IQ4_XS, BF16, IQ3_XXS, 21, 22])
 @pytest.mark.parametrize("rows", [1, 3, 8, 20])
 def test_dense_gguf_source_parity_and_bank(probe, oracle, enc, rows):
     n_in, n_out = 1024, 96
@@ -180,7 +180,7 @@ def test_dense_gguf_source_not_retained(probe, oracle):
 def test_dense_gguf_source_unsupported_reads_nothing(probe):
     x = np.ones((1, 512), np.float32)
     w = np.zeros(64 * 512, np.uint8)
-    res, y = probe.gguf(1, IQ3_XXS, w, x, 64)  # encoding not run here
+    res, y = probe.gguf(1, 3, w, x, 64)  # GGML type 3 (Q4_1): no encoding here
     assert res == UNSUPPORTED
     res, _ = probe.gguf(1, Q4_0, w, np.ones((1, 48), np.float32), 64)  # 48 % 32 != 0
     assert res == UNSUPPORTED
@@ -221,7 +221,7 @@ def test_dense_gguf_batch_shared_input(probe, oracle):
 def test_dense_gguf_batch_unsupported_job_reads_nothing(probe):
     x = np.ones((1, 256), np.float32)
     w = synth.gguf_weights(Q8_0, 0xDC, 32, 256)
-    res, ys = probe.batch([(1, Q8_0, w, x, 32), (2, IQ3_XXS, np.zeros(32 * 98, np.uint8), x, 32)])
+    res, ys = probe.batch([(1, Q8_0, w, x, 32), (2, 3, np.zeros(32 * 20, np.uint8), x, 32)])
     assert res == UNSUPPORTED and probe.reads == 0 and np.isnan(ys[0]).all()
 
 

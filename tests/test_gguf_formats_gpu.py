@@ -1,5 +1,6 @@
 """GPU parity of the decode and the exact product for the encodings without a streaming
-kernel (Q3_K, Q6_K, IQ4_NL, IQ4_XS, BF16; IW/include/kadan/gguf_quantization.hpp:631-762).
+kernel (Q3_K, Q6_K, IQ4_NL, IQ4_XS, IQ3_XXS, IQ2_S, IQ3_S, BF16;
+IW/include/kadan/gguf_quantization.hpp:631-762).
 
 Decoded weights must be bit-exact to the oracle (NaN matches NaN, as
 IW/tests/gguf_quantization.cpp:21-29 compares), including the special fp16 block scales
@@ -16,10 +17,13 @@ from tests.util import assert_close
 pytestmark = pytest.mark.gpu
 
 Q3_K, Q6_K, IQ4_NL, IQ4_XS, BF16 = 11, 14, 20, 23, 30
-ENCODINGS = [Q3_K, Q6_K, IQ4_NL, IQ4_XS, BF16]
-BV = {Q3_K: 256, Q6_K: 256, IQ4_NL: 32, IQ4_XS: 256, BF16: 1}
-BB = {Q3_K: 110, Q6_K: 210, IQ4_NL: 18, IQ4_XS: 136, BF16: 2}
-SCALE_AT = {Q3_K: 108, Q6_K: 208, IQ4_NL: 0, IQ4_XS: 0}
+IQ3_XXS, IQ3_S, IQ2_S = 18, 21, 22
+ENCODINGS = [Q3_K, Q6_K, IQ4_NL, IQ4_XS, IQ3_XXS, IQ2_S, IQ3_S, BF16]
+BV = {Q3_K: 256, Q6_K: 256, IQ4_NL: 32, IQ4_XS: 256, BF16: 1, IQ3_XXS: 256, IQ2_S: 256,
+      IQ3_S: 256}
+BB = {Q3_K: 110, Q6_K: 210, IQ4_NL: 18, IQ4_XS: 136, BF16: 2, IQ3_XXS: 98, IQ2_S: 82,
+      IQ3_S: 110}
+SCALE_AT = {Q3_K: 108, Q6_K: 208, IQ4_NL: 0, IQ4_XS: 0, IQ3_XXS: 0, IQ2_S: 0, IQ3_S: 0}
 SPECIAL_HALVES = [0x0000, 0x8000, 0x0001, 0x8001, 0x03FF, 0x83FF, 0x0400, 0x8400, 0x3C00,
                   0xBC00, 0x7BFF, 0xFBFF, 0x7C00, 0xFC00, 0x7E01, 0x7C01]
 
@@ -48,6 +52,27 @@ def special_rows(encoding, seed):
     for i, h in enumerate(SPECIAL_HALVES):
         blocks[i, at], blocks[i, at + 1] = h & 0xFF, h >> 8
     return blocks.reshape(count // 8, 8 * BB[encoding]), 8 * BV[encoding]
+
+
+def test_iq_grids_every_entry(device, oracle, golden_iq):
+    """Blocks whose grid indices enumerate each IQ grid: every device table entry decodes
+    as the oracle's (itself pinned to ggml on the same blocks)."""
+    torch = _torch()
+    from kadan_amd import ops
+    for encoding, blocks in golden_iq.items():
+        expected = oracle.dequantize(encoding, blocks, 256)
+        got = ops.dequantize(encoding, torch.from_numpy(blocks).to(device), 256)
+        assert same_bits_or_nan(got.cpu().numpy(), expected), encoding
+
+
+@pytest.fixture(scope="module")
+def golden_iq():
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                        "reference_vectors.npz")
+    with np.load(path, allow_pickle=False) as f:
+        return {IQ3_XXS: f["decode_iq3_xxs_blocks"], IQ2_S: f["decode_iq2_s_blocks"],
+                IQ3_S: f["decode_iq3_s_blocks"]}
 
 
 @pytest.mark.parametrize("encoding", ENCODINGS)
@@ -95,7 +120,7 @@ def test_gemv_parity(device, oracle, encoding, exact, shape):
     assert int(status.item()) == 0
 
 
-@pytest.mark.parametrize("encoding", [Q3_K, Q6_K, IQ4_NL, IQ4_XS])
+@pytest.mark.parametrize("encoding", [Q3_K, Q6_K, IQ4_NL, IQ4_XS, IQ3_XXS, IQ2_S, IQ3_S])
 def test_gemv_nonfinite_scale_status(device, encoding):
     torch = _torch()
     w = synth.gguf_weights(encoding, 3, 16, 512)
@@ -115,7 +140,7 @@ def test_batch_mixes_streamed_and_exact_encodings(device, oracle):
     shared = synth.normal(19, 1, 2 * 1024).reshape(2, 1024)
     xs = torch.from_numpy(shared).to(device)
     jobs, expected = [], []
-    for i, enc in enumerate([12, Q6_K, 8, Q3_K, IQ4_XS, 2, IQ4_NL, BF16]):
+    for i, enc in enumerate([12, Q6_K, 8, Q3_K, IQ4_XS, 2, IQ4_NL, BF16, IQ3_XXS, IQ2_S, IQ3_S]):
         n_out = 40 + 8 * i
         w = synth.gguf_weights(enc, 60 + i, n_out, 1024)
         jobs.append({"encoding": enc, "weights": torch.from_numpy(w).to(device), "input": xs,

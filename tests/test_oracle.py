@@ -18,11 +18,15 @@ from kadan_amd import synth
 
 Q4_0, Q8_0, Q4_K = 2, 8, 12
 Q3_K, Q6_K, IQ4_NL, IQ4_XS, BF16 = 11, 14, 20, 23, 30
-NEW = [Q3_K, Q6_K, IQ4_NL, IQ4_XS, BF16]
-BV = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q3_K: 256, Q6_K: 256, IQ4_NL: 32, IQ4_XS: 256, BF16: 1}
-BB = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q3_K: 110, Q6_K: 210, IQ4_NL: 18, IQ4_XS: 136, BF16: 2}
+IQ3_XXS, IQ3_S, IQ2_S = 18, 21, 22
+NEW = [Q3_K, Q6_K, IQ4_NL, IQ4_XS, BF16, IQ3_XXS, IQ2_S, IQ3_S]
+BV = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q3_K: 256, Q6_K: 256, IQ4_NL: 32, IQ4_XS: 256, BF16: 1,
+      IQ3_XXS: 256, IQ2_S: 256, IQ3_S: 256}
+BB = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q3_K: 110, Q6_K: 210, IQ4_NL: 18, IQ4_XS: 136, BF16: 2,
+      IQ3_XXS: 98, IQ2_S: 82, IQ3_S: 110}
 NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q3_K: "q3_k", Q6_K: "q6_k",
-         IQ4_NL: "iq4_nl", IQ4_XS: "iq4_xs", BF16: "bf16"}
+         IQ4_NL: "iq4_nl", IQ4_XS: "iq4_xs", BF16: "bf16", IQ3_XXS: "iq3_xxs",
+         IQ2_S: "iq2_s", IQ3_S: "iq3_s"}
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
                       "reference_vectors.npz")
 
@@ -180,11 +184,28 @@ def test_bf16_is_the_upper_half_of_binary32(oracle):
 
 @pytest.mark.parametrize("encoding", NEW)
 def test_new_formats_vs_reference_vectors(oracle, golden, encoding):
-    """ggml to_float and kadan::gguf::decode of the same blocks (specials included)."""
+    """ggml to_float of the same blocks (specials included; kadan::gguf::decode equal to
+    it on every block, checked when the fixture was made).  For the IQ grid formats the
+    256 blocks draw every grid entry, pinning the re-encoded grid tables."""
     blocks = golden[f"decode_{NAMES[encoding]}_blocks"]
     got = oracle.dequantize(encoding, blocks, BV[encoding])
     assert same_bits(got, golden[f"decode_{NAMES[encoding]}_values"])
-    assert same_bits(got, golden[f"kadan_{NAMES[encoding]}_values"])
+
+
+def test_iq_grid_fixture_draws_every_entry(golden):
+    """The golden IQ blocks index every entry of each grid at least once (so a wrong
+    entry of a re-encoded table cannot pass test_new_formats_vs_reference_vectors)."""
+    b = golden["decode_iq2_s_blocks"].astype(np.int64)
+    q = np.arange(4)
+    idx = b[:, 2:34].reshape(-1, 8, 4) | ((b[:, 66:74, None] << (8 - 2 * q)) & 0x300)
+    assert np.unique(idx).size == 1024
+    b = golden["decode_iq3_xxs_blocks"]
+    assert np.unique(b[:, 2:66]).size == 256
+    b = golden["decode_iq3_s_blocks"].astype(np.int64)
+    lo = b[:, 2:66].reshape(-1, 8, 4, 2)
+    shift = (8 - 2 * q[:, None] - np.arange(2)[None, :])
+    idx = lo | ((b[:, 66:74, None, None] << shift) & 256)
+    assert np.unique(idx).size == 512
 
 
 @pytest.mark.parametrize("encoding", NEW)
