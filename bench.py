@@ -42,6 +42,7 @@ FP16_PEAK_TFLOPS = 2500.0      # dense fp16/bf16 MFMA
 FP4_PEAK_TFLOPS = 10100.0      # dense MXFP4 MFMA
 Q4_K, Q8_0, Q4_0 = 12, 8, 2
 Q3_K, Q6_K, IQ4_NL, IQ4_XS, BF16 = 11, 14, 20, 23, 30
+IQ3_XXS, IQ3_S, IQ2_S = 18, 21, 22
 
 
 def parse():
@@ -82,7 +83,8 @@ def keep_mask(encoding: int, shape) -> np.ndarray:
     if encoding == BF16:
         return np.ones(shape, bool)
     keep = np.zeros(row_bytes, bool)
-    block = {Q4_K: 144, Q8_0: 34, Q4_0: 18, Q3_K: 110, Q6_K: 210, IQ4_NL: 18, IQ4_XS: 136}[encoding]
+    block = {Q4_K: 144, Q8_0: 34, Q4_0: 18, Q3_K: 110, Q6_K: 210, IQ4_NL: 18, IQ4_XS: 136,
+             IQ3_XXS: 98, IQ3_S: 110, IQ2_S: 82}[encoding]
     at, head = {Q4_K: (0, 4), Q3_K: (108, 2), Q6_K: (208, 2)}.get(encoding, (0, 2))
     for b in range(0, row_bytes, block):
         keep[b + at:b + at + head] = True
@@ -477,7 +479,8 @@ def main():
         gemv_line("c2_q4_k_gate_up_pair", Q4_K, n_in, n_out, 0xC2C, 1000,
                   "C2 Q4_K gate+up 2 x (4096->14336), batch 1, one kdq_gemv_batch "
                   "submission (one fused launch)", per_step=2)
-        for enc, tag in ((Q6_K, "q6_k"), (Q3_K, "q3_k"), (IQ4_XS, "iq4_xs"), (BF16, "bf16")):
+        for enc, tag in ((Q6_K, "q6_k"), (Q3_K, "q3_k"), (IQ4_XS, "iq4_xs"), (IQ3_XXS, "iq3_xxs"),
+                         (IQ2_S, "iq2_s"), (BF16, "bf16")):
             gemv_line(f"gemv_{tag}_4096x14336_exact", enc, n_in, n_out, 0xF0 + enc, 50,
                       f"{tag.upper()} GEMV 4096->14336, batch 1, row-major bytes (exact-decode "
                       "product: no streaming kernel for this encoding yet)", packed=False,
