@@ -356,6 +356,47 @@ def bench_gemm(torch, reps=10, count=20, packed=True):
             "note": "per launch: activation quantize + fp16-MFMA GEMM"}
 
 
+def bench_moe_gguf(torch, rows, reps=10, count=20):
+    """The GGUF MoE layer (kdq_moe_gguf) at Qwen3-30B-A3B's geometry: hidden 2048, 128
+    experts, top-8, expert ff 768, a 768-wide shared expert; Q4_K expert gate/up, Q6_K
+    expert down, Q8_0 shared gate/up, Q4_K shared down, an fp32 router.  Each launch takes
+    the next of 16 inputs, so the routed experts change between calls."""
+    from kadan_amd import ops, row_bytes, synth
+    H, E, K, F, S = 2048, 128, 8, 768, 768
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    g = np.random.default_rng(0xE3)
+    spec = dict(hidden=H, experts=E, top_k=K, ff=F, shared_ff=S,
+                shared_gate=dev((g.standard_normal(H) * 0.05).astype(np.float32)),
+                router=(0, dev((g.standard_normal((E, H)) * 0.1).astype(np.float32)
+                               .view(np.uint8).reshape(E, -1))))
+    encs = {"gate_exps": (Q4_K, (E, F, H)), "up_exps": (Q4_K, (E, F, H)),
+            "down_exps": (Q6_K, (E, H, F)), "gate_shexp": (Q8_0, (S, H)),
+            "up_shexp": (Q8_0, (S, H)), "down_shexp": (Q4_K, (H, S))}
+    for i, (name, (enc, shape)) in enumerate(encs.items()):
+        w = synth.gguf_weights(enc, 0xE30 + i, int(np.prod(shape[:-1])), shape[-1])
+        spec[name] = (enc, dev(w.reshape(*shape[:-1], -1)))
+    xs = [dev(synth.normal(0xE4 + i, 1, rows * H).reshape(rows, H)) for i in range(16)]
+    launch = lambda i: ops.moe_gguf(spec, xs[i % 16])
+    for i in range(5):
+        launch(i)
+    ms = time_launches(torch, launch, count, reps)
+    sel = set()
+    for i in range(16):
+        sel.update(int(e) for e in launch(i)[1].cpu().numpy().ravel())
+    per_call = np.mean([len(set(launch(i)[1].cpu().numpy().ravel().tolist())) for i in range(16)])
+    expert = 2 * F * row_bytes(Q4_K, H) + H * row_bytes(Q6_K, F)
+    shared = 2 * S * row_bytes(Q8_0, H) + H * row_bytes(Q4_K, S)
+    nbytes = per_call * expert + shared + E * H * 4 + H * 4 + 2 * rows * H * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"workload": f"GGUF MoE layer (Qwen3-30B-A3B geometry) rows={rows}",
+            "ms": round(ms, 4), "experts_touched_per_call": round(float(per_call), 1),
+            "algorithmic_bytes": int(nbytes), "gbs": round(gbs, 1),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "note": "one kdq_moe_gguf submission: router + shared GEMV batch, device routing, "
+                    "device-indexed expert GEMVs (MFMA for Q4_K / Q8_0, exact for Q6_K), "
+                    "combine; bytes = touched experts + shared expert + router + x + y"}
+
+
 def moe_bytes(tokens, hidden, inter, experts_touched):
     per_expert = 3 * inter * hidden // 2 + 3 * inter * hidden // 32
     return experts_touched * per_expert + tokens * hidden * 2 + tokens * hidden * 4
@@ -489,6 +530,10 @@ def main():
             extra["c3_q4_0_gemm"] = bench_gemm(torch)
         if want("c3_q4_0_gemm_row_major"):
             extra["c3_q4_0_gemm_row_major"] = bench_gemm(torch, packed=False)
+        if want("moe_gguf_t1"):
+            extra["moe_gguf_t1"] = bench_moe_gguf(torch, 1)
+        if want("moe_gguf_t4"):
+            extra["moe_gguf_t4"] = bench_moe_gguf(torch, 4)
         if want("c4_moe_t1"):
             extra["c4_moe_t1"] = bench_moe(torch, 1, 32, 0, 0xC4, copies=2, count=50)
         if want("c4_moe_t256"):

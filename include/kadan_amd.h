@@ -42,6 +42,8 @@ enum kdq_status {
  * have the tile-packed layout.  Q4_0 is not a kadan device encoding: it is ggml's
  * block_q4_0, added for the prefill GEMM and the products. */
 enum kdq_encoding {
+    KDQ_F32 = 0,  /* plain fp32 / fp16 matrices (e.g. GGUF routers): exact product only */
+    KDQ_F16 = 1,
     KDQ_Q4_0 = 2,
     KDQ_Q8_0 = 8,
     KDQ_Q3_K = 11,
@@ -176,6 +178,43 @@ int kdq_gemm_q4_0_packed(const void* packed, size_t n, size_t k, const uint16_t*
  * q int8 [m x k], d fp32 [m x k/32]. */
 int kdq_quantize_q8(const uint16_t* x_f16, size_t m, size_t k, int8_t* q, float* d,
                     void* stream);
+
+/* ---- GGUF mixture-of-experts layer (the reference runs it on the host, calling the
+ * device three times: MoeLayer::forward, IW/src/models/text/qwen_layers.cpp:378-492;
+ * this is one stream-ordered submission with device-side routing).
+ * One weight tensor: `weights` (device) holds row-major GGUF rows of `row_bytes`; an
+ * expert stack holds `experts` slices of `expert_bytes` each (a multiple of 16). */
+typedef struct kdq_gguf_tensor {
+    const void* weights;
+    size_t row_bytes;
+    size_t expert_bytes; /* expert stacks only */
+    int32_t encoding;    /* kdq_encoding */
+} kdq_gguf_tensor;
+
+/* The layer's MoeSpec (IW/src/models/text/qwen_layers.hpp:96-98) and tensors
+ * (bind_moe, qwen_layers.cpp:357-371). */
+typedef struct kdq_moe_gguf_layer {
+    size_t hidden, experts, top_k, ff, shared_ff;
+    kdq_gguf_tensor router;     /* ffn_gate_inp: experts x hidden */
+    kdq_gguf_tensor gate_exps;  /* ffn_gate_exps: experts x (ff x hidden) */
+    kdq_gguf_tensor up_exps;    /* ffn_up_exps: experts x (ff x hidden) */
+    kdq_gguf_tensor down_exps;  /* ffn_down_exps: experts x (hidden x ff) */
+    kdq_gguf_tensor gate_shexp; /* ffn_gate_shexp: shared_ff x hidden */
+    kdq_gguf_tensor up_shexp;   /* ffn_up_shexp: shared_ff x hidden */
+    kdq_gguf_tensor down_shexp; /* ffn_down_shexp: hidden x shared_ff */
+    const float* shared_gate;   /* ffn_gate_inp_shexp: hidden floats */
+} kdq_moe_gguf_layer;
+
+/* y[rows x hidden] = MoeLayer::forward(x[rows x hidden]) (qwen_layers.cpp:378-492):
+ * router softmax (double total), top-k by probability, weights / max(sum, 2^-14); per
+ * selection silu(gate_e . x) * (up_e . x) -> down_e, summed in selection order with
+ * its weight; plus the shared expert's down(silu(gate_s . x) * (up_s . x)) scaled by
+ * sigmoid(shared_gate . x).  Optional outputs: `selected` / `weights` [rows x top_k]
+ * (the routing), `status` |= 1 for a non-finite weight scale.  Every projection decodes
+ * its weights exactly (kdq_gemv semantics).  rows * top_k <= 512, experts <= 256,
+ * top_k <= 8; x, y, shared_gate 16-byte aligned. */
+int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, size_t rows, float* y,
+                 int32_t* selected, float* weights, unsigned* status, void* stream);
 
 /* ---- MXFP4 mixture-of-experts layer (the reference has no device MoE; this composes
  * MoeLayer::forward, IW/src/models/text/qwen_layers.cpp:378-492, with the MXFP4

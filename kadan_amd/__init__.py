@@ -37,6 +37,23 @@ class KdqUnsupported(KdqError):
     pass
 
 
+class GgufTensor(C.Structure):
+    """kdq_gguf_tensor (include/kadan_amd.h)."""
+    _fields_ = [("weights", C.c_void_p), ("row_bytes", C.c_size_t),
+                ("expert_bytes", C.c_size_t), ("encoding", C.c_int32)]
+
+
+MOE_GGUF_TENSORS = ("router", "gate_exps", "up_exps", "down_exps", "gate_shexp", "up_shexp",
+                    "down_shexp")
+
+
+class MoeGgufLayer(C.Structure):
+    """kdq_moe_gguf_layer (include/kadan_amd.h)."""
+    _fields_ = [("hidden", C.c_size_t), ("experts", C.c_size_t), ("top_k", C.c_size_t),
+                ("ff", C.c_size_t), ("shared_ff", C.c_size_t)] + [
+        (name, GgufTensor) for name in MOE_GGUF_TENSORS] + [("shared_gate", C.c_void_p)]
+
+
 # (name, argtypes); every entry point returns int
 _SZ, _VP, _I = C.c_size_t, C.c_void_p, C.c_int
 _SIGNATURES = {
@@ -49,6 +66,7 @@ _SIGNATURES = {
     "kdq_gemv_packed_batch": [_VP, _SZ, _VP],
     "kdq_gemm_q4_0": [_VP, _SZ, _SZ, _VP, _SZ, _VP, _VP],
     "kdq_gemm_q4_0_packed": [_VP, _SZ, _SZ, _VP, _SZ, _VP, _VP],
+    "kdq_moe_gguf": [_VP, _VP, _SZ, _VP, _VP, _VP, _VP, _VP],
     "kdq_quantize_q8": [_VP, _SZ, _SZ, _VP, _VP, _VP],
     "kdq_moe_route": [_VP, _SZ, _SZ, _SZ, _VP, _VP, _VP, _VP, _VP],
     "kdq_mxfp4_dequantize": [_VP, _VP, _SZ, _SZ, _VP, _VP, _VP],

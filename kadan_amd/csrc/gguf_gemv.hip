@@ -51,6 +51,12 @@ template <> struct Format<KDQ_IQ4_XS> {
 template <> struct Format<KDQ_BF16> {
     static constexpr int values = 1, bytes = 2;
 };
+template <> struct Format<KDQ_F32> {
+    static constexpr int values = 1, bytes = 4;
+};
+template <> struct Format<KDQ_F16> {
+    static constexpr int values = 1, bytes = 2;
+};
 template <> struct Format<KDQ_IQ3_XXS> {
     static constexpr int values = 256, bytes = 98;
 };
@@ -113,6 +119,16 @@ __device__ __forceinline__ void decode_run(const uint8_t* block, unsigned within
 #pragma unroll
         for (int i = 0; i < 8; ++i)
             v[i] = __uint_as_float(half_bits_at(block + 2 * i) << 16);
+        return;
+    } else if constexpr (ENC == KDQ_F32) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            v[i] = __uint_as_float(half_bits_at(block + 4 * i) | (half_bits_at(block + 4 * i + 2) << 16));
+        return;
+    } else if constexpr (ENC == KDQ_F16) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            v[i] = half_exact(half_bits_at(block + 2 * i));
         return;
     } else if constexpr (ENC == KDQ_Q3_K) {
         // 16 groups of 16 with 6-bit scales (low nibbles at 96.., high pairs at 104..),
@@ -269,16 +285,25 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* packed, size
 
 // ------------------------------------------------------------- exact GEMV
 
+// `index` (optional): the weights start at weights + min(*index, index_limit - 1) *
+// index_stride (the expert a device-side routing chose).
 template <int ENC, int ROWS>
 __global__ __launch_bounds__(256) void exact_gemv(const uint8_t* weights, size_t row_bytes,
                                                   const float* x, unsigned rows, unsigned in,
                                                   unsigned out, float* y, size_t stride,
-                                                  unsigned* status) {
+                                                  unsigned* status, const int32_t* index,
+                                                  size_t index_stride, unsigned index_limit,
+                                                  size_t x_step, size_t y_step) {
     using F = Format<ENC>;
     const unsigned column = blockIdx.x * 4 + threadIdx.x / 64;
     const unsigned lane = threadIdx.x % 64;
     if (column >= out)
         return;
+    // job blockIdx.y of an affine batch: its input, output and expert index step along
+    x += blockIdx.y * x_step;
+    y += blockIdx.y * y_step;
+    if (index)
+        weights += size_t(min(unsigned(index[blockIdx.y]), index_limit - 1)) * index_stride;
     const uint8_t* row = weights + size_t(column) * row_bytes;
     float sums[ROWS] = {};
     bool finite = true;
@@ -945,17 +970,24 @@ struct UnitCursor {
 // reference runs every job of a submission in one launch per format,
 // IW/src/cuda/h3_compute.cu:336-382).
 constexpr int kMaxFused = 8;
-struct MfmaJob {  // one job's fields together: one scalar load brings them
+struct MfmaJob {  // one job's fields together
     const uint8_t* weights;
     const float* x;
     float* y;
     unsigned* status;
     size_t row_bytes, stride;
-    unsigned out, pad;
+    unsigned out, index_limit;
+    // optional: the weights start at weights + min(*index, index_limit - 1) * index_stride
+    const int32_t* index;
+    size_t index_stride;
 };
 struct MfmaJobs {
     MfmaJob job[kMaxFused];
     unsigned count, columns, in, rows_per_wg;
+    // affine batch: `count` jobs all described by job[0], job j's x, y and index advanced
+    // by j * x_step, j * y_step and j
+    unsigned affine;
+    size_t x_step, y_step;
 };
 
 // Workgroup: W wavefronts (W <= 16), rows [r0, r1) of its job, processed in passes of up
@@ -966,11 +998,15 @@ struct MfmaJobs {
 // activation unit, the first units' packed weights, then the staging.
 template <int ENC, int R, int W, bool PACKED>
 __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
-    const MfmaJob& jb = jobs.job[blockIdx.y];
-    const uint8_t* __restrict__ weights = jb.weights;
+    const unsigned jid = jobs.affine ? 0 : blockIdx.y, step = jobs.affine ? blockIdx.y : 0;
+    const MfmaJob& jb = jobs.job[jid];
+    const uint8_t* __restrict__ weights =
+        jb.index ? jb.weights + size_t(min(unsigned(jb.index[step]), jb.index_limit - 1)) *
+                                    jb.index_stride
+                 : jb.weights;
     const size_t row_bytes = jb.row_bytes, stride = jb.stride;
-    const float* x = jb.x;
-    float* __restrict__ y = jb.y;
+    const float* x = jb.x + step * jobs.x_step;
+    float* __restrict__ y = jb.y + step * jobs.y_step;
     unsigned* status = jb.status;
     const unsigned in = jobs.in, out = jb.out, rows_per_wg = jobs.rows_per_wg;
     constexpr int kTiles = mfma_tiles<R>;
@@ -1112,18 +1148,23 @@ int launch_decode(const void* packed, size_t row_bytes, size_t rows, size_t in, 
 
 template <int ENC>
 int launch_exact(const void* w, size_t row_bytes, const float* x, size_t rows, size_t in,
-                 size_t out, float* y, size_t stride, unsigned* status, hipStream_t stream) {
-    const unsigned grid = unsigned((out + 3) / 4);
+                 size_t out, float* y, size_t stride, unsigned* status, hipStream_t stream,
+                 const int32_t* index = nullptr, size_t index_stride = 0,
+                 unsigned index_limit = 1, unsigned batch = 1, size_t x_step = 0,
+                 size_t y_step = 0) {
+    const dim3 grid(unsigned((out + 3) / 4), batch);
     for (size_t first = 0; first < rows; first += 8) {
         const unsigned group = unsigned(std::min<size_t>(8, rows - first));
         if (group == 1)
-            hipLaunchKernelGGL((exact_gemv<ENC, 1>), dim3(grid), dim3(256), 0, stream,
+            hipLaunchKernelGGL((exact_gemv<ENC, 1>), grid, dim3(256), 0, stream,
                                static_cast<const uint8_t*>(w), row_bytes, x + first * in, 1u,
-                               unsigned(in), unsigned(out), y + first * stride, stride, status);
+                               unsigned(in), unsigned(out), y + first * stride, stride, status,
+                               index, index_stride, index_limit, x_step, y_step);
         else
-            hipLaunchKernelGGL((exact_gemv<ENC, 8>), dim3(grid), dim3(256), 0, stream,
+            hipLaunchKernelGGL((exact_gemv<ENC, 8>), grid, dim3(256), 0, stream,
                                static_cast<const uint8_t*>(w), row_bytes, x + first * in, group,
-                               unsigned(in), unsigned(out), y + first * stride, stride, status);
+                               unsigned(in), unsigned(out), y + first * stride, stride, status,
+                               index, index_stride, index_limit, x_step, y_step);
         KDQ_HIP(hipGetLastError());
     }
     return KDQ_OK;
@@ -1247,7 +1288,7 @@ bool plan_mfma(size_t rows, size_t in, size_t total_out, MfmaPlan& p, bool packe
 void number_workgroups(MfmaJobs& jobs, unsigned rows_per_wg) {
     jobs.rows_per_wg = rows_per_wg;
     jobs.columns = 0;
-    for (unsigned k = 0; k < jobs.count; ++k)
+    for (unsigned k = 0; k < (jobs.affine ? 1u : jobs.count); ++k)
         jobs.columns = std::max(jobs.columns, (jobs.job[k].out + rows_per_wg - 1) / rows_per_wg);
 }
 
@@ -1445,6 +1486,10 @@ int with_encoding(int encoding, F&& f) {
         return f(std::integral_constant<int, KDQ_IQ2_S>{});
     case KDQ_IQ3_S:
         return f(std::integral_constant<int, KDQ_IQ3_S>{});
+    case KDQ_F32:
+        return f(std::integral_constant<int, KDQ_F32>{});
+    case KDQ_F16:
+        return f(std::integral_constant<int, KDQ_F16>{});
     default:
         return KDQ_ERR_UNSUPPORTED;
     }
@@ -1644,7 +1689,8 @@ namespace {
 
 // One fused MFMA launch for jobs[idx[0..n)] (same encoding, rows, in; checked).
 template <bool PACKED>
-int launch_fused(const kdq_matvec_job* jobs, const size_t* idx, size_t n, hipStream_t stream) {
+int launch_fused(const kdq_matvec_job* jobs, const size_t* idx, size_t n, hipStream_t stream,
+                 const IndexedJob* indexed = nullptr) {
     const kdq_matvec_job& j0 = jobs[idx[0]];
     size_t total = 0;
     for (size_t k = 0; k < n; ++k)
@@ -1659,6 +1705,11 @@ int launch_fused(const kdq_matvec_job* jobs, const size_t* idx, size_t n, hipStr
         const kdq_matvec_job& j = jobs[idx[k]];
         mj.job[k] = MfmaJob{static_cast<const uint8_t*>(j.weights), j.input, j.output,
                             j.status, PACKED ? 0 : j.row_bytes, j.stride, j.columns, 0};
+        if (indexed) {
+            mj.job[k].index = indexed[idx[k]].index;
+            mj.job[k].index_stride = indexed[idx[k]].index_stride;
+            mj.job[k].index_limit = indexed[idx[k]].index_limit;
+        }
     }
     number_workgroups(mj, p.rows_per_wg);
     switch (j0.encoding) {
@@ -1722,6 +1773,83 @@ int run_batch(const kdq_matvec_job* jobs, size_t count, void* stream) {
 }
 
 }  // namespace
+
+int indexed_gemv_affine(const IndexedJob& first, unsigned count, size_t x_step,
+                        size_t y_step, hipStream_t s) {
+    const kdq_matvec_job& j = first.job;
+    if (count > 65535)
+        return KDQ_ERR_UNSUPPORTED;
+    if (count == 1)
+        return indexed_gemv_batch(&first, 1, s);
+    MfmaPlan p;  // planned over every job's rows, as launch_fused plans a fused group
+    if (fusable(j, false) && plan_mfma(j.rows, j.in, size_t(j.columns) * count, p, false)) {
+        MfmaJobs mj{};
+        mj.count = count;
+        mj.in = j.in;
+        mj.affine = 1;
+        mj.x_step = x_step;
+        mj.y_step = y_step;
+        mj.job[0] = MfmaJob{static_cast<const uint8_t*>(j.weights), j.input, j.output, j.status,
+                            j.row_bytes, j.stride, j.columns, first.index ? first.index_limit : 0,
+                            first.index, first.index_stride};
+        number_workgroups(mj, p.rows_per_wg);
+        switch (j.encoding) {
+        case KDQ_Q8_0:
+            return launch_mfma_rows<KDQ_Q8_0, false>(j.rows, p.waves, mj, s);
+        case KDQ_Q4_0:
+            return launch_mfma_rows<KDQ_Q4_0, false>(j.rows, p.waves, mj, s);
+        case KDQ_Q4_K:
+            return launch_mfma_rows<KDQ_Q4_K, false>(j.rows, p.waves, mj, s);
+        default:
+            return KDQ_ERR_UNSUPPORTED;
+        }
+    }
+    return with_encoding(j.encoding, [&](auto enc) {
+        return launch_exact<decltype(enc)::value>(j.weights, j.row_bytes, j.input, j.rows, j.in,
+                                                  j.columns, j.output, j.stride, j.status, s,
+                                                  first.index, first.index_stride,
+                                                  first.index ? first.index_limit : 1u, count,
+                                                  x_step, y_step);
+    });
+}
+
+int indexed_gemv_batch(const IndexedJob* jobs, size_t count, hipStream_t s) {
+    std::vector<kdq_matvec_job> plain(count);
+    for (size_t i = 0; i < count; ++i)
+        plain[i] = jobs[i].job;
+    std::vector<char> done(count, 0);
+    for (size_t i = 0; i < count; ++i) {  // fused MFMA launches, as run_batch groups them
+        if (done[i] || !fusable(plain[i], false))
+            continue;
+        size_t idx[kMaxFused], n = 0;
+        for (size_t k = i; k < count && n < size_t(kMaxFused); ++k)
+            if (!done[k] && plain[k].encoding == plain[i].encoding &&
+                plain[k].rows == plain[i].rows && plain[k].in == plain[i].in &&
+                fusable(plain[k], false))
+                idx[n++] = k;
+        const int rc = launch_fused<false>(plain.data(), idx, n, s, jobs);
+        if (rc)
+            return rc;
+        for (size_t k = 0; k < n; ++k)
+            done[idx[k]] = 1;
+    }
+    for (size_t i = 0; i < count; ++i) {
+        if (done[i])
+            continue;
+        const IndexedJob& ij = jobs[i];
+        const kdq_matvec_job& j = ij.job;
+        const int rc = with_encoding(j.encoding, [&](auto enc) {
+            return launch_exact<decltype(enc)::value>(j.weights, j.row_bytes, j.input, j.rows,
+                                                      j.in, j.columns, j.output, j.stride,
+                                                      j.status, s, ij.index, ij.index_stride,
+                                                      ij.index ? ij.index_limit : 1u);
+        });
+        if (rc)
+            return rc;
+    }
+    return KDQ_OK;
+}
+
 }  // namespace kdq
 
 extern "C" int kdq_gemv_batch(const kdq_matvec_job* jobs, size_t count, void* stream) {

@@ -117,9 +117,33 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // Host helpers --------------------------------------------------------------
 
+// A decode-time product whose weights start at job.weights + min(*index, index_limit - 1)
+// * index_stride when `index` (a device pointer) is set: the expert slice a device-side
+// routing chose.  Products of streamed encodings run fused on the MFMA kernel, the rest
+// on the exact kernel.  The jobs must satisfy kdq_gemv's argument rules (unchecked).
+struct IndexedJob {
+    kdq_matvec_job job;
+    const int32_t* index;
+    size_t index_stride;
+    unsigned index_limit;
+};
+int indexed_gemv_batch(const IndexedJob* jobs, size_t count, hipStream_t stream);
+// `count` products in one launch, all as `first` except that job j reads x + j * x_step,
+// writes y + j * y_step and takes its expert from index[j] (rows of `first` must be 1
+// when count > 1 runs on the MFMA kernel; any rows on the exact kernel).
+int indexed_gemv_affine(const IndexedJob& first, unsigned count, size_t x_step, size_t y_step,
+                        hipStream_t stream);
+
+// The MoE router of kdq_moe_route (softmax with a double total, top-k by probability,
+// weights renormalised by max(sum, 2^-14)) without the expert permutation.
+int route_selection(const float* logits, size_t tokens, size_t experts, size_t top_k,
+                    int32_t* idx, float* w, hipStream_t stream);
+
 inline size_t block_values(int encoding) {
     switch (encoding) {
     case KDQ_BF16:
+    case KDQ_F32:
+    case KDQ_F16:
         return 1;
     case KDQ_Q4_0:
     case KDQ_Q8_0:
@@ -159,7 +183,10 @@ inline size_t block_bytes(int encoding) {
     case KDQ_IQ4_XS:
         return 136;
     case KDQ_BF16:
+    case KDQ_F16:
         return 2;
+    case KDQ_F32:
+        return 4;
     default:
         return 0;
     }

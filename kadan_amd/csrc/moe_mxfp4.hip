@@ -1123,6 +1123,21 @@ int launch_route(const float* logits, size_t tokens, size_t experts, size_t top_
 
 using namespace kdq;
 
+namespace kdq {
+
+int route_selection(const float* logits, size_t tokens, size_t experts, size_t top_k,
+                    int32_t* idx, float* w, hipStream_t stream) {
+    const int rc = check_route(logits, tokens, experts, top_k);
+    if (rc)
+        return rc;
+    hipLaunchKernelGGL(route_kernel, dim3(unsigned((tokens + 3) / 4)), dim3(256), 0, stream,
+                       logits, unsigned(tokens), unsigned(experts), unsigned(top_k), idx, w);
+    KDQ_HIP(hipGetLastError());
+    return KDQ_OK;
+}
+
+}  // namespace kdq
+
 extern "C" int kdq_moe_route(const float* logits, size_t tokens, size_t experts, size_t top_k,
                              int32_t* idx, float* w, int32_t* offsets, int32_t* perm,
                              void* stream) {

@@ -6,6 +6,8 @@ current HIP stream to the corresponding ``kdq_*`` entry point, and raises
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import BLOCK_BYTES, BLOCK_VALUES, MatvecJob, call, lib
@@ -160,6 +162,31 @@ def gemm_q4_0_packed(packed: torch.Tensor, x_f16: torch.Tensor, n_out: int,
     return out
 
 
+def moe_gguf(spec: dict, x: torch.Tensor, status: torch.Tensor | None = None):
+    """GGUF MoE layer (kdq_moe_gguf).  spec: hidden, experts, top_k, ff, shared_ff,
+    shared_gate (fp32 device tensor [hidden]) and per tensor name (encoding, uint8 device
+    tensor [rows, row_bytes] or [experts, rows, row_bytes]).  x fp32 [rows, hidden] ->
+    (y fp32 [rows, hidden], selected int32 [rows, top_k], weights fp32 [rows, top_k])."""
+    from . import MOE_GGUF_TENSORS, GgufTensor, MoeGgufLayer
+    _need(x, torch.float32, "x")
+    layer = MoeGgufLayer(spec["hidden"], spec["experts"], spec["top_k"], spec["ff"],
+                         spec["shared_ff"])
+    for name in MOE_GGUF_TENSORS:
+        enc, t = spec[name]
+        _need(t, torch.uint8, name)
+        expert_bytes = t.shape[1] * t.shape[2] if t.dim() == 3 else 0
+        setattr(layer, name, GgufTensor(t.data_ptr(), t.shape[-1], expert_bytes, enc))
+    _need(spec["shared_gate"], torch.float32, "shared_gate")
+    layer.shared_gate = spec["shared_gate"].data_ptr()
+    rows = x.shape[0]
+    y = torch.empty(rows, spec["hidden"], dtype=torch.float32, device=x.device)
+    sel = torch.empty(rows, spec["top_k"], dtype=torch.int32, device=x.device)
+    w = torch.empty(rows, spec["top_k"], dtype=torch.float32, device=x.device)
+    call("kdq_moe_gguf", ctypes.addressof(layer), x.data_ptr(), rows, y.data_ptr(),
+         sel.data_ptr(), w.data_ptr(), _ptr(status), _stream())
+    return y, sel, w
+
+
 def moe_route(logits: torch.Tensor, top_k: int):
     """fp32 [tokens, experts] -> idx, w, offsets, perm (kdq_moe_route)."""
     _need(logits, torch.float32, "logits")
@@ -254,6 +281,6 @@ def moe_mxfp4_packed(x_bf16: torch.Tensor, logits: torch.Tensor, top_k: int, int
 
 
 __all__ = ["dequantize", "gemv", "gemv_batch", "quantize_q8", "gemm_q4_0", "gemm_q4_0_packed",
-           "moe_route",
+           "moe_gguf", "moe_route",
            "mxfp4_dequantize", "moe_mxfp4", "moe_mxfp4_pack", "moe_mxfp4_packed", "lib",
            "BLOCK_BYTES", "BLOCK_VALUES"]

@@ -57,6 +57,7 @@ class Oracle:
         lib.kdo_float_to_half.argtypes = [C.c_float]
         lib.kdo_dequantize_row.argtypes = [i, vp, sz, vp]
         lib.kdo_gemv.argtypes = [i, vp, sz, vp, sz, sz, sz, vp, sz]
+        lib.kdo_moe_gguf_forward.argtypes = [vp, vp, sz, vp, vp, vp]
         lib.kdo_quantize_row_q8_0.argtypes = [vp, sz, vp, vp]
         lib.kdo_quantize_row_q8_K.argtypes = [vp, sz, vp, vp, vp]
         lib.kdo_quantize_q8_f16.argtypes = [vp, sz, sz, vp, vp]
@@ -207,6 +208,26 @@ class Oracle:
         self.lib.kdo_moe_permute(_p(idx), t, k, experts, _p(offsets), _p(perm))
         return offsets, perm
 
+    def moe_gguf_forward(self, spec: dict, x):
+        """kdo_moe_gguf_forward: (y [rows, hidden], idx, w [rows, top_k])."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        rows = x.shape[0]
+        host = dict(spec)
+        for name in MOE_TENSORS:
+            enc, arr = spec[name]
+            host[name] = (int(enc), np.ascontiguousarray(arr, dtype=np.uint8))
+        host["shared_gate"] = np.ascontiguousarray(spec["shared_gate"], dtype=np.float32)
+        keep = []
+        layer = moe_gguf_layer(host, lambda a: a.ctypes.data, keep)
+        y = np.empty((rows, spec["hidden"]), np.float32)
+        idx = np.empty((rows, spec["top_k"]), np.int32)
+        w = np.empty((rows, spec["top_k"]), np.float32)
+        rc = self.lib.kdo_moe_gguf_forward(C.addressof(layer), _p(x), rows, _p(y), _p(idx),
+                                           _p(w))
+        if rc:
+            raise ValueError(f"kdo_moe_gguf_forward rc={rc}")
+        return y, idx, w
+
     def moe_forward(self, x_bf16, logits, top_k, gate_b, gate_s, up_b, up_s, down_b, down_s,
                     threads=1):
         x_bf16 = np.ascontiguousarray(x_bf16, dtype=np.uint16)
@@ -227,6 +248,40 @@ class Oracle:
         if rc:
             raise ValueError(f"kdo_moe_forward rc={rc}")
         return y, idx, w, offsets, perm
+
+
+class GgufTensor(C.Structure):
+    _fields_ = [("weights", C.c_void_p), ("row_bytes", C.c_size_t),
+                ("expert_bytes", C.c_size_t), ("encoding", C.c_int)]
+
+
+class MoeGgufLayer(C.Structure):
+    _fields_ = [("hidden", C.c_size_t), ("experts", C.c_size_t), ("top_k", C.c_size_t),
+                ("ff", C.c_size_t), ("shared_ff", C.c_size_t)] + [
+        (name, GgufTensor) for name in ("router", "gate_exps", "up_exps", "down_exps",
+                                        "gate_shexp", "up_shexp", "down_shexp")] + [
+        ("shared_gate", C.c_void_p)]
+
+
+MOE_TENSORS = ("router", "gate_exps", "up_exps", "down_exps", "gate_shexp", "up_shexp",
+               "down_shexp")
+
+
+def moe_gguf_layer(spec: dict, pointer, keep: list) -> MoeGgufLayer:
+    """spec: hidden, experts, top_k, ff, shared_ff, shared_gate (float32 [hidden]) and per
+    tensor name (encoding, uint8 array [rows, row_bytes] or [experts, rows, row_bytes]).
+    `pointer(array)` gives the address to store (host or device); `keep` holds what must
+    stay alive."""
+    layer = MoeGgufLayer(spec["hidden"], spec["experts"], spec["top_k"], spec["ff"],
+                         spec["shared_ff"])
+    for name in MOE_TENSORS:
+        enc, arr = spec[name]
+        keep.append(arr)
+        expert_bytes = arr.shape[1] * arr.shape[2] if arr.ndim == 3 else 0
+        setattr(layer, name, GgufTensor(pointer(arr), arr.shape[-1], expert_bytes, enc))
+    keep.append(spec["shared_gate"])
+    layer.shared_gate = pointer(spec["shared_gate"])
+    return layer
 
 
 class Reference:

@@ -84,6 +84,8 @@ static uint16_t load_u16(const uint8_t* p) {
 
 int kdo_block_values(int encoding) {
     switch (encoding) {
+    case KDO_F32:
+    case KDO_F16:
     case KDO_BF16:
         return 1;
     case KDO_Q4_0:
@@ -120,7 +122,10 @@ int kdo_block_bytes(int encoding) {
     case KDO_IQ4_XS:
         return 136; /* fp16 d, 16-bit high scale bits, 4 low scale bytes, 128 index bytes */
     case KDO_BF16:
+    case KDO_F16:
         return 2;
+    case KDO_F32:
+        return 4;
     case KDO_IQ3_XXS:
         return 98; /* fp16 d, 64 grid bytes, 8 sign/scale words */
     case KDO_IQ2_S:
@@ -307,6 +312,12 @@ static void decode_block(int encoding, const uint8_t* block, float* out) {
         return decode_iq4_xs(block, out);
     case KDO_BF16:
         out[0] = kdo_bf16_to_float(load_u16(block));
+        return;
+    case KDO_F32:
+        out[0] = bits_to_float(load_u32(block));
+        return;
+    case KDO_F16:
+        out[0] = kdo_half_to_float(load_u16(block));
         return;
     case KDO_IQ3_XXS:
         return decode_iq3_xxs(block, out);
@@ -849,5 +860,79 @@ int kdo_moe_forward(const uint16_t* x, const float* logits, size_t tokens, size_
                 y[t * hidden + d] = sum;
             }
     free(contribution);
+    return rc;
+}
+
+/* ------------------------------------------------------------ GGUF MoE layer */
+
+static float silu_f(float v) {
+    return v / (1.0f + expf(-v));
+}
+
+static float sigmoid_f(float v) {
+    return 1.0f / (1.0f + expf(-v));
+}
+
+static int product(const kdo_gguf_tensor* m, size_t expert, const float* x, size_t rows,
+                   size_t in, size_t out, float* y) {
+    return kdo_gemv(m->encoding, m->weights + expert * m->expert_bytes, m->row_bytes, x, rows,
+                    in, out, y, out);
+}
+
+int kdo_moe_gguf_forward(const kdo_moe_gguf_layer* L, const float* x, size_t rows, float* y,
+                         int32_t* idx, float* w) {
+    if (!L || !x || !y || !idx || !w || !rows || !L->top_k || L->top_k > L->experts)
+        return -1;
+    const size_t H = L->hidden, E = L->experts, K = L->top_k, F = L->ff, S = L->shared_ff;
+    float* logits = (float*)malloc(rows * E * sizeof(float));
+    float* sg = (float*)malloc(rows * S * sizeof(float));
+    float* su = (float*)malloc(rows * S * sizeof(float));
+    float* shared_down = (float*)malloc(rows * H * sizeof(float));
+    float* g = (float*)malloc(F * sizeof(float));
+    float* u = (float*)malloc(F * sizeof(float));
+    float* down = (float*)malloc(rows * K * H * sizeof(float));
+    int rc = -2;
+    if (!logits || !sg || !su || !shared_down || !g || !u || !down)
+        goto done;
+    rc = -1;
+    /* router and the shared expert's gate / up (qwen_layers.cpp:383-396) */
+    if (product(&L->router, 0, x, rows, H, E, logits) ||
+        product(&L->gate_shexp, 0, x, rows, H, S, sg) ||
+        product(&L->up_shexp, 0, x, rows, H, S, su))
+        goto done;
+    for (size_t i = 0; i < rows * S; ++i)
+        sg[i] = silu_f(sg[i]) * su[i];
+    kdo_moe_route(logits, rows, E, K, idx, w); /* :397-425 */
+    /* each selection: gate / up, silu * up, down, times its weight (:427-468) */
+    for (size_t s = 0; s < rows * K; ++s) {
+        const size_t e = (size_t)idx[s];
+        const float* xs = x + (s / K) * H;
+        if (product(&L->gate_exps, e, xs, 1, H, F, g) || product(&L->up_exps, e, xs, 1, H, F, u))
+            goto done;
+        for (size_t j = 0; j < F; ++j)
+            g[j] = silu_f(g[j]) * u[j];
+        if (product(&L->down_exps, e, g, 1, F, H, down + s * H))
+            goto done;
+        for (size_t d = 0; d < H; ++d)
+            down[s * H + d] = down[s * H + d] * w[s];
+    }
+    if (product(&L->down_shexp, 0, sg, rows, S, H, shared_down))
+        goto done;
+    /* :469-491: selection-order sum plus the gated shared expert */
+    for (size_t t = 0; t < rows; ++t) {
+        float gate = 0.0f;
+        for (size_t c = 0; c < H; ++c)
+            gate += L->shared_gate[c] * x[t * H + c];
+        gate = sigmoid_f(gate);
+        for (size_t d = 0; d < H; ++d) {
+            float sum = 0.0f;
+            for (size_t i = 0; i < K; ++i)
+                sum += down[(t * K + i) * H + d];
+            y[t * H + d] = sum + shared_down[t * H + d] * gate;
+        }
+    }
+    rc = 0;
+done:
+    free(logits), free(sg), free(su), free(shared_down), free(g), free(u), free(down);
     return rc;
 }

@@ -24,6 +24,10 @@
  *   kdo_gemv / kdo_gemm_q4_0_q8  brute-force double products over decoded weights,
  *                          linearity and permutation properties
  *   kdo_moe_route/permute  hand-derived cases (2 tokens x 4 experts) and invariants
+ *   kdo_moe_gguf_forward   parity unpinned against the reference as a whole (the
+ *                          compiled reference's MoeLayer needs the model runtime); its
+ *                          parts are pinned individually (decode, products, routing) and
+ *                          the composition by hand-computed small cases
  *   kdo_moe_forward        parity unpinned against the reference as a whole: the
  *                          reference never runs MXFP4 weights through MoeLayer
  *                          (IW/src/models/text/qwen_layers.cpp:378-492); its parts
@@ -41,6 +45,8 @@ extern "C" {
 
 /* GGML type ids, as IW/include/kadan/gguf_quantization.hpp:30-55 maps them. */
 enum {
+    KDO_F32 = 0,
+    KDO_F16 = 1,
     KDO_Q4_0 = 2,
     KDO_Q8_0 = 8,
     KDO_Q3_K = 11,
@@ -75,6 +81,7 @@ int kdo_block_bytes(int encoding);
  * IQ4_NL  IW/include/kadan/gguf_quantization.hpp:695-701 (G/src/ggml-quants.c:2726, dequantize_row_iq4_nl)
  * IQ4_XS  IW/include/kadan/gguf_quantization.hpp:736-748 (G/src/ggml-quants.c:2744, dequantize_row_iq4_xs)
  * BF16    IW/include/kadan/gguf_quantization.hpp:633-636 (one value per 2-byte block)
+ * F32, F16 plain values (one per 4- / 2-byte block; F16 through kdo_half_to_float)
  * IQ3_XXS IW/include/kadan/gguf_quantization.hpp:674-694 (G/src/ggml-quants.c dequantize_row_iq3_xxs)
  * IQ2_S   IW/include/kadan/gguf_quantization.hpp:702-718 (dequantize_row_iq2_s)
  * IQ3_S   IW/include/kadan/gguf_quantization.hpp:719-735 (dequantize_row_iq3_s)
@@ -167,6 +174,31 @@ int kdo_moe_forward(const uint16_t* x, const float* logits, size_t tokens, size_
                     const uint8_t* down_blocks, const uint8_t* down_scales,
                     float* y, int32_t* idx, float* w, int32_t* offsets, int32_t* perm,
                     int threads);
+
+/* One GGUF weight tensor (host memory): row-major rows of `row_bytes`; expert stacks
+ * hold slices of `expert_bytes`. */
+typedef struct kdo_gguf_tensor {
+    const uint8_t* weights;
+    size_t row_bytes;
+    size_t expert_bytes;
+    int encoding;
+} kdo_gguf_tensor;
+
+typedef struct kdo_moe_gguf_layer {
+    size_t hidden, experts, top_k, ff, shared_ff;
+    kdo_gguf_tensor router, gate_exps, up_exps, down_exps, gate_shexp, up_shexp, down_shexp;
+    const float* shared_gate; /* hidden floats */
+} kdo_moe_gguf_layer;
+
+/* MoeLayer::forward (IW/src/models/text/qwen_layers.cpp:378-492) over GGUF weights:
+ * every projection is kdo_gemv (exactly decoded weights, double-accumulated products,
+ * rounded to fp32 once), routing is kdo_moe_route, silu / sigmoid are the reference's
+ * fp32 x / (1 + exp(-x)) and 1 / (1 + exp(-x)) (IW/src/models/text/gguf_weights.cpp:
+ * 627-633), the shared gate is the reference's sequential fp32 dot, and the
+ * contributions are summed in selection order.  y [rows x hidden], idx / w [rows x
+ * top_k].  Returns 0, or -1 for a bad argument, -2 when out of memory. */
+int kdo_moe_gguf_forward(const kdo_moe_gguf_layer* layer, const float* x, size_t rows,
+                         float* y, int32_t* idx, float* w);
 
 #ifdef __cplusplus
 }

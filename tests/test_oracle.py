@@ -551,3 +551,71 @@ def test_moe_forward_vs_numpy_composition(oracle):
     np.testing.assert_allclose(y, want, rtol=1e-5, atol=1e-5 * np.abs(want).max())
     # dropping the routing weight, or the up projection, is far off
     assert np.abs(y - want / np.maximum(w.max(), 1e-9)).max() > 1e-4 * np.abs(want).max()
+
+
+# ---------------------------------------------------------------- GGUF MoE layer
+
+def _moe_numpy(spec_f32, x):
+    """Independent float64 restatement of MoeLayer::forward (IW/src/models/text/
+    qwen_layers.cpp:378-492) over already-decoded weights."""
+    r, ge, ue, de, gs, us, ds, sg = (spec_f32[k].astype(np.float64) for k in
+                                     ("router", "gate_exps", "up_exps", "down_exps",
+                                      "gate_shexp", "up_shexp", "down_shexp", "shared_gate"))
+    K = spec_f32["top_k"]
+    X = x.astype(np.float64)
+    silu = lambda v: v / (1 + np.exp(-v))
+    logits = X @ r.T
+    p = np.exp(logits - logits.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    sel = np.argsort(-p, axis=1, kind="stable")[:, :K]
+    pw = np.take_along_axis(p, sel, 1)
+    pw /= np.maximum(pw.sum(1, keepdims=True), 6.103515625e-5)
+    Y = np.zeros((x.shape[0], r.shape[1]))
+    for t in range(x.shape[0]):
+        for i in range(K):
+            e = sel[t, i]
+            Y[t] += (de[e] @ (silu(ge[e] @ X[t]) * (ue[e] @ X[t]))) * pw[t, i]
+        gate = 1 / (1 + np.exp(-(sg @ X[t])))
+        Y[t] += (ds @ (silu(gs @ X[t]) * (us @ X[t]))) * gate
+    return Y, sel, pw
+
+
+def test_moe_gguf_forward_vs_numpy(oracle):
+    """The composition (routing, SwiGLU, selection weights, the sigmoid-gated shared
+    expert) against an independent numpy restatement, with F32 weights and with Q4_K / Q6_K /
+    Q8_0 weights decoded by the (separately pinned) oracle decode."""
+    H, E, K, F, S = 256, 6, 2, 256, 256
+    g = np.random.default_rng(5)
+    x = g.standard_normal((3, H)).astype(np.float32)
+    f32 = {"router": g.standard_normal((E, H)).astype(np.float32),
+           "gate_exps": (g.standard_normal((E, F, H)) * 0.05).astype(np.float32),
+           "up_exps": (g.standard_normal((E, F, H)) * 0.05).astype(np.float32),
+           "down_exps": (g.standard_normal((E, H, F)) * 0.05).astype(np.float32),
+           "gate_shexp": (g.standard_normal((S, H)) * 0.05).astype(np.float32),
+           "up_shexp": (g.standard_normal((S, H)) * 0.05).astype(np.float32),
+           "down_shexp": (g.standard_normal((H, S)) * 0.05).astype(np.float32)}
+    sg = (g.standard_normal(H) * 0.05).astype(np.float32)
+    spec = dict(hidden=H, experts=E, top_k=K, ff=F, shared_ff=S, shared_gate=sg,
+                **{k: (0, v.view(np.uint8).reshape(*v.shape[:-1], -1)) for k, v in f32.items()})
+    y, idx, w = oracle.moe_gguf_forward(spec, x)
+    Y, sel, pw = _moe_numpy(dict(f32, shared_gate=sg, top_k=K), x)
+    assert np.array_equal(idx, sel)
+    assert np.abs(w - pw).max() < 1e-6
+    assert np.abs(y - Y).max() <= 1e-5 * np.abs(Y).max()
+    # quantized tensors: the same composition over the oracle's decode of them
+    encs = {"router": Q8_0, "gate_exps": Q4_K, "up_exps": Q4_K, "down_exps": Q6_K,
+            "gate_shexp": Q8_0, "up_shexp": Q8_0, "down_shexp": Q4_K}
+    qspec = dict(hidden=H, experts=E, top_k=K, ff=F, shared_ff=S, shared_gate=sg)
+    decoded = {}
+    for i, (name, enc) in enumerate(encs.items()):
+        shape = f32[name].shape
+        rows = int(np.prod(shape[:-1]))
+        packed = synth.gguf_weights(enc, 40 + i, rows, shape[-1])
+        qspec[name] = (enc, packed.reshape(*shape[:-1], -1))
+        decoded[name] = oracle.dequantize(enc, packed, shape[-1]).reshape(shape)
+    decoded["router"] *= 300.0  # well-separated routing logits
+    qspec["router"] = (0, decoded["router"].astype(np.float32).view(np.uint8).reshape(E, -1))
+    y, idx, w = oracle.moe_gguf_forward(qspec, x)
+    Y, sel, pw = _moe_numpy(dict(decoded, shared_gate=sg, top_k=K), x)
+    assert np.array_equal(idx, sel)
+    assert np.abs(y - Y).max() <= 1e-5 * np.abs(Y).max()
