@@ -434,7 +434,7 @@ __device__ __forceinline__ void stage_unit(unsigned in, unsigned u, const XUnit&
 // layout the two code loads of a lane each use half of the same 128-byte lines, and the
 // non-temporal policy would drop the lines between them (measured 9.4 -> 12.4 us at C2).
 struct Lane {
-    unsigned w[17];
+    unsigned w[19];
 };
 
 template <int ENC>
@@ -463,6 +463,28 @@ __device__ __forceinline__ void load_lane(const uint8_t* row, unsigned slot, Lan
         L.w[12] = d.x, L.w[13] = d.y, L.w[14] = d.z, L.w[15] = d.w;
         L.w[16] = load4(p + 64);
     }
+}
+
+// Q6_K (210-byte super-block: ql[128] low nibbles, qh[64] high bit pairs, 16 int8
+// scales, f16 d; G/src/ggml-common.h block_q6_K).  MFMA chunk G = 2h + p of super-block
+// `group` takes both nibbles of ql[32G .. 32G+31]: its block 0 is super-block positions
+// 128h + 32p + t (low nibble, qh[32h + t] bits 2p, 2p+1; scales 8h + 2p + t/16), its
+// block 1 positions 128h + 64 + 32p + t (high nibble, qh bits 4 + 2p, 5 + 2p; scales
+// 8h + 4 + 2p + t/16).  Image: w[0..7] = the lane's 32 ql bytes, w[8..15] = qh[32h ..
+// 32h+31], w[16..17] = scales 8h .. 8h+7, w[18] = bytes 206..209 (d in the high half).
+__device__ __forceinline__ void load_lane_q6k(const uint8_t* row, unsigned group, unsigned G,
+                                              Lane& L) {
+    const uint8_t* block = row + size_t(group) * 210;
+    const unsigned h = G / 2;
+    const u32x4 a = load16_a2(block + 32 * G), b = load16_a2(block + 32 * G + 16);
+    const u32x4 c = load16_a2(block + 128 + 32 * h), d = load16_a2(block + 144 + 32 * h);
+    const uint2 sc = load8_a2(block + 192 + 8 * h);
+    L.w[0] = a.x, L.w[1] = a.y, L.w[2] = a.z, L.w[3] = a.w;
+    L.w[4] = b.x, L.w[5] = b.y, L.w[6] = b.z, L.w[7] = b.w;
+    L.w[8] = c.x, L.w[9] = c.y, L.w[10] = c.z, L.w[11] = c.w;
+    L.w[12] = d.x, L.w[13] = d.y, L.w[14] = d.z, L.w[15] = d.w;
+    L.w[16] = sc.x, L.w[17] = sc.y;
+    L.w[18] = load4_a2(block + 206);
 }
 
 struct XSlot {
@@ -730,7 +752,7 @@ constexpr int mfma_units = R == 1 ? 2 : (R == 2 ? 2 : 1);
 //       bytes 8b..8b+7 hold plane `plane` of positions 8m..8m+7 of block b of chunk
 //       4g + G; the other 8 bytes are zero
 //   block table, per batch row r and 32-value block: float4 (s, sum x, sum of codes as
-//       int bits, 0)
+//       int bits, sum of the codes of its first 16 values as int bits)
 //   partials [R][tiles][64 lanes][kPartialPitch] floats
 struct MfmaLds {
     size_t a, blocks, partial, total;
@@ -746,12 +768,27 @@ __host__ __device__ inline MfmaLds mfma_layout(unsigned batch, unsigned in) {
     return l;
 }
 
+// The MFMA chunk G and block b (of the chunk) that carry 32-value block k (0..7) of a
+// 256-value group: chunk G is blocks 2G, 2G+1, except for Q6_K, whose chunk G = 2h + p
+// is blocks 4h + p and 4h + 2 + p (the two nibbles of one run of ql bytes).
+template <int ENC> __host__ __device__ __forceinline__ unsigned chunk_of(unsigned k) {
+    return ENC == KDQ_Q6_K ? 2 * (k / 4) + k % 2 : k / 2;
+}
+template <int ENC> __host__ __device__ __forceinline__ unsigned half_of(unsigned k) {
+    return ENC == KDQ_Q6_K ? (k / 2) % 2 : k % 2;
+}
+template <int ENC> __host__ __device__ __forceinline__ unsigned block_of(unsigned G, unsigned b) {
+    return ENC == KDQ_Q6_K ? 4 * (G / 2) + 2 * b + G % 2 : 2 * G + b;
+}
+
 // Quantizes one unit of 8 activation values (the 16-bit block code of stage_unit) into
 // the A table and the block table.  The four threads of a DPP quad hold one block.
+template <int ENC>
 __device__ __forceinline__ void mstage_unit(unsigned in, unsigned u, const XUnit& xu,
                                             uint8_t* atab, float4* blocks) {
     const unsigned r = u / (in / 8), e0 = (u % (in / 8)) * 8;
-    const unsigned g = e0 / 256, G = (e0 % 256) / 64, b = (e0 % 64) / 32, m = (e0 % 32) / 8;
+    const unsigned k = (e0 % 256) / 32;
+    const unsigned g = e0 / 256, G = chunk_of<ENC>(k), b = half_of<ENC>(k), m = (e0 % 32) / 8;
     const float v[8] = {xu.a.x, xu.a.y, xu.a.z, xu.a.w, xu.b.x, xu.b.y, xu.b.z, xu.b.w};
     float amax = 0.f, sum = 0.f;
     int ok = 1;
@@ -782,13 +819,15 @@ __device__ __forceinline__ void mstage_unit(unsigned in, unsigned u, const XUnit
         lo[i / 4] |= (unsigned(l) & 255u) << (8 * (i % 4));
     }
     codes += quad_xor1(codes);
+    const int first16 = codes;  // quad threads 0, 1: the block's first 16 values
     codes += quad_xor2(codes);
     uint8_t* entry = atab + (size_t(r) * (in / 256) + g) * kAGroup + (m * 16 + 4 * G + 2 * b) * 16;
     *reinterpret_cast<uint4*>(entry) = b ? make_uint4(0, 0, hi[0], hi[1]) : make_uint4(hi[0], hi[1], 0, 0);
     *reinterpret_cast<uint4*>(entry + 16) =
         b ? make_uint4(0, 0, lo[0], lo[1]) : make_uint4(lo[0], lo[1], 0, 0);
     if (m == 0)
-        blocks[size_t(r) * (in / 32) + e0 / 32] = make_float4(scale, sum, __int_as_float(codes), 0.f);
+        blocks[size_t(r) * (in / 32) + e0 / 32] =
+            make_float4(scale, sum, __int_as_float(codes), __int_as_float(first16));
 }
 
 // Tile-packed weights (kdq_gguf_pack), this library's resident GGUF layout.  Rows are
@@ -841,8 +880,18 @@ __device__ __forceinline__ void load_packed(const uint8_t* unit, unsigned G, uns
 // B operand of MFMA m from one lane's packed chunk (load_lane layout, or load_packed's
 // when PACKED).
 template <int ENC, bool PACKED = false>
-__device__ __forceinline__ i32x4 b_operand(const Lane& L, int m) {
-    if constexpr (PACKED && ENC == KDQ_Q8_0) {
+__device__ __forceinline__ i32x4 b_operand(const Lane& L, int m, unsigned q6_shift) {
+    if constexpr (ENC == KDQ_Q6_K) {
+        // the 6-bit codes (0..63) of positions 8m..8m+7: low nibble | qh bits 2p, 2p+1
+        // (block 0), high nibble | qh bits 4+2p, 5+2p (block 1); q6_shift = 2p
+        const unsigned l0 = L.w[2 * m], l1 = L.w[2 * m + 1];
+        const unsigned h0 = L.w[8 + 2 * m], h1 = L.w[9 + 2 * m];
+        const unsigned up = 4 - q6_shift;
+        return i32x4{int((l0 & 0x0f0f0f0fu) | ((h0 << up) & 0x30303030u)),
+                     int((l1 & 0x0f0f0f0fu) | ((h1 << up) & 0x30303030u)),
+                     int(((l0 >> 4) & 0x0f0f0f0fu) | ((h0 >> q6_shift) & 0x30303030u)),
+                     int(((l1 >> 4) & 0x0f0f0f0fu) | ((h1 >> q6_shift) & 0x30303030u))};
+    } else if constexpr (PACKED && ENC == KDQ_Q8_0) {
         // block 0 codes in w[0..7], block 1 in w[8..15]
         return i32x4{int(L.w[2 * m]), int(L.w[2 * m + 1]), int(L.w[8 + 2 * m]),
                      int(L.w[9 + 2 * m])};
@@ -887,9 +936,22 @@ struct ScaleSel {
 // The chunk's contribution from the four integer sums of this lane (c.x, c.y: block 0
 // high and low planes; c.z, c.w: block 1) with the activation block entries x0, x1.
 template <int ENC, bool PACKED = false>
-__device__ __forceinline__ float chunk_value(const Lane& L, ScaleSel sel, i32x4 c, float4 x0,
-                                             float4 x1, bool& bad) {
-    if constexpr (PACKED && ENC != KDQ_Q4_K) {
+__device__ __forceinline__ float chunk_value(const Lane& L, ScaleSel sel, i32x4 c, i32x4 c2,
+                                             float4 x0, float4 x1, bool& bad) {
+    if constexpr (ENC == KDQ_Q6_K) {
+        // c: positions 0..15 of each block, c2: 16..31; sum (q - 32) x_q per 16 values is
+        // an exact integer below 2^24 in magnitude, then the int8 scales and d in fp32
+        const float d = half_hw(L.w[18] >> 16);
+        bad |= !isfinite(d);
+        const unsigned s0 = L.w[16] >> (8 * sel.shift), s1 = L.w[17] >> (8 * sel.shift);
+        const int f0 = __float_as_int(x0.w), f1 = __float_as_int(x1.w);
+        const int t0 = __float_as_int(x0.z) - f0, t1 = __float_as_int(x1.z) - f1;
+        const float a00 = float(c.x * 256 + c.y - 32 * f0), a01 = float(c2.x * 256 + c2.y - 32 * t0);
+        const float a10 = float(c.z * 256 + c.w - 32 * f1), a11 = float(c2.z * 256 + c2.w - 32 * t1);
+        const float b0 = fmaf(float(int8_t(s0 >> 8)), a01, float(int8_t(s0)) * a00);
+        const float b1 = fmaf(float(int8_t(s1 >> 8)), a11, float(int8_t(s1)) * a10);
+        return d * fmaf(x1.x, b1, x0.x * b0);
+    } else if constexpr (PACKED && ENC != KDQ_Q4_K) {
         // the two block scales share one dword after the code pieces
         const unsigned sc = L.w[4 * PackedFormat<ENC>::pieces];
         const float d0 = half_hw(sc & 0xffffu), d1 = half_hw(sc >> 16);
@@ -1026,7 +1088,9 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
     // A operand base: carrier lanes (row j of A lies in their group) read their table
     // entry, the others a zero region; MFMA m adds m * 256 bytes
     const bool carrier = j / 4 == G;
-    const ScaleSel sel{8 * ((2 * G) & 3), G >= 2};
+    // Q4_K: the scale bytes of sub-blocks 2G, 2G+1; Q6_K: 2p for chunk G = 2h + p
+    const ScaleSel sel = ENC == KDQ_Q6_K ? ScaleSel{2 * (G % 2), false}
+                                         : ScaleSel{8 * ((2 * G) & 3), G >= 2};
     // every argument in one round of scalar loads, then the exit test
     asm volatile("" ::"s"(weights), "s"(x), "s"(y), "s"(status), "s"(row_bytes), "s"(stride),
                  "s"(in), "s"(out), "s"(rows_per_wg));
@@ -1049,6 +1113,8 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
             if constexpr (PACKED)
                 load_packed<ENC>(weights + (size_t(n / 16) * groups + g) * PackedFormat<ENC>::unit,
                                  G, n % 16, L[k]);
+            else if constexpr (ENC == KDQ_Q6_K)
+                load_lane_q6k(weights + size_t(n) * row_bytes, g, G, L[k]);
             else
                 load_lane<ENC>(weights + size_t(n) * row_bytes, 4 * g + G, L[k]);
             cur.next(tiles, W);
@@ -1065,11 +1131,11 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
     if (threadIdx.x < units_x)
-        mstage_unit(in, threadIdx.x, first_unit, atab, blocks);
+        mstage_unit<ENC>(in, threadIdx.x, first_unit, atab, blocks);
     for (unsigned u = threadIdx.x + kThreads; u < units_x; u += kThreads) {
         XUnit more;
         load_unit(x, in, u, more);
-        mstage_unit(in, u, more, atab, blocks);
+        mstage_unit<ENC>(in, u, more, atab, blocks);
     }
     __syncthreads();
 
@@ -1089,21 +1155,28 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
             for (int k = 0; k < kUnits; ++k) {
                 if (cur.g >= groups)
                     break;
-                const unsigned chunk = 4 * cur.g + G;
+                const unsigned b0 = 8 * cur.g + block_of<ENC>(G, 0);
+                const unsigned b1 = 8 * cur.g + block_of<ENC>(G, 1);
 #pragma unroll kRowUnroll
                 for (int r = 0; r < R; ++r) {
                     const uint8_t* a = carrier ? atab + (size_t(r) * groups + cur.g) * kAGroup +
                                                      (4 * G + j % 4) * 16
                                                : lds;
-                    i32x4 c = {0, 0, 0, 0};
+                    // Q6_K keeps positions 0..15 (MFMAs 0, 1) and 16..31 (2, 3) of each
+                    // block apart: its scales change every 16 values
+                    i32x4 c = {0, 0, 0, 0}, c2 = {0, 0, 0, 0};
 #pragma unroll
-                    for (int m = 0; m < 4; ++m)
-                        c = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                            *reinterpret_cast<const i32x4*>(a + m * 256),
-                            b_operand<ENC, PACKED>(L[k], m), c, 0, 0, 0);
-                    const float4* xb = blocks + size_t(r) * (in / 32) + 2 * chunk;
+                    for (int m = 0; m < 4; ++m) {
+                        const i32x4 av = *reinterpret_cast<const i32x4*>(a + m * 256);
+                        const i32x4 bv = b_operand<ENC, PACKED>(L[k], m, sel.shift);
+                        if (ENC == KDQ_Q6_K && m >= 2)
+                            c2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, c2, 0, 0, 0);
+                        else
+                            c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, c, 0, 0, 0);
+                    }
+                    const float4* xb = blocks + size_t(r) * (in / 32);
                     mine[size_t(r * kTiles + cur.t) * 64 * kPartialPitch] +=
-                        chunk_value<ENC, PACKED>(L[k], sel, c, xb[0], xb[1], bad);
+                        chunk_value<ENC, PACKED>(L[k], sel, c, c2, xb[b0], xb[b1], bad);
                 }
                 cur.next(tiles, W);
             }
@@ -1370,6 +1443,10 @@ int launch_mfma_any(int encoding, const void* w, size_t row_bytes, const float* 
         return launch_mfma<KDQ_Q4_0, PACKED>(w, row_bytes, x, rows, in, out, y, stride, status, s);
     case KDQ_Q4_K:
         return launch_mfma<KDQ_Q4_K, PACKED>(w, row_bytes, x, rows, in, out, y, stride, status, s);
+    case KDQ_Q6_K:  // row-major only: the packed layout has no Q6_K unit
+        if constexpr (!PACKED)
+            return launch_mfma<KDQ_Q6_K, false>(w, row_bytes, x, rows, in, out, y, stride, status, s);
+        return KDQ_ERR_UNSUPPORTED;
     default:
         return KDQ_ERR_UNSUPPORTED;
     }
@@ -1495,14 +1572,19 @@ int with_encoding(int encoding, F&& f) {
     }
 }
 
-// The encodings the streaming and MFMA products (and the packed layout) take.
+// The encodings the streaming and MFMA products take over row-major weights (the packed
+// layout: Q8_0, Q4_0, Q4_K).
 bool streamed_encoding(int encoding) {
-    return encoding == KDQ_Q8_0 || encoding == KDQ_Q4_0 || encoding == KDQ_Q4_K;
+    return encoding == KDQ_Q8_0 || encoding == KDQ_Q4_0 || encoding == KDQ_Q4_K ||
+           encoding == KDQ_Q6_K;
 }
 
 // The streaming kernels need whole 64-value lane slots, 4-byte aligned rows and packed
-// rows of exactly the format's size (16-byte aligned for Q4_K).
+// rows of exactly the format's size (16-byte aligned for Q4_K); Q6_K (MFMA kernel only)
+// 256-value groups and 2-byte aligned rows.
 bool streams(int encoding, const void* weights, size_t row_bytes, size_t in) {
+    if (encoding == KDQ_Q6_K)
+        return in % 256 == 0 && row_bytes % 2 == 0 && aligned(weights, 2);
     return streamed_encoding(encoding) && in % 256 == 0 && row_bytes % 4 == 0 &&
            aligned(weights, 4) &&
            (encoding != KDQ_Q4_K || (row_bytes % 16 == 0 && aligned(weights, 16)));
@@ -1719,6 +1801,10 @@ int launch_fused(const kdq_matvec_job* jobs, const size_t* idx, size_t n, hipStr
         return launch_mfma_rows<KDQ_Q4_0, PACKED>(j0.rows, p.waves, mj, stream);
     case KDQ_Q4_K:
         return launch_mfma_rows<KDQ_Q4_K, PACKED>(j0.rows, p.waves, mj, stream);
+    case KDQ_Q6_K:
+        if constexpr (!PACKED)
+            return launch_mfma_rows<KDQ_Q6_K, false>(j0.rows, p.waves, mj, stream);
+        return KDQ_ERR_UNSUPPORTED;
     default:
         return KDQ_ERR_UNSUPPORTED;
     }
@@ -1800,6 +1886,8 @@ int indexed_gemv_affine(const IndexedJob& first, unsigned count, size_t x_step,
             return launch_mfma_rows<KDQ_Q4_0, false>(j.rows, p.waves, mj, s);
         case KDQ_Q4_K:
             return launch_mfma_rows<KDQ_Q4_K, false>(j.rows, p.waves, mj, s);
+        case KDQ_Q6_K:
+            return launch_mfma_rows<KDQ_Q6_K, false>(j.rows, p.waves, mj, s);
         default:
             return KDQ_ERR_UNSUPPORTED;
         }

@@ -22,6 +22,27 @@ __device__ __forceinline__ unsigned load4(const uint8_t* p) {
     return *reinterpret_cast<const unsigned*>(p);
 }
 
+// Loads at 2-byte alignment (Q6_K super-blocks are 210 bytes, so every other one starts
+// two bytes past a dword): gfx950 global loads run in unaligned-access mode, and the
+// compiler still emits one global_load_dwordx4 / dwordx2 / dword for each.
+typedef unsigned u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
+typedef unsigned u32x2_a2 __attribute__((ext_vector_type(2), aligned(2)));
+typedef unsigned u32_a2 __attribute__((aligned(2)));
+
+__device__ __forceinline__ u32x4 load16_a2(const uint8_t* p) {
+    const u32x4_a2 v = *reinterpret_cast<const u32x4_a2*>(p);
+    return u32x4{v.x, v.y, v.z, v.w};
+}
+
+__device__ __forceinline__ uint2 load8_a2(const uint8_t* p) {
+    const u32x2_a2 v = *reinterpret_cast<const u32x2_a2*>(p);
+    return make_uint2(v.x, v.y);
+}
+
+__device__ __forceinline__ unsigned load4_a2(const uint8_t* p) {
+    return *reinterpret_cast<const u32_a2*>(p);
+}
+
 // Non-temporal (streaming) variants for weight bytes read once per launch: the loads
 // carry the nt cache policy so a weight stream larger than the caches does not evict
 // what is reused (activations, outputs).  Same alignment rules as load16 / load4.

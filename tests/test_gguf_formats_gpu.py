@@ -1,12 +1,13 @@
-"""GPU parity of the decode and the exact product for the encodings without a streaming
-kernel (Q3_K, Q6_K, IQ4_NL, IQ4_XS, IQ3_XXS, IQ2_S, IQ3_S, BF16;
+"""GPU parity of the decode and the products for the encodings beyond Q4_0 / Q8_0 / Q4_K
+(Q3_K, Q6_K, IQ4_NL, IQ4_XS, IQ3_XXS, IQ2_S, IQ3_S, BF16;
 IW/include/kadan/gguf_quantization.hpp:631-762).
 
 Decoded weights must be bit-exact to the oracle (NaN matches NaN, as
 IW/tests/gguf_quantization.cpp:21-29 compares), including the special fp16 block scales
-of that test at each format's scale offset; products (kdq_gemv, which runs the exact
-kernel for these encodings, and kdq_gemv_exact) within rel-L2 <= 1e-3 and max-abs <=
-2e-2 of the output RMS against the oracle's double product of exactly decoded weights.
+of that test at each format's scale offset; products (kdq_gemv, which runs the MFMA
+GEMV for Q6_K rows of whole 256-value groups and the exact kernel otherwise, and
+kdq_gemv_exact) within rel-L2 <= 1e-3 and max-abs <= 2e-2 of the output RMS against the
+oracle's double product of exactly decoded weights.
 """
 import numpy as np
 import pytest
@@ -150,3 +151,22 @@ def test_batch_mixes_streamed_and_exact_encodings(device, oracle):
     ops.gemv_batch(jobs)
     for j, e in zip(jobs, expected):
         assert_close(j["output"].cpu().numpy(), e, what=f"enc={j['encoding']}")
+
+
+@pytest.mark.parametrize("shift", [0, 1])
+def test_q6_k_mfma_two_byte_aligned_rows(device, oracle, shift):
+    """Q6_K rows start 210 bytes apart, so super-blocks and whole rows alternate between
+    dword and half-dword alignment; a base two bytes past a dword flips every one of
+    them.  Rows of 3 super-blocks (630 bytes), batch 1, 2 and 5."""
+    torch = _torch()
+    from kadan_amd import ops
+    n_in, n_out = 768, 77
+    w = synth.gguf_weights(Q6_K, 41 + shift, n_out + 1, n_in)
+    dev = torch.from_numpy(w).to(device)
+    view = dev[shift:shift + n_out]  # shift 1: the base moves by 630 bytes
+    assert (view.data_ptr() % 4) == (2 if shift else 0)
+    for rows in (1, 2, 5):
+        x = synth.normal(7 + rows, 3, rows * n_in).reshape(rows, n_in)
+        expected = oracle.gemv(Q6_K, w[shift:shift + n_out], x, n_in, n_out)
+        got = ops.gemv(Q6_K, view, torch.from_numpy(x).to(device), n_out)
+        assert_close(got.cpu().numpy(), expected, what=f"shift={shift} rows={rows}")
