@@ -293,14 +293,15 @@ __global__ __launch_bounds__(256) void exact_gemv(const uint8_t* weights, size_t
                                                   unsigned out, float* y, size_t stride,
                                                   unsigned* status, const int32_t* index,
                                                   size_t index_stride, unsigned index_limit,
-                                                  size_t x_step, size_t y_step) {
+                                                  size_t x_step, size_t y_step, unsigned x_every) {
     using F = Format<ENC>;
     const unsigned column = blockIdx.x * 4 + threadIdx.x / 64;
     const unsigned lane = threadIdx.x % 64;
     if (column >= out)
         return;
-    // job blockIdx.y of an affine batch: its input, output and expert index step along
-    x += blockIdx.y * x_step;
+    // job blockIdx.y of an affine batch: its input (every x_every jobs), output and expert
+    // index step along
+    x += (blockIdx.y / x_every) * x_step;
     y += blockIdx.y * y_step;
     if (index)
         weights += size_t(min(unsigned(index[blockIdx.y]), index_limit - 1)) * index_stride;
@@ -753,13 +754,14 @@ constexpr int mfma_units = R == 1 ? 2 : (R == 2 ? 2 : 1);
 //       4g + G; the other 8 bytes are zero
 //   block table, per batch row r and 32-value block: float4 (s, sum x, sum of codes as
 //       int bits, sum of the codes of its first 16 values as int bits)
-//   partials [R][tiles][64 lanes][kPartialPitch] floats
+//   partials [R][mats * tiles][64 lanes][kPartialPitch] floats (mats = 2 for paired jobs:
+//       the gate tiles, then the up tiles)
 struct MfmaLds {
     size_t a, blocks, partial, total;
 };
 
-__host__ __device__ inline MfmaLds mfma_layout(unsigned batch, unsigned in) {
-    const size_t tiles = batch >= 4 ? 1 : 4 / batch;
+__host__ __device__ inline MfmaLds mfma_layout(unsigned batch, unsigned in, unsigned mats = 1) {
+    const size_t tiles = (batch >= 4 ? 1 : 4 / batch) * mats;
     MfmaLds l;
     l.a = 1024;
     l.blocks = l.a + size_t(batch) * (in / 256) * kAGroup;
@@ -1042,14 +1044,19 @@ struct MfmaJob {  // one job's fields together
     // optional: the weights start at weights + min(*index, index_limit - 1) * index_stride
     const int32_t* index;
     size_t index_stride;
+    // paired launches: the second matrix (same shape, same expert offset); y = silu(W x) * (up x)
+    const uint8_t* up;
 };
 struct MfmaJobs {
     MfmaJob job[kMaxFused];
     unsigned count, columns, in, rows_per_wg;
     // affine batch: `count` jobs all described by job[0], job j's x, y and index advanced
-    // by j * x_step, j * y_step and j
-    unsigned affine;
+    // by (j / x_every) * x_step, j * y_step and j
+    unsigned affine, x_every;
     size_t x_step, y_step;
+    // 2 when every job of the launch is paired (a launch-wide shape: the LDS layout
+    // depends on it), else 1
+    unsigned mats;
 };
 
 // Workgroup: W wavefronts (W <= 16), rows [r0, r1) of its job, processed in passes of up
@@ -1062,12 +1069,13 @@ template <int ENC, int R, int W, bool PACKED>
 __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
     const unsigned jid = jobs.affine ? 0 : blockIdx.y, step = jobs.affine ? blockIdx.y : 0;
     const MfmaJob& jb = jobs.job[jid];
-    const uint8_t* __restrict__ weights =
-        jb.index ? jb.weights + size_t(min(unsigned(jb.index[step]), jb.index_limit - 1)) *
-                                    jb.index_stride
-                 : jb.weights;
+    const size_t expert =
+        jb.index ? size_t(min(unsigned(jb.index[step]), jb.index_limit - 1)) * jb.index_stride : 0;
+    const uint8_t* __restrict__ weights = jb.weights + expert;
+    const unsigned mats = jobs.mats == 2 ? 2 : 1;
+    const uint8_t* __restrict__ up = mats == 2 ? jb.up + expert : weights;
     const size_t row_bytes = jb.row_bytes, stride = jb.stride;
-    const float* x = jb.x + step * jobs.x_step;
+    const float* x = jb.x + (jobs.affine ? step / jobs.x_every : 0) * jobs.x_step;
     float* __restrict__ y = jb.y + step * jobs.y_step;
     unsigned* status = jb.status;
     const unsigned in = jobs.in, out = jb.out, rows_per_wg = jobs.rows_per_wg;
@@ -1076,7 +1084,7 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
     constexpr int kRowUnroll = R <= 2 ? R : 1;  // larger batches: one row's operands at a time
     constexpr unsigned kThreads = W * 64;
     extern __shared__ __align__(16) uint8_t lds[];
-    const MfmaLds layout = mfma_layout(R, in);
+    const MfmaLds layout = mfma_layout(R, in, mats);
     const unsigned groups = in / 256;
     uint8_t* atab = lds + layout.a;
     float4* blocks = reinterpret_cast<float4*>(lds + layout.blocks);
@@ -1092,8 +1100,8 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
     const ScaleSel sel = ENC == KDQ_Q6_K ? ScaleSel{2 * (G % 2), false}
                                          : ScaleSel{8 * ((2 * G) & 3), G >= 2};
     // every argument in one round of scalar loads, then the exit test
-    asm volatile("" ::"s"(weights), "s"(x), "s"(y), "s"(status), "s"(row_bytes), "s"(stride),
-                 "s"(in), "s"(out), "s"(rows_per_wg));
+    asm volatile("" ::"s"(weights), "s"(up), "s"(x), "s"(y), "s"(status), "s"(row_bytes),
+                 "s"(stride), "s"(in), "s"(out), "s"(rows_per_wg));
     const unsigned r0 = blockIdx.x * rows_per_wg, r1 = min(out, r0 + rows_per_wg);
     if (r0 >= out)
         return;  // the whole workgroup, before any barrier
@@ -1103,21 +1111,24 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
         reinterpret_cast<uint32_t*>(lds)[t] = 0u;
 
     auto pass_tiles = [&](unsigned p0) { return min(unsigned(kTiles), (r1 - p0 + 15) / 16); };
+    // cursor tile t < tiles is row tile t of `weights`, t >= tiles row tile t - tiles of `up`
     auto load_units = [&](unsigned p0, UnitCursor cur, Lane(&L)[kUnits]) {
         const unsigned tiles = pass_tiles(p0);
 #pragma unroll
         for (int k = 0; k < kUnits; ++k) {
             const bool valid = cur.g < groups;
             const unsigned g = valid ? cur.g : wave % groups, t = valid ? cur.t : 0;
-            const unsigned n = min(p0 + 16 * t + j, r1 - 1);
+            const bool second = t >= tiles;
+            const uint8_t* w = second ? up : weights;
+            const unsigned n = min(p0 + 16 * (second ? t - tiles : t) + j, r1 - 1);
             if constexpr (PACKED)
-                load_packed<ENC>(weights + (size_t(n / 16) * groups + g) * PackedFormat<ENC>::unit,
+                load_packed<ENC>(w + (size_t(n / 16) * groups + g) * PackedFormat<ENC>::unit,
                                  G, n % 16, L[k]);
             else if constexpr (ENC == KDQ_Q6_K)
-                load_lane_q6k(weights + size_t(n) * row_bytes, g, G, L[k]);
+                load_lane_q6k(w + size_t(n) * row_bytes, g, G, L[k]);
             else
-                load_lane<ENC>(weights + size_t(n) * row_bytes, 4 * g + G, L[k]);
-            cur.next(tiles, W);
+                load_lane<ENC>(w + size_t(n) * row_bytes, 4 * g + G, L[k]);
+            cur.next(tiles * mats, W);
         }
     };
 
@@ -1144,8 +1155,7 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
         const unsigned tiles = pass_tiles(p0);
         // partial[((r*kTiles + t)*64 + lane)*kPartialPitch + wave] belongs to this thread
         float* mine = partial + size_t(lane) * kPartialPitch + wave;
-#pragma unroll
-        for (int i = 0; i < R * kTiles; ++i)
+        for (unsigned i = 0; i < R * kTiles * mats; ++i)
             mine[size_t(i) * 64 * kPartialPitch] = 0.f;
         for (UnitCursor cur{wave, 0}; cur.g < groups;) {
             if (!first)
@@ -1175,10 +1185,12 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
                             c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, c, 0, 0, 0);
                     }
                     const float4* xb = blocks + size_t(r) * (in / 32);
-                    mine[size_t(r * kTiles + cur.t) * 64 * kPartialPitch] +=
+                    // partial slot of (matrix, row tile): m * kTiles + tile
+                    const unsigned slot = cur.t < tiles ? cur.t : kTiles + cur.t - tiles;
+                    mine[size_t(r * kTiles * mats + slot) * 64 * kPartialPitch] +=
                         chunk_value<ENC, PACKED>(L[k], sel, c, c2, xb[b0], xb[b1], bad);
                 }
-                cur.next(tiles, W);
+                cur.next(tiles * mats, W);
             }
         }
         first = false;  // a wavefront without units in the first pass never used its loads
@@ -1189,11 +1201,19 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
         for (unsigned o = threadIdx.x / 16; o < outputs; o += kThreads / 16) {
             const unsigned k = threadIdx.x % 16;
             const unsigned jj = o % 16, t = (o / 16) % tiles, r = o / (16 * tiles);
-            const float* src = partial + (size_t(r * kTiles + t) * 64 + jj) * kPartialPitch + k;
+            const float* src =
+                partial + (size_t(r * kTiles * mats + t) * 64 + jj) * kPartialPitch + k;
             float v = k < W ? ((src[0] + src[16 * kPartialPitch]) + src[32 * kPartialPitch]) +
                                   src[48 * kPartialPitch]
                             : 0.f;
             v = row16_total(v);
+            if (mats == 2) {  // the up row of the same output, kTiles slots on
+                const float* us = src + size_t(kTiles) * 64 * kPartialPitch;
+                float u = k < W ? ((us[0] + us[16 * kPartialPitch]) + us[32 * kPartialPitch]) +
+                                      us[48 * kPartialPitch]
+                                : 0.f;
+                v = silu_of(v) * row16_total(u);
+            }
             const unsigned n = p0 + 16 * t + jj;
             if (k == 0 && n < r1)
                 y[size_t(r) * stride + n] = v;
@@ -1224,7 +1244,7 @@ int launch_exact(const void* w, size_t row_bytes, const float* x, size_t rows, s
                  size_t out, float* y, size_t stride, unsigned* status, hipStream_t stream,
                  const int32_t* index = nullptr, size_t index_stride = 0,
                  unsigned index_limit = 1, unsigned batch = 1, size_t x_step = 0,
-                 size_t y_step = 0) {
+                 size_t y_step = 0, unsigned x_every = 1) {
     const dim3 grid(unsigned((out + 3) / 4), batch);
     for (size_t first = 0; first < rows; first += 8) {
         const unsigned group = unsigned(std::min<size_t>(8, rows - first));
@@ -1232,12 +1252,12 @@ int launch_exact(const void* w, size_t row_bytes, const float* x, size_t rows, s
             hipLaunchKernelGGL((exact_gemv<ENC, 1>), grid, dim3(256), 0, stream,
                                static_cast<const uint8_t*>(w), row_bytes, x + first * in, 1u,
                                unsigned(in), unsigned(out), y + first * stride, stride, status,
-                               index, index_stride, index_limit, x_step, y_step);
+                               index, index_stride, index_limit, x_step, y_step, x_every);
         else
             hipLaunchKernelGGL((exact_gemv<ENC, 8>), grid, dim3(256), 0, stream,
                                static_cast<const uint8_t*>(w), row_bytes, x + first * in, group,
                                unsigned(in), unsigned(out), y + first * stride, stride, status,
-                               index, index_stride, index_limit, x_step, y_step);
+                               index, index_stride, index_limit, x_step, y_step, x_every);
         KDQ_HIP(hipGetLastError());
     }
     return KDQ_OK;
@@ -1325,9 +1345,9 @@ int launch_fast(const void* w, size_t row_bytes, const float* x, size_t rows, si
     return KDQ_OK;
 }
 
-// LDS bytes of mfma_gemv for `batch` rows.
-size_t mfma_lds(size_t batch, size_t in) {
-    return mfma_layout(unsigned(batch), unsigned(in)).total;
+// LDS bytes of mfma_gemv for `batch` rows (mats = 2: paired jobs).
+size_t mfma_lds(size_t batch, size_t in, unsigned mats = 1) {
+    return mfma_layout(unsigned(batch), unsigned(in), mats).total;
 }
 
 struct MfmaPlan {
@@ -1335,22 +1355,32 @@ struct MfmaPlan {
 };
 
 // Batch rows per pass as the LDS allows (at most 8); `waves` wavefronts per workgroup and
-// ceil(total_out / compute units) rows per workgroup, total_out summed over the jobs of
-// one launch.  Over packed weights the rows per workgroup are a multiple of 8, so every
-// 128-byte line of a unit (8 row slots of one chunk) belongs to one workgroup.
-bool plan_mfma(size_t rows, size_t in, size_t total_out, MfmaPlan& p, bool packed = false) {
+// ceil(total_out / workgroup slots) rows per workgroup, total_out summed over the jobs of
+// one launch (paired jobs: mats = 2, each output row two rows of work).  Over packed
+// weights the rows per workgroup are a multiple of 8, so every 128-byte line of a unit
+// (8 row slots of one chunk) belongs to one workgroup.
+bool plan_mfma(size_t rows, size_t in, size_t total_out, MfmaPlan& p, bool packed = false,
+               unsigned mats = 1) {
     constexpr size_t limit = 160 * 1024;
-    if (in % 256 || mfma_lds(1, in) > limit)
+    if (in % 256 || mfma_lds(1, in, mats) > limit)
         return false;
     unsigned batch = 1;
-    while (batch < 8 && batch < rows && mfma_lds(batch * 2, in) <= limit)
+    while (batch < 8 && batch < rows && mfma_lds(batch * 2, in, mats) <= limit)
         batch *= 2;
-    const size_t cus = compute_units();
-    size_t rows_per_wg = std::max<size_t>(1, (total_out + cus - 1) / cus);
+    // A wavefront takes the 256-value groups w, w + W, ...: narrow products (the MoE
+    // experts' 768 / 2048 inputs) use 4 or 8 wavefronts, and correspondingly more
+    // workgroups per compute unit (as many as the LDS holds, up to 16 wavefronts).
+    const size_t groups = in / 256;
+    unsigned waves = groups <= 4 ? 4 : (groups <= 8 ? 8 : 16);
+    size_t per_cu = 16 / waves;
+    while (per_cu > 1 && per_cu * mfma_lds(batch, in, mats) > limit)
+        per_cu /= 2;
+    const size_t slots = compute_units() * per_cu;
+    size_t rows_per_wg = std::max<size_t>(1, (total_out * mats + slots - 1) / slots / mats);
     if (packed)
         rows_per_wg = (rows_per_wg + 7) & ~size_t(7);
     p.batch = batch;
-    p.waves = 16;
+    p.waves = waves;
     p.rows_per_wg = unsigned(rows_per_wg);
     p.grid = unsigned((total_out + rows_per_wg - 1) / rows_per_wg);
     return true;
@@ -1374,7 +1404,7 @@ int launch_mfma_shape(const MfmaJobs& jobs, hipStream_t stream) {
         configured = true;
     }
     hipLaunchKernelGGL((mfma_gemv<ENC, R, W, PACKED>), dim3(jobs.columns, jobs.count),
-                       dim3(W * 64), mfma_lds(R, jobs.in), stream, jobs);
+                       dim3(W * 64), mfma_lds(R, jobs.in, jobs.mats == 2 ? 2 : 1), stream, jobs);
     KDQ_HIP(hipGetLastError());
     return KDQ_OK;
 }
@@ -1777,12 +1807,14 @@ int launch_fused(const kdq_matvec_job* jobs, const size_t* idx, size_t n, hipStr
     size_t total = 0;
     for (size_t k = 0; k < n; ++k)
         total += jobs[idx[k]].columns;
+    const unsigned mats = indexed && indexed[idx[0]].paired ? 2 : 1;  // one kind per launch
     MfmaPlan p;
-    if (!plan_mfma(j0.rows, j0.in, total, p, PACKED))
+    if (!plan_mfma(j0.rows, j0.in, total, p, PACKED, mats))
         return KDQ_ERR_UNSUPPORTED;
     MfmaJobs mj{};
     mj.count = unsigned(n);
     mj.in = j0.in;
+    mj.mats = mats;
     for (size_t k = 0; k < n; ++k) {
         const kdq_matvec_job& j = jobs[idx[k]];
         mj.job[k] = MfmaJob{static_cast<const uint8_t*>(j.weights), j.input, j.output,
@@ -1791,6 +1823,7 @@ int launch_fused(const kdq_matvec_job* jobs, const size_t* idx, size_t n, hipStr
             mj.job[k].index = indexed[idx[k]].index;
             mj.job[k].index_stride = indexed[idx[k]].index_stride;
             mj.job[k].index_limit = indexed[idx[k]].index_limit;
+            mj.job[k].up = static_cast<const uint8_t*>(indexed[idx[k]].paired);
         }
     }
     number_workgroups(mj, p.rows_per_wg);
@@ -1860,24 +1893,35 @@ int run_batch(const kdq_matvec_job* jobs, size_t count, void* stream) {
 
 }  // namespace
 
+bool swiglu_pairable(const kdq_matvec_job& j, size_t count) {
+    MfmaPlan p;
+    return fusable(j, false) && plan_mfma(j.rows, j.in, size_t(j.columns) * count, p, false, 2) &&
+           p.batch >= j.rows && (count == 1 || j.rows == 1);
+}
+
 int indexed_gemv_affine(const IndexedJob& first, unsigned count, size_t x_step,
-                        size_t y_step, hipStream_t s) {
+                        size_t y_step, hipStream_t s, unsigned x_every) {
     const kdq_matvec_job& j = first.job;
-    if (count > 65535)
+    if (count > 65535 || !x_every)
         return KDQ_ERR_UNSUPPORTED;
     if (count == 1)
         return indexed_gemv_batch(&first, 1, s);
+    const unsigned mats = first.paired ? 2 : 1;
     MfmaPlan p;  // planned over every job's rows, as launch_fused plans a fused group
-    if (fusable(j, false) && plan_mfma(j.rows, j.in, size_t(j.columns) * count, p, false)) {
+    if (fusable(j, false) &&
+        plan_mfma(j.rows, j.in, size_t(j.columns) * count, p, false, mats)) {
         MfmaJobs mj{};
         mj.count = count;
         mj.in = j.in;
         mj.affine = 1;
+        mj.x_every = x_every;
+        mj.mats = mats;
         mj.x_step = x_step;
         mj.y_step = y_step;
         mj.job[0] = MfmaJob{static_cast<const uint8_t*>(j.weights), j.input, j.output, j.status,
                             j.row_bytes, j.stride, j.columns, first.index ? first.index_limit : 0,
-                            first.index, first.index_stride};
+                            first.index, first.index_stride,
+                            static_cast<const uint8_t*>(first.paired)};
         number_workgroups(mj, p.rows_per_wg);
         switch (j.encoding) {
         case KDQ_Q8_0:
@@ -1892,12 +1936,14 @@ int indexed_gemv_affine(const IndexedJob& first, unsigned count, size_t x_step,
             return KDQ_ERR_UNSUPPORTED;
         }
     }
+    if (first.paired)
+        return KDQ_ERR_UNSUPPORTED;  // the exact kernel has no paired form
     return with_encoding(j.encoding, [&](auto enc) {
         return launch_exact<decltype(enc)::value>(j.weights, j.row_bytes, j.input, j.rows, j.in,
                                                   j.columns, j.output, j.stride, j.status, s,
                                                   first.index, first.index_stride,
                                                   first.index ? first.index_limit : 1u, count,
-                                                  x_step, y_step);
+                                                  x_step, y_step, x_every);
     });
 }
 
@@ -1913,7 +1959,7 @@ int indexed_gemv_batch(const IndexedJob* jobs, size_t count, hipStream_t s) {
         for (size_t k = i; k < count && n < size_t(kMaxFused); ++k)
             if (!done[k] && plain[k].encoding == plain[i].encoding &&
                 plain[k].rows == plain[i].rows && plain[k].in == plain[i].in &&
-                fusable(plain[k], false))
+                !jobs[k].paired == !jobs[i].paired && fusable(plain[k], false))
                 idx[n++] = k;
         const int rc = launch_fused<false>(plain.data(), idx, n, s, jobs);
         if (rc)
@@ -1926,6 +1972,8 @@ int indexed_gemv_batch(const IndexedJob* jobs, size_t count, hipStream_t s) {
             continue;
         const IndexedJob& ij = jobs[i];
         const kdq_matvec_job& j = ij.job;
+        if (ij.paired)
+            return KDQ_ERR_UNSUPPORTED;  // the exact kernel has no paired form
         const int rc = with_encoding(j.encoding, [&](auto enc) {
             return launch_exact<decltype(enc)::value>(j.weights, j.row_bytes, j.input, j.rows,
                                                       j.in, j.columns, j.output, j.stride,

@@ -142,18 +142,34 @@ __device__ __forceinline__ float wave_max(float v) {
 // * index_stride when `index` (a device pointer) is set: the expert slice a device-side
 // routing chose.  Products of streamed encodings run fused on the MFMA kernel, the rest
 // on the exact kernel.  The jobs must satisfy kdq_gemv's argument rules (unchecked).
+// With `paired` set (MFMA kernel only: swiglu_pairable), the job multiplies x by two
+// matrices of the same shape and encoding, job.weights (gate) and `paired` (up, at the
+// same expert offset), and writes silu(gate x) * (up x).
 struct IndexedJob {
     kdq_matvec_job job;
     const int32_t* index;
     size_t index_stride;
     unsigned index_limit;
+    const void* paired;
 };
 int indexed_gemv_batch(const IndexedJob* jobs, size_t count, hipStream_t stream);
-// `count` products in one launch, all as `first` except that job j reads x + j * x_step,
-// writes y + j * y_step and takes its expert from index[j] (rows of `first` must be 1
-// when count > 1 runs on the MFMA kernel; any rows on the exact kernel).
+// `count` products in one launch, all as `first` except that job j reads
+// x + (j / x_every) * x_step, writes y + j * y_step and takes its expert from index[j]
+// (rows of `first` must be 1 when count > 1 runs on the MFMA kernel; any rows on the
+// exact kernel, which does not take `paired`).
 int indexed_gemv_affine(const IndexedJob& first, unsigned count, size_t x_step, size_t y_step,
-                        hipStream_t stream);
+                        hipStream_t stream, unsigned x_every = 1);
+// Whether `count` jobs like j (an affine launch when count > 1) run on the MFMA kernel
+// with a paired matrix.
+bool swiglu_pairable(const kdq_matvec_job& j, size_t count);
+
+// silu and sigmoid as the reference defines them (IW/src/models/text/gguf_weights.cpp:627-633)
+__device__ __forceinline__ float silu_of(float v) {
+    return v / (1.0f + expf(-v));
+}
+__device__ __forceinline__ float sigmoid_of(float v) {
+    return 1.0f / (1.0f + expf(-v));
+}
 
 // The MoE router of kdq_moe_route (softmax with a double total, top-k by probability,
 // weights renormalised by max(sum, 2^-14)) without the expert permutation.

@@ -4,33 +4,27 @@
 // trip between its stages (the reference returns to the host three times per layer).
 //
 // Stages, all on `stream`:
-//   1. one GEMV batch over x: router logits, the shared expert's gate and up rows, and the
-//      shared-expert gate scalar ffn_gate_inp_shexp . x (as a one-row fp32 matrix)
+//   1. one GEMV batch over x: router logits, the shared-expert gate scalar
+//      ffn_gate_inp_shexp . x (as a one-row fp32 matrix), and the shared expert's gate and
+//      up rows, as one paired MFMA job that writes silu(gate) * up when the kernel takes
+//      the pair (gate and up stored alike)
 //   2. routing (route_selection: the kdq_moe_route kernel; softmax with a double total,
 //      top-k by probability, weights renormalised by max(sum, 2^-14))
-//   3. swiglu_kernel on the shared rows: silu(gate) * up
-//   4. per token, one launch of its top_k gate GEMVs and one of its up GEMVs, each job's
-//      weights starting at the expert slice the routing wrote on the device, then
-//      swiglu_kernel
+//   3. swiglu_kernel on the shared rows, unless paired in 1
+//   4. one launch of every slot's expert gate / up GEMV (slot s reads token s / top_k's
+//      row), each job's weights starting at the expert slice the routing wrote on the
+//      device; paired with the swiglu like 1, else gate and up launches and swiglu_kernel
 //   5. one launch of every slot's expert down GEMV, plus the shared expert's down
 //   6. combine_kernel: y = sum over the selections, in selection order, of down * weight,
 //      plus shared_down * sigmoid(gate scalar)
-// GEMVs of Q4_0 / Q8_0 / Q4_K run on the MFMA kernel (fused per shape), every other
-// encoding on the exact kernel.
+// GEMVs of Q4_0 / Q8_0 / Q4_K / Q6_K run on the MFMA kernel (fused per shape), every
+// other encoding on the exact kernel.
 #include "kdq_common.hpp"
 
 #include <vector>
 
 namespace kdq {
 namespace {
-
-// silu and sigmoid as the reference defines them (IW/src/models/text/gguf_weights.cpp:627-633)
-__device__ __forceinline__ float silu_of(float v) {
-    return v / (1.0f + expf(-v));
-}
-__device__ __forceinline__ float sigmoid_of(float v) {
-    return 1.0f / (1.0f + expf(-v));
-}
 
 __global__ __launch_bounds__(256) void swiglu_kernel(float* gate, const float* up, size_t n) {
     const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
@@ -74,6 +68,12 @@ kdq_matvec_job job(const kdq_gguf_tensor& m, const float* x, size_t rows, size_t
     j.rows = uint32_t(rows);
     j.encoding = m.encoding;
     return j;
+}
+
+// Gate and up stored alike (so one launch can read both at the same expert offset).
+bool same_layout(const kdq_gguf_tensor& a, const kdq_gguf_tensor& b) {
+    return a.encoding == b.encoding && a.row_bytes == b.row_bytes &&
+           a.expert_bytes == b.expert_bytes;
 }
 
 size_t align256(size_t n) {
@@ -134,43 +134,53 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
     auto* ds = static_cast<float*>(part[9]);
     auto st = static_cast<hipStream_t>(stream);
 
-    // 1. router, shared gate / up, shared-gate scalar
+    // 1. router, shared-gate scalar, shared gate / up (with the swiglu in the same launch
+    //    when the MFMA kernel takes the pair)
     const kdq_gguf_tensor gate_vector{L.shared_gate, H * 4, 0, KDQ_F32};
-    const IndexedJob first[4] = {{job(L.router, x, rows, H, E, logits, status), nullptr, 0, 1},
-                                 {job(L.gate_shexp, x, rows, H, S, sg, status), nullptr, 0, 1},
-                                 {job(L.up_shexp, x, rows, H, S, su, status), nullptr, 0, 1},
-                                 {job(gate_vector, x, rows, H, 1, gate, status), nullptr, 0, 1}};
-    if ((rc = indexed_gemv_batch(first, 4, st)))
+    const kdq_matvec_job shared_gate = job(L.gate_shexp, x, rows, H, S, sg, status);
+    const bool pair_shared =
+        same_layout(L.gate_shexp, L.up_shexp) && swiglu_pairable(shared_gate, 1);
+    IndexedJob first[4] = {{job(L.router, x, rows, H, E, logits, status), nullptr, 0, 1, nullptr},
+                           {job(gate_vector, x, rows, H, 1, gate, status), nullptr, 0, 1, nullptr},
+                           {shared_gate, nullptr, 0, 1, pair_shared ? L.up_shexp.weights : nullptr},
+                           {job(L.up_shexp, x, rows, H, S, su, status), nullptr, 0, 1, nullptr}};
+    if ((rc = indexed_gemv_batch(first, pair_shared ? 3 : 4, st)))
         return rc;
     // 2. routing, straight into the caller's buffers when given
     if ((rc = route_selection(logits, rows, E, K, idx, w, st)))
         return rc;
-    // 3. shared swiglu
-    hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((rows * S + 255) / 256)), dim3(256), 0, st,
-                       sg, su, rows * S);
-    KDQ_HIP(hipGetLastError());
-    // 4. expert gate / up at the routed slices (one launch each: slot s reads token s / K),
-    //    then swiglu.  Slots of one token share its row, so the affine step is per token:
-    //    each token's K slots run as one launch of K jobs over the same x row.
-    for (size_t t = 0; t < rows; ++t) {
-        const float* xt = x + t * H;
-        const IndexedJob gj{job(L.gate_exps, xt, 1, H, F, g + t * K * F, status), idx + t * K,
-                            L.gate_exps.expert_bytes, unsigned(E)};
-        const IndexedJob uj{job(L.up_exps, xt, 1, H, F, u + t * K * F, status), idx + t * K,
-                            L.up_exps.expert_bytes, unsigned(E)};
-        if ((rc = indexed_gemv_affine(gj, unsigned(K), 0, F, st)) ||
-            (rc = indexed_gemv_affine(uj, unsigned(K), 0, F, st)))
-            return rc;
+    // 3. shared swiglu, unless paired above
+    if (!pair_shared) {
+        hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((rows * S + 255) / 256)), dim3(256), 0,
+                           st, sg, su, rows * S);
+        KDQ_HIP(hipGetLastError());
     }
-    hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((slots * F + 255) / 256)), dim3(256), 0, st,
-                       g, u, slots * F);
-    KDQ_HIP(hipGetLastError());
+    // 4. expert gate / up at the routed slices, every slot in one launch (slot s reads
+    //    token s / K's row and writes row s), as a pair with the swiglu when the MFMA
+    //    kernel takes it, else two launches and the swiglu
+    const IndexedJob gj{job(L.gate_exps, x, 1, H, F, g, status), idx, L.gate_exps.expert_bytes,
+                        unsigned(E), nullptr};
+    if (same_layout(L.gate_exps, L.up_exps) && swiglu_pairable(gj.job, slots)) {
+        IndexedJob pj = gj;
+        pj.paired = L.up_exps.weights;
+        if ((rc = indexed_gemv_affine(pj, unsigned(slots), H, F, st, unsigned(K))))
+            return rc;
+    } else {
+        const IndexedJob uj{job(L.up_exps, x, 1, H, F, u, status), idx, L.up_exps.expert_bytes,
+                            unsigned(E), nullptr};
+        if ((rc = indexed_gemv_affine(gj, unsigned(slots), H, F, st, unsigned(K))) ||
+            (rc = indexed_gemv_affine(uj, unsigned(slots), H, F, st, unsigned(K))))
+            return rc;
+        hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((slots * F + 255) / 256)), dim3(256), 0,
+                           st, g, u, slots * F);
+        KDQ_HIP(hipGetLastError());
+    }
     // 5. expert downs (one launch over every slot) and the shared down
     const IndexedJob dj{job(L.down_exps, g, 1, F, H, d, status), idx, L.down_exps.expert_bytes,
-                        unsigned(E)};
+                        unsigned(E), nullptr};
     if ((rc = indexed_gemv_affine(dj, unsigned(slots), F, H, st)))
         return rc;
-    const IndexedJob sj{job(L.down_shexp, sg, rows, S, H, ds, status), nullptr, 0, 1};
+    const IndexedJob sj{job(L.down_shexp, sg, rows, S, H, ds, status), nullptr, 0, 1, nullptr};
     if ((rc = indexed_gemv_batch(&sj, 1, st)))
         return rc;
     // 6. combine

@@ -1,8 +1,12 @@
 """GPU parity of the GGUF MoE layer (kdq_moe_gguf) against the oracle's restatement of
 MoeLayer::forward (IW/src/models/text/qwen_layers.cpp:378-492): the routing (selected
 experts bit-exact, weights to 1e-6) and y within rel-L2 <= 1e-3, max-abs <= 2e-2 of its
-RMS.  Expert projections of Q4_K / Q8_0 / Q4_0 run on the MFMA kernel with the expert
-slice chosen on the device, the other encodings on the exact kernel."""
+RMS.  Expert projections of Q4_K / Q8_0 / Q4_0 / Q6_K run on the MFMA kernel with the
+expert slice chosen on the device, the other encodings on the exact kernel.  The three
+encoding mixes cover each launch form: gate and up stored alike run as one paired launch
+that applies the swiglu (MIXED: experts and shared expert; EXACT: the shared expert),
+gate and up stored differently as two launches and the swiglu kernel (SPLIT), and the
+exact kernel's slot-affine launch (EXACT experts)."""
 import numpy as np
 import pytest
 
@@ -47,10 +51,12 @@ MIXED = {"gate_exps": Q4_K, "up_exps": Q4_K, "down_exps": Q6_K, "gate_shexp": Q8
          "up_shexp": Q8_0, "down_shexp": Q4_K}
 EXACT = {"gate_exps": IQ4_XS, "up_exps": IQ4_XS, "down_exps": Q3_K, "gate_shexp": Q4_0,
          "up_shexp": Q4_0, "down_shexp": Q6_K}
+SPLIT = {"gate_exps": Q4_K, "up_exps": Q8_0, "down_exps": Q4_0, "gate_shexp": Q8_0,
+         "up_shexp": Q4_K, "down_shexp": Q8_0}
 
 
 @pytest.mark.parametrize("rows", [1, 3, 8])
-@pytest.mark.parametrize("encs", [MIXED, EXACT], ids=["mixed", "exact"])
+@pytest.mark.parametrize("encs", [MIXED, EXACT, SPLIT], ids=["mixed", "exact", "split"])
 def test_moe_gguf_parity(device, oracle, rows, encs):
     import torch
     H, E, K, F, S = 512, 16, 4, 256, 512
