@@ -129,6 +129,18 @@ __device__ __forceinline__ int quad_xor2(int v) {
     return __builtin_amdgcn_update_dpp(0, v, 0x4e, 0xf, 0xf, false);
 }
 
+// Maximum over the 64 lanes by DPP (as wave_total), for values >= 0: lanes outside a
+// broadcast's row mask read 0, and fmaxf skips NaN.  Every lane returns it.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+    v = fmaxf(v, dpp_read<0xb1, 0xf>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_read<0x4e, 0xf>(v));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_read<0x141, 0xf>(v));  // row_half_mirror
+    v = fmaxf(v, dpp_read<0x140, 0xf>(v));  // row_mirror
+    v = fmaxf(v, dpp_read<0x142, 0xa>(v));  // row_bcast:15
+    v = fmaxf(v, dpp_read<0x143, 0xc>(v));  // row_bcast:31
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int offset = 32; offset > 0; offset >>= 1)

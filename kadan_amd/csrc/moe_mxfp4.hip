@@ -4,7 +4,7 @@
 // IW/src/weights/quantization.cpp:79-99,207-247, behind include/kadan_amd.h.
 //
 //   route_kernel      one wavefront per token: softmax (float exp, double total),
-//                     top-k by logit (equal logits keep the lower expert), renormalise;
+//                     top-k by probability (equal ones keep the lower expert), renormalise;
 //                     the token's activations as FP8 terms with E8M0 block scales
 //   permute_kernel    one workgroup: stable counting sort of the slots by expert
 //                     (expert-major, slot ascending) plus the list of work items
@@ -72,37 +72,44 @@ __device__ __forceinline__ void route_token(const float* __restrict__ logits, un
     for (int j = 0; j < 4; ++j)
         p[j] = float(double(p[j]) / total);
 
+    // Selection by probability, as the reference's partial sort orders it: the largest p
+    // first, equal p keep the lower expert; and as its scan keeps its first candidate
+    // while nothing compares greater, a NaN p at the lowest untaken expert is taken
+    // there.  Per pick: one DPP maximum and a ballot per register (no LDS round trips).
+    bool valid[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        valid[j] = lane + 64 * j < experts;
     unsigned taken = 0;
     float sum = 0.f, chosen_p = 0.f;
     int chosen_e = 0;
     for (unsigned i = 0; i < top_k; ++i) {
-        float bv = -INFINITY;
-        int be = 0x7fffffff;
+        float c = 0.f;  // every probability that is not NaN is >= 0
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (valid[j] && !((taken >> j) & 1u))
+                c = fmaxf(c, p[j]);
+        c = wave_max_nonneg(c);
+        int e0 = -1, eb = -1;  // lowest untaken expert; lowest one whose p equals c
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int e = int(lane + 64 * j);
-            if (unsigned(e) < experts && !(taken & (1u << j)) && (v[j] > bv || (v[j] == bv && e < be))) {
-                bv = v[j];
-                be = e;
-            }
+            const bool open = valid[j] && !((taken >> j) & 1u);
+            const unsigned long long any = __ballot(open), hit = __ballot(open && p[j] == c);
+            if (e0 < 0 && any)
+                e0 = 64 * j + __builtin_ctzll(any);
+            if (eb < 0 && hit)
+                eb = 64 * j + __builtin_ctzll(hit);
         }
-#pragma unroll
-        for (int offset = 32; offset > 0; offset >>= 1) {
-            const float ov = __shfl_xor(bv, offset, 64);
-            const int oe = __shfl_xor(be, offset, 64);
-            if (ov > bv || (ov == bv && oe < be)) {
-                bv = ov;
-                be = oe;
-            }
-        }
-        const unsigned owner = unsigned(be) % 64, slot = unsigned(be) / 64;
-        if (lane == owner)
-            taken |= 1u << slot;
-        float mine = p[0];
-#pragma unroll
-        for (int j = 1; j < 4; ++j)
-            mine = slot == unsigned(j) ? p[j] : mine;
-        const float pb = __shfl(mine, int(owner), 64);
+        auto p_of = [&](int e) {  // p of expert e (wave-uniform)
+            const int j = e / 64;
+            const float pj = j == 0 ? p[0] : (j == 1 ? p[1] : (j == 2 ? p[2] : p[3]));
+            return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), e % 64));
+        };
+        const float p0 = p_of(e0);
+        const int be = (isnan(p0) || eb < 0) ? e0 : eb;
+        const float pb = be == e0 ? p0 : p_of(be);
+        if (lane == unsigned(be % 64))
+            taken |= 1u << (be / 64);
         sum += pb;  // sequential, in selection order
         if (lane == i) {
             chosen_p = pb;

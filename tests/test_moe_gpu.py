@@ -64,6 +64,24 @@ def test_route_equal_logits_keep_lower_expert(device):
     np.testing.assert_allclose(gw.cpu().numpy()[0], 0.25, rtol=1e-6)
 
 
+def test_route_equal_probabilities_keep_lower_expert(device, oracle):
+    """Logits 0 and 1e-8 both give p = 1 after the float exp (1 - 1e-8 rounds to 1): the
+    reference's partial sort by probability keeps the lower expert first, whatever the
+    logits' order (qwen_layers.cpp:403-425)."""
+    torch = _torch()
+    logits = np.full((3, 16), -5.0, np.float32)
+    logits[0, :2] = [0.0, 1e-8]
+    logits[1, [4, 7]] = [1e-8, 0.0]
+    logits[2, [2, 9, 11]] = [1e-8, 0.0, 1e-8]
+    idx, w = oracle.moe_route(logits, 3)
+    assert list(idx[0][:2]) == [0, 1] and list(idx[1][:2]) == [4, 7]
+    assert list(idx[2]) == [2, 9, 11]
+    from kadan_amd import ops
+    gi, gw, _, _ = ops.moe_route(torch.from_numpy(logits).to(device), 3)
+    assert np.array_equal(gi.cpu().numpy(), idx)
+    assert_close(gw.cpu().numpy(), w, rel=1e-6, mabs=1e-6, what="routing weights")
+
+
 def test_mxfp4_dequantize_bit_exact(device, oracle):
     torch = _torch()
     rows, cols = 64, 256

@@ -503,6 +503,17 @@ def test_route_ties_and_masked_experts(oracle):
     assert w[2].tolist() == [1.0, 0.0, 0.0]
 
 
+def test_route_orders_by_probability_not_logit(oracle):
+    # logits 0 and 1e-8 differ, their float probabilities do not (expf(-1e-8) rounds to
+    # 1): the sort by probability keeps the lower expert first
+    assert np.float32(np.exp(np.float32(-1e-8))) == np.float32(1.0)
+    logits = np.full((1, 8), -5.0, np.float32)
+    logits[0, [2, 5]] = [0.0, 1e-8]
+    logits[0, 6] = 1e-8
+    idx, _ = oracle.moe_route(logits, 3)
+    assert idx.tolist() == [[2, 5, 6]]
+
+
 @pytest.mark.parametrize("tokens,experts,top_k", [(64, 8, 2), (50, 32, 4), (20, 128, 8)])
 def test_route_vs_numpy(oracle, tokens, experts, top_k):
     _, logits = synth.moe_inputs(9 + experts, tokens, 32, experts, hot=4 if experts > 8 else 0)
