@@ -524,6 +524,9 @@ def main():
                   "Q6_K GEMV 4096->14336, batch 1, row-major GGUF bytes (kdq_gemv_batch: "
                   "the MFMA GEMV reading 210-byte super-blocks in place)", packed=False,
                   copies=8)
+        gemv_line("gemv_q6_k_4096x14336_packed", Q6_K, n_in, n_out, 0xF0 + Q6_K, 500,
+                  "Q6_K GEMV 4096->14336, batch 1, tile-packed resident copy (kdq_gguf_pack; "
+                  "what the host layer's bank keeps)", copies=8)
         gemv_line("gemv_q6_k_14336_to_4096", Q6_K, 14336, 4096, 0xF1 + Q6_K, 500,
                   "Q6_K GEMV 14336->4096, batch 1, row-major GGUF bytes (an ffn_down shape)",
                   packed=False, copies=8)

@@ -39,7 +39,7 @@ enum kdq_status {
 /* ---- encodings (GGML type ids; IW/include/kadan/gguf_quantization.hpp:16-55).
  * Every one decodes (kdq_dequantize) and multiplies (kdq_gemv, kdq_gemv_exact,
  * kdq_gemv_batch); Q4_0, Q8_0 and Q4_K also run the streaming / MFMA products and
- * have the tile-packed layout; Q6_K runs the MFMA product over its row-major bytes.  Q4_0 is not a kadan device encoding: it is ggml's
+ * have the tile-packed layout; Q6_K runs the MFMA product (row-major or packed).  Q4_0 is not a kadan device encoding: it is ggml's
  * block_q4_0, added for the prefill GEMM and the products. */
 enum kdq_encoding {
     KDQ_F32 = 0,  /* plain fp32 / fp16 matrices (e.g. GGUF routers): exact product only */
@@ -128,8 +128,9 @@ int kdq_gemv_batch(const kdq_matvec_job* jobs, size_t count, void* stream);
  * that keeps weights resident) reorders them once so every wavefront load of the
  * product is whole 128-byte lines.  The bytes are the same bytes, reordered: tiles of
  * 16 rows (zero rows after the last), per tile and 256-value group one unit of
- * 16 x group bytes (Q4_K 2304, Q4_0 2304, Q8_0 4352) of 1 KB code pieces (lane
- * l = 16*chunk + row%16 at 16*l) followed by the block headers / scales.
+ * 16 x group bytes (Q4_K 2304, Q4_0 2304, Q8_0 4352, Q6_K 3360) of 1 KB code pieces
+ * (lane l = 16*chunk + row%16 at 16*l) followed by the block headers / scales (Q6_K's
+ * high-bit pairs regrouped per lane within the unit).
  *
  * Device bytes of the packed form of `out` rows of `in` values (0 unless in % 256 == 0). */
 size_t kdq_gguf_packed_bytes(int encoding, size_t in, size_t out);

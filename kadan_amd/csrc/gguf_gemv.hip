@@ -840,11 +840,18 @@ __device__ __forceinline__ void mstage_unit(unsigned in, unsigned u, const XUnit
 //     Q4_K  pieces 0, 1: code bytes 0..15, 16..31 of sub-block pair G
 //     Q4_0  piece c: the 16 code bytes of block 2G + c of the group
 //     Q8_0  piece 2c + h: code bytes 16h .. 16h+15 of block 2G + c
+//     Q6_K  pieces 0, 1: ql bytes 32G .. 32G+15, 32G+16 .. 32G+31 (chunk G = 2h + p,
+//           mfma_gemv's Q6_K chunk map); piece 2: the chunk's qh bit pairs, dword m for
+//           positions 8m..8m+7: byte i holds, for position 8m+i in its high nibble and
+//           8m+4+i in its low nibble, (block-0 bits) | (block-1 bits) << 2
 //   side data at pieces * 1024:
 //     Q4_K  the 16-byte block header (d, dmin, scales) of row slot s at + 16 s
 //     Q4_0, Q8_0  one dword at + 4 l: d of block 2G | d of block 2G + 1 << 16
+//     Q6_K  one dword at + 4 l: the chunk's scales 8h+2p, 8h+2p+1, 8h+4+2p, 8h+5+2p;
+//           then at + 256 + 4 (s/2): d of row slots s & ~1 | d of s | 1 << 16
 // A wavefront's load of one piece is 1 KB contiguous; the bytes are the row bytes
-// reordered (unit = 16 rows x one group's bytes), nothing is added or converted.
+// reordered (unit = 16 rows x one group's bytes), nothing is added or converted (Q6_K's
+// qh bit pairs are regrouped within the unit so that no two lanes load the same byte).
 template <int ENC> struct PackedFormat;
 template <> struct PackedFormat<KDQ_Q4_K> {
     static constexpr int pieces = 2, unit = 2304;
@@ -854,6 +861,9 @@ template <> struct PackedFormat<KDQ_Q4_0> {
 };
 template <> struct PackedFormat<KDQ_Q8_0> {
     static constexpr int pieces = 4, unit = 4352;
+};
+template <> struct PackedFormat<KDQ_Q6_K> {
+    static constexpr int pieces = 3, unit = 3360;
 };
 
 // One lane's chunk from a packed unit, in the register image the packed operand
@@ -876,6 +886,8 @@ __device__ __forceinline__ void load_packed(const uint8_t* unit, unsigned G, uns
         L.w[0] = h.x, L.w[1] = h.y, L.w[2] = h.z, L.w[3] = h.w;
     } else {
         L.w[4 * P] = stream4(unit + P * 1024 + 4 * l);
+        if constexpr (ENC == KDQ_Q6_K)
+            L.w[4 * P + 1] = stream4(unit + P * 1024 + 256 + 4 * (s / 2));
     }
 }
 
@@ -883,7 +895,15 @@ __device__ __forceinline__ void load_packed(const uint8_t* unit, unsigned G, uns
 // when PACKED).
 template <int ENC, bool PACKED = false>
 __device__ __forceinline__ i32x4 b_operand(const Lane& L, int m, unsigned q6_shift) {
-    if constexpr (ENC == KDQ_Q6_K) {
+    if constexpr (PACKED && ENC == KDQ_Q6_K) {
+        // the qh pairs of positions 8m+i sit in bits 4-7 of byte i of w[8+m], those of
+        // 8m+4+i in bits 0-3 (block 0 bits low, block 1 bits high in each nibble)
+        const unsigned l0 = L.w[2 * m], l1 = L.w[2 * m + 1], h = L.w[8 + m];
+        return i32x4{int((l0 & 0x0f0f0f0fu) | (h & 0x30303030u)),
+                     int((l1 & 0x0f0f0f0fu) | ((h << 4) & 0x30303030u)),
+                     int(((l0 >> 4) & 0x0f0f0f0fu) | ((h >> 2) & 0x30303030u)),
+                     int(((l1 >> 4) & 0x0f0f0f0fu) | ((h << 2) & 0x30303030u))};
+    } else if constexpr (ENC == KDQ_Q6_K) {
         // the 6-bit codes (0..63) of positions 8m..8m+7: low nibble | qh bits 2p, 2p+1
         // (block 0), high nibble | qh bits 4+2p, 5+2p (block 1); q6_shift = 2p
         const unsigned l0 = L.w[2 * m], l1 = L.w[2 * m + 1];
@@ -943,9 +963,13 @@ __device__ __forceinline__ float chunk_value(const Lane& L, ScaleSel sel, i32x4 
     if constexpr (ENC == KDQ_Q6_K) {
         // c: positions 0..15 of each block, c2: 16..31; sum (q - 32) x_q per 16 values is
         // an exact integer below 2^24 in magnitude, then the int8 scales and d in fp32
-        const float d = half_hw(L.w[18] >> 16);
+        // row-major image: scales 8h..8h+7 in w[16..17], d high in w[18]; packed: the
+        // chunk's four scales in w[12], the d pair of the lane's row slots in w[13]
+        // (sel.high: odd row slot)
+        const float d = PACKED ? half_hw(L.w[13] >> (sel.high ? 16 : 0)) : half_hw(L.w[18] >> 16);
         bad |= !isfinite(d);
-        const unsigned s0 = L.w[16] >> (8 * sel.shift), s1 = L.w[17] >> (8 * sel.shift);
+        const unsigned s0 = PACKED ? L.w[12] : L.w[16] >> (8 * sel.shift);
+        const unsigned s1 = PACKED ? L.w[12] >> 16 : L.w[17] >> (8 * sel.shift);
         const int f0 = __float_as_int(x0.w), f1 = __float_as_int(x1.w);
         const int t0 = __float_as_int(x0.z) - f0, t1 = __float_as_int(x1.z) - f1;
         const float a00 = float(c.x * 256 + c.y - 32 * f0), a01 = float(c2.x * 256 + c2.y - 32 * t0);
@@ -1097,7 +1121,7 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
     // entry, the others a zero region; MFMA m adds m * 256 bytes
     const bool carrier = j / 4 == G;
     // Q4_K: the scale bytes of sub-blocks 2G, 2G+1; Q6_K: 2p for chunk G = 2h + p
-    const ScaleSel sel = ENC == KDQ_Q6_K ? ScaleSel{2 * (G % 2), false}
+    const ScaleSel sel = ENC == KDQ_Q6_K ? ScaleSel{2 * (G % 2), (j & 1) != 0}
                                          : ScaleSel{8 * ((2 * G) & 3), G >= 2};
     // every argument in one round of scalar loads, then the exit test
     asm volatile("" ::"s"(weights), "s"(up), "s"(x), "s"(y), "s"(status), "s"(row_bytes),
@@ -1473,10 +1497,8 @@ int launch_mfma_any(int encoding, const void* w, size_t row_bytes, const float* 
         return launch_mfma<KDQ_Q4_0, PACKED>(w, row_bytes, x, rows, in, out, y, stride, status, s);
     case KDQ_Q4_K:
         return launch_mfma<KDQ_Q4_K, PACKED>(w, row_bytes, x, rows, in, out, y, stride, status, s);
-    case KDQ_Q6_K:  // row-major only: the packed layout has no Q6_K unit
-        if constexpr (!PACKED)
-            return launch_mfma<KDQ_Q6_K, false>(w, row_bytes, x, rows, in, out, y, stride, status, s);
-        return KDQ_ERR_UNSUPPORTED;
+    case KDQ_Q6_K:
+        return launch_mfma<KDQ_Q6_K, PACKED>(w, row_bytes, x, rows, in, out, y, stride, status, s);
     default:
         return KDQ_ERR_UNSUPPORTED;
     }
@@ -1492,6 +1514,8 @@ size_t packed_unit(int encoding) {
         return PackedFormat<KDQ_Q4_0>::unit;
     case KDQ_Q8_0:
         return PackedFormat<KDQ_Q8_0>::unit;
+    case KDQ_Q6_K:
+        return PackedFormat<KDQ_Q6_K>::unit;
     default:
         return 0;
     }
@@ -1533,6 +1557,33 @@ __global__ __launch_bounds__(256) void pack_kernel(const uint8_t* __restrict__ r
                 live ? bytes16(block + 16 + 32 * G + 16 * p) : zero;
         if (G == 0)
             *reinterpret_cast<uint4*>(unit + P * 1024 + 16 * s) = live ? bytes16(block) : zero;
+    } else if constexpr (ENC == KDQ_Q6_K) {
+        const uint8_t* block = row + size_t(g) * 210;
+        const unsigned h = G / 2, p = G % 2;
+        *reinterpret_cast<uint4*>(unit + 16 * l) = live ? bytes16(block + 32 * G) : zero;
+        *reinterpret_cast<uint4*>(unit + 1024 + 16 * l) = live ? bytes16(block + 32 * G + 16) : zero;
+        // qh pairs of position t: block 0 bits 2p, 2p+1 and block 1 bits 4+2p, 5+2p of
+        // qh[32h + t], as one nibble
+        auto pairs = [&](unsigned t) {
+            const unsigned q = block[128 + 32 * h + t];
+            return ((q >> (2 * p)) & 3u) | (((q >> (4 + 2 * p)) & 3u) << 2);
+        };
+        uint4 x = zero;
+        unsigned* xw = &x.x;
+        if (live)
+            for (unsigned m = 0; m < 4; ++m)
+                for (unsigned i = 0; i < 4; ++i)
+                    xw[m] |= ((pairs(8 * m + i) << 4) | pairs(8 * m + 4 + i)) << (8 * i);
+        *reinterpret_cast<uint4*>(unit + 2048 + 16 * l) = x;
+        const uint8_t* sc = block + 192 + 8 * h + 2 * p;
+        *reinterpret_cast<unsigned*>(unit + 3072 + 4 * l) =
+            live ? unsigned(sc[0]) | unsigned(sc[1]) << 8 | unsigned(sc[4]) << 16 |
+                       unsigned(sc[5]) << 24
+                 : 0u;
+        if (G == 0) {  // this row slot's d, in the dword of its pair of slots
+            const unsigned dh = live ? half_bits_at(block + 208) : 0u;
+            reinterpret_cast<uint16_t*>(unit + 3328)[s] = uint16_t(dh);
+        }
     } else {
         constexpr int bytes = Format<ENC>::bytes;
         const uint8_t* b0 = row + (size_t(g) * 8 + 2 * G) * bytes;
@@ -1747,6 +1798,8 @@ extern "C" int kdq_gguf_pack(int encoding, const void* weights, size_t row_bytes
         return launch_pack<KDQ_Q4_0>(weights, row_bytes, in, out, packed, s);
     case KDQ_Q4_K:
         return launch_pack<KDQ_Q4_K>(weights, row_bytes, in, out, packed, s);
+    case KDQ_Q6_K:
+        return launch_pack<KDQ_Q6_K>(weights, row_bytes, in, out, packed, s);
     default:
         return KDQ_ERR_UNSUPPORTED;
     }
@@ -1835,9 +1888,7 @@ int launch_fused(const kdq_matvec_job* jobs, const size_t* idx, size_t n, hipStr
     case KDQ_Q4_K:
         return launch_mfma_rows<KDQ_Q4_K, PACKED>(j0.rows, p.waves, mj, stream);
     case KDQ_Q6_K:
-        if constexpr (!PACKED)
-            return launch_mfma_rows<KDQ_Q6_K, false>(j0.rows, p.waves, mj, stream);
-        return KDQ_ERR_UNSUPPORTED;
+        return launch_mfma_rows<KDQ_Q6_K, PACKED>(j0.rows, p.waves, mj, stream);
     default:
         return KDQ_ERR_UNSUPPORTED;
     }

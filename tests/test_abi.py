@@ -132,6 +132,8 @@ def test_gguf_packed_geometry_and_argument_errors():
     assert lib.kdq_gguf_packed_bytes(12, 256, 17) == 2 * 2304
     assert lib.kdq_gguf_packed_bytes(8, 512, 16) == 2 * 4352
     assert lib.kdq_gguf_packed_bytes(2, 512, 1) == 2 * 2304
+    assert lib.kdq_gguf_packed_bytes(14, 4096, 14336) == 14336 * 16 * 210  # Q6_K
+    assert lib.kdq_gguf_packed_bytes(14, 768, 17) == 2 * 3 * 3360
     assert lib.kdq_gguf_packed_bytes(2, 96, 16) == 0
     assert lib.kdq_gguf_packed_bytes(3, 256, 16) == 0
     pack = lib.kdq_gguf_pack

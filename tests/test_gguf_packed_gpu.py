@@ -15,18 +15,23 @@ from tests.util import assert_close, bits_equal
 
 pytestmark = pytest.mark.gpu
 
-Q4_0, Q8_0, Q4_K = 2, 8, 12
-ENCODINGS = [Q8_0, Q4_0, Q4_K]
-BLOCK = {Q4_0: 18, Q8_0: 34, Q4_K: 144}
-UNIT = {Q4_K: 2304, Q4_0: 2304, Q8_0: 4352}
-PIECES = {Q4_K: 2, Q4_0: 2, Q8_0: 4}
+Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
+ENCODINGS = [Q8_0, Q4_0, Q4_K, Q6_K]
+BLOCK = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210}
+UNIT = {Q4_K: 2304, Q4_0: 2304, Q8_0: 4352, Q6_K: 3360}
+PIECES = {Q4_K: 2, Q4_0: 2, Q8_0: 4, Q6_K: 3}
+SCALE_AT = {Q4_K: 0, Q4_0: 0, Q8_0: 0, Q6_K: 208}  # first fp16 block scale
 
 
 def numpy_pack(encoding, w, n_in):
     """Restates the packed layout: tiles of 16 rows, per (tile, 256-value group) one unit;
     lane l = 16 G + s (chunk G, row slot s) owns the 16-byte code pieces at p*1024 + 16 l,
     then the side data (Q4_K: row slot s's 16-byte header at 2048 + 16 s; Q4_0 / Q8_0: the
-    two block scales of chunk G as one dword at pieces*1024 + 4 l)."""
+    two block scales of chunk G as one dword at pieces*1024 + 4 l).  Q6_K: chunk G = 2h + p
+    takes ql bytes 32G..32G+31 (pieces 0, 1); piece 2 holds its qh bit pairs, byte 4m + i
+    = pairs(8m + i) << 4 | pairs(8m + 4 + i) with pairs(t) = qh[32h+t] bits 2p..2p+1 |
+    bits 4+2p..5+2p << 2; side: scales 8h+2p, 8h+2p+1, 8h+4+2p, 8h+5+2p as one dword at
+    3072 + 4 l, and row slot s's d at 3328 + 2 s."""
     n_out = w.shape[0]
     groups, tiles = n_in // 256, (n_out + 15) // 16
     rows = np.zeros((tiles * 16, w.shape[1]), np.uint8)
@@ -39,7 +44,21 @@ def numpy_pack(encoding, w, n_in):
             for lane in range(64):
                 G, s = lane // 16, lane % 16
                 row = rows[16 * t + s]
-                if encoding == Q4_K:
+                if encoding == Q6_K:
+                    block = row[210 * g:210 * (g + 1)].astype(np.uint32)
+                    h, p = G // 2, G % 2
+                    u[16 * lane:16 * lane + 16] = block[32 * G:32 * G + 16]
+                    u[1024 + 16 * lane:1024 + 16 * lane + 16] = block[32 * G + 16:32 * G + 32]
+                    qh = block[128 + 32 * h:160 + 32 * h]
+                    pairs = ((qh >> (2 * p)) & 3) | (((qh >> (4 + 2 * p)) & 3) << 2)
+                    for m in range(4):
+                        for i in range(4):
+                            u[2048 + 16 * lane + 4 * m + i] = \
+                                (pairs[8 * m + i] << 4) | pairs[8 * m + 4 + i]
+                    sc = 192 + 8 * h + 2 * p
+                    u[3072 + 4 * lane:3076 + 4 * lane] = block[[sc, sc + 1, sc + 4, sc + 5]]
+                    u[3328 + 2 * s:3330 + 2 * s] = block[208:210]
+                elif encoding == Q4_K:
                     block = row[144 * g:144 * (g + 1)]
                     for p in range(2):
                         u[p * 1024 + 16 * lane:p * 1024 + 16 * lane + 16] = \
@@ -128,7 +147,8 @@ def test_gemv_packed_nonfinite_scale(device, encoding):
                     x, n_out, status=st)
     assert int(st.item()) == 0
     bad = w.copy()
-    bad[20, 0], bad[20, 1] = 0x00, 0x7C  # +inf scale in the last row's first block
+    at = SCALE_AT[encoding]
+    bad[20, at], bad[20, at + 1] = 0x00, 0x7C  # +inf scale in the last row's first block
     st.zero_()
     y = ops.gemv_packed(encoding, ops.gguf_pack(encoding, torch.from_numpy(bad).to(device), n_in),
                         x, n_out, status=st)
