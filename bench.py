@@ -530,7 +530,10 @@ def main():
         gemv_line("gemv_q6_k_14336_to_4096", Q6_K, 14336, 4096, 0xF1 + Q6_K, 500,
                   "Q6_K GEMV 14336->4096, batch 1, row-major GGUF bytes (an ffn_down shape)",
                   packed=False, copies=8)
-        for enc, tag in ((Q3_K, "q3_k"), (IQ4_XS, "iq4_xs"), (IQ3_XXS, "iq3_xxs"),
+        gemv_line("gemv_iq4_xs_4096x14336", IQ4_XS, n_in, n_out, 0xF0 + IQ4_XS, 500,
+                  "IQ4_XS GEMV 4096->14336, batch 1, row-major GGUF bytes (kdq_gemv_batch: "
+                  "the MFMA GEMV, grid values looked up with v_perm)", packed=False, copies=8)
+        for enc, tag in ((Q3_K, "q3_k"), (IQ3_XXS, "iq3_xxs"),
                          (IQ2_S, "iq2_s"), (BF16, "bf16")):
             gemv_line(f"gemv_{tag}_4096x14336_exact", enc, n_in, n_out, 0xF0 + enc, 50,
                       f"{tag.upper()} GEMV 4096->14336, batch 1, row-major bytes (exact-decode "

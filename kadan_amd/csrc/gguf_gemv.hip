@@ -466,6 +466,20 @@ __device__ __forceinline__ void load_lane(const uint8_t* row, unsigned slot, Lan
     }
 }
 
+// IQ4_XS (136-byte super-block: d, scales_h, scales_l[4], qs[128]; G/src/ggml-common.h
+// block_iq4_xs): chunk G is blocks 2G, 2G+1, whose indices lie as Q4_0's codes (16 bytes
+// a block, positions 0..15 low nibbles, 16..31 high).  Image: w[0..3], w[4..7] = the two
+// blocks' 16 index bytes, w[8] = d | scales_h << 16, w[9] = scales_l.
+__device__ __forceinline__ void load_lane_iq4xs(const uint8_t* row, unsigned group, unsigned G,
+                                                Lane& L) {
+    const uint8_t* block = row + size_t(group) * 136;
+    const u32x4 a = load16(block + 8 + 32 * G), b = load16(block + 24 + 32 * G);
+    const uint2 h = *reinterpret_cast<const uint2*>(block);
+    L.w[0] = a.x, L.w[1] = a.y, L.w[2] = a.z, L.w[3] = a.w;
+    L.w[4] = b.x, L.w[5] = b.y, L.w[6] = b.z, L.w[7] = b.w;
+    L.w[8] = h.x, L.w[9] = h.y;
+}
+
 // Q6_K (210-byte super-block: ql[128] low nibbles, qh[64] high bit pairs, 16 int8
 // scales, f16 d; G/src/ggml-common.h block_q6_K).  MFMA chunk G = 2h + p of super-block
 // `group` takes both nibbles of ql[32G .. 32G+31]: its block 0 is super-block positions
@@ -903,6 +917,20 @@ __device__ __forceinline__ i32x4 b_operand(const Lane& L, int m, unsigned q6_shi
                      int((l1 & 0x0f0f0f0fu) | ((h << 4) & 0x30303030u)),
                      int(((l0 >> 4) & 0x0f0f0f0fu) | ((h >> 2) & 0x30303030u)),
                      int(((l1 >> 4) & 0x0f0f0f0fu) | ((h << 2) & 0x30303030u))};
+    } else if constexpr (ENC == KDQ_IQ4_XS) {
+        // the grid values (int8) of the indices of positions 8m..8m+7 of both blocks:
+        // v_perm looks up indices 0-7 and 8-15 in the grid's four words, a third v_perm
+        // keeps per byte the one its index's bit 3 names
+        const int k = 2 * (m % 2);
+        const unsigned shift = m >= 2 ? 4 : 0;
+        auto grid = [](unsigned n) {
+            const unsigned sel = n & 0x07070707u;
+            const unsigned lo = __builtin_amdgcn_perm(0xf6eaddcfu, 0xbfad9881u, sel);
+            const unsigned hi = __builtin_amdgcn_perm(0x71594535u, 0x26190d01u, sel);
+            return __builtin_amdgcn_perm(hi, lo, 0x03020100u | ((n >> 1) & 0x04040404u));
+        };
+        return i32x4{int(grid(L.w[k] >> shift)), int(grid(L.w[k + 1] >> shift)),
+                     int(grid(L.w[4 + k] >> shift)), int(grid(L.w[5 + k] >> shift))};
     } else if constexpr (ENC == KDQ_Q6_K) {
         // the 6-bit codes (0..63) of positions 8m..8m+7: low nibble | qh bits 2p, 2p+1
         // (block 0), high nibble | qh bits 4+2p, 5+2p (block 1); q6_shift = 2p
@@ -960,7 +988,17 @@ struct ScaleSel {
 template <int ENC, bool PACKED = false>
 __device__ __forceinline__ float chunk_value(const Lane& L, ScaleSel sel, i32x4 c, i32x4 c2,
                                              float4 x0, float4 x1, bool& bad) {
-    if constexpr (ENC == KDQ_Q6_K) {
+    if constexpr (ENC == KDQ_IQ4_XS) {
+        // block scales d * (ls - 32), ls = 4 bits of scales_l | 2 bits of scales_h << 4
+        // (sel.shift = G: blocks 2G, 2G+1)
+        const float d = half_hw(L.w[8] & 0xffffu);
+        bad |= !isfinite(d);
+        const unsigned G = sel.shift, sl = L.w[9] >> (8 * G), sh = L.w[8] >> (16 + 4 * G);
+        const int ls0 = int((sl & 15u) | ((sh & 3u) << 4)) - 32;
+        const int ls1 = int(((sl >> 4) & 15u) | (((sh >> 2) & 3u) << 4)) - 32;
+        const float A0 = float(c.x * 256 + c.y), A1 = float(c.z * 256 + c.w);
+        return fmaf(d * float(ls1) * x1.x, A1, d * float(ls0) * x0.x * A0);
+    } else if constexpr (ENC == KDQ_Q6_K) {
         // c: positions 0..15 of each block, c2: 16..31; sum (q - 32) x_q per 16 values is
         // an exact integer below 2^24 in magnitude, then the int8 scales and d in fp32
         // row-major image: scales 8h..8h+7 in w[16..17], d high in w[18]; packed: the
@@ -1121,8 +1159,9 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
     // entry, the others a zero region; MFMA m adds m * 256 bytes
     const bool carrier = j / 4 == G;
     // Q4_K: the scale bytes of sub-blocks 2G, 2G+1; Q6_K: 2p for chunk G = 2h + p
-    const ScaleSel sel = ENC == KDQ_Q6_K ? ScaleSel{2 * (G % 2), (j & 1) != 0}
-                                         : ScaleSel{8 * ((2 * G) & 3), G >= 2};
+    const ScaleSel sel = ENC == KDQ_Q6_K     ? ScaleSel{2 * (G % 2), (j & 1) != 0}
+                         : ENC == KDQ_IQ4_XS ? ScaleSel{G, false}
+                                             : ScaleSel{8 * ((2 * G) & 3), G >= 2};
     // every argument in one round of scalar loads, then the exit test
     asm volatile("" ::"s"(weights), "s"(up), "s"(x), "s"(y), "s"(status), "s"(row_bytes),
                  "s"(stride), "s"(in), "s"(out), "s"(rows_per_wg));
@@ -1150,6 +1189,8 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
                                  G, n % 16, L[k]);
             else if constexpr (ENC == KDQ_Q6_K)
                 load_lane_q6k(w + size_t(n) * row_bytes, g, G, L[k]);
+            else if constexpr (ENC == KDQ_IQ4_XS)
+                load_lane_iq4xs(w + size_t(n) * row_bytes, g, G, L[k]);
             else
                 load_lane<ENC>(w + size_t(n) * row_bytes, 4 * g + G, L[k]);
             cur.next(tiles * mats, W);
@@ -1499,6 +1540,11 @@ int launch_mfma_any(int encoding, const void* w, size_t row_bytes, const float* 
         return launch_mfma<KDQ_Q4_K, PACKED>(w, row_bytes, x, rows, in, out, y, stride, status, s);
     case KDQ_Q6_K:
         return launch_mfma<KDQ_Q6_K, PACKED>(w, row_bytes, x, rows, in, out, y, stride, status, s);
+    case KDQ_IQ4_XS:  // row-major only: no packed unit
+        if constexpr (!PACKED)
+            return launch_mfma<KDQ_IQ4_XS, false>(w, row_bytes, x, rows, in, out, y, stride,
+                                                  status, s);
+        return KDQ_ERR_UNSUPPORTED;
     default:
         return KDQ_ERR_UNSUPPORTED;
     }
@@ -1657,7 +1703,7 @@ int with_encoding(int encoding, F&& f) {
 // layout: Q8_0, Q4_0, Q4_K).
 bool streamed_encoding(int encoding) {
     return encoding == KDQ_Q8_0 || encoding == KDQ_Q4_0 || encoding == KDQ_Q4_K ||
-           encoding == KDQ_Q6_K;
+           encoding == KDQ_Q6_K || encoding == KDQ_IQ4_XS;
 }
 
 // The streaming kernels need whole 64-value lane slots, 4-byte aligned rows and packed
@@ -1666,6 +1712,8 @@ bool streamed_encoding(int encoding) {
 bool streams(int encoding, const void* weights, size_t row_bytes, size_t in) {
     if (encoding == KDQ_Q6_K)
         return in % 256 == 0 && row_bytes % 2 == 0 && aligned(weights, 2);
+    if (encoding == KDQ_IQ4_XS)  // 136-byte super-blocks: 8-byte aligned rows
+        return in % 256 == 0 && row_bytes % 8 == 0 && aligned(weights, 8);
     return streamed_encoding(encoding) && in % 256 == 0 && row_bytes % 4 == 0 &&
            aligned(weights, 4) &&
            (encoding != KDQ_Q4_K || (row_bytes % 16 == 0 && aligned(weights, 16)));
@@ -1889,6 +1937,10 @@ int launch_fused(const kdq_matvec_job* jobs, const size_t* idx, size_t n, hipStr
         return launch_mfma_rows<KDQ_Q4_K, PACKED>(j0.rows, p.waves, mj, stream);
     case KDQ_Q6_K:
         return launch_mfma_rows<KDQ_Q6_K, PACKED>(j0.rows, p.waves, mj, stream);
+    case KDQ_IQ4_XS:
+        if constexpr (!PACKED)
+            return launch_mfma_rows<KDQ_IQ4_XS, false>(j0.rows, p.waves, mj, stream);
+        return KDQ_ERR_UNSUPPORTED;
     default:
         return KDQ_ERR_UNSUPPORTED;
     }
@@ -1983,6 +2035,8 @@ int indexed_gemv_affine(const IndexedJob& first, unsigned count, size_t x_step,
             return launch_mfma_rows<KDQ_Q4_K, false>(j.rows, p.waves, mj, s);
         case KDQ_Q6_K:
             return launch_mfma_rows<KDQ_Q6_K, false>(j.rows, p.waves, mj, s);
+        case KDQ_IQ4_XS:
+            return launch_mfma_rows<KDQ_IQ4_XS, false>(j.rows, p.waves, mj, s);
         default:
             return KDQ_ERR_UNSUPPORTED;
         }
