@@ -533,6 +533,10 @@ def main():
         gemv_line("gemv_iq4_xs_4096x14336", IQ4_XS, n_in, n_out, 0xF0 + IQ4_XS, 500,
                   "IQ4_XS GEMV 4096->14336, batch 1, row-major GGUF bytes (kdq_gemv_batch: "
                   "the MFMA GEMV, grid values looked up with v_perm)", packed=False, copies=8)
+        gemv_line("gemv_iq4_nl_4096x14336", IQ4_NL, n_in, n_out, 0xF0 + IQ4_NL, 500,
+                  "IQ4_NL GEMV 4096->14336, batch 1, row-major GGUF bytes (kdq_gemv_batch: "
+                  "the MFMA GEMV, Q4_0's block layout with grid values)", packed=False,
+                  copies=8)
         for enc, tag in ((Q3_K, "q3_k"), (IQ3_XXS, "iq3_xxs"),
                          (IQ2_S, "iq2_s"), (BF16, "bf16")):
             gemv_line(f"gemv_{tag}_4096x14336_exact", enc, n_in, n_out, 0xF0 + enc, 50,

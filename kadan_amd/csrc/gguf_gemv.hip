@@ -480,6 +480,16 @@ __device__ __forceinline__ void load_lane_iq4xs(const uint8_t* row, unsigned gro
     L.w[8] = h.x, L.w[9] = h.y;
 }
 
+// Four IQ4 indices (bits 0-3 of each byte of n; bits 4-7 ignored) -> their int8 grid
+// values: v_perm looks up indices 0-7 and 8-15 in the grid's four words, a third v_perm
+// keeps per byte the one its index's bit 3 names.
+__device__ __forceinline__ unsigned iq4_grid4(unsigned n) {
+    const unsigned sel = n & 0x07070707u;
+    const unsigned lo = __builtin_amdgcn_perm(0xf6eaddcfu, 0xbfad9881u, sel);
+    const unsigned hi = __builtin_amdgcn_perm(0x71594535u, 0x26190d01u, sel);
+    return __builtin_amdgcn_perm(hi, lo, 0x03020100u | ((n >> 1) & 0x04040404u));
+}
+
 // Q6_K (210-byte super-block: ql[128] low nibbles, qh[64] high bit pairs, 16 int8
 // scales, f16 d; G/src/ggml-common.h block_q6_K).  MFMA chunk G = 2h + p of super-block
 // `group` takes both nibbles of ql[32G .. 32G+31]: its block 0 is super-block positions
@@ -918,19 +928,19 @@ __device__ __forceinline__ i32x4 b_operand(const Lane& L, int m, unsigned q6_shi
                      int(((l0 >> 4) & 0x0f0f0f0fu) | ((h >> 2) & 0x30303030u)),
                      int(((l1 >> 4) & 0x0f0f0f0fu) | ((h << 2) & 0x30303030u))};
     } else if constexpr (ENC == KDQ_IQ4_XS) {
-        // the grid values (int8) of the indices of positions 8m..8m+7 of both blocks:
-        // v_perm looks up indices 0-7 and 8-15 in the grid's four words, a third v_perm
-        // keeps per byte the one its index's bit 3 names
+        // the grid values (int8) of the indices of positions 8m..8m+7 of both blocks
         const int k = 2 * (m % 2);
         const unsigned shift = m >= 2 ? 4 : 0;
-        auto grid = [](unsigned n) {
-            const unsigned sel = n & 0x07070707u;
-            const unsigned lo = __builtin_amdgcn_perm(0xf6eaddcfu, 0xbfad9881u, sel);
-            const unsigned hi = __builtin_amdgcn_perm(0x71594535u, 0x26190d01u, sel);
-            return __builtin_amdgcn_perm(hi, lo, 0x03020100u | ((n >> 1) & 0x04040404u));
-        };
-        return i32x4{int(grid(L.w[k] >> shift)), int(grid(L.w[k + 1] >> shift)),
-                     int(grid(L.w[4 + k] >> shift)), int(grid(L.w[5 + k] >> shift))};
+        return i32x4{int(iq4_grid4(L.w[k] >> shift)), int(iq4_grid4(L.w[k + 1] >> shift)),
+                     int(iq4_grid4(L.w[4 + k] >> shift)), int(iq4_grid4(L.w[5 + k] >> shift))};
+    } else if constexpr (ENC == KDQ_IQ4_NL) {
+        // Q4_0's row-major image (18-byte blocks: d, 16 index bytes), grid values
+        const int k = 2 * (m % 2);
+        const unsigned shift = m >= 2 ? 4 : 0;
+        const unsigned a0 = __builtin_amdgcn_alignbyte(L.w[k + 1], L.w[k], 2);
+        const unsigned a1 = __builtin_amdgcn_alignbyte(L.w[k + 2], L.w[k + 1], 2);
+        return i32x4{int(iq4_grid4(a0 >> shift)), int(iq4_grid4(a1 >> shift)),
+                     int(iq4_grid4(L.w[5 + k] >> shift)), int(iq4_grid4(L.w[6 + k] >> shift))};
     } else if constexpr (ENC == KDQ_Q6_K) {
         // the 6-bit codes (0..63) of positions 8m..8m+7: low nibble | qh bits 2p, 2p+1
         // (block 0), high nibble | qh bits 4+2p, 5+2p (block 1); q6_shift = 2p
@@ -988,7 +998,12 @@ struct ScaleSel {
 template <int ENC, bool PACKED = false>
 __device__ __forceinline__ float chunk_value(const Lane& L, ScaleSel sel, i32x4 c, i32x4 c2,
                                              float4 x0, float4 x1, bool& bad) {
-    if constexpr (ENC == KDQ_IQ4_XS) {
+    if constexpr (ENC == KDQ_IQ4_NL) {
+        const float d0 = half_hw(L.w[0] & 0xffffu), d1 = half_hw(L.w[4] >> 16);
+        bad |= !isfinite(d0) || !isfinite(d1);
+        const float A0 = float(c.x * 256 + c.y), A1 = float(c.z * 256 + c.w);
+        return fmaf(d1 * x1.x, A1, d0 * x0.x * A0);
+    } else if constexpr (ENC == KDQ_IQ4_XS) {
         // block scales d * (ls - 32), ls = 4 bits of scales_l | 2 bits of scales_h << 4
         // (sel.shift = G: blocks 2G, 2G+1)
         const float d = half_hw(L.w[8] & 0xffffu);
@@ -1191,6 +1206,8 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
                 load_lane_q6k(w + size_t(n) * row_bytes, g, G, L[k]);
             else if constexpr (ENC == KDQ_IQ4_XS)
                 load_lane_iq4xs(w + size_t(n) * row_bytes, g, G, L[k]);
+            else if constexpr (ENC == KDQ_IQ4_NL)  // Q4_0's block size and layout
+                load_lane<KDQ_Q4_0>(w + size_t(n) * row_bytes, 4 * g + G, L[k]);
             else
                 load_lane<ENC>(w + size_t(n) * row_bytes, 4 * g + G, L[k]);
             cur.next(tiles * mats, W);
@@ -1545,6 +1562,11 @@ int launch_mfma_any(int encoding, const void* w, size_t row_bytes, const float* 
             return launch_mfma<KDQ_IQ4_XS, false>(w, row_bytes, x, rows, in, out, y, stride,
                                                   status, s);
         return KDQ_ERR_UNSUPPORTED;
+    case KDQ_IQ4_NL:
+        if constexpr (!PACKED)
+            return launch_mfma<KDQ_IQ4_NL, false>(w, row_bytes, x, rows, in, out, y, stride,
+                                                  status, s);
+        return KDQ_ERR_UNSUPPORTED;
     default:
         return KDQ_ERR_UNSUPPORTED;
     }
@@ -1703,7 +1725,7 @@ int with_encoding(int encoding, F&& f) {
 // layout: Q8_0, Q4_0, Q4_K).
 bool streamed_encoding(int encoding) {
     return encoding == KDQ_Q8_0 || encoding == KDQ_Q4_0 || encoding == KDQ_Q4_K ||
-           encoding == KDQ_Q6_K || encoding == KDQ_IQ4_XS;
+           encoding == KDQ_Q6_K || encoding == KDQ_IQ4_XS || encoding == KDQ_IQ4_NL;
 }
 
 // The streaming kernels need whole 64-value lane slots, 4-byte aligned rows and packed
@@ -1941,6 +1963,10 @@ int launch_fused(const kdq_matvec_job* jobs, const size_t* idx, size_t n, hipStr
         if constexpr (!PACKED)
             return launch_mfma_rows<KDQ_IQ4_XS, false>(j0.rows, p.waves, mj, stream);
         return KDQ_ERR_UNSUPPORTED;
+    case KDQ_IQ4_NL:
+        if constexpr (!PACKED)
+            return launch_mfma_rows<KDQ_IQ4_NL, false>(j0.rows, p.waves, mj, stream);
+        return KDQ_ERR_UNSUPPORTED;
     default:
         return KDQ_ERR_UNSUPPORTED;
     }
@@ -2037,6 +2063,8 @@ int indexed_gemv_affine(const IndexedJob& first, unsigned count, size_t x_step,
             return launch_mfma_rows<KDQ_Q6_K, false>(j.rows, p.waves, mj, s);
         case KDQ_IQ4_XS:
             return launch_mfma_rows<KDQ_IQ4_XS, false>(j.rows, p.waves, mj, s);
+        case KDQ_IQ4_NL:
+            return launch_mfma_rows<KDQ_IQ4_NL, false>(j.rows, p.waves, mj, s);
         default:
             return KDQ_ERR_UNSUPPORTED;
         }
