@@ -537,7 +537,11 @@ def main():
                   "IQ4_NL GEMV 4096->14336, batch 1, row-major GGUF bytes (kdq_gemv_batch: "
                   "the MFMA GEMV, Q4_0's block layout with grid values)", packed=False,
                   copies=8)
-        for enc, tag in ((Q3_K, "q3_k"), (IQ3_XXS, "iq3_xxs"),
+        gemv_line("gemv_q3_k_4096x14336", Q3_K, n_in, n_out, 0xF0 + Q3_K, 500,
+                  "Q3_K GEMV 4096->14336, batch 1, row-major GGUF bytes (kdq_gemv_batch: "
+                  "the MFMA GEMV reading 110-byte super-blocks in place)", packed=False,
+                  copies=8)
+        for enc, tag in ((IQ3_XXS, "iq3_xxs"),
                          (IQ2_S, "iq2_s"), (BF16, "bf16")):
             gemv_line(f"gemv_{tag}_4096x14336_exact", enc, n_in, n_out, 0xF0 + enc, 50,
                       f"{tag.upper()} GEMV 4096->14336, batch 1, row-major bytes (exact-decode "

@@ -39,8 +39,8 @@ enum kdq_status {
 /* ---- encodings (GGML type ids; IW/include/kadan/gguf_quantization.hpp:16-55).
  * Every one decodes (kdq_dequantize) and multiplies (kdq_gemv, kdq_gemv_exact,
  * kdq_gemv_batch); Q4_0, Q8_0 and Q4_K also run the streaming / MFMA products and
- * have the tile-packed layout; Q6_K runs the MFMA product (row-major or packed), IQ4_XS
- * and IQ4_NL the MFMA product over their row-major bytes.  Q4_0 is not a kadan device encoding: it is ggml's
+ * have the tile-packed layout; Q6_K runs the MFMA product (row-major or packed), IQ4_XS,
+ * IQ4_NL and Q3_K the MFMA product over their row-major bytes.  Q4_0 is not a kadan device encoding: it is ggml's
  * block_q4_0, added for the prefill GEMM and the products. */
 enum kdq_encoding {
     KDQ_F32 = 0,  /* plain fp32 / fp16 matrices (e.g. GGUF routers): exact product only */
@@ -88,7 +88,8 @@ int kdq_dequantize(int encoding, const void* packed, size_t row_bytes, size_t ro
  * rows: 1..4096 (more than one pass when needed; gguf_batch_max_rows,
  * IW/include/kadan/dense_compute.hpp:201).  fp32 accumulation.  Q4_0 / Q8_0 / Q4_K
  * (in % 256 == 0, 4-byte aligned rows), Q6_K (in % 256 == 0, 2-byte aligned rows),
- * IQ4_XS (8-byte aligned rows) and IQ4_NL (4-byte aligned rows):
+ * IQ4_XS (8-byte aligned rows), IQ4_NL (4-byte aligned rows) and Q3_K (2-byte aligned
+ * rows):
  * the activation operand is carried as 16-bit
  * block fixed point per 32 values (relative error below 2^-15 of the block maximum),
  * products exact in int32; every other shape and encoding runs kdq_gemv_exact.

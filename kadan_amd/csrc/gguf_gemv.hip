@@ -480,6 +480,29 @@ __device__ __forceinline__ void load_lane_iq4xs(const uint8_t* row, unsigned gro
     L.w[8] = h.x, L.w[9] = h.y;
 }
 
+// Q3_K (110-byte super-block: hmask[32], qs[64], 12 packed 6-bit scales, f16 d;
+// G/src/ggml-common.h block_q3_K).  Position 128n + 32j + l holds 2-bit field j of
+// qs[32n + l] and bit 4n + j of hmask[l], scale 8n + 2j + l/16.  MFMA chunk G = 2n + p
+// takes fields j = 2p (block 0) and 2p + 1 (block 1), scales 4G .. 4G+3.  Image:
+// w[0..7] = qs[32n .. 32n+31], w[8..15] = hmask, w[16] = scale bytes 4p .. 4p+3 (low
+// nibbles of scales 4G.. when n = 0, high nibbles when n = 1), w[17] = scale bytes 8..11
+// (the high bit pairs), w[18] = bytes 106..109 (d in the high half; a load ending inside
+// the block).
+__device__ __forceinline__ void load_lane_q3k(const uint8_t* row, unsigned group, unsigned G,
+                                              Lane& L) {
+    const uint8_t* block = row + size_t(group) * 110;
+    const unsigned n = G / 2, p = G % 2;
+    const u32x4 a = load16_a2(block + 32 + 32 * n), b = load16_a2(block + 48 + 32 * n);
+    const u32x4 c = load16_a2(block), d = load16_a2(block + 16);
+    L.w[0] = a.x, L.w[1] = a.y, L.w[2] = a.z, L.w[3] = a.w;
+    L.w[4] = b.x, L.w[5] = b.y, L.w[6] = b.z, L.w[7] = b.w;
+    L.w[8] = c.x, L.w[9] = c.y, L.w[10] = c.z, L.w[11] = c.w;
+    L.w[12] = d.x, L.w[13] = d.y, L.w[14] = d.z, L.w[15] = d.w;
+    L.w[16] = load4_a2(block + 96 + 4 * p);
+    L.w[17] = load4_a2(block + 104);
+    L.w[18] = load4_a2(block + 106);
+}
+
 // Four IQ4 indices (bits 0-3 of each byte of n; bits 4-7 ignored) -> their int8 grid
 // values: v_perm looks up indices 0-7 and 8-15 in the grid's four words, a third v_perm
 // keeps per byte the one its index's bit 3 names.
@@ -927,6 +950,17 @@ __device__ __forceinline__ i32x4 b_operand(const Lane& L, int m, unsigned q6_shi
                      int((l1 & 0x0f0f0f0fu) | ((h << 4) & 0x30303030u)),
                      int(((l0 >> 4) & 0x0f0f0f0fu) | ((h >> 2) & 0x30303030u)),
                      int(((l1 >> 4) & 0x0f0f0f0fu) | ((h << 2) & 0x30303030u))};
+    } else if constexpr (ENC == KDQ_Q3_K) {
+        // unsigned codes q + 4 (0..7) of positions 8m..8m+7: field 2p (block 0) or 2p+1
+        // (block 1) of the qs bytes, hmask bit 2G (or 2G+1) above them; q6_shift = G
+        const unsigned G = q6_shift, sq = 4 * (G % 2), sh = 2 * G;
+        const unsigned q0 = L.w[2 * m], q1 = L.w[2 * m + 1];
+        const unsigned h0 = L.w[8 + 2 * m], h1 = L.w[9 + 2 * m];
+        auto code = [](unsigned q, unsigned h, unsigned fq, unsigned fh) {
+            return ((q >> fq) & 0x03030303u) | (((h >> fh) & 0x01010101u) << 2);
+        };
+        return i32x4{int(code(q0, h0, sq, sh)), int(code(q1, h1, sq, sh)),
+                     int(code(q0, h0, sq + 2, sh + 1)), int(code(q1, h1, sq + 2, sh + 1))};
     } else if constexpr (ENC == KDQ_IQ4_XS) {
         // the grid values (int8) of the indices of positions 8m..8m+7 of both blocks
         const int k = 2 * (m % 2);
@@ -998,7 +1032,24 @@ struct ScaleSel {
 template <int ENC, bool PACKED = false>
 __device__ __forceinline__ float chunk_value(const Lane& L, ScaleSel sel, i32x4 c, i32x4 c2,
                                              float4 x0, float4 x1, bool& bad) {
-    if constexpr (ENC == KDQ_IQ4_NL) {
+    if constexpr (ENC == KDQ_Q3_K) {
+        // scales 4G + t (t = 2b + half): low 4 bits from w[16] (nibble n), high 2 bits
+        // from w[17]; sum (q + 4 - 4) x_q per 16 values exact, then (scale - 32) and d
+        const unsigned G = sel.shift;
+        const float d = half_hw(L.w[18] >> 16);
+        bad |= !isfinite(d);
+        const unsigned lo = L.w[16] >> (4 * (G / 2)), hi = L.w[17] >> (2 * G);
+        auto scale = [&](unsigned t) {
+            return float(int(((lo >> (8 * t)) & 15u) | (((hi >> (8 * t)) & 3u) << 4)) - 32);
+        };
+        const int f0 = __float_as_int(x0.w), f1 = __float_as_int(x1.w);
+        const int t0 = __float_as_int(x0.z) - f0, t1 = __float_as_int(x1.z) - f1;
+        const float a00 = float(c.x * 256 + c.y - 4 * f0), a01 = float(c2.x * 256 + c2.y - 4 * t0);
+        const float a10 = float(c.z * 256 + c.w - 4 * f1), a11 = float(c2.z * 256 + c2.w - 4 * t1);
+        const float b0 = fmaf(scale(1), a01, scale(0) * a00);
+        const float b1 = fmaf(scale(3), a11, scale(2) * a10);
+        return d * fmaf(x1.x, b1, x0.x * b0);
+    } else if constexpr (ENC == KDQ_IQ4_NL) {
         const float d0 = half_hw(L.w[0] & 0xffffu), d1 = half_hw(L.w[4] >> 16);
         bad |= !isfinite(d0) || !isfinite(d1);
         const float A0 = float(c.x * 256 + c.y), A1 = float(c.z * 256 + c.w);
@@ -1175,7 +1226,7 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
     const bool carrier = j / 4 == G;
     // Q4_K: the scale bytes of sub-blocks 2G, 2G+1; Q6_K: 2p for chunk G = 2h + p
     const ScaleSel sel = ENC == KDQ_Q6_K     ? ScaleSel{2 * (G % 2), (j & 1) != 0}
-                         : ENC == KDQ_IQ4_XS ? ScaleSel{G, false}
+                         : ENC == KDQ_IQ4_XS || ENC == KDQ_Q3_K ? ScaleSel{G, false}
                                              : ScaleSel{8 * ((2 * G) & 3), G >= 2};
     // every argument in one round of scalar loads, then the exit test
     asm volatile("" ::"s"(weights), "s"(up), "s"(x), "s"(y), "s"(status), "s"(row_bytes),
@@ -1206,6 +1257,8 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
                 load_lane_q6k(w + size_t(n) * row_bytes, g, G, L[k]);
             else if constexpr (ENC == KDQ_IQ4_XS)
                 load_lane_iq4xs(w + size_t(n) * row_bytes, g, G, L[k]);
+            else if constexpr (ENC == KDQ_Q3_K)
+                load_lane_q3k(w + size_t(n) * row_bytes, g, G, L[k]);
             else if constexpr (ENC == KDQ_IQ4_NL)  // Q4_0's block size and layout
                 load_lane<KDQ_Q4_0>(w + size_t(n) * row_bytes, 4 * g + G, L[k]);
             else
@@ -1261,7 +1314,7 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
                     for (int m = 0; m < 4; ++m) {
                         const i32x4 av = *reinterpret_cast<const i32x4*>(a + m * 256);
                         const i32x4 bv = b_operand<ENC, PACKED>(L[k], m, sel.shift);
-                        if (ENC == KDQ_Q6_K && m >= 2)
+                        if ((ENC == KDQ_Q6_K || ENC == KDQ_Q3_K) && m >= 2)
                             c2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, c2, 0, 0, 0);
                         else
                             c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, c, 0, 0, 0);
@@ -1567,6 +1620,11 @@ int launch_mfma_any(int encoding, const void* w, size_t row_bytes, const float* 
             return launch_mfma<KDQ_IQ4_NL, false>(w, row_bytes, x, rows, in, out, y, stride,
                                                   status, s);
         return KDQ_ERR_UNSUPPORTED;
+    case KDQ_Q3_K:
+        if constexpr (!PACKED)
+            return launch_mfma<KDQ_Q3_K, false>(w, row_bytes, x, rows, in, out, y, stride,
+                                                status, s);
+        return KDQ_ERR_UNSUPPORTED;
     default:
         return KDQ_ERR_UNSUPPORTED;
     }
@@ -1725,14 +1783,15 @@ int with_encoding(int encoding, F&& f) {
 // layout: Q8_0, Q4_0, Q4_K).
 bool streamed_encoding(int encoding) {
     return encoding == KDQ_Q8_0 || encoding == KDQ_Q4_0 || encoding == KDQ_Q4_K ||
-           encoding == KDQ_Q6_K || encoding == KDQ_IQ4_XS || encoding == KDQ_IQ4_NL;
+           encoding == KDQ_Q6_K || encoding == KDQ_IQ4_XS || encoding == KDQ_IQ4_NL ||
+           encoding == KDQ_Q3_K;
 }
 
 // The streaming kernels need whole 64-value lane slots, 4-byte aligned rows and packed
 // rows of exactly the format's size (16-byte aligned for Q4_K); Q6_K (MFMA kernel only)
 // 256-value groups and 2-byte aligned rows.
 bool streams(int encoding, const void* weights, size_t row_bytes, size_t in) {
-    if (encoding == KDQ_Q6_K)
+    if (encoding == KDQ_Q6_K || encoding == KDQ_Q3_K)  // 210- / 110-byte super-blocks
         return in % 256 == 0 && row_bytes % 2 == 0 && aligned(weights, 2);
     if (encoding == KDQ_IQ4_XS)  // 136-byte super-blocks: 8-byte aligned rows
         return in % 256 == 0 && row_bytes % 8 == 0 && aligned(weights, 8);
@@ -1967,6 +2026,10 @@ int launch_fused(const kdq_matvec_job* jobs, const size_t* idx, size_t n, hipStr
         if constexpr (!PACKED)
             return launch_mfma_rows<KDQ_IQ4_NL, false>(j0.rows, p.waves, mj, stream);
         return KDQ_ERR_UNSUPPORTED;
+    case KDQ_Q3_K:
+        if constexpr (!PACKED)
+            return launch_mfma_rows<KDQ_Q3_K, false>(j0.rows, p.waves, mj, stream);
+        return KDQ_ERR_UNSUPPORTED;
     default:
         return KDQ_ERR_UNSUPPORTED;
     }
@@ -2065,6 +2128,8 @@ int indexed_gemv_affine(const IndexedJob& first, unsigned count, size_t x_step,
             return launch_mfma_rows<KDQ_IQ4_XS, false>(j.rows, p.waves, mj, s);
         case KDQ_IQ4_NL:
             return launch_mfma_rows<KDQ_IQ4_NL, false>(j.rows, p.waves, mj, s);
+        case KDQ_Q3_K:
+            return launch_mfma_rows<KDQ_Q3_K, false>(j.rows, p.waves, mj, s);
         default:
             return KDQ_ERR_UNSUPPORTED;
         }

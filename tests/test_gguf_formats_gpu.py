@@ -5,8 +5,8 @@ IW/include/kadan/gguf_quantization.hpp:631-762).
 Decoded weights must be bit-exact to the oracle (NaN matches NaN, as
 IW/tests/gguf_quantization.cpp:21-29 compares), including the special fp16 block scales
 of that test at each format's scale offset; products (kdq_gemv, which runs the MFMA
-GEMV for Q6_K, IQ4_XS and IQ4_NL rows of whole 256-value groups and the exact kernel
-otherwise, and
+GEMV for Q3_K, Q6_K, IQ4_XS and IQ4_NL rows of whole 256-value groups and the exact
+kernel otherwise, and
 kdq_gemv_exact) within rel-L2 <= 1e-3 and max-abs <= 2e-2 of the output RMS against the
 oracle's double product of exactly decoded weights.
 """
