@@ -17,8 +17,8 @@
 //   5. one launch of every slot's expert down GEMV, plus the shared expert's down
 //   6. combine_kernel: y = sum over the selections, in selection order, of down * weight,
 //      plus shared_down * sigmoid(gate scalar)
-// GEMVs of Q4_0 / Q8_0 / Q4_K / Q6_K run on the MFMA kernel (fused per shape), every
-// other encoding on the exact kernel.
+// GEMVs of Q4_0 / Q8_0 / Q4_K / Q3_K / Q6_K / IQ4_XS / IQ4_NL run on the MFMA kernel
+// (fused per shape), every other encoding on the exact kernel.
 #include "kdq_common.hpp"
 
 #include <vector>

@@ -1,8 +1,9 @@
 """GPU parity of the GGUF MoE layer (kdq_moe_gguf) against the oracle's restatement of
 MoeLayer::forward (IW/src/models/text/qwen_layers.cpp:378-492): the routing (selected
 experts bit-exact, weights to 1e-6) and y within rel-L2 <= 1e-3, max-abs <= 2e-2 of its
-RMS.  Expert projections of Q4_K / Q8_0 / Q4_0 / Q6_K run on the MFMA kernel with the
-expert slice chosen on the device, the other encodings on the exact kernel.  The three
+RMS.  Expert projections of Q4_0 / Q8_0 / Q4_K / Q3_K / Q6_K / IQ4_XS / IQ4_NL run on
+the MFMA kernel with the expert slice chosen on the device, the other encodings (IQ3_S,
+IQ3_XXS in EXACT) on the exact kernel.  The three
 encoding mixes cover each launch form: gate and up stored alike run as one paired launch
 that applies the swiglu (MIXED: experts and shared expert; EXACT: the shared expert),
 gate and up stored differently as two launches and the swiglu kernel (SPLIT), and the
@@ -16,6 +17,7 @@ from tests.util import assert_close
 pytestmark = pytest.mark.gpu
 
 F32, Q4_0, Q8_0, Q3_K, Q4_K, Q6_K, IQ4_XS = 0, 2, 8, 11, 12, 14, 23
+IQ3_XXS, IQ3_S = 18, 21
 NAMES = ("router", "gate_exps", "up_exps", "down_exps", "gate_shexp", "up_shexp", "down_shexp")
 
 
@@ -49,7 +51,7 @@ def to_device(torch, device, spec):
 
 MIXED = {"gate_exps": Q4_K, "up_exps": Q4_K, "down_exps": Q6_K, "gate_shexp": Q8_0,
          "up_shexp": Q8_0, "down_shexp": Q4_K}
-EXACT = {"gate_exps": IQ4_XS, "up_exps": IQ4_XS, "down_exps": Q3_K, "gate_shexp": Q4_0,
+EXACT = {"gate_exps": IQ3_S, "up_exps": IQ3_S, "down_exps": IQ3_XXS, "gate_shexp": Q4_0,
          "up_shexp": Q4_0, "down_shexp": Q6_K}
 SPLIT = {"gate_exps": Q4_K, "up_exps": Q8_0, "down_exps": Q4_0, "gate_shexp": Q8_0,
          "up_shexp": Q4_K, "down_shexp": Q8_0}
