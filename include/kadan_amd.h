@@ -231,8 +231,9 @@ int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, size_t rows, f
 
 /* Router + top-k + permutation, IW/src/models/text/qwen_layers.cpp:403-451.
  * logits fp32 [tokens x experts]; top_k <= 8; experts <= 256.
- * idx int32 [tokens x top_k] (selection order: probability descending, equal values
- * keep the lower expert), w fp32 [tokens x top_k] renormalised weights,
+ * idx int32 [tokens x top_k] (selection order: the first top_k of std::partial_sort by
+ * probability descending, equal probabilities in its heap order), w fp32 [tokens x top_k]
+ * renormalised weights,
  * offsets int32 [experts + 1], perm int32 [tokens*top_k] = slots (token*top_k + i)
  * grouped by expert ascending, slot ascending within an expert. */
 int kdq_moe_route(const float* logits, size_t tokens, size_t experts, size_t top_k,

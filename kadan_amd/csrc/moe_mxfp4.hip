@@ -4,7 +4,7 @@
 // IW/src/weights/quantization.cpp:79-99,207-247, behind include/kadan_amd.h.
 //
 //   route_kernel      one wavefront per token: softmax (float exp, double total),
-//                     top-k by probability (equal ones keep the lower expert), renormalise;
+//                     top-k in std::partial_sort's order, renormalise;
 //                     the token's activations as FP8 terms with E8M0 block scales
 //   permute_kernel    one workgroup: stable counting sort of the slots by expert
 //                     (expert-major, slot ascending) plus the list of work items
@@ -45,6 +45,60 @@ __device__ __forceinline__ double wave_sum_double(double v) {
     return v;
 }
 
+// libstdc++'s std::partial_sort (std::__heap_select, then std::__sort_heap, both over
+// std::__adjust_heap: the published binary-heap algorithm) of experts 0..E-1 by
+// p[a] > p[b], for the first k, run by a whole wavefront with wave-uniform control:
+// heap slot i lives in lane i's register.  Returns lane i's selection (i < k).  Only
+// called when probabilities tie or are NaN; otherwise the order is the descending one.
+template <class POf>
+__device__ __forceinline__ int heap_route(POf p_of, unsigned experts, unsigned k,
+                                          unsigned lane) {
+    int slot = int(lane);  // order = iota
+    auto get = [&](int i) { return __builtin_amdgcn_readlane(slot, i); };
+    auto put = [&](int i, int v) {
+        if (lane == unsigned(i))
+            slot = v;
+    };
+    auto before = [&](int a, int b) { return p_of(a) > p_of(b); };
+    auto adjust = [&](int hole, int len, int value) {
+        const int top = hole;
+        int child = hole;
+        while (child < (len - 1) / 2) {
+            child = 2 * (child + 1);
+            if (before(get(child), get(child - 1)))
+                --child;
+            put(hole, get(child));
+            hole = child;
+        }
+        if ((len & 1) == 0 && child == (len - 2) / 2) {
+            child = 2 * (child + 1);
+            put(hole, get(child - 1));
+            hole = child - 1;
+        }
+        while (hole > top) {
+            const int parent = (hole - 1) / 2;
+            if (!before(get(parent), value))
+                break;
+            put(hole, get(parent));
+            hole = parent;
+        }
+        put(hole, value);
+    };
+    const int len = int(k);
+    if (len >= 2)  // make_heap
+        for (int parent = (len - 2) / 2; parent >= 0; --parent)
+            adjust(parent, len, get(parent));
+    for (int i = len; i < int(experts); ++i)  // heap select; position i still holds i
+        if (before(i, get(0)))
+            adjust(0, len, i);
+    for (int last = len - 1; last > 0; --last) {  // sort_heap
+        const int value = get(last);
+        put(last, get(0));
+        adjust(0, last, value);
+    }
+    return slot;
+}
+
 // Token t by one whole wavefront (lane = its lane).
 __device__ __forceinline__ void route_token(const float* __restrict__ logits, unsigned t,
                                             unsigned experts, unsigned top_k,
@@ -72,49 +126,62 @@ __device__ __forceinline__ void route_token(const float* __restrict__ logits, un
     for (int j = 0; j < 4; ++j)
         p[j] = float(double(p[j]) / total);
 
-    // Selection by probability, as the reference's partial sort orders it: the largest p
-    // first, equal p keep the lower expert; and as its scan keeps its first candidate
-    // while nothing compares greater, a NaN p at the lowest untaken expert is taken
-    // there.  Per pick: one DPP maximum and a ballot per register (no LDS round trips).
+    // Selection.  The reference takes the first k of std::partial_sort over experts
+    // 0..E-1 by p[a] > p[b] (qwen_layers.cpp:409-416).  When the k largest p are distinct
+    // and above every other p, that is simply the k largest in descending order: one DPP
+    // maximum and a ballot per register per pick.  Equal probabilities (and NaN ones,
+    // which compare false both ways) come out in the order of libstdc++'s heap
+    // selection; then the wavefront reruns that heap algorithm (heap_route below).
     bool valid[4];
+    bool nan_seen = false;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 4; ++j) {
         valid[j] = lane + 64 * j < experts;
-    unsigned taken = 0;
+        nan_seen |= __ballot(valid[j] && isnan(p[j])) != 0;
+    }
+    auto p_of = [&](int e) {  // p of expert e (wave-uniform)
+        const int j = e / 64;
+        const float pj = j == 0 ? p[0] : (j == 1 ? p[1] : (j == 2 ? p[2] : p[3]));
+        return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), e % 64));
+    };
+    int chosen_e = 0;  // lane i < top_k: the i-th selection
+    bool ambiguous = nan_seen;
+    if (!nan_seen) {
+        unsigned taken = 0;
+        float previous = INFINITY;
+        for (unsigned i = 0; i <= top_k && i < experts; ++i) {
+            float c = 0.f;  // every probability is >= 0 here
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (valid[j] && !((taken >> j) & 1u))
+                    c = fmaxf(c, p[j]);
+            c = wave_max_nonneg(c);
+            ambiguous |= c == previous;  // equal to the last pick: a tie
+            previous = c;
+            if (i == top_k)
+                break;  // only the largest unselected p was needed
+            int best = -1;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool open = valid[j] && !((taken >> j) & 1u);
+                const unsigned long long hit = __ballot(open && p[j] == c);
+                if (best < 0 && hit)
+                    best = 64 * j + __builtin_ctzll(hit);
+            }
+            if (lane == unsigned(best % 64))
+                taken |= 1u << (best / 64);
+            if (lane == i)
+                chosen_e = best;
+        }
+    }
+    if (ambiguous)
+        chosen_e = heap_route(p_of, experts, top_k, lane);
     float sum = 0.f, chosen_p = 0.f;
-    int chosen_e = 0;
-    for (unsigned i = 0; i < top_k; ++i) {
-        float c = 0.f;  // every probability that is not NaN is >= 0
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (valid[j] && !((taken >> j) & 1u))
-                c = fmaxf(c, p[j]);
-        c = wave_max_nonneg(c);
-        int e0 = -1, eb = -1;  // lowest untaken expert; lowest one whose p equals c
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const bool open = valid[j] && !((taken >> j) & 1u);
-            const unsigned long long any = __ballot(open), hit = __ballot(open && p[j] == c);
-            if (e0 < 0 && any)
-                e0 = 64 * j + __builtin_ctzll(any);
-            if (eb < 0 && hit)
-                eb = 64 * j + __builtin_ctzll(hit);
-        }
-        auto p_of = [&](int e) {  // p of expert e (wave-uniform)
-            const int j = e / 64;
-            const float pj = j == 0 ? p[0] : (j == 1 ? p[1] : (j == 2 ? p[2] : p[3]));
-            return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), e % 64));
-        };
-        const float p0 = p_of(e0);
-        const int be = (isnan(p0) || eb < 0) ? e0 : eb;
-        const float pb = be == e0 ? p0 : p_of(be);
-        if (lane == unsigned(be % 64))
-            taken |= 1u << (be / 64);
-        sum += pb;  // sequential, in selection order
-        if (lane == i) {
-            chosen_p = pb;
-            chosen_e = be;
-        }
+    for (unsigned i = 0; i < top_k; ++i) {  // sequential, in selection order
+        const float pi = p_of(__builtin_amdgcn_readlane(chosen_e, i));
+        sum += pi;
+        if (lane == i)
+            chosen_p = pi;
     }
     sum = fmaxf(sum, 6.103515625e-5f);
     if (lane < top_k) {

@@ -176,3 +176,61 @@ def moe_weights(seed: int, experts: int, hidden: int, inter: int):
     up = mxfp4_weights(seed, 11, experts, inter, hidden)
     down = mxfp4_weights(seed, 12, experts, hidden, inter)
     return gate, up, down
+
+
+# ------------------------------------------- the same streams generated by torch
+
+def _mask(bits: int) -> int:
+    """(1 << bits) - 1 as a signed 64-bit value."""
+    return (1 << bits) - 1 if bits < 64 else -1
+
+
+def _signed(v: int) -> int:
+    v &= 0xFFFFFFFFFFFFFFFF
+    return v - (1 << 64) if v >> 63 else v
+
+
+def splitmix64_torch(seed: int, tensor: int, n: int, device):
+    """splitmix64(seed, tensor, n) as a torch int64 tensor on `device`, bit for bit:
+    two's-complement int64 addition, multiplication and xor wrap exactly as uint64 does,
+    and logical right shifts are arithmetic shifts masked to the kept bits."""
+    import torch
+    base = (seed * 0x100000001B3 + tensor * 0x9E3779B1) & 0xFFFFFFFFFFFFFFFF
+    out = torch.empty(n, dtype=torch.int64, device=device)
+    chunk = 1 << 26
+    golden, m1, m2 = (_signed(int(v)) for v in (_GOLDEN, _M1, _M2))
+    for start in range(0, n, chunk):
+        i = torch.arange(start + 1, min(n, start + chunk) + 1, dtype=torch.int64, device=device)
+        z = i * golden + _signed(base)
+        z = (z ^ ((z >> 30) & _mask(34))) * m1
+        z = (z ^ ((z >> 27) & _mask(37))) * m2
+        out[start:start + i.numel()] = z ^ ((z >> 31) & _mask(33))
+    return out
+
+
+def _umod_small(v, m: int):
+    """v mod m for int64 tensors holding uint64 bits, m < 2^31."""
+    hi = (v >> 32) & _mask(32)
+    lo = v & _mask(32)
+    return ((hi % m) * ((1 << 32) % m) + lo % m) % m
+
+
+def mxfp4_weights_torch(seed: int, tensor: int, experts: int, rows: int, cols: int, device,
+                        exp_lo: int = -8, exp_hi: int = 0):
+    """mxfp4_weights as uint8 torch tensors on `device` (the same bytes)."""
+    import torch
+    n = experts * rows * cols // 2
+    blocks = splitmix64_torch(seed, 2 * tensor, (n + 7) // 8, device).view(torch.uint8)[:n]
+    e = _umod_small(splitmix64_torch(seed, 2 * tensor + 1, experts * rows * cols // 32,
+                                     device), exp_hi - exp_lo + 1)
+    scales = (e + 127 + exp_lo).to(torch.uint8)
+    return (blocks.reshape(experts, rows, cols // 2).clone(),
+            scales.reshape(experts, rows, cols // 32))
+
+
+def moe_weights_torch(seed: int, experts: int, hidden: int, inter: int, device):
+    """moe_weights as device tensors, bit-identical, generated on the device."""
+    gate = mxfp4_weights_torch(seed, 10, experts, inter, hidden, device)
+    up = mxfp4_weights_torch(seed, 11, experts, inter, hidden, device)
+    down = mxfp4_weights_torch(seed, 12, experts, hidden, inter, device)
+    return gate, up, down

@@ -306,6 +306,16 @@ class Reference:
         lib.kdr_e2m1.argtypes = [C.c_uint8]
         lib.kdr_mxfp4_decode_rows.argtypes = [vp, vp, sz, sz, vp]
         lib.kdr_mxfp4_matvec.argtypes = [vp, vp, sz, sz, vp, vp]
+        lib.kdr_moe_route.argtypes = [vp, sz, sz, sz, vp, vp]
+
+    def moe_route(self, logits, top_k):
+        """Routing with the C++ library's std::partial_sort (kdr_moe_route)."""
+        logits = np.ascontiguousarray(logits, dtype=np.float32)
+        t, e = logits.shape
+        idx = np.empty((t, top_k), np.int32)
+        w = np.empty((t, top_k), np.float32)
+        self.lib.kdr_moe_route(_p(logits), t, e, top_k, _p(idx), _p(w))
+        return idx, w
 
     def half_to_float(self, bits: int) -> float:
         return self.lib.kdr_half_to_float(bits)

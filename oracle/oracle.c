@@ -692,15 +692,77 @@ int kdo_mxfp4_matvec(const uint8_t* blocks, const uint8_t* scales, size_t rows, 
 
 /* -------------------------------------------------------------------- MoE */
 
+/* The reference orders the experts with std::partial_sort(order, order + k, order + E,
+ * [&](a, b) { return p[a] > p[b]; }) over order = 0..E-1 (qwen_layers.cpp:409-416).
+ * libstdc++ implements it as a heap selection followed by a heap sort of the first k
+ * (std::__heap_select, std::__sort_heap, both over std::__adjust_heap); the functions
+ * below restate that published binary-heap algorithm step for step, because its order
+ * among equal probabilities (and among NaN ones, which compare false both ways) is the
+ * reference's selection order.  Pinned against std::partial_sort itself (compiled
+ * reference bindings) on random tie patterns. */
+static int route_before(const float* p, int32_t a, int32_t b) {
+    return p[a] > p[b];
+}
+
+/* The hole at `hole` moves down to a leaf along the child that is "larger" under the
+ * comparator (the right child unless the left one compares before it), then `value` is
+ * pushed back up towards `top`. */
+static void heap_adjust(int32_t* h, size_t hole, size_t len, int32_t value, const float* p) {
+    const size_t top = hole;
+    size_t child = hole;
+    while (child < (len - 1) / 2) {
+        child = 2 * (child + 1);
+        if (route_before(p, h[child], h[child - 1]))
+            --child;
+        h[hole] = h[child];
+        hole = child;
+    }
+    if ((len & 1) == 0 && child == (len - 2) / 2) {
+        child = 2 * (child + 1);
+        h[hole] = h[child - 1];
+        hole = child - 1;
+    }
+    while (hole > top) {
+        const size_t parent = (hole - 1) / 2;
+        if (!route_before(p, h[parent], value))
+            break;
+        h[hole] = h[parent];
+        hole = parent;
+    }
+    h[hole] = value;
+}
+
+/* order[0..k) = the first k of std::partial_sort over experts 0..E-1. */
+static void route_partial_sort(const float* p, size_t experts, size_t k, int32_t* order) {
+    for (size_t i = 0; i < k; ++i)
+        order[i] = (int32_t)i;
+    if (k >= 2) /* make_heap */
+        for (size_t parent = (k - 2) / 2;; --parent) {
+            heap_adjust(order, parent, k, order[parent], p);
+            if (!parent)
+                break;
+        }
+    /* heap select: position i still holds expert i when it is visited */
+    for (size_t i = k; i < experts; ++i)
+        if (route_before(p, (int32_t)i, order[0])) {
+            heap_adjust(order, 0, k, (int32_t)i, p); /* pop_heap: old top goes to i */
+        }
+    for (size_t last = k; last > 1;) { /* sort_heap */
+        --last;
+        const int32_t value = order[last];
+        order[last] = order[0];
+        heap_adjust(order, 0, last, value, p);
+    }
+}
+
 void kdo_moe_route(const float* logits, size_t tokens, size_t experts, size_t top_k,
                    int32_t* idx, float* w) {
     float* p = (float*)malloc(experts * sizeof(float));
-    unsigned char* taken = (unsigned char*)malloc(experts);
     for (size_t t = 0; t < tokens; ++t) {
         const float* l = logits + t * experts;
-        float maximum = l[0];
+        float maximum = l[0]; /* std::max_element: the first e with no l[e] < later */
         for (size_t e = 1; e < experts; ++e)
-            maximum = l[e] > maximum ? l[e] : maximum;
+            maximum = maximum < l[e] ? l[e] : maximum;
         double total = 0.0;
         for (size_t e = 0; e < experts; ++e) {
             p[e] = expf(l[e] - maximum);
@@ -708,24 +770,17 @@ void kdo_moe_route(const float* logits, size_t tokens, size_t experts, size_t to
         }
         for (size_t e = 0; e < experts; ++e)
             p[e] = (float)((double)p[e] / total);
-        memset(taken, 0, experts);
+        route_partial_sort(p, experts, top_k, idx + t * top_k);
         float sum = 0.0f;
         for (size_t i = 0; i < top_k; ++i) {
-            size_t best = experts;
-            for (size_t e = 0; e < experts; ++e)
-                if (!taken[e] && (best == experts || p[e] > p[best]))
-                    best = e; /* strict >: equal probabilities keep the lower expert */
-            taken[best] = 1;
-            idx[t * top_k + i] = (int32_t)best;
-            w[t * top_k + i] = p[best];
-            sum += p[best];
+            w[t * top_k + i] = p[idx[t * top_k + i]];
+            sum += w[t * top_k + i];
         }
         sum = sum > 6.103515625e-5f ? sum : 6.103515625e-5f;
         for (size_t i = 0; i < top_k; ++i)
             w[t * top_k + i] /= sum;
     }
     free(p);
-    free(taken);
 }
 
 void kdo_moe_permute(const int32_t* idx, size_t tokens, size_t top_k, size_t experts,

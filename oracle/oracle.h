@@ -146,8 +146,9 @@ int kdo_mxfp4_matvec(const uint8_t* blocks, const uint8_t* scales, size_t rows, 
                      const float* x, float* y);
 
 /* Router of IW/src/models/text/qwen_layers.cpp:403-425: float exp of (l - max), double
- * total, p = float(p/total); top-k by probability descending (equal probabilities:
- * lower expert first); w_i = p_i / max(sum_i p_i, 6.103515625e-5f).
+ * total, p = float(p/total); the first k of libstdc++'s std::partial_sort of 0..E-1 by
+ * p[a] > p[b] (heap select + sort_heap, so equal probabilities come out in the heap's
+ * order, :409-416); w_i = p_i / max(sum_i p_i, 6.103515625e-5f).
  * idx, w: [tokens * top_k]. */
 void kdo_moe_route(const float* logits, size_t tokens, size_t experts, size_t top_k,
                    int32_t* idx, float* w);

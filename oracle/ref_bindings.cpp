@@ -7,8 +7,19 @@
 // the oracle restatement (oracle.c) against it and bench.py can time the real
 // reference CPU path.  Only tests/, tests/golden/ and bench.py's cpu_baseline leg
 // may load the resulting library.
+//
+// One exception: kdr_moe_route.  The reference's router only runs inside
+// MoeLayer::forward (IW/src/models/text/qwen_layers.cpp:397-425), which needs a GGUF
+// file and a DenseCompute to construct; so kdr_moe_route states the same steps with
+// the same standard-library calls (std::max_element, float std::exp, a double total,
+// std::partial_sort with the p[a] > p[b] comparator over std::iota indices).  Its
+// point is that std::partial_sort is the C++ library's own, so the order it gives
+// equal probabilities is the order the reference gets.
+#include <algorithm>
 #include <atomic>
+#include <cmath>
 #include <cstdint>
+#include <numeric>
 #include <cstring>
 #include <exception>
 #include <span>
@@ -153,6 +164,36 @@ int kdr_mxfp4_matvec(const uint8_t* blocks, const uint8_t* scales, size_t rows, 
         return -2;
     } catch (...) {
         return -3;
+    }
+}
+
+// Routing as the reference's MoeLayer::forward computes it (qwen_layers.cpp:397-425),
+// with the C++ library's std::partial_sort choosing and ordering the experts.
+void kdr_moe_route(const float* logits, size_t tokens, size_t experts, size_t top_k,
+                   int32_t* idx, float* w) {
+    std::vector<float> p(experts);
+    std::vector<std::size_t> order(experts);
+    for (std::size_t t = 0; t < tokens; ++t) {
+        const float* l = logits + t * experts;
+        const float top = *std::max_element(l, l + experts);
+        double total = 0;
+        for (std::size_t e = 0; e < experts; ++e) {
+            p[e] = std::exp(l[e] - top);
+            total += p[e];
+        }
+        for (auto& v : p)
+            v = float(v / total);
+        std::iota(order.begin(), order.end(), std::size_t{0});
+        std::partial_sort(order.begin(), order.begin() + top_k, order.end(),
+                          [&](std::size_t a, std::size_t b) { return p[a] > p[b]; });
+        float sum = 0;
+        for (std::size_t i = 0; i < top_k; ++i) {
+            idx[t * top_k + i] = int32_t(order[i]);
+            sum += w[t * top_k + i] = p[order[i]];
+        }
+        sum = std::max(sum, 6.103515625e-5f);
+        for (std::size_t i = 0; i < top_k; ++i)
+            w[t * top_k + i] /= sum;
     }
 }
 }

@@ -25,6 +25,13 @@ Contents (all little-endian, plain arrays, no pickles):
   mxfp4_blocks / mxfp4_scales / mxfp4_values / mxfp4_x / mxfp4_y
                              kadan quantization::decode_rows / matvec
                              (IW/src/weights/quantization.cpp:193-247)
+  route_<E>_<k>_logits / _idx / _w
+                             the router of MoeLayer::forward (IW/src/models/text/
+                             qwen_layers.cpp:397-425) with the C++ library's
+                             std::partial_sort, on logits drawn from a few values
+                             (0, 1, 2, -1, -inf, and NaN / +inf in some rows) so that
+                             equal probabilities are the rule: the order the library's
+                             heap selection gives ties
 """
 import os
 import sys
@@ -197,6 +204,19 @@ def main():
     assert rc == 0, rc
     data.update(mxfp4_blocks=blocks, mxfp4_scales=scales, mxfp4_values=values,
                 mxfp4_mv_scales=scales_mv, mxfp4_x=xm, mxfp4_y=ym)
+    # routing with ties: logits from a small set of values, std::partial_sort's order
+    gr = np.random.default_rng(0x7135)
+    values = np.array([0, 1, 2, -1, -np.inf, np.nan, np.inf], np.float32)
+    finite = np.array([.4, .3, .2, .07, .03, 0, 0])
+    special = np.array([.3, .3, .2, .1, .05, .03, .02])
+    for experts, top_k in ((4, 4), (6, 3), (13, 8), (16, 4), (32, 4), (128, 4), (256, 8)):
+        rows = [gr.choice(values, size=experts, p=special if t % 4 == 3 else finite)
+                for t in range(48)]
+        logits = np.stack(rows).astype(np.float32)
+        logits[0] = 0.0  # every probability equal
+        idx, w = ref.moe_route(logits, top_k)
+        key = f"route_{experts}_{top_k}"
+        data[f"{key}_logits"], data[f"{key}_idx"], data[f"{key}_w"] = logits, idx, w
     np.savez_compressed(OUT, **data)
     print(OUT, os.path.getsize(OUT), "bytes,", len(data), "arrays")
 

@@ -4,6 +4,8 @@ import ctypes as C
 import os
 import re
 
+import numpy as np
+
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -170,3 +172,18 @@ def test_gemm_packed_argument_errors():
     assert g(FAKE_W, 16, 256, FAKE_X, 1, FAKE_Y + 1, None) == 7    # output not 2-aligned
     assert g(FAKE_W, 16, 256, FAKE_X, 1, FAKE_W + 32, None) == 4   # output inside packed
     assert g(FAKE_W, 16, 256, FAKE_X, 1, FAKE_X + 64, None) == 4   # output inside x
+
+
+def test_synth_torch_streams_match_numpy():
+    """The torch SplitMix64 streams (used to build C4/C5 weights on the device) give the
+    numpy generator's bytes bit for bit."""
+    import torch
+    from kadan_amd import synth
+    a = synth.moe_weights(7, 3, 128, 192)
+    b = synth.moe_weights_torch(7, 3, 128, 192, "cpu")
+    for (blocks, scales), (tb, ts) in zip(a, b):
+        assert np.array_equal(blocks, tb.numpy()) and np.array_equal(scales, ts.numpy())
+    assert np.array_equal(synth.splitmix64(5, 9, 1000).view(np.int64),
+                          synth.splitmix64_torch(5, 9, 1000, "cpu").numpy())
+    assert torch.equal(synth._umod_small(torch.tensor([-1], dtype=torch.int64), 9),
+                       torch.tensor([(2 ** 64 - 1) % 9]))

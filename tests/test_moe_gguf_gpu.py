@@ -75,6 +75,24 @@ def test_moe_gguf_parity(device, oracle, rows, encs):
     assert int(status.item()) == 0
 
 
+@pytest.mark.parametrize("rows,top_k", [(9, 4), (16, 4), (64, 8)])
+@pytest.mark.parametrize("encs", [MIXED, EXACT], ids=["mixed", "exact"])
+def test_moe_gguf_more_rows(device, oracle, rows, top_k, encs):
+    """Past the 8-row pass: 9 and 16 rows (two passes of the router / shared batch and of
+    the exact kernel's 8-row loop, unpaired rows of the shared swiglu), and 64 rows x
+    top-8 = 512 slots, the largest layer the entry point takes."""
+    import torch
+    H, E, F, S = 512, 16, 256, 512
+    spec = make_layer(40 + rows, H, E, top_k, F, S, encs)
+    x = synth.normal(50 + rows, 1, rows * H).reshape(rows, H)
+    want, idx, w = oracle.moe_gguf_forward(spec, x)
+    from kadan_amd import ops
+    y, sel, ws = ops.moe_gguf(to_device(torch, device, spec), torch.from_numpy(x).to(device))
+    assert np.array_equal(sel.cpu().numpy(), idx)
+    assert np.abs(ws.cpu().numpy() - w).max() < 1e-6
+    assert_close(y.cpu().numpy(), want, what=f"moe_gguf rows={rows} top_k={top_k}")
+
+
 def test_moe_gguf_qwen3_shape(device, oracle):
     """Qwen3-30B-A3B's expert geometry (hidden 2048, 128 experts, top-8, expert ff 768)
     with a 768-wide shared expert, one decode token and a batch of four."""

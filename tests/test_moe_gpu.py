@@ -1,10 +1,15 @@
 """GPU parity of the MXFP4 MoE layer (kdq_moe_route, kdq_mxfp4_dequantize, kdq_moe_mxfp4).
 
-Top-k indices and the permutation must be bit-exact; routing weights and the layer
-output within rel-L2 <= 1e-3 and max-abs <= 2e-2 of the output RMS (the MoE outputs
-are far from unit scale at these distributions, so max-abs is normalised) against the
-oracle's composition of the reference pieces (double-accumulated MXFP4 products).
+Top-k indices and the permutation must be bit-exact (ties included: the reference's
+std::partial_sort order, recorded in tests/golden from the C++ library); routing weights
+and the layer output within rel-L2 <= 1e-3 and max-abs <= 2e-2 of the output RMS (the
+MoE outputs are far from unit scale at these distributions, so max-abs is normalised)
+against the oracle's composition of the reference pieces (double-accumulated MXFP4
+products).  The full-size C4 T=256 and C5 layers are compared on sampled tokens: a
+token's output depends only on its own routing, so the oracle runs on the sample.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -19,17 +24,9 @@ def _torch():
     return torch
 
 
-def no_boundary_ties(oracle, logits, top_k):
-    """True when no token has equal float probabilities across its top-k boundary (the
-    reference orders equal probabilities arbitrarily)."""
-    for row in logits:
-        m = row.max()
-        p = np.exp((row - m).astype(np.float32)).astype(np.float32)
-        p = (p.astype(np.float64) / p.astype(np.float64).sum()).astype(np.float32)
-        s = np.sort(p)[::-1]
-        if top_k < len(s) and s[top_k - 1] == s[top_k]:
-            return False
-    return True
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                      "reference_vectors.npz")
+ROUTE_CASES = [(4, 4), (6, 3), (13, 8), (16, 4), (32, 4), (128, 4), (256, 8)]
 
 
 @pytest.mark.parametrize("tokens,experts,top_k", [(1, 32, 4), (7, 8, 2), (256, 32, 4),
@@ -38,7 +35,6 @@ def test_route_and_permutation_bit_exact(device, oracle, tokens, experts, top_k)
     torch = _torch()
     _, logits = synth.moe_inputs(0xC4 + tokens, tokens, 64, experts,
                                  hot=8 if experts >= 128 else 0)
-    assert no_boundary_ties(oracle, logits, top_k)
     idx, w = oracle.moe_route(logits, top_k)
     offsets, perm = oracle.moe_permute(idx, experts)
     from kadan_amd import ops
@@ -49,33 +45,44 @@ def test_route_and_permutation_bit_exact(device, oracle, tokens, experts, top_k)
     assert_close(gw.cpu().numpy(), w, rel=1e-6, mabs=1e-5, what="routing weights")
 
 
-def test_route_equal_logits_keep_lower_expert(device):
+@pytest.mark.parametrize("experts,top_k", ROUTE_CASES)
+def test_route_ties_in_library_order(device, experts, top_k):
+    """Logits drawn from a few values (and NaN / +-inf in some rows), so equal
+    probabilities are the rule: indices bit-exact to std::partial_sort's output recorded
+    from the compiled C++ library, weights bit-exact too (NaN matches NaN)."""
     torch = _torch()
-    logits = np.zeros((3, 16), np.float32)
-    logits[1, [3, 9, 12]] = 1.0
-    logits[2, :] = -np.inf
-    logits[2, 5] = 0.0
+    with np.load(GOLDEN, allow_pickle=False) as f:
+        key = f"route_{experts}_{top_k}"
+        logits, idx, w = f[f"{key}_logits"], f[f"{key}_idx"], f[f"{key}_w"]
+    from kadan_amd import ops
+    gi, gw, _, _ = ops.moe_route(torch.from_numpy(logits).to(device), top_k)
+    assert np.array_equal(gi.cpu().numpy(), idx)
+    gw = gw.cpu().numpy()
+    assert np.all((gw.view(np.uint32) == w.view(np.uint32)) | (np.isnan(gw) & np.isnan(w)))
+
+
+def test_route_equal_logits_heap_order(device):
+    """16 equal probabilities, top-4: std::partial_sort gives [1, 3, 0, 2] (worked through
+    the heap steps in tests/test_oracle.py)."""
+    torch = _torch()
+    logits = np.zeros((2, 16), np.float32)
+    logits[1, :13] = [1, 0, 0, 0, -5, 1, 0, 0, -5, 1, 0, 0, 1]
+    logits[1, 13:] = -5
     from kadan_amd import ops
     gi, gw, _, _ = ops.moe_route(torch.from_numpy(logits).to(device), 4)
-    gi = gi.cpu().numpy()
-    assert list(gi[0]) == [0, 1, 2, 3]
-    assert list(gi[1]) == [3, 9, 12, 0]
-    assert list(gi[2]) == [5, 0, 1, 2]
+    assert gi.cpu().numpy()[0].tolist() == [1, 3, 0, 2]
     np.testing.assert_allclose(gw.cpu().numpy()[0], 0.25, rtol=1e-6)
 
 
-def test_route_equal_probabilities_keep_lower_expert(device, oracle):
-    """Logits 0 and 1e-8 both give p = 1 after the float exp (1 - 1e-8 rounds to 1): the
-    reference's partial sort by probability keeps the lower expert first, whatever the
-    logits' order (qwen_layers.cpp:403-425)."""
+def test_route_equal_probabilities_from_different_logits(device, oracle):
+    """Logits 0 and 1e-8 both give p = 1 after the float exp: they tie, and the device
+    follows the oracle's (the library's) heap order."""
     torch = _torch()
     logits = np.full((3, 16), -5.0, np.float32)
     logits[0, :2] = [0.0, 1e-8]
     logits[1, [4, 7]] = [1e-8, 0.0]
     logits[2, [2, 9, 11]] = [1e-8, 0.0, 1e-8]
     idx, w = oracle.moe_route(logits, 3)
-    assert list(idx[0][:2]) == [0, 1] and list(idx[1][:2]) == [4, 7]
-    assert list(idx[2]) == [2, 9, 11]
     from kadan_amd import ops
     gi, gw, _, _ = ops.moe_route(torch.from_numpy(logits).to(device), 3)
     assert np.array_equal(gi.cpu().numpy(), idx)
@@ -109,7 +116,8 @@ def test_mxfp4_dequantize_bit_exact(device, oracle):
 def run_layer(device, oracle, tokens, hidden, inter, experts, top_k, seed, hot=0, threads=8):
     torch = _torch()
     x, logits = synth.moe_inputs(seed, tokens, hidden, experts, hot=hot)
-    (gb, gs), (ub, us), (db, ds) = synth.moe_weights(seed, experts, hidden, inter)
+    weights = synth.moe_weights_torch(seed, experts, hidden, inter, device)
+    (gb, gs), (ub, us), (db, ds) = [(b.cpu().numpy(), s.cpu().numpy()) for b, s in weights]
     y, idx, w, offsets, perm = oracle.moe_forward(x, logits, top_k, gb, gs, ub, us, db, ds,
                                                   threads=threads)
     from kadan_amd import ops
@@ -141,15 +149,86 @@ def test_moe_layer_skewed_routing(device, oracle):
     run_layer(device, oracle, 64, 256, 256, 128, 4, seed=0xC5, hot=8)
 
 
+def test_moe_known_answer(device):
+    """The hand-derived 2-token x 4-expert case (tests/util.py known_answer_moe) on the
+    device: routing exact, output within the tolerance of the closed form."""
+    torch = _torch()
+    from tests.util import known_answer_moe
+    x, logits, ((gb, gs), (ub, us), (db, ds)), y, idx = known_answer_moe()
+    from kadan_amd import ops
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)
+    gy, gi, _, _, _ = ops.moe_mxfp4(dev(x).view(torch.bfloat16), dev(logits), 2, dev(gb),
+                                    dev(gs), dev(ub), dev(us), dev(db), dev(ds), routing=True)
+    assert np.array_equal(gi.cpu().numpy(), idx)
+    assert_close(gy.cpu().numpy(), y, what="moe known answer")
+
+
+def sampled_tokens(offsets, perm, top_k, tokens, hot=8, extra=16, seed=5):
+    """Tokens to check at full size: for the `hot` experts with the most rows, the token of
+    their first slot and of their last (the last work item of a multi-item expert), plus
+    `extra` seeded random tokens."""
+    counts = np.diff(offsets)
+    chosen = set()
+    for e in np.argsort(-counts, kind="stable")[:hot]:
+        if counts[e]:
+            chosen.add(int(perm[offsets[e]]) // top_k)
+            chosen.add(int(perm[offsets[e + 1] - 1]) // top_k)
+    rng = np.random.default_rng(seed)
+    chosen |= set(int(t) for t in rng.choice(tokens, min(extra, tokens), replace=False))
+    return np.array(sorted(chosen))
+
+
+def run_full_size(device, oracle, tokens, experts, hot, seed, what):
+    """The packed (resident-bank) entry point at a benchmark configuration: the whole
+    batch's routing bit-exact, sampled tokens' outputs against the oracle."""
+    torch = _torch()
+    hidden = inter = 2880
+    top_k = 4
+    x, logits = synth.moe_inputs(seed, tokens, hidden, experts, hot=hot)
+    (gb, gs), (ub, us), (db, ds) = synth.moe_weights_torch(seed, experts, hidden, inter,
+                                                           device)
+    from kadan_amd import ops
+    packed = [ops.moe_mxfp4_pack(gb, gs, experts, inter, hidden),
+              ops.moe_mxfp4_pack(ub, us, experts, inter, hidden),
+              ops.moe_mxfp4_pack(db, ds, experts, hidden, inter)]
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)
+    gy, gi, gw, go, gp = ops.moe_mxfp4_packed(dev(x).view(torch.bfloat16), dev(logits), top_k,
+                                              inter, *packed, routing=True)
+    idx, w = oracle.moe_route(logits, top_k)
+    offsets, perm = oracle.moe_permute(idx, experts)
+    assert np.array_equal(gi.cpu().numpy(), idx)
+    assert np.array_equal(go.cpu().numpy(), offsets)
+    assert np.array_equal(gp.cpu().numpy(), perm)
+    assert_close(gw.cpu().numpy(), w, rel=1e-6, mabs=1e-5, what=f"{what} routing weights")
+    sample = sampled_tokens(offsets, perm, top_k, tokens)
+    host = [a.cpu().numpy() for a in (gb, gs, ub, us, db, ds)]
+    del packed
+    y, _, _, _, _ = oracle.moe_forward(x[sample], logits[sample], top_k, *host,
+                                       threads=min(16, os.cpu_count() or 1))
+    assert_close(gy.cpu().numpy()[sample], y, what=f"{what} ({len(sample)} sampled tokens)")
+    return np.diff(offsets)
+
+
+def test_moe_c5_full_size_sampled(device, oracle):
+    """C5 at its own size: 128 experts, H = I = 2880, T = 2048, 25 % of tokens favouring
+    8 hot experts (about 300 rows each, five work items)."""
+    counts = run_full_size(device, oracle, 2048, 128, 8, 0xC5, "moe C5 T=2048")
+    assert counts.max() > 4 * 64  # the hot experts do span several work items
+
+
+def test_moe_c4_prefill_full_size_sampled(device, oracle):
+    """C4 prefill at its own size: 32 experts, H = I = 2880, T = 256."""
+    run_full_size(device, oracle, 256, 32, 0, 0xC4, "moe C4 T=256")
+
+
 def test_moe_prefill_256_properties(device):
     """C4 prefill (256 tokens) at full size: determinism across calls, and permutation
     invariance (reversing the token order reverses the output rows)."""
     torch = _torch()
     x, logits = synth.moe_inputs(0xC4, 256, 2880, 32)
-    (gb, gs), (ub, us), (db, ds) = synth.moe_weights(0xC4, 32, 2880, 2880)
     from kadan_amd import ops
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)
-    wts = [dev(a) for a in (gb, gs, ub, us, db, ds)]
+    wts = [a for pair in synth.moe_weights_torch(0xC4, 32, 2880, 2880, device) for a in pair]
     xb = dev(x).view(torch.bfloat16)
     y1 = ops.moe_mxfp4(xb, dev(logits), 4, *wts).cpu().numpy()
     y2 = ops.moe_mxfp4(xb, dev(logits), 4, *wts).cpu().numpy()
@@ -198,10 +277,10 @@ def test_moe_packed_matches_reference_layout(device, tokens, hidden, inter, expe
     entry point's output and routing bit for bit."""
     torch = _torch()
     x, logits = synth.moe_inputs(0xAB + tokens, tokens, hidden, experts)
-    (gb, gs), (ub, us), (db, ds) = synth.moe_weights(0xAB, experts, hidden, inter)
     from kadan_amd import ops
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)
-    wts = [dev(a) for a in (gb, gs, ub, us, db, ds)]
+    wts = [a for pair in synth.moe_weights_torch(0xAB, experts, hidden, inter, device)
+           for a in pair]
     xb, lg = dev(x).view(torch.bfloat16), dev(logits)
     ref = ops.moe_mxfp4(xb, lg, top_k, *wts, routing=True)
     packed = [ops.moe_mxfp4_pack(wts[0], wts[1], experts, inter, hidden),

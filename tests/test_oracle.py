@@ -475,7 +475,7 @@ def brute_route(logits, top_k):
     for t, row in enumerate(logits.astype(np.float32)):
         e = np.exp(row - row.max()).astype(np.float32)
         p = (e.astype(np.float64) / e.astype(np.float64).sum()).astype(np.float32)
-        order = np.argsort(-p, kind="stable")[:top_k]  # ties: lower expert first
+        order = np.argsort(-p, kind="stable")[:top_k]  # callers keep ties out
         idx[t] = order
         s = np.float32(0)
         for v in p[order]:
@@ -492,26 +492,65 @@ def test_route_hand_case(oracle):
     np.testing.assert_allclose(w, [[4 / 7, 3 / 7], [4 / 7, 3 / 7]], rtol=1e-6)
 
 
-def test_route_ties_and_masked_experts(oracle):
-    logits = np.zeros((3, 6), np.float32)
-    logits[1, [4, 1]] = 2.0
-    logits[2, :] = -np.inf
-    logits[2, 3] = 0.0
+def test_route_ties_follow_the_library_heap(oracle):
+    """Equal probabilities come out in the order of libstdc++'s std::partial_sort (heap
+    selection, then sort_heap), not by expert number.  Worked by hand through the heap
+    steps: with 16 equal probabilities make_heap turns order [0, 1, 2, 3] into
+    [2, 3, 0, 1] and sort_heap pops it as [1, 3, 0, 2]."""
+    logits = np.zeros((2, 16), np.float32)
+    logits[1] = [1, 0, 0, 0, -5, 1, 0, 0, -5, 1, 0, 0, 1, 0, 0, 0]
+    idx, w = oracle.moe_route(logits[:1], 4)
+    assert idx.tolist() == [[1, 3, 0, 2]]
+    np.testing.assert_allclose(w, 0.25, rtol=1e-6)
+    idx, _ = oracle.moe_route(logits[1:, :13], 8)
+    # the four logits of 1 first (heap order), then four of the zeros: expert 7, not 6
+    assert idx.tolist() == [[12, 0, 5, 9, 3, 7, 1, 2]]
+
+
+def test_route_masked_experts(oracle):
+    logits = np.full((1, 6), -np.inf, np.float32)
+    logits[0, 3] = 0.0
     idx, w = oracle.moe_route(logits, 3)
-    assert idx.tolist() == [[0, 1, 2], [1, 4, 0], [3, 0, 1]]
-    np.testing.assert_allclose(w[0], 1 / 3, rtol=1e-6)
-    assert w[2].tolist() == [1.0, 0.0, 0.0]
+    assert idx[0, 0] == 3 and w[0].tolist() == [1.0, 0.0, 0.0]
+
+
+ROUTE_CASES = [(4, 4), (6, 3), (13, 8), (16, 4), (32, 4), (128, 4), (256, 8)]
+
+
+@pytest.mark.parametrize("experts,top_k", ROUTE_CASES)
+def test_route_ties_vs_reference_vectors(oracle, golden, experts, top_k):
+    """Tie-heavy logits (NaN and +-inf in some rows) against std::partial_sort's output
+    recorded from the compiled reference bindings: indices and weights bit for bit."""
+    key = f"route_{experts}_{top_k}"
+    idx, w = oracle.moe_route(golden[f"{key}_logits"], top_k)
+    assert np.array_equal(idx, golden[f"{key}_idx"])
+    assert same_bits(w, golden[f"{key}_w"])
+
+
+def test_route_ties_vs_compiled_library(oracle, reference):
+    """Random tie patterns against std::partial_sort itself, over every expert count
+    from 1 to 140 and top_k up to 8."""
+    rng = np.random.default_rng(77)
+    values = np.array([0, 1, 2, -1, -np.inf, np.nan, np.inf], np.float32)
+    for trial in range(3000):
+        experts = int(rng.integers(1, 141))
+        top_k = int(rng.integers(1, min(experts, 8) + 1))
+        p = [.3, .3, .2, .1, .05, .03, .02] if trial % 3 == 0 else [.4, .3, .2, .1, 0, 0, 0]
+        logits = rng.choice(values, size=(2, experts), p=p).astype(np.float32)
+        a, b = oracle.moe_route(logits, top_k), reference.moe_route(logits, top_k)
+        assert np.array_equal(a[0], b[0]), (logits, top_k)
+        assert same_bits(a[1], b[1])
 
 
 def test_route_orders_by_probability_not_logit(oracle):
     # logits 0 and 1e-8 differ, their float probabilities do not (expf(-1e-8) rounds to
-    # 1): the sort by probability keeps the lower expert first
+    # 1): they tie, and the heap order decides (std::partial_sort over 8 experts, top 3)
     assert np.float32(np.exp(np.float32(-1e-8))) == np.float32(1.0)
     logits = np.full((1, 8), -5.0, np.float32)
     logits[0, [2, 5]] = [0.0, 1e-8]
     logits[0, 6] = 1e-8
     idx, _ = oracle.moe_route(logits, 3)
-    assert idx.tolist() == [[2, 5, 6]]
+    assert sorted(idx[0].tolist()) == [2, 5, 6]
 
 
 @pytest.mark.parametrize("tokens,experts,top_k", [(64, 8, 2), (50, 32, 4), (20, 128, 8)])
@@ -533,6 +572,16 @@ def test_permute_is_stable_sort_by_expert(oracle, tokens, experts, top_k):
     assert np.array_equal(perm, np.argsort(idx.ravel(), kind="stable"))
     assert np.array_equal(offsets, np.concatenate([[0], np.cumsum(np.bincount(idx.ravel(),
                                                                               minlength=experts))]))
+
+
+def test_moe_forward_known_answer(oracle):
+    """The composed layer against a case worked out by hand from MoeLayer::forward's
+    definition (tests/util.py known_answer_moe: 2 tokens x 4 experts, closed form)."""
+    from tests.util import known_answer_moe
+    x, logits, ((gb, gs), (ub, us), (db, ds)), y, idx = known_answer_moe()
+    got, gi, gw, _, _ = oracle.moe_forward(x, logits, 2, gb, gs, ub, us, db, ds)
+    assert np.array_equal(gi, idx)
+    np.testing.assert_allclose(got, y, rtol=1e-6, atol=0)
 
 
 def test_moe_forward_vs_numpy_composition(oracle):

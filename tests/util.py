@@ -1,4 +1,8 @@
-"""Comparison helpers shared by the parity tests."""
+"""Comparison helpers and hand-derived cases shared by the parity tests."""
+import json
+import math
+import os
+
 import numpy as np
 
 # Tolerances of the quantized matmul path for fp32-accumulated outputs (rel-L2, and
@@ -24,6 +28,10 @@ def normalized_max_abs(actual, expected) -> float:
 def assert_close(actual, expected, rel=REL_L2, mabs=MAX_ABS, what=""):
     r = rel_l2(actual, expected)
     m = normalized_max_abs(actual, expected)
+    log = os.environ.get("KDQ_PARITY_LOG")
+    if log and what:  # measured margins, one JSON line per comparison
+        with open(log, "a") as f:
+            f.write(json.dumps({"what": what, "rel_l2": r, "max_abs_over_rms": m}) + "\n")
     assert r <= rel and m <= mabs, f"{what}: rel_l2={r:.3e} (<= {rel}) max_abs/rms={m:.3e} (<= {mabs})"
     return r, m
 
@@ -32,3 +40,51 @@ def bits_equal(a, b) -> bool:
     a = np.ascontiguousarray(a, np.float32).view(np.uint32)
     b = np.ascontiguousarray(b, np.float32).view(np.uint32)
     return a.shape == b.shape and bool(np.array_equal(a, b))
+
+
+def known_answer_moe():
+    """An MXFP4 MoE layer (2 tokens, 4 experts, top-2, hidden = inter = 64) whose output
+    follows in closed form from MoeLayer::forward's definition (IW/src/models/text/
+    qwen_layers.cpp:378-492), computed here in float64 without any of the oracle's code:
+
+      gate_e = 2^-e * ones;  up_e[n, c] = 2^(e % 2) for c < 32, else 0;
+      down_e[d, c] = 2^-(1 + e // 2) * q(d), q(d) = E2M1 value of code 1 + d % 7;
+      x_t[c] = v_t for c < 32, 2 v_t after (v = 1/16, -1/32, exact in bf16);
+      g = 96 v 2^-e,  u = 32 v 2^(e % 2),  h = silu(g) u,  down_d = 64 2^-(1+e//2) q(d) h,
+      y_t[d] = sum_i w_i down_{e_i, d},  w = p / sum of the two chosen p.
+
+    Logits [2, 1, 0, -inf] choose experts 0, 1; [-1, 3, 0.5, 2] choose 1, 3.  A dropped
+    silu, swapped gate/up, a transposed down or a misplaced routing weight each change y.
+    Returns (x bf16 bits, logits, (gate, up, down) as (blocks, scales), y, idx)."""
+    H = I = 64
+    E = 4
+    e2m1 = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]
+    gate_b = np.full((E, I, H // 2), 0x22, np.uint8)
+    gate_s = np.array([[[127 - e] * (H // 32)] * I for e in range(E)], np.uint8)
+    up_b = np.zeros((E, I, H // 2), np.uint8)
+    up_b[:, :, :16] = 0x22
+    up_s = np.array([[[127 + e % 2, 127]] * I for e in range(E)], np.uint8)
+    codes = np.array([1 + d % 7 for d in range(H)], np.uint8)
+    down_b = np.broadcast_to((codes | (codes << 4))[None, :, None], (E, H, I // 2)).copy()
+    down_s = np.array([[[126 - e // 2] * (I // 32)] * H for e in range(E)], np.uint8)
+    v = [1.0 / 16, -1.0 / 32]
+    x = np.zeros((2, H), np.float32)
+    for t in range(2):
+        x[t, :32], x[t, 32:] = v[t], 2 * v[t]
+    x_bits = (x.view(np.uint32) >> 16).astype(np.uint16)  # exact: bf16 keeps these
+    logits = np.array([[2, 1, 0, -np.inf], [-1, 3, 0.5, 2]], np.float32)
+    idx = np.array([[0, 1], [1, 3]], np.int32)
+    y = np.zeros((2, H), np.float64)
+    for t in range(2):
+        top = max(float(l) for l in logits[t])
+        p = [math.exp(float(l) - top) for l in logits[t]]
+        p = [q / sum(p) for q in p]
+        chosen = [p[e] for e in idx[t]]
+        for i, e in enumerate(idx[t]):
+            g = 96 * v[t] * 2.0 ** -e
+            u = 32 * v[t] * 2.0 ** (e % 2)
+            h = g / (1 + math.exp(-g)) * u
+            for d in range(H):
+                down = 64 * 2.0 ** -(1 + e // 2) * e2m1[1 + d % 7] * h
+                y[t, d] += chosen[i] / sum(chosen) * down
+    return x_bits, logits, ((gate_b, gate_s), (up_b, up_s), (down_b, down_s)), y, idx
