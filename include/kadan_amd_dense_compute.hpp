@@ -101,6 +101,13 @@ public:
                                        const std::atomic_bool& cancel, bool precise = false,
                                        bool retain_misses = true);
 
+    // IW/include/kadan/dense_compute.hpp:332-341 (the interface's one pure virtual): plain
+    // F32 projection, weights [out x in] row-major, output [rows x out] = input . W^T +
+    // bias.  Runs the exact-product kernel over F32 rows; nothing is retained.
+    void dense(std::span<const float> weights, std::span<const float> bias,
+               std::span<const float> input, std::size_t in, std::size_t out,
+               std::span<float> output, const std::atomic_bool& cancel, bool precise = false);
+
     // IW/include/kadan/dense_compute.hpp:215-221: every job in one synchronous
     // submission; jobs sharing an input span upload it once.  Returns unvalidated (the
     // caller checks finiteness, IW/src/models/text/gguf_weights.cpp:478-484).

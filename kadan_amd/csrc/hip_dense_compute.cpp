@@ -327,6 +327,53 @@ ProjectionResult HipDenseCompute::dense_gguf_source(
     return finite ? ProjectionResult::finite : ProjectionResult::unvalidated;
 }
 
+void HipDenseCompute::dense(std::span<const float> weights, std::span<const float> bias,
+                            std::span<const float> input, std::size_t in, std::size_t out,
+                            std::span<float> output, const std::atomic_bool& cancel,
+                            bool precise) {
+    (void)precise;  // the product is fp32 either way
+    std::lock_guard<std::mutex> lock(mutex_);
+    require(!cancel.load(), "kdq_cancelled");
+    require(in && out && in <= std::size_t(INT_MAX) && out <= std::size_t(INT_MAX) &&
+                weights.size() == in * out && !input.empty() && input.size() % in == 0 &&
+                output.size() == input.size() / in * out && (bias.empty() || bias.size() == out),
+            "kdq_projection_shape");
+    require(!overlap(output, input) && !overlap(output, bias) && !overlap(output, weights),
+            "kdq_alias");
+    hip_check(hipSetDevice(device_));
+    const std::size_t rows = input.size() / in;
+    // F32 rows of the exact kernel need in % 8 == 0: zero-pad each row (and x) on upload
+    const std::size_t padded = (in + 7) / 8 * 8;
+    auto st = static_cast<hipStream_t>(stream_);
+    auto* dw = static_cast<float*>(device_buffer(5, out * padded * sizeof(float)));
+    auto* dx = static_cast<float*>(device_buffer(0, rows * padded * sizeof(float)));
+    auto* dy = static_cast<float*>(device_buffer(1, rows * out * sizeof(float)));
+    if (padded == in) {
+        hip_check(hipMemcpyAsync(dw, weights.data(), weights.size_bytes(), hipMemcpyHostToDevice,
+                                 st));
+        hip_check(hipMemcpyAsync(dx, input.data(), input.size_bytes(), hipMemcpyHostToDevice, st));
+    } else {
+        hip_check(hipMemsetAsync(dw, 0, out * padded * sizeof(float), st));
+        hip_check(hipMemsetAsync(dx, 0, rows * padded * sizeof(float), st));
+        hip_check(hipMemcpy2DAsync(dw, padded * sizeof(float), weights.data(), in * sizeof(float),
+                                   in * sizeof(float), out, hipMemcpyHostToDevice, st));
+        hip_check(hipMemcpy2DAsync(dx, padded * sizeof(float), input.data(), in * sizeof(float),
+                                   in * sizeof(float), rows, hipMemcpyHostToDevice, st));
+    }
+    for (std::size_t first = 0; first < rows; first += gguf_batch_max_rows) {
+        require(!cancel.load(), "kdq_cancelled");
+        const std::size_t n = std::min(gguf_batch_max_rows, rows - first);
+        kdq_check(kdq_gemv(KDQ_F32, dw, padded * sizeof(float), dx + first * padded, n, padded,
+                           out, dy + first * out, out, nullptr, st));
+    }
+    hip_check(hipMemcpyAsync(output.data(), dy, output.size_bytes(), hipMemcpyDeviceToHost, st));
+    synchronize();
+    if (!bias.empty())
+        for (std::size_t r = 0; r < rows; ++r)
+            for (std::size_t c = 0; c < out; ++c)
+                output[r * out + c] += bias[c];
+}
+
 ProjectionResult HipDenseCompute::dense_gguf_batch(std::span<const GgufBatchJob> jobs,
                                                    const std::atomic_bool& cancel) {
     std::lock_guard<std::mutex> lock(mutex_);
