@@ -282,6 +282,21 @@ int kdq_moe_mxfp4_packed(const uint16_t* x_bf16, const float* logits, size_t tok
                          const uint8_t* down_packed, float* y, int32_t* idx, float* w,
                          int32_t* offsets, int32_t* perm, void* stream);
 
+/* kdq_moe_mxfp4_packed without any allocation.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments, kernels and results
+ * (bit for bit) as kdq_moe_mxfp4_packed; the layer's scratch lives in a static device
+ * array of 64 MiB that each device holds for the life of the process, and a layer whose
+ * scratch does not fit it is refused with KDQ_ERR_SCRATCH (at the C4 geometry, 32
+ * experts of 2880 x 2880: up to 128 tokens; with 128 experts: up to 16 tokens).  It
+ * calls no hipMalloc / hipFree.  Every call on a device shares that device's array:
+ * calls that overlap on one device (other streams, other threads) race. */
+int kdq_moe_mxfp4_packed_noalloc(const uint16_t* x_bf16, const float* logits, size_t tokens,
+                                 size_t hidden, size_t inter, size_t experts, size_t top_k,
+                                 const uint8_t* gate_packed, const uint8_t* up_packed,
+                                 const uint8_t* down_packed, float* y, int32_t* idx,
+                                 float* w, int32_t* offsets, int32_t* perm, void* stream);
+
 /* Frees this thread's current device's cached workspace (synchronizes the device).
  * IW/include/kadan/dense_compute.hpp:66-68 release_scratch counterpart. */
 int kdq_release_scratch(void);

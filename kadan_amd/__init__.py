@@ -75,6 +75,8 @@ _SIGNATURES = {
     "kdq_moe_mxfp4_pack": [_VP, _VP, _SZ, _SZ, _SZ, _VP, _VP],
     "kdq_moe_mxfp4_packed": [_VP, _VP, _SZ, _SZ, _SZ, _SZ, _SZ, _VP, _VP, _VP, _VP, _VP, _VP,
                              _VP, _VP, _VP],
+    "kdq_moe_mxfp4_packed_noalloc": [_VP, _VP, _SZ, _SZ, _SZ, _SZ, _SZ, _VP, _VP, _VP, _VP,
+                                     _VP, _VP, _VP, _VP, _VP],
     "kdq_release_scratch": [],
 }
 _OTHER = {

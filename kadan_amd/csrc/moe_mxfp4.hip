@@ -22,6 +22,7 @@
 #include "kdq_common.hpp"
 
 #include <cmath>
+#include <mutex>
 
 namespace kdq {
 namespace {
@@ -35,6 +36,11 @@ constexpr int kTileRows = 32, kTiles = 2, kItemRows = kTileRows * kTiles;
 constexpr int kGemmWaves = 4;  // wavefronts per grouped-GEMM workgroup, 64 weight rows each
 constexpr int kStepK = 64;     // K values per step: 16 FP4 bytes per lane
 constexpr int kPrologueSlots = 64;  // layers of at most this many slots use prologue_kernel
+}  // namespace
+// Bytes of kdq_moe_mxfp4_packed_noalloc's static scratch (64 MiB: C4 geometry up to 128
+// tokens, 128 experts up to 16 tokens).
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+namespace {
 
 // ------------------------------------------------------------------ routing
 
@@ -1352,6 +1358,42 @@ int launch_layer(const uint16_t* x_bf16, const float* logits, size_t tokens, siz
 }  // namespace
 }  // namespace kdq
 
+// Scratch of kdq_moe_mxfp4_packed_noalloc: a file-scope device array, so that entry point
+// never allocates.  Every device the library runs on holds its own copy until the process
+// ends, and every call on a device shares that copy (calls that overlap on one device
+// race).  The layer's kernels write every scratch byte they later read, so nothing needs
+// clearing between calls.
+static __device__ __align__(256) uint8_t scratch[kdq::kNoAllocScratchBytes];
+
+namespace kdq {
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex noalloc_mutex;
+uint8_t* noalloc_address[kMaxDevices];  // the device address of `scratch`, per device
+
+// The current device's address of `scratch`, looked up once per device with that device
+// current (the host-side name of the array is not a device address).
+int noalloc_scratch(uint8_t** out) {
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess)
+        return hip_failure(e);
+    if (device < 0 || device >= kMaxDevices)
+        return KDQ_ERR_UNSUPPORTED;
+    std::lock_guard<std::mutex> lock(noalloc_mutex);
+    if (!noalloc_address[device]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess)
+            return hip_failure(e);
+        noalloc_address[device] = static_cast<uint8_t*>(p);
+    }
+    *out = noalloc_address[device];
+    return KDQ_OK;
+}
+}  // namespace
+}  // namespace kdq
+
 extern "C" size_t kdq_moe_mxfp4_packed_bytes(size_t experts, size_t rows, size_t cols) {
     if (!experts || !rows || !cols || rows % 32 || cols % 64)
         return 0;
@@ -1380,12 +1422,37 @@ extern "C" int kdq_moe_mxfp4_packed(const uint16_t* x_bf16, const float* logits,
     if (misaligned(gate, 256) || misaligned(up, 256) || misaligned(down, 256))
         return KDQ_ERR_ALIGNMENT;
     const MoeSlices ks = moe_slices(tokens, hidden, inter, experts, top_k);
-    auto* scratch = static_cast<uint8_t*>(
+    auto* work = static_cast<uint8_t*>(
         workspace(moe_scratch_bytes(tokens, hidden, inter, experts, top_k, ks), &rc));
     if (rc)
         return rc;
     return launch_layer(x_bf16, logits, tokens, hidden, inter, experts, top_k, gate, up, down,
-                        y, idx, w, offsets, perm, scratch, ks, static_cast<hipStream_t>(stream));
+                        y, idx, w, offsets, perm, work, ks, static_cast<hipStream_t>(stream));
+}
+
+// The allocation-free variant of kdq_moe_mxfp4_packed: the same kernels, with the layer's
+// scratch in the file-scope device array below instead of the per-device workspace.
+extern "C" int kdq_moe_mxfp4_packed_noalloc(const uint16_t* x_bf16, const float* logits,
+                                            size_t tokens, size_t hidden, size_t inter,
+                                            size_t experts, size_t top_k, const uint8_t* gate,
+                                            const uint8_t* up, const uint8_t* down, float* y,
+                                            int32_t* idx, float* w, int32_t* offsets,
+                                            int32_t* perm, void* stream) {
+    int rc = check_layer(x_bf16, logits, tokens, hidden, inter, experts, top_k, y);
+    if (rc)
+        return rc;
+    if (!gate || !up || !down)
+        return KDQ_ERR_ARGUMENT;
+    if (misaligned(gate, 256) || misaligned(up, 256) || misaligned(down, 256))
+        return KDQ_ERR_ALIGNMENT;
+    const MoeSlices ks = moe_slices(tokens, hidden, inter, experts, top_k);
+    if (moe_scratch_bytes(tokens, hidden, inter, experts, top_k, ks) > kdq::kNoAllocScratchBytes)
+        return KDQ_ERR_SCRATCH;  // the layer's scratch does not fit the static array
+    uint8_t* work = nullptr;
+    if ((rc = kdq::noalloc_scratch(&work)))
+        return rc;
+    return launch_layer(x_bf16, logits, tokens, hidden, inter, experts, top_k, gate, up, down,
+                        y, idx, w, offsets, perm, work, ks, static_cast<hipStream_t>(stream));
 }
 
 // Reference-layout weights: packed into the workspace on every call, then the layer.
