@@ -109,18 +109,25 @@ def time_launches(torch, launch, count: int, reps: int = 1):
     return statistics.median(results)
 
 
-def time_steps(torch, submit, steps: int):
-    """ms per step over `steps` steps issued by `submit(n)` (which enqueues n steps),
-    events on the launch stream."""
+def time_steps(torch, submit, steps: int, reps: int = 10):
+    """ms per step: exactly `steps` steps issued by `submit(n)` (which enqueues n steps),
+    bracketed by synchronizations, split into `reps` back-to-back repetitions of
+    steps // reps launches each (the last takes the remainder), each timed by its own
+    pair of events on the launch stream; the median of the repetitions' per-step times."""
     stream = torch.cuda.current_stream()
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
+    reps = max(1, min(reps, steps))
+    counts = [steps // reps] * reps
+    counts[-1] += steps - sum(counts)
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
     torch.cuda.synchronize()
-    start.record(stream)
-    submit(steps)
-    stop.record(stream)
-    stop.synchronize()
-    return start.elapsed_time(stop) / steps
+    events[0].record(stream)
+    for i, n in enumerate(counts):
+        submit(n)
+        events[i + 1].record(stream)
+    events[-1].synchronize()
+    torch.cuda.synchronize()
+    return statistics.median(events[i].elapsed_time(events[i + 1]) / counts[i]
+                             for i in range(reps))
 
 
 def gemv_bytes(n_in: int, n_out: int, encoding: int) -> int:
@@ -311,9 +318,12 @@ def bench_gemv(torch, encoding, n_in, n_out, steps, warmup, seed, copies=16, per
     fn = kadan_amd.lib().kdq_gemv_packed_batch if packed else kadan_amd.lib().kdq_gemv_batch
     stream = torch.cuda.current_stream().cuda_stream
 
+    issued = [0]  # rotation continues across calls, so every copy is 15 launches old
+
     def submit(n):
-        for i in range(n):
-            status = fn(addresses[i % len(addresses)], per_step, stream)
+        for _ in range(n):
+            status = fn(addresses[issued[0] % len(addresses)], per_step, stream)
+            issued[0] += 1
             if status:
                 kadan_amd.check("kdq_gemv_packed_batch" if packed else "kdq_gemv_batch", status)
 
