@@ -179,6 +179,20 @@ int kdq_gemm_q4_0(const void* weights, size_t n, size_t k, const uint16_t* x_f16
 int kdq_gemm_q4_0_packed(const void* packed, size_t n, size_t k, const uint16_t* x_f16,
                          size_t m, uint16_t* y_f16, void* stream);
 
+/* ---- prefill GEMM for the kadan encodings over the tile-packed bank copy (replaces the
+ * decode-to-F32 tile + cublasSgemm of project<float>, IW/src/cuda/h3_compute.cu:2201-2218,
+ * 2451, behind dense_gguf_source with more than gguf_batch_rows input rows).
+ * y[m x n] fp32 = x[m x k] fp32 . W^T, W = `n` rows of `k` values of Q4_K, Q8_0 or Q6_K
+ * in the tile-packed layout (kdq_gguf_pack: kdq_gguf_packed_bytes(encoding, k, n)
+ * bytes, 16-byte aligned).  Activations are scaled per row by a power of two and rounded
+ * once to fp16; weights are dequantised to fp16 (Q8_0: d * q; Q4_K: q * fp16(d * sc) -
+ * fp16(dmin * m); Q6_K: (q - 32) * fp16(d * sc)); products accumulate in fp32.
+ * k % 256 == 0, k <= 32768; x 16-byte aligned.  `status` (optional, zeroed by the
+ * caller): |= 1 for a non-finite weight scale, |= 2 when a dequantised weight could pass
+ * the fp16 range (those outputs are not to be used: run kdq_gemv_packed instead). */
+int kdq_gemm_packed(int encoding, const void* packed, size_t n, size_t k, const float* x,
+                    size_t m, float* y, unsigned* status, void* stream);
+
 /* The activation quantizer of kdq_gemm_q4_0 on its own (for bit-exact checks):
  * q int8 [m x k], d fp32 [m x k/32]. */
 int kdq_quantize_q8(const uint16_t* x_f16, size_t m, size_t k, int8_t* q, float* d,

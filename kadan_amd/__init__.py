@@ -66,6 +66,7 @@ _SIGNATURES = {
     "kdq_gemv_packed_batch": [_VP, _SZ, _VP],
     "kdq_gemm_q4_0": [_VP, _SZ, _SZ, _VP, _SZ, _VP, _VP],
     "kdq_gemm_q4_0_packed": [_VP, _SZ, _SZ, _VP, _SZ, _VP, _VP],
+    "kdq_gemm_packed": [_I, _VP, _SZ, _SZ, _VP, _SZ, _VP, _VP, _VP],
     "kdq_moe_gguf": [_VP, _VP, _SZ, _VP, _VP, _VP, _VP, _VP],
     "kdq_quantize_q8": [_VP, _SZ, _SZ, _VP, _VP, _VP],
     "kdq_moe_route": [_VP, _SZ, _SZ, _SZ, _VP, _VP, _VP, _VP, _VP],

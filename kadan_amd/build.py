@@ -17,7 +17,8 @@ INCLUDE = os.path.join(ROOT, "include")
 BUILD = os.path.join(ROOT, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-DEVICE_SOURCES = ["capi.hip", "gguf_gemv.hip", "q4_0_gemm.hip", "moe_mxfp4.hip", "moe_gguf.hip"]
+DEVICE_SOURCES = ["capi.hip", "gguf_gemv.hip", "gguf_gemm.hip", "q4_0_gemm.hip", "moe_mxfp4.hip",
+                  "moe_gguf.hip"]
 HOST_SOURCES = ["hip_dense_compute.cpp"]
 LIBRARY = os.path.join(PACKAGE, "libkadan_amd.so")
 HOST_LIBRARY = os.path.join(PACKAGE, "libkadan_amd_host.so")

@@ -162,6 +162,23 @@ def gemm_q4_0_packed(packed: torch.Tensor, x_f16: torch.Tensor, n_out: int,
     return out
 
 
+def gemm_packed(encoding: int, packed: torch.Tensor, x: torch.Tensor, n_out: int,
+                out: torch.Tensor | None = None,
+                status: torch.Tensor | None = None) -> torch.Tensor:
+    """Tile-packed Q4_K / Q8_0 / Q6_K weights (gguf_pack) x fp32 [m, k] -> fp32 [m, n_out]
+    (kdq_gemm_packed, the prefill product)."""
+    _need(packed, torch.uint8, "packed")
+    _need(x, torch.float32, "x")
+    m, k = x.shape
+    if packed.numel() != gguf_packed_bytes(encoding, k, n_out):
+        raise ValueError("packed size does not match (k, n_out)")
+    if out is None:
+        out = torch.empty(m, n_out, dtype=torch.float32, device=x.device)
+    call("kdq_gemm_packed", encoding, packed.data_ptr(), n_out, k, x.data_ptr(), m,
+         out.data_ptr(), _ptr(status), _stream())
+    return out
+
+
 def moe_gguf(spec: dict, x: torch.Tensor, status: torch.Tensor | None = None):
     """GGUF MoE layer (kdq_moe_gguf).  spec: hidden, experts, top_k, ff, shared_ff,
     shared_gate (fp32 device tensor [hidden]) and per tensor name (encoding, uint8 device
@@ -281,6 +298,7 @@ def moe_mxfp4_packed(x_bf16: torch.Tensor, logits: torch.Tensor, top_k: int, int
 
 
 __all__ = ["dequantize", "gemv", "gemv_batch", "quantize_q8", "gemm_q4_0", "gemm_q4_0_packed",
+           "gemm_packed",
            "moe_gguf", "moe_route",
            "mxfp4_dequantize", "moe_mxfp4", "moe_mxfp4_pack", "moe_mxfp4_packed", "lib",
            "BLOCK_BYTES", "BLOCK_VALUES"]
