@@ -366,6 +366,28 @@ def bench_gemm(torch, reps=10, count=20, packed=True):
             "note": "per launch: activation quantize + fp16-MFMA GEMM"}
 
 
+def bench_gemm_gguf(torch, encoding, k, n, m=512, reps=10, count=20, copies=8):
+    """Prefill GEMM for a kadan encoding (kdq_gemm_packed over the tile-packed bank copy):
+    one 512-token chunk x fp32 [m, k] -> fp32 [m, n]; per launch the activation staging
+    kernel and the GEMM."""
+    from kadan_amd import ops, synth
+    w = synth.gguf_weights(encoding, 0xD0 + encoding, n, k)
+    ws = [ops.gguf_pack(encoding, wi, k)
+          for wi in rotated_copies(torch, w, copies, keep_mask(encoding, w.shape), 0xD0)]
+    x = torch.from_numpy(synth.normal(0xD0, 9, m * k).reshape(m, k)).cuda()
+    y = torch.empty(m, n, dtype=torch.float32, device="cuda")
+    launch = lambda i: ops.gemm_packed(encoding, ws[i % copies], x, n, out=y)
+    for i in range(5):
+        launch(i)
+    ms = time_launches(torch, launch, count, reps)
+    tflops = 2.0 * m * k * n / (ms * 1e-3) / 1e12
+    name = {Q4_K: "Q4_K", Q8_0: "Q8_0", Q6_K: "Q6_K"}[encoding]
+    return {"workload": f"{name} prefill GEMM M{m} K{k} N{n} (fp32 in/out, tile-packed weights)",
+            "ms": round(ms, 4), "tflops": round(tflops, 2), "mfma_peak_tflops": FP16_PEAK_TFLOPS,
+            "mfma_frac": round(tflops / FP16_PEAK_TFLOPS, 4),
+            "note": "per launch: activation staging (fp16, row scale) + fp16-MFMA GEMM"}
+
+
 def bench_moe_gguf(torch, rows, reps=10, count=20):
     """The GGUF MoE layer (kdq_moe_gguf) at Qwen3-30B-A3B's geometry: hidden 2048, 128
     experts, top-8, expert ff 768, a 768-wide shared expert; Q4_K expert gate/up, Q6_K
@@ -559,6 +581,11 @@ def main():
                       copies=4)
         if want("c3_q4_0_gemm"):
             extra["c3_q4_0_gemm"] = bench_gemm(torch)
+        for enc, tag in ((Q4_K, "q4_k"), (Q8_0, "q8_0"), (Q6_K, "q6_k")):
+            for k_, n_ in ((4096, 14336), (14336, 4096)):
+                name = f"gemm_{tag}_prefill_{k_}x{n_}"
+                if want(name):
+                    extra[name] = bench_gemm_gguf(torch, enc, k_, n_)
         if want("c3_q4_0_gemm_row_major"):
             extra["c3_q4_0_gemm_row_major"] = bench_gemm(torch, packed=False)
         if want("moe_gguf_t1"):

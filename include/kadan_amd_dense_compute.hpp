@@ -92,7 +92,8 @@ public:
     HipDenseCompute& operator=(const HipDenseCompute&) = delete;
 
     // IW/include/kadan/dense_compute.hpp:180-194.  Rows <= gguf_batch_rows run the
-    // decode-time product; more rows run it per group of gguf_batch_rows.  Bias is added
+    // decode-time product; more rows run the prefill GEMM (kdq_gemm_packed) over packed
+    // Q4_K / Q8_0 / Q6_K weights, else the decode-time product per group.  Bias is added
     // to every output row.  `precise` is accepted for interface parity (fp32 products).
     ProjectionResult dense_gguf_source(const WeightIdentity&, gguf::Encoding,
                                        const GgufWeightSource&, std::span<const float> bias,

@@ -274,6 +274,15 @@ const HipDenseCompute::Resident& HipDenseCompute::weights_for(
     return *slot;
 }
 
+// The prefill GEMM (kdq_gemm_packed) takes packed Q4_K / Q8_0 / Q6_K rows of up to 32K
+// values; the decode-time product takes everything else (and batches of at most
+// gguf_batch_rows rows, where one weight pass serves every row anyway).
+bool gemm_takes(gguf::Encoding enc, std::size_t in, std::size_t rows, bool packed) {
+    return packed && rows > HipDenseCompute::gguf_batch_rows && in % 256 == 0 && in <= 32768 &&
+           (enc == gguf::Encoding::q4_k || enc == gguf::Encoding::q8_0 ||
+            enc == gguf::Encoding::q6_k);
+}
+
 ProjectionResult HipDenseCompute::dense_gguf_source(
     const WeightIdentity& identity, gguf::Encoding enc, const GgufWeightSource& source,
     std::span<const float> bias, std::span<const float> input, std::size_t in, std::size_t out,
@@ -303,17 +312,33 @@ ProjectionResult HipDenseCompute::dense_gguf_source(
     auto* dstatus = static_cast<unsigned*>(device_buffer(2, 256));
     hip_check(hipMemsetAsync(dstatus, 0, sizeof(unsigned), st));
     hip_check(hipMemcpyAsync(dx, input.data(), input.size_bytes(), hipMemcpyHostToDevice, st));
-    for (std::size_t first = 0; first < rows; first += gguf_batch_max_rows) {
-        require(!cancel.load(), "kdq_cancelled");
-        const std::size_t n = std::min(gguf_batch_max_rows, rows - first);
-        kdq_check(w.packed ? kdq_gemv_packed(ggml_type(enc), w.device, dx + first * in, n, in,
-                                             out, dy + first * out, out, dstatus, st)
-                           : kdq_gemv(ggml_type(enc), w.device, w.row_bytes, dx + first * in, n,
-                                      in, out, dy + first * out, out, dstatus, st));
-    }
+    auto decode_product = [&] {
+        for (std::size_t first = 0; first < rows; first += gguf_batch_max_rows) {
+            require(!cancel.load(), "kdq_cancelled");
+            const std::size_t n = std::min(gguf_batch_max_rows, rows - first);
+            kdq_check(w.packed ? kdq_gemv_packed(ggml_type(enc), w.device, dx + first * in, n,
+                                                 in, out, dy + first * out, out, dstatus, st)
+                               : kdq_gemv(ggml_type(enc), w.device, w.row_bytes, dx + first * in,
+                                          n, in, out, dy + first * out, out, dstatus, st));
+        }
+    };
+    // Prefill (the reference's decode-tile + SGEMM path, h3_compute.cu:2201-2218,2451): one
+    // GEMM reads each weight byte once for all rows; its status bit 2 (a dequantised weight
+    // past the fp16 range) sends the rows through the decode-time product instead.
+    const bool gemm = gemm_takes(enc, in, rows, w.packed);
+    if (gemm)
+        kdq_check(kdq_gemm_packed(ggml_type(enc), w.device, out, in, dx, rows, dy, dstatus, st));
+    else
+        decode_product();
     unsigned status = 0;
-    hip_check(hipMemcpyAsync(output.data(), dy, output.size_bytes(), hipMemcpyDeviceToHost, st));
     hip_check(hipMemcpyAsync(&status, dstatus, sizeof status, hipMemcpyDeviceToHost, st));
+    synchronize();
+    if (gemm && (status & 2u) && !(status & 1u)) {
+        hip_check(hipMemsetAsync(dstatus, 0, sizeof(unsigned), st));
+        decode_product();
+        hip_check(hipMemcpyAsync(&status, dstatus, sizeof status, hipMemcpyDeviceToHost, st));
+    }
+    hip_check(hipMemcpyAsync(output.data(), dy, output.size_bytes(), hipMemcpyDeviceToHost, st));
     synchronize();
     require(status == 0, "kdq_nonfinite_weight");
     bool finite = true;
@@ -451,20 +476,34 @@ ProjectionResult HipDenseCompute::dense_gguf_batch(std::span<const GgufBatchJob>
                                   ggml_type(*j.encoding)};
     }
     require(!cancel.load(), "kdq_cancelled");
-    // packed and row-major residents go in one submission each (jobs keep their order
-    // within each; every job writes its own output region)
-    std::vector<kdq_matvec_job> packed_jobs, row_jobs;
-    for (std::size_t i = 0; i < jobs.size(); ++i)
-        (weights[i]->packed ? packed_jobs : row_jobs).push_back(table[i]);
+    // Jobs of more than gguf_batch_rows rows over packed Q4_K / Q8_0 / Q6_K (routed experts
+    // at prefill) run the GEMM, one launch each; the rest go in one submission per layout
+    // (jobs keep their order within each; every job writes its own output region).
+    std::vector<kdq_matvec_job> packed_jobs, row_jobs, gemm_jobs;
+    for (std::size_t i = 0; i < jobs.size(); ++i) {
+        const bool gemm = gemm_takes(*jobs[i].encoding, jobs[i].in, table[i].rows,
+                                     weights[i]->packed);
+        (gemm ? gemm_jobs : weights[i]->packed ? packed_jobs : row_jobs).push_back(table[i]);
+    }
+    for (const auto& j : gemm_jobs)
+        kdq_check(kdq_gemm_packed(j.encoding, j.weights, j.columns, j.in, j.input, j.rows,
+                                  j.output, dstatus, st));
     if (!packed_jobs.empty())
         kdq_check(kdq_gemv_packed_batch(packed_jobs.data(), packed_jobs.size(), st));
     if (!row_jobs.empty())
         kdq_check(kdq_gemv_batch(row_jobs.data(), row_jobs.size(), st));
+    unsigned status = 0;
+    hip_check(hipMemcpyAsync(&status, dstatus, sizeof status, hipMemcpyDeviceToHost, st));
+    synchronize();
+    if (!gemm_jobs.empty() && (status & 2u) && !(status & 1u)) {
+        // a dequantised weight past the fp16 range: the GEMM jobs again, decode-time
+        hip_check(hipMemsetAsync(dstatus, 0, sizeof(unsigned), st));
+        kdq_check(kdq_gemv_packed_batch(gemm_jobs.data(), gemm_jobs.size(), st));
+        hip_check(hipMemcpyAsync(&status, dstatus, sizeof status, hipMemcpyDeviceToHost, st));
+    }
     for (std::size_t i = 0; i < jobs.size(); ++i)
         hip_check(hipMemcpyAsync(jobs[i].output.data(), dy + output_at[i],
                                  jobs[i].output.size_bytes(), hipMemcpyDeviceToHost, st));
-    unsigned status = 0;
-    hip_check(hipMemcpyAsync(&status, dstatus, sizeof status, hipMemcpyDeviceToHost, st));
     synchronize();
     require(status == 0, "kdq_nonfinite_weight");
     return ProjectionResult::unvalidated;

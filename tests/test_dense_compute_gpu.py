@@ -149,7 +149,7 @@ def probe(device):
 
 
 @pytest.mark.parametrize("enc", [Q8_0, Q4_0, Q4_K, Q3_K, Q6_K, IQ4_NL, IQ4_XS, BF16, IQ3_XXS, 21, 22])
-@pytest.mark.parametrize("rows", [1, 3, 8, 20])
+@pytest.mark.parametrize("rows", [1, 3, 8, 20, 200])
 def test_dense_gguf_source_parity_and_bank(probe, oracle, enc, rows):
     n_in, n_out = 1024, 96
     w = synth.gguf_weights(enc, 0xD0 + enc, n_out, n_in)
@@ -216,6 +216,41 @@ def test_dense_gguf_batch_shared_input(probe, oracle):
     assert_close(ys[1], oracle.gemv(Q4_0, wu, x, h, f), what="batch up")
     assert_close(ys[2], oracle.gemv(Q8_0, wd, xf, f, h), what="batch down")
     assert probe.reads == 2 * f + h
+
+
+def test_dense_gguf_batch_row_groups_take_the_gemm(probe, oracle):
+    """Routed-expert jobs at prefill (more than gguf_batch_rows rows, up to
+    gguf_batch_max_rows) over packed Q4_K / Q6_K / Q8_0 run the prefill GEMM; a decode job
+    in the same submission stays on the decode-time product."""
+    h, f = 512, 384
+    x40 = synth.normal(0xE1, 1, 40 * h).reshape(40, h)
+    x16 = synth.normal(0xE2, 1, 16 * h).reshape(16, h)
+    x2 = synth.normal(0xE3, 1, 2 * h).reshape(2, h)
+    x300 = synth.normal(0xE4, 1, 300 * h).reshape(300, h)
+    w1 = synth.gguf_weights(Q4_K, 0xE5, f, h)
+    w2 = synth.gguf_weights(Q6_K, 0xE6, f, h)
+    w3 = synth.gguf_weights(Q8_0, 0xE7, f, h)
+    res, ys = probe.batch([(21, Q4_K, w1, x40, f), (22, Q6_K, w2, x16, f),
+                           (23, Q8_0, w3, x2, f), (24, Q8_0, w3, x300, f)])
+    assert res == UNVALIDATED
+    assert_close(ys[0], oracle.gemv(Q4_K, w1, x40, h, f), what="batch gemm q4_k 40 rows")
+    assert_close(ys[1], oracle.gemv(Q6_K, w2, x16, h, f), what="batch gemm q6_k 16 rows")
+    assert_close(ys[2], oracle.gemv(Q8_0, w3, x2, h, f), what="batch decode q8_0 2 rows")
+    assert_close(ys[3], oracle.gemv(Q8_0, w3, x300, h, f), what="batch gemm q8_0 300 rows")
+
+
+def test_dense_gguf_source_prefill_fp16_range_fallback(probe, oracle):
+    """A block scale whose dequantised weights could pass the fp16 range (d = 1000, codes up
+    to 127) makes the prefill GEMM flag the call, which then runs the decode-time product:
+    the result is still the exact product."""
+    rows, n_in, n_out = 24, 512, 64
+    w = synth.gguf_weights(Q8_0, 0xE8, n_out, n_in).reshape(n_out, -1).copy()
+    big = np.array([1000.0], np.float16).view(np.uint16)[0]
+    w[3, 0], w[3, 1] = big & 255, big >> 8
+    x = synth.normal(0xE9, 1, rows * n_in).reshape(rows, n_in)
+    res, y = probe.gguf(31, Q8_0, w, x, n_out)
+    assert res == FINITE
+    assert_close(y, oracle.gemv(Q8_0, w, x, n_in, n_out), what="prefill fp16-range fallback")
 
 
 def test_dense_gguf_batch_unsupported_job_reads_nothing(probe):
