@@ -24,6 +24,8 @@
 //                      DMA; the fp32 output tile leaves through LDS as whole rows.
 #include "kdq_common.hpp"
 
+#include <algorithm>
+
 namespace kdq {
 namespace {
 
@@ -359,12 +361,18 @@ __global__ __launch_bounds__(256) void stage_kernel(const float* __restrict__ x,
 // `xs` has rows up to the next multiple of 128 tokens (rows past m are computed, never
 // stored).  *status |= 1 for a non-finite weight scale, |= 2 when a dequantised weight
 // could pass the fp16 range (the caller then takes another path).
+//
+// K slices (narrow products, too few tiles for the compute units): workgroup slice `ks`
+// runs groups [ks * per, (ks + 1) * per) and writes its fp32 tile to part[ks] (m x n);
+// reduce_kernel then sums the slices in order.
 template <int ENC>
 __global__ __launch_bounds__(256, 1) void gemm_kernel(const uint16_t* __restrict__ xs,
                                                       const float* __restrict__ sigma,
                                                       const uint8_t* __restrict__ w,
                                                       unsigned m, unsigned n, unsigned k,
+                                                      unsigned slices, unsigned per,
                                                       float* __restrict__ y,
+                                                      float* __restrict__ part,
                                                       unsigned* __restrict__ status) {
     using F = GemmFormat<ENC>;
     using Regs = typename F::Regs;
@@ -373,13 +381,18 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const uint16_t* __restrict
 
     const unsigned groups = k / 256, wtiles = (n + 15) / 16;
     const unsigned m_tiles = (m + PM - 1) / PM, n_tiles = (wtiles + kTiles - 1) / kTiles;
-    // XCD-aware order: the M tiles of one weight tile run together on one XCD (L2).
+    // XCD-aware order: the M tiles of one weight tile (and K slice) run together on one
+    // XCD (L2).
     const unsigned id = blockIdx.x, xcd = id % 8, local = id / 8;
-    const unsigned per_xcd = (m_tiles * n_tiles + 7) / 8;
+    const unsigned per_xcd = (m_tiles * n_tiles * slices + 7) / 8;
     const unsigned linear = xcd * per_xcd + local;
-    if (local >= per_xcd || linear >= m_tiles * n_tiles)
+    if (local >= per_xcd || linear >= m_tiles * n_tiles * slices)
         return;
-    const unsigned n_tile = linear / m_tiles, m0 = (linear % m_tiles) * PM;
+    const unsigned n_tile = linear / (m_tiles * slices);
+    const unsigned slice = (linear / m_tiles) % slices, m0 = (linear % m_tiles) * PM;
+    // slices = ceil(groups / per), so every slice has at least one group
+    const unsigned g_begin = slice * per, g_end = min(groups, g_begin + per);
+    float* __restrict__ dst_base = slices > 1 ? part + size_t(slice) * m * n : y;
 
     const unsigned wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const unsigned lane = threadIdx.x % 64;
@@ -499,10 +512,10 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const uint16_t* __restrict
     // rb; each compute issues the other buffer's loads.  After the last pair the prefetch
     // reloads the last group (consumed only when the group count is odd).
     Regs ra[NB], rb[NB];
-    const unsigned last = groups - 1;
-    issue_all(0, 0, ra);
-    unsigned g = 0;
-    for (; g + 1 < groups; g += 2) {
+    const unsigned last = g_end - 1;
+    issue_all(g_begin, 0, ra);
+    unsigned g = g_begin;
+    for (; g + 1 < g_end; g += 2) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         compute(0, ra, g + 1, 1, rb);
@@ -511,7 +524,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const uint16_t* __restrict
         compute(1, rb, min(g + 2, last), 0, ra);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA outlives the workgroup
-    if (g < groups) {  // odd group count: the last group sits in buffer 0 / ra
+    if (g < g_end) {  // odd group count: the last group sits in buffer 0 / ra
         __syncthreads();
         compute(0, ra, last, 1, rb);  // its prefetch reloads the last group (never used)
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -546,7 +559,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const uint16_t* __restrict
         if (tok >= m || f >= n)
             continue;
         const float4 v = *reinterpret_cast<const float4*>(lds + t * kOutPitch + 16 * ch);
-        float* dst = y + size_t(tok) * n + f;
+        float* dst = dst_base + size_t(tok) * n + f;
         if (f + 3 < n && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
             *reinterpret_cast<float4*>(dst) = v;
         } else {
@@ -564,17 +577,60 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const uint16_t* __restrict
     }
 }
 
+// y[i] = sum of the K slices' partials part[s][i] in slice order (4 values per thread).
+__global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ part,
+                                                     size_t count, unsigned slices,
+                                                     float* __restrict__ y) {
+    const size_t i = (size_t(blockIdx.x) * 256 + threadIdx.x) * 4;
+    if (i >= count)
+        return;
+    if (i + 4 <= count && (count % 4) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0) {
+        float4 acc = *reinterpret_cast<const float4*>(part + i);
+        for (unsigned s = 1; s < slices; ++s) {
+            const float4 v = *reinterpret_cast<const float4*>(part + size_t(s) * count + i);
+            acc = make_float4(acc.x + v.x, acc.y + v.y, acc.z + v.z, acc.w + v.w);
+        }
+        *reinterpret_cast<float4*>(y + i) = acc;
+    } else {
+        for (size_t j = i; j < i + 4 && j < count; ++j) {
+            float acc = part[j];
+            for (unsigned s = 1; s < slices; ++s)
+                acc += part[size_t(s) * count + j];
+            y[j] = acc;
+        }
+    }
+}
+
+// K slices: enough workgroups for the compute units when the output tiles are few, each
+// slice at least 8 groups (2048 values) deep.
+// Returns the groups per slice; the slice count is ceil(groups / per) (no empty slice).
+unsigned gemm_slice_depth(size_t m, size_t n, size_t k) {
+    const size_t groups = k / 256;
+    const size_t tiles = ((m + PM - 1) / PM) * (((n + 15) / 16 + kTiles - 1) / kTiles);
+    const size_t units = compute_units();
+    if (tiles * 3 >= units * 2)
+        return unsigned(groups);
+    size_t ks = std::max<size_t>(1, units / tiles);
+    ks = std::min(ks, std::max<size_t>(1, groups / 8));
+    return unsigned((groups + ks - 1) / ks);
+}
+
 template <int ENC>
 int launch_gemm(const float* x, const uint8_t* packed, size_t m, size_t n, size_t k, float* y,
                 unsigned* status, hipStream_t st) {
     int rc;
     const size_t m_pad = (m + PM - 1) / PM * PM;
     const size_t xs_bytes = (m_pad * k * 2 + 255) & ~size_t(255);
-    auto* base = static_cast<uint8_t*>(workspace(xs_bytes + m * 4, &rc));
+    const size_t sig_bytes = (m * 4 + 255) & ~size_t(255);
+    const unsigned per = gemm_slice_depth(m, n, k);
+    const unsigned slices = unsigned((k / 256 + per - 1) / per);
+    const size_t part_bytes = slices > 1 ? size_t(slices) * m * n * 4 : 0;
+    auto* base = static_cast<uint8_t*>(workspace(xs_bytes + sig_bytes + part_bytes, &rc));
     if (rc)
         return rc;
     auto* xs = reinterpret_cast<uint16_t*>(base);
     auto* sigma = reinterpret_cast<float*>(base + xs_bytes);
+    auto* part = slices > 1 ? reinterpret_cast<float*>(base + xs_bytes + sig_bytes) : nullptr;
     static bool configured = false;  // one attribute call per instantiation
     if (!configured) {
         KDQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&stage_kernel<ENC>),
@@ -587,11 +643,17 @@ int launch_gemm(const float* x, const uint8_t* packed, size_t m, size_t n, size_
                        unsigned(k), xs, sigma);
     KDQ_HIP(hipGetLastError());
     const size_t wtiles = (n + 15) / 16;
-    const size_t tiles = (m_pad / PM) * ((wtiles + kTiles - 1) / kTiles);
+    const size_t tiles = (m_pad / PM) * ((wtiles + kTiles - 1) / kTiles) * slices;
     const unsigned grid = unsigned((tiles + 7) / 8 * 8);
     hipLaunchKernelGGL(gemm_kernel<ENC>, dim3(grid), dim3(256), kLds, st, xs, sigma, packed,
-                       unsigned(m), unsigned(n), unsigned(k), y, status);
+                       unsigned(m), unsigned(n), unsigned(k), slices, per, y, part, status);
     KDQ_HIP(hipGetLastError());
+    if (slices > 1) {
+        const size_t count = m * n;
+        hipLaunchKernelGGL(reduce_kernel, dim3(unsigned((count / 4 + 256) / 256)), dim3(256), 0,
+                           st, part, count, slices, y);
+        KDQ_HIP(hipGetLastError());
+    }
     return KDQ_OK;
 }
 

@@ -50,8 +50,11 @@ def run(device, oracle, enc, m, k, n, seed, cols=None):
 
 @pytest.mark.parametrize("enc", ENCODINGS)
 @pytest.mark.parametrize("m,k,n", [(1, 256, 16), (9, 512, 40), (130, 1024, 300),
-                                   (129, 768, 257), (256, 2048, 512)])
+                                   (129, 768, 257), (256, 2048, 512), (64, 6912, 520),
+                                   (200, 4352, 96)])
 def test_gemm_small_shapes(device, oracle, enc, m, k, n):
+    """(64, 6912, 520) and (200, 4352, 96) have few output tiles: they run K slices (three
+    slices of 9 of the 27 groups; two slices of 9 and 8 of 17) and the ordered slice sum."""
     run(device, oracle, enc, m, k, n, seed=0x9E + m + n)
 
 
