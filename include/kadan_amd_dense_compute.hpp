@@ -133,6 +133,13 @@ public:
                                std::span<std::int32_t> selected, std::span<float> weights,
                                const std::atomic_bool& cancel);
 
+    // Whole packed rows of `in` values decoded on the device exactly as kadan::gguf::decode
+    // (kdq_dequantize), output [rows x in]; throws "kdq_nonfinite_weight" when a decoded
+    // value is not finite (the reference's gguf_nonfinite_weight check of read_rows,
+    // IW/src/weights/gguf_checkpoint.cpp:628-636).
+    void dequantize_rows(gguf::Encoding, std::span<const std::byte> packed, std::size_t in,
+                         std::span<float> output);
+
     // IW/include/kadan/dense_compute.hpp:72-80: retire these identities from the bank.
     std::size_t release_weights(std::span<const WeightIdentity>);
     // Device bytes held by the weight bank.

@@ -19,7 +19,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 DEVICE_SOURCES = ["capi.hip", "gguf_gemv.hip", "gguf_gemm.hip", "q4_0_gemm.hip", "moe_mxfp4.hip",
                   "moe_gguf.hip"]
-HOST_SOURCES = ["hip_dense_compute.cpp"]
+HOST_SOURCES = ["hip_dense_compute.cpp", "checkpoint.cpp"]
 LIBRARY = os.path.join(PACKAGE, "libkadan_amd.so")
 HOST_LIBRARY = os.path.join(PACKAGE, "libkadan_amd_host.so")
 PROBE_SOURCE = os.path.join(ROOT, "tests", "cpp", "dense_compute_probe.cpp")

@@ -399,6 +399,32 @@ void HipDenseCompute::dense(std::span<const float> weights, std::span<const floa
                 output[r * out + c] += bias[c];
 }
 
+void HipDenseCompute::dequantize_rows(gguf::Encoding enc, std::span<const std::byte> packed,
+                                      std::size_t in, std::span<float> output) {
+    std::lock_guard<std::mutex> lock(mutex_);
+    require(gguf::supported(enc) && in && in % gguf::block_values(enc) == 0,
+            "kdq_projection_shape");
+    const std::size_t row_bytes = in / gguf::block_values(enc) * gguf::block_bytes(enc);
+    require(packed.size() % row_bytes == 0 && output.size() == packed.size() / row_bytes * in,
+            "kdq_projection_shape");
+    if (packed.empty())
+        return;
+    hip_check(hipSetDevice(device_));
+    auto st = static_cast<hipStream_t>(stream_);
+    const std::size_t rows = packed.size() / row_bytes;
+    auto* dw = static_cast<std::uint8_t*>(device_buffer(5, packed.size()));
+    auto* dy = static_cast<float*>(device_buffer(1, output.size_bytes()));
+    auto* dstatus = static_cast<unsigned*>(device_buffer(2, 256));
+    hip_check(hipMemsetAsync(dstatus, 0, sizeof(unsigned), st));
+    hip_check(hipMemcpyAsync(dw, packed.data(), packed.size(), hipMemcpyHostToDevice, st));
+    kdq_check(kdq_dequantize(ggml_type(enc), dw, row_bytes, rows, in, dy, dstatus, st));
+    unsigned status = 0;
+    hip_check(hipMemcpyAsync(output.data(), dy, output.size_bytes(), hipMemcpyDeviceToHost, st));
+    hip_check(hipMemcpyAsync(&status, dstatus, sizeof status, hipMemcpyDeviceToHost, st));
+    synchronize();
+    require(status == 0, "kdq_nonfinite_weight");
+}
+
 ProjectionResult HipDenseCompute::dense_gguf_batch(std::span<const GgufBatchJob> jobs,
                                                    const std::atomic_bool& cancel) {
     std::lock_guard<std::mutex> lock(mutex_);
