@@ -19,6 +19,7 @@
 #include <map>
 #include <memory>
 #include <mutex>
+#include <thread>
 #include <optional>
 #include <span>
 #include <tuple>
@@ -140,6 +141,13 @@ public:
     void dequantize_rows(gguf::Encoding, std::span<const std::byte> packed, std::size_t in,
                          std::span<float> output);
 
+    // The weight bank's device byte limit (0: none), the DeviceWeights envelope of the
+    // reference (IW/include/kadan/device_weights.hpp:35-60,203-206).  A miss that would
+    // pass it is not admitted and evicts nothing: dense_gguf_source streams it (existing
+    // hits stay resident), a batch job holds it for the call only.  MoE expert sets count
+    // against the limit but are always admitted.
+    void set_weight_limit(std::size_t bytes);
+
     // IW/include/kadan/dense_compute.hpp:72-80: retire these identities from the bank.
     std::size_t release_weights(std::span<const WeightIdentity>);
     // Device bytes held by the weight bank.
@@ -149,15 +157,29 @@ public:
 
 private:
     struct Resident;
+    struct ReadTeam;
     using BankKey = std::tuple<WeightIdentity, int, std::size_t, std::size_t>;
 
     // The resident weights of one projection, uploaded through the pinned staging on a
     // miss.  `product`: for the decode GEMV or the prefill GEMM (tile-packed where the
-    // packed GEMV takes the shape, one copy for both), else row-major rows.
-    const Resident& weights_for(const WeightIdentity&, gguf::Encoding, std::size_t in,
+    // packed GEMV takes the shape, one copy for both), else row-major rows.  Returns
+    // nullptr when `stream_miss` is set and the weights are not in the bank, or would
+    // not fit its limit (the caller then streams them, stream_product).
+    const Resident* weights_for(const WeightIdentity&, gguf::Encoding, std::size_t in,
                                 std::size_t out, const GgufWeightSource&, bool retain,
                                 const std::atomic_bool& cancel,
-                                std::unique_ptr<Resident>& transient, bool product);
+                                std::unique_ptr<Resident>& transient, bool product,
+                                bool stream_miss = false);
+    // Reads rows [first, first + n) of `source` into pinned staging buffer `b` with the read
+    // team, after the device has finished with that buffer's previous chunk.
+    std::byte* stage_rows(unsigned b, const GgufWeightSource&, std::size_t first, std::size_t n,
+                          std::size_t row_bytes);
+    void staged(unsigned b);  // the device's reads of staging buffer b are enqueued
+    // y[rows x out] = x . W^T with W streamed chunk by chunk through the staging buffers
+    // (reads of one chunk overlap the upload, packing and product of the previous).
+    void stream_product(gguf::Encoding, std::size_t in, std::size_t out, std::size_t rows,
+                        const GgufWeightSource&, const float* dx, float* dy, unsigned* dstatus,
+                        const std::atomic_bool& cancel, bool gemm);
     void* device_buffer(std::size_t slot, std::size_t bytes);
     void synchronize();
 
@@ -166,8 +188,12 @@ private:
     mutable std::mutex mutex_;
     std::map<BankKey, std::unique_ptr<Resident>> bank_;
     std::vector<std::pair<void*, std::size_t>> buffers_;  // reusable device scratch
-    void* pinned_ = nullptr;
+    void* pinned_[2] = {nullptr, nullptr};  // double-buffered host staging
     std::size_t pinned_bytes_ = 0;
+    void* staged_[2] = {nullptr, nullptr};  // hipEvent_t: the device is done with pinned_[b]
+    bool staged_pending_[2] = {false, false};
+    std::unique_ptr<ReadTeam> team_;
+    std::size_t weight_limit_ = 0;
 };
 
 }  // namespace kadan_amd

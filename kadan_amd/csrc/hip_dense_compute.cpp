@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <condition_variable>
+#include <exception>
 #include <climits>
 #include <cmath>
 #include <cstring>
@@ -175,23 +177,138 @@ struct HipDenseCompute::Resident {
     }
 };
 
+// Three persistent host threads and the caller read one staging chunk's disjoint whole
+// rows from the weight source in parallel (the source contract allows concurrent calls
+// on disjoint rows, IW/include/kadan/dense_compute.hpp:174-179), as the reference's
+// PackedReadTeam does (IW/include/kadan/packed_read_team.hpp:24-134).  Small chunks are
+// read by the caller alone.
+struct HipDenseCompute::ReadTeam {
+    static constexpr std::size_t kParallelBytes = std::size_t(2) << 20;
+    static constexpr int kWorkers = 3;
+
+    ReadTeam() {
+        for (int i = 0; i < kWorkers; ++i)
+            threads_.emplace_back([this, i] { run(i); });
+    }
+    ~ReadTeam() {
+        {
+            std::lock_guard<std::mutex> lock(mutex_);
+            closing_ = true;
+        }
+        ready_.notify_all();
+        for (auto& t : threads_)
+            t.join();
+    }
+
+    void read(const GgufWeightSource& source, std::size_t first, std::size_t row_bytes,
+              std::span<std::byte> dst) {
+        const std::size_t rows = dst.size() / row_bytes;
+        if (dst.size() < kParallelBytes || rows < kWorkers + 1) {
+            source(first, dst);
+            return;
+        }
+        {
+            std::lock_guard<std::mutex> lock(mutex_);
+            source_ = &source;
+            first_ = first;
+            row_bytes_ = row_bytes;
+            dst_ = dst;
+            rows_ = rows;
+            remaining_ = kWorkers;
+            for (auto& e : errors_)
+                e = nullptr;
+            ++round_;
+        }
+        ready_.notify_all();
+        std::exception_ptr mine;
+        try {
+            part(kWorkers);
+        } catch (...) {
+            mine = std::current_exception();
+        }
+        std::unique_lock<std::mutex> lock(mutex_);
+        done_.wait(lock, [&] { return remaining_ == 0; });
+        source_ = nullptr;
+        if (mine)
+            std::rethrow_exception(mine);
+        for (auto& e : errors_)
+            if (e)
+                std::rethrow_exception(e);
+    }
+
+private:
+    // part k of kWorkers + 1 contiguous row ranges
+    void part(int k) {
+        const std::size_t a = rows_ * std::size_t(k) / (kWorkers + 1);
+        const std::size_t b = rows_ * std::size_t(k + 1) / (kWorkers + 1);
+        if (b > a)
+            (*source_)(first_ + a, dst_.subspan(a * row_bytes_, (b - a) * row_bytes_));
+    }
+    void run(int k) {
+        std::uint64_t seen = 0;
+        for (;;) {
+            {
+                std::unique_lock<std::mutex> lock(mutex_);
+                ready_.wait(lock, [&] { return closing_ || round_ != seen; });
+                if (closing_)
+                    return;
+                seen = round_;
+            }
+            std::exception_ptr error;
+            try {
+                part(k);
+            } catch (...) {
+                error = std::current_exception();
+            }
+            {
+                std::lock_guard<std::mutex> lock(mutex_);
+                errors_[k] = error;
+                --remaining_;
+            }
+            done_.notify_all();
+        }
+    }
+
+    std::vector<std::thread> threads_;
+    std::mutex mutex_;
+    std::condition_variable ready_, done_;
+    bool closing_ = false;
+    std::uint64_t round_ = 0;
+    const GgufWeightSource* source_ = nullptr;
+    std::size_t first_ = 0, row_bytes_ = 0, rows_ = 0;
+    std::span<std::byte> dst_;
+    int remaining_ = 0;
+    std::exception_ptr errors_[kWorkers];
+};
+
 HipDenseCompute::HipDenseCompute(int device) : device_(device) {
     hip_check(hipSetDevice(device));
     hipStream_t s = nullptr;
     hip_check(hipStreamCreate(&s));  // default priority
     stream_ = s;
+    for (auto& e : staged_) {
+        hipEvent_t ev = nullptr;
+        hip_check(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+        e = ev;
+    }
+    team_ = std::make_unique<ReadTeam>();
 }
 
 HipDenseCompute::~HipDenseCompute() {
     (void)hipSetDevice(device_);
     if (stream_)
         (void)hipStreamSynchronize(static_cast<hipStream_t>(stream_));
+    team_.reset();
     bank_.clear();
     for (auto& b : buffers_)
         if (b.first)
             (void)hipFree(b.first);
-    if (pinned_)
-        (void)hipHostFree(pinned_);
+    for (auto* p : pinned_)
+        if (p)
+            (void)hipHostFree(p);
+    for (auto* e : staged_)
+        if (e)
+            (void)hipEventDestroy(static_cast<hipEvent_t>(e));
     if (stream_)
         (void)hipStreamDestroy(static_cast<hipStream_t>(stream_));
 }
@@ -216,62 +333,157 @@ void* HipDenseCompute::device_buffer(std::size_t slot, std::size_t bytes) {
     return b.first;
 }
 
-const HipDenseCompute::Resident& HipDenseCompute::weights_for(
+void HipDenseCompute::set_weight_limit(std::size_t bytes) {
+    std::lock_guard<std::mutex> lock(mutex_);
+    weight_limit_ = bytes;
+}
+
+std::byte* HipDenseCompute::stage_rows(unsigned b, const GgufWeightSource& source,
+                                       std::size_t first, std::size_t n, std::size_t row_bytes) {
+    const std::size_t need = std::max(kStagingBytes, n * row_bytes);
+    if (pinned_bytes_ < need) {
+        synchronize();  // no copy may still read the old buffers
+        for (auto& p : pinned_) {
+            if (p)
+                hip_check(hipHostFree(p));
+            p = nullptr;
+        }
+        pinned_bytes_ = 0;
+        for (auto& p : pinned_)
+            hip_check(hipHostMalloc(&p, need, hipHostMallocDefault));
+        pinned_bytes_ = need;
+        staged_pending_[0] = staged_pending_[1] = false;
+    }
+    if (staged_pending_[b]) {  // the upload of this buffer's previous chunk is done
+        hip_check(hipEventSynchronize(static_cast<hipEvent_t>(staged_[b])));
+        staged_pending_[b] = false;
+    }
+    auto* bytes = static_cast<std::byte*>(pinned_[b]);
+    team_->read(source, first, row_bytes, std::span<std::byte>(bytes, n * row_bytes));
+    return bytes;
+}
+
+void HipDenseCompute::staged(unsigned b) {
+    hip_check(hipEventRecord(static_cast<hipEvent_t>(staged_[b]),
+                             static_cast<hipStream_t>(stream_)));
+    staged_pending_[b] = true;
+}
+
+const HipDenseCompute::Resident* HipDenseCompute::weights_for(
     const WeightIdentity& identity, gguf::Encoding enc, std::size_t in, std::size_t out,
     const GgufWeightSource& source, bool retain, const std::atomic_bool& cancel,
-    std::unique_ptr<Resident>& transient, bool product) {
+    std::unique_ptr<Resident>& transient, bool product, bool stream_miss) {
     // Products (decode GEMV and prefill GEMM) keep the tile-packed layout when the packed
     // GEMV takes the shape, so one resident copy serves both; the layout is part of the
     // bank key.
     const bool packed = product && kdq_gemv_packed_supported(ggml_type(enc), in);
     const BankKey key{identity, 2 * int(enc) + (packed ? 1 : 0), in, out};
     if (auto it = bank_.find(key); it != bank_.end())
-        return *it->second;
+        return it->second.get();
     const std::size_t row_bytes = in / gguf::block_values(enc) * gguf::block_bytes(enc);
+    const std::size_t bytes =
+        packed ? kdq_gguf_packed_bytes(ggml_type(enc), in, out) : out * row_bytes;
+    if (retain && weight_limit_) {
+        // the reference's envelope refusal (IW/include/kadan/device_weights.hpp:203-206):
+        // a miss that would pass the limit is not admitted, and nothing is evicted for it
+        std::size_t used = 0;
+        for (const auto& [k, r] : bank_)
+            used += r->bytes;
+        retain = used <= weight_limit_ && bytes <= weight_limit_ - used;
+    }
+    if (!retain && stream_miss)
+        return nullptr;
     auto r = std::make_unique<Resident>();
     r->row_bytes = row_bytes;
     r->packed = packed;
-    r->bytes = packed ? kdq_gguf_packed_bytes(ggml_type(enc), in, out) : out * row_bytes;
+    r->bytes = bytes;
     hip_check(hipMalloc(&r->device, r->bytes));
-    // chunks of whole 16-row tiles when packing (each chunk packs into its own tiles)
+    // chunks of whole 16-row tiles when packing (each chunk packs into its own tiles);
+    // the reads of chunk c + 1 overlap the upload and packing of chunk c
     std::size_t rows_per_chunk = std::max<std::size_t>(1, kStagingBytes / row_bytes);
     if (packed)
         rows_per_chunk = std::max<std::size_t>(16, rows_per_chunk / 16 * 16);
-    const std::size_t chunk_bytes = std::min(out, rows_per_chunk) * row_bytes;
-    if (pinned_bytes_ < chunk_bytes) {
-        if (pinned_)
-            hip_check(hipHostFree(pinned_));
-        pinned_ = nullptr;
-        pinned_bytes_ = 0;
-        hip_check(hipHostMalloc(&pinned_, chunk_bytes, hipHostMallocDefault));
-        pinned_bytes_ = chunk_bytes;
-    }
     const std::size_t tile_bytes = packed ? kdq_gguf_packed_bytes(ggml_type(enc), in, 16) : 0;
-    auto* raw = packed ? static_cast<std::uint8_t*>(device_buffer(4, chunk_bytes)) : nullptr;
-    auto* bytes = static_cast<std::byte*>(pinned_);
     auto st = static_cast<hipStream_t>(stream_);
-    for (std::size_t first = 0; first < out; first += rows_per_chunk) {
-        require(!cancel.load(), "kdq_cancelled");
-        const std::size_t n = std::min(rows_per_chunk, out - first);
-        source(first, std::span<std::byte>(bytes, n * row_bytes));
-        if (packed) {
-            hip_check(hipMemcpyAsync(raw, pinned_, n * row_bytes, hipMemcpyHostToDevice, st));
-            kdq_check(kdq_gguf_pack(ggml_type(enc), raw, row_bytes, in, n,
-                                    static_cast<std::uint8_t*>(r->device) + first / 16 * tile_bytes,
-                                    st));
-        } else {
-            hip_check(hipMemcpyAsync(static_cast<std::uint8_t*>(r->device) + first * row_bytes,
-                                     pinned_, n * row_bytes, hipMemcpyHostToDevice, st));
+    try {
+        unsigned b = 0;
+        for (std::size_t first = 0; first < out; first += rows_per_chunk, b ^= 1) {
+            require(!cancel.load(), "kdq_cancelled");
+            const std::size_t n = std::min(rows_per_chunk, out - first);
+            std::byte* host = stage_rows(b, source, first, n, row_bytes);
+            if (packed) {
+                auto* raw = static_cast<std::uint8_t*>(device_buffer(6 + b, n * row_bytes));
+                hip_check(hipMemcpyAsync(raw, host, n * row_bytes, hipMemcpyHostToDevice, st));
+                staged(b);
+                kdq_check(kdq_gguf_pack(ggml_type(enc), raw, row_bytes, in, n,
+                                        static_cast<std::uint8_t*>(r->device) +
+                                            first / 16 * tile_bytes,
+                                        st));
+            } else {
+                hip_check(hipMemcpyAsync(static_cast<std::uint8_t*>(r->device) + first * row_bytes,
+                                         host, n * row_bytes, hipMemcpyHostToDevice, st));
+                staged(b);
+            }
         }
-        synchronize();  // the staging buffers are reused by the next chunk
+    } catch (...) {
+        (void)hipStreamSynchronize(st);  // nothing in flight reads what unwinding frees
+        throw;
     }
     if (!retain) {
         transient = std::move(r);
-        return *transient;
+        return transient.get();
     }
     auto& slot = bank_[key];
     slot = std::move(r);
-    return *slot;
+    return slot.get();
+}
+
+void HipDenseCompute::stream_product(gguf::Encoding enc, std::size_t in, std::size_t out,
+                                     std::size_t rows, const GgufWeightSource& source,
+                                     const float* dx, float* dy, unsigned* dstatus,
+                                     const std::atomic_bool& cancel, bool gemm) {
+    const bool packed = kdq_gemv_packed_supported(ggml_type(enc), in);
+    const std::size_t row_bytes = in / gguf::block_values(enc) * gguf::block_bytes(enc);
+    std::size_t rows_per_chunk = std::max<std::size_t>(1, kStagingBytes / row_bytes);
+    if (packed)
+        rows_per_chunk = std::max<std::size_t>(16, rows_per_chunk / 16 * 16);
+    rows_per_chunk = std::min(rows_per_chunk, out);
+    auto st = static_cast<hipStream_t>(stream_);
+    try {
+        unsigned b = 0;
+        for (std::size_t first = 0; first < out; first += rows_per_chunk, b ^= 1) {
+            require(!cancel.load(), "kdq_cancelled");
+            const std::size_t n = std::min(rows_per_chunk, out - first);
+            std::byte* host = stage_rows(b, source, first, n, row_bytes);
+            auto* raw = static_cast<std::uint8_t*>(device_buffer(6 + b, n * row_bytes));
+            hip_check(hipMemcpyAsync(raw, host, n * row_bytes, hipMemcpyHostToDevice, st));
+            staged(b);
+            const void* w = raw;
+            if (packed) {
+                auto* pk = static_cast<std::uint8_t*>(
+                    device_buffer(8 + b, kdq_gguf_packed_bytes(ggml_type(enc), in, n)));
+                kdq_check(kdq_gguf_pack(ggml_type(enc), raw, row_bytes, in, n, pk, st));
+                w = pk;
+            }
+            if (gemm) {  // columns [first, first + n) of y through a [rows x n] tile
+                auto* tile = static_cast<float*>(device_buffer(10 + b, rows * n * 4));
+                kdq_check(kdq_gemm_packed(ggml_type(enc), w, n, in, dx, rows, tile, dstatus, st));
+                hip_check(hipMemcpy2DAsync(dy + first, out * 4, tile, n * 4, n * 4, rows,
+                                           hipMemcpyDeviceToDevice, st));
+            } else {
+                for (std::size_t r0 = 0; r0 < rows; r0 += gguf_batch_max_rows) {
+                    const std::size_t m = std::min(gguf_batch_max_rows, rows - r0);
+                    kdq_check(packed ? kdq_gemv_packed(ggml_type(enc), w, dx + r0 * in, m, in, n,
+                                                       dy + r0 * out + first, out, dstatus, st)
+                                     : kdq_gemv(ggml_type(enc), w, row_bytes, dx + r0 * in, m,
+                                                in, n, dy + r0 * out + first, out, dstatus, st));
+                }
+            }
+        }
+    } catch (...) {
+        (void)hipStreamSynchronize(st);
+        throw;
+    }
 }
 
 // The prefill GEMM (kdq_gemm_packed) takes packed Q4_K / Q8_0 / Q6_K rows of up to 32K
@@ -303,31 +515,41 @@ ProjectionResult HipDenseCompute::dense_gguf_source(
     require(!overlap(output, input) && !overlap(output, bias), "kdq_alias");
     hip_check(hipSetDevice(device_));
     const std::size_t rows = input.size() / in;
-    std::unique_ptr<Resident> transient;
-    const Resident& w = weights_for(identity, enc, in, out, source, retain_misses, cancel, transient,
-                                    true);
     auto st = static_cast<hipStream_t>(stream_);
     auto* dx = static_cast<float*>(device_buffer(0, rows * in * sizeof(float)));
     auto* dy = static_cast<float*>(device_buffer(1, rows * out * sizeof(float)));
     auto* dstatus = static_cast<unsigned*>(device_buffer(2, 256));
     hip_check(hipMemsetAsync(dstatus, 0, sizeof(unsigned), st));
     hip_check(hipMemcpyAsync(dx, input.data(), input.size_bytes(), hipMemcpyHostToDevice, st));
+    // A miss that is not to be retained (or does not fit the bank's limit) is streamed: the
+    // reference "keeps existing hits and streams uncached tiles" (dense_compute.hpp:174-179).
+    std::unique_ptr<Resident> transient;
+    const Resident* w = weights_for(identity, enc, in, out, source, retain_misses, cancel,
+                                    transient, true, /*stream_miss=*/true);
+    const bool packed = w ? w->packed : kdq_gemv_packed_supported(ggml_type(enc), in) != 0;
     auto decode_product = [&] {
+        if (!w) {
+            stream_product(enc, in, out, rows, source, dx, dy, dstatus, cancel, false);
+            return;
+        }
         for (std::size_t first = 0; first < rows; first += gguf_batch_max_rows) {
             require(!cancel.load(), "kdq_cancelled");
             const std::size_t n = std::min(gguf_batch_max_rows, rows - first);
-            kdq_check(w.packed ? kdq_gemv_packed(ggml_type(enc), w.device, dx + first * in, n,
-                                                 in, out, dy + first * out, out, dstatus, st)
-                               : kdq_gemv(ggml_type(enc), w.device, w.row_bytes, dx + first * in,
-                                          n, in, out, dy + first * out, out, dstatus, st));
+            kdq_check(w->packed ? kdq_gemv_packed(ggml_type(enc), w->device, dx + first * in, n,
+                                                  in, out, dy + first * out, out, dstatus, st)
+                                : kdq_gemv(ggml_type(enc), w->device, w->row_bytes,
+                                           dx + first * in, n, in, out, dy + first * out, out,
+                                           dstatus, st));
         }
     };
     // Prefill (the reference's decode-tile + SGEMM path, h3_compute.cu:2201-2218,2451): one
     // GEMM reads each weight byte once for all rows; its status bit 2 (a dequantised weight
     // past the fp16 range) sends the rows through the decode-time product instead.
-    const bool gemm = gemm_takes(enc, in, rows, w.packed);
-    if (gemm)
-        kdq_check(kdq_gemm_packed(ggml_type(enc), w.device, out, in, dx, rows, dy, dstatus, st));
+    const bool gemm = gemm_takes(enc, in, rows, packed);
+    if (gemm && w)
+        kdq_check(kdq_gemm_packed(ggml_type(enc), w->device, out, in, dx, rows, dy, dstatus, st));
+    else if (gemm)
+        stream_product(enc, in, out, rows, source, dx, dy, dstatus, cancel, true);
     else
         decode_product();
     unsigned status = 0;
@@ -454,7 +676,7 @@ ProjectionResult HipDenseCompute::dense_gguf_batch(std::span<const GgufBatchJob>
     std::vector<std::unique_ptr<Resident>> transients(jobs.size());
     std::vector<const Resident*> weights(jobs.size());
     for (std::size_t i = 0; i < jobs.size(); ++i)
-        weights[i] = &weights_for(*jobs[i].identity, *jobs[i].encoding, jobs[i].in, jobs[i].out,
+        weights[i] = weights_for(*jobs[i].identity, *jobs[i].encoding, jobs[i].in, jobs[i].out,
                                   *jobs[i].source, jobs[i].retain_misses, cancel, transients[i],
                                   true);
     // One upload of each distinct input span, one device output region per job.
@@ -551,8 +773,8 @@ ProjectionResult HipDenseCompute::dense_gguf_q8_source(
     const std::size_t rows = input.size() / in;
     std::unique_ptr<Resident> transient;
     // the same resident copy (tile-packed when the decode product takes it) serves both
-    const Resident& w = weights_for(identity, enc, in, out, source, true, cancel, transient,
-                                    true);
+    const Resident& w = *weights_for(identity, enc, in, out, source, true, cancel, transient,
+                                     true);
     auto st = static_cast<hipStream_t>(stream_);
     auto* dx = static_cast<std::uint16_t*>(device_buffer(0, input.size_bytes()));
     auto* dy = static_cast<std::uint16_t*>(device_buffer(1, output.size_bytes()));

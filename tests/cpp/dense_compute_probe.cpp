@@ -2,6 +2,7 @@
 // (kadan_amd::checkpoint) so the Python tests can drive the C++ host layer with host
 // arrays and files and compare its results with the oracle.  Every entry returns 0 on
 // success, or -1 with the exception text copied into `err`.
+#include <atomic>
 #include <cstring>
 #include <exception>
 #include <vector>
@@ -17,7 +18,9 @@ namespace {
 
 struct Probe {
     HipDenseCompute compute;
-    std::size_t source_reads = 0;  // rows handed out by every weight source so far
+    // rows handed out by every weight source so far (the read team calls sources from
+    // several threads at once)
+    std::atomic<std::size_t> source_reads{0};
     explicit Probe(int device) : compute(device) {}
 };
 
@@ -67,6 +70,10 @@ void kdc_destroy(void* p) {
 
 std::size_t kdc_source_reads(void* p) {
     return static_cast<Probe*>(p)->source_reads;
+}
+
+void kdc_set_weight_limit(void* p, std::size_t bytes) {
+    static_cast<Probe*>(p)->compute.set_weight_limit(bytes);
 }
 
 std::size_t kdc_retained(void* p) {

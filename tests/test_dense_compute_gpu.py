@@ -47,6 +47,7 @@ class Probe:
         L.kdc_source_reads.argtypes = [c_p]
         L.kdc_retained.restype = c_sz
         L.kdc_retained.argtypes = [c_p]
+        L.kdc_set_weight_limit.argtypes = [c_p, c_sz]
         L.kdc_release.restype = c_sz
         L.kdc_release.argtypes = [c_p, ctypes.c_ulonglong]
         L.kdc_release_scratch.argtypes = [c_p, ctypes.c_char_p, c_sz]
@@ -79,6 +80,9 @@ class Probe:
     @property
     def retained(self):
         return self.lib.kdc_retained(self.h)
+
+    def set_weight_limit(self, nbytes):
+        self.lib.kdc_set_weight_limit(self.h, nbytes)
 
     def release(self, ident):
         return self.lib.kdc_release(self.h, ident)
@@ -325,3 +329,80 @@ def test_bank_shares_one_copy_between_decode_and_prefill(probe, oracle):
     want = oracle.gemm_q4_0_q8(w, n_out, n_in, xq, xd)
     assert_close(yq.view(np.float16).astype(np.float32), want, what="prefill from the bank")
     assert probe.release(43) == packed and probe.retained == 0
+
+
+def _columns(seed, n, chunk):
+    """Sampled output columns, with both sides of every staging-chunk boundary."""
+    pick = set(np.random.default_rng(seed).choice(n, 96, replace=False).tolist())
+    for b in range(chunk, n, chunk):
+        pick.update((b - 1, b))
+    pick.update((0, n - 1))
+    return np.array(sorted(pick))
+
+
+# (encoding, in, out, rows per 16 MiB staging chunk): several chunks each, the last one
+# partial; Q4_K and Q8_0 stream through the packed layout, Q3_K through plain rows.
+STREAMED = [(Q4_K, 4096, 16000, 7280), (Q8_0, 4096, 8000, 3840), (Q3_K, 4096, 20000, 9532)]
+
+
+@pytest.mark.parametrize("enc,n_in,n_out,chunk", STREAMED)
+@pytest.mark.parametrize("rows", [3, 40])
+def test_dense_gguf_source_streams_misses(probe, oracle, enc, n_in, n_out, chunk, rows):
+    """A miss that is not retained is streamed in staging chunks (the reads of one chunk
+    overlapping the upload, packing and product of the previous one): every row is read
+    exactly once per call, nothing is banked, and the result is the exact product (the
+    decode-time product at 3 rows, the prefill GEMM for the packed encodings at 40)."""
+    w = synth.gguf_weights(enc, 0xF0 + enc, n_out, n_in)
+    x = synth.normal(0xF1, rows, rows * n_in).reshape(rows, n_in)
+    bias = synth.normal(0xF2, 1, n_out)
+    res, y = probe.gguf(51, enc, w, x, n_out, bias=bias, retain=False)
+    assert res == FINITE
+    assert probe.reads == n_out and probe.retained == 0
+    pick = _columns(enc + rows, n_out, chunk)
+    want = oracle.gemv(enc, w[pick], x, n_in, len(pick)) + bias[None, pick]
+    assert_close(y[:, pick], want, what=f"streamed enc={enc} rows={rows}")
+    assert np.isfinite(y).all()
+    res, y2 = probe.gguf(51, enc, w, x, n_out, bias=bias, retain=False)
+    assert res == FINITE and probe.reads == 2 * n_out and np.array_equal(y, y2)
+
+
+def test_weight_limit_refuses_and_streams(probe, oracle):
+    """IW/include/kadan/device_weights.hpp:203-206: under a byte limit the bank admits
+    misses until the next would pass it; later misses are streamed (read again on every
+    call) while the admitted weights keep hitting, and nothing is evicted."""
+    import kadan_amd
+    n_in, n_out, rows = 512, 64, 2
+    size = kadan_amd.lib().kdq_gguf_packed_bytes(Q4_K, n_in, n_out)
+    probe.set_weight_limit(2 * size + size // 2)
+    ws = {i: synth.gguf_weights(Q4_K, 0xF4 + i, n_out, n_in) for i in (1, 2, 3)}
+    x = synth.normal(0xF8, rows, rows * n_in).reshape(rows, n_in)
+    want = {i: oracle.gemv(Q4_K, w, x, n_in, n_out) for i, w in ws.items()}
+    # (weight, rows read so far, weights banked): 1 and 2 admitted, 3 refused every time
+    for ident, reads, banked in ((1, 64, 1), (2, 128, 2), (3, 192, 2), (1, 192, 2),
+                                 (3, 256, 2), (2, 256, 2)):
+        res, y = probe.gguf(60 + ident, Q4_K, ws[ident], x, n_out)
+        assert res == FINITE
+        assert_close(y, want[ident], what=f"limited bank weight {ident}")
+        assert (probe.reads, probe.retained) == (reads, banked * size), ident
+    assert probe.release(63) == 0  # never admitted
+    assert probe.release(61) == size and probe.release(62) == size and probe.retained == 0
+    probe.set_weight_limit(size // 2)  # below one weight: streamed, nothing evicted
+    res, y = probe.gguf(61, Q4_K, ws[1], x, n_out)
+    assert res == FINITE and probe.retained == 0
+    assert_close(y, want[1], what="weight larger than the limit")
+
+
+def test_streamed_prefill_fp16_range_fallback(probe, oracle):
+    """A streamed GEMM chunk that flags the fp16 range (one block scale of 1000 in the
+    second staging chunk) sends the call through the streamed decode-time product: every
+    row is read twice and the result is still the exact product."""
+    rows, n_in, n_out = 24, 4096, 8000
+    w = synth.gguf_weights(Q8_0, 0xF9, n_out, n_in).reshape(n_out, -1).copy()
+    big = np.array([1000.0], np.float16).view(np.uint16)[0]
+    w[5000, 0], w[5000, 1] = big & 255, big >> 8
+    x = synth.normal(0xFA, 1, rows * n_in).reshape(rows, n_in)
+    res, y = probe.gguf(71, Q8_0, w, x, n_out, retain=False)
+    assert res == FINITE and probe.reads == 2 * n_out and probe.retained == 0
+    pick = np.union1d(_columns(0xFB, n_out, 3840), [5000])
+    assert_close(y[:, pick], oracle.gemv(Q8_0, w[pick], x, n_in, len(pick)),
+                 what="streamed fp16-range fallback")
