@@ -17,9 +17,11 @@ The same line carries
                 reference sources), on the reference worker split (64-column units,
                 clamp(cores/2, 1, 16) threads), on a bounded sample of the same workload
                 rotating over 4 weight copies
-  extra         the other BASELINE configurations (C1 Q8_0 GEMV, C2 down, C3 Q4_0 GEMM,
-                C4 MoE at 1 and 256 tokens, C5 MoE at 2048 skewed tokens), each timed
-                with events over back-to-back launches (median of repetitions)
+  extra         the HBM read ceiling at the headline's size (kdq_hbm_read, timed the same
+                way), the other BASELINE configurations (C1 Q8_0 GEMV, C2 down, C3 Q4_0
+                GEMM, C4 MoE at 1 and 256 tokens, C5 MoE at 2048 skewed tokens) and the
+                prefill GEMMs, each timed with events over back-to-back launches (median
+                of repetitions)
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-extra] [--skip-cpu]
 """
@@ -183,6 +185,7 @@ def cpu_baseline(seconds: float, copies: int = 4):
         "unit": "GB/s",
         "cores": threads,
         "kind": kind,
+        "cpu_model": cpu_model(),
         "sample": (f"{len(times)} runs (median) of the C2 gate/up Q4_K matvec 4096->14336, "
                    f"batch 1, over {copies} rotated weight copies: quantize_row_q8_K + "
                    f"vec_dot_q4_K_q8_K via CpuMatvec, 64-column units on {threads} threads "
@@ -227,7 +230,7 @@ def cpu_baselines(seconds: float = 2.0):
     impl = ref or oracle.Oracle()
     kind = "reference" if ref else "port"
     port = oracle.Oracle()
-    out = {"cores_available": cores, "threads": counts}
+    out = {"cores_available": cores, "threads": counts, "cpu_model": cpu_model()}
 
     def gemv_leg(name, encoding, n_in, n_out, seed, copies=4):
         base = synth.gguf_weights(encoding, seed, n_out, n_in)
@@ -252,6 +255,7 @@ def cpu_baselines(seconds: float = 2.0):
 
     gemv_leg("c1_q8_0_gemv_4096x4096", Q8_0, 4096, 4096, 0xC1)
     gemv_leg("c2_q4_k_gemv_4096_to_14336", Q4_K, 4096, 14336, 0xC2A)
+    gemv_leg("c2_q4_k_gemv_14336_to_4096", Q4_K, 14336, 4096, 0xC2B)
 
     # C3: Q8_0-quantised activation rows x Q4_0 weights (CpuMatvec over the rows)
     n_out, k, rows = 14336, 4096, 32
@@ -268,22 +272,42 @@ def cpu_baselines(seconds: float = 2.0):
                                      "fp32), all 14336 outputs: quantize_row_q8_0 + "
                                      "vec_dot_q4_0_q8_0 via CpuMatvec"}
 
-    # C4: the MoE layer flow with exact MXFP4 products (the oracle's composition: the
-    # reference has no compiled MXFP4 MoeLayer)
-    (gb, gs), (ub, us), (db, ds) = synth.moe_weights(0xC4, 32, 2880, 2880)
-    for name, tokens, sample in (("c4_moe_t1", 1, 1), ("c4_moe_t256", 256, 4)):
-        xa, la = synth.moe_inputs(0xC4, tokens, 2880, 32)
-        xa, la = xa[:sample], la[:sample]
-        legs = {}
-        for th in counts:
-            med, n = timed_median(lambda: port.moe_forward(xa, la, 4, gb, gs, ub, us, db, ds,
-                                                           threads=th), seconds, least=1)
-            legs[str(th)] = {"tokens_per_s": round(sample / med, 2), "ms": round(med * 1e3, 2),
-                             "runs": n}
-        out[name] = {"kind": "port", "unit": "tokens/s", "by_threads": legs,
-                     "sample": f"{sample} token(s) of the T={tokens} inputs, 32 experts, "
-                               "top-4, double-accumulated MXFP4 products"}
+    # C4 and C5: the MoE layer flow with exact MXFP4 products (the oracle's composition:
+    # the reference has no compiled MXFP4 MoeLayer)
+    for experts, hot, seed, legs_of in ((32, 0, 0xC4, (("c4_moe_t1", 1, [0]),
+                                                       ("c4_moe_t256", 256, [0, 1, 2, 3]))),
+                                        (128, 8, 0xC5, (("c5_moe_t2048_skewed", 2048,
+                                                         [0, 1]),))):
+        (gb, gs), (ub, us), (db, ds) = synth.moe_weights(seed, experts, 2880, 2880)
+        for name, tokens, sample in legs_of:
+            xa, la = synth.moe_inputs(seed, tokens, 2880, experts, hot=hot)
+            xa, la = xa[sample], la[sample]
+            legs = {}
+            for th in counts:
+                med, n = timed_median(lambda: port.moe_forward(xa, la, 4, gb, gs, ub, us, db,
+                                                               ds, threads=th),
+                                      seconds, least=1)
+                legs[str(th)] = {"tokens_per_s": round(len(sample) / med, 2),
+                                 "ms": round(med * 1e3, 2), "runs": n}
+            out[name] = {"kind": "port", "unit": "tokens/s", "by_threads": legs,
+                         "sample": f"tokens {sample} of the T={tokens} inputs"
+                                   + (" (token 0 boosted onto the hot experts)" if hot else "")
+                                   + f", {experts} experts, top-4, double-accumulated MXFP4 "
+                                     "products"}
+        del gb, gs, ub, us, db, ds
     return out
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (what lscpu reports), for the CPU baselines."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def bench_gemv(torch, encoding, n_in, n_out, steps, warmup, seed, copies=16, per_step=1,
@@ -329,6 +353,67 @@ def bench_gemv(torch, encoding, n_in, n_out, steps, warmup, seed, copies=16, per
 
     submit(warmup)
     return time_steps(torch, submit, steps)
+
+
+def bench_read_ceiling(torch, nbytes: int, steps: int, copies: int = 16,
+                       shapes=((256, 1024), (256, 2048), (256, 4096), (1024, 256),
+                               (1024, 512), (1024, 1024))):
+    """The HBM read ceiling at the headline's size: kdq_hbm_read (a plain streaming read,
+    16-byte non-temporal loads) over `copies` distinct buffers of `nbytes` each (the
+    headline's per-launch bytes, rotated the same way), timed by time_steps exactly as
+    the headline is, at several launch shapes, in both forms: every workgroup storing
+    its fold (a kernel with output) and the read alone (no store on the critical path).
+    The fastest shape of each form is its ceiling.  A single read of 64x the size gives
+    the streaming rate without the per-launch cost."""
+    import kadan_amd
+    from kadan_amd import ops
+    nbytes = (nbytes + 15) // 16 * 16
+    bufs = [torch.full((nbytes,), c, dtype=torch.uint8, device="cuda") for c in range(copies)]
+    sink = torch.zeros(max(w for _, w in shapes), dtype=torch.int32, device="cuda")
+    ops.hbm_read(bufs[0], sink, shapes[0][1], shapes[0][0])  # checked once through ops
+    # launches as lean as the headline's (one ctypes call, arguments bound beforehand),
+    # so the host enqueues faster than the kernels retire
+    fn = kadan_amd.lib().kdq_hbm_read
+    stream = torch.cuda.current_stream().cuda_stream
+    pointers = [b.data_ptr() for b in bufs]
+    sp = sink.data_ptr()
+    never = 0x9E3779B9  # a constant-filled buffer folds to 0 or its fill word
+    forms = {}
+    for store_all in (1, 0):
+        shape_ms = {}
+        for threads, wg in shapes:
+            issued = [0]
+
+            def submit(n, wg=wg, threads=threads, store_all=store_all):
+                for _ in range(n):
+                    if fn(pointers[issued[0] % copies], nbytes, sp, wg, threads, store_all,
+                          never, stream):
+                        raise RuntimeError("kdq_hbm_read failed")
+                    issued[0] += 1
+            submit(50)
+            shape_ms[f"{wg}x{threads}"] = time_steps(torch, submit, steps)
+        best = min(shape_ms, key=shape_ms.get)
+        gbs = nbytes / (shape_ms[best] * 1e-3) / 1e9
+        forms["with_store" if store_all else "read_only"] = {
+            "ms": round(shape_ms[best], 6), "gbs": round(gbs, 1),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "best_shape": best,
+            "ms_by_shape (workgroups x lanes)": {k: round(v, 6) for k, v in shape_ms.items()}}
+    del bufs
+    big = torch.ones(64 * nbytes // 4, dtype=torch.int32, device="cuda")
+    ops.hbm_read(big, sink, 4096)
+    big_ms = time_launches(torch, lambda i: ops.hbm_read(big, sink, 4096), 10, 5)
+    del big
+    torch.cuda.empty_cache()
+    store = forms["with_store"]
+    return {"workload": f"HBM read ceiling: {nbytes} bytes per launch, {copies} rotated "
+                        "buffers (the headline's bytes and rotation)",
+            "ms": store["ms"], "gbs": store["gbs"], "hbm_frac": store["hbm_frac"],
+            **forms,
+            "streaming_gbs": round(64 * nbytes / (big_ms * 1e-3) / 1e9, 1),
+            "note": "kdq_hbm_read: the least a reader can do; ms/gbs are the form that "
+                    "stores a word per workgroup, as every kernel with output must; the "
+                    "headline GEMV's time over that time is its distance from reading its "
+                    "bytes once and writing its result"}
 
 
 def calibrate_copy(torch, mib: int = 256, count: int = 5):
@@ -388,11 +473,13 @@ def bench_gemm_gguf(torch, encoding, k, n, m=512, reps=10, count=20, copies=8):
             "note": "per launch: activation staging (fp16, row scale) + fp16-MFMA GEMM"}
 
 
-def bench_moe_gguf(torch, rows, reps=10, count=20):
+def bench_moe_gguf(torch, rows, reps=10, count=64):
     """The GGUF MoE layer (kdq_moe_gguf) at Qwen3-30B-A3B's geometry: hidden 2048, 128
     experts, top-8, expert ff 768, a 768-wide shared expert; Q4_K expert gate/up, Q6_K
     expert down, Q8_0 shared gate/up, Q4_K shared down, an fp32 router.  Each launch takes
-    the next of 16 inputs, so the routed experts change between calls."""
+    the next of 64 inputs and the next of 2 weight copies (392 MB of experts each), so the
+    routed experts change between calls and the Infinity Cache cannot hold what they
+    read."""
     from kadan_amd import ops, row_bytes, synth
     H, E, K, F, S = 2048, 128, 8, 768, 768
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
@@ -404,18 +491,19 @@ def bench_moe_gguf(torch, rows, reps=10, count=20):
     encs = {"gate_exps": (Q4_K, (E, F, H)), "up_exps": (Q4_K, (E, F, H)),
             "down_exps": (Q6_K, (E, H, F)), "gate_shexp": (Q8_0, (S, H)),
             "up_shexp": (Q8_0, (S, H)), "down_shexp": (Q4_K, (H, S))}
+    specs = [dict(spec), dict(spec)]
     for i, (name, (enc, shape)) in enumerate(encs.items()):
         w = synth.gguf_weights(enc, 0xE30 + i, int(np.prod(shape[:-1])), shape[-1])
-        spec[name] = (enc, dev(w.reshape(*shape[:-1], -1)))
-    xs = [dev(synth.normal(0xE4 + i, 1, rows * H).reshape(rows, H)) for i in range(16)]
-    launch = lambda i: ops.moe_gguf(spec, xs[i % 16])
+        for c, wc in enumerate(rotated_copies(torch, w, 2, keep_mask(enc, w.shape), 0xE30 + i)):
+            specs[c][name] = (enc, wc.reshape(*shape[:-1], -1))
+    inputs = 64
+    xs = [dev(synth.normal(0xE4 + i, 1, rows * H).reshape(rows, H)) for i in range(inputs)]
+    launch = lambda i: ops.moe_gguf(specs[i % 2], xs[i % inputs])
     for i in range(5):
         launch(i)
     ms = time_launches(torch, launch, count, reps)
-    sel = set()
-    for i in range(16):
-        sel.update(int(e) for e in launch(i)[1].cpu().numpy().ravel())
-    per_call = np.mean([len(set(launch(i)[1].cpu().numpy().ravel().tolist())) for i in range(16)])
+    per_call = np.mean([len(set(launch(i)[1].cpu().numpy().ravel().tolist()))
+                        for i in range(inputs)])
     expert = 2 * F * row_bytes(Q4_K, H) + H * row_bytes(Q6_K, F)
     shared = 2 * S * row_bytes(Q8_0, H) + H * row_bytes(Q4_K, S)
     nbytes = per_call * expert + shared + E * H * 4 + H * 4 + 2 * rows * H * 4
@@ -434,11 +522,22 @@ def moe_bytes(tokens, hidden, inter, experts_touched):
     return experts_touched * per_expert + tokens * hidden * 2 + tokens * hidden * 4
 
 
-def bench_moe(torch, tokens, experts, hot, seed, copies, reps=10, count=10):
+def bench_moe(torch, tokens, experts, hot, seed, copies, reps=10, count=10, inputs=1):
+    """The MXFP4 MoE layer over `copies` resident weight sets.  With inputs > 1 the
+    launches cycle through that many token batches whose routing is steered to disjoint
+    expert groups (input i boosts experts [i * top_k, (i + 1) * top_k) mod experts), so
+    consecutive decode calls touch different experts, as real decode steps do, and the
+    weights they read (copies x experts x 13.2 MB) stay far beyond the 256 MB Infinity
+    Cache."""
     from kadan_amd import ops, synth
     hidden = inter = 2880
     top_k = 4
-    x, logits = synth.moe_inputs(seed, tokens, hidden, experts, hot=hot)
+    batches = []
+    for i in range(inputs):
+        x, logits = synth.moe_inputs(seed + i, tokens, hidden, experts, hot=hot)
+        if inputs > 1:
+            logits[:, [(i * top_k + j) % experts for j in range(top_k)]] += np.float32(8.0)
+        batches.append((x, logits))
     (gb, gs), (ub, us), (db, ds) = synth.moe_weights(seed, experts, hidden, inter)
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
     sets = []  # resident weights: packed once, as the host layer's bank keeps them
@@ -455,23 +554,26 @@ def bench_moe(torch, tokens, experts, hot, seed, copies, reps=10, count=10):
                      ops.moe_mxfp4_pack(arrays[4], arrays[5], experts, hidden, inter)])
         del arrays
     del gb, gs, ub, us, db, ds
-    xb = dev(x).view(torch.bfloat16)
-    lg = dev(logits)
+    xbs = [dev(x).view(torch.bfloat16) for x, _ in batches]
+    lgs = [dev(lg) for _, lg in batches]
     y = torch.empty(tokens, hidden, device="cuda")
-    launch = lambda i: ops.moe_mxfp4_packed(xb, lg, top_k, inter, *sets[i % copies], out=y)
+    launch = lambda i: ops.moe_mxfp4_packed(xbs[i % inputs], lgs[i % inputs], top_k, inter,
+                                            *sets[i % copies], out=y)
     for i in range(3):
         launch(i)
     ms = time_launches(torch, launch, count, reps)
-    touched = len(np.unique(_route_host(logits, top_k)))
+    touched = np.mean([len(np.unique(_route_host(lg, top_k))) for _, lg in batches])
     nbytes = moe_bytes(tokens, hidden, inter, touched)
     flops = 2.0 * tokens * top_k * 3 * hidden * inter
     gbs = nbytes / (ms * 1e-3) / 1e9
     tflops = flops / (ms * 1e-3) / 1e12
     del sets
     torch.cuda.empty_cache()
-    return {"workload": f"MXFP4 MoE H=I=2880 E={experts} top-4 T={tokens}" + (" skewed" if hot else ""),
+    cycle = "" if inputs == 1 else f", {inputs} inputs routed to disjoint experts"
+    return {"workload": f"MXFP4 MoE H=I=2880 E={experts} top-4 T={tokens}"
+                        + (" skewed" if hot else "") + f" ({copies} weight copies{cycle})",
             "ms": round(ms, 4), "tokens_per_s": round(tokens / (ms * 1e-3), 1),
-            "experts_touched": int(touched), "algorithmic_bytes": int(nbytes),
+            "experts_touched": round(float(touched), 2), "algorithmic_bytes": int(nbytes),
             "gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
             "tflops": round(tflops, 2),
             "fp4_mfma_frac": round(tflops / FP4_PEAK_TFLOPS, 5),
@@ -544,7 +646,11 @@ def main():
                 line = {"workload": workload, **line}
             extra[name] = line
 
-        gemv_line("c1_q8_0_gemv_4096x4096", Q8_0, 4096, 4096, 0xC1, 500)
+        if want("hbm_read_ceiling"):
+            extra["hbm_read_ceiling"] = bench_read_ceiling(torch, nbytes, args.steps)
+        gemv_line("c1_q8_0_gemv_4096x4096", Q8_0, 4096, 4096, 0xC1, 1000,
+                  "C1 Q8_0 GEMV 4096x4096, batch 1, tile-packed, 32 rotated weight copies "
+                  "(570 MB)", copies=32)
         gemv_line("c2_q4_k_gemv_14336_to_4096", Q4_K, 14336, 4096, 0xC2B, 500)
         gemv_line("c2_q4_k_gemv_row_major", Q4_K, n_in, n_out, 0xC2A, 1000,
                   "C2 Q4_K GEMV 4096->14336, batch 1, over the row-major GGUF bytes "
@@ -593,7 +699,8 @@ def main():
         if want("moe_gguf_t4"):
             extra["moe_gguf_t4"] = bench_moe_gguf(torch, 4)
         if want("c4_moe_t1"):
-            extra["c4_moe_t1"] = bench_moe(torch, 1, 32, 0, 0xC4, copies=2, count=50)
+            extra["c4_moe_t1"] = bench_moe(torch, 1, 32, 0, 0xC4, copies=3, count=48,
+                                           inputs=8)
         if want("c4_moe_t256"):
             extra["c4_moe_t256"] = bench_moe(torch, 256, 32, 0, 0xC4, copies=2)
         if want("c5_moe_t2048_skewed"):

@@ -311,6 +311,16 @@ int kdq_moe_mxfp4_packed_noalloc(const uint16_t* x_bf16, const float* logits, si
                                  const uint8_t* down_packed, float* y, int32_t* idx,
                                  float* w, int32_t* offsets, int32_t* perm, void* stream);
 
+/* Measurement aid, no counterpart in the reference: one streaming read of `bytes`
+ * (a multiple of 16; `src` 16-byte aligned) over `workgroups` workgroups of `threads`
+ * (256 or 1024) lanes.  Workgroup b folds (xor) the 32-bit words of its share, units of
+ * 16 bytes [b * per, (b + 1) * per) with per = ceil(units / workgroups) rounded up to a
+ * multiple of 64, and stores the fold into sink[b] always (store_all != 0) or only when
+ * it equals `match`.  Its best time over launch shapes is the HBM read ceiling the
+ * GEMV's bandwidth is judged against. */
+int kdq_hbm_read(const void* src, size_t bytes, unsigned* sink, size_t workgroups,
+                 int threads, int store_all, unsigned match, void* stream);
+
 /* Frees this thread's current device's cached workspace (synchronizes the device).
  * IW/include/kadan/dense_compute.hpp:66-68 release_scratch counterpart. */
 int kdq_release_scratch(void);

@@ -78,6 +78,7 @@ _SIGNATURES = {
                              _VP, _VP, _VP],
     "kdq_moe_mxfp4_packed_noalloc": [_VP, _VP, _SZ, _SZ, _SZ, _SZ, _SZ, _VP, _VP, _VP, _VP,
                                      _VP, _VP, _VP, _VP, _VP],
+    "kdq_hbm_read": [_VP, _SZ, _VP, _SZ, _I, _I, C.c_uint, _VP],
     "kdq_release_scratch": [],
 }
 _OTHER = {

@@ -297,8 +297,20 @@ def moe_mxfp4_packed(x_bf16: torch.Tensor, logits: torch.Tensor, top_k: int, int
     return (out, *extra) if routing else out
 
 
+def hbm_read(buffer: torch.Tensor, sink: torch.Tensor, workgroups: int,
+             threads: int = 256, store_all: bool = True, match: int = 0) -> None:
+    """kdq_hbm_read: one streaming read of `buffer` (the HBM read ceiling's probe) over
+    `workgroups` workgroups of `threads` lanes; `sink` holds one int32 per workgroup,
+    written always (store_all) or where the workgroup's fold equals `match`."""
+    _need(sink, torch.int32, "sink")
+    if not buffer.is_cuda or not buffer.is_contiguous() or sink.numel() < workgroups:
+        raise ValueError("hbm_read: a contiguous device buffer and a sink per workgroup")
+    call("kdq_hbm_read", buffer.data_ptr(), buffer.numel() * buffer.element_size(),
+         sink.data_ptr(), workgroups, threads, int(store_all), match & 0xFFFFFFFF, _stream())
+
+
 __all__ = ["dequantize", "gemv", "gemv_batch", "quantize_q8", "gemm_q4_0", "gemm_q4_0_packed",
-           "gemm_packed",
+           "gemm_packed", "hbm_read",
            "moe_gguf", "moe_route",
            "mxfp4_dequantize", "moe_mxfp4", "moe_mxfp4_pack", "moe_mxfp4_packed", "lib",
            "BLOCK_BYTES", "BLOCK_VALUES"]
