@@ -230,8 +230,11 @@ typedef struct kdq_moe_gguf_layer {
  * its weight; plus the shared expert's down(silu(gate_s . x) * (up_s . x)) scaled by
  * sigmoid(shared_gate . x).  Optional outputs: `selected` / `weights` [rows x top_k]
  * (the routing), `status` |= 1 for a non-finite weight scale.  Every projection decodes
- * its weights exactly (kdq_gemv semantics).  rows * top_k <= 512, experts <= 256,
- * top_k <= 8; x, y, shared_gate 16-byte aligned. */
+ * its weights exactly (kdq_gemv semantics).  rows <= 4096, rows * top_k <= 8192,
+ * experts <= 256, top_k <= 8; x, y, shared_gate 16-byte aligned.  Up to 8 rows run
+ * every slot's expert product directly; larger batches (prefill chunks) group the
+ * slots by expert into 8-row items, so an expert's weights are read once per 8 of its
+ * rows (the reference's per-expert batch jobs, IW/include/kadan/dense_compute.hpp:197-201). */
 int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, size_t rows, float* y,
                  int32_t* selected, float* weights, unsigned* status, void* stream);
 

@@ -300,18 +300,27 @@ __device__ __forceinline__ void load_item(const uint8_t* base, size_t off, unsig
 // (1 for an all-zero row), and fp16(x / sigma) permuted per 256-value group: logical
 // 16-byte chunk q = 16j + 8h + 4p + u of a group holds operand elements 0..7 of sub-step
 // s = 8j + 4p + u for lane half h.  One 256-thread workgroup per row; the row passes
-// through LDS.
+// through LDS.  Grouped (MoE) form: row t is x[slot_of[t] / topk] (a zero row when
+// slot_of[t] < 0) and rows from *used on are not staged.
 template <int ENC>
 __global__ __launch_bounds__(256) void stage_kernel(const float* __restrict__ x, unsigned k,
                                                     uint16_t* __restrict__ xs,
-                                                    float* __restrict__ sigma) {
+                                                    float* __restrict__ sigma,
+                                                    const int32_t* __restrict__ slot_of,
+                                                    unsigned topk,
+                                                    const unsigned* __restrict__ used) {
     extern __shared__ __align__(16) float row[];
     __shared__ float wave_max[4];
     const unsigned t = blockIdx.x;
-    const float* src = x + size_t(t) * k;
+    if (used && t >= *used)
+        return;
+    const int slot = slot_of ? slot_of[t] : 0;
+    const bool zero = slot < 0;
+    const float* src = x + (slot_of ? size_t(zero ? 0 : slot / int(topk)) : size_t(t)) * k;
     float amax = 0.f;
     for (unsigned i = threadIdx.x; i < k / 4; i += 256) {
-        const float4 v = reinterpret_cast<const float4*>(src)[i];
+        const float4 v = zero ? make_float4(0.f, 0.f, 0.f, 0.f)
+                              : reinterpret_cast<const float4*>(src)[i];
         reinterpret_cast<float4*>(row)[i] = v;
         amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         if (!(isfinite(v.x) && isfinite(v.y) && isfinite(v.z) && isfinite(v.w)))
@@ -365,6 +374,10 @@ __global__ __launch_bounds__(256) void stage_kernel(const float* __restrict__ x,
 // K slices (narrow products, too few tiles for the compute units): workgroup slice `ks`
 // runs groups [ks * per, (ks + 1) * per) and writes its fp32 tile to part[ks] (m x n);
 // reduce_kernel then sums the slices in order.
+//
+// Grouped (MoE) form, `tile_expert` given: token tile t multiplies the weights of expert
+// tile_expert[t] of a stack of packed experts `expert_bytes` apart; tiles whose entry is
+// negative are skipped (the whole workgroup returns before any barrier).
 template <int ENC>
 __global__ __launch_bounds__(256, 1) void gemm_kernel(const uint16_t* __restrict__ xs,
                                                       const float* __restrict__ sigma,
@@ -373,7 +386,9 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const uint16_t* __restrict
                                                       unsigned slices, unsigned per,
                                                       float* __restrict__ y,
                                                       float* __restrict__ part,
-                                                      unsigned* __restrict__ status) {
+                                                      unsigned* __restrict__ status,
+                                                      const int32_t* __restrict__ tile_expert,
+                                                      size_t expert_bytes) {
     using F = GemmFormat<ENC>;
     using Regs = typename F::Regs;
     extern __shared__ __align__(16) uint8_t lds[];
@@ -390,6 +405,12 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const uint16_t* __restrict
         return;
     const unsigned n_tile = linear / (m_tiles * slices);
     const unsigned slice = (linear / m_tiles) % slices, m0 = (linear % m_tiles) * PM;
+    if (tile_expert) {
+        const int e = tile_expert[m0 / PM];
+        if (e < 0)
+            return;
+        w += size_t(e) * expert_bytes;
+    }
     // slices = ceil(groups / per), so every slice has at least one group
     const unsigned g_begin = slice * per, g_end = min(groups, g_begin + per);
     float* __restrict__ dst_base = slices > 1 ? part + size_t(slice) * m * n : y;
@@ -616,6 +637,41 @@ unsigned gemm_slice_depth(size_t m, size_t n, size_t k) {
 }
 
 template <int ENC>
+int configure() {
+    static bool configured = false;  // one attribute call per instantiation
+    if (!configured) {
+        KDQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&stage_kernel<ENC>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024));
+        KDQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<ENC>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, int(kLds)));
+        configured = true;
+    }
+    return KDQ_OK;
+}
+
+template <int ENC>
+int launch_grouped(const void* packed, size_t expert_bytes, const int32_t* tile_expert, size_t n,
+                   size_t k, const float* x, const int32_t* inv, unsigned topk,
+                   const unsigned* used, size_t positions, float* y, unsigned* status,
+                   uint16_t* xs, float* sigma, hipStream_t st) {
+    int rc;
+    if ((rc = configure<ENC>()))
+        return rc;
+    hipLaunchKernelGGL(stage_kernel<ENC>, dim3(unsigned(positions)), dim3(256), k * 4, st, x,
+                       unsigned(k), xs, sigma, inv, topk, used);
+    KDQ_HIP(hipGetLastError());
+    const size_t wtiles = (n + 15) / 16;
+    const size_t tiles = (positions / PM) * ((wtiles + kTiles - 1) / kTiles);
+    const unsigned grid = unsigned((tiles + 7) / 8 * 8);
+    hipLaunchKernelGGL(gemm_kernel<ENC>, dim3(grid), dim3(256), kLds, st, xs, sigma,
+                       static_cast<const uint8_t*>(packed), unsigned(positions), unsigned(n),
+                       unsigned(k), 1u, unsigned(k / 256), y, nullptr, status, tile_expert,
+                       expert_bytes);
+    KDQ_HIP(hipGetLastError());
+    return KDQ_OK;
+}
+
+template <int ENC>
 int launch_gemm(const float* x, const uint8_t* packed, size_t m, size_t n, size_t k, float* y,
                 unsigned* status, hipStream_t st) {
     int rc;
@@ -631,22 +687,17 @@ int launch_gemm(const float* x, const uint8_t* packed, size_t m, size_t n, size_
     auto* xs = reinterpret_cast<uint16_t*>(base);
     auto* sigma = reinterpret_cast<float*>(base + xs_bytes);
     auto* part = slices > 1 ? reinterpret_cast<float*>(base + xs_bytes + sig_bytes) : nullptr;
-    static bool configured = false;  // one attribute call per instantiation
-    if (!configured) {
-        KDQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&stage_kernel<ENC>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024));
-        KDQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<ENC>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, int(kLds)));
-        configured = true;
-    }
+    if ((rc = configure<ENC>()))
+        return rc;
     hipLaunchKernelGGL(stage_kernel<ENC>, dim3(unsigned(m)), dim3(256), k * 4, st, x,
-                       unsigned(k), xs, sigma);
+                       unsigned(k), xs, sigma, nullptr, 1u, nullptr);
     KDQ_HIP(hipGetLastError());
     const size_t wtiles = (n + 15) / 16;
     const size_t tiles = (m_pad / PM) * ((wtiles + kTiles - 1) / kTiles) * slices;
     const unsigned grid = unsigned((tiles + 7) / 8 * 8);
     hipLaunchKernelGGL(gemm_kernel<ENC>, dim3(grid), dim3(256), kLds, st, xs, sigma, packed,
-                       unsigned(m), unsigned(n), unsigned(k), slices, per, y, part, status);
+                       unsigned(m), unsigned(n), unsigned(k), slices, per, y, part, status,
+                       nullptr, size_t(0));
     KDQ_HIP(hipGetLastError());
     if (slices > 1) {
         const size_t count = m * n;
@@ -658,6 +709,31 @@ int launch_gemm(const float* x, const uint8_t* packed, size_t m, size_t n, size_
 }
 
 }  // namespace
+
+bool grouped_gemm_takes(int encoding, size_t k) {
+    return (encoding == KDQ_Q4_K || encoding == KDQ_Q8_0 || encoding == KDQ_Q6_K) &&
+           k % 256 == 0 && k <= 32768;
+}
+
+int grouped_gemm(int encoding, const void* packed, size_t expert_bytes,
+                 const int32_t* tile_expert, size_t n, size_t k, const float* x,
+                 const int32_t* inv, unsigned topk, const unsigned* used, size_t positions,
+                 float* y, unsigned* status, uint16_t* xs, float* sigma, hipStream_t st) {
+    if (!grouped_gemm_takes(encoding, k) || positions % PM)
+        return KDQ_ERR_UNSUPPORTED;
+    switch (encoding) {
+    case KDQ_Q4_K:
+        return launch_grouped<KDQ_Q4_K>(packed, expert_bytes, tile_expert, n, k, x, inv, topk,
+                                        used, positions, y, status, xs, sigma, st);
+    case KDQ_Q8_0:
+        return launch_grouped<KDQ_Q8_0>(packed, expert_bytes, tile_expert, n, k, x, inv, topk,
+                                        used, positions, y, status, xs, sigma, st);
+    default:
+        return launch_grouped<KDQ_Q6_K>(packed, expert_bytes, tile_expert, n, k, x, inv, topk,
+                                        used, positions, y, status, xs, sigma, st);
+    }
+}
+
 }  // namespace kdq
 
 using namespace kdq;

@@ -286,7 +286,8 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* packed, size
 // ------------------------------------------------------------- exact GEMV
 
 // `index` (optional): the weights start at weights + min(*index, index_limit - 1) *
-// index_stride (the expert a device-side routing chose).
+// index_stride (the expert a device-side routing chose); a job whose index is negative
+// is skipped (an unused item of a grouped launch sized for the most items).
 template <int ENC, int ROWS>
 __global__ __launch_bounds__(256) void exact_gemv(const uint8_t* weights, size_t row_bytes,
                                                   const float* x, unsigned rows, unsigned in,
@@ -303,8 +304,12 @@ __global__ __launch_bounds__(256) void exact_gemv(const uint8_t* weights, size_t
     // index step along
     x += (blockIdx.y / x_every) * x_step;
     y += blockIdx.y * y_step;
-    if (index)
-        weights += size_t(min(unsigned(index[blockIdx.y]), index_limit - 1)) * index_stride;
+    if (index) {
+        const int e = index[blockIdx.y];
+        if (e < 0)
+            return;
+        weights += size_t(min(unsigned(e), index_limit - 1)) * index_stride;
+    }
     const uint8_t* row = weights + size_t(column) * row_bytes;
     float sums[ROWS] = {};
     bool finite = true;
@@ -1169,7 +1174,8 @@ struct MfmaJob {  // one job's fields together
     unsigned* status;
     size_t row_bytes, stride;
     unsigned out, index_limit;
-    // optional: the weights start at weights + min(*index, index_limit - 1) * index_stride
+    // optional: the weights start at weights + min(*index, index_limit - 1) * index_stride;
+    // a negative index skips the job (the whole workgroup returns before any barrier)
     const int32_t* index;
     size_t index_stride;
     // paired launches: the second matrix (same shape, same expert offset); y = silu(W x) * (up x)
@@ -1202,10 +1208,12 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
     const bool affine = !PLAIN && jobs.affine;
     const unsigned jid = affine ? 0 : blockIdx.y, step = affine ? blockIdx.y : 0;
     const MfmaJob& jb = jobs.job[jid];
-    const size_t expert = !PLAIN && jb.index
-                              ? size_t(min(unsigned(jb.index[step]), jb.index_limit - 1)) *
-                                    jb.index_stride
-                              : 0;
+    const int chosen = !PLAIN && jb.index ? jb.index[step] : 0;
+    if (chosen < 0)
+        return;
+    const size_t expert =
+        !PLAIN && jb.index ? size_t(min(unsigned(chosen), jb.index_limit - 1)) * jb.index_stride
+                           : 0;
     const uint8_t* __restrict__ weights = jb.weights + expert;
     const unsigned mats = !PLAIN && jobs.mats == 2 ? 2 : 1;
     const uint8_t* __restrict__ up = mats == 2 ? jb.up + expert : weights;
@@ -2106,7 +2114,7 @@ int run_batch(const kdq_matvec_job* jobs, size_t count, void* stream) {
 bool swiglu_pairable(const kdq_matvec_job& j, size_t count) {
     MfmaPlan p;
     return fusable(j, false) && plan_mfma(j.rows, j.in, size_t(j.columns) * count, p, false, 2) &&
-           p.batch >= j.rows && (count == 1 || j.rows == 1);
+           p.batch >= j.rows;
 }
 
 int indexed_gemv_affine(const IndexedJob& first, unsigned count, size_t x_step,
@@ -2119,7 +2127,8 @@ int indexed_gemv_affine(const IndexedJob& first, unsigned count, size_t x_step,
     const unsigned mats = first.paired ? 2 : 1;
     MfmaPlan p;  // planned over every job's rows, as launch_fused plans a fused group
     if (fusable(j, false) &&
-        plan_mfma(j.rows, j.in, size_t(j.columns) * count, p, false, mats)) {
+        plan_mfma(j.rows, j.in, size_t(j.columns) * count, p, false, mats) &&
+        p.batch >= j.rows) {
         MfmaJobs mj{};
         mj.count = count;
         mj.in = j.in;

@@ -167,8 +167,9 @@ struct IndexedJob {
 int indexed_gemv_batch(const IndexedJob* jobs, size_t count, hipStream_t stream);
 // `count` products in one launch, all as `first` except that job j reads
 // x + (j / x_every) * x_step, writes y + j * y_step and takes its expert from index[j]
-// (rows of `first` must be 1 when count > 1 runs on the MFMA kernel; any rows on the
-// exact kernel, which does not take `paired`).
+// (each job takes `first`'s rows, x rows at x + r * in and y rows at y + r * stride; the
+// MFMA kernel takes up to its plan's batch of rows, the exact kernel any, without
+// `paired`).  A job whose index[j] is negative is skipped.
 int indexed_gemv_affine(const IndexedJob& first, unsigned count, size_t x_step, size_t y_step,
                         hipStream_t stream, unsigned x_every = 1);
 // Whether `count` jobs like j (an affine launch when count > 1) run on the MFMA kernel
@@ -185,6 +186,17 @@ __device__ __forceinline__ float sigmoid_of(float v) {
 
 // The MoE router of kdq_moe_route (softmax with a double total, top-k by probability,
 // weights renormalised by max(sum, 2^-14)) without the expert permutation.
+// Grouped prefill GEMM (gguf_gemm.hip): y[p, :] = W_{e(p)} x_p for positions p in token
+// tiles of 128 (positions a multiple of 128), tile t's weights expert tile_expert[t] of a
+// stack of tile-packed experts expert_bytes apart (tiles with a negative entry skipped);
+// x_p = x[inv[p] / topk] (zero rows where inv[p] < 0), rows from *used on unstaged.
+// xs (positions * k * 2 bytes) and sigma (positions * 4) are the caller's scratch.
+// Q4_K / Q8_0 / Q6_K, k % 256 == 0, k <= 32768.
+bool grouped_gemm_takes(int encoding, size_t k);
+int grouped_gemm(int encoding, const void* packed, size_t expert_bytes,
+                 const int32_t* tile_expert, size_t n, size_t k, const float* x,
+                 const int32_t* inv, unsigned topk, const unsigned* used, size_t positions,
+                 float* y, unsigned* status, uint16_t* xs, float* sigma, hipStream_t st);
 int route_selection(const float* logits, size_t tokens, size_t experts, size_t top_k,
                     int32_t* idx, float* w, hipStream_t stream);
 

@@ -19,8 +19,22 @@
 //      plus shared_down * sigmoid(gate scalar)
 // GEMVs of Q4_0 / Q8_0 / Q4_K / Q3_K / Q6_K / IQ4_XS / IQ4_NL run on the MFMA kernel
 // (fused per shape), every other encoding on the exact kernel.
+//
+// Batches of more than kSlotRows rows (prefill chunks; the reference runs MoeLayer::forward
+// on them with per-expert batch jobs of gathered rows, IW/include/kadan/dense_compute.hpp:
+// 197-201) take stages 4-6 grouped by expert instead of per slot, so each expert's
+// weights are read once per 8 of its rows rather than once per slot:
+//   4'. group_kernel: a counting sort of the slots by expert into segments padded to whole
+//       items of kItemRows rows (slot -> position, position -> slot, the expert of every
+//       item, -1 past the used ones); gather_kernel: x rows into position order (padding
+//       rows zero)
+//   4''. one launch over the items of expert gate / up (8 rows each, weights at the
+//       item's expert), paired with the swiglu like 4
+//   5'. one launch over the items of expert down, plus the shared down
+//   6'. combine_pos_kernel: as 6, each slot's down row read at its position
 #include "kdq_common.hpp"
 
+#include <algorithm>
 #include <vector>
 
 namespace kdq {
@@ -44,6 +58,129 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* down, const f
     float sum = 0.f;
     for (unsigned i = 0; i < k; ++i)
         sum += down[(t * k + i) * hidden + d] * w[t * k + i];
+    y[e] = sum + shared[e] * sigmoid_of(gate[t]);
+}
+
+constexpr size_t kSlotRows = 8;          // batches up to this many rows run per slot
+constexpr unsigned kItemRows = 8;        // rows of a grouped item (the MFMA GEMV's batch)
+constexpr unsigned kTileRows = 128;      // rows of a grouped GEMM token tile
+constexpr size_t kMaxGroupedSlots = 8192;
+
+// Slots by expert into segments padded to multiples of `pad` (kItemRows, or kTileRows when
+// a projection runs on the grouped GEMM): pos[s] (slot -> position), inv[p] (position ->
+// slot, -1 for padding), item_expert[i] for the kItemRows-row items (-1 for items of
+// padding only and past the used ones), tile_expert[j] for the kTileRows-row tiles when
+// pad == kTileRows (-1 past the used ones), *used = positions in use, *gemm_status = 0.
+// Positions within an expert follow the order of an LDS atomic (each slot's result depends
+// only on its own row, so the layer's output does not).  One workgroup of 1024 threads;
+// experts <= 256.
+__global__ __launch_bounds__(1024) void group_kernel(const int32_t* __restrict__ idx,
+                                                     unsigned slots, unsigned experts,
+                                                     unsigned pad, unsigned max_items,
+                                                     int32_t* __restrict__ pos,
+                                                     int32_t* __restrict__ inv,
+                                                     int32_t* __restrict__ item_expert,
+                                                     int32_t* __restrict__ tile_expert,
+                                                     unsigned* __restrict__ used,
+                                                     unsigned* __restrict__ gemm_status) {
+    __shared__ unsigned count[256], start[256], fill[256];
+    __shared__ unsigned total;
+    const unsigned t = threadIdx.x;
+    if (t < 256) {
+        count[t] = 0;
+        fill[t] = 0;
+    }
+    __syncthreads();
+    for (unsigned s = t; s < slots; s += 1024)
+        atomicAdd(&count[min(unsigned(idx[s]), experts - 1)], 1u);
+    __syncthreads();
+    if (t < 64) {  // exclusive scan of the padded counts, four experts per lane
+        unsigned padded[4], sum = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const unsigned e = 4 * t + k;
+            padded[k] = e < experts ? (count[e] + pad - 1) / pad * pad : 0;
+            sum += padded[k];
+        }
+        unsigned incl = sum;
+        for (int off = 1; off < 64; off <<= 1) {
+            const unsigned v = __shfl_up(incl, off);
+            if (int(t) >= off)
+                incl += v;
+        }
+        unsigned at = incl - sum;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            start[4 * t + k] = at;
+            at += padded[k];
+        }
+        if (t == 63)
+            total = incl;
+    }
+    __syncthreads();
+    for (unsigned s = t; s < slots; s += 1024) {
+        const unsigned e = min(unsigned(idx[s]), experts - 1);
+        const unsigned p = start[e] + atomicAdd(&fill[e], 1u);
+        pos[s] = int32_t(p);
+        inv[p] = int32_t(s);
+    }
+    if (t < experts) {  // padding rows, the expert's items and tiles
+        const unsigned first = start[t], n = count[t];
+        const unsigned end = first + (n + pad - 1) / pad * pad;
+        const unsigned live = first + (n + kItemRows - 1) / kItemRows * kItemRows;
+        for (unsigned p = first + n; p < end; ++p)
+            inv[p] = -1;
+        for (unsigned i = first / kItemRows; i < end / kItemRows; ++i)
+            item_expert[i] = i < live / kItemRows ? int32_t(t) : -1;
+        if (pad == kTileRows)
+            for (unsigned j = first / kTileRows; j < end / kTileRows; ++j)
+                tile_expert[j] = int32_t(t);
+    }
+    for (unsigned i = total / kItemRows + t; i < max_items; i += 1024)
+        item_expert[i] = -1;
+    if (pad == kTileRows)
+        for (unsigned j = total / kTileRows + t; j < max_items * kItemRows / kTileRows;
+             j += 1024)
+            tile_expert[j] = -1;
+    if (t == 0) {
+        *used = total;
+        *gemm_status = 0;
+    }
+}
+
+// xp[p] = x[inv[p] / k] (zero for padding rows), positions below *used; 4 values a thread.
+__global__ __launch_bounds__(256) void gather_kernel(const float* __restrict__ x,
+                                                     const int32_t* __restrict__ inv,
+                                                     const unsigned* __restrict__ used,
+                                                     unsigned k, unsigned hidden,
+                                                     size_t positions, float* __restrict__ xp) {
+    const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
+    const unsigned quads = hidden / 4;
+    const size_t p = i / quads;
+    if (p >= positions || p >= *used)
+        return;
+    const size_t d = (i % quads) * 4;
+    const int s = inv[p];
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (s >= 0)
+        v = *reinterpret_cast<const float4*>(x + size_t(s / int(k)) * hidden + d);
+    *reinterpret_cast<float4*>(xp + p * hidden + d) = v;
+}
+
+// combine_kernel over down rows in position order: slot s's row is down[pos[s]].
+__global__ __launch_bounds__(256) void combine_pos_kernel(const float* down,
+                                                          const int32_t* pos, const float* w,
+                                                          const float* shared,
+                                                          const float* gate, unsigned k,
+                                                          unsigned hidden, size_t tokens,
+                                                          float* y) {
+    const size_t e = size_t(blockIdx.x) * 256 + threadIdx.x;
+    if (e >= tokens * hidden)
+        return;
+    const size_t t = e / hidden, d = e % hidden;
+    float sum = 0.f;
+    for (unsigned i = 0; i < k; ++i)
+        sum += down[size_t(pos[t * k + i]) * hidden + d] * w[t * k + i];
     y[e] = sum + shared[e] * sigmoid_of(gate[t]);
 }
 
@@ -80,6 +217,48 @@ size_t align256(size_t n) {
     return (n + 255) & ~size_t(255);
 }
 
+// A product over more than kItemRows rows as one launch of kItemRows-row jobs (x and y
+// stepping by kItemRows rows; the MFMA kernel when the format takes it, with `paired`),
+// then the remaining rows; up to kItemRows rows as one job.
+int run_rows(const IndexedJob& ij, hipStream_t st) {
+    const kdq_matvec_job& j = ij.job;
+    if (j.rows <= kItemRows)
+        return indexed_gemv_batch(&ij, 1, st);
+    IndexedJob a = ij;
+    a.job.rows = kItemRows;
+    const size_t full = j.rows / kItemRows;
+    int rc = indexed_gemv_affine(a, unsigned(full), size_t(kItemRows) * j.in,
+                                 size_t(kItemRows) * j.stride, st);
+    if (rc || j.rows % kItemRows == 0)
+        return rc;
+    IndexedJob rest = ij;
+    rest.job.rows = j.rows % kItemRows;
+    rest.job.input = j.input + full * kItemRows * j.in;
+    rest.job.output = j.output + full * kItemRows * j.stride;
+    return indexed_gemv_batch(&rest, 1, st);
+}
+
+// Whether an expert stack can run on the grouped GEMM: an encoding it takes, whole 16-row
+// tiles per expert and experts stored back to back (one pack covers the stack).
+bool gemm_stack(const kdq_gguf_tensor& m, size_t rows, size_t in) {
+    return grouped_gemm_takes(m.encoding, in) && rows % 16 == 0 &&
+           m.expert_bytes == rows * m.row_bytes && kdq_gguf_packed_bytes(m.encoding, in, rows);
+}
+
+__global__ void or_status_kernel(unsigned* status, const unsigned* from, unsigned mask) {
+    if (threadIdx.x == 0 && (*from & mask))
+        atomicOr(status, *from & mask);
+}
+
+// Whether a gate job of `rows` rows can run paired with its up matrix through run_rows.
+bool rows_pairable(const kdq_matvec_job& gate) {
+    if (gate.rows <= kItemRows)
+        return swiglu_pairable(gate, 1);
+    kdq_matvec_job a = gate;
+    a.rows = kItemRows;
+    return gate.rows % kItemRows == 0 && swiglu_pairable(a, gate.rows / kItemRows);
+}
+
 }  // namespace
 }  // namespace kdq
 
@@ -95,8 +274,9 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
     if (!H || !E || !K || !F || !S || !L.shared_gate)
         return KDQ_ERR_ARGUMENT;
     const size_t slots = rows * K;
-    if (E > 256 || K > 8 || K > E || slots > 512 || H > 0xffffffu || F > 0xffffffu ||
-        S > 0xffffffu)
+    const bool grouped = rows > kSlotRows;
+    if (E > 256 || K > 8 || K > E || rows > 4096 || slots > kMaxGroupedSlots ||
+        H > 0xffffffu || F > 0xffffffu || S > 0xffffffu)
         return KDQ_ERR_SHAPE;
     if (!tensor_ok(L.router, E, H, false) || !tensor_ok(L.gate_exps, F, H, true) ||
         !tensor_ok(L.up_exps, F, H, true) || !tensor_ok(L.down_exps, H, F, true) ||
@@ -108,9 +288,29 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
     if (overlaps(y, rows * H * 4, x, rows * H * 4))
         return KDQ_ERR_ALIAS;
     // workspace: logits, shared gate/up rows, gate scalars, routing (unless the caller
-    // takes it), expert gate/up rows, expert downs, shared down
-    const size_t sizes[] = {rows * E * 4, rows * S * 4, rows * S * 4, rows * 4, slots * 4,
-                            slots * 4, slots * F * 4, slots * F * 4, slots * H * 4, rows * H * 4};
+    // takes it), expert gate/up rows, expert downs, shared down; grouped: per position
+    // (slots padded per expert to whole items), plus x in position order, the slot and
+    // position maps, the items' experts and the count of positions in use
+    // (grouped on the GEMM: token tiles of kTileRows, the packed expert stacks, fp16 x)
+    const bool gemm_gu = grouped && gemm_stack(L.gate_exps, F, H) &&
+                         gemm_stack(L.up_exps, F, H);
+    const bool gemm_dn = grouped && gemm_stack(L.down_exps, H, F);
+    const size_t pad = gemm_gu || gemm_dn ? kTileRows : kItemRows;
+    const size_t positions = grouped ? (slots + (pad - 1) * E + pad - 1) / pad * pad : slots;
+    const size_t items = positions / kItemRows;
+    const size_t gu_bytes = gemm_gu ? kdq_gguf_packed_bytes(L.gate_exps.encoding, H, F) : 0;
+    const size_t up_bytes = gemm_gu ? kdq_gguf_packed_bytes(L.up_exps.encoding, H, F) : 0;
+    const size_t dn_bytes = gemm_dn ? kdq_gguf_packed_bytes(L.down_exps.encoding, F, H) : 0;
+    const size_t xs_bytes = gemm_gu || gemm_dn ? positions * std::max(H, F) * 2 : 0;
+    const size_t sizes[] = {rows * E * 4,      rows * S * 4,      rows * S * 4,
+                            rows * 4,          slots * 4,         slots * 4,
+                            positions * F * 4, positions * F * 4, positions * H * 4,
+                            rows * H * 4,      grouped ? positions * H * 4 : 0,
+                            grouped ? slots * 4 : 0, grouped ? positions * 4 : 0,
+                            grouped ? items * 4 : 0, size_t(grouped ? 8 : 0),
+                            grouped ? positions / kTileRows * 4 + 4 : 0,
+                            gu_bytes * E, up_bytes * E, dn_bytes * E, xs_bytes,
+                            gemm_gu || gemm_dn ? positions * 4 : 0};
     constexpr size_t kParts = sizeof(sizes) / sizeof(sizes[0]);
     size_t total = 0;
     for (size_t b : sizes)
@@ -132,6 +332,18 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
     auto* u = static_cast<float*>(part[7]);
     auto* d = static_cast<float*>(part[8]);
     auto* ds = static_cast<float*>(part[9]);
+    auto* xp = static_cast<float*>(part[10]);
+    auto* pos = static_cast<int32_t*>(part[11]);
+    auto* inv = static_cast<int32_t*>(part[12]);
+    auto* item_expert = static_cast<int32_t*>(part[13]);
+    auto* used = static_cast<unsigned*>(part[14]);
+    auto* gemm_status = used + 1;
+    auto* tile_expert = static_cast<int32_t*>(part[15]);
+    auto* packed_gate = part[16];
+    auto* packed_up = part[17];
+    auto* packed_down = part[18];
+    auto* xs = static_cast<uint16_t*>(part[19]);
+    auto* sigma = static_cast<float*>(part[20]);
     auto st = static_cast<hipStream_t>(stream);
 
     // 1. router, shared-gate scalar, shared gate / up (with the swiglu in the same launch
@@ -139,13 +351,19 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
     const kdq_gguf_tensor gate_vector{L.shared_gate, H * 4, 0, KDQ_F32};
     const kdq_matvec_job shared_gate = job(L.gate_shexp, x, rows, H, S, sg, status);
     const bool pair_shared =
-        same_layout(L.gate_shexp, L.up_shexp) && swiglu_pairable(shared_gate, 1);
+        same_layout(L.gate_shexp, L.up_shexp) && rows_pairable(shared_gate);
     IndexedJob first[4] = {{job(L.router, x, rows, H, E, logits, status), nullptr, 0, 1, nullptr},
                            {job(gate_vector, x, rows, H, 1, gate, status), nullptr, 0, 1, nullptr},
                            {shared_gate, nullptr, 0, 1, pair_shared ? L.up_shexp.weights : nullptr},
                            {job(L.up_shexp, x, rows, H, S, su, status), nullptr, 0, 1, nullptr}};
-    if ((rc = indexed_gemv_batch(first, pair_shared ? 3 : 4, st)))
-        return rc;
+    if (!grouped) {
+        if ((rc = indexed_gemv_batch(first, pair_shared ? 3 : 4, st)))
+            return rc;
+    } else {
+        for (int i = 0; i < (pair_shared ? 3 : 4); ++i)
+            if ((rc = run_rows(first[i], st)))
+                return rc;
+    }
     // 2. routing, straight into the caller's buffers when given
     if ((rc = route_selection(logits, rows, E, K, idx, w, st)))
         return rc;
@@ -154,6 +372,106 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
         hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((rows * S + 255) / 256)), dim3(256), 0,
                            st, sg, su, rows * S);
         KDQ_HIP(hipGetLastError());
+    }
+    if (grouped) {
+        // 4'. slots grouped by expert into padded segments (8-row items, 128-row tiles)
+        hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, st, idx, unsigned(slots),
+                           unsigned(E), unsigned(pad), unsigned(items), pos, inv, item_expert,
+                           tile_expert, used, gemm_status);
+        KDQ_HIP(hipGetLastError());
+        const size_t xs8 = kItemRows * H, fs8 = kItemRows * F;
+        // the expert products on the GEMV items (every encoding; the fallback of the GEMM)
+        auto items_gate_up = [&]() -> int {
+            hipLaunchKernelGGL(gather_kernel, dim3(unsigned((positions * (H / 4) + 255) / 256)),
+                               dim3(256), 0, st, x, inv, used, unsigned(K), unsigned(H),
+                               positions, xp);
+            KDQ_HIP(hipGetLastError());
+            const IndexedJob gj{job(L.gate_exps, xp, kItemRows, H, F, g, status), item_expert,
+                                L.gate_exps.expert_bytes, unsigned(E), nullptr};
+            if (same_layout(L.gate_exps, L.up_exps) && swiglu_pairable(gj.job, items)) {
+                IndexedJob pj = gj;
+                pj.paired = L.up_exps.weights;
+                return indexed_gemv_affine(pj, unsigned(items), xs8, fs8, st);
+            }
+            const IndexedJob uj{job(L.up_exps, xp, kItemRows, H, F, u, status), item_expert,
+                                L.up_exps.expert_bytes, unsigned(E), nullptr};
+            int r;
+            if ((r = indexed_gemv_affine(gj, unsigned(items), xs8, fs8, st)) ||
+                (r = indexed_gemv_affine(uj, unsigned(items), xs8, fs8, st)))
+                return r;
+            hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((positions * F + 255) / 256)),
+                               dim3(256), 0, st, g, u, positions * F);
+            KDQ_HIP(hipGetLastError());
+            return KDQ_OK;
+        };
+        auto items_down = [&]() -> int {
+            const IndexedJob dj{job(L.down_exps, g, kItemRows, F, H, d, status), item_expert,
+                                L.down_exps.expert_bytes, unsigned(E), nullptr};
+            return indexed_gemv_affine(dj, unsigned(items), fs8, xs8, st);
+        };
+        // 4''. expert gate / up
+        if (gemm_gu) {  // both stacks packed (this call), one grouped GEMM each, swiglu
+            if ((rc = kdq_gguf_pack(L.gate_exps.encoding, L.gate_exps.weights,
+                                    L.gate_exps.row_bytes, H, E * F, packed_gate, st)) ||
+                (rc = kdq_gguf_pack(L.up_exps.encoding, L.up_exps.weights, L.up_exps.row_bytes,
+                                    H, E * F, packed_up, st)) ||
+                (rc = grouped_gemm(L.gate_exps.encoding, packed_gate, gu_bytes, tile_expert, F,
+                                   H, x, inv, unsigned(K), used, positions, g, gemm_status, xs,
+                                   sigma, st)) ||
+                (rc = grouped_gemm(L.up_exps.encoding, packed_up, up_bytes, tile_expert, F, H,
+                                   x, inv, unsigned(K), used, positions, u, gemm_status, xs,
+                                   sigma, st)))
+                return rc;
+            hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((positions * F + 255) / 256)),
+                               dim3(256), 0, st, g, u, positions * F);
+            KDQ_HIP(hipGetLastError());
+        } else if ((rc = items_gate_up())) {
+            return rc;
+        }
+        // 5'. expert downs, the shared down
+        if (gemm_dn) {
+            if ((rc = kdq_gguf_pack(L.down_exps.encoding, L.down_exps.weights,
+                                    L.down_exps.row_bytes, F, E * H, packed_down, st)) ||
+                (rc = grouped_gemm(L.down_exps.encoding, packed_down, dn_bytes, tile_expert, H,
+                                   F, g, nullptr, 1u, used, positions, d, gemm_status, xs,
+                                   sigma, st)))
+                return rc;
+        } else if ((rc = items_down())) {
+            return rc;
+        }
+        const IndexedJob sj{job(L.down_shexp, sg, rows, S, H, ds, status), nullptr, 0, 1,
+                            nullptr};
+        if ((rc = run_rows(sj, st)))
+            return rc;
+        auto combine = [&]() -> int {
+            hipLaunchKernelGGL(combine_pos_kernel, dim3(unsigned((rows * H + 255) / 256)),
+                               dim3(256), 0, st, d, pos, w, ds, gate, unsigned(K), unsigned(H),
+                               rows, y);
+            KDQ_HIP(hipGetLastError());
+            return KDQ_OK;
+        };
+        // 6'. combine in selection order, each slot's down at its position
+        if ((rc = combine()))
+            return rc;
+        if (gemm_gu || gemm_dn) {
+            // the GEMM's flags: a non-finite scale is the caller's status bit 1; a scale
+            // that could take a dequantised weight past the fp16 range (never in real
+            // checkpoints) makes this call redo its expert products on the GEMV items,
+            // which decode exactly (one host wait, only on this path)
+            unsigned flags = 0;
+            KDQ_HIP(hipMemcpyAsync(&flags, gemm_status, sizeof flags, hipMemcpyDeviceToHost,
+                                   st));
+            KDQ_HIP(hipStreamSynchronize(st));
+            if (flags & 2u) {
+                if ((rc = items_gate_up()) || (rc = items_down()) || (rc = combine()))
+                    return rc;
+            } else if ((flags & 1u) && status) {
+                hipLaunchKernelGGL(or_status_kernel, dim3(1), dim3(64), 0, st, status,
+                                   gemm_status, 1u);
+                KDQ_HIP(hipGetLastError());
+            }
+        }
+        return KDQ_OK;
     }
     // 4. expert gate / up at the routed slices, every slot in one launch (slot s reads
     //    token s / K's row and writes row s), as a pair with the swiglu when the MFMA

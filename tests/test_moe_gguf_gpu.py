@@ -75,12 +75,15 @@ def test_moe_gguf_parity(device, oracle, rows, encs):
     assert int(status.item()) == 0
 
 
-@pytest.mark.parametrize("rows,top_k", [(9, 4), (16, 4), (64, 8)])
-@pytest.mark.parametrize("encs", [MIXED, EXACT], ids=["mixed", "exact"])
+@pytest.mark.parametrize("rows,top_k", [(9, 4), (16, 4), (64, 8), (200, 8)])
+@pytest.mark.parametrize("encs", [MIXED, EXACT, SPLIT], ids=["mixed", "exact", "split"])
 def test_moe_gguf_more_rows(device, oracle, rows, top_k, encs):
-    """Past the 8-row pass: 9 and 16 rows (two passes of the router / shared batch and of
-    the exact kernel's 8-row loop, unpaired rows of the shared swiglu), and 64 rows x
-    top-8 = 512 slots, the largest layer the entry point takes."""
+    """Past 8 rows the slots are grouped by expert into padded segments: 9 and 16 rows (two
+    passes of the router / shared batch), 64 rows x top-8 = 512 slots, and 200 rows x
+    top-8 (100 slots per expert).  MIXED runs gate, up and down on the grouped prefill
+    GEMM (128-row token tiles of one expert each); SPLIT runs gate / up on the GEMM and
+    its Q4_0 down on 8-row GEMV items over the same tiles; EXACT runs the exact kernel's
+    8-row items."""
     import torch
     H, E, F, S = 512, 16, 256, 512
     spec = make_layer(40 + rows, H, E, top_k, F, S, encs)
@@ -109,6 +112,54 @@ def test_moe_gguf_qwen3_shape(device, oracle):
         assert_close(y.cpu().numpy(), want, what=f"qwen3 shape rows={rows}")
 
 
+@pytest.mark.parametrize("encs", [MIXED, SPLIT], ids=["mixed", "split"])
+def test_moe_gguf_prefill_chunk(device, oracle, encs):
+    """A 512-token prefill chunk at Qwen3-30B-A3B's geometry (4096 slots over 128
+    experts).  Each token's output depends only on its own row and routing, so the
+    oracle runs on a sample of tokens (the first, the last, and a seeded spread)."""
+    import torch
+    H, E, K, F, S, rows = 2048, 128, 8, 768, 768, 512
+    spec = make_layer(9, H, E, K, F, S, encs)
+    from kadan_amd import ops
+    x = synth.normal(91, 1, rows * H).reshape(rows, H)
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    y, sel, ws = ops.moe_gguf(to_device(torch, device, spec), torch.from_numpy(x).to(device),
+                              status=status)
+    y, sel, ws = y.cpu().numpy(), sel.cpu().numpy(), ws.cpu().numpy()
+    assert int(status.item()) == 0 and np.isfinite(y).all()
+    pick = np.union1d(np.random.default_rng(92).choice(rows, 22, replace=False), [0, rows - 1])
+    want, idx, w = oracle.moe_gguf_forward(spec, x[pick])
+    assert np.array_equal(sel[pick], idx)
+    assert np.abs(ws[pick] - w).max() < 1e-6
+    assert_close(y[pick], want, what=f"moe_gguf prefill chunk {len(pick)} sampled tokens")
+    # deterministic: the same call again gives the same bits
+    y2, _, _ = ops.moe_gguf(to_device(torch, device, spec), torch.from_numpy(x).to(device))
+    assert np.array_equal(y, y2.cpu().numpy())
+
+
+def test_moe_gguf_grouped_fp16_range_fallback(device, oracle):
+    """An expert gate scale whose dequantised weights could pass the fp16 range (d = 1000)
+    makes the grouped GEMM flag the call, which then redoes its expert products on the
+    8-row GEMV items (exact decode): y is still the exact product and status stays 0."""
+    import torch
+    H, E, K, F, S, rows = 512, 16, 4, 256, 512, 32
+    spec = make_layer(12, H, E, K, F, S, MIXED)
+    enc, arr = spec["gate_exps"]
+    arr = arr.copy()
+    big = np.array([1000.0], np.float16).view(np.uint16)[0]
+    arr[:, :, 0], arr[:, :, 1] = big & 255, big >> 8  # d of every expert's first block
+    spec["gate_exps"] = (enc, arr)
+    x = synth.normal(13, 1, rows * H).reshape(rows, H)
+    want, idx, w = oracle.moe_gguf_forward(spec, x)
+    from kadan_amd import ops
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    y, sel, _ = ops.moe_gguf(to_device(torch, device, spec), torch.from_numpy(x).to(device),
+                             status=status)
+    assert np.array_equal(sel.cpu().numpy(), idx)
+    assert int(status.item()) == 0
+    assert_close(y.cpu().numpy(), want, what="moe_gguf grouped fp16-range fallback")
+
+
 def test_moe_gguf_nonfinite_weight_status(device):
     import torch
     H, E, K, F, S = 256, 8, 2, 256, 256
@@ -130,5 +181,7 @@ def test_moe_gguf_rejections(device):
     dev = to_device(torch, device, make_layer(6, H, E, K, F, S, MIXED))
     with pytest.raises(KdqError, match="kdq_projection_shape"):
         ops.moe_gguf(dict(dev, top_k=9), torch.ones(1, H, device=device))
-    with pytest.raises(KdqError, match="kdq_projection_shape"):  # rows * top_k > 512
-        ops.moe_gguf(dev, torch.ones(257, H, device=device))
+    with pytest.raises(KdqError, match="kdq_projection_shape"):  # rows > 4096
+        ops.moe_gguf(dev, torch.ones(4097, H, device=device))
+    with pytest.raises(KdqError, match="kdq_projection_shape"):  # rows * top_k > 8192
+        ops.moe_gguf(dict(dev, top_k=8), torch.ones(1025, H, device=device))
