@@ -40,9 +40,12 @@
 namespace kdq {
 namespace {
 
-__global__ __launch_bounds__(256) void swiglu_kernel(float* gate, const float* up, size_t n) {
+// gate[i] = silu(gate[i]) * up[i] for i < n, and (grouped layers) rows below *used of
+// `width` values each
+__global__ __launch_bounds__(256) void swiglu_kernel(float* gate, const float* up, size_t n,
+                                                     const unsigned* used, unsigned width) {
     const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
-    if (i < n)
+    if (i < n && (!used || i / width < *used))
         gate[i] = silu_of(gate[i]) * up[i];
 }
 
@@ -370,7 +373,7 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
     // 3. shared swiglu, unless paired above
     if (!pair_shared) {
         hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((rows * S + 255) / 256)), dim3(256), 0,
-                           st, sg, su, rows * S);
+                           st, sg, su, rows * S, nullptr, 1u);
         KDQ_HIP(hipGetLastError());
     }
     if (grouped) {
@@ -400,7 +403,7 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
                 (r = indexed_gemv_affine(uj, unsigned(items), xs8, fs8, st)))
                 return r;
             hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((positions * F + 255) / 256)),
-                               dim3(256), 0, st, g, u, positions * F);
+                               dim3(256), 0, st, g, u, positions * F, used, unsigned(F));
             KDQ_HIP(hipGetLastError());
             return KDQ_OK;
         };
@@ -423,7 +426,7 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
                                    sigma, st)))
                 return rc;
             hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((positions * F + 255) / 256)),
-                               dim3(256), 0, st, g, u, positions * F);
+                               dim3(256), 0, st, g, u, positions * F, used, unsigned(F));
             KDQ_HIP(hipGetLastError());
         } else if ((rc = items_gate_up())) {
             return rc;
@@ -490,7 +493,7 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
             (rc = indexed_gemv_affine(uj, unsigned(slots), H, F, st, unsigned(K))))
             return rc;
         hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((slots * F + 255) / 256)), dim3(256), 0,
-                           st, g, u, slots * F);
+                           st, g, u, slots * F, nullptr, 1u);
         KDQ_HIP(hipGetLastError());
     }
     // 5. expert downs (one launch over every slot) and the shared down
