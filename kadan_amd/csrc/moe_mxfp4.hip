@@ -109,7 +109,7 @@ __device__ __forceinline__ int heap_route(POf p_of, unsigned experts, unsigned k
 __device__ __forceinline__ void route_token(const float* __restrict__ logits, unsigned t,
                                             unsigned experts, unsigned top_k,
                                             int32_t* __restrict__ idx, float* __restrict__ weight,
-                                            unsigned lane) {
+                                            unsigned lane, int* lds_idx = nullptr) {
     const float* l = logits + size_t(t) * experts;
     float v[4], p[4];
     float maximum = -INFINITY;
@@ -193,6 +193,8 @@ __device__ __forceinline__ void route_token(const float* __restrict__ logits, un
     if (lane < top_k) {
         idx[size_t(t) * top_k + lane] = chosen_e;
         weight[size_t(t) * top_k + lane] = chosen_p / sum;
+        if (lds_idx)
+            lds_idx[t * top_k + lane] = chosen_e;
     }
 }
 
@@ -207,13 +209,17 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
 
 // Stable counting sort of slots by expert by one workgroup of 1024 threads (every thread
 // calls it); also the work items.
+// Also slot_row[r] = item * kItemRows + row of the slot at position r (the K-sliced
+// finalize runs over occupied rows only).
 __device__ __forceinline__ void permute_slots(const int32_t* __restrict__ idx, unsigned slots,
                                               unsigned experts, int32_t* __restrict__ offsets,
                                               int32_t* __restrict__ perm,
                                               int32_t* __restrict__ items,
                                               int32_t* __restrict__ item_count,
-                                              int32_t* __restrict__ position) {
-    __shared__ int counts[kMaxExperts], base[kMaxExperts];
+                                              int32_t* __restrict__ position,
+                                              int32_t* __restrict__ slot_row) {
+    __shared__ int counts[kMaxExperts], base[kMaxExperts], segment[kMaxExperts],
+        item_base[kMaxExperts];
     __shared__ int wave_counts[16][kMaxExperts];
     const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     for (unsigned e = tid; e < experts; e += 1024)
@@ -227,6 +233,8 @@ __device__ __forceinline__ void permute_slots(const int32_t* __restrict__ idx, u
         for (unsigned e = 0; e < experts; ++e) {
             offsets[e] = acc;
             base[e] = acc;
+            segment[e] = acc;
+            item_base[e] = n;
             for (int r = 0; r < counts[e]; r += kItemRows) {
                 items[2 * n] = int(e);
                 items[2 * n + 1] = r;
@@ -264,6 +272,8 @@ __device__ __forceinline__ void permute_slots(const int32_t* __restrict__ idx, u
             perm[r] = int(s);
             if (position)
                 position[s] = r;  // inverse permutation
+            const int within = r - segment[e];
+            slot_row[r] = (item_base[e] + within / kItemRows) * kItemRows + within % kItemRows;
         }
         __syncthreads();
         for (unsigned x = tid; x < experts; x += 1024) {
@@ -282,8 +292,9 @@ __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* __restrict
                                                        int32_t* __restrict__ perm,
                                                        int32_t* __restrict__ items,
                                                        int32_t* __restrict__ item_count,
-                                                       int32_t* __restrict__ position) {
-    permute_slots(idx, slots, experts, offsets, perm, items, item_count, position);
+                                                       int32_t* __restrict__ position,
+                                                       int32_t* __restrict__ slot_row) {
+    permute_slots(idx, slots, experts, offsets, perm, items, item_count, position, slot_row);
 }
 
 // --------------------------------------------------------------- grouped GEMMs
@@ -538,48 +549,90 @@ __global__ __launch_bounds__(256) void gather_kernel(const uint16_t* __restrict_
     gather_block(x, hidden, token, xa, tiles, tau, id / blocks % 32, id % blocks);
 }
 
-// Small layers (decode): routing, permutation and gather in one workgroup of 1024 threads,
-// one launch instead of three.  Phases are separated by workgroup barriers, which make
-// each phase's global writes visible to the next (all of them run on this compute unit).
-// The gather walks the items' occupied rows only, from a row prefix kept in LDS.
+// Small layers (decode, at most kPrologueSlots slots): routing, permutation and gather in
+// one workgroup of 1024 threads, one launch instead of three, with every intermediate in
+// LDS: the routed experts, the permutation (one wavefront: a slot's position is the number
+// of slots of a lower expert plus those of its own expert before it, the same stable order
+// as permute_slots; with at most kItemRows slots per expert each expert is one item) and,
+// when they fit, the token rows of x, which the waves that do not route copy into LDS
+// while routing runs.  The global outputs are those of route_kernel + permute_kernel.
+constexpr unsigned kPrologueXBytes = 48 * 1024;
+
 __global__ __launch_bounds__(1024) void prologue_kernel(
     const float* __restrict__ logits, unsigned tokens, unsigned experts, unsigned top_k,
     int32_t* __restrict__ idx, float* __restrict__ weight, int32_t* __restrict__ offsets,
     int32_t* __restrict__ perm, int32_t* __restrict__ items, int32_t* __restrict__ item_count,
-    int32_t* __restrict__ position, const uint16_t* __restrict__ x, unsigned hidden,
-    uint8_t* __restrict__ xa, size_t tiles) {
-    __shared__ int row0[kPrologueSlots + 1], first_pos[kPrologueSlots];
-    __shared__ int n_items;
-    const unsigned wave = threadIdx.x / 64;
+    int32_t* __restrict__ position, int32_t* __restrict__ slot_row,
+    const uint16_t* __restrict__ x, unsigned hidden, uint8_t* __restrict__ xa, size_t tiles) {
+    extern __shared__ __align__(16) uint8_t x_rows[];  // tokens * hidden bf16, if they fit
+    __shared__ int s_idx[kPrologueSlots], s_perm[kPrologueSlots], s_row[kPrologueSlots];
+    const unsigned wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const unsigned slots = tokens * top_k;
+    const size_t x_bytes = size_t(tokens) * hidden * 2;
+    const bool x_in_lds = x_bytes <= kPrologueXBytes;
+    const unsigned routers = min(tokens, 16u);
     for (unsigned t = wave; t < tokens; t += 16)
-        route_token(logits, t, experts, top_k, idx, weight, threadIdx.x % 64);
-    __syncthreads();
-    permute_slots(idx, unsigned(tokens * top_k), experts, offsets, perm, items, item_count,
-                  position);
-    __syncthreads();
-    if (threadIdx.x == 0) {  // items hold at least one row each: at most one per slot
-        const int n = *item_count;
-        int acc = 0;
-        for (int i = 0; i < n; ++i) {
-            const Item it = load_item(items, offsets, unsigned(i));
-            row0[i] = acc;
-            first_pos[i] = it.segment + it.first;
-            acc += it.count;
-        }
-        row0[n] = acc;
-        n_items = n;
+        route_token(logits, t, experts, top_k, idx, weight, lane, s_idx);
+    if (x_in_lds && wave >= routers) {  // x rows into LDS meanwhile (16-byte units)
+        const unsigned helpers = (16 - routers) * 64, me = threadIdx.x - routers * 64;
+        for (size_t u = me; u < x_bytes / 16; u += helpers)
+            *reinterpret_cast<u32x4*>(x_rows + 16 * u) =
+                load16(reinterpret_cast<const uint8_t*>(x) + 16 * u);
     }
     __syncthreads();
+    if (x_in_lds && routers == 16) {  // every wave routed: copy now
+        for (size_t u = threadIdx.x; u < x_bytes / 16; u += 1024)
+            *reinterpret_cast<u32x4*>(x_rows + 16 * u) =
+                load16(reinterpret_cast<const uint8_t*>(x) + 16 * u);
+    }
+    if (wave == 0) {
+        const bool valid = lane < slots;
+        const int e = valid ? s_idx[lane] : 0x7fffffff;
+        int lower = 0, before = 0;
+        for (unsigned j = 0; j < slots; ++j) {
+            const int ej = s_idx[j];
+            lower += ej < e;
+            before += (ej == e) & (j < lane);
+        }
+        // the expert's first slots, one per used expert
+        const unsigned long long leads = __ballot(valid && before == 0);
+        if (valid) {
+            perm[lower + before] = int(lane);
+            position[lane] = lower + before;
+            s_perm[lower + before] = int(lane);
+        }
+        // offsets[e] = slots routed to experts below e
+        for (unsigned x_e = lane; x_e <= experts; x_e += 64) {
+            int below = 0;
+            for (unsigned j = 0; j < slots; ++j)
+                below += s_idx[j] < int(x_e);
+            offsets[x_e] = below;
+        }
+        // item of each used expert: the number of used experts below it
+        int item = 0;
+        for (unsigned j = 0; j < slots; ++j)
+            item += ((leads >> j) & 1ull) && s_idx[j] < e;
+        if (valid) {
+            slot_row[lower + before] = item * kItemRows + before;
+            s_row[lower + before] = item * kItemRows + before;
+            if (before == 0) {
+                items[2 * item] = e;
+                items[2 * item + 1] = 0;
+            }
+        }
+        if (lane == 0)
+            *item_count = int(__popcll(leads));
+    }
+    __syncthreads();
+    // every occupied row: position g, 32-value block b
     const unsigned blocks = hidden / 32;
-    const unsigned units = unsigned(row0[n_items]) * blocks;
-    for (unsigned u = threadIdx.x; u < units; u += 1024) {
-        const int g = int(u / blocks);  // occupied row, counted over the items
-        int i = 0;
-        while (row0[i + 1] <= g)
-            ++i;
-        const unsigned row = unsigned(g - row0[i]);
-        const size_t token = size_t(perm[first_pos[i] + int(row)] / int(top_k));
-        gather_block(x, hidden, token, xa, tiles, 2 * size_t(i) + row / 32, row % 32, u % blocks);
+    const uint16_t* rows = x_in_lds ? reinterpret_cast<const uint16_t*>(x_rows) : x;
+    for (unsigned u = threadIdx.x; u < slots * blocks; u += 1024) {
+        const unsigned g = u / blocks;
+        const unsigned item = unsigned(s_row[g]) / kItemRows, row = unsigned(s_row[g]) % kItemRows;
+        const size_t token = size_t(s_perm[g] / int(top_k));
+        gather_block(rows, hidden, token, xa, tiles, 2 * size_t(item) + row / 32, row % 32,
+                     u % blocks);
     }
 }
 
@@ -898,25 +951,20 @@ __global__ __launch_bounds__(kGemmWaves * 64, 3) void gate_up_kernel(
 }
 
 // h = silu(sum_s g_s) * (sum_s u_s), slices summed in order, into the down product's
-// activation tiles: grid (inter / 256, item rows); one thread per (item row, feature), each
-// half wavefront one 32-feature block (inter % 64 == 0).
+// activation tiles: grid (inter / 256, slots): one thread per (occupied row, feature),
+// the row slot_row[position] = item * kItemRows + row; each half wavefront one 32-feature
+// block (inter % 64 == 0).
 __global__ __launch_bounds__(256) void finalize_kernel(const float* __restrict__ part_g,
                                                        const float* __restrict__ part_u,
                                                        size_t part_stride, unsigned inter,
                                                        unsigned slices,
-                                                       const int32_t* __restrict__ offsets,
-                                                       const int32_t* __restrict__ items,
-                                                       const int32_t* __restrict__ item_count,
+                                                       const int32_t* __restrict__ slot_row,
                                                        uint8_t* __restrict__ ha, size_t tiles) {
-    const unsigned item = blockIdx.y / kItemRows, row = blockIdx.y % kItemRows;
-    if (int(item) >= *item_count)
-        return;
-    const Item it = load_item(items, offsets, item);
-    if (int(row) >= it.count)
-        return;  // the whole workgroup
+    const unsigned at_row = unsigned(slot_row[blockIdx.y]);
+    const unsigned item = at_row / kItemRows, row = at_row % kItemRows;
     const unsigned f = blockIdx.x * 256 + threadIdx.x;
     const bool live = f < inter;
-    const size_t at = size_t(blockIdx.y) * inter + (live ? f : 0);
+    const size_t at = size_t(at_row) * inter + (live ? f : 0);
     float gs = 0.f, us = 0.f;
     for (unsigned s = 0; s < slices; ++s) {
         gs += part_g[s * part_stride + at];
@@ -1054,7 +1102,7 @@ __global__ __launch_bounds__(256) void mxfp4_dequant_kernel(const uint8_t* __res
 
 // Workspace carve-up (device bytes, 256-aligned pieces).
 struct MoeScratch {
-    int32_t *idx, *offsets, *perm, *position, *items, *item_count;
+    int32_t *idx, *offsets, *perm, *position, *slot_row, *items, *item_count;
     float* weight;
     uint8_t *xa, *ha;  // activation tiles of gate/up (x) and of down (h)
     float *part_g, *part_u, *part_d;
@@ -1107,7 +1155,7 @@ size_t moe_scratch_bytes(size_t tokens, size_t hidden, size_t inter, size_t expe
     const size_t tiles = 2 * max_items(slots, experts);
     const size_t partial_gu =
         ks.gate_up > 1 ? 2 * align256(ks.gate_up * tiles * kTileRows * inter * 4) : 0;
-    return align256(slots * 4) * 4 + align256((experts + 1) * 4) + align256(items * 8) +
+    return align256(slots * 4) * 5 + align256((experts + 1) * 4) + align256(items * 8) +
            align256(4) + align256(tile_bytes(tiles, hidden / 64, kXTerms)) +
            align256(tile_bytes(tiles, inter / 64, kHTerms)) + partial_gu +
            align256(ks.down * slots * hidden * 4);
@@ -1127,6 +1175,7 @@ MoeScratch carve(uint8_t* p, size_t tokens, size_t hidden, size_t inter, size_t 
     s.weight = reinterpret_cast<float*>(take(slots * 4));
     s.perm = reinterpret_cast<int32_t*>(take(slots * 4));
     s.position = reinterpret_cast<int32_t*>(take(slots * 4));
+    s.slot_row = reinterpret_cast<int32_t*>(take(slots * 4));
     s.offsets = reinterpret_cast<int32_t*>(take((experts + 1) * 4));
     s.items = reinterpret_cast<int32_t*>(take(items * 8));
     s.item_count = reinterpret_cast<int32_t*>(take(4));
@@ -1187,13 +1236,14 @@ int check_route(const float* logits, size_t tokens, size_t experts, size_t top_k
 
 int launch_route(const float* logits, size_t tokens, size_t experts, size_t top_k,
                  int32_t* idx, float* w, int32_t* offsets, int32_t* perm, int32_t* items,
-                 int32_t* item_count, int32_t* position, hipStream_t stream) {
+                 int32_t* item_count, int32_t* position, int32_t* slot_row,
+                 hipStream_t stream) {
     hipLaunchKernelGGL(route_kernel, dim3(unsigned((tokens + 3) / 4)), dim3(256), 0, stream,
                        logits, unsigned(tokens), unsigned(experts), unsigned(top_k), idx, w);
     KDQ_HIP(hipGetLastError());
     hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, stream, idx,
                        unsigned(tokens * top_k), unsigned(experts), offsets, perm, items,
-                       item_count, position);
+                       item_count, position, slot_row);
     KDQ_HIP(hipGetLastError());
     return KDQ_OK;
 }
@@ -1227,11 +1277,13 @@ extern "C" int kdq_moe_route(const float* logits, size_t tokens, size_t experts,
     if (!idx || !w || !offsets || !perm)
         return KDQ_ERR_ARGUMENT;
     const size_t items = tokens * top_k / kItemRows + experts + 1;
-    auto* scratch = static_cast<int32_t*>(workspace(items * 8 + 256, &rc));
+    auto* scratch =
+        static_cast<int32_t*>(workspace(items * 8 + 256 + tokens * top_k * 4, &rc));
     if (rc)
         return rc;
     return launch_route(logits, tokens, experts, top_k, idx, w, offsets, perm, scratch,
-                        scratch + items * 2, nullptr, static_cast<hipStream_t>(stream));
+                        scratch + items * 2, nullptr, scratch + items * 2 + 64,
+                        static_cast<hipStream_t>(stream));
 }
 
 extern "C" int kdq_mxfp4_dequantize(const uint8_t* blocks, const uint8_t* scales, size_t rows,
@@ -1288,14 +1340,16 @@ int launch_layer(const uint16_t* x_bf16, const float* logits, size_t tokens, siz
     const size_t tiles = 2 * size_t(items);
     const bool small = slots <= size_t(kPrologueSlots);
     if (small) {
-        hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(1024), 0, st, logits, unsigned(tokens),
-                           unsigned(experts), unsigned(top_k), s.idx, s.weight, s.offsets, s.perm,
-                           s.items, s.item_count, s.position, x_bf16, unsigned(hidden), s.xa,
-                           tiles);
+        const size_t x_bytes = tokens * hidden * 2;
+        hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(1024),
+                           x_bytes <= kPrologueXBytes ? x_bytes : 0, st, logits,
+                           unsigned(tokens), unsigned(experts), unsigned(top_k), s.idx, s.weight,
+                           s.offsets, s.perm, s.items, s.item_count, s.position, s.slot_row,
+                           x_bf16, unsigned(hidden), s.xa, tiles);
         KDQ_HIP(hipGetLastError());
     } else {
         int rc = launch_route(logits, tokens, experts, top_k, s.idx, s.weight, s.offsets, s.perm,
-                              s.items, s.item_count, s.position, st);
+                              s.items, s.item_count, s.position, s.slot_row, st);
         if (rc)
             return rc;
         hipLaunchKernelGGL(gather_kernel,
@@ -1321,9 +1375,9 @@ int launch_layer(const uint16_t* x_bf16, const float* logits, size_t tokens, siz
                            s.offsets, s.items, s.item_count, s.ha, s.part_g, s.part_u, part_gu);
     KDQ_HIP(hipGetLastError());
     if (ks.gate_up > 1) {
-        hipLaunchKernelGGL(finalize_kernel, dim3(unsigned((inter + 255) / 256), items * kItemRows),
+        hipLaunchKernelGGL(finalize_kernel, dim3(unsigned((inter + 255) / 256), unsigned(slots)),
                            dim3(256), 0, st, s.part_g, s.part_u, part_gu, unsigned(inter),
-                           ks.gate_up, s.offsets, s.items, s.item_count, s.ha, tiles);
+                           ks.gate_up, s.slot_row, s.ha, tiles);
         KDQ_HIP(hipGetLastError());
     }
     const size_t stride = slots * hidden;
