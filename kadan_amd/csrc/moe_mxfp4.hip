@@ -33,7 +33,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kMaxTopK = 8, kMaxExperts = 256;
 constexpr int kTileRows = 32, kTiles = 2, kItemRows = kTileRows * kTiles;
-constexpr int kGemmWaves = 4;  // wavefronts per grouped-GEMM workgroup, 64 weight rows each
+constexpr int kGemmWaves = 4;  // wavefronts per gate/up workgroup, 64 weight rows each
+constexpr int kDownWaves = 8;  // wavefronts per down workgroup (two per SIMD share a staging)
 constexpr int kStepK = 64;     // K values per step: 16 FP4 bytes per lane
 constexpr int kPrologueSlots = 64;  // layers of at most this many slots use prologue_kernel
 }  // namespace
@@ -707,21 +708,27 @@ __device__ __forceinline__ void issue_order() {
 // slower; so was a register cap for three workgroups per compute unit, which spills.)
 constexpr int kChunk = 2;
 
-template <int TERMS, int TILES> struct StageCopy {
+template <int TERMS, int TILES, int WAVES = kGemmWaves> struct StageCopy {
     static constexpr int chunk_bytes = TILES * kChunk * TERMS * 2048;  // one LDS buffer
-    static constexpr int pieces = chunk_bytes / 16 / (kGemmWaves * 64);  // per thread
+    static constexpr int threads = WAVES * 64;
+    // per thread; when the chunk's 16-byte pieces are not a multiple of the threads, the
+    // last piece of the threads past the end is clamped on load and not stored
+    static constexpr int pieces = (chunk_bytes / 16 + threads - 1) / threads;
+    static constexpr bool ragged = chunk_bytes / 16 % threads != 0;
     const uint8_t* src[pieces];  // piece j of this thread at step 0 (tile base + offset)
     unsigned step[pieces];       // step of the piece within the chunk
 };
 
-template <int TERMS, int TILES>
-__device__ __forceinline__ StageCopy<TERMS, TILES> stage_copy(const Tiles& l, unsigned item) {
-    using C = StageCopy<TERMS, TILES>;
+template <int TERMS, int TILES, int WAVES>
+__device__ __forceinline__ StageCopy<TERMS, TILES, WAVES> stage_copy(const Tiles& l,
+                                                                     unsigned item) {
+    using C = StageCopy<TERMS, TILES, WAVES>;
     C c;
     constexpr int per_tile = kChunk * TERMS * 2048;
 #pragma unroll
     for (int j = 0; j < C::pieces; ++j) {
-        const unsigned o = (threadIdx.x + j * kGemmWaves * 64) * 16;  // byte in the chunk
+        const unsigned o = min(unsigned(threadIdx.x + j * WAVES * 64) * 16,
+                               unsigned(C::chunk_bytes - 16));  // byte in the chunk
         const unsigned t = o / per_tile, within = o % per_tile;
         c.step[j] = within / (TERMS * 2048);
         c.src[j] = l.codes + (2 * size_t(item) + t) * l.code_stride + within % (TERMS * 2048);
@@ -733,13 +740,13 @@ __device__ __forceinline__ StageCopy<TERMS, TILES> stage_copy(const Tiles& l, un
 // acc[m][t] += A(tile t, steps [q0, q1)) * B(group m), q0 % 8 == 0; A through LDS, weights
 // BRING - 1 steps ahead (BRING = 4 or 8 steps: whole scale groups and LDS buffer pairs),
 // with the non-temporal policy when NT (weights read once per layer call).
-template <int TERMS, int TILES, bool NT, int BRING = 4>
+template <int TERMS, int TILES, bool NT, int BRING = 4, int WAVES = kGemmWaves>
 __device__ __forceinline__ void staged_pair(const Tiles& l, unsigned item, unsigned lane,
                                             const WavePair& w, unsigned q0, unsigned q1,
                                             bool active, uint8_t* stage,
                                             f32x16 (&acc)[2][TILES]) {
-    using C = StageCopy<TERMS, TILES>;
-    const C cp = stage_copy<TERMS, TILES>(l, item);
+    using C = StageCopy<TERMS, TILES, WAVES>;
+    const C cp = stage_copy<TERMS, TILES, WAVES>(l, item);
     const unsigned* ascale[TILES];
 #pragma unroll
     for (int t = 0; t < TILES; ++t)
@@ -773,9 +780,11 @@ __device__ __forceinline__ void staged_pair(const Tiles& l, unsigned item, unsig
     };
     auto stage_store = [&](const Pieces& P, int buffer) {
 #pragma unroll
-        for (int j = 0; j < C::pieces; ++j)
-            *reinterpret_cast<u32x4*>(stage + buffer * C::chunk_bytes +
-                                      (threadIdx.x + j * kGemmWaves * 64) * 16) = P.v[j];
+        for (int j = 0; j < C::pieces; ++j) {
+            const unsigned o = (threadIdx.x + j * WAVES * 64) * 16;
+            if (!C::ragged || j + 1 < C::pieces || o < unsigned(C::chunk_bytes))
+                *reinterpret_cast<u32x4*>(stage + buffer * C::chunk_bytes + o) = P.v[j];
+        }
     };
 #pragma unroll
     for (int m = 0; m < 2; ++m)
@@ -980,19 +989,19 @@ __global__ __launch_bounds__(256) void finalize_kernel(const float* __restrict__
 // multiplies the down rows 64 (kGemmWaves x + w) .. +63 (two groups of 32).  fp32 partial
 // sums of h x down per slice, indexed by the slot's position in the permutation.
 template <bool NT>
-__global__ __launch_bounds__(kGemmWaves * 64) void down_kernel(
+__global__ __launch_bounds__(kDownWaves * 64) void down_kernel(
     const uint8_t* __restrict__ ha, size_t tiles, unsigned hidden, unsigned inter,
     unsigned experts, const uint8_t* __restrict__ down, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ items, const int32_t* __restrict__ item_count,
     float* __restrict__ part_d, size_t part_stride) {
-    __shared__ __align__(16) uint8_t stage[2 * StageCopy<kHTerms, 2>::chunk_bytes];
+    __shared__ __align__(16) uint8_t stage[2 * StageCopy<kHTerms, 2, kDownWaves>::chunk_bytes];
     if (int(blockIdx.y) >= *item_count)
         return;
     const Item it = load_item(items, offsets, blockIdx.y);
     const unsigned wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const unsigned i32 = lane % 32, h = lane / 32;
     const Packed shape = packed_shape(1, hidden, inter);  // per expert
-    const unsigned pair = blockIdx.x * kGemmWaves + wave;
+    const unsigned pair = blockIdx.x * kDownWaves + wave;
     const bool active = pair < shape.groups / 2;
     const unsigned g0 = (active ? pair : 0) * 2;
     unsigned q0, q1;
@@ -1005,7 +1014,8 @@ __global__ __launch_bounds__(kGemmWaves * 64) void down_kernel(
     const Tiles hl = tile_layout(const_cast<uint8_t*>(ha), tiles, inter / 64, kHTerms);
     auto run = [&]<int TILES>() {
         f32x16 acc[2][TILES];
-        staged_pair<kHTerms, TILES, NT>(hl, blockIdx.y, lane, w, q0, q1, active, stage, acc);
+        staged_pair<kHTerms, TILES, NT, 4, kDownWaves>(hl, blockIdx.y, lane, w, q0, q1, active,
+                                                       stage, acc);
         if (!active)
             return;
 #pragma unroll
@@ -1115,7 +1125,7 @@ unsigned gate_up_columns(size_t inter) {
 }
 
 unsigned down_columns(size_t hidden) {
-    return unsigned((hidden / 64 + kGemmWaves - 1) / kGemmWaves);
+    return unsigned((hidden / 64 + kDownWaves - 1) / kDownWaves);
 }
 
 // K slices of the grouped GEMMs: enough workgroups for about two per compute unit (two
@@ -1128,15 +1138,17 @@ struct MoeSlices {
 MoeSlices moe_slices(size_t tokens, size_t hidden, size_t inter, size_t experts,
                      size_t top_k) {
     const size_t items = std::min(tokens * top_k, experts);  // at least this many
-    const size_t target = 2 * size_t(compute_units());
-    auto slices = [&](size_t columns, size_t steps) {
+    // workgroups for about two gate/up (four waves) or one down (eight waves) per compute
+    // unit
+    auto slices = [&](size_t columns, size_t steps, size_t per_cu) {
+        const size_t target = per_cu * size_t(compute_units());
         size_t ks = std::max<size_t>(1, (target + columns * items - 1) / (columns * items));
         ks = std::min(ks, steps);
         const size_t per = ((steps + ks - 1) / ks + 7) / 8 * 8;
         return unsigned((steps + per - 1) / per);
     };
-    return MoeSlices{slices(gate_up_columns(inter), hidden / kStepK),
-                     slices(down_columns(hidden), inter / kStepK)};
+    return MoeSlices{slices(gate_up_columns(inter), hidden / kStepK, 2),
+                     slices(down_columns(hidden), inter / kStepK, 1)};
 }
 
 size_t align256(size_t n) {
@@ -1383,11 +1395,11 @@ int launch_layer(const uint16_t* x_bf16, const float* logits, size_t tokens, siz
     const size_t stride = slots * hidden;
     const dim3 d_grid(down_columns(hidden), items, ks.down);
     if (nt)
-        hipLaunchKernelGGL(down_kernel<true>, d_grid, dim3(kGemmWaves * 64), 0, st, s.ha, tiles,
+        hipLaunchKernelGGL(down_kernel<true>, d_grid, dim3(kDownWaves * 64), 0, st, s.ha, tiles,
                            unsigned(hidden), unsigned(inter), unsigned(experts), down, s.offsets,
                            s.items, s.item_count, s.part_d, stride);
     else
-        hipLaunchKernelGGL(down_kernel<false>, d_grid, dim3(kGemmWaves * 64), 0, st, s.ha, tiles,
+        hipLaunchKernelGGL(down_kernel<false>, d_grid, dim3(kDownWaves * 64), 0, st, s.ha, tiles,
                            unsigned(hidden), unsigned(inter), unsigned(experts), down, s.offsets,
                            s.items, s.item_count, s.part_d, stride);
     KDQ_HIP(hipGetLastError());
