@@ -40,13 +40,18 @@
 namespace kdq {
 namespace {
 
-// gate[i] = silu(gate[i]) * up[i] for i < n, and (grouped layers) rows below *used of
-// `width` values each
+// gate[i] = silu(gate[i]) * up[i] for i < n; grouped layers: only rows below *used of
+// `width` values that hold a slot (padding rows of zero x keep gate = up = 0, which is
+// already silu(0) * 0)
 __global__ __launch_bounds__(256) void swiglu_kernel(float* gate, const float* up, size_t n,
-                                                     const unsigned* used, unsigned width) {
+                                                     const unsigned* used, unsigned width,
+                                                     const int32_t* slot_of) {
     const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
-    if (i < n && (!used || i / width < *used))
-        gate[i] = silu_of(gate[i]) * up[i];
+    if (i >= n)
+        return;
+    if (used && (i / width >= *used || slot_of[i / width] < 0))
+        return;
+    gate[i] = silu_of(gate[i]) * up[i];
 }
 
 // y[t, d] = (sum_{i < k} down[t*k + i, d] * w[t*k + i]) + shared[t, d] * sigmoid(gate[t])
@@ -373,7 +378,7 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
     // 3. shared swiglu, unless paired above
     if (!pair_shared) {
         hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((rows * S + 255) / 256)), dim3(256), 0,
-                           st, sg, su, rows * S, nullptr, 1u);
+                           st, sg, su, rows * S, nullptr, 1u, nullptr);
         KDQ_HIP(hipGetLastError());
     }
     if (grouped) {
@@ -403,7 +408,7 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
                 (r = indexed_gemv_affine(uj, unsigned(items), xs8, fs8, st)))
                 return r;
             hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((positions * F + 255) / 256)),
-                               dim3(256), 0, st, g, u, positions * F, used, unsigned(F));
+                               dim3(256), 0, st, g, u, positions * F, used, unsigned(F), inv);
             KDQ_HIP(hipGetLastError());
             return KDQ_OK;
         };
@@ -426,7 +431,7 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
                                    sigma, st)))
                 return rc;
             hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((positions * F + 255) / 256)),
-                               dim3(256), 0, st, g, u, positions * F, used, unsigned(F));
+                               dim3(256), 0, st, g, u, positions * F, used, unsigned(F), inv);
             KDQ_HIP(hipGetLastError());
         } else if ((rc = items_gate_up())) {
             return rc;
@@ -493,7 +498,7 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
             (rc = indexed_gemv_affine(uj, unsigned(slots), H, F, st, unsigned(K))))
             return rc;
         hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((slots * F + 255) / 256)), dim3(256), 0,
-                           st, g, u, slots * F, nullptr, 1u);
+                           st, g, u, slots * F, nullptr, 1u, nullptr);
         KDQ_HIP(hipGetLastError());
     }
     // 5. expert downs (one launch over every slot) and the shared down
