@@ -681,8 +681,11 @@ def main():
                   "Q3_K GEMV 4096->14336, batch 1, row-major GGUF bytes (kdq_gemv_batch: "
                   "the MFMA GEMV reading 110-byte super-blocks in place)", packed=False,
                   copies=8)
-        for enc, tag in ((IQ3_XXS, "iq3_xxs"),
-                         (IQ2_S, "iq2_s"), (BF16, "bf16")):
+        gemv_line("gemv_iq3_xxs_4096x14336", IQ3_XXS, n_in, n_out, 0xF0 + IQ3_XXS, 500,
+                  "IQ3_XXS GEMV 4096->14336, batch 1, row-major GGUF bytes (kdq_gemv_batch: "
+                  "the MFMA GEMV, grid magnitudes and sign selectors from LDS tables)",
+                  packed=False, copies=8)
+        for enc, tag in ((IQ2_S, "iq2_s"), (BF16, "bf16")):
             gemv_line(f"gemv_{tag}_4096x14336_exact", enc, n_in, n_out, 0xF0 + enc, 50,
                       f"{tag.upper()} GEMV 4096->14336, batch 1, row-major bytes (exact-decode "
                       "product: no streaming kernel for this encoding yet)", packed=False,

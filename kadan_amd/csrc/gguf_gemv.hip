@@ -508,6 +508,22 @@ __device__ __forceinline__ void load_lane_q3k(const uint8_t* row, unsigned group
     L.w[18] = load4_a2(block + 106);
 }
 
+// IQ3_XXS (98-byte super-block: f16 d, 64 grid-index bytes, 8 sign-and-scale words;
+// G/src/ggml-common.h block_iq3_xxs).  Block k (32 values) has index bytes 8k .. 8k+7
+// (byte i: positions 4i .. 4i+3) and word k of the tail: four 7-bit sign sets (set i:
+// positions 8i .. 8i+7, eighth sign their parity) and a 4-bit scale on top.  MFMA chunk
+// G is blocks 2G, 2G+1.  Image: w[0..3] = the two blocks' index bytes, w[4], w[5] = their
+// words, w[6] = bytes 0..3 (d in the low half).
+__device__ __forceinline__ void load_lane_iq3xxs(const uint8_t* row, unsigned group, unsigned G,
+                                                 Lane& L) {
+    const uint8_t* block = row + size_t(group) * 98;
+    const u32x4 a = load16_a2(block + 2 + 16 * G);
+    const uint2 s = load8_a2(block + 66 + 8 * G);
+    L.w[0] = a.x, L.w[1] = a.y, L.w[2] = a.z, L.w[3] = a.w;
+    L.w[4] = s.x, L.w[5] = s.y;
+    L.w[6] = load4_a2(block);
+}
+
 // Four IQ4 indices (bits 0-3 of each byte of n; bits 4-7 ignored) -> their int8 grid
 // values: v_perm looks up indices 0-7 and 8-15 in the grid's four words, a third v_perm
 // keeps per byte the one its index's bit 3 names.
@@ -808,17 +824,26 @@ constexpr int mfma_units = R == 1 ? 2 : (R == 2 ? 2 : 1);
 //       int bits, sum of the codes of its first 16 values as int bits)
 //   partials [R][mats * tiles][64 lanes][kPartialPitch] floats (mats = 2 for paired jobs:
 //       the gate tiles, then the up tiles)
+//   lookup tables of the lattice encodings (mfma_table_bytes; none for the others)
 struct MfmaLds {
-    size_t a, blocks, partial, total;
+    size_t a, blocks, partial, table, total;
 };
 
-__host__ __device__ inline MfmaLds mfma_layout(unsigned batch, unsigned in, unsigned mats = 1) {
+// IQ3_XXS: 256 grid entries as (magnitudes, negated magnitudes) byte quads, then 128
+// v_perm selector pairs, one per 7-bit sign set.
+__host__ __device__ constexpr size_t mfma_table_bytes(int encoding) {
+    return encoding == KDQ_IQ3_XXS ? 256 * 8 + 128 * 8 : 0;
+}
+
+__host__ __device__ inline MfmaLds mfma_layout(unsigned batch, unsigned in, unsigned mats = 1,
+                                               size_t table = 0) {
     const size_t tiles = (batch >= 4 ? 1 : 4 / batch) * mats;
     MfmaLds l;
     l.a = 1024;
     l.blocks = l.a + size_t(batch) * (in / 256) * kAGroup;
     l.partial = l.blocks + size_t(batch) * (in / 32) * 16;
-    l.total = l.partial + size_t(batch) * tiles * 64 * kPartialPitch * 4;
+    l.table = l.partial + size_t(batch) * tiles * 64 * kPartialPitch * 4;
+    l.total = l.table + table;
     return l;
 }
 
@@ -943,11 +968,57 @@ __device__ __forceinline__ void load_packed(const uint8_t* unit, unsigned G, uns
     }
 }
 
+// Fills the IQ3_XXS lookup tables (mfma_table_bytes) from this thread's grid entry
+// (threads 0..255 own entry threadIdx.x; lane b of the entry, bits 3b .. 3b+2, is an
+// index into the levels 4, 12, .., 52, 62).
+__device__ __forceinline__ void iq3xxs_table(uint8_t* table, unsigned entry) {
+    const unsigned t = threadIdx.x;
+    if (t < 256) {
+        unsigned pos = 0, neg = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const unsigned i = (entry >> (3 * b)) & 7u;
+            const unsigned level = i == 7 ? 62u : 8u * i + 4u;
+            pos |= level << (8 * b);
+            neg |= ((256u - level) & 255u) << (8 * b);
+        }
+        reinterpret_cast<uint2*>(table)[t] = make_uint2(pos, neg);
+    }
+    if (t < 128) {
+        // eight signs: the set's seven, then their parity; selector byte i picks byte i of
+        // the magnitudes (i) or of their negations (i + 4)
+        const unsigned s = t | ((__builtin_popcount(t) & 1u) << 7);
+        unsigned lo = 0, hi = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            lo |= (unsigned(i) + 4u * ((s >> i) & 1u)) << (8 * i);
+            hi |= (unsigned(i) + 4u * ((s >> (4 + i)) & 1u)) << (8 * i);
+        }
+        reinterpret_cast<uint2*>(table + 256 * 8)[t] = make_uint2(lo, hi);
+    }
+}
+
 // B operand of MFMA m from one lane's packed chunk (load_lane layout, or load_packed's
-// when PACKED).
+// when PACKED).  `table`: the encoding's LDS lookup tables (IQ3_XXS).
 template <int ENC, bool PACKED = false>
-__device__ __forceinline__ i32x4 b_operand(const Lane& L, int m, unsigned q6_shift) {
-    if constexpr (PACKED && ENC == KDQ_Q6_K) {
+__device__ __forceinline__ i32x4 b_operand(const Lane& L, int m, unsigned q6_shift,
+                                           const uint8_t* table = nullptr) {
+    if constexpr (ENC == KDQ_IQ3_XXS) {
+        // positions 8m .. 8m+7 of block b: index bytes 2m, 2m+1 (four positions each),
+        // sign set m; v_perm takes per byte the magnitude or its negation
+        const uint2* grid = reinterpret_cast<const uint2*>(table);
+        const uint2* sels = reinterpret_cast<const uint2*>(table + 256 * 8);
+        unsigned v[4];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const unsigned idx = L.w[2 * b + m / 2] >> (16 * (m % 2));
+            const uint2 sel = sels[(L.w[4 + b] >> (7 * m)) & 127u];
+            const uint2 g0 = grid[idx & 255u], g1 = grid[(idx >> 8) & 255u];
+            v[2 * b] = __builtin_amdgcn_perm(g0.y, g0.x, sel.x);
+            v[2 * b + 1] = __builtin_amdgcn_perm(g1.y, g1.x, sel.y);
+        }
+        return i32x4{int(v[0]), int(v[1]), int(v[2]), int(v[3])};
+    } else if constexpr (PACKED && ENC == KDQ_Q6_K) {
         // the qh pairs of positions 8m+i sit in bits 4-7 of byte i of w[8+m], those of
         // 8m+4+i in bits 0-3 (block 0 bits low, block 1 bits high in each nibble)
         const unsigned l0 = L.w[2 * m], l1 = L.w[2 * m + 1], h = L.w[8 + m];
@@ -1059,6 +1130,15 @@ __device__ __forceinline__ float chunk_value(const Lane& L, ScaleSel sel, i32x4 
         bad |= !isfinite(d0) || !isfinite(d1);
         const float A0 = float(c.x * 256 + c.y), A1 = float(c.z * 256 + c.w);
         return fmaf(d1 * x1.x, A1, d0 * x0.x * A0);
+    } else if constexpr (ENC == KDQ_IQ3_XXS) {
+        // block scales d * (0.5 + s) / 2 = d * (2s + 1) / 4, s = bits 28..31 of the
+        // block's word
+        const float d = half_hw(L.w[6] & 0xffffu);
+        bad |= !isfinite(d);
+        const float f0 = 0.25f * d * float(2 * (L.w[4] >> 28) + 1);
+        const float f1 = 0.25f * d * float(2 * (L.w[5] >> 28) + 1);
+        const float A0 = float(c.x * 256 + c.y), A1 = float(c.z * 256 + c.w);
+        return fmaf(f1 * x1.x, A1, f0 * x0.x * A0);
     } else if constexpr (ENC == KDQ_IQ4_XS) {
         // block scales d * (ls - 32), ls = 4 bits of scales_l | 2 bits of scales_h << 4
         // (sel.shift = G: blocks 2G, 2G+1)
@@ -1227,9 +1307,10 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
     constexpr int kRowUnroll = R <= 2 ? R : 1;  // larger batches: one row's operands at a time
     constexpr unsigned kThreads = W * 64;
     extern __shared__ __align__(16) uint8_t lds[];
-    const MfmaLds layout = mfma_layout(R, in, mats);
+    const MfmaLds layout = mfma_layout(R, in, mats, mfma_table_bytes(ENC));
     const unsigned groups = in / 256;
     uint8_t* atab = lds + layout.a;
+    uint8_t* table = lds + layout.table;
     float4* blocks = reinterpret_cast<float4*>(lds + layout.blocks);
     float* partial = reinterpret_cast<float*>(lds + layout.partial);
 
@@ -1274,6 +1355,8 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
                 load_lane_iq4xs(w + size_t(n) * row_bytes, g, G, L[k]);
             else if constexpr (ENC == KDQ_Q3_K)
                 load_lane_q3k(w + size_t(n) * row_bytes, g, G, L[k]);
+            else if constexpr (ENC == KDQ_IQ3_XXS)
+                load_lane_iq3xxs(w + size_t(n) * row_bytes, g, G, L[k]);
             else if constexpr (ENC == KDQ_IQ4_NL)  // Q4_0's block size and layout
                 load_lane<KDQ_Q4_0>(w + size_t(n) * row_bytes, 4 * g + G, L[k]);
             else
@@ -1285,12 +1368,19 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
     const unsigned units_x = R * in / 8;
     XUnit first_unit;
     load_unit(x, in, min(unsigned(threadIdx.x), units_x - 1), first_unit);
+    // the lookup table's source entry, requested before the weights (the staging waits
+    // for it)
+    unsigned entry = 0;
+    if constexpr (ENC == KDQ_IQ3_XXS)
+        entry = kIq3xxsGrid[min(unsigned(threadIdx.x), 255u)];
     asm volatile("" ::: "memory");  // x is not restrict: its loads stay before this point
     __builtin_amdgcn_sched_barrier(0);
     Lane L[kUnits];
     load_units(r0, UnitCursor{wave, 0}, L);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (ENC == KDQ_IQ3_XXS)
+        iq3xxs_table(table, entry);
     if (threadIdx.x < units_x)
         mstage_unit<ENC>(in, threadIdx.x, first_unit, atab, blocks);
     for (unsigned u = threadIdx.x + kThreads; u < units_x; u += kThreads) {
@@ -1328,7 +1418,7 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
 #pragma unroll
                     for (int m = 0; m < 4; ++m) {
                         const i32x4 av = *reinterpret_cast<const i32x4*>(a + m * 256);
-                        const i32x4 bv = b_operand<ENC, PACKED>(L[k], m, sel.shift);
+                        const i32x4 bv = b_operand<ENC, PACKED>(L[k], m, sel.shift, table);
                         if ((ENC == KDQ_Q6_K || ENC == KDQ_Q3_K) && m >= 2)
                             c2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, c2, 0, 0, 0);
                         else
@@ -1496,8 +1586,8 @@ int launch_fast(const void* w, size_t row_bytes, const float* x, size_t rows, si
 }
 
 // LDS bytes of mfma_gemv for `batch` rows (mats = 2: paired jobs).
-size_t mfma_lds(size_t batch, size_t in, unsigned mats = 1) {
-    return mfma_layout(unsigned(batch), unsigned(in), mats).total;
+size_t mfma_lds(size_t batch, size_t in, unsigned mats = 1, size_t table = 0) {
+    return mfma_layout(unsigned(batch), unsigned(in), mats, table).total;
 }
 
 struct MfmaPlan {
@@ -1510,12 +1600,12 @@ struct MfmaPlan {
 // weights the rows per workgroup are a multiple of 8, so every 128-byte line of a unit
 // (8 row slots of one chunk) belongs to one workgroup.
 bool plan_mfma(size_t rows, size_t in, size_t total_out, MfmaPlan& p, bool packed = false,
-               unsigned mats = 1) {
+               unsigned mats = 1, size_t table = 0) {
     constexpr size_t limit = 160 * 1024;
-    if (in % 256 || mfma_lds(1, in, mats) > limit)
+    if (in % 256 || mfma_lds(1, in, mats, table) > limit)
         return false;
     unsigned batch = 1;
-    while (batch < 8 && batch < rows && mfma_lds(batch * 2, in, mats) <= limit)
+    while (batch < 8 && batch < rows && mfma_lds(batch * 2, in, mats, table) <= limit)
         batch *= 2;
     // A wavefront takes the 256-value groups w, w + W, ...: narrow products (the MoE
     // experts' 768 / 2048 inputs) use 4 or 8 wavefronts, and correspondingly more
@@ -1523,7 +1613,7 @@ bool plan_mfma(size_t rows, size_t in, size_t total_out, MfmaPlan& p, bool packe
     const size_t groups = in / 256;
     unsigned waves = groups <= 4 ? 4 : (groups <= 8 ? 8 : 16);
     size_t per_cu = 16 / waves;
-    while (per_cu > 1 && per_cu * mfma_lds(batch, in, mats) > limit)
+    while (per_cu > 1 && per_cu * mfma_lds(batch, in, mats, table) > limit)
         per_cu /= 2;
     const size_t slots = compute_units() * per_cu;
     size_t rows_per_wg = std::max<size_t>(1, (total_out * mats + slots - 1) / slots / mats);
@@ -1563,7 +1653,8 @@ int launch_mfma_form(const MfmaJobs& jobs, hipStream_t stream) {
         configured = true;
     }
     hipLaunchKernelGGL((mfma_gemv<ENC, R, W, PACKED, PLAIN>), dim3(jobs.columns, jobs.count),
-                       dim3(W * 64), mfma_lds(R, jobs.in, jobs.mats == 2 ? 2 : 1), stream, jobs);
+                       dim3(W * 64), mfma_lds(R, jobs.in, jobs.mats == 2 ? 2 : 1, mfma_table_bytes(ENC)),
+                       stream, jobs);
     KDQ_HIP(hipGetLastError());
     return KDQ_OK;
 }
@@ -1610,7 +1701,7 @@ template <int ENC, bool PACKED>
 int launch_mfma(const void* w, size_t row_bytes, const float* x, size_t rows, size_t in,
                 size_t out, float* y, size_t stride, unsigned* status, hipStream_t stream) {
     MfmaPlan p;
-    if (!plan_mfma(rows, in, out, p, PACKED))
+    if (!plan_mfma(rows, in, out, p, PACKED, 1, mfma_table_bytes(ENC)))
         return KDQ_ERR_UNSUPPORTED;
     for (size_t first = 0; first < rows;) {
         const size_t left = rows - first;
@@ -1658,6 +1749,11 @@ int launch_mfma_any(int encoding, const void* w, size_t row_bytes, const float* 
         if constexpr (!PACKED)
             return launch_mfma<KDQ_Q3_K, false>(w, row_bytes, x, rows, in, out, y, stride,
                                                 status, s);
+        return KDQ_ERR_UNSUPPORTED;
+    case KDQ_IQ3_XXS:
+        if constexpr (!PACKED)
+            return launch_mfma<KDQ_IQ3_XXS, false>(w, row_bytes, x, rows, in, out, y, stride,
+                                                   status, s);
         return KDQ_ERR_UNSUPPORTED;
     default:
         return KDQ_ERR_UNSUPPORTED;
@@ -1818,14 +1914,15 @@ int with_encoding(int encoding, F&& f) {
 bool streamed_encoding(int encoding) {
     return encoding == KDQ_Q8_0 || encoding == KDQ_Q4_0 || encoding == KDQ_Q4_K ||
            encoding == KDQ_Q6_K || encoding == KDQ_IQ4_XS || encoding == KDQ_IQ4_NL ||
-           encoding == KDQ_Q3_K;
+           encoding == KDQ_Q3_K || encoding == KDQ_IQ3_XXS;
 }
 
 // The streaming kernels need whole 64-value lane slots, 4-byte aligned rows and packed
 // rows of exactly the format's size (16-byte aligned for Q4_K); Q6_K (MFMA kernel only)
 // 256-value groups and 2-byte aligned rows.
 bool streams(int encoding, const void* weights, size_t row_bytes, size_t in) {
-    if (encoding == KDQ_Q6_K || encoding == KDQ_Q3_K)  // 210- / 110-byte super-blocks
+    // 210- / 110- / 98-byte super-blocks
+    if (encoding == KDQ_Q6_K || encoding == KDQ_Q3_K || encoding == KDQ_IQ3_XXS)
         return in % 256 == 0 && row_bytes % 2 == 0 && aligned(weights, 2);
     if (encoding == KDQ_IQ4_XS)  // 136-byte super-blocks: 8-byte aligned rows
         return in % 256 == 0 && row_bytes % 8 == 0 && aligned(weights, 8);
@@ -2025,7 +2122,7 @@ int launch_fused(const kdq_matvec_job* jobs, const size_t* idx, size_t n, hipStr
         total += jobs[idx[k]].columns;
     const unsigned mats = indexed && indexed[idx[0]].paired ? 2 : 1;  // one kind per launch
     MfmaPlan p;
-    if (!plan_mfma(j0.rows, j0.in, total, p, PACKED, mats))
+    if (!plan_mfma(j0.rows, j0.in, total, p, PACKED, mats, mfma_table_bytes(j0.encoding)))
         return KDQ_ERR_UNSUPPORTED;
     MfmaJobs mj{};
     mj.count = unsigned(n);
@@ -2064,6 +2161,10 @@ int launch_fused(const kdq_matvec_job* jobs, const size_t* idx, size_t n, hipStr
         if constexpr (!PACKED)
             return launch_mfma_rows<KDQ_Q3_K, false>(j0.rows, p.waves, mj, stream);
         return KDQ_ERR_UNSUPPORTED;
+    case KDQ_IQ3_XXS:
+        if constexpr (!PACKED)
+            return launch_mfma_rows<KDQ_IQ3_XXS, false>(j0.rows, p.waves, mj, stream);
+        return KDQ_ERR_UNSUPPORTED;
     default:
         return KDQ_ERR_UNSUPPORTED;
     }
@@ -2074,7 +2175,8 @@ int launch_fused(const kdq_matvec_job* jobs, const size_t* idx, size_t n, hipStr
 bool fusable(const kdq_matvec_job& j, bool packed) {
     MfmaPlan p;
     return (packed || streams(j.encoding, j.weights, j.row_bytes, j.in)) &&
-           (j.rows & (j.rows - 1)) == 0 && plan_mfma(j.rows, j.in, j.columns, p, packed) &&
+           (j.rows & (j.rows - 1)) == 0 &&
+           plan_mfma(j.rows, j.in, j.columns, p, packed, 1, mfma_table_bytes(j.encoding)) &&
            p.batch >= j.rows;
 }
 
@@ -2121,7 +2223,9 @@ int run_batch(const kdq_matvec_job* jobs, size_t count, void* stream) {
 
 bool swiglu_pairable(const kdq_matvec_job& j, size_t count) {
     MfmaPlan p;
-    return fusable(j, false) && plan_mfma(j.rows, j.in, size_t(j.columns) * count, p, false, 2) &&
+    return fusable(j, false) &&
+           plan_mfma(j.rows, j.in, size_t(j.columns) * count, p, false, 2,
+                     mfma_table_bytes(j.encoding)) &&
            p.batch >= j.rows;
 }
 
@@ -2135,7 +2239,8 @@ int indexed_gemv_affine(const IndexedJob& first, unsigned count, size_t x_step,
     const unsigned mats = first.paired ? 2 : 1;
     MfmaPlan p;  // planned over every job's rows, as launch_fused plans a fused group
     if (fusable(j, false) &&
-        plan_mfma(j.rows, j.in, size_t(j.columns) * count, p, false, mats) &&
+        plan_mfma(j.rows, j.in, size_t(j.columns) * count, p, false, mats,
+                  mfma_table_bytes(j.encoding)) &&
         p.batch >= j.rows) {
         MfmaJobs mj{};
         mj.count = count;
@@ -2165,6 +2270,8 @@ int indexed_gemv_affine(const IndexedJob& first, unsigned count, size_t x_step,
             return launch_mfma_rows<KDQ_IQ4_NL, false>(j.rows, p.waves, mj, s);
         case KDQ_Q3_K:
             return launch_mfma_rows<KDQ_Q3_K, false>(j.rows, p.waves, mj, s);
+        case KDQ_IQ3_XXS:
+            return launch_mfma_rows<KDQ_IQ3_XXS, false>(j.rows, p.waves, mj, s);
         default:
             return KDQ_ERR_UNSUPPORTED;
         }
