@@ -685,7 +685,14 @@ def main():
                   "IQ3_XXS GEMV 4096->14336, batch 1, row-major GGUF bytes (kdq_gemv_batch: "
                   "the MFMA GEMV, grid magnitudes and sign selectors from LDS tables)",
                   packed=False, copies=8)
-        for enc, tag in ((IQ2_S, "iq2_s"), (BF16, "bf16")):
+        gemv_line("gemv_iq3_s_4096x14336", IQ3_S, n_in, n_out, 0xF0 + IQ3_S, 500,
+                  "IQ3_S GEMV 4096->14336, batch 1, row-major GGUF bytes (kdq_gemv_batch: "
+                  "the MFMA GEMV, 9-bit grid indices, LDS tables)", packed=False, copies=8)
+        gemv_line("gemv_iq2_s_4096x14336", IQ2_S, n_in, n_out, 0xF0 + IQ2_S, 500,
+                  "IQ2_S GEMV 4096->14336, batch 1, row-major GGUF bytes (kdq_gemv_batch: "
+                  "the MFMA GEMV, 8-value grid entries from an LDS table, scales per 16 "
+                  "values)", packed=False, copies=8)
+        for enc, tag in ((BF16, "bf16"),):
             gemv_line(f"gemv_{tag}_4096x14336_exact", enc, n_in, n_out, 0xF0 + enc, 50,
                       f"{tag.upper()} GEMV 4096->14336, batch 1, row-major bytes (exact-decode "
                       "product: no streaming kernel for this encoding yet)", packed=False,

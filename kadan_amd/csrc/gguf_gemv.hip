@@ -1,6 +1,7 @@
 // GGUF block-quantized decode and decode-time products for gfx950: Q8_0, Q4_0, Q4_K on
-// every kernel below, Q3_K, Q6_K, IQ4_NL, IQ4_XS, IQ3_XXS, IQ2_S, IQ3_S and BF16 on
-// decode_kernel and exact_gemv.  Replaces the reference's gguf_decode_kernel and gguf_matvec_kernel
+// every kernel below; Q3_K, Q6_K, IQ4_NL, IQ4_XS and the lattice encodings IQ3_XXS, IQ3_S,
+// IQ2_S on decode_kernel, exact_gemv and mfma_gemv; BF16 on decode_kernel and
+// exact_gemv.  Replaces the reference's gguf_decode_kernel and gguf_matvec_kernel
 // (IW/src/cuda/h3_compute.cu:76-95,165-240; IW = services/hikari/inference_worker)
 // behind the C ABI of include/kadan_amd.h.
 //
@@ -524,6 +525,43 @@ __device__ __forceinline__ void load_lane_iq3xxs(const uint8_t* row, unsigned gr
     L.w[6] = load4_a2(block);
 }
 
+// IQ3_S (110-byte super-block: f16 d, qs[64] low index bits, qh[8], signs[32], scales[4];
+// G/src/ggml-common.h block_iq3_s).  Block k has index bytes 8k .. 8k+7 (byte i:
+// positions 4i .. 4i+3, bit 8 of the index in bit i of qh[k]), sign bytes 4k .. 4k+3
+// (byte i: positions 8i .. 8i+7) and scale nibble k (low nibble of scales[k/2] for even
+// k).  Image for chunk G: w[0..3] = the two blocks' index bytes, w[4], w[5] = their sign
+// bytes, w[6] = bytes 0..3 (d low), w[7] = bytes 66+2G .. 69+2G (their qh bytes low),
+// w[8] = the four scale bytes.
+__device__ __forceinline__ void load_lane_iq3s(const uint8_t* row, unsigned group, unsigned G,
+                                               Lane& L) {
+    const uint8_t* block = row + size_t(group) * 110;
+    const u32x4 a = load16_a2(block + 2 + 16 * G);
+    const uint2 s = load8_a2(block + 74 + 8 * G);
+    L.w[0] = a.x, L.w[1] = a.y, L.w[2] = a.z, L.w[3] = a.w;
+    L.w[4] = s.x, L.w[5] = s.y;
+    L.w[6] = load4_a2(block);
+    L.w[7] = load4_a2(block + 66 + 2 * G);
+    L.w[8] = load4_a2(block + 106);
+}
+
+// IQ2_S (82-byte super-block: f16 d, qs[32] low index bits, signs[32], qh[8], scales[8];
+// G/src/ggml-common.h block_iq2_s).  Block k has index bytes 4k .. 4k+3 (byte i:
+// positions 8i .. 8i+7, bits 8, 9 of the index in bits 2i, 2i+1 of qh[k]), sign bytes
+// 32 + 4k .. (byte i: positions 8i .. 8i+7) and scales[k] (low nibble: positions 0..15,
+// high: 16..31).  Image for chunk G: w[0], w[1] = the two blocks' index bytes, w[2],
+// w[3] = their sign bytes, w[4] = bytes 66+2G .. (their qh bytes low), w[5] = scale bytes
+// 74 + 4(G/2) .. (theirs at byte 2(G%2)), w[6] = bytes 0..3 (d low).  Every load ends
+// inside the super-block.
+__device__ __forceinline__ void load_lane_iq2s(const uint8_t* row, unsigned group, unsigned G,
+                                               Lane& L) {
+    const uint8_t* block = row + size_t(group) * 82;
+    const uint2 q = load8_a2(block + 2 + 8 * G), s = load8_a2(block + 34 + 8 * G);
+    L.w[0] = q.x, L.w[1] = q.y, L.w[2] = s.x, L.w[3] = s.y;
+    L.w[4] = load4_a2(block + 66 + 2 * G);
+    L.w[5] = load4_a2(block + 74 + 4 * (G / 2));
+    L.w[6] = load4_a2(block);
+}
+
 // Four IQ4 indices (bits 0-3 of each byte of n; bits 4-7 ignored) -> their int8 grid
 // values: v_perm looks up indices 0-7 and 8-15 in the grid's four words, a third v_perm
 // keeps per byte the one its index's bit 3 names.
@@ -829,10 +867,29 @@ struct MfmaLds {
     size_t a, blocks, partial, table, total;
 };
 
-// IQ3_XXS: 256 grid entries as (magnitudes, negated magnitudes) byte quads, then 128
-// v_perm selector pairs, one per 7-bit sign set.
+// The lattice encodings' grids and sign sets: IQ3_XXS 256 entries of 4 values and
+// 7-bit sign sets (the eighth sign their parity), IQ3_S 512 entries of 4 values and
+// 8-bit sign bytes, IQ2_S 1024 entries of 8 values and 8-bit sign bytes.
+__host__ __device__ constexpr unsigned lattice_entries(int encoding) {
+    return encoding == KDQ_IQ3_XXS ? 256 : (encoding == KDQ_IQ3_S ? 512 : 1024);
+}
+__host__ __device__ constexpr unsigned lattice_signs(int encoding) {
+    return encoding == KDQ_IQ3_XXS ? 128 : 256;
+}
+__host__ __device__ constexpr unsigned lattice_width(int encoding) {
+    return encoding == KDQ_IQ2_S ? 8 : 4;
+}
+__host__ __device__ constexpr bool lattice(int encoding) {
+    return encoding == KDQ_IQ3_XXS || encoding == KDQ_IQ3_S || encoding == KDQ_IQ2_S;
+}
+
+// LDS lookup tables of the lattice encodings: per grid entry its magnitude bytes then
+// their negations (8 bytes for 4 values, 16 for 8), then per sign set a pair of v_perm
+// selectors (8 bytes).
 __host__ __device__ constexpr size_t mfma_table_bytes(int encoding) {
-    return encoding == KDQ_IQ3_XXS ? 256 * 8 + 128 * 8 : 0;
+    return lattice(encoding) ? size_t(lattice_entries(encoding)) * 2 * lattice_width(encoding) +
+                                   size_t(lattice_signs(encoding)) * 8
+                             : 0;
 }
 
 __host__ __device__ inline MfmaLds mfma_layout(unsigned batch, unsigned in, unsigned mats = 1,
@@ -968,33 +1025,67 @@ __device__ __forceinline__ void load_packed(const uint8_t* unit, unsigned G, uns
     }
 }
 
-// Fills the IQ3_XXS lookup tables (mfma_table_bytes) from this thread's grid entry
-// (threads 0..255 own entry threadIdx.x; lane b of the entry, bits 3b .. 3b+2, is an
-// index into the levels 4, 12, .., 52, 62).
-__device__ __forceinline__ void iq3xxs_table(uint8_t* table, unsigned entry) {
+// Magnitude of level index i (0..7) of a lattice encoding's grid.
+template <int ENC> __device__ __forceinline__ unsigned lattice_level(unsigned i) {
+    if constexpr (ENC == KDQ_IQ3_XXS)
+        return i == 7 ? 62u : 8u * i + 4u;
+    else if constexpr (ENC == KDQ_IQ3_S)
+        return 2u * i + 1u;
+    else
+        return i == 0 ? 8u : (i == 1 ? 25u : 43u);
+}
+
+// The grid entry of index i (lane b, the level index of value b, at bits [w*b, w*b + w),
+// w = 3, or 2 for IQ2_S).
+template <int ENC> __device__ __forceinline__ unsigned lattice_entry(unsigned i) {
+    if constexpr (ENC == KDQ_IQ3_XXS)
+        return kIq3xxsGrid[i];
+    else if constexpr (ENC == KDQ_IQ3_S)
+        return kIq3sGrid[i];
+    else
+        return kIq2sGrid[i];
+}
+
+// Entries of the grid each thread of a kThreads workgroup converts into the LDS table.
+template <int ENC, unsigned kThreads>
+constexpr unsigned lattice_per_thread = (lattice_entries(ENC) + kThreads - 1) / kThreads;
+
+// Fills a lattice encoding's LDS tables (mfma_table_bytes): thread t converts grid entries
+// t, t + kThreads, .. (already read into `entry`) and sign set t.  A selector byte i picks
+// byte i of the magnitudes (i) or of their negations (i + 4).
+template <int ENC, unsigned kThreads>
+__device__ __forceinline__ void lattice_table(uint8_t* table,
+                                              const unsigned (&entry)[lattice_per_thread<ENC, kThreads>]) {
+    constexpr unsigned E = lattice_entries(ENC), S = lattice_signs(ENC);
+    constexpr unsigned bits = ENC == KDQ_IQ2_S ? 2 : 3;
     const unsigned t = threadIdx.x;
-    if (t < 256) {
-        unsigned pos = 0, neg = 0;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const unsigned i = (entry >> (3 * b)) & 7u;
-            const unsigned level = i == 7 ? 62u : 8u * i + 4u;
-            pos |= level << (8 * b);
-            neg |= ((256u - level) & 255u) << (8 * b);
+    for (unsigned k = 0; k < lattice_per_thread<ENC, kThreads>; ++k) {
+        const unsigned i = t + k * kThreads;
+        if (i >= E)
+            break;
+        unsigned pos[2] = {0, 0}, neg[2] = {0, 0};
+#pragma unroll
+        for (unsigned b = 0; b < lattice_width(ENC); ++b) {
+            const unsigned level = lattice_level<ENC>((entry[k] >> (bits * b)) & ((1u << bits) - 1));
+            pos[b / 4] |= level << (8 * (b % 4));
+            neg[b / 4] |= ((256u - level) & 255u) << (8 * (b % 4));
         }
-        reinterpret_cast<uint2*>(table)[t] = make_uint2(pos, neg);
+        if constexpr (lattice_width(ENC) == 8)
+            reinterpret_cast<uint4*>(table)[i] = make_uint4(pos[0], pos[1], neg[0], neg[1]);
+        else
+            reinterpret_cast<uint2*>(table)[i] = make_uint2(pos[0], neg[0]);
     }
-    if (t < 128) {
-        // eight signs: the set's seven, then their parity; selector byte i picks byte i of
-        // the magnitudes (i) or of their negations (i + 4)
-        const unsigned s = t | ((__builtin_popcount(t) & 1u) << 7);
+    uint2* sels = reinterpret_cast<uint2*>(table + size_t(E) * 2 * lattice_width(ENC));
+    for (unsigned i = t; i < S; i += kThreads) {
+        const unsigned s = ENC == KDQ_IQ3_XXS ? i | ((__builtin_popcount(i) & 1u) << 7) : i;
         unsigned lo = 0, hi = 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            lo |= (unsigned(i) + 4u * ((s >> i) & 1u)) << (8 * i);
-            hi |= (unsigned(i) + 4u * ((s >> (4 + i)) & 1u)) << (8 * i);
+        for (int b = 0; b < 4; ++b) {
+            lo |= (unsigned(b) + 4u * ((s >> b) & 1u)) << (8 * b);
+            hi |= (unsigned(b) + 4u * ((s >> (4 + b)) & 1u)) << (8 * b);
         }
-        reinterpret_cast<uint2*>(table + 256 * 8)[t] = make_uint2(lo, hi);
+        sels[i] = make_uint2(lo, hi);
     }
 }
 
@@ -1003,19 +1094,41 @@ __device__ __forceinline__ void iq3xxs_table(uint8_t* table, unsigned entry) {
 template <int ENC, bool PACKED = false>
 __device__ __forceinline__ i32x4 b_operand(const Lane& L, int m, unsigned q6_shift,
                                            const uint8_t* table = nullptr) {
-    if constexpr (ENC == KDQ_IQ3_XXS) {
-        // positions 8m .. 8m+7 of block b: index bytes 2m, 2m+1 (four positions each),
-        // sign set m; v_perm takes per byte the magnitude or its negation
-        const uint2* grid = reinterpret_cast<const uint2*>(table);
-        const uint2* sels = reinterpret_cast<const uint2*>(table + 256 * 8);
+    if constexpr (lattice(ENC)) {
+        // positions 8m .. 8m+7 of block b: one 8-value grid entry (IQ2_S) or two 4-value
+        // ones, and sign set m; v_perm takes per byte the magnitude or its negation
+        const uint2* sels = reinterpret_cast<const uint2*>(
+            table + size_t(lattice_entries(ENC)) * 2 * lattice_width(ENC));
         unsigned v[4];
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
-            const unsigned idx = L.w[2 * b + m / 2] >> (16 * (m % 2));
-            const uint2 sel = sels[(L.w[4 + b] >> (7 * m)) & 127u];
-            const uint2 g0 = grid[idx & 255u], g1 = grid[(idx >> 8) & 255u];
-            v[2 * b] = __builtin_amdgcn_perm(g0.y, g0.x, sel.x);
-            v[2 * b + 1] = __builtin_amdgcn_perm(g1.y, g1.x, sel.y);
+            if constexpr (ENC == KDQ_IQ2_S) {
+                // index byte m of the block | its qh bits 2m, 2m+1 as bits 8, 9
+                const unsigned i = ((L.w[b] >> (8 * m)) & 255u) |
+                                   (((L.w[4] >> (8 * b + 2 * m)) & 3u) << 8);
+                const uint2 sel = sels[(L.w[2 + b] >> (8 * m)) & 255u];
+                const uint4 g = reinterpret_cast<const uint4*>(table)[i];
+                v[2 * b] = __builtin_amdgcn_perm(g.z, g.x, sel.x);
+                v[2 * b + 1] = __builtin_amdgcn_perm(g.w, g.y, sel.y);
+            } else {
+                // index bytes 2m, 2m+1 (four positions each); IQ3_S adds their qh bits
+                // 2m, 2m+1 as bit 8
+                const unsigned idx = L.w[2 * b + m / 2] >> (16 * (m % 2));
+                unsigned i0 = idx & 255u, i1 = (idx >> 8) & 255u, sign;
+                if constexpr (ENC == KDQ_IQ3_S) {
+                    const unsigned qh = L.w[7] >> (8 * b + 2 * m);
+                    i0 |= (qh & 1u) << 8;
+                    i1 |= (qh & 2u) << 7;
+                    sign = (L.w[4 + b] >> (8 * m)) & 255u;
+                } else {
+                    sign = (L.w[4 + b] >> (7 * m)) & 127u;
+                }
+                const uint2* grid = reinterpret_cast<const uint2*>(table);
+                const uint2 sel = sels[sign];
+                const uint2 g0 = grid[i0], g1 = grid[i1];
+                v[2 * b] = __builtin_amdgcn_perm(g0.y, g0.x, sel.x);
+                v[2 * b + 1] = __builtin_amdgcn_perm(g1.y, g1.x, sel.y);
+            }
         }
         return i32x4{int(v[0]), int(v[1]), int(v[2]), int(v[3])};
     } else if constexpr (PACKED && ENC == KDQ_Q6_K) {
@@ -1139,6 +1252,28 @@ __device__ __forceinline__ float chunk_value(const Lane& L, ScaleSel sel, i32x4 
         const float f1 = 0.25f * d * float(2 * (L.w[5] >> 28) + 1);
         const float A0 = float(c.x * 256 + c.y), A1 = float(c.z * 256 + c.w);
         return fmaf(f1 * x1.x, A1, f0 * x0.x * A0);
+    } else if constexpr (ENC == KDQ_IQ3_S) {
+        // block scales d * (1 + 2s), s = nibble 2G (block 0), 2G+1 (block 1) of the scale
+        // bytes (sel.shift = G)
+        const float d = half_hw(L.w[6] & 0xffffu);
+        bad |= !isfinite(d);
+        const unsigned sc = L.w[8] >> (8 * sel.shift);
+        const float f0 = d * float(2 * (sc & 15u) + 1), f1 = d * float(2 * ((sc >> 4) & 15u) + 1);
+        const float A0 = float(c.x * 256 + c.y), A1 = float(c.z * 256 + c.w);
+        return fmaf(f1 * x1.x, A1, f0 * x0.x * A0);
+    } else if constexpr (ENC == KDQ_IQ2_S) {
+        // scales d * (0.5 + s) / 4 = d * (2s + 1) / 8 per 16 values: c holds positions
+        // 0..15 of each block, c2 16..31; the block's scale byte is byte 2(G%2) + b of w[5]
+        const float d = half_hw(L.w[6] & 0xffffu);
+        bad |= !isfinite(d);
+        const unsigned sc = L.w[5] >> (16 * (sel.shift % 2));
+        const float e = 0.125f * d;
+        auto f = [&](unsigned n) { return e * float(2 * (n & 15u) + 1); };
+        const float a00 = float(c.x * 256 + c.y), a01 = float(c2.x * 256 + c2.y);
+        const float a10 = float(c.z * 256 + c.w), a11 = float(c2.z * 256 + c2.w);
+        const float b0 = fmaf(f(sc >> 4), a01, f(sc) * a00);
+        const float b1 = fmaf(f(sc >> 12), a11, f(sc >> 8) * a10);
+        return fmaf(x1.x, b1, x0.x * b0);
     } else if constexpr (ENC == KDQ_IQ4_XS) {
         // block scales d * (ls - 32), ls = 4 bits of scales_l | 2 bits of scales_h << 4
         // (sel.shift = G: blocks 2G, 2G+1)
@@ -1322,7 +1457,7 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
     const bool carrier = j / 4 == G;
     // Q4_K: the scale bytes of sub-blocks 2G, 2G+1; Q6_K: 2p for chunk G = 2h + p
     const ScaleSel sel = ENC == KDQ_Q6_K     ? ScaleSel{2 * (G % 2), (j & 1) != 0}
-                         : ENC == KDQ_IQ4_XS || ENC == KDQ_Q3_K ? ScaleSel{G, false}
+                         : ENC == KDQ_IQ4_XS || ENC == KDQ_Q3_K || lattice(ENC) ? ScaleSel{G, false}
                                              : ScaleSel{8 * ((2 * G) & 3), G >= 2};
     // every argument in one round of scalar loads, then the exit test
     asm volatile("" ::"s"(weights), "s"(up), "s"(x), "s"(y), "s"(status), "s"(row_bytes),
@@ -1357,6 +1492,10 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
                 load_lane_q3k(w + size_t(n) * row_bytes, g, G, L[k]);
             else if constexpr (ENC == KDQ_IQ3_XXS)
                 load_lane_iq3xxs(w + size_t(n) * row_bytes, g, G, L[k]);
+            else if constexpr (ENC == KDQ_IQ3_S)
+                load_lane_iq3s(w + size_t(n) * row_bytes, g, G, L[k]);
+            else if constexpr (ENC == KDQ_IQ2_S)
+                load_lane_iq2s(w + size_t(n) * row_bytes, g, G, L[k]);
             else if constexpr (ENC == KDQ_IQ4_NL)  // Q4_0's block size and layout
                 load_lane<KDQ_Q4_0>(w + size_t(n) * row_bytes, 4 * g + G, L[k]);
             else
@@ -1368,19 +1507,22 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
     const unsigned units_x = R * in / 8;
     XUnit first_unit;
     load_unit(x, in, min(unsigned(threadIdx.x), units_x - 1), first_unit);
-    // the lookup table's source entry, requested before the weights (the staging waits
-    // for it)
-    unsigned entry = 0;
-    if constexpr (ENC == KDQ_IQ3_XXS)
-        entry = kIq3xxsGrid[min(unsigned(threadIdx.x), 255u)];
+    // the lattice grid entries this thread converts, requested before the weights (the
+    // staging waits for them)
+    unsigned entry[lattice(ENC) ? lattice_per_thread<ENC, kThreads> : 1];
+    if constexpr (lattice(ENC)) {
+#pragma unroll
+        for (unsigned k = 0; k < lattice_per_thread<ENC, kThreads>; ++k)
+            entry[k] = lattice_entry<ENC>(min(threadIdx.x + k * kThreads, lattice_entries(ENC) - 1));
+    }
     asm volatile("" ::: "memory");  // x is not restrict: its loads stay before this point
     __builtin_amdgcn_sched_barrier(0);
     Lane L[kUnits];
     load_units(r0, UnitCursor{wave, 0}, L);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (ENC == KDQ_IQ3_XXS)
-        iq3xxs_table(table, entry);
+    if constexpr (lattice(ENC))
+        lattice_table<ENC, kThreads>(table, entry);
     if (threadIdx.x < units_x)
         mstage_unit<ENC>(in, threadIdx.x, first_unit, atab, blocks);
     for (unsigned u = threadIdx.x + kThreads; u < units_x; u += kThreads) {
@@ -1419,7 +1561,7 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
                     for (int m = 0; m < 4; ++m) {
                         const i32x4 av = *reinterpret_cast<const i32x4*>(a + m * 256);
                         const i32x4 bv = b_operand<ENC, PACKED>(L[k], m, sel.shift, table);
-                        if ((ENC == KDQ_Q6_K || ENC == KDQ_Q3_K) && m >= 2)
+                        if ((ENC == KDQ_Q6_K || ENC == KDQ_Q3_K || ENC == KDQ_IQ2_S) && m >= 2)
                             c2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, c2, 0, 0, 0);
                         else
                             c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, c, 0, 0, 0);
@@ -1755,6 +1897,16 @@ int launch_mfma_any(int encoding, const void* w, size_t row_bytes, const float* 
             return launch_mfma<KDQ_IQ3_XXS, false>(w, row_bytes, x, rows, in, out, y, stride,
                                                    status, s);
         return KDQ_ERR_UNSUPPORTED;
+    case KDQ_IQ3_S:
+        if constexpr (!PACKED)
+            return launch_mfma<KDQ_IQ3_S, false>(w, row_bytes, x, rows, in, out, y, stride,
+                                                 status, s);
+        return KDQ_ERR_UNSUPPORTED;
+    case KDQ_IQ2_S:
+        if constexpr (!PACKED)
+            return launch_mfma<KDQ_IQ2_S, false>(w, row_bytes, x, rows, in, out, y, stride,
+                                                 status, s);
+        return KDQ_ERR_UNSUPPORTED;
     default:
         return KDQ_ERR_UNSUPPORTED;
     }
@@ -1914,15 +2066,15 @@ int with_encoding(int encoding, F&& f) {
 bool streamed_encoding(int encoding) {
     return encoding == KDQ_Q8_0 || encoding == KDQ_Q4_0 || encoding == KDQ_Q4_K ||
            encoding == KDQ_Q6_K || encoding == KDQ_IQ4_XS || encoding == KDQ_IQ4_NL ||
-           encoding == KDQ_Q3_K || encoding == KDQ_IQ3_XXS;
+           encoding == KDQ_Q3_K || lattice(encoding);
 }
 
 // The streaming kernels need whole 64-value lane slots, 4-byte aligned rows and packed
 // rows of exactly the format's size (16-byte aligned for Q4_K); Q6_K (MFMA kernel only)
 // 256-value groups and 2-byte aligned rows.
 bool streams(int encoding, const void* weights, size_t row_bytes, size_t in) {
-    // 210- / 110- / 98-byte super-blocks
-    if (encoding == KDQ_Q6_K || encoding == KDQ_Q3_K || encoding == KDQ_IQ3_XXS)
+    // 210-, 110-, 98- and 82-byte super-blocks: 2-byte aligned rows
+    if (encoding == KDQ_Q6_K || encoding == KDQ_Q3_K || lattice(encoding))
         return in % 256 == 0 && row_bytes % 2 == 0 && aligned(weights, 2);
     if (encoding == KDQ_IQ4_XS)  // 136-byte super-blocks: 8-byte aligned rows
         return in % 256 == 0 && row_bytes % 8 == 0 && aligned(weights, 8);
@@ -2165,6 +2317,14 @@ int launch_fused(const kdq_matvec_job* jobs, const size_t* idx, size_t n, hipStr
         if constexpr (!PACKED)
             return launch_mfma_rows<KDQ_IQ3_XXS, false>(j0.rows, p.waves, mj, stream);
         return KDQ_ERR_UNSUPPORTED;
+    case KDQ_IQ3_S:
+        if constexpr (!PACKED)
+            return launch_mfma_rows<KDQ_IQ3_S, false>(j0.rows, p.waves, mj, stream);
+        return KDQ_ERR_UNSUPPORTED;
+    case KDQ_IQ2_S:
+        if constexpr (!PACKED)
+            return launch_mfma_rows<KDQ_IQ2_S, false>(j0.rows, p.waves, mj, stream);
+        return KDQ_ERR_UNSUPPORTED;
     default:
         return KDQ_ERR_UNSUPPORTED;
     }
@@ -2272,6 +2432,10 @@ int indexed_gemv_affine(const IndexedJob& first, unsigned count, size_t x_step,
             return launch_mfma_rows<KDQ_Q3_K, false>(j.rows, p.waves, mj, s);
         case KDQ_IQ3_XXS:
             return launch_mfma_rows<KDQ_IQ3_XXS, false>(j.rows, p.waves, mj, s);
+        case KDQ_IQ3_S:
+            return launch_mfma_rows<KDQ_IQ3_S, false>(j.rows, p.waves, mj, s);
+        case KDQ_IQ2_S:
+            return launch_mfma_rows<KDQ_IQ2_S, false>(j.rows, p.waves, mj, s);
         default:
             return KDQ_ERR_UNSUPPORTED;
         }

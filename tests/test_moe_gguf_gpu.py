@@ -1,13 +1,14 @@
 """GPU parity of the GGUF MoE layer (kdq_moe_gguf) against the oracle's restatement of
 MoeLayer::forward (IW/src/models/text/qwen_layers.cpp:378-492): the routing (selected
 experts bit-exact, weights to 1e-6) and y within rel-L2 <= 1e-3, max-abs <= 2e-2 of its
-RMS.  Expert projections of Q4_0 / Q8_0 / Q4_K / Q3_K / Q6_K / IQ4_XS / IQ4_NL run on
-the MFMA kernel with the expert slice chosen on the device, the other encodings (IQ3_S,
-IQ3_XXS in EXACT) on the exact kernel.  The three
+RMS.  Expert projections of the block encodings (Q4_0 / Q8_0 / Q4_K / Q3_K / Q6_K /
+IQ4_XS / IQ4_NL and the lattice encodings IQ3_XXS / IQ3_S / IQ2_S) run on the MFMA
+kernel with the expert slice chosen on the device, BF16 on the exact kernel.  The
 encoding mixes cover each launch form: gate and up stored alike run as one paired launch
-that applies the swiglu (MIXED: experts and shared expert; EXACT: the shared expert),
-gate and up stored differently as two launches and the swiglu kernel (SPLIT), and the
-exact kernel's slot-affine launch (EXACT experts)."""
+that applies the swiglu (MIXED: experts and shared expert; EXACT and LATTICE: IQ3_S /
+IQ2_S experts and the shared expert), gate and up stored differently as two launches and
+the swiglu kernel (SPLIT), and the exact kernel's slot-affine launch (EXACT: BF16
+down experts)."""
 import numpy as np
 import pytest
 
@@ -17,7 +18,7 @@ from tests.util import assert_close
 pytestmark = pytest.mark.gpu
 
 F32, Q4_0, Q8_0, Q3_K, Q4_K, Q6_K, IQ4_XS = 0, 2, 8, 11, 12, 14, 23
-IQ3_XXS, IQ3_S = 18, 21
+IQ3_XXS, IQ3_S, IQ2_S, BF16 = 18, 21, 22, 30
 NAMES = ("router", "gate_exps", "up_exps", "down_exps", "gate_shexp", "up_shexp", "down_shexp")
 
 
@@ -51,14 +52,17 @@ def to_device(torch, device, spec):
 
 MIXED = {"gate_exps": Q4_K, "up_exps": Q4_K, "down_exps": Q6_K, "gate_shexp": Q8_0,
          "up_shexp": Q8_0, "down_shexp": Q4_K}
-EXACT = {"gate_exps": IQ3_S, "up_exps": IQ3_S, "down_exps": IQ3_XXS, "gate_shexp": Q4_0,
+EXACT = {"gate_exps": IQ3_S, "up_exps": IQ3_S, "down_exps": BF16, "gate_shexp": Q4_0,
          "up_shexp": Q4_0, "down_shexp": Q6_K}
+LATTICE = {"gate_exps": IQ2_S, "up_exps": IQ2_S, "down_exps": IQ3_XXS, "gate_shexp": IQ3_S,
+           "up_shexp": IQ3_S, "down_shexp": IQ3_XXS}
 SPLIT = {"gate_exps": Q4_K, "up_exps": Q8_0, "down_exps": Q4_0, "gate_shexp": Q8_0,
          "up_shexp": Q4_K, "down_shexp": Q8_0}
 
 
 @pytest.mark.parametrize("rows", [1, 3, 8])
-@pytest.mark.parametrize("encs", [MIXED, EXACT, SPLIT], ids=["mixed", "exact", "split"])
+@pytest.mark.parametrize("encs", [MIXED, EXACT, SPLIT, LATTICE],
+                         ids=["mixed", "exact", "split", "lattice"])
 def test_moe_gguf_parity(device, oracle, rows, encs):
     import torch
     H, E, K, F, S = 512, 16, 4, 256, 512
@@ -82,8 +86,8 @@ def test_moe_gguf_more_rows(device, oracle, rows, top_k, encs):
     passes of the router / shared batch), 64 rows x top-8 = 512 slots, and 200 rows x
     top-8 (100 slots per expert).  MIXED runs gate, up and down on the grouped prefill
     GEMM (128-row token tiles of one expert each); SPLIT runs gate / up on the GEMM and
-    its Q4_0 down on 8-row GEMV items over the same tiles; EXACT runs the exact kernel's
-    8-row items."""
+    its Q4_0 down on 8-row GEMV items over the same tiles; EXACT runs its IQ3_S gate / up
+    on 8-row MFMA items and its BF16 down on the exact kernel's 8-row items."""
     import torch
     H, E, F, S = 512, 16, 256, 512
     spec = make_layer(40 + rows, H, E, top_k, F, S, encs)
