@@ -23,6 +23,7 @@
 
 #include <cmath>
 #include <mutex>
+#include <utility>
 
 namespace kdq {
 namespace {
@@ -45,11 +46,41 @@ namespace {
 
 // ------------------------------------------------------------------ routing
 
+// Routing reductions by DPP row operations (no LDS round trips): within each row of 16
+// lanes by pair, quad, half-row and row permutations, then the four rows in a fixed order
+// through readlane.  Every lane returns the same bits; all 64 lanes must be active.
+template <int CTRL>
+__device__ __forceinline__ double dpp_read_double(double v) {
+    const unsigned long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, int(b), CTRL, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, int(b >> 32), CTRL, 0xf, 0xf, false);
+    return __longlong_as_double((static_cast<long long>(hi) << 32) | unsigned(lo));
+}
+
+__device__ __forceinline__ double readlane_double(double v, int lane) {
+    const unsigned long long b = __double_as_longlong(v);
+    const unsigned lo = __builtin_amdgcn_readlane(int(b), lane);
+    const unsigned hi = __builtin_amdgcn_readlane(int(b >> 32), lane);
+    return __longlong_as_double((static_cast<long long>(hi) << 32) | lo);
+}
+
 __device__ __forceinline__ double wave_sum_double(double v) {
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1)
-        v += __shfl_xor(v, offset, 64);
-    return v;
+    v += dpp_read_double<0xb1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_read_double<0x4e>(v);   // quad_perm [2,3,0,1]
+    v += dpp_read_double<0x141>(v);  // row_half_mirror
+    v += dpp_read_double<0x140>(v);  // row_mirror: every lane holds its row's sum
+    return (readlane_double(v, 0) + readlane_double(v, 16)) +
+           (readlane_double(v, 32) + readlane_double(v, 48));
+}
+
+// Maximum over the 64 lanes of any floats (fmaxf: a NaN loses to a number).
+__device__ __forceinline__ float wave_max_rows(float v) {
+    v = fmaxf(v, dpp_read<0xb1, 0xf>(v));
+    v = fmaxf(v, dpp_read<0x4e, 0xf>(v));
+    v = fmaxf(v, dpp_read<0x141, 0xf>(v));
+    v = fmaxf(v, dpp_read<0x140, 0xf>(v));
+    auto at = [&](int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); };
+    return fmaxf(fmaxf(at(0), at(16)), fmaxf(at(32), at(48)));
 }
 
 // libstdc++'s std::partial_sort (std::__heap_select, then std::__sort_heap, both over
@@ -106,31 +137,32 @@ __device__ __forceinline__ int heap_route(POf p_of, unsigned experts, unsigned k
     return slot;
 }
 
-// Token t by one whole wavefront (lane = its lane).
-__device__ __forceinline__ void route_token(const float* __restrict__ logits, unsigned t,
-                                            unsigned experts, unsigned top_k,
-                                            int32_t* __restrict__ idx, float* __restrict__ weight,
-                                            unsigned lane, int* lds_idx = nullptr) {
+// Token t by one whole wavefront (lane = its lane): lane i < top_k gets the i-th selected
+// expert and its renormalised weight.  R probabilities per lane (experts <= 64 R).
+template <int R>
+__device__ __forceinline__ void route_select_r(const float* __restrict__ logits, unsigned t,
+                                               unsigned experts, unsigned top_k, unsigned lane,
+                                               int& selected, float& selected_weight) {
     const float* l = logits + size_t(t) * experts;
-    float v[4], p[4];
+    float v[R], p[R];
     float maximum = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < R; ++j) {
         const unsigned e = lane + 64 * j;
         v[j] = e < experts ? l[e] : -INFINITY;
         maximum = fmaxf(maximum, v[j]);
     }
-    maximum = wave_max(maximum);
+    maximum = wave_max_rows(maximum);
     double total = 0.0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < R; ++j) {
         const unsigned e = lane + 64 * j;
         p[j] = e < experts ? expf(v[j] - maximum) : 0.f;
         total += double(p[j]);
     }
     total = wave_sum_double(total);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < R; ++j)
         p[j] = float(double(p[j]) / total);
 
     // Selection.  The reference takes the first k of std::partial_sort over experts
@@ -139,16 +171,19 @@ __device__ __forceinline__ void route_token(const float* __restrict__ logits, un
     // maximum and a ballot per register per pick.  Equal probabilities (and NaN ones,
     // which compare false both ways) come out in the order of libstdc++'s heap
     // selection; then the wavefront reruns that heap algorithm (heap_route below).
-    bool valid[4];
+    bool valid[R];
     bool nan_seen = false;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < R; ++j) {
         valid[j] = lane + 64 * j < experts;
         nan_seen |= __ballot(valid[j] && isnan(p[j])) != 0;
     }
     auto p_of = [&](int e) {  // p of expert e (wave-uniform)
         const int j = e / 64;
-        const float pj = j == 0 ? p[0] : (j == 1 ? p[1] : (j == 2 ? p[2] : p[3]));
+        float pj = p[0];
+#pragma unroll
+        for (int r = 1; r < R; ++r)
+            pj = j == r ? p[r] : pj;
         return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), e % 64));
     };
     int chosen_e = 0;  // lane i < top_k: the i-th selection
@@ -159,7 +194,7 @@ __device__ __forceinline__ void route_token(const float* __restrict__ logits, un
         for (unsigned i = 0; i <= top_k && i < experts; ++i) {
             float c = 0.f;  // every probability is >= 0 here
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < R; ++j)
                 if (valid[j] && !((taken >> j) & 1u))
                     c = fmaxf(c, p[j]);
             c = wave_max_nonneg(c);
@@ -169,7 +204,7 @@ __device__ __forceinline__ void route_token(const float* __restrict__ logits, un
                 break;  // only the largest unselected p was needed
             int best = -1;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < R; ++j) {
                 const bool open = valid[j] && !((taken >> j) & 1u);
                 const unsigned long long hit = __ballot(open && p[j] == c);
                 if (best < 0 && hit)
@@ -191,11 +226,32 @@ __device__ __forceinline__ void route_token(const float* __restrict__ logits, un
             chosen_p = pi;
     }
     sum = fmaxf(sum, 6.103515625e-5f);
+    selected = chosen_e;
+    selected_weight = chosen_p / sum;
+}
+
+__device__ __forceinline__ void route_select(const float* __restrict__ logits, unsigned t,
+                                             unsigned experts, unsigned top_k, unsigned lane,
+                                             int& selected, float& selected_weight) {
+    if (experts <= 64)
+        route_select_r<1>(logits, t, experts, top_k, lane, selected, selected_weight);
+    else
+        route_select_r<4>(logits, t, experts, top_k, lane, selected, selected_weight);
+}
+
+// Token t by one whole wavefront: its selection stored to idx / weight (and lds_idx).
+__device__ __forceinline__ void route_token(const float* __restrict__ logits, unsigned t,
+                                            unsigned experts, unsigned top_k,
+                                            int32_t* __restrict__ idx, float* __restrict__ weight,
+                                            unsigned lane, int* lds_idx = nullptr) {
+    int e;
+    float we;
+    route_select(logits, t, experts, top_k, lane, e, we);
     if (lane < top_k) {
-        idx[size_t(t) * top_k + lane] = chosen_e;
-        weight[size_t(t) * top_k + lane] = chosen_p / sum;
+        idx[size_t(t) * top_k + lane] = e;
+        weight[size_t(t) * top_k + lane] = we;
         if (lds_idx)
-            lds_idx[t * top_k + lane] = chosen_e;
+            lds_idx[t * top_k + lane] = e;
     }
 }
 
@@ -469,9 +525,11 @@ __device__ __forceinline__ void fp8_terms16(float (&v)[16], u32x4 (&out)[TERMS])
 
 // Row r's 32-value block b of one tile (codes/scales of that tile): block b = 2q + hb of
 // step q; its values 0..15 belong to lane r (piece hb), 16..31 to lane r + 32 (piece hb).
+// A 32-value block as TERMS FP8 terms: values 0..15 into tl, 16..31 into th; returns the
+// block's E8M0 scale byte.
 template <int TERMS>
-__device__ __forceinline__ void store_tile_block(float (&v)[32], bool finite, uint8_t* codes,
-                                                 uint8_t* scales, unsigned r, unsigned b) {
+__device__ __forceinline__ uint8_t block_terms(float (&v)[32], bool finite, u32x4 (&tl)[TERMS],
+                                               u32x4 (&th)[TERMS]) {
     float amax = 0.f;
 #pragma unroll
     for (int i = 0; i < 32; ++i)
@@ -483,7 +541,6 @@ __device__ __forceinline__ void store_tile_block(float (&v)[32], bool finite, ui
         lo[i] = finite ? __builtin_amdgcn_ldexpf(v[i], -e) : 0.f;
         hi[i] = finite ? __builtin_amdgcn_ldexpf(v[16 + i], -e) : 0.f;
     }
-    u32x4 tl[TERMS], th[TERMS];
     fp8_terms16<TERMS>(lo, tl);
     fp8_terms16<TERMS>(hi, th);
     if (!finite) {  // FP8 NaN codes as well as the NaN scale: NaN however it is read
@@ -491,6 +548,14 @@ __device__ __forceinline__ void store_tile_block(float (&v)[32], bool finite, ui
         for (int k = 0; k < TERMS; ++k)
             tl[k] = th[k] = u32x4{0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu};
     }
+    return finite ? uint8_t(e + 127) : uint8_t(255);
+}
+
+template <int TERMS>
+__device__ __forceinline__ void store_tile_block(float (&v)[32], bool finite, uint8_t* codes,
+                                                 uint8_t* scales, unsigned r, unsigned b) {
+    u32x4 tl[TERMS], th[TERMS];
+    const uint8_t scale = block_terms<TERMS>(v, finite, tl, th);
     const unsigned q = b / 2, hb = b % 2;
     uint8_t* at = codes + size_t(q) * TERMS * 2048 + hb * 1024;
 #pragma unroll
@@ -498,16 +563,14 @@ __device__ __forceinline__ void store_tile_block(float (&v)[32], bool finite, ui
         *reinterpret_cast<u32x4*>(at + k * 2048 + 16 * r) = tl[k];
         *reinterpret_cast<u32x4*>(at + k * 2048 + 16 * (r + 32)) = th[k];
     }
-    scales[(q / 4) * 256 + 4 * (r + 32 * hb) + q % 4] = finite ? uint8_t(e + 127) : uint8_t(255);
+    scales[(q / 4) * 256 + 4 * (r + 32 * hb) + q % 4] = scale;
 }
 
 // Row r (of 32) of activation tile tau from token row `token` of x (bf16 [tokens][hidden]),
 // 32-value block b: its kXTerms FP8 terms and scale in the tile layout.
-__device__ __forceinline__ void gather_block(const uint16_t* __restrict__ x, unsigned hidden,
-                                             size_t token, uint8_t* __restrict__ xa,
-                                             size_t tiles, size_t tau, unsigned r, unsigned b) {
-    const uint8_t* src = reinterpret_cast<const uint8_t*>(x + token * hidden + 32 * b);
-    float v[32];
+// 32 bf16 values from src as fp32 (exact); returns whether all are finite.
+__device__ __forceinline__ bool load_bf16_block(const uint16_t* src16, float (&v)[32]) {
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(src16);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         const u32x4 w = load16(src + 16 * c);
@@ -522,6 +585,14 @@ __device__ __forceinline__ void gather_block(const uint16_t* __restrict__ x, uns
 #pragma unroll
     for (int i = 0; i < 32; ++i)
         finite = finite && isfinite(v[i]);
+    return finite;
+}
+
+__device__ __forceinline__ void gather_block(const uint16_t* __restrict__ x, unsigned hidden,
+                                             size_t token, uint8_t* __restrict__ xa,
+                                             size_t tiles, size_t tau, unsigned r, unsigned b) {
+    float v[32];
+    const bool finite = load_bf16_block(x + token * hidden + 32 * b, v);
     const Tiles l = tile_layout(xa, tiles, hidden / 64, kXTerms);
     store_tile_block<kXTerms>(v, finite, l.codes + tau * l.code_stride,
                               l.scales + tau * l.scale_stride, r, b);
@@ -1079,6 +1150,383 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     *reinterpret_cast<f32x4*>(y + t * hidden + d) = sum;
 }
 
+
+// ------------------------------------------------------------ single-token decode
+//
+// One token routes to top_k distinct experts, so every slot is a one-row product of its
+// own expert.  Two launches replace the five of the general path:
+//
+//   decode_gate_up_kernel  grid (inter / 32 feature groups, top_k slots), 2 * runs waves:
+//     waves 0 .. runs-1 multiply the gate rows and waves runs .. 2 runs-1 the up rows of
+//     the slot's expert for the group's 32 features, each over its own run of whole quads
+//     (4 steps of 64 K values) of the hidden dimension.  Wavefront 0 routes the token
+//     (route_select over its logits) while the others write x into LDS as kXTerms FP8
+//     terms with 32-value block scales, in the term-row layout below; then every
+//     wavefront issues all weight loads of a batch of quads at once.  The runs' results
+//     meet in LDS and are summed in run order; h = silu(g) * u is stored as kHTerms FP8
+//     terms in the term-row layout for the down product.  Workgroup (0, 0) also writes
+//     the routing outputs.
+//   decode_down_kernel  grid (hidden / 32 row groups), top_k * runs waves: wave (i, p)
+//     multiplies slot i's h by its expert's down rows over run p of the inter dimension;
+//     per slot the runs are summed in order, then y = sum_i w_i * down_i in selection
+//     order (the general path's combine).
+//
+// Term rows: the token's activation is a sum of FP8 terms (kXTerms for x, kHTerms for h)
+// sharing one E8M0 scale per 32-value block, and row k of the MFMA's A operand carries
+// term k (rows past the terms are zero), so one MFMA per step multiplies every term by
+// the weights and the token's product is the sum of result rows 0 .. terms-1 (accumulator
+// elements 0 .. terms-1 of lanes 0..31).  Per step q of a row vector and per term k, 64
+// bytes: bytes 32h .. 32h+15 hold term k of values 64q + 16h .. +15 and bytes
+// 32h+16 .. 32h+31 of values 64q + 32 + 16h .. +15 (what lane k + 32h of the A operand
+// holds); the block scales are shared by the rows (lane r + 32b supplies block b's).
+
+constexpr int kDecodeWaves = 16;
+constexpr unsigned kDecodeMaxSteps = 256;  // hidden / 64 of the single-token path (x in LDS)
+
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    [&]<int... I>(std::integer_sequence<int, I...>) {
+        (f.template operator()<I>(), ...);
+    }(std::make_integer_sequence<int, N>{});
+}
+
+// One packed 32-row group of an expert as buffer resources (wave-uniform): its codes
+// (steps KB) and its scale dwords (per 4 steps, 256 bytes).  Loads address a lane's bytes
+// by a per-lane offset and the step by a uniform one, so a batch of loads costs one
+// address register.
+struct DecodeGroup {
+    __amdgpu_buffer_rsrc_t codes, scales;
+};
+
+__device__ __forceinline__ DecodeGroup decode_group(const uint8_t* packed, const Packed& whole,
+                                                    const Packed& one, size_t eg) {
+    constexpr int kRawWord3 = 0x00020000;  // raw (untyped) buffer, 32-bit data
+    DecodeGroup g;
+    g.codes = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(packed + eg * one.steps * 1024), 0, int(one.steps * 1024),
+        kRawWord3);
+    g.scales = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(packed + whole.code_bytes + eg * one.scale_groups * 256), 0,
+        int(one.scale_groups * 256), kRawWord3);
+    return g;
+}
+
+// The streamed weights of quads [qb, qb + NQ) of one group: all 4 NQ code loads and NQ
+// scale loads in flight at once (non-temporal), loads past the last step clamped to it.
+template <int NQ> struct DecodeB {
+    u32x4 c[4 * NQ];
+    unsigned s[NQ];
+};
+
+template <int NQ>
+__device__ __forceinline__ void decode_load_b(const DecodeGroup& g, unsigned lane, unsigned qb,
+                                              unsigned steps, DecodeB<NQ>& b) {
+    typedef unsigned u4 __attribute__((ext_vector_type(4)));
+    constexpr int kNonTemporal = 2;
+    const unsigned quads = (steps + 3) / 4;
+#pragma unroll
+    for (int j = 0; j < 4 * NQ; ++j) {
+        const u4 v = __builtin_amdgcn_raw_buffer_load_b128(
+            g.codes, int(lane * 16), int(min(4 * qb + j, steps - 1) * 1024), kNonTemporal);
+        b.c[j] = u32x4{v.x, v.y, v.z, v.w};
+    }
+#pragma unroll
+    for (int j = 0; j < NQ; ++j)
+        b.s[j] = __builtin_amdgcn_raw_buffer_load_b32(
+            g.scales, int(lane * 4), int(min(qb + j, quads - 1) * 256), kNonTemporal);
+}
+
+// acc += A x B over the steps of quads [qb, qb + NQ) below `end` (the end of the
+// wavefront's run, or of the dimension): the lane's A operand of step q (its term row)
+// from a_of(q, lo, hi) (LDS) and its scale byte from as_of(q).
+template <int NQ, class AOf, class SOf>
+__device__ __forceinline__ void decode_mma(const DecodeB<NQ>& b, unsigned qb, unsigned end,
+                                           AOf a_of, SOf as_of, f32x16& acc) {
+    static_for<4 * NQ>([&]<int J>() {
+        const unsigned q = 4 * qb + J;
+        if (q < end) {
+            u32x4 lo, hi;
+            a_of(q, lo, hi);
+            acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                a_operand(lo, hi), b_operand(b.c[J]), acc, 0 /* A: fp8 e4m3 */,
+                4 /* B: fp4 e2m1 */, 0, int(as_of(q)), J % 4, int(b.s[J / 4]));
+        }
+    });
+}
+
+// The token's product: the sum of the term rows (accumulator elements 0 .. TERMS-1 of
+// lanes 0..31), in term order.
+template <int TERMS>
+__device__ __forceinline__ float term_sum(const f32x16& acc) {
+    float v = acc[0];
+#pragma unroll
+    for (int k = 1; k < TERMS; ++k)
+        v += acc[k];
+    return v;
+}
+
+// h of feature 32 * group + i (i = lane % 32; both halves of the wavefront hold the same
+// 32 values): block scale from the half's maximum, kHTerms FP8 terms into the term-row
+// layout of the slot (codes: the slot's steps, scales: its blocks); lanes < 32 store.
+__device__ __forceinline__ void store_decode_h(float hv, unsigned group, unsigned lane,
+                                               uint8_t* codes, uint8_t* scales) {
+    const bool finite = half_max(isfinite(hv) ? 0.f : 1.f) == 0.f;
+    const int e = block_exponent(half_max(fabsf(hv)));
+    float v = finite ? __builtin_amdgcn_ldexpf(hv, -e) : 0.f;
+    if (lane >= 32)
+        return;
+    const unsigned q = group / 2, b = group % 2;
+    uint8_t* at = codes + size_t(q) * kHTerms * 64 + (lane / 16) * 32 + b * 16 + lane % 16;
+#pragma unroll
+    for (int t = 0; t < kHTerms; ++t) {
+        const int c = __builtin_amdgcn_cvt_pk_fp8_f32(v, 0.f, 0, false);
+        at[t * 64] = finite ? uint8_t(c & 0xff) : uint8_t(0x7f);  // 0x7f: FP8 NaN
+        v -= __builtin_amdgcn_cvt_f32_fp8(c, 0);
+    }
+    if (lane == 0)
+        scales[group] = finite ? uint8_t(e + 127) : uint8_t(255);
+}
+
+// Quarter u (values 8u .. 8u+7) of x into the term-row layout: the four lanes of a DPP
+// quad hold one 32-value block (u = 4b + j, lane % 4 = j) and share its maximum and its
+// finiteness, so every lane converts 8 values; lanes with `live` false take part in the
+// quad reductions only.  Bit-identical to converting the block in one lane.
+__device__ __forceinline__ void stage_x_quarter(const uint16_t* __restrict__ x, unsigned u,
+                                                bool live, uint8_t* xq, uint8_t* xs) {
+    const u32x4 w = live ? load16(reinterpret_cast<const uint8_t*>(x + 8 * u))
+                         : u32x4{0u, 0u, 0u, 0u};
+    const unsigned ws[4] = {w.x, w.y, w.z, w.w};
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // bf16 -> fp32 is exact
+        v[2 * i] = __uint_as_float(ws[i] << 16);
+        v[2 * i + 1] = __uint_as_float(ws[i] & 0xffff0000u);
+    }
+    float amax = 0.f, bad = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        amax = fmaxf(amax, fabsf(v[i]));
+        bad = isfinite(v[i]) ? bad : 1.f;
+    }
+    amax = fmaxf(amax, quad_xor1(amax));
+    amax = fmaxf(amax, quad_xor2(amax));
+    bad = fmaxf(bad, quad_xor1(bad));
+    bad = fmaxf(bad, quad_xor2(bad));
+    if (!live)
+        return;
+    const bool finite = bad == 0.f;
+    const int e = block_exponent(amax);
+    unsigned t[kXTerms][2];
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+        float q[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            q[i] = finite ? __builtin_amdgcn_ldexpf(v[4 * d + i], -e) : 0.f;
+#pragma unroll
+        for (int k = 0; k < kXTerms; ++k) {
+            const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+            const int both = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], lo, true);
+            t[k][d] = finite ? unsigned(both) : 0x7f7f7f7fu;
+            if (k + 1 < kXTerms) {  // the remainder is exact in fp32 (Sterbenz)
+                q[0] -= __builtin_amdgcn_cvt_f32_fp8(both, 0);
+                q[1] -= __builtin_amdgcn_cvt_f32_fp8(both, 1);
+                q[2] -= __builtin_amdgcn_cvt_f32_fp8(both, 2);
+                q[3] -= __builtin_amdgcn_cvt_f32_fp8(both, 3);
+            }
+        }
+    }
+    const unsigned b = u / 4, j = u % 4;
+    uint8_t* at = xq + (b / 2) * kXTerms * 64 + (j / 2) * 32 + (b % 2) * 16 + (j % 2) * 8;
+#pragma unroll
+    for (int k = 0; k < kXTerms; ++k)
+        *reinterpret_cast<uint2*>(at + k * 64) = make_uint2(t[k][0], t[k][1]);
+    if (j == 0)
+        xs[b] = finite ? uint8_t(e + 127) : uint8_t(255);
+}
+
+template <int NQ, int R>
+__global__ __launch_bounds__(kDecodeWaves * 64) void decode_gate_up_kernel(
+    const uint16_t* __restrict__ x, const float* __restrict__ logits, unsigned hidden,
+    unsigned inter, unsigned experts, unsigned top_k, const uint8_t* __restrict__ gate,
+    const uint8_t* __restrict__ up, unsigned runs, unsigned run_quads,
+    int32_t* __restrict__ idx, float* __restrict__ weight, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ perm, uint8_t* __restrict__ hq, uint8_t* __restrict__ hs) {
+    // x in the term-row layout (every step), its block scales, 32 zero bytes
+    __shared__ __align__(16) uint8_t xq[kDecodeMaxSteps * kXTerms * 64 + 32];
+    __shared__ uint8_t xs[kDecodeMaxSteps * 2];
+    __shared__ int s_expert;
+    __shared__ float red[kDecodeWaves][32];
+    // the wavefront index as a uniform value (the weight loads' offsets and resources are
+    // per wavefront)
+    const unsigned wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+    const unsigned steps = hidden / 64, quads = (steps + 3) / 4;
+    const unsigned slot = blockIdx.y, group = blockIdx.x;
+    uint8_t* zero = xq + steps * kXTerms * 64;
+    if (wave == 0) {
+        // wavefront 0 routes the token (a few hundred bytes of logits) ...
+        int selected;
+        float selected_weight;
+        route_select_r<R>(logits, 0, experts, top_k, lane, selected, selected_weight);
+        if (lane == 0)
+            s_expert = __builtin_amdgcn_readlane(selected, slot);
+        if (blockIdx.x == 0 && blockIdx.y == 0) {
+            // routing outputs; the experts of one token are distinct, so a slot's position
+            // in the permutation is the number of selected experts below its own
+            int lower = 0;
+            for (unsigned j = 0; j < top_k; ++j)
+                lower += __builtin_amdgcn_readlane(selected, j) < selected;
+            if (lane < top_k) {
+                idx[lane] = selected;
+                weight[lane] = selected_weight;
+                perm[lower] = int(lane);
+            }
+            for (unsigned b = lane; b <= experts; b += 64) {
+                int below = 0;
+                for (unsigned j = 0; j < top_k; ++j)
+                    below += __builtin_amdgcn_readlane(selected, j) < int(b);
+                offsets[b] = below;
+            }
+        }
+    } else {
+        // ... while the others write x as FP8 terms into LDS, one lane per 8 values
+        if (threadIdx.x - 64 < 8)
+            reinterpret_cast<unsigned*>(zero)[threadIdx.x - 64] = 0u;
+        for (unsigned first = 0; first < 8 * steps; first += blockDim.x - 64) {
+            const unsigned u = first + threadIdx.x - 64;
+            if (__ballot(u < 8 * steps))  // whole wavefronts (the quads reduce by DPP)
+                stage_x_quarter(x, u, u < 8 * steps, xq, xs);
+        }
+    }
+    __syncthreads();
+    const unsigned m = wave / runs, run = wave % runs;  // m = 0: gate rows, 1: up rows
+    const unsigned qa = run * run_quads, qe = min(quads, qa + run_quads);
+    const Packed whole = packed_shape(experts, inter, hidden), one = packed_shape(1, inter, hidden);
+    const int expert = __builtin_amdgcn_readfirstlane(s_expert);
+    const DecodeGroup wg =
+        decode_group(m ? up : gate, whole, one, size_t(expert) * one.groups + group);
+    // lane k + 32h reads term k's half h (rows past the terms read the zero bytes)
+    const unsigned row = lane % 32;
+    const uint8_t* xa = row < kXTerms ? xq + row * 64 + (lane / 32) * 32 : zero;
+    const unsigned xstep = row < kXTerms ? kXTerms * 64 : 0;
+    auto a_of = [&](unsigned q, u32x4& lo, u32x4& hi) {
+        lo = *reinterpret_cast<const u32x4*>(xa + q * xstep);
+        hi = *reinterpret_cast<const u32x4*>(xa + q * xstep + 16);
+    };
+    auto as_of = [&](unsigned q) { return unsigned(xs[2 * q + lane / 32]); };
+    f32x16 acc = {};
+    for (unsigned qb = qa; qb < qe; qb += NQ) {
+        DecodeB<NQ> b;
+        decode_load_b<NQ>(wg, lane, qb, steps, b);
+        decode_mma<NQ>(b, qb, min(4 * qe, steps), a_of, as_of, acc);
+    }
+    if (lane < 32)
+        red[wave][lane] = term_sum<kXTerms>(acc);
+    __syncthreads();
+    if (wave == 0) {
+        const unsigned i = lane % 32;
+        float g = 0.f, u = 0.f;
+        for (unsigned r = 0; r < runs; ++r)
+            g += red[r][i];
+        for (unsigned r = 0; r < runs; ++r)
+            u += red[runs + r][i];
+        store_decode_h(silu(g) * u, group, lane, hq + size_t(slot) * (inter / 64) * kHTerms * 64,
+                       hs + size_t(slot) * (inter / 32));
+    }
+}
+
+// Per wavefront of decode_down_kernel, one batch of h in LDS: 4 NQ steps of kHTerms * 64
+// code bytes, copied as whole 16-byte pieces per lane (the copy rounded up to 64 pieces),
+// then their 8 NQ block scales.
+template <int NQ> constexpr unsigned decode_stage_pieces() {
+    return (4 * NQ * kHTerms * 64 / 16 + 63) / 64;  // per lane
+}
+template <int NQ> constexpr unsigned decode_stage_bytes() {
+    return decode_stage_pieces<NQ>() * 64 * 16 + 8 * NQ;
+}
+
+template <int NQ>
+__global__ __launch_bounds__(kDecodeWaves * 64) void decode_down_kernel(
+    const uint8_t* __restrict__ hq, const uint8_t* __restrict__ hs, unsigned hidden,
+    unsigned inter, unsigned experts, unsigned top_k, const uint8_t* __restrict__ down,
+    const int32_t* __restrict__ idx, const float* __restrict__ weight, unsigned runs,
+    unsigned run_quads, float* __restrict__ y) {
+    constexpr unsigned kStage = decode_stage_bytes<NQ>();
+    constexpr unsigned kPieces = decode_stage_pieces<NQ>();  // per lane
+    constexpr unsigned kScalesAt = kPieces * 64 * 16;
+    __shared__ __align__(16) uint8_t stage[kDecodeWaves][kStage];
+    __shared__ float red[kDecodeWaves][32];
+    __shared__ __align__(16) uint8_t zero32[32];
+    // the wavefront index as a uniform value (the weight loads' offsets and resources are
+    // per wavefront)
+    const unsigned wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+    const unsigned slot = wave / runs, run = wave % runs;
+    if (threadIdx.x < 8)
+        reinterpret_cast<unsigned*>(zero32)[threadIdx.x] = 0u;
+    __syncthreads();
+    const unsigned steps = inter / 64, quads = (steps + 3) / 4;
+    const unsigned group = blockIdx.x;
+    f32x16 acc = {};
+    if (slot < top_k) {
+        const Packed whole = packed_shape(experts, hidden, inter),
+                     one = packed_shape(1, hidden, inter);
+        const int expert = __builtin_amdgcn_readfirstlane(idx[slot]);
+        const DecodeGroup wg = decode_group(down, whole, one, size_t(expert) * one.groups + group);
+        const uint8_t* h_codes = hq + size_t(slot) * steps * kHTerms * 64;  // the slot's h
+        const uint8_t* h_scales = hs + size_t(slot) * (inter / 32);
+        uint8_t* mine = stage[wave];
+        unsigned base = 0;  // the batch's first step
+        // lane k + 32h reads term k's half h (rows past the terms read the zero block)
+        const unsigned row = lane % 32;
+        const uint8_t* ha = row < kHTerms ? mine + row * 64 + (lane / 32) * 32 : zero32;
+        const unsigned hstep = row < kHTerms ? kHTerms * 64 : 0;
+        auto a_of = [&](unsigned q, u32x4& lo, u32x4& hi) {
+            const uint8_t* p = ha + (q - base) * hstep;
+            lo = *reinterpret_cast<const u32x4*>(p);
+            hi = *reinterpret_cast<const u32x4*>(p + 16);
+        };
+        auto as_of = [&](unsigned q) {
+            return unsigned(mine[kScalesAt + 2 * (q - base) + lane / 32]);
+        };
+        const unsigned qe = min(quads, (run + 1) * run_quads);
+        for (unsigned qb = run * run_quads; qb < qe; qb += NQ) {
+            base = 4 * qb;
+            // this batch's h (the steps of quads qb .., contiguous in the slot's h) first:
+            // cache hits that arrive before the weights; then every weight load of the batch
+            const size_t first = size_t(4 * qb) * kHTerms * 64, end = size_t(steps) * kHTerms * 64;
+            u32x4 piece[kPieces];
+#pragma unroll
+            for (unsigned j = 0; j < kPieces; ++j) {
+                const size_t at = first + 16 * size_t(lane + 64 * j);
+                piece[j] = load16(h_codes + min(at, end - 16));
+            }
+            const unsigned scale_at = min(8 * qb + lane, inter / 32 - 1);
+            const uint8_t scale = h_scales[scale_at];
+            DecodeB<NQ> b;
+            decode_load_b<NQ>(wg, lane, qb, steps, b);
+#pragma unroll
+            for (unsigned j = 0; j < kPieces; ++j)
+                *reinterpret_cast<u32x4*>(mine + 16 * (lane + 64 * j)) = piece[j];
+            if (lane < 8 * NQ)
+                mine[kScalesAt + lane] = scale;
+            decode_mma<NQ>(b, qb, min(4 * qe, steps), a_of, as_of, acc);
+        }
+    }
+    if (lane < 32)
+        red[wave][lane] = term_sum<kHTerms>(acc);
+    __syncthreads();
+    if (wave == 0 && lane < 32) {
+        float sum = 0.f;
+        for (unsigned i = 0; i < top_k; ++i) {
+            float d = 0.f;
+            for (unsigned r = 0; r < runs; ++r)
+                d += red[i * runs + r][lane];
+            sum += d * weight[i];
+        }
+        y[size_t(group) * 32 + lane] = sum;
+    }
+}
+
 __global__ __launch_bounds__(256) void mxfp4_dequant_kernel(const uint8_t* __restrict__ blocks,
                                                             const uint8_t* __restrict__ scales,
                                                             size_t rows, size_t cols,
@@ -1332,6 +1780,64 @@ int check_layer(const uint16_t* x_bf16, const float* logits, size_t tokens, size
     return KDQ_OK;
 }
 
+// The single-token path (decode_gate_up_kernel + decode_down_kernel) takes one token
+// whose x steps fit the gate/up kernel's LDS.
+bool single_token_path(size_t tokens, size_t hidden) {
+    return tokens == 1 && hidden / kStepK <= kDecodeMaxSteps;
+}
+
+// Runs of whole quads per wavefront: gate/up up to 8 runs per matrix (2 runs per
+// workgroup's wave pair), down up to 16 / top_k runs per slot; `quads` per run.
+struct DecodePlan {
+    unsigned gu_runs, gu_quads, dn_runs, dn_quads;
+};
+
+DecodePlan decode_plan(size_t hidden, size_t inter, size_t top_k) {
+    const unsigned qh = unsigned((hidden / kStepK + 3) / 4), qi = unsigned((inter / kStepK + 3) / 4);
+    const unsigned gq = (qh + 7) / 8, gr = (qh + gq - 1) / gq;
+    const unsigned dmax = std::max(1u, unsigned(kDecodeWaves / top_k));
+    const unsigned dq = (qi + dmax - 1) / dmax, dr = (qi + dq - 1) / dq;
+    return DecodePlan{gr, gq, dr, dq};
+}
+
+// The single-token layer: h in the term-row layout at the start of the scratch's h
+// tiles (top_k * inter / 64 steps of kHTerms * 64 bytes, then top_k * inter / 32 scale
+// bytes; the tiles hold far more).
+int launch_decode(const uint16_t* x_bf16, const float* logits, size_t hidden, size_t inter,
+                  size_t experts, size_t top_k, const uint8_t* gate, const uint8_t* up,
+                  const uint8_t* down, float* y, const MoeScratch& s, hipStream_t st) {
+    const DecodePlan p = decode_plan(hidden, inter, top_k);
+    uint8_t* hq = s.ha;
+    uint8_t* hs = s.ha + align256(top_k * (inter / kStepK) * kHTerms * 64);
+    const dim3 gu_grid(unsigned(inter / 32), unsigned(top_k));
+    const dim3 gu_block(2 * p.gu_runs * 64);
+    auto gate_up = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, gu_grid, gu_block, 0, st, x_bf16, logits, unsigned(hidden),
+                           unsigned(inter), unsigned(experts), unsigned(top_k), gate, up,
+                           p.gu_runs, p.gu_quads, s.idx, s.weight, s.offsets, s.perm, hq, hs);
+    };
+    const bool few = experts <= 64;  // one routing probability per lane
+    if (p.gu_quads == 1)
+        few ? gate_up(decode_gate_up_kernel<1, 1>) : gate_up(decode_gate_up_kernel<1, 4>);
+    else
+        few ? gate_up(decode_gate_up_kernel<2, 1>) : gate_up(decode_gate_up_kernel<2, 4>);
+    KDQ_HIP(hipGetLastError());
+    const dim3 dn_grid(unsigned(hidden / 32)), dn_block(unsigned(top_k) * p.dn_runs * 64);
+    auto down_launch = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dn_grid, dn_block, 0, st, hq, hs, unsigned(hidden),
+                           unsigned(inter), unsigned(experts), unsigned(top_k), down, s.idx,
+                           s.weight, p.dn_runs, p.dn_quads, y);
+    };
+    if (p.dn_quads == 1)
+        down_launch(decode_down_kernel<1>);
+    else if (p.dn_quads == 2)
+        down_launch(decode_down_kernel<2>);
+    else
+        down_launch(decode_down_kernel<3>);
+    KDQ_HIP(hipGetLastError());
+    return KDQ_OK;
+}
+
 // The layer over packed weights; `scratch` holds moe_scratch_bytes(...).
 int launch_layer(const uint16_t* x_bf16, const float* logits, size_t tokens, size_t hidden,
                  size_t inter, size_t experts, size_t top_k, const uint8_t* gate,
@@ -1350,6 +1856,9 @@ int launch_layer(const uint16_t* x_bf16, const float* logits, size_t tokens, siz
     const size_t slots = tokens * top_k;
     const unsigned items = unsigned(max_items(slots, experts));
     const size_t tiles = 2 * size_t(items);
+    if (single_token_path(tokens, hidden))
+        return launch_decode(x_bf16, logits, hidden, inter, experts, top_k, gate, up, down, y, s,
+                             st);
     const bool small = slots <= size_t(kPrologueSlots);
     if (small) {
         const size_t x_bytes = tokens * hidden * 2;

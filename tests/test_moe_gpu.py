@@ -144,6 +144,19 @@ def test_moe_layer_decode_shape(device, oracle):
     run_layer(device, oracle, 1, 2880, 2880, 32, 4, seed=0xC4)
 
 
+@pytest.mark.parametrize("hidden,inter,experts,top_k", [
+    (192, 320, 8, 3),     # partial quads in both products
+    (4480, 448, 16, 8),   # gate/up runs of 3 quads taken in batches of 2
+    (256, 1856, 8, 3),    # down runs of 2 quads, 4 runs per slot
+    (128, 3520, 16, 8),   # down runs of 7 quads in batches of 3, the last step partial
+    (1024, 1024, 256, 1), # the most experts, one slot
+])
+def test_moe_single_token_path(device, oracle, hidden, inter, experts, top_k):
+    """One token runs the two-launch decode (routing in every gate/up workgroup, gate/up
+    and down split into runs of whole quads over the K dimension)."""
+    run_layer(device, oracle, 1, hidden, inter, experts, top_k, seed=0x1D + hidden + top_k)
+
+
 def test_moe_layer_skewed_routing(device, oracle):
     """C5-like skew (25% of tokens favour 8 hot experts) at a size the oracle finishes."""
     run_layer(device, oracle, 64, 256, 256, 128, 4, seed=0xC5, hot=8)
@@ -291,7 +304,7 @@ def test_moe_packed_matches_reference_layout(device, tokens, hidden, inter, expe
         assert np.array_equal(a.cpu().numpy().view(np.uint8), b.cpu().numpy().view(np.uint8))
 
 
-@pytest.mark.parametrize("tokens", [3, 40])  # the one-workgroup prologue and the large path
+@pytest.mark.parametrize("tokens", [1, 3, 40])  # single-token, one-workgroup prologue, large
 @pytest.mark.parametrize("bad", [float("nan"), float("inf")])
 def test_moe_nonfinite_activation(device, tokens, bad):
     """A non-finite activation poisons its own token's outputs and nothing else: the FP8
@@ -309,11 +322,12 @@ def test_moe_nonfinite_activation(device, tokens, bad):
     clean = ops.moe_mxfp4(dev(x).view(torch.bfloat16), dev(logits), top_k, *wts).cpu().numpy()
     poisoned = x.copy()
     bits = np.array([bad], np.float32).view(np.uint32)[0] >> 16
-    poisoned[1, 37] = np.uint16(bits)
+    bad_row = min(1, tokens - 1)
+    poisoned[bad_row, 37] = np.uint16(bits)
     got = ops.moe_mxfp4(dev(poisoned).view(torch.bfloat16), dev(logits), top_k,
                         *wts).cpu().numpy()
-    assert not np.isfinite(got[1]).any()
-    others = [t for t in range(tokens) if t != 1]
+    assert not np.isfinite(got[bad_row]).any()
+    others = [t for t in range(tokens) if t != bad_row]
     assert np.array_equal(got[others], clean[others])
 
 
