@@ -956,6 +956,57 @@ __device__ __forceinline__ void store_h(float hv, unsigned r, unsigned f, uint8_
             finite ? uint8_t(e + 127) : uint8_t(255);
 }
 
+// h = silu(g) * u of the wavefront's 32 features (feature group fg; lanes i and i + 32
+// hold feature i) for every row of the item's tiles, into the down product's activation
+// tiles: kHTerms FP8 terms and one E8M0 scale per row's 32-value block (the half-wavefront
+// maximum).  The features fill one 1 KB piece of each (tile, step, term) block, so the term
+// bytes are assembled in the wavefront's 1 KB of LDS and leave as one 16-byte store per
+// lane; every row is written (rows past the item's count only reach result rows that are
+// never stored).
+template <int TILES>
+__device__ __forceinline__ void store_h_tiles(const f32x16 (&acc)[2][TILES], unsigned fg,
+                                              unsigned lane, size_t item, const Tiles& hl,
+                                              uint8_t* lds) {
+    const unsigned i32 = lane % 32, h = lane / 32;
+    const unsigned q = fg / 2, piece = fg % 2;
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) {
+        const size_t tau = 2 * item + t;
+        uint8_t* codes = hl.codes + tau * hl.code_stride + size_t(q) * kHTerms * 2048 + piece * 1024;
+        uint8_t* scales = hl.scales + tau * hl.scale_stride + (q / 4) * 256 + q % 4;
+        uint8_t term[kHTerms][16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const unsigned r = 8 * (v / 4) + 4 * h + v % 4;
+            const float hv = silu(acc[0][t][v]) * acc[1][t][v];
+            // one maximum for the block scale and its finiteness: a non-finite value
+            // counts as +inf
+            const float m = half_max(isfinite(hv) ? fabsf(hv) : INFINITY);
+            const bool finite = m != INFINITY;
+            const int e = block_exponent(m);
+            float val = finite ? __builtin_amdgcn_ldexpf(hv, -e) : 0.f;
+#pragma unroll
+            for (int k = 0; k < kHTerms; ++k) {
+                const int c = __builtin_amdgcn_cvt_pk_fp8_f32(val, 0.f, 0, false);
+                term[k][v] = finite ? uint8_t(c & 0xff) : uint8_t(0x7f);  // 0x7f: FP8 NaN
+                val -= __builtin_amdgcn_cvt_f32_fp8(c, 0);
+            }
+            if (i32 == 0)
+                scales[4 * (r + 32 * piece)] = finite ? uint8_t(e + 127) : uint8_t(255);
+        }
+#pragma unroll
+        for (int k = 0; k < kHTerms; ++k) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const unsigned r = 8 * (v / 4) + 4 * h + v % 4;
+                lds[(r + 32 * (i32 / 16)) * 16 + i32 % 16] = term[k][v];
+            }
+            *reinterpret_cast<u32x4*>(codes + k * 2048 + 16 * lane) =
+                *reinterpret_cast<const u32x4*>(lds + 16 * lane);
+        }
+    }
+}
+
 // gate/up: grid (groups of kGemmWaves feature groups of 32, items, K slices).  Wavefront w
 // multiplies gate and up rows of features 32 (kGemmWaves x + w) .. +31.  One slice:
 // h = silu(g) * u into the down product's activation tiles; more: fp32 partials of g and u
@@ -1012,17 +1063,9 @@ __global__ __launch_bounds__(kGemmWaves * 64, 3) void gate_up_kernel(
                 }
             return;
         }
-#pragma unroll
-        for (int t = 0; t < TILES; ++t) {
-            const size_t tau = 2 * size_t(blockIdx.y) + t;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int r = acc_row(t, v, h);
-                const float hv = silu(acc[0][t][v]) * acc[1][t][v];
-                store_h(hv, unsigned(r - t * kTileRows), f, hl.codes + tau * hl.code_stride,
-                        hl.scales + tau * hl.scale_stride, r < it.count);
-            }
-        }
+        // the LDS stage is free once staged_pair has returned (it ends on a barrier
+        // after the last MFMA read); each wavefront takes its own 1 KB of it
+        store_h_tiles<TILES>(acc, fg, lane, blockIdx.y, hl, stage + wave * 1024);
     };
     if (it.count <= kTileRows)
         run.template operator()<1>();
@@ -1166,10 +1209,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 //     meet in LDS and are summed in run order; h = silu(g) * u is stored as kHTerms FP8
 //     terms in the term-row layout for the down product.  Workgroup (0, 0) also writes
 //     the routing outputs.
-//   decode_down_kernel  grid (hidden / 32 row groups), top_k * runs waves: wave (i, p)
-//     multiplies slot i's h by its expert's down rows over run p of the inter dimension;
-//     per slot the runs are summed in order, then y = sum_i w_i * down_i in selection
-//     order (the general path's combine).
+//   decode_down_kernel  grid (hidden / 32 row groups, 2 halves of the slots), half_slots *
+//     runs waves: wave (i, p) multiplies slot i's h by its expert's down rows over run p
+//     of the inter dimension; per slot the runs are summed in order, then sum_i w_i *
+//     down_i over the half's slots in selection order; the two halves' sums meet by
+//     atomic addition onto y, which the gate/up kernel zeroed (two addends onto zero: the
+//     result does not depend on their order).
 //
 // Term rows: the token's activation is a sum of FP8 terms (kXTerms for x, kHTerms for h)
 // sharing one E8M0 scale per 32-value block, and row k of the MFMA's A operand carries
@@ -1351,7 +1396,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_gate_up_kernel(
     unsigned inter, unsigned experts, unsigned top_k, const uint8_t* __restrict__ gate,
     const uint8_t* __restrict__ up, unsigned runs, unsigned run_quads,
     int32_t* __restrict__ idx, float* __restrict__ weight, int32_t* __restrict__ offsets,
-    int32_t* __restrict__ perm, uint8_t* __restrict__ hq, uint8_t* __restrict__ hs) {
+    int32_t* __restrict__ perm, uint8_t* __restrict__ hq, uint8_t* __restrict__ hs,
+    float* __restrict__ y_zero) {
     // x in the term-row layout (every step), its block scales, 32 zero bytes
     __shared__ __align__(16) uint8_t xq[kDecodeMaxSteps * kXTerms * 64 + 32];
     __shared__ uint8_t xs[kDecodeMaxSteps * 2];
@@ -1363,6 +1409,11 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_gate_up_kernel(
     const unsigned steps = hidden / 64, quads = (steps + 3) / 4;
     const unsigned slot = blockIdx.y, group = blockIdx.x;
     uint8_t* zero = xq + steps * kXTerms * 64;
+    if (y_zero) {  // the output the down kernel's two halves add into
+        const unsigned wg = blockIdx.y * gridDim.x + blockIdx.x, wgs = gridDim.x * gridDim.y;
+        for (unsigned i = wg * blockDim.x + threadIdx.x; i < hidden; i += wgs * blockDim.x)
+            y_zero[i] = 0.f;
+    }
     if (wave == 0) {
         // wavefront 0 routes the token (a few hundred bytes of logits) ...
         int selected;
@@ -1450,7 +1501,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_down_kernel(
     const uint8_t* __restrict__ hq, const uint8_t* __restrict__ hs, unsigned hidden,
     unsigned inter, unsigned experts, unsigned top_k, const uint8_t* __restrict__ down,
     const int32_t* __restrict__ idx, const float* __restrict__ weight, unsigned runs,
-    unsigned run_quads, float* __restrict__ y) {
+    unsigned run_quads, unsigned half_slots, float* __restrict__ y) {
     constexpr unsigned kStage = decode_stage_bytes<NQ>();
     constexpr unsigned kPieces = decode_stage_pieces<NQ>();  // per lane
     constexpr unsigned kScalesAt = kPieces * 64 * 16;
@@ -1460,14 +1511,17 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_down_kernel(
     // the wavefront index as a uniform value (the weight loads' offsets and resources are
     // per wavefront)
     const unsigned wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
-    const unsigned slot = wave / runs, run = wave % runs;
+    // this workgroup's half of the slots: [first_slot, last_slot)
+    const unsigned first_slot = blockIdx.y * half_slots;
+    const unsigned last_slot = min(top_k, first_slot + half_slots);
+    const unsigned slot = first_slot + wave / runs, run = wave % runs;
     if (threadIdx.x < 8)
         reinterpret_cast<unsigned*>(zero32)[threadIdx.x] = 0u;
     __syncthreads();
     const unsigned steps = inter / 64, quads = (steps + 3) / 4;
     const unsigned group = blockIdx.x;
     f32x16 acc = {};
-    if (slot < top_k) {
+    if (slot < last_slot) {
         const Packed whole = packed_shape(experts, hidden, inter),
                      one = packed_shape(1, hidden, inter);
         const int expert = __builtin_amdgcn_readfirstlane(idx[slot]);
@@ -1517,13 +1571,18 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_down_kernel(
     __syncthreads();
     if (wave == 0 && lane < 32) {
         float sum = 0.f;
-        for (unsigned i = 0; i < top_k; ++i) {
+        for (unsigned i = first_slot; i < last_slot; ++i) {
             float d = 0.f;
             for (unsigned r = 0; r < runs; ++r)
-                d += red[i * runs + r][lane];
+                d += red[(i - first_slot) * runs + r][lane];
             sum += d * weight[i];
         }
-        y[size_t(group) * 32 + lane] = sum;
+        // two halves meet by atomic addition onto the zeroed output: 0 + a + b is the same
+        // float whichever half arrives first
+        if (gridDim.y == 1)
+            y[size_t(group) * 32 + lane] = sum;
+        else if (first_slot < last_slot)
+            atomicAdd(y + size_t(group) * 32 + lane, sum);
     }
 }
 
@@ -1786,8 +1845,9 @@ bool single_token_path(size_t tokens, size_t hidden) {
     return tokens == 1 && hidden / kStepK <= kDecodeMaxSteps;
 }
 
-// Runs of whole quads per wavefront: gate/up up to 8 runs per matrix (2 runs per
-// workgroup's wave pair), down up to 16 / top_k runs per slot; `quads` per run.
+// Runs of whole quads per wavefront: gate/up up to 8 runs per matrix, down up to
+// 16 / ceil(top_k / 2) runs per slot (a down workgroup takes half the slots); `quads` per
+// run.
 struct DecodePlan {
     unsigned gu_runs, gu_quads, dn_runs, dn_quads;
 };
@@ -1795,7 +1855,8 @@ struct DecodePlan {
 DecodePlan decode_plan(size_t hidden, size_t inter, size_t top_k) {
     const unsigned qh = unsigned((hidden / kStepK + 3) / 4), qi = unsigned((inter / kStepK + 3) / 4);
     const unsigned gq = (qh + 7) / 8, gr = (qh + gq - 1) / gq;
-    const unsigned dmax = std::max(1u, unsigned(kDecodeWaves / top_k));
+    const unsigned half = unsigned((top_k + 1) / 2);  // slots per down workgroup
+    const unsigned dmax = std::max(1u, unsigned(kDecodeWaves / half));
     const unsigned dq = (qi + dmax - 1) / dmax, dr = (qi + dq - 1) / dq;
     return DecodePlan{gr, gq, dr, dq};
 }
@@ -1807,6 +1868,7 @@ int launch_decode(const uint16_t* x_bf16, const float* logits, size_t hidden, si
                   size_t experts, size_t top_k, const uint8_t* gate, const uint8_t* up,
                   const uint8_t* down, float* y, const MoeScratch& s, hipStream_t st) {
     const DecodePlan p = decode_plan(hidden, inter, top_k);
+    const unsigned half = unsigned((top_k + 1) / 2), halves = top_k > 1 ? 2u : 1u;
     uint8_t* hq = s.ha;
     uint8_t* hs = s.ha + align256(top_k * (inter / kStepK) * kHTerms * 64);
     const dim3 gu_grid(unsigned(inter / 32), unsigned(top_k));
@@ -1814,7 +1876,8 @@ int launch_decode(const uint16_t* x_bf16, const float* logits, size_t hidden, si
     auto gate_up = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, gu_grid, gu_block, 0, st, x_bf16, logits, unsigned(hidden),
                            unsigned(inter), unsigned(experts), unsigned(top_k), gate, up,
-                           p.gu_runs, p.gu_quads, s.idx, s.weight, s.offsets, s.perm, hq, hs);
+                           p.gu_runs, p.gu_quads, s.idx, s.weight, s.offsets, s.perm, hq, hs,
+                           halves > 1 ? y : nullptr);
     };
     const bool few = experts <= 64;  // one routing probability per lane
     if (p.gu_quads == 1)
@@ -1822,11 +1885,11 @@ int launch_decode(const uint16_t* x_bf16, const float* logits, size_t hidden, si
     else
         few ? gate_up(decode_gate_up_kernel<2, 1>) : gate_up(decode_gate_up_kernel<2, 4>);
     KDQ_HIP(hipGetLastError());
-    const dim3 dn_grid(unsigned(hidden / 32)), dn_block(unsigned(top_k) * p.dn_runs * 64);
+    const dim3 dn_grid(unsigned(hidden / 32), halves), dn_block(half * p.dn_runs * 64);
     auto down_launch = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, dn_grid, dn_block, 0, st, hq, hs, unsigned(hidden),
                            unsigned(inter), unsigned(experts), unsigned(top_k), down, s.idx,
-                           s.weight, p.dn_runs, p.dn_quads, y);
+                           s.weight, p.dn_runs, p.dn_quads, half, y);
     };
     if (p.dn_quads == 1)
         down_launch(decode_down_kernel<1>);
