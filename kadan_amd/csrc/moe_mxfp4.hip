@@ -235,6 +235,8 @@ __device__ __forceinline__ void route_select(const float* __restrict__ logits, u
                                              int& selected, float& selected_weight) {
     if (experts <= 64)
         route_select_r<1>(logits, t, experts, top_k, lane, selected, selected_weight);
+    else if (experts <= 128)
+        route_select_r<2>(logits, t, experts, top_k, lane, selected, selected_weight);
     else
         route_select_r<4>(logits, t, experts, top_k, lane, selected, selected_weight);
 }
@@ -285,24 +287,51 @@ __device__ __forceinline__ void permute_slots(const int32_t* __restrict__ idx, u
     for (unsigned s = tid; s < slots; s += 1024)
         atomicAdd(&counts[idx[s]], 1);
     __syncthreads();
-    if (tid == 0) {
-        int acc = 0, n = 0;
-        for (unsigned e = 0; e < experts; ++e) {
-            offsets[e] = acc;
-            base[e] = acc;
-            segment[e] = acc;
-            item_base[e] = n;
-            for (int r = 0; r < counts[e]; r += kItemRows) {
-                items[2 * n] = int(e);
-                items[2 * n + 1] = r;
-                ++n;
-            }
-            acc += counts[e];
+    if (wave == 0) {
+        // exclusive prefix sums over the experts of their slots and of their work items
+        // (ceil(count / kItemRows) each): lane l takes experts 4l .. 4l + 3
+        int c[4], n[4], slot_sum = 0, item_sum = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const unsigned e = 4 * lane + j;
+            c[j] = e < experts ? counts[e] : 0;
+            n[j] = (c[j] + kItemRows - 1) / kItemRows;
+            slot_sum += c[j];
+            item_sum += n[j];
         }
-        offsets[experts] = acc;
-        *item_count = n;
+        int slot_scan = slot_sum, item_scan = item_sum;  // inclusive over the lanes
+#pragma unroll
+        for (int d = 1; d < 64; d *= 2) {
+            const int a = __shfl_up(slot_scan, d, 64), b = __shfl_up(item_scan, d, 64);
+            if (lane >= unsigned(d)) {
+                slot_scan += a;
+                item_scan += b;
+            }
+        }
+        int acc = slot_scan - slot_sum, nb = item_scan - item_sum;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const unsigned e = 4 * lane + j;
+            if (e < experts) {
+                offsets[e] = acc;
+                base[e] = acc;
+                segment[e] = acc;
+                item_base[e] = nb;
+            }
+            acc += c[j];
+            nb += n[j];
+        }
+        if (lane == 63) {
+            offsets[experts] = slot_scan;
+            *item_count = item_scan;
+        }
     }
     __syncthreads();
+    for (unsigned e = tid; e < experts; e += 1024)  // each expert's work items
+        for (int r = 0, n = item_base[e]; r < counts[e]; r += kItemRows, ++n) {
+            items[2 * n] = int(e);
+            items[2 * n + 1] = r;
+        }
     const unsigned long long below = (1ull << lane) - 1ull;
     for (unsigned first = 0; first < slots; first += 1024) {
         for (unsigned i = tid; i < 16 * kMaxExperts; i += 1024)
@@ -599,8 +628,8 @@ __device__ __forceinline__ void gather_block(const uint16_t* __restrict__ x, uns
 }
 
 // x gathered by the permutation into gate/up's activation tiles as kXTerms FP8 terms:
-// grid (row-blocks / 256, tiles); thread `id` of tile tau takes tile row id / blocks,
-// 32-value block id % blocks.  Rows past an item's count and absent tiles are not written:
+// grid (row-blocks / 256, tiles); thread `id` of tile tau takes tile row id % 32,
+// 32-value block id / 32.  Rows past an item's count and absent tiles are not written:
 // a row of an MFMA's A operand only reaches the same row of its result, which is not stored.
 __global__ __launch_bounds__(256) void gather_kernel(const uint16_t* __restrict__ x,
                                                      unsigned hidden, unsigned top_k,
@@ -614,11 +643,13 @@ __global__ __launch_bounds__(256) void gather_kernel(const uint16_t* __restrict_
     if (id >= 32 * blocks || int(item) >= *item_count)
         return;
     const Item it = load_item(items, offsets, item);
-    const int row = int(32 * t + id / blocks);
+    // rows fastest: a wavefront's lanes take 32 rows of two blocks, so each term's stores
+    // fill 512 contiguous bytes of the tile layout (lane r + 32h holds row r)
+    const int row = int(32 * t + id % 32);
     if (row >= it.count)
         return;
     const size_t token = size_t(perm[it.segment + it.first + row] / int(top_k));
-    gather_block(x, hidden, token, xa, tiles, tau, id / blocks % 32, id % blocks);
+    gather_block(x, hidden, token, xa, tiles, tau, id % 32, id / 32);
 }
 
 // Small layers (decode, at most kPrologueSlots slots): routing, permutation and gather in
