@@ -1678,15 +1678,18 @@ MoeSlices moe_slices(size_t tokens, size_t hidden, size_t inter, size_t experts,
     const size_t items = std::min(tokens * top_k, experts);  // at least this many
     // workgroups for about two gate/up (four waves) or one down (eight waves) per compute
     // unit
-    auto slices = [&](size_t columns, size_t steps, size_t per_cu) {
+    auto slices = [&](size_t columns, size_t steps, size_t per_cu, bool round_up) {
         const size_t target = per_cu * size_t(compute_units());
-        size_t ks = std::max<size_t>(1, (target + columns * items - 1) / (columns * items));
-        ks = std::min(ks, steps);
+        size_t ks = round_up ? (target + columns * items - 1) / (columns * items)
+                             : target / (columns * items);
+        ks = std::min(std::max<size_t>(ks, 1), steps);
         const size_t per = ((steps + ks - 1) / ks + 7) / 8 * 8;
         return unsigned((steps + per - 1) / per);
     };
-    return MoeSlices{slices(gate_up_columns(inter), hidden / kStepK, 2),
-                     slices(down_columns(hidden), inter / kStepK, 1)};
+    // down rounds down: its workgroups (one per compute unit at its register count) then
+    // run in one round rather than one and a part (C4 T=256: 1 slice, 192 workgroups)
+    return MoeSlices{slices(gate_up_columns(inter), hidden / kStepK, 2, true),
+                     slices(down_columns(hidden), inter / kStepK, 1, false)};
 }
 
 size_t align256(size_t n) {
