@@ -389,8 +389,12 @@ __device__ __forceinline__ float e8m0(unsigned s) {
     return __uint_as_float(s << 23);  // exponent field only: the converter reads 2^(s-127)
 }
 
+// silu(x) = x / (1 + e^-x) from the hardware exponential and reciprocal (each within an
+// ulp or two): h leaves as FP8 terms good to about 12 bits, so the epilogue's cost, not
+// the last bits of silu, is what matters; infinities and NaN come out as in the
+// reference's x / (1 + expf(-x)).
 __device__ __forceinline__ float silu(float x) {
-    return x / (1.0f + expf(-x));
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504088896341f));
 }
 
 __device__ __forceinline__ uint16_t bf16_rne(float x) {
