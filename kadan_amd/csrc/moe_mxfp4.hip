@@ -956,13 +956,17 @@ __device__ __forceinline__ int acc_row(int t, int v, unsigned h) {
     return t * kTileRows + 8 * (v / 4) + 4 * int(h) + (v % 4);
 }
 
-// Maximum over the 32 lanes of this lane's half of the wavefront.
+// Maximum over the 32 lanes of this lane's half of the wavefront (all 64 lanes active):
+// the row of 16 by DPP, then rows 0/1 and 2/3 by gfx950's row swap (v_permlane16_swap:
+// each lane ends with its own row's value and its partner row's, in some order).
 __device__ __forceinline__ float half_max(float v) {
     v = fmaxf(v, dpp_read<0xb1, 0xf>(v));   // quad_perm [1,0,3,2]
     v = fmaxf(v, dpp_read<0x4e, 0xf>(v));   // quad_perm [2,3,0,1]
     v = fmaxf(v, dpp_read<0x141, 0xf>(v));  // row_half_mirror
     v = fmaxf(v, dpp_read<0x140, 0xf>(v));  // row_mirror: the row of 16's maximum
-    return fmaxf(v, __shfl_xor(v, 16, 64));
+    const auto pair = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                       false, false);
+    return fmaxf(__uint_as_float(pair[0]), __uint_as_float(pair[1]));
 }
 
 // h for row r (0..31) of an activation tile of the down product, feature f, held with the
