@@ -300,9 +300,13 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
     // (slots padded per expert to whole items), plus x in position order, the slot and
     // position maps, the items' experts and the count of positions in use
     // (grouped on the GEMM: token tiles of kTileRows, the packed expert stacks, fp16 x)
-    const bool gemm_gu = grouped && gemm_stack(L.gate_exps, F, H) &&
+    // the grouped GEMM pads every expert's rows to 128-row token tiles: it pays once the
+    // experts average 16 rows or more; fewer (a 64-token chunk spreads 512 slots over 128
+    // experts) run as 8-row GEMV items, which read each expert's weights about once
+    const bool dense = slots >= 16 * E;
+    const bool gemm_gu = grouped && dense && gemm_stack(L.gate_exps, F, H) &&
                          gemm_stack(L.up_exps, F, H);
-    const bool gemm_dn = grouped && gemm_stack(L.down_exps, H, F);
+    const bool gemm_dn = grouped && dense && gemm_stack(L.down_exps, H, F);
     const size_t pad = gemm_gu || gemm_dn ? kTileRows : kItemRows;
     const size_t positions = grouped ? (slots + (pad - 1) * E + pad - 1) / pad * pad : slots;
     const size_t items = positions / kItemRows;
