@@ -16,12 +16,13 @@
 //   stage_kernel<ENC>  one workgroup per token row: the row's power-of-two scale, and the
 //                      row as fp16 in the order the weight lanes consume each 256-value
 //                      group (the permutation depends on the format's packed lane image)
-//   gemm_kernel<ENC>   128 tokens x 256 weight rows per workgroup, 4 wavefronts each
-//                      owning two 32-row weight operands and all 128 tokens; weights go
-//                      from HBM straight into operand registers (16-byte loads of the
-//                      packed lane images, issued one group ahead) and are dequantised
-//                      there; activations are staged into swizzled LDS by global->LDS
-//                      DMA; the fp32 output tile leaves through LDS as whole rows.
+//   gemm_kernel<ENC, W> 128 tokens x 256 weight rows per workgroup, W = 4 wavefronts
+//                      each owning two 32-row weight operands (W = 8: one) and all 128
+//                      tokens; weights go from HBM straight into operand registers
+//                      (16-byte loads of the packed lane images, issued one group
+//                      ahead) and are dequantised there; activations are staged into
+//                      swizzled LDS by global->LDS DMA; the fp32 output tile leaves
+//                      through LDS as whole rows.
 #include "kdq_common.hpp"
 
 #include <algorithm>
@@ -378,8 +379,8 @@ __global__ __launch_bounds__(256) void stage_kernel(const float* __restrict__ x,
 // Grouped (MoE) form, `tile_expert` given: token tile t multiplies the weights of expert
 // tile_expert[t] of a stack of packed experts `expert_bytes` apart; tiles whose entry is
 // negative are skipped (the whole workgroup returns before any barrier).
-template <int ENC>
-__global__ __launch_bounds__(256, 1) void gemm_kernel(const uint16_t* __restrict__ xs,
+template <int ENC, int W>
+__global__ __launch_bounds__(W * 64, 1) void gemm_kernel(const uint16_t* __restrict__ xs,
                                                       const float* __restrict__ sigma,
                                                       const uint8_t* __restrict__ w,
                                                       unsigned m, unsigned n, unsigned k,
@@ -392,7 +393,9 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const uint16_t* __restrict
     using F = GemmFormat<ENC>;
     using Regs = typename F::Regs;
     extern __shared__ __align__(16) uint8_t lds[];
-    constexpr int DMAS = PM / kDmaRows / 4;  // DMA instructions per wavefront per group
+    // W wavefronts of NBW 32-row operands each (8 operands, 256 rows, per workgroup)
+    constexpr int NBW = 8 / W;
+    constexpr int DMAS = PM / kDmaRows / W;  // DMA instructions per wavefront per group
 
     const unsigned groups = k / 256, wtiles = (n + 15) / 16;
     const unsigned m_tiles = (m + PM - 1) / PM, n_tiles = (wtiles + kTiles - 1) / kTiles;
@@ -422,10 +425,10 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const uint16_t* __restrict
 
     // operand c = tiles tile0 + 2c (rows 0-15) and tile0 + 2c + 1 (rows 16-31); tiles
     // past the end load the last tile, and their results are never stored
-    const unsigned tile0 = (n_tile * 4 + wave) * 2 * NB;
-    const uint8_t* base[NB];
+    const unsigned tile0 = n_tile * kTiles + wave * 2 * NBW;
+    const uint8_t* base[NBW];
 #pragma unroll
-    for (int c = 0; c < NB; ++c)
+    for (int c = 0; c < NBW; ++c)
         base[c] = w + size_t(min(tile0 + 2 * c + r / 16, wtiles - 1)) * groups * F::unit +
                   16 * (16 * h + r % 16);
     auto load_weight = [&](unsigned g, Regs* rg, int i) {
@@ -448,7 +451,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const uint16_t* __restrict
             (global_void*)(xtile + size_t(g) * 512 + (J / 8) * (16 * row_pitch) + xlane[J % 8]),
             (lds_void*)(lds + buf * kStageBytes + J * 1024), 16, 0, 0);
     };
-    constexpr int kLoads = DMAS + F::loads * NB, kPerStep = 4;
+    constexpr int kLoads = DMAS + F::loads * NBW, kPerStep = 4;
     static_assert(kLoads <= 16 * kPerStep, "the loads must fit the group's sub-steps");
     auto issue = [&](int s, unsigned g, unsigned buf, Regs* rg) {
 #pragma unroll
@@ -469,9 +472,9 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const uint16_t* __restrict
         }
     };
 
-    f32x16 acc[NB][4];
+    f32x16 acc[NBW][4];
 #pragma unroll
-    for (int c = 0; c < NB; ++c)
+    for (int c = 0; c < NBW; ++c)
 #pragma unroll
         for (int b = 0; b < 4; ++b)
             acc[c][b] = f32x16{};
@@ -479,7 +482,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const uint16_t* __restrict
     unsigned flags = 0;
     unsigned magic = 0x64006400u;  // kept in a VGPR: the mask-and-or takes one SGPR only
     asm volatile("" : "+v"(magic));
-    // 16 sub-steps per group, software-pipelined by one sub-step: while the 4 * NB MFMAs
+    // 16 sub-steps per group, software-pipelined by one sub-step: while the 4 * NBW MFMAs
     // of sub-step s run, the activation operands of s + 1 are read from LDS and its
     // weights dequantised; one MFMA, then up to four VALU ops / one LDS read / one load.
     auto compute = [&](unsigned buf, const Regs* rg, unsigned next_g, unsigned next_buf,
@@ -492,14 +495,14 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const uint16_t* __restrict
                 xf[b] = *reinterpret_cast<const f16x8*>(a + b * 32 * kStageRow +
                                                          16 * (q ^ (r % 16)));
         };
-        Scales<ENC> sc[NB];
+        Scales<ENC> sc[NBW];
 #pragma unroll
-        for (int c = 0; c < NB; ++c)
+        for (int c = 0; c < NBW; ++c)
             sc[c].prepare(rg[c], ENC == KDQ_Q6_K ? r : h, flags);
-        f16x8 xf[2][4], wf[2][NB];
+        f16x8 xf[2][4], wf[2][NBW];
         read_x(0, xf[0]);
 #pragma unroll
-        for (int c = 0; c < NB; ++c)
+        for (int c = 0; c < NBW; ++c)
             wf[0][c] = dequant<ENC>(rg[c], sc[c], 0, magic);
 #pragma unroll
         for (int s = 0; s < 16; ++s) {
@@ -508,19 +511,22 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const uint16_t* __restrict
             if (s + 1 < 16) {
                 read_x(s + 1, xf[(s + 1) % 2]);
 #pragma unroll
-                for (int c = 0; c < NB; ++c)
+                for (int c = 0; c < NBW; ++c)
                     wf[(s + 1) % 2][c] = dequant<ENC>(rg[c], sc[c], s + 1, magic);
             }
 #pragma unroll
-            for (int c = 0; c < NB; ++c)
+            for (int c = 0; c < NBW; ++c)
 #pragma unroll
-                for (int b = 0; b < 4; ++b)
+                for (int b = 0; b < 4; ++b) {
                     acc[c][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[s % 2][c], xf[s % 2][b],
                                                                        acc[c][b], 0, 0, 0);
+                    if constexpr (NBW == 1)  // the MFMAs stay in their sub-step (else the
+                        asm volatile("" : "+v"(acc[c][b]));  // compiler sinks them all)
+                }
 #pragma unroll
-            for (int q = 0; q < 4 * NB; ++q) {
+            for (int q = 0; q < 4 * NBW; ++q) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // up to four VALU
+                __builtin_amdgcn_sched_group_barrier(0x002, 8 / NBW, 0);  // 4 or 8 VALU
                 if (q < 4)
                     __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
                 if (q < kPerStep)
@@ -532,7 +538,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const uint16_t* __restrict
     // Ping-pong over group pairs: group g in buffer 0 / registers ra, g + 1 in buffer 1 /
     // rb; each compute issues the other buffer's loads.  After the last pair the prefetch
     // reloads the last group (consumed only when the group count is odd).
-    Regs ra[NB], rb[NB];
+    Regs ra[NBW], rb[NBW];
     const unsigned last = g_end - 1;
     issue_all(g_begin, 0, ra);
     unsigned g = g_begin;
@@ -562,12 +568,12 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const uint16_t* __restrict
     }
     __syncthreads();  // every wavefront is done reading the activation stages
 #pragma unroll
-    for (int c = 0; c < NB; ++c)
+    for (int c = 0; c < NBW; ++c)
 #pragma unroll
         for (int b = 0; b < 4; ++b)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const unsigned row = (wave * NB + c) * 32 + 8 * q + 4 * h;
+                const unsigned row = (wave * NBW + c) * 32 + 8 * q + 4 * h;
                 *reinterpret_cast<float4*>(lds + (32 * b + r) * kOutPitch + 4 * row) =
                     make_float4(acc[c][b][4 * q] * sig[b], acc[c][b][4 * q + 1] * sig[b],
                                 acc[c][b][4 * q + 2] * sig[b], acc[c][b][4 * q + 3] * sig[b]);
@@ -575,7 +581,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const uint16_t* __restrict
     __syncthreads();
     const unsigned f0 = n_tile * kTiles * 16;       // first weight row of the tile
     constexpr int kChunks = kTiles * 16 * 4 / 16;  // 16-byte chunks per token row
-    for (unsigned e = threadIdx.x; e < PM * kChunks; e += 256) {
+    for (unsigned e = threadIdx.x; e < PM * kChunks; e += W * 64) {
         const unsigned t = e / kChunks, ch = e % kChunks, tok = m0 + t, f = f0 + 4 * ch;
         if (tok >= m || f >= n)
             continue;
@@ -636,13 +642,18 @@ unsigned gemm_slice_depth(size_t m, size_t n, size_t k) {
     return unsigned((groups + ks - 1) / ks);
 }
 
+// Wavefronts per GEMM workgroup: 8 with one 32-row operand each where two operands per
+// wavefront do not fit the registers (Q6_K spilled 240 bytes per lane: 4096->14336 at 512
+// tokens 125 -> 83 us with 8), else 4 (Q4_K and Q8_0 measured 2-4 % slower with 8).
+template <int ENC> constexpr int gemm_waves = ENC == KDQ_Q6_K ? 8 : 4;
+
 template <int ENC>
 int configure() {
     static bool configured = false;  // one attribute call per instantiation
     if (!configured) {
         KDQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&stage_kernel<ENC>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024));
-        KDQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<ENC>),
+        KDQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<ENC, gemm_waves<ENC>>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(kLds)));
         configured = true;
     }
@@ -663,7 +674,7 @@ int launch_grouped(const void* packed, size_t expert_bytes, const int32_t* tile_
     const size_t wtiles = (n + 15) / 16;
     const size_t tiles = (positions / PM) * ((wtiles + kTiles - 1) / kTiles);
     const unsigned grid = unsigned((tiles + 7) / 8 * 8);
-    hipLaunchKernelGGL(gemm_kernel<ENC>, dim3(grid), dim3(256), kLds, st, xs, sigma,
+    hipLaunchKernelGGL((gemm_kernel<ENC, gemm_waves<ENC>>), dim3(grid), dim3(gemm_waves<ENC> * 64), kLds, st, xs, sigma,
                        static_cast<const uint8_t*>(packed), unsigned(positions), unsigned(n),
                        unsigned(k), 1u, unsigned(k / 256), y, nullptr, status, tile_expert,
                        expert_bytes);
@@ -695,7 +706,7 @@ int launch_gemm(const float* x, const uint8_t* packed, size_t m, size_t n, size_
     const size_t wtiles = (n + 15) / 16;
     const size_t tiles = (m_pad / PM) * ((wtiles + kTiles - 1) / kTiles) * slices;
     const unsigned grid = unsigned((tiles + 7) / 8 * 8);
-    hipLaunchKernelGGL(gemm_kernel<ENC>, dim3(grid), dim3(256), kLds, st, xs, sigma, packed,
+    hipLaunchKernelGGL((gemm_kernel<ENC, gemm_waves<ENC>>), dim3(grid), dim3(gemm_waves<ENC> * 64), kLds, st, xs, sigma, packed,
                        unsigned(m), unsigned(n), unsigned(k), slices, per, y, part, status,
                        nullptr, size_t(0));
     KDQ_HIP(hipGetLastError());
