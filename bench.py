@@ -509,14 +509,15 @@ def bench_moe_gguf(torch, rows, reps=10, count=64):
     nbytes = per_call * expert + shared + E * H * 4 + H * 4 + 2 * rows * H * 4
     gbs = nbytes / (ms * 1e-3) / 1e9
     path = ("every slot's expert GEMV" if rows <= 8 else
-            "slots grouped by expert into 8-row items")
+            "slots grouped by expert into 8-row items" if rows * 8 < 16 * 128 else
+            "slots grouped by expert into 128-row tiles of the prefill GEMM")
     return {"workload": f"GGUF MoE layer (Qwen3-30B-A3B geometry) rows={rows} ({path})",
             "ms": round(ms, 4), "experts_touched_per_call": round(float(per_call), 1),
             "algorithmic_bytes": int(nbytes), "gbs": round(gbs, 1),
             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
             "note": "one kdq_moe_gguf submission: router + shared GEMV batch, device routing, "
-                    "device-indexed expert GEMVs (MFMA for Q4_K / Q8_0, exact for Q6_K), "
-                    "combine; bytes = touched experts + shared expert + router + x + y"}
+                    "device-indexed expert GEMVs or grouped GEMMs (MFMA for Q4_K / Q8_0 / "
+                    "Q6_K), combine; bytes = touched experts + shared expert + router + x + y"}
 
 
 def moe_bytes(tokens, hidden, inter, experts_touched):
@@ -581,9 +582,13 @@ def bench_moe(torch, tokens, experts, hot, seed, copies, reps=10, count=10, inpu
             "fp4_mfma_frac": round(tflops / FP4_PEAK_TFLOPS, 5),
             "bf16_mfma_frac": round(tflops / FP16_PEAK_TFLOPS, 4),
             "note": "resident weights in the packed layout (packed once, outside the timed "
-                    "region); grouped GEMMs on the scaled MFMA v_mfma_scale_f32_32x32x64_f8f6f4 "
+                    "region); products on the scaled MFMA v_mfma_scale_f32_32x32x64_f8f6f4 "
                     "(FP4 E2M1 weights with their E8M0 scales as they lie, activations as FP8 "
-                    "E4M3 terms with E8M0 block scales: 2 terms for x, 3 for h)"}
+                    "E4M3 terms with E8M0 block scales: 2 terms for x, 3 for h); "
+                    + ("one token: the two-launch single-token path (routing in the gate/up "
+                       "workgroups, the terms as MFMA rows, the combine in the down kernel)"
+                       if tokens == 1 else
+                       "route, permute, gather, grouped gate/up and down GEMMs, combine")}
 
 
 def _route_host(logits, top_k):
