@@ -1415,11 +1415,16 @@ struct MfmaJobs {
 // data and their results discarded), so waits count exactly.  Order: this thread's first
 // activation unit, the first units' packed weights, then the staging.
 //
-// PLAIN launches (no device-side expert index, no affine batch, no pairing: every decode
-// product of kdq_gemv / kdq_gemv_batch) take job blockIdx.y as it stands; the MoE forms
-// carry those fields (measured: the plain C2 launch 8.29 -> 7.77 us without them).
-template <int ENC, int R, int W, bool PACKED, bool PLAIN>
+// FORM 0 is the general kernel.  PLAIN launches (FORM 1 and 2: no device-side expert
+// index, no affine batch, no pairing: every decode product of kdq_gemv / kdq_gemv_batch)
+// take job blockIdx.y as it stands; the MoE forms carry those fields (measured: the plain
+// C2 launch 8.29 -> 7.77 us without them).  FORM 2, for inputs of more than 8 values a
+// thread, requests a thread's second activation unit together with its first, before the
+// weights (C2 down 14336 -> 4096: 9.54 -> 9.29 us; the same test in FORM 1's code made
+// the one-unit launches 0.1-0.3 us slower, hence a form of its own).
+template <int ENC, int R, int W, bool PACKED, int FORM>
 __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
+    constexpr bool PLAIN = FORM > 0, X2 = FORM == 2;
     const bool affine = !PLAIN && jobs.affine;
     const unsigned jid = affine ? 0 : blockIdx.y, step = affine ? blockIdx.y : 0;
     const MfmaJob& jb = jobs.job[jid];
@@ -1505,8 +1510,10 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
     };
 
     const unsigned units_x = R * in / 8;
-    XUnit first_unit;
+    XUnit first_unit, second_unit;
     load_unit(x, in, min(unsigned(threadIdx.x), units_x - 1), first_unit);
+    if constexpr (X2)
+        load_unit(x, in, min(unsigned(threadIdx.x) + kThreads, units_x - 1), second_unit);
     // the lattice grid entries this thread converts, requested before the weights (the
     // staging waits for them)
     unsigned entry[lattice(ENC) ? lattice_per_thread<ENC, kThreads> : 1];
@@ -1525,7 +1532,9 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
         lattice_table<ENC, kThreads>(table, entry);
     if (threadIdx.x < units_x)
         mstage_unit<ENC>(in, threadIdx.x, first_unit, atab, blocks);
-    for (unsigned u = threadIdx.x + kThreads; u < units_x; u += kThreads) {
+    if (X2 && threadIdx.x + kThreads < units_x)
+        mstage_unit<ENC>(in, threadIdx.x + kThreads, second_unit, atab, blocks);
+    for (unsigned u = threadIdx.x + (X2 ? 2 : 1) * kThreads; u < units_x; u += kThreads) {
         XUnit more;
         load_unit(x, in, u, more);
         mstage_unit<ENC>(in, u, more, atab, blocks);
@@ -1785,30 +1794,35 @@ void number_workgroups(MfmaJobs& jobs, unsigned rows_per_wg) {
         jobs.columns = std::max(jobs.columns, (jobs.job[k].out + rows_per_wg - 1) / rows_per_wg);
 }
 
-template <int ENC, int R, int W, bool PACKED, bool PLAIN>
+template <int ENC, int R, int W, bool PACKED, int FORM>
 int launch_mfma_form(const MfmaJobs& jobs, hipStream_t stream) {
     static bool configured = false;  // one attribute call per instantiation
     if (!configured) {
         KDQ_HIP(hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&mfma_gemv<ENC, R, W, PACKED, PLAIN>),
+            reinterpret_cast<const void*>(&mfma_gemv<ENC, R, W, PACKED, FORM>),
             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
         configured = true;
     }
-    hipLaunchKernelGGL((mfma_gemv<ENC, R, W, PACKED, PLAIN>), dim3(jobs.columns, jobs.count),
+    hipLaunchKernelGGL((mfma_gemv<ENC, R, W, PACKED, FORM>), dim3(jobs.columns, jobs.count),
                        dim3(W * 64), mfma_lds(R, jobs.in, jobs.mats == 2 ? 2 : 1, mfma_table_bytes(ENC)),
                        stream, jobs);
     KDQ_HIP(hipGetLastError());
     return KDQ_OK;
 }
 
-// Plain launches (no job with a device index, not affine, not paired) run the lean form.
+// Plain launches (no job with a device index, not affine, not paired) run the lean form,
+// and with 16 wavefronts and more than 8 input values a thread its two-unit staging.
 template <int ENC, int R, int W, bool PACKED>
 int launch_mfma_shape(const MfmaJobs& jobs, hipStream_t stream) {
     bool plain = !jobs.affine && jobs.mats != 2;
     for (unsigned k = 0; plain && k < jobs.count; ++k)
         plain = jobs.job[k].index == nullptr;
-    return plain ? launch_mfma_form<ENC, R, W, PACKED, true>(jobs, stream)
-                 : launch_mfma_form<ENC, R, W, PACKED, false>(jobs, stream);
+    if (!plain)
+        return launch_mfma_form<ENC, R, W, PACKED, 0>(jobs, stream);
+    if constexpr (W == 16)
+        if (size_t(R) * jobs.in / 8 > size_t(W) * 64)
+            return launch_mfma_form<ENC, R, W, PACKED, 2>(jobs, stream);
+    return launch_mfma_form<ENC, R, W, PACKED, 1>(jobs, stream);
 }
 
 template <int ENC, int R, bool PACKED>
