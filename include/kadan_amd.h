@@ -238,6 +238,41 @@ typedef struct kdq_moe_gguf_layer {
 int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, size_t rows, float* y,
                  int32_t* selected, float* weights, unsigned* status, void* stream);
 
+/* Tile-packed copies of a GGUF MoE layer's matrices that a caller keeps resident (a
+ * weight bank): each non-null pointer replaces the packing kdq_moe_gguf does in every
+ * prefill call for that matrix.  Expert stacks are packed as one matrix of experts x rows
+ * rows: kdq_gguf_pack(encoding, weights, row_bytes, in, experts * rows, out) (gate/up:
+ * in = hidden, rows = ff; down: in = ff, rows = hidden); shared matrices as themselves.
+ * Only the encodings the prefill GEMM takes (Q4_K, Q8_0, Q6_K) are read packed. */
+typedef struct kdq_moe_gguf_packed_stacks {
+    const void* gate_exps;
+    const void* up_exps;
+    const void* down_exps;
+    const void* gate_shexp;
+    const void* up_shexp;
+    const void* down_shexp;
+    /* 1 when kdq_gguf_gemm_check found no flag in any matrix given here: the layer then
+     * never waits on the host for the prefill GEMM's range flag (see kdq_moe_gguf) */
+    unsigned checked;
+} kdq_moe_gguf_packed_stacks;
+
+/* kdq_moe_gguf with resident packed copies (`packed` may be null: kdq_moe_gguf).  No
+ * counterpart in the reference, whose layer reads every expert through DenseCompute
+ * batch jobs (IW/include/kadan/dense_compute.hpp:197-201); the row-major tensors of
+ * `layer` stay required (decode batches and the exact fallback read them) and must hold
+ * the same weights as the packed copies.  Same results as kdq_moe_gguf. */
+/* The prefill GEMM's scale checks over a tile-packed matrix (n rows of k inputs), once,
+ * without the product: *flags (device memory) |= 1 for a non-finite scale, |= 2 when a
+ * dequantised weight could pass the fp16 range (the GEMM would then refuse the matrix
+ * and its callers take the exact-decode products).  Q4_K, Q8_0, Q6_K.  No counterpart in
+ * the reference (it decodes to fp32); for callers that keep packed copies resident. */
+int kdq_gguf_gemm_check(int encoding, const void* packed, size_t n, size_t k, unsigned* flags,
+                        void* stream);
+
+int kdq_moe_gguf_packed(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* packed,
+                        const float* x, size_t rows, float* y, int32_t* selected, float* weights,
+                        unsigned* status, void* stream);
+
 /* ---- MXFP4 mixture-of-experts layer (the reference has no device MoE; this composes
  * MoeLayer::forward, IW/src/models/text/qwen_layers.cpp:378-492, with the MXFP4
  * product semantics of IW/src/weights/quantization.cpp:79-99,207-247).

@@ -47,6 +47,12 @@ MOE_GGUF_TENSORS = ("router", "gate_exps", "up_exps", "down_exps", "gate_shexp",
                     "down_shexp")
 
 
+class MoeGgufPackedStacks(C.Structure):
+    """kdq_moe_gguf_packed_stacks (include/kadan_amd.h)."""
+    _fields_ = [(name, C.c_void_p) for name in MOE_GGUF_TENSORS[1:]] + [
+        ("checked", C.c_uint)]
+
+
 class MoeGgufLayer(C.Structure):
     """kdq_moe_gguf_layer (include/kadan_amd.h)."""
     _fields_ = [("hidden", C.c_size_t), ("experts", C.c_size_t), ("top_k", C.c_size_t),
@@ -68,6 +74,8 @@ _SIGNATURES = {
     "kdq_gemm_q4_0_packed": [_VP, _SZ, _SZ, _VP, _SZ, _VP, _VP],
     "kdq_gemm_packed": [_I, _VP, _SZ, _SZ, _VP, _SZ, _VP, _VP, _VP],
     "kdq_moe_gguf": [_VP, _VP, _SZ, _VP, _VP, _VP, _VP, _VP],
+    "kdq_moe_gguf_packed": [_VP, _VP, _VP, _SZ, _VP, _VP, _VP, _VP, _VP],
+    "kdq_gguf_gemm_check": [_I, _VP, _SZ, _SZ, _VP, _VP],
     "kdq_quantize_q8": [_VP, _SZ, _SZ, _VP, _VP, _VP],
     "kdq_moe_route": [_VP, _SZ, _SZ, _SZ, _VP, _VP, _VP, _VP, _VP],
     "kdq_mxfp4_dequantize": [_VP, _VP, _SZ, _SZ, _VP, _VP, _VP],

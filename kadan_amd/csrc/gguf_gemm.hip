@@ -295,6 +295,33 @@ __device__ __forceinline__ void load_item(const uint8_t* base, size_t off, unsig
     }
 }
 
+// The GEMM's scale checks over a whole packed matrix, without the product: 32 threads
+// per (16-row tile, 256-value group), lane (r = s, h) of the GEMM's operand lanes for row
+// slot s, each loading that lane's registers as the GEMM does and running the same
+// Scales::prepare, so a matrix this finds clean never raises a flag in the GEMM.
+template <int ENC>
+__global__ __launch_bounds__(256) void check_kernel(const uint8_t* __restrict__ w,
+                                                    unsigned groups, size_t units,
+                                                    unsigned* __restrict__ flags) {
+    using F = GemmFormat<ENC>;
+    const size_t id = size_t(blockIdx.x) * 256 + threadIdx.x;
+    const size_t unit = id / 32;
+    if (unit >= units)
+        return;
+    const unsigned s = threadIdx.x % 16, h = (threadIdx.x / 16) % 2;
+    const uint8_t* base = w + unit * F::unit + 16 * (16 * h + s);
+    typename F::Regs g;
+#pragma unroll
+    for (int i = 0; i < F::loads; ++i)
+        load_item<ENC>(base, 0, h, s, g, i);
+    unsigned f = 0;
+    Scales<ENC> sc;
+    sc.prepare(g, ENC == KDQ_Q6_K ? s : h, f);
+    if (f)
+        atomicOr(flags, f);
+    (void)groups;
+}
+
 // ------------------------------------------------------------------ staging
 
 // Row t of x (fp32, k values): its scale sigma = 2^e with max|x| / sigma in [2^14, 2^15)
@@ -629,7 +656,7 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ p
 }
 
 // K slices: enough workgroups for the compute units when the output tiles are few, each
-// slice at least 8 groups (2048 values) deep.
+// slice at least 2 groups (512 values) deep.
 // Returns the groups per slice; the slice count is ceil(groups / per) (no empty slice).
 unsigned gemm_slice_depth(size_t m, size_t n, size_t k) {
     const size_t groups = k / 256;
@@ -638,7 +665,7 @@ unsigned gemm_slice_depth(size_t m, size_t n, size_t k) {
     if (tiles * 3 >= units * 2)
         return unsigned(groups);
     size_t ks = std::max<size_t>(1, units / tiles);
-    ks = std::min(ks, std::max<size_t>(1, groups / 8));
+    ks = std::min(ks, std::max<size_t>(1, groups / 2));
     return unsigned((groups + ks - 1) / ks);
 }
 
@@ -682,22 +709,35 @@ int launch_grouped(const void* packed, size_t expert_bytes, const int32_t* tile_
     return KDQ_OK;
 }
 
-template <int ENC>
-int launch_gemm(const float* x, const uint8_t* packed, size_t m, size_t n, size_t k, float* y,
-                unsigned* status, hipStream_t st) {
-    int rc;
+// Scratch of one dense GEMM call: x staged as fp16 rows padded to whole token tiles, the
+// row scales, and the K slices' partials (none with one slice).
+struct GemmScratch {
+    size_t xs, sigma, part, total;
+};
+
+GemmScratch gemm_scratch(size_t m, size_t n, size_t k) {
     const size_t m_pad = (m + PM - 1) / PM * PM;
-    const size_t xs_bytes = (m_pad * k * 2 + 255) & ~size_t(255);
-    const size_t sig_bytes = (m * 4 + 255) & ~size_t(255);
     const unsigned per = gemm_slice_depth(m, n, k);
     const unsigned slices = unsigned((k / 256 + per - 1) / per);
-    const size_t part_bytes = slices > 1 ? size_t(slices) * m * n * 4 : 0;
-    auto* base = static_cast<uint8_t*>(workspace(xs_bytes + sig_bytes + part_bytes, &rc));
-    if (rc)
-        return rc;
-    auto* xs = reinterpret_cast<uint16_t*>(base);
-    auto* sigma = reinterpret_cast<float*>(base + xs_bytes);
-    auto* part = slices > 1 ? reinterpret_cast<float*>(base + xs_bytes + sig_bytes) : nullptr;
+    GemmScratch g;
+    g.xs = (m_pad * k * 2 + 255) & ~size_t(255);
+    g.sigma = (m * 4 + 255) & ~size_t(255);
+    g.part = slices > 1 ? (size_t(slices) * m * n * 4 + 255) & ~size_t(255) : 0;
+    g.total = g.xs + g.sigma + g.part;
+    return g;
+}
+
+template <int ENC>
+int launch_gemm(const float* x, const uint8_t* packed, size_t m, size_t n, size_t k, float* y,
+                unsigned* status, uint8_t* scratch, hipStream_t st) {
+    int rc;
+    const size_t m_pad = (m + PM - 1) / PM * PM;
+    const unsigned per = gemm_slice_depth(m, n, k);
+    const unsigned slices = unsigned((k / 256 + per - 1) / per);
+    const GemmScratch g = gemm_scratch(m, n, k);
+    auto* xs = reinterpret_cast<uint16_t*>(scratch);
+    auto* sigma = reinterpret_cast<float*>(scratch + g.xs);
+    auto* part = slices > 1 ? reinterpret_cast<float*>(scratch + g.xs + g.sigma) : nullptr;
     if ((rc = configure<ENC>()))
         return rc;
     hipLaunchKernelGGL(stage_kernel<ENC>, dim3(unsigned(m)), dim3(256), k * 4, st, x,
@@ -720,6 +760,51 @@ int launch_gemm(const float* x, const uint8_t* packed, size_t m, size_t n, size_
 }
 
 }  // namespace
+
+int gemm_check(int encoding, const void* packed, size_t n, size_t k, unsigned* flags,
+               hipStream_t st) {
+    const size_t units = (n + 15) / 16 * (k / 256);
+    const dim3 grid(unsigned((units * 32 + 255) / 256));
+    auto* w = static_cast<const uint8_t*>(packed);
+    switch (encoding) {
+    case KDQ_Q4_K:
+        hipLaunchKernelGGL(check_kernel<KDQ_Q4_K>, grid, dim3(256), 0, st, w, unsigned(k / 256),
+                           units, flags);
+        break;
+    case KDQ_Q8_0:
+        hipLaunchKernelGGL(check_kernel<KDQ_Q8_0>, grid, dim3(256), 0, st, w, unsigned(k / 256),
+                           units, flags);
+        break;
+    case KDQ_Q6_K:
+        hipLaunchKernelGGL(check_kernel<KDQ_Q6_K>, grid, dim3(256), 0, st, w, unsigned(k / 256),
+                           units, flags);
+        break;
+    default:
+        return KDQ_ERR_UNSUPPORTED;
+    }
+    KDQ_HIP(hipGetLastError());
+    return KDQ_OK;
+}
+
+size_t dense_gemm_scratch(size_t m, size_t n, size_t k) {
+    return gemm_scratch(m, n, k).total;
+}
+
+int dense_gemm(int encoding, const void* packed, size_t n, size_t k, const float* x, size_t m,
+               float* y, unsigned* status, void* scratch, hipStream_t st) {
+    auto* w = static_cast<const uint8_t*>(packed);
+    auto* sc = static_cast<uint8_t*>(scratch);
+    switch (encoding) {
+    case KDQ_Q4_K:
+        return launch_gemm<KDQ_Q4_K>(x, w, m, n, k, y, status, sc, st);
+    case KDQ_Q8_0:
+        return launch_gemm<KDQ_Q8_0>(x, w, m, n, k, y, status, sc, st);
+    case KDQ_Q6_K:
+        return launch_gemm<KDQ_Q6_K>(x, w, m, n, k, y, status, sc, st);
+    default:
+        return KDQ_ERR_UNSUPPORTED;
+    }
+}
 
 bool grouped_gemm_takes(int encoding, size_t k) {
     return (encoding == KDQ_Q4_K || encoding == KDQ_Q8_0 || encoding == KDQ_Q6_K) &&
@@ -764,14 +849,23 @@ extern "C" int kdq_gemm_packed(int encoding, const void* packed, size_t n, size_
     const size_t packed_bytes = kdq_gguf_packed_bytes(encoding, k, n);
     if (overlaps(y, m * n * 4, x, m * k * 4) || overlaps(y, m * n * 4, packed, packed_bytes))
         return KDQ_ERR_ALIAS;
-    auto st = static_cast<hipStream_t>(stream);
-    auto* w = static_cast<const uint8_t*>(packed);
-    switch (encoding) {
-    case KDQ_Q4_K:
-        return launch_gemm<KDQ_Q4_K>(x, w, m, n, k, y, status, st);
-    case KDQ_Q8_0:
-        return launch_gemm<KDQ_Q8_0>(x, w, m, n, k, y, status, st);
-    default:
-        return launch_gemm<KDQ_Q6_K>(x, w, m, n, k, y, status, st);
-    }
+    int rc;
+    void* scratch = workspace(dense_gemm_scratch(m, n, k), &rc);
+    if (rc)
+        return rc;
+    return dense_gemm(encoding, packed, n, k, x, m, y, status, scratch,
+                      static_cast<hipStream_t>(stream));
+}
+
+extern "C" int kdq_gguf_gemm_check(int encoding, const void* packed, size_t n, size_t k,
+                                   unsigned* flags, void* stream) {
+    if (!packed || !flags || !n || !k)
+        return KDQ_ERR_ARGUMENT;
+    if (encoding != KDQ_Q4_K && encoding != KDQ_Q8_0 && encoding != KDQ_Q6_K)
+        return KDQ_ERR_UNSUPPORTED;
+    if (k % 256 || k > 32768 || n > 0xffffffu)
+        return KDQ_ERR_SHAPE;
+    if (reinterpret_cast<uintptr_t>(packed) % 16 || reinterpret_cast<uintptr_t>(flags) % 4)
+        return KDQ_ERR_ALIGNMENT;
+    return gemm_check(encoding, packed, n, k, flags, static_cast<hipStream_t>(stream));
 }

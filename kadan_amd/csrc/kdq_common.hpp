@@ -199,6 +199,11 @@ int grouped_gemm(int encoding, const void* packed, size_t expert_bytes,
                  float* y, unsigned* status, uint16_t* xs, float* sigma, hipStream_t st);
 int route_selection(const float* logits, size_t tokens, size_t experts, size_t top_k,
                     int32_t* idx, float* w, hipStream_t stream);
+// Dense prefill GEMM over one tile-packed matrix (kdq_gemm_packed's product) with the
+// caller's scratch of dense_gemm_scratch(m, n, k) bytes: y[m x n] = x[m x k] W^T.
+size_t dense_gemm_scratch(size_t m, size_t n, size_t k);
+int dense_gemm(int encoding, const void* packed, size_t n, size_t k, const float* x, size_t m,
+               float* y, unsigned* status, void* scratch, hipStream_t st);
 
 inline size_t block_values(int encoding) {
     switch (encoding) {

@@ -73,6 +73,8 @@ constexpr size_t kSlotRows = 8;          // batches up to this many rows run per
 constexpr unsigned kItemRows = 8;        // rows of a grouped item (the MFMA GEMV's batch)
 constexpr unsigned kTileRows = 128;      // rows of a grouped GEMM token tile
 constexpr size_t kMaxGroupedSlots = 8192;
+constexpr size_t kSharedGemmRows = 64;   // batches from this many rows run the shared
+                                         // expert on the prefill GEMM
 
 // Slots by expert into segments padded to multiples of `pad` (kItemRows, or kTileRows when
 // a projection runs on the grouped GEMM): pos[s] (slot -> position), inv[p] (position ->
@@ -258,6 +260,11 @@ __global__ void or_status_kernel(unsigned* status, const unsigned* from, unsigne
         atomicOr(status, *from & mask);
 }
 
+// Whether a shared matrix (out x in) can run on the dense prefill GEMM.
+bool gemm_matrix(const kdq_gguf_tensor& m, size_t out, size_t in) {
+    return grouped_gemm_takes(m.encoding, in) && kdq_gguf_packed_bytes(m.encoding, in, out);
+}
+
 // Whether a gate job of `rows` rows can run paired with its up matrix through run_rows.
 bool rows_pairable(const kdq_matvec_job& gate) {
     if (gate.rows <= kItemRows)
@@ -267,14 +274,9 @@ bool rows_pairable(const kdq_matvec_job& gate) {
     return gate.rows % kItemRows == 0 && swiglu_pairable(a, gate.rows / kItemRows);
 }
 
-}  // namespace
-}  // namespace kdq
-
-using namespace kdq;
-
-extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, size_t rows,
-                            float* y, int32_t* selected, float* weights, unsigned* status,
-                            void* stream) {
+int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* packed,
+             const float* x, size_t rows, float* y, int32_t* selected, float* weights,
+             unsigned* status, void* stream) {
     if (!layer || !x || !y || !rows)
         return KDQ_ERR_ARGUMENT;
     const kdq_moe_gguf_layer& L = *layer;
@@ -293,6 +295,11 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
         return KDQ_ERR_SHAPE;
     if (misaligned(x, 16) || misaligned(y, 16) || misaligned(L.shared_gate, 16))
         return KDQ_ERR_ALIGNMENT;
+    if (packed)
+        for (const void* p : {packed->gate_exps, packed->up_exps, packed->down_exps,
+                              packed->gate_shexp, packed->up_shexp, packed->down_shexp})
+            if (misaligned(p, 16))
+                return KDQ_ERR_ALIGNMENT;
     if (overlaps(y, rows * H * 4, x, rows * H * 4))
         return KDQ_ERR_ALIAS;
     // workspace: logits, shared gate/up rows, gate scalars, routing (unless the caller
@@ -307,6 +314,20 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
     const bool gemm_gu = grouped && dense && gemm_stack(L.gate_exps, F, H) &&
                          gemm_stack(L.up_exps, F, H);
     const bool gemm_dn = grouped && dense && gemm_stack(L.down_exps, H, F);
+    const kdq_moe_gguf_packed_stacks none{};
+    const kdq_moe_gguf_packed_stacks& pk = packed ? *packed : none;
+    // Matrices the caller keeps packed and has checked (kdq_gguf_gemm_check) cannot raise
+    // the GEMM's fp16-range flag; any other matrix on a GEMM makes the call wait once on
+    // the host for that flag (below).
+    const bool sh_checked = pk.checked && pk.gate_shexp && pk.up_shexp && pk.down_shexp;
+    // the shared expert (every row) on the dense prefill GEMM from kSharedGemmRows rows,
+    // when the call does not wait for the flag because of it alone (the wait costs more
+    // than the shared products at these sizes)
+    const bool gemm_sh = grouped && rows >= kSharedGemmRows && gemm_matrix(L.gate_shexp, S, H) &&
+                         gemm_matrix(L.up_shexp, S, H) && gemm_matrix(L.down_shexp, H, S) &&
+                         (gemm_gu || gemm_dn || sh_checked);
+    const bool wait = (gemm_gu && !(pk.checked && pk.gate_exps && pk.up_exps)) ||
+                      (gemm_dn && !(pk.checked && pk.down_exps)) || (gemm_sh && !sh_checked);
     const size_t pad = gemm_gu || gemm_dn ? kTileRows : kItemRows;
     const size_t positions = grouped ? (slots + (pad - 1) * E + pad - 1) / pad * pad : slots;
     const size_t items = positions / kItemRows;
@@ -314,6 +335,15 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
     const size_t up_bytes = gemm_gu ? kdq_gguf_packed_bytes(L.up_exps.encoding, H, F) : 0;
     const size_t dn_bytes = gemm_dn ? kdq_gguf_packed_bytes(L.down_exps.encoding, F, H) : 0;
     const size_t xs_bytes = gemm_gu || gemm_dn ? positions * std::max(H, F) * 2 : 0;
+    // the shared GEMMs: packed copies unless the caller keeps them, one GEMM scratch
+    auto sh_pack = [&](const kdq_gguf_tensor& m, const void* given, size_t out, size_t in) {
+        return gemm_sh && !given ? kdq_gguf_packed_bytes(m.encoding, in, out) : 0;
+    };
+    const size_t shg_bytes = sh_pack(L.gate_shexp, pk.gate_shexp, S, H);
+    const size_t shu_bytes = sh_pack(L.up_shexp, pk.up_shexp, S, H);
+    const size_t shd_bytes = sh_pack(L.down_shexp, pk.down_shexp, H, S);
+    const size_t sh_scratch =
+        gemm_sh ? std::max(dense_gemm_scratch(rows, S, H), dense_gemm_scratch(rows, H, S)) : 0;
     const size_t sizes[] = {rows * E * 4,      rows * S * 4,      rows * S * 4,
                             rows * 4,          slots * 4,         slots * 4,
                             positions * F * 4, positions * F * 4, positions * H * 4,
@@ -321,8 +351,10 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
                             grouped ? slots * 4 : 0, grouped ? positions * 4 : 0,
                             grouped ? items * 4 : 0, size_t(grouped ? 8 : 0),
                             grouped ? positions / kTileRows * 4 + 4 : 0,
-                            gu_bytes * E, up_bytes * E, dn_bytes * E, xs_bytes,
-                            gemm_gu || gemm_dn ? positions * 4 : 0};
+                            pk.gate_exps ? 0 : gu_bytes * E, pk.up_exps ? 0 : up_bytes * E,
+                            pk.down_exps ? 0 : dn_bytes * E, xs_bytes,
+                            gemm_gu || gemm_dn ? positions * 4 : 0, shg_bytes, shu_bytes,
+                            shd_bytes, sh_scratch};
     constexpr size_t kParts = sizeof(sizes) / sizeof(sizes[0]);
     size_t total = 0;
     for (size_t b : sizes)
@@ -351,11 +383,15 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
     auto* used = static_cast<unsigned*>(part[14]);
     auto* gemm_status = used + 1;
     auto* tile_expert = static_cast<int32_t*>(part[15]);
-    auto* packed_gate = part[16];
-    auto* packed_up = part[17];
-    auto* packed_down = part[18];
+    auto* packed_gate = pk.gate_exps ? const_cast<void*>(pk.gate_exps) : part[16];
+    auto* packed_up = pk.up_exps ? const_cast<void*>(pk.up_exps) : part[17];
+    auto* packed_down = pk.down_exps ? const_cast<void*>(pk.down_exps) : part[18];
     auto* xs = static_cast<uint16_t*>(part[19]);
     auto* sigma = static_cast<float*>(part[20]);
+    const void* sh_gate = pk.gate_shexp ? pk.gate_shexp : part[21];
+    const void* sh_up = pk.up_shexp ? pk.up_shexp : part[22];
+    const void* sh_down = pk.down_shexp ? pk.down_shexp : part[23];
+    void* sh_work = part[24];
     auto st = static_cast<hipStream_t>(stream);
 
     // 1. router, shared-gate scalar, shared gate / up (with the swiglu in the same launch
@@ -368,19 +404,34 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
                            {job(gate_vector, x, rows, H, 1, gate, status), nullptr, 0, 1, nullptr},
                            {shared_gate, nullptr, 0, 1, pair_shared ? L.up_shexp.weights : nullptr},
                            {job(L.up_shexp, x, rows, H, S, su, status), nullptr, 0, 1, nullptr}};
+    // the shared gate / up on the row path (stage 1, or the GEMM path's exact fallback)
+    auto shared_rows = [&]() -> int {
+        int r;
+        for (int i = 2; i < (pair_shared ? 3 : 4); ++i)
+            if ((r = run_rows(first[i], st)))
+                return r;
+        if (!pair_shared) {
+            hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((rows * S + 255) / 256)), dim3(256),
+                               0, st, sg, su, rows * S, nullptr, 1u, nullptr);
+            KDQ_HIP(hipGetLastError());
+        }
+        return KDQ_OK;
+    };
     if (!grouped) {
         if ((rc = indexed_gemv_batch(first, pair_shared ? 3 : 4, st)))
             return rc;
     } else {
-        for (int i = 0; i < (pair_shared ? 3 : 4); ++i)
+        for (int i = 0; i < 2; ++i)
             if ((rc = run_rows(first[i], st)))
                 return rc;
+        if (!gemm_sh && (rc = shared_rows()))
+            return rc;
     }
     // 2. routing, straight into the caller's buffers when given
     if ((rc = route_selection(logits, rows, E, K, idx, w, st)))
         return rc;
-    // 3. shared swiglu, unless paired above
-    if (!pair_shared) {
+    // 3. shared swiglu, unless paired above (grouped batches: done with the shared rows)
+    if (!grouped && !pair_shared) {
         hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((rows * S + 255) / 256)), dim3(256), 0,
                            st, sg, su, rows * S, nullptr, 1u, nullptr);
         KDQ_HIP(hipGetLastError());
@@ -391,6 +442,27 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
                            unsigned(E), unsigned(pad), unsigned(items), pos, inv, item_expert,
                            tile_expert, used, gemm_status);
         KDQ_HIP(hipGetLastError());
+        // the shared gate / up on the dense GEMM (after group_kernel, which clears the
+        // GEMM flags), packed here unless the caller keeps them packed
+        if (gemm_sh) {
+            if ((!pk.gate_shexp &&
+                 (rc = kdq_gguf_pack(L.gate_shexp.encoding, L.gate_shexp.weights,
+                                     L.gate_shexp.row_bytes, H, S, part[21], st))) ||
+                (!pk.up_shexp &&
+                 (rc = kdq_gguf_pack(L.up_shexp.encoding, L.up_shexp.weights,
+                                     L.up_shexp.row_bytes, H, S, part[22], st))) ||
+                (!pk.down_shexp &&
+                 (rc = kdq_gguf_pack(L.down_shexp.encoding, L.down_shexp.weights,
+                                     L.down_shexp.row_bytes, S, H, part[23], st))) ||
+                (rc = dense_gemm(L.gate_shexp.encoding, sh_gate, S, H, x, rows, sg, gemm_status,
+                                 sh_work, st)) ||
+                (rc = dense_gemm(L.up_shexp.encoding, sh_up, S, H, x, rows, su, gemm_status,
+                                 sh_work, st)))
+                return rc;
+            hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((rows * S + 255) / 256)), dim3(256),
+                               0, st, sg, su, rows * S, nullptr, 1u, nullptr);
+            KDQ_HIP(hipGetLastError());
+        }
         const size_t xs8 = kItemRows * H, fs8 = kItemRows * F;
         // the expert products on the GEMV items (every encoding; the fallback of the GEMM)
         auto items_gate_up = [&]() -> int {
@@ -422,11 +494,14 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
             return indexed_gemv_affine(dj, unsigned(items), fs8, xs8, st);
         };
         // 4''. expert gate / up
-        if (gemm_gu) {  // both stacks packed (this call), one grouped GEMM each, swiglu
-            if ((rc = kdq_gguf_pack(L.gate_exps.encoding, L.gate_exps.weights,
-                                    L.gate_exps.row_bytes, H, E * F, packed_gate, st)) ||
-                (rc = kdq_gguf_pack(L.up_exps.encoding, L.up_exps.weights, L.up_exps.row_bytes,
-                                    H, E * F, packed_up, st)) ||
+        if (gemm_gu) {  // both stacks packed (this call or the caller's), one grouped GEMM
+                        // each, swiglu
+            if ((!pk.gate_exps &&
+                 (rc = kdq_gguf_pack(L.gate_exps.encoding, L.gate_exps.weights,
+                                     L.gate_exps.row_bytes, H, E * F, packed_gate, st))) ||
+                (!pk.up_exps &&
+                 (rc = kdq_gguf_pack(L.up_exps.encoding, L.up_exps.weights, L.up_exps.row_bytes,
+                                     H, E * F, packed_up, st))) ||
                 (rc = grouped_gemm(L.gate_exps.encoding, packed_gate, gu_bytes, tile_expert, F,
                                    H, x, inv, unsigned(K), used, positions, g, gemm_status, xs,
                                    sigma, st)) ||
@@ -442,8 +517,9 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
         }
         // 5'. expert downs, the shared down
         if (gemm_dn) {
-            if ((rc = kdq_gguf_pack(L.down_exps.encoding, L.down_exps.weights,
-                                    L.down_exps.row_bytes, F, E * H, packed_down, st)) ||
+            if ((!pk.down_exps &&
+                 (rc = kdq_gguf_pack(L.down_exps.encoding, L.down_exps.weights,
+                                     L.down_exps.row_bytes, F, E * H, packed_down, st))) ||
                 (rc = grouped_gemm(L.down_exps.encoding, packed_down, dn_bytes, tile_expert, H,
                                    F, g, nullptr, 1u, used, positions, d, gemm_status, xs,
                                    sigma, st)))
@@ -453,7 +529,9 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
         }
         const IndexedJob sj{job(L.down_shexp, sg, rows, S, H, ds, status), nullptr, 0, 1,
                             nullptr};
-        if ((rc = run_rows(sj, st)))
+        if (gemm_sh ? (rc = dense_gemm(L.down_shexp.encoding, sh_down, H, S, sg, rows, ds,
+                                       gemm_status, sh_work, st))
+                    : (rc = run_rows(sj, st)))
             return rc;
         auto combine = [&]() -> int {
             hipLaunchKernelGGL(combine_pos_kernel, dim3(unsigned((rows * H + 255) / 256)),
@@ -465,7 +543,15 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
         // 6'. combine in selection order, each slot's down at its position
         if ((rc = combine()))
             return rc;
-        if (gemm_gu || gemm_dn) {
+        if ((gemm_gu || gemm_dn || gemm_sh) && !wait) {
+            // checked matrices: only the non-finite bit can be set; it goes to the
+            // caller's status on the device
+            if (status) {
+                hipLaunchKernelGGL(or_status_kernel, dim3(1), dim3(64), 0, st, status,
+                                   gemm_status, 1u);
+                KDQ_HIP(hipGetLastError());
+            }
+        } else if (gemm_gu || gemm_dn || gemm_sh) {
             // the GEMM's flags: a non-finite scale is the caller's status bit 1; a scale
             // that could take a dequantised weight past the fp16 range (never in real
             // checkpoints) makes this call redo its expert products on the GEMV items,
@@ -475,7 +561,8 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
                                    st));
             KDQ_HIP(hipStreamSynchronize(st));
             if (flags & 2u) {
-                if ((rc = items_gate_up()) || (rc = items_down()) || (rc = combine()))
+                if ((gemm_sh && ((rc = shared_rows()) || (rc = run_rows(sj, st)))) ||
+                    (rc = items_gate_up()) || (rc = items_down()) || (rc = combine()))
                     return rc;
             } else if ((flags & 1u) && status) {
                 hipLaunchKernelGGL(or_status_kernel, dim3(1), dim3(64), 0, st, status,
@@ -518,4 +605,22 @@ extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, siz
                        d, w, ds, gate, unsigned(K), unsigned(H), rows, y);
     KDQ_HIP(hipGetLastError());
     return KDQ_OK;
+}
+
+}  // namespace
+}  // namespace kdq
+
+using namespace kdq;
+
+extern "C" int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, size_t rows,
+                            float* y, int32_t* selected, float* weights, unsigned* status,
+                            void* stream) {
+    return moe_gguf(layer, nullptr, x, rows, y, selected, weights, status, stream);
+}
+
+extern "C" int kdq_moe_gguf_packed(const kdq_moe_gguf_layer* layer,
+                                   const kdq_moe_gguf_packed_stacks* packed, const float* x,
+                                   size_t rows, float* y, int32_t* selected, float* weights,
+                                   unsigned* status, void* stream) {
+    return moe_gguf(layer, packed, x, rows, y, selected, weights, status, stream);
 }

@@ -179,12 +179,47 @@ def gemm_packed(encoding: int, packed: torch.Tensor, x: torch.Tensor, n_out: int
     return out
 
 
-def moe_gguf(spec: dict, x: torch.Tensor, status: torch.Tensor | None = None):
-    """GGUF MoE layer (kdq_moe_gguf).  spec: hidden, experts, top_k, ff, shared_ff,
+def gguf_gemm_check(encoding: int, packed: torch.Tensor, n_out: int, n_in: int) -> int:
+    """The prefill GEMM's scale checks over a tile-packed matrix (kdq_gguf_gemm_check):
+    bit 1 a non-finite scale, bit 2 a dequantised weight that could pass the fp16 range
+    (waits for the device)."""
+    flags = torch.zeros(1, dtype=torch.int32, device=packed.device)
+    call("kdq_gguf_gemm_check", encoding, packed.data_ptr(), n_out, n_in, flags.data_ptr(),
+         _stream())
+    return int(flags.item())
+
+
+def moe_gguf_pack(spec: dict) -> dict:
+    """Tile-packed copies (kdq_gguf_pack) of a GGUF MoE spec's expert stacks and shared
+    matrices, for moe_gguf(..., packed=...): name -> uint8 device tensor, for the
+    encodings the prefill GEMM reads packed (Q4_K, Q8_0, Q6_K), and "checked": every copy
+    passed kdq_gguf_gemm_check with no flag."""
+    from . import MOE_GGUF_TENSORS
+    H, F, S = spec["hidden"], spec["ff"], spec["shared_ff"]
+    shape = {"gate_exps": (H, F), "up_exps": (H, F), "down_exps": (F, H),
+             "gate_shexp": (H, S), "up_shexp": (H, S), "down_shexp": (S, H)}
+    out = {}
+    for name in MOE_GGUF_TENSORS[1:]:
+        enc, t = spec[name]
+        if enc not in (12, 8, 14):  # Q4_K, Q8_0, Q6_K
+            continue
+        n_in, rows = shape[name]
+        count = rows * (t.shape[0] if t.dim() == 3 else 1)
+        out[name] = gguf_pack(enc, t.reshape(count, t.shape[-1]), n_in)
+    out["checked"] = all(gguf_gemm_check(spec[n][0], out[n], shape[n][1] * (
+        spec[n][1].shape[0] if spec[n][1].dim() == 3 else 1), shape[n][0]) == 0
+        for n in list(out))
+    return out
+
+
+def moe_gguf(spec: dict, x: torch.Tensor, status: torch.Tensor | None = None,
+             packed: dict | None = None):
+    """GGUF MoE layer (kdq_moe_gguf; kdq_moe_gguf_packed when `packed` holds resident
+    tile-packed copies from moe_gguf_pack).  spec: hidden, experts, top_k, ff, shared_ff,
     shared_gate (fp32 device tensor [hidden]) and per tensor name (encoding, uint8 device
     tensor [rows, row_bytes] or [experts, rows, row_bytes]).  x fp32 [rows, hidden] ->
     (y fp32 [rows, hidden], selected int32 [rows, top_k], weights fp32 [rows, top_k])."""
-    from . import MOE_GGUF_TENSORS, GgufTensor, MoeGgufLayer
+    from . import MOE_GGUF_TENSORS, GgufTensor, MoeGgufLayer, MoeGgufPackedStacks
     _need(x, torch.float32, "x")
     layer = MoeGgufLayer(spec["hidden"], spec["experts"], spec["top_k"], spec["ff"],
                          spec["shared_ff"])
@@ -199,8 +234,16 @@ def moe_gguf(spec: dict, x: torch.Tensor, status: torch.Tensor | None = None):
     y = torch.empty(rows, spec["hidden"], dtype=torch.float32, device=x.device)
     sel = torch.empty(rows, spec["top_k"], dtype=torch.int32, device=x.device)
     w = torch.empty(rows, spec["top_k"], dtype=torch.float32, device=x.device)
-    call("kdq_moe_gguf", ctypes.addressof(layer), x.data_ptr(), rows, y.data_ptr(),
-         sel.data_ptr(), w.data_ptr(), _ptr(status), _stream())
+    if packed is None:
+        call("kdq_moe_gguf", ctypes.addressof(layer), x.data_ptr(), rows, y.data_ptr(),
+             sel.data_ptr(), w.data_ptr(), _ptr(status), _stream())
+    else:
+        stacks = MoeGgufPackedStacks(*[packed[n].data_ptr() if n in packed else None
+                                       for n in MOE_GGUF_TENSORS[1:]],
+                                     int(bool(packed.get("checked", False))))
+        call("kdq_moe_gguf_packed", ctypes.addressof(layer), ctypes.addressof(stacks),
+             x.data_ptr(), rows, y.data_ptr(), sel.data_ptr(), w.data_ptr(), _ptr(status),
+             _stream())
     return y, sel, w
 
 

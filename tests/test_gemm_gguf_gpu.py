@@ -53,8 +53,9 @@ def run(device, oracle, enc, m, k, n, seed, cols=None):
                                    (129, 768, 257), (256, 2048, 512), (64, 6912, 520),
                                    (200, 4352, 96)])
 def test_gemm_small_shapes(device, oracle, enc, m, k, n):
-    """(64, 6912, 520) and (200, 4352, 96) have few output tiles: they run K slices (three
-    slices of 9 of the 27 groups; two slices of 9 and 8 of 17) and the ordered slice sum."""
+    """(64, 6912, 520) and (200, 4352, 96) have few output tiles: they run K slices (nine
+    slices of 3 of the 27 groups; six slices of 3, 3, 3, 3, 3 and 2 of 17) and the ordered
+    slice sum."""
     run(device, oracle, enc, m, k, n, seed=0x9E + m + n)
 
 
@@ -79,6 +80,31 @@ def test_gemm_status_flags(device):
         status = torch.zeros(1, dtype=torch.int32, device=device)
         ops.gemm_packed(Q8_0, packed, torch.ones(4, k, device=device), n, status=status)
         assert int(status.item()) & flag
+
+
+D_AT = {Q8_0: 0, Q4_K: 0, Q6_K: 208}  # byte offset of the first block's fp16 d
+
+
+@pytest.mark.parametrize("enc", ENCODINGS)
+def test_gemm_check_matches_the_gemm_flags(device, enc):
+    """kdq_gguf_gemm_check runs the GEMM's own scale checks over a packed matrix without
+    the product: a clean matrix gives 0, a non-finite d bit 1, a d of 512 (every encoding's
+    dequantised weights then pass the fp16 range) bit 2 -- the same bits the GEMM sets."""
+    torch = _torch()
+    from kadan_amd import ops
+    k, n = 512, 40
+    clean = synth.gguf_weights(enc, 5, n, k)
+    packed = ops.gguf_pack(enc, torch.from_numpy(clean).to(device), k)
+    assert ops.gguf_gemm_check(enc, packed, n, k) == 0
+    for d_bits, flag in ((0x7C00, 1), (0x6000, 2)):
+        w = clean.copy()
+        w[33, D_AT[enc]], w[33, D_AT[enc] + 1] = d_bits & 255, d_bits >> 8
+        packed = ops.gguf_pack(enc, torch.from_numpy(w).to(device), k)
+        got = ops.gguf_gemm_check(enc, packed, n, k)
+        assert got & flag
+        status = torch.zeros(1, dtype=torch.int32, device=device)
+        ops.gemm_packed(enc, packed, torch.ones(4, k, device=device), n, status=status)
+        assert int(status.item()) == got
 
 
 def test_gemm_nonfinite_input_poisons_its_row(device):

@@ -189,3 +189,99 @@ def test_moe_gguf_rejections(device):
         ops.moe_gguf(dev, torch.ones(4097, H, device=device))
     with pytest.raises(KdqError, match="kdq_projection_shape"):  # rows * top_k > 8192
         ops.moe_gguf(dict(dev, top_k=8), torch.ones(1025, H, device=device))
+
+
+@pytest.mark.parametrize("rows", [4, 64, 200])
+def test_moe_gguf_packed_stacks_bit_identical(device, oracle, rows):
+    """kdq_moe_gguf_packed over resident tile-packed copies (expert stacks and shared
+    matrices packed once, as a weight bank keeps them) gives the same bits as
+    kdq_moe_gguf, which packs them in the call: 4 rows (the per-slot decode path, which
+    reads rows and ignores the copies), 64 (8-row items for the experts, the shared expert
+    on the dense GEMM) and 200 (everything on the GEMM); checked against the oracle too."""
+    import torch
+    H, E, K, F, S = 512, 16, 8, 256, 512
+    spec = make_layer(60 + rows, H, E, K, F, S, MIXED)
+    from kadan_amd import ops
+    dev = to_device(torch, device, spec)
+    packed = ops.moe_gguf_pack(dev)
+    assert sorted(k for k in packed if k != "checked") == sorted(NAMES[1:])
+    assert packed["checked"]
+    x = synth.normal(61 + rows, 1, rows * H).reshape(rows, H)
+    xd = torch.from_numpy(x).to(device)
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    y, sel, ws = ops.moe_gguf(dev, xd, status=status, packed=packed)
+    y0, sel0, ws0 = ops.moe_gguf(dev, xd)
+    assert np.array_equal(y.cpu().numpy(), y0.cpu().numpy())
+    assert np.array_equal(sel.cpu().numpy(), sel0.cpu().numpy())
+    assert np.array_equal(ws.cpu().numpy(), ws0.cpu().numpy())
+    assert int(status.item()) == 0
+    want, idx, _ = oracle.moe_gguf_forward(spec, x)
+    assert np.array_equal(sel.cpu().numpy(), idx)
+    assert_close(y.cpu().numpy(), want, what=f"moe_gguf_packed rows={rows}")
+
+
+def test_moe_gguf_shared_gemm_fp16_range_fallback(device, oracle):
+    """A shared gate scale whose dequantised weights could pass the fp16 range (Q8_0
+    d = 1000) at 64 rows, where the shared expert runs on the dense GEMM: the call redoes
+    the shared expert (and the experts) on the exact-decode rows, so y is still the exact
+    product and status stays 0."""
+    import torch
+    H, E, K, F, S, rows = 512, 16, 4, 256, 512, 64
+    spec = make_layer(14, H, E, K, F, S, MIXED)
+    enc, arr = spec["gate_shexp"]
+    arr = arr.copy()
+    big = np.array([1000.0], np.float16).view(np.uint16)[0]
+    arr[:, 0], arr[:, 1] = big & 255, big >> 8  # d of every row's first Q8_0 block
+    spec["gate_shexp"] = (enc, arr)
+    x = synth.normal(15, 1, rows * H).reshape(rows, H)
+    want, idx, _ = oracle.moe_gguf_forward(spec, x)
+    from kadan_amd import ops
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    y, sel, _ = ops.moe_gguf(to_device(torch, device, spec), torch.from_numpy(x).to(device),
+                             status=status)
+    assert np.array_equal(sel.cpu().numpy(), idx)
+    assert int(status.item()) == 0
+    assert_close(y.cpu().numpy(), want, what="moe_gguf shared GEMM fp16-range fallback")
+
+
+def test_moe_gguf_packed_unchecked_still_falls_back(device, oracle):
+    """Resident packed copies of a layer whose expert gate has a scale past the fp16 range
+    (Q4_K d = 1000): kdq_gguf_gemm_check flags it, so the copies are not marked checked and
+    the 200-row call still waits for the GEMM's flag and redoes its products exactly."""
+    import torch
+    H, E, K, F, S, rows = 512, 16, 8, 256, 512, 200
+    spec = make_layer(17, H, E, K, F, S, MIXED)
+    enc, arr = spec["gate_exps"]
+    arr = arr.copy()
+    big = np.array([1000.0], np.float16).view(np.uint16)[0]
+    arr[:, :, 0], arr[:, :, 1] = big & 255, big >> 8
+    spec["gate_exps"] = (enc, arr)
+    from kadan_amd import ops
+    dev = to_device(torch, device, spec)
+    packed = ops.moe_gguf_pack(dev)
+    assert not packed["checked"]
+    x = synth.normal(18, 1, rows * H).reshape(rows, H)
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    y, sel, _ = ops.moe_gguf(dev, torch.from_numpy(x).to(device), status=status, packed=packed)
+    assert int(status.item()) == 0
+    pick = np.arange(0, rows, 9)
+    want, idx, _ = oracle.moe_gguf_forward(spec, x[pick])
+    assert np.array_equal(sel.cpu().numpy()[pick], idx)
+    assert_close(y.cpu().numpy()[pick], want, what="moe_gguf_packed unchecked fallback")
+
+
+def test_moe_gguf_shared_gemm_nonfinite_status(device):
+    """A non-finite scale in the shared down (Q4_K) at 64 rows (the shared expert on the
+    dense GEMM) reaches the caller's status as bit 1."""
+    import torch
+    H, E, K, F, S, rows = 256, 8, 2, 256, 256, 64
+    spec = make_layer(16, H, E, K, F, S, MIXED)
+    enc, arr = spec["down_shexp"]
+    arr = arr.copy()
+    arr[3, 0], arr[3, 1] = 0x00, 0x7C  # +inf d
+    spec["down_shexp"] = (enc, arr)
+    from kadan_amd import ops
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    ops.moe_gguf(to_device(torch, device, spec), torch.ones(rows, H, device=device),
+                 status=status)
+    assert int(status.item()) & 1
