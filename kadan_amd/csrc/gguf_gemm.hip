@@ -38,12 +38,12 @@ constexpr int PM = 128;                      // tokens per workgroup tile (4 blo
 constexpr int NB = 2;                        // 32-row weight operands per wavefront
 constexpr int kTiles = 8 * NB;               // 16-row packed tiles per workgroup
 constexpr int kStageRow = 512;               // LDS bytes per token of one staged group
-constexpr int kStageBytes = PM * kStageRow;  // 64 KB
 constexpr int kDmaRows = 1024 / kStageRow;   // token rows per 64-lane 16-byte DMA
 constexpr int kOutPitch = kTiles * 16 * 4 + 16;  // fp32 output row in LDS (+16: banks)
-constexpr size_t kLds = size_t(PM) * kOutPitch > 2 * size_t(kStageBytes)
-                            ? size_t(PM) * kOutPitch
-                            : 2 * size_t(kStageBytes);
+// LDS of a workgroup with TM-token tiles: two activation stages, reused for the output
+template <int TM> constexpr size_t gemm_lds =
+    std::max(size_t(TM) * kOutPitch, 2 * size_t(TM) * kStageRow);
+constexpr size_t kLds = gemm_lds<PM>;
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) void global_void;
@@ -406,26 +406,27 @@ __global__ __launch_bounds__(256) void stage_kernel(const float* __restrict__ x,
 // Grouped (MoE) form, `tile_expert` given: token tile t multiplies the weights of expert
 // tile_expert[t] of a stack of packed experts `expert_bytes` apart; tiles whose entry is
 // negative are skipped (the whole workgroup returns before any barrier).
-template <int ENC, int W>
-__global__ __launch_bounds__(W * 64, 1) void gemm_kernel(const uint16_t* __restrict__ xs,
-                                                      const float* __restrict__ sigma,
-                                                      const uint8_t* __restrict__ w,
-                                                      unsigned m, unsigned n, unsigned k,
-                                                      unsigned slices, unsigned per,
-                                                      float* __restrict__ y,
-                                                      float* __restrict__ part,
-                                                      unsigned* __restrict__ status,
-                                                      const int32_t* __restrict__ tile_expert,
-                                                      size_t expert_bytes) {
+//
+// TM = 64 (the grouped form's token tiles: experts average a few dozen rows) halves the
+// token tile: two token blocks per operand, two workgroups per compute unit (Q8_0: one;
+// at two its registers spill).
+template <int ENC, int W, int TM>
+__global__ __launch_bounds__(W * 64, TM == PM || ENC == KDQ_Q8_0 ? 1 : 2) void gemm_kernel(
+    const uint16_t* __restrict__ xs, const float* __restrict__ sigma,
+    const uint8_t* __restrict__ w, unsigned m, unsigned n, unsigned k, unsigned slices,
+    unsigned per, float* __restrict__ y, float* __restrict__ part, unsigned* __restrict__ status,
+    const int32_t* __restrict__ tile_expert, size_t expert_bytes) {
     using F = GemmFormat<ENC>;
     using Regs = typename F::Regs;
     extern __shared__ __align__(16) uint8_t lds[];
-    // W wavefronts of NBW 32-row operands each (8 operands, 256 rows, per workgroup)
-    constexpr int NBW = 8 / W;
-    constexpr int DMAS = PM / kDmaRows / W;  // DMA instructions per wavefront per group
+    // W wavefronts of NBW 32-row operands each (8 operands, 256 rows, per workgroup), TB
+    // token blocks of 32
+    constexpr int NBW = 8 / W, TB = TM / 32;
+    constexpr int DMAS = TM / kDmaRows / W;  // DMA instructions per wavefront per group
+    constexpr int SB = TM * kStageRow;       // bytes of one activation stage
 
     const unsigned groups = k / 256, wtiles = (n + 15) / 16;
-    const unsigned m_tiles = (m + PM - 1) / PM, n_tiles = (wtiles + kTiles - 1) / kTiles;
+    const unsigned m_tiles = (m + TM - 1) / TM, n_tiles = (wtiles + kTiles - 1) / kTiles;
     // XCD-aware order: the M tiles of one weight tile (and K slice) run together on one
     // XCD (L2).
     const unsigned id = blockIdx.x, xcd = id % 8, local = id / 8;
@@ -434,9 +435,9 @@ __global__ __launch_bounds__(W * 64, 1) void gemm_kernel(const uint16_t* __restr
     if (local >= per_xcd || linear >= m_tiles * n_tiles * slices)
         return;
     const unsigned n_tile = linear / (m_tiles * slices);
-    const unsigned slice = (linear / m_tiles) % slices, m0 = (linear % m_tiles) * PM;
+    const unsigned slice = (linear / m_tiles) % slices, m0 = (linear % m_tiles) * TM;
     if (tile_expert) {
-        const int e = tile_expert[m0 / PM];
+        const int e = tile_expert[m0 / TM];
         if (e < 0)
             return;
         w += size_t(e) * expert_bytes;
@@ -476,7 +477,7 @@ __global__ __launch_bounds__(W * 64, 1) void gemm_kernel(const uint16_t* __restr
         const unsigned J = wave * DMAS + j;
         __builtin_amdgcn_global_load_lds(
             (global_void*)(xtile + size_t(g) * 512 + (J / 8) * (16 * row_pitch) + xlane[J % 8]),
-            (lds_void*)(lds + buf * kStageBytes + J * 1024), 16, 0, 0);
+            (lds_void*)(lds + buf * SB + J * 1024), 16, 0, 0);
     };
     constexpr int kLoads = DMAS + F::loads * NBW, kPerStep = 4;
     static_assert(kLoads <= 16 * kPerStep, "the loads must fit the group's sub-steps");
@@ -499,26 +500,26 @@ __global__ __launch_bounds__(W * 64, 1) void gemm_kernel(const uint16_t* __restr
         }
     };
 
-    f32x16 acc[NBW][4];
+    f32x16 acc[NBW][TB];
 #pragma unroll
     for (int c = 0; c < NBW; ++c)
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
+        for (int b = 0; b < TB; ++b)
             acc[c][b] = f32x16{};
 
     unsigned flags = 0;
     unsigned magic = 0x64006400u;  // kept in a VGPR: the mask-and-or takes one SGPR only
     asm volatile("" : "+v"(magic));
-    // 16 sub-steps per group, software-pipelined by one sub-step: while the 4 * NBW MFMAs
+    // 16 sub-steps per group, software-pipelined by one sub-step: while the TB * NBW MFMAs
     // of sub-step s run, the activation operands of s + 1 are read from LDS and its
     // weights dequantised; one MFMA, then up to four VALU ops / one LDS read / one load.
     auto compute = [&](unsigned buf, const Regs* rg, unsigned next_g, unsigned next_buf,
                        Regs* next_rg) {
-        const uint8_t* a = lds + buf * kStageBytes + r * kStageRow;
+        const uint8_t* a = lds + buf * SB + r * kStageRow;
         auto read_x = [&](int s, f16x8* xf) {
             const unsigned q = 16 * (s / 8) + 8 * h + 4 * ((s / 4) % 2) + s % 4;
 #pragma unroll
-            for (int b = 0; b < 4; ++b)
+            for (int b = 0; b < TB; ++b)
                 xf[b] = *reinterpret_cast<const f16x8*>(a + b * 32 * kStageRow +
                                                          16 * (q ^ (r % 16)));
         };
@@ -526,7 +527,7 @@ __global__ __launch_bounds__(W * 64, 1) void gemm_kernel(const uint16_t* __restr
 #pragma unroll
         for (int c = 0; c < NBW; ++c)
             sc[c].prepare(rg[c], ENC == KDQ_Q6_K ? r : h, flags);
-        f16x8 xf[2][4], wf[2][NBW];
+        f16x8 xf[2][TB], wf[2][NBW];
         read_x(0, xf[0]);
 #pragma unroll
         for (int c = 0; c < NBW; ++c)
@@ -544,17 +545,17 @@ __global__ __launch_bounds__(W * 64, 1) void gemm_kernel(const uint16_t* __restr
 #pragma unroll
             for (int c = 0; c < NBW; ++c)
 #pragma unroll
-                for (int b = 0; b < 4; ++b) {
+                for (int b = 0; b < TB; ++b) {
                     acc[c][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[s % 2][c], xf[s % 2][b],
                                                                        acc[c][b], 0, 0, 0);
                     if constexpr (NBW == 1)  // the MFMAs stay in their sub-step (else the
                         asm volatile("" : "+v"(acc[c][b]));  // compiler sinks them all)
                 }
 #pragma unroll
-            for (int q = 0; q < 4 * NBW; ++q) {
+            for (int q = 0; q < TB * NBW; ++q) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-                __builtin_amdgcn_sched_group_barrier(0x002, 8 / NBW, 0);  // 4 or 8 VALU
-                if (q < 4)
+                __builtin_amdgcn_sched_group_barrier(0x002, 32 / (TB * NBW), 0);  // VALU
+                if (q < TB)
                     __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
                 if (q < kPerStep)
                     __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
@@ -587,9 +588,9 @@ __global__ __launch_bounds__(W * 64, 1) void gemm_kernel(const uint16_t* __restr
     // Output tile through LDS (free after the K loop): D of operand c, token block b holds
     // token 32b + r and weight rows 8(v / 4) + 4h + v % 4 of the operand's 32; scaled
     // back by the token's sigma, written as [token][row] fp32, then stored as whole rows.
-    float sig[4];
+    float sig[TB];
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
+    for (int b = 0; b < TB; ++b) {
         const unsigned tok = m0 + 32 * b + r;
         sig[b] = tok < m ? sigma[tok] : 1.f;
     }
@@ -597,7 +598,7 @@ __global__ __launch_bounds__(W * 64, 1) void gemm_kernel(const uint16_t* __restr
 #pragma unroll
     for (int c = 0; c < NBW; ++c)
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
+        for (int b = 0; b < TB; ++b)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const unsigned row = (wave * NBW + c) * 32 + 8 * q + 4 * h;
@@ -608,7 +609,7 @@ __global__ __launch_bounds__(W * 64, 1) void gemm_kernel(const uint16_t* __restr
     __syncthreads();
     const unsigned f0 = n_tile * kTiles * 16;       // first weight row of the tile
     constexpr int kChunks = kTiles * 16 * 4 / 16;  // 16-byte chunks per token row
-    for (unsigned e = threadIdx.x; e < PM * kChunks; e += W * 64) {
+    for (unsigned e = threadIdx.x; e < TM * kChunks; e += W * 64) {
         const unsigned t = e / kChunks, ch = e % kChunks, tok = m0 + t, f = f0 + 4 * ch;
         if (tok >= m || f >= n)
             continue;
@@ -674,14 +675,22 @@ unsigned gemm_slice_depth(size_t m, size_t n, size_t k) {
 // tokens 125 -> 83 us with 8), else 4 (Q4_K and Q8_0 measured 2-4 % slower with 8).
 template <int ENC> constexpr int gemm_waves = ENC == KDQ_Q6_K ? 8 : 4;
 
+// Token tile of the grouped (MoE) form: an expert's rows are padded to whole tiles, and
+// experts average a few dozen rows in a prefill chunk, so its tiles are 64 tokens.
+constexpr int kGroupTM = int(kGroupedTileRows);
+
 template <int ENC>
 int configure() {
     static bool configured = false;  // one attribute call per instantiation
     if (!configured) {
         KDQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&stage_kernel<ENC>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024));
-        KDQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<ENC, gemm_waves<ENC>>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, int(kLds)));
+        KDQ_HIP(hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&gemm_kernel<ENC, gemm_waves<ENC>, PM>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, int(kLds)));
+        KDQ_HIP(hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&gemm_kernel<ENC, gemm_waves<ENC>, kGroupTM>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, int(gemm_lds<kGroupTM>)));
         configured = true;
     }
     return KDQ_OK;
@@ -699,9 +708,10 @@ int launch_grouped(const void* packed, size_t expert_bytes, const int32_t* tile_
                        unsigned(k), xs, sigma, inv, topk, used);
     KDQ_HIP(hipGetLastError());
     const size_t wtiles = (n + 15) / 16;
-    const size_t tiles = (positions / PM) * ((wtiles + kTiles - 1) / kTiles);
+    const size_t tiles = (positions / kGroupTM) * ((wtiles + kTiles - 1) / kTiles);
     const unsigned grid = unsigned((tiles + 7) / 8 * 8);
-    hipLaunchKernelGGL((gemm_kernel<ENC, gemm_waves<ENC>>), dim3(grid), dim3(gemm_waves<ENC> * 64), kLds, st, xs, sigma,
+    hipLaunchKernelGGL((gemm_kernel<ENC, gemm_waves<ENC>, kGroupTM>), dim3(grid),
+                       dim3(gemm_waves<ENC> * 64), gemm_lds<kGroupTM>, st, xs, sigma,
                        static_cast<const uint8_t*>(packed), unsigned(positions), unsigned(n),
                        unsigned(k), 1u, unsigned(k / 256), y, nullptr, status, tile_expert,
                        expert_bytes);
@@ -746,7 +756,7 @@ int launch_gemm(const float* x, const uint8_t* packed, size_t m, size_t n, size_
     const size_t wtiles = (n + 15) / 16;
     const size_t tiles = (m_pad / PM) * ((wtiles + kTiles - 1) / kTiles) * slices;
     const unsigned grid = unsigned((tiles + 7) / 8 * 8);
-    hipLaunchKernelGGL((gemm_kernel<ENC, gemm_waves<ENC>>), dim3(grid), dim3(gemm_waves<ENC> * 64), kLds, st, xs, sigma, packed,
+    hipLaunchKernelGGL((gemm_kernel<ENC, gemm_waves<ENC>, PM>), dim3(grid), dim3(gemm_waves<ENC> * 64), kLds, st, xs, sigma, packed,
                        unsigned(m), unsigned(n), unsigned(k), slices, per, y, part, status,
                        nullptr, size_t(0));
     KDQ_HIP(hipGetLastError());
@@ -815,7 +825,7 @@ int grouped_gemm(int encoding, const void* packed, size_t expert_bytes,
                  const int32_t* tile_expert, size_t n, size_t k, const float* x,
                  const int32_t* inv, unsigned topk, const unsigned* used, size_t positions,
                  float* y, unsigned* status, uint16_t* xs, float* sigma, hipStream_t st) {
-    if (!grouped_gemm_takes(encoding, k) || positions % PM)
+    if (!grouped_gemm_takes(encoding, k) || positions % kGroupTM)
         return KDQ_ERR_UNSUPPORTED;
     switch (encoding) {
     case KDQ_Q4_K:

@@ -187,11 +187,12 @@ __device__ __forceinline__ float sigmoid_of(float v) {
 // The MoE router of kdq_moe_route (softmax with a double total, top-k by probability,
 // weights renormalised by max(sum, 2^-14)) without the expert permutation.
 // Grouped prefill GEMM (gguf_gemm.hip): y[p, :] = W_{e(p)} x_p for positions p in token
-// tiles of 128 (positions a multiple of 128), tile t's weights expert tile_expert[t] of a
+// tiles of kGroupedTileRows (positions a multiple of it), tile t's weights expert tile_expert[t] of a
 // stack of tile-packed experts expert_bytes apart (tiles with a negative entry skipped);
 // x_p = x[inv[p] / topk] (zero rows where inv[p] < 0), rows from *used on unstaged.
 // xs (positions * k * 2 bytes) and sigma (positions * 4) are the caller's scratch.
 // Q4_K / Q8_0 / Q6_K, k % 256 == 0, k <= 32768.
+constexpr unsigned kGroupedTileRows = 64;
 bool grouped_gemm_takes(int encoding, size_t k);
 int grouped_gemm(int encoding, const void* packed, size_t expert_bytes,
                  const int32_t* tile_expert, size_t n, size_t k, const float* x,

@@ -71,7 +71,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* down, const f
 
 constexpr size_t kSlotRows = 8;          // batches up to this many rows run per slot
 constexpr unsigned kItemRows = 8;        // rows of a grouped item (the MFMA GEMV's batch)
-constexpr unsigned kTileRows = 128;      // rows of a grouped GEMM token tile
+constexpr unsigned kTileRows = kGroupedTileRows;  // rows of a grouped GEMM token tile
 constexpr size_t kMaxGroupedSlots = 8192;
 constexpr size_t kSharedGemmRows = 64;   // batches from this many rows run the shared
                                          // expert on the prefill GEMM
@@ -307,7 +307,7 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
     // (slots padded per expert to whole items), plus x in position order, the slot and
     // position maps, the items' experts and the count of positions in use
     // (grouped on the GEMM: token tiles of kTileRows, the packed expert stacks, fp16 x)
-    // the grouped GEMM pads every expert's rows to 128-row token tiles: it pays once the
+    // the grouped GEMM pads every expert's rows to 64-row token tiles: it pays once the
     // experts average 16 rows or more; fewer (a 64-token chunk spreads 512 slots over 128
     // experts) run as 8-row GEMV items, which read each expert's weights about once
     const bool dense = slots >= 16 * E;
@@ -437,7 +437,7 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
         KDQ_HIP(hipGetLastError());
     }
     if (grouped) {
-        // 4'. slots grouped by expert into padded segments (8-row items, 128-row tiles)
+        // 4'. slots grouped by expert into padded segments (8-row items, 64-row tiles)
         hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, st, idx, unsigned(slots),
                            unsigned(E), unsigned(pad), unsigned(items), pos, inv, item_expert,
                            tile_expert, used, gemm_status);
