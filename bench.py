@@ -511,8 +511,8 @@ def bench_moe_gguf(torch, rows, reps=10, count=64, resident=False):
     nbytes = per_call * expert + shared + E * H * 4 + H * 4 + 2 * rows * H * 4
     gbs = nbytes / (ms * 1e-3) / 1e9
     path = ("every slot's expert GEMV" if rows <= 8 else
-            "slots grouped by expert into 8-row items" if rows * 8 < 16 * 128 else
-            "slots grouped by expert into 128-row tiles of the prefill GEMM")
+            "slots grouped by expert into 8-row items" if rows * 8 < 4 * 128 else
+            "slots grouped by expert into 64-row tiles of the prefill GEMM")
     if resident:
         path += "; expert stacks and shared matrices resident in the tile-packed form"
     return {"workload": f"GGUF MoE layer (Qwen3-30B-A3B geometry) rows={rows} ({path})",
@@ -721,6 +721,8 @@ def main():
             extra["moe_gguf_t4"] = bench_moe_gguf(torch, 4)
         if want("moe_gguf_t64"):
             extra["moe_gguf_t64"] = bench_moe_gguf(torch, 64, count=16)
+        if want("moe_gguf_t64_resident"):
+            extra["moe_gguf_t64_resident"] = bench_moe_gguf(torch, 64, count=16, resident=True)
         if want("moe_gguf_t512"):
             extra["moe_gguf_t512"] = bench_moe_gguf(torch, 512, reps=5, count=8)
         if want("moe_gguf_t512_resident"):

@@ -73,8 +73,10 @@ constexpr size_t kSlotRows = 8;          // batches up to this many rows run per
 constexpr unsigned kItemRows = 8;        // rows of a grouped item (the MFMA GEMV's batch)
 constexpr unsigned kTileRows = kGroupedTileRows;  // rows of a grouped GEMM token tile
 constexpr size_t kMaxGroupedSlots = 8192;
-constexpr size_t kSharedGemmRows = 64;   // batches from this many rows run the shared
-                                         // expert on the prefill GEMM
+// Batches from this many rows run the shared expert on the prefill GEMM (its launches
+// cost more than the 8-row items below that: measured at 64 rows 33 us slower, at 512
+// rows 65 us faster)
+constexpr size_t kSharedGemmRows = 256;
 
 // Slots by expert into segments padded to multiples of `pad` (kItemRows, or kTileRows when
 // a projection runs on the grouped GEMM): pos[s] (slot -> position), inv[p] (position ->
@@ -307,10 +309,12 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
     // (slots padded per expert to whole items), plus x in position order, the slot and
     // position maps, the items' experts and the count of positions in use
     // (grouped on the GEMM: token tiles of kTileRows, the packed expert stacks, fp16 x)
-    // the grouped GEMM pads every expert's rows to 64-row token tiles: it pays once the
-    // experts average 16 rows or more; fewer (a 64-token chunk spreads 512 slots over 128
-    // experts) run as 8-row GEMV items, which read each expert's weights about once
-    const bool dense = slots >= 16 * E;
+    // the grouped GEMM pads every expert's rows to 64-row token tiles; it pays once the
+    // experts average 4 rows or more (a 64-token top-8 chunk over 128 experts: 559 us
+    // against 564 on 8-row GEMV items per call, 315 against 597 over checked resident
+    // copies); sparser batches run as 8-row GEMV items, which read each expert's weights
+    // about once
+    const bool dense = slots >= 4 * E;
     const bool gemm_gu = grouped && dense && gemm_stack(L.gate_exps, F, H) &&
                          gemm_stack(L.up_exps, F, H);
     const bool gemm_dn = grouped && dense && gemm_stack(L.down_exps, H, F);
