@@ -410,12 +410,19 @@ __global__ __launch_bounds__(256) void stage_kernel(const float* __restrict__ x,
 // TM = 64 (the grouped form's token tiles: experts average a few dozen rows) halves the
 // token tile: two token blocks per operand, two workgroups per compute unit (Q8_0: one;
 // at two its registers spill).
-template <int ENC, int W, int TM>
+//
+// PAIR (grouped, four wavefronts): a workgroup takes 128 output rows of two matrices
+// stored alike, `w` (gate) and `w2` (up); wavefront w's operand 0 is gate rows
+// 32w .. 32w + 31 of the tile and operand 1 the same rows of up, and the epilogue writes
+// silu(gate) * up (the reference's silu, on the scaled-back fp32 values) — one staging
+// of x and no SwiGLU pass, the same bits as the two products and the pass.
+template <int ENC, int W, int TM, bool PAIR = false>
 __global__ __launch_bounds__(W * 64, TM == PM || ENC == KDQ_Q8_0 ? 1 : 2) void gemm_kernel(
     const uint16_t* __restrict__ xs, const float* __restrict__ sigma,
     const uint8_t* __restrict__ w, unsigned m, unsigned n, unsigned k, unsigned slices,
     unsigned per, float* __restrict__ y, float* __restrict__ part, unsigned* __restrict__ status,
-    const int32_t* __restrict__ tile_expert, size_t expert_bytes) {
+    const int32_t* __restrict__ tile_expert, size_t expert_bytes,
+    const uint8_t* __restrict__ w2 = nullptr) {
     using F = GemmFormat<ENC>;
     using Regs = typename F::Regs;
     extern __shared__ __align__(16) uint8_t lds[];
@@ -424,9 +431,11 @@ __global__ __launch_bounds__(W * 64, TM == PM || ENC == KDQ_Q8_0 ? 1 : 2) void g
     constexpr int NBW = 8 / W, TB = TM / 32;
     constexpr int DMAS = TM / kDmaRows / W;  // DMA instructions per wavefront per group
     constexpr int SB = TM * kStageRow;       // bytes of one activation stage
+    static_assert(!PAIR || NBW == 2, "a pair is two operands of one wavefront");
+    constexpr int TILES = PAIR ? kTiles / 2 : kTiles;  // 16-row output tiles per workgroup
 
     const unsigned groups = k / 256, wtiles = (n + 15) / 16;
-    const unsigned m_tiles = (m + TM - 1) / TM, n_tiles = (wtiles + kTiles - 1) / kTiles;
+    const unsigned m_tiles = (m + TM - 1) / TM, n_tiles = (wtiles + TILES - 1) / TILES;
     // XCD-aware order: the M tiles of one weight tile (and K slice) run together on one
     // XCD (L2).
     const unsigned id = blockIdx.x, xcd = id % 8, local = id / 8;
@@ -441,6 +450,8 @@ __global__ __launch_bounds__(W * 64, TM == PM || ENC == KDQ_Q8_0 ? 1 : 2) void g
         if (e < 0)
             return;
         w += size_t(e) * expert_bytes;
+        if constexpr (PAIR)
+            w2 += size_t(e) * expert_bytes;
     }
     // slices = ceil(groups / per), so every slice has at least one group
     const unsigned g_begin = slice * per, g_end = min(groups, g_begin + per);
@@ -453,11 +464,13 @@ __global__ __launch_bounds__(W * 64, TM == PM || ENC == KDQ_Q8_0 ? 1 : 2) void g
 
     // operand c = tiles tile0 + 2c (rows 0-15) and tile0 + 2c + 1 (rows 16-31); tiles
     // past the end load the last tile, and their results are never stored
-    const unsigned tile0 = n_tile * kTiles + wave * 2 * NBW;
+    const unsigned tile0 = n_tile * TILES + wave * 2 * (PAIR ? 1 : NBW);
     const uint8_t* base[NBW];
 #pragma unroll
     for (int c = 0; c < NBW; ++c)
-        base[c] = w + size_t(min(tile0 + 2 * c + r / 16, wtiles - 1)) * groups * F::unit +
+        base[c] = (PAIR && c == 1 ? w2 : w) +
+                  size_t(min(tile0 + (PAIR ? 0 : 2 * c) + r / 16, wtiles - 1)) * groups *
+                      F::unit +
                   16 * (16 * h + r % 16);
     auto load_weight = [&](unsigned g, Regs* rg, int i) {
         load_item<ENC>(base[i / F::loads], size_t(g) * F::unit, h, r, rg[i / F::loads],
@@ -595,20 +608,35 @@ __global__ __launch_bounds__(W * 64, TM == PM || ENC == KDQ_Q8_0 ? 1 : 2) void g
         sig[b] = tok < m ? sigma[tok] : 1.f;
     }
     __syncthreads();  // every wavefront is done reading the activation stages
-#pragma unroll
-    for (int c = 0; c < NBW; ++c)
+    if constexpr (PAIR) {
 #pragma unroll
         for (int b = 0; b < TB; ++b)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const unsigned row = (wave * NBW + c) * 32 + 8 * q + 4 * h;
+                const unsigned row = wave * 32 + 8 * q + 4 * h;
+                float v[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    v[i] = silu_of(acc[0][b][4 * q + i] * sig[b]) * (acc[1][b][4 * q + i] * sig[b]);
                 *reinterpret_cast<float4*>(lds + (32 * b + r) * kOutPitch + 4 * row) =
-                    make_float4(acc[c][b][4 * q] * sig[b], acc[c][b][4 * q + 1] * sig[b],
-                                acc[c][b][4 * q + 2] * sig[b], acc[c][b][4 * q + 3] * sig[b]);
+                    make_float4(v[0], v[1], v[2], v[3]);
             }
+    } else {
+#pragma unroll
+        for (int c = 0; c < NBW; ++c)
+#pragma unroll
+            for (int b = 0; b < TB; ++b)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const unsigned row = (wave * NBW + c) * 32 + 8 * q + 4 * h;
+                    *reinterpret_cast<float4*>(lds + (32 * b + r) * kOutPitch + 4 * row) =
+                        make_float4(acc[c][b][4 * q] * sig[b], acc[c][b][4 * q + 1] * sig[b],
+                                    acc[c][b][4 * q + 2] * sig[b], acc[c][b][4 * q + 3] * sig[b]);
+                }
+    }
     __syncthreads();
-    const unsigned f0 = n_tile * kTiles * 16;       // first weight row of the tile
-    constexpr int kChunks = kTiles * 16 * 4 / 16;  // 16-byte chunks per token row
+    const unsigned f0 = n_tile * TILES * 16;       // first weight row of the tile
+    constexpr int kChunks = TILES * 16 * 4 / 16;  // 16-byte chunks per token row
     for (unsigned e = threadIdx.x; e < TM * kChunks; e += W * 64) {
         const unsigned t = e / kChunks, ch = e % kChunks, tok = m0 + t, f = f0 + 4 * ch;
         if (tok >= m || f >= n)
@@ -691,16 +719,23 @@ int configure() {
         KDQ_HIP(hipFuncSetAttribute(
             reinterpret_cast<const void*>(&gemm_kernel<ENC, gemm_waves<ENC>, kGroupTM>),
             hipFuncAttributeMaxDynamicSharedMemorySize, int(gemm_lds<kGroupTM>)));
+        if constexpr (gemm_waves<ENC> == 4)
+            KDQ_HIP(hipFuncSetAttribute(
+                reinterpret_cast<const void*>(&gemm_kernel<ENC, 4, kGroupTM, true>),
+                hipFuncAttributeMaxDynamicSharedMemorySize, int(gemm_lds<kGroupTM>)));
         configured = true;
     }
     return KDQ_OK;
 }
 
+// Grouped form: x staged through the position -> slot map, then one GEMM launch over the
+// token tiles; `up` given (four-wavefront encodings): the paired launch writing
+// silu(gate x) * (up x).
 template <int ENC>
-int launch_grouped(const void* packed, size_t expert_bytes, const int32_t* tile_expert, size_t n,
-                   size_t k, const float* x, const int32_t* inv, unsigned topk,
-                   const unsigned* used, size_t positions, float* y, unsigned* status,
-                   uint16_t* xs, float* sigma, hipStream_t st) {
+int launch_grouped(const void* packed, const void* up, size_t expert_bytes,
+                   const int32_t* tile_expert, size_t n, size_t k, const float* x,
+                   const int32_t* inv, unsigned topk, const unsigned* used, size_t positions,
+                   float* y, unsigned* status, uint16_t* xs, float* sigma, hipStream_t st) {
     int rc;
     if ((rc = configure<ENC>()))
         return rc;
@@ -708,13 +743,28 @@ int launch_grouped(const void* packed, size_t expert_bytes, const int32_t* tile_
                        unsigned(k), xs, sigma, inv, topk, used);
     KDQ_HIP(hipGetLastError());
     const size_t wtiles = (n + 15) / 16;
+    const auto* w = static_cast<const uint8_t*>(packed);
+    if (up) {
+        if constexpr (gemm_waves<ENC> == 4) {
+            constexpr size_t pair_tiles = kTiles / 2;
+            const size_t tiles = (positions / kGroupTM) * ((wtiles + pair_tiles - 1) / pair_tiles);
+            hipLaunchKernelGGL((gemm_kernel<ENC, 4, kGroupTM, true>),
+                               dim3(unsigned((tiles + 7) / 8 * 8)), dim3(4 * 64),
+                               gemm_lds<kGroupTM>, st, xs, sigma, w, unsigned(positions),
+                               unsigned(n), unsigned(k), 1u, unsigned(k / 256), y, nullptr,
+                               status, tile_expert, expert_bytes,
+                               static_cast<const uint8_t*>(up));
+            KDQ_HIP(hipGetLastError());
+            return KDQ_OK;
+        }
+        return KDQ_ERR_UNSUPPORTED;
+    }
     const size_t tiles = (positions / kGroupTM) * ((wtiles + kTiles - 1) / kTiles);
     const unsigned grid = unsigned((tiles + 7) / 8 * 8);
     hipLaunchKernelGGL((gemm_kernel<ENC, gemm_waves<ENC>, kGroupTM>), dim3(grid),
-                       dim3(gemm_waves<ENC> * 64), gemm_lds<kGroupTM>, st, xs, sigma,
-                       static_cast<const uint8_t*>(packed), unsigned(positions), unsigned(n),
-                       unsigned(k), 1u, unsigned(k / 256), y, nullptr, status, tile_expert,
-                       expert_bytes);
+                       dim3(gemm_waves<ENC> * 64), gemm_lds<kGroupTM>, st, xs, sigma, w,
+                       unsigned(positions), unsigned(n), unsigned(k), 1u, unsigned(k / 256), y,
+                       nullptr, status, tile_expert, expert_bytes, nullptr);
     KDQ_HIP(hipGetLastError());
     return KDQ_OK;
 }
@@ -824,20 +874,26 @@ bool grouped_gemm_takes(int encoding, size_t k) {
 int grouped_gemm(int encoding, const void* packed, size_t expert_bytes,
                  const int32_t* tile_expert, size_t n, size_t k, const float* x,
                  const int32_t* inv, unsigned topk, const unsigned* used, size_t positions,
-                 float* y, unsigned* status, uint16_t* xs, float* sigma, hipStream_t st) {
-    if (!grouped_gemm_takes(encoding, k) || positions % kGroupTM)
+                 float* y, unsigned* status, uint16_t* xs, float* sigma, hipStream_t st,
+                 const void* up) {
+    if (!grouped_gemm_takes(encoding, k) || positions % kGroupTM ||
+        (up && !grouped_gemm_pairs(encoding)))
         return KDQ_ERR_UNSUPPORTED;
     switch (encoding) {
     case KDQ_Q4_K:
-        return launch_grouped<KDQ_Q4_K>(packed, expert_bytes, tile_expert, n, k, x, inv, topk,
-                                        used, positions, y, status, xs, sigma, st);
+        return launch_grouped<KDQ_Q4_K>(packed, up, expert_bytes, tile_expert, n, k, x, inv,
+                                        topk, used, positions, y, status, xs, sigma, st);
     case KDQ_Q8_0:
-        return launch_grouped<KDQ_Q8_0>(packed, expert_bytes, tile_expert, n, k, x, inv, topk,
-                                        used, positions, y, status, xs, sigma, st);
+        return launch_grouped<KDQ_Q8_0>(packed, up, expert_bytes, tile_expert, n, k, x, inv,
+                                        topk, used, positions, y, status, xs, sigma, st);
     default:
-        return launch_grouped<KDQ_Q6_K>(packed, expert_bytes, tile_expert, n, k, x, inv, topk,
-                                        used, positions, y, status, xs, sigma, st);
+        return launch_grouped<KDQ_Q6_K>(packed, up, expert_bytes, tile_expert, n, k, x, inv,
+                                        topk, used, positions, y, status, xs, sigma, st);
     }
+}
+
+bool grouped_gemm_pairs(int encoding) {
+    return encoding == KDQ_Q4_K || encoding == KDQ_Q8_0;
 }
 
 }  // namespace kdq

@@ -194,10 +194,15 @@ __device__ __forceinline__ float sigmoid_of(float v) {
 // Q4_K / Q8_0 / Q6_K, k % 256 == 0, k <= 32768.
 constexpr unsigned kGroupedTileRows = 64;
 bool grouped_gemm_takes(int encoding, size_t k);
+// `up` (another stack stored alike; grouped_gemm_pairs(encoding)): one launch writing
+// y = silu(W_gate x) * (W_up x) with the reference's silu, bit-identical to the two
+// products followed by that SwiGLU.
 int grouped_gemm(int encoding, const void* packed, size_t expert_bytes,
                  const int32_t* tile_expert, size_t n, size_t k, const float* x,
                  const int32_t* inv, unsigned topk, const unsigned* used, size_t positions,
-                 float* y, unsigned* status, uint16_t* xs, float* sigma, hipStream_t st);
+                 float* y, unsigned* status, uint16_t* xs, float* sigma, hipStream_t st,
+                 const void* up = nullptr);
+bool grouped_gemm_pairs(int encoding);
 int route_selection(const float* logits, size_t tokens, size_t experts, size_t top_k,
                     int32_t* idx, float* w, hipStream_t stream);
 // Dense prefill GEMM over one tile-packed matrix (kdq_gemm_packed's product) with the

@@ -505,17 +505,28 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
                                      L.gate_exps.row_bytes, H, E * F, packed_gate, st))) ||
                 (!pk.up_exps &&
                  (rc = kdq_gguf_pack(L.up_exps.encoding, L.up_exps.weights, L.up_exps.row_bytes,
-                                     H, E * F, packed_up, st))) ||
-                (rc = grouped_gemm(L.gate_exps.encoding, packed_gate, gu_bytes, tile_expert, F,
-                                   H, x, inv, unsigned(K), used, positions, g, gemm_status, xs,
-                                   sigma, st)) ||
-                (rc = grouped_gemm(L.up_exps.encoding, packed_up, up_bytes, tile_expert, F, H,
-                                   x, inv, unsigned(K), used, positions, u, gemm_status, xs,
-                                   sigma, st)))
+                                     H, E * F, packed_up, st))))
                 return rc;
-            hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((positions * F + 255) / 256)),
-                               dim3(256), 0, st, g, u, positions * F, used, unsigned(F), inv);
-            KDQ_HIP(hipGetLastError());
+            if (same_layout(L.gate_exps, L.up_exps) &&
+                grouped_gemm_pairs(L.gate_exps.encoding)) {
+                // one paired launch: x staged once, h = silu(gate) * up in its epilogue
+                if ((rc = grouped_gemm(L.gate_exps.encoding, packed_gate, gu_bytes, tile_expert,
+                                       F, H, x, inv, unsigned(K), used, positions, g,
+                                       gemm_status, xs, sigma, st, packed_up)))
+                    return rc;
+            } else {
+                if ((rc = grouped_gemm(L.gate_exps.encoding, packed_gate, gu_bytes, tile_expert,
+                                       F, H, x, inv, unsigned(K), used, positions, g,
+                                       gemm_status, xs, sigma, st)) ||
+                    (rc = grouped_gemm(L.up_exps.encoding, packed_up, up_bytes, tile_expert, F,
+                                       H, x, inv, unsigned(K), used, positions, u, gemm_status,
+                                       xs, sigma, st)))
+                    return rc;
+                hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((positions * F + 255) / 256)),
+                                   dim3(256), 0, st, g, u, positions * F, used, unsigned(F),
+                                   inv);
+                KDQ_HIP(hipGetLastError());
+            }
         } else if ((rc = items_gate_up())) {
             return rc;
         }

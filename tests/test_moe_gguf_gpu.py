@@ -288,3 +288,22 @@ def test_moe_gguf_shared_gemm_nonfinite_status(device):
     ops.moe_gguf(to_device(torch, device, spec), torch.ones(rows, H, device=device),
                  status=status)
     assert int(status.item()) & 1
+
+
+def test_moe_gguf_paired_gemm_bit_identical(device):
+    """Gate and up stored alike run as one paired grouped GEMM whose epilogue applies the
+    SwiGLU; the same weights with the up rows stored 16 bytes apart (another layout) run
+    as two GEMMs and the SwiGLU pass.  Both give the same bits (200 rows, MIXED)."""
+    import torch
+    H, E, K, F, S, rows = 512, 16, 8, 256, 512, 200
+    spec = make_layer(19, H, E, K, F, S, MIXED)
+    enc, arr = spec["up_exps"]
+    padded = np.zeros(arr.shape[:-1] + (arr.shape[-1] + 16,), np.uint8)
+    padded[..., :arr.shape[-1]] = arr
+    other = dict(spec, up_exps=(enc, padded))
+    from kadan_amd import ops
+    x = torch.from_numpy(synth.normal(20, 1, rows * H).reshape(rows, H)).to(device)
+    y, sel, _ = ops.moe_gguf(to_device(torch, device, spec), x)
+    y2, sel2, _ = ops.moe_gguf(to_device(torch, device, other), x)
+    assert np.array_equal(sel.cpu().numpy(), sel2.cpu().numpy())
+    assert np.array_equal(y.cpu().numpy(), y2.cpu().numpy())
