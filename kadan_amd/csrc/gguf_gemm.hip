@@ -866,6 +866,36 @@ int dense_gemm(int encoding, const void* packed, size_t n, size_t k, const float
     }
 }
 
+int dense_gemm_pair(int encoding, const void* gate, const void* up, size_t n, size_t k,
+                    const float* x, size_t m, float* y, unsigned* status, void* scratch,
+                    hipStream_t st) {
+    if (!grouped_gemm_takes(encoding, k) || !grouped_gemm_pairs(encoding))
+        return KDQ_ERR_UNSUPPORTED;
+    auto* sc = static_cast<uint8_t*>(scratch);
+    const GemmScratch g = gemm_scratch(m, n, k);  // covers m rounded up to 128 rows
+    auto launch = [&](auto kernel, auto stage) -> int {
+        int rc;
+        if ((rc = encoding == KDQ_Q4_K ? configure<KDQ_Q4_K>() : configure<KDQ_Q8_0>()))
+            return rc;
+        auto* xs = reinterpret_cast<uint16_t*>(sc);
+        auto* sigma = reinterpret_cast<float*>(sc + g.xs);
+        hipLaunchKernelGGL(stage, dim3(unsigned(m)), dim3(256), k * 4, st, x, unsigned(k), xs,
+                           sigma, nullptr, 1u, nullptr);
+        KDQ_HIP(hipGetLastError());
+        const size_t tiles = (m + kGroupTM - 1) / kGroupTM * (((n + 15) / 16 + 7) / 8);
+        hipLaunchKernelGGL(kernel, dim3(unsigned((tiles + 7) / 8 * 8)), dim3(4 * 64),
+                           gemm_lds<kGroupTM>, st, xs, sigma, static_cast<const uint8_t*>(gate),
+                           unsigned(m), unsigned(n), unsigned(k), 1u, unsigned(k / 256), y,
+                           nullptr, status, nullptr, size_t(0),
+                           static_cast<const uint8_t*>(up));
+        KDQ_HIP(hipGetLastError());
+        return KDQ_OK;
+    };
+    return encoding == KDQ_Q4_K
+               ? launch(gemm_kernel<KDQ_Q4_K, 4, kGroupTM, true>, stage_kernel<KDQ_Q4_K>)
+               : launch(gemm_kernel<KDQ_Q8_0, 4, kGroupTM, true>, stage_kernel<KDQ_Q8_0>);
+}
+
 bool grouped_gemm_takes(int encoding, size_t k) {
     return (encoding == KDQ_Q4_K || encoding == KDQ_Q8_0 || encoding == KDQ_Q6_K) &&
            k % 256 == 0 && k <= 32768;

@@ -208,6 +208,12 @@ int route_selection(const float* logits, size_t tokens, size_t experts, size_t t
 // Dense prefill GEMM over one tile-packed matrix (kdq_gemm_packed's product) with the
 // caller's scratch of dense_gemm_scratch(m, n, k) bytes: y[m x n] = x[m x k] W^T.
 size_t dense_gemm_scratch(size_t m, size_t n, size_t k);
+// y[m x n] = silu(x Wg^T) * (x Wu^T) for two tile-packed matrices stored alike
+// (grouped_gemm_pairs(encoding)), one launch on 64-token tiles, no K slices; the same
+// scratch as dense_gemm.
+int dense_gemm_pair(int encoding, const void* gate, const void* up, size_t n, size_t k,
+                    const float* x, size_t m, float* y, unsigned* status, void* scratch,
+                    hipStream_t st);
 int dense_gemm(int encoding, const void* packed, size_t n, size_t k, const float* x, size_t m,
                float* y, unsigned* status, void* scratch, hipStream_t st);
 

@@ -457,15 +457,24 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
                                      L.up_shexp.row_bytes, H, S, part[22], st))) ||
                 (!pk.down_shexp &&
                  (rc = kdq_gguf_pack(L.down_shexp.encoding, L.down_shexp.weights,
-                                     L.down_shexp.row_bytes, S, H, part[23], st))) ||
-                (rc = dense_gemm(L.gate_shexp.encoding, sh_gate, S, H, x, rows, sg, gemm_status,
-                                 sh_work, st)) ||
-                (rc = dense_gemm(L.up_shexp.encoding, sh_up, S, H, x, rows, su, gemm_status,
-                                 sh_work, st)))
+                                     L.down_shexp.row_bytes, S, H, part[23], st))))
                 return rc;
-            hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((rows * S + 255) / 256)), dim3(256),
-                               0, st, sg, su, rows * S, nullptr, 1u, nullptr);
-            KDQ_HIP(hipGetLastError());
+            if (same_layout(L.gate_shexp, L.up_shexp) &&
+                grouped_gemm_pairs(L.gate_shexp.encoding)) {
+                // one paired launch writing silu(gate) * up
+                if ((rc = dense_gemm_pair(L.gate_shexp.encoding, sh_gate, sh_up, S, H, x, rows,
+                                          sg, gemm_status, sh_work, st)))
+                    return rc;
+            } else {
+                if ((rc = dense_gemm(L.gate_shexp.encoding, sh_gate, S, H, x, rows, sg,
+                                     gemm_status, sh_work, st)) ||
+                    (rc = dense_gemm(L.up_shexp.encoding, sh_up, S, H, x, rows, su, gemm_status,
+                                     sh_work, st)))
+                    return rc;
+                hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((rows * S + 255) / 256)),
+                                   dim3(256), 0, st, sg, su, rows * S, nullptr, 1u, nullptr);
+                KDQ_HIP(hipGetLastError());
+            }
         }
         const size_t xs8 = kItemRows * H, fs8 = kItemRows * F;
         // the expert products on the GEMV items (every encoding; the fallback of the GEMM)

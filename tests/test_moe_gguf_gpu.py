@@ -291,16 +291,19 @@ def test_moe_gguf_shared_gemm_nonfinite_status(device):
 
 
 def test_moe_gguf_paired_gemm_bit_identical(device):
-    """Gate and up stored alike run as one paired grouped GEMM whose epilogue applies the
-    SwiGLU; the same weights with the up rows stored 16 bytes apart (another layout) run
-    as two GEMMs and the SwiGLU pass.  Both give the same bits (200 rows, MIXED)."""
+    """Gate and up stored alike run as one paired GEMM whose epilogue applies the SwiGLU
+    (the experts' grouped GEMM and, from 256 rows, the shared expert's dense one); the
+    same weights with the up rows stored 16 bytes apart (another layout) run as two GEMMs
+    and the SwiGLU pass.  Both give the same bits (256 rows, MIXED)."""
     import torch
-    H, E, K, F, S, rows = 512, 16, 8, 256, 512, 200
+    H, E, K, F, S, rows = 512, 16, 8, 256, 512, 256
     spec = make_layer(19, H, E, K, F, S, MIXED)
-    enc, arr = spec["up_exps"]
-    padded = np.zeros(arr.shape[:-1] + (arr.shape[-1] + 16,), np.uint8)
-    padded[..., :arr.shape[-1]] = arr
-    other = dict(spec, up_exps=(enc, padded))
+    other = dict(spec)
+    for name in ("up_exps", "up_shexp"):
+        enc, arr = spec[name]
+        padded = np.zeros(arr.shape[:-1] + (arr.shape[-1] + 16,), np.uint8)
+        padded[..., :arr.shape[-1]] = arr
+        other[name] = (enc, padded)
     from kadan_amd import ops
     x = torch.from_numpy(synth.normal(20, 1, rows * H).reshape(rows, H)).to(device)
     y, sel, _ = ops.moe_gguf(to_device(torch, device, spec), x)
