@@ -1415,16 +1415,20 @@ struct MfmaJobs {
 // data and their results discarded), so waits count exactly.  Order: this thread's first
 // activation unit, the first units' packed weights, then the staging.
 //
-// FORM 0 is the general kernel.  PLAIN launches (FORM 1 and 2: no device-side expert
+// FORM 0 is the general kernel.  PLAIN launches (FORM 1, 2 and 3: no device-side expert
 // index, no affine batch, no pairing: every decode product of kdq_gemv / kdq_gemv_batch)
 // take job blockIdx.y as it stands; the MoE forms carry those fields (measured: the plain
 // C2 launch 8.29 -> 7.77 us without them).  FORM 2, for inputs of more than 8 values a
 // thread, requests a thread's second activation unit together with its first, before the
 // weights (C2 down 14336 -> 4096: 9.54 -> 9.29 us; the same test in FORM 1's code made
-// the one-unit launches 0.1-0.3 us slower, hence a form of its own).
+// the one-unit launches 0.1-0.3 us slower, hence a form of its own).  FORM 3, for
+// workgroups of several row tiles: every wavefront's activation request is issued before
+// any wavefront's weight requests (one barrier between them), so the staging's data does
+// not return behind other wavefronts' weights (C2 4096 -> 14336: 7.95 -> 7.77 us; with
+// one tile a workgroup, C1, it measured 0.35 us slower).
 template <int ENC, int R, int W, bool PACKED, int FORM>
 __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
-    constexpr bool PLAIN = FORM > 0, X2 = FORM == 2;
+    constexpr bool PLAIN = FORM > 0, X2 = FORM == 2, XFIRST = FORM == 3;
     const bool affine = !PLAIN && jobs.affine;
     const unsigned jid = affine ? 0 : blockIdx.y, step = affine ? blockIdx.y : 0;
     const MfmaJob& jb = jobs.job[jid];
@@ -1524,6 +1528,10 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
     }
     asm volatile("" ::: "memory");  // x is not restrict: its loads stay before this point
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (XFIRST) {
+        __builtin_amdgcn_s_barrier();  // every wavefront's x request ahead of any weight request
+        __builtin_amdgcn_sched_barrier(0);
+    }
     Lane L[kUnits];
     load_units(r0, UnitCursor{wave, 0}, L);
     asm volatile("" ::: "memory");
@@ -1810,8 +1818,10 @@ int launch_mfma_form(const MfmaJobs& jobs, hipStream_t stream) {
     return KDQ_OK;
 }
 
-// Plain launches (no job with a device index, not affine, not paired) run the lean form,
-// and with 16 wavefronts and more than 8 input values a thread its two-unit staging.
+// Plain launches (no job with a device index, not affine, not paired) run the lean form:
+// with 16 wavefronts and more than 8 input values a thread its two-unit staging, with
+// 16 wavefronts and workgroups of 32 rows or more its activation-first form (not Q6_K,
+// which measured 0.1-0.2 us slower with it).
 template <int ENC, int R, int W, bool PACKED>
 int launch_mfma_shape(const MfmaJobs& jobs, hipStream_t stream) {
     bool plain = !jobs.affine && jobs.mats != 2;
@@ -1819,9 +1829,13 @@ int launch_mfma_shape(const MfmaJobs& jobs, hipStream_t stream) {
         plain = jobs.job[k].index == nullptr;
     if (!plain)
         return launch_mfma_form<ENC, R, W, PACKED, 0>(jobs, stream);
-    if constexpr (W == 16)
+    if constexpr (W == 16) {
         if (size_t(R) * jobs.in / 8 > size_t(W) * 64)
             return launch_mfma_form<ENC, R, W, PACKED, 2>(jobs, stream);
+        if constexpr (ENC != KDQ_Q6_K)
+            if (jobs.rows_per_wg >= 32)
+                return launch_mfma_form<ENC, R, W, PACKED, 3>(jobs, stream);
+    }
     return launch_mfma_form<ENC, R, W, PACKED, 1>(jobs, stream);
 }
 
