@@ -270,7 +270,14 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
 // calls it); also the work items.
 // Also slot_row[r] = item * kItemRows + row of the slot at position r (the K-sliced
 // finalize runs over occupied rows only).
+// With heavy_first, work items are numbered heavy first: every item of more than
+// kTileRows rows (two activation tiles, twice the MFMAs of a one-tile item), by expert,
+// then the one-tile items.  The grouped GEMMs' workgroups are dispatched in item order,
+// so the two-tile ones start first and spread over the compute units instead of landing
+// together (C4 T=256, every workgroup resident at once: 149 -> 144 us).  Otherwise
+// items follow the experts (C5, several rounds of workgroups: 689 against 704 us).
 __device__ __forceinline__ void permute_slots(const int32_t* __restrict__ idx, unsigned slots,
+                                              bool heavy_first,
                                               unsigned experts, int32_t* __restrict__ offsets,
                                               int32_t* __restrict__ perm,
                                               int32_t* __restrict__ items,
@@ -278,7 +285,8 @@ __device__ __forceinline__ void permute_slots(const int32_t* __restrict__ idx, u
                                               int32_t* __restrict__ position,
                                               int32_t* __restrict__ slot_row) {
     __shared__ int counts[kMaxExperts], base[kMaxExperts], segment[kMaxExperts],
-        item_base[kMaxExperts];
+        heavy_base[kMaxExperts], light_base[kMaxExperts];
+    __shared__ int heavy_total;
     __shared__ int wave_counts[16][kMaxExperts];
     const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     for (unsigned e = tid; e < experts; e += 1024)
@@ -288,27 +296,33 @@ __device__ __forceinline__ void permute_slots(const int32_t* __restrict__ idx, u
         atomicAdd(&counts[idx[s]], 1);
     __syncthreads();
     if (wave == 0) {
-        // exclusive prefix sums over the experts of their slots and of their work items
-        // (ceil(count / kItemRows) each): lane l takes experts 4l .. 4l + 3
-        int c[4], n[4], slot_sum = 0, item_sum = 0;
+        // exclusive prefix sums over the experts of their slots and of their heavy and
+        // light work items (ceil(count / kItemRows) items, the last one light when it
+        // has at most kTileRows rows): lane l takes experts 4l .. 4l + 3
+        int c[4], hv[4], lt[4], slot_sum = 0, heavy_sum = 0, light_sum = 0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const unsigned e = 4 * lane + j;
             c[j] = e < experts ? counts[e] : 0;
-            n[j] = (c[j] + kItemRows - 1) / kItemRows;
+            const int n = (c[j] + kItemRows - 1) / kItemRows;
+            lt[j] = heavy_first && n > 0 && c[j] - (n - 1) * kItemRows <= kTileRows ? 1 : 0;
+            hv[j] = n - lt[j];
             slot_sum += c[j];
-            item_sum += n[j];
+            heavy_sum += hv[j];
+            light_sum += lt[j];
         }
-        int slot_scan = slot_sum, item_scan = item_sum;  // inclusive over the lanes
+        int slot_scan = slot_sum, heavy_scan = heavy_sum, light_scan = light_sum;
 #pragma unroll
-        for (int d = 1; d < 64; d *= 2) {
-            const int a = __shfl_up(slot_scan, d, 64), b = __shfl_up(item_scan, d, 64);
+        for (int d = 1; d < 64; d *= 2) {  // inclusive over the lanes
+            const int a = __shfl_up(slot_scan, d, 64), b = __shfl_up(heavy_scan, d, 64),
+                      l = __shfl_up(light_scan, d, 64);
             if (lane >= unsigned(d)) {
                 slot_scan += a;
-                item_scan += b;
+                heavy_scan += b;
+                light_scan += l;
             }
         }
-        int acc = slot_scan - slot_sum, nb = item_scan - item_sum;
+        int acc = slot_scan - slot_sum, hb = heavy_scan - heavy_sum, lb = light_scan - light_sum;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const unsigned e = 4 * lane + j;
@@ -316,19 +330,30 @@ __device__ __forceinline__ void permute_slots(const int32_t* __restrict__ idx, u
                 offsets[e] = acc;
                 base[e] = acc;
                 segment[e] = acc;
-                item_base[e] = nb;
+                heavy_base[e] = hb;
+                light_base[e] = lb;
             }
             acc += c[j];
-            nb += n[j];
+            hb += hv[j];
+            lb += lt[j];
         }
         if (lane == 63) {
             offsets[experts] = slot_scan;
-            *item_count = item_scan;
+            *item_count = heavy_scan + light_scan;
+            heavy_total = heavy_scan;
         }
     }
     __syncthreads();
+    // item of chunk k (rows 64k ..) of expert e: its heavy items in order, then its light one
+    auto item_of = [&](unsigned e, int k) {
+        const int n = (counts[e] + kItemRows - 1) / kItemRows;  // chunks of expert e
+        const int heavy =
+            n - (heavy_first && n > 0 && counts[e] - (n - 1) * kItemRows <= kTileRows ? 1 : 0);
+        return k < heavy ? heavy_base[e] + k : heavy_total + light_base[e];
+    };
     for (unsigned e = tid; e < experts; e += 1024)  // each expert's work items
-        for (int r = 0, n = item_base[e]; r < counts[e]; r += kItemRows, ++n) {
+        for (int r = 0, k = 0; r < counts[e]; r += kItemRows, ++k) {
+            const int n = item_of(e, k);
             items[2 * n] = int(e);
             items[2 * n + 1] = r;
         }
@@ -359,7 +384,7 @@ __device__ __forceinline__ void permute_slots(const int32_t* __restrict__ idx, u
             if (position)
                 position[s] = r;  // inverse permutation
             const int within = r - segment[e];
-            slot_row[r] = (item_base[e] + within / kItemRows) * kItemRows + within % kItemRows;
+            slot_row[r] = item_of(unsigned(e), within / kItemRows) * kItemRows + within % kItemRows;
         }
         __syncthreads();
         for (unsigned x = tid; x < experts; x += 1024) {
@@ -379,8 +404,10 @@ __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* __restrict
                                                        int32_t* __restrict__ items,
                                                        int32_t* __restrict__ item_count,
                                                        int32_t* __restrict__ position,
-                                                       int32_t* __restrict__ slot_row) {
-    permute_slots(idx, slots, experts, offsets, perm, items, item_count, position, slot_row);
+                                                       int32_t* __restrict__ slot_row,
+                                                       unsigned heavy_first) {
+    permute_slots(idx, slots, heavy_first != 0, experts, offsets, perm, items, item_count,
+                  position, slot_row);
 }
 
 // --------------------------------------------------------------- grouped GEMMs
@@ -1802,9 +1829,12 @@ int launch_route(const float* logits, size_t tokens, size_t experts, size_t top_
     hipLaunchKernelGGL(route_kernel, dim3(unsigned((tokens + 3) / 4)), dim3(256), 0, stream,
                        logits, unsigned(tokens), unsigned(experts), unsigned(top_k), idx, w);
     KDQ_HIP(hipGetLastError());
+    // heavy items first when an average expert's rows fit one work item (the grouped
+    // GEMMs' workgroups then all fit the compute units at once)
+    const unsigned heavy_first = tokens * top_k <= experts * (kItemRows / 2) ? 1u : 0u;
     hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, stream, idx,
                        unsigned(tokens * top_k), unsigned(experts), offsets, perm, items,
-                       item_count, position, slot_row);
+                       item_count, position, slot_row, heavy_first);
     KDQ_HIP(hipGetLastError());
     return KDQ_OK;
 }
