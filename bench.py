@@ -721,6 +721,10 @@ def main():
             extra["moe_gguf_t4"] = bench_moe_gguf(torch, 4)
         if want("moe_gguf_t64"):
             extra["moe_gguf_t64"] = bench_moe_gguf(torch, 64, count=16)
+        if want("moe_gguf_t1_resident"):
+            extra["moe_gguf_t1_resident"] = bench_moe_gguf(torch, 1, resident=True)
+        if want("moe_gguf_t4_resident"):
+            extra["moe_gguf_t4_resident"] = bench_moe_gguf(torch, 4, resident=True)
         if want("moe_gguf_t64_resident"):
             extra["moe_gguf_t64_resident"] = bench_moe_gguf(torch, 64, count=16, resident=True)
         if want("moe_gguf_t512"):

@@ -2479,6 +2479,43 @@ int indexed_gemv_affine(const IndexedJob& first, unsigned count, size_t x_step,
     });
 }
 
+int indexed_gemv_affine_packed(const IndexedJob& first, unsigned count, size_t x_step,
+                               size_t y_step, hipStream_t s, unsigned x_every) {
+    const kdq_matvec_job& j = first.job;
+    const unsigned mats = first.paired ? 2 : 1;
+    MfmaPlan p;
+    if (count > 65535 || !x_every || !packed_unit(j.encoding) || j.columns % 16 ||
+        (j.rows & (j.rows - 1)) != 0 ||
+        !plan_mfma(j.rows, j.in, size_t(j.columns) * count, p, true, mats, 0) ||
+        p.batch < j.rows)
+        return KDQ_ERR_UNSUPPORTED;
+    MfmaJobs mj{};
+    mj.count = count;
+    mj.in = j.in;
+    mj.affine = 1;
+    mj.x_every = x_every;
+    mj.mats = mats;
+    mj.x_step = x_step;
+    mj.y_step = y_step;
+    mj.job[0] = MfmaJob{static_cast<const uint8_t*>(j.weights), j.input, j.output, j.status,
+                        0, j.stride, j.columns, first.index ? first.index_limit : 0,
+                        first.index, first.index_stride,
+                        static_cast<const uint8_t*>(first.paired)};
+    number_workgroups(mj, p.rows_per_wg);
+    switch (j.encoding) {
+    case KDQ_Q8_0:
+        return launch_mfma_rows<KDQ_Q8_0, true>(j.rows, p.waves, mj, s);
+    case KDQ_Q4_0:
+        return launch_mfma_rows<KDQ_Q4_0, true>(j.rows, p.waves, mj, s);
+    case KDQ_Q4_K:
+        return launch_mfma_rows<KDQ_Q4_K, true>(j.rows, p.waves, mj, s);
+    case KDQ_Q6_K:
+        return launch_mfma_rows<KDQ_Q6_K, true>(j.rows, p.waves, mj, s);
+    default:
+        return KDQ_ERR_UNSUPPORTED;
+    }
+}
+
 int indexed_gemv_batch(const IndexedJob* jobs, size_t count, hipStream_t s) {
     std::vector<kdq_matvec_job> plain(count);
     for (size_t i = 0; i < count; ++i)

@@ -172,6 +172,11 @@ int indexed_gemv_batch(const IndexedJob* jobs, size_t count, hipStream_t stream)
 // `paired`).  A job whose index[j] is negative is skipped.
 int indexed_gemv_affine(const IndexedJob& first, unsigned count, size_t x_step, size_t y_step,
                         hipStream_t stream, unsigned x_every = 1);
+// The same over tile-packed weights (kdq_gguf_pack; Q4_0 / Q8_0 / Q4_K / Q6_K, columns a
+// multiple of 16): `first.job.weights` (and `paired`) are packed stacks whose experts lie
+// `index_stride` bytes apart; KDQ_ERR_UNSUPPORTED where the MFMA kernel does not take it.
+int indexed_gemv_affine_packed(const IndexedJob& first, unsigned count, size_t x_step,
+                               size_t y_step, hipStream_t stream, unsigned x_every = 1);
 // Whether `count` jobs like j (an affine launch when count > 1) run on the MFMA kernel
 // with a paired matrix.
 bool swiglu_pairable(const kdq_matvec_job& j, size_t count);

@@ -601,7 +601,21 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
     //    kernel takes it, else two launches and the swiglu
     const IndexedJob gj{job(L.gate_exps, x, 1, H, F, g, status), idx, L.gate_exps.expert_bytes,
                         unsigned(E), nullptr};
-    if (same_layout(L.gate_exps, L.up_exps) && swiglu_pairable(gj.job, slots)) {
+    // resident packed stacks (kdq_moe_gguf_packed): the paired launch over them when the
+    // MFMA kernel takes the packed form, else the row-major tensors
+    rc = KDQ_ERR_UNSUPPORTED;
+    if (pk.gate_exps && pk.up_exps && same_layout(L.gate_exps, L.up_exps)) {
+        IndexedJob pj{job(L.gate_exps, x, 1, H, F, g, status), idx,
+                      kdq_gguf_packed_bytes(L.gate_exps.encoding, H, F), unsigned(E),
+                      pk.up_exps};
+        pj.job.weights = pk.gate_exps;
+        rc = indexed_gemv_affine_packed(pj, unsigned(slots), H, F, st, unsigned(K));
+        if (rc && rc != KDQ_ERR_UNSUPPORTED)
+            return rc;
+    }
+    if (rc == KDQ_OK) {
+        // gate / up done on the packed stacks
+    } else if (same_layout(L.gate_exps, L.up_exps) && swiglu_pairable(gj.job, slots)) {
         IndexedJob pj = gj;
         pj.paired = L.up_exps.weights;
         if ((rc = indexed_gemv_affine(pj, unsigned(slots), H, F, st, unsigned(K))))
@@ -619,7 +633,16 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
     // 5. expert downs (one launch over every slot) and the shared down
     const IndexedJob dj{job(L.down_exps, g, 1, F, H, d, status), idx, L.down_exps.expert_bytes,
                         unsigned(E), nullptr};
-    if ((rc = indexed_gemv_affine(dj, unsigned(slots), F, H, st)))
+    rc = KDQ_ERR_UNSUPPORTED;
+    if (pk.down_exps) {
+        IndexedJob pj = dj;
+        pj.job.weights = pk.down_exps;
+        pj.index_stride = kdq_gguf_packed_bytes(L.down_exps.encoding, F, H);
+        rc = indexed_gemv_affine_packed(pj, unsigned(slots), F, H, st);
+        if (rc && rc != KDQ_ERR_UNSUPPORTED)
+            return rc;
+    }
+    if (rc != KDQ_OK && (rc = indexed_gemv_affine(dj, unsigned(slots), F, H, st)))
         return rc;
     const IndexedJob sj{job(L.down_shexp, sg, rows, S, H, ds, status), nullptr, 0, 1, nullptr};
     if ((rc = indexed_gemv_batch(&sj, 1, st)))

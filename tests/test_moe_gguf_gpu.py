@@ -196,10 +196,10 @@ def test_moe_gguf_rejections(device):
 def test_moe_gguf_packed_stacks_bit_identical(device, oracle, rows):
     """kdq_moe_gguf_packed over resident tile-packed copies (expert stacks and shared
     matrices packed once, as a weight bank keeps them) gives the same bits as
-    kdq_moe_gguf, which packs them in the call: 4 rows (the per-slot decode path, which
-    reads rows and ignores the copies), 16 (the experts on the grouped GEMM, the shared
-    expert on 8-row items) and 256 (the shared expert on the dense GEMM too); checked
-    against the oracle too."""
+    kdq_moe_gguf, which packs them in the call: 4 rows (the per-slot decode path: the
+    expert GEMVs over the packed stacks, bit-identical to the row-major form), 16 (the
+    experts on the grouped GEMM, the shared expert on 8-row items) and 256 (the shared
+    expert on the dense GEMM too); checked against the oracle too."""
     import torch
     H, E, K, F, S = 512, 16, 8, 256, 512
     spec = make_layer(60 + rows, H, E, K, F, S, MIXED)
