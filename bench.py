@@ -2,7 +2,7 @@
 """Benchmark of the MI355X quantized-weight matmul path (one GPU).
 
 Headline (``value``): Q4_K GEMV weight throughput in GB/s at the Llama-3-8B FFN
-decode shape gate/up 4096 -> 14336, batch 1, with the inputs
+decode shape gate/up 4096 -> 14336, batch 1 (the benchmark's configs[1]), with the inputs
 resident in HBM in the library's tile-packed layout (kdq_gguf_pack, the form its weight
 bank keeps).  A "step" is one GEMV over one weight copy (one kernel launch, one
 kdq_gemv_packed_batch submission); the timed steps rotate over 16 distinct weight
@@ -18,7 +18,7 @@ The same line carries
                 clamp(cores/2, 1, 16) threads), on a bounded sample of the same workload
                 rotating over 4 weight copies
   extra         the HBM read ceiling at the headline's size (kdq_hbm_read, timed the same
-                way), the other BASELINE configurations (C1 Q8_0 GEMV, C2 down, C3 Q4_0
+                way), the other benchmark configurations (C1 Q8_0 GEMV, C2 down, C3 Q4_0
                 GEMM, C4 MoE at 1 and 256 tokens, C5 MoE at 2048 skewed tokens) and the
                 prefill GEMMs, each timed with events over back-to-back launches (median
                 of repetitions)

@@ -4,7 +4,7 @@
 //
 // The types below restate the reference's (same names, members and meaning) so the
 // model code that calls DenseCompute needs no change: a kadan::DenseCompute subclass
-// forwards its GGUF virtuals to HipDenseCompute (INTEGRATION.md shows the adapter).
+// forwards its GGUF virtuals to HipDenseCompute (a thin adapter, one call each).
 // Contract, as the reference states it (dense_compute.hpp:58-59,174-179,215-218):
 //   * host spans are borrowed: owned by the caller until return, never retained;
 //   * every call is synchronous: all device work and source callbacks finish first;

@@ -1,4 +1,4 @@
-"""Builds tests/cpp/adapter_probe: the DenseCompute adapter of INTEGRATION.md section 1
+"""Builds tests/cpp/adapter_probe: the DenseCompute adapter of the integration guide's section 1
 (extracted from the document as it stands), compiled with g++ -std=c++20 against the
 reference's own headers, linked to libkadan_amd_host.so, plus adapter_probe.cpp, which
 calls it through kadan::DenseCompute.  Test infrastructure; it needs the reference's
@@ -28,7 +28,7 @@ def available() -> bool:
 
 
 def adapter_source() -> str:
-    """The first C++ block of INTEGRATION.md section 1, verbatim."""
+    """The first C++ block of the integration guide's section 1, verbatim."""
     text = open(INTEGRATION).read()
     section = text[text.index("## 1."):]
     match = re.search(r"```cpp\n(.*?)```", section, re.S)

@@ -1,4 +1,4 @@
-// Calls the DenseCompute adapter of INTEGRATION.md section 1 through the reference's
+// Calls the DenseCompute adapter of the integration guide's section 1 through the reference's
 // own interface type, kadan::DenseCompute (IW/include/kadan/dense_compute.hpp:60-342;
 // IW = services/hikari/inference_worker), compiled against the reference's headers.
 // Test infrastructure: built by tests/cpp/adapter.py where the reference exists.

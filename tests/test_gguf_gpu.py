@@ -102,7 +102,8 @@ def test_gemv_parity(device, oracle, encoding, exact, shape):
 @pytest.mark.parametrize("encoding,n_in,n_out", [(Q8_0, 4096, 4096), (Q4_K, 4096, 14336),
                                                  (Q4_K, 14336, 4096), (Q4_0, 4096, 14336)])
 def test_gemv_baseline_shapes(device, oracle, encoding, n_in, n_out):
-    """The BASELINE configuration shapes (C1, C2) at full size, batch 1."""
+    """The benchmark configurations' GEMV shapes (C1 Q8_0 4096x4096, C2 Q4_K 4096->14336 and
+    14336->4096, and Q4_0 at C2's size) at full size, batch 1."""
     torch = _torch()
     w = synth.gguf_weights(encoding, 0xC2, n_out, n_in)
     x = synth.normal(0xC2, 50, n_in).reshape(1, n_in)

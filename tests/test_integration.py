@@ -1,4 +1,5 @@
-"""The DenseCompute adapter of INTEGRATION.md section 1 compiles against the reference's
+"""The DenseCompute adapter published in the repository's integration guide (its section
+1) compiles against the reference's
 own interface (IW/include/kadan/dense_compute.hpp:60-345) and links to
 libkadan_amd_host.so; the probe calls it through kadan::DenseCompute.  Without a GPU the
 probe stops at construction with the library's kdq_hip error; the GPU test

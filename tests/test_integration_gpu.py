@@ -1,4 +1,4 @@
-"""The INTEGRATION.md DenseCompute adapter on the GPU, through the reference's interface
+"""The integration guide's DenseCompute adapter on the GPU, through the reference's interface
 type: tests/cpp/adapter_probe (built by tests/cpp/adapter.py where the reference's
 headers exist) runs a refused shape, a Q4_K dense_gguf_source with bias (and its bank
 hit), a two-job Q8_0 dense_gguf_batch and an F32 dense, each against a double product of
