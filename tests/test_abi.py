@@ -187,3 +187,30 @@ def test_synth_torch_streams_match_numpy():
                           synth.splitmix64_torch(5, 9, 1000, "cpu").numpy())
     assert torch.equal(synth._umod_small(torch.tensor([-1], dtype=torch.int64), 9),
                        torch.tensor([(2 ** 64 - 1) % 9]))
+
+
+def test_gemm_check_and_moe_gguf_packed_argument_errors():
+    """kdq_gguf_gemm_check and kdq_moe_gguf_packed refuse bad arguments before any launch:
+    null pointers, encodings the prefill GEMM does not read, a K off the 256-value grid,
+    and misaligned device pointers (a resident packed copy included)."""
+    import kadan_amd
+    lib = kadan_amd.lib()
+    chk = lib.kdq_gguf_gemm_check
+    assert chk(12, None, 16, 256, FAKE_Y, None) == 1
+    assert chk(12, FAKE_W, 16, 256, None, None) == 1
+    assert chk(2, FAKE_W, 16, 256, FAKE_Y, None) == 3      # Q4_0: not read by the GEMM
+    assert chk(12, FAKE_W, 16, 200, FAKE_Y, None) == 2     # k % 256
+    assert chk(12, FAKE_W + 4, 16, 256, FAKE_Y, None) == 7  # packed not 16-aligned
+    assert chk(12, FAKE_W, 16, 256, FAKE_Y + 2, None) == 7  # flags not 4-aligned
+    H, E, K, F, S = 256, 8, 2, 256, 256
+    layer = kadan_amd.MoeGgufLayer(H, E, K, F, S)
+    q4k = lambda rows: kadan_amd.GgufTensor(FAKE_W, 144, rows * 144, 12)
+    layer.router = kadan_amd.GgufTensor(FAKE_W, H * 4, 0, 0)
+    layer.gate_exps, layer.up_exps, layer.down_exps = q4k(F), q4k(F), q4k(H)
+    layer.gate_shexp = layer.up_shexp = layer.down_shexp = kadan_amd.GgufTensor(FAKE_W, 144, 0, 12)
+    layer.shared_gate = FAKE_W
+    stacks = kadan_amd.MoeGgufPackedStacks(FAKE_W + 8, None, None, None, None, None, 1)
+    f = lib.kdq_moe_gguf_packed
+    assert f(None, C.addressof(stacks), FAKE_X, 1, FAKE_Y, None, None, None, None) == 1
+    assert f(C.addressof(layer), C.addressof(stacks), FAKE_X, 1, FAKE_Y, None, None, None,
+             None) == 7
