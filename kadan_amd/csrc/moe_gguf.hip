@@ -4,10 +4,9 @@
 // trip between its stages (the reference returns to the host three times per layer).
 //
 // Stages, all on `stream`:
-//   1. one GEMV batch over x: router logits, the shared-expert gate scalar
-//      ffn_gate_inp_shexp . x (as a one-row fp32 matrix), and the shared expert's gate and
-//      up rows, as one paired MFMA job that writes silu(gate) * up when the kernel takes
-//      the pair (gate and up stored alike)
+//   1. one GEMV batch over x: router logits and the shared expert's gate and up rows, as
+//      one paired MFMA job that writes silu(gate) * up when the kernel takes the pair
+//      (gate and up stored alike)
 //   2. routing (route_selection: the kdq_moe_route kernel; softmax with a double total,
 //      top-k by probability, weights renormalised by max(sum, 2^-14))
 //   3. swiglu_kernel on the shared rows, unless paired in 1
@@ -16,7 +15,8 @@
 //      device; paired with the swiglu like 1, else gate and up launches and swiglu_kernel
 //   5. one launch of every slot's expert down GEMV, plus the shared expert's down
 //   6. combine_kernel: y = sum over the selections, in selection order, of down * weight,
-//      plus shared_down * sigmoid(gate scalar)
+//      plus shared_down * sigmoid(ffn_gate_inp_shexp . x); the scalar is taken inside the
+//      combine (a dot product of H values per workgroup), not by a launch of its own
 // GEMVs of Q4_0 / Q8_0 / Q4_K / Q3_K / Q6_K / IQ4_XS / IQ4_NL run on the MFMA kernel
 // (fused per shape), every other encoding on the exact kernel.
 //
@@ -31,7 +31,7 @@
 //   4''. one launch over the items of expert gate / up (8 rows each, weights at the
 //       item's expert), paired with the swiglu like 4
 //   5'. one launch over the items of expert down, plus the shared down
-//   6'. combine_pos_kernel: as 6, each slot's down row read at its position
+//   6'. combine_kernel as 6, each slot's down row read at its position
 #include "kdq_common.hpp"
 
 #include <algorithm>
@@ -54,19 +54,51 @@ __global__ __launch_bounds__(256) void swiglu_kernel(float* gate, const float* u
     gate[i] = silu_of(gate[i]) * up[i];
 }
 
-// y[t, d] = (sum_{i < k} down[t*k + i, d] * w[t*k + i]) + shared[t, d] * sigmoid(gate[t])
-__global__ __launch_bounds__(256) void combine_kernel(const float* down, const float* w,
-                                                      const float* shared, const float* gate,
-                                                      unsigned k, unsigned hidden,
-                                                      size_t tokens, float* y) {
-    const size_t e = size_t(blockIdx.x) * 256 + threadIdx.x;
-    if (e >= tokens * hidden)
+// y[t, d] = (sum_{i < k} down[row(t, i), d] * w[t*k + i]) + shared[t, d] * sigmoid(s_t),
+// row(t, i) = t*k + i (slot order) or pos[t*k + i] (grouped layers), in selection order;
+// s_t = ffn_gate_inp_shexp . x[t], which every workgroup of token t takes itself in one
+// fixed order (thread j: its float4 columns j, j + 256, ... with the four products of each
+// fused in turn; the wavefront: an xor butterfly, which leaves the same float in every
+// lane; the four wavefronts: (0 + 1) + (2 + 3)), so all of them use the same value.
+// Grid (ceil(hidden / 1024), tokens), 256 threads of 4 consecutive d each.
+__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ down,
+                                                      const int32_t* __restrict__ pos,
+                                                      const float* __restrict__ w,
+                                                      const float* __restrict__ shared,
+                                                      const float* __restrict__ gate_vector,
+                                                      const float* __restrict__ x, unsigned k,
+                                                      unsigned hidden, float* __restrict__ y) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    __shared__ float wave_sum[4];
+    const size_t t = blockIdx.y;
+    const unsigned quads = hidden / 4;
+    const f32x4* xr = reinterpret_cast<const f32x4*>(x + t * hidden);
+    const f32x4* vr = reinterpret_cast<const f32x4*>(gate_vector);
+    float s = 0.f;
+    for (unsigned q = threadIdx.x; q < quads; q += 256) {
+        const f32x4 a = xr[q], b = vr[q];
+        s = fmaf(a.x, b.x, s);
+        s = fmaf(a.y, b.y, s);
+        s = fmaf(a.z, b.z, s);
+        s = fmaf(a.w, b.w, s);
+    }
+    for (int m = 32; m >= 1; m /= 2)
+        s += __shfl_xor(s, m, 64);
+    if (threadIdx.x % 64 == 0)
+        wave_sum[threadIdx.x / 64] = s;
+    __syncthreads();
+    const float gate = sigmoid_of((wave_sum[0] + wave_sum[1]) + (wave_sum[2] + wave_sum[3]));
+    const unsigned q = blockIdx.x * 256 + threadIdx.x;
+    if (q >= quads)
         return;
-    const size_t t = e / hidden, d = e % hidden;
-    float sum = 0.f;
-    for (unsigned i = 0; i < k; ++i)
-        sum += down[(t * k + i) * hidden + d] * w[t * k + i];
-    y[e] = sum + shared[e] * sigmoid_of(gate[t]);
+    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+    for (unsigned i = 0; i < k; ++i) {
+        const size_t slot = t * k + i;
+        const size_t row = pos ? size_t(pos[slot]) : slot;
+        sum += *reinterpret_cast<const f32x4*>(down + row * hidden + 4 * size_t(q)) * w[slot];
+    }
+    const size_t at = t * hidden + 4 * size_t(q);
+    *reinterpret_cast<f32x4*>(y + at) = sum + *reinterpret_cast<const f32x4*>(shared + at) * gate;
 }
 
 constexpr size_t kSlotRows = 8;          // batches up to this many rows run per slot
@@ -179,23 +211,6 @@ __global__ __launch_bounds__(256) void gather_kernel(const float* __restrict__ x
     *reinterpret_cast<float4*>(xp + p * hidden + d) = v;
 }
 
-// combine_kernel over down rows in position order: slot s's row is down[pos[s]].
-__global__ __launch_bounds__(256) void combine_pos_kernel(const float* down,
-                                                          const int32_t* pos, const float* w,
-                                                          const float* shared,
-                                                          const float* gate, unsigned k,
-                                                          unsigned hidden, size_t tokens,
-                                                          float* y) {
-    const size_t e = size_t(blockIdx.x) * 256 + threadIdx.x;
-    if (e >= tokens * hidden)
-        return;
-    const size_t t = e / hidden, d = e % hidden;
-    float sum = 0.f;
-    for (unsigned i = 0; i < k; ++i)
-        sum += down[size_t(pos[t * k + i]) * hidden + d] * w[t * k + i];
-    y[e] = sum + shared[e] * sigmoid_of(gate[t]);
-}
-
 bool tensor_ok(const kdq_gguf_tensor& m, size_t rows, size_t in, bool expert) {
     const size_t values = block_values(m.encoding);
     return m.weights && values && in % values == 0 && in % 8 == 0 &&
@@ -304,8 +319,8 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
                 return KDQ_ERR_ALIGNMENT;
     if (overlaps(y, rows * H * 4, x, rows * H * 4))
         return KDQ_ERR_ALIAS;
-    // workspace: logits, shared gate/up rows, gate scalars, routing (unless the caller
-    // takes it), expert gate/up rows, expert downs, shared down; grouped: per position
+    // workspace: logits, shared gate/up rows, an empty part (index 3), routing (unless the
+    // caller takes it), expert gate/up rows, expert downs, shared down; grouped: per position
     // (slots padded per expert to whole items), plus x in position order, the slot and
     // position maps, the items' experts and the count of positions in use
     // (grouped on the GEMM: token tiles of kTileRows, the packed expert stacks, fp16 x)
@@ -349,7 +364,7 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
     const size_t sh_scratch =
         gemm_sh ? std::max(dense_gemm_scratch(rows, S, H), dense_gemm_scratch(rows, H, S)) : 0;
     const size_t sizes[] = {rows * E * 4,      rows * S * 4,      rows * S * 4,
-                            rows * 4,          slots * 4,         slots * 4,
+                            size_t(0),         slots * 4,         slots * 4,
                             positions * F * 4, positions * F * 4, positions * H * 4,
                             rows * H * 4,      grouped ? positions * H * 4 : 0,
                             grouped ? slots * 4 : 0, grouped ? positions * 4 : 0,
@@ -373,7 +388,7 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
     auto* logits = static_cast<float*>(part[0]);
     auto* sg = static_cast<float*>(part[1]);
     auto* su = static_cast<float*>(part[2]);
-    auto* gate = static_cast<float*>(part[3]);
+    // part[3] is empty: the shared-gate scalars are taken inside the combine
     auto* idx = selected ? selected : static_cast<int32_t*>(part[4]);
     auto* w = weights ? weights : static_cast<float*>(part[5]);
     auto* g = static_cast<float*>(part[6]);
@@ -398,20 +413,18 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
     void* sh_work = part[24];
     auto st = static_cast<hipStream_t>(stream);
 
-    // 1. router, shared-gate scalar, shared gate / up (with the swiglu in the same launch
-    //    when the MFMA kernel takes the pair)
-    const kdq_gguf_tensor gate_vector{L.shared_gate, H * 4, 0, KDQ_F32};
+    // 1. router, shared gate / up (with the swiglu in the same launch when the MFMA kernel
+    //    takes the pair); the shared-gate scalar is taken by the combine
     const kdq_matvec_job shared_gate = job(L.gate_shexp, x, rows, H, S, sg, status);
     const bool pair_shared =
         same_layout(L.gate_shexp, L.up_shexp) && rows_pairable(shared_gate);
-    IndexedJob first[4] = {{job(L.router, x, rows, H, E, logits, status), nullptr, 0, 1, nullptr},
-                           {job(gate_vector, x, rows, H, 1, gate, status), nullptr, 0, 1, nullptr},
+    IndexedJob first[3] = {{job(L.router, x, rows, H, E, logits, status), nullptr, 0, 1, nullptr},
                            {shared_gate, nullptr, 0, 1, pair_shared ? L.up_shexp.weights : nullptr},
                            {job(L.up_shexp, x, rows, H, S, su, status), nullptr, 0, 1, nullptr}};
     // the shared gate / up on the row path (stage 1, or the GEMM path's exact fallback)
     auto shared_rows = [&]() -> int {
         int r;
-        for (int i = 2; i < (pair_shared ? 3 : 4); ++i)
+        for (int i = 1; i < (pair_shared ? 2 : 3); ++i)
             if ((r = run_rows(first[i], st)))
                 return r;
         if (!pair_shared) {
@@ -422,12 +435,11 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
         return KDQ_OK;
     };
     if (!grouped) {
-        if ((rc = indexed_gemv_batch(first, pair_shared ? 3 : 4, st)))
+        if ((rc = indexed_gemv_batch(first, pair_shared ? 2 : 3, st)))
             return rc;
     } else {
-        for (int i = 0; i < 2; ++i)
-            if ((rc = run_rows(first[i], st)))
-                return rc;
+        if ((rc = run_rows(first[0], st)))
+            return rc;
         if (!gemm_sh && (rc = shared_rows()))
             return rc;
     }
@@ -558,9 +570,9 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
                     : (rc = run_rows(sj, st)))
             return rc;
         auto combine = [&]() -> int {
-            hipLaunchKernelGGL(combine_pos_kernel, dim3(unsigned((rows * H + 255) / 256)),
-                               dim3(256), 0, st, d, pos, w, ds, gate, unsigned(K), unsigned(H),
-                               rows, y);
+            hipLaunchKernelGGL(combine_kernel, dim3(unsigned((H / 4 + 255) / 256), unsigned(rows)),
+                               dim3(256), 0, st, d, pos, w, ds, L.shared_gate, x, unsigned(K),
+                               unsigned(H), y);
             KDQ_HIP(hipGetLastError());
             return KDQ_OK;
         };
@@ -648,8 +660,9 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
     if ((rc = indexed_gemv_batch(&sj, 1, st)))
         return rc;
     // 6. combine
-    hipLaunchKernelGGL(combine_kernel, dim3(unsigned((rows * H + 255) / 256)), dim3(256), 0, st,
-                       d, w, ds, gate, unsigned(K), unsigned(H), rows, y);
+    hipLaunchKernelGGL(combine_kernel, dim3(unsigned((H / 4 + 255) / 256), unsigned(rows)),
+                       dim3(256), 0, st, d, static_cast<const int32_t*>(nullptr), w, ds,
+                       L.shared_gate, x, unsigned(K), unsigned(H), y);
     KDQ_HIP(hipGetLastError());
     return KDQ_OK;
 }
