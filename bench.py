@@ -111,13 +111,27 @@ def time_launches(torch, launch, count: int, reps: int = 1):
     return statistics.median(results)
 
 
+MIN_LAUNCHES = 1000      # launches timed per measurement, whatever --steps asks for
+MIN_PER_REP = 100        # back-to-back launches inside each pair of events
+MIN_WARMUP = 200         # untimed launches first, so the clocks leave their idle state
+
+
+def timed_launches(steps: int) -> int:
+    """Launches a measurement times: `steps`, raised to MIN_LAUNCHES so every one of the
+    10 repetitions brackets at least MIN_PER_REP back-to-back launches (a pair of events
+    around 2 launches of a 7 us kernel times the launch gap, not the kernel)."""
+    return max(steps, MIN_LAUNCHES)
+
+
 def time_steps(torch, submit, steps: int, reps: int = 10):
-    """ms per step: exactly `steps` steps issued by `submit(n)` (which enqueues n steps),
-    bracketed by synchronizations, split into `reps` back-to-back repetitions of
-    steps // reps launches each (the last takes the remainder), each timed by its own
-    pair of events on the launch stream; the median of the repetitions' per-step times."""
+    """ms per step: timed_launches(steps) steps issued by `submit(n)` (which enqueues n
+    steps), bracketed by synchronizations, split into `reps` back-to-back repetitions of
+    at least MIN_PER_REP launches each (the last takes the remainder), each timed by its
+    own pair of events on the launch stream; the median of the repetitions' per-step
+    times."""
     stream = torch.cuda.current_stream()
-    reps = max(1, min(reps, steps))
+    steps = timed_launches(steps)
+    reps = max(1, min(reps, steps // MIN_PER_REP))
     counts = [steps // reps] * reps
     counts[-1] += steps - sum(counts)
     events = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
@@ -247,11 +261,10 @@ def cpu_baselines(seconds: float = 2.0):
                 impl.cpu_matvec(encoding, ws[state["i"] % copies], x, n_in, n_out, th)
                 state["i"] += 1
             med, n = timed_median(run, seconds)
-            legs[str(th)] = {"gbs": round(nb / med / 1e9, 3), "ms": round(med * 1e3, 3),
+            legs[str(th)] = {"gbs": round(nb / med / 1e9, 2), "ms": round(med * 1e3, 3),
                              "runs": n}
-        out[name] = {"kind": kind, "unit": "GB/s of algorithmic bytes", "by_threads": legs,
-                     "sample": f"whole {n_in}->{n_out} matvec, batch 1, {copies} rotated "
-                               "weight copies; median of the runs"}
+        out[name] = {"kind": kind, "unit": "GB/s", "by_threads": legs,
+                     "sample": f"whole matvec, {copies} weight copies"}
 
     gemv_leg("c1_q8_0_gemv_4096x4096", Q8_0, 4096, 4096, 0xC1)
     gemv_leg("c2_q4_k_gemv_4096_to_14336", Q4_K, 4096, 14336, 0xC2A)
@@ -268,9 +281,7 @@ def cpu_baselines(seconds: float = 2.0):
         legs[str(th)] = {"tflops": round(2.0 * rows * k * n_out / med / 1e12, 4),
                          "ms": round(med * 1e3, 2), "runs": n}
     out["c3_q4_0_gemm"] = {"kind": kind, "unit": "TFLOP/s", "by_threads": legs,
-                           "sample": f"{rows} of the 512 activation rows (fp16 values in "
-                                     "fp32), all 14336 outputs: quantize_row_q8_0 + "
-                                     "vec_dot_q4_0_q8_0 via CpuMatvec"}
+                           "sample": f"{rows} of 512 rows, all outputs"}
 
     # C4 and C5: the MoE layer flow with exact MXFP4 products (the oracle's composition:
     # the reference has no compiled MXFP4 MoeLayer)
@@ -290,24 +301,43 @@ def cpu_baselines(seconds: float = 2.0):
                 legs[str(th)] = {"tokens_per_s": round(len(sample) / med, 2),
                                  "ms": round(med * 1e3, 2), "runs": n}
             out[name] = {"kind": "port", "unit": "tokens/s", "by_threads": legs,
-                         "sample": f"tokens {sample} of the T={tokens} inputs"
-                                   + (" (token 0 boosted onto the hot experts)" if hot else "")
-                                   + f", {experts} experts, top-4, double-accumulated MXFP4 "
-                                     "products"}
+                         "sample": f"tokens {sample}" + (" (0 hot)" if hot else "")
+                                   + ", exact double-accumulated products"}
         del gb, gs, ub, us, db, ds
     return out
 
 
-def cpu_model() -> str:
-    """The host CPU's model name (what lscpu reports), for the CPU baselines."""
+def cpu_model() -> dict:
+    """The host CPU as lscpu reports it: model name, sockets, physical cores and logical
+    CPUs of the machine, and the logical CPUs this process may run on."""
+    info = {"model": "unknown", "sockets": None, "physical_cores": None,
+            "logical_cpus": os.cpu_count()}
     try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
+        import subprocess
+        text = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        fields = dict(line.split(":", 1) for line in text.splitlines() if ":" in line)
+        fields = {k.strip(): v.strip() for k, v in fields.items()}
+        info["model"] = fields.get("Model name", info["model"])
+        parsable = subprocess.run(["lscpu", "-p=CPU,CORE,SOCKET"], capture_output=True,
+                                  text=True, timeout=10).stdout
+        rows = [r.split(",") for r in parsable.splitlines() if r and not r.startswith("#")]
+        info["logical_cpus"] = len(rows)
+        info["physical_cores"] = len({(r[2], r[1]) for r in rows})
+        info["sockets"] = len({r[2] for r in rows})
+    except (OSError, ValueError, IndexError):
+        try:
+            with open("/proc/cpuinfo") as f:
+                for line in f:
+                    if line.startswith("model name"):
+                        info["model"] = line.split(":", 1)[1].strip()
+                        break
+        except OSError:
+            pass
+    try:
+        info["allowed_cpus"] = len(os.sched_getaffinity(0))
+    except AttributeError:
+        info["allowed_cpus"] = info["logical_cpus"]
+    return info
 
 
 def bench_gemv(torch, encoding, n_in, n_out, steps, warmup, seed, copies=16, per_step=1,
@@ -351,7 +381,7 @@ def bench_gemv(torch, encoding, n_in, n_out, steps, warmup, seed, copies=16, per
             if status:
                 kadan_amd.check("kdq_gemv_packed_batch" if packed else "kdq_gemv_batch", status)
 
-    submit(warmup)
+    submit(max(warmup, MIN_WARMUP))
     return time_steps(torch, submit, steps)
 
 
@@ -364,7 +394,10 @@ def bench_read_ceiling(torch, nbytes: int, steps: int, copies: int = 16,
     the headline is, at several launch shapes, in both forms: every workgroup storing
     its fold (a kernel with output) and the read alone (no store on the critical path).
     The fastest shape of each form is its ceiling.  A single read of 64x the size gives
-    the streaming rate without the per-launch cost."""
+    the streaming rate without the per-launch cost.  kdq_hbm_read is the least a reader
+    can do; ms/gbs are the form that stores a word per workgroup, as every kernel with
+    output must, so the headline GEMV's time over that time is its distance from reading
+    its bytes once and writing its result."""
     import kadan_amd
     from kadan_amd import ops
     nbytes = (nbytes + 15) // 16 * 16
@@ -390,14 +423,13 @@ def bench_read_ceiling(torch, nbytes: int, steps: int, copies: int = 16,
                           never, stream):
                         raise RuntimeError("kdq_hbm_read failed")
                     issued[0] += 1
-            submit(50)
+            submit(MIN_WARMUP)
             shape_ms[f"{wg}x{threads}"] = time_steps(torch, submit, steps)
         best = min(shape_ms, key=shape_ms.get)
         gbs = nbytes / (shape_ms[best] * 1e-3) / 1e9
         forms["with_store" if store_all else "read_only"] = {
             "ms": round(shape_ms[best], 6), "gbs": round(gbs, 1),
-            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "best_shape": best,
-            "ms_by_shape (workgroups x lanes)": {k: round(v, 6) for k, v in shape_ms.items()}}
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "best_shape": best}
     del bufs
     big = torch.ones(64 * nbytes // 4, dtype=torch.int32, device="cuda")
     ops.hbm_read(big, sink, 4096)
@@ -405,15 +437,10 @@ def bench_read_ceiling(torch, nbytes: int, steps: int, copies: int = 16,
     del big
     torch.cuda.empty_cache()
     store = forms["with_store"]
-    return {"workload": f"HBM read ceiling: {nbytes} bytes per launch, {copies} rotated "
-                        "buffers (the headline's bytes and rotation)",
+    return {"workload": f"HBM read ceiling, {nbytes} B/launch, {copies} buffers",
             "ms": store["ms"], "gbs": store["gbs"], "hbm_frac": store["hbm_frac"],
-            **forms,
-            "streaming_gbs": round(64 * nbytes / (big_ms * 1e-3) / 1e9, 1),
-            "note": "kdq_hbm_read: the least a reader can do; ms/gbs are the form that "
-                    "stores a word per workgroup, as every kernel with output must; the "
-                    "headline GEMV's time over that time is its distance from reading its "
-                    "bytes once and writing its result"}
+            "read_only": forms["read_only"], "best_shape": store["best_shape"],
+            "streaming_gbs": round(64 * nbytes / (big_ms * 1e-3) / 1e9, 1)}
 
 
 def calibrate_copy(torch, mib: int = 256, count: int = 5):
@@ -444,11 +471,10 @@ def bench_gemm(torch, reps=10, count=20, packed=True):
     ms = time_launches(torch, launch, count, reps)
     flops = 2.0 * m * k * n
     tflops = flops / (ms * 1e-3) / 1e12
-    layout = "tile-packed weights" if packed else "row-major GGUF weights"
-    return {"workload": f"C3 Q4_0 GEMM M512 K4096 N14336 (fp16 out, {layout})",
-            "ms": round(ms, 4), "tflops": round(tflops, 2), "mfma_peak_tflops": FP16_PEAK_TFLOPS,
-            "mfma_frac": round(tflops / FP16_PEAK_TFLOPS, 4),
-            "note": "per launch: activation quantize + fp16-MFMA GEMM"}
+    layout = "tile-packed" if packed else "row-major"
+    return {"workload": f"C3 Q4_0 GEMM M512 K4096 N14336, {layout}; quantize + GEMM",
+            "ms": round(ms, 4), "tflops": round(tflops, 2),
+            "mfma_frac": round(tflops / FP16_PEAK_TFLOPS, 4)}
 
 
 def bench_gemm_gguf(torch, encoding, k, n, m=512, reps=10, count=20, copies=8):
@@ -466,11 +492,8 @@ def bench_gemm_gguf(torch, encoding, k, n, m=512, reps=10, count=20, copies=8):
         launch(i)
     ms = time_launches(torch, launch, count, reps)
     tflops = 2.0 * m * k * n / (ms * 1e-3) / 1e12
-    name = {Q4_K: "Q4_K", Q8_0: "Q8_0", Q6_K: "Q6_K"}[encoding]
-    return {"workload": f"{name} prefill GEMM M{m} K{k} N{n} (fp32 in/out, tile-packed weights)",
-            "ms": round(ms, 4), "tflops": round(tflops, 2), "mfma_peak_tflops": FP16_PEAK_TFLOPS,
-            "mfma_frac": round(tflops / FP16_PEAK_TFLOPS, 4),
-            "note": "per launch: activation staging (fp16, row scale) + fp16-MFMA GEMM"}
+    return {"ms": round(ms, 4), "tflops": round(tflops, 2),
+            "mfma_frac": round(tflops / FP16_PEAK_TFLOPS, 4)}
 
 
 def bench_moe_gguf(torch, rows, reps=10, count=64, resident=False):
@@ -510,18 +533,14 @@ def bench_moe_gguf(torch, rows, reps=10, count=64, resident=False):
     shared = 2 * S * row_bytes(Q8_0, H) + H * row_bytes(Q4_K, S)
     nbytes = per_call * expert + shared + E * H * 4 + H * 4 + 2 * rows * H * 4
     gbs = nbytes / (ms * 1e-3) / 1e9
-    path = ("every slot's expert GEMV" if rows <= 8 else
-            "slots grouped by expert into 8-row items" if rows * 8 < 4 * 128 else
-            "slots grouped by expert into 64-row tiles of the prefill GEMM")
+    path = ("expert GEMVs" if rows <= 8 else
+            "8-row items" if rows * 8 < 4 * 128 else "64-row GEMM tiles")
     if resident:
-        path += "; expert stacks and shared matrices resident in the tile-packed form"
-    return {"workload": f"GGUF MoE layer (Qwen3-30B-A3B geometry) rows={rows} ({path})",
+        path += ", resident"
+    return {"workload": f"GGUF MoE Qwen3-30B-A3B rows={rows} ({path})",
             "ms": round(ms, 4), "experts_touched_per_call": round(float(per_call), 1),
             "algorithmic_bytes": int(nbytes), "gbs": round(gbs, 1),
-            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-            "note": "one kdq_moe_gguf submission: router + shared GEMV batch, device routing, "
-                    "device-indexed expert GEMVs or grouped GEMMs (MFMA for Q4_K / Q8_0 / "
-                    "Q6_K), combine; bytes = touched experts + shared expert + router + x + y"}
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def moe_bytes(tokens, hidden, inter, experts_touched):
@@ -535,7 +554,10 @@ def bench_moe(torch, tokens, experts, hot, seed, copies, reps=10, count=10, inpu
     expert groups (input i boosts experts [i * top_k, (i + 1) * top_k) mod experts), so
     consecutive decode calls touch different experts, as real decode steps do, and the
     weights they read (copies x experts x 13.2 MB) stay far beyond the 256 MB Infinity
-    Cache."""
+    Cache.  Weights are packed once, outside the timed region; the products run on the
+    scaled MFMA (FP4 E2M1 weights with their E8M0 scales as they lie, activations as FP8
+    E4M3 terms with E8M0 block scales).  One token takes the two-launch single-token
+    path; more take route, permute, gather, grouped gate/up and down GEMMs, combine."""
     from kadan_amd import ops, synth
     hidden = inter = 2880
     top_k = 4
@@ -584,15 +606,12 @@ def bench_moe(torch, tokens, experts, hot, seed, copies, reps=10, count=10, inpu
             "gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
             "tflops": round(tflops, 2),
             "fp4_mfma_frac": round(tflops / FP4_PEAK_TFLOPS, 5),
-            "bf16_mfma_frac": round(tflops / FP16_PEAK_TFLOPS, 4),
-            "note": "resident weights in the packed layout (packed once, outside the timed "
-                    "region); products on the scaled MFMA v_mfma_scale_f32_32x32x64_f8f6f4 "
-                    "(FP4 E2M1 weights with their E8M0 scales as they lie, activations as FP8 "
-                    "E4M3 terms with E8M0 block scales: 2 terms for x, 3 for h); "
-                    + ("one token: the two-launch single-token path (routing in the gate/up "
-                       "workgroups, the terms as MFMA rows, the combine in the down kernel)"
-                       if tokens == 1 else
-                       "route, permute, gather, grouped gate/up and down GEMMs, combine")}
+            "bf16_mfma_frac": round(tflops / FP16_PEAK_TFLOPS, 4)}
+
+
+LAST_LINES = ("gemm_q4_k_prefill_4096x14336", "moe_gguf_t1_resident", "hbm_read_ceiling",
+              "c1_q8_0_gemv_4096x4096", "c2_q4_k_gemv_14336_to_4096", "c3_q4_0_gemm",
+              "c4_moe_t1", "c4_moe_t256", "c5_moe_t2048_skewed")
 
 
 def _route_host(logits, top_k):
@@ -627,6 +646,8 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "launches_timed": timed_launches(args.steps),
+        "warmup_launches": max(args.warmup, MIN_WARMUP),
         "ms_per_step": round(ms, 6),
         "higher_is_better": True,
         "scaling": "weak",
@@ -640,6 +661,9 @@ def main():
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic_for(workload),
                      "algorithmic_bytes": nbytes},
+        # the peaks every fraction in "extra" is taken against (mfma_frac: fp16 MFMA)
+        "peaks": {"hbm_gbs": HBM_PEAK_GBS, "fp16_tflops": FP16_PEAK_TFLOPS,
+                  "fp4_tflops": FP4_PEAK_TFLOPS},
     }
     if not args.skip_extra:
         extra = {}
@@ -659,53 +683,28 @@ def main():
 
         if want("hbm_read_ceiling"):
             extra["hbm_read_ceiling"] = bench_read_ceiling(torch, nbytes, args.steps)
+        # (name, encoding, in, out, seed, launches, note, options); "row-major" lines read
+        # the GGUF rows in place (kdq_gemv_batch), the others the tile-packed bank copy
         gemv_line("c1_q8_0_gemv_4096x4096", Q8_0, 4096, 4096, 0xC1, 1000,
-                  "C1 Q8_0 GEMV 4096x4096, batch 1, tile-packed, 32 rotated weight copies "
-                  "(570 MB)", copies=32)
-        gemv_line("c2_q4_k_gemv_14336_to_4096", Q4_K, 14336, 4096, 0xC2B, 500)
-        gemv_line("c2_q4_k_gemv_row_major", Q4_K, n_in, n_out, 0xC2A, 1000,
-                  "C2 Q4_K GEMV 4096->14336, batch 1, over the row-major GGUF bytes "
-                  "(kdq_gemv_batch; no resident repack)", packed=False)
+                  "C1 Q8_0 GEMV 4096x4096, tile-packed, 32 copies", copies=32)
+        gemv_line("c2_q4_k_gemv_14336_to_4096", Q4_K, 14336, 4096, 0xC2B, 1000,
+                  "C2 Q4_K GEMV 14336->4096, tile-packed, 16 copies")
+        gemv_line("c2_q4_k_gemv_row_major", Q4_K, n_in, n_out, 0xC2A, 1000, "row-major",
+                  packed=False)
         gemv_line("c2_q4_k_gate_up_pair", Q4_K, n_in, n_out, 0xC2C, 1000,
-                  "C2 Q4_K gate+up 2 x (4096->14336), batch 1, one kdq_gemv_batch "
-                  "submission (one fused launch)", per_step=2)
-        gemv_line("gemv_q6_k_4096x14336", Q6_K, n_in, n_out, 0xF0 + Q6_K, 500,
-                  "Q6_K GEMV 4096->14336, batch 1, row-major GGUF bytes (kdq_gemv_batch: "
-                  "the MFMA GEMV reading 210-byte super-blocks in place)", packed=False,
-                  copies=8)
-        gemv_line("gemv_q6_k_4096x14336_packed", Q6_K, n_in, n_out, 0xF0 + Q6_K, 500,
-                  "Q6_K GEMV 4096->14336, batch 1, tile-packed resident copy (kdq_gguf_pack; "
-                  "what the host layer's bank keeps)", copies=8)
-        gemv_line("gemv_q6_k_14336_to_4096", Q6_K, 14336, 4096, 0xF1 + Q6_K, 500,
-                  "Q6_K GEMV 14336->4096, batch 1, row-major GGUF bytes (an ffn_down shape)",
-                  packed=False, copies=8)
-        gemv_line("gemv_iq4_xs_4096x14336", IQ4_XS, n_in, n_out, 0xF0 + IQ4_XS, 500,
-                  "IQ4_XS GEMV 4096->14336, batch 1, row-major GGUF bytes (kdq_gemv_batch: "
-                  "the MFMA GEMV, grid values looked up with v_perm)", packed=False, copies=8)
-        gemv_line("gemv_iq4_nl_4096x14336", IQ4_NL, n_in, n_out, 0xF0 + IQ4_NL, 500,
-                  "IQ4_NL GEMV 4096->14336, batch 1, row-major GGUF bytes (kdq_gemv_batch: "
-                  "the MFMA GEMV, Q4_0's block layout with grid values)", packed=False,
-                  copies=8)
-        gemv_line("gemv_q3_k_4096x14336", Q3_K, n_in, n_out, 0xF0 + Q3_K, 500,
-                  "Q3_K GEMV 4096->14336, batch 1, row-major GGUF bytes (kdq_gemv_batch: "
-                  "the MFMA GEMV reading 110-byte super-blocks in place)", packed=False,
-                  copies=8)
-        gemv_line("gemv_iq3_xxs_4096x14336", IQ3_XXS, n_in, n_out, 0xF0 + IQ3_XXS, 500,
-                  "IQ3_XXS GEMV 4096->14336, batch 1, row-major GGUF bytes (kdq_gemv_batch: "
-                  "the MFMA GEMV, grid magnitudes and sign selectors from LDS tables)",
-                  packed=False, copies=8)
-        gemv_line("gemv_iq3_s_4096x14336", IQ3_S, n_in, n_out, 0xF0 + IQ3_S, 500,
-                  "IQ3_S GEMV 4096->14336, batch 1, row-major GGUF bytes (kdq_gemv_batch: "
-                  "the MFMA GEMV, 9-bit grid indices, LDS tables)", packed=False, copies=8)
-        gemv_line("gemv_iq2_s_4096x14336", IQ2_S, n_in, n_out, 0xF0 + IQ2_S, 500,
-                  "IQ2_S GEMV 4096->14336, batch 1, row-major GGUF bytes (kdq_gemv_batch: "
-                  "the MFMA GEMV, 8-value grid entries from an LDS table, scales per 16 "
-                  "values)", packed=False, copies=8)
-        for enc, tag in ((BF16, "bf16"),):
-            gemv_line(f"gemv_{tag}_4096x14336_exact", enc, n_in, n_out, 0xF0 + enc, 50,
-                      f"{tag.upper()} GEMV 4096->14336, batch 1, row-major bytes (exact-decode "
-                      "product: no streaming kernel for this encoding yet)", packed=False,
-                      copies=4)
+                  "gate+up in one launch", per_step=2)
+        for enc, tag, a_, b_, packed in (
+                (Q6_K, "q6_k", n_in, n_out, False), (Q6_K, "q6_k", n_in, n_out, True),
+                (Q6_K, "q6_k", 14336, 4096, False), (IQ4_XS, "iq4_xs", n_in, n_out, False),
+                (IQ4_NL, "iq4_nl", n_in, n_out, False), (Q3_K, "q3_k", n_in, n_out, False),
+                (IQ3_XXS, "iq3_xxs", n_in, n_out, False), (IQ3_S, "iq3_s", n_in, n_out, False),
+                (IQ2_S, "iq2_s", n_in, n_out, False)):
+            name = (f"gemv_{tag}_4096x14336" if a_ == n_in else f"gemv_{tag}_14336_to_4096")
+            gemv_line(name + ("_packed" if packed else ""), enc, a_, b_,
+                      0xF0 + enc + (a_ != n_in), 1000, "packed" if packed else "row-major",
+                      packed=packed, copies=8)
+        gemv_line("gemv_bf16_4096x14336_exact", BF16, n_in, n_out, 0xF0 + BF16, 1000,
+                  "row-major, exact-decode product", packed=False, copies=4)
         if want("c3_q4_0_gemm"):
             extra["c3_q4_0_gemm"] = bench_gemm(torch)
         for enc, tag in ((Q4_K, "q4_k"), (Q8_0, "q8_0"), (Q6_K, "q6_k")):
@@ -740,12 +739,17 @@ def main():
         if want("c5_moe_t2048_skewed"):
             extra["c5_moe_t2048_skewed"] = bench_moe(torch, 2048, 128, 8, 0xC5, copies=1,
                                                      reps=5, count=5)
-        result["extra"] = extra
     if not args.skip_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
         if not args.skip_extra:
             result["cpu_baselines"] = cpu_baselines()
-    print(json.dumps(result))
+    if not args.skip_extra:
+        # the benchmark's own configurations and the read ceiling last, so a reader that
+        # keeps only the end of the line still has them
+        last = [k for k in LAST_LINES if k in extra]
+        result["extra"] = {**{k: v for k, v in extra.items() if k not in last},
+                           **{k: extra[k] for k in last}}
+    print(json.dumps(result, separators=(",", ":")))
 
 
 if __name__ == "__main__":
