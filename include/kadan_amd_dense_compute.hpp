@@ -30,6 +30,11 @@ namespace kadan_amd {
 // IW/include/kadan/dense_compute.hpp:44-56
 enum class ProjectionResult { unsupported, unvalidated, finite };
 
+// IW/include/kadan/projection_math.hpp:16-19.  image_feed_forward lets the reference use
+// TF32 products for image workloads; every product here is fp32 (or finer), so both
+// policies run the same kernels.
+enum class ProjectionPolicy { standard, image_feed_forward };
+
 // IW/include/kadan/weight_identity.hpp:7-19
 struct WeightIdentity {
     std::uint64_t device = 0;
@@ -61,12 +66,16 @@ class HipDenseCompute {
 public:
     // IW/include/kadan/dense_compute.hpp:170-172: whole packed rows; first is a row.
     using GgufWeightSource = std::function<void(std::size_t, std::span<std::byte>)>;
+    // IW/include/kadan/dense_compute.hpp:223: F32 weights; first is an element offset, a
+    // whole number of rows (first_row * in), as IW/src/cuda/h3_compute.cu:2113-2115 calls it.
+    using FloatWeightSource = std::function<void(std::size_t, std::span<float>)>;
 
     // IW/include/kadan/dense_compute.hpp:197,201
     static constexpr std::size_t gguf_batch_rows = 8;
     static constexpr std::size_t gguf_batch_max_rows = 4096;
 
-    // IW/include/kadan/dense_compute.hpp:205-213
+    // IW/include/kadan/dense_compute.hpp:205-213.  No encoding means F32 rows: the source
+    // then delivers in * 4 bytes per row (IW/src/models/text/gguf_weights.cpp:460-461).
     struct GgufBatchJob {
         const WeightIdentity* identity;
         std::optional<gguf::Encoding> encoding;
@@ -93,9 +102,12 @@ public:
     HipDenseCompute& operator=(const HipDenseCompute&) = delete;
 
     // IW/include/kadan/dense_compute.hpp:180-194.  Rows <= gguf_batch_rows run the
-    // decode-time product; more rows run the prefill GEMM (kdq_gemm_packed) over packed
-    // Q4_K / Q8_0 / Q6_K weights, else the decode-time product per group.  Bias is added
-    // to every output row.  `precise` is accepted for interface parity (fp32 products).
+    // decode-time product (fp32 decode, fp32 accumulation); more rows run the prefill GEMM
+    // (kdq_gemm_packed: fp16 MFMA operands, weights dequantised to fp16 and x after a
+    // per-row power-of-two scale, fp32 accumulation) over packed Q4_K / Q8_0 / Q6_K
+    // weights, else the decode-time product per group.  `precise` keeps fp32 operands for
+    // every row count: the exact-decode product (kdq_gemv_exact) over a row-major resident
+    // copy of its own.  Bias is added to every output row.
     ProjectionResult dense_gguf_source(const WeightIdentity&, gguf::Encoding,
                                        const GgufWeightSource&, std::span<const float> bias,
                                        std::span<const float> input, std::size_t in,
@@ -112,8 +124,28 @@ public:
 
     // IW/include/kadan/dense_compute.hpp:215-221: every job in one synchronous
     // submission; jobs sharing an input span upload it once.  Returns unvalidated (the
-    // caller checks finiteness, IW/src/models/text/gguf_weights.cpp:478-484).
+    // caller checks finiteness, IW/src/models/text/gguf_weights.cpp:478-484).  F32 jobs
+    // (no encoding) follow the eligibility of IW/include/kadan/gguf_batch_partition.hpp:
+    // 15-37 (in % 8 == 0, a row of at most 16 MiB) and run the exact fp32 product
+    // (IW/src/cuda/h3_compute.cu:4076-4082).
     ProjectionResult dense_gguf_batch(std::span<const GgufBatchJob>, const std::atomic_bool&);
+    // The eligibility rule dense_gguf_batch applies before any source read
+    // (IW/include/kadan/gguf_batch_partition.hpp:15-37 gguf_batch_supported, restricted to
+    // the encodings this implementation runs); needs no device.
+    static bool batch_supported(std::span<const GgufBatchJob>);
+
+    // IW/include/kadan/dense_compute.hpp:239-249: F32 projection whose weights [out x in]
+    // come from `source`, kept in the weight bank under `identity` (the same entry an F32
+    // batch job of that identity uses).  output [rows x out] = input . W^T + bias by the
+    // exact fp32 product; any `in` (rows are zero-padded to a multiple of 8 on the
+    // device).  Non-finite weights throw kdq_nonfinite_weight; returns finite when every
+    // output is finite, else unvalidated.  `precise` and `policy` select nothing: the
+    // product is fp32 either way (the reference's TF32 applies to image workloads only).
+    ProjectionResult dense_source(const WeightIdentity&, const FloatWeightSource&,
+                                  std::span<const float> bias, std::span<const float> input,
+                                  std::size_t in, std::size_t out, std::span<float> output,
+                                  const std::atomic_bool& cancel, bool precise = false,
+                                  ProjectionPolicy policy = ProjectionPolicy::standard);
 
     // Prefill with quantized activations (no reference device counterpart: the reference's
     // CPU path, IW/src/models/text/cpu_matvec.cpp:28-66, quantizes activations the same
@@ -161,11 +193,13 @@ private:
     using BankKey = std::tuple<WeightIdentity, int, std::size_t, std::size_t>;
 
     // The resident weights of one projection, uploaded through the pinned staging on a
-    // miss.  `product`: for the decode GEMV or the prefill GEMM (tile-packed where the
-    // packed GEMV takes the shape, one copy for both), else row-major rows.  Returns
-    // nullptr when `stream_miss` is set and the weights are not in the bank, or would
-    // not fit its limit (the caller then streams them, stream_product).
-    const Resident* weights_for(const WeightIdentity&, gguf::Encoding, std::size_t in,
+    // miss.  `type`: the GGML type of the rows (KDQ_F32 for F32 rows, stored with each
+    // row zero-padded to a multiple of 8 values).  `product`: for the decode GEMV or the
+    // prefill GEMM (tile-packed where the packed GEMV takes the shape, one copy for both),
+    // else row-major rows.  Returns nullptr when `stream_miss` is set and the weights are
+    // not in the bank, or would not fit its limit (the caller then streams them,
+    // stream_product).
+    const Resident* weights_for(const WeightIdentity&, int type, std::size_t in,
                                 std::size_t out, const GgufWeightSource&, bool retain,
                                 const std::atomic_bool& cancel,
                                 std::unique_ptr<Resident>& transient, bool product,

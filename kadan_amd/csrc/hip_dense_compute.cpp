@@ -370,19 +370,21 @@ void HipDenseCompute::staged(unsigned b) {
 }
 
 const HipDenseCompute::Resident* HipDenseCompute::weights_for(
-    const WeightIdentity& identity, gguf::Encoding enc, std::size_t in, std::size_t out,
+    const WeightIdentity& identity, int type, std::size_t in, std::size_t out,
     const GgufWeightSource& source, bool retain, const std::atomic_bool& cancel,
     std::unique_ptr<Resident>& transient, bool product, bool stream_miss) {
     // Products (decode GEMV and prefill GEMM) keep the tile-packed layout when the packed
     // GEMV takes the shape, so one resident copy serves both; the layout is part of the
-    // bank key.
-    const bool packed = product && kdq_gemv_packed_supported(ggml_type(enc), in);
-    const BankKey key{identity, 2 * int(enc) + (packed ? 1 : 0), in, out};
+    // bank key.  F32 rows are kept with each row zero-padded to a multiple of 8 values,
+    // the exact product's granule.
+    const bool f32 = type == KDQ_F32;
+    const bool packed = product && !f32 && kdq_gemv_packed_supported(type, in);
+    const BankKey key{identity, 2 * type + (packed ? 1 : 0), in, out};
     if (auto it = bank_.find(key); it != bank_.end())
         return it->second.get();
-    const std::size_t row_bytes = in / gguf::block_values(enc) * gguf::block_bytes(enc);
-    const std::size_t bytes =
-        packed ? kdq_gguf_packed_bytes(ggml_type(enc), in, out) : out * row_bytes;
+    const std::size_t source_row_bytes = kdq_row_bytes(type, in);
+    const std::size_t row_bytes = f32 ? (in + 7) / 8 * 8 * sizeof(float) : source_row_bytes;
+    const std::size_t bytes = packed ? kdq_gguf_packed_bytes(type, in, out) : out * row_bytes;
     if (retain && weight_limit_) {
         // the reference's envelope refusal (IW/include/kadan/device_weights.hpp:203-206):
         // a miss that would pass the limit is not admitted, and nothing is evicted for it
@@ -400,25 +402,33 @@ const HipDenseCompute::Resident* HipDenseCompute::weights_for(
     hip_check(hipMalloc(&r->device, r->bytes));
     // chunks of whole 16-row tiles when packing (each chunk packs into its own tiles);
     // the reads of chunk c + 1 overlap the upload and packing of chunk c
-    std::size_t rows_per_chunk = std::max<std::size_t>(1, kStagingBytes / row_bytes);
+    std::size_t rows_per_chunk = std::max<std::size_t>(1, kStagingBytes / source_row_bytes);
     if (packed)
         rows_per_chunk = std::max<std::size_t>(16, rows_per_chunk / 16 * 16);
-    const std::size_t tile_bytes = packed ? kdq_gguf_packed_bytes(ggml_type(enc), in, 16) : 0;
+    const std::size_t tile_bytes = packed ? kdq_gguf_packed_bytes(type, in, 16) : 0;
     auto st = static_cast<hipStream_t>(stream_);
     try {
+        if (row_bytes != source_row_bytes)  // the padding of every F32 row
+            hip_check(hipMemsetAsync(r->device, 0, r->bytes, st));
         unsigned b = 0;
         for (std::size_t first = 0; first < out; first += rows_per_chunk, b ^= 1) {
             require(!cancel.load(), "kdq_cancelled");
             const std::size_t n = std::min(rows_per_chunk, out - first);
-            std::byte* host = stage_rows(b, source, first, n, row_bytes);
+            std::byte* host = stage_rows(b, source, first, n, source_row_bytes);
             if (packed) {
                 auto* raw = static_cast<std::uint8_t*>(device_buffer(6 + b, n * row_bytes));
                 hip_check(hipMemcpyAsync(raw, host, n * row_bytes, hipMemcpyHostToDevice, st));
                 staged(b);
-                kdq_check(kdq_gguf_pack(ggml_type(enc), raw, row_bytes, in, n,
+                kdq_check(kdq_gguf_pack(type, raw, row_bytes, in, n,
                                         static_cast<std::uint8_t*>(r->device) +
                                             first / 16 * tile_bytes,
                                         st));
+            } else if (row_bytes != source_row_bytes) {
+                hip_check(hipMemcpy2DAsync(static_cast<std::uint8_t*>(r->device) +
+                                               first * row_bytes,
+                                           row_bytes, host, source_row_bytes, source_row_bytes,
+                                           n, hipMemcpyHostToDevice, st));
+                staged(b);
             } else {
                 hip_check(hipMemcpyAsync(static_cast<std::uint8_t*>(r->device) + first * row_bytes,
                                          host, n * row_bytes, hipMemcpyHostToDevice, st));
@@ -499,7 +509,6 @@ ProjectionResult HipDenseCompute::dense_gguf_source(
     const WeightIdentity& identity, gguf::Encoding enc, const GgufWeightSource& source,
     std::span<const float> bias, std::span<const float> input, std::size_t in, std::size_t out,
     std::span<float> output, const std::atomic_bool& cancel, bool precise, bool retain_misses) {
-    (void)precise;  // products are fp32 either way
     std::lock_guard<std::mutex> lock(mutex_);
     if (!gguf::supported(enc) || !in || in % gguf::block_values(enc) || in % 8)
         return ProjectionResult::unsupported;
@@ -523,9 +532,45 @@ ProjectionResult HipDenseCompute::dense_gguf_source(
     hip_check(hipMemcpyAsync(dx, input.data(), input.size_bytes(), hipMemcpyHostToDevice, st));
     // A miss that is not to be retained (or does not fit the bank's limit) is streamed: the
     // reference "keeps existing hits and streams uncached tiles" (dense_compute.hpp:174-179).
+    // status into `status`, the rows into `output`, bias added; finite when every output is
+    auto finish = [&](unsigned status) {
+        hip_check(hipMemcpyAsync(output.data(), dy, output.size_bytes(), hipMemcpyDeviceToHost,
+                                 st));
+        synchronize();
+        require(status == 0, "kdq_nonfinite_weight");
+        bool finite = true;
+        for (std::size_t r = 0; r < rows; ++r)
+            for (std::size_t c = 0; c < out; ++c) {
+                float& v = output[r * out + c];
+                if (!bias.empty())
+                    v += bias[c];
+                finite = finite && std::isfinite(v);
+            }
+        return finite ? ProjectionResult::finite : ProjectionResult::unvalidated;
+    };
+    auto read_status = [&] {
+        unsigned status = 0;
+        hip_check(hipMemcpyAsync(&status, dstatus, sizeof status, hipMemcpyDeviceToHost, st));
+        synchronize();
+        return status;
+    };
     std::unique_ptr<Resident> transient;
-    const Resident* w = weights_for(identity, enc, in, out, source, retain_misses, cancel,
-                                    transient, true, /*stream_miss=*/true);
+    if (precise) {
+        // fp32 operands throughout: the exact-decode product (every weight decoded as
+        // kdq_dequantize does, one fp32 fused multiply-add chain per output) over a
+        // row-major copy, for every row count
+        const Resident& rw = *weights_for(identity, ggml_type(enc), in, out, source,
+                                          retain_misses, cancel, transient, false);
+        for (std::size_t first = 0; first < rows; first += gguf_batch_max_rows) {
+            require(!cancel.load(), "kdq_cancelled");
+            const std::size_t n = std::min(gguf_batch_max_rows, rows - first);
+            kdq_check(kdq_gemv_exact(ggml_type(enc), rw.device, rw.row_bytes, dx + first * in, n,
+                                     in, out, dy + first * out, out, dstatus, st));
+        }
+        return finish(read_status());
+    }
+    const Resident* w = weights_for(identity, ggml_type(enc), in, out, source, retain_misses,
+                                    cancel, transient, true, /*stream_miss=*/true);
     const bool packed = w ? w->packed : kdq_gemv_packed_supported(ggml_type(enc), in) != 0;
     auto decode_product = [&] {
         if (!w) {
@@ -552,26 +597,13 @@ ProjectionResult HipDenseCompute::dense_gguf_source(
         stream_product(enc, in, out, rows, source, dx, dy, dstatus, cancel, true);
     else
         decode_product();
-    unsigned status = 0;
-    hip_check(hipMemcpyAsync(&status, dstatus, sizeof status, hipMemcpyDeviceToHost, st));
-    synchronize();
+    unsigned status = read_status();
     if (gemm && (status & 2u) && !(status & 1u)) {
         hip_check(hipMemsetAsync(dstatus, 0, sizeof(unsigned), st));
         decode_product();
-        hip_check(hipMemcpyAsync(&status, dstatus, sizeof status, hipMemcpyDeviceToHost, st));
+        status = read_status();
     }
-    hip_check(hipMemcpyAsync(output.data(), dy, output.size_bytes(), hipMemcpyDeviceToHost, st));
-    synchronize();
-    require(status == 0, "kdq_nonfinite_weight");
-    bool finite = true;
-    for (std::size_t r = 0; r < rows; ++r)
-        for (std::size_t c = 0; c < out; ++c) {
-            float& v = output[r * out + c];
-            if (!bias.empty())
-                v += bias[c];
-            finite = finite && std::isfinite(v);
-        }
-    return finite ? ProjectionResult::finite : ProjectionResult::unvalidated;
+    return finish(status);
 }
 
 void HipDenseCompute::dense(std::span<const float> weights, std::span<const float> bias,
@@ -621,6 +653,70 @@ void HipDenseCompute::dense(std::span<const float> weights, std::span<const floa
                 output[r * out + c] += bias[c];
 }
 
+ProjectionResult HipDenseCompute::dense_source(const WeightIdentity& identity,
+                                               const FloatWeightSource& source,
+                                               std::span<const float> bias,
+                                               std::span<const float> input, std::size_t in,
+                                               std::size_t out, std::span<float> output,
+                                               const std::atomic_bool& cancel, bool precise,
+                                               ProjectionPolicy policy) {
+    (void)precise;  // fp32 operands and accumulation whatever is asked
+    (void)policy;
+    std::lock_guard<std::mutex> lock(mutex_);
+    require(!cancel.load(), "kdq_cancelled");
+    require(in && out && in <= std::size_t(INT_MAX) && out <= std::size_t(INT_MAX) &&
+                !input.empty() && input.size() % in == 0 &&
+                output.size() == input.size() / in * out && (bias.empty() || bias.size() == out),
+            "kdq_projection_shape");
+    for (float v : input)
+        require(std::isfinite(v), "kdq_nonfinite_input");
+    for (float v : bias)
+        require(std::isfinite(v), "kdq_nonfinite_bias");
+    require(!overlap(output, input) && !overlap(output, bias), "kdq_alias");
+    hip_check(hipSetDevice(device_));
+    // The bank reads whole rows as bytes; the F32 source takes element offsets.
+    const GgufWeightSource rows_of = [&](std::size_t first_row, std::span<std::byte> dst) {
+        source(first_row * in, std::span<float>(reinterpret_cast<float*>(dst.data()),
+                                                dst.size() / sizeof(float)));
+    };
+    std::unique_ptr<Resident> transient;
+    const Resident& w =
+        *weights_for(identity, KDQ_F32, in, out, rows_of, true, cancel, transient, true);
+    const std::size_t rows = input.size() / in, padded = w.row_bytes / sizeof(float);
+    auto st = static_cast<hipStream_t>(stream_);
+    auto* dx = static_cast<float*>(device_buffer(0, rows * padded * sizeof(float)));
+    auto* dy = static_cast<float*>(device_buffer(1, rows * out * sizeof(float)));
+    auto* dstatus = static_cast<unsigned*>(device_buffer(2, 256));
+    hip_check(hipMemsetAsync(dstatus, 0, sizeof(unsigned), st));
+    if (padded == in) {
+        hip_check(hipMemcpyAsync(dx, input.data(), input.size_bytes(), hipMemcpyHostToDevice, st));
+    } else {
+        hip_check(hipMemsetAsync(dx, 0, rows * padded * sizeof(float), st));
+        hip_check(hipMemcpy2DAsync(dx, padded * sizeof(float), input.data(), in * sizeof(float),
+                                   in * sizeof(float), rows, hipMemcpyHostToDevice, st));
+    }
+    for (std::size_t first = 0; first < rows; first += gguf_batch_max_rows) {
+        require(!cancel.load(), "kdq_cancelled");
+        const std::size_t n = std::min(gguf_batch_max_rows, rows - first);
+        kdq_check(kdq_gemv(KDQ_F32, w.device, w.row_bytes, dx + first * padded, n, padded, out,
+                           dy + first * out, out, dstatus, st));
+    }
+    unsigned status = 0;
+    hip_check(hipMemcpyAsync(&status, dstatus, sizeof status, hipMemcpyDeviceToHost, st));
+    hip_check(hipMemcpyAsync(output.data(), dy, output.size_bytes(), hipMemcpyDeviceToHost, st));
+    synchronize();
+    require(status == 0, "kdq_nonfinite_weight");
+    bool finite = true;
+    for (std::size_t r = 0; r < rows; ++r)
+        for (std::size_t c = 0; c < out; ++c) {
+            float& v = output[r * out + c];
+            if (!bias.empty())
+                v += bias[c];
+            finite = finite && std::isfinite(v);
+        }
+    return finite ? ProjectionResult::finite : ProjectionResult::unvalidated;
+}
+
 void HipDenseCompute::dequantize_rows(gguf::Encoding enc, std::span<const std::byte> packed,
                                       std::size_t in, std::span<float> output) {
     std::lock_guard<std::mutex> lock(mutex_);
@@ -647,23 +743,30 @@ void HipDenseCompute::dequantize_rows(gguf::Encoding enc, std::span<const std::b
     require(status == 0, "kdq_nonfinite_weight");
 }
 
-ProjectionResult HipDenseCompute::dense_gguf_batch(std::span<const GgufBatchJob> jobs,
-                                                   const std::atomic_bool& cancel) {
-    std::lock_guard<std::mutex> lock(mutex_);
-    // Eligibility of IW/include/kadan/gguf_batch_partition.hpp:15-37, restricted to the
-    // encodings this implementation runs; decided before any source read.
+bool HipDenseCompute::batch_supported(std::span<const GgufBatchJob> jobs) {
     if (jobs.empty())
-        return ProjectionResult::unsupported;
+        return false;
     for (const auto& j : jobs) {
         if (!j.identity || !j.source || !j.in || !j.out || j.in > std::size_t(INT_MAX) ||
             j.out > std::size_t(INT_MAX) || j.input.empty() || j.input.size() % j.in ||
             j.input.size() / j.in > gguf_batch_max_rows ||
-            j.output.size() != j.input.size() / j.in * j.out || !j.encoding ||
-            !gguf::supported(*j.encoding) || j.in % gguf::block_values(*j.encoding) ||
-            j.in / gguf::block_values(*j.encoding) > kStagingBytes / gguf::block_bytes(*j.encoding) ||
-            j.in % 8)
-            return ProjectionResult::unsupported;
+            j.output.size() != j.input.size() / j.in * j.out ||
+            (j.encoding && (!gguf::supported(*j.encoding) ||
+                            j.in % gguf::block_values(*j.encoding) ||
+                            j.in / gguf::block_values(*j.encoding) >
+                                kStagingBytes / gguf::block_bytes(*j.encoding))) ||
+            (!j.encoding && j.in > kStagingBytes / sizeof(float)) || j.in % 8)
+            return false;
     }
+    return true;
+}
+
+ProjectionResult HipDenseCompute::dense_gguf_batch(std::span<const GgufBatchJob> jobs,
+                                                   const std::atomic_bool& cancel) {
+    std::lock_guard<std::mutex> lock(mutex_);
+    // decided before any source read
+    if (!batch_supported(jobs))
+        return ProjectionResult::unsupported;
     require(!cancel.load(), "kdq_cancelled");
     for (const auto& j : jobs) {
         for (float v : j.input)
@@ -675,8 +778,12 @@ ProjectionResult HipDenseCompute::dense_gguf_batch(std::span<const GgufBatchJob>
     auto st = static_cast<hipStream_t>(stream_);
     std::vector<std::unique_ptr<Resident>> transients(jobs.size());
     std::vector<const Resident*> weights(jobs.size());
+    // F32 rows (no encoding) take the exact fp32 product, IW/src/cuda/h3_compute.cu:4076-4082
+    std::vector<int> types(jobs.size());
     for (std::size_t i = 0; i < jobs.size(); ++i)
-        weights[i] = weights_for(*jobs[i].identity, *jobs[i].encoding, jobs[i].in, jobs[i].out,
+        types[i] = jobs[i].encoding ? ggml_type(*jobs[i].encoding) : int(KDQ_F32);
+    for (std::size_t i = 0; i < jobs.size(); ++i)
+        weights[i] = weights_for(*jobs[i].identity, types[i], jobs[i].in, jobs[i].out,
                                   *jobs[i].source, jobs[i].retain_misses, cancel, transients[i],
                                   true);
     // One upload of each distinct input span, one device output region per job.
@@ -721,7 +828,7 @@ ProjectionResult HipDenseCompute::dense_gguf_batch(std::span<const GgufBatchJob>
                                   std::uint32_t(j.in),
                                   std::uint32_t(j.out),
                                   std::uint32_t(j.input.size() / j.in),
-                                  ggml_type(*j.encoding)};
+                                  types[i]};
     }
     require(!cancel.load(), "kdq_cancelled");
     // Jobs of more than gguf_batch_rows rows over packed Q4_K / Q8_0 / Q6_K (routed experts
@@ -729,8 +836,8 @@ ProjectionResult HipDenseCompute::dense_gguf_batch(std::span<const GgufBatchJob>
     // (jobs keep their order within each; every job writes its own output region).
     std::vector<kdq_matvec_job> packed_jobs, row_jobs, gemm_jobs;
     for (std::size_t i = 0; i < jobs.size(); ++i) {
-        const bool gemm = gemm_takes(*jobs[i].encoding, jobs[i].in, table[i].rows,
-                                     weights[i]->packed);
+        const bool gemm = jobs[i].encoding && gemm_takes(*jobs[i].encoding, jobs[i].in,
+                                                         table[i].rows, weights[i]->packed);
         (gemm ? gemm_jobs : weights[i]->packed ? packed_jobs : row_jobs).push_back(table[i]);
     }
     for (const auto& j : gemm_jobs)
@@ -773,8 +880,8 @@ ProjectionResult HipDenseCompute::dense_gguf_q8_source(
     const std::size_t rows = input.size() / in;
     std::unique_ptr<Resident> transient;
     // the same resident copy (tile-packed when the decode product takes it) serves both
-    const Resident& w = *weights_for(identity, enc, in, out, source, true, cancel, transient,
-                                     true);
+    const Resident& w = *weights_for(identity, ggml_type(enc), in, out, source, true, cancel,
+                                     transient, true);
     auto st = static_cast<hipStream_t>(stream_);
     auto* dx = static_cast<std::uint16_t*>(device_buffer(0, input.size_bytes()));
     auto* dy = static_cast<std::uint16_t*>(device_buffer(1, output.size_bytes()));

@@ -11,6 +11,7 @@
 #include <cstdio>
 #include <cstring>
 #include <memory>
+#include <optional>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -209,7 +210,118 @@ int main() {
         check(rel_l2(fy, fw) < 1e-6, "dense (F32) matches the double product");
     }
 
-    // 5. the bank: retained bytes reported, then released
+    // 5. MoeLayer::forward's first batch (IW/src/models/text/qwen_layers.cpp:383-389) in the
+    // job form GgufWeights::project builds (IW/src/models/text/gguf_weights.cpp:456-466):
+    // the F32 router ffn_gate_inp (no encoding, F32 rows from a byte source) and the Q8_0
+    // shared gate and up, all three on the same input rows
+    {
+        const std::size_t hidden = 256, experts = 16, shared_ff = 96, mrows = 2;
+        std::vector<float> router(experts * hidden), xm(mrows * hidden);
+        for (auto& v : router)
+            v = rng.normal() * 0.1f;
+        for (auto& v : xm)
+            v = rng.normal();
+        const auto wg = random_rows(kadan::gguf::Encoding::q8_0, shared_ff, hidden, rng);
+        const auto wu = random_rows(kadan::gguf::Encoding::q8_0, shared_ff, hidden, rng);
+        const std::size_t rb = hidden / 32 * 34, fb = hidden * sizeof(float);
+        std::size_t router_reads = 0;
+        const kadan::DenseCompute::GgufWeightSource rs = [&](std::size_t f,
+                                                            std::span<std::byte> d) {
+            ++router_reads;
+            std::memcpy(d.data(), reinterpret_cast<const std::byte*>(router.data()) + f * fb,
+                        d.size());
+        };
+        const kadan::DenseCompute::GgufWeightSource gs = [&](std::size_t f,
+                                                            std::span<std::byte> d) {
+            std::memcpy(d.data(), wg.data() + f * rb, d.size());
+        };
+        const kadan::DenseCompute::GgufWeightSource us = [&](std::size_t f,
+                                                            std::span<std::byte> d) {
+            std::memcpy(d.data(), wu.data() + f * rb, d.size());
+        };
+        std::vector<float> logits(mrows * experts), gate(mrows * shared_ff),
+            up(mrows * shared_ff);
+        const auto ir = identity(20), ig = identity(21), iu = identity(22);
+        const kadan::DenseCompute::GgufBatchJob jobs[3] = {
+            {&ir, std::nullopt, &rs, xm, hidden, experts, logits, true},
+            {&ig, kadan::gguf::Encoding::q8_0, &gs, xm, hidden, shared_ff, gate, true},
+            {&iu, kadan::gguf::Encoding::q8_0, &us, xm, hidden, shared_ff, up, true}};
+        const auto r = dc.dense_gguf_batch(jobs, cancel);
+        check(r != kadan::ProjectionResult::unsupported, "moe first batch (F32 router) accepted");
+        std::vector<double> want(mrows * experts, 0.0);
+        for (std::size_t t = 0; t < mrows; ++t)
+            for (std::size_t e = 0; e < experts; ++e)
+                for (std::size_t k = 0; k < hidden; ++k)
+                    want[t * experts + e] += double(router[e * hidden + k]) *
+                                             double(xm[t * hidden + k]);
+        check(rel_l2(logits, want) < 1e-6, "F32 router job matches the double product");
+        check(rel_l2(gate, expected(kadan::gguf::Encoding::q8_0, wg, xm, hidden, shared_ff)) <
+                      1e-4 &&
+                  rel_l2(up, expected(kadan::gguf::Encoding::q8_0, wu, xm, hidden, shared_ff)) <
+                      1e-4,
+              "shared gate/up jobs match the reference decode");
+
+        // the caller's fallback for an F32 tensor: dense_source over a FloatWeightSource
+        // whose offsets are elements (first row * in), here on a fresh identity
+        std::size_t float_reads = 0;
+        const kadan::DenseCompute::FloatWeightSource fs = [&](std::size_t first,
+                                                             std::span<float> d) {
+            ++float_reads;
+            std::memcpy(d.data(), router.data() + first, d.size_bytes());
+        };
+        std::vector<float> ls(mrows * experts, -1.0f);
+        const auto r2 = dc.dense_source(identity(23), fs, {}, xm, hidden, experts, ls, cancel);
+        check(r2 == kadan::ProjectionResult::finite && float_reads > 0 &&
+                  rel_l2(ls, want) < 1e-6,
+              "dense_source (F32 source) matches the double product");
+        const std::size_t seen = float_reads;
+        dc.dense_source(identity(23), fs, {}, xm, hidden, experts, ls, cancel);
+        check(float_reads == seen && rel_l2(ls, want) < 1e-6, "dense_source bank hit reads nothing");
+
+        // an F32 dense_source of any width (rows zero-padded on the device)
+        const std::size_t odd = 37;
+        std::vector<float> wodd(experts * odd), xo(mrows * odd), yo(mrows * experts);
+        for (auto& v : wodd)
+            v = rng.normal();
+        for (auto& v : xo)
+            v = rng.normal();
+        const kadan::DenseCompute::FloatWeightSource os = [&](std::size_t first,
+                                                             std::span<float> d) {
+            std::memcpy(d.data(), wodd.data() + first, d.size_bytes());
+        };
+        std::vector<double> wo(mrows * experts, 0.0);
+        for (std::size_t t = 0; t < mrows; ++t)
+            for (std::size_t e = 0; e < experts; ++e)
+                for (std::size_t k = 0; k < odd; ++k)
+                    wo[t * experts + e] += double(wodd[e * odd + k]) * double(xo[t * odd + k]);
+        dc.dense_source(identity(24), os, {}, xo, odd, experts, yo, cancel);
+        check(rel_l2(yo, wo) < 1e-6, "dense_source with in = 37 matches the double product");
+
+        // F32 batch jobs the reference's eligibility refuses (gguf_batch_partition.hpp:32-34):
+        // in % 8 != 0, and a row past the 16 MiB staging; no source read, no output write
+        std::vector<float> x36(36, 1.0f), y36(1, -7.0f);
+        bool read = false;
+        const kadan::DenseCompute::GgufWeightSource never = [&](std::size_t,
+                                                               std::span<std::byte>) {
+            read = true;
+        };
+        const auto i36 = identity(25);
+        const kadan::DenseCompute::GgufBatchJob bad[1] = {
+            {&i36, std::nullopt, &never, x36, 36, 1, y36, true}};
+        check(dc.dense_gguf_batch(bad, cancel) == kadan::ProjectionResult::unsupported &&
+                  !read && y36[0] == -7.0f,
+              "F32 batch job with in % 8 != 0: unsupported, no read, no write");
+        const std::size_t wide = (std::size_t(16) << 20) / sizeof(float) + 8;
+        std::vector<float> xw(wide, 0.0f), yw(1, -7.0f);
+        const kadan::DenseCompute::GgufBatchJob big[1] = {
+            {&i36, std::nullopt, &never, xw, wide, 1, yw, true}};
+        check(dc.dense_gguf_batch(big, cancel) == kadan::ProjectionResult::unsupported &&
+                  !read && yw[0] == -7.0f,
+              "F32 batch job over 16 MiB per row: unsupported, no read, no write");
+        check(router_reads > 0, "router rows were read once for the bank");
+    }
+
+    // 6. the bank: retained bytes reported, then released
     const auto before = dc.retained_weights();
     check(before.size() == 2 && before[1] > 0, "retained_weights reports the bank");
     const kadan::WeightIdentity gone[2] = {identity(2), identity(3)};

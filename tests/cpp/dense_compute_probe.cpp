@@ -98,7 +98,8 @@ int kdc_release_scratch(void* p, char* err, std::size_t len) {
 int kdc_dense_gguf(void* handle, unsigned long long id, unsigned ggml_type,
                    const unsigned char* weights, std::size_t row_bytes, const float* bias,
                    const float* x, std::size_t rows, std::size_t in, std::size_t out, float* y,
-                   int retain, int cancel, int* result, char* err, std::size_t len) {
+                   int retain, int cancel, int precise, int* result, char* err,
+                   std::size_t len) {
     try {
         auto* p = static_cast<Probe*>(handle);
         const auto enc = kadan_amd::gguf::encoding(ggml_type);
@@ -111,14 +112,15 @@ int kdc_dense_gguf(void* handle, unsigned long long id, unsigned ggml_type,
         *result = encode(p->compute.dense_gguf_source(
             identity(id), *enc, src, std::span<const float>(bias, bias ? out : 0),
             std::span<const float>(x, rows * in), in, out, std::span<float>(y, rows * out), stop,
-            false, retain != 0));
+            precise != 0, retain != 0));
         return 0;
     } catch (const std::exception& e) {
         return fail(e, err, len);
     }
 }
 
-// Parallel arrays, one entry per job; inputs[i] may repeat a pointer to share an input.
+// Parallel arrays, one entry per job; inputs[i] may repeat a pointer to share an input;
+// ggml type 0 is an F32 job.
 int kdc_dense_gguf_batch(void* handle, std::size_t count, const unsigned long long* ids,
                          const unsigned* ggml_types, const unsigned char* const* weights,
                          const std::size_t* row_bytes, const float* const* inputs,
@@ -131,15 +133,65 @@ int kdc_dense_gguf_batch(void* handle, std::size_t count, const unsigned long lo
         std::vector<HipDenseCompute::GgufWeightSource> sources(count);
         std::vector<HipDenseCompute::GgufBatchJob> jobs(count);
         for (std::size_t i = 0; i < count; ++i) {
+            // type 0: F32 rows (no encoding); another type without a kadan encoding is
+            // refused here, before any read, as the integration adapter refuses it
+            const auto enc = kadan_amd::gguf::encoding(ggml_types[i]);
+            if (ggml_types[i] && !enc) {
+                *result = 0;
+                return 0;
+            }
             idents[i] = identity(ids[i]);
             sources[i] = source_for(p, weights[i], row_bytes[i]);
             jobs[i] = HipDenseCompute::GgufBatchJob{
-                &idents[i], kadan_amd::gguf::encoding(ggml_types[i]), &sources[i],
+                &idents[i], enc, &sources[i],
                 std::span<const float>(inputs[i], rows[i] * ins[i]), ins[i], outs[i],
                 std::span<float>(outputs[i], rows[i] * outs[i]), true};
         }
         const std::atomic_bool stop{false};
         *result = encode(p->compute.dense_gguf_batch(jobs, stop));
+        return 0;
+    } catch (const std::exception& e) {
+        return fail(e, err, len);
+    }
+}
+
+// HipDenseCompute::batch_supported over jobs described as in kdc_dense_gguf_batch (ggml type
+// 0: an F32 job, no encoding); no device, no weights.  1 eligible, 0 refused, -1 a type
+// with no kadan encoding.
+int kdc_batch_supported(std::size_t count, const unsigned* ggml_types, const std::size_t* rows,
+                        const std::size_t* ins, const std::size_t* outs) {
+    std::vector<WeightIdentity> idents(count);
+    const HipDenseCompute::GgufWeightSource none = [](std::size_t, std::span<std::byte>) {};
+    std::vector<std::vector<float>> inputs(count), outputs(count);
+    std::vector<HipDenseCompute::GgufBatchJob> jobs(count);
+    for (std::size_t i = 0; i < count; ++i) {
+        const auto enc = kadan_amd::gguf::encoding(ggml_types[i]);
+        if (ggml_types[i] && !enc)
+            return -1;
+        inputs[i].resize(rows[i] * ins[i]);
+        outputs[i].resize(rows[i] * outs[i]);
+        jobs[i] = HipDenseCompute::GgufBatchJob{&idents[i], enc, &none, inputs[i], ins[i], outs[i],
+                                                outputs[i], true};
+    }
+    return HipDenseCompute::batch_supported(jobs) ? 1 : 0;
+}
+
+// HipDenseCompute::dense_source with F32 weights [out x in] from a FloatWeightSource.
+int kdc_dense_source(void* handle, unsigned long long id, const float* weights,
+                     const float* bias, const float* x, std::size_t rows, std::size_t in,
+                     std::size_t out, float* y, int* result, char* err, std::size_t len) {
+    try {
+        auto* p = static_cast<Probe*>(handle);
+        const HipDenseCompute::FloatWeightSource src = [p, weights, in](std::size_t first,
+                                                                        std::span<float> dst) {
+            std::memcpy(dst.data(), weights + first, dst.size_bytes());
+            p->source_reads += dst.size() / in;
+        };
+        const std::atomic_bool stop{false};
+        *result = encode(p->compute.dense_source(
+            identity(id), src, std::span<const float>(bias, bias ? out : 0),
+            std::span<const float>(x, rows * in), in, out, std::span<float>(y, rows * out),
+            stop));
         return 0;
     } catch (const std::exception& e) {
         return fail(e, err, len);

@@ -52,8 +52,10 @@ class Probe:
         L.kdc_release.argtypes = [c_p, ctypes.c_ulonglong]
         L.kdc_release_scratch.argtypes = [c_p, ctypes.c_char_p, c_sz]
         L.kdc_dense_gguf.argtypes = [c_p, ctypes.c_ulonglong, ctypes.c_uint, c_p, c_sz, c_p, c_p,
-                                     c_sz, c_sz, c_sz, c_p, ctypes.c_int, ctypes.c_int, c_p,
-                                     ctypes.c_char_p, c_sz]
+                                     c_sz, c_sz, c_sz, c_p, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_int, c_p, ctypes.c_char_p, c_sz]
+        L.kdc_dense_source.argtypes = [c_p, ctypes.c_ulonglong, c_p, c_p, c_p, c_sz, c_sz, c_sz,
+                                       c_p, c_p, ctypes.c_char_p, c_sz]
         L.kdc_dense_gguf_batch.argtypes = [c_p, c_sz, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p,
                                            c_p, ctypes.c_char_p, c_sz]
         L.kdc_dense_gguf_q8.argtypes = [c_p, ctypes.c_ulonglong, c_p, c_sz, c_p, c_sz, c_sz, c_sz,
@@ -91,7 +93,8 @@ class Probe:
         if self.lib.kdc_release_scratch(self.h, self.err, 512):
             raise RuntimeError(self.err.value.decode())
 
-    def gguf(self, ident, enc, w, x, n_out, bias=None, retain=True, cancel=False):
+    def gguf(self, ident, enc, w, x, n_out, bias=None, retain=True, cancel=False,
+             precise=False):
         w = np.ascontiguousarray(w, np.uint8)
         x = np.ascontiguousarray(x, np.float32)
         rows, n_in = x.shape
@@ -100,7 +103,20 @@ class Probe:
         bias = None if bias is None else np.ascontiguousarray(bias, np.float32)
         rc = self.lib.kdc_dense_gguf(self.h, ident, enc, _p(w), w.size // n_out, _p(bias), _p(x),
                                      rows, n_in, n_out, _p(y), int(retain), int(cancel),
-                                     ctypes.byref(res), self.err, 512)
+                                     int(precise), ctypes.byref(res), self.err, 512)
+        return self._done(rc, res), y
+
+    def dense_source(self, ident, w, x, bias=None):
+        """F32 weights [out x in] through dense_source (a FloatWeightSource over w)."""
+        w = np.ascontiguousarray(w, np.float32)
+        x = np.ascontiguousarray(x, np.float32)
+        rows, n_in = x.shape
+        n_out = w.shape[0]
+        y = np.full((rows, n_out), np.nan, np.float32)
+        res = ctypes.c_int(-1)
+        bias = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        rc = self.lib.kdc_dense_source(self.h, ident, _p(w), _p(bias), _p(x), rows, n_in, n_out,
+                                       _p(y), ctypes.byref(res), self.err, 512)
         return self._done(rc, res), y
 
     def batch(self, jobs):
@@ -406,3 +422,98 @@ def test_streamed_prefill_fp16_range_fallback(probe, oracle):
     pick = np.union1d(_columns(0xFB, n_out, 3840), [5000])
     assert_close(y[:, pick], oracle.gemv(Q8_0, w[pick], x, n_in, len(pick)),
                  what="streamed fp16-range fallback")
+
+
+def _f64_product(w, x, bias=None):
+    y = x.astype(np.float64) @ w.astype(np.float64).T
+    return y if bias is None else y + bias.astype(np.float64)
+
+
+@pytest.mark.parametrize("rows", [1, 4, 8, 33])
+def test_batch_f32_router_with_shared_gate_up(probe, oracle, rows):
+    """MoeLayer::forward's first batch (IW/src/models/text/qwen_layers.cpp:383-389): an F32
+    router job (no encoding: F32 rows from a byte source, IW/src/models/text/
+    gguf_weights.cpp:456-466) and the Q8_0 shared gate and up, all on one input."""
+    hidden, experts, shared_ff = 2048, 128, 768
+    g = np.random.default_rng(0xF32 + rows)
+    router = (g.standard_normal((experts, hidden)) * 0.05).astype(np.float32)
+    wg = synth.gguf_weights(Q8_0, 0xF33, shared_ff, hidden)
+    wu = synth.gguf_weights(Q8_0, 0xF34, shared_ff, hidden)
+    x = synth.normal(0xF35, rows, rows * hidden).reshape(rows, hidden)
+    rv = router.view(np.uint8).reshape(experts, -1)
+    res, (logits, gate, up) = probe.batch([(900 + rows, 0, rv, x, experts),
+                                           (910 + rows, Q8_0, wg, x, shared_ff),
+                                           (920 + rows, Q8_0, wu, x, shared_ff)])
+    assert res == UNVALIDATED
+    want = _f64_product(router, x)
+    rel = np.linalg.norm(logits - want) / np.linalg.norm(want)
+    assert rel < 1e-6, rel  # the exact fp32 product, fp32 accumulation in a fixed order
+    assert_close(gate, oracle.gemv(Q8_0, wg, x, hidden, shared_ff))
+    assert_close(up, oracle.gemv(Q8_0, wu, x, hidden, shared_ff))
+    # a second call finds all three in the bank
+    before = probe.reads
+    res, (logits2, _, _) = probe.batch([(900 + rows, 0, rv, x, experts),
+                                        (910 + rows, Q8_0, wg, x, shared_ff),
+                                        (920 + rows, Q8_0, wu, x, shared_ff)])
+    assert probe.reads == before and np.array_equal(logits, logits2)
+
+
+def test_batch_f32_nonfinite_weight_throws(probe):
+    router = np.ones((16, 64), np.float32)
+    router[3, 5] = np.inf
+    x = np.ones((1, 64), np.float32)
+    with pytest.raises(RuntimeError, match="kdq_nonfinite_weight"):
+        probe.batch([(950, 0, router.view(np.uint8).reshape(16, -1), x, 16)])
+
+
+def test_batch_f32_refusals_read_nothing(probe):
+    # in % 8 != 0 (IW/include/kadan/gguf_batch_partition.hpp:35), on a mixed batch: the
+    # whole batch is refused before any read or write
+    x36 = np.ones((1, 36), np.float32)
+    w = np.ones((4, 36), np.float32).view(np.uint8).reshape(4, -1)
+    xq = np.ones((1, 256), np.float32)
+    wq = synth.gguf_weights(Q8_0, 0xF36, 8, 256)
+    res, (y0, y1) = probe.batch([(960, Q8_0, wq, xq, 8), (961, 0, w, x36, 4)])
+    assert res == UNSUPPORTED and probe.reads == 0
+    assert np.isnan(y0).all() and np.isnan(y1).all()
+
+
+@pytest.mark.parametrize("n_in", [37, 256, 4100])
+def test_dense_source_f32(probe, n_in):
+    """dense_source (IW/include/kadan/dense_compute.hpp:239-249): F32 weights from a
+    FloatWeightSource (element offsets), any width, bias, the bank shared across calls."""
+    g = np.random.default_rng(n_in)
+    n_out, rows = 96, 3
+    w = g.standard_normal((n_out, n_in)).astype(np.float32)
+    x = g.standard_normal((rows, n_in)).astype(np.float32)
+    b = g.standard_normal(n_out).astype(np.float32)
+    res, y = probe.dense_source(970 + n_in, w, x, b)
+    assert res == FINITE
+    want = _f64_product(w, x, b)
+    assert np.linalg.norm(y - want) / np.linalg.norm(want) < 1e-6
+    reads = probe.reads
+    assert reads == n_out
+    res, y2 = probe.dense_source(970 + n_in, w, x, b)
+    assert probe.reads == reads and np.array_equal(y, y2)
+
+
+def test_dense_source_nonfinite_weight_throws(probe):
+    w = np.ones((8, 64), np.float32)
+    w[7, 63] = np.nan
+    with pytest.raises(RuntimeError, match="kdq_nonfinite_weight"):
+        probe.dense_source(990, w, np.ones((1, 64), np.float32))
+
+
+def test_precise_prefill_takes_the_exact_product(probe, oracle):
+    """precise=true keeps fp32 operands at prefill row counts (the exact-decode product:
+    fp32 weights as kdq_dequantize decodes them, fp32 fused multiply-adds), so it sits
+    within fp32 rounding of the oracle's product, far inside the fp16 GEMM's error."""
+    n_in, n_out, rows = 1024, 96, 40
+    w = synth.gguf_weights(Q4_K, 0xF37, n_out, n_in)
+    x = synth.normal(0xF38, rows, rows * n_in).reshape(rows, n_in)
+    res, y = probe.gguf(995, Q4_K, w, x, n_out, precise=True)
+    assert res == FINITE
+    want = oracle.gemv(Q4_K, w, x, n_in, n_out)
+    assert_close(y, want)
+    rel = np.linalg.norm(y - want) / np.linalg.norm(want)
+    assert rel < 1e-6, rel
