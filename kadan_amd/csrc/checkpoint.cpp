@@ -1,11 +1,22 @@
-// On-disk readers of the quantized-weight matmul path: GGUF v3 (one file or a numbered
-// split set) and safetensors shards with GPT-OSS MXFP4 experts.  Contracts restated from
-// IW/src/weights/gguf_checkpoint.cpp:438-720 and IW/src/weights/checkpoint.cpp:669-730
-// (IW = services/hikari/inference_worker): bounded metadata, immutable descriptors
-// checked unchanged around every payload read, pread of whole rows, identities keyed by
-// the file's stat tuple and the payload byte range.  The parsers are this library's own
-// (the reference parses GGUF through ggml's gguf.cpp; safetensors through its own JSON
-// reader).
+// kadan_amd checkpoint readers (include/kadan_amd_checkpoint.hpp), host only.
+//
+// GGUF v3, as ggml's published format description (docs/gguf.md) lays it out, all
+// little-endian: "GGUF", u32 version, u64 tensor count, u64 metadata count; the metadata
+// pairs (string key, u32 value type, value); per tensor its name, u32 dimension count,
+// the dimensions (u64, fastest first), u32 GGML type and u64 offset into the data
+// section, which begins at the first multiple of general.alignment (default 32) past
+// the header.  Strings are a u64 byte count and the bytes; arrays a u32 element type, a
+// u64 count and the elements.
+//
+// safetensors, as its specification lays it out: u64 little-endian header length N, N
+// bytes of JSON mapping each tensor name to {"dtype", "shape", "data_offsets": [begin,
+// end]} (offsets into the payload that follows the header) plus an optional
+// "__metadata__" object of strings, then the payload.
+//
+// Bounds are derived rather than listed: a count or length is accepted only if the
+// bytes it implies fit in what is left of the header, and the header itself is capped
+// (GGUF: kGgufHeaderLimit; safetensors: the specification's 100,000,000 bytes), so no
+// allocation is sized by an unchecked field.
 #include "kadan_amd_checkpoint.hpp"
 
 #include <algorithm>
@@ -13,671 +24,796 @@
 #include <cerrno>
 #include <cmath>
 #include <cstring>
+#include <dirent.h>
 #include <fcntl.h>
-#include <filesystem>
-#include <limits>
-#include <regex>
-#include <stdexcept>
+#include <optional>
 #include <sys/stat.h>
 #include <unistd.h>
-#include <unordered_set>
-#include <utility>
-#include <variant>
 
 #include "kadan_amd.h"
+
+static_assert(std::endian::native == std::endian::little,
+              "the readers take file integers as they lie (both formats are little-endian)");
 
 namespace kadan_amd::checkpoint {
 namespace {
 
-void require(bool ok, const char* what) {
+[[noreturn]] void fail(const char* code) {
+    throw CheckpointError(code);
+}
+
+void expect(bool ok, const char* code) {
     if (!ok)
-        throw std::invalid_argument(what);
+        fail(code);
 }
 
-void stop(const std::atomic_bool& cancel, const char* what = "gguf_cancelled") {
-    if (cancel.load())
-        throw std::runtime_error(what);
+std::uint64_t add_or(std::uint64_t a, std::uint64_t b, const char* code) {
+    std::uint64_t r = 0;
+    expect(!__builtin_add_overflow(a, b, &r), code);
+    return r;
 }
 
-std::uint64_t add(std::uint64_t a, std::uint64_t b, const char* what = "gguf_size_overflow") {
-    require(b <= UINT64_MAX - a, what);
-    return a + b;
+std::uint64_t mul_or(std::uint64_t a, std::uint64_t b, const char* code) {
+    std::uint64_t r = 0;
+    expect(!__builtin_mul_overflow(a, b, &r), code);
+    return r;
 }
 
-std::uint64_t mul(std::uint64_t a, std::uint64_t b, const char* what = "gguf_size_overflow") {
-    require(!b || a <= UINT64_MAX / b, what);
-    return a * b;
-}
+// ------------------------------------------------------------------ files
 
-// An open regular file and the stat it was opened with; every payload read is bracketed
-// by unchanged() (size, mtime and ctime as at open).
-struct File {
-    int fd = -1;
-    struct stat initial {};
-    const char* changed_code = "gguf_checkpoint_changed";
-
-    File(int descriptor, const char* changed, std::uint64_t minimum, bool directory = false)
-        : fd(descriptor), changed_code(changed) {
-        if (fd < 0)
-            throw std::runtime_error(directory ? "checkpoint_open_failed" : "gguf_open_failed");
-        if (::fstat(fd, &initial) ||
-            (directory ? !S_ISDIR(initial.st_mode)
-                       : (!S_ISREG(initial.st_mode) ||
-                          std::uint64_t(initial.st_size) < minimum))) {
-            ::close(fd);
-            fd = -1;
-            throw std::invalid_argument("gguf_not_regular_file");
+// A read-only descriptor and the status the file had when it was opened.  Opened
+// non-blocking so that a FIFO or device node at the path cannot stall the constructor
+// (it is then refused as not a regular file).
+class Descriptor {
+public:
+    Descriptor(const std::string& path, const char* cannot_open, const char* not_regular) {
+        fd_ = ::open(path.c_str(), O_RDONLY | O_CLOEXEC | O_NONBLOCK);
+        expect(fd_ >= 0, cannot_open);
+        if (::fstat(fd_, &seen_) != 0 || !S_ISREG(seen_.st_mode)) {
+            ::close(fd_);
+            fd_ = -1;
+            fail(not_regular);
         }
     }
-    File(File&& o) noexcept
-        : fd(std::exchange(o.fd, -1)), initial(o.initial), changed_code(o.changed_code) {}
-    File(const File&) = delete;
-    ~File() {
-        if (fd >= 0)
-            ::close(fd);
+    Descriptor(Descriptor&& other) noexcept : fd_(other.fd_), seen_(other.seen_) {
+        other.fd_ = -1;
+    }
+    Descriptor(const Descriptor&) = delete;
+    Descriptor& operator=(const Descriptor&) = delete;
+    Descriptor& operator=(Descriptor&&) = delete;
+    ~Descriptor() {
+        if (fd_ >= 0)
+            ::close(fd_);
     }
 
-    std::uint64_t size() const { return std::uint64_t(initial.st_size); }
+    std::uint64_t size() const { return std::uint64_t(seen_.st_size); }
 
-    void unchanged() const {
+    // Exactly out.size() bytes from byte `at`.
+    void read(std::uint64_t at, std::span<std::byte> out, const char* beyond,
+              const char* failed) const {
+        expect(at <= size() && out.size() <= size() - at, beyond);
+        std::size_t done = 0;
+        while (done < out.size()) {
+            const ssize_t got = ::pread(fd_, out.data() + done, out.size() - done,
+                                        off_t(at + done));
+            if (got < 0 && errno == EINTR)
+                continue;
+            expect(got > 0, failed);  // an error, or the file ended early
+            done += std::size_t(got);
+        }
+    }
+
+    // Whether device, inode, size, modification or status-change time differ now.
+    bool moved() const {
         struct stat now {};
-        if (::fstat(fd, &now) || now.st_size != initial.st_size ||
-            now.st_mtim.tv_sec != initial.st_mtim.tv_sec ||
-            now.st_mtim.tv_nsec != initial.st_mtim.tv_nsec ||
-            now.st_ctim.tv_sec != initial.st_ctim.tv_sec ||
-            now.st_ctim.tv_nsec != initial.st_ctim.tv_nsec)
-            throw std::invalid_argument(changed_code);
+        if (::fstat(fd_, &now) != 0)
+            return true;
+        auto same_time = [](const timespec& a, const timespec& b) {
+            return a.tv_sec == b.tv_sec && a.tv_nsec == b.tv_nsec;
+        };
+        return now.st_dev != seen_.st_dev || now.st_ino != seen_.st_ino ||
+               now.st_size != seen_.st_size || !same_time(now.st_mtim, seen_.st_mtim) ||
+               !same_time(now.st_ctim, seen_.st_ctim);
     }
 
     WeightIdentity identity(std::uint64_t begin, std::uint64_t end) const {
-        const auto& s = initial;
-        return {std::uint64_t(s.st_dev), std::uint64_t(s.st_ino), std::uint64_t(s.st_size),
-                std::uint64_t(s.st_mtim.tv_sec), std::uint64_t(s.st_mtim.tv_nsec),
-                std::uint64_t(s.st_ctim.tv_sec), std::uint64_t(s.st_ctim.tv_nsec), begin, end};
+        WeightIdentity w;
+        w.device = std::uint64_t(seen_.st_dev);
+        w.inode = std::uint64_t(seen_.st_ino);
+        w.file_size = size();
+        w.modified_seconds = std::uint64_t(seen_.st_mtim.tv_sec);
+        w.modified_nanoseconds = std::uint64_t(seen_.st_mtim.tv_nsec);
+        w.changed_seconds = std::uint64_t(seen_.st_ctim.tv_sec);
+        w.changed_nanoseconds = std::uint64_t(seen_.st_ctim.tv_nsec);
+        w.payload_begin = begin;
+        w.payload_end = end;
+        return w;
     }
 
-    void read(std::uint64_t at, std::span<std::uint8_t> out, const std::atomic_bool* cancel,
-              const char* bounds = "gguf_read_bounds") const {
-        require(at <= size() && out.size() <= size() - at, bounds);
-        while (!out.empty()) {
-            if (cancel)
-                stop(*cancel);
-            const auto n = ::pread(fd, out.data(), out.size(), off_t(at));
-            if (n < 0 && errno == EINTR)
-                continue;
-            if (n <= 0)
-                throw std::runtime_error("gguf_read_failed");
-            at += std::uint64_t(n);
-            out = out.subspan(std::size_t(n));
+private:
+    int fd_ = -1;
+    struct stat seen_ {};
+};
+
+// Exact IEEE binary16 -> binary32 (normal, subnormal, infinity and NaN payloads).
+float half_to_float(std::uint16_t h) {
+    const std::uint32_t sign = std::uint32_t(h >> 15) << 31;
+    std::uint32_t exponent = (h >> 10) & 31u, fraction = h & 1023u;
+    std::uint32_t bits;
+    if (exponent == 31) {
+        bits = sign | 0x7f800000u | (fraction << 13);
+    } else if (exponent) {
+        bits = sign | ((exponent + 112) << 23) | (fraction << 13);
+    } else if (!fraction) {
+        bits = sign;
+    } else {  // subnormal: shift the fraction up to a leading one
+        int shift = 0;
+        while (!(fraction & 1024u)) {
+            fraction <<= 1;
+            ++shift;
         }
+        bits = sign | (std::uint32_t(113 - shift) << 23) | ((fraction & 1023u) << 13);
     }
+    return std::bit_cast<float>(bits);
+}
+
+// ------------------------------------------------------------------ GGUF header
+
+constexpr std::uint32_t kGgufMagic = 0x46554747;  // "GGUF" read as a little-endian u32
+constexpr std::uint64_t kGgufHeaderLimit = std::uint64_t(256) << 20;
+constexpr std::uint64_t kDefaultAlignment = 32;
+
+// GGUF metadata value types.
+enum GgufType : std::uint32_t {
+    kU8, kI8, kU16, kI16, kU32, kI32, kF32, kBool, kString, kArray, kU64, kI64, kF64
 };
 
-// ------------------------------------------------------------------- GGUF
-
-// GGUF value types (the GGUF v3 specification).
-enum : std::uint32_t {
-    kU8 = 0, kI8 = 1, kU16 = 2, kI16 = 3, kU32 = 4, kI32 = 5, kF32 = 6, kBool = 7,
-    kString = 8, kArray = 9, kU64 = 10, kI64 = 11, kF64 = 12
-};
-constexpr std::uint64_t kMetadataLimit = 32 * 1024 * 1024;
-
-std::size_t scalar_width(std::uint32_t type) {
+// Fewest header bytes one element of `type` can take (a string: its length field).
+std::uint64_t least_bytes(std::uint32_t type) {
     switch (type) {
     case kU8: case kI8: case kBool: return 1;
     case kU16: case kI16: return 2;
     case kU32: case kI32: case kF32: return 4;
-    case kU64: case kI64: case kF64: return 8;
-    default: throw std::invalid_argument("gguf_metadata_type");
+    default: return 8;
     }
 }
 
-// One scalar kept as its type and raw little-endian bits.
-struct Scalar {
-    std::uint32_t type = kU8;
-    std::uint64_t bits = 0;
-};
-struct Array {
-    std::uint32_t element = kU8;
-    std::vector<Scalar> values;
-    std::vector<std::string> texts;
-};
-using Value = std::variant<Scalar, std::string, Array>;
-
-bool is_integer(std::uint32_t t) {
-    return t == kU8 || t == kI8 || t == kU16 || t == kI16 || t == kU32 || t == kI32 ||
-           t == kU64 || t == kI64;
-}
-
-std::int64_t signed_of(const Scalar& s) {
-    switch (s.type) {
-    case kI8: return std::int8_t(s.bits);
-    case kI16: return std::int16_t(s.bits);
-    case kI32: return std::int32_t(s.bits);
-    case kI64: return std::int64_t(s.bits);
-    default: return std::int64_t(s.bits);
-    }
-}
-
-double number_of(const Scalar& s) {
-    if (s.type == kF32)
-        return double(std::bit_cast<float>(std::uint32_t(s.bits)));
-    if (s.type == kF64)
-        return std::bit_cast<double>(s.bits);
-    if (is_integer(s.type))
-        return (s.type == kI8 || s.type == kI16 || s.type == kI32 || s.type == kI64)
-                   ? double(signed_of(s))
-                   : double(s.bits);
-    throw std::invalid_argument("gguf_metadata_number");
-}
-
-// Values and bytes per block of the GGML types this reader accepts (F32 and the
-// encodings of include/kadan_amd.h that kadan loads, plus Q4_0).
-bool block_geometry(std::uint32_t type, std::uint64_t& values, std::uint64_t& bytes) {
-    if (type == KDQ_F32) {
-        values = 1, bytes = 4;
-        return true;
-    }
-    if (type == KDQ_F16 || !kdq_block_values(int(type)))
-        return false;
-    values = kdq_block_values(int(type));
-    bytes = kdq_block_bytes(int(type));
-    return true;
-}
-
-// The GGUF header of one file, parsed with bounded reads through a 64 KiB window that
-// never reaches past the metadata limit or the file.
-class HeaderParser {
+// Sequential decoding over the front of a file.  The bytes held grow on demand (at least
+// doubling, at least 1 MiB at a time) up to kGgufHeaderLimit, so a header is read in a few
+// large preads whatever its metadata holds.
+class HeaderCursor {
 public:
-    HeaderParser(const File& f, const std::atomic_bool& cancel) : file_(f), cancel_(cancel) {}
+    explicit HeaderCursor(const Descriptor& file) : file_(file) {}
 
-    std::uint64_t at = 0;
+    std::uint64_t at() const { return at_; }
+    // Bytes a field could still take: to the end of the file or of the header limit.
+    std::uint64_t room() const { return std::min(file_.size(), kGgufHeaderLimit) - at_; }
 
-    void bytes(std::span<std::uint8_t> out) {
-        stop(cancel_);
-        require(at <= kMetadataLimit && out.size() <= kMetadataLimit - at, "gguf_metadata_limit");
-        require(at <= file_.size() && out.size() <= file_.size() - at, "gguf_read_bounds");
-        while (!out.empty()) {
-            if (at < begin_ || at - begin_ >= size_) {
-                begin_ = at;
-                size_ = std::size_t(std::min<std::uint64_t>(
-                    window_.size(), std::min(file_.size(), kMetadataLimit) - at));
-                file_.read(at, std::span(window_).first(size_), &cancel_);
-            }
-            const std::size_t offset = std::size_t(at - begin_);
-            const std::size_t n = std::min(out.size(), size_ - offset);
-            std::memcpy(out.data(), window_.data() + offset, n);
-            at += n;
-            out = out.subspan(n);
-        }
-    }
-
-    std::uint64_t u64() {
-        std::array<std::uint8_t, 8> b{};
-        bytes(b);
-        std::uint64_t v = 0;
-        for (int i = 0; i < 8; ++i)
-            v |= std::uint64_t(b[i]) << (8 * i);
+    template <class T> T get() {
+        T v;
+        std::memcpy(&v, take(sizeof v), sizeof v);
         return v;
     }
-    std::uint32_t u32() {
-        std::array<std::uint8_t, 4> b{};
-        bytes(b);
-        return std::uint32_t(b[0]) | std::uint32_t(b[1]) << 8 | std::uint32_t(b[2]) << 16 |
-               std::uint32_t(b[3]) << 24;
-    }
-    std::string text(std::uint64_t limit) {
-        const auto n = u64();
-        require(n <= limit, "gguf_string_limit");
-        std::string s(std::size_t(n), '\0');
-        bytes({reinterpret_cast<std::uint8_t*>(s.data()), s.size()});
-        require(s.find('\0') == std::string::npos, "gguf_string_nul");
-        return s;
-    }
-    Scalar scalar(std::uint32_t type) {
-        const std::size_t w = scalar_width(type);
-        std::array<std::uint8_t, 8> b{};
-        bytes(std::span(b).first(w));
-        Scalar s{type, 0};
-        for (std::size_t i = 0; i < w; ++i)
-            s.bits |= std::uint64_t(b[i]) << (8 * i);
-        return s;
-    }
-    Value value(std::uint32_t type) {
-        if (type == kString)
-            return text(1024 * 1024);
-        if (type == kArray) {
-            Array a;
-            a.element = u32();
-            const auto count = u64();
-            require(count <= 524288 && a.element != kArray, "gguf_array_limit");
-            if (a.element == kString) {
-                for (std::uint64_t i = 0; i < count; ++i)
-                    a.texts.push_back(text(1024 * 1024));
-            } else {
-                (void)scalar_width(a.element);
-                for (std::uint64_t i = 0; i < count; ++i)
-                    a.values.push_back(scalar(a.element));
-            }
-            return a;
-        }
-        return scalar(type);
+
+    std::string text() {
+        const auto n = get<std::uint64_t>();
+        const auto* p = take(n);
+        return std::string(reinterpret_cast<const char*>(p), std::size_t(n));
     }
 
 private:
-    const File& file_;
-    const std::atomic_bool& cancel_;
-    std::array<std::uint8_t, 64 * 1024> window_{};
-    std::uint64_t begin_ = 0;
-    std::size_t size_ = 0;
-};
-
-struct ParsedFile {
-    std::map<std::string, Value, std::less<>> metadata;
-    std::vector<GgufTensor> tensors;
-    std::vector<std::uint64_t> offsets;  // relative to the data section
-    std::uint64_t data_begin = 0;
-};
-
-ParsedFile parse_gguf(const File& file, const std::atomic_bool& cancel) {
-    HeaderParser p(file, cancel);
-    ParsedFile out;
-    require(p.u32() == 0x46554747u, "gguf_version");  // "GGUF"
-    require(p.u32() == 3, "gguf_version");
-    const auto tensor_count = p.u64(), kv_count = p.u64();
-    require(tensor_count <= 200000 && kv_count <= 16384, "gguf_header_count");
-    std::uint64_t alignment = 32;
-    for (std::uint64_t i = 0; i < kv_count; ++i) {
-        auto key = p.text(256);
-        const auto type = p.u32();
-        Value v = p.value(type);
-        if (key == "general.alignment") {
-            const auto* s = std::get_if<Scalar>(&v);
-            require(s && s->type == kU32, "gguf_alignment");
-            alignment = s->bits;
-            require(alignment && alignment <= 4096 && !(alignment & (alignment - 1)),
-                    "gguf_alignment");
+    const std::byte* take(std::uint64_t n) {
+        const auto end = add_or(at_, n, "gguf_read_bounds");
+        if (end > held_.size()) {
+            expect(end <= file_.size(), "gguf_read_bounds");
+            expect(end <= kGgufHeaderLimit, "gguf_metadata_limit");
+            std::uint64_t want = std::max<std::uint64_t>({end, 2 * held_.size(), 1u << 20});
+            want = std::min({want, file_.size(), kGgufHeaderLimit});
+            const std::size_t old = held_.size();
+            held_.resize(std::size_t(want));
+            file_.read(old, std::span<std::byte>(held_.data() + old, held_.size() - old),
+                       "gguf_read_bounds", "gguf_read_failed");
         }
-        require(out.metadata.emplace(std::move(key), std::move(v)).second, "gguf_duplicate_key");
+        const std::byte* p = held_.data() + at_;
+        at_ = end;
+        return p;
     }
-    std::unordered_set<std::string> names;
+
+    const Descriptor& file_;
+    std::vector<std::byte> held_;
+    std::uint64_t at_ = 0;
+};
+
+GgufValue::Scalar scalar_of(HeaderCursor& c, std::uint32_t type) {
+    switch (type) {
+    case kU8: return std::uint64_t(c.get<std::uint8_t>());
+    case kI8: return std::int64_t(c.get<std::int8_t>());
+    case kU16: return std::uint64_t(c.get<std::uint16_t>());
+    case kI16: return std::int64_t(c.get<std::int16_t>());
+    case kU32: return std::uint64_t(c.get<std::uint32_t>());
+    case kI32: return std::int64_t(c.get<std::int32_t>());
+    case kU64: return c.get<std::uint64_t>();
+    case kI64: return c.get<std::int64_t>();
+    case kF32: return double(c.get<float>());
+    case kF64: return c.get<double>();
+    case kBool: {
+        const auto b = c.get<std::uint8_t>();
+        expect(b <= 1, "gguf_invalid_metadata");
+        return b == 1;
+    }
+    case kString: return c.text();
+    default: fail("gguf_metadata_type");
+    }
+}
+
+GgufValue value_of(HeaderCursor& c) {
+    const auto type = c.get<std::uint32_t>();
+    if (type != kArray)
+        return GgufValue(type, false, {scalar_of(c, type)});
+    const auto element = c.get<std::uint32_t>();
+    expect(element <= kF64 && element != kArray, "gguf_metadata_type");
+    const auto n = c.get<std::uint64_t>();
+    // nothing is reserved for more elements than the rest of the header could hold
+    expect(n <= c.room() / least_bytes(element), "gguf_array_limit");
+    std::vector<GgufValue::Scalar> items;
+    items.reserve(std::size_t(n));
+    for (std::uint64_t i = 0; i < n; ++i)
+        items.push_back(scalar_of(c, element));
+    return GgufValue(element, true, std::move(items));
+}
+
+// A key or tensor name must be non-empty and hold no NUL (names are matched as text).
+void check_name(const std::string& s, const char* empty) {
+    expect(!s.empty(), empty);
+    expect(s.find('\0') == std::string::npos, "gguf_string_nul");
+}
+
+using Metadata = std::map<std::string, GgufValue, std::less<>>;
+
+// One decoded GGUF file: its metadata and tensors (offsets already absolute).
+struct GgufHeader {
+    Metadata metadata;
+    std::vector<GgufTensorInfo> tensors;
+};
+
+GgufHeader decode_header(const Descriptor& file, std::size_t file_index) {
+    HeaderCursor c(file);
+    expect(c.get<std::uint32_t>() == kGgufMagic, "gguf_magic");
+    expect(c.get<std::uint32_t>() == 3, "gguf_version");
+    const auto tensor_count = c.get<std::uint64_t>();
+    const auto pair_count = c.get<std::uint64_t>();
+    // a pair takes at least 14 bytes (key length, one key byte, type, one value byte), a
+    // tensor record at least 33 (name length, one name byte, rank, one dimension, type,
+    // offset)
+    expect(pair_count <= c.room() / 14 && tensor_count <= c.room() / 33, "gguf_header_count");
+
+    GgufHeader h;
+    for (std::uint64_t i = 0; i < pair_count; ++i) {
+        std::string key = c.text();
+        check_name(key, "gguf_metadata_key");
+        GgufValue v = value_of(c);
+        expect(h.metadata.emplace(std::move(key), std::move(v)).second, "gguf_duplicate_key");
+    }
+    std::uint64_t alignment = kDefaultAlignment;
+    if (auto it = h.metadata.find("general.alignment"); it != h.metadata.end()) {
+        const GgufValue& a = it->second;
+        expect(!a.is_array() && a.gguf_type() == kU32, "gguf_alignment");
+        alignment = a.count();
+        expect(alignment && std::has_single_bit(alignment), "gguf_alignment");
+    }
+
+    std::vector<std::uint64_t> relative;
+    relative.reserve(std::size_t(tensor_count));
     for (std::uint64_t i = 0; i < tensor_count; ++i) {
-        GgufTensor t;
-        t.name = p.text(255);
-        require(!t.name.empty() && names.insert(t.name).second, "gguf_duplicate_tensor");
-        t.rank = p.u32();
-        require(t.rank >= 1 && t.rank <= 3, "gguf_tensor_rank");
-        std::uint64_t rows = 1;
-        for (std::size_t d = 0; d < t.rank; ++d) {
-            t.shape[d] = p.u64();
-            require(t.shape[d] && t.shape[d] <= std::uint64_t(INT64_MAX), "gguf_tensor_shape");
-            if (d)
-                rows = mul(rows, t.shape[d]);
+        GgufTensorInfo t;
+        t.name = c.text();
+        check_name(t.name, "gguf_tensor_name");
+        const auto rank = c.get<std::uint32_t>();
+        expect(rank >= 1 && rank <= 3, "gguf_tensor_rank");
+        t.rank = rank;
+        std::uint64_t dims[3] = {1, 1, 1};
+        for (std::uint32_t d = 0; d < rank; ++d) {
+            dims[d] = c.get<std::uint64_t>();
+            expect(dims[d] >= 1, "gguf_tensor_shape");
         }
-        t.type = p.u32();
-        std::uint64_t values = 0, bytes = 0;
-        require(block_geometry(t.type, values, bytes), "gguf_tensor_type");
-        require(t.shape[0] % values == 0, "gguf_tensor_block_alignment");
-        t.bytes = mul(mul(t.shape[0] / values, bytes), rows);
-        require(t.bytes <= std::uint64_t(INT64_MAX), "gguf_tensor_shape");
-        out.offsets.push_back(p.u64());
-        out.tensors.push_back(std::move(t));
+        t.columns = dims[0];
+        t.rows = dims[1];
+        t.experts = dims[2];
+        t.ggml_type = c.get<std::uint32_t>();
+        const std::size_t values = kdq_block_values(int(t.ggml_type));
+        expect(values != 0, "gguf_tensor_type");
+        expect(t.columns % values == 0, "gguf_tensor_block_alignment");
+        t.row_bytes = mul_or(t.columns / values, kdq_block_bytes(int(t.ggml_type)),
+                             "gguf_size_overflow");
+        t.slice_bytes = mul_or(t.rows, t.row_bytes, "gguf_size_overflow");
+        t.bytes = mul_or(t.experts, t.slice_bytes, "gguf_size_overflow");
+        const auto offset = c.get<std::uint64_t>();
+        expect(offset % alignment == 0, "gguf_alignment");
+        t.file = file_index;
+        relative.push_back(offset);
+        h.tensors.push_back(std::move(t));
     }
-    out.data_begin = (p.at + alignment - 1) / alignment * alignment;
-    std::vector<std::pair<std::uint64_t, std::uint64_t>> ranges;
-    for (std::size_t t = 0; t < out.tensors.size(); ++t) {
-        const auto off = out.offsets[t];
-        const auto end = add(add(out.data_begin, off), out.tensors[t].bytes);
-        require(off % alignment == 0 && end <= file.size(), "gguf_tensor_bounds");
-        ranges.emplace_back(off, add(off, out.tensors[t].bytes));
+
+    // payloads: the data section starts at the header's end rounded up to the alignment
+    const std::uint64_t data = add_or(c.at(), alignment - 1, "gguf_tensor_bounds") /
+                               alignment * alignment;
+    for (std::size_t i = 0; i < h.tensors.size(); ++i) {
+        auto& t = h.tensors[i];
+        t.offset = add_or(data, relative[i], "gguf_tensor_bounds");
+        const auto end = add_or(t.offset, t.bytes, "gguf_tensor_bounds");
+        expect(end <= file.size(), "gguf_tensor_bounds");
     }
-    std::sort(ranges.begin(), ranges.end());
-    for (std::size_t t = 1; t < ranges.size(); ++t)
-        require(ranges[t].first >= ranges[t - 1].second, "gguf_tensor_overlap");
-    file.unchanged();
-    return out;
+    // no two payloads share a byte
+    std::vector<std::size_t> order(h.tensors.size());
+    for (std::size_t i = 0; i < order.size(); ++i)
+        order[i] = i;
+    std::sort(order.begin(), order.end(), [&](std::size_t a, std::size_t b) {
+        return h.tensors[a].offset < h.tensors[b].offset;
+    });
+    for (std::size_t k = 1; k < order.size(); ++k) {
+        const auto& before = h.tensors[order[k - 1]];
+        expect(h.tensors[order[k]].offset >= before.offset + before.bytes, "gguf_tensor_overlap");
+    }
+    return h;
 }
 
-const Value& find_key(const std::map<std::string, Value, std::less<>>& m, std::string_view key) {
-    require(key.size() <= 256, "gguf_metadata_key");
+// ------------------------------------------------------------------ split sets
+
+// <stem>-NNNNN-of-NNNNN.gguf: the numbered split naming of llama.cpp's gguf-split.
+struct SplitPart {
+    std::string stem;
+    unsigned index = 0, count = 0;
+};
+
+std::optional<unsigned> five_digits(std::string_view s) {
+    if (s.size() != 5)
+        return std::nullopt;
+    unsigned v = 0;
+    for (char ch : s) {
+        if (ch < '0' || ch > '9')
+            return std::nullopt;
+        v = 10 * v + unsigned(ch - '0');
+    }
+    return v;
+}
+
+std::optional<SplitPart> split_part(std::string_view name) {
+    // suffix "-IIIII-of-CCCCC.gguf": 20 bytes after the stem
+    constexpr std::size_t suffix = 20;
+    if (name.size() <= suffix || !name.ends_with(".gguf"))
+        return std::nullopt;
+    const std::string_view tail = name.substr(name.size() - suffix);
+    if (tail[0] != '-' || tail.substr(6, 4) != "-of-")
+        return std::nullopt;
+    const auto index = five_digits(tail.substr(1, 5));
+    const auto count = five_digits(tail.substr(10, 5));
+    if (!index || !count)
+        return std::nullopt;
+    return SplitPart{std::string(name.substr(0, name.size() - suffix)), *index, *count};
+}
+
+// The .gguf files of `directory` in the order the set is read: one file, or a whole
+// split set by part number.
+std::vector<std::string> set_members(const std::string& directory, bool& split) {
+    std::vector<std::string> names;
+    if (DIR* d = ::opendir(directory.c_str())) {
+        while (const dirent* e = ::readdir(d)) {
+            const std::string_view n = e->d_name;
+            if (n.size() > 5 && n.ends_with(".gguf"))
+                names.emplace_back(n);
+        }
+        ::closedir(d);
+    }
+    expect(!names.empty(), "gguf_missing_files");
+    std::sort(names.begin(), names.end());
+    split = false;
+    if (names.size() == 1 && !split_part(names[0]))
+        return {directory + "/" + names[0]};
+    split = true;
+    std::vector<SplitPart> parts;
+    for (const auto& n : names) {
+        auto p = split_part(n);
+        expect(p && p->count >= 1 && p->index >= 1 && p->index <= p->count, "gguf_split_name");
+        expect(parts.empty() || (p->stem == parts[0].stem && p->count == parts[0].count),
+               "gguf_split_name");
+        parts.push_back(*p);
+    }
+    expect(parts.size() == parts[0].count, "gguf_split_count");
+    std::vector<std::string> ordered(parts.size());
+    for (std::size_t i = 0; i < parts.size(); ++i) {
+        auto& slot = ordered[parts[i].index - 1];
+        expect(slot.empty(), "gguf_split_name");  // a part number twice
+        slot = directory + "/" + names[i];
+    }
+    return ordered;
+}
+
+// An integer-valued metadata entry, or nothing when absent or of another kind.
+std::optional<std::uint64_t> whole_number(const Metadata& m, std::string_view key) {
     const auto it = m.find(key);
-    require(it != m.end(), "gguf_missing_metadata");
-    return it->second;
-}
-
-std::uint64_t integer_of(const Value& v) {
-    const auto* s = std::get_if<Scalar>(&v);
-    require(s && is_integer(s->type), "gguf_metadata_integer");
-    if (s->type == kI8 || s->type == kI16 || s->type == kI32 || s->type == kI64)
-        require(signed_of(*s) >= 0, "gguf_metadata_integer");
-    return s->bits;
+    if (it == m.end() || it->second.is_array())
+        return std::nullopt;
+    try {
+        return it->second.count();
+    } catch (const CheckpointError&) {
+        return std::nullopt;
+    }
 }
 
 }  // namespace
 
-struct GgufCheckpoint::Impl {
-    struct Entry {
-        GgufTensor tensor;
-        std::size_t file;
-        std::uint64_t begin;  // absolute byte offset in its file
-    };
-    std::vector<File> files;
-    std::vector<Entry> tensors;  // sorted by name
-    std::map<std::string, Value, std::less<>> metadata;
+// ------------------------------------------------------------------ GgufValue
 
-    const Entry& find(std::string_view name) const {
-        const auto it = std::lower_bound(tensors.begin(), tensors.end(), name,
-                                         [](const Entry& e, std::string_view n) {
-                                             return e.tensor.name < n;
-                                         });
-        require(it != tensors.end() && it->tensor.name == name, "gguf_missing_tensor");
-        return *it;
+namespace {
+template <class T> bool holds(const GgufValue::Scalar& s) {
+    return std::holds_alternative<T>(s);
+}
+}  // namespace
+
+std::string GgufValue::text() const {
+    expect(!array_ && items_.size() == 1 && holds<std::string>(items_[0]),
+           "gguf_metadata_string");
+    return std::get<std::string>(items_[0]);
+}
+
+std::uint64_t GgufValue::count() const {
+    expect(!array_ && items_.size() == 1, "gguf_metadata_integer");
+    if (holds<std::uint64_t>(items_[0]))
+        return std::get<std::uint64_t>(items_[0]);
+    expect(holds<std::int64_t>(items_[0]) && std::get<std::int64_t>(items_[0]) >= 0,
+           "gguf_metadata_integer");
+    return std::uint64_t(std::get<std::int64_t>(items_[0]));
+}
+
+double GgufValue::real() const {
+    expect(!array_ && items_.size() == 1 && holds<double>(items_[0]), "gguf_metadata_number");
+    return std::get<double>(items_[0]);
+}
+
+bool GgufValue::flag() const {
+    expect(!array_ && items_.size() == 1 && holds<bool>(items_[0]), "gguf_metadata_boolean");
+    return std::get<bool>(items_[0]);
+}
+
+std::vector<std::string> GgufValue::texts() const {
+    expect(array_ && type_ == kString, "gguf_metadata_strings");
+    std::vector<std::string> out;
+    out.reserve(items_.size());
+    for (const auto& s : items_)
+        out.push_back(std::get<std::string>(s));
+    return out;
+}
+
+std::vector<std::int64_t> GgufValue::integers() const {
+    const bool integral = type_ == kU8 || type_ == kI8 || type_ == kU16 || type_ == kI16 ||
+                          type_ == kU32 || type_ == kI32 || type_ == kU64 || type_ == kI64;
+    expect(array_ && integral, "gguf_metadata_integers");
+    std::vector<std::int64_t> out;
+    out.reserve(items_.size());
+    for (const auto& s : items_) {
+        if (holds<std::int64_t>(s)) {
+            out.push_back(std::get<std::int64_t>(s));
+        } else {
+            const auto u = std::get<std::uint64_t>(s);
+            expect(u <= std::uint64_t(INT64_MAX), "gguf_metadata_integers");
+            out.push_back(std::int64_t(u));
+        }
     }
+    return out;
+}
+
+std::vector<double> GgufValue::reals() const {
+    expect(array_ && (type_ == kF32 || type_ == kF64), "gguf_metadata_numbers");
+    std::vector<double> out;
+    out.reserve(items_.size());
+    for (const auto& s : items_)
+        out.push_back(std::get<double>(s));
+    return out;
+}
+
+std::vector<bool> GgufValue::flags() const {
+    expect(array_ && type_ == kBool, "gguf_metadata_booleans");
+    std::vector<bool> out;
+    out.reserve(items_.size());
+    for (const auto& s : items_)
+        out.push_back(std::get<bool>(s));
+    return out;
+}
+
+// ------------------------------------------------------------------ GgufFiles
+
+struct GgufFiles::State {
+    std::vector<Descriptor> files;
+    std::vector<GgufTensorInfo> tensors;
+    std::map<std::string, std::size_t, std::less<>> by_name;
+    Metadata metadata;  // the first file's
 };
 
-GgufCheckpoint::GgufCheckpoint(const std::string& root, const std::atomic_bool& cancel)
-    : impl_(std::make_unique<Impl>()) {
-    static_assert(std::endian::native == std::endian::little);
-    stop(cancel);
-    const std::regex pattern(R"((.+)-([0-9]{5})-of-([0-9]{5})\.gguf)");
-    std::vector<std::string> names;
-    for (const auto& entry : std::filesystem::directory_iterator(root)) {
-        stop(cancel);
-        if (entry.path().extension() == ".gguf")
-            names.push_back(entry.path().filename().string());
-        require(names.size() <= 512, "gguf_split_count");
-    }
-    require(!names.empty(), "gguf_missing_files");
-    std::sort(names.begin(), names.end());
-    File directory(::open(root.c_str(), O_RDONLY | O_DIRECTORY | O_NOFOLLOW | O_CLOEXEC),
-                   "gguf_checkpoint_changed", 0, true);
-    // One unsplit file carries no split metadata; a split set is numbered from 1.
-    const bool single = names.size() == 1 && !std::regex_match(names[0], pattern);
-    std::string prefix;
-    std::uint64_t total = 0, metadata_bytes = 0;
-    for (std::size_t i = 0; i < names.size(); ++i) {
-        std::smatch match;
-        require(names[i].size() <= 255 && (single || std::regex_match(names[i], match, pattern)),
-                "gguf_split_name");
-        if (!single && i == 0)
-            prefix = match[1];
-        require(single || (match[1] == prefix && std::stoul(match[2]) == i + 1 &&
-                           std::stoul(match[3]) == names.size()),
-                "gguf_split_name");
-        impl_->files.emplace_back(
-            ::openat(directory.fd, names[i].c_str(), O_RDONLY | O_NOFOLLOW | O_CLOEXEC),
-            "gguf_checkpoint_changed", 24);
-        const File& file = impl_->files.back();
-        ParsedFile parsed = parse_gguf(file, cancel);
-        metadata_bytes = add(metadata_bytes, parsed.data_begin);
-        require(metadata_bytes <= 64 * 1024 * 1024, "gguf_metadata_limit");
-        if (!single) {
-            require(integer_of(find_key(parsed.metadata, "split.no")) == i &&
-                        integer_of(find_key(parsed.metadata, "split.count")) == names.size(),
-                    "gguf_split_metadata");
+GgufFiles::GgufFiles(const std::string& directory, const std::atomic_bool& cancel)
+    : state_(std::make_unique<State>()) {
+    auto& s = *state_;
+    bool split = false;
+    const auto members = set_members(directory, split);
+    std::vector<Metadata> per_file;
+    for (std::size_t i = 0; i < members.size(); ++i) {
+        expect(!cancel.load(), "gguf_cancelled");
+        s.files.emplace_back(members[i], "gguf_open_failed", "gguf_not_regular_file");
+        GgufHeader h = decode_header(s.files.back(), i);
+        for (auto& t : h.tensors) {
+            expect(s.by_name.emplace(t.name, s.tensors.size()).second, "gguf_duplicate_tensor");
+            s.tensors.push_back(std::move(t));
         }
-        const std::uint64_t expected =
-            single ? parsed.tensors.size()
-                   : integer_of(find_key(parsed.metadata, "split.tensors.count"));
-        if (i == 0)
-            total = expected;
-        require(expected == total && total <= 200000, "gguf_split_metadata");
-        for (std::size_t t = 0; t < parsed.tensors.size(); ++t)
-            impl_->tensors.push_back({std::move(parsed.tensors[t]), i,
-                                      add(parsed.data_begin, parsed.offsets[t])});
-        if (i == 0)
-            impl_->metadata = std::move(parsed.metadata);
+        per_file.push_back(std::move(h.metadata));
     }
-    require(impl_->tensors.size() == total, "gguf_tensor_count");
-    std::sort(impl_->tensors.begin(), impl_->tensors.end(),
-              [](const auto& a, const auto& b) { return a.tensor.name < b.tensor.name; });
-    for (std::size_t i = 1; i < impl_->tensors.size(); ++i)
-        require(impl_->tensors[i - 1].tensor.name != impl_->tensors[i].tensor.name,
-                "gguf_duplicate_tensor");
-    check_unchanged();
-}
-
-GgufCheckpoint::~GgufCheckpoint() = default;
-
-std::size_t GgufCheckpoint::tensor_count() const {
-    return impl_->tensors.size();
-}
-
-const GgufTensor& GgufCheckpoint::tensor(std::string_view name) const {
-    return impl_->find(name).tensor;
-}
-
-const GgufTensor& GgufCheckpoint::tensor_at(std::size_t index) const {
-    if (index >= impl_->tensors.size())
-        throw std::out_of_range("gguf_tensor_index");
-    return impl_->tensors[index].tensor;
-}
-
-void GgufCheckpoint::check_unchanged() const {
-    for (const auto& f : impl_->files)
-        f.unchanged();
-}
-
-WeightIdentity GgufCheckpoint::identity(std::string_view name, std::size_t expert) const {
-    const auto& e = impl_->find(name);
-    require(expert < e.tensor.shape[2], "gguf_expert_range");
-    const File& file = impl_->files[e.file];
-    file.unchanged();
-    const auto bytes = e.tensor.bytes / e.tensor.shape[2];
-    const auto begin = add(e.begin, mul(expert, bytes));
-    return file.identity(begin, add(begin, bytes));
-}
-
-void GgufCheckpoint::read_packed_rows(std::string_view name, std::size_t expert,
-                                      std::size_t first_row, std::span<std::byte> output,
-                                      const std::atomic_bool& cancel) const {
-    stop(cancel);
-    const auto& e = impl_->find(name);
-    const auto& t = e.tensor;
-    std::uint64_t values = 0, bytes = 0;
-    (void)block_geometry(t.type, values, bytes);
-    const std::uint64_t row_bytes = t.shape[0] / values * bytes;
-    require(t.rank >= 2 && expert < t.shape[2] && output.size() % row_bytes == 0 &&
-                first_row <= t.shape[1] && output.size() / row_bytes <= t.shape[1] - first_row,
-            "gguf_row_range");
-    const File& file = impl_->files[e.file];
-    file.unchanged();
-    const auto first = add(mul(expert, t.shape[1]), first_row);
-    const auto offset = add(e.begin, mul(first, row_bytes));
-    auto raw = std::span(reinterpret_cast<std::uint8_t*>(output.data()), output.size());
-    for (std::size_t at = 0; at < raw.size();) {
-        stop(cancel);
-        const std::size_t n = std::min<std::size_t>(1024 * 1024, raw.size() - at);
-        file.read(add(offset, at), raw.subspan(at, n), &cancel);
-        at += n;
-    }
-    file.unchanged();
-    stop(cancel);
-}
-
-void GgufCheckpoint::read_vector(std::string_view name, std::span<float> output,
-                                 const std::atomic_bool& cancel) const {
-    stop(cancel);
-    const auto& e = impl_->find(name);
-    const auto& t = e.tensor;
-    require(t.type == KDQ_F32 && output.size() == t.shape[0] * t.shape[1] * t.shape[2] &&
-                output.size_bytes() == t.bytes,
-            "gguf_vector_shape");
-    const File& file = impl_->files[e.file];
-    file.unchanged();
-    auto raw = std::span(reinterpret_cast<std::uint8_t*>(output.data()), output.size_bytes());
-    for (std::size_t at = 0; at < raw.size();) {
-        stop(cancel);
-        const std::size_t n = std::min<std::size_t>(65536, raw.size() - at);
-        file.read(add(e.begin, at), raw.subspan(at, n), &cancel);
-        at += n;
-    }
-    for (float v : output)
-        require(std::isfinite(v), "gguf_nonfinite_weight");
-    file.unchanged();
-    stop(cancel);
-}
-
-void GgufCheckpoint::read_rows(std::string_view name, std::size_t expert, std::size_t first_row,
-                               std::span<float> output, const std::atomic_bool& cancel,
-                               HipDenseCompute& compute) const {
-    stop(cancel);
-    const auto& t = impl_->find(name).tensor;
-    std::uint64_t values = 0, bytes = 0;
-    (void)block_geometry(t.type, values, bytes);
-    const std::uint64_t row_bytes = t.shape[0] / values * bytes;
-    require(t.rank >= 2 && expert < t.shape[2] && output.size() % t.shape[0] == 0 &&
-                first_row <= t.shape[1] && output.size() / t.shape[0] <= t.shape[1] - first_row,
-            "gguf_row_range");
-    const std::size_t rows = output.size() / t.shape[0];
-    const std::size_t batch = std::max<std::size_t>(1, std::min<std::size_t>(
-                                                           rows, (16u << 20) / row_bytes));
-    std::vector<std::byte> packed(batch * row_bytes);
-    for (std::size_t r = 0; r < rows; r += batch) {
-        const std::size_t n = std::min(batch, rows - r);
-        auto chunk = std::span(packed).first(n * row_bytes);
-        read_packed_rows(name, expert, first_row + r, chunk, cancel);
-        auto out = output.subspan(r * t.shape[0], n * t.shape[0]);
-        if (t.type == KDQ_F32) {
-            std::memcpy(out.data(), chunk.data(), chunk.size());
-            for (float v : out)
-                require(std::isfinite(v), "gguf_nonfinite_weight");
-        } else {
-            const auto enc = gguf::encoding(t.type);
-            require(enc.has_value(), "gguf_tensor_type");
-            compute.dequantize_rows(*enc, chunk, t.shape[0], out);  // throws when nonfinite
+    if (split) {
+        // every part names its place in the set, and any tensor total it states is the set's
+        for (std::size_t i = 0; i < per_file.size(); ++i) {
+            expect(whole_number(per_file[i], "split.no") == std::uint64_t(i) &&
+                       whole_number(per_file[i], "split.count") == per_file.size(),
+                   "gguf_split_metadata");
+            const auto total = whole_number(per_file[i], "split.tensors.count");
+            expect(!per_file[i].contains("split.tensors.count") || total == s.tensors.size(),
+                   "gguf_split_metadata");
         }
     }
+    s.metadata = std::move(per_file.front());
 }
 
-HipDenseCompute::GgufWeightSource GgufCheckpoint::source(std::string_view name,
-                                                         std::size_t expert,
-                                                         const std::atomic_bool& cancel) const {
-    (void)impl_->find(name);  // the tensor exists
-    std::string key(name);
-    return [this, key, expert, &cancel](std::size_t first, std::span<std::byte> rows) {
-        read_packed_rows(key, expert, first, rows, cancel);
+GgufFiles::~GgufFiles() = default;
+
+std::size_t GgufFiles::size() const {
+    return state_->tensors.size();
+}
+
+const GgufTensorInfo& GgufFiles::info(std::size_t index) const {
+    expect(index < state_->tensors.size(), "gguf_tensor_index");
+    return state_->tensors[index];
+}
+
+const GgufTensorInfo& GgufFiles::info(std::string_view name) const {
+    const auto it = state_->by_name.find(name);
+    expect(it != state_->by_name.end(), "gguf_missing_tensor");
+    return state_->tensors[it->second];
+}
+
+WeightIdentity GgufFiles::slice_identity(std::string_view name, std::size_t expert) const {
+    const auto& t = info(name);
+    expect(expert < t.experts, "gguf_expert_range");
+    const auto begin = t.offset + expert * t.slice_bytes;
+    return state_->files[t.file].identity(begin, begin + t.slice_bytes);
+}
+
+void GgufFiles::verify_unchanged() const {
+    for (const auto& f : state_->files)
+        expect(!f.moved(), "gguf_checkpoint_changed");
+}
+
+void GgufFiles::copy_rows(std::string_view name, std::size_t expert, std::size_t first_row,
+                          std::span<std::byte> out, const std::atomic_bool& cancel) const {
+    const auto& t = info(name);
+    const bool whole = t.rank >= 2 && out.size() % t.row_bytes == 0;
+    const std::uint64_t rows = whole ? out.size() / t.row_bytes : 0;
+    expect(whole && expert < t.experts && first_row <= t.rows && rows <= t.rows - first_row,
+           "gguf_row_range");
+    verify_unchanged();
+    expect(!cancel.load(), "gguf_cancelled");
+    if (out.empty())
+        return;
+    state_->files[t.file].read(t.offset + expert * t.slice_bytes + first_row * t.row_bytes, out,
+                               "gguf_read_bounds", "gguf_read_failed");
+}
+
+void GgufFiles::copy_vector(std::string_view name, std::span<float> out,
+                            const std::atomic_bool& cancel) const {
+    const auto& t = info(name);
+    expect(t.rank == 1 && t.ggml_type == KDQ_F32 && out.size() == t.columns, "gguf_vector_shape");
+    verify_unchanged();
+    expect(!cancel.load(), "gguf_cancelled");
+    state_->files[t.file].read(t.offset, std::as_writable_bytes(out), "gguf_read_bounds",
+                               "gguf_read_failed");
+    for (float v : out)
+        expect(std::isfinite(v), "gguf_nonfinite_weight");
+}
+
+void GgufFiles::decode_rows(std::string_view name, std::size_t expert, std::size_t first_row,
+                            std::span<float> out, const std::atomic_bool& cancel,
+                            HipDenseCompute& compute) const {
+    const auto& t = info(name);
+    expect(out.size() % t.columns == 0, "gguf_row_range");
+    const std::size_t rows = out.size() / t.columns;
+    std::vector<std::byte> packed(rows * t.row_bytes);
+    copy_rows(name, expert, first_row, packed, cancel);
+    if (t.ggml_type == KDQ_F32 || t.ggml_type == KDQ_F16) {
+        for (std::size_t i = 0; i < out.size(); ++i) {
+            if (t.ggml_type == KDQ_F32) {
+                std::memcpy(&out[i], packed.data() + 4 * i, 4);
+            } else {
+                std::uint16_t h;
+                std::memcpy(&h, packed.data() + 2 * i, 2);
+                out[i] = half_to_float(h);
+            }
+            expect(std::isfinite(out[i]), "gguf_nonfinite_weight");
+        }
+        return;
+    }
+    const auto enc = gguf::encoding(t.ggml_type);
+    expect(enc.has_value(), "gguf_tensor_type");
+    try {
+        compute.dequantize_rows(*enc, packed, t.columns, out);
+    } catch (const std::runtime_error& e) {
+        if (std::string_view(e.what()) == "kdq_nonfinite_weight")
+            fail("gguf_nonfinite_weight");
+        throw;
+    }
+}
+
+HipDenseCompute::GgufWeightSource GgufFiles::row_source(std::string_view name,
+                                                        std::size_t expert,
+                                                        const std::atomic_bool& cancel) const {
+    info(name);  // an unknown name is refused now, not at the first read
+    return [this, tensor = std::string(name), expert, &cancel](std::size_t first,
+                                                               std::span<std::byte> out) {
+        copy_rows(tensor, expert, first, out, cancel);
     };
 }
 
-bool GgufCheckpoint::has(std::string_view key) const {
-    return impl_->metadata.find(key) != impl_->metadata.end();
+bool GgufFiles::has(std::string_view key) const {
+    return state_->metadata.contains(key);
 }
 
-std::string GgufCheckpoint::string(std::string_view key) const {
-    const auto* s = std::get_if<std::string>(&find_key(impl_->metadata, key));
-    require(s != nullptr, "gguf_metadata_string");
-    return *s;
+const GgufValue& GgufFiles::value(std::string_view key) const {
+    const auto it = state_->metadata.find(key);
+    expect(it != state_->metadata.end(), "gguf_missing_metadata");
+    return it->second;
 }
 
-std::uint64_t GgufCheckpoint::integer(std::string_view key) const {
-    return integer_of(find_key(impl_->metadata, key));
-}
-
-double GgufCheckpoint::number(std::string_view key) const {
-    const auto* s = std::get_if<Scalar>(&find_key(impl_->metadata, key));
-    require(s && s->type != kBool, "gguf_metadata_number");
-    return number_of(*s);
-}
-
-bool GgufCheckpoint::boolean(std::string_view key) const {
-    const auto* s = std::get_if<Scalar>(&find_key(impl_->metadata, key));
-    require(s && s->type == kBool, "gguf_metadata_boolean");
-    return s->bits != 0;
-}
-
-std::vector<bool> GgufCheckpoint::booleans(std::string_view key) const {
-    const auto* a = std::get_if<Array>(&find_key(impl_->metadata, key));
-    require(a && a->element == kBool, "gguf_metadata_boolean");
-    std::vector<bool> out;
-    for (const auto& s : a->values)
-        out.push_back(s.bits != 0);
-    return out;
-}
-
-std::vector<std::string> GgufCheckpoint::strings(std::string_view key) const {
-    const auto* a = std::get_if<Array>(&find_key(impl_->metadata, key));
-    require(a && a->element == kString, "gguf_metadata_string");
-    return a->texts;
-}
-
-std::vector<std::int64_t> GgufCheckpoint::integers(std::string_view key) const {
-    const auto* a = std::get_if<Array>(&find_key(impl_->metadata, key));
-    require(a && is_integer(a->element), "gguf_metadata_integer");
-    std::vector<std::int64_t> out;
-    for (const auto& s : a->values) {
-        require(s.type != kU64 || s.bits <= std::uint64_t(INT64_MAX), "gguf_metadata_integer");
-        out.push_back(signed_of(s));
-    }
-    return out;
-}
-
-std::vector<double> GgufCheckpoint::numbers(std::string_view key) const {
-    const auto* a = std::get_if<Array>(&find_key(impl_->metadata, key));
-    require(a && a->element != kBool, "gguf_metadata_number");
-    std::vector<double> out;
-    for (const auto& s : a->values)
-        out.push_back(number_of(s));
-    return out;
-}
-
-// ------------------------------------------------------------- safetensors
+// ------------------------------------------------------------------ safetensors
 
 namespace {
 
-// A JSON reader for safetensors headers: objects, arrays, strings, integers (and the
-// literals); depth and size bounded.  Numbers other than non-negative integers are kept
-// as text.
+constexpr std::uint64_t kSafetensorsHeaderLimit = 100000000;  // the specification's cap
+
+// A parsed JSON value.  Numbers keep their literal text; only the unsigned integers the
+// header's fields need are ever converted.
 struct Json {
-    enum Kind { object, array, string, number, literal } kind = literal;
-    std::string text;  // string value, number text or literal
-    std::vector<std::pair<std::string, Json>> members;
+    enum class Kind { null, boolean, number, string, array, object } kind = Kind::null;
+    bool flag = false;
+    std::string text;
     std::vector<Json> items;
+    std::vector<std::pair<std::string, Json>> members;  // in file order
 };
 
-class JsonParser {
+// Recursive descent over the header text.  Strings must be ASCII (raw bytes and \u
+// escapes alike), escapes exactly as JSON defines them.
+class JsonReader {
 public:
-    explicit JsonParser(std::string_view s) : s_(s) {}
+    explicit JsonReader(std::string_view s) : s_(s) {}
 
     Json document() {
         Json v = value(0);
         space();
-        require(i_ == s_.size(), "safetensors_header_json");
+        expect(i_ == s_.size(), "safetensors_header_json");
         return v;
     }
 
 private:
-    std::string_view s_;
-    std::size_t i_ = 0;
-
     void space() {
         while (i_ < s_.size() && (s_[i_] == ' ' || s_[i_] == '\t' || s_[i_] == '\n' ||
                                   s_[i_] == '\r'))
             ++i_;
     }
-    char peek() {
+    char next() {
+        expect(i_ < s_.size(), "safetensors_header_json");
+        return s_[i_++];
+    }
+    void literal(std::string_view word) {
+        expect(s_.substr(i_, word.size()) == word, "safetensors_header_json");
+        i_ += word.size();
+    }
+
+    Json value(int depth) {
+        expect(depth < 32, "safetensors_header_json");
         space();
-        require(i_ < s_.size(), "safetensors_header_json");
-        return s_[i_];
+        expect(i_ < s_.size(), "safetensors_header_json");
+        Json v;
+        const char c = s_[i_];
+        if (c == '{') {
+            v.kind = Json::Kind::object;
+            ++i_;
+            space();
+            if (i_ < s_.size() && s_[i_] == '}') {
+                ++i_;
+                return v;
+            }
+            for (;;) {
+                space();
+                expect(i_ < s_.size() && s_[i_] == '"', "safetensors_header_json");
+                std::string key = string();
+                space();
+                expect(next() == ':', "safetensors_header_json");
+                v.members.emplace_back(std::move(key), value(depth + 1));
+                space();
+                const char sep = next();
+                if (sep == '}')
+                    return v;
+                expect(sep == ',', "safetensors_header_json");
+            }
+        }
+        if (c == '[') {
+            v.kind = Json::Kind::array;
+            ++i_;
+            space();
+            if (i_ < s_.size() && s_[i_] == ']') {
+                ++i_;
+                return v;
+            }
+            for (;;) {
+                v.items.push_back(value(depth + 1));
+                space();
+                const char sep = next();
+                if (sep == ']')
+                    return v;
+                expect(sep == ',', "safetensors_header_json");
+            }
+        }
+        if (c == '"') {
+            v.kind = Json::Kind::string;
+            v.text = string();
+            return v;
+        }
+        if (c == 't' || c == 'f') {
+            v.kind = Json::Kind::boolean;
+            v.flag = c == 't';
+            literal(v.flag ? "true" : "false");
+            return v;
+        }
+        if (c == 'n') {
+            literal("null");
+            return v;
+        }
+        v.kind = Json::Kind::number;
+        v.text = number();
+        return v;
     }
-    void expect(char c) {
-        require(peek() == c, "safetensors_header_json");
-        ++i_;
+
+    std::string number() {
+        const std::size_t begin = i_;
+        auto digits = [&] {
+            const std::size_t from = i_;
+            while (i_ < s_.size() && s_[i_] >= '0' && s_[i_] <= '9')
+                ++i_;
+            expect(i_ > from, "safetensors_header_json");
+        };
+        if (s_[i_] == '-')
+            ++i_;
+        digits();
+        if (i_ < s_.size() && s_[i_] == '.') {
+            ++i_;
+            digits();
+        }
+        if (i_ < s_.size() && (s_[i_] == 'e' || s_[i_] == 'E')) {
+            ++i_;
+            if (i_ < s_.size() && (s_[i_] == '+' || s_[i_] == '-'))
+                ++i_;
+            digits();
+        }
+        return std::string(s_.substr(begin, i_ - begin));
     }
-    std::string str() {
-        expect('"');
+
+    std::string string() {
+        ++i_;  // the opening quote
         std::string out;
         for (;;) {
-            require(i_ < s_.size(), "safetensors_header_json");
-            const char c = s_[i_++];
+            const auto c = static_cast<unsigned char>(next());
             if (c == '"')
                 return out;
+            expect(c >= 0x20, "safetensors_header_json");  // control characters
+            expect(c < 0x80, "safetensors_header_ascii");
             if (c != '\\') {
-                out.push_back(c);
+                out.push_back(char(c));
                 continue;
             }
-            require(i_ < s_.size(), "safetensors_header_json");
-            const char e = s_[i_++];
+            const char e = next();
             switch (e) {
             case '"': case '\\': case '/': out.push_back(e); break;
             case 'b': out.push_back('\b'); break;
@@ -686,275 +822,247 @@ private:
             case 'r': out.push_back('\r'); break;
             case 't': out.push_back('\t'); break;
             case 'u': {
-                require(i_ + 4 <= s_.size(), "safetensors_header_json");
-                const unsigned cp = unsigned(std::stoul(std::string(s_.substr(i_, 4)), nullptr, 16));
-                i_ += 4;
-                if (cp < 0x80) {
-                    out.push_back(char(cp));
-                } else if (cp < 0x800) {
-                    out.push_back(char(0xC0 | (cp >> 6)));
-                    out.push_back(char(0x80 | (cp & 63)));
-                } else {
-                    out.push_back(char(0xE0 | (cp >> 12)));
-                    out.push_back(char(0x80 | ((cp >> 6) & 63)));
-                    out.push_back(char(0x80 | (cp & 63)));
+                unsigned code = 0;
+                for (int k = 0; k < 4; ++k) {
+                    const char h = next();
+                    const unsigned digit = h >= '0' && h <= '9'   ? unsigned(h - '0')
+                                           : h >= 'a' && h <= 'f' ? unsigned(h - 'a' + 10)
+                                           : h >= 'A' && h <= 'F' ? unsigned(h - 'A' + 10)
+                                                                  : 16u;
+                    expect(digit < 16, "safetensors_header_json");
+                    code = 16 * code + digit;
                 }
+                expect(code < 0x80, "safetensors_header_ascii");
+                out.push_back(char(code));
                 break;
             }
-            default: throw std::invalid_argument("safetensors_header_json");
+            default: fail("safetensors_header_json");
             }
         }
     }
-    Json value(int depth) {
-        require(depth < 16, "safetensors_header_json");
-        Json v;
-        const char c = peek();
-        if (c == '{') {
-            v.kind = Json::object;
-            ++i_;
-            if (peek() == '}') {
-                ++i_;
-                return v;
-            }
-            for (;;) {
-                std::string k = str();
-                expect(':');
-                v.members.emplace_back(std::move(k), value(depth + 1));
-                if (peek() == ',') {
-                    ++i_;
-                    continue;
-                }
-                expect('}');
-                return v;
-            }
-        }
-        if (c == '[') {
-            v.kind = Json::array;
-            ++i_;
-            if (peek() == ']') {
-                ++i_;
-                return v;
-            }
-            for (;;) {
-                v.items.push_back(value(depth + 1));
-                if (peek() == ',') {
-                    ++i_;
-                    continue;
-                }
-                expect(']');
-                return v;
-            }
-        }
-        if (c == '"') {
-            v.kind = Json::string;
-            v.text = str();
-            return v;
-        }
-        const std::size_t start = i_;
-        while (i_ < s_.size() && s_[i_] != ',' && s_[i_] != '}' && s_[i_] != ']' &&
-               s_[i_] != ' ' && s_[i_] != '\n' && s_[i_] != '\r' && s_[i_] != '\t')
-            ++i_;
-        require(i_ > start, "safetensors_header_json");
-        v.text = std::string(s_.substr(start, i_ - start));
-        v.kind = (v.text == "true" || v.text == "false" || v.text == "null") ? Json::literal
-                                                                               : Json::number;
-        return v;
-    }
+
+    std::string_view s_;
+    std::size_t i_ = 0;
 };
 
-std::uint64_t json_integer(const Json& j) {
-    require(j.kind == Json::number && !j.text.empty() && j.text.size() <= 19 &&
-                std::all_of(j.text.begin(), j.text.end(), [](char c) { return c >= '0' && c <= '9'; }),
-            "safetensors_header_integer");
-    return std::stoull(j.text);
+// A JSON number that is a plain non-negative integer within 64 bits.
+std::uint64_t unsigned_of(const Json& v) {
+    expect(v.kind == Json::Kind::number && !v.text.empty(), "safetensors_header_integer");
+    std::uint64_t r = 0;
+    for (char c : v.text) {
+        expect(c >= '0' && c <= '9', "safetensors_header_integer");
+        r = add_or(mul_or(r, 10, "safetensors_header_integer"), std::uint64_t(c - '0'),
+                   "safetensors_header_integer");
+    }
+    return r;
 }
 
-Dtype dtype_of(const std::string& s, std::uint64_t& width) {
-    if (s == "U8") return width = 1, Dtype::u8;
-    if (s == "I8") return width = 1, Dtype::i8;
-    if (s == "F16") return width = 2, Dtype::f16;
-    if (s == "BF16") return width = 2, Dtype::bf16;
-    if (s == "F32") return width = 4, Dtype::f32;
-    static const std::map<std::string, std::uint64_t> others = {
-        {"BOOL", 1}, {"F8_E4M3", 1}, {"F8_E5M2", 1}, {"I16", 2}, {"U16", 2}, {"I32", 4},
-        {"U32", 4}, {"I64", 8}, {"U64", 8}, {"F64", 8}};
-    const auto it = others.find(s);
-    require(it != others.end(), "safetensors_dtype");
-    width = it->second;
-    return Dtype::other;
+struct DtypeName {
+    std::string_view name;
+    Dtype dtype;
+    std::uint64_t bytes;
+};
+
+constexpr DtypeName kDtypes[] = {
+    {"BOOL", Dtype::boolean, 1}, {"U8", Dtype::u8, 1},        {"I8", Dtype::i8, 1},
+    {"U16", Dtype::u16, 2},      {"I16", Dtype::i16, 2},      {"F16", Dtype::f16, 2},
+    {"BF16", Dtype::bf16, 2},    {"U32", Dtype::u32, 4},      {"I32", Dtype::i32, 4},
+    {"F32", Dtype::f32, 4},      {"U64", Dtype::u64, 8},      {"I64", Dtype::i64, 8},
+    {"F64", Dtype::f64, 8},      {"F8_E4M3", Dtype::f8_e4m3, 1}, {"F8_E5M2", Dtype::f8_e5m2, 1},
+};
+
+// One tensor entry: exactly the fields dtype, shape and data_offsets, each once.
+SafetensorsInfo tensor_entry(const std::string& name, const Json& entry,
+                             std::uint64_t payload_at) {
+    expect(entry.kind == Json::Kind::object, "safetensors_tensor");
+    const Json *dtype = nullptr, *shape = nullptr, *offsets = nullptr;
+    for (const auto& [field, v] : entry.members) {
+        const Json** slot = field == "dtype"          ? &dtype
+                            : field == "shape"        ? &shape
+                            : field == "data_offsets" ? &offsets
+                                                      : nullptr;
+        expect(slot != nullptr, "safetensors_tensor");
+        expect(*slot == nullptr, "safetensors_duplicate");
+        *slot = &v;
+    }
+    expect(dtype && shape && offsets, "safetensors_tensor");
+    expect(dtype->kind == Json::Kind::string, "safetensors_dtype");
+    const DtypeName* kind = nullptr;
+    for (const auto& d : kDtypes)
+        if (d.name == dtype->text)
+            kind = &d;
+    expect(kind != nullptr, "safetensors_dtype");
+    SafetensorsInfo t;
+    t.name = name;
+    t.dtype = kind->dtype;
+    expect(shape->kind == Json::Kind::array, "safetensors_tensor_shape");
+    std::uint64_t elements = 1;
+    for (const auto& d : shape->items) {
+        t.shape.push_back(unsigned_of(d));
+        elements = mul_or(elements, t.shape.back(), "safetensors_tensor_shape");
+    }
+    expect(offsets->kind == Json::Kind::array && offsets->items.size() == 2,
+           "safetensors_tensor");
+    const auto begin = unsigned_of(offsets->items[0]), end = unsigned_of(offsets->items[1]);
+    expect(begin <= end &&
+               end - begin == mul_or(elements, kind->bytes, "safetensors_tensor_shape"),
+           "safetensors_tensor_shape");
+    t.begin = add_or(payload_at, begin, "safetensors_tensor_bounds");
+    t.end = add_or(payload_at, end, "safetensors_tensor_bounds");
+    return t;
 }
 
 }  // namespace
 
-struct SafetensorsShard::Impl {
-    std::unique_ptr<File> file;
-    std::vector<SafetensorsTensor> tensors;  // sorted by name
+struct SafetensorsFile::State {
+    Descriptor file;
+    std::vector<SafetensorsInfo> tensors;
+    std::map<std::string, std::size_t, std::less<>> by_name;
     std::map<std::string, std::string, std::less<>> metadata;
-
-    const SafetensorsTensor& find(std::string_view name) const {
-        const auto it = std::lower_bound(tensors.begin(), tensors.end(), name,
-                                         [](const SafetensorsTensor& t, std::string_view n) {
-                                             return t.name < n;
-                                         });
-        require(it != tensors.end() && it->name == name, "missing_tensor");
-        return *it;
-    }
-    void read(const SafetensorsTensor& t, std::uint64_t offset, std::span<std::uint8_t> out) const {
-        require(offset <= t.end - t.begin && out.size() <= t.end - t.begin - offset,
-                "checkpoint_read_bounds");
-        file->read(t.begin + offset, out, nullptr, "checkpoint_read_bounds");
-    }
+    explicit State(const std::string& path)
+        : file(path, "checkpoint_open_failed", "checkpoint_not_regular_file") {}
 };
 
-SafetensorsShard::SafetensorsShard(const std::string& path) : impl_(std::make_unique<Impl>()) {
-    impl_->file = std::make_unique<File>(::open(path.c_str(), O_RDONLY | O_NOFOLLOW | O_CLOEXEC),
-                                         "checkpoint_changed", 8);
-    const File& f = *impl_->file;
-    std::array<std::uint8_t, 8> head{};
-    f.read(0, head, nullptr, "safetensors_header");
-    std::uint64_t n = 0;
-    for (int i = 0; i < 8; ++i)
-        n |= std::uint64_t(head[i]) << (8 * i);
-    require(n <= 100 * 1024 * 1024 && n <= f.size() - 8, "safetensors_header_size");
-    std::string text(std::size_t(n), '\0');
-    f.read(8, {reinterpret_cast<std::uint8_t*>(text.data()), text.size()}, nullptr,
-           "safetensors_header");
-    const Json doc = JsonParser(text).document();
-    require(doc.kind == Json::object, "safetensors_header_json");
-    const std::uint64_t data = 8 + n;
-    std::vector<std::pair<std::uint64_t, std::uint64_t>> ranges;
-    for (const auto& [name, v] : doc.members) {
-        if (name == "__metadata__") {
-            require(v.kind == Json::object, "safetensors_metadata");
-            for (const auto& [k, s] : v.members) {
-                require(s.kind == Json::string, "safetensors_metadata");
-                impl_->metadata[k] = s.text;
+SafetensorsFile::SafetensorsFile(const std::string& path)
+    : state_(std::make_unique<State>(path)) {
+    auto& s = *state_;
+    std::uint64_t header = 0;
+    s.file.read(0, std::as_writable_bytes(std::span<std::uint64_t>(&header, 1)),
+                "safetensors_header_size", "checkpoint_read_bounds");
+    expect(header <= kSafetensorsHeaderLimit && header <= s.file.size() - 8,
+           "safetensors_header_size");
+    std::string text(std::size_t(header), '\0');
+    s.file.read(8, std::as_writable_bytes(std::span<char>(text)), "safetensors_header_size",
+                "checkpoint_read_bounds");
+    const Json root = JsonReader(text).document();
+    expect(root.kind == Json::Kind::object, "safetensors_header");
+    const std::uint64_t payload_at = 8 + header, payload = s.file.size() - payload_at;
+    bool seen_metadata = false;
+    for (const auto& [key, v] : root.members) {
+        if (key == "__metadata__") {
+            expect(!seen_metadata, "safetensors_duplicate");
+            seen_metadata = true;
+            expect(v.kind == Json::Kind::object, "safetensors_metadata");
+            for (const auto& [k, m] : v.members) {
+                expect(m.kind == Json::Kind::string, "safetensors_metadata");
+                expect(s.metadata.emplace(k, m.text).second, "safetensors_duplicate");
             }
             continue;
         }
-        require(v.kind == Json::object && !name.empty() && name.size() <= 1024,
-                "safetensors_tensor");
-        SafetensorsTensor t;
-        t.name = name;
-        const Json *dtype = nullptr, *shape = nullptr, *offsets = nullptr;
-        for (const auto& [k, m] : v.members) {
-            if (k == "dtype")
-                dtype = &m;
-            else if (k == "shape")
-                shape = &m;
-            else if (k == "data_offsets")
-                offsets = &m;
-        }
-        require(dtype && shape && offsets && dtype->kind == Json::string &&
-                    shape->kind == Json::array && offsets->kind == Json::array &&
-                    offsets->items.size() == 2 && shape->items.size() <= 8,
-                "safetensors_tensor");
-        std::uint64_t width = 0;
-        t.dtype = dtype_of(dtype->text, width);
-        std::uint64_t count = 1;
-        for (const auto& d : shape->items) {
-            t.shape.push_back(json_integer(d));
-            count = mul(count, t.shape.back(), "safetensors_tensor_shape");
-        }
-        const auto a = json_integer(offsets->items[0]), b = json_integer(offsets->items[1]);
-        require(a <= b && b - a == mul(count, width, "safetensors_tensor_shape") &&
-                    b <= f.size() - data,
-                "safetensors_tensor_bounds");
-        t.begin = data + a;
-        t.end = data + b;
-        ranges.emplace_back(a, b);
-        impl_->tensors.push_back(std::move(t));
+        expect(!key.empty(), "safetensors_tensor");
+        expect(s.by_name.emplace(key, s.tensors.size()).second, "safetensors_duplicate");
+        s.tensors.push_back(tensor_entry(key, v, payload_at));
     }
-    std::sort(ranges.begin(), ranges.end());
-    for (std::size_t i = 1; i < ranges.size(); ++i)
-        require(ranges[i].first >= ranges[i - 1].second, "safetensors_tensor_overlap");
-    std::sort(impl_->tensors.begin(), impl_->tensors.end(),
-              [](const auto& x, const auto& y) { return x.name < y.name; });
-    for (std::size_t i = 1; i < impl_->tensors.size(); ++i)
-        require(impl_->tensors[i - 1].name != impl_->tensors[i].name, "safetensors_duplicate");
-    f.unchanged();
+    // the tensors tile the payload: from its first byte, no overlap, no gap, to its end
+    std::vector<const SafetensorsInfo*> order;
+    for (const auto& t : s.tensors)
+        order.push_back(&t);
+    std::sort(order.begin(), order.end(), [](const auto* a, const auto* b) {
+        return a->begin != b->begin ? a->begin < b->begin : a->end < b->end;
+    });
+    std::uint64_t covered = payload_at;
+    for (const auto* t : order) {
+        expect(t->begin >= covered, "safetensors_tensor_overlap");
+        expect(t->begin == covered, "safetensors_tensor_gap");
+        covered = t->end;
+    }
+    expect(covered == payload_at + payload, "safetensors_payload_coverage");
 }
 
-SafetensorsShard::~SafetensorsShard() = default;
+SafetensorsFile::~SafetensorsFile() = default;
 
-std::size_t SafetensorsShard::tensor_count() const {
-    return impl_->tensors.size();
+std::size_t SafetensorsFile::size() const {
+    return state_->tensors.size();
 }
 
-const SafetensorsTensor& SafetensorsShard::tensor(std::string_view name) const {
-    return impl_->find(name);
+const SafetensorsInfo& SafetensorsFile::info(std::string_view name) const {
+    const auto it = state_->by_name.find(name);
+    expect(it != state_->by_name.end(), "missing_tensor");
+    return state_->tensors[it->second];
 }
 
-WeightIdentity SafetensorsShard::identity(std::string_view name) const {
-    const auto& t = impl_->find(name);
-    impl_->file->unchanged();
-    return impl_->file->identity(t.begin, t.end);
+WeightIdentity SafetensorsFile::identity(std::string_view name) const {
+    const auto& t = info(name);
+    return state_->file.identity(t.begin, t.end);
 }
 
-void SafetensorsShard::check_unchanged() const {
-    impl_->file->unchanged();
+void SafetensorsFile::verify_unchanged() const {
+    expect(!state_->file.moved(), "checkpoint_changed");
 }
 
-std::string SafetensorsShard::metadata(std::string_view key) const {
-    const auto it = impl_->metadata.find(key);
-    require(it != impl_->metadata.end(), "safetensors_missing_metadata");
+std::string SafetensorsFile::metadata(std::string_view key) const {
+    const auto it = state_->metadata.find(key);
+    expect(it != state_->metadata.end(), "safetensors_missing_metadata");
     return it->second;
 }
 
-Mxfp4Rows SafetensorsShard::load_mxfp4_expert_rows(std::string_view prefix, std::size_t expert,
-                                                   std::size_t first, std::size_t count,
-                                                   std::size_t payload_budget) const {
-    require(!prefix.empty() && prefix.size() <= 480 && count != 0, "projection_range_or_name");
-    const auto& blocks = impl_->find(std::string(prefix) + "_blocks");
-    const auto& scales = impl_->find(std::string(prefix) + "_scales");
-    require(blocks.dtype == Dtype::u8 && scales.dtype == Dtype::u8, "mxfp4_dtype");
-    require(blocks.shape.size() == 4 && scales.shape.size() == 3 && blocks.shape[3] == 16 &&
-                blocks.shape[2] > 0 && expert < blocks.shape[0] && first <= blocks.shape[1] &&
-                count <= blocks.shape[1] - first &&
-                std::equal(scales.shape.begin(), scales.shape.end(), blocks.shape.begin()),
-            "mxfp4_expert_shape");
-    const std::uint64_t groups = blocks.shape[2];
-    const std::uint64_t scale_bytes = mul(count, groups);
-    const std::uint64_t weight_bytes = mul(scale_bytes, 16);
-    const std::uint64_t total = add(weight_bytes, scale_bytes);
-    require(total <= payload_budget, "payload_budget");
-    const std::uint64_t scale_offset = mul(add(mul(expert, blocks.shape[1]), first), groups);
+namespace {
+
+// The pair <prefix>_blocks U8 [E, R, G, 16] / <prefix>_scales U8 [E, R, G].
+struct Mxfp4Pair {
+    const SafetensorsInfo* blocks;
+    const SafetensorsInfo* scales;
+    std::uint64_t experts, rows, groups;
+};
+
+Mxfp4Pair mxfp4_pair(const SafetensorsFile& f, std::string_view prefix) {
+    expect(!prefix.empty(), "projection_range_or_name");
+    const std::string stem(prefix);
+    const auto& b = f.info(stem + "_blocks");
+    const auto& s = f.info(stem + "_scales");
+    expect(b.dtype == Dtype::u8 && s.dtype == Dtype::u8, "mxfp4_dtype");
+    expect(b.shape.size() == 4 && s.shape.size() == 3 && b.shape[3] == 16 && b.shape[2] > 0 &&
+               std::equal(s.shape.begin(), s.shape.end(), b.shape.begin()),
+           "mxfp4_expert_shape");
+    return {&b, &s, b.shape[0], b.shape[1], b.shape[2]};
+}
+
+// `count` rows of scales then blocks, from row `row` of the flattened [E * R] rows; every
+// scale byte checked before a block byte is read.
+void read_mxfp4(const Descriptor& file, const Mxfp4Pair& p, std::uint64_t row,
+                std::uint64_t count, Mxfp4Rows& out) {
+    out.scales.resize(std::size_t(count * p.groups));
+    out.blocks.resize(std::size_t(count * p.groups * 16));
+    file.read(p.scales->begin + row * p.groups, std::as_writable_bytes(std::span(out.scales)),
+              "checkpoint_read_bounds", "checkpoint_read_bounds");
+    for (std::uint8_t e : out.scales)
+        expect(e != 255, "invalid_block_scale");  // E8M0 255 is NaN, not a scale
+    file.read(p.blocks->begin + row * p.groups * 16, std::as_writable_bytes(std::span(out.blocks)),
+              "checkpoint_read_bounds", "checkpoint_read_bounds");
+}
+
+}  // namespace
+
+Mxfp4Rows SafetensorsFile::mxfp4_rows(std::string_view prefix, std::size_t expert,
+                                      std::size_t first, std::size_t count,
+                                      std::size_t payload_budget) const {
+    expect(count > 0, "projection_range_or_name");
+    const Mxfp4Pair p = mxfp4_pair(*this, prefix);
+    expect(expert < p.experts && first <= p.rows && count <= p.rows - first,
+           "mxfp4_expert_shape");
+    // count <= rows, so the sizes stay below the tensors' own byte counts
+    const std::uint64_t bytes = count * p.groups * 17;
+    expect(bytes <= payload_budget, "payload_budget");
+    verify_unchanged();
     Mxfp4Rows out;
     out.rows = count;
-    out.columns = std::size_t(mul(groups, 32));
-    out.blocks.resize(std::size_t(weight_bytes));
-    out.scales.resize(std::size_t(scale_bytes));
-    impl_->file->unchanged();
-    impl_->read(blocks, mul(scale_offset, 16), out.blocks);
-    impl_->read(scales, scale_offset, out.scales);
-    impl_->file->unchanged();
-    for (auto s : out.scales)  // IW/src/weights/quantization.cpp:46-56
-        require(s != 255, "invalid_block_scale");
+    out.columns = std::size_t(p.groups * 32);
+    read_mxfp4(state_->file, p, expert * p.rows + first, count, out);
     return out;
 }
 
-Mxfp4Rows SafetensorsShard::load_mxfp4_experts(std::string_view prefix, std::size_t& experts,
-                                               std::size_t payload_budget) const {
-    const auto& blocks = impl_->find(std::string(prefix) + "_blocks");
-    require(blocks.shape.size() == 4 && blocks.shape[0] > 0, "mxfp4_expert_shape");
-    experts = std::size_t(blocks.shape[0]);
-    const std::size_t rows = std::size_t(blocks.shape[1]);
-    // the experts' rows lie one after another in both tensors: one load of all of them
-    const std::uint64_t per = add(mul(mul(rows, blocks.shape[2]), 16), mul(rows, blocks.shape[2]));
-    require(mul(per, experts) <= payload_budget, "payload_budget");
-    Mxfp4Rows all;
-    for (std::size_t e = 0; e < experts; ++e) {
-        Mxfp4Rows one = load_mxfp4_expert_rows(prefix, e, 0, rows, payload_budget);
-        if (e == 0) {
-            all.rows = rows;
-            all.columns = one.columns;
-            all.blocks.reserve(one.blocks.size() * experts);
-            all.scales.reserve(one.scales.size() * experts);
-        }
-        all.blocks.insert(all.blocks.end(), one.blocks.begin(), one.blocks.end());
-        all.scales.insert(all.scales.end(), one.scales.begin(), one.scales.end());
-    }
-    return all;
+Mxfp4Rows SafetensorsFile::mxfp4_experts(std::string_view prefix, std::size_t& experts,
+                                         std::size_t payload_budget) const {
+    const Mxfp4Pair p = mxfp4_pair(*this, prefix);
+    const std::uint64_t rows = p.experts * p.rows;  // both bounded by the tensor sizes
+    expect(rows * p.groups * 17 <= payload_budget, "payload_budget");
+    verify_unchanged();
+    Mxfp4Rows out;
+    out.rows = std::size_t(p.rows);
+    out.columns = std::size_t(p.groups * 32);
+    read_mxfp4(state_->file, p, 0, rows, out);
+    experts = std::size_t(p.experts);
+    return out;
 }
 
 }  // namespace kadan_amd::checkpoint

@@ -252,13 +252,13 @@ int kdc_moe_mxfp4(void* handle, unsigned long long id, std::size_t experts, std:
 
 // ------------------------------------------------------------- checkpoints
 
-using kadan_amd::checkpoint::GgufCheckpoint;
-using kadan_amd::checkpoint::SafetensorsShard;
+using kadan_amd::checkpoint::GgufFiles;
+using kadan_amd::checkpoint::SafetensorsFile;
 
 void* kcp_gguf_open(const char* root, int cancelled, char* err, std::size_t len) {
     try {
         const std::atomic_bool cancel{cancelled != 0};
-        return new GgufCheckpoint(root, cancel);
+        return new GgufFiles(root, cancel);
     } catch (const std::exception& e) {
         fail(e, err, len);
         return nullptr;
@@ -266,21 +266,23 @@ void* kcp_gguf_open(const char* root, int cancelled, char* err, std::size_t len)
 }
 
 void kcp_gguf_close(void* c) {
-    delete static_cast<GgufCheckpoint*>(c);
+    delete static_cast<GgufFiles*>(c);
 }
 
 std::size_t kcp_gguf_tensor_count(void* c) {
-    return static_cast<GgufCheckpoint*>(c)->tensor_count();
+    return static_cast<GgufFiles*>(c)->size();
 }
 
+// shape in GGUF order (columns, rows, experts), the listed rank, GGML type, payload bytes
 int kcp_gguf_tensor(void* c, const char* name, unsigned long long* shape, std::size_t* rank,
                     unsigned* type, unsigned long long* bytes, char* err, std::size_t len) {
     try {
-        const auto& t = static_cast<GgufCheckpoint*>(c)->tensor(name);
-        for (int d = 0; d < 3; ++d)
-            shape[d] = t.shape[d];
+        const auto& t = static_cast<GgufFiles*>(c)->info(std::string_view(name));
+        shape[0] = t.columns;
+        shape[1] = t.rows;
+        shape[2] = t.experts;
         *rank = t.rank;
-        *type = t.type;
+        *type = t.ggml_type;
         *bytes = t.bytes;
         return 0;
     } catch (const std::exception& e) {
@@ -299,7 +301,7 @@ static void put_identity(const WeightIdentity& w, unsigned long long* out) {
 int kcp_gguf_identity(void* c, const char* name, std::size_t expert, unsigned long long* out,
                       char* err, std::size_t len) {
     try {
-        put_identity(static_cast<GgufCheckpoint*>(c)->identity(name, expert), out);
+        put_identity(static_cast<GgufFiles*>(c)->slice_identity(name, expert), out);
         return 0;
     } catch (const std::exception& e) {
         return fail(e, err, len);
@@ -308,7 +310,7 @@ int kcp_gguf_identity(void* c, const char* name, std::size_t expert, unsigned lo
 
 int kcp_gguf_check_unchanged(void* c, char* err, std::size_t len) {
     try {
-        static_cast<GgufCheckpoint*>(c)->check_unchanged();
+        static_cast<GgufFiles*>(c)->verify_unchanged();
         return 0;
     } catch (const std::exception& e) {
         return fail(e, err, len);
@@ -320,7 +322,7 @@ int kcp_gguf_read_packed(void* c, const char* name, std::size_t expert, std::siz
                          std::size_t len) {
     try {
         const std::atomic_bool cancel{cancelled != 0};
-        static_cast<GgufCheckpoint*>(c)->read_packed_rows(
+        static_cast<GgufFiles*>(c)->copy_rows(
             name, expert, first, std::span<std::byte>(static_cast<std::byte*>(out), bytes),
             cancel);
         return 0;
@@ -333,58 +335,62 @@ int kcp_gguf_read_vector(void* c, const char* name, float* out, std::size_t n, c
                          std::size_t len) {
     try {
         const std::atomic_bool cancel{false};
-        static_cast<GgufCheckpoint*>(c)->read_vector(name, std::span<float>(out, n), cancel);
+        static_cast<GgufFiles*>(c)->copy_vector(name, std::span<float>(out, n), cancel);
         return 0;
     } catch (const std::exception& e) {
         return fail(e, err, len);
     }
 }
 
-// kind: 0 string, 1 integer, 2 number, 3 boolean, 4 strings (joined by 0x1f), 5 integers,
-// 6 numbers, 7 booleans, 8 has.  Arrays write up to *count values and set *count.
+// kind: 0 text, 1 count, 2 real, 3 flag, 4 texts (joined by 0x1f), 5 integers, 6 reals,
+// 7 flags, 8 has.  Arrays write up to *count values and set *count.
 int kcp_gguf_meta(void* c, const char* key, int kind, char* text, std::size_t text_len,
                   long long* ints, double* nums, std::size_t* count, char* err,
                   std::size_t len) {
     try {
-        const auto* g = static_cast<GgufCheckpoint*>(c);
+        const auto* g = static_cast<GgufFiles*>(c);
         auto put_text = [&](const std::string& s) {
             std::strncpy(text, s.c_str(), text_len - 1);
             text[text_len - 1] = 0;
         };
+        if (kind == 8) {
+            ints[0] = g->has(key);
+            return 0;
+        }
+        const auto& v = g->value(key);
         switch (kind) {
-        case 0: put_text(g->string(key)); break;
-        case 1: ints[0] = (long long)g->integer(key); break;
-        case 2: nums[0] = g->number(key); break;
-        case 3: ints[0] = g->boolean(key); break;
+        case 0: put_text(v.text()); break;
+        case 1: ints[0] = (long long)v.count(); break;
+        case 2: nums[0] = v.real(); break;
+        case 3: ints[0] = v.flag(); break;
         case 4: {
             std::string joined;
-            for (const auto& s : g->strings(key))
+            for (const auto& s : v.texts())
                 joined += s + "\x1f";
             put_text(joined);
             break;
         }
         case 5: {
-            const auto v = g->integers(key);
-            for (std::size_t i = 0; i < v.size() && i < *count; ++i)
-                ints[i] = v[i];
-            *count = v.size();
+            const auto a = v.integers();
+            for (std::size_t i = 0; i < a.size() && i < *count; ++i)
+                ints[i] = a[i];
+            *count = a.size();
             break;
         }
         case 6: {
-            const auto v = g->numbers(key);
-            for (std::size_t i = 0; i < v.size() && i < *count; ++i)
-                nums[i] = v[i];
-            *count = v.size();
+            const auto a = v.reals();
+            for (std::size_t i = 0; i < a.size() && i < *count; ++i)
+                nums[i] = a[i];
+            *count = a.size();
             break;
         }
-        case 7: {
-            const auto v = g->booleans(key);
-            for (std::size_t i = 0; i < v.size() && i < *count; ++i)
-                ints[i] = v[i];
-            *count = v.size();
+        default: {
+            const auto a = v.flags();
+            for (std::size_t i = 0; i < a.size() && i < *count; ++i)
+                ints[i] = a[i];
+            *count = a.size();
             break;
         }
-        default: ints[0] = g->has(key); break;
         }
         return 0;
     } catch (const std::exception& e) {
@@ -392,40 +398,41 @@ int kcp_gguf_meta(void* c, const char* key, int kind, char* text, std::size_t te
     }
 }
 
-// Decoded rows through the device of a dense probe (GgufCheckpoint::read_rows).
+// Decoded rows through the device of a dense probe (GgufFiles::decode_rows).
 int kcp_gguf_read_rows(void* c, void* probe, const char* name, std::size_t expert,
                        std::size_t first, float* out, std::size_t n, char* err,
                        std::size_t len) {
     try {
         const std::atomic_bool cancel{false};
-        static_cast<GgufCheckpoint*>(c)->read_rows(name, expert, first, std::span<float>(out, n),
-                                                   cancel, static_cast<Probe*>(probe)->compute);
+        static_cast<GgufFiles*>(c)->decode_rows(name, expert, first, std::span<float>(out, n),
+                                                cancel, static_cast<Probe*>(probe)->compute);
         return 0;
     } catch (const std::exception& e) {
         return fail(e, err, len);
     }
 }
 
-// dense_gguf_source with the checkpoint's own identity and packed-row source: x [rows x
-// in] -> y [rows x out] (in, out from the tensor's shape).
+// dense_gguf_source with the file set's own identity and row source: x [rows x in] ->
+// y [rows x out] (in, out from the tensor's shape).
 int kcp_gguf_dense_source(void* c, void* probe, const char* name, std::size_t expert,
                           const float* x, std::size_t rows, float* y, int* result,
                           char* err, std::size_t len) {
     try {
-        auto* g = static_cast<GgufCheckpoint*>(c);
+        auto* g = static_cast<GgufFiles*>(c);
         auto* p = static_cast<Probe*>(probe);
-        const auto& t = g->tensor(name);
-        const auto enc = kadan_amd::gguf::encoding(t.type);
+        const auto& t = g->info(std::string_view(name));
+        const auto enc = kadan_amd::gguf::encoding(t.ggml_type);
         if (!enc) {
             *result = 0;
             return 0;
         }
         const std::atomic_bool cancel{false};
-        const auto source = g->source(name, expert, cancel);
-        const std::size_t in = t.shape[0], out = t.shape[1];
+        const auto source = g->row_source(name, expert, cancel);
+        const std::size_t in = t.columns, out = t.rows;
         *result = encode(p->compute.dense_gguf_source(
-            g->identity(name, expert), *enc, source, {}, std::span<const float>(x, rows * in),
-            in, out, std::span<float>(y, rows * out), cancel));
+            g->slice_identity(name, expert), *enc, source, {},
+            std::span<const float>(x, rows * in), in, out, std::span<float>(y, rows * out),
+            cancel));
         return 0;
     } catch (const std::exception& e) {
         return fail(e, err, len);
@@ -434,7 +441,7 @@ int kcp_gguf_dense_source(void* c, void* probe, const char* name, std::size_t ex
 
 void* kcp_st_open(const char* path, char* err, std::size_t len) {
     try {
-        return new SafetensorsShard(path);
+        return new SafetensorsFile(path);
     } catch (const std::exception& e) {
         fail(e, err, len);
         return nullptr;
@@ -442,13 +449,25 @@ void* kcp_st_open(const char* path, char* err, std::size_t len) {
 }
 
 void kcp_st_close(void* s) {
-    delete static_cast<SafetensorsShard*>(s);
+    delete static_cast<SafetensorsFile*>(s);
 }
 
 int kcp_st_identity(void* s, const char* name, unsigned long long* out, char* err,
                     std::size_t len) {
     try {
-        put_identity(static_cast<SafetensorsShard*>(s)->identity(name), out);
+        put_identity(static_cast<SafetensorsFile*>(s)->identity(name), out);
+        return 0;
+    } catch (const std::exception& e) {
+        return fail(e, err, len);
+    }
+}
+
+int kcp_st_metadata(void* s, const char* key, char* text, std::size_t text_len, char* err,
+                    std::size_t len) {
+    try {
+        const auto v = static_cast<SafetensorsFile*>(s)->metadata(key);
+        std::strncpy(text, v.c_str(), text_len - 1);
+        text[text_len - 1] = 0;
         return 0;
     } catch (const std::exception& e) {
         return fail(e, err, len);
@@ -460,8 +479,8 @@ int kcp_st_load_rows(void* s, const char* prefix, std::size_t expert, std::size_
                      std::size_t blocks_n, unsigned char* scales, std::size_t scales_n,
                      std::size_t* columns, char* err, std::size_t len) {
     try {
-        const auto r = static_cast<SafetensorsShard*>(s)->load_mxfp4_expert_rows(
-            prefix, expert, first, count, budget);
+        const auto r = static_cast<SafetensorsFile*>(s)->mxfp4_rows(prefix, expert, first, count,
+                                                                    budget);
         *columns = r.columns;
         std::memcpy(blocks, r.blocks.data(), std::min(blocks_n, r.blocks.size()));
         std::memcpy(scales, r.scales.data(), std::min(scales_n, r.scales.size()));
@@ -471,24 +490,24 @@ int kcp_st_load_rows(void* s, const char* prefix, std::size_t expert, std::size_
     }
 }
 
-// The MXFP4 MoE layer over a shard's expert tensors: the <gate>, <up> and <down> prefixes'
-// _blocks / _scales, loaded by load_mxfp4_experts; the set's bank identity is the gate
-// blocks tensor's.
+// The MXFP4 MoE layer over a file's expert tensors: the <gate>, <up> and <down> prefixes'
+// _blocks / _scales, loaded by mxfp4_experts; the set's bank identity is the gate blocks
+// tensor's.
 int kcp_st_moe(void* s, void* probe, const char* gate, const char* up, const char* down,
                const std::uint16_t* x, const float* logits, std::size_t tokens,
                std::size_t top_k, float* y, int* selected, float* weights, int* result,
                char* err, std::size_t len) {
     try {
-        auto* shard = static_cast<SafetensorsShard*>(s);
+        auto* file = static_cast<SafetensorsFile*>(s);
         std::size_t eg = 0, eu = 0, ed = 0;
         const std::size_t budget = std::size_t(1) << 34;
-        const auto g = shard->load_mxfp4_experts(gate, eg, budget);
-        const auto u = shard->load_mxfp4_experts(up, eu, budget);
-        const auto d = shard->load_mxfp4_experts(down, ed, budget);
+        const auto g = file->mxfp4_experts(gate, eg, budget);
+        const auto u = file->mxfp4_experts(up, eu, budget);
+        const auto d = file->mxfp4_experts(down, ed, budget);
         if (eg != eu || eg != ed || g.rows != u.rows || g.columns != d.rows ||
             d.columns != g.rows)
             throw std::invalid_argument("mxfp4_expert_shape");
-        const WeightIdentity ident = shard->identity(std::string(gate) + "_blocks");
+        const WeightIdentity ident = file->identity(std::string(gate) + "_blocks");
         HipDenseCompute::Mxfp4Experts e{&ident, eg, g.columns, g.rows,
                                         g.blocks, g.scales, u.blocks, u.scales,
                                         d.blocks, d.scales};

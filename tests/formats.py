@@ -116,6 +116,8 @@ def _lib():
     lib.kcp_st_open.argtypes = [ctypes.c_char_p, ctypes.c_char_p, _sz]
     lib.kcp_st_close.argtypes = [_c_p]
     lib.kcp_st_identity.argtypes = [_c_p, ctypes.c_char_p, _c_p, ctypes.c_char_p, _sz]
+    lib.kcp_st_metadata.argtypes = [_c_p, ctypes.c_char_p, ctypes.c_char_p, _sz, ctypes.c_char_p,
+                                    _sz]
     lib.kcp_st_load_rows.argtypes = [_c_p, ctypes.c_char_p, _sz, _sz, _sz, _sz, _c_p, _sz,
                                      _c_p, _sz, _c_p, ctypes.c_char_p, _sz]
     lib.kcp_st_moe.argtypes = [_c_p, _c_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p,
@@ -129,7 +131,7 @@ def _p(a):
 
 
 class Gguf:
-    """GgufCheckpoint (include/kadan_amd_checkpoint.hpp) over a directory."""
+    """GgufFiles (include/kadan_amd_checkpoint.hpp) over a directory."""
 
     def __init__(self, root: str, cancelled: bool = False):
         self.lib = _lib()
@@ -207,7 +209,7 @@ class Gguf:
 
 
 class Safetensors:
-    """SafetensorsShard (include/kadan_amd_checkpoint.hpp) over one file."""
+    """SafetensorsFile (include/kadan_amd_checkpoint.hpp) over one file."""
 
     def __init__(self, path: str):
         self.lib = _lib()
@@ -229,6 +231,11 @@ class Safetensors:
         out = np.zeros(9, np.uint64)
         self._ok(self.lib.kcp_st_identity(self.h, name.encode(), _p(out), self.err, 512))
         return [int(v) for v in out]
+
+    def metadata(self, key):
+        text = ctypes.create_string_buffer(4096)
+        self._ok(self.lib.kcp_st_metadata(self.h, key.encode(), text, 4096, self.err, 512))
+        return text.value.decode()
 
     def load_rows(self, prefix, expert, first, count, groups, budget=1 << 30):
         blocks = np.zeros(count * groups * 16, np.uint8)

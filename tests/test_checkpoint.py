@@ -256,3 +256,154 @@ def test_safetensors_header_refusals(tmp_path):
     path.write_bytes(bytes(raw))
     with pytest.raises(ReaderError, match="safetensors_tensor_overlap"):
         Safetensors(str(path))
+
+
+# ------------------------------------------------------------- header refusals
+
+def raw_safetensors(path, header_text: str, payload: bytes):
+    """A file with this exact JSON header text (padded with spaces to 8 bytes)."""
+    text = header_text.encode("latin-1")
+    text += b" " * ((8 - len(text) % 8) % 8)
+    path.write_bytes(len(text).to_bytes(8, "little") + text + payload)
+
+
+@pytest.mark.parametrize("header,payload,code", [
+    # a gap between two tensors, and payload bytes no tensor covers
+    ('{"a":{"dtype":"U8","shape":[4],"data_offsets":[0,4]},'
+     '"b":{"dtype":"U8","shape":[4],"data_offsets":[6,10]}}', bytes(10), "safetensors_tensor_gap"),
+    ('{"a":{"dtype":"U8","shape":[4],"data_offsets":[0,4]}}', bytes(6),
+     "safetensors_payload_coverage"),
+    ('{"a":{"dtype":"U8","shape":[4],"data_offsets":[2,6]}}', bytes(6), "safetensors_tensor_gap"),
+    # a field twice, a tensor twice, __metadata__ twice, an unknown field, a missing one
+    ('{"a":{"dtype":"U8","dtype":"U8","shape":[4],"data_offsets":[0,4]}}', bytes(4),
+     "safetensors_duplicate"),
+    ('{"a":{"dtype":"U8","shape":[4],"data_offsets":[0,4]},'
+     '"a":{"dtype":"U8","shape":[4],"data_offsets":[4,8]}}', bytes(8), "safetensors_duplicate"),
+    ('{"__metadata__":{"k":"v"},"__metadata__":{"k":"w"},'
+     '"a":{"dtype":"U8","shape":[4],"data_offsets":[0,4]}}', bytes(4), "safetensors_duplicate"),
+    ('{"a":{"dtype":"U8","shape":[4],"data_offsets":[0,4],"extra":1}}', bytes(4),
+     "safetensors_tensor"),
+    ('{"a":{"dtype":"U8","shape":[4]}}', bytes(0), "safetensors_tensor"),
+    # non-ASCII text, raw or escaped; \\u with fewer than four hex digits
+    ('{"é":{"dtype":"U8","shape":[4],"data_offsets":[0,4]}}', bytes(4),
+     "safetensors_header_ascii"),
+    ('{"\\u00e9":{"dtype":"U8","shape":[4],"data_offsets":[0,4]}}', bytes(4),
+     "safetensors_header_ascii"),
+    ('{"\\u12zz":{"dtype":"U8","shape":[4],"data_offsets":[0,4]}}', bytes(4),
+     "safetensors_header_json"),
+    ('{"\\u004":{"dtype":"U8","shape":[4],"data_offsets":[0,4]}}', bytes(4),
+     "safetensors_header_json"),
+    # numbers that are not plain unsigned integers; sizes that disagree; unknown dtype
+    ('{"a":{"dtype":"U8","shape":[-4],"data_offsets":[0,4]}}', bytes(4),
+     "safetensors_header_integer"),
+    ('{"a":{"dtype":"U8","shape":[4.0],"data_offsets":[0,4]}}', bytes(4),
+     "safetensors_header_integer"),
+    ('{"a":{"dtype":"U8","shape":[18446744073709551616],"data_offsets":[0,4]}}', bytes(4),
+     "safetensors_header_integer"),
+    ('{"a":{"dtype":"F32","shape":[4],"data_offsets":[0,4]}}', bytes(4),
+     "safetensors_tensor_shape"),
+    ('{"a":{"dtype":"Q4","shape":[4],"data_offsets":[0,4]}}', bytes(4), "safetensors_dtype"),
+    # not JSON, or trailing text after the object
+    ('{"a":', bytes(0), "safetensors_header_json"),
+    ('{} x', bytes(0), "safetensors_header_json"),
+    ('[]', bytes(0), "safetensors_header"),
+])
+def test_safetensors_refusals(tmp_path, header, payload, code):
+    path = tmp_path / "m.safetensors"
+    raw_safetensors(path, header, payload)
+    with pytest.raises(ReaderError, match=code):
+        Safetensors(str(path))
+
+
+def test_safetensors_accepts_escapes_metadata_and_empty_tensors(tmp_path):
+    path = tmp_path / "m.safetensors"
+    raw_safetensors(path, '{"__metadata__":{"format":"pt","note":"a\\u0041\\n"},'
+                          '"x\\/y":{"dtype":"U8","shape":[4],"data_offsets":[0,4]},'
+                          '"e":{"dtype":"F32","shape":[0,3],"data_offsets":[4,4]}}',
+                    bytes([1, 2, 3, 4]))
+    s = Safetensors(str(path))
+    ident = s.identity("x/y")
+    assert ident[8] - ident[7] == 4
+    assert s.metadata("note") == "aA\n"
+    with pytest.raises(ReaderError, match="safetensors_missing_metadata"):
+        s.metadata("absent")
+    s.close()
+
+
+def test_readers_refuse_a_fifo_without_blocking(tmp_path):
+    fifo = tmp_path / "m.safetensors"
+    os.mkfifo(fifo)
+    with pytest.raises(ReaderError, match="checkpoint_not_regular_file"):
+        Safetensors(str(fifo))
+    d = tmp_path / "g"
+    d.mkdir()
+    os.mkfifo(d / "m.gguf")
+    with pytest.raises(ReaderError, match="gguf_not_regular_file"):
+        Gguf(str(d))
+
+
+def _gguf_dir(tmp_path, name, raw: bytes):
+    d = tmp_path / name
+    d.mkdir()
+    (d / "m.gguf").write_bytes(raw)
+    return str(d)
+
+
+def test_gguf_header_refusals(tmp_path):
+    import struct
+    good = formats.gguf_bytes(metadata(), [("q8", Q8_0, [32, 1], bytes(34))])
+    assert Gguf(_gguf_dir(tmp_path, "good", good)).tensor_count() == 1
+    cases = {
+        "gguf_magic": b"GGUG" + good[4:],
+        # more pairs / tensors than the header could hold
+        "gguf_header_count": good[:8] + struct.pack("<QQ", 1, 1 << 40) + good[24:],
+        # an array whose element count the file cannot hold
+        "gguf_array_limit": formats.gguf_bytes([("k", ARRAY, (U64, [1]))], [])
+        .replace(struct.pack("<IQ", U64, 1), struct.pack("<IQ", U64, 1 << 50)),
+        "gguf_duplicate_key": formats.gguf_bytes([("k", U32, 1), ("k", U32, 2)], []),
+        "gguf_string_nul": formats.gguf_bytes([("k\0x", U32, 1)], []),
+        "gguf_metadata_key": formats.gguf_bytes([("", U32, 1)], []),
+        "gguf_metadata_type": formats.gguf_bytes([("k", U32, 1)], []).replace(
+            struct.pack("<I", U32) + struct.pack("<I", 1), struct.pack("<I", 13) + struct.pack("<I", 1)),
+        "gguf_invalid_metadata": formats.gguf_bytes([("k", BOOL, True)], [])[:-1] + b"\x02",
+        "gguf_alignment": formats.gguf_bytes([("general.alignment", U32, 24)], []),
+        "gguf_duplicate_tensor": formats.gguf_bytes([], [("t", Q8_0, [32, 1], bytes(34)),
+                                                         ("t", Q8_0, [32, 1], bytes(34))]),
+        "gguf_tensor_rank": formats.gguf_bytes([], [("t", Q8_0, [32, 1, 1, 1], bytes(34))]),
+        "gguf_tensor_shape": formats.gguf_bytes([], [("t", Q8_0, [32, 0], b"")]),
+        "gguf_tensor_bounds": formats.gguf_bytes([], [("t", Q8_0, [32, 2], bytes(34))]),
+        "gguf_read_bounds": good[:200],  # ends inside the metadata
+    }
+    for code, raw in cases.items():
+        with pytest.raises(ReaderError, match=code):
+            Gguf(_gguf_dir(tmp_path, code, raw))
+
+
+def test_gguf_split_set_part_missing(tmp_path):
+    formats.write_gguf(tmp_path / "a-00001-of-00003.gguf", metadata(0), [])
+    formats.write_gguf(tmp_path / "a-00002-of-00003.gguf", metadata(1), [])
+    with pytest.raises(ReaderError, match="gguf_split_count"):
+        Gguf(str(tmp_path))
+    empty = tmp_path / "empty"
+    empty.mkdir()
+    with pytest.raises(ReaderError, match="gguf_missing_files"):
+        Gguf(str(empty))
+
+
+def test_gguf_metadata_kinds(tmp_path):
+    formats.write_gguf(tmp_path / "m.gguf",
+                       [("neg", I32, -3), ("reals", ARRAY, (F32, [0.5, -2.0])),
+                        ("big", ARRAY, (U64, [2**63])), ("s", STRING, "x")], [])
+    g = Gguf(str(tmp_path))
+    with pytest.raises(ReaderError, match="gguf_metadata_integer"):
+        g.meta("neg", 1)  # a count is never negative
+    assert g.meta("reals", 6) == [0.5, -2.0]
+    with pytest.raises(ReaderError, match="gguf_metadata_integers"):
+        g.meta("big", 5)  # beyond int64
+    with pytest.raises(ReaderError, match="gguf_metadata_numbers"):
+        g.meta("big", 6)
+    with pytest.raises(ReaderError, match="gguf_metadata_strings"):
+        g.meta("s", 4)  # a scalar is not an array
+    with pytest.raises(ReaderError, match="gguf_metadata_boolean"):
+        g.meta("s", 3)
+    g.close()

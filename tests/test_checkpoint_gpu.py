@@ -1,5 +1,5 @@
 """Checkpoint bytes through the device path: GGUF rows decoded on the device
-(GgufCheckpoint::read_rows, the literal blocks of IW/tests/gguf_checkpoint.cpp:399-460),
+(GgufFiles::decode_rows, the literal blocks of IW/tests/gguf_checkpoint.cpp:399-460),
 GGUF expert tensors as the weight source of HipDenseCompute::dense_gguf_source (decode-
 time product and prefill GEMM) against the oracle, and a GPT-OSS MXFP4 expert set loaded
 from a safetensors shard into the MoE layer against the oracle."""
@@ -63,7 +63,7 @@ def test_gguf_expert_through_dense_gguf_source(tmp_path, probe, oracle, enc, row
 
 def test_safetensors_mxfp4_experts_into_the_moe_layer(tmp_path, probe, oracle):
     """GPT-OSS expert tensors (<prefix>_blocks U8 [E, rows, groups, 16], <prefix>_scales U8
-    [E, rows, groups]) loaded by SafetensorsShard::load_mxfp4_experts into
+    [E, rows, groups]) loaded by SafetensorsFile::mxfp4_experts into
     HipDenseCompute::moe_mxfp4."""
     experts, hidden, inter, tokens, top_k = 4, 128, 192, 5, 2
     (gb, gs), (ub, us), (db, ds) = synth.moe_weights(0xF3, experts, hidden, inter)
