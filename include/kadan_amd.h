@@ -6,8 +6,10 @@
  * IW = services/hikari/inference_worker).  Every entry point takes plain device
  * pointers, sizes and a hipStream_t passed as void*; no C++ or torch type crosses
  * it.  All pointers are device pointers unless stated otherwise.  Calls enqueue on
- * `stream` and return without synchronizing; a status code other than KDQ_OK means
- * nothing was enqueued (argument errors are detected before any launch).
+ * `stream` and return without synchronizing (one exception, stated at kdq_moe_gguf: a
+ * prefill call over weights nobody has range-checked reads one flag back to the host);
+ * a status code other than KDQ_OK means nothing was enqueued (argument errors are
+ * detected before any launch).
  *
  * Encodings are named by their GGML type id, as IW/include/kadan/gguf_quantization.hpp:30-55
  * maps them (Q4_0 = 2 is added here; the reference has no kadan encoding for it).
@@ -233,8 +235,16 @@ typedef struct kdq_moe_gguf_layer {
  * its weights exactly (kdq_gemv semantics).  rows <= 4096, rows * top_k <= 8192,
  * experts <= 256, top_k <= 8; x, y, shared_gate 16-byte aligned.  Up to 8 rows run
  * every slot's expert product directly; larger batches (prefill chunks) group the
- * slots by expert into 8-row items, so an expert's weights are read once per 8 of its
- * rows (the reference's per-expert batch jobs, IW/include/kadan/dense_compute.hpp:197-201). */
+ * slots by expert, either into 8-row items of the decode product (an expert's weights
+ * read once per 8 of its rows, the reference's per-expert batch jobs,
+ * IW/include/kadan/dense_compute.hpp:197-201) or, for Q4_K / Q8_0 / Q6_K, into 64-row
+ * tiles of the prefill GEMM (fp16 operands, fp32 accumulation).
+ * Host wait: when the prefill GEMM runs here, this call packs the weights itself and
+ * cannot know in advance whether a block scale could take a dequantised weight past
+ * the fp16 range (never so in real checkpoints); it copies the GEMM's flag to the host
+ * and synchronizes `stream` once, mid-layer, and on that flag redoes the expert
+ * products on the exact decode.  Callers that must not block use kdq_moe_gguf_packed
+ * with copies checked once by kdq_gguf_gemm_check (`checked` = 1): it never waits. */
 int kdq_moe_gguf(const kdq_moe_gguf_layer* layer, const float* x, size_t rows, float* y,
                  int32_t* selected, float* weights, unsigned* status, void* stream);
 
@@ -256,11 +266,6 @@ typedef struct kdq_moe_gguf_packed_stacks {
     unsigned checked;
 } kdq_moe_gguf_packed_stacks;
 
-/* kdq_moe_gguf with resident packed copies (`packed` may be null: kdq_moe_gguf).  No
- * counterpart in the reference, whose layer reads every expert through DenseCompute
- * batch jobs (IW/include/kadan/dense_compute.hpp:197-201); the row-major tensors of
- * `layer` stay required (decode batches and the exact fallback read them) and must hold
- * the same weights as the packed copies.  Same results as kdq_moe_gguf. */
 /* The prefill GEMM's scale checks over a tile-packed matrix (n rows of k inputs), once,
  * without the product: *flags (device memory) |= 1 for a non-finite scale, |= 2 when a
  * dequantised weight could pass the fp16 range (the GEMM would then refuse the matrix
@@ -269,6 +274,12 @@ typedef struct kdq_moe_gguf_packed_stacks {
 int kdq_gguf_gemm_check(int encoding, const void* packed, size_t n, size_t k, unsigned* flags,
                         void* stream);
 
+/* kdq_moe_gguf with resident packed copies (`packed` may be null: kdq_moe_gguf).  No
+ * counterpart in the reference, whose layer reads every expert through DenseCompute
+ * batch jobs (IW/include/kadan/dense_compute.hpp:197-201); the row-major tensors of
+ * `layer` stay required (decode batches and the exact fallback read them) and must hold
+ * the same weights as the packed copies.  Same results as kdq_moe_gguf; with
+ * `packed->checked` = 1 it returns without synchronizing. */
 int kdq_moe_gguf_packed(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* packed,
                         const float* x, size_t rows, float* y, int32_t* selected, float* weights,
                         unsigned* status, void* stream);

@@ -60,6 +60,8 @@ __global__ __launch_bounds__(256) void swiglu_kernel(float* gate, const float* u
 // fixed order (thread j: its float4 columns j, j + 256, ... with the four products of each
 // fused in turn; the wavefront: an xor butterfly, which leaves the same float in every
 // lane; the four wavefronts: (0 + 1) + (2 + 3)), so all of them use the same value.
+// A non-finite value of ffn_gate_inp_shexp sets bit 1 of `status` (when given), as every
+// other weight of the layer does; workgroup (0, 0) reports it, having read every value.
 // Grid (ceil(hidden / 1024), tokens), 256 threads of 4 consecutive d each.
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ down,
                                                       const int32_t* __restrict__ pos,
@@ -67,16 +69,20 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
                                                       const float* __restrict__ shared,
                                                       const float* __restrict__ gate_vector,
                                                       const float* __restrict__ x, unsigned k,
-                                                      unsigned hidden, float* __restrict__ y) {
+                                                      unsigned hidden, float* __restrict__ y,
+                                                      unsigned* __restrict__ status) {
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     __shared__ float wave_sum[4];
+    __shared__ int wave_bad[4];
     const size_t t = blockIdx.y;
     const unsigned quads = hidden / 4;
     const f32x4* xr = reinterpret_cast<const f32x4*>(x + t * hidden);
     const f32x4* vr = reinterpret_cast<const f32x4*>(gate_vector);
     float s = 0.f;
+    bool finite = true;
     for (unsigned q = threadIdx.x; q < quads; q += 256) {
         const f32x4 a = xr[q], b = vr[q];
+        finite = finite && isfinite(b.x) && isfinite(b.y) && isfinite(b.z) && isfinite(b.w);
         s = fmaf(a.x, b.x, s);
         s = fmaf(a.y, b.y, s);
         s = fmaf(a.z, b.z, s);
@@ -84,9 +90,15 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     }
     for (int m = 32; m >= 1; m /= 2)
         s += __shfl_xor(s, m, 64);
-    if (threadIdx.x % 64 == 0)
+    const bool bad = __any(!finite);
+    if (threadIdx.x % 64 == 0) {
         wave_sum[threadIdx.x / 64] = s;
+        wave_bad[threadIdx.x / 64] = bad;
+    }
     __syncthreads();
+    if (status && threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y == 0 &&
+        (wave_bad[0] | wave_bad[1] | wave_bad[2] | wave_bad[3]))
+        atomicOr(status, 1u);
     const float gate = sigmoid_of((wave_sum[0] + wave_sum[1]) + (wave_sum[2] + wave_sum[3]));
     const unsigned q = blockIdx.x * 256 + threadIdx.x;
     if (q >= quads)
@@ -572,7 +584,7 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
         auto combine = [&]() -> int {
             hipLaunchKernelGGL(combine_kernel, dim3(unsigned((H / 4 + 255) / 256), unsigned(rows)),
                                dim3(256), 0, st, d, pos, w, ds, L.shared_gate, x, unsigned(K),
-                               unsigned(H), y);
+                               unsigned(H), y, status);
             KDQ_HIP(hipGetLastError());
             return KDQ_OK;
         };
@@ -662,7 +674,7 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
     // 6. combine
     hipLaunchKernelGGL(combine_kernel, dim3(unsigned((H / 4 + 255) / 256), unsigned(rows)),
                        dim3(256), 0, st, d, static_cast<const int32_t*>(nullptr), w, ds,
-                       L.shared_gate, x, unsigned(K), unsigned(H), y);
+                       L.shared_gate, x, unsigned(K), unsigned(H), y, status);
     KDQ_HIP(hipGetLastError());
     return KDQ_OK;
 }

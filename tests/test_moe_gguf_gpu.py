@@ -179,6 +179,27 @@ def test_moe_gguf_nonfinite_weight_status(device):
     assert int(status.item()) == 1
 
 
+@pytest.mark.parametrize("rows", [1, 64])
+def test_moe_gguf_nonfinite_shared_gate_status(device, rows):
+    """ffn_gate_inp_shexp is a weight like any other: a NaN in it sets status bit 1 (the
+    combine kernel takes its dot product; decode and grouped paths alike)."""
+    import torch
+    from kadan_amd import ops
+    H, E, K, F, S = 256, 8, 2, 256, 256
+    spec = make_layer(6, H, E, K, F, S, MIXED)
+    spec["shared_gate"] = spec["shared_gate"].copy()
+    spec["shared_gate"][200] = np.nan
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    ops.moe_gguf(to_device(torch, device, spec), torch.ones(rows, H, device=device),
+                 status=status)
+    assert int(status.item()) == 1
+    spec["shared_gate"][200] = 0.5  # finite again: nothing flagged
+    status.zero_()
+    ops.moe_gguf(to_device(torch, device, spec), torch.ones(rows, H, device=device),
+                 status=status)
+    assert int(status.item()) == 0
+
+
 def test_moe_gguf_rejections(device):
     import torch
     from kadan_amd import KdqError, ops
