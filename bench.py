@@ -235,8 +235,10 @@ def timed_median(fn, seconds: float, least: int = 3):
 
 def cpu_baselines(seconds: float = 2.0):
     """The reference CPU path (oracle/_ref where built, else the oracle restatement) for
-    C1, C2, C3 and C4 at each thread count of cpu_thread_counts(), bounded samples of
-    about `seconds` each; C3 and C4 T=256 time a stated subset of rows or tokens."""
+    C1, C2, C3, C4 and C5 at each thread count of cpu_thread_counts(), bounded samples of
+    about `seconds` each; C3 and the MoE legs time a stated subset of rows or tokens.  The
+    MoE layer runs twice: the exact flow (double accumulation, the reference's
+    quantization::matvec semantics) and an AVX2 fp32 form (`*_f32`)."""
     from kadan_amd import synth
     import oracle
     cores, counts = cpu_thread_counts()
@@ -303,6 +305,19 @@ def cpu_baselines(seconds: float = 2.0):
             out[name] = {"kind": "port", "unit": "tokens/s", "by_threads": legs,
                          "sample": f"tokens {sample}" + (" (0 hot)" if hot else "")
                                    + ", exact double-accumulated products"}
+            # the fast CPU form: fp32 products on AVX2 FMA, 64-row units over the threads
+            fsample = list(range(min(tokens, 32 if experts == 32 else 64)))
+            xf, lf = synth.moe_inputs(seed, tokens, 2880, experts, hot=hot)
+            xf, lf = xf[fsample], lf[fsample]
+            legs = {}
+            for th in counts:
+                med, n = timed_median(lambda: port.moe_forward_f32(xf, lf, 4, gb, gs, ub, us, db,
+                                                                   ds, threads=th),
+                                      seconds, least=1)
+                legs[str(th)] = {"tokens_per_s": round(len(fsample) / med, 2),
+                                 "ms": round(med * 1e3, 2), "runs": n}
+            out[name + "_f32"] = {"kind": "port", "unit": "tokens/s", "by_threads": legs,
+                                  "sample": f"tokens 0..{len(fsample) - 1}, AVX2 fp32 products"}
         del gb, gs, ub, us, db, ds
     return out
 

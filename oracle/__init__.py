@@ -76,6 +76,8 @@ class Oracle:
         lib.kdo_moe_permute.argtypes = [vp, sz, sz, sz, vp, vp]
         lib.kdo_moe_forward.argtypes = [vp, vp, sz, sz, sz, sz, sz, vp, vp, vp, vp, vp, vp,
                                         vp, vp, vp, vp, vp, i]
+        lib.kdo_moe_forward_f32.argtypes = [vp, vp, sz, sz, sz, sz, sz, vp, vp, vp, vp, vp,
+                                            vp, vp, i]
 
     # -- scalars
     def half_to_float(self, bits: int) -> float:
@@ -248,6 +250,24 @@ class Oracle:
         if rc:
             raise ValueError(f"kdo_moe_forward rc={rc}")
         return y, idx, w, offsets, perm
+
+
+    def moe_forward_f32(self, x_bf16, logits, top_k, gate_b, gate_s, up_b, up_s, down_b,
+                        down_s, threads=1):
+        """kdo_moe_forward_f32: the layer with AVX2 fp32 products (a timed CPU baseline,
+        not a checker): y [tokens, hidden]."""
+        x_bf16 = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+        logits = np.ascontiguousarray(logits, dtype=np.float32)
+        t, h = x_bf16.shape
+        arrays = [np.ascontiguousarray(a, dtype=np.uint8)
+                  for a in (gate_b, gate_s, up_b, up_s, down_b, down_s)]
+        y = np.empty((t, h), np.float32)
+        rc = self.lib.kdo_moe_forward_f32(_p(x_bf16), _p(logits), t, h, gate_s.shape[1],
+                                          logits.shape[1], top_k, *[_p(a) for a in arrays],
+                                          _p(y), threads)
+        if rc:
+            raise ValueError(f"kdo_moe_forward_f32 rc={rc}")
+        return y
 
 
 class GgufTensor(C.Structure):

@@ -6,6 +6,7 @@
 #include "oracle.h"
 
 #include <math.h>
+#include <immintrin.h>
 #include <pthread.h>
 #include <stdatomic.h>
 #include <stdlib.h>
@@ -914,6 +915,182 @@ int kdo_moe_forward(const uint16_t* x, const float* logits, size_t tokens, size_
                     sum += contribution[(t * top_k + i) * hidden + d];
                 y[t * hidden + d] = sum;
             }
+    free(contribution);
+    return rc;
+}
+
+/* ------------------------------------------- MoE, fp32 products (CPU baseline) */
+
+/* The same layer with every product accumulated in fp32 and vectorised with AVX2 FMA
+ * (eight lanes, four accumulators, summed pairwise at the end): the fast CPU form that
+ * sits beside the exact double-accumulation flow as a baseline.  It is timed only, not a
+ * checker.  Work is split as the reference worker splits a projection, into units of 64
+ * output rows (IW/src/models/text/gguf_weights.cpp:400-446) taken from a shared counter:
+ * phase 1 the (expert, 64 gate/up rows) units, phase 2 the (expert, 64 down rows) units. */
+
+typedef struct {
+    const uint16_t* x;
+    size_t hidden, inter, experts, top_k;
+    const uint8_t *gate_blocks, *gate_scales, *up_blocks, *up_scales, *down_blocks, *down_scales;
+    const int32_t *offsets, *perm;
+    const float* w;
+    float *xs, *g, *u, *contribution; /* xs, g, u: rows in permuted (expert-major) order */
+    size_t units, phase;
+    atomic_size_t next;
+    atomic_int error;
+} moe32_work;
+
+/* One decoded MXFP4 row in fp32 (exact: an E2M1 value times a power of two). */
+static int mxfp4_row_f32(const uint8_t* blocks, const uint8_t* scales, size_t cols, float* out) {
+    static const float value[16] = {0.0f, 0.5f,  1.0f,  1.5f,  2.0f,  3.0f,  4.0f,  6.0f,
+                                    -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
+    for (size_t b = 0; b < cols / 32; ++b) {
+        if (scales[b] == 255)
+            return -2;
+        const float scale = ldexpf(1.0f, (int)scales[b] - 127);
+        for (size_t i = 0; i < 16; ++i) {
+            const uint8_t byte = blocks[16 * b + i];
+            out[32 * b + 2 * i] = value[byte & 15u] * scale;
+            out[32 * b + 2 * i + 1] = value[byte >> 4] * scale;
+        }
+    }
+    for (size_t c = 0; c < cols; ++c)
+        if (!isfinite(out[c]))
+            return -3;
+    return 0;
+}
+
+__attribute__((target("avx2,fma"))) static float dot_avx2(const float* a, const float* b,
+                                                          size_t n) {
+    __m256 s0 = _mm256_setzero_ps(), s1 = s0, s2 = s0, s3 = s0;
+    size_t i = 0;
+    for (; i + 32 <= n; i += 32) {
+        s0 = _mm256_fmadd_ps(_mm256_loadu_ps(a + i), _mm256_loadu_ps(b + i), s0);
+        s1 = _mm256_fmadd_ps(_mm256_loadu_ps(a + i + 8), _mm256_loadu_ps(b + i + 8), s1);
+        s2 = _mm256_fmadd_ps(_mm256_loadu_ps(a + i + 16), _mm256_loadu_ps(b + i + 16), s2);
+        s3 = _mm256_fmadd_ps(_mm256_loadu_ps(a + i + 24), _mm256_loadu_ps(b + i + 24), s3);
+    }
+    for (; i + 8 <= n; i += 8)
+        s0 = _mm256_fmadd_ps(_mm256_loadu_ps(a + i), _mm256_loadu_ps(b + i), s0);
+    const __m256 s = _mm256_add_ps(_mm256_add_ps(s0, s1), _mm256_add_ps(s2, s3));
+    float lanes[8];
+    _mm256_storeu_ps(lanes, s);
+    float total = ((lanes[0] + lanes[1]) + (lanes[2] + lanes[3])) +
+                  ((lanes[4] + lanes[5]) + (lanes[6] + lanes[7]));
+    for (; i < n; ++i)
+        total += a[i] * b[i];
+    return total;
+}
+
+static float dot_f32(const float* a, const float* b, size_t n) {
+    if (__builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma"))
+        return dot_avx2(a, b, n);
+    float s = 0.0f;
+    for (size_t i = 0; i < n; ++i)
+        s += a[i] * b[i];
+    return s;
+}
+
+static void* moe32_worker(void* arg) {
+    moe32_work* m = (moe32_work*)arg;
+    const size_t H = m->hidden, I = m->inter;
+    const size_t in = m->phase == 1 ? H : I, out = m->phase == 1 ? I : H;
+    const size_t blocks_per_expert = (out + 63) / 64;
+    float* wrow = (float*)malloc(in * sizeof(float));
+    for (;;) {
+        const size_t unit = atomic_fetch_add(&m->next, 1);
+        if (unit >= m->units || atomic_load(&m->error))
+            break;
+        const size_t e = unit / blocks_per_expert, r0 = unit % blocks_per_expert * 64;
+        const size_t first = (size_t)m->offsets[e], count = (size_t)m->offsets[e + 1] - first;
+        const size_t r1 = r0 + 64 < out ? r0 + 64 : out;
+        int rc = 0;
+        for (size_t n = r0; n < r1 && count && !rc; ++n) {
+            if (m->phase == 1) {
+                for (int which = 0; which < 2 && !rc; ++which) {
+                    const uint8_t* b = (which ? m->up_blocks : m->gate_blocks) + (e * I + n) * (H / 2);
+                    const uint8_t* sc = (which ? m->up_scales : m->gate_scales) + (e * I + n) * (H / 32);
+                    float* o = which ? m->u : m->g;
+                    rc = mxfp4_row_f32(b, sc, H, wrow);
+                    for (size_t r = 0; r < count && !rc; ++r)
+                        o[(first + r) * I + n] = dot_f32(wrow, m->xs + (first + r) * H, H);
+                }
+            } else {
+                rc = mxfp4_row_f32(m->down_blocks + (e * H + n) * (I / 2),
+                                   m->down_scales + (e * H + n) * (I / 32), I, wrow);
+                for (size_t r = 0; r < count && !rc; ++r) {
+                    const size_t slot = (size_t)m->perm[first + r];
+                    m->contribution[slot * H + n] =
+                        dot_f32(wrow, m->g + (first + r) * I, I) * m->w[slot];
+                }
+            }
+        }
+        if (rc)
+            atomic_store(&m->error, rc);
+    }
+    free(wrow);
+    return NULL;
+}
+
+static int moe32_phase(moe32_work* m, size_t phase, int threads) {
+    const size_t out = phase == 1 ? m->inter : m->hidden;
+    m->phase = phase;
+    m->units = m->experts * ((out + 63) / 64);
+    atomic_store(&m->next, 0);
+    pthread_t* pool = (pthread_t*)malloc(sizeof(pthread_t) * (size_t)threads);
+    int started = 0;
+    for (int t = 1; t < threads && pool; ++t)
+        if (pthread_create(&pool[started], NULL, moe32_worker, m) == 0)
+            ++started;
+    moe32_worker(m);
+    for (int t = 0; t < started; ++t)
+        pthread_join(pool[t], NULL);
+    free(pool);
+    return atomic_load(&m->error);
+}
+
+int kdo_moe_forward_f32(const uint16_t* x, const float* logits, size_t tokens, size_t hidden,
+                        size_t inter, size_t experts, size_t top_k,
+                        const uint8_t* gate_blocks, const uint8_t* gate_scales,
+                        const uint8_t* up_blocks, const uint8_t* up_scales,
+                        const uint8_t* down_blocks, const uint8_t* down_scales, float* y,
+                        int threads) {
+    if (!hidden || !inter || hidden % 32 || inter % 32 || !top_k || top_k > experts ||
+        threads < 1)
+        return -1;
+    const size_t slots = tokens * top_k;
+    int32_t* idx = (int32_t*)malloc(slots * sizeof(int32_t));
+    float* w = (float*)malloc(slots * sizeof(float));
+    int32_t* offsets = (int32_t*)malloc((experts + 1) * sizeof(int32_t));
+    int32_t* perm = (int32_t*)malloc((slots + 1) * sizeof(int32_t));
+    float* xs = (float*)malloc((slots * hidden + 1) * sizeof(float));
+    float* g = (float*)malloc((slots * inter + 1) * sizeof(float));
+    float* u = (float*)malloc((slots * inter + 1) * sizeof(float));
+    float* contribution = (float*)calloc(slots * hidden + 1, sizeof(float));
+    int rc = (idx && w && offsets && perm && xs && g && u && contribution) ? 0 : -5;
+    if (!rc) {
+        kdo_moe_route(logits, tokens, experts, top_k, idx, w);
+        kdo_moe_permute(idx, tokens, top_k, experts, offsets, perm);
+        for (size_t p = 0; p < slots; ++p)
+            for (size_t c = 0; c < hidden; ++c)
+                xs[p * hidden + c] = kdo_bf16_to_float(x[(size_t)perm[p] / top_k * hidden + c]);
+        moe32_work work = {x, hidden, inter, experts, top_k, gate_blocks, gate_scales,
+                           up_blocks, up_scales, down_blocks, down_scales, offsets, perm, w,
+                           xs, g, u, contribution, 0, 0, 0, 0};
+        rc = moe32_phase(&work, 1, threads);
+        for (size_t i = 0; !rc && i < slots * inter; ++i)
+            g[i] = silu(g[i]) * u[i];
+        if (!rc)
+            rc = moe32_phase(&work, 2, threads);
+        for (size_t t = 0; !rc && t < tokens; ++t)
+            for (size_t d = 0; d < hidden; ++d) {
+                float sum = 0.0f;
+                for (size_t i = 0; i < top_k; ++i)
+                    sum += contribution[(t * top_k + i) * hidden + d];
+                y[t * hidden + d] = sum;
+            }
+    }
+    free(idx), free(w), free(offsets), free(perm), free(xs), free(g), free(u);
     free(contribution);
     return rc;
 }

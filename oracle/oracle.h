@@ -24,10 +24,14 @@
  *   kdo_gemv / kdo_gemm_q4_0_q8  brute-force double products over decoded weights,
  *                          linearity and permutation properties
  *   kdo_moe_route/permute  hand-derived cases (2 tokens x 4 experts) and invariants
- *   kdo_moe_gguf_forward   parity unpinned against the reference as a whole (the
- *                          compiled reference's MoeLayer needs the model runtime); its
- *                          parts are pinned individually (decode, products, routing) and
- *                          the composition by hand-computed small cases
+ *   kdo_moe_gguf_forward   the compiled reference's MoeLayer needs the model runtime,
+ *                          so the whole is pinned by a closed-form known answer with the
+ *                          sigmoid-gated shared expert (tests/util.py
+ *                          known_answer_moe_gguf, float64, no oracle code) and a float64
+ *                          numpy composition; its parts individually (decode, products,
+ *                          routing)
+ *   kdo_moe_forward_f32    not a checker: the timed AVX2 fp32 CPU baseline, checked
+ *                          against kdo_moe_forward to fp32 rounding
  *   kdo_moe_forward        parity unpinned against the reference as a whole: the
  *                          reference never runs MXFP4 weights through MoeLayer
  *                          (IW/src/models/text/qwen_layers.cpp:378-492); its parts
@@ -175,6 +179,17 @@ int kdo_moe_forward(const uint16_t* x, const float* logits, size_t tokens, size_
                     const uint8_t* down_blocks, const uint8_t* down_scales,
                     float* y, int32_t* idx, float* w, int32_t* offsets, int32_t* perm,
                     int threads);
+
+/* The layer with fp32 products vectorised with AVX2 FMA (scalar where the CPU lacks it),
+ * parallel over 64-row units: a timed CPU baseline beside kdo_moe_forward's exact double
+ * flow, not a checker.  Same routing and combine; y within fp32 rounding of
+ * kdo_moe_forward's. */
+int kdo_moe_forward_f32(const uint16_t* x, const float* logits, size_t tokens, size_t hidden,
+                        size_t inter, size_t experts, size_t top_k,
+                        const uint8_t* gate_blocks, const uint8_t* gate_scales,
+                        const uint8_t* up_blocks, const uint8_t* up_scales,
+                        const uint8_t* down_blocks, const uint8_t* down_scales, float* y,
+                        int threads);
 
 /* One GGUF weight tensor (host memory): row-major rows of `row_bytes`; expert stacks
  * hold slices of `expert_bytes`. */

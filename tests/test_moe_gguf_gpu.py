@@ -179,6 +179,22 @@ def test_moe_gguf_nonfinite_weight_status(device):
     assert int(status.item()) == 1
 
 
+@pytest.mark.parametrize("copies", [1, 32])
+def test_moe_gguf_known_answer(device, copies):
+    """The closed-form layer with a shared expert (tests/util.py known_answer_moe_gguf):
+    2 tokens (the per-slot decode path) and the same 2 tokens 32 times over (64 rows: the
+    grouped prefill GEMM for the Q8_0 experts)."""
+    import torch
+    from kadan_amd import ops
+    from tests.util import known_answer_moe_gguf
+    spec, x, want, idx = known_answer_moe_gguf()
+    x = np.tile(x, (copies, 1))
+    want = np.tile(want, (copies, 1))
+    y, sel, _ = ops.moe_gguf(to_device(torch, device, spec), torch.from_numpy(x).to(device))
+    assert np.array_equal(sel.cpu().numpy(), np.tile(idx, (copies, 1)))
+    assert_close(y.cpu().numpy(), want, what=f"moe_gguf known answer rows={2 * copies}")
+
+
 @pytest.mark.parametrize("rows", [1, 64])
 def test_moe_gguf_nonfinite_shared_gate_status(device, rows):
     """ffn_gate_inp_shexp is a weight like any other: a NaN in it sets status bit 1 (the

@@ -679,3 +679,35 @@ def test_moe_gguf_forward_vs_numpy(oracle):
     Y, sel, pw = _moe_numpy(dict(decoded, shared_gate=sg, top_k=K), x)
     assert np.array_equal(idx, sel)
     assert np.abs(y - Y).max() <= 1e-5 * np.abs(Y).max()
+
+
+def test_moe_gguf_forward_known_answer(oracle):
+    """The oracle's GGUF MoE composition against the closed form of MoeLayer::forward with
+    its sigmoid-gated shared expert (tests/util.py known_answer_moe_gguf), which no oracle
+    code computes; the shared term is a large part of y, so dropping it, or its gate,
+    would fail."""
+    from tests.util import known_answer_moe_gguf
+    spec, x, want, idx = known_answer_moe_gguf()
+    y, got_idx, w = oracle.moe_gguf_forward(spec, x)
+    assert np.array_equal(got_idx, idx)
+    assert np.abs(y - want).max() <= 1e-6 * np.abs(want).max()
+    # the closed form's parts are each large against that tolerance: the shared term
+    silu = lambda a: a / (1 + np.exp(-a))
+    for t, v in enumerate((1.0 / 16, -1.0 / 32)):
+        shared = 8 * (1 + np.arange(64) % 5) * silu(32 * v) * 64 * v / (1 + np.exp(-8 * v))
+        assert np.abs(shared).max() > 0.05 * np.abs(want[t]).max()
+        # a sigmoid swapped for silu (or no gate at all) moves y far past the tolerance
+        assert np.abs(shared * (1 - 1 / (1 + np.exp(-8 * v)))).max() > 1e-3 * np.abs(want[t]).max()
+
+
+def test_moe_forward_f32_baseline_agrees(oracle):
+    """The AVX2 fp32 MoE baseline (timed by bench.py beside the exact flow) computes the
+    same layer: within fp32 rounding of the exact double-accumulation flow, any thread
+    count."""
+    from kadan_amd import synth
+    x, logits = synth.moe_inputs(0x51, 7, 128, 8)
+    (gb, gs), (ub, us), (db, ds) = synth.moe_weights(0x51, 8, 128, 192)
+    want = oracle.moe_forward(x, logits, 2, gb, gs, ub, us, db, ds)[0]
+    for threads in (1, 3):
+        got = oracle.moe_forward_f32(x, logits, 2, gb, gs, ub, us, db, ds, threads=threads)
+        assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()

@@ -88,3 +88,74 @@ def known_answer_moe():
                 down = 64 * 2.0 ** -(1 + e // 2) * e2m1[1 + d % 7] * h
                 y[t, d] += chosen[i] / sum(chosen) * down
     return x_bits, logits, ((gate_b, gate_s), (up_b, up_s), (down_b, down_s)), y, idx
+
+
+def _q8_0_rows(rows, cols, d_of_row, q_of):
+    """Q8_0 rows [rows, cols]: per row fp16 d = d_of_row(r) (a power of two) and codes
+    q_of(r, c) (int8), blocks of 32 as [d:fp16][qs:int8 x 32]."""
+    out = np.zeros((rows, cols // 32 * 34), np.uint8)
+    for r in range(rows):
+        d = np.float16(d_of_row(r)).view(np.uint16)
+        for b in range(cols // 32):
+            out[r, 34 * b] = d & 255
+            out[r, 34 * b + 1] = d >> 8
+            out[r, 34 * b + 2:34 * b + 34] = [np.int8(q_of(r, 32 * b + i)).view(np.uint8)
+                                              for i in range(32)]
+    return out
+
+
+def known_answer_moe_gguf():
+    """A GGUF MoE layer with a shared expert (2 tokens, hidden 64, 4 experts, top-2,
+    expert ff 32, shared ff 32; every matrix Q8_0, the router F32) whose output follows
+    in closed form from MoeLayer::forward's definition (IW/src/models/text/
+    qwen_layers.cpp:378-492), computed here in float64 without any of the oracle's code:
+
+      x_t = v_t * ones, v = 1/16, -1/32;  router[e, :] = rho_e = 1/2, 1/4, 0, -1/4,
+      so logits = 64 v rho: token 0 [2, 1, 0, -1] picks experts 0, 1; token 1
+      [-1, -1/2, 0, 1/2] picks 3, 2;
+      gate_e = 2^-e,  up_e = 2^(e % 2)  (every weight):  g = 64 v 2^-e,  u = 64 v 2^(e % 2);
+      down_e[d, :] = 2^-(1 + e // 2) (1 + d % 7):  down_e(h)[d] = 32 2^-(1 + e // 2) (1 + d % 7) h;
+      shared: gate 1/2, up 1,  down[d, :] = (1 + d % 5) / 4,  gate vector 1/8, so
+      s_t = 8 v and the shared term is sigmoid(8 v) * 8 (1 + d % 5) silu(32 v) 64 v;
+      y_t[d] = sum_i w_i down_{e_i}(h_i)[d] + that shared term, w = p_i / (p_0 + p_1).
+
+    A dropped shared expert or gate, sigmoid swapped for silu, gate/up swapped, a
+    transposed down or a misplaced routing weight each change y.  Returns (spec in the
+    layout kdq_moe_gguf takes, x [2, 64] float32, y [2, 64] float64, idx [2, 2])."""
+    H, E, K, F, S = 64, 4, 2, 32, 32
+    Q8 = 8
+    v = [1.0 / 16, -1.0 / 32]
+    rho = [0.5, 0.25, 0.0, -0.25]
+    x = np.array([[v[0]] * H, [v[1]] * H], np.float32)
+    router = np.array([[r] * H for r in rho], np.float32)
+    gate = np.stack([_q8_0_rows(F, H, lambda r, e=e: 2.0 ** -e, lambda r, c: 1)
+                     for e in range(E)])
+    up = np.stack([_q8_0_rows(F, H, lambda r, e=e: 2.0 ** (e % 2), lambda r, c: 1)
+                   for e in range(E)])
+    down = np.stack([_q8_0_rows(H, F, lambda r, e=e: 2.0 ** -(1 + e // 2),
+                                lambda r, c: 1 + r % 7) for e in range(E)])
+    spec = dict(hidden=H, experts=E, top_k=K, ff=F, shared_ff=S,
+                shared_gate=np.full(H, 0.125, np.float32),
+                router=(0, router.view(np.uint8).reshape(E, -1)),
+                gate_exps=(Q8, gate), up_exps=(Q8, up), down_exps=(Q8, down),
+                gate_shexp=(Q8, _q8_0_rows(S, H, lambda r: 0.5, lambda r, c: 1)),
+                up_shexp=(Q8, _q8_0_rows(S, H, lambda r: 1.0, lambda r, c: 1)),
+                down_shexp=(Q8, _q8_0_rows(H, S, lambda r: 0.25, lambda r, c: 1 + r % 5)))
+    idx = np.array([[0, 1], [3, 2]], np.int32)
+    silu = lambda a: a / (1 + math.exp(-a))
+    y = np.zeros((2, H), np.float64)
+    for t in range(2):
+        logits = [64 * v[t] * r for r in rho]
+        top = max(logits)
+        p = [math.exp(l - top) for l in logits]
+        p = [q / sum(p) for q in p]
+        chosen = [p[e] for e in idx[t]]
+        for i, e in enumerate(idx[t]):
+            h = silu(64 * v[t] * 2.0 ** -e) * 64 * v[t] * 2.0 ** (e % 2)
+            for d in range(H):
+                y[t, d] += chosen[i] / sum(chosen) * 32 * 2.0 ** -(1 + e // 2) * (1 + d % 7) * h
+        hs = silu(32 * v[t]) * 64 * v[t]
+        gate_t = 1 / (1 + math.exp(-8 * v[t]))
+        for d in range(H):
+            y[t, d] += gate_t * 32 * 0.25 * (1 + d % 5) * hs
+    return spec, x, y, idx
