@@ -195,6 +195,22 @@ int kdq_gemm_q4_0_packed(const void* packed, size_t n, size_t k, const uint16_t*
 int kdq_gemm_packed(int encoding, const void* packed, size_t n, size_t k, const float* x,
                     size_t m, float* y, unsigned* status, void* stream);
 
+/* ---- prefill GEMM over row-major GGUF rows, any encoding (replaces the same decode-to-
+ * F32 tile + cublasSgemm, IW/src/cuda/h3_compute.cu:2201-2218,2451, for the encodings the
+ * packed GEMM does not take: Q3_K, IQ4_XS, IQ4_NL, IQ3_XXS, IQ3_S, IQ2_S, BF16, Q4_0; it
+ * also runs Q4_K, Q8_0 and Q6_K rows as they lie in the file).
+ * y[m x n] fp32 = x[m x k] fp32 . W^T, W = `n` rows of `row_bytes` (>= kdq_row_bytes, even)
+ * as the file holds them, 2-byte aligned.  Every weight is decoded exactly as
+ * kdq_dequantize does, then rounded once to fp16; activations are scaled per row by a
+ * power of two and rounded once to fp16; products accumulate in fp32.  Each workgroup
+ * reads the bytes of its 128 weight rows once for 128 activation rows.
+ * k % kdq_gemm_rows_values(encoding) == 0 (256; BF16 64), k <= 65536; x and y 16-byte
+ * aligned.  `status` (optional, zeroed by the caller): |= 1 for a non-finite decoded
+ * weight, |= 2 for one past the fp16 range (then run kdq_gemv for these rows). */
+size_t kdq_gemm_rows_values(int encoding);
+int kdq_gemm_rows(int encoding, const void* weights, size_t row_bytes, size_t n, size_t k,
+                  const float* x, size_t m, float* y, unsigned* status, void* stream);
+
 /* The activation quantizer of kdq_gemm_q4_0 on its own (for bit-exact checks):
  * q int8 [m x k], d fp32 [m x k/32]. */
 int kdq_quantize_q8(const uint16_t* x_f16, size_t m, size_t k, int8_t* q, float* d,

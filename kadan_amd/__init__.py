@@ -73,6 +73,7 @@ _SIGNATURES = {
     "kdq_gemm_q4_0": [_VP, _SZ, _SZ, _VP, _SZ, _VP, _VP],
     "kdq_gemm_q4_0_packed": [_VP, _SZ, _SZ, _VP, _SZ, _VP, _VP],
     "kdq_gemm_packed": [_I, _VP, _SZ, _SZ, _VP, _SZ, _VP, _VP, _VP],
+    "kdq_gemm_rows": [_I, _VP, _SZ, _SZ, _SZ, _VP, _SZ, _VP, _VP, _VP],
     "kdq_moe_gguf": [_VP, _VP, _SZ, _VP, _VP, _VP, _VP, _VP],
     "kdq_moe_gguf_packed": [_VP, _VP, _VP, _SZ, _VP, _VP, _VP, _VP, _VP],
     "kdq_gguf_gemm_check": [_I, _VP, _SZ, _SZ, _VP, _VP],
@@ -96,6 +97,7 @@ _OTHER = {
     "kdq_block_bytes": (_SZ, [_I]),
     "kdq_row_bytes": (_SZ, [_I, _SZ]),
     "kdq_gguf_packed_bytes": (_SZ, [_I, _SZ, _SZ]),
+    "kdq_gemm_rows_values": (_SZ, [_I]),
     "kdq_gemv_packed_supported": (_I, [_I, _SZ]),
     "kdq_moe_mxfp4_packed_bytes": (_SZ, [_SZ, _SZ, _SZ]),
 }

@@ -17,8 +17,8 @@ INCLUDE = os.path.join(ROOT, "include")
 BUILD = os.path.join(ROOT, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-DEVICE_SOURCES = ["capi.hip", "gguf_gemv.hip", "gguf_gemm.hip", "q4_0_gemm.hip", "moe_mxfp4.hip",
-                  "moe_gguf.hip", "hbm_read.hip"]
+DEVICE_SOURCES = ["capi.hip", "gguf_gemv.hip", "gguf_gemm.hip", "gguf_gemm_rows.hip",
+                  "q4_0_gemm.hip", "moe_mxfp4.hip", "moe_gguf.hip", "hbm_read.hip"]
 HOST_SOURCES = ["hip_dense_compute.cpp", "checkpoint.cpp"]
 LIBRARY = os.path.join(PACKAGE, "libkadan_amd.so")
 HOST_LIBRARY = os.path.join(PACKAGE, "libkadan_amd_host.so")

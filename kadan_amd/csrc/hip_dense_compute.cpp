@@ -477,7 +477,10 @@ void HipDenseCompute::stream_product(gguf::Encoding enc, std::size_t in, std::si
             }
             if (gemm) {  // columns [first, first + n) of y through a [rows x n] tile
                 auto* tile = static_cast<float*>(device_buffer(10 + b, rows * n * 4));
-                kdq_check(kdq_gemm_packed(ggml_type(enc), w, n, in, dx, rows, tile, dstatus, st));
+                kdq_check(packed ? kdq_gemm_packed(ggml_type(enc), w, n, in, dx, rows, tile,
+                                                   dstatus, st)
+                                 : kdq_gemm_rows(ggml_type(enc), w, row_bytes, n, in, dx, rows,
+                                                 tile, dstatus, st));
                 hip_check(hipMemcpy2DAsync(dy + first, out * 4, tile, n * 4, n * 4, rows,
                                            hipMemcpyDeviceToDevice, st));
             } else {
@@ -497,12 +500,21 @@ void HipDenseCompute::stream_product(gguf::Encoding enc, std::size_t in, std::si
 }
 
 // The prefill GEMM (kdq_gemm_packed) takes packed Q4_K / Q8_0 / Q6_K rows of up to 32K
-// values; the decode-time product takes everything else (and batches of at most
-// gguf_batch_rows rows, where one weight pass serves every row anyway).
+// values; the decode-time product takes batches of at most gguf_batch_rows rows (one
+// weight pass serves every row anyway).
 bool gemm_takes(gguf::Encoding enc, std::size_t in, std::size_t rows, bool packed) {
     return packed && rows > HipDenseCompute::gguf_batch_rows && in % 256 == 0 && in <= 32768 &&
            (enc == gguf::Encoding::q4_k || enc == gguf::Encoding::q8_0 ||
             enc == gguf::Encoding::q6_k);
+}
+
+// The prefill GEMM over row-major rows (kdq_gemm_rows) takes every other encoding kept
+// row-major, so a prefill chunk reads its weights once instead of once per
+// gguf_batch_rows rows.
+bool rows_gemm_takes(gguf::Encoding enc, std::size_t in, std::size_t rows, bool packed) {
+    const std::size_t values = kdq_gemm_rows_values(ggml_type(enc));
+    return !packed && rows > HipDenseCompute::gguf_batch_rows && values && in % values == 0 &&
+           in <= 65536;
 }
 
 ProjectionResult HipDenseCompute::dense_gguf_source(
@@ -590,9 +602,12 @@ ProjectionResult HipDenseCompute::dense_gguf_source(
     // Prefill (the reference's decode-tile + SGEMM path, h3_compute.cu:2201-2218,2451): one
     // GEMM reads each weight byte once for all rows; its status bit 2 (a dequantised weight
     // past the fp16 range) sends the rows through the decode-time product instead.
-    const bool gemm = gemm_takes(enc, in, rows, packed);
-    if (gemm && w)
+    const bool gemm = gemm_takes(enc, in, rows, packed) || rows_gemm_takes(enc, in, rows, packed);
+    if (gemm && w && packed)
         kdq_check(kdq_gemm_packed(ggml_type(enc), w->device, out, in, dx, rows, dy, dstatus, st));
+    else if (gemm && w)
+        kdq_check(kdq_gemm_rows(ggml_type(enc), w->device, w->row_bytes, out, in, dx, rows, dy,
+                                dstatus, st));
     else if (gemm)
         stream_product(enc, in, out, rows, source, dx, dy, dstatus, cancel, true);
     else
@@ -834,15 +849,27 @@ ProjectionResult HipDenseCompute::dense_gguf_batch(std::span<const GgufBatchJob>
     // Jobs of more than gguf_batch_rows rows over packed Q4_K / Q8_0 / Q6_K (routed experts
     // at prefill) run the GEMM, one launch each; the rest go in one submission per layout
     // (jobs keep their order within each; every job writes its own output region).
-    std::vector<kdq_matvec_job> packed_jobs, row_jobs, gemm_jobs;
+    // (GEMM jobs over row-major rows, the other encodings, run kdq_gemm_rows)
+    std::vector<kdq_matvec_job> packed_jobs, row_jobs, gemm_jobs, rows_gemm_jobs;
     for (std::size_t i = 0; i < jobs.size(); ++i) {
-        const bool gemm = jobs[i].encoding && gemm_takes(*jobs[i].encoding, jobs[i].in,
-                                                         table[i].rows, weights[i]->packed);
-        (gemm ? gemm_jobs : weights[i]->packed ? packed_jobs : row_jobs).push_back(table[i]);
+        const bool packed = weights[i]->packed;
+        const bool gemm = jobs[i].encoding &&
+                          gemm_takes(*jobs[i].encoding, jobs[i].in, table[i].rows, packed);
+        const bool rows_gemm =
+            jobs[i].encoding && rows_gemm_takes(*jobs[i].encoding, jobs[i].in, table[i].rows,
+                                                packed);
+        (gemm        ? gemm_jobs
+         : rows_gemm ? rows_gemm_jobs
+         : packed    ? packed_jobs
+                     : row_jobs)
+            .push_back(table[i]);
     }
     for (const auto& j : gemm_jobs)
         kdq_check(kdq_gemm_packed(j.encoding, j.weights, j.columns, j.in, j.input, j.rows,
                                   j.output, dstatus, st));
+    for (const auto& j : rows_gemm_jobs)
+        kdq_check(kdq_gemm_rows(j.encoding, j.weights, j.row_bytes, j.columns, j.in, j.input,
+                                j.rows, j.output, dstatus, st));
     if (!packed_jobs.empty())
         kdq_check(kdq_gemv_packed_batch(packed_jobs.data(), packed_jobs.size(), st));
     if (!row_jobs.empty())
@@ -850,10 +877,13 @@ ProjectionResult HipDenseCompute::dense_gguf_batch(std::span<const GgufBatchJob>
     unsigned status = 0;
     hip_check(hipMemcpyAsync(&status, dstatus, sizeof status, hipMemcpyDeviceToHost, st));
     synchronize();
-    if (!gemm_jobs.empty() && (status & 2u) && !(status & 1u)) {
+    if ((!gemm_jobs.empty() || !rows_gemm_jobs.empty()) && (status & 2u) && !(status & 1u)) {
         // a dequantised weight past the fp16 range: the GEMM jobs again, decode-time
         hip_check(hipMemsetAsync(dstatus, 0, sizeof(unsigned), st));
-        kdq_check(kdq_gemv_packed_batch(gemm_jobs.data(), gemm_jobs.size(), st));
+        if (!gemm_jobs.empty())
+            kdq_check(kdq_gemv_packed_batch(gemm_jobs.data(), gemm_jobs.size(), st));
+        if (!rows_gemm_jobs.empty())
+            kdq_check(kdq_gemv_batch(rows_gemm_jobs.data(), rows_gemm_jobs.size(), st));
         hip_check(hipMemcpyAsync(&status, dstatus, sizeof status, hipMemcpyDeviceToHost, st));
     }
     for (std::size_t i = 0; i < jobs.size(); ++i)

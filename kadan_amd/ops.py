@@ -179,6 +179,23 @@ def gemm_packed(encoding: int, packed: torch.Tensor, x: torch.Tensor, n_out: int
     return out
 
 
+def gemm_rows(encoding: int, w: torch.Tensor, x: torch.Tensor, n_out: int,
+              out: torch.Tensor | None = None,
+              status: torch.Tensor | None = None) -> torch.Tensor:
+    """Row-major GGUF rows [n_out, row_bytes] (uint8, as the file holds them) x fp32
+    [m, k] -> fp32 [m, n_out] (kdq_gemm_rows, the prefill product of every encoding)."""
+    _need(w, torch.uint8, "w")
+    _need(x, torch.float32, "x")
+    m, k = x.shape
+    if w.dim() != 2 or w.shape[0] != n_out:
+        raise ValueError("w must be [n_out, row_bytes]")
+    if out is None:
+        out = torch.empty(m, n_out, dtype=torch.float32, device=x.device)
+    call("kdq_gemm_rows", encoding, w.data_ptr(), w.shape[1], n_out, k, x.data_ptr(), m,
+         out.data_ptr(), _ptr(status), _stream())
+    return out
+
+
 def gguf_gemm_check(encoding: int, packed: torch.Tensor, n_out: int, n_in: int) -> int:
     """The prefill GEMM's scale checks over a tile-packed matrix (kdq_gguf_gemm_check):
     bit 1 a non-finite scale, bit 2 a dequantised weight that could pass the fp16 range
