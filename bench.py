@@ -511,6 +511,31 @@ def bench_gemm_gguf(torch, encoding, k, n, m=512, reps=10, count=20, copies=8):
             "mfma_frac": round(tflops / FP16_PEAK_TFLOPS, 4)}
 
 
+def bench_gemm_rows(torch, encoding, k, n, m=512, reps=10, count=20, copies=4):
+    """Prefill GEMM over row-major GGUF rows (kdq_gemm_rows), the encodings that have no
+    tile-packed form: one 512-token chunk x fp32 [m, k] -> fp32 [m, n]; per launch the
+    activation staging kernel and the GEMM.  BF16 weights are random bits with a fixed
+    exponent (the timing does not depend on the values; the seeded normal generator
+    takes half a minute at this size)."""
+    from kadan_amd import ops, synth
+    if encoding == BF16:
+        bits = synth.random_bytes(0xD0, 1, n * k * 2).view(np.uint16)
+        w = ((bits & np.uint16(0x807F)) | np.uint16(0x3C00)).view(np.uint8).reshape(n, 2 * k)
+    else:
+        w = synth.gguf_weights(encoding, 0xD0 + encoding, n, k)
+    ws = rotated_copies(torch, w, copies, keep_mask(encoding, w.shape), 0xD0)
+    x = torch.from_numpy(synth.normal(0xD0, 9, m * k).reshape(m, k)).cuda()
+    y = torch.empty(m, n, dtype=torch.float32, device="cuda")
+    launch = lambda i: ops.gemm_rows(encoding, ws[i % copies], x, n, out=y)
+    for i in range(5):
+        launch(i)
+    ms = time_launches(torch, launch, count, reps)
+    tflops = 2.0 * m * k * n / (ms * 1e-3) / 1e12
+    return {"ms": round(ms, 4), "tflops": round(tflops, 2),
+            "mfma_frac": round(tflops / FP16_PEAK_TFLOPS, 4),
+            "weight_gbps": round(gemv_bytes(k, n, encoding) / (ms * 1e-3) / 1e9, 1)}
+
+
 def bench_moe_gguf(torch, rows, reps=10, count=64, resident=False):
     """The GGUF MoE layer (kdq_moe_gguf) at Qwen3-30B-A3B's geometry: hidden 2048, 128
     experts, top-8, expert ff 768, a 768-wide shared expert; Q4_K expert gate/up, Q6_K
@@ -727,6 +752,12 @@ def main():
                 name = f"gemm_{tag}_prefill_{k_}x{n_}"
                 if want(name):
                     extra[name] = bench_gemm_gguf(torch, enc, k_, n_)
+        for enc, tag in ((IQ4_XS, "iq4_xs"), (IQ4_NL, "iq4_nl"), (Q3_K, "q3_k"),
+                         (IQ3_XXS, "iq3_xxs"), (IQ3_S, "iq3_s"), (IQ2_S, "iq2_s"),
+                         (BF16, "bf16")):
+            name = f"gemm_rows_{tag}_prefill_4096x14336"
+            if want(name):
+                extra[name] = bench_gemm_rows(torch, enc, 4096, 14336)
         if want("c3_q4_0_gemm_row_major"):
             extra["c3_q4_0_gemm_row_major"] = bench_gemm(torch, packed=False)
         if want("moe_gguf_t1"):

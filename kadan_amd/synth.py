@@ -17,14 +17,21 @@ def splitmix64(seed: int, tensor: int, n: int) -> np.ndarray:
     """n 64-bit outputs of SplitMix64 started at hash(seed, tensor)."""
     base = np.uint64((seed * 0x100000001B3 + tensor * 0x9E3779B1) & 0xFFFFFFFFFFFFFFFF)
     out = np.empty(n, np.uint64)
-    chunk = 1 << 22
+    chunk = 1 << 18  # cache-sized pieces, updated in place
+    t = np.empty(chunk, np.uint64)
     with np.errstate(over="ignore"):
         for start in range(0, n, chunk):
-            i = np.arange(start + 1, min(n, start + chunk) + 1, dtype=np.uint64)
-            z = base + i * _GOLDEN
-            z = (z ^ (z >> np.uint64(30))) * _M1
-            z = (z ^ (z >> np.uint64(27))) * _M2
-            out[start:start + i.size] = z ^ (z >> np.uint64(31))
+            z = out[start:start + chunk]
+            w = t[:z.size]
+            z[:] = np.arange(start + 1, start + z.size + 1, dtype=np.uint64)
+            np.multiply(z, _GOLDEN, out=z)
+            np.add(z, base, out=z)
+            for shift, mul in ((30, _M1), (27, _M2)):
+                np.right_shift(z, np.uint64(shift), out=w)
+                np.bitwise_xor(z, w, out=z)
+                np.multiply(z, mul, out=z)
+            np.right_shift(z, np.uint64(31), out=w)
+            np.bitwise_xor(z, w, out=z)
     return out
 
 
