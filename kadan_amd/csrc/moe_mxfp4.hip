@@ -28,6 +28,10 @@
 namespace kdq {
 namespace {
 
+#define KDQ_EXPF_FN __device__ __forceinline__
+#include "kdq_expf.hpp"
+#undef KDQ_EXPF_FN
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -153,14 +157,36 @@ __device__ __forceinline__ void route_select_r(const float* __restrict__ logits,
         maximum = fmaxf(maximum, v[j]);
     }
     maximum = wave_max_rows(maximum);
+    auto value_of = [&](const float (&a)[R], unsigned e) {  // a of expert e (wave-uniform)
+        const unsigned j = e / 64;
+        float aj = a[0];
+#pragma unroll
+        for (int r = 1; r < R; ++r)
+            aj = j == unsigned(r) ? a[r] : aj;
+        return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(aj), e % 64));
+    };
+    // p = the host library's expf (glibc_expf reproduces it bit for bit) and the total in
+    // double, summed in expert order as the reference's loop does.  When every p is a
+    // multiple of 2^-45 every partial sum is exact (all stay below 2^8), so any order
+    // gives that total and one wavefront reduction computes it; otherwise (p below
+    // 2^-22 with low bits set, NaN) the wavefront adds them one by one in order.
     double total = 0.0;
+    bool exact = true;
 #pragma unroll
     for (int j = 0; j < R; ++j) {
         const unsigned e = lane + 64 * j;
-        p[j] = e < experts ? expf(v[j] - maximum) : 0.f;
+        p[j] = e < experts ? glibc_expf(v[j] - maximum) : 0.f;
+        const double scaled = double(p[j]) * 0x1p45;
+        exact = exact && scaled == __builtin_trunc(scaled);
         total += double(p[j]);
     }
-    total = wave_sum_double(total);
+    if (__ballot(!exact) == 0) {
+        total = wave_sum_double(total);
+    } else {
+        total = 0.0;
+        for (unsigned e = 0; e < experts; ++e)
+            total += double(value_of(p, e));
+    }
 #pragma unroll
     for (int j = 0; j < R; ++j)
         p[j] = float(double(p[j]) / total);
@@ -178,14 +204,7 @@ __device__ __forceinline__ void route_select_r(const float* __restrict__ logits,
         valid[j] = lane + 64 * j < experts;
         nan_seen |= __ballot(valid[j] && isnan(p[j])) != 0;
     }
-    auto p_of = [&](int e) {  // p of expert e (wave-uniform)
-        const int j = e / 64;
-        float pj = p[0];
-#pragma unroll
-        for (int r = 1; r < R; ++r)
-            pj = j == r ? p[r] : pj;
-        return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), e % 64));
-    };
+    auto p_of = [&](int e) { return value_of(p, unsigned(e)); };  // p of expert e
     int chosen_e = 0;  // lane i < top_k: the i-th selection
     bool ambiguous = nan_seen;
     if (!nan_seen) {

@@ -32,6 +32,11 @@ Contents (all little-endian, plain arrays, no pickles):
                              (0, 1, 2, -1, -inf, and NaN / +inf in some rows) so that
                              equal probabilities are the rule: the order the library's
                              heap selection gives ties
+  route_near_<E>_<k>_logits / _idx / _w
+                             the same router on 256 rows whose top-k boundary sits among
+                             logits a few ulps apart (tests/util.py near_tie_logits):
+                             the order comes from the last bits of the library's expf,
+                             the double total and the division
 """
 import os
 import sys
@@ -216,6 +221,13 @@ def main():
         logits[0] = 0.0  # every probability equal
         idx, w = ref.moe_route(logits, top_k)
         key = f"route_{experts}_{top_k}"
+        data[f"{key}_logits"], data[f"{key}_idx"], data[f"{key}_w"] = logits, idx, w
+    # routing near ties: values a few ulps apart at the top-k boundary
+    from tests.util import near_tie_logits
+    for experts, top_k, seed in ((32, 4, 0x7136), (128, 8, 0x7137)):
+        logits = near_tie_logits(seed, 256, experts, top_k)
+        idx, w = ref.moe_route(logits, top_k)
+        key = f"route_near_{experts}_{top_k}"
         data[f"{key}_logits"], data[f"{key}_idx"], data[f"{key}_w"] = logits, idx, w
     np.savez_compressed(OUT, **data)
     print(OUT, os.path.getsize(OUT), "bytes,", len(data), "arrays")

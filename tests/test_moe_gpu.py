@@ -61,6 +61,39 @@ def test_route_ties_in_library_order(device, experts, top_k):
     assert np.all((gw.view(np.uint32) == w.view(np.uint32)) | (np.isnan(gw) & np.isnan(w)))
 
 
+@pytest.mark.parametrize("experts,top_k", [(32, 4), (128, 8)])
+def test_route_near_ties_golden(device, experts, top_k):
+    """Logits a few ulps apart at the top-k boundary, recorded through the compiled
+    reference's router: indices and weights bit-exact."""
+    torch = _torch()
+    with np.load(GOLDEN, allow_pickle=False) as f:
+        key = f"route_near_{experts}_{top_k}"
+        logits, idx, w = f[f"{key}_logits"], f[f"{key}_idx"], f[f"{key}_w"]
+    from kadan_amd import ops
+    gi, gw, _, _ = ops.moe_route(torch.from_numpy(logits).to(device), top_k)
+    assert np.array_equal(gi.cpu().numpy(), idx)
+    assert np.array_equal(gw.cpu().numpy().view(np.uint32), w.view(np.uint32))
+
+
+@pytest.mark.parametrize("experts,top_k,seed", [(32, 4, 0x713B), (128, 8, 0x713C),
+                                                (256, 8, 0x713D)])
+def test_route_near_ties_bit_exact(device, oracle, experts, top_k, seed):
+    """100000 near-tie rows (tests/util.py near_tie_logits; a third of them with
+    probabilities below 2^-22, where the double total's order matters): the device's
+    indices and weights bit for bit equal to the oracle's router (the host C library's
+    expf, the total summed in expert order), which tests/test_oracle.py pins to the
+    compiled reference on the same kind of rows."""
+    torch = _torch()
+    from kadan_amd import ops
+    from tests.util import near_tie_logits
+    logits = near_tie_logits(seed, 100000, experts, top_k)
+    idx, w = oracle.moe_route(logits, top_k)
+    gi, gw, _, _ = ops.moe_route(torch.from_numpy(logits).to(device), top_k)
+    gi, gw = gi.cpu().numpy(), gw.cpu().numpy()
+    bad = np.flatnonzero((gi != idx).any(1) | (gw.view(np.uint32) != w.view(np.uint32)).any(1))
+    assert bad.size == 0, (bad.size, bad[:5])
+
+
 def test_route_equal_logits_heap_order(device):
     """16 equal probabilities, top-4: std::partial_sort gives [1, 3, 0, 2] (worked through
     the heap steps in tests/test_oracle.py)."""

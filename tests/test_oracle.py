@@ -542,6 +542,27 @@ def test_route_ties_vs_compiled_library(oracle, reference):
         assert same_bits(a[1], b[1])
 
 
+@pytest.mark.parametrize("experts,top_k", [(32, 4), (128, 8)])
+def test_route_near_ties_vs_reference_vectors(oracle, golden, experts, top_k):
+    """Logits a few ulps apart at the top-k boundary (tests/util.py near_tie_logits):
+    indices and weights bit for bit against the compiled reference's router.  The order
+    rests on the last bits of expf, of the double total and of the division."""
+    key = f"route_near_{experts}_{top_k}"
+    idx, w = oracle.moe_route(golden[f"{key}_logits"], top_k)
+    assert np.array_equal(idx, golden[f"{key}_idx"])
+    assert same_bits(w, golden[f"{key}_w"])
+
+
+def test_route_near_ties_vs_compiled_library(oracle, reference):
+    """20000 fresh near-tie rows per configuration against the compiled reference."""
+    from tests.util import near_tie_logits
+    for experts, top_k, seed in ((32, 4, 0x7138), (128, 8, 0x7139), (256, 8, 0x713A)):
+        logits = near_tie_logits(seed, 20000, experts, top_k)
+        a, b = oracle.moe_route(logits, top_k), reference.moe_route(logits, top_k)
+        assert np.array_equal(a[0], b[0])
+        assert same_bits(a[1], b[1])
+
+
 def test_route_orders_by_probability_not_logit(oracle):
     # logits 0 and 1e-8 differ, their float probabilities do not (expf(-1e-8) rounds to
     # 1): they tie, and the heap order decides (std::partial_sort over 8 experts, top 3)

@@ -159,3 +159,31 @@ def known_answer_moe_gguf():
         for d in range(H):
             y[t, d] += gate_t * 32 * 0.25 * (1 + d % 5) * hs
     return spec, x, y, idx
+
+
+def near_tie_logits(seed, rows, experts, top_k):
+    """Router logits whose top-k boundary sits among values a few ulps apart.
+
+    Per row: logits ~ N(0, sigma) with sigma from {0.5, 2, 6} (the widest spreads give
+    probabilities below 2^-22, where the double total's summation order matters); then
+    top_k + 2 experts get one value v plus 0..4 ulps each, v either the row's maximum or
+    up to 3 below it, so exp(l - max) of the group are near-equal or equal floats and
+    their order is decided in the last bits of expf, of the total and of the division.
+    A quarter of the rows put a second group of near-equal values just above the
+    first."""
+    g = np.random.default_rng(seed)
+    sigma = g.choice(np.array([0.5, 2.0, 6.0], np.float32), size=rows)
+    logits = (g.standard_normal((rows, experts)).astype(np.float32) * sigma[:, None])
+    m = min(experts, top_k + 2)
+    for r in range(rows):
+        top = logits[r].max()
+        v = np.float32(top - (0.0 if r % 3 == 0 else g.uniform(0.0, 3.0)))
+        group = g.choice(experts, size=m, replace=False)
+        steps = g.integers(0, 5, size=m).astype(np.int32)
+        logits[r, group] = (np.full(m, v, np.float32).view(np.int32) + steps).view(np.float32)
+        if r % 4 == 1:
+            second = g.choice(experts, size=2, replace=False)
+            w = np.float32(v + np.float32(1e-3))
+            logits[r, second] = (np.full(2, w, np.float32).view(np.int32) +
+                                 g.integers(0, 3, size=2).astype(np.int32)).view(np.float32)
+    return logits
