@@ -1193,21 +1193,41 @@ struct MfmaJobs {
 // any wavefront's weight requests (one barrier between them), so the staging's data does
 // not return behind other wavefronts' weights (C2 4096 -> 14336: 7.95 -> 7.77 us; with
 // one tile a workgroup, C1, it measured 0.35 us slower).
-template <int ENC, int R, int W, bool PACKED, int FORM>
-__global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
+//
+// mfma_gemv_body is the workgroup (bx, by) of that grid; `routed` >= 0 stands in for the
+// job's device index (the fused MoE decode, which selects the experts itself).  COHERENT
+// stores y at device scope (written through to where every XCD reads it), for another
+// workgroup to read after this one's completion count.  A `late` functor (anything but
+// EarlyRoute) gives the expert only after the activation loads are in flight, just before
+// the first weight loads (the fused decode routes there, every thread calling it).
+struct EarlyRoute {};
+template <int ENC, int R, int W, bool PACKED, int FORM, bool COHERENT = false,
+          class LateRoute = EarlyRoute>
+__device__ __forceinline__ void mfma_gemv_body(const MfmaJobs& jobs, unsigned bx,
+                                               unsigned by, int routed,
+                                               const LateRoute& late = LateRoute{}) {
     constexpr bool PLAIN = FORM > 0, X2 = FORM == 2, XFIRST = FORM == 3;
+    constexpr bool LATE = !std::is_same_v<LateRoute, EarlyRoute>;
     const bool affine = !PLAIN && jobs.affine;
-    const unsigned jid = affine ? 0 : blockIdx.y, step = affine ? blockIdx.y : 0;
+    const unsigned jid = affine ? 0 : by, step = affine ? by : 0;
     const MfmaJob& jb = jobs.job[jid];
-    const int chosen = !PLAIN && jb.index ? jb.index[step] : 0;
-    if (chosen < 0)
-        return;
-    const size_t expert =
-        !PLAIN && jb.index ? size_t(min(unsigned(chosen), jb.index_limit - 1)) * jb.index_stride
-                           : 0;
-    const uint8_t* __restrict__ weights = jb.weights + expert;
     const unsigned mats = !PLAIN && jobs.mats == 2 ? 2 : 1;
-    const uint8_t* __restrict__ up = mats == 2 ? jb.up + expert : weights;
+    const uint8_t* __restrict__ weights = jb.weights;
+    const uint8_t* __restrict__ up = mats == 2 ? jb.up : weights;
+    auto place = [&](int chosen) {  // the expert slice's weights
+        const size_t expert =
+            !PLAIN && jb.index
+                ? size_t(min(unsigned(chosen), jb.index_limit - 1)) * jb.index_stride
+                : 0;
+        weights = jb.weights + expert;
+        up = mats == 2 ? jb.up + expert : weights;
+    };
+    if constexpr (!LATE) {
+        const int chosen = routed >= 0 ? routed : (!PLAIN && jb.index ? jb.index[step] : 0);
+        if (chosen < 0)
+            return;
+        place(chosen);
+    }
     const size_t row_bytes = jb.row_bytes, stride = jb.stride;
     const float* x = jb.x + (affine ? step / jobs.x_every : 0) * jobs.x_step;
     float* __restrict__ y = jb.y + (affine ? step * jobs.y_step : 0);
@@ -1236,9 +1256,13 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
                          : ENC == KDQ_IQ4_XS || ENC == KDQ_Q3_K || lattice(ENC) ? ScaleSel{G, false}
                                              : ScaleSel{8 * ((2 * G) & 3), G >= 2};
     // every argument in one round of scalar loads, then the exit test
-    asm volatile("" ::"s"(weights), "s"(up), "s"(x), "s"(y), "s"(status), "s"(row_bytes),
-                 "s"(stride), "s"(in), "s"(out), "s"(rows_per_wg));
-    const unsigned r0 = blockIdx.x * rows_per_wg, r1 = min(out, r0 + rows_per_wg);
+    if constexpr (LATE)
+        asm volatile("" ::"s"(x), "s"(y), "s"(status), "s"(row_bytes), "s"(stride), "s"(in),
+                     "s"(out), "s"(rows_per_wg));
+    else
+        asm volatile("" ::"s"(weights), "s"(up), "s"(x), "s"(y), "s"(status), "s"(row_bytes),
+                     "s"(stride), "s"(in), "s"(out), "s"(rows_per_wg));
+    const unsigned r0 = bx * rows_per_wg, r1 = min(out, r0 + rows_per_wg);
     if (r0 >= out)
         return;  // the whole workgroup, before any barrier
     bool bad = false;
@@ -1299,6 +1323,8 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
         __builtin_amdgcn_s_barrier();  // every wavefront's x request ahead of any weight request
         __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (LATE)
+        place(late());
     Lane L[kUnits];
     load_units(r0, UnitCursor{wave, 0}, L);
     asm volatile("" ::: "memory");
@@ -1381,13 +1407,23 @@ __global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
                 v = silu_of(v) * row16_total(u);
             }
             const unsigned n = p0 + 16 * t + jj;
-            if (k == 0 && n < r1)
-                y[size_t(r) * stride + n] = v;
+            if (k == 0 && n < r1) {
+                if constexpr (COHERENT)
+                    __hip_atomic_store(&y[size_t(r) * stride + n], v, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                else
+                    y[size_t(r) * stride + n] = v;
+            }
         }
         __syncthreads();
     }
     if (status && __any(bad) && lane == 0)
         atomicOr(status, 1u);
+}
+
+template <int ENC, int R, int W, bool PACKED, int FORM>
+__global__ __launch_bounds__(W * 64) void mfma_gemv(const MfmaJobs jobs) {
+    mfma_gemv_body<ENC, R, W, PACKED, FORM>(jobs, blockIdx.x, blockIdx.y, -1);
 }
 
 // ----------------------------------------------------------------- host side
@@ -2320,6 +2356,303 @@ int indexed_gemv_batch(const IndexedJob* jobs, size_t count, hipStream_t s) {
             return rc;
     }
     return KDQ_OK;
+}
+
+// ----------------------------------------------------------------- fused MoE decode
+
+namespace {
+
+#include "kdq_route.hpp"
+
+// The routing a decode launch computes for itself, and the counters of the down launch's
+// row blocks, which the up launch clears.
+struct DecodeRoute {
+    const float* logits;
+    unsigned experts, top_k;
+    int32_t* idx;
+    float* w;
+    unsigned* counters;
+    unsigned counter_count;
+    // the shared expert's gate sigmoid(gate_vector . x), taken once for the down launch
+    const float* gate_vector;
+    const float* x;
+    unsigned hidden;
+    float* gate;
+    unsigned* status;
+};
+
+// *out = sigmoid(v . x) over `hidden` values by threads 0..255 of the workgroup, in
+// combine_kernel's order (a thread's float4 columns j, j + 256, ... with the four products
+// of each fused in turn, an xor butterfly per wavefront, then (0 + 1) + (2 + 3)), so the
+// fused and the separate decode take the same value; a non-finite entry of v sets bit 1
+// of *status.  Every thread of the workgroup calls it.
+__device__ __forceinline__ void shared_gate(const float* __restrict__ v,
+                                            const float* __restrict__ x, unsigned hidden,
+                                            float* out, unsigned* status) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    __shared__ float wave_sum[4];
+    __shared__ int wave_bad[4];
+    if (threadIdx.x < 256) {
+        const f32x4* xr = reinterpret_cast<const f32x4*>(x);
+        const f32x4* vr = reinterpret_cast<const f32x4*>(v);
+        float s = 0.f;
+        bool finite = true;
+        for (unsigned q = threadIdx.x; q < hidden / 4; q += 256) {
+            const f32x4 a = xr[q], b = vr[q];
+            finite = finite && isfinite(b.x) && isfinite(b.y) && isfinite(b.z) && isfinite(b.w);
+            s = fmaf(a.x, b.x, s);
+            s = fmaf(a.y, b.y, s);
+            s = fmaf(a.z, b.z, s);
+            s = fmaf(a.w, b.w, s);
+        }
+        for (int m = 32; m >= 1; m /= 2)
+            s += __shfl_xor(s, m, 64);
+        const bool bad = __any(!finite);
+        if (threadIdx.x % 64 == 0) {
+            wave_sum[threadIdx.x / 64] = s;
+            wave_bad[threadIdx.x / 64] = bad;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        *out = sigmoid_of((wave_sum[0] + wave_sum[1]) + (wave_sum[2] + wave_sum[3]));
+        if (status && (wave_bad[0] | wave_bad[1] | wave_bad[2] | wave_bad[3]))
+            atomicOr(status, 1u);
+    }
+}
+
+// Workgroups [0, a.columns * a.count) run the experts' paired gate / up (job step = slot,
+// the slot's expert from this workgroup's own routing of the token), the rest the shared
+// expert's paired gate / up.  Wavefront 0 routes (the whole softmax and top-k of the one
+// token, as route_kernel does it) while the others wait; workgroup 0 also stores the
+// selection and clears the down launch's counters.
+template <int EA, bool PA, int EB, int W>
+__global__ __launch_bounds__(W * 64) void moe_decode_up_kernel(const MfmaJobs a,
+                                                               const MfmaJobs b,
+                                                               const DecodeRoute route) {
+    __shared__ int chosen[kMaxFused];
+    const unsigned a_workgroups = a.columns * a.count;
+    if (blockIdx.x < a_workgroups) {
+        const unsigned slot = blockIdx.x / a.columns;
+        // routed once the token's activation loads are in flight
+        auto late = [&]() -> int {
+            if (threadIdx.x < 64) {
+                int e;
+                float we;
+                route_select(route.logits, 0, route.experts, route.top_k, threadIdx.x, e, we);
+                if (threadIdx.x < route.top_k) {
+                    chosen[threadIdx.x] = e;
+                    if (blockIdx.x == 0) {
+                        route.idx[threadIdx.x] = e;
+                        route.w[threadIdx.x] = we;
+                    }
+                }
+            }
+            if (blockIdx.x == 0)
+                for (unsigned i = threadIdx.x; i < route.counter_count; i += W * 64)
+                    route.counters[i] = 0u;
+            __syncthreads();
+            return chosen[slot];
+        };
+        mfma_gemv_body<EA, 1, W, PA, 0, false, decltype(late)>(a, blockIdx.x % a.columns, slot,
+                                                               -1, late);
+    } else {
+        const unsigned k = blockIdx.x - a_workgroups;
+        if (k == 0) {
+            shared_gate(route.gate_vector, route.x, route.hidden, route.gate, route.status);
+            __syncthreads();  // its LDS words before the product's
+        }
+        mfma_gemv_body<EB, 1, W, false, 0>(b, k % b.columns, k / b.columns, -1);
+    }
+}
+
+// y = sum over the selections, in selection order, of down * weight, plus shared_down *
+// sigmoid(gate_vector . x), as combine_kernel computes it for one token.
+struct DecodeCombine {
+    const float* down;    // [top_k][hidden]
+    const float* shared;  // [hidden]
+    const float* w;       // [top_k]
+    const float* gate;    // sigmoid(gate_vector . x), from the up launch
+    unsigned top_k, hidden;
+    float* y;
+    unsigned* counters;  // one per row block, zero on entry
+};
+
+// Workgroups [0, a.columns * a.count) run the experts' down rows (slot = job step), the
+// rest the shared down; both halves cut the hidden rows into the same blocks of
+// a.rows_per_wg.  Each workgroup then counts itself into its row block; the last of the
+// top_k + 1 to arrive (its fences make the others' stored rows visible) combines that
+// block, so the layer needs no launch of its own for the combine.  The sum runs in the
+// fixed selection order whichever workgroup is last.
+template <int EA, bool PA, int EB, int W>
+__global__ __launch_bounds__(W * 64) void moe_decode_down_kernel(const MfmaJobs a,
+                                                                 const MfmaJobs b,
+                                                                 const DecodeCombine c) {
+    __shared__ unsigned arrived;
+    const unsigned a_workgroups = a.columns * a.count;
+    unsigned block;
+    if (blockIdx.x < a_workgroups) {
+        block = blockIdx.x % a.columns;
+        mfma_gemv_body<EA, 1, W, PA, 0, true>(a, block, blockIdx.x / a.columns, -1);
+    } else {
+        block = blockIdx.x - a_workgroups;
+        mfma_gemv_body<EB, 1, W, false, 0, true>(b, block, 0, -1);
+    }
+    // The rows went out as device-scope stores; once every one of them has completed
+    // (the wait below, then the barrier) the count may announce them.  The combining
+    // workgroup reads them with device-scope loads.  No cache-wide fence: one per
+    // workgroup (an L2 write-back and invalidate each) cost more than the layer.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        arrived = atomicAdd(&c.counters[block], 1u);
+    __syncthreads();
+    if (arrived != c.top_k)
+        return;  // the whole workgroup: another one combines this block
+
+    const float gate = *c.gate;
+    const unsigned r0 = block * a.rows_per_wg, r1 = min(c.hidden, r0 + a.rows_per_wg);
+    auto coherent = [](const float* p) {
+        return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    for (unsigned r = r0 + threadIdx.x; r < r1; r += W * 64) {
+        float sum = 0.f;
+        for (unsigned i = 0; i < c.top_k; ++i)
+            sum += coherent(c.down + size_t(i) * c.hidden + r) * c.w[i];
+        c.y[r] = sum + coherent(c.shared + r) * gate;
+    }
+    if (threadIdx.x == 0)
+        c.counters[block] = 0u;  // ready for the next layer call
+}
+
+// An affine launch over `count` slots of one token (job step = slot; x rows x_step apart,
+// a new one every x_every slots; y rows y_step apart), as indexed_gemv_affine(_packed)
+// builds it; false when the MFMA kernel does not take it.
+bool decode_half(const IndexedJob& ij, unsigned count, size_t x_step, unsigned x_every,
+                 size_t y_step, bool packed, MfmaJobs& mj, MfmaPlan& p) {
+    const kdq_matvec_job& j = ij.job;
+    const unsigned mats = ij.paired ? 2 : 1;
+    if (j.rows != 1 || mfma_table_bytes(j.encoding) ||
+        (packed ? (!packed_unit(j.encoding) || j.columns % 16) : !fusable(j, false)) ||
+        !plan_mfma(1, j.in, size_t(j.columns) * count, p, packed, mats, 0))
+        return false;
+    mj = MfmaJobs{};
+    mj.count = count;
+    mj.in = j.in;
+    mj.affine = count > 1 || ij.index ? 1 : 0;
+    mj.x_every = x_every;
+    mj.mats = mats;
+    mj.x_step = x_step;
+    mj.y_step = y_step;
+    mj.job[0] = MfmaJob{static_cast<const uint8_t*>(j.weights), j.input, j.output, j.status,
+                        packed ? 0 : j.row_bytes, j.stride, j.columns,
+                        ij.index ? ij.index_limit : 0, ij.index, ij.index_stride,
+                        static_cast<const uint8_t*>(ij.paired)};
+    number_workgroups(mj, p.rows_per_wg);
+    return true;
+}
+
+// the fused decode kernels keep a few static LDS words beside the dynamic area
+constexpr int kDecodeDynamicLds = 159 * 1024;
+
+template <int EA, bool PA, int EB, int W>
+int launch_decode_up(const MfmaJobs& a, const MfmaJobs& b, const DecodeRoute& r, size_t lds,
+                     hipStream_t s) {
+    static bool configured = false;
+    if (!configured) {
+        KDQ_HIP(hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&moe_decode_up_kernel<EA, PA, EB, W>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, kDecodeDynamicLds));
+        configured = true;
+    }
+    hipLaunchKernelGGL((moe_decode_up_kernel<EA, PA, EB, W>),
+                       dim3(a.columns * a.count + b.columns * b.count), dim3(W * 64), lds, s,
+                       a, b, r);
+    KDQ_HIP(hipGetLastError());
+    return KDQ_OK;
+}
+
+template <int EA, bool PA, int EB>
+int launch_decode_down(const MfmaJobs& a, const MfmaJobs& b, const DecodeCombine& c,
+                       size_t lds, hipStream_t s) {
+    static bool configured = false;
+    if (!configured) {
+        KDQ_HIP(hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&moe_decode_down_kernel<EA, PA, EB, 4>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, kDecodeDynamicLds));
+        configured = true;
+    }
+    hipLaunchKernelGGL((moe_decode_down_kernel<EA, PA, EB, 4>),
+                       dim3(a.columns * a.count + b.columns * b.count), dim3(256), lds, s, a,
+                       b, c);
+    KDQ_HIP(hipGetLastError());
+    return KDQ_OK;
+}
+
+}  // namespace
+
+int moe_decode_fused(const DecodeMoe& m, hipStream_t s, bool check_only) {
+    const unsigned K = m.top_k;
+    if (K == 0 || K > unsigned(kMaxFused) || m.experts > 256 || m.hidden % 4)
+        return KDQ_ERR_UNSUPPORTED;
+    MfmaJobs ua, ub, da, db;
+    MfmaPlan pua, pub, pda, pdb;
+    const size_t F = m.experts_up.job.columns;
+    if (m.experts_down.job.in != F ||
+        !decode_half(m.experts_up, K, 0, K, F, m.up_packed, ua, pua) ||
+        !decode_half(m.shared_up, 1, 0, 1, 0, false, ub, pub) ||
+        !decode_half(m.experts_down, K, F, 1, m.hidden, m.down_packed, da, pda) ||
+        !decode_half(m.shared_down, 1, 0, 1, 0, false, db, pdb))
+        return KDQ_ERR_UNSUPPORTED;
+    // both halves of a launch: one workgroup size; the down halves cut the hidden rows
+    // alike (packed halves: rows per workgroup a multiple of 8)
+    if (pua.waves != pub.waves || pua.waves < 8 || pdb.waves != 4 || pda.waves != 4 ||
+        m.experts_down.job.columns != m.hidden || m.shared_down.job.columns != m.hidden ||
+        !m.experts_up.paired || !m.shared_up.paired || m.experts_down.paired ||
+        m.shared_down.paired)
+        return KDQ_ERR_UNSUPPORTED;
+    const unsigned rows = (std::max(da.rows_per_wg, db.rows_per_wg) + 7) & ~7u;
+    number_workgroups(da, rows);
+    number_workgroups(db, rows);
+    const size_t up_lds = std::max(mfma_lds(1, ua.in, 2), mfma_lds(1, ub.in, 2));
+    const size_t down_lds = std::max(mfma_lds(1, da.in, 1), mfma_lds(1, db.in, 1));
+    if (std::max(up_lds, down_lds) > size_t(kDecodeDynamicLds))
+        return KDQ_ERR_UNSUPPORTED;
+    const int ea = m.experts_up.job.encoding, eb = m.shared_up.job.encoding;
+    const int da_enc = m.experts_down.job.encoding, db_enc = m.shared_down.job.encoding;
+    // the instantiated pairs (the Q4_K / Q6_K / Q8_0 mixes of K-quant MoE checkpoints)
+    const bool up_ok = ea == KDQ_Q4_K && (eb == KDQ_Q8_0 || eb == KDQ_Q4_K) &&
+                       (pua.waves == 8 || pua.waves == 16);
+    const bool down_ok = (da_enc == KDQ_Q6_K || da_enc == KDQ_Q4_K) &&
+                         (db_enc == KDQ_Q4_K || db_enc == KDQ_Q6_K);
+    if (!up_ok || !down_ok || da.columns != db.columns || da.columns > m.counter_count)
+        return KDQ_ERR_UNSUPPORTED;
+    if (check_only)
+        return KDQ_OK;
+
+    const DecodeRoute route{m.logits, m.experts,     K,       m.idx,    m.w,
+                            m.counters, da.columns, m.gate_vector, m.x, m.hidden,
+                            m.gate,   m.status};
+    int rc;
+    auto up = [&]<bool PA>() -> int {
+        if (pua.waves == 8)
+            return eb == KDQ_Q8_0 ? launch_decode_up<KDQ_Q4_K, PA, KDQ_Q8_0, 8>(ua, ub, route, up_lds, s)
+                                  : launch_decode_up<KDQ_Q4_K, PA, KDQ_Q4_K, 8>(ua, ub, route, up_lds, s);
+        return eb == KDQ_Q8_0 ? launch_decode_up<KDQ_Q4_K, PA, KDQ_Q8_0, 16>(ua, ub, route, up_lds, s)
+                              : launch_decode_up<KDQ_Q4_K, PA, KDQ_Q4_K, 16>(ua, ub, route, up_lds, s);
+    };
+    if ((rc = m.up_packed ? up.template operator()<true>() : up.template operator()<false>()))
+        return rc;
+    const DecodeCombine comb{m.experts_down.job.output, m.shared_down.job.output, m.w, m.gate,
+                             K, m.hidden, m.y, m.counters};
+    auto down = [&]<bool PA>() -> int {
+        if (da_enc == KDQ_Q6_K)
+            return db_enc == KDQ_Q4_K ? launch_decode_down<KDQ_Q6_K, PA, KDQ_Q4_K>(da, db, comb, down_lds, s)
+                                      : launch_decode_down<KDQ_Q6_K, PA, KDQ_Q6_K>(da, db, comb, down_lds, s);
+        return db_enc == KDQ_Q4_K ? launch_decode_down<KDQ_Q4_K, PA, KDQ_Q4_K>(da, db, comb, down_lds, s)
+                                  : launch_decode_down<KDQ_Q4_K, PA, KDQ_Q6_K>(da, db, comb, down_lds, s);
+    };
+    return m.down_packed ? down.template operator()<true>() : down.template operator()<false>();
 }
 
 }  // namespace kdq

@@ -181,6 +181,38 @@ int indexed_gemv_affine_packed(const IndexedJob& first, unsigned count, size_t x
 // with a paired matrix.
 bool swiglu_pairable(const kdq_matvec_job& j, size_t count);
 
+// One token's MoE layer after its router logits, in two launches (gguf_gemv.hip):
+//   up:   every workgroup of the experts' paired gate / up routes the token itself
+//         (route_select) and multiplies its slot's expert; the shared expert's paired
+//         gate / up in the same launch;
+//   down: the experts' and the shared expert's down rows, the last workgroup of each row
+//         block combining it (selection order, plus shared * sigmoid(gate_vector . x)).
+// experts_up: paired, x = the token, y = [top_k][ff], index = idx (which the up launch
+// writes, with w); experts_down: x = experts_up's y, y = [top_k][hidden], index = idx;
+// shared_up: paired, one job; shared_down: x = shared_up's y, y = [hidden].  counters:
+// device scratch of counter_count unsigned (the up launch clears them); gate: one float
+// of device scratch.  Returns
+// KDQ_ERR_UNSUPPORTED, having launched nothing, when the shapes or encodings are not
+// among those instantiated (Q4_K expert gate / up with Q8_0 or Q4_K shared gate / up,
+// inputs of 1280..4096 values; Q6_K or Q4_K downs of at most 1024 inputs); with
+// check_only it launches nothing either way.
+struct DecodeMoe {
+    IndexedJob experts_up, shared_up, experts_down, shared_down;
+    bool up_packed, down_packed;
+    const float* logits;
+    unsigned experts, top_k, hidden;
+    int32_t* idx;
+    float* w;
+    const float* gate_vector;
+    const float* x;
+    float* y;
+    unsigned* status;
+    unsigned* counters;
+    unsigned counter_count;
+    float* gate;  // device scratch: the shared gate's sigmoid, between the two launches
+};
+int moe_decode_fused(const DecodeMoe& m, hipStream_t stream, bool check_only);
+
 // silu and sigmoid as the reference defines them (IW/src/models/text/gguf_weights.cpp:627-633)
 __device__ __forceinline__ float silu_of(float v) {
     return v / (1.0f + expf(-v));

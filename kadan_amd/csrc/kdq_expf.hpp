@@ -16,10 +16,9 @@
 // reduction two inputs differ (-0x1.f8cbb2p5 is one).
 //
 // The includer defines KDQ_EXPF_FN (for example `__device__ __forceinline__` in HIP
-// code, `inline` in host code) and provides fma(double, double, double).
+// code, `inline` in host code) and provides uint32_t / uint64_t and
+// fma(double, double, double); the header may be included inside a namespace.
 #pragma once
-
-#include <cstdint>
 
 namespace kdq_expf {
 

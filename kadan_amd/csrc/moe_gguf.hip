@@ -121,6 +121,7 @@ constexpr size_t kMaxGroupedSlots = 8192;
 // cost more than the 8-row items below that: measured at 64 rows 33 us slower, at 512
 // rows 65 us faster)
 constexpr size_t kSharedGemmRows = 256;
+constexpr size_t kDecodeCounters = 1024;  // row blocks of the fused decode's down launch
 
 // Slots by expert into segments padded to multiples of `pad` (kItemRows, or kTileRows when
 // a projection runs on the grouped GEMM): pos[s] (slot -> position), inv[p] (position ->
@@ -385,7 +386,7 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
                             pk.gate_exps ? 0 : gu_bytes * E, pk.up_exps ? 0 : up_bytes * E,
                             pk.down_exps ? 0 : dn_bytes * E, xs_bytes,
                             gemm_gu || gemm_dn ? positions * 4 : 0, shg_bytes, shu_bytes,
-                            shd_bytes, sh_scratch};
+                            shd_bytes, sh_scratch, rows == 1 ? kDecodeCounters * 4 : 0};
     constexpr size_t kParts = sizeof(sizes) / sizeof(sizes[0]);
     size_t total = 0;
     for (size_t b : sizes)
@@ -423,7 +424,54 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
     const void* sh_up = pk.up_shexp ? pk.up_shexp : part[22];
     const void* sh_down = pk.down_shexp ? pk.down_shexp : part[23];
     void* sh_work = part[24];
+    auto* counters = static_cast<unsigned*>(part[25]);
     auto st = static_cast<hipStream_t>(stream);
+
+    // one token: the router, then two fused launches (moe_decode_fused) where the
+    // encodings and shapes are among those it instantiates
+    if (rows == 1 && same_layout(L.gate_exps, L.up_exps) && same_layout(L.gate_shexp, L.up_shexp)) {
+        const bool up_packed = pk.gate_exps && pk.up_exps;
+        const bool down_packed = pk.down_exps != nullptr;
+        DecodeMoe m{};
+        m.experts_up = IndexedJob{job(L.gate_exps, x, 1, H, F, g, status), idx,
+                                  up_packed ? kdq_gguf_packed_bytes(L.gate_exps.encoding, H, F)
+                                            : L.gate_exps.expert_bytes,
+                                  unsigned(E), up_packed ? pk.up_exps : L.up_exps.weights};
+        if (up_packed)
+            m.experts_up.job.weights = pk.gate_exps;
+        m.shared_up = IndexedJob{job(L.gate_shexp, x, 1, H, S, sg, status), nullptr, 0, 1,
+                                 L.up_shexp.weights};
+        m.experts_down = IndexedJob{job(L.down_exps, g, 1, F, H, d, status), idx,
+                                    down_packed ? kdq_gguf_packed_bytes(L.down_exps.encoding, F, H)
+                                                : L.down_exps.expert_bytes,
+                                    unsigned(E), nullptr};
+        if (down_packed)
+            m.experts_down.job.weights = pk.down_exps;
+        m.shared_down = IndexedJob{job(L.down_shexp, sg, 1, S, H, ds, status), nullptr, 0, 1,
+                                   nullptr};
+        m.up_packed = up_packed;
+        m.down_packed = down_packed;
+        m.logits = logits;
+        m.experts = unsigned(E);
+        m.top_k = unsigned(K);
+        m.hidden = unsigned(H);
+        m.idx = idx;
+        m.w = w;
+        m.gate_vector = L.shared_gate;
+        m.x = x;
+        m.y = y;
+        m.status = status;
+        m.counters = counters;
+        m.counter_count = unsigned(kDecodeCounters) - 1;
+        m.gate = reinterpret_cast<float*>(counters + kDecodeCounters - 1);
+        if (moe_decode_fused(m, st, true) == KDQ_OK) {
+            const IndexedJob router{job(L.router, x, 1, H, E, logits, status), nullptr, 0, 1,
+                                    nullptr};
+            if ((rc = indexed_gemv_batch(&router, 1, st)))
+                return rc;
+            return moe_decode_fused(m, st, false);
+        }
+    }
 
     // 1. router, shared gate / up (with the swiglu in the same launch when the MFMA kernel
     //    takes the pair); the shared-gate scalar is taken by the combine

@@ -347,3 +347,39 @@ def test_moe_gguf_paired_gemm_bit_identical(device):
     y2, sel2, _ = ops.moe_gguf(to_device(torch, device, other), x)
     assert np.array_equal(sel.cpu().numpy(), sel2.cpu().numpy())
     assert np.array_equal(y.cpu().numpy(), y2.cpu().numpy())
+
+
+FUSED_DECODE = [  # (gate/up experts, down experts, shared gate/up, shared down)
+    (Q4_K, Q6_K, Q8_0, Q4_K), (Q4_K, Q4_K, Q4_K, Q6_K), (Q4_K, Q6_K, Q4_K, Q4_K),
+    (Q4_K, Q4_K, Q8_0, Q6_K)]
+
+
+@pytest.mark.parametrize("resident", [False, True], ids=["rows", "packed"])
+@pytest.mark.parametrize("encs", FUSED_DECODE, ids=lambda e: "-".join(map(str, e)))
+@pytest.mark.parametrize("H", [2048, 4096])
+def test_moe_gguf_fused_decode(device, oracle, encs, resident, H):
+    """One token on the fused decode (the router, then one launch that routes inside every
+    expert workgroup and runs the experts' and the shared expert's gate / up, and one that
+    runs every down and lets the last workgroup of each row block combine it): each
+    instantiated encoding mix, over row-major and resident packed stacks, hidden 2048 and
+    4096 (8 and 16 wavefronts).  Three calls in a row with different tokens (the row-block
+    counters reset between calls), each against the oracle, routing exact."""
+    import torch
+    E, K, F, S = 32, 8, 768, 512
+    gu, dn, sgu, sdn = encs
+    layer_encs = {"gate_exps": gu, "up_exps": gu, "down_exps": dn, "gate_shexp": sgu,
+                  "up_shexp": sgu, "down_shexp": sdn}
+    spec = make_layer(70 + H // 1024 + dn, H, E, K, F, S, layer_encs)
+    from kadan_amd import ops
+    dev = to_device(torch, device, spec)
+    packed = ops.moe_gguf_pack(dev) if resident else None
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    for call in range(3):
+        x = synth.normal(71 + call + H, 1, H).reshape(1, H)
+        want, idx, w = oracle.moe_gguf_forward(spec, x)
+        y, sel, ws = ops.moe_gguf(dev, torch.from_numpy(x).to(device), status=status,
+                                  packed=packed)
+        assert np.array_equal(sel.cpu().numpy(), idx)
+        assert np.abs(ws.cpu().numpy() - w).max() < 1e-6
+        assert_close(y.cpu().numpy(), want, what=f"fused decode {encs} call {call}")
+    assert int(status.item()) == 0
