@@ -18,6 +18,7 @@
 #include "kdq_common.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <type_traits>
 #include <vector>
@@ -2364,10 +2365,14 @@ namespace {
 
 #include "kdq_route.hpp"
 
-// The routing a decode launch computes for itself, and the counters of the down launch's
-// row blocks, which the up launch clears.
+// The router, the routing and the shared gate the up launch computes, and the counters
+// of the down launch's row blocks, which it clears.
 struct DecodeRoute {
-    const float* logits;
+    const uint8_t* router;  // F32 rows [experts][row_bytes]
+    size_t router_row_bytes;
+    unsigned router_workgroups;  // the grid's first workgroups: one router row per wavefront
+    unsigned epoch;              // this call's number on this device (never 0)
+    float* logits;
     unsigned experts, top_k;
     int32_t* idx;
     float* w;
@@ -2426,38 +2431,115 @@ __device__ __forceinline__ void shared_gate(const float* __restrict__ v,
 // expert's paired gate / up.  Wavefront 0 routes (the whole softmax and top-k of the one
 // token, as route_kernel does it) while the others wait; workgroup 0 also stores the
 // selection and clears the down launch's counters.
+// The fused decode's device-wide state (one copy per GPU, zero at load): the router
+// workgroups' completion count (the last one resets it) and, per slot, the published
+// selection: (epoch << 8) | expert of the call that routed last.  Calls that overlap on
+// one GPU race on them (and on the workspace), as on the rest of the library's scratch.
+__device__ unsigned g_router_arrived;
+__device__ unsigned g_routed_slot[kMaxFused];
+// Bounded wait for the routing: about 2^20 sleeps of 64 clocks (tens of ms); past it
+// the workgroup goes on with expert 0 and sets status bit 3 (a routing that never came).
+constexpr unsigned kRouteSpinLimit = 1u << 20;
+
+// Workgroups [0, router_workgroups): the router GEMV, one F32 row per wavefront in
+// exact_gemv<KDQ_F32, 1>'s arithmetic (the same logits as the staged path), stored at
+// device scope; the last of them to finish routes the token (route_select over those
+// logits, read at device scope), publishes the selection and then this call's epoch.
+// Then the experts' paired gate / up workgroups (job step = slot): their activation
+// loads go out first, then thread 0 waits for the epoch and reads its slot's expert.
+// Then the shared expert's paired gate / up; its first workgroup also takes the gate
+// scalar.  The router workgroups come first in the grid, so they are dispatched before
+// any workgroup that waits on them.
 template <int EA, bool PA, int EB, int W>
 __global__ __launch_bounds__(W * 64) void moe_decode_up_kernel(const MfmaJobs a,
                                                                const MfmaJobs b,
                                                                const DecodeRoute route) {
-    __shared__ int chosen[kMaxFused];
-    const unsigned a_workgroups = a.columns * a.count;
-    if (blockIdx.x < a_workgroups) {
-        const unsigned slot = blockIdx.x / a.columns;
-        // routed once the token's activation loads are in flight
-        auto late = [&]() -> int {
-            if (threadIdx.x < 64) {
-                int e;
-                float we;
-                route_select(route.logits, 0, route.experts, route.top_k, threadIdx.x, e, we);
-                if (threadIdx.x < route.top_k) {
-                    chosen[threadIdx.x] = e;
-                    if (blockIdx.x == 0) {
-                        route.idx[threadIdx.x] = e;
-                        route.w[threadIdx.x] = we;
-                    }
-                }
+    __shared__ int chosen;
+    __shared__ unsigned arrived;
+    const unsigned wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    if (blockIdx.x < route.router_workgroups) {
+        const unsigned column = blockIdx.x * W + wave;
+        if (column < route.experts) {
+            const float4* row = reinterpret_cast<const float4*>(
+                route.router + size_t(column) * route.router_row_bytes);
+            float sum = 0.f;
+            bool finite = true;
+            for (unsigned i = lane * 8; i < a.in; i += 64 * 8) {
+                const float4 w0 = row[i / 4], w1 = row[i / 4 + 1];
+                const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    finite = finite && isfinite(w[k]);
+                const float* xr = route.x + i;
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    sum = fmaf(w[k], xr[k], sum);
             }
-            if (blockIdx.x == 0)
-                for (unsigned i = threadIdx.x; i < route.counter_count; i += W * 64)
-                    route.counters[i] = 0u;
+            if (route.status && __any(!finite) && lane == 0)
+                atomicOr(route.status, 1u);
+            sum = wave_sum(sum);
+            if (lane == 0)
+                __hip_atomic_store(&route.logits[column], sum, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the logits stored first
+        __syncthreads();
+        if (threadIdx.x == 0)
+            arrived = atomicAdd(&g_router_arrived, 1u);
+        __syncthreads();
+        if (arrived != route.router_workgroups - 1)
+            return;
+        if (wave == 0) {
+            int e;
+            float we;
+            route_select<true>(route.logits, 0, route.experts, route.top_k, lane, e, we);
+            if (lane < route.top_k) {
+                __hip_atomic_store(&route.idx[lane], e, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&route.w[lane], we, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            }
+            for (unsigned i = lane; i < route.counter_count; i += 64)
+                route.counters[i] = 0u;
+            if (lane < unsigned(kMaxFused))  // each slot's word: this call's epoch and its
+                                              // expert (0 for slots past top_k)
+                __hip_atomic_store(&g_routed_slot[lane],
+                                   lane < route.top_k ? (route.epoch << 8) | unsigned(e) : 0u,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (lane == 0)
+                g_router_arrived = 0u;
+        }
+        return;
+    }
+    const unsigned a_workgroups = a.columns * a.count;
+    const unsigned id = blockIdx.x - route.router_workgroups;
+    if (id < a_workgroups) {
+        const unsigned slot = id / a.columns;
+        // the slot's expert, once the routing is published (the activation loads are in
+        // flight meanwhile)
+        auto late = [&]() -> int {
+            if (threadIdx.x == 0) {
+                unsigned spins = 0, word;
+                while (((word = __hip_atomic_load(&g_routed_slot[slot], __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT)) >> 8) !=
+                       route.epoch) {
+                    if (++spins == kRouteSpinLimit) {
+                        if (route.status)
+                            atomicOr(route.status, 8u);
+                        word = 0;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                chosen = int(word & 0xffu);
+            }
             __syncthreads();
-            return chosen[slot];
+            return chosen;
         };
-        mfma_gemv_body<EA, 1, W, PA, 0, false, decltype(late)>(a, blockIdx.x % a.columns, slot,
-                                                               -1, late);
+        mfma_gemv_body<EA, 1, W, PA, 0, false, decltype(late)>(a, id % a.columns, slot, -1,
+                                                               late);
     } else {
-        const unsigned k = blockIdx.x - a_workgroups;
+        const unsigned k = id - a_workgroups;
         if (k == 0) {
             shared_gate(route.gate_vector, route.x, route.hidden, route.gate, route.status);
             __syncthreads();  // its LDS words before the product's
@@ -2566,8 +2648,8 @@ int launch_decode_up(const MfmaJobs& a, const MfmaJobs& b, const DecodeRoute& r,
         configured = true;
     }
     hipLaunchKernelGGL((moe_decode_up_kernel<EA, PA, EB, W>),
-                       dim3(a.columns * a.count + b.columns * b.count), dim3(W * 64), lds, s,
-                       a, b, r);
+                       dim3(r.router_workgroups + a.columns * a.count + b.columns * b.count),
+                       dim3(W * 64), lds, s, a, b, r);
     KDQ_HIP(hipGetLastError());
     return KDQ_OK;
 }
@@ -2625,14 +2707,40 @@ int moe_decode_fused(const DecodeMoe& m, hipStream_t s, bool check_only) {
                        (pua.waves == 8 || pua.waves == 16);
     const bool down_ok = (da_enc == KDQ_Q6_K || da_enc == KDQ_Q4_K) &&
                          (db_enc == KDQ_Q4_K || db_enc == KDQ_Q6_K);
-    if (!up_ok || !down_ok || da.columns != db.columns || da.columns > m.counter_count)
+    if (!up_ok || !down_ok || da.columns != db.columns || da.columns > m.counter_count ||
+        m.experts > 256 ||
+        m.router.encoding != KDQ_F32 || m.router.in != m.hidden ||
+        m.router.columns != m.experts || m.router.row_bytes % 16 ||
+        reinterpret_cast<uintptr_t>(m.router.weights) % 16 ||
+        reinterpret_cast<uintptr_t>(m.x) % 16)
         return KDQ_ERR_UNSUPPORTED;
     if (check_only)
         return KDQ_OK;
 
-    const DecodeRoute route{m.logits, m.experts,     K,       m.idx,    m.w,
-                            m.counters, da.columns, m.gate_vector, m.x, m.hidden,
-                            m.gate,   m.status};
+    // this call's number on this device, 24 bits and never 0 (the published words start
+    // at 0)
+    static std::atomic<unsigned> calls[64];
+    int device = 0;
+    KDQ_HIP(hipGetDevice(&device));
+    unsigned epoch = ++calls[unsigned(device) % 64] & 0xffffffu;
+    if (epoch == 0)
+        epoch = ++calls[unsigned(device) % 64] & 0xffffffu;
+    const DecodeRoute route{static_cast<const uint8_t*>(m.router.weights),
+                            m.router.row_bytes,
+                            unsigned((m.experts + pua.waves - 1) / pua.waves),
+                            epoch,
+                            m.logits,
+                            m.experts,
+                            K,
+                            m.idx,
+                            m.w,
+                            m.counters,
+                            da.columns,
+                            m.gate_vector,
+                            m.x,
+                            m.hidden,
+                            m.gate,
+                            m.status};
     int rc;
     auto up = [&]<bool PA>() -> int {
         if (pua.waves == 8)

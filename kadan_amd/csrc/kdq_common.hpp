@@ -181,10 +181,11 @@ int indexed_gemv_affine_packed(const IndexedJob& first, unsigned count, size_t x
 // with a paired matrix.
 bool swiglu_pairable(const kdq_matvec_job& j, size_t count);
 
-// One token's MoE layer after its router logits, in two launches (gguf_gemv.hip):
-//   up:   every workgroup of the experts' paired gate / up routes the token itself
-//         (route_select) and multiplies its slot's expert; the shared expert's paired
-//         gate / up in the same launch;
+// One token's MoE layer in two launches (gguf_gemv.hip):
+//   up:   the F32 router GEMV, whose last workgroup routes the token (route_select) and
+//         publishes the selection; the experts' paired gate / up, each workgroup waiting
+//         (bounded; status bit 3 past the bound) for the selection once its activation
+//         loads are out; the shared expert's paired gate / up in the same launch;
 //   down: the experts' and the shared expert's down rows, the last workgroup of each row
 //         block combining it (selection order, plus shared * sigmoid(gate_vector . x)).
 // experts_up: paired, x = the token, y = [top_k][ff], index = idx (which the up launch
@@ -197,9 +198,10 @@ bool swiglu_pairable(const kdq_matvec_job& j, size_t count);
 // inputs of 1280..4096 values; Q6_K or Q4_K downs of at most 1024 inputs); with
 // check_only it launches nothing either way.
 struct DecodeMoe {
+    kdq_matvec_job router;  // F32, x = the token, y = logits (device scratch)
     IndexedJob experts_up, shared_up, experts_down, shared_down;
     bool up_packed, down_packed;
-    const float* logits;
+    float* logits;
     unsigned experts, top_k, hidden;
     int32_t* idx;
     float* w;

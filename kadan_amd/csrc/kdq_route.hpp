@@ -103,7 +103,9 @@ __device__ __forceinline__ int heap_route(POf p_of, unsigned experts, unsigned k
 
 // Token t by one whole wavefront (lane = its lane): lane i < top_k gets the i-th selected
 // expert and its renormalised weight.  R probabilities per lane (experts <= 64 R).
-template <int R>
+// COHERENT reads the logits at device scope (another workgroup of the same launch wrote
+// them with device-scope stores).
+template <int R, bool COHERENT = false>
 __device__ __forceinline__ void route_select_r(const float* __restrict__ logits, unsigned t,
                                                unsigned experts, unsigned top_k, unsigned lane,
                                                int& selected, float& selected_weight) {
@@ -113,7 +115,12 @@ __device__ __forceinline__ void route_select_r(const float* __restrict__ logits,
 #pragma unroll
     for (int j = 0; j < R; ++j) {
         const unsigned e = lane + 64 * j;
-        v[j] = e < experts ? l[e] : -INFINITY;
+        if constexpr (COHERENT)
+            v[j] = e < experts ? __hip_atomic_load(l + e, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT)
+                               : -INFINITY;
+        else
+            v[j] = e < experts ? l[e] : -INFINITY;
         maximum = fmaxf(maximum, v[j]);
     }
     maximum = wave_max_rows(maximum);
@@ -215,13 +222,14 @@ __device__ __forceinline__ void route_select_r(const float* __restrict__ logits,
     selected_weight = chosen_p / sum;
 }
 
+template <bool COHERENT = false>
 __device__ __forceinline__ void route_select(const float* __restrict__ logits, unsigned t,
                                              unsigned experts, unsigned top_k, unsigned lane,
                                              int& selected, float& selected_weight) {
     if (experts <= 64)
-        route_select_r<1>(logits, t, experts, top_k, lane, selected, selected_weight);
+        route_select_r<1, COHERENT>(logits, t, experts, top_k, lane, selected, selected_weight);
     else if (experts <= 128)
-        route_select_r<2>(logits, t, experts, top_k, lane, selected, selected_weight);
+        route_select_r<2, COHERENT>(logits, t, experts, top_k, lane, selected, selected_weight);
     else
-        route_select_r<4>(logits, t, experts, top_k, lane, selected, selected_weight);
+        route_select_r<4, COHERENT>(logits, t, experts, top_k, lane, selected, selected_weight);
 }

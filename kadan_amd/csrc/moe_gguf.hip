@@ -427,12 +427,13 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
     auto* counters = static_cast<unsigned*>(part[25]);
     auto st = static_cast<hipStream_t>(stream);
 
-    // one token: the router, then two fused launches (moe_decode_fused) where the
-    // encodings and shapes are among those it instantiates
+    // one token: two fused launches (moe_decode_fused) where the encodings and shapes are
+    // among those it instantiates
     if (rows == 1 && same_layout(L.gate_exps, L.up_exps) && same_layout(L.gate_shexp, L.up_shexp)) {
         const bool up_packed = pk.gate_exps && pk.up_exps;
         const bool down_packed = pk.down_exps != nullptr;
         DecodeMoe m{};
+        m.router = job(L.router, x, 1, H, E, logits, status);
         m.experts_up = IndexedJob{job(L.gate_exps, x, 1, H, F, g, status), idx,
                                   up_packed ? kdq_gguf_packed_bytes(L.gate_exps.encoding, H, F)
                                             : L.gate_exps.expert_bytes,
@@ -464,13 +465,8 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
         m.counters = counters;
         m.counter_count = unsigned(kDecodeCounters) - 1;
         m.gate = reinterpret_cast<float*>(counters + kDecodeCounters - 1);
-        if (moe_decode_fused(m, st, true) == KDQ_OK) {
-            const IndexedJob router{job(L.router, x, 1, H, E, logits, status), nullptr, 0, 1,
-                                    nullptr};
-            if ((rc = indexed_gemv_batch(&router, 1, st)))
-                return rc;
+        if (moe_decode_fused(m, st, true) == KDQ_OK)
             return moe_decode_fused(m, st, false);
-        }
     }
 
     // 1. router, shared gate / up (with the swiglu in the same launch when the MFMA kernel
