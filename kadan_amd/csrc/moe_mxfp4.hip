@@ -880,8 +880,21 @@ __device__ __forceinline__ void store_h_tiles(const f32x16 (&acc)[2][TILES], uns
     }
 }
 
-// gate/up: grid (groups of kGemmWaves feature groups of 32, items, K slices).  Wavefront w
-// multiplies gate and up rows of features 32 (kGemmWaves x + w) .. +31.  One slice:
+// The (column, item) cell of a grouped GEMM workgroup.  The grid's x dimension holds
+// cols x items_pad cells (items_pad a multiple of 8): workgroup L runs on XCD L % 8, and
+// XCD k takes items k, k + 8, ..., each with all its column workgroups in a row, so one
+// XCD's L2 serves an item's activation tiles to every column that multiplies them.
+struct ItemCell {
+    unsigned col, item;
+};
+__device__ __forceinline__ ItemCell item_cell(unsigned cols) {
+    const unsigned xcd = blockIdx.x % 8, j = blockIdx.x / 8;
+    return ItemCell{j % cols, (j / cols) * 8 + xcd};
+}
+
+// gate/up: grid (cells of item_cell: groups of kGemmWaves feature groups of 32 x items,
+// K slices).  Wavefront w multiplies gate and up rows of features 32 (kGemmWaves col + w)
+// .. +31.  One slice:
 // h = silu(g) * u into the down product's activation tiles; more: fp32 partials of g and u
 // per (tile row, feature) (finalize_kernel).
 // Three workgroups per compute unit (168 registers, no spill): measured 187 -> 174 us at
@@ -892,15 +905,17 @@ __global__ __launch_bounds__(kGemmWaves * 64, 3) void gate_up_kernel(
     size_t tiles, const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up,
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ items,
     const int32_t* __restrict__ item_count, uint8_t* __restrict__ ha,
-    float* __restrict__ part_g, float* __restrict__ part_u, size_t part_stride) {
+    float* __restrict__ part_g, float* __restrict__ part_u, size_t part_stride,
+    unsigned cols) {
     __shared__ __align__(16) uint8_t stage[2 * StageCopy<kXTerms, 2>::chunk_bytes];
-    if (int(blockIdx.y) >= *item_count)
+    const ItemCell cell = item_cell(cols);
+    if (int(cell.item) >= *item_count)
         return;
-    const Item it = load_item(items, offsets, blockIdx.y);
+    const Item it = load_item(items, offsets, cell.item);
     const unsigned wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const unsigned i32 = lane % 32, h = lane / 32;
     const Packed shape = packed_shape(1, inter, hidden);  // per expert
-    const unsigned fg = blockIdx.x * kGemmWaves + wave;   // feature group of 32
+    const unsigned fg = cell.col * kGemmWaves + wave;     // feature group of 32
     const bool active = fg < shape.groups;                // uniform per wavefront
     const unsigned f = (active ? fg : 0) * 32 + i32;
     unsigned q0, q1;
@@ -918,7 +933,7 @@ __global__ __launch_bounds__(kGemmWaves * 64, 3) void gate_up_kernel(
 
     auto run = [&]<int TILES>() {
         f32x16 acc[2][TILES];
-        staged_pair<kXTerms, TILES, NT>(xl, blockIdx.y, lane, wp, q0, q1, active, stage, acc);
+        staged_pair<kXTerms, TILES, NT>(xl, cell.item, lane, wp, q0, q1, active, stage, acc);
         if (!active)
             return;
         if (gridDim.z > 1) {
@@ -929,7 +944,7 @@ __global__ __launch_bounds__(kGemmWaves * 64, 3) void gate_up_kernel(
                     const int r = acc_row(t, v, h);
                     if (r < it.count) {
                         const size_t at = blockIdx.z * part_stride +
-                                          (size_t(blockIdx.y) * kItemRows + r) * inter + f;
+                                          (size_t(cell.item) * kItemRows + r) * inter + f;
                         part_g[at] = acc[0][t][v];
                         part_u[at] = acc[1][t][v];
                     }
@@ -938,7 +953,7 @@ __global__ __launch_bounds__(kGemmWaves * 64, 3) void gate_up_kernel(
         }
         // the LDS stage is free once staged_pair has returned (it ends on a barrier
         // after the last MFMA read); each wavefront takes its own 1 KB of it
-        store_h_tiles<TILES>(acc, fg, lane, blockIdx.y, hl, stage + wave * 1024);
+        store_h_tiles<TILES>(acc, fg, lane, cell.item, hl, stage + wave * 1024);
     };
     if (it.count <= kTileRows)
         run.template operator()<1>();
@@ -972,23 +987,24 @@ __global__ __launch_bounds__(256) void finalize_kernel(const float* __restrict__
             hl.scales + tau * hl.scale_stride, live);
 }
 
-// down: grid (groups of kGemmWaves row pairs of 64, items, K slices); wavefront w
-// multiplies the down rows 64 (kGemmWaves x + w) .. +63 (two groups of 32).  fp32 partial
+// down: grid (cells of item_cell: groups of row pairs of 64 x items, K slices); wavefront w
+// multiplies the down rows 64 (kDownWaves col + w) .. +63 (two groups of 32).  fp32 partial
 // sums of h x down per slice, indexed by the slot's position in the permutation.
 template <bool NT>
 __global__ __launch_bounds__(kDownWaves * 64) void down_kernel(
     const uint8_t* __restrict__ ha, size_t tiles, unsigned hidden, unsigned inter,
     unsigned experts, const uint8_t* __restrict__ down, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ items, const int32_t* __restrict__ item_count,
-    float* __restrict__ part_d, size_t part_stride) {
+    float* __restrict__ part_d, size_t part_stride, unsigned cols) {
     __shared__ __align__(16) uint8_t stage[2 * StageCopy<kHTerms, 2, kDownWaves>::chunk_bytes];
-    if (int(blockIdx.y) >= *item_count)
+    const ItemCell cell = item_cell(cols);
+    if (int(cell.item) >= *item_count)
         return;
-    const Item it = load_item(items, offsets, blockIdx.y);
+    const Item it = load_item(items, offsets, cell.item);
     const unsigned wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const unsigned i32 = lane % 32, h = lane / 32;
     const Packed shape = packed_shape(1, hidden, inter);  // per expert
-    const unsigned pair = blockIdx.x * kDownWaves + wave;
+    const unsigned pair = cell.col * kDownWaves + wave;
     const bool active = pair < shape.groups / 2;
     const unsigned g0 = (active ? pair : 0) * 2;
     unsigned q0, q1;
@@ -1001,7 +1017,7 @@ __global__ __launch_bounds__(kDownWaves * 64) void down_kernel(
     const Tiles hl = tile_layout(const_cast<uint8_t*>(ha), tiles, inter / 64, kHTerms);
     auto run = [&]<int TILES>() {
         f32x16 acc[2][TILES];
-        staged_pair<kHTerms, TILES, NT, 4, kDownWaves>(hl, blockIdx.y, lane, w, q0, q1, active,
+        staged_pair<kHTerms, TILES, NT, 4, kDownWaves>(hl, cell.item, lane, w, q0, q1, active,
                                                        stage, acc);
         if (!active)
             return;
@@ -1827,15 +1843,21 @@ int launch_layer(const uint16_t* x_bf16, const float* logits, size_t tokens, siz
     // it; C5: 0.75 -> 0.77 ms).
     const bool nt = slots <= experts * (kItemRows / 2);
     const size_t part_gu = tiles * kTileRows * inter;
-    const dim3 gu_grid(gate_up_columns(inter), items, ks.gate_up);
+    // (column, item) cells in one grid dimension, items padded to a multiple of 8
+    // (item_cell: an item's columns on one XCD)
+    const unsigned items8 = (items + 7) / 8 * 8;
+    const unsigned gu_cols = gate_up_columns(inter), d_cols = down_columns(hidden);
+    const dim3 gu_grid(gu_cols * items8, 1, ks.gate_up);
     if (nt)
         hipLaunchKernelGGL(gate_up_kernel<true>, gu_grid, dim3(kGemmWaves * 64), 0, st, s.xa,
                            unsigned(hidden), unsigned(inter), unsigned(experts), tiles, gate, up,
-                           s.offsets, s.items, s.item_count, s.ha, s.part_g, s.part_u, part_gu);
+                           s.offsets, s.items, s.item_count, s.ha, s.part_g, s.part_u, part_gu,
+                           gu_cols);
     else
         hipLaunchKernelGGL(gate_up_kernel<false>, gu_grid, dim3(kGemmWaves * 64), 0, st, s.xa,
                            unsigned(hidden), unsigned(inter), unsigned(experts), tiles, gate, up,
-                           s.offsets, s.items, s.item_count, s.ha, s.part_g, s.part_u, part_gu);
+                           s.offsets, s.items, s.item_count, s.ha, s.part_g, s.part_u, part_gu,
+                           gu_cols);
     KDQ_HIP(hipGetLastError());
     if (ks.gate_up > 1) {
         hipLaunchKernelGGL(finalize_kernel, dim3(unsigned((inter + 255) / 256), unsigned(slots)),
@@ -1844,15 +1866,15 @@ int launch_layer(const uint16_t* x_bf16, const float* logits, size_t tokens, siz
         KDQ_HIP(hipGetLastError());
     }
     const size_t stride = slots * hidden;
-    const dim3 d_grid(down_columns(hidden), items, ks.down);
+    const dim3 d_grid(d_cols * items8, 1, ks.down);
     if (nt)
         hipLaunchKernelGGL(down_kernel<true>, d_grid, dim3(kDownWaves * 64), 0, st, s.ha, tiles,
                            unsigned(hidden), unsigned(inter), unsigned(experts), down, s.offsets,
-                           s.items, s.item_count, s.part_d, stride);
+                           s.items, s.item_count, s.part_d, stride, d_cols);
     else
         hipLaunchKernelGGL(down_kernel<false>, d_grid, dim3(kDownWaves * 64), 0, st, s.ha, tiles,
                            unsigned(hidden), unsigned(inter), unsigned(experts), down, s.offsets,
-                           s.items, s.item_count, s.part_d, stride);
+                           s.items, s.item_count, s.part_d, stride, d_cols);
     KDQ_HIP(hipGetLastError());
     const size_t n = tokens * hidden / 4;
     const dim3 grid(unsigned((n + 255) / 256));
