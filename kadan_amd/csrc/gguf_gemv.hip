@@ -2462,15 +2462,34 @@ __global__ __launch_bounds__(W * 64) void moe_decode_up_kernel(const MfmaJobs a,
         if (column < route.experts) {
             const float4* row = reinterpret_cast<const float4*>(
                 route.router + size_t(column) * route.router_row_bytes);
+            const float4* xq = reinterpret_cast<const float4*>(route.x);
+            // every chunk's loads first (hidden <= 4096: at most 8 chunks of 8 values a
+            // lane), then the products in exact_gemv's order
+            constexpr int kChunks = 8;
+            float4 wv[kChunks][2], xv[kChunks][2];
+#pragma unroll
+            for (int c = 0; c < kChunks; ++c) {
+                const unsigned i = lane * 8 + c * 512;
+                if (i < a.in) {
+                    wv[c][0] = row[i / 4];
+                    wv[c][1] = row[i / 4 + 1];
+                    xv[c][0] = xq[i / 4];
+                    xv[c][1] = xq[i / 4 + 1];
+                }
+            }
             float sum = 0.f;
             bool finite = true;
-            for (unsigned i = lane * 8; i < a.in; i += 64 * 8) {
-                const float4 w0 = row[i / 4], w1 = row[i / 4 + 1];
-                const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int c = 0; c < kChunks; ++c) {
+                if (lane * 8 + c * 512 >= a.in)
+                    break;
+                const float w[8] = {wv[c][0].x, wv[c][0].y, wv[c][0].z, wv[c][0].w,
+                                    wv[c][1].x, wv[c][1].y, wv[c][1].z, wv[c][1].w};
+                const float xr[8] = {xv[c][0].x, xv[c][0].y, xv[c][0].z, xv[c][0].w,
+                                     xv[c][1].x, xv[c][1].y, xv[c][1].z, xv[c][1].w};
 #pragma unroll
                 for (int k = 0; k < 8; ++k)
                     finite = finite && isfinite(w[k]);
-                const float* xr = route.x + i;
 #pragma unroll
                 for (int k = 0; k < 8; ++k)
                     sum = fmaf(w[k], xr[k], sum);
@@ -2708,7 +2727,7 @@ int moe_decode_fused(const DecodeMoe& m, hipStream_t s, bool check_only) {
     const bool down_ok = (da_enc == KDQ_Q6_K || da_enc == KDQ_Q4_K) &&
                          (db_enc == KDQ_Q4_K || db_enc == KDQ_Q6_K);
     if (!up_ok || !down_ok || da.columns != db.columns || da.columns > m.counter_count ||
-        m.experts > 256 ||
+        m.experts > 256 || m.hidden > 4096 ||
         m.router.encoding != KDQ_F32 || m.router.in != m.hidden ||
         m.router.columns != m.experts || m.router.row_bytes % 16 ||
         reinterpret_cast<uintptr_t>(m.router.weights) % 16 ||
