@@ -383,3 +383,28 @@ def test_moe_gguf_fused_decode(device, oracle, encs, resident, H):
         assert np.abs(ws.cpu().numpy() - w).max() < 1e-6
         assert_close(y.cpu().numpy(), want, what=f"fused decode {encs} call {call}")
     assert int(status.item()) == 0
+
+
+@pytest.mark.parametrize("rows,seed", [(256, 2), (512, 3)])
+def test_moe_gguf_grouped_matches_fp16_model(device, oracle, rows, seed):
+    """The grouped-GEMM layer (experts and the shared expert on the prefill GEMMs) equals
+    its numeric design, tests/util.py moe_gguf_fp16_model: x and h rounded to fp16 once
+    after a per-row power-of-two scale, each weight as the GEMM's dequantisation forms it
+    in fp16, everything else float64.  The device differs from that model only in fp32
+    accumulation order (rel-L2 <= 1e-4), while the model itself differs from the exact
+    product by the fp16 roundings: at this seed max-abs 2.4e-2 of the RMS at outputs 30x
+    the RMS (weights 1.9e-2, x 7.8e-3, h 5.0e-3 of it), i.e. ~8e-4 of those outputs."""
+    import torch
+    from tests.util import moe_gguf_fp16_model, rel_l2, normalized_max_abs
+    H, E, K, F, S = 512, 16, 4, 256, 512
+    spec = make_layer(100 + seed * 7 + rows, H, E, K, F, S, MIXED)
+    x = synth.normal(200 + seed + rows, 1, rows * H).reshape(rows, H)
+    want, idx, w = oracle.moe_gguf_forward(spec, x)
+    from kadan_amd import ops
+    y, sel, _ = ops.moe_gguf(to_device(torch, device, spec), torch.from_numpy(x).to(device))
+    assert np.array_equal(sel.cpu().numpy(), idx)
+    model = moe_gguf_fp16_model(oracle, spec, x, idx, w.astype(np.float64))
+    y = y.cpu().numpy().astype(np.float64)
+    assert rel_l2(y, model) <= 1e-4, rel_l2(y, model)
+    assert normalized_max_abs(y, model) <= 1e-2, normalized_max_abs(y, model)
+    assert rel_l2(y, want) <= 1e-3

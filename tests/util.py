@@ -187,3 +187,85 @@ def near_tie_logits(seed, rows, experts, top_k):
             logits[r, second] = (np.full(2, w, np.float32).view(np.int32) +
                                  g.integers(0, 3, size=2).astype(np.int32)).view(np.float32)
     return logits
+
+
+# ---------------------------------------------------------------- fp16 operand model
+
+def _fp16(a):
+    return np.asarray(a, np.float64).astype(np.float16).astype(np.float64)
+
+
+def sigma_fp16(a):
+    """a rounded as the prefill GEMMs stage it: per row a power of two sigma with
+    max|a| / sigma in [2^14, 2^15), fp16(a / sigma) * sigma."""
+    a = np.asarray(a, np.float64)
+    m = np.abs(a).max(axis=-1, keepdims=True)
+    e = np.floor(np.log2(np.maximum(m, 1e-300))) + 1
+    s = 2.0 ** (e - 15)
+    return _fp16(a / s) * s
+
+
+def gemm_fp16_weights(oracle, encoding, rows, n_in):
+    """Rows as the prefill GEMM's dequantisation gives them (float64 of fp16 values):
+    Q4_K fma16(q, fp16(d sc), fp16(-dmin m)), Q6_K fp16((q - 32) * fp16(d sc)), Q8_0
+    fp16(q d) (d is fp16 already: exact); the codes and scales are read back from the
+    exactly decoded values and the block bytes."""
+    rows = np.ascontiguousarray(rows)
+    n = rows.shape[0]
+    exact = oracle.dequantize(encoding, rows, n_in).astype(np.float64)
+    if encoding == 8:  # Q8_0
+        return _fp16(exact)
+    nb = n_in // 256
+    if encoding == 14:  # Q6_K
+        blk = rows.reshape(n, nb, 210)
+        d = blk[..., 208:210].copy().view(np.float16).astype(np.float64)[..., 0]
+        sc = blk[..., 192:208].view(np.int8).astype(np.float64)
+        s = np.repeat(d[..., None] * sc, 16, axis=-1).reshape(n, n_in)
+        with np.errstate(invalid="ignore", divide="ignore"):
+            q = np.where(s != 0, np.round(exact / s), 0)
+        return _fp16(q * _fp16(s))
+    if encoding == 12:  # Q4_K
+        blk = rows.reshape(n, nb, 144)
+        d = blk[..., 0:2].copy().view(np.float16).astype(np.float64)[..., 0]
+        dmin = blk[..., 2:4].copy().view(np.float16).astype(np.float64)[..., 0]
+        sb = blk[..., 4:16].astype(np.int64)
+        sc = np.zeros((n, nb, 8))
+        m = np.zeros((n, nb, 8))
+        for k in range(8):
+            if k < 4:
+                sc[..., k], m[..., k] = sb[..., k] & 63, sb[..., k + 4] & 63
+            else:
+                sc[..., k] = (sb[..., k + 4] & 15) | ((sb[..., k - 4] >> 6) << 4)
+                m[..., k] = (sb[..., k + 4] >> 4) | ((sb[..., k] >> 6) << 4)
+        a = np.repeat(d[..., None] * sc, 32, axis=-1).reshape(n, n_in)
+        c = np.repeat(dmin[..., None] * m, 32, axis=-1).reshape(n, n_in)
+        with np.errstate(invalid="ignore", divide="ignore"):
+            q = np.where(a != 0, np.round((exact + c) / a), 0)
+        return _fp16(q * _fp16(a) + _fp16(-c))  # one rounding of the fp16 fma
+    raise ValueError(encoding)
+
+
+def moe_gguf_fp16_model(oracle, spec, x, idx, w):
+    """The GGUF MoE layer with every product on the prefill GEMMs' numeric model: x and h
+    staged by sigma_fp16, weights as gemm_fp16_weights, float64 accumulation and
+    element-wise work (the routing taken as given)."""
+    H, E, K, F, S = (spec[k] for k in ("hidden", "experts", "top_k", "ff", "shared_ff"))
+
+    def wt(name, n_in):
+        enc, arr = spec[name]
+        flat = arr.reshape(-1, arr.shape[-1])
+        return gemm_fp16_weights(oracle, enc, flat, n_in).reshape(*arr.shape[:-1], n_in)
+
+    silu = lambda v: v / (1.0 + np.exp(-v))
+    gate, up, down = wt("gate_exps", H), wt("up_exps", H), wt("down_exps", F)
+    xs = sigma_fp16(x)
+    y = np.zeros((x.shape[0], H))
+    for e in range(E):
+        t, i = np.nonzero(idx == e)
+        if t.size == 0:
+            continue
+        h = sigma_fp16(silu(xs[t] @ gate[e].T) * (xs[t] @ up[e].T))
+        y[t] += w[t, i][:, None] * (h @ down[e].T)
+    hs = sigma_fp16(silu(xs @ wt("gate_shexp", H).T) * (xs @ wt("up_shexp", H).T))
+    g = 1.0 / (1.0 + np.exp(-(x.astype(np.float64) @ spec["shared_gate"].astype(np.float64))))
+    return y + (hs @ wt("down_shexp", S).T) * g[:, None]
