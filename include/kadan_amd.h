@@ -206,7 +206,9 @@ int kdq_gemm_packed(int encoding, const void* packed, size_t n, size_t k, const 
  * reads the bytes of its 128 weight rows once for 128 activation rows.
  * k % kdq_gemm_rows_values(encoding) == 0 (256; BF16 64), k <= 65536; x and y 16-byte
  * aligned.  `status` (optional, zeroed by the caller): |= 1 for a non-finite decoded
- * weight, |= 2 for one past the fp16 range (then run kdq_gemv for these rows). */
+ * weight (for Q4_0, Q8_0, Q4_K, Q3_K, IQ4_NL and IQ4_XS: a non-finite block scale), |= 2
+ * for a weight past the fp16 range (for those encodings: a block scale that could take
+ * one past it, as kdq_gemm_packed checks) -- then run kdq_gemv for these rows. */
 size_t kdq_gemm_rows_values(int encoding);
 int kdq_gemm_rows(int encoding, const void* weights, size_t row_bytes, size_t n, size_t k,
                   const float* x, size_t m, float* y, unsigned* status, void* stream);

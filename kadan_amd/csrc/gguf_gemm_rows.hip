@@ -65,6 +65,199 @@ template <int ENC> struct RowsGroup {
 template <int ENC> constexpr size_t rows_lds = 2 * size_t(RN) * RowsGroup<ENC>::pitch +
                                                2 * size_t(RM) * RK * 2;
 
+// ----------------------------------------------------------- operand decode
+
+// A lane's 8 fp16 weights: fp16 of each value exactly as decode_run gives it (the same
+// fp32 operations in the same order), from the row's raw group bytes in LDS.  The
+// encodings below read whole code words and look values up four at a time; their range
+// flags are taken once per call from the block scale: `nonfinite` for a non-finite
+// scale, `wide` when the scale could take a weight past the fp16 range (the largest code
+// times |scale| above 65504, as the packed GEMM checks it); their fp16 scales convert in
+// hardware (exact for every finite half; a NaN stays a NaN).  Other encodings decode
+// value by value and check each value; BF16 checks its bits.
+struct RowFlags {
+    bool nonfinite = false, wide = false;
+    unsigned bf16_max = 0;  // BF16: the largest |bits| seen (two 16-bit lanes)
+};
+
+typedef unsigned u32x2_a8 __attribute__((ext_vector_type(2), aligned(8)));
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ unsigned lds_u16(const uint8_t* p) {
+    return *reinterpret_cast<const uint16_t*>(p);
+}
+// Eight bytes from a 2-byte aligned LDS address: three dword reads, realigned.
+__device__ __forceinline__ u32x2_a8 lds_bytes8_a2(const uint8_t* p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const unsigned* w = reinterpret_cast<const unsigned*>(a & ~uintptr_t(3));
+    const unsigned w0 = w[0], w1 = w[1], w2 = w[2];
+    if (a & 2u)
+        return u32x2_a8{__builtin_amdgcn_alignbyte(w1, w0, 2), __builtin_amdgcn_alignbyte(w2, w1, 2)};
+    return u32x2_a8{w0, w1};
+}
+// Four IQ4 code points (the formats' fixed grid, as iq4_value holds it) for the four
+// 4-bit indices in the bytes of `nib`, by two byte permutations and a select on bit 3.
+__device__ __forceinline__ unsigned iq4_bytes(unsigned nib) {
+    const unsigned sel = nib & 0x07070707u;
+    const unsigned lo = __builtin_amdgcn_perm(0xf6eaddcfu, 0xbfad9881u, sel);  // entries 0..7
+    const unsigned hi = __builtin_amdgcn_perm(0x71594535u, 0x26190d01u, sel);  // 8..15
+    const unsigned mask = ((nib >> 3) & 0x01010101u) * 0xffu;
+    return (hi & mask) | (lo & ~mask);
+}
+// step * (signed byte i of q, i = 0..3) into a[at..at+3]
+__device__ __forceinline__ void scale_signed(f16x8& a, int at, float step, unsigned q) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        a[at + i] = _Float16(mul_rn(step, float(int8_t(q >> (8 * i)))));
+}
+
+template <int ENC> struct RowsDecode {
+    // every other encoding: decode_run, each value checked
+    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f) {
+        using F = Format<ENC>;
+        float v[8];
+        decode_run<ENC>(row + (kk / F::values) * F::bytes, kk % F::values, v);
+        f16x8 a;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            f.nonfinite = f.nonfinite || !isfinite(v[i]);
+            f.wide = f.wide || fabsf(v[i]) > 65504.f;
+            a[i] = _Float16(v[i]);
+        }
+        return a;
+    }
+};
+
+template <> struct RowsDecode<KDQ_IQ4_XS> {  // the group is one 136-byte super-block
+    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f) {
+        const unsigned g = kk / 32, at = kk % 32;
+        const float d = half_hw(lds_u16(row));
+        const unsigned high = lds_u16(row + 2);
+        const int scale = int(((unsigned(row[4 + g / 2]) >> (4 * (g % 2))) & 15u) |
+                              (((high >> (2 * g)) & 3u) << 4)) - 32;
+        const float step = mul_rn(d, float(scale));
+        f.nonfinite = f.nonfinite || !isfinite(step);
+        f.wide = f.wide || 127.f * fabsf(step) > 65504.f;
+        const u32x2_a8 b = *reinterpret_cast<const u32x2_a8*>(row + 8 + 16 * g + at % 16);
+        const unsigned sh = at < 16 ? 0u : 4u;
+        f16x8 a;
+        scale_signed(a, 0, step, iq4_bytes((b.x >> sh) & 0x0f0f0f0fu));
+        scale_signed(a, 4, step, iq4_bytes((b.y >> sh) & 0x0f0f0f0fu));
+        return a;
+    }
+};
+
+template <> struct RowsDecode<KDQ_IQ4_NL> {  // eight 18-byte blocks of 32 values
+    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f) {
+        const uint8_t* block = row + (kk / 32) * 18;
+        const unsigned at = kk % 32;
+        const float d = half_hw(lds_u16(block));
+        f.nonfinite = f.nonfinite || !isfinite(d);
+        f.wide = f.wide || 127.f * fabsf(d) > 65504.f;
+        const u32x2_a8 b = lds_bytes8_a2(block + 2 + at % 16);
+        const unsigned sh = at < 16 ? 0u : 4u;
+        f16x8 a;
+        scale_signed(a, 0, d, iq4_bytes((b.x >> sh) & 0x0f0f0f0fu));
+        scale_signed(a, 4, d, iq4_bytes((b.y >> sh) & 0x0f0f0f0fu));
+        return a;
+    }
+};
+
+template <> struct RowsDecode<KDQ_Q4_0> {  // eight 18-byte blocks: (q - 8) * d
+    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f) {
+        const uint8_t* block = row + (kk / 32) * 18;
+        const unsigned at = kk % 32;
+        const float d = half_hw(lds_u16(block));
+        f.nonfinite = f.nonfinite || !isfinite(d);
+        f.wide = f.wide || 8.f * fabsf(d) > 65504.f;
+        const u32x2_a8 b = lds_bytes8_a2(block + 2 + at % 16);
+        const unsigned sh = at < 16 ? 0u : 4u;
+        const unsigned n[2] = {(b.x >> sh) & 0x0f0f0f0fu, (b.y >> sh) & 0x0f0f0f0fu};
+        f16x8 a;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            a[i] = _Float16(mul_rn(float(int((n[i / 4] >> (8 * (i % 4))) & 255u) - 8), d));
+        return a;
+    }
+};
+
+template <> struct RowsDecode<KDQ_Q8_0> {  // eight 34-byte blocks: q * d
+    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f) {
+        const uint8_t* block = row + (kk / 32) * 34;
+        const float d = half_hw(lds_u16(block));
+        f.nonfinite = f.nonfinite || !isfinite(d);
+        f.wide = f.wide || 128.f * fabsf(d) > 65504.f;
+        const u32x2_a8 b = lds_bytes8_a2(block + 2 + kk % 32);
+        f16x8 a;
+        scale_signed(a, 0, d, b.x);
+        scale_signed(a, 4, d, b.y);
+        return a;
+    }
+};
+
+template <> struct RowsDecode<KDQ_Q4_K> {  // one 144-byte super-block
+    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f) {
+        const float d = half_hw(lds_u16(row)), dmin = half_hw(lds_u16(row + 2));
+        const unsigned g = kk / 32;
+        unsigned sc, m;
+        q4k_scale_min(row + 4, g, sc, m);
+        const float scaled = mul_rn(d, float(sc));
+        const float offset = mul_rn(dmin, float(m));
+        f.nonfinite = f.nonfinite || !isfinite(scaled) || !isfinite(offset);
+        f.wide = f.wide || 15.f * fabsf(scaled) + fabsf(offset) > 65504.f;
+        const u32x2_a8 b = *reinterpret_cast<const u32x2_a8*>(row + 16 + (kk / 64) * 32 + kk % 32);
+        const unsigned sh = (g & 1u) ? 4u : 0u;
+        const unsigned n[2] = {(b.x >> sh) & 0x0f0f0f0fu, (b.y >> sh) & 0x0f0f0f0fu};
+        f16x8 a;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            a[i] = _Float16(sub_rn(mul_rn(scaled, float((n[i / 4] >> (8 * (i % 4))) & 255u)),
+                                   offset));
+        return a;
+    }
+};
+
+template <> struct RowsDecode<KDQ_Q3_K> {  // one 110-byte super-block
+    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f) {
+        const float d = half_hw(lds_u16(row + 108));
+        const unsigned g = kk / 16;
+        const uint8_t* scales = row + 96;
+        const unsigned low = g < 8 ? scales[g] & 15u : unsigned(scales[g - 8]) >> 4;
+        const unsigned high = (unsigned(scales[8 + g % 4]) >> (2 * (g / 4))) & 3u;
+        const float step = mul_rn(d, float(int(low | (high << 4)) - 32));
+        f.nonfinite = f.nonfinite || !isfinite(step);
+        f.wide = f.wide || 4.f * fabsf(step) > 65504.f;
+        const unsigned shift = 2 * ((kk % 128) / 32), mask_bit = kk / 32;
+        const u32x2_a8 c = *reinterpret_cast<const u32x2_a8*>(row + 32 + (kk / 128) * 32 + kk % 32);
+        const u32x2_a8 h = *reinterpret_cast<const u32x2_a8*>(row + kk % 32);
+        // code = 2-bit field - 4 unless the high-mask bit is set: (field | bit << 2) - 4
+        const unsigned q[2] = {((c.x >> shift) & 0x03030303u) | (((h.x >> mask_bit) & 0x01010101u) << 2),
+                               ((c.y >> shift) & 0x03030303u) | (((h.y >> mask_bit) & 0x01010101u) << 2)};
+        f16x8 a;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            a[i] = _Float16(mul_rn(step, float(int((q[i / 4] >> (8 * (i % 4))) & 255u) - 4)));
+        return a;
+    }
+};
+
+template <> struct RowsDecode<KDQ_BF16> {  // 64 values of 2 bytes: exact, bits checked
+    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(row + 2 * kk);
+        f16x8 a;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const unsigned m = w[i] & 0x7fff7fffu;  // |bits| of the two values
+            f.bf16_max = __builtin_bit_cast(
+                unsigned, __builtin_elementwise_max(__builtin_bit_cast(us2, f.bf16_max),
+                                                    __builtin_bit_cast(us2, m)));
+            a[2 * i] = _Float16(__uint_as_float(w[i] << 16));
+            a[2 * i + 1] = _Float16(__uint_as_float(w[i] & 0xffff0000u));
+        }
+        return a;
+    }
+};
+
 __device__ __forceinline__ float row_max(float v) {
     for (int s = 32; s >= 1; s /= 2)
         v = fmaxf(v, __shfl_xor(v, s, 64));
@@ -223,7 +416,7 @@ __global__ __launch_bounds__(kThreads, 2) void rows_gemm_kernel(
 #pragma unroll
     for (int b = 0; b < 4; ++b)
         acc[b] = f32x16{};
-    bool nonfinite = false, wide = false;
+    RowFlags flags;
 
     // Software pipeline, one barrier per step.  The top of step s refills the LDS buffers
     // that step s - 1 finished reading: activations of step s + 1 (from a register ring,
@@ -272,15 +465,7 @@ __global__ __launch_bounds__(kThreads, 2) void rows_gemm_kernel(
         for (int sub = 0; sub < 2; ++sub) {
             // this lane's 8 weights: values 16 sub + 8 h .. +7 of the step
             const unsigned kk = within * RK + 16 * sub + 8 * h;
-            float v[8];
-            decode_run<ENC>(row + (kk / F::values) * F::bytes, kk % F::values, v);
-            f16x8 a;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                nonfinite = nonfinite || !isfinite(v[i]);
-                wide = wide || fabsf(v[i]) > 65504.f;
-                a[i] = _Float16(v[i]);
-            }
+            const f16x8 a = RowsDecode<ENC>::run(row, kk, flags);
             const unsigned c = 2 * sub + h;  // 16-byte chunk of the token's 64 bytes
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
@@ -328,7 +513,12 @@ __global__ __launch_bounds__(kThreads, 2) void rows_gemm_kernel(
         }
     }
     if (status) {
-        const unsigned f = (__any(nonfinite) ? 1u : 0u) | (__any(wide) ? 2u : 0u);
+        if constexpr (ENC == KDQ_BF16) {  // |bits| 0x7f80 and up: inf / NaN; 0x4780 (65536) up
+            const unsigned mx = max(flags.bf16_max & 0xffffu, flags.bf16_max >> 16);
+            flags.nonfinite = mx >= 0x7f80u;
+            flags.wide = mx >= 0x4780u && mx < 0x7f80u;
+        }
+        const unsigned f = (__any(flags.nonfinite) ? 1u : 0u) | (__any(flags.wide) ? 2u : 0u);
         if (f && lane == 0)
             atomicOr(status, f);
     }
