@@ -62,8 +62,42 @@ template <int ENC> struct RowsGroup {
     static constexpr int per_thread = (chunks + kThreads - 1) / kThreads;
 };
 
+// The lattice encodings' grids as LDS tables: per grid entry its level magnitudes as
+// bytes (IQ3_XXS 256 and IQ3_S 512 entries of 4, IQ2_S 1024 entries of 8).
+template <int ENC> constexpr unsigned lattice_rows_entries =
+    ENC == KDQ_IQ3_XXS ? 256 : ENC == KDQ_IQ3_S ? 512 : ENC == KDQ_IQ2_S ? 1024 : 0;
+template <int ENC> constexpr unsigned lattice_rows_width = ENC == KDQ_IQ2_S ? 8 : 4;
+template <int ENC> constexpr size_t lattice_rows_bytes =
+    size_t(lattice_rows_entries<ENC>) * lattice_rows_width<ENC>;
+
 template <int ENC> constexpr size_t rows_lds = 2 * size_t(RN) * RowsGroup<ENC>::pitch +
-                                               2 * size_t(RM) * RK * 2;
+                                               2 * size_t(RM) * RK * 2 + lattice_rows_bytes<ENC>;
+
+// Fills the LDS grid table (every thread of the workgroup; a barrier follows before use):
+// entry i's level indices (3 or 2 bits each, as iq_grids.inc encodes them) as the levels
+// themselves, kIq3xxsGridLevels / kIq3sGridLevels / kIq2sGridLevels, one byte each.
+template <int ENC> __device__ __forceinline__ void lattice_rows_table(uint8_t* table) {
+    constexpr unsigned E = lattice_rows_entries<ENC>, Wd = lattice_rows_width<ENC>;
+    constexpr unsigned bits = ENC == KDQ_IQ2_S ? 2 : 3;
+    for (unsigned i = threadIdx.x; i < E; i += kThreads) {
+        const unsigned entry = ENC == KDQ_IQ3_XXS ? kIq3xxsGrid[i]
+                               : ENC == KDQ_IQ3_S ? kIq3sGrid[i]
+                                                  : kIq2sGrid[i];
+        unsigned w[2] = {0u, 0u};
+#pragma unroll
+        for (unsigned b = 0; b < Wd; ++b) {
+            const unsigned li = (entry >> (bits * b)) & ((1u << bits) - 1);
+            const unsigned level = ENC == KDQ_IQ3_XXS ? kIq3xxsGridLevels[li]
+                                   : ENC == KDQ_IQ3_S ? kIq3sGridLevels[li]
+                                                      : kIq2sGridLevels[li];
+            w[b / 4] |= level << (8 * (b % 4));
+        }
+        if constexpr (Wd == 8)
+            reinterpret_cast<uint2*>(table)[i] = make_uint2(w[0], w[1]);
+        else
+            reinterpret_cast<unsigned*>(table)[i] = w[0];
+    }
+}
 
 // ----------------------------------------------------------- operand decode
 
@@ -113,7 +147,8 @@ __device__ __forceinline__ void scale_signed(f16x8& a, int at, float step, unsig
 
 template <int ENC> struct RowsDecode {
     // every other encoding: decode_run, each value checked
-    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f) {
+    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f,
+                                                const uint8_t*) {
         using F = Format<ENC>;
         float v[8];
         decode_run<ENC>(row + (kk / F::values) * F::bytes, kk % F::values, v);
@@ -129,7 +164,8 @@ template <int ENC> struct RowsDecode {
 };
 
 template <> struct RowsDecode<KDQ_IQ4_XS> {  // the group is one 136-byte super-block
-    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f) {
+    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f,
+                                                const uint8_t*) {
         const unsigned g = kk / 32, at = kk % 32;
         const float d = half_hw(lds_u16(row));
         const unsigned high = lds_u16(row + 2);
@@ -148,7 +184,8 @@ template <> struct RowsDecode<KDQ_IQ4_XS> {  // the group is one 136-byte super-
 };
 
 template <> struct RowsDecode<KDQ_IQ4_NL> {  // eight 18-byte blocks of 32 values
-    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f) {
+    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f,
+                                                const uint8_t*) {
         const uint8_t* block = row + (kk / 32) * 18;
         const unsigned at = kk % 32;
         const float d = half_hw(lds_u16(block));
@@ -164,7 +201,8 @@ template <> struct RowsDecode<KDQ_IQ4_NL> {  // eight 18-byte blocks of 32 value
 };
 
 template <> struct RowsDecode<KDQ_Q4_0> {  // eight 18-byte blocks: (q - 8) * d
-    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f) {
+    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f,
+                                                const uint8_t*) {
         const uint8_t* block = row + (kk / 32) * 18;
         const unsigned at = kk % 32;
         const float d = half_hw(lds_u16(block));
@@ -182,7 +220,8 @@ template <> struct RowsDecode<KDQ_Q4_0> {  // eight 18-byte blocks: (q - 8) * d
 };
 
 template <> struct RowsDecode<KDQ_Q8_0> {  // eight 34-byte blocks: q * d
-    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f) {
+    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f,
+                                                const uint8_t*) {
         const uint8_t* block = row + (kk / 32) * 34;
         const float d = half_hw(lds_u16(block));
         f.nonfinite = f.nonfinite || !isfinite(d);
@@ -196,7 +235,8 @@ template <> struct RowsDecode<KDQ_Q8_0> {  // eight 34-byte blocks: q * d
 };
 
 template <> struct RowsDecode<KDQ_Q4_K> {  // one 144-byte super-block
-    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f) {
+    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f,
+                                                const uint8_t*) {
         const float d = half_hw(lds_u16(row)), dmin = half_hw(lds_u16(row + 2));
         const unsigned g = kk / 32;
         unsigned sc, m;
@@ -218,7 +258,8 @@ template <> struct RowsDecode<KDQ_Q4_K> {  // one 144-byte super-block
 };
 
 template <> struct RowsDecode<KDQ_Q3_K> {  // one 110-byte super-block
-    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f) {
+    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f,
+                                                const uint8_t*) {
         const float d = half_hw(lds_u16(row + 108));
         const unsigned g = kk / 16;
         const uint8_t* scales = row + 96;
@@ -241,8 +282,80 @@ template <> struct RowsDecode<KDQ_Q3_K> {  // one 110-byte super-block
     }
 };
 
+// +-(scale * level byte i of m), sign bit i of `signs` (decode_run's signed_level: the
+// product, then an exact sign change), into a[at..at+3]
+__device__ __forceinline__ void signed_levels(f16x8& a, int at, float scale, unsigned m,
+                                              unsigned signs) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float v = mul_rn(scale, float((m >> (8 * i)) & 255u));
+        a[at + i] = _Float16((signs >> i) & 1u ? -v : v);
+    }
+}
+
+template <> struct RowsDecode<KDQ_IQ3_XXS> {  // one 98-byte super-block
+    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f,
+                                                const uint8_t* table) {
+        const unsigned g = kk / 32, pair = (kk % 32) / 8;
+        const float d = half_hw(lds_u16(row));
+        const unsigned aux = lds_u16(row + 66 + 4 * g) | (lds_u16(row + 68 + 4 * g) << 16);
+        const float scale = mul_rn(mul_rn(d, 0.5f + float(aux >> 28)), 0.5f);
+        f.nonfinite = f.nonfinite || !isfinite(scale);
+        f.wide = f.wide || 62.f * fabsf(scale) > 65504.f;
+        unsigned signs = (aux >> (7 * pair)) & 127u;
+        signs |= (__builtin_popcount(signs) & 1u) << 7;
+        const unsigned idx = lds_u16(row + 2 + 8 * g + 2 * pair);
+        const unsigned* t = reinterpret_cast<const unsigned*>(table);
+        f16x8 a;
+        signed_levels(a, 0, scale, t[idx & 255u], signs);
+        signed_levels(a, 4, scale, t[idx >> 8], signs >> 4);
+        return a;
+    }
+};
+
+template <> struct RowsDecode<KDQ_IQ3_S> {  // one 110-byte super-block
+    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f,
+                                                const uint8_t* table) {
+        const unsigned g = kk / 32, q = (kk % 32) / 8;
+        const float d = half_hw(lds_u16(row));
+        const unsigned sb = row[106 + g / 2];
+        const unsigned nibble = g % 2 ? sb >> 4 : sb & 15u;
+        const float scale = mul_rn(d, float(int(1 + 2 * nibble)));
+        f.nonfinite = f.nonfinite || !isfinite(scale);
+        f.wide = f.wide || 15.f * fabsf(scale) > 65504.f;
+        const unsigned high = row[66 + g], signs = row[74 + 4 * g + q];
+        const unsigned idx = lds_u16(row + 2 + 8 * g + 2 * q);
+        const unsigned* t = reinterpret_cast<const unsigned*>(table);
+        f16x8 a;
+        signed_levels(a, 0, scale, t[(idx & 255u) | ((high << (8 - 2 * q)) & 256u)], signs);
+        signed_levels(a, 4, scale, t[(idx >> 8) | ((high << (7 - 2 * q)) & 256u)], signs >> 4);
+        return a;
+    }
+};
+
+template <> struct RowsDecode<KDQ_IQ2_S> {  // one 82-byte super-block
+    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f,
+                                                const uint8_t* table) {
+        const unsigned g = kk / 32, q = (kk % 32) / 8;
+        const float d = half_hw(lds_u16(row));
+        const unsigned sb = row[74 + g];
+        const unsigned nibble = q < 2 ? sb & 15u : sb >> 4;
+        const float scale = mul_rn(mul_rn(d, 0.5f + float(nibble)), 0.25f);
+        f.nonfinite = f.nonfinite || !isfinite(scale);
+        f.wide = f.wide || 43.f * fabsf(scale) > 65504.f;
+        const unsigned index = row[2 + 4 * g + q] | ((unsigned(row[66 + g]) << (8 - 2 * q)) & 0x300u);
+        const uint2 m = reinterpret_cast<const uint2*>(table)[index];
+        const unsigned signs = row[34 + 4 * g + q];
+        f16x8 a;
+        signed_levels(a, 0, scale, m.x, signs);
+        signed_levels(a, 4, scale, m.y, signs >> 4);
+        return a;
+    }
+};
+
 template <> struct RowsDecode<KDQ_BF16> {  // 64 values of 2 bytes: exact, bits checked
-    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f) {
+    static __device__ __forceinline__ f16x8 run(const uint8_t* row, unsigned kk, RowFlags& f,
+                                                const uint8_t*) {
         const u32x4 w = *reinterpret_cast<const u32x4*>(row + 2 * kk);
         f16x8 a;
 #pragma unroll
@@ -337,10 +450,12 @@ __global__ __launch_bounds__(kThreads, 2) void rows_gemm_kernel(
     unsigned m, unsigned n, unsigned k, unsigned slices, unsigned per, float* __restrict__ y,
     float* __restrict__ part, unsigned* __restrict__ status) {
     using G = RowsGroup<ENC>;
-    using F = Format<ENC>;
     extern __shared__ __align__(16) uint8_t lds[];
     uint8_t* raw = lds;                        // [2][RN][pitch]
     uint8_t* xt = lds + 2 * RN * G::pitch;     // [2][RM][RK] fp16, 16-byte chunks swizzled
+    uint8_t* table = xt + 2 * RM * RK * 2;     // lattice encodings: the grid's levels
+    if constexpr (lattice_rows_entries<ENC> > 0)
+        lattice_rows_table<ENC>(table);  // before the prologue's barrier
 
     const unsigned m_tiles = (m + RM - 1) / RM, n_tiles = (n + RN - 1) / RN;
     const unsigned id = blockIdx.x, xcd = id % 8, local = id / 8;
@@ -465,7 +580,7 @@ __global__ __launch_bounds__(kThreads, 2) void rows_gemm_kernel(
         for (int sub = 0; sub < 2; ++sub) {
             // this lane's 8 weights: values 16 sub + 8 h .. +7 of the step
             const unsigned kk = within * RK + 16 * sub + 8 * h;
-            const f16x8 a = RowsDecode<ENC>::run(row, kk, flags);
+            const f16x8 a = RowsDecode<ENC>::run(row, kk, flags, table);
             const unsigned c = 2 * sub + h;  // 16-byte chunk of the token's 64 bytes
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
