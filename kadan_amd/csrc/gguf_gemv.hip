@@ -2367,11 +2367,23 @@ namespace {
 
 // The router, the routing and the shared gate the up launch computes, and the counters
 // of the down launch's row blocks, which it clears.
+// The fused decode's device-wide state (one copy per GPU, zero at load): the router
+// workgroups' completion count (the last one resets it) and, per slot, the published
+// selection: (epoch << 8) | expert of the call that routed last.  Calls that overlap on
+// one GPU race on them (and on the workspace), as on the rest of the library's scratch.
+// Kernels take its address as an argument (DecodeRoute::state), not through the symbol.
+struct DecodeState {
+    unsigned router_arrived;
+    unsigned routed_slot[kMaxFused];
+};
+__device__ DecodeState g_decode_state;
+
 struct DecodeRoute {
     const uint8_t* router;  // F32 rows [experts][row_bytes]
     size_t router_row_bytes;
     unsigned router_workgroups;  // the grid's first workgroups: one router row per wavefront
     unsigned epoch;              // this call's number on this device (never 0)
+    DecodeState* state;          // this device's g_decode_state
     float* logits;
     unsigned experts, top_k;
     int32_t* idx;
@@ -2426,25 +2438,15 @@ __device__ __forceinline__ void shared_gate(const float* __restrict__ v,
     }
 }
 
-// Workgroups [0, a.columns * a.count) run the experts' paired gate / up (job step = slot,
-// the slot's expert from this workgroup's own routing of the token), the rest the shared
-// expert's paired gate / up.  Wavefront 0 routes (the whole softmax and top-k of the one
-// token, as route_kernel does it) while the others wait; workgroup 0 also stores the
-// selection and clears the down launch's counters.
-// The fused decode's device-wide state (one copy per GPU, zero at load): the router
-// workgroups' completion count (the last one resets it) and, per slot, the published
-// selection: (epoch << 8) | expert of the call that routed last.  Calls that overlap on
-// one GPU race on them (and on the workspace), as on the rest of the library's scratch.
-__device__ unsigned g_router_arrived;
-__device__ unsigned g_routed_slot[kMaxFused];
 // Bounded wait for the routing: about 2^20 sleeps of 64 clocks (tens of ms); past it
 // the workgroup goes on with expert 0 and sets status bit 3 (a routing that never came).
 constexpr unsigned kRouteSpinLimit = 1u << 20;
 
 // Workgroups [0, router_workgroups): the router GEMV, one F32 row per wavefront in
 // exact_gemv<KDQ_F32, 1>'s arithmetic (the same logits as the staged path), stored at
-// device scope; the last of them to finish routes the token (route_select over those
-// logits, read at device scope), publishes the selection and then this call's epoch.
+// device scope; the last of them to finish routes the token (route_select_wg, the whole
+// workgroup over those logits, read at device scope) and publishes each slot's expert
+// with this call's epoch.
 // Then the experts' paired gate / up workgroups (job step = slot): their activation
 // loads go out first, then thread 0 waits for the epoch and reads its slot's expert.
 // Then the shared expert's paired gate / up; its first workgroup also takes the gate
@@ -2463,36 +2465,50 @@ __global__ __launch_bounds__(W * 64) void moe_decode_up_kernel(const MfmaJobs a,
             const float4* row = reinterpret_cast<const float4*>(
                 route.router + size_t(column) * route.router_row_bytes);
             const float4* xq = reinterpret_cast<const float4*>(route.x);
-            // every chunk's loads first (hidden <= 4096: at most 8 chunks of 8 values a
-            // lane), then the products in exact_gemv's order
-            constexpr int kChunks = 8;
-            float4 wv[kChunks][2], xv[kChunks][2];
-#pragma unroll
-            for (int c = 0; c < kChunks; ++c) {
-                const unsigned i = lane * 8 + c * 512;
-                if (i < a.in) {
-                    wv[c][0] = row[i / 4];
-                    wv[c][1] = row[i / 4 + 1];
-                    xv[c][0] = xq[i / 4];
-                    xv[c][1] = xq[i / 4 + 1];
-                }
-            }
+            // chunks of 8 values a lane (hidden <= 4096: at most 8), four at a time: the
+            // four chunks' loads all issued (at clamped, in-bounds addresses), then the
+            // products of the lane's valid ones in exact_gemv's order
+            constexpr int kChunks = 8, kBatch = 4;
             float sum = 0.f;
             bool finite = true;
 #pragma unroll
-            for (int c = 0; c < kChunks; ++c) {
-                if (lane * 8 + c * 512 >= a.in)
-                    break;
-                const float w[8] = {wv[c][0].x, wv[c][0].y, wv[c][0].z, wv[c][0].w,
-                                    wv[c][1].x, wv[c][1].y, wv[c][1].z, wv[c][1].w};
-                const float xr[8] = {xv[c][0].x, xv[c][0].y, xv[c][0].z, xv[c][0].w,
-                                     xv[c][1].x, xv[c][1].y, xv[c][1].z, xv[c][1].w};
+            for (int c0 = 0; c0 < kChunks; c0 += kBatch) {
+                if (c0 * 512 >= a.in)
+                    break;  // uniform: lane 0 has the lowest index
+                u32x4 wv[kBatch][2], xv[kBatch][2];
 #pragma unroll
-                for (int k = 0; k < 8; ++k)
-                    finite = finite && isfinite(w[k]);
+                for (int c = 0; c < kBatch; ++c) {
+                    const unsigned i = min(lane * 8 + (c0 + c) * 512, a.in - 8);
+                    wv[c][0] = reinterpret_cast<const u32x4*>(row)[i / 4];
+                    wv[c][1] = reinterpret_cast<const u32x4*>(row)[i / 4 + 1];
+                    xv[c][0] = reinterpret_cast<const u32x4*>(xq)[i / 4];
+                    xv[c][1] = reinterpret_cast<const u32x4*>(xq)[i / 4 + 1];
+                }
+                // every value here (the compiler would otherwise sink each chunk's loads
+                // into its guarded products: one memory round trip per chunk)
 #pragma unroll
-                for (int k = 0; k < 8; ++k)
-                    sum = fmaf(w[k], xr[k], sum);
+                for (int c = 0; c < kBatch; ++c)
+                    asm volatile("" : "+v"(wv[c][0]), "+v"(wv[c][1]), "+v"(xv[c][0]),
+                                 "+v"(xv[c][1]));
+#pragma unroll
+                for (int c = 0; c < kBatch; ++c) {
+                    if (lane * 8 + (c0 + c) * 512 >= a.in)
+                        break;
+                    float w[8], xr[8];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        w[k] = __uint_as_float(wv[c][0][k]);
+                        w[4 + k] = __uint_as_float(wv[c][1][k]);
+                        xr[k] = __uint_as_float(xv[c][0][k]);
+                        xr[4 + k] = __uint_as_float(xv[c][1][k]);
+                    }
+#pragma unroll
+                    for (int k = 0; k < 8; ++k)
+                        finite = finite && isfinite(w[k]);
+#pragma unroll
+                    for (int k = 0; k < 8; ++k)
+                        sum = fmaf(w[k], xr[k], sum);
+                }
             }
             if (route.status && __any(!finite) && lane == 0)
                 atomicOr(route.status, 1u);
@@ -2504,30 +2520,30 @@ __global__ __launch_bounds__(W * 64) void moe_decode_up_kernel(const MfmaJobs a,
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the logits stored first
         __syncthreads();
         if (threadIdx.x == 0)
-            arrived = atomicAdd(&g_router_arrived, 1u);
+            arrived = atomicAdd(&route.state->router_arrived, 1u);
         __syncthreads();
         if (arrived != route.router_workgroups - 1)
             return;
-        if (wave == 0) {
-            int e;
-            float we;
-            route_select<true>(route.logits, 0, route.experts, route.top_k, lane, e, we);
-            if (lane < route.top_k) {
-                __hip_atomic_store(&route.idx[lane], e, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(&route.w[lane], we, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-            }
-            for (unsigned i = lane; i < route.counter_count; i += 64)
-                route.counters[i] = 0u;
-            if (lane < unsigned(kMaxFused))  // each slot's word: this call's epoch and its
-                                              // expert (0 for slots past top_k)
-                __hip_atomic_store(&g_routed_slot[lane],
-                                   lane < route.top_k ? (route.epoch << 8) | unsigned(e) : 0u,
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (lane == 0)
-                g_router_arrived = 0u;
+        // the whole workgroup routes (its LDS is the GEMV's, unused here)
+        extern __shared__ __align__(16) uint8_t lds[];
+        int e = 0;
+        float we = 0.f;
+        route_select_wg<W, kMaxFused, true>(route.logits, route.experts, route.top_k,
+                                            *reinterpret_cast<RouteScratch*>(lds), e, we);
+        const unsigned t = threadIdx.x;
+        if (t < route.top_k) {
+            __hip_atomic_store(&route.idx[t], e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&route.w[t], we, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+        if (t < unsigned(kMaxFused))  // each slot's word: this call's epoch and its expert
+                                       // (0 for slots past top_k)
+            __hip_atomic_store(&route.state->routed_slot[t],
+                               t < route.top_k ? (route.epoch << 8) | unsigned(e) : 0u,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (unsigned i = t; i < route.counter_count; i += W * 64)
+            route.counters[i] = 0u;
+        if (t == 0)
+            route.state->router_arrived = 0u;
         return;
     }
     const unsigned a_workgroups = a.columns * a.count;
@@ -2539,7 +2555,8 @@ __global__ __launch_bounds__(W * 64) void moe_decode_up_kernel(const MfmaJobs a,
         auto late = [&]() -> int {
             if (threadIdx.x == 0) {
                 unsigned spins = 0, word;
-                while (((word = __hip_atomic_load(&g_routed_slot[slot], __ATOMIC_RELAXED,
+                const unsigned* published = &route.state->routed_slot[slot];
+                while (((word = __hip_atomic_load(published, __ATOMIC_RELAXED,
                                                   __HIP_MEMORY_SCOPE_AGENT)) >> 8) !=
                        route.epoch) {
                     if (++spins == kRouteSpinLimit) {
@@ -2617,10 +2634,21 @@ __global__ __launch_bounds__(W * 64) void moe_decode_down_kernel(const MfmaJobs 
         return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
     for (unsigned r = r0 + threadIdx.x; r < r1; r += W * 64) {
+        // the row's top_k + 1 loads all issued (clamped to the last slot), then the sum
+        float v[kMaxFused + 1];
+#pragma unroll
+        for (int i = 0; i < kMaxFused; ++i)
+            v[i] = coherent(c.down + size_t(min(unsigned(i), c.top_k - 1)) * c.hidden + r);
+        v[kMaxFused] = coherent(c.shared + r);
+#pragma unroll
+        for (int i = 0; i <= kMaxFused; ++i)
+            asm volatile("" : "+v"(v[i]));
         float sum = 0.f;
-        for (unsigned i = 0; i < c.top_k; ++i)
-            sum += coherent(c.down + size_t(i) * c.hidden + r) * c.w[i];
-        c.y[r] = sum + coherent(c.shared + r) * gate;
+#pragma unroll
+        for (int i = 0; i < kMaxFused; ++i)
+            if (unsigned(i) < c.top_k)
+                sum += v[i] * c.w[i];
+        c.y[r] = sum + v[kMaxFused] * gate;
     }
     if (threadIdx.x == 0)
         c.counters[block] = 0u;  // ready for the next layer call
@@ -2715,7 +2743,9 @@ int moe_decode_fused(const DecodeMoe& m, hipStream_t s, bool check_only) {
     const unsigned rows = (std::max(da.rows_per_wg, db.rows_per_wg) + 7) & ~7u;
     number_workgroups(da, rows);
     number_workgroups(db, rows);
-    const size_t up_lds = std::max(mfma_lds(1, ua.in, 2), mfma_lds(1, ub.in, 2));
+    // (the routing workgroup's scratch lies in the same dynamic LDS)
+    const size_t up_lds = std::max({mfma_lds(1, ua.in, 2), mfma_lds(1, ub.in, 2),
+                                    sizeof(RouteScratch)});
     const size_t down_lds = std::max(mfma_lds(1, da.in, 1), mfma_lds(1, db.in, 1));
     if (std::max(up_lds, down_lds) > size_t(kDecodeDynamicLds))
         return KDQ_ERR_UNSUPPORTED;
@@ -2733,21 +2763,33 @@ int moe_decode_fused(const DecodeMoe& m, hipStream_t s, bool check_only) {
         reinterpret_cast<uintptr_t>(m.router.weights) % 16 ||
         reinterpret_cast<uintptr_t>(m.x) % 16)
         return KDQ_ERR_UNSUPPORTED;
+    constexpr int kDevices = 64;  // per-device state kept for devices 0..63
+    int device = 0;
+    KDQ_HIP(hipGetDevice(&device));
+    if (device < 0 || device >= kDevices)
+        return KDQ_ERR_UNSUPPORTED;
     if (check_only)
         return KDQ_OK;
 
     // this call's number on this device, 24 bits and never 0 (the published words start
     // at 0)
-    static std::atomic<unsigned> calls[64];
-    int device = 0;
-    KDQ_HIP(hipGetDevice(&device));
-    unsigned epoch = ++calls[unsigned(device) % 64] & 0xffffffu;
+    static std::atomic<unsigned> calls[kDevices];
+    static std::atomic<DecodeState*> states[kDevices];  // g_decode_state's address
+    DecodeState* state = states[device].load();
+    if (!state) {
+        void* address = nullptr;
+        KDQ_HIP(hipGetSymbolAddress(&address, HIP_SYMBOL(g_decode_state)));
+        state = static_cast<DecodeState*>(address);
+        states[device].store(state);
+    }
+    unsigned epoch = ++calls[device] & 0xffffffu;
     if (epoch == 0)
-        epoch = ++calls[unsigned(device) % 64] & 0xffffffu;
+        epoch = ++calls[device] & 0xffffffu;
     const DecodeRoute route{static_cast<const uint8_t*>(m.router.weights),
                             m.router.row_bytes,
                             unsigned((m.experts + pua.waves - 1) / pua.waves),
                             epoch,
+                            state,
                             m.logits,
                             m.experts,
                             K,

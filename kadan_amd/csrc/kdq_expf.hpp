@@ -11,8 +11,8 @@
 // double, rounded once to float.  The x86-64 build runs its FMA variant on CPUs with FMA
 // (glibc's ifunc picks __expf_fma): the range reduction is then contracted, z + 1.5 * 2^52
 // and z - kd each one fused multiply-add of (N / ln2) * x, and so is the cubic.  This
-// restatement equals that glibc's expf on every float from -104 to 88.72 (checked
-// exhaustively on the host against the installed library).  Without the fused range
+// restatement equals that glibc's expf on every float (checked exhaustively on the host
+// against the installed library).  Without the fused range
 // reduction two inputs differ (-0x1.f8cbb2p5 is one).
 //
 // The includer defines KDQ_EXPF_FN (for example `__device__ __forceinline__` in HIP
@@ -43,29 +43,35 @@ constexpr double kC2 = 0x1.62e42ff0c52d6p-1 / 32.0;
 
 }  // namespace kdq_expf
 
-KDQ_EXPF_FN float glibc_expf(float x) {
+// glibc_expf with the table of 2^(i/32) read from `table` (kdq_expf::kTable or a copy of
+// it, e.g. in LDS, where a latency-bound caller has staged it ahead of time).
+KDQ_EXPF_FN float glibc_expf_with(float x, const uint64_t* table) {
     using namespace kdq_expf;
+    // the general path for every input, then the library's special cases chosen by
+    // selection (no branches: a taken branch costs a latency-bound wavefront tens of
+    // clocks); outside the range the general path's value is discarded
     const uint32_t bits = __builtin_bit_cast(uint32_t, x);
     const uint32_t top = (bits >> 20) & 0x7ffu;
-    if (top >= 0x42bu) {  // |x| >= 88 (top 12 bits of 88.0f), or x is not finite
-        if (bits == 0xff800000u)
-            return 0.0f;  // -inf
-        if (top >= 0x7f8u)
-            return x + x;  // +inf, NaN
-        if (x > 0x1.62e42ep6f)
-            return __builtin_inff();  // past log(2^128)
-        if (x < -0x1.9fe368p6f)
-            return 0.0f;  // below log(2^-150)
-    }
     const double xd = double(x);
     double kd = fma(kInvLn2N, xd, kShift);
     const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
     kd -= kShift;
     const double r = fma(kInvLn2N, xd, -kd);
-    const double s = __builtin_bit_cast(double, kTable[ki % 32] + (ki << 47));
+    const double s = __builtin_bit_cast(double, table[ki % 32] + (ki << 47));
     const double z = fma(kC0, r, kC1);
     const double r2 = r * r;
     double y = fma(kC2, r, 1.0);
     y = fma(z, r2, y);
-    return float(y * s);
+    float result = float(y * s);
+    // |x| >= 88 (top 12 bits of 88.0f), or x is not finite
+    const bool large = top >= 0x42bu;
+    result = large && x < -0x1.9fe368p6f ? 0.0f : result;            // below log(2^-150)
+    result = large && x > 0x1.62e42ep6f ? __builtin_inff() : result;  // past log(2^128)
+    result = top >= 0x7f8u ? x + x : result;                          // +inf, NaN
+    result = bits == 0xff800000u ? 0.0f : result;                     // -inf
+    return result;
+}
+
+KDQ_EXPF_FN float glibc_expf(float x) {
+    return glibc_expf_with(x, kdq_expf::kTable);
 }

@@ -233,3 +233,169 @@ __device__ __forceinline__ void route_select(const float* __restrict__ logits, u
     else
         route_select_r<4, COHERENT>(logits, t, experts, top_k, lane, selected, selected_weight);
 }
+
+// LDS of route_select_wg (16-byte aligned, in the caller's LDS).
+struct RouteScratch {
+    uint64_t exp_table[32];  // kdq_expf::kTable, staged while the logits load
+    float p[320];        // expf(v - max) (+0 past the experts)
+    float q[320];        // probabilities (NaN past the experts: compares false)
+    unsigned rank[256];  // per expert: probabilities above it | equal ones << 16
+    double part[16];
+    float wave_max[16];
+    unsigned inexact, ambiguous;
+    int sel[64];
+    float sel_p[64];
+};
+
+// route_select_r's result for one token, bit for bit, computed by a whole workgroup of
+// 64 W threads (4 <= W <= 16; experts <= 256, top_k <= KMAX <= 64): thread i < top_k gets
+// the i-th selected expert and its renormalised weight.  Thread e takes expert e's
+// probability; the total is exact in any order when every p is a multiple of 2^-45, and
+// otherwise every wavefront adds the p in expert order.  The selection ranks every expert
+// by counting the probabilities above it and equal to it: a task is 64 experts (one a
+// lane) against a chunk of 32 probabilities, which every lane of the wavefront reads at
+// the same LDS address.  With the top_k + 1 largest distinct, expert e's count is its
+// position in the descending order, which is std::partial_sort's; equal or NaN
+// probabilities there go to heap_route by wavefront 0.  The code is straight-line where
+// it can be (selections rather than branches, loops of fixed length): one wavefront per
+// SIMD has nothing to hide a taken branch behind.  Every thread must call it.
+template <int W, int KMAX, bool COHERENT>
+__device__ __forceinline__ void route_select_wg(const float* __restrict__ logits,
+                                                unsigned experts, unsigned top_k,
+                                                RouteScratch& s, int& selected,
+                                                float& selected_weight) {
+    static_assert(W >= 4 && W <= 16 && KMAX <= 64, "route_select_wg: 4..16 waves");
+    constexpr unsigned kThreads = W * 64;
+    const unsigned t = threadIdx.x, lane = t % 64, wave = t / 64;
+    const bool mine = t < experts;
+    const float* at = logits + min(t, experts - 1);
+    float v;
+    if constexpr (COHERENT)
+        v = __hip_atomic_load(at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+        v = *at;
+    if (t < 32)  // a global load, in flight with the logits
+        s.exp_table[t] = kdq_expf::kTable[t];
+    v = mine ? v : -INFINITY;
+    const float wave_max = wave_max_rows(v);
+    if (lane == 0)
+        s.wave_max[wave] = wave_max;
+    if (t < 256)
+        s.rank[t] = 0u;
+    if (t == 0) {
+        s.inexact = 0u;
+        s.ambiguous = 0u;
+    }
+    __syncthreads();
+    // the maximum of a set by fmaxf is the same in any order (up to the sign of a zero,
+    // which leaves every v - maximum, and so every p, unchanged)
+    float maximum = s.wave_max[0];
+#pragma unroll
+    for (int i = 1; i < W; ++i)
+        maximum = fmaxf(maximum, s.wave_max[i]);
+    const float e_v = glibc_expf_with(v - maximum, s.exp_table);
+    const float p = mine ? e_v : 0.f;
+    const double scaled = double(p) * 0x1p45;
+    const bool exact = scaled == __builtin_trunc(scaled);
+#pragma unroll
+    for (unsigned i = 0; i < 320; i += kThreads)
+        if (i + t < 320)
+            s.p[i + t] = i == 0 ? p : 0.f;  // +0 past the experts leaves the in-order total
+    const double wave_total = wave_sum_double(double(p));
+    const bool wave_inexact = __ballot(!exact) != 0;
+    if (lane == 0) {
+        s.part[wave] = wave_total;
+        atomicOr(&s.inexact, wave_inexact ? 1u : 0u);
+    }
+    __syncthreads();
+    double total = s.part[0];
+#pragma unroll
+    for (int i = 1; i < W; ++i)
+        total += s.part[i];  // exact: every partial sum a multiple of 2^-45 below 2^9
+    if (s.inexact) {
+        // every lane of every wavefront adds the same p in expert order, 64 at a time
+        // (reading past the experts adds +0); no barrier needed for the result
+        const float4* q4 = reinterpret_cast<const float4*>(s.p);
+        double in_order = 0.0;
+        for (unsigned b = 0; b < experts; b += 64) {
+            float4 f[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                f[j] = q4[b / 4 + j];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                in_order += double(f[j].x);
+                in_order += double(f[j].y);
+                in_order += double(f[j].z);
+                in_order += double(f[j].w);
+            }
+        }
+        total = in_order;
+    }
+    const float pf = float(double(p) / total);
+    const bool nan_here = mine && isnan(pf);
+#pragma unroll
+    for (unsigned i = 0; i < 320; i += kThreads)
+        if (i + t < 320)
+            s.q[i + t] = i + t < experts ? pf : __builtin_nanf("");
+    const bool wave_nan = __ballot(nan_here) != 0;
+    if (lane == 0)
+        atomicOr(&s.ambiguous, wave_nan ? 1u : 0u);
+    __syncthreads();
+
+    // tasks (chunk c of 32 probabilities, experts 64 g .. 64 g + 63), by wavefronts
+    const unsigned chunks = (experts + 31) / 32, tasks = chunks * ((experts + 63) / 64);
+    for (unsigned task = wave; task < tasks; task += W) {
+        const unsigned c = task % chunks, e = (task / chunks) * 64 + lane;
+        const float pe = s.q[e];  // NaN past the experts: counts nothing
+        const float4* q4 = reinterpret_cast<const float4*>(s.q + 32 * c);
+        float4 f[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            f[j] = q4[j];
+        unsigned count = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            count += unsigned(f[j].x > pe) + unsigned(f[j].y > pe) + unsigned(f[j].z > pe) +
+                     unsigned(f[j].w > pe);
+            count += (unsigned(f[j].x == pe) + unsigned(f[j].y == pe) +
+                      unsigned(f[j].z == pe) + unsigned(f[j].w == pe)) << 16;
+        }
+        atomicAdd(&s.rank[e], count);
+    }
+    __syncthreads();
+    const unsigned rank = s.rank[min(t, 255u)];
+    const unsigned greater = rank & 0xffffu, equal = rank >> 16;  // equal counts t itself
+    const bool top = mine && greater < top_k;
+    const bool tie = top && (isnan(pf) || equal > 1);
+    if (top && !tie) {
+        s.sel[greater] = int(t);
+        s.sel_p[greater] = pf;
+    }
+    const bool wave_tie = __ballot(tie) != 0;
+    if (lane == 0)
+        atomicOr(&s.ambiguous, wave_tie ? 1u : 0u);
+    __syncthreads();
+    if (s.ambiguous) {
+        if (wave == 0) {
+            const int slot =
+                heap_route([&](int i) { return s.q[i]; }, experts, top_k, lane);
+            if (lane < top_k) {
+                s.sel[lane] = slot;
+                s.sel_p[lane] = s.q[slot];
+            }
+        }
+        __syncthreads();
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < KMAX; ++i) {  // sequential, in selection order (+0 past top_k)
+        const float pi = s.sel_p[i];
+        sum += unsigned(i) < top_k ? pi : 0.f;
+    }
+    sum = fmaxf(sum, 6.103515625e-5f);
+    if (t < top_k) {
+        selected = s.sel[t];
+        selected_weight = s.sel_p[t] / sum;
+    }
+}

@@ -6,6 +6,7 @@
 //   route_kernel      one wavefront per token: softmax (float exp, double total),
 //                     top-k in std::partial_sort's order, renormalise;
 //                     the token's activations as FP8 terms with E8M0 block scales
+//   route_wg_kernel   the same selection, one workgroup per token (few tokens)
 //   permute_kernel    one workgroup: stable counting sort of the slots by expert
 //                     (expert-major, slot ascending) plus the list of work items
 //                     (expert, first row) of at most kItemRows rows each
@@ -71,6 +72,39 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
     const unsigned t = blockIdx.x * 4 + threadIdx.x / 64;
     if (t < tokens)
         route_token(logits, t, experts, top_k, idx, weight, threadIdx.x % 64);
+}
+
+// Token blockIdx.x by a whole workgroup of 256 threads (route_select_wg): the same
+// selection as route_kernel's in a fraction of its latency, for a few tokens.
+__global__ __launch_bounds__(256) void route_wg_kernel(const float* __restrict__ logits,
+                                                       unsigned experts, unsigned top_k,
+                                                       int32_t* __restrict__ idx,
+                                                       float* __restrict__ weight) {
+    __shared__ __align__(16) RouteScratch scratch;
+    const unsigned t = blockIdx.x;
+    int e = 0;
+    float we = 0.f;
+    route_select_wg<4, kMaxTopK, false>(logits + size_t(t) * experts, experts, top_k, scratch,
+                                        e, we);
+    if (threadIdx.x < top_k) {
+        idx[size_t(t) * top_k + threadIdx.x] = e;
+        weight[size_t(t) * top_k + threadIdx.x] = we;
+    }
+}
+
+// Up to this many tokens one workgroup routes each token (route_wg_kernel), past it one
+// wavefront (route_kernel).
+constexpr size_t kRouteWgTokens = 64;
+
+void launch_route_selection(const float* logits, size_t tokens, size_t experts,
+                            size_t top_k, int32_t* idx, float* w, hipStream_t stream) {
+    if (tokens <= kRouteWgTokens)
+        hipLaunchKernelGGL(route_wg_kernel, dim3(unsigned(tokens)), dim3(256), 0, stream,
+                           logits, unsigned(experts), unsigned(top_k), idx, w);
+    else
+        hipLaunchKernelGGL(route_kernel, dim3(unsigned((tokens + 3) / 4)), dim3(256), 0,
+                           stream, logits, unsigned(tokens), unsigned(experts),
+                           unsigned(top_k), idx, w);
 }
 
 // Stable counting sort of slots by expert by one workgroup of 1024 threads (every thread
@@ -1649,8 +1683,7 @@ int launch_route(const float* logits, size_t tokens, size_t experts, size_t top_
                  int32_t* idx, float* w, int32_t* offsets, int32_t* perm, int32_t* items,
                  int32_t* item_count, int32_t* position, int32_t* slot_row,
                  hipStream_t stream) {
-    hipLaunchKernelGGL(route_kernel, dim3(unsigned((tokens + 3) / 4)), dim3(256), 0, stream,
-                       logits, unsigned(tokens), unsigned(experts), unsigned(top_k), idx, w);
+    launch_route_selection(logits, tokens, experts, top_k, idx, w, stream);
     KDQ_HIP(hipGetLastError());
     // heavy items first when an average expert's rows fit one work item (the grouped
     // GEMMs' workgroups then all fit the compute units at once)
@@ -1674,8 +1707,7 @@ int route_selection(const float* logits, size_t tokens, size_t experts, size_t t
     const int rc = check_route(logits, tokens, experts, top_k);
     if (rc)
         return rc;
-    hipLaunchKernelGGL(route_kernel, dim3(unsigned((tokens + 3) / 4)), dim3(256), 0, stream,
-                       logits, unsigned(tokens), unsigned(experts), unsigned(top_k), idx, w);
+    launch_route_selection(logits, tokens, experts, top_k, idx, w, stream);
     KDQ_HIP(hipGetLastError());
     return KDQ_OK;
 }

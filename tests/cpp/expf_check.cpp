@@ -1,7 +1,8 @@
 // Host check of glibc_expf (kadan_amd/csrc/kdq_expf.hpp, the restatement the device
-// router runs) against the installed C library's expf: every float from -104 to 88.72
-// (the finite, nonzero range, both signs of zero included).  Prints the number of
-// inputs whose result bits differ and the first few; exit status 1 if any.
+// router runs) against the installed C library's expf: every one of the 2^32 float bit
+// patterns (zeros, subnormals, the overflow and underflow ranges, infinities and NaNs
+// included).  Prints the number of inputs whose result bits differ and the first few;
+// exit status 1 if any.
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -20,9 +21,8 @@ static uint32_t bits_of(float f) {
 }
 
 int main() {
-    // two ranges of float bit patterns: [+0, 88.72] and [-0, -104]
-    const uint64_t ranges[2][2] = {{0x00000000u, bits_of(88.72f)},
-                                   {0x80000000u, bits_of(-104.0f)}};
+    // every bit pattern: [+0, +NaN with all payload bits] and [-0, -NaN with all]
+    const uint64_t ranges[2][2] = {{0x00000000u, 0x7fffffffu}, {0x80000000u, 0xffffffffu}};
     const unsigned workers = std::max(1u, std::thread::hardware_concurrency());
     std::vector<uint64_t> bad(workers, 0);
     std::vector<uint32_t> first(workers, 0);

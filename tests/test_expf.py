@@ -2,8 +2,9 @@
 host C library's expf, which the reference's router calls through std::exp(float)
 (IW/src/models/text/qwen_layers.cpp:404-408; IW = services/hikari/inference_worker).
 
-tests/cpp/expf_check.cpp compiles the same header for the host and compares every float
-from -104 to 88.72 (2.24e9 inputs, about 6 s on 8 threads) bit for bit.  glibc's x86-64
+tests/cpp/expf_check.cpp compiles the same header for the host and compares every one of
+the 2^32 float bit patterns (about 12 s on 8 threads) bit for bit: the finite range, the
+overflow and underflow ends, zeros, infinities and NaNs.  glibc's x86-64
 build runs its FMA variant on CPUs with FMA and AVX2; the header restates that variant.
 On a CPU without them the library takes the unfused variant, which differs on two of
 those inputs, so the check is skipped there."""

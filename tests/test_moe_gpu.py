@@ -94,6 +94,28 @@ def test_route_near_ties_bit_exact(device, oracle, experts, top_k, seed):
     assert bad.size == 0, (bad.size, bad[:5])
 
 
+@pytest.mark.parametrize("experts,top_k,seed", [(32, 4, 0x714B), (128, 8, 0x714C),
+                                                (256, 8, 0x714D), (100, 6, 0x714E)])
+def test_route_few_tokens_near_ties_bit_exact(device, oracle, experts, top_k, seed):
+    """Calls of at most 64 tokens route one token per workgroup (route_wg_kernel: the
+    probabilities ranked by counting, the in-order total by one thread): 8192 near-tie
+    rows in calls of 64, 17 and 1 tokens, bit for bit equal to the oracle's router."""
+    torch = _torch()
+    from kadan_amd import ops
+    from tests.util import near_tie_logits
+    logits = near_tie_logits(seed, 8192, experts, top_k)
+    idx, w = oracle.moe_route(logits, top_k)
+    cuts = list(range(0, 8192 - 18, 64)) + [8192 - 18, 8192 - 1, 8192]
+    dev = torch.from_numpy(logits).to(device)
+    gi = np.zeros_like(idx)
+    gw = np.zeros_like(w)
+    for a, b in zip(cuts[:-1], cuts[1:]):
+        ci, cw, _, _ = ops.moe_route(dev[a:b].contiguous(), top_k)
+        gi[a:b], gw[a:b] = ci.cpu().numpy(), cw.cpu().numpy()
+    bad = np.flatnonzero((gi != idx).any(1) | (gw.view(np.uint32) != w.view(np.uint32)).any(1))
+    assert bad.size == 0, (bad.size, bad[:5])
+
+
 def test_route_equal_logits_heap_order(device):
     """16 equal probabilities, top-4: std::partial_sort gives [1, 3, 0, 2] (worked through
     the heap steps in tests/test_oracle.py)."""
