@@ -257,7 +257,8 @@ typedef struct kdq_moe_gguf_layer {
  * read once per 8 of its rows, the reference's per-expert batch jobs,
  * IW/include/kadan/dense_compute.hpp:197-201) or, for Q4_K / Q8_0 / Q6_K, into 64-row
  * tiles of the prefill GEMM (fp16 operands, fp32 accumulation).
- * One row with an F32 router and the common K-quant mixes runs in two launches whose
+ * Up to 8 rows (rows x hidden x 4 bytes <= 64 KB) with an F32 router and the common
+ * K-quant mixes run in two launches whose
  * workgroups hand the routing and the rows to combine to one another through
  * device-wide counters (one set per GPU): calls that overlap on one GPU race (as they
  * do on the library's workspace); `status` |= 8 if a workgroup waited past its bound

@@ -2372,9 +2372,10 @@ namespace {
 // selection: (epoch << 8) | expert of the call that routed last.  Calls that overlap on
 // one GPU race on them (and on the workspace), as on the rest of the library's scratch.
 // Kernels take its address as an argument (DecodeRoute::state), not through the symbol.
+constexpr unsigned kDecodeTokens = kFusedDecodeTokens;
 struct DecodeState {
     unsigned router_arrived;
-    unsigned routed_slot[kMaxFused];
+    unsigned routed_slot[kDecodeTokens * kMaxFused];  // token t's slot i at t * top_k + i
 };
 __device__ DecodeState g_decode_state;
 
@@ -2385,7 +2386,7 @@ struct DecodeRoute {
     unsigned epoch;              // this call's number on this device (never 0)
     DecodeState* state;          // this device's g_decode_state
     float* logits;
-    unsigned experts, top_k;
+    unsigned experts, top_k, tokens;
     int32_t* idx;
     float* w;
     unsigned* counters;
@@ -2460,62 +2461,81 @@ __global__ __launch_bounds__(W * 64) void moe_decode_up_kernel(const MfmaJobs a,
     __shared__ unsigned arrived;
     const unsigned wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     if (blockIdx.x < route.router_workgroups) {
+        // x of every token staged in LDS (its first bytes; the routing's scratch later
+        // reuses them)
+        extern __shared__ __align__(16) uint8_t lds[];
+        float4* xs = reinterpret_cast<float4*>(lds);
         const unsigned column = blockIdx.x * W + wave;
+        const u32x4* row = reinterpret_cast<const u32x4*>(
+            route.router + size_t(min(column, route.experts - 1)) * route.router_row_bytes);
+        // chunks of 8 values a lane (hidden <= 4096: at most 8), four at a time: the four
+        // chunks' loads all issued (at clamped, in-bounds addresses), then the products of
+        // the lane's valid ones in exact_gemv's order, one chain per token
+        constexpr int kChunks = 8, kBatch = 4;
+        u32x4 wv[kBatch][2];
+        auto load_batch = [&](int c0) {
+#pragma unroll
+            for (int c = 0; c < kBatch; ++c) {
+                const unsigned i = min(lane * 8 + (c0 + c) * 512, a.in - 8);
+                wv[c][0] = row[i / 4];
+                wv[c][1] = row[i / 4 + 1];
+            }
+        };
+        load_batch(0);
+        for (unsigned q = threadIdx.x; q < route.tokens * a.in / 4; q += W * 64)
+            xs[q] = reinterpret_cast<const float4*>(route.x)[q];
+        __syncthreads();
         if (column < route.experts) {
-            const float4* row = reinterpret_cast<const float4*>(
-                route.router + size_t(column) * route.router_row_bytes);
-            const float4* xq = reinterpret_cast<const float4*>(route.x);
-            // chunks of 8 values a lane (hidden <= 4096: at most 8), four at a time: the
-            // four chunks' loads all issued (at clamped, in-bounds addresses), then the
-            // products of the lane's valid ones in exact_gemv's order
-            constexpr int kChunks = 8, kBatch = 4;
-            float sum = 0.f;
+            float sum[kDecodeTokens] = {};
             bool finite = true;
 #pragma unroll
             for (int c0 = 0; c0 < kChunks; c0 += kBatch) {
                 if (c0 * 512 >= a.in)
                     break;  // uniform: lane 0 has the lowest index
-                u32x4 wv[kBatch][2], xv[kBatch][2];
-#pragma unroll
-                for (int c = 0; c < kBatch; ++c) {
-                    const unsigned i = min(lane * 8 + (c0 + c) * 512, a.in - 8);
-                    wv[c][0] = reinterpret_cast<const u32x4*>(row)[i / 4];
-                    wv[c][1] = reinterpret_cast<const u32x4*>(row)[i / 4 + 1];
-                    xv[c][0] = reinterpret_cast<const u32x4*>(xq)[i / 4];
-                    xv[c][1] = reinterpret_cast<const u32x4*>(xq)[i / 4 + 1];
-                }
+                if (c0 > 0)
+                    load_batch(c0);
                 // every value here (the compiler would otherwise sink each chunk's loads
                 // into its guarded products: one memory round trip per chunk)
 #pragma unroll
                 for (int c = 0; c < kBatch; ++c)
-                    asm volatile("" : "+v"(wv[c][0]), "+v"(wv[c][1]), "+v"(xv[c][0]),
-                                 "+v"(xv[c][1]));
+                    asm volatile("" : "+v"(wv[c][0]), "+v"(wv[c][1]));
 #pragma unroll
                 for (int c = 0; c < kBatch; ++c) {
-                    if (lane * 8 + (c0 + c) * 512 >= a.in)
+                    const unsigned i = lane * 8 + (c0 + c) * 512;
+                    if (i >= a.in)
                         break;
-                    float w[8], xr[8];
+                    float w[8];
 #pragma unroll
                     for (int k = 0; k < 4; ++k) {
                         w[k] = __uint_as_float(wv[c][0][k]);
                         w[4 + k] = __uint_as_float(wv[c][1][k]);
-                        xr[k] = __uint_as_float(xv[c][0][k]);
-                        xr[4 + k] = __uint_as_float(xv[c][1][k]);
                     }
 #pragma unroll
                     for (int k = 0; k < 8; ++k)
                         finite = finite && isfinite(w[k]);
 #pragma unroll
-                    for (int k = 0; k < 8; ++k)
-                        sum = fmaf(w[k], xr[k], sum);
+                    for (unsigned t = 0; t < kDecodeTokens; ++t) {
+                        if (t >= route.tokens)
+                            break;  // uniform
+                        const float4 x0 = xs[(t * a.in + i) / 4], x1 = xs[(t * a.in + i) / 4 + 1];
+                        const float xr[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                        for (int k = 0; k < 8; ++k)
+                            sum[t] = fmaf(w[k], xr[k], sum[t]);
+                    }
                 }
             }
             if (route.status && __any(!finite) && lane == 0)
                 atomicOr(route.status, 1u);
-            sum = wave_sum(sum);
-            if (lane == 0)
-                __hip_atomic_store(&route.logits[column], sum, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (unsigned t = 0; t < kDecodeTokens; ++t) {
+                if (t >= route.tokens)
+                    break;
+                const float total = wave_sum(sum[t]);
+                if (lane == 0)
+                    __hip_atomic_store(&route.logits[size_t(t) * route.experts + column], total,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the logits stored first
         __syncthreads();
@@ -2524,25 +2544,31 @@ __global__ __launch_bounds__(W * 64) void moe_decode_up_kernel(const MfmaJobs a,
         __syncthreads();
         if (arrived != route.router_workgroups - 1)
             return;
-        // the whole workgroup routes (its LDS is the GEMV's, unused here)
-        extern __shared__ __align__(16) uint8_t lds[];
+        // the routing, its LDS the GEMV's, no longer used: one token by the whole
+        // workgroup, several by a wavefront each; then each slot's word, this call's epoch
+        // and its expert
         int e = 0;
         float we = 0.f;
-        route_select_wg<W, kMaxFused, true>(route.logits, route.experts, route.top_k,
-                                            *reinterpret_cast<RouteScratch*>(lds), e, we);
-        const unsigned t = threadIdx.x;
-        if (t < route.top_k) {
-            __hip_atomic_store(&route.idx[t], e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&route.w[t], we, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        if (t < unsigned(kMaxFused))  // each slot's word: this call's epoch and its expert
-                                       // (0 for slots past top_k)
-            __hip_atomic_store(&route.state->routed_slot[t],
-                               t < route.top_k ? (route.epoch << 8) | unsigned(e) : 0u,
+        auto publish = [&](unsigned token, unsigned slot) {
+            const unsigned at = token * route.top_k + slot;
+            __hip_atomic_store(&route.idx[at], e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&route.w[at], we, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&route.state->routed_slot[at], (route.epoch << 8) | unsigned(e),
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        for (unsigned i = t; i < route.counter_count; i += W * 64)
+        };
+        if (route.tokens == 1) {
+            route_select_wg<W, kMaxFused, true>(route.logits, route.experts, route.top_k,
+                                                *reinterpret_cast<RouteScratch*>(lds), e, we);
+            if (threadIdx.x < route.top_k)
+                publish(0, threadIdx.x);
+        } else if (wave < route.tokens) {
+            route_select<true>(route.logits, wave, route.experts, route.top_k, lane, e, we);
+            if (lane < route.top_k)
+                publish(wave, lane);
+        }
+        for (unsigned i = threadIdx.x; i < route.counter_count; i += W * 64)
             route.counters[i] = 0u;
-        if (t == 0)
+        if (threadIdx.x == 0)
             route.state->router_arrived = 0u;
         return;
     }
@@ -2576,46 +2602,52 @@ __global__ __launch_bounds__(W * 64) void moe_decode_up_kernel(const MfmaJobs a,
                                                                late);
     } else {
         const unsigned k = id - a_workgroups;
-        if (k == 0) {
-            shared_gate(route.gate_vector, route.x, route.hidden, route.gate, route.status);
+        if (k < route.tokens) {  // token k's gate scalar
+            shared_gate(route.gate_vector, route.x + size_t(k) * route.hidden, route.hidden,
+                        route.gate + k, route.status);
             __syncthreads();  // its LDS words before the product's
         }
         mfma_gemv_body<EB, 1, W, false, 0>(b, k % b.columns, k / b.columns, -1);
     }
 }
 
-// y = sum over the selections, in selection order, of down * weight, plus shared_down *
-// sigmoid(gate_vector . x), as combine_kernel computes it for one token.
+// y of each token = sum over its selections, in selection order, of down * weight, plus
+// shared_down * sigmoid(gate_vector . x), as combine_kernel computes it.
 struct DecodeCombine {
-    const float* down;    // [top_k][hidden]
-    const float* shared;  // [hidden]
-    const float* w;       // [top_k]
-    const float* gate;    // sigmoid(gate_vector . x), from the up launch
+    const float* down;    // [tokens][top_k][hidden]
+    const float* shared;  // [tokens][hidden]
+    const float* w;       // [tokens][top_k]
+    const float* gate;    // [tokens]: sigmoid(gate_vector . x), from the up launch
     unsigned top_k, hidden;
-    float* y;
-    unsigned* counters;  // one per row block, zero on entry
+    float* y;             // [tokens][hidden]
+    unsigned* counters;   // one per (token, row block), zero on entry
 };
 
-// Workgroups [0, a.columns * a.count) run the experts' down rows (slot = job step), the
-// rest the shared down; both halves cut the hidden rows into the same blocks of
-// a.rows_per_wg.  Each workgroup then counts itself into its row block; the last of the
-// top_k + 1 to arrive (its fences make the others' stored rows visible) combines that
-// block, so the layer needs no launch of its own for the combine.  The sum runs in the
-// fixed selection order whichever workgroup is last.
+// Workgroups [0, a.columns * a.count) run the experts' down rows (job step = token *
+// top_k + slot), the rest the shared down (job step = token); both halves cut the hidden
+// rows into the same blocks of a.rows_per_wg.  Each workgroup then counts itself into its
+// token's row block; the last of the top_k + 1 to arrive (its fences make the others'
+// stored rows visible) combines that block, so the layer needs no launch of its own for
+// the combine.  The sum runs in the fixed selection order whichever workgroup is last.
 template <int EA, bool PA, int EB, int W>
 __global__ __launch_bounds__(W * 64) void moe_decode_down_kernel(const MfmaJobs a,
                                                                  const MfmaJobs b,
                                                                  const DecodeCombine c) {
     __shared__ unsigned arrived;
     const unsigned a_workgroups = a.columns * a.count;
-    unsigned block;
+    unsigned block, token;
     if (blockIdx.x < a_workgroups) {
         block = blockIdx.x % a.columns;
-        mfma_gemv_body<EA, 1, W, PA, 0, true>(a, block, blockIdx.x / a.columns, -1);
+        const unsigned step = blockIdx.x / a.columns;
+        token = step / c.top_k;
+        mfma_gemv_body<EA, 1, W, PA, 0, true>(a, block, step, -1);
     } else {
-        block = blockIdx.x - a_workgroups;
-        mfma_gemv_body<EB, 1, W, false, 0, true>(b, block, 0, -1);
+        const unsigned k = blockIdx.x - a_workgroups;
+        block = k % b.columns;
+        token = k / b.columns;
+        mfma_gemv_body<EB, 1, W, false, 0, true>(b, block, token, -1);
     }
+    unsigned* counter = &c.counters[token * a.columns + block];
     // The rows went out as device-scope stores; once every one of them has completed
     // (the wait below, then the barrier) the count may announce them.  The combining
     // workgroup reads them with device-scope loads.  No cache-wide fence: one per
@@ -2623,12 +2655,16 @@ __global__ __launch_bounds__(W * 64) void moe_decode_down_kernel(const MfmaJobs 
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0)
-        arrived = atomicAdd(&c.counters[block], 1u);
+        arrived = atomicAdd(counter, 1u);
     __syncthreads();
     if (arrived != c.top_k)
         return;  // the whole workgroup: another one combines this block
 
-    const float gate = *c.gate;
+    const float gate = c.gate[token];
+    const float* down = c.down + size_t(token) * c.top_k * c.hidden;
+    const float* shared = c.shared + size_t(token) * c.hidden;
+    const float* w = c.w + size_t(token) * c.top_k;
+    float* y = c.y + size_t(token) * c.hidden;
     const unsigned r0 = block * a.rows_per_wg, r1 = min(c.hidden, r0 + a.rows_per_wg);
     auto coherent = [](const float* p) {
         return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -2638,8 +2674,8 @@ __global__ __launch_bounds__(W * 64) void moe_decode_down_kernel(const MfmaJobs 
         float v[kMaxFused + 1];
 #pragma unroll
         for (int i = 0; i < kMaxFused; ++i)
-            v[i] = coherent(c.down + size_t(min(unsigned(i), c.top_k - 1)) * c.hidden + r);
-        v[kMaxFused] = coherent(c.shared + r);
+            v[i] = coherent(down + size_t(min(unsigned(i), c.top_k - 1)) * c.hidden + r);
+        v[kMaxFused] = coherent(shared + r);
 #pragma unroll
         for (int i = 0; i <= kMaxFused; ++i)
             asm volatile("" : "+v"(v[i]));
@@ -2647,11 +2683,11 @@ __global__ __launch_bounds__(W * 64) void moe_decode_down_kernel(const MfmaJobs 
 #pragma unroll
         for (int i = 0; i < kMaxFused; ++i)
             if (unsigned(i) < c.top_k)
-                sum += v[i] * c.w[i];
-        c.y[r] = sum + v[kMaxFused] * gate;
+                sum += v[i] * w[i];
+        y[r] = sum + v[kMaxFused] * gate;
     }
     if (threadIdx.x == 0)
-        c.counters[block] = 0u;  // ready for the next layer call
+        *counter = 0u;  // ready for the next layer call
 }
 
 // An affine launch over `count` slots of one token (job step = slot; x rows x_step apart,
@@ -2721,17 +2757,21 @@ int launch_decode_down(const MfmaJobs& a, const MfmaJobs& b, const DecodeCombine
 }  // namespace
 
 int moe_decode_fused(const DecodeMoe& m, hipStream_t s, bool check_only) {
-    const unsigned K = m.top_k;
-    if (K == 0 || K > unsigned(kMaxFused) || m.experts > 256 || m.hidden % 4)
+    const unsigned K = m.top_k, T = m.tokens, H = m.hidden;
+    // the router's x rows are staged in LDS: at most 64 KB of them
+    if (K == 0 || K > unsigned(kMaxFused) || T == 0 || T > kDecodeTokens ||
+        m.experts > 256 || H % 4 || size_t(T) * H * 4 > 64 * 1024)
         return KDQ_ERR_UNSUPPORTED;
     MfmaJobs ua, ub, da, db;
     MfmaPlan pua, pub, pda, pdb;
-    const size_t F = m.experts_up.job.columns;
-    if (m.experts_down.job.in != F ||
-        !decode_half(m.experts_up, K, 0, K, F, m.up_packed, ua, pua) ||
-        !decode_half(m.shared_up, 1, 0, 1, 0, false, ub, pub) ||
-        !decode_half(m.experts_down, K, F, 1, m.hidden, m.down_packed, da, pda) ||
-        !decode_half(m.shared_down, 1, 0, 1, 0, false, db, pdb))
+    const size_t F = m.experts_up.job.columns, S = m.shared_up.job.columns;
+    // slot j = token * K + i: the expert products read x row j / K and write g row j; the
+    // shared ones read x row t and write row t
+    if (m.experts_down.job.in != F || m.shared_down.job.in != S ||
+        !decode_half(m.experts_up, T * K, H, K, F, m.up_packed, ua, pua) ||
+        !decode_half(m.shared_up, T, H, 1, S, false, ub, pub) ||
+        !decode_half(m.experts_down, T * K, F, 1, H, m.down_packed, da, pda) ||
+        !decode_half(m.shared_down, T, S, 1, H, false, db, pdb))
         return KDQ_ERR_UNSUPPORTED;
     // both halves of a launch: one workgroup size; the down halves cut the hidden rows
     // alike (packed halves: rows per workgroup a multiple of 8)
@@ -2743,9 +2783,9 @@ int moe_decode_fused(const DecodeMoe& m, hipStream_t s, bool check_only) {
     const unsigned rows = (std::max(da.rows_per_wg, db.rows_per_wg) + 7) & ~7u;
     number_workgroups(da, rows);
     number_workgroups(db, rows);
-    // (the routing workgroup's scratch lies in the same dynamic LDS)
+    // (the router's staged x and the routing's scratch lie in the same dynamic LDS)
     const size_t up_lds = std::max({mfma_lds(1, ua.in, 2), mfma_lds(1, ub.in, 2),
-                                    sizeof(RouteScratch)});
+                                    sizeof(RouteScratch), size_t(T) * H * 4});
     const size_t down_lds = std::max(mfma_lds(1, da.in, 1), mfma_lds(1, db.in, 1));
     if (std::max(up_lds, down_lds) > size_t(kDecodeDynamicLds))
         return KDQ_ERR_UNSUPPORTED;
@@ -2756,7 +2796,8 @@ int moe_decode_fused(const DecodeMoe& m, hipStream_t s, bool check_only) {
                        (pua.waves == 8 || pua.waves == 16);
     const bool down_ok = (da_enc == KDQ_Q6_K || da_enc == KDQ_Q4_K) &&
                          (db_enc == KDQ_Q4_K || db_enc == KDQ_Q6_K);
-    if (!up_ok || !down_ok || da.columns != db.columns || da.columns > m.counter_count ||
+    if (!up_ok || !down_ok || da.columns != db.columns ||
+        size_t(T) * da.columns > m.counter_count ||
         m.experts > 256 || m.hidden > 4096 ||
         m.router.encoding != KDQ_F32 || m.router.in != m.hidden ||
         m.router.columns != m.experts || m.router.row_bytes % 16 ||
@@ -2793,10 +2834,11 @@ int moe_decode_fused(const DecodeMoe& m, hipStream_t s, bool check_only) {
                             m.logits,
                             m.experts,
                             K,
+                            T,
                             m.idx,
                             m.w,
                             m.counters,
-                            da.columns,
+                            T * da.columns,
                             m.gate_vector,
                             m.x,
                             m.hidden,

@@ -197,12 +197,14 @@ bool swiglu_pairable(const kdq_matvec_job& j, size_t count);
 // among those instantiated (Q4_K expert gate / up with Q8_0 or Q4_K shared gate / up,
 // inputs of 1280..4096 values; Q6_K or Q4_K downs of at most 1024 inputs); with
 // check_only it launches nothing either way.
+// Tokens of one fused decode call (moe_decode_fused): more take the staged path.
+constexpr unsigned kFusedDecodeTokens = 8;
 struct DecodeMoe {
-    kdq_matvec_job router;  // F32, x = the token, y = logits (device scratch)
+    kdq_matvec_job router;  // F32, x = the tokens, y = logits (device scratch)
     IndexedJob experts_up, shared_up, experts_down, shared_down;
     bool up_packed, down_packed;
     float* logits;
-    unsigned experts, top_k, hidden;
+    unsigned experts, top_k, hidden, tokens;
     int32_t* idx;
     float* w;
     const float* gate_vector;
@@ -211,7 +213,7 @@ struct DecodeMoe {
     unsigned* status;
     unsigned* counters;
     unsigned counter_count;
-    float* gate;  // device scratch: the shared gate's sigmoid, between the two launches
+    float* gate;  // device scratch: the shared gate's sigmoid per token, between the launches
 };
 int moe_decode_fused(const DecodeMoe& m, hipStream_t stream, bool check_only);
 

@@ -386,7 +386,8 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
                             pk.gate_exps ? 0 : gu_bytes * E, pk.up_exps ? 0 : up_bytes * E,
                             pk.down_exps ? 0 : dn_bytes * E, xs_bytes,
                             gemm_gu || gemm_dn ? positions * 4 : 0, shg_bytes, shu_bytes,
-                            shd_bytes, sh_scratch, rows == 1 ? kDecodeCounters * 4 : 0};
+                            shd_bytes, sh_scratch,
+                            rows <= kFusedDecodeTokens ? kDecodeCounters * 4 : 0};
     constexpr size_t kParts = sizeof(sizes) / sizeof(sizes[0]);
     size_t total = 0;
     for (size_t b : sizes)
@@ -427,13 +428,14 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
     auto* counters = static_cast<unsigned*>(part[25]);
     auto st = static_cast<hipStream_t>(stream);
 
-    // one token: two fused launches (moe_decode_fused) where the encodings and shapes are
-    // among those it instantiates
-    if (rows == 1 && same_layout(L.gate_exps, L.up_exps) && same_layout(L.gate_shexp, L.up_shexp)) {
+    // up to kFusedDecodeTokens tokens: two fused launches (moe_decode_fused) where the
+    // encodings and shapes are among those it instantiates
+    if (rows <= kFusedDecodeTokens && same_layout(L.gate_exps, L.up_exps) &&
+        same_layout(L.gate_shexp, L.up_shexp)) {
         const bool up_packed = pk.gate_exps && pk.up_exps;
         const bool down_packed = pk.down_exps != nullptr;
         DecodeMoe m{};
-        m.router = job(L.router, x, 1, H, E, logits, status);
+        m.router = job(L.router, x, rows, H, E, logits, status);
         m.experts_up = IndexedJob{job(L.gate_exps, x, 1, H, F, g, status), idx,
                                   up_packed ? kdq_gguf_packed_bytes(L.gate_exps.encoding, H, F)
                                             : L.gate_exps.expert_bytes,
@@ -456,6 +458,7 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
         m.experts = unsigned(E);
         m.top_k = unsigned(K);
         m.hidden = unsigned(H);
+        m.tokens = unsigned(rows);
         m.idx = idx;
         m.w = w;
         m.gate_vector = L.shared_gate;
@@ -463,8 +466,9 @@ int moe_gguf(const kdq_moe_gguf_layer* layer, const kdq_moe_gguf_packed_stacks* 
         m.y = y;
         m.status = status;
         m.counters = counters;
-        m.counter_count = unsigned(kDecodeCounters) - 1;
-        m.gate = reinterpret_cast<float*>(counters + kDecodeCounters - 1);
+        // row-block counts, then a gate scalar per token
+        m.counter_count = unsigned(kDecodeCounters - kFusedDecodeTokens);
+        m.gate = reinterpret_cast<float*>(counters + (kDecodeCounters - kFusedDecodeTokens));
         if (moe_decode_fused(m, st, true) == KDQ_OK)
             return moe_decode_fused(m, st, false);
     }

@@ -354,16 +354,20 @@ FUSED_DECODE = [  # (gate/up experts, down experts, shared gate/up, shared down)
     (Q4_K, Q4_K, Q8_0, Q6_K)]
 
 
+@pytest.mark.parametrize("tokens", [1, 3, 8])
 @pytest.mark.parametrize("resident", [False, True], ids=["rows", "packed"])
 @pytest.mark.parametrize("encs", FUSED_DECODE, ids=lambda e: "-".join(map(str, e)))
 @pytest.mark.parametrize("H", [2048, 4096])
-def test_moe_gguf_fused_decode(device, oracle, encs, resident, H):
-    """One token on the fused decode (the router, then one launch that routes inside every
-    expert workgroup and runs the experts' and the shared expert's gate / up, and one that
-    runs every down and lets the last workgroup of each row block combine it): each
-    instantiated encoding mix, over row-major and resident packed stacks, hidden 2048 and
-    4096 (8 and 16 wavefronts).  Three calls in a row with different tokens (the row-block
-    counters reset between calls), each against the oracle, routing exact."""
+def test_moe_gguf_fused_decode(device, oracle, encs, resident, H, tokens):
+    """Up to 8 tokens on the fused decode (one launch that computes the router, routes in
+    its last router workgroup -- one token by the whole workgroup, several by a wavefront
+    each -- and runs every slot's expert gate / up and the shared expert's, then one that
+    runs every down and lets the last workgroup of each token's row block combine it):
+    each instantiated encoding mix, over row-major and resident packed stacks, hidden 2048
+    and 4096 (8 and 16 wavefronts), 1, 3 and 8 tokens (8 tokens of hidden 4096, past the
+    64 KB of staged router rows, take the staged path).  Three calls in a row with
+    different tokens (the row-block counters reset between calls), each against the
+    oracle, routing exact."""
     import torch
     E, K, F, S = 32, 8, 768, 512
     gu, dn, sgu, sdn = encs
@@ -375,12 +379,14 @@ def test_moe_gguf_fused_decode(device, oracle, encs, resident, H):
     packed = ops.moe_gguf_pack(dev) if resident else None
     status = torch.zeros(1, dtype=torch.int32, device=device)
     for call in range(3):
-        x = synth.normal(71 + call + H, 1, H).reshape(1, H)
+        x = synth.normal(71 + call + H + 10 * tokens, 1, tokens * H).reshape(tokens, H)
         want, idx, w = oracle.moe_gguf_forward(spec, x)
         y, sel, ws = ops.moe_gguf(dev, torch.from_numpy(x).to(device), status=status,
                                   packed=packed)
         assert np.array_equal(sel.cpu().numpy(), idx)
-        assert np.abs(ws.cpu().numpy() - w).max() < 1e-6
+        # the device's logits are fp32 sums of H products, the oracle's double: at hidden
+        # 4096 the renormalised weights differ by up to ~1e-6 (1.01e-6 seen at 8 tokens)
+        assert np.abs(ws.cpu().numpy() - w).max() < (1e-6 if H <= 2048 else 2e-6)
         assert_close(y.cpu().numpy(), want, what=f"fused decode {encs} call {call}")
     assert int(status.item()) == 0
 
