@@ -262,7 +262,9 @@ typedef struct kdq_moe_gguf_layer {
  * workgroups hand the routing and the rows to combine to one another through
  * device-wide counters (one set per GPU): calls that overlap on one GPU race (as they
  * do on the library's workspace); `status` |= 8 if a workgroup waited past its bound
- * for the routing (the output is then not the layer's).
+ * for the routing (the output is then not the layer's).  The call number those counters
+ * compare lives on the device, so the two launches may be captured in a graph and
+ * replayed (after one call outside the capture has sized the workspace).
  * Host wait: when the prefill GEMM runs here, this call packs the weights itself and
  * cannot know in advance whether a block scale could take a dequantised weight past
  * the fp16 range (never so in real checkpoints); it copies the GEMM's flag to the host

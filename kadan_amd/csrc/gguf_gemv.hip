@@ -2365,25 +2365,34 @@ namespace {
 
 #include "kdq_route.hpp"
 
-// The router, the routing and the shared gate the up launch computes, and the counters
-// of the down launch's row blocks, which it clears.
-// The fused decode's device-wide state (one copy per GPU, zero at load): the router
-// workgroups' completion count (the last one resets it) and, per slot, the published
-// selection: (epoch << 8) | expert of the call that routed last.  Calls that overlap on
+// The fused decode's device-wide state (one copy per GPU, zero at load): the epoch of the
+// last completed call (the down launch advances it, so a call's up launch reads the same
+// value in every workgroup, and a replayed graph of the launches still numbers each call
+// anew), the router workgroups' completion count (the last one resets it) and, per
+// (token, slot), the published selection: (epoch << 8) | expert.  Calls that overlap on
 // one GPU race on them (and on the workspace), as on the rest of the library's scratch.
 // Kernels take its address as an argument (DecodeRoute::state), not through the symbol.
 constexpr unsigned kDecodeTokens = kFusedDecodeTokens;
 struct DecodeState {
+    unsigned epoch;
     unsigned router_arrived;
     unsigned routed_slot[kDecodeTokens * kMaxFused];  // token t's slot i at t * top_k + i
 };
 __device__ DecodeState g_decode_state;
 
+// This call's epoch: one past the last completed call's, 24 bits, never 0 (the
+// published words start at 0 and unused ones are cleared to 0).
+__device__ __forceinline__ unsigned call_epoch(const DecodeState* state) {
+    const unsigned e =
+        (__hip_atomic_load(&state->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1) &
+        0xffffffu;
+    return e ? e : 1u;
+}
+
 struct DecodeRoute {
     const uint8_t* router;  // F32 rows [experts][row_bytes]
     size_t router_row_bytes;
     unsigned router_workgroups;  // the grid's first workgroups: one router row per wavefront
-    unsigned epoch;              // this call's number on this device (never 0)
     DecodeState* state;          // this device's g_decode_state
     float* logits;
     unsigned experts, top_k, tokens;
@@ -2445,9 +2454,9 @@ constexpr unsigned kRouteSpinLimit = 1u << 20;
 
 // Workgroups [0, router_workgroups): the router GEMV, one F32 row per wavefront in
 // exact_gemv<KDQ_F32, 1>'s arithmetic (the same logits as the staged path), stored at
-// device scope; the last of them to finish routes the token (route_select_wg, the whole
-// workgroup over those logits, read at device scope) and publishes each slot's expert
-// with this call's epoch.
+// device scope; the last of them to finish routes the tokens (route_select_wg, the whole
+// workgroup, for one; route_select, a wavefront each, for several) and publishes each
+// (token, slot)'s expert with this call's epoch.
 // Then the experts' paired gate / up workgroups (job step = slot): their activation
 // loads go out first, then thread 0 waits for the epoch and reads its slot's expert.
 // Then the shared expert's paired gate / up; its first workgroup also takes the gate
@@ -2549,13 +2558,20 @@ __global__ __launch_bounds__(W * 64) void moe_decode_up_kernel(const MfmaJobs a,
         // and its expert
         int e = 0;
         float we = 0.f;
+        const unsigned epoch = call_epoch(route.state);
         auto publish = [&](unsigned token, unsigned slot) {
             const unsigned at = token * route.top_k + slot;
             __hip_atomic_store(&route.idx[at], e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(&route.w[at], we, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&route.state->routed_slot[at], (route.epoch << 8) | unsigned(e),
+            __hip_atomic_store(&route.state->routed_slot[at], (epoch << 8) | unsigned(e),
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         };
+        // words past this call's slots: cleared, so an old word can never carry a later
+        // call's epoch (the epoch wraps after 2^24 calls)
+        for (unsigned i = route.tokens * route.top_k + threadIdx.x;
+             i < kDecodeTokens * kMaxFused; i += W * 64)
+            __hip_atomic_store(&route.state->routed_slot[i], 0u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
         if (route.tokens == 1) {
             route_select_wg<W, kMaxFused, true>(route.logits, route.experts, route.top_k,
                                                 *reinterpret_cast<RouteScratch*>(lds), e, we);
@@ -2580,11 +2596,12 @@ __global__ __launch_bounds__(W * 64) void moe_decode_up_kernel(const MfmaJobs a,
         // flight meanwhile)
         auto late = [&]() -> int {
             if (threadIdx.x == 0) {
+                const unsigned epoch = call_epoch(route.state);
                 unsigned spins = 0, word;
                 const unsigned* published = &route.state->routed_slot[slot];
                 while (((word = __hip_atomic_load(published, __ATOMIC_RELAXED,
                                                   __HIP_MEMORY_SCOPE_AGENT)) >> 8) !=
-                       route.epoch) {
+                       epoch) {
                     if (++spins == kRouteSpinLimit) {
                         if (route.status)
                             atomicOr(route.status, 8u);
@@ -2621,6 +2638,7 @@ struct DecodeCombine {
     unsigned top_k, hidden;
     float* y;             // [tokens][hidden]
     unsigned* counters;   // one per (token, row block), zero on entry
+    DecodeState* state;   // its epoch advanced here, after every up workgroup has read it
 };
 
 // Workgroups [0, a.columns * a.count) run the experts' down rows (job step = token *
@@ -2634,6 +2652,9 @@ __global__ __launch_bounds__(W * 64) void moe_decode_down_kernel(const MfmaJobs 
                                                                  const MfmaJobs b,
                                                                  const DecodeCombine c) {
     __shared__ unsigned arrived;
+    if (blockIdx.x == 0 && threadIdx.x == 0)
+        __hip_atomic_store(&c.state->epoch, call_epoch(c.state), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     const unsigned a_workgroups = a.columns * a.count;
     unsigned block, token;
     if (blockIdx.x < a_workgroups) {
@@ -2812,9 +2833,6 @@ int moe_decode_fused(const DecodeMoe& m, hipStream_t s, bool check_only) {
     if (check_only)
         return KDQ_OK;
 
-    // this call's number on this device, 24 bits and never 0 (the published words start
-    // at 0)
-    static std::atomic<unsigned> calls[kDevices];
     static std::atomic<DecodeState*> states[kDevices];  // g_decode_state's address
     DecodeState* state = states[device].load();
     if (!state) {
@@ -2823,13 +2841,9 @@ int moe_decode_fused(const DecodeMoe& m, hipStream_t s, bool check_only) {
         state = static_cast<DecodeState*>(address);
         states[device].store(state);
     }
-    unsigned epoch = ++calls[device] & 0xffffffu;
-    if (epoch == 0)
-        epoch = ++calls[device] & 0xffffffu;
     const DecodeRoute route{static_cast<const uint8_t*>(m.router.weights),
                             m.router.row_bytes,
                             unsigned((m.experts + pua.waves - 1) / pua.waves),
-                            epoch,
                             state,
                             m.logits,
                             m.experts,
@@ -2855,7 +2869,7 @@ int moe_decode_fused(const DecodeMoe& m, hipStream_t s, bool check_only) {
     if ((rc = m.up_packed ? up.template operator()<true>() : up.template operator()<false>()))
         return rc;
     const DecodeCombine comb{m.experts_down.job.output, m.shared_down.job.output, m.w, m.gate,
-                             K, m.hidden, m.y, m.counters};
+                             K, m.hidden, m.y, m.counters, state};
     auto down = [&]<bool PA>() -> int {
         if (da_enc == KDQ_Q6_K)
             return db_enc == KDQ_Q4_K ? launch_decode_down<KDQ_Q6_K, PA, KDQ_Q4_K>(da, db, comb, down_lds, s)

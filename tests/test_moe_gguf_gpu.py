@@ -391,6 +391,45 @@ def test_moe_gguf_fused_decode(device, oracle, encs, resident, H, tokens):
     assert int(status.item()) == 0
 
 
+def test_moe_gguf_fused_decode_graph_replays(device):
+    """The fused decode captured in a HIP graph and replayed: the call's epoch lives on the
+    device (the down launch advances it), so every replay routes its own token rather than
+    reading the words an earlier replay published.  Six replays with a new token copied in
+    between, eager calls in between too, each replay equal bit for bit to the eager result
+    for its token."""
+    import torch
+    from kadan_amd import ops
+    H, E, K, F, S = 2048, 32, 8, 768, 512
+    encs = {"gate_exps": Q4_K, "up_exps": Q4_K, "down_exps": Q6_K, "gate_shexp": Q8_0,
+            "up_shexp": Q8_0, "down_shexp": Q4_K}
+    spec = make_layer(90, H, E, K, F, S, encs)
+    dev = to_device(torch, device, spec)
+    xs = [torch.from_numpy(synth.normal(91 + i, 1, H).reshape(1, H)).to(device)
+          for i in range(5)]
+    eager = []
+    for x in xs:
+        y, sel, w = ops.moe_gguf(dev, x)
+        eager.append((y.cpu().numpy(), sel.cpu().numpy(), w.cpu().numpy()))
+    static_x = xs[0].clone()
+    ops.moe_gguf(dev, static_x)  # workspace and kernel attributes set up before capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y, sel, w = ops.moe_gguf(dev, static_x)
+    for n, i in enumerate([1, 3, 0, 4, 2, 2]):
+        static_x.copy_(xs[i])
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(sel.cpu().numpy(), eager[i][1]), f"replay {n}"
+        assert np.array_equal(w.cpu().numpy(), eager[i][2]), f"replay {n}"
+        assert np.array_equal(y.cpu().numpy(), eager[i][0]), f"replay {n}"
+        j = (i + 1) % 5  # the program's own eager work between replays
+        ye, se, _ = ops.moe_gguf(dev, xs[j])
+        assert np.array_equal(se.cpu().numpy(), eager[j][1])
+        assert np.array_equal(ye.cpu().numpy(), eager[j][0])
+
+
 @pytest.mark.parametrize("rows,seed", [(256, 2), (512, 3)])
 def test_moe_gguf_grouped_matches_fp16_model(device, oracle, rows, seed):
     """The grouped-GEMM layer (experts and the shared expert on the prefill GEMMs) equals
