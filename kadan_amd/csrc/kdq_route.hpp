@@ -1,5 +1,6 @@
-// Expert routing by one wavefront, shared by the MoE layers (moe_mxfp4.hip, and the
-// GGUF layer's fused decode in gguf_gemv.hip): the softmax of the reference's
+// Expert routing, by one wavefront (route_select) or by a whole workgroup for one token's
+// latency (route_select_wg), shared by the MoE layers (moe_mxfp4.hip, and the GGUF
+// layer's fused decode in gguf_gemv.hip): the softmax of the reference's
 // MoeLayer::forward (IW/src/models/text/qwen_layers.cpp:397-425; IW =
 // services/hikari/inference_worker) with the host library's expf and the total in expert
 // order, then its std::partial_sort top-k and the renormalised weights.  Included inside
@@ -237,10 +238,10 @@ __device__ __forceinline__ void route_select(const float* __restrict__ logits, u
 // LDS of route_select_wg (16-byte aligned, in the caller's LDS).
 struct RouteScratch {
     uint64_t exp_table[32];  // kdq_expf::kTable, staged while the logits load
-    float p[320];        // expf(v - max) (+0 past the experts)
-    float q[320];        // probabilities (NaN past the experts: compares false)
-    unsigned rank[256];  // per expert: probabilities above it | equal ones << 16
-    double part[16];
+    float p[320];            // expf(v - max) (+0 past the experts)
+    float q[320];            // probabilities (NaN past the experts: compares false)
+    unsigned rank[256];      // per expert: probabilities above it | equal ones << 16
+    double part[16];         // per wavefront: its p total
     float wave_max[16];
     unsigned inexact, ambiguous;
     int sel[64];
