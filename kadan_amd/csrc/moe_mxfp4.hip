@@ -29,8 +29,6 @@
 namespace kdq {
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kMaxTopK = 8, kMaxExperts = 256;
@@ -253,24 +251,12 @@ __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* __restrict
 
 // --------------------------------------------------------------- grouped GEMMs
 
-__device__ __forceinline__ float e8m0(unsigned s) {
-    return __uint_as_float(s << 23);  // exponent field only: the converter reads 2^(s-127)
-}
-
 // silu(x) = x / (1 + e^-x) from the hardware exponential and reciprocal (each within an
 // ulp or two): h leaves as FP8 terms good to about 12 bits, so the epilogue's cost, not
 // the last bits of silu, is what matters; infinities and NaN come out as in the
 // reference's x / (1 + expf(-x)).
 __device__ __forceinline__ float silu(float x) {
     return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504088896341f));
-}
-
-__device__ __forceinline__ uint16_t bf16_rne(float x) {
-    return __builtin_bit_cast(uint16_t, __bf16(x));
-}
-
-__device__ __forceinline__ float bf16_value(uint16_t b) {
-    return __uint_as_float(unsigned(b) << 16);
 }
 
 struct Item {
