@@ -32,10 +32,14 @@
  *                          routing)
  *   kdo_moe_forward_f32    not a checker: the timed AVX2 fp32 CPU baseline, checked
  *                          against kdo_moe_forward to fp32 rounding
- *   kdo_moe_forward        parity unpinned against the reference as a whole: the
- *                          reference never runs MXFP4 weights through MoeLayer
- *                          (IW/src/models/text/qwen_layers.cpp:378-492); its parts
- *                          are pinned individually as listed above.
+ *   kdo_moe_forward        the reference never runs MXFP4 weights through MoeLayer
+ *                          (IW/src/models/text/qwen_layers.cpp:378-492), so no
+ *                          reference output exists for the whole; it is pinned by a
+ *                          closed-form known answer worked out from that definition
+ *                          (tests/util.py known_answer_moe, float64, no oracle code:
+ *                          a dropped silu, swapped gate/up, transposed down or misplaced
+ *                          routing weight each fail it) and its parts individually as
+ *                          listed above.
  */
 #ifndef KADAN_ORACLE_H
 #define KADAN_ORACLE_H

@@ -607,8 +607,9 @@ def test_moe_forward_known_answer(oracle):
 
 def test_moe_forward_vs_numpy_composition(oracle):
     """MoeLayer::forward (IW/src/models/text/qwen_layers.cpp:378-492) composed in float64
-    from pinned parts; the composition itself is unpinned against the reference, which
-    never runs MXFP4 weights through MoeLayer."""
+    from pinned parts.  The reference never runs MXFP4 weights through MoeLayer, so the
+    whole is pinned by the closed-form case above, and this checks the composition at a
+    size that case does not reach."""
     tokens, hidden, inter, experts, top_k = 6, 64, 96, 4, 2
     x, logits = synth.moe_inputs(12, tokens, hidden, experts)
     (gb, gs), (ub, us), (db, ds) = synth.moe_weights(12, experts, hidden, inter)
