@@ -10,6 +10,8 @@
 //   permute_kernel    one workgroup: stable counting sort of the slots by expert
 //                     (expert-major, slot ascending) plus the list of work items
 //                     (expert, first row) of at most kItemRows rows each
+//   chunk_count_kernel, chunk_place_kernel  the same sort for more slots, one workgroup
+//                     per 1024 slots: ranks and counts per chunk, then the placement
 //   gate_up_kernel    grouped GEMM over work items on the scaled MFMA
 //                     (v_mfma_scale_f32_32x32x64_f8f6f4): FP8 activation terms x the packed
 //                     FP4 gate and up rows with their E8M0 scales, fp32 accumulation, fused
@@ -105,10 +107,119 @@ void launch_route_selection(const float* logits, size_t tokens, size_t experts,
                            unsigned(top_k), idx, w);
 }
 
-// Stable counting sort of slots by expert by one workgroup of 1024 threads (every thread
-// calls it); also the work items.
-// Also slot_row[r] = item * kItemRows + row of the slot at position r (the K-sliced
-// finalize runs over occupied rows only).
+// The experts' layout for a permutation, in LDS: per expert its slot count, its first
+// position (segment), and the first numbers of its heavy and light work items.
+struct ExpertLayout {
+    int counts[kMaxExperts], segment[kMaxExperts], heavy_base[kMaxExperts],
+        light_base[kMaxExperts];
+    int heavy_total;
+};
+
+// Wavefront 0, counts filled: exclusive prefix sums over the experts of their slots and
+// of their heavy and light work items (ceil(count / kItemRows) items, the last one light
+// when it has at most kTileRows rows); lane l takes experts 4l .. 4l + 3.  offsets
+// [experts + 1] and *item_count are written when given.
+__device__ __forceinline__ void expert_layout(ExpertLayout& L, unsigned experts,
+                                              bool heavy_first, unsigned lane,
+                                              int32_t* __restrict__ offsets,
+                                              int32_t* __restrict__ item_count) {
+    int c[4], hv[4], lt[4], slot_sum = 0, heavy_sum = 0, light_sum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const unsigned e = 4 * lane + j;
+        c[j] = e < experts ? L.counts[e] : 0;
+        const int n = (c[j] + kItemRows - 1) / kItemRows;
+        lt[j] = heavy_first && n > 0 && c[j] - (n - 1) * kItemRows <= kTileRows ? 1 : 0;
+        hv[j] = n - lt[j];
+        slot_sum += c[j];
+        heavy_sum += hv[j];
+        light_sum += lt[j];
+    }
+    int slot_scan = slot_sum, heavy_scan = heavy_sum, light_scan = light_sum;
+#pragma unroll
+    for (int d = 1; d < 64; d *= 2) {  // inclusive over the lanes
+        const int a = __shfl_up(slot_scan, d, 64), b = __shfl_up(heavy_scan, d, 64),
+                  l = __shfl_up(light_scan, d, 64);
+        if (lane >= unsigned(d)) {
+            slot_scan += a;
+            heavy_scan += b;
+            light_scan += l;
+        }
+    }
+    int acc = slot_scan - slot_sum, hb = heavy_scan - heavy_sum, lb = light_scan - light_sum;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const unsigned e = 4 * lane + j;
+        if (e < experts) {
+            if (offsets)
+                offsets[e] = acc;
+            L.segment[e] = acc;
+            L.heavy_base[e] = hb;
+            L.light_base[e] = lb;
+        }
+        acc += c[j];
+        hb += hv[j];
+        lb += lt[j];
+    }
+    if (lane == 63) {
+        if (offsets)
+            offsets[experts] = slot_scan;
+        if (item_count)
+            *item_count = heavy_scan + light_scan;
+        L.heavy_total = heavy_scan;
+    }
+}
+
+// Item of chunk k (rows 64k ..) of expert e: its heavy items in order, then its light one.
+__device__ __forceinline__ int item_of(const ExpertLayout& L, bool heavy_first, unsigned e,
+                                       int k) {
+    const int n = (L.counts[e] + kItemRows - 1) / kItemRows;  // chunks of expert e
+    const int heavy =
+        n - (heavy_first && n > 0 && L.counts[e] - (n - 1) * kItemRows <= kTileRows ? 1 : 0);
+    return k < heavy ? L.heavy_base[e] + k : L.heavy_total + L.light_base[e];
+}
+
+// Every expert's work items (expert, first row), by all threads of the workgroup.
+__device__ __forceinline__ void write_items(const ExpertLayout& L, bool heavy_first,
+                                            unsigned experts, int32_t* __restrict__ items) {
+    for (unsigned e = threadIdx.x; e < experts; e += blockDim.x)
+        for (int r = 0, k = 0; r < L.counts[e]; r += kItemRows, ++k) {
+            const int n = item_of(L, heavy_first, e, k);
+            items[2 * n] = int(e);
+            items[2 * n + 1] = r;
+        }
+}
+
+// Within a wavefront: the rank of this lane's slot among the lanes below it with the same
+// expert, and how many lanes have that expert (experts below 256).
+__device__ __forceinline__ void wave_match(bool valid, int e, unsigned lane, int& rank,
+                                           int& group) {
+    unsigned long long same = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        const unsigned long long ones = __ballot(valid && ((e >> b) & 1));
+        same &= ((e >> b) & 1) ? ones : ~ones;
+    }
+    rank = __popcll(same & ((1ull << lane) - 1ull));
+    group = __popcll(same);
+}
+
+// Slot at position r: perm[r], position[s] (when given) and slot_row[r] = item *
+// kItemRows + row (the K-sliced finalize runs over occupied rows only).
+__device__ __forceinline__ void place_slot(const ExpertLayout& L, bool heavy_first, unsigned s,
+                                           int e, int r, int32_t* __restrict__ perm,
+                                           int32_t* __restrict__ position,
+                                           int32_t* __restrict__ slot_row) {
+    perm[r] = int(s);
+    if (position)
+        position[s] = r;  // inverse permutation
+    const int within = r - L.segment[e];
+    slot_row[r] = item_of(L, heavy_first, unsigned(e), within / kItemRows) * kItemRows +
+                  within % kItemRows;
+}
+
+// Stable counting sort of slots by expert (expert-major, slot ascending) by one workgroup
+// of 1024 threads (every thread calls it), 1024 slots at a time; also the work items.
 // With heavy_first, work items are numbered heavy first: every item of more than
 // kTileRows rows (two activation tiles, twice the MFMAs of a one-tile item), by expert,
 // then the one-tile items.  The grouped GEMMs' workgroups are dispatched in item order,
@@ -123,80 +234,22 @@ __device__ __forceinline__ void permute_slots(const int32_t* __restrict__ idx, u
                                               int32_t* __restrict__ item_count,
                                               int32_t* __restrict__ position,
                                               int32_t* __restrict__ slot_row) {
-    __shared__ int counts[kMaxExperts], base[kMaxExperts], segment[kMaxExperts],
-        heavy_base[kMaxExperts], light_base[kMaxExperts];
-    __shared__ int heavy_total;
+    __shared__ ExpertLayout L;
+    __shared__ int base[kMaxExperts];
     __shared__ int wave_counts[16][kMaxExperts];
     const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     for (unsigned e = tid; e < experts; e += 1024)
-        counts[e] = 0;
+        L.counts[e] = 0;
     __syncthreads();
     for (unsigned s = tid; s < slots; s += 1024)
-        atomicAdd(&counts[idx[s]], 1);
+        atomicAdd(&L.counts[idx[s]], 1);
     __syncthreads();
-    if (wave == 0) {
-        // exclusive prefix sums over the experts of their slots and of their heavy and
-        // light work items (ceil(count / kItemRows) items, the last one light when it
-        // has at most kTileRows rows): lane l takes experts 4l .. 4l + 3
-        int c[4], hv[4], lt[4], slot_sum = 0, heavy_sum = 0, light_sum = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const unsigned e = 4 * lane + j;
-            c[j] = e < experts ? counts[e] : 0;
-            const int n = (c[j] + kItemRows - 1) / kItemRows;
-            lt[j] = heavy_first && n > 0 && c[j] - (n - 1) * kItemRows <= kTileRows ? 1 : 0;
-            hv[j] = n - lt[j];
-            slot_sum += c[j];
-            heavy_sum += hv[j];
-            light_sum += lt[j];
-        }
-        int slot_scan = slot_sum, heavy_scan = heavy_sum, light_scan = light_sum;
-#pragma unroll
-        for (int d = 1; d < 64; d *= 2) {  // inclusive over the lanes
-            const int a = __shfl_up(slot_scan, d, 64), b = __shfl_up(heavy_scan, d, 64),
-                      l = __shfl_up(light_scan, d, 64);
-            if (lane >= unsigned(d)) {
-                slot_scan += a;
-                heavy_scan += b;
-                light_scan += l;
-            }
-        }
-        int acc = slot_scan - slot_sum, hb = heavy_scan - heavy_sum, lb = light_scan - light_sum;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const unsigned e = 4 * lane + j;
-            if (e < experts) {
-                offsets[e] = acc;
-                base[e] = acc;
-                segment[e] = acc;
-                heavy_base[e] = hb;
-                light_base[e] = lb;
-            }
-            acc += c[j];
-            hb += hv[j];
-            lb += lt[j];
-        }
-        if (lane == 63) {
-            offsets[experts] = slot_scan;
-            *item_count = heavy_scan + light_scan;
-            heavy_total = heavy_scan;
-        }
-    }
+    if (wave == 0)
+        expert_layout(L, experts, heavy_first, lane, offsets, item_count);
     __syncthreads();
-    // item of chunk k (rows 64k ..) of expert e: its heavy items in order, then its light one
-    auto item_of = [&](unsigned e, int k) {
-        const int n = (counts[e] + kItemRows - 1) / kItemRows;  // chunks of expert e
-        const int heavy =
-            n - (heavy_first && n > 0 && counts[e] - (n - 1) * kItemRows <= kTileRows ? 1 : 0);
-        return k < heavy ? heavy_base[e] + k : heavy_total + light_base[e];
-    };
-    for (unsigned e = tid; e < experts; e += 1024)  // each expert's work items
-        for (int r = 0, k = 0; r < counts[e]; r += kItemRows, ++k) {
-            const int n = item_of(e, k);
-            items[2 * n] = int(e);
-            items[2 * n + 1] = r;
-        }
-    const unsigned long long below = (1ull << lane) - 1ull;
+    for (unsigned e = tid; e < experts; e += 1024)
+        base[e] = L.segment[e];
+    write_items(L, heavy_first, experts, items);
     for (unsigned first = 0; first < slots; first += 1024) {
         for (unsigned i = tid; i < 16 * kMaxExperts; i += 1024)
             (&wave_counts[0][0])[i] = 0;
@@ -204,14 +257,8 @@ __device__ __forceinline__ void permute_slots(const int32_t* __restrict__ idx, u
         const unsigned s = first + tid;
         const bool valid = s < slots;
         const int e = valid ? idx[s] : 0;
-        unsigned long long same = __ballot(valid);
-#pragma unroll
-        for (int b = 0; b < 8; ++b) {
-            const unsigned long long ones = __ballot(valid && ((e >> b) & 1));
-            same &= ((e >> b) & 1) ? ones : ~ones;
-        }
-        const int rank = __popcll(same & below);
-        const int group = __popcll(same);
+        int rank, group;
+        wave_match(valid, e, lane, rank, group);
         if (valid && rank == group - 1)
             wave_counts[wave][e] = group;
         __syncthreads();
@@ -219,11 +266,7 @@ __device__ __forceinline__ void permute_slots(const int32_t* __restrict__ idx, u
             int r = base[e] + rank;
             for (unsigned w = 0; w < wave; ++w)
                 r += wave_counts[w][e];
-            perm[r] = int(s);
-            if (position)
-                position[s] = r;  // inverse permutation
-            const int within = r - segment[e];
-            slot_row[r] = item_of(unsigned(e), within / kItemRows) * kItemRows + within % kItemRows;
+            place_slot(L, heavy_first, s, e, r, perm, position, slot_row);
         }
         __syncthreads();
         for (unsigned x = tid; x < experts; x += 1024) {
@@ -234,6 +277,86 @@ __device__ __forceinline__ void permute_slots(const int32_t* __restrict__ idx, u
         }
         __syncthreads();
     }
+}
+
+// The same sort over many chunks of 1024 slots, one workgroup a chunk, in two launches
+// (the one-workgroup form spends ~1.9 us a chunk on one compute unit).
+// chunk_count_kernel: each slot's rank among the earlier slots of its chunk with the same
+// expert (chunk_rank[s]) and each chunk's count of every expert (chunk_counts[c][e]).
+__global__ __launch_bounds__(1024) void chunk_count_kernel(const int32_t* __restrict__ idx,
+                                                           unsigned slots, unsigned experts,
+                                                           int32_t* __restrict__ chunk_counts,
+                                                           int32_t* __restrict__ chunk_rank) {
+    __shared__ int wave_counts[16][kMaxExperts];
+    const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    for (unsigned i = tid; i < 16 * kMaxExperts; i += 1024)
+        (&wave_counts[0][0])[i] = 0;
+    const unsigned s = blockIdx.x * 1024 + tid;
+    const bool valid = s < slots;
+    const int e = valid ? idx[s] : 0;
+    __syncthreads();
+    int rank, group;
+    wave_match(valid, e, lane, rank, group);
+    if (valid && rank == group - 1)
+        wave_counts[wave][e] = group;
+    __syncthreads();
+    if (valid) {
+        int r = rank;
+        for (unsigned w = 0; w < wave; ++w)
+            r += wave_counts[w][e];
+        chunk_rank[s] = r;
+    }
+    for (unsigned x = tid; x < experts; x += 1024) {
+        int total = 0;
+        for (unsigned w = 0; w < 16; ++w)
+            total += wave_counts[w][x];
+        chunk_counts[size_t(blockIdx.x) * experts + x] = total;
+    }
+}
+
+// chunk_place_kernel: every workgroup sums the chunks' counts (the experts' totals and, for
+// its own chunk, the slots of each expert in earlier chunks) and places its chunk's slots;
+// workgroup 0 also writes offsets, the work items and their count.
+__global__ __launch_bounds__(1024) void chunk_place_kernel(
+    const int32_t* __restrict__ idx, unsigned slots, unsigned experts, unsigned heavy_first,
+    const int32_t* __restrict__ chunk_counts, const int32_t* __restrict__ chunk_rank,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ items,
+    int32_t* __restrict__ item_count, int32_t* __restrict__ position,
+    int32_t* __restrict__ slot_row) {
+    __shared__ ExpertLayout L;
+    __shared__ int before[kMaxExperts];
+    const unsigned tid = threadIdx.x, wave = tid / 64, lane = tid % 64, c = blockIdx.x;
+    const unsigned s = c * 1024 + tid;
+    const bool valid = s < slots;
+    const int e = valid ? idx[s] : 0;
+    const int r_chunk = valid ? chunk_rank[s] : 0;
+    for (unsigned x = tid; x < experts; x += 1024) {
+        int total = 0, earlier = 0;
+        for (unsigned k0 = 0; k0 < gridDim.x; k0 += 8) {  // eight loads in flight at once
+            int v[8];
+#pragma unroll
+            for (unsigned j = 0; j < 8; ++j)
+                v[j] = chunk_counts[size_t(min(k0 + j, gridDim.x - 1)) * experts + x];
+#pragma unroll
+            for (unsigned j = 0; j < 8; ++j) {
+                const unsigned k = k0 + j;
+                total += k < gridDim.x ? v[j] : 0;
+                earlier += k < c ? v[j] : 0;
+            }
+        }
+        L.counts[x] = total;
+        before[x] = earlier;
+    }
+    __syncthreads();
+    if (wave == 0)
+        expert_layout(L, experts, heavy_first != 0, lane, c == 0 ? offsets : nullptr,
+                      c == 0 ? item_count : nullptr);
+    __syncthreads();
+    if (c == 0)
+        write_items(L, heavy_first != 0, experts, items);
+    if (valid)
+        place_slot(L, heavy_first != 0, s, e, L.segment[e] + before[e] + r_chunk, perm, position,
+                   slot_row);
 }
 
 __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* __restrict__ idx,
@@ -1665,18 +1788,40 @@ int check_route(const float* logits, size_t tokens, size_t experts, size_t top_k
     return KDQ_OK;
 }
 
+// Scratch words of the chunked permutation (slot ranks, then per chunk a count per expert).
+size_t chunk_scratch_words(size_t slots, size_t experts) {
+    return slots + (slots + 1023) / 1024 * experts;
+}
+
+// `chunk_scratch` (chunk_scratch_words int32, or null): with more than kOneWgSlots slots
+// the permutation runs chunked in two launches there.
+constexpr size_t kOneWgSlots = 4096;
+
 int launch_route(const float* logits, size_t tokens, size_t experts, size_t top_k,
                  int32_t* idx, float* w, int32_t* offsets, int32_t* perm, int32_t* items,
                  int32_t* item_count, int32_t* position, int32_t* slot_row,
-                 hipStream_t stream) {
+                 int32_t* chunk_scratch, hipStream_t stream) {
     launch_route_selection(logits, tokens, experts, top_k, idx, w, stream);
     KDQ_HIP(hipGetLastError());
     // heavy items first when an average expert's rows fit one work item (the grouped
     // GEMMs' workgroups then all fit the compute units at once)
-    const unsigned heavy_first = tokens * top_k <= experts * (kItemRows / 2) ? 1u : 0u;
-    hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, stream, idx,
-                       unsigned(tokens * top_k), unsigned(experts), offsets, perm, items,
-                       item_count, position, slot_row, heavy_first);
+    const size_t slots = tokens * top_k;
+    const unsigned heavy_first = slots <= experts * (kItemRows / 2) ? 1u : 0u;
+    if (chunk_scratch && slots > kOneWgSlots) {
+        const unsigned chunks = unsigned((slots + 1023) / 1024);
+        int32_t* rank = chunk_scratch;
+        int32_t* counts = chunk_scratch + slots;
+        hipLaunchKernelGGL(chunk_count_kernel, dim3(chunks), dim3(1024), 0, stream, idx,
+                           unsigned(slots), unsigned(experts), counts, rank);
+        KDQ_HIP(hipGetLastError());
+        hipLaunchKernelGGL(chunk_place_kernel, dim3(chunks), dim3(1024), 0, stream, idx,
+                           unsigned(slots), unsigned(experts), heavy_first, counts, rank, offsets,
+                           perm, items, item_count, position, slot_row);
+    } else {
+        hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, stream, idx, unsigned(slots),
+                           unsigned(experts), offsets, perm, items, item_count, position,
+                           slot_row, heavy_first);
+    }
     KDQ_HIP(hipGetLastError());
     return KDQ_OK;
 }
@@ -1708,14 +1853,14 @@ extern "C" int kdq_moe_route(const float* logits, size_t tokens, size_t experts,
         return rc;
     if (!idx || !w || !offsets || !perm)
         return KDQ_ERR_ARGUMENT;
-    const size_t items = tokens * top_k / kItemRows + experts + 1;
-    auto* scratch =
-        static_cast<int32_t*>(workspace(items * 8 + 256 + tokens * top_k * 4, &rc));
+    const size_t items = tokens * top_k / kItemRows + experts + 1, slots = tokens * top_k;
+    auto* scratch = static_cast<int32_t*>(
+        workspace(items * 8 + 256 + slots * 4 + chunk_scratch_words(slots, experts) * 4, &rc));
     if (rc)
         return rc;
     return launch_route(logits, tokens, experts, top_k, idx, w, offsets, perm, scratch,
                         scratch + items * 2, nullptr, scratch + items * 2 + 64,
-                        static_cast<hipStream_t>(stream));
+                        scratch + items * 2 + 64 + slots, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int kdq_mxfp4_dequantize(const uint8_t* blocks, const uint8_t* scales, size_t rows,
@@ -1845,8 +1990,13 @@ int launch_layer(const uint16_t* x_bf16, const float* logits, size_t tokens, siz
                            x_bf16, unsigned(hidden), s.xa, tiles);
         KDQ_HIP(hipGetLastError());
     } else {
+        // the activation tiles are written after the permutation: their space holds its
+        // chunked form's scratch meanwhile
+        const bool room = chunk_scratch_words(slots, experts) * 4 <=
+                          tile_bytes(tiles, hidden / 64, kXTerms);
         int rc = launch_route(logits, tokens, experts, top_k, s.idx, s.weight, s.offsets, s.perm,
-                              s.items, s.item_count, s.position, s.slot_row, st);
+                              s.items, s.item_count, s.position, s.slot_row,
+                              room ? reinterpret_cast<int32_t*>(s.xa) : nullptr, st);
         if (rc)
             return rc;
         hipLaunchKernelGGL(gather_kernel,

@@ -31,7 +31,7 @@ ROUTE_CASES = [(4, 4), (6, 3), (13, 8), (16, 4), (32, 4), (128, 4), (256, 8)]
 
 @pytest.mark.parametrize("tokens,experts,top_k", [(1, 32, 4), (7, 8, 2), (256, 32, 4),
                                                   (2048, 128, 4), (300, 256, 8), (5, 4, 4),
-                                                  (3000, 128, 4)])
+                                                  (3000, 128, 4), (700, 256, 8)])
 def test_route_and_permutation_bit_exact(device, oracle, tokens, experts, top_k):
     torch = _torch()
     _, logits = synth.moe_inputs(0xC4 + tokens, tokens, 64, experts,
