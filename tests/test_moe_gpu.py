@@ -190,6 +190,9 @@ def run_layer(device, oracle, tokens, hidden, inter, experts, top_k, seed, hot=0
 @pytest.mark.parametrize("tokens,hidden,inter,experts,top_k", [
     (1, 64, 64, 4, 2), (3, 128, 192, 8, 2), (37, 256, 128, 8, 4), (130, 128, 128, 4, 4),
     (16, 2880, 2880, 32, 4),
+    # more than 4096 slots (the chunked permutation): heavy items first, and experts of
+    # several work items each
+    (1100, 64, 64, 256, 4), (1300, 64, 64, 16, 4),
 ])
 def test_moe_layer_parity(device, oracle, tokens, hidden, inter, experts, top_k):
     run_layer(device, oracle, tokens, hidden, inter, experts, top_k, seed=0xC4 + tokens)
