@@ -2392,8 +2392,7 @@ __device__ __forceinline__ unsigned call_epoch(const DecodeState* state) {
 struct DecodeRoute {
     const uint8_t* router;  // F32 rows [experts][row_bytes]
     size_t router_row_bytes;
-    unsigned router_workgroups;  // the grid's first workgroups, router_rows rows each
-    unsigned router_rows;        // router rows a workgroup (one a wavefront, the first ones)
+    unsigned router_workgroups;  // the grid's first workgroups: one router row per wavefront
     DecodeState* state;          // this device's g_decode_state
     float* logits;
     unsigned experts, top_k, tokens;
@@ -2475,8 +2474,7 @@ __global__ __launch_bounds__(W * 64) void moe_decode_up_kernel(const MfmaJobs a,
         // reuses them)
         extern __shared__ __align__(16) uint8_t lds[];
         float4* xs = reinterpret_cast<float4*>(lds);
-        // wavefronts past router_rows load an active one's row (cache hits) and store nothing
-        const unsigned column = blockIdx.x * route.router_rows + wave % route.router_rows;
+        const unsigned column = blockIdx.x * W + wave;
         const u32x4* row = reinterpret_cast<const u32x4*>(
             route.router + size_t(min(column, route.experts - 1)) * route.router_row_bytes);
         // chunks of 8 values a lane (hidden <= 4096: at most 8), four at a time: the four
@@ -2496,7 +2494,7 @@ __global__ __launch_bounds__(W * 64) void moe_decode_up_kernel(const MfmaJobs a,
         for (unsigned q = threadIdx.x; q < route.tokens * a.in / 4; q += W * 64)
             xs[q] = reinterpret_cast<const float4*>(route.x)[q];
         __syncthreads();
-        if (wave < route.router_rows && column < route.experts) {
+        if (column < route.experts) {
             float sum[kDecodeTokens] = {};
             bool finite = true;
 #pragma unroll
@@ -2740,11 +2738,6 @@ bool decode_half(const IndexedJob& ij, unsigned count, size_t x_step, unsigned x
     return true;
 }
 
-// router rows per router workgroup of the fused decode: fewer than its 8 or 16 wavefronts
-// spreads the router's reads over more compute units (T=1 at the Qwen3 geometry: 25.5-25.8
-// us with a row a wavefront, 25.1-25.2 with 4 a workgroup, 26.4-26.5 with 2)
-constexpr unsigned kRouterRows = 4;
-
 // the fused decode kernels keep a few static LDS words beside the dynamic area
 constexpr int kDecodeDynamicLds = 159 * 1024;
 
@@ -2848,11 +2841,9 @@ int moe_decode_fused(const DecodeMoe& m, hipStream_t s, bool check_only) {
         state = static_cast<DecodeState*>(address);
         states[device].store(state);
     }
-    const unsigned router_rows = std::min(pua.waves, kRouterRows);
     const DecodeRoute route{static_cast<const uint8_t*>(m.router.weights),
                             m.router.row_bytes,
-                            unsigned((m.experts + router_rows - 1) / router_rows),
-                            router_rows,
+                            unsigned((m.experts + pua.waves - 1) / pua.waves),
                             state,
                             m.logits,
                             m.experts,
